@@ -1,0 +1,236 @@
+/*
+ * libsharplight_hip -- C ABI of the Sharplight HIP execution provider (MI355X / gfx950).
+ *
+ * The managed provider (Sharplight.Hip) binds these entry points with [LibraryImport], the way
+ * Sharplight.Metal binds its system frameworks (src/Sharplight.Metal/Interop/MetalFramework.cs:14-18);
+ * the Python package sharplight_amd binds the same symbols with ctypes.
+ *
+ * Conventions
+ *  - Every function returns an int status: SLHIP_OK (0) or a negative slhip_status. The message of the
+ *    last failure on the calling thread is slhip_last_error(). The managed side turns statuses into
+ *    the exceptions the reference's providers throw: SLHIP_ERR_INVALID -> ArgumentException,
+ *    SLHIP_ERR_UNSUPPORTED -> NotSupportedException, SLHIP_ERR_INDEX -> ArgumentOutOfRangeException.
+ *  - Tensor pointers are device pointers (slhip_malloc). Sizes and strides are in ELEMENTS of the
+ *    tensor's own dtype, rows are the leading dims flattened, the normalized/activated axis is last and
+ *    dense.
+ *  - Op entry points only enqueue work on the given stream (NULL = the device's null stream) and return;
+ *    nothing is synchronous except slhip_stream_sync / slhip_event_synchronize / slhip_memcpy_*_sync.
+ *  - Ops read inputs and write outputs only; outputs may alias an input of the same shape and layout
+ *    (in-place) unless stated otherwise.
+ *  - No op entry point allocates device memory, except slhip_gather's first call on a device, which
+ *    allocates that device's 16-byte index-error word.
+ */
+#ifndef SHARPLIGHT_HIP_H
+#define SHARPLIGHT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#if defined(_WIN32)
+#define SLHIP_API __declspec(dllexport)
+#else
+#define SLHIP_API __attribute__((visibility("default")))
+#endif
+
+#define SLHIP_ABI_VERSION 1
+
+typedef enum slhip_status {
+    SLHIP_OK = 0,
+    SLHIP_ERR_INVALID = -1,     /* bad argument: null pointer, size, stride, dtype combination */
+    SLHIP_ERR_UNSUPPORTED = -2, /* valid request this library has no kernel for */
+    SLHIP_ERR_HIP = -3,         /* the HIP runtime reported an error */
+    SLHIP_ERR_INDEX = -4,       /* a gather index was outside [0, V) (reported by slhip_stream_sync) */
+    SLHIP_ERR_NO_DEVICE = -5    /* no usable device / driver */
+} slhip_status;
+
+/* Element types of activations. */
+typedef enum slhip_dtype { SLHIP_F32 = 0, SLHIP_F16 = 1, SLHIP_BF16 = 2 } slhip_dtype;
+
+/* Row formats of a gathered table (Sharplight.Tensors.WeightFormat for these formats; the block
+ * layouts are ggml's, src/Sharplight.Cpu/Quant.cs:181-216). */
+typedef enum slhip_format {
+    SLHIP_FMT_F32 = 0,
+    SLHIP_FMT_F16 = 1,
+    SLHIP_FMT_BF16 = 2,
+    SLHIP_FMT_Q8_0 = 3, /* 34-byte blocks: f16 d, int8 q[32]           -> q*d        */
+    SLHIP_FMT_Q4_0 = 4, /* 18-byte blocks: f16 d, u8 qs[16] (nibbles)   -> (q-8)*d    */
+    SLHIP_FMT_Q4_1 = 5, /* 20-byte blocks: f16 d, f16 m, u8 qs[16]      -> q*d + m    */
+    SLHIP_FMT_Q5_0 = 6, /* 22-byte blocks: f16 d, u32 qh, u8 qs[16]     -> (q-16)*d   */
+    SLHIP_FMT_Q5_1 = 7  /* 24-byte blocks: f16 d, f16 m, u32 qh, qs[16] -> q*d + m    */
+} slhip_format;
+
+/* Row-norm kinds (StandardOps RmsNorm / L2Norm / LayerNorm). */
+typedef enum slhip_norm { SLHIP_NORM_RMS = 0, SLHIP_NORM_L2 = 1, SLHIP_NORM_LAYER = 2 } slhip_norm;
+
+/* Gate activations of the gated MLP (MlpActivations.cs:38-40). */
+typedef enum slhip_act { SLHIP_ACT_SILU = 0, SLHIP_ACT_GELU_TANH = 1, SLHIP_ACT_GELU_ERF = 2 } slhip_act;
+
+typedef void* slhip_stream; /* a hipStream_t */
+typedef void* slhip_event;  /* a hipEvent_t  */
+
+typedef struct slhip_device_props {
+    char name[256];        /* marketing name, e.g. "AMD Instinct MI355X" */
+    char arch[64];         /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+    int64_t total_memory;  /* bytes of device memory */
+    int32_t compute_units;
+    int32_t wavefront_size;
+    int32_t pci_domain, pci_bus, pci_device;
+    int32_t clock_khz;
+    int64_t l2_bytes;
+    int32_t max_threads_per_block;
+    int32_t lds_bytes_per_block;
+} slhip_device_props;
+
+/* ---- library / errors ------------------------------------------------------------------------- */
+
+/* Message of the last failed call on this thread ("" if none). Never NULL. */
+SLHIP_API const char* slhip_last_error(void);
+SLHIP_API int slhip_abi_version(void);
+
+/* ---- devices (IExecutionProvider.CheckAvailability / GetDevices, IExecutionProvider.cs:25-40;
+ *      DeviceInfo fields, src/Sharplight.Core/Runtime/DeviceInfo.cs:4-50) ------------------------ */
+
+/* Number of visible devices; 0 with SLHIP_OK when the driver loads but reports none, SLHIP_ERR_NO_DEVICE
+ * when the runtime cannot start. */
+SLHIP_API int slhip_device_count(int* count);
+SLHIP_API int slhip_device_props_get(int device, slhip_device_props* props);
+/* Makes `device` current for the calling thread (IExecutionProvider.OpenDevice). */
+SLHIP_API int slhip_set_device(int device);
+SLHIP_API int slhip_get_device(int* device);
+/* Free / total bytes of the current device (IComputeDevice.AvailableMemory / GetMemoryInfo). */
+SLHIP_API int slhip_mem_info(size_t* free_bytes, size_t* total_bytes);
+
+/* ---- memory (weights, state and activations a compiled segment owns, IComputeDevice.Compile) --- */
+
+SLHIP_API int slhip_malloc(void** ptr, size_t bytes);
+SLHIP_API int slhip_free(void* ptr);
+SLHIP_API int slhip_host_malloc(void** ptr, size_t bytes); /* pinned host staging buffer */
+SLHIP_API int slhip_host_free(void* ptr);
+/* Asynchronous copies on `stream` (ICompiledSegment.SetInput / GetOutput stage through these). */
+SLHIP_API int slhip_memcpy_h2d(void* dst, const void* src, size_t bytes, slhip_stream stream);
+SLHIP_API int slhip_memcpy_d2h(void* dst, const void* src, size_t bytes, slhip_stream stream);
+SLHIP_API int slhip_memcpy_d2d(void* dst, const void* src, size_t bytes, slhip_stream stream);
+SLHIP_API int slhip_memset(void* dst, int value, size_t bytes, slhip_stream stream);
+
+/* ---- streams and events ---------------------------------------------------------------------- */
+
+SLHIP_API int slhip_stream_create(slhip_stream* stream); /* default priority */
+SLHIP_API int slhip_stream_destroy(slhip_stream stream);
+/* Waits for the stream, then reports (and clears) a pending gather index error on the current device
+ * as SLHIP_ERR_INDEX, like GatherOp's ArgumentOutOfRangeException (src/Sharplight.Cpu/GatherOp.cs:60-63). */
+SLHIP_API int slhip_stream_sync(slhip_stream stream);
+SLHIP_API int slhip_event_create(slhip_event* event);
+SLHIP_API int slhip_event_destroy(slhip_event event);
+SLHIP_API int slhip_event_record(slhip_event event, slhip_stream stream);
+SLHIP_API int slhip_event_synchronize(slhip_event event);
+SLHIP_API int slhip_event_elapsed_ms(float* ms, slhip_event start, slhip_event stop);
+
+/* ---- graphs: record a sequence of launches once, replay it without host work per launch ------------
+ * The HIP counterpart of the Vulkan segment's command buffer recorded once per symbol binding and
+ * resubmitted every step (src/Sharplight.Vulkan/VulkanSegment.cs:440-457). Capture every op call made on
+ * `stream` between begin and end (the op entry points enqueue only kernels: no memset or copy is
+ * recorded); replay with slhip_graph_launch on any stream. */
+typedef void* slhip_graph; /* an instantiated hipGraphExec_t */
+SLHIP_API int slhip_graph_begin(slhip_stream stream);
+SLHIP_API int slhip_graph_end(slhip_stream stream, slhip_graph* graph);
+SLHIP_API int slhip_graph_launch(slhip_graph graph, slhip_stream stream);
+SLHIP_API int slhip_graph_destroy(slhip_graph graph);
+
+/* ---- fused layer ops ------------------------------------------------------------------------- */
+
+/*
+ * Row normalization over the last axis, with an optional residual add fused in front.
+ *   h = res ? x + res : x                            (f32)
+ *   RMS:   y = h * (1/sqrt(sum(h^2)/D + eps)) * w
+ *   L2:    y = h * (1/sqrt(sum(h^2) + eps))          (w must be NULL)
+ *   LAYER: y = ((h - mean) * (1/sqrt(var + eps))) * w + b
+ * w, b: f32 [D] or NULL. x, res, h_out have dtype_in; y has dtype_out. h_out (the updated residual
+ * stream) is written only when res is given and h_out is not NULL; the norm reads the unrounded f32 sum.
+ * Replaces: RowOp RmsNorm/L2Norm/LayerNorm (src/Sharplight.Cpu/RowOp.cs:63-113) and the Vulkan lowerer's
+ * norm kernels, including the Add+RmsNorm unit of FoldNormTails
+ * (src/Sharplight.Shaders/Lowering/GraphLowerer.Fusion.cs:215-238, GraphLowerer.Elementwise.cs:110-117,
+ * GraphLowerer.Transformer.cs:9-34, Kernels/norm.slang:20-47, Kernels/rows.slang:41-138).
+ * dtype_in/dtype_out: F32 or BF16 (any combination).
+ */
+SLHIP_API int slhip_rownorm(int kind, int dtype_in, int dtype_out, const void* x, const void* res, const float* w,
+                            const float* b, void* y, void* h_out, int64_t rows, int64_t D, int64_t x_stride,
+                            int64_t res_stride, int64_t y_stride, int64_t h_stride, float eps, slhip_stream stream);
+
+/*
+ * Gated activation out = act(gate) * up over [rows, cols] (IMlpActivation.ActivateGated,
+ * src/Sharplight.Core/Architectures/IMlpActivation.cs:12; CPU: UnaryOp then BinaryOp Mul,
+ * src/Sharplight.Cpu/ScalarMath.cs:552-641, BinaryOp.cs:8-103; Vulkan: the fused[Silu,Mul]
+ * elementwise unit, GraphLowerer.Fusion.cs:89-142).
+ *   SILU:      g / (1 + exp(-g))
+ *   GELU_TANH: g / (1 + exp(-u)), u = 2*0.7978845608*(g + 0.044715*g^3)
+ *   GELU_ERF:  0.5*g*(1 + erf(g/sqrt(2)))
+ * Row strides let gate and up be the two halves of one merged [rows, 2*cols] projection.
+ * dtype_in/dtype_out: F32 or BF16.
+ */
+SLHIP_API int slhip_gated_act(int act, int dtype_in, int dtype_out, const void* gate, const void* up, void* out,
+                              int64_t rows, int64_t cols, int64_t gate_stride, int64_t up_stride, int64_t out_stride,
+                              slhip_stream stream);
+
+/* One tensor of a rope launch: x and y are [T, heads, D] with the given token/head strides
+ * (innermost stride 1). norm_w: f32 [D] per-head RMSNorm weight, used when cfg->norm is set. */
+typedef struct slhip_rope_tensor {
+    const void* x;
+    void* y;
+    const float* norm_w;
+    int64_t heads;
+    int64_t x_stride_t, x_stride_h;
+    int64_t y_stride_t, y_stride_h;
+} slhip_rope_tensor;
+
+typedef struct slhip_rope_cfg {
+    int32_t dims;      /* rotated dims (even, <= D); 0 means D. Dims past it are copied */
+    int32_t neox;      /* 1: pairs (i, i + dims/2); 0: "normal"/gptj pairs (2i, 2i+1) */
+    float base;        /* theta base */
+    float freq_scale;  /* multiplies every inverse frequency */
+    float attn_factor; /* multiplies cos and sin */
+    int32_t norm;      /* 1: per-head RMSNorm (norm_w, eps) before the rotation */
+    float eps;
+    int32_t reserved;
+} slhip_rope_cfg;
+
+/*
+ * Rotary embedding of up to 4 tensors that share positions (q and k of one layer in one launch), with
+ * the per-head q/k RMSNorm of Qwen3-style blocks fused in front when cfg->norm is set:
+ *   inv_i = base^(-2i/dims) * freq_scale (f64); theta = pos[t] * inv_i (/ ff[i]) (f64);
+ *   c = (float)cos(theta) * attn_factor, s = (float)sin(theta) * attn_factor;
+ *   y0 = x0*c - x1*s, y1 = x0*s + x1*c.
+ * pos: int32 [T]; ff: f32 [dims/2] frequency divisors or NULL. dtype_in/dtype_out: F32 or BF16.
+ * Replaces: RopeOp (src/Sharplight.Cpu/RopeOp.cs:28-183) after RowOp RmsNorm, and the Vulkan rope kernels
+ * with the absorbed norm (GraphLowerer.Fusion.cs:618-630, GraphLowerer.Transformer.cs:40, Kernels/rope.slang:150-195)
+ * for the single-axis styles.
+ */
+SLHIP_API int slhip_rope(int dtype_in, int dtype_out, const slhip_rope_tensor* tensors, int n_tensors,
+                         const int32_t* pos, const float* ff, int64_t T, int64_t D, const slhip_rope_cfg* cfg,
+                         slhip_stream stream);
+
+/*
+ * Embedding gather y[i, :] = dequant(table[ids[i], :]) for i < N; table is the [V, row_bytes] image of a
+ * [V, D] tensor in `format`. dtype_out: F32 or BF16 (f32 values rounded to nearest even). An id outside
+ * [0, V) leaves its output row zero and raises SLHIP_ERR_INDEX at the next slhip_stream_sync.
+ * Replaces: GatherOp (src/Sharplight.Cpu/GatherOp.cs:22-75) with Quant.Dequantize
+ * (src/Sharplight.Cpu/Quant.cs:242-405), and the Vulkan gather (GraphLowerer.Transformer.cs:133-179,
+ * Kernels/data.slang:4-37).
+ */
+SLHIP_API int slhip_gather(int format, const void* table, int64_t V, int64_t D, const int32_t* ids, int64_t N,
+                           int dtype_out, void* y, int64_t y_stride, slhip_stream stream);
+
+/*
+ * Element type conversion y = cast(x) of n elements (F32, F16, BF16 in any direction); f32 -> bf16 rounds
+ * to nearest even with NaNs quieted (Simd.FloatToBFloat, src/Sharplight.Cpu/Simd.cs:530-540).
+ * Replaces the CPU provider's Cast of activations.
+ */
+SLHIP_API int slhip_convert(int dtype_in, int dtype_out, const void* x, void* y, int64_t n, slhip_stream stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SHARPLIGHT_HIP_H */

@@ -1,0 +1,264 @@
+"""CPU oracle for the fused layer ops -- TEST INFRASTRUCTURE ONLY.
+
+A numpy/ctypes face over ``liboracle.so`` (``sl_oracle.c``), the C restatement of the reference CPU
+provider's arithmetic (``src/Sharplight.Cpu``). Only ``tests/``, ``__graft_entry__.smoke()`` and
+``bench.py``'s ``cpu_baseline`` leg import this package; it is the checker, never the thing measured
+or shipped.
+
+The composite functions (``add_rmsnorm``, ``gated``, ``qk_norm_rope``, ``gather``) run the
+reference's *unfused* f32 decomposition -- the CPU provider executes ``Add`` then ``RmsNorm``,
+``Silu`` then ``Mul``, ``RmsNorm`` then ``Rope`` as separate ops -- and, for bf16 tensors, convert
+with the provider's own casts (``Simd.BFloatToFloat`` on the way in, ``Simd.FloatToBFloat`` on the
+way out, ``src/Sharplight.Cpu/Simd.cs:527-540``). bf16 arrays are carried as ``uint16``.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+
+F32, F16, BF16, Q8_0, Q4_0, Q4_1, Q5_0, Q5_1 = range(8)
+FORMATS = {"f32": F32, "f16": F16, "bf16": BF16, "q8_0": Q8_0, "q4_0": Q4_0, "q4_1": Q4_1, "q5_0": Q5_0,
+           "q5_1": Q5_1}
+ACTS = {"silu": 0, "gelu_tanh": 1, "gelu_erf": 2}
+
+_lib = None
+
+
+def build() -> str:
+    """Compile liboracle.so with the committed Makefile (gcc)."""
+    import subprocess
+    subprocess.run(["make", "-s", "-C", _HERE, "liboracle.so"], check=True)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        _lib = ctypes.CDLL(_LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_F = ctypes.c_float
+_I = ctypes.c_int
+
+
+def _declare(L):
+    sig = {
+        "orc_f32_to_bf16_n": (None, [_P, _P, _I64]),
+        "orc_bf16_to_f32_n": (None, [_P, _P, _I64]),
+        "orc_f16_to_f32_n": (None, [_P, _P, _I64]),
+        "orc_sumsq": (_F, [_P, _I64]),
+        "orc_sum": (_F, [_P, _I64]),
+        "orc_rmsnorm": (None, [_P, _P, _P, _I64, _I64, _F, _I]),
+        "orc_layernorm": (None, [_P, _P, _P, _P, _I64, _I64, _F]),
+        "orc_add": (None, [_P, _P, _P, _I64]),
+        "orc_mul": (None, [_P, _P, _P, _I64]),
+        "orc_unary": (None, [_I, _P, _P, _I64]),
+        "orc_erf": (ctypes.c_double, [ctypes.c_double]),
+        "orc_erf_rational": (_F, [_F]),
+        "orc_rope": (None, [_P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _F, _F, _F]),
+        "orc_row_bytes": (_I64, [_I, _I64]),
+        "orc_dequant": (_I, [_I, _P, _I64, _P]),
+        "orc_gather": (_I, [_I, _P, _I64, _I64, _P, _I64, _P, ctypes.POINTER(_I64)]),
+        "orc_set_threads": (None, [_I]),
+        "orc_get_threads": (_I, []),
+        "orc_rmsnorm_mt": (None, [_P, _P, _P, _I64, _I64, _F, _I]),
+        "orc_layernorm_mt": (None, [_P, _P, _P, _P, _I64, _I64, _F]),
+        "orc_add_mt": (None, [_P, _P, _P, _I64]),
+        "orc_mul_mt": (None, [_P, _P, _P, _I64]),
+        "orc_unary_mt": (None, [_I, _P, _P, _I64]),
+        "orc_rope_mt": (None, [_P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _F, _F, _F]),
+        "orc_gather_mt": (_I, [_I, _P, _I64, _I64, _P, _I64, _P, ctypes.POINTER(_I64)]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data
+
+
+def _c(a, dtype):
+    return None if a is None else np.ascontiguousarray(a, dtype=dtype)
+
+
+class OutOfRange(IndexError):
+    """The reference's GatherOp throws ArgumentOutOfRangeException (GatherOp.cs:60-63)."""
+
+
+# ---- casts ---------------------------------------------------------------------------------------
+
+def to_bf16(x):
+    x = _c(x, np.float32)
+    y = np.empty(x.shape, np.uint16)
+    lib().orc_f32_to_bf16_n(_p(x), _p(y), x.size)
+    return y
+
+
+def from_bf16(x):
+    x = _c(x, np.uint16)
+    y = np.empty(x.shape, np.float32)
+    lib().orc_bf16_to_f32_n(_p(x), _p(y), x.size)
+    return y
+
+
+def f16_bits_to_f32(x):
+    x = _c(x, np.uint16)
+    y = np.empty(x.shape, np.float32)
+    lib().orc_f16_to_f32_n(_p(x), _p(y), x.size)
+    return y
+
+
+def _as_f32(x, dtype):
+    return from_bf16(x) if dtype == "bf16" else _c(x, np.float32)
+
+
+def _out(y, dtype):
+    return to_bf16(y) if dtype == "bf16" else y
+
+
+# ---- primitives ----------------------------------------------------------------------------------
+
+def sumsq(x):
+    x = _c(x, np.float32)
+    return float(lib().orc_sumsq(_p(x), x.size))
+
+
+def rmsnorm(x, w=None, eps=1e-6, mode=0, threads=None):
+    """RowOp RmsNorm (mode 0) / L2Norm (mode 1) over the last axis, f32."""
+    x = _c(x, np.float32)
+    w = _c(w, np.float32)
+    n = x.shape[-1]
+    rows = x.size // n if n else 0
+    y = np.empty_like(x)
+    fn = lib().orc_rmsnorm_mt if threads else lib().orc_rmsnorm
+    fn(_p(x), _p(w), _p(y), rows, n, eps, mode)
+    return y
+
+
+def layernorm(x, w=None, b=None, eps=1e-5, threads=None):
+    x = _c(x, np.float32)
+    w = _c(w, np.float32)
+    b = _c(b, np.float32)
+    n = x.shape[-1]
+    rows = x.size // n if n else 0
+    y = np.empty_like(x)
+    fn = lib().orc_layernorm_mt if threads else lib().orc_layernorm
+    fn(_p(x), _p(w), _p(b), _p(y), rows, n, eps)
+    return y
+
+
+def add(a, b, threads=None):
+    a = _c(a, np.float32)
+    b = _c(b, np.float32)
+    y = np.empty_like(a)
+    (lib().orc_add_mt if threads else lib().orc_add)(_p(a), _p(b), _p(y), a.size)
+    return y
+
+
+def mul(a, b, threads=None):
+    a = _c(a, np.float32)
+    b = _c(b, np.float32)
+    y = np.empty_like(a)
+    (lib().orc_mul_mt if threads else lib().orc_mul)(_p(a), _p(b), _p(y), a.size)
+    return y
+
+
+def unary(act, x, threads=None):
+    x = _c(x, np.float32)
+    y = np.empty_like(x)
+    (lib().orc_unary_mt if threads else lib().orc_unary)(ACTS[act], _p(x), _p(y), x.size)
+    return y
+
+
+def rope(x, pos, dims=None, neox=True, base=10000.0, freq_scale=1.0, attn_factor=1.0, ff=None, threads=None):
+    """RopeOp over x [T, H, D] (f32) with int32 positions [T]."""
+    x = _c(x, np.float32)
+    T, H, D = x.shape
+    pos = _c(pos, np.int32).reshape(-1)
+    assert pos.size == T
+    ff = _c(ff, np.float32)
+    dims = D if not dims else dims
+    y = np.empty_like(x)
+    fn = lib().orc_rope_mt if threads else lib().orc_rope
+    fn(_p(x), _p(pos), _p(ff), _p(y), T, H, D, dims, int(bool(neox)), base, freq_scale, attn_factor)
+    return y
+
+
+def row_bytes(fmt, d):
+    return int(lib().orc_row_bytes(FORMATS[fmt], d))
+
+
+def dequant(fmt, raw, count):
+    raw = _c(raw, np.uint8)
+    y = np.empty(count, np.float32)
+    if lib().orc_dequant(FORMATS[fmt], _p(raw), count, _p(y)):
+        raise ValueError(f"cannot dequantize {count} values of {fmt}")
+    return y
+
+
+def gather(fmt, table, V, D, ids, threads=None):
+    """GatherOp with f32 output: table is the raw [V, row_bytes] byte image."""
+    table = _c(table, np.uint8)
+    ids = _c(ids, np.int32).reshape(-1)
+    y = np.empty((ids.size, D), np.float32)
+    bad = _I64(0)
+    fn = lib().orc_gather_mt if threads else lib().orc_gather
+    st = fn(FORMATS[fmt], _p(table), V, D, _p(ids), ids.size, _p(y), ctypes.byref(bad))
+    if st == -1:
+        raise OutOfRange(f"Gather index {bad.value} out of range [0,{V}).")
+    if st:
+        raise ValueError(f"gather: unsupported format/shape {fmt} D={D}")
+    return y
+
+
+def set_threads(n):
+    lib().orc_set_threads(int(n))
+
+
+# ---- composites: the reference's unfused decomposition ------------------------------------------
+
+def add_rmsnorm(x, res, w, eps, dtype="f32", mode=0):
+    """Add then RmsNorm (CPU provider order); returns (y, h) in ``dtype``. The norm reads the f32 sum."""
+    h = add(_as_f32(x, dtype), _as_f32(res, dtype))
+    y = rmsnorm(h, w, eps, mode)
+    return _out(y, dtype), _out(h, dtype)
+
+
+def norm(x, w, eps, dtype="f32", mode=0):
+    return _out(rmsnorm(_as_f32(x, dtype), w, eps, mode), dtype)
+
+
+def add_layernorm(x, res, w, b, eps, dtype="f32"):
+    h = add(_as_f32(x, dtype), _as_f32(res, dtype)) if res is not None else _as_f32(x, dtype)
+    y = layernorm(h, w, b, eps)
+    return _out(y, dtype), (_out(h, dtype) if res is not None else None)
+
+
+def gated(act, gate, up, dtype="f32"):
+    """Mul(act(gate), up) as two ops (IMlpActivation.cs:12)."""
+    return _out(mul(unary(act, _as_f32(gate, dtype)), _as_f32(up, dtype)), dtype)
+
+
+def qk_norm_rope(x, pos, w=None, eps=1e-6, dtype="f32", **rope_kw):
+    """RmsNorm over each head row (if w is given or norm requested) then Rope, x [T, H, D]."""
+    xf = _as_f32(x, dtype)
+    if w is not None:
+        xf = rmsnorm(xf, w, eps)
+    return _out(rope(xf, pos, **rope_kw), dtype)
+
+
+def gather_as(fmt, table, V, D, ids, dtype="f32"):
+    return _out(gather(fmt, table, V, D, ids), dtype)

@@ -1,0 +1,676 @@
+/*
+ * CPU oracle for the Sharplight fused layer ops -- TEST INFRASTRUCTURE ONLY (see sl_oracle.h).
+ *
+ * Every function restates the arithmetic of the reference's CPU provider and cites the
+ * reference file:line it follows (paths relative to the reference repository root). The
+ * restatement keeps the reference's operation order where it is visible in the source
+ * (accumulator layout of the SIMD reductions, which products are fused, f64 where the
+ * reference uses f64); the .NET runtime's own Exp/Cos/Sin polynomials are not in the
+ * reference's sources, so libm stands in for them (agreement is to tolerance, not bits).
+ *
+ * Built with -ffp-contract=off so that only the fmaf() calls written below are fused.
+ */
+#include "sl_oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------------------------------ */
+/* conversions                                                                                */
+/* ------------------------------------------------------------------------------------------ */
+
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+/* Simd.FloatToBFloat (src/Sharplight.Cpu/Simd.cs:530-540): NaN keeps its top half with the quiet
+ * bit set; everything else rounds to nearest even by adding 0x7FFF + lsb. */
+uint16_t orc_f32_to_bf16(float f)
+{
+    uint32_t b = f2u(f);
+    if ((b & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((b >> 16) | 0x40u);
+    b += 0x7FFFu + ((b >> 16) & 1u);
+    return (uint16_t)(b >> 16);
+}
+
+/* Simd.BFloatToFloat (Simd.cs:527-528). */
+float orc_bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
+
+/* Quant.H (src/Sharplight.Cpu/Quant.cs:371-381) for normal codes; zero, subnormal, inf and NaN
+ * go through the IEEE half->single conversion (Simd.HalfToFloat, Simd.cs:518), restated here
+ * from the binary16 definition: a subnormal m*2^-24 is renormalised, inf/NaN keep the payload. */
+float orc_f16_to_f32(uint16_t hh)
+{
+    uint32_t h = hh;
+    uint32_t sign = (h & 0x8000u) << 16;
+    uint32_t e = h & 0x7C00u;
+    uint32_t m = h & 0x03FFu;
+    if (e != 0 && e != 0x7C00u) return u2f(sign | (((h & 0x7FFFu) << 13) + 0x38000000u));
+    if (e == 0x7C00u) return u2f(sign | 0x7F800000u | (m << 13));
+    if (m == 0) return u2f(sign);
+    /* subnormal: value = m * 2^-24, exact in f32 */
+    int shift = 0;
+    while ((m & 0x0400u) == 0) { m <<= 1; shift++; }
+    m &= 0x03FFu;
+    uint32_t exp = (uint32_t)(127 - 15 - shift + 1);
+    return u2f(sign | (exp << 23) | (m << 13));
+}
+
+void orc_f32_to_bf16_n(const float* x, uint16_t* y, int64_t n)
+{
+    for (int64_t i = 0; i < n; i++) y[i] = orc_f32_to_bf16(x[i]);
+}
+
+void orc_bf16_to_f32_n(const uint16_t* x, float* y, int64_t n)
+{
+    for (int64_t i = 0; i < n; i++) y[i] = orc_bf16_to_f32(x[i]);
+}
+
+void orc_f16_to_f32_n(const uint16_t* x, float* y, int64_t n)
+{
+    for (int64_t i = 0; i < n; i++) y[i] = orc_f16_to_f32(x[i]);
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* reductions                                                                                 */
+/* ------------------------------------------------------------------------------------------ */
+
+/* Horizontal sum of a vector register, pairwise halving (the lane order of Vector512/256.Sum is
+ * the runtime's; pairwise is what its x86 lowering does). */
+static float hsum(const float* v, int lanes)
+{
+    float t[16];
+    for (int i = 0; i < lanes; i++) t[i] = v[i];
+    for (int w = lanes / 2; w >= 1; w /= 2)
+        for (int i = 0; i < w; i++) t[i] = t[i] + t[i + w];
+    return t[0];
+}
+
+/* Simd.SumSq, AVX-512 tier (src/Sharplight.Cpu/Simd.cs:274-317): two 16-lane FMA accumulators
+ * over 32 elements per step, one more 16-lane step, Sum(s0+s1), then a scalar tail. */
+float orc_sumsq(const float* a, int64_t n)
+{
+    int64_t i = 0;
+    float s0[16] = {0}, s1[16] = {0};
+    for (; i + 32 <= n; i += 32)
+        for (int j = 0; j < 16; j++) {
+            s0[j] = fmaf(a[i + j], a[i + j], s0[j]);
+            s1[j] = fmaf(a[i + 16 + j], a[i + 16 + j], s1[j]);
+        }
+    for (; i + 16 <= n; i += 16)
+        for (int j = 0; j < 16; j++) s0[j] = fmaf(a[i + j], a[i + j], s0[j]);
+    float s[16];
+    for (int j = 0; j < 16; j++) s[j] = s0[j] + s1[j];
+    float sum = hsum(s, 16);
+    for (; i < n; i++) sum += a[i] * a[i];
+    return sum;
+}
+
+/* Simd.Sum, AVX2 tier (Simd.cs:319-340): one 8-lane accumulator, Sum, scalar tail. */
+float orc_sum(const float* a, int64_t n)
+{
+    int64_t i = 0;
+    float s[8] = {0};
+    for (; i + 8 <= n; i += 8)
+        for (int j = 0; j < 8; j++) s[j] += a[i + j];
+    float sum = hsum(s, 8);
+    for (; i < n; i++) sum += a[i];
+    return sum;
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* row ops                                                                                    */
+/* ------------------------------------------------------------------------------------------ */
+
+/* RowOp.Body, cases RmsNorm and L2Norm (src/Sharplight.Cpu/RowOp.cs:63-84) with Simd.ScaleMul /
+ * Simd.Scale (Simd.cs:441-480): scale = 1/sqrt(SumSq/n + eps) (L2: SumSq + eps), y = x*scale*w. */
+static void rmsnorm_rows(const float* x, const float* w, float* y, int64_t r0, int64_t r1, int64_t n, float eps,
+                         int mode)
+{
+    for (int64_t r = r0; r < r1; r++) {
+        const float* xr = x + r * n;
+        float* yr = y + r * n;
+        float ss = orc_sumsq(xr, n);
+        float scale = mode == 0 ? 1.0f / sqrtf(ss / (float)n + eps) : 1.0f / sqrtf(ss + eps);
+        if (w) {
+            for (int64_t i = 0; i < n; i++) yr[i] = xr[i] * scale * w[i];
+        } else {
+            for (int64_t i = 0; i < n; i++) yr[i] = xr[i] * scale;
+        }
+    }
+}
+
+void orc_rmsnorm(const float* x, const float* w, float* y, int64_t rows, int64_t n, float eps, int mode)
+{
+    rmsnorm_rows(x, w, y, 0, rows, n, eps, mode);
+}
+
+/* RowOp.Body, case LayerNorm (RowOp.cs:85-113): mean = Sum(x)/n in f32, variance accumulated in
+ * f64 over the f32 differences, inv = 1/sqrt((float)(v/n) + eps), y = ((x-mean)*inv)*w + b. */
+static void layernorm_rows(const float* x, const float* w, const float* b, float* y, int64_t r0, int64_t r1, int64_t n,
+                           float eps)
+{
+    for (int64_t r = r0; r < r1; r++) {
+        const float* xr = x + r * n;
+        float* yr = y + r * n;
+        float mean = orc_sum(xr, n) / (float)n;
+        double v = 0;
+        for (int64_t i = 0; i < n; i++) {
+            double d = (double)(xr[i] - mean);
+            v += d * d;
+        }
+        float inv = 1.0f / sqrtf((float)(v / (double)n) + eps);
+        for (int64_t i = 0; i < n; i++) {
+            float o = (xr[i] - mean) * inv;
+            if (w) o *= w[i];
+            if (b) o += b[i];
+            yr[i] = o;
+        }
+    }
+}
+
+void orc_layernorm(const float* x, const float* w, const float* b, float* y, int64_t rows, int64_t n, float eps)
+{
+    layernorm_rows(x, w, b, y, 0, rows, n, eps);
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* elementwise                                                                                */
+/* ------------------------------------------------------------------------------------------ */
+
+/* BinaryOp Add / Mul on dense equal-shape operands (src/Sharplight.Cpu/BinaryOp.cs:60-103). */
+void orc_add(const float* a, const float* b, float* y, int64_t n)
+{
+    for (int64_t i = 0; i < n; i++) y[i] = a[i] + b[i];
+}
+
+void orc_mul(const float* a, const float* b, float* y, int64_t n)
+{
+    for (int64_t i = 0; i < n; i++) y[i] = a[i] * b[i];
+}
+
+/* ScalarMath.Erf (src/Sharplight.Cpu/ScalarMath.cs:11-49): f64 series below 2.5, continued
+ * fraction for erfc up to 6, 1 beyond. */
+double orc_erf(double x)
+{
+    double ax = fabs(x), r;
+    if (ax < 2.5) {
+        double x2 = ax * ax, term = ax, sum = ax;
+        for (int k = 1; k < 200; k++) {
+            term *= 2 * x2 / (2 * k + 1);
+            sum += term;
+            if (term < sum * 1e-17) break;
+        }
+        r = 1.1283791670955126 * exp(-x2) * sum;
+    } else if (ax > 6) {
+        r = 1.0;
+    } else {
+        double f = ax;
+        for (int k = 80; k >= 1; k--) f = ax + 0.5 * k / f;
+        r = 1.0 - exp(-ax * ax) / (1.7724538509055159 * f);
+    }
+    return x < 0 ? -r : r;
+}
+
+/* ScalarMath.ErfD / ErfV (ScalarMath.cs:51-98): the Eigen/XLA rational erf evaluated in f64 on
+ * the argument clamped to +-3.8325, narrowed to f32. The coefficients are the published ones of
+ * that approximation (Eigen's generic_fast_erf_float). */
+float orc_erf_rational(float xf)
+{
+    const double clampv = (double)3.832506856900711f;
+    const double A1 = -1.60960333262415e-02, A3 = -2.95459980854025e-03, A5 = -7.34990630326855e-04,
+                 A7 = -5.69250639462346e-05, A9 = -2.10102402082508e-06, A11 = 2.77068142495902e-08,
+                 A13 = -2.72614225801306e-10, B0 = -1.42647390514189e-02, B2 = -7.37332916720468e-03,
+                 B4 = -1.68282697438203e-03, B6 = -2.13374055278905e-04, B8 = -1.45660718464996e-05;
+    double x = (double)xf;
+    if (x < -clampv) x = -clampv;
+    if (x > clampv) x = clampv;
+    double x2 = x * x;
+    double p = A13;
+    p = fma(p, x2, A11);
+    p = fma(p, x2, A9);
+    p = fma(p, x2, A7);
+    p = fma(p, x2, A5);
+    p = fma(p, x2, A3);
+    p = fma(p, x2, A1);
+    p *= x;
+    double q = B8;
+    q = fma(q, x2, B6);
+    q = fma(q, x2, B4);
+    q = fma(q, x2, B2);
+    q = fma(q, x2, B0);
+    return (float)(p / q);
+}
+
+/* ScalarMath.Unary (ScalarMath.cs:552-641) over one contiguous range, AVX2 tier: the vector form
+ * on whole groups of 8, the scalar form on the tail.
+ *   Silu     (552-584): v / (1 + exp(-v)) in both forms.
+ *   GeluTanh (593-623): vector v / (1 + exp(-u)), u = 2*0.79788456*fma(0.044715*v, v*v, v);
+ *                       tail 0.5*v*(1 + tanh(0.79788456*(v + 0.044715*v^3))).
+ *   Gelu     (625-641): vector 0.5*v*(1 + erf_rational(v/sqrt2)); tail in f64 with the series erf. */
+static void unary_range(int act, const float* x, float* y, int64_t n)
+{
+    int64_t vec = n - n % 8;
+    int64_t i = 0;
+    switch (act) {
+    case 0:
+        for (; i < n; i++) y[i] = x[i] / (1.0f + expf(-x[i]));
+        break;
+    case 1: {
+        const float c0 = 0.7978845608028654f * 2.0f, c1 = 0.044715f;
+        for (; i < vec; i++) {
+            float v = x[i];
+            float u = c0 * fmaf(c1 * v, v * v, v);
+            y[i] = v / (1.0f + expf(-u));
+        }
+        for (; i < n; i++) {
+            float v = x[i];
+            y[i] = 0.5f * v * (1.0f + tanhf(0.7978845608028654f * (v + 0.044715f * v * v * v)));
+        }
+        break;
+    }
+    case 2:
+        for (; i < vec; i++) {
+            float v = x[i];
+            y[i] = 0.5f * v * (1.0f + orc_erf_rational(v * 0.7071067811865476f));
+        }
+        for (; i < n; i++) {
+            double v = x[i];
+            y[i] = (float)(0.5 * v * (1.0 + orc_erf(v * 0.7071067811865476)));
+        }
+        break;
+    default:
+        break;
+    }
+}
+
+void orc_unary(int act, const float* x, float* y, int64_t n) { unary_range(act, x, y, n); }
+
+/* ------------------------------------------------------------------------------------------ */
+/* rope                                                                                       */
+/* ------------------------------------------------------------------------------------------ */
+
+/* RopeOp (src/Sharplight.Cpu/RopeOp.cs): inverse frequencies in f64 (ctor, :47-52), per token
+ * theta = pos * invFreq (/ ff[i]) in f64, cos/sin narrowed to f32 then times attn_factor
+ * (:133-150); neox pairs (i, i+half), normal pairs (2i, 2i+1) (:151-176); elements from dims to
+ * D are copied (:177-180). Single position axis. */
+static void rope_tokens(const float* x, const int32_t* pos, const float* ff, float* y, int64_t t0, int64_t t1,
+                        int64_t H, int64_t D, int dims, int neox, float base, float freq_scale, float attn_factor)
+{
+    int half = dims / 2;
+    double* inv = (double*)malloc(sizeof(double) * (size_t)(half > 0 ? half : 1));
+    float* cs = (float*)malloc(sizeof(float) * (size_t)(half > 0 ? half : 1) * 2);
+    for (int i = 0; i < half; i++) inv[i] = pow((double)base, -2.0 * i / dims) * (double)freq_scale;
+    for (int64_t t = t0; t < t1; t++) {
+        double p = (double)pos[t];
+        for (int i = 0; i < half; i++) {
+            double theta = p * inv[i];
+            if (ff) theta /= (double)ff[i];
+            cs[2 * i] = (float)cos(theta) * attn_factor;
+            cs[2 * i + 1] = (float)sin(theta) * attn_factor;
+        }
+        for (int64_t h = 0; h < H; h++) {
+            const float* xr = x + (t * H + h) * D;
+            float* yr = y + (t * H + h) * D;
+            for (int i = 0; i < half; i++) {
+                int i0 = neox ? i : 2 * i;
+                int i1 = neox ? i + half : 2 * i + 1;
+                float x0 = xr[i0], x1 = xr[i1];
+                float c = cs[2 * i], s = cs[2 * i + 1];
+                yr[i0] = x0 * c - x1 * s;
+                yr[i1] = x0 * s + x1 * c;
+            }
+            for (int64_t i = dims; i < D; i++) yr[i] = xr[i];
+        }
+    }
+    free(inv);
+    free(cs);
+}
+
+void orc_rope(const float* x, const int32_t* pos, const float* ff, float* y, int64_t T, int64_t H, int64_t D, int dims,
+              int neox, float base, float freq_scale, float attn_factor)
+{
+    rope_tokens(x, pos, ff, y, 0, T, H, D, dims, neox, base, freq_scale, attn_factor);
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* dequant / gather                                                                           */
+/* ------------------------------------------------------------------------------------------ */
+
+/* Quant.BlockSize / BlockBytes (src/Sharplight.Cpu/Quant.cs:181-216) for the formats here. */
+static int block_size(int fmt) { return fmt >= ORC_Q8_0 ? 32 : 1; }
+static int block_bytes(int fmt)
+{
+    switch (fmt) {
+    case ORC_F32: return 4;
+    case ORC_F16: case ORC_BF16: return 2;
+    case ORC_Q8_0: return 34;
+    case ORC_Q4_0: return 18;
+    case ORC_Q4_1: return 20;
+    case ORC_Q5_0: return 22;
+    case ORC_Q5_1: return 24;
+    default: return -1;
+    }
+}
+
+int64_t orc_row_bytes(int fmt, int64_t d)
+{
+    int bb = block_bytes(fmt);
+    if (bb < 0 || d % block_size(fmt) != 0) return -1;
+    return d / block_size(fmt) * bb;
+}
+
+static inline float rd_h(const uint8_t* p) { return orc_f16_to_f32((uint16_t)(p[0] | (p[1] << 8))); }
+
+/* Quant.Dequantize (Quant.cs:242-368) with the block decoders Q4_0/Q8_0 (:384-405),
+ * Q4_1/Q5_0/Q5_1 (:449-500) and Simd.StoreI8x16/StoreU8x16 (Simd.cs:699-753): value =
+ * fma(q, d, offset), offset 0 (Q8_0), -8d (Q4_0), -16d (Q5_0), m (Q4_1, Q5_1). */
+int orc_dequant(int fmt, const uint8_t* p, int64_t count, float* dst)
+{
+    switch (fmt) {
+    case ORC_F32: memcpy(dst, p, (size_t)count * 4); return 0;
+    case ORC_F16:
+        for (int64_t i = 0; i < count; i++) dst[i] = rd_h(p + 2 * i);
+        return 0;
+    case ORC_BF16:
+        for (int64_t i = 0; i < count; i++) dst[i] = orc_bf16_to_f32((uint16_t)(p[2 * i] | (p[2 * i + 1] << 8)));
+        return 0;
+    default: break;
+    }
+    if (count % 32) return -1;
+    int64_t nb = count / 32;
+    for (int64_t b = 0; b < nb; b++, dst += 32) {
+        switch (fmt) {
+        case ORC_Q8_0: {
+            float d = rd_h(p);
+            for (int j = 0; j < 32; j++) dst[j] = fmaf((float)(int8_t)p[2 + j], d, 0.0f);
+            p += 34;
+            break;
+        }
+        case ORC_Q4_0: {
+            float d = rd_h(p), o = -8.0f * d;
+            for (int j = 0; j < 16; j++) {
+                dst[j] = fmaf((float)(p[2 + j] & 15), d, o);
+                dst[j + 16] = fmaf((float)(p[2 + j] >> 4), d, o);
+            }
+            p += 18;
+            break;
+        }
+        case ORC_Q4_1: {
+            float d = rd_h(p), m = rd_h(p + 2);
+            for (int j = 0; j < 16; j++) {
+                dst[j] = fmaf((float)(p[4 + j] & 15), d, m);
+                dst[j + 16] = fmaf((float)(p[4 + j] >> 4), d, m);
+            }
+            p += 20;
+            break;
+        }
+        case ORC_Q5_0: {
+            float d = rd_h(p), o = -16.0f * d;
+            uint32_t qh = (uint32_t)p[2] | ((uint32_t)p[3] << 8) | ((uint32_t)p[4] << 16) | ((uint32_t)p[5] << 24);
+            for (int j = 0; j < 16; j++) {
+                uint32_t lo = (p[6 + j] & 15u) | (((qh >> j) & 1u) << 4);
+                uint32_t hi = (p[6 + j] >> 4) | (((qh >> (j + 16)) & 1u) << 4);
+                dst[j] = fmaf((float)lo, d, o);
+                dst[j + 16] = fmaf((float)hi, d, o);
+            }
+            p += 22;
+            break;
+        }
+        case ORC_Q5_1: {
+            float d = rd_h(p), m = rd_h(p + 2);
+            uint32_t qh = (uint32_t)p[4] | ((uint32_t)p[5] << 8) | ((uint32_t)p[6] << 16) | ((uint32_t)p[7] << 24);
+            for (int j = 0; j < 16; j++) {
+                uint32_t lo = (p[8 + j] & 15u) | (((qh >> j) & 1u) << 4);
+                uint32_t hi = (p[8 + j] >> 4) | (((qh >> (j + 16)) & 1u) << 4);
+                dst[j] = fmaf((float)lo, d, m);
+                dst[j + 16] = fmaf((float)hi, d, m);
+            }
+            p += 24;
+            break;
+        }
+        default: return -1;
+        }
+    }
+    return 0;
+}
+
+/* GatherOp.Body (src/Sharplight.Cpu/GatherOp.cs:53-75): bounds check, then dequantize the row. */
+static int gather_range(int fmt, const uint8_t* table, int64_t V, int64_t D, const int32_t* ids, int64_t i0, int64_t i1,
+                        float* y, int64_t* bad)
+{
+    int64_t rb = orc_row_bytes(fmt, D);
+    if (rb < 0) return -2;
+    for (int64_t i = i0; i < i1; i++) {
+        int64_t id = ids[i];
+        if ((uint64_t)id >= (uint64_t)V) {
+            if (bad) *bad = id;
+            return -1;
+        }
+        if (orc_dequant(fmt, table + id * rb, D, y + i * D)) return -2;
+    }
+    return 0;
+}
+
+int orc_gather(int fmt, const uint8_t* table, int64_t V, int64_t D, const int32_t* ids, int64_t N, float* y,
+               int64_t* bad_index)
+{
+    return gather_range(fmt, table, V, D, ids, 0, N, y, bad_index);
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* threading (CpuParallel.cs:34-78)                                                           */
+/* ------------------------------------------------------------------------------------------ */
+
+static int g_threads = 1;
+
+void orc_set_threads(int threads) { g_threads = threads < 1 ? 1 : threads; }
+int orc_get_threads(void) { return g_threads; }
+
+/* CpuParallel.Chunks: 1 when total <= minChunk, else min(threads*4, total/minChunk). */
+static int64_t chunks_for(int64_t total, int64_t min_chunk)
+{
+    if (total <= min_chunk) return 1;
+    int64_t c = (int64_t)g_threads * 4;
+    if (total / min_chunk < c) c = total / min_chunk;
+    return c < 1 ? 1 : c;
+}
+
+typedef void (*chunk_fn)(void* ctx, int64_t c);
+
+typedef struct {
+    chunk_fn fn;
+    void* ctx;
+    int64_t n;
+    int64_t next; /* guarded by mu */
+    pthread_mutex_t mu;
+} pfor_t;
+
+static void* pfor_worker(void* arg)
+{
+    pfor_t* p = (pfor_t*)arg;
+    for (;;) {
+        pthread_mutex_lock(&p->mu);
+        int64_t c = p->next++;
+        pthread_mutex_unlock(&p->mu);
+        if (c >= p->n) break;
+        p->fn(p->ctx, c);
+    }
+    return NULL;
+}
+
+/* CpuParallel.For: chunk indices 0..n-1 handed to min(n, threads) workers. */
+static void parallel_for(int64_t n, chunk_fn fn, void* ctx)
+{
+    if (n <= 0) return;
+    int workers = g_threads < n ? g_threads : (int)n;
+    if (workers <= 1) {
+        for (int64_t c = 0; c < n; c++) fn(ctx, c);
+        return;
+    }
+    pfor_t p;
+    p.fn = fn;
+    p.ctx = ctx;
+    p.n = n;
+    p.next = 0;
+    pthread_mutex_init(&p.mu, NULL);
+    pthread_t* th = (pthread_t*)malloc(sizeof(pthread_t) * (size_t)workers);
+    for (int i = 1; i < workers; i++) pthread_create(&th[i], NULL, pfor_worker, &p);
+    pfor_worker(&p);
+    for (int i = 1; i < workers; i++) pthread_join(th[i], NULL);
+    free(th);
+    pthread_mutex_destroy(&p.mu);
+}
+
+typedef struct {
+    const float *x, *w, *b;
+    float* y;
+    int64_t rows, n, per;
+    float eps;
+    int mode;
+} row_ctx;
+
+static void rms_chunk(void* v, int64_t c)
+{
+    row_ctx* r = (row_ctx*)v;
+    int64_t s = c * r->per, e = s + r->per < r->rows ? s + r->per : r->rows;
+    rmsnorm_rows(r->x, r->w, r->y, s, e, r->n, r->eps, r->mode);
+}
+
+static void ln_chunk(void* v, int64_t c)
+{
+    row_ctx* r = (row_ctx*)v;
+    int64_t s = c * r->per, e = s + r->per < r->rows ? s + r->per : r->rows;
+    layernorm_rows(r->x, r->w, r->b, r->y, s, e, r->n, r->eps);
+}
+
+/* RowOp.Run (RowOp.cs:37-49): chunks = min(rows, Chunks(rows*cols, 16384)). */
+void orc_rmsnorm_mt(const float* x, const float* w, float* y, int64_t rows, int64_t n, float eps, int mode)
+{
+    if (rows == 0 || n == 0) return;
+    int64_t ch = chunks_for(rows * n, 16384);
+    if (ch > rows) ch = rows;
+    row_ctx r = {x, w, NULL, y, rows, n, (rows + ch - 1) / ch, eps, mode};
+    parallel_for(ch, rms_chunk, &r);
+}
+
+void orc_layernorm_mt(const float* x, const float* w, const float* b, float* y, int64_t rows, int64_t n, float eps)
+{
+    if (rows == 0 || n == 0) return;
+    int64_t ch = chunks_for(rows * n, 16384);
+    if (ch > rows) ch = rows;
+    row_ctx r = {x, w, b, y, rows, n, (rows + ch - 1) / ch, eps, 0};
+    parallel_for(ch, ln_chunk, &r);
+}
+
+typedef struct {
+    const float *a, *b;
+    float* y;
+    int64_t n, per;
+    int kind; /* 0 add, 1 mul, 2+ unary act (kind-2) */
+} ew_ctx;
+
+static void ew_chunk(void* v, int64_t c)
+{
+    ew_ctx* e = (ew_ctx*)v;
+    int64_t s = c * e->per, t = s + e->per < e->n ? s + e->per : e->n;
+    if (s >= t) return;
+    if (e->kind == 0) orc_add(e->a + s, e->b + s, e->y + s, t - s);
+    else if (e->kind == 1) orc_mul(e->a + s, e->b + s, e->y + s, t - s);
+    else unary_range(e->kind - 2, e->a + s, e->y + s, t - s);
+}
+
+/* UnaryOp.Run / BinaryOp.Run on dense operands (UnaryOp.cs:30-48, BinaryOp.cs:60-100): flat
+ * chunks of at least 32768 elements. */
+static void ew_run(int kind, const float* a, const float* b, float* y, int64_t n)
+{
+    if (n == 0) return;
+    int64_t ch = chunks_for(n, 32768);
+    ew_ctx e = {a, b, y, n, (n + ch - 1) / ch, kind};
+    parallel_for(ch, ew_chunk, &e);
+}
+
+void orc_add_mt(const float* a, const float* b, float* y, int64_t n) { ew_run(0, a, b, y, n); }
+void orc_mul_mt(const float* a, const float* b, float* y, int64_t n) { ew_run(1, a, b, y, n); }
+void orc_unary_mt(int act, const float* x, float* y, int64_t n) { ew_run(2 + act, x, NULL, y, n); }
+
+typedef struct {
+    const float* x;
+    const int32_t* pos;
+    const float* ff;
+    float* y;
+    int64_t T, H, D, per;
+    int dims, neox;
+    float base, fs, af;
+} rope_ctx;
+
+static void rope_chunk(void* v, int64_t c)
+{
+    rope_ctx* r = (rope_ctx*)v;
+    int64_t s = c * r->per, e = s + r->per < r->T ? s + r->per : r->T;
+    if (s < e) rope_tokens(r->x, r->pos, r->ff, r->y, s, e, r->H, r->D, r->dims, r->neox, r->base, r->fs, r->af);
+}
+
+/* RopeOp.Run (RopeOp.cs:108-119): chunks = min(T, Chunks(T*H*D, 16384)). */
+void orc_rope_mt(const float* x, const int32_t* pos, const float* ff, float* y, int64_t T, int64_t H, int64_t D, int dims,
+                 int neox, float base, float freq_scale, float attn_factor)
+{
+    if (T == 0) return;
+    int64_t ch = chunks_for(T * H * D, 16384);
+    if (ch > T) ch = T;
+    rope_ctx r = {x, pos, ff, y, T, H, D, (T + ch - 1) / ch, dims, neox, base, freq_scale, attn_factor};
+    parallel_for(ch, rope_chunk, &r);
+}
+
+typedef struct {
+    int fmt;
+    const uint8_t* table;
+    int64_t V, D, N, per;
+    const int32_t* ids;
+    float* y;
+    int status;
+    int64_t bad;
+    pthread_mutex_t mu;
+} gather_ctx;
+
+static void gather_chunk(void* v, int64_t c)
+{
+    gather_ctx* g = (gather_ctx*)v;
+    int64_t s = c * g->per, e = s + g->per < g->N ? s + g->per : g->N;
+    int64_t bad = 0;
+    int st = s < e ? gather_range(g->fmt, g->table, g->V, g->D, g->ids, s, e, g->y, &bad) : 0;
+    if (st) {
+        pthread_mutex_lock(&g->mu);
+        if (!g->status) {
+            g->status = st;
+            g->bad = bad;
+        }
+        pthread_mutex_unlock(&g->mu);
+    }
+}
+
+/* GatherOp.Run (GatherOp.cs:40-51): chunks = min(N, Chunks(N*D, 8192)). */
+int orc_gather_mt(int fmt, const uint8_t* table, int64_t V, int64_t D, const int32_t* ids, int64_t N, float* y,
+                  int64_t* bad_index)
+{
+    if (N == 0) return 0;
+    int64_t ch = chunks_for(N * D, 8192);
+    if (ch > N) ch = N;
+    gather_ctx g;
+    g.fmt = fmt;
+    g.table = table;
+    g.V = V;
+    g.D = D;
+    g.N = N;
+    g.per = (N + ch - 1) / ch;
+    g.ids = ids;
+    g.y = y;
+    g.status = 0;
+    g.bad = 0;
+    pthread_mutex_init(&g.mu, NULL);
+    parallel_for(ch, gather_chunk, &g);
+    pthread_mutex_destroy(&g.mu);
+    if (g.status && bad_index) *bad_index = g.bad;
+    return g.status;
+}

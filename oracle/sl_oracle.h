@@ -1,0 +1,77 @@
+/*
+ * CPU oracle for the Sharplight fused layer ops -- TEST INFRASTRUCTURE ONLY.
+ *
+ * A restatement in plain C of the arithmetic of the reference's CPU execution provider
+ * (src/Sharplight.Cpu) for the ops on the fused-layer path. It is the parity checker for the
+ * HIP kernels of libsharplight_hip and the timed CPU baseline of bench.py; nothing in the
+ * product links it. Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg
+ * load it.
+ *
+ * Conventions: all activations are f32 (the reference CPU provider has no bf16 activations);
+ * the bf16 helpers restate the provider's own f32<->bf16 casts. Every function that touches a
+ * row range runs on the calling thread; the *_mt variants split the work the way the
+ * reference's CpuParallel.For does (chunks = min(threads*4, total/minChunk)).
+ */
+#ifndef SL_ORACLE_H
+#define SL_ORACLE_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Table formats, numbered like the C ABI's slhip_format (include/sharplight_hip.h). */
+enum { ORC_F32 = 0, ORC_F16 = 1, ORC_BF16 = 2, ORC_Q8_0 = 3, ORC_Q4_0 = 4, ORC_Q4_1 = 5, ORC_Q5_0 = 6, ORC_Q5_1 = 7 };
+
+/* ---- scalar conversions (Simd.cs:518-540, Quant.cs:371-381) ---- */
+uint16_t orc_f32_to_bf16(float f);
+float orc_bf16_to_f32(uint16_t h);
+float orc_f16_to_f32(uint16_t h);
+void orc_f32_to_bf16_n(const float* x, uint16_t* y, int64_t n);
+void orc_bf16_to_f32_n(const uint16_t* x, float* y, int64_t n);
+void orc_f16_to_f32_n(const uint16_t* x, float* y, int64_t n);
+
+/* ---- reductions (Simd.cs:274-340) ---- */
+float orc_sumsq(const float* a, int64_t n);
+float orc_sum(const float* a, int64_t n);
+
+/* ---- row ops (RowOp.cs:37-113); mode 0 = RmsNorm, 1 = L2Norm ---- */
+void orc_rmsnorm(const float* x, const float* w, float* y, int64_t rows, int64_t n, float eps, int mode);
+void orc_layernorm(const float* x, const float* w, const float* b, float* y, int64_t rows, int64_t n, float eps);
+
+/* ---- elementwise (BinaryOp.cs:8-103, ScalarMath.cs:521-641) ---- */
+void orc_add(const float* a, const float* b, float* y, int64_t n);
+void orc_mul(const float* a, const float* b, float* y, int64_t n);
+/* act: 0 = Silu, 1 = GeluTanh, 2 = Gelu (erf) */
+void orc_unary(int act, const float* x, float* y, int64_t n);
+double orc_erf(double x);
+float orc_erf_rational(float x);
+
+/* ---- rope (RopeOp.cs:28-183); x,y [T,H,D] dense; pos [T]; ff [dims/2] or NULL ---- */
+void orc_rope(const float* x, const int32_t* pos, const float* ff, float* y, int64_t T, int64_t H, int64_t D, int dims,
+              int neox, float base, float freq_scale, float attn_factor);
+
+/* ---- dequant / gather (Quant.cs:242-405, GatherOp.cs:22-75) ---- */
+int64_t orc_row_bytes(int fmt, int64_t d);
+int orc_dequant(int fmt, const uint8_t* src, int64_t count, float* dst);
+/* Returns 0, or -1 with *bad_index set to the first out-of-range id (the reference throws). */
+int orc_gather(int fmt, const uint8_t* table, int64_t V, int64_t D, const int32_t* ids, int64_t N, float* y,
+               int64_t* bad_index);
+
+/* ---- threaded variants for the CPU baseline (CpuParallel.cs:34-78) ---- */
+void orc_set_threads(int threads);
+int orc_get_threads(void);
+void orc_rmsnorm_mt(const float* x, const float* w, float* y, int64_t rows, int64_t n, float eps, int mode);
+void orc_layernorm_mt(const float* x, const float* w, const float* b, float* y, int64_t rows, int64_t n, float eps);
+void orc_add_mt(const float* a, const float* b, float* y, int64_t n);
+void orc_mul_mt(const float* a, const float* b, float* y, int64_t n);
+void orc_unary_mt(int act, const float* x, float* y, int64_t n);
+void orc_rope_mt(const float* x, const int32_t* pos, const float* ff, float* y, int64_t T, int64_t H, int64_t D, int dims,
+                 int neox, float base, float freq_scale, float attn_factor);
+int orc_gather_mt(int fmt, const uint8_t* table, int64_t V, int64_t D, const int32_t* ids, int64_t N, float* y,
+                  int64_t* bad_index);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

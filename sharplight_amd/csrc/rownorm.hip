@@ -1,0 +1,327 @@
+// Row normalization kernels: RMSNorm, L2Norm and LayerNorm over the last axis, each with an optional
+// residual add fused in front (the Add+RmsNorm unit). Bandwidth-bound: one HBM read of every input and
+// one write of every output.
+//
+// Semantics follow the reference CPU provider (src/Sharplight.Cpu/RowOp.cs:63-113):
+//   RMS:   scale = 1/sqrt(sum(h^2)/D + eps), y = (h*scale)*w
+//   L2:    scale = 1/sqrt(sum(h^2) + eps),   y = h*scale
+//   LAYER: mean = sum(h)/D, inv = 1/sqrt(sum((h-mean)^2)/D + eps), y = ((h-mean)*inv)*w + b
+// with h = x + res in f32 when a residual is given, written back as the updated residual stream (the
+// pass-1 output of the fused unit, src/Sharplight.Shaders/Lowering/RowNormKernelSource.cs:5-9).
+//
+// Layout: a row is split over a "row group" of WPR wavefronts (64*WPR lanes). Lane t of the group owns
+// the 16-byte vectors t, t + 64*WPR, t + 2*64*WPR, ... (NV of them), so every load and store
+// instruction of a wave covers 1 KiB of consecutive bytes. The row stays in VGPRs between the
+// reduction and the scaling pass. Reductions are a butterfly within the wave, then (WPR > 1) one LDS
+// exchange between the group's waves. A block holds 256/(64*WPR) row groups (or one group of up to
+// 16 waves). Rows that do not fit the vector path (D not a multiple of the vector width, unaligned
+// pointers or strides, or D beyond 8*64*16 vectors) take a scalar block-per-row kernel.
+#include "common.hpp"
+
+#include <stdlib.h>
+
+namespace slhip {
+
+struct RowNormArgs {
+    const void* x;
+    const void* res;
+    const float* w;
+    const float* b;
+    void* y;
+    void* h;
+    int64_t rows;
+    int64_t D;
+    int64_t xs, rs, ys, hs;  // row strides in elements
+    float eps;
+    int kind;
+};
+
+template <int NG>  // number of row groups sharing the LDS exchange
+__device__ __forceinline__ float group_reduce(float v, int wpr, int group, int wave_in_group, float* red)
+{
+    v = wave_sum(v);
+    if (wpr == 1) return v;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[group * 16 + wave_in_group] = v;
+    __syncthreads();
+    float s = 0.f;
+    for (int i = 0; i < wpr; i++) s += red[group * 16 + i];
+    return s;
+}
+
+template <int DTI, int DTO, int NV, bool RES>
+__global__ __launch_bounds__(1024) void rownorm_vec(RowNormArgs a, int wpr)
+{
+    using VI = Vec<DTI>;
+    constexpr int E = VI::N;  // elements per 16-byte input vector
+    __shared__ float red[4 * 16];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int group = wave / wpr;
+    const int wig = wave - group * wpr;
+    const int groups = blockDim.x / (64 * wpr);
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * groups + group;
+    const bool live = row < a.rows;
+    const int tpr = 64 * wpr;
+    const int t = wig * 64 + lane;
+    const int nvec = static_cast<int>(a.D / E);
+
+    float v[NV][E];
+    const char* xr = static_cast<const char*>(a.x) + row * a.xs * VI::BYTES;
+    if (live) {
+        uint4 raw[NV];
+#pragma unroll
+        for (int k = 0; k < NV; k++) {
+            int j = t + k * tpr;
+            if (j < nvec) raw[k] = reinterpret_cast<const uint4*>(xr)[j];
+        }
+        if (RES) {
+            const char* rr = static_cast<const char*>(a.res) + row * a.rs * VI::BYTES;
+            uint4 rraw[NV];
+#pragma unroll
+            for (int k = 0; k < NV; k++) {
+                int j = t + k * tpr;
+                if (j < nvec) rraw[k] = reinterpret_cast<const uint4*>(rr)[j];
+            }
+#pragma unroll
+            for (int k = 0; k < NV; k++) {
+                int j = t + k * tpr;
+                if (j < nvec) {
+                    float xf[E], rf[E];
+                    VI::unpack(raw[k], xf);
+                    VI::unpack(rraw[k], rf);
+#pragma unroll
+                    for (int e = 0; e < E; e++) v[k][e] = xf[e] + rf[e];
+                }
+            }
+            if (a.h) {
+                char* hr = static_cast<char*>(a.h) + row * a.hs * VI::BYTES;
+#pragma unroll
+                for (int k = 0; k < NV; k++) {
+                    int j = t + k * tpr;
+                    if (j < nvec) reinterpret_cast<uint4*>(hr)[j] = VI::pack(v[k]);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < NV; k++) {
+                int j = t + k * tpr;
+                if (j < nvec) VI::unpack(raw[k], v[k]);
+            }
+        }
+    }
+
+    const float inv_d = 1.0f / static_cast<float>(a.D);
+    float mean = 0.f, scale;
+    if (a.kind == SLHIP_NORM_LAYER) {
+        float s = 0.f;
+        if (live) {
+#pragma unroll
+            for (int k = 0; k < NV; k++)
+                if (t + k * tpr < nvec)
+#pragma unroll
+                    for (int e = 0; e < E; e++) s += v[k][e];
+        }
+        mean = group_reduce<4>(s, wpr, group, wig, red) * inv_d;
+        float q = 0.f;
+        if (live) {
+#pragma unroll
+            for (int k = 0; k < NV; k++)
+                if (t + k * tpr < nvec)
+#pragma unroll
+                    for (int e = 0; e < E; e++) {
+                        float d = v[k][e] - mean;
+                        q = fmaf(d, d, q);
+                    }
+        }
+        float var = group_reduce<4>(q, wpr, group, wig, red) * inv_d;
+        scale = 1.0f / sqrtf(var + a.eps);
+    } else {
+        float q = 0.f;
+        if (live) {
+#pragma unroll
+            for (int k = 0; k < NV; k++)
+                if (t + k * tpr < nvec)
+#pragma unroll
+                    for (int e = 0; e < E; e++) q = fmaf(v[k][e], v[k][e], q);
+        }
+        float ss = group_reduce<4>(q, wpr, group, wig, red);
+        scale = a.kind == SLHIP_NORM_RMS ? 1.0f / sqrtf(ss * inv_d + a.eps) : 1.0f / sqrtf(ss + a.eps);
+    }
+    if (!live) return;
+
+    char* yr = static_cast<char*>(a.y) + row * a.ys * Vec<DTO>::BYTES;
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        int j = t + k * tpr;
+        if (j >= nvec) continue;
+        float o[E];
+        if (a.kind == SLHIP_NORM_LAYER) {
+#pragma unroll
+            for (int e = 0; e < E; e++) o[e] = (v[k][e] - mean) * scale;
+        } else {
+#pragma unroll
+            for (int e = 0; e < E; e++) o[e] = v[k][e] * scale;
+        }
+        if (a.w) {
+            const float4* wp = reinterpret_cast<const float4*>(a.w + static_cast<int64_t>(j) * E);
+#pragma unroll
+            for (int q4 = 0; q4 < E / 4; q4++) {
+                float4 w4 = wp[q4];
+                o[4 * q4 + 0] *= w4.x;
+                o[4 * q4 + 1] *= w4.y;
+                o[4 * q4 + 2] *= w4.z;
+                o[4 * q4 + 3] *= w4.w;
+            }
+        }
+        if (a.b) {
+            const float4* bp = reinterpret_cast<const float4*>(a.b + static_cast<int64_t>(j) * E);
+#pragma unroll
+            for (int q4 = 0; q4 < E / 4; q4++) {
+                float4 b4 = bp[q4];
+                o[4 * q4 + 0] += b4.x;
+                o[4 * q4 + 1] += b4.y;
+                o[4 * q4 + 2] += b4.z;
+                o[4 * q4 + 3] += b4.w;
+            }
+        }
+        store_packed<DTO, E>(yr + static_cast<int64_t>(j) * E * Vec<DTO>::BYTES, o);
+    }
+}
+
+// Scalar fallback: one 256-thread block per row, re-reading the row from global memory (cache-resident)
+// for each pass.
+template <int DTI, int DTO>
+__global__ __launch_bounds__(256) void rownorm_scalar(RowNormArgs a)
+{
+    using VI = Vec<DTI>;
+    __shared__ float red[4];
+    const int64_t row = blockIdx.x;
+    const void* xr = static_cast<const char*>(a.x) + row * a.xs * VI::BYTES;
+    const void* rr = a.res ? static_cast<const char*>(a.res) + row * a.rs * VI::BYTES : nullptr;
+    void* hr = (a.res && a.h) ? static_cast<char*>(a.h) + row * a.hs * VI::BYTES : nullptr;
+    void* yr = static_cast<char*>(a.y) + row * a.ys * Vec<DTO>::BYTES;
+    const int64_t D = a.D;
+
+    auto reduce = [&](float s) {
+        s = wave_sum(s);
+        __syncthreads();
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+        __syncthreads();
+        return red[0] + red[1] + red[2] + red[3];
+    };
+    auto value = [&](int64_t i) {
+        float v = VI::load1(xr, i);
+        if (rr) v += VI::load1(rr, i);
+        return v;
+    };
+
+    float mean = 0.f, scale;
+    if (a.kind == SLHIP_NORM_LAYER) {
+        float s = 0.f;
+        for (int64_t i = threadIdx.x; i < D; i += 256) s += value(i);
+        mean = reduce(s) / static_cast<float>(D);
+        float q = 0.f;
+        for (int64_t i = threadIdx.x; i < D; i += 256) {
+            float d = value(i) - mean;
+            q = fmaf(d, d, q);
+        }
+        scale = 1.0f / sqrtf(reduce(q) / static_cast<float>(D) + a.eps);
+    } else {
+        float q = 0.f;
+        for (int64_t i = threadIdx.x; i < D; i += 256) {
+            float v = value(i);
+            q = fmaf(v, v, q);
+        }
+        float ss = reduce(q);
+        scale = a.kind == SLHIP_NORM_RMS ? 1.0f / sqrtf(ss / static_cast<float>(D) + a.eps) : 1.0f / sqrtf(ss + a.eps);
+    }
+    for (int64_t i = threadIdx.x; i < D; i += 256) {
+        float v = value(i);
+        if (hr) VI::store1(hr, i, v);
+        float o = a.kind == SLHIP_NORM_LAYER ? (v - mean) * scale : v * scale;
+        if (a.w) o *= a.w[i];
+        if (a.b) o += a.b[i];
+        Vec<DTO>::store1(yr, i, o);
+    }
+}
+
+// ---- host dispatch --------------------------------------------------------------------------------
+
+static int env_int(const char* name, int dflt)
+{
+    const char* s = getenv(name);
+    return s && *s ? atoi(s) : dflt;
+}
+
+template <int DTI, int DTO, bool RES>
+static int launch_vec(const RowNormArgs& a, int nv, int wpr, hipStream_t st)
+{
+    int groups = wpr >= 4 ? 1 : 4 / wpr;
+    int threads = 64 * wpr * groups;
+    dim3 grid(static_cast<unsigned>((a.rows + groups - 1) / groups));
+    switch (nv) {
+    case 1: rownorm_vec<DTI, DTO, 1, RES><<<grid, threads, 0, st>>>(a, wpr); break;
+    case 2: rownorm_vec<DTI, DTO, 2, RES><<<grid, threads, 0, st>>>(a, wpr); break;
+    case 4: rownorm_vec<DTI, DTO, 4, RES><<<grid, threads, 0, st>>>(a, wpr); break;
+    case 8: rownorm_vec<DTI, DTO, 8, RES><<<grid, threads, 0, st>>>(a, wpr); break;
+    default: return fail(SLHIP_ERR_INVALID, "internal: bad vector count %d", nv);
+    }
+    return check_launch("rownorm_vec");
+}
+
+template <int DTI, int DTO>
+static int dispatch(const RowNormArgs& a, hipStream_t st)
+{
+    constexpr int E = Vec<DTI>::N;
+    constexpr int OA = E * Vec<DTO>::BYTES < 16 ? E * Vec<DTO>::BYTES : 16;  // output store alignment
+    bool vec_ok = a.D % E == 0 && aligned16(a.x) && a.xs % E == 0 && (!a.res || (aligned16(a.res) && a.rs % E == 0)) &&
+                  (!a.h || (aligned16(a.h) && a.hs % E == 0)) &&
+                  reinterpret_cast<uintptr_t>(a.y) % OA == 0 && (a.ys * Vec<DTO>::BYTES) % OA == 0 &&
+                  (!a.w || aligned16(a.w)) && (!a.b || aligned16(a.b));
+    int64_t nvec = a.D / E;
+    if (vec_ok && nvec <= 8 * 64 * 16) {
+        // Smallest row group that keeps the row within 8 vectors per lane, widened while the launch has
+        // fewer than ~4096 waves (short launches need the extra parallelism more than the registers).
+        int wpr = 1;
+        while (nvec > static_cast<int64_t>(8) * 64 * wpr) wpr *= 2;
+        while (wpr < 16 && a.rows * wpr < 4096 && nvec >= static_cast<int64_t>(64) * wpr * 2) wpr *= 2;
+        int forced = env_int("SLHIP_ROWNORM_WPR", 0);
+        if (forced == 1 || forced == 2 || forced == 4 || forced == 8 || forced == 16) {
+            if (nvec <= static_cast<int64_t>(8) * 64 * forced) wpr = forced;
+        }
+        int64_t per = (nvec + 64 * wpr - 1) / (64 * wpr);
+        int nv = per <= 1 ? 1 : per <= 2 ? 2 : per <= 4 ? 4 : 8;
+        return a.res ? launch_vec<DTI, DTO, true>(a, nv, wpr, st) : launch_vec<DTI, DTO, false>(a, nv, wpr, st);
+    }
+    rownorm_scalar<DTI, DTO><<<dim3(static_cast<unsigned>(a.rows)), 256, 0, st>>>(a);
+    return check_launch("rownorm_scalar");
+}
+
+}  // namespace slhip
+
+using namespace slhip;
+
+extern "C" SLHIP_API int slhip_rownorm(int kind, int dtype_in, int dtype_out, const void* x, const void* res,
+                                       const float* w, const float* b, void* y, void* h_out, int64_t rows, int64_t D,
+                                       int64_t x_stride, int64_t res_stride, int64_t y_stride, int64_t h_stride,
+                                       float eps, slhip_stream stream)
+{
+    if (kind < SLHIP_NORM_RMS || kind > SLHIP_NORM_LAYER) return fail(SLHIP_ERR_INVALID, "rownorm: bad kind %d", kind);
+    if (rows < 0 || D < 0) return fail(SLHIP_ERR_INVALID, "rownorm: negative shape");
+    if (rows == 0 || D == 0) return SLHIP_OK;
+    if (!x || !y) return fail(SLHIP_ERR_INVALID, "rownorm: x and y are required");
+    if (kind == SLHIP_NORM_L2 && w) return fail(SLHIP_ERR_INVALID, "rownorm: L2Norm takes no weight");
+    if (kind != SLHIP_NORM_LAYER && b) return fail(SLHIP_ERR_INVALID, "rownorm: only LayerNorm takes a bias");
+    if (x_stride < D || y_stride < D || (res && res_stride < D) || (res && h_out && h_stride < D))
+        return fail(SLHIP_ERR_INVALID, "rownorm: a row stride is smaller than D");
+    if (rows > 0x7FFFFFFF) return fail(SLHIP_ERR_UNSUPPORTED, "rownorm: more than 2^31-1 rows");
+    RowNormArgs a{x, res, w, b, y, res ? h_out : nullptr, rows, D, x_stride, res_stride, y_stride, h_stride, eps, kind};
+    hipStream_t st = to_stream(stream);
+    if (dtype_in == SLHIP_F32 && dtype_out == SLHIP_F32) return dispatch<SLHIP_F32, SLHIP_F32>(a, st);
+    if (dtype_in == SLHIP_BF16 && dtype_out == SLHIP_BF16) return dispatch<SLHIP_BF16, SLHIP_BF16>(a, st);
+    if (dtype_in == SLHIP_BF16 && dtype_out == SLHIP_F32) return dispatch<SLHIP_BF16, SLHIP_F32>(a, st);
+    if (dtype_in == SLHIP_F32 && dtype_out == SLHIP_BF16) return dispatch<SLHIP_F32, SLHIP_BF16>(a, st);
+    return fail(SLHIP_ERR_UNSUPPORTED, "rownorm: dtype pair (%d -> %d) not supported", dtype_in, dtype_out);
+}

@@ -1,0 +1,314 @@
+// Device, memory, stream and event entry points of libsharplight_hip, and the shared error plumbing.
+//
+// These are what the managed provider needs around the kernels: CheckAvailability / GetDevices /
+// OpenDevice (src/Sharplight.Core/Runtime/IExecutionProvider.cs:25-40), the memory a compiled segment
+// owns (IComputeDevice.Compile, IComputeDevice.cs:33-38) and SetInput / Execute / GetOutput
+// (ICompiledSegment.cs:6-25), which the Vulkan provider implements with its own device, buffer and
+// fence calls (src/Sharplight.Vulkan/VulkanDevice.cs, VulkanSegment.cs:374-479).
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+
+#include "common.hpp"
+
+namespace slhip {
+
+static thread_local char t_last_error[512] = "";
+
+int fail(int status, const char* fmt, ...)
+{
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(t_last_error, sizeof t_last_error, fmt, ap);
+    va_end(ap);
+    return status;
+}
+
+int hip_fail(hipError_t e, const char* what)
+{
+    if (e == hipSuccess) return SLHIP_OK;
+    return fail(SLHIP_ERR_HIP, "%s: %s (%d)", what, hipGetErrorString(e), static_cast<int>(e));
+}
+
+int check_launch(const char* kernel)
+{
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(SLHIP_ERR_HIP, "launch of %s failed: %s", kernel, hipGetErrorString(e));
+    return SLHIP_OK;
+}
+
+static constexpr int kMaxDevices = 64;
+static std::mutex g_err_mu;
+static uint32_t* g_err_word[kMaxDevices] = {};
+
+int index_error_word(uint32_t** word)
+{
+    int dev = 0;
+    SLHIP_CHECK_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) return fail(SLHIP_ERR_INVALID, "device index %d out of range", dev);
+    std::lock_guard<std::mutex> lock(g_err_mu);
+    if (!g_err_word[dev]) {
+        void* p = nullptr;
+        SLHIP_CHECK_HIP(hipMalloc(&p, 16));
+        SLHIP_CHECK_HIP(hipMemset(p, 0, 16));
+        g_err_word[dev] = static_cast<uint32_t*>(p);
+    }
+    *word = g_err_word[dev];
+    return SLHIP_OK;
+}
+
+// Reads and clears the current device's index-error word after the stream drained.
+static int take_index_error()
+{
+    int dev = 0;
+    SLHIP_CHECK_HIP(hipGetDevice(&dev));
+    uint32_t* w = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_err_mu);
+        if (dev >= 0 && dev < kMaxDevices) w = g_err_word[dev];
+    }
+    if (!w) return SLHIP_OK;
+    uint32_t host[4] = {0, 0, 0, 0};
+    SLHIP_CHECK_HIP(hipMemcpy(host, w, 16, hipMemcpyDeviceToHost));
+    if (!host[0]) return SLHIP_OK;
+    SLHIP_CHECK_HIP(hipMemset(w, 0, 16));
+    int64_t id = static_cast<int64_t>(static_cast<uint64_t>(host[1]) | (static_cast<uint64_t>(host[2]) << 32));
+    return fail(SLHIP_ERR_INDEX, "Gather index %lld out of range [0,%u).", static_cast<long long>(id), host[3]);
+}
+
+}  // namespace slhip
+
+using namespace slhip;
+
+extern "C" {
+
+SLHIP_API const char* slhip_last_error(void) { return t_last_error; }
+
+SLHIP_API int slhip_abi_version(void) { return SLHIP_ABI_VERSION; }
+
+SLHIP_API int slhip_device_count(int* count)
+{
+    if (!count) return fail(SLHIP_ERR_INVALID, "count is null");
+    *count = 0;
+    hipError_t e = hipGetDeviceCount(count);
+    if (e == hipErrorNoDevice) {
+        *count = 0;
+        return SLHIP_OK;
+    }
+    if (e != hipSuccess) {
+        *count = 0;
+        return fail(SLHIP_ERR_NO_DEVICE, "HIP runtime unavailable: %s", hipGetErrorString(e));
+    }
+    return SLHIP_OK;
+}
+
+SLHIP_API int slhip_device_props_get(int device, slhip_device_props* props)
+{
+    if (!props) return fail(SLHIP_ERR_INVALID, "props is null");
+    int n = 0;
+    int st = slhip_device_count(&n);
+    if (st) return st;
+    if (device < 0 || device >= n) return fail(SLHIP_ERR_INVALID, "device %d out of range [0,%d)", device, n);
+    hipDeviceProp_t p;
+    SLHIP_CHECK_HIP(hipGetDeviceProperties(&p, device));
+    memset(props, 0, sizeof *props);
+    snprintf(props->name, sizeof props->name, "%s", p.name);
+    snprintf(props->arch, sizeof props->arch, "%s", p.gcnArchName);
+    props->total_memory = static_cast<int64_t>(p.totalGlobalMem);
+    props->compute_units = p.multiProcessorCount;
+    props->wavefront_size = p.warpSize;
+    props->pci_domain = p.pciDomainID;
+    props->pci_bus = p.pciBusID;
+    props->pci_device = p.pciDeviceID;
+    props->clock_khz = p.clockRate;
+    props->l2_bytes = p.l2CacheSize;
+    props->max_threads_per_block = p.maxThreadsPerBlock;
+    props->lds_bytes_per_block = static_cast<int32_t>(p.sharedMemPerBlock);
+    return SLHIP_OK;
+}
+
+SLHIP_API int slhip_set_device(int device)
+{
+    SLHIP_CHECK_HIP(hipSetDevice(device));
+    // The device's index-error word is allocated here, at open time, so that no later op call (possibly
+    // under graph capture) allocates.
+    uint32_t* w = nullptr;
+    return index_error_word(&w);
+}
+
+SLHIP_API int slhip_get_device(int* device)
+{
+    if (!device) return fail(SLHIP_ERR_INVALID, "device is null");
+    SLHIP_CHECK_HIP(hipGetDevice(device));
+    return SLHIP_OK;
+}
+
+SLHIP_API int slhip_mem_info(size_t* free_bytes, size_t* total_bytes)
+{
+    size_t f = 0, t = 0;
+    SLHIP_CHECK_HIP(hipMemGetInfo(&f, &t));
+    if (free_bytes) *free_bytes = f;
+    if (total_bytes) *total_bytes = t;
+    return SLHIP_OK;
+}
+
+SLHIP_API int slhip_malloc(void** ptr, size_t bytes)
+{
+    if (!ptr) return fail(SLHIP_ERR_INVALID, "ptr is null");
+    *ptr = nullptr;
+    if (bytes == 0) return SLHIP_OK;
+    SLHIP_CHECK_HIP(hipMalloc(ptr, bytes));
+    return SLHIP_OK;
+}
+
+SLHIP_API int slhip_free(void* ptr)
+{
+    if (!ptr) return SLHIP_OK;
+    SLHIP_CHECK_HIP(hipFree(ptr));
+    return SLHIP_OK;
+}
+
+SLHIP_API int slhip_host_malloc(void** ptr, size_t bytes)
+{
+    if (!ptr) return fail(SLHIP_ERR_INVALID, "ptr is null");
+    *ptr = nullptr;
+    if (bytes == 0) return SLHIP_OK;
+    SLHIP_CHECK_HIP(hipHostMalloc(ptr, bytes, hipHostMallocDefault));
+    return SLHIP_OK;
+}
+
+SLHIP_API int slhip_host_free(void* ptr)
+{
+    if (!ptr) return SLHIP_OK;
+    SLHIP_CHECK_HIP(hipHostFree(ptr));
+    return SLHIP_OK;
+}
+
+static int copy(void* dst, const void* src, size_t bytes, hipMemcpyKind kind, slhip_stream stream)
+{
+    if (bytes == 0) return SLHIP_OK;
+    if (!dst || !src) return fail(SLHIP_ERR_INVALID, "memcpy with a null pointer");
+    SLHIP_CHECK_HIP(hipMemcpyAsync(dst, src, bytes, kind, to_stream(stream)));
+    return SLHIP_OK;
+}
+
+SLHIP_API int slhip_memcpy_h2d(void* dst, const void* src, size_t bytes, slhip_stream stream)
+{
+    return copy(dst, src, bytes, hipMemcpyHostToDevice, stream);
+}
+
+SLHIP_API int slhip_memcpy_d2h(void* dst, const void* src, size_t bytes, slhip_stream stream)
+{
+    return copy(dst, src, bytes, hipMemcpyDeviceToHost, stream);
+}
+
+SLHIP_API int slhip_memcpy_d2d(void* dst, const void* src, size_t bytes, slhip_stream stream)
+{
+    return copy(dst, src, bytes, hipMemcpyDeviceToDevice, stream);
+}
+
+SLHIP_API int slhip_memset(void* dst, int value, size_t bytes, slhip_stream stream)
+{
+    if (bytes == 0) return SLHIP_OK;
+    if (!dst) return fail(SLHIP_ERR_INVALID, "memset of a null pointer");
+    SLHIP_CHECK_HIP(hipMemsetAsync(dst, value, bytes, to_stream(stream)));
+    return SLHIP_OK;
+}
+
+SLHIP_API int slhip_stream_create(slhip_stream* stream)
+{
+    if (!stream) return fail(SLHIP_ERR_INVALID, "stream is null");
+    hipStream_t s = nullptr;
+    SLHIP_CHECK_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    *stream = s;
+    return SLHIP_OK;
+}
+
+SLHIP_API int slhip_stream_destroy(slhip_stream stream)
+{
+    if (!stream) return SLHIP_OK;
+    SLHIP_CHECK_HIP(hipStreamDestroy(to_stream(stream)));
+    return SLHIP_OK;
+}
+
+SLHIP_API int slhip_stream_sync(slhip_stream stream)
+{
+    SLHIP_CHECK_HIP(hipStreamSynchronize(to_stream(stream)));
+    return take_index_error();
+}
+
+SLHIP_API int slhip_event_create(slhip_event* event)
+{
+    if (!event) return fail(SLHIP_ERR_INVALID, "event is null");
+    hipEvent_t e = nullptr;
+    SLHIP_CHECK_HIP(hipEventCreate(&e));
+    *event = e;
+    return SLHIP_OK;
+}
+
+SLHIP_API int slhip_event_destroy(slhip_event event)
+{
+    if (!event) return SLHIP_OK;
+    SLHIP_CHECK_HIP(hipEventDestroy(reinterpret_cast<hipEvent_t>(event)));
+    return SLHIP_OK;
+}
+
+SLHIP_API int slhip_event_record(slhip_event event, slhip_stream stream)
+{
+    if (!event) return fail(SLHIP_ERR_INVALID, "event is null");
+    SLHIP_CHECK_HIP(hipEventRecord(reinterpret_cast<hipEvent_t>(event), to_stream(stream)));
+    return SLHIP_OK;
+}
+
+SLHIP_API int slhip_event_synchronize(slhip_event event)
+{
+    if (!event) return fail(SLHIP_ERR_INVALID, "event is null");
+    SLHIP_CHECK_HIP(hipEventSynchronize(reinterpret_cast<hipEvent_t>(event)));
+    return SLHIP_OK;
+}
+
+SLHIP_API int slhip_event_elapsed_ms(float* ms, slhip_event start, slhip_event stop)
+{
+    if (!ms || !start || !stop) return fail(SLHIP_ERR_INVALID, "null argument");
+    SLHIP_CHECK_HIP(hipEventElapsedTime(ms, reinterpret_cast<hipEvent_t>(start), reinterpret_cast<hipEvent_t>(stop)));
+    return SLHIP_OK;
+}
+
+SLHIP_API int slhip_graph_begin(slhip_stream stream)
+{
+    if (!stream) return fail(SLHIP_ERR_INVALID, "graph capture needs a created stream, not the null stream");
+    SLHIP_CHECK_HIP(hipStreamBeginCapture(to_stream(stream), hipStreamCaptureModeThreadLocal));
+    return SLHIP_OK;
+}
+
+SLHIP_API int slhip_graph_end(slhip_stream stream, slhip_graph* graph)
+{
+    if (!stream || !graph) return fail(SLHIP_ERR_INVALID, "null argument");
+    *graph = nullptr;
+    hipGraph_t g = nullptr;
+    SLHIP_CHECK_HIP(hipStreamEndCapture(to_stream(stream), &g));
+    hipGraphExec_t exec = nullptr;
+    hipError_t e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+    hipGraphDestroy(g);
+    if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+    *graph = exec;
+    return SLHIP_OK;
+}
+
+SLHIP_API int slhip_graph_launch(slhip_graph graph, slhip_stream stream)
+{
+    if (!graph) return fail(SLHIP_ERR_INVALID, "graph is null");
+    SLHIP_CHECK_HIP(hipGraphLaunch(reinterpret_cast<hipGraphExec_t>(graph), to_stream(stream)));
+    return SLHIP_OK;
+}
+
+SLHIP_API int slhip_graph_destroy(slhip_graph graph)
+{
+    if (!graph) return SLHIP_OK;
+    SLHIP_CHECK_HIP(hipGraphExecDestroy(reinterpret_cast<hipGraphExec_t>(graph)));
+    return SLHIP_OK;
+}
+
+}  // extern "C"

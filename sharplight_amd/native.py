@@ -1,0 +1,336 @@
+"""ctypes binding of libsharplight_hip (include/sharplight_hip.h).
+
+This is the Python twin of the managed provider's ``[LibraryImport]`` declarations: one typed foreign
+function per C entry point, statuses turned into the exceptions the reference's providers throw
+(``ArgumentException`` -> ``ValueError``, ``NotSupportedException`` -> ``NotImplementedError``,
+``ArgumentOutOfRangeException`` -> ``IndexError``). There is no fallback: if the library is not built
+or cannot load, every call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libsharplight_hip.so")
+
+OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP, ERR_INDEX, ERR_NO_DEVICE = 0, -1, -2, -3, -4, -5
+F32, F16, BF16 = 0, 1, 2
+DTYPES = {"f32": F32, "f16": F16, "bf16": BF16}
+NP_DTYPES = {F32: np.float32, F16: np.float16, BF16: np.uint16}  # bf16 travels as raw uint16 bits
+FMT_F32, FMT_F16, FMT_BF16, FMT_Q8_0, FMT_Q4_0, FMT_Q4_1, FMT_Q5_0, FMT_Q5_1 = range(8)
+FORMATS = {"f32": FMT_F32, "f16": FMT_F16, "bf16": FMT_BF16, "q8_0": FMT_Q8_0, "q4_0": FMT_Q4_0,
+           "q4_1": FMT_Q4_1, "q5_0": FMT_Q5_0, "q5_1": FMT_Q5_1}
+NORM_RMS, NORM_L2, NORM_LAYER = 0, 1, 2
+NORMS = {"rms": NORM_RMS, "l2": NORM_L2, "layer": NORM_LAYER}
+ACT_SILU, ACT_GELU_TANH, ACT_GELU_ERF = 0, 1, 2
+ACTS = {"silu": ACT_SILU, "gelu_tanh": ACT_GELU_TANH, "gelu_erf": ACT_GELU_ERF}
+
+
+class SlhipError(RuntimeError):
+    """A HIP runtime failure (SLHIP_ERR_HIP) or a missing device (SLHIP_ERR_NO_DEVICE)."""
+
+
+class SlhipArgumentError(ValueError):
+    pass
+
+
+class SlhipNotSupported(NotImplementedError):
+    pass
+
+
+class SlhipIndexError(IndexError):
+    pass
+
+
+class DeviceProps(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char * 256), ("arch", ctypes.c_char * 64), ("total_memory", ctypes.c_int64),
+                ("compute_units", ctypes.c_int32), ("wavefront_size", ctypes.c_int32),
+                ("pci_domain", ctypes.c_int32), ("pci_bus", ctypes.c_int32), ("pci_device", ctypes.c_int32),
+                ("clock_khz", ctypes.c_int32), ("l2_bytes", ctypes.c_int64),
+                ("max_threads_per_block", ctypes.c_int32), ("lds_bytes_per_block", ctypes.c_int32)]
+
+
+class RopeTensor(ctypes.Structure):
+    _fields_ = [("x", ctypes.c_void_p), ("y", ctypes.c_void_p), ("norm_w", ctypes.c_void_p),
+                ("heads", ctypes.c_int64), ("x_stride_t", ctypes.c_int64), ("x_stride_h", ctypes.c_int64),
+                ("y_stride_t", ctypes.c_int64), ("y_stride_h", ctypes.c_int64)]
+
+
+class RopeCfg(ctypes.Structure):
+    _fields_ = [("dims", ctypes.c_int32), ("neox", ctypes.c_int32), ("base", ctypes.c_float),
+                ("freq_scale", ctypes.c_float), ("attn_factor", ctypes.c_float), ("norm", ctypes.c_int32),
+                ("eps", ctypes.c_float), ("reserved", ctypes.c_int32)]
+
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_I64 = ctypes.c_int64
+_F = ctypes.c_float
+_SZ = ctypes.c_size_t
+
+SIGNATURES = {
+    "slhip_last_error": (ctypes.c_char_p, []),
+    "slhip_abi_version": (_I, []),
+    "slhip_device_count": (_I, [ctypes.POINTER(_I)]),
+    "slhip_device_props_get": (_I, [_I, ctypes.POINTER(DeviceProps)]),
+    "slhip_set_device": (_I, [_I]),
+    "slhip_get_device": (_I, [ctypes.POINTER(_I)]),
+    "slhip_mem_info": (_I, [ctypes.POINTER(_SZ), ctypes.POINTER(_SZ)]),
+    "slhip_malloc": (_I, [ctypes.POINTER(_P), _SZ]),
+    "slhip_free": (_I, [_P]),
+    "slhip_host_malloc": (_I, [ctypes.POINTER(_P), _SZ]),
+    "slhip_host_free": (_I, [_P]),
+    "slhip_memcpy_h2d": (_I, [_P, _P, _SZ, _P]),
+    "slhip_memcpy_d2h": (_I, [_P, _P, _SZ, _P]),
+    "slhip_memcpy_d2d": (_I, [_P, _P, _SZ, _P]),
+    "slhip_memset": (_I, [_P, _I, _SZ, _P]),
+    "slhip_stream_create": (_I, [ctypes.POINTER(_P)]),
+    "slhip_stream_destroy": (_I, [_P]),
+    "slhip_stream_sync": (_I, [_P]),
+    "slhip_event_create": (_I, [ctypes.POINTER(_P)]),
+    "slhip_event_destroy": (_I, [_P]),
+    "slhip_event_record": (_I, [_P, _P]),
+    "slhip_event_synchronize": (_I, [_P]),
+    "slhip_event_elapsed_ms": (_I, [ctypes.POINTER(_F), _P, _P]),
+    "slhip_graph_begin": (_I, [_P]),
+    "slhip_graph_end": (_I, [_P, ctypes.POINTER(_P)]),
+    "slhip_graph_launch": (_I, [_P, _P]),
+    "slhip_graph_destroy": (_I, [_P]),
+    "slhip_rownorm": (_I, [_I, _I, _I, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P]),
+    "slhip_gated_act": (_I, [_I, _I, _I, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P]),
+    "slhip_rope": (_I, [_I, _I, ctypes.POINTER(RopeTensor), _I, _P, _P, _I64, _I64, ctypes.POINTER(RopeCfg), _P]),
+    "slhip_gather": (_I, [_I, _P, _I64, _I64, _P, _I64, _I, _P, _I64, _P]),
+    "slhip_convert": (_I, [_I, _I, _P, _P, _I64, _P]),
+}
+
+_lib = None
+
+
+def lib():
+    """The loaded library; raises if it is not built (no fallback path exists)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise SlhipError(f"{LIB_PATH} is not built: run `python -m sharplight_amd.build`")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def last_error() -> str:
+    return lib().slhip_last_error().decode(errors="replace")
+
+
+def check(status: int) -> None:
+    if status == OK:
+        return
+    msg = last_error()
+    if status == ERR_INVALID:
+        raise SlhipArgumentError(msg)
+    if status == ERR_UNSUPPORTED:
+        raise SlhipNotSupported(msg)
+    if status == ERR_INDEX:
+        raise SlhipIndexError(msg)
+    raise SlhipError(f"status {status}: {msg}")
+
+
+def call(name: str, *args) -> None:
+    check(getattr(lib(), name)(*args))
+
+
+# ---- devices ----------------------------------------------------------------------------------------
+
+def device_count() -> int:
+    n = _I(0)
+    call("slhip_device_count", ctypes.byref(n))
+    return n.value
+
+
+def device_props(index: int = 0) -> DeviceProps:
+    p = DeviceProps()
+    call("slhip_device_props_get", index, ctypes.byref(p))
+    return p
+
+
+def set_device(index: int) -> None:
+    call("slhip_set_device", index)
+
+
+def synchronize(stream=None) -> None:
+    call("slhip_stream_sync", stream)
+
+
+# ---- memory -----------------------------------------------------------------------------------------
+
+class DeviceBuffer:
+    """Owning device allocation (slhip_malloc / slhip_free)."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        p = _P(0)
+        call("slhip_malloc", ctypes.byref(p), self.nbytes)
+        self.ptr = p.value or 0
+
+    @classmethod
+    def from_numpy(cls, arr: np.ndarray, stream=None) -> "DeviceBuffer":
+        arr = np.ascontiguousarray(arr)
+        buf = cls(arr.nbytes)
+        buf.upload(arr, stream)
+        return buf
+
+    def upload(self, arr: np.ndarray, stream=None, offset: int = 0) -> None:
+        arr = np.ascontiguousarray(arr)
+        if offset + arr.nbytes > self.nbytes:
+            raise ValueError("upload past the end of the buffer")
+        call("slhip_memcpy_h2d", self.ptr + offset, arr.ctypes.data, arr.nbytes, stream)
+        call("slhip_stream_sync", stream)
+
+    def download(self, shape, dtype, stream=None, offset: int = 0) -> np.ndarray:
+        out = np.empty(shape, dtype)
+        if offset + out.nbytes > self.nbytes:
+            raise ValueError("download past the end of the buffer")
+        call("slhip_memcpy_d2h", out.ctypes.data, self.ptr + offset, out.nbytes, stream)
+        call("slhip_stream_sync", stream)
+        return out
+
+    def zero(self, stream=None) -> None:
+        call("slhip_memset", self.ptr, 0, self.nbytes, stream)
+
+    def free(self) -> None:
+        if self.ptr:
+            call("slhip_free", self.ptr)
+            self.ptr = 0
+
+    def __del__(self):
+        try:
+            if self.ptr and _lib is not None:
+                _lib.slhip_free(self.ptr)
+                self.ptr = 0
+        except Exception:
+            pass
+
+    def __int__(self):
+        return self.ptr
+
+
+def ptr(x) -> int | None:
+    """Device address of a DeviceBuffer / int / None."""
+    if x is None:
+        return None
+    if isinstance(x, DeviceBuffer):
+        return x.ptr
+    return int(x)
+
+
+class Event:
+    def __init__(self):
+        e = _P(0)
+        call("slhip_event_create", ctypes.byref(e))
+        self.handle = e.value
+
+    def record(self, stream=None):
+        call("slhip_event_record", self.handle, stream)
+
+    def synchronize(self):
+        call("slhip_event_synchronize", self.handle)
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = _F(0)
+        call("slhip_event_elapsed_ms", ctypes.byref(ms), self.handle, end.handle)
+        return ms.value
+
+    def __del__(self):
+        try:
+            if self.handle and _lib is not None:
+                _lib.slhip_event_destroy(self.handle)
+        except Exception:
+            pass
+
+
+class Stream:
+    def __init__(self):
+        s = _P(0)
+        call("slhip_stream_create", ctypes.byref(s))
+        self.handle = s.value
+
+    def sync(self):
+        call("slhip_stream_sync", self.handle)
+
+    def __del__(self):
+        try:
+            if self.handle and _lib is not None:
+                _lib.slhip_stream_destroy(self.handle)
+        except Exception:
+            pass
+
+
+class Graph:
+    """Launches recorded once on a stream (slhip_graph_begin/end), replayed with launch()."""
+
+    def __init__(self, stream: "Stream", record):
+        call("slhip_graph_begin", stream.handle)
+        try:
+            record()
+        finally:
+            g = _P(0)
+            st = lib().slhip_graph_end(stream.handle, ctypes.byref(g))
+        check(st)
+        self.handle = g.value
+
+    def launch(self, stream: "Stream"):
+        call("slhip_graph_launch", self.handle, stream.handle)
+
+    def __del__(self):
+        try:
+            if self.handle and _lib is not None:
+                _lib.slhip_graph_destroy(self.handle)
+        except Exception:
+            pass
+
+
+# ---- ops (device pointers in, nothing synchronous) -------------------------------------------------
+
+def rownorm(kind, dtype_in, dtype_out, x, y, rows, D, *, res=None, w=None, b=None, h_out=None, eps=1e-6,
+            x_stride=None, res_stride=None, y_stride=None, h_stride=None, stream=None):
+    call("slhip_rownorm", NORMS.get(kind, kind), DTYPES.get(dtype_in, dtype_in), DTYPES.get(dtype_out, dtype_out),
+         ptr(x), ptr(res), ptr(w), ptr(b), ptr(y), ptr(h_out), rows, D,
+         D if x_stride is None else x_stride, D if res_stride is None else res_stride,
+         D if y_stride is None else y_stride, D if h_stride is None else h_stride, eps, stream)
+
+
+def gated_act(act, dtype_in, dtype_out, gate, up, out, rows, cols, *, gate_stride=None, up_stride=None,
+              out_stride=None, stream=None):
+    call("slhip_gated_act", ACTS.get(act, act), DTYPES.get(dtype_in, dtype_in), DTYPES.get(dtype_out, dtype_out),
+         ptr(gate), ptr(up), ptr(out), rows, cols, cols if gate_stride is None else gate_stride,
+         cols if up_stride is None else up_stride, cols if out_stride is None else out_stride, stream)
+
+
+def rope(dtype_in, dtype_out, tensors, pos, T, D, *, dims=0, neox=True, base=10000.0, freq_scale=1.0,
+         attn_factor=1.0, norm=False, eps=1e-6, ff=None, stream=None):
+    """tensors: list of dicts with x, y, heads and optional norm_w / strides (elements)."""
+    arr = (RopeTensor * len(tensors))()
+    for i, t in enumerate(tensors):
+        H = t["heads"]
+        arr[i] = RopeTensor(ptr(t["x"]), ptr(t["y"]), ptr(t.get("norm_w")), H,
+                            t.get("x_stride_t", H * D), t.get("x_stride_h", D),
+                            t.get("y_stride_t", H * D), t.get("y_stride_h", D))
+    cfg = RopeCfg(dims, 1 if neox else 0, base, freq_scale, attn_factor, 1 if norm else 0, eps, 0)
+    call("slhip_rope", DTYPES.get(dtype_in, dtype_in), DTYPES.get(dtype_out, dtype_out), arr, len(tensors),
+         ptr(pos), ptr(ff), T, D, ctypes.byref(cfg), stream)
+
+
+def gather(fmt, table, V, D, ids, N, dtype_out, y, *, y_stride=None, stream=None):
+    call("slhip_gather", FORMATS.get(fmt, fmt), ptr(table), V, D, ptr(ids), N, DTYPES.get(dtype_out, dtype_out),
+         ptr(y), D if y_stride is None else y_stride, stream)
+
+
+def convert(dtype_in, dtype_out, x, y, n, stream=None):
+    call("slhip_convert", DTYPES.get(dtype_in, dtype_in), DTYPES.get(dtype_out, dtype_out), ptr(x), ptr(y), n,
+         stream)

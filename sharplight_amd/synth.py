@@ -1,0 +1,123 @@
+"""Seeded synthetic inputs of the benchmark configurations (C1..C5) and of the parity tests.
+
+Every tensor comes from its own numpy PCG64 stream keyed by (seed, tensor id), so a tensor's bits do not
+depend on which other tensors were generated. N(0,1) values are drawn in f32 and stored to bf16 by
+round-to-nearest-even; quantized tables are built block by block in ggml's layout (f16 scale first).
+bf16 arrays are carried as raw uint16 bits.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+
+
+def rng(seed: int, tensor_id: int) -> np.random.Generator:
+    return np.random.default_rng([seed, tensor_id])
+
+
+def bf16_bits(x: np.ndarray) -> np.ndarray:
+    """f32 -> bf16 bits, round to nearest even, NaN quieted."""
+    b = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+    r = ((b + np.uint32(0x7FFF) + ((b >> np.uint32(16)) & np.uint32(1))) >> np.uint32(16)).astype(np.uint16)
+    nan = (b & np.uint32(0x7FFFFFFF)) > np.uint32(0x7F800000)
+    if nan.any():
+        r[nan] = ((b[nan] >> np.uint32(16)) | np.uint32(0x40)).astype(np.uint16)
+    return r
+
+
+def bf16_to_f32(bits: np.ndarray) -> np.ndarray:
+    return (np.ascontiguousarray(bits, dtype=np.uint16).astype(np.uint32) << np.uint32(16)).view(np.float32)
+
+
+def normal(seed, tid, shape, mean=0.0, std=1.0, dtype="f32"):
+    x = rng(seed, tid).standard_normal(size=shape, dtype=np.float32)
+    if std != 1.0 or mean != 0.0:
+        x = (x * np.float32(std) + np.float32(mean)).astype(np.float32)
+    return bf16_bits(x) if dtype == "bf16" else x
+
+
+BLOCK = {"q8_0": 34, "q4_0": 18, "q4_1": 20, "q5_0": 22, "q5_1": 24}
+
+
+def row_bytes(fmt: str, D: int) -> int:
+    if fmt == "f32":
+        return 4 * D
+    if fmt in ("f16", "bf16"):
+        return 2 * D
+    assert D % 32 == 0
+    return D // 32 * BLOCK[fmt]
+
+
+def quant_table(fmt: str, V: int, D: int, seed: int = 0, tid: int = 0, scale_lo=0.001, scale_hi=0.02):
+    """Raw [V, row_bytes] uint8 image of a table in ``fmt``.
+
+    q8_0: int8 codes ~ U{-127..127}; q4_*/q5_*: bytes ~ U{0..255} (so nibbles ~ U{0..15}); scales and
+    mins f16 ~ U[scale_lo, scale_hi]; f16: values N(0,1)*0.02; bf16 / f32: N(0,1)*0.02."""
+    g = rng(seed, tid)
+    if fmt in ("f16", "bf16", "f32"):
+        x = (g.standard_normal(size=(V, D), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+        if fmt == "f16":
+            return x.astype(np.float16).view(np.uint8).reshape(V, -1)
+        if fmt == "bf16":
+            return bf16_bits(x).view(np.uint8).reshape(V, -1)
+        return x.view(np.uint8).reshape(V, -1)
+    nb = D // 32
+    bb = BLOCK[fmt]
+    t = np.empty((V, nb, bb), np.uint8)
+    d = g.uniform(scale_lo, scale_hi, size=(V, nb)).astype(np.float16)
+    t[:, :, 0:2] = d.view(np.uint8).reshape(V, nb, 2)
+    if fmt == "q8_0":
+        t[:, :, 2:34] = g.integers(-127, 128, size=(V, nb, 32), dtype=np.int8).view(np.uint8)
+    else:
+        off = 2
+        if fmt in ("q4_1", "q5_1"):
+            m = g.uniform(-scale_hi, scale_hi, size=(V, nb)).astype(np.float16)
+            t[:, :, 2:4] = m.view(np.uint8).reshape(V, nb, 2)
+            off = 4
+        t[:, :, off:] = g.integers(0, 256, size=(V, nb, bb - off), dtype=np.uint8)
+    return t.reshape(V, nb * bb)
+
+
+@dataclass(frozen=True)
+class Config:
+    name: str
+    description: str
+
+
+CONFIGS = {
+    "c1_rmsnorm_f32": Config("c1_rmsnorm_f32", "RMSNorm f32 x[512,1024], gamma ~ N(1,0.1), eps 1e-6 (Qwen3-0.6B)"),
+    "c2_add_rmsnorm_bf16": Config("c2_add_rmsnorm_bf16",
+                                  "residual add + RMSNorm bf16 x,res[8192,4096], gamma f32, eps 1e-5 (Llama-3-8B)"),
+    "c3_swiglu_bf16": Config("c3_swiglu_bf16", "SwiGLU bf16 gate,up[8192,14336] (Llama-3-8B FFN)"),
+    "c3_geglu_bf16": Config("c3_geglu_bf16", "GeGLU (tanh GELU) bf16 gate,up[8192,14336]"),
+    "c4_qknorm_rope_bf16": Config("c4_qknorm_rope_bf16",
+                                  "q[4096,32,128], k[4096,8,128] bf16: per-head RMSNorm + neox RoPE theta 1e6 (Qwen3-8B)"),
+    "c5_gather_q8_0": Config("c5_gather_q8_0", "gather 16384 ids from Q8_0 [151936,4096] -> bf16"),
+    "c5_gather_q4_0": Config("c5_gather_q4_0", "gather 16384 ids from Q4_0 [151936,4096] -> bf16"),
+    "c5_gather_f16": Config("c5_gather_f16", "gather 16384 ids from F16 [151936,4096] -> bf16"),
+}
+
+
+def c1(seed=0, rows=512, D=1024):
+    return dict(x=normal(seed, 0, (rows, D)), w=normal(seed, 1, (D,), 1.0, 0.1), eps=1e-6)
+
+
+def c2(seed=0, rows=8192, D=4096):
+    return dict(x=normal(seed, 0, (rows, D), dtype="bf16"), res=normal(seed, 1, (rows, D), dtype="bf16"),
+                w=normal(seed, 2, (D,), 1.0, 0.1), eps=1e-5)
+
+
+def c3(seed=0, rows=8192, cols=14336):
+    return dict(gate=normal(seed, 0, (rows, cols), dtype="bf16"), up=normal(seed, 1, (rows, cols), dtype="bf16"))
+
+
+def c4(seed=0, T=4096, Hq=32, Hk=8, D=128, max_pos=32768):
+    return dict(q=normal(seed, 0, (T, Hq, D), dtype="bf16"), k=normal(seed, 1, (T, Hk, D), dtype="bf16"),
+                wq=normal(seed, 2, (D,), 1.0, 0.1), wk=normal(seed, 3, (D,), 1.0, 0.1),
+                pos=rng(seed, 4).integers(0, max_pos, size=T, dtype=np.int32), eps=1e-6, base=1e6)
+
+
+def c5(fmt="q8_0", seed=0, V=151936, D=4096, N=16384):
+    return dict(table=quant_table(fmt, V, D, seed, 0), ids=rng(seed, 1).integers(0, V, size=N, dtype=np.int32),
+                V=V, D=D, fmt=fmt)

@@ -1,0 +1,68 @@
+"""Comparison rules of the parity tests.
+
+* f32 outputs: the reference's own rule ``|d| <= atol + rtol*|ref|`` (tests/Sharplight.Vulkan.Tests/Diff.cs:206)
+  with rtol = 1e-5 and atol = 1e-5 * RMS of the reference row, so near-zero outputs are not over-weighted.
+* bf16 outputs: at most ``ulp`` (default 2) units in the last place from bf16_RNE(oracle f32 result),
+  counted on the ordered integer line of bf16 codes (so -0 and +0 are 0 apart).
+* integer / byte / dequantized outputs: bit-exact.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+F32_RTOL = 1e-5
+F32_ATOL_ROW = 1e-5
+BF16_ULP = 2
+
+
+def bf16_ordered(bits: np.ndarray) -> np.ndarray:
+    b = np.asarray(bits, dtype=np.uint16).astype(np.int64)
+    return np.where(b & 0x8000, -(b & 0x7FFF), b)
+
+
+def bf16_ulp_diff(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    return np.abs(bf16_ordered(a) - bf16_ordered(b))
+
+
+def assert_bf16_close(got, ref, ulp: int = BF16_ULP, what: str = ""):
+    got = np.asarray(got, np.uint16)
+    ref = np.asarray(ref, np.uint16)
+    assert got.shape == ref.shape, (got.shape, ref.shape)
+    d = bf16_ulp_diff(got, ref)
+    if d.size and d.max() > ulp:
+        i = np.unravel_index(np.argmax(d), d.shape)
+        raise AssertionError(f"{what}: {int((d > ulp).sum())} of {d.size} bf16 values beyond {ulp} ulp; "
+                             f"worst at {i}: got {got[i]:#06x} ref {ref[i]:#06x} ({int(d[i])} ulp)")
+    return int(d.max()) if d.size else 0
+
+
+def assert_f32_close(got, ref, rtol=F32_RTOL, atol_row=F32_ATOL_ROW, what: str = ""):
+    got = np.asarray(got, np.float32)
+    ref = np.asarray(ref, np.float32)
+    assert got.shape == ref.shape, (got.shape, ref.shape)
+    if ref.size == 0:
+        return 0.0
+    r2 = ref.reshape(-1, ref.shape[-1]).astype(np.float64)
+    rms = np.sqrt(np.mean(r2 * r2, axis=1, keepdims=True))
+    atol = atol_row * np.broadcast_to(rms, r2.shape).reshape(ref.shape)
+    d = np.abs(got.astype(np.float64) - ref.astype(np.float64))
+    bad = ~(d <= atol + rtol * np.abs(ref.astype(np.float64)))
+    if bad.any():
+        i = np.unravel_index(np.argmax(bad), bad.shape)
+        raise AssertionError(f"{what}: {int(bad.sum())} of {bad.size} f32 values out of tolerance; first at {i}: "
+                             f"got {got[i]!r} ref {ref[i]!r}")
+    big = np.abs(ref) > 1e-3
+    return float((d[big] / np.abs(ref[big])).max()) if big.any() else 0.0
+
+
+def assert_bits_equal(got, ref, what: str = ""):
+    got = np.ascontiguousarray(got)
+    ref = np.ascontiguousarray(ref)
+    assert got.shape == ref.shape and got.dtype == ref.dtype, (got.shape, got.dtype, ref.shape, ref.dtype)
+    gv = got.view(np.uint8).reshape(-1, got.dtype.itemsize)
+    rv = ref.view(np.uint8).reshape(-1, ref.dtype.itemsize)
+    neq = np.any(gv != rv, axis=1)
+    if neq.any():
+        i = int(np.argmax(neq))
+        raise AssertionError(f"{what}: {int(neq.sum())} of {neq.size} values differ bitwise; first flat index {i}: "
+                             f"got {got.reshape(-1)[i]!r} ref {ref.reshape(-1)[i]!r}")

@@ -1,0 +1,144 @@
+"""GPU parity of slhip_rope (neox / normal RoPE, fused per-head q/k RMSNorm, q and k in one launch) against
+the oracle's RmsNorm-then-Rope (the reference's RopeTests.cs, GgmlCrossCheckTests.RopeMatchesGgml and
+FusionTests.cs:142-157 pattern: GPU vs CPU)."""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from sharplight_amd import native, synth
+from tests.devutil import Dev, log
+from tests.parity import assert_bf16_close, assert_f32_close
+
+pytestmark = pytest.mark.gpu
+
+NP = {"f32": np.float32, "bf16": np.uint16}
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def _run(din, dout, tensors, pos, D, *, pads=None, ff=None, **cfg):
+    """tensors: list of (x [T,H,D], w or None); returns list of outputs."""
+    T = len(pos)
+    with Dev() as d:
+        specs, outs = [], []
+        for i, (x, w) in enumerate(tensors):
+            pad = pads[i] if pads else 0
+            H = x.shape[1]
+            px = d.put(x, pad)
+            py = d.empty(x.size * np.dtype(NP[dout]).itemsize, pad)
+            specs.append(dict(x=px, y=py, heads=H, norm_w=d.put(w) if w is not None else None))
+            outs.append((py, x.shape))
+        pp = d.put(np.asarray(pos, np.int32))
+        pf = d.put(ff) if ff is not None else None
+        log(f"rope {din}->{dout} T={T} D={D} heads={[t[0].shape[1] for t in tensors]} cfg={cfg}")
+        native.rope(din, dout, specs, pp, T, D, ff=pf, **cfg)
+        native.synchronize()
+        return [d.get(py, shp, NP[dout]) for py, shp in outs]
+
+
+def _ref(din, dout, x, pos, w, eps, **kw):
+    y = oracle.qk_norm_rope(x, pos, w, eps, dtype="bf16" if din == "bf16" else "f32", **kw)
+    if din == "bf16" and dout == "f32":
+        return oracle.qk_norm_rope(oracle.from_bf16(x), pos, w, eps, **kw)
+    if din == "f32" and dout == "bf16":
+        return oracle.to_bf16(y)
+    return y
+
+
+def _check(dout, y, ref, what):
+    if dout == "bf16":
+        assert_bf16_close(y, ref, what=what)
+    else:
+        assert_f32_close(y, ref, what=what)
+
+
+def test_c4_qk_norm_rope(device):
+    """Qwen3-8B attention prologue, q [4096,32,128] and k [4096,8,128] bf16 in one launch:
+    per-head RMSNorm (eps 1e-6) then neox RoPE, theta 1e6, positions ~ U{0..32767}."""
+    c = synth.c4()
+    yq, yk = _run("bf16", "bf16", [(c["q"], c["wq"]), (c["k"], c["wk"])], c["pos"], 128, neox=True, base=c["base"],
+                  norm=True, eps=c["eps"])
+    assert_bf16_close(yq, oracle.qk_norm_rope(c["q"], c["pos"], c["wq"], c["eps"], dtype="bf16", base=c["base"]),
+                      what="C4 q")
+    assert_bf16_close(yk, oracle.qk_norm_rope(c["k"], c["pos"], c["wk"], c["eps"], dtype="bf16", base=c["base"]),
+                      what="C4 k")
+
+
+def test_rope_matches_ggml_fixture(device):
+    """The reference's ggml rope cases (normal, neox, neox with dims 8 of 16 and freq_scale 0.5), f32."""
+    fx = np.load(os.path.join(GOLDEN, "ggml_rope.npz"))
+    for k in range(3):
+        mode, dims, T, H, D = (int(v) for v in fx[f"case{k}_meta"])
+        fs = float(fx[f"case{k}_freq_scale"][0])
+        (y,) = _run("f32", "f32", [(fx[f"case{k}_x"], None)], fx[f"case{k}_pos"][:, 0], D, dims=dims,
+                    neox=mode == 2, base=10000.0, freq_scale=fs)
+        np.testing.assert_allclose(y, fx[f"case{k}_y"], rtol=2e-4, atol=2e-4)  # GgmlCrossCheckTests.cs:96
+        ref = oracle.rope(fx[f"case{k}_x"], fx[f"case{k}_pos"][:, 0], dims=dims, neox=mode == 2, base=10000.0,
+                          freq_scale=fs)
+        assert_f32_close(y, ref, what=f"ggml case {k}")
+
+
+@pytest.mark.parametrize("neox", [True, False])
+@pytest.mark.parametrize("din,dout", [("f32", "f32"), ("bf16", "bf16"), ("bf16", "f32"), ("f32", "bf16")])
+@pytest.mark.parametrize("norm", [False, True])
+def test_rope_variants(device, neox, din, dout, norm):
+    T, D = 29, 128
+    x = synth.normal(3, 0, (T, 4, D), std=2.0, dtype=din)
+    k = synth.normal(3, 1, (T, 2, D), dtype=din)
+    wq = synth.normal(3, 2, (D,), 1.0, 0.1) if norm else None
+    wk = synth.normal(3, 3, (D,), 1.0, 0.1) if norm else None
+    pos = synth.rng(3, 4).integers(0, 40000, T).astype(np.int32)
+    yq, yk = _run(din, dout, [(x, wq), (k, wk)], pos, D, neox=neox, base=1e6, norm=norm, eps=1e-6)
+    kw = dict(neox=neox, base=1e6)
+    eps = 1e-6
+    if norm:
+        _check(dout, yq, _ref(din, dout, x, pos, wq, eps, **kw), "q")
+        _check(dout, yk, _ref(din, dout, k, pos, wk, eps, **kw), "k")
+    else:
+        _check(dout, yq, _ref(din, dout, x, pos, None, eps, **kw), "q")
+        _check(dout, yk, _ref(din, dout, k, pos, None, eps, **kw), "k")
+
+
+@pytest.mark.parametrize("D,dims", [(64, 64), (256, 256), (16, 8), (96, 64), (80, 80), (128, 32)])
+def test_rope_head_sizes_and_partial_dims(device, D, dims):
+    """Other head sizes (vector path for dims == D with D/2 a multiple of the vector width, general path
+    otherwise) and partial rotation (dims < D: the tail is copied, normed when the norm is fused)."""
+    T = 13
+    x = synth.normal(D, 0, (T, 3, D), dtype="bf16")
+    w = synth.normal(D, 1, (D,), 1.0, 0.1)
+    pos = synth.rng(D, 2).integers(0, 32768, T).astype(np.int32)
+    for neox in (True, False):
+        for norm in (False, True):
+            (y,) = _run("bf16", "bf16", [(x, w if norm else None)], pos, D, dims=dims, neox=neox, base=1e4,
+                        norm=norm, eps=1e-6)
+            ref = oracle.qk_norm_rope(x, pos, w if norm else None, 1e-6, dtype="bf16", dims=dims, neox=neox,
+                                      base=1e4)
+            assert_bf16_close(y, ref, what=f"D={D} dims={dims} neox={neox} norm={norm}")
+
+
+def test_rope_freq_factors_and_scaling(device):
+    T, D = 17, 128
+    x = synth.normal(8, 0, (T, 2, D))
+    ff = synth.rng(8, 1).uniform(1, 8, D // 2).astype(np.float32)
+    pos = synth.rng(8, 2).integers(0, 100000, T).astype(np.int32)
+    (y,) = _run("f32", "f32", [(x, None)], pos, D, ff=ff, base=5e5, freq_scale=0.25, attn_factor=1.3)
+    ref = oracle.rope(x, pos, base=5e5, freq_scale=0.25, attn_factor=1.3, ff=ff)
+    assert_f32_close(y, ref, what="ff")
+
+
+def test_rope_unaligned_and_single_token(device):
+    x = synth.normal(1, 0, (1, 8, 128), dtype="bf16")
+    (y,) = _run("bf16", "bf16", [(x, None)], np.array([32767], np.int32), 128, pads=[2], base=1e6)
+    assert_bf16_close(y, oracle.qk_norm_rope(x, np.array([32767]), None, dtype="bf16", base=1e6), what="pad")
+
+
+def test_rope_position_zero_is_identity(device):
+    x = synth.normal(2, 0, (5, 4, 128))
+    (y,) = _run("f32", "f32", [(x, None)], np.zeros(5, np.int32), 128, base=1e6)
+    assert np.array_equal(y, x)
+
+
+def test_rope_empty(device):
+    native.rope("bf16", "bf16", [dict(x=16, y=16, heads=4)], 16, 0, 128)
+    native.synchronize()

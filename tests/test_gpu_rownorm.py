@@ -1,0 +1,170 @@
+"""GPU parity of slhip_rownorm (RMSNorm / L2Norm / LayerNorm, optional fused residual add) against the CPU
+oracle's unfused decomposition (Add, then RowOp), mirroring the reference's NormTests.cs, RowOpTests.cs
+and FusionTests.cs:18-26 (GPU vs CPU provider)."""
+import numpy as np
+import pytest
+
+import oracle
+from sharplight_amd import native, synth
+from tests.devutil import Dev, log
+from tests.parity import assert_bf16_close, assert_f32_close
+
+pytestmark = pytest.mark.gpu
+
+NP = {"f32": np.float32, "bf16": np.uint16}
+
+
+def _inputs(rows, D, din, seed, scale=1.0):
+    x = synth.normal(seed, 0, (rows, D), std=scale, dtype=din)
+    r = synth.normal(seed, 1, (rows, D), std=scale, dtype=din)
+    w = synth.normal(seed, 2, (D,), 1.0, 0.1)
+    b = synth.normal(seed, 3, (D,), 0.0, 0.5)
+    return x, r, w, b
+
+
+def _run(kind, din, dout, x, r, w, b, eps, *, with_res, with_h, pad=0, x_stride=None):
+    rows, D = x.shape
+    with Dev() as d:
+        xs = D if x_stride is None else x_stride
+        if xs != D:
+            xp = np.zeros((rows, xs), x.dtype)
+            xp[:, :D] = x
+        else:
+            xp = x
+        px = d.put(xp, pad)
+        pr = d.put(r, pad) if with_res else None
+        pw = d.put(w) if w is not None else None
+        pb = d.put(b) if b is not None else None
+        osz = np.dtype(NP[dout]).itemsize
+        py = d.empty(rows * D * osz, pad)
+        ph = d.empty(rows * D * np.dtype(NP[din]).itemsize, pad) if with_h else None
+        log(f"rownorm kind={kind} {din}->{dout} rows={rows} D={D} res={with_res} h={with_h} pad={pad} xs={xs}")
+        native.rownorm(kind, din, dout, px, py, rows, D, res=pr, w=pw, b=pb, h_out=ph, eps=eps, x_stride=xs)
+        native.synchronize()
+        y = d.get(py, (rows, D), NP[dout])
+        h = d.get(ph, (rows, D), NP[din]) if with_h else None
+    return y, h
+
+
+def _reference(kind, din, dout, x, r, w, b, eps, with_res):
+    xf = oracle.from_bf16(x) if din == "bf16" else x
+    if with_res:
+        rf = oracle.from_bf16(r) if din == "bf16" else r
+        hf = oracle.add(xf, rf)
+    else:
+        hf = xf
+    if kind == "layer":
+        yf = oracle.layernorm(hf, w, b, eps)
+    else:
+        yf = oracle.rmsnorm(hf, w if kind == "rms" else None, eps, mode=0 if kind == "rms" else 1)
+    y = oracle.to_bf16(yf) if dout == "bf16" else yf
+    h = oracle.to_bf16(hf) if din == "bf16" else hf
+    return y, h, yf
+
+
+def _check(dout, y, yref, what):
+    if dout == "bf16":
+        assert_bf16_close(y, yref, what=what)
+    else:
+        assert_f32_close(y, yref, what=what)
+
+
+def test_c1_rmsnorm_f32(device):
+    """RMSNorm f32 [512, 1024], gamma ~ N(1, 0.1), eps 1e-6, seed 0."""
+    c = synth.c1()
+    y, _ = _run("rms", "f32", "f32", c["x"], None, c["w"], None, c["eps"], with_res=False, with_h=False)
+    yref, _, _ = _reference("rms", "f32", "f32", c["x"], None, c["w"], None, c["eps"], False)
+    rel = assert_f32_close(y, yref, what="C1")
+    assert rel < 1e-5
+
+
+def test_c2_add_rmsnorm_bf16(device):
+    """residual add + RMSNorm bf16 [8192, 4096], gamma f32, eps 1e-5; y and h both bf16."""
+    c = synth.c2()
+    y, h = _run("rms", "bf16", "bf16", c["x"], c["res"], c["w"], None, c["eps"], with_res=True, with_h=True)
+    yref, href, _ = _reference("rms", "bf16", "bf16", c["x"], c["res"], c["w"], None, c["eps"], True)
+    assert_bf16_close(h, href, ulp=0, what="C2 h (x+res rounded once: exact)")
+    assert_bf16_close(y, yref, what="C2 y")
+
+
+CASES = [
+    # kind, din, dout, rows, D
+    ("rms", "f32", "f32", 3, 1),
+    ("rms", "f32", "f32", 5, 70),
+    ("rms", "f32", "f32", 33, 1024),
+    ("rms", "f32", "f32", 2, 2048),
+    ("rms", "bf16", "bf16", 7, 4096),
+    ("rms", "bf16", "f32", 9, 896),
+    ("rms", "f32", "bf16", 9, 5120),
+    ("rms", "bf16", "bf16", 1, 40960),
+    ("rms", "f32", "f32", 2, 70000),   # beyond the vector path: scalar kernel
+    ("l2", "f32", "f32", 6, 256),
+    ("l2", "bf16", "bf16", 6, 4100),   # D % 8 != 0: scalar kernel
+    ("layer", "f32", "f32", 5, 70),
+    ("layer", "f32", "f32", 197, 768),
+    ("layer", "f32", "f32", 4, 5000),
+    ("layer", "bf16", "bf16", 16, 4096),
+]
+
+
+@pytest.mark.parametrize("kind,din,dout,rows,D", CASES)
+@pytest.mark.parametrize("with_res", [False, True])
+def test_rownorm_matrix(device, kind, din, dout, rows, D, with_res):
+    x, r, w, b = _inputs(rows, D, din, seed=rows * 1000 + D, scale=3.0)
+    w = None if kind == "l2" else w
+    b = b if kind == "layer" else None
+    eps = 1e-5
+    y, h = _run(kind, din, dout, x, r, w, b, eps, with_res=with_res, with_h=with_res)
+    yref, href, _ = _reference(kind, din, dout, x, r, w, b, eps, with_res)
+    _check(dout, y, yref, f"{kind} {din}->{dout} [{rows},{D}] res={with_res}")
+    if with_res:
+        if din == "bf16":
+            assert_bf16_close(h, href, ulp=0, what="h")
+        else:
+            assert np.array_equal(h.view(np.uint32), href.view(np.uint32))
+
+
+def test_rownorm_without_weight_and_unaligned(device):
+    """RmsNorm without weight (RowOp's Simd.Scale branch) on tensors misaligned by 4 bytes (scalar path),
+    and with a padded x row stride (strided view of a wider tensor)."""
+    x, r, w, _ = _inputs(11, 512, "f32", seed=5)
+    y, _ = _run("rms", "f32", "f32", x, r, None, None, 1e-6, with_res=False, with_h=False, pad=4)
+    yref, _, _ = _reference("rms", "f32", "f32", x, r, None, None, 1e-6, False)
+    assert_f32_close(y, yref, what="unaligned")
+    y, _ = _run("rms", "f32", "f32", x, r, w, None, 1e-6, with_res=False, with_h=False, x_stride=520)
+    yref, _, _ = _reference("rms", "f32", "f32", x, r, w, None, 1e-6, False)
+    assert_f32_close(y, yref, what="strided")
+
+
+def test_rownorm_in_place_residual(device):
+    """y written over x and h over res (the residual stream updated in place), bf16."""
+    rows, D = 64, 4096
+    x, r, w, _ = _inputs(rows, D, "bf16", seed=9)
+    with Dev() as d:
+        px = d.put(x)
+        pr = d.put(r)
+        pw = d.put(w)
+        log("rownorm in-place residual")
+        native.rownorm("rms", "bf16", "bf16", px, px, rows, D, res=pr, w=pw, h_out=pr, eps=1e-6)
+        native.synchronize()
+        y = d.get(px, (rows, D), np.uint16)
+        h = d.get(pr, (rows, D), np.uint16)
+    yref, href, _ = _reference("rms", "bf16", "bf16", x, r, w, None, 1e-6, True)
+    assert_bf16_close(y, yref, what="in-place y")
+    assert_bf16_close(h, href, ulp=0, what="in-place h")
+
+
+def test_rownorm_zero_rows_is_noop(device):
+    native.rownorm("rms", "f32", "f32", None, None, 0, 1024)
+    native.synchronize()
+
+
+def test_rownorm_forced_row_groups(device, monkeypatch):
+    """Every row-group width of the vector kernel gives the same result (tuning override)."""
+    x, r, w, _ = _inputs(37, 4096, "bf16", seed=3)
+    yref, href, _ = _reference("rms", "bf16", "bf16", x, r, w, None, 1e-5, True)
+    for wpr in (1, 2, 4, 8, 16):
+        monkeypatch.setenv("SLHIP_ROWNORM_WPR", str(wpr))
+        y, h = _run("rms", "bf16", "bf16", x, r, w, None, 1e-5, with_res=True, with_h=True)
+        assert_bf16_close(y, yref, what=f"wpr={wpr}")
+        assert_bf16_close(h, href, ulp=0, what=f"h wpr={wpr}")

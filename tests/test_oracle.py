@@ -1,0 +1,333 @@
+"""Pins the CPU oracle before it is trusted as the checker of the HIP kernels.
+
+Each oracle function is checked against something independent of its own formula: the reference's
+ggml golden vectors (tests/golden, extracted from tests/Sharplight.Cpu.Tests/Fixtures), an exhaustive
+or brute-force enumeration, a closed form in f64, a library routine (numpy, torch, math.erf) or an
+invariant -- chosen so that a dropped term, a wrong sign, a swapped pair index or an off-by-one in the
+block layouts fails.
+"""
+import math
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from sharplight_amd import synth
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+@pytest.fixture(scope="module")
+def quant_fx():
+    return np.load(os.path.join(GOLDEN, "ggml_quant.npz"))
+
+
+@pytest.fixture(scope="module")
+def rope_fx():
+    return np.load(os.path.join(GOLDEN, "ggml_rope.npz"))
+
+
+# ---- dequantization: ggml golden vectors (QuantTests.DequantizeMatchesGgml, QuantTests.cs:49-69) ----
+
+@pytest.mark.parametrize("fmt", ["q8_0", "q4_0", "q4_1", "q5_0", "q5_1"])
+def test_dequant_matches_ggml(quant_fx, fmt):
+    rows, cols = quant_fx[f"{fmt}_shape"]
+    got = oracle.dequant(fmt, quant_fx[f"{fmt}_blocks"].reshape(-1), rows * cols).reshape(rows, cols)
+    ref = quant_fx[f"{fmt}_deq"]
+    # Equal as values: ggml computes (q-8)*d, which is -0 for q = 8 and d < 0; the reference (and the
+    # oracle) compute fma(q, d, -8d) = +0. Every nonzero value is bit-identical.
+    np.testing.assert_array_equal(got, ref)
+    nz = ref != 0
+    assert np.array_equal(got[nz].view(np.uint32), ref[nz].view(np.uint32))
+    src = quant_fx[f"{fmt}_src"]
+    assert float(np.sum((src - got) ** 2) / np.sum(src ** 2)) < 0.05  # the fixture is a real quantization
+
+
+@pytest.mark.parametrize("fmt", ["q8_0", "q4_0", "q4_1", "q5_0", "q5_1"])
+def test_gather_dequantizes_fixture_rows(quant_fx, fmt):
+    """QuantTests.GatherDequantizes (QuantTests.cs:71-95): rows [3, 0, 2, 2] of the fixture table."""
+    rows, cols = quant_fx[f"{fmt}_shape"]
+    y = oracle.gather(fmt, quant_fx[f"{fmt}_blocks"], rows, cols, np.array([3, 0, 2, 2], np.int32))
+    np.testing.assert_array_equal(y, quant_fx[f"{fmt}_deq"][[3, 0, 2, 2]])
+
+
+def test_gather_out_of_range_raises():
+    """QuantTests.GatherOutOfRangeThrows (QuantTests.cs:97): GatherOp checks every id."""
+    t = np.zeros((4, 8), np.float32).view(np.uint8)
+    for bad in (4, -1, 1 << 30):
+        with pytest.raises(oracle.OutOfRange):
+            oracle.gather("f32", t, 4, 8, np.array([0, bad], np.int32))
+
+
+def _f16_codes():
+    return np.arange(65536, dtype=np.uint32).astype(np.uint16)
+
+
+def test_f16_to_f32_exhaustive():
+    """All 65,536 binary16 codes against numpy's conversion (subnormals, infinities, NaN payloads)."""
+    h = _f16_codes()
+    got = oracle.f16_bits_to_f32(h)
+    ref = h.view(np.float16).astype(np.float32)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def _scale_codes():
+    """f16 scale codes: normal, subnormal, negative, tiny and large (no inf/NaN)."""
+    return np.array([0x3C00, 0x2E66, 0x1A36, 0x0001, 0x03FF, 0x0400, 0x8001, 0xBC00, 0xA0A4, 0x7BFF, 0xFBFF, 0x0000,
+                     0x8000], np.uint16)
+
+
+def test_q8_0_brute_force():
+    """Every int8 code at every scale: q * d exactly; a zero product is +0 (fma(q, d, +0))."""
+    codes = np.arange(-128, 128, dtype=np.int32)
+    for s in _scale_codes():
+        blocks = np.zeros((8, 34), np.uint8)
+        blocks[:, 0:2] = np.frombuffer(np.uint16(s).tobytes(), np.uint8)
+        blocks[:, 2:] = codes.astype(np.int8).view(np.uint8).reshape(8, 32)
+        got = oracle.dequant("q8_0", blocks.reshape(-1), 256)
+        d = np.float32(np.uint16(s).view(np.float16))
+        ref = codes.astype(np.float32) * d
+        ref[ref == 0] = 0.0
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), hex(s)
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "q4_1", "q5_0", "q5_1"])
+def test_nibble_formats_brute_force(fmt):
+    """Every nibble (and high bit) in every position: (q - 8) d, (q - 16) d, q d + m."""
+    bb = synth.BLOCK[fmt]
+    qs_off = {"q4_0": 2, "q4_1": 4, "q5_0": 6, "q5_1": 8}[fmt]
+    five = fmt.startswith("q5")
+    rng = np.random.default_rng(7)
+    for s in _scale_codes():
+        m_code = np.uint16(0xB266)  # m = -0.2
+        blocks = np.zeros((16, bb), np.uint8)
+        blocks[:, 0:2] = np.frombuffer(np.uint16(s).tobytes(), np.uint8)
+        if fmt in ("q4_1", "q5_1"):
+            blocks[:, 2:4] = np.frombuffer(m_code.tobytes(), np.uint8)
+        blocks[:, qs_off:] = rng.integers(0, 256, size=(16, bb - qs_off), dtype=np.uint8)
+        blocks[0, qs_off:] = np.arange(16, dtype=np.uint8) * 17  # every nibble, both halves
+        if five:
+            blocks[:, qs_off - 4:qs_off] = rng.integers(0, 256, size=(16, 4), dtype=np.uint8)
+        got = oracle.dequant(fmt, blocks.reshape(-1), 16 * 32).reshape(16, 32)
+        d = np.float32(np.uint16(s).view(np.float16))
+        m = np.float32(m_code.view(np.float16))
+        for b in range(16):
+            qs = blocks[b, qs_off:qs_off + 16].astype(np.int64)
+            q = np.concatenate([qs & 15, qs >> 4])
+            if five:
+                qh = int(np.frombuffer(blocks[b, qs_off - 4:qs_off].tobytes(), np.uint32)[0])
+                q = q | (((qh >> np.arange(32)) & 1) << 4)
+            if fmt == "q4_0":
+                ref = (q - 8).astype(np.float32) * d
+            elif fmt == "q5_0":
+                ref = (q - 16).astype(np.float32) * d
+            else:
+                ref = (q.astype(np.float64) * np.float64(d) + np.float64(m)).astype(np.float32)
+            np.testing.assert_array_equal(got[b], ref, err_msg=f"{fmt} scale {s:#x} block {b}")
+
+
+# ---- f32 -> bf16 --------------------------------------------------------------------------------------
+
+def test_bf16_rounding_matches_torch():
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(1)
+    x = np.concatenate([rng.standard_normal(100000).astype(np.float32) * np.float32(10) ** rng.integers(-40, 38, 100000).astype(np.float32),
+                        np.array([0.0, -0.0, np.inf, -np.inf, 1.0, 3.4028235e38, 1e-45, -1e-45,
+                                  1.00390625, 1.01171875, 1.0039063, 1.0117188], np.float32)])
+    # exact ties: mantissa ending in 0x8000 with both parities of the kept lsb
+    ties = (np.arange(1000, dtype=np.uint32) << np.uint32(16) | np.uint32(0x8000)) + np.uint32(0x3F800000)
+    x = np.concatenate([x, ties.view(np.float32)])
+    got = oracle.to_bf16(x)
+    ref = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, ref)
+    assert np.array_equal(got, synth.bf16_bits(x))
+
+
+def test_bf16_nan_quieting():
+    """Simd.FloatToBFloat: a NaN keeps its top half with the quiet bit set."""
+    nans = np.array([0x7F800001, 0x7FC00000, 0xFF800001, 0x7FBFFFFF, 0xFFFFFFFF], np.uint32).view(np.float32)
+    got = oracle.to_bf16(nans)
+    ref = ((nans.view(np.uint32) >> 16) | 0x40).astype(np.uint16)
+    assert np.array_equal(got, ref)
+    assert np.array_equal(oracle.from_bf16(got).view(np.uint32) >> 16, got.astype(np.uint32))
+
+
+# ---- norms --------------------------------------------------------------------------------------------
+
+def _rms_f64(x, w, eps, mode=0):
+    x = x.astype(np.float64)
+    ss = (x * x).sum(-1, keepdims=True)
+    s = 1.0 / np.sqrt(ss / x.shape[-1] + eps) if mode == 0 else 1.0 / np.sqrt(ss + eps)
+    y = x * s
+    return y * w if w is not None else y
+
+
+@pytest.mark.parametrize("n", [1, 7, 16, 70, 1024, 4099])
+def test_rmsnorm_closed_form(n):
+    """Ref.RmsNorm (tests/Sharplight.Cpu.Tests/Ref.cs:6-23): f64 scale; the reference tolerance is 1e-5/1e-4."""
+    rng = np.random.default_rng(n)
+    x = (rng.standard_normal((5, n)) * 3).astype(np.float32)
+    w = rng.standard_normal(n).astype(np.float32)
+    got = oracle.rmsnorm(x, w, 1e-5)
+    np.testing.assert_allclose(got, _rms_f64(x, w, 1e-5), rtol=2e-6, atol=1e-6)
+    np.testing.assert_allclose(oracle.rmsnorm(x, None, 1e-5), _rms_f64(x, None, 1e-5), rtol=2e-6, atol=1e-6)
+    np.testing.assert_allclose(oracle.rmsnorm(x, None, 1e-6, mode=1), _rms_f64(x, None, 1e-6, 1), rtol=2e-6, atol=1e-7)
+
+
+def test_rmsnorm_invariants():
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((16, 512)).astype(np.float32)
+    y = oracle.rmsnorm(x, None, 0.0)
+    np.testing.assert_allclose(np.sqrt((y.astype(np.float64) ** 2).mean(-1)), 1.0, rtol=1e-6)  # unit RMS
+    np.testing.assert_allclose(oracle.rmsnorm(x * np.float32(8), None, 0.0), y, rtol=1e-6, atol=1e-7)  # scale-free
+    # eps is added to the mean square, not the sum: a zero row stays zero, a constant row c -> c/sqrt(c^2+eps)
+    c = np.full((1, 64), 0.01, np.float32)
+    np.testing.assert_allclose(oracle.rmsnorm(c, None, 1e-4), 0.01 / math.sqrt(1e-4 + 1e-4), rtol=1e-6)
+
+
+def _layernorm_f64(x, w, b, eps):
+    """ViewAndNormTests.Norms' LayerNorm reference (ViewAndNormTests.cs:161-182)."""
+    x = x.astype(np.float64)
+    m = x.mean(-1, keepdims=True)
+    v = ((x - m) ** 2).mean(-1, keepdims=True)
+    y = (x - m) / np.sqrt(v + eps)
+    if w is not None:
+        y = y * w
+    if b is not None:
+        y = y + b
+    return y
+
+
+@pytest.mark.parametrize("n", [1, 8, 70, 768, 5000])
+def test_layernorm_closed_form(n):
+    rng = np.random.default_rng(n + 1)
+    x = (rng.standard_normal((5, n)) * 3 + 1).astype(np.float32)
+    w = rng.standard_normal(n).astype(np.float32)
+    b = rng.standard_normal(n).astype(np.float32)
+    np.testing.assert_allclose(oracle.layernorm(x, w, b, 1e-5), _layernorm_f64(x, w, b, 1e-5), rtol=1e-5, atol=1e-5)
+    y = oracle.layernorm(x, None, None, 1e-5)
+    if n > 1:
+        assert np.abs(y.astype(np.float64).mean(-1)).max() < 1e-5  # zero mean
+        np.testing.assert_allclose((y.astype(np.float64) ** 2).mean(-1), 1.0, rtol=1e-3)
+
+
+def test_row_ops_threaded_match_single_thread():
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((300, 1000)).astype(np.float32)
+    w = rng.standard_normal(1000).astype(np.float32)
+    oracle.set_threads(4)
+    try:
+        assert np.array_equal(oracle.rmsnorm(x, w, 1e-6, threads=4), oracle.rmsnorm(x, w, 1e-6))
+        assert np.array_equal(oracle.layernorm(x, w, w, 1e-6, threads=4), oracle.layernorm(x, w, w, 1e-6))
+        g = rng.standard_normal(200000).astype(np.float32)
+        assert np.array_equal(oracle.unary("silu", g, threads=4), oracle.unary("silu", g))
+    finally:
+        oracle.set_threads(1)
+
+
+# ---- activations --------------------------------------------------------------------------------------
+
+def _x_activations():
+    rng = np.random.default_rng(11)
+    return np.concatenate([rng.standard_normal(4000).astype(np.float32) * 3,
+                           np.linspace(-12, 12, 4001, dtype=np.float32)[:4000]])
+
+
+def test_silu_closed_form():
+    x = _x_activations()
+    ref = x.astype(np.float64) / (1 + np.exp(-x.astype(np.float64)))
+    np.testing.assert_allclose(oracle.unary("silu", x), ref, rtol=1e-6, atol=1e-7)  # Ref.Silu, Ref.cs:65
+
+
+def test_gelu_tanh_closed_form():
+    x = _x_activations()
+    xd = x.astype(np.float64)
+    ref = 0.5 * xd * (1 + np.tanh(0.7978845608028654 * (xd + 0.044715 * xd ** 3)))
+    got = oracle.unary("gelu_tanh", x)
+    np.testing.assert_allclose(got, ref, rtol=2e-6, atol=1e-7)
+    # the tail form (n % 8 elements) agrees with the vector form
+    got7 = oracle.unary("gelu_tanh", x[:7])
+    np.testing.assert_allclose(got7, ref[:7], rtol=2e-6, atol=1e-6)
+
+
+def test_gelu_erf_closed_form():
+    x = _x_activations()
+    ref = np.array([0.5 * v * (1 + math.erf(v / math.sqrt(2))) for v in x.astype(np.float64)])
+    # 1 + erf cancels for x << 0, so the f32 result carries the rational's ~1e-7 absolute error times |x|/2
+    np.testing.assert_allclose(oracle.unary("gelu_erf", x), ref, rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(oracle.unary("gelu_erf", x[:5]), ref[:5], rtol=1e-6, atol=2e-7)
+
+
+def test_erf_implementations():
+    for v in np.linspace(-7, 7, 2801):
+        assert abs(oracle.lib().orc_erf(float(v)) - math.erf(v)) < 2e-15
+        assert abs(oracle.lib().orc_erf_rational(float(v)) - math.erf(float(np.float32(v)))) < 4e-7
+
+
+# ---- rope ---------------------------------------------------------------------------------------------
+
+def test_rope_matches_ggml(rope_fx):
+    """GgmlCrossCheckTests.RopeMatchesGgml (GgmlCrossCheckTests.cs:75-98), single-axis cases: normal (mode
+    0), neox (mode 2), neox with partial dims and freq_scale 0.5. Reference tolerance 2e-4."""
+    for k in range(3):
+        mode, dims, T, H, D = (int(v) for v in rope_fx[f"case{k}_meta"])
+        assert mode in (0, 2)
+        got = oracle.rope(rope_fx[f"case{k}_x"], rope_fx[f"case{k}_pos"][:, 0], dims=dims, neox=mode == 2,
+                          base=10000.0, freq_scale=float(rope_fx[f"case{k}_freq_scale"][0]))
+        ref = rope_fx[f"case{k}_y"]
+        np.testing.assert_allclose(got, ref, rtol=2e-4, atol=2e-4)
+        assert np.abs(got - ref).max() < 1e-5
+
+
+def _rope_f64(x, pos, dims, neox, base, fs=1.0, af=1.0, ff=None):
+    T, H, D = x.shape
+    half = dims // 2
+    inv = base ** (-2.0 * np.arange(half) / dims) * fs
+    th = pos.astype(np.float64)[:, None] * inv[None, :]
+    if ff is not None:
+        th = th / ff.astype(np.float64)
+    c, s = np.cos(th) * af, np.sin(th) * af
+    y = x.astype(np.float64).copy()
+    i0 = np.arange(half) if neox else 2 * np.arange(half)
+    i1 = i0 + half if neox else i0 + 1
+    x0, x1 = x[:, :, i0].astype(np.float64), x[:, :, i1].astype(np.float64)
+    y[:, :, i0] = x0 * c[:, None, :] - x1 * s[:, None, :]
+    y[:, :, i1] = x0 * s[:, None, :] + x1 * c[:, None, :]
+    return y
+
+
+@pytest.mark.parametrize("neox", [True, False])
+def test_rope_closed_form_large_positions(neox):
+    """Qwen3 shape, theta 1e6, positions up to 32767: f64 angles keep the f32 result within 1e-5."""
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((64, 4, 128)).astype(np.float32)
+    pos = rng.integers(0, 32768, 64).astype(np.int32)
+    pos[0] = 32767
+    got = oracle.rope(x, pos, neox=neox, base=1e6)
+    np.testing.assert_allclose(got, _rope_f64(x, pos, 128, neox, 1e6), rtol=1e-5, atol=1e-5)
+    ff = rng.uniform(1, 8, 64).astype(np.float32)
+    got = oracle.rope(x, pos, neox=neox, base=1e6, freq_scale=0.25, attn_factor=1.5, ff=ff)
+    np.testing.assert_allclose(got, _rope_f64(x, pos, 128, neox, 1e6, 0.25, 1.5, ff), rtol=1e-5, atol=1e-5)
+
+
+def test_rope_invariants():
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((8, 3, 64)).astype(np.float32)
+    assert np.array_equal(oracle.rope(x, np.zeros(8, np.int32), base=1e4), x)  # position 0: identity
+    y = oracle.rope(x, rng.integers(0, 5000, 8).astype(np.int32), base=1e4)
+    n0 = x[..., :32] ** 2 + x[..., 32:] ** 2
+    n1 = y[..., :32] ** 2 + y[..., 32:] ** 2
+    np.testing.assert_allclose(n1, n0, rtol=1e-5, atol=1e-6)  # each neox pair keeps its norm
+    yp = oracle.rope(x, np.full(8, 100, np.int32), dims=16, base=1e4)
+    assert np.array_equal(yp[..., 16:], x[..., 16:])  # dims past `dims` are copied
+
+
+def test_qk_norm_rope_composition():
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal((16, 4, 128)).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(128)).astype(np.float32)
+    pos = rng.integers(0, 32768, 16).astype(np.int32)
+    got = oracle.qk_norm_rope(x, pos, w, 1e-6, base=1e6)
+    ref = _rope_f64(_rms_f64(x, w, 1e-6).astype(np.float32), pos, 128, True, 1e6)
+    np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-5)
