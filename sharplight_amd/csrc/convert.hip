@@ -10,11 +10,11 @@ __device__ __forceinline__ void cvt8(const void* x, void* y, int64_t i8)
 {
     float f[8];
     if (DI == SLHIP_F32) {
-        const uint4* p = static_cast<const uint4*>(x) + 2 * i8;
-        Vec<SLHIP_F32>::unpack(p[0], f);
-        Vec<SLHIP_F32>::unpack(p[1], f + 4);
+        const char* p = static_cast<const char*>(x) + 32 * i8;
+        Vec<SLHIP_F32>::unpack(load_nt(p), f);
+        Vec<SLHIP_F32>::unpack(load_nt(p + 16), f + 4);
     } else {
-        Vec<DI>::unpack(static_cast<const uint4*>(x)[i8], f);
+        Vec<DI>::unpack(load_nt(static_cast<const char*>(x) + 16 * i8), f);
     }
     store_packed<DO, 8>(static_cast<char*>(y) + i8 * 8 * Vec<DO>::BYTES, f);
 }

@@ -92,8 +92,8 @@ __global__ __launch_bounds__(256) void gated_vec(GatedArgs a)
                 oi[k] = r * a.os + c;
             }
             if (ok[k]) {
-                gr[k] = *reinterpret_cast<const uint4*>(static_cast<const char*>(a.g) + gi[k] * VI::BYTES);
-                ur[k] = *reinterpret_cast<const uint4*>(static_cast<const char*>(a.u) + ui[k] * VI::BYTES);
+                gr[k] = load_nt(static_cast<const char*>(a.g) + gi[k] * VI::BYTES);
+                ur[k] = load_nt(static_cast<const char*>(a.u) + ui[k] * VI::BYTES);
             }
         }
 #pragma unroll

@@ -151,8 +151,8 @@ __global__ __launch_bounds__(256) void gather_quant(GatherArgs a)
             const int nb = static_cast<int>(nblocks - b0 < kChunkBlocks ? nblocks - b0 : kChunkBlocks);
             const int nvec16 = nb * BB / 16;  // chunk starts and lengths are multiples of 16 bytes
             if (live && !bad) {
-                const uint4* g = reinterpret_cast<const uint4*>(src + b0 * BB);
-                for (int i = lane; i < nvec16; i += 64) reinterpret_cast<uint4*>(s)[i] = g[i];
+                const uint8_t* g = src + b0 * BB;
+                for (int i = lane; i < nvec16; i += 64) reinterpret_cast<uint4*>(s)[i] = load_nt(g + 16 * i);
             }
             __syncthreads();
             if (live) {
@@ -191,14 +191,13 @@ __global__ __launch_bounds__(256) void gather_plain(GatherArgs a)
 #pragma unroll
                 for (int e = 0; e < 8; e++) f[e] = 0.f;
             } else if (FMT == SLHIP_FMT_F32) {
-                const uint4* g = reinterpret_cast<const uint4*>(src) + 2 * v;
-                uint4 p0 = g[0], p1 = g[1];
+                uint4 p0 = load_nt(src + 32 * v), p1 = load_nt(src + 32 * v + 16);
                 Vec<SLHIP_F32>::unpack(p0, f);
                 Vec<SLHIP_F32>::unpack(p1, f + 4);
             } else if (FMT == SLHIP_FMT_F16) {
-                Vec<SLHIP_F16>::unpack(reinterpret_cast<const uint4*>(src)[v], f);
+                Vec<SLHIP_F16>::unpack(load_nt(src + 16 * v), f);
             } else {
-                Vec<SLHIP_BF16>::unpack(reinterpret_cast<const uint4*>(src)[v], f);
+                Vec<SLHIP_BF16>::unpack(load_nt(src + 16 * v), f);
             }
             store8<DTO>(a.y, row * a.ys + v * 8, f);
         }

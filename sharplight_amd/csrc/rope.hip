@@ -11,17 +11,25 @@
 //   elements from dims to D are copied (normed when the norm is fused).
 // The angles are f64 because positions reach 32767 and more: an f32 argument would be off by ~1e-3 rad.
 //
-// Layout: one block per token. The block first computes the token's dims/2 (cos, sin) pairs once in
-// LDS (f64 pow/sincos, one lane per pair), shared by every head of every tensor. Then each head row is
-// handled by L lanes (L = dims/2 / V, V = elements per 16-byte vector): lane c of a head holds pairs
-// [c*V, c*V + V) as two 16-byte vectors, so a wave covers 64/L whole heads with fully used 16-byte
-// loads and stores, and the fused norm is a butterfly over the L lanes of the head.
+// Layout: one block per group of tokens. The block computes each token's dims/2 (cos, sin) pairs once
+// in LDS (f64 sincos of f64 angles; the inverse frequencies come from the host in f64), shared by every
+// head of every tensor; the first loads are issued before that work so their latency overlaps it. Each
+// head row is handled by L lanes (L = dims/2 / V, V = elements per 16-byte vector): lane c of a head
+// holds pairs [c*V, c*V + V) as two 16-byte vectors, so a wave covers 64/L whole heads with fully used
+// 16-byte loads and stores, and the fused norm is a butterfly over the L lanes of the head.
 #include "common.hpp"
+#include "rope_math.hpp"
+
+#include <stdlib.h>
+
+#include <cmath>
 
 namespace slhip {
 
 constexpr int kMaxRopeTensors = 4;
-constexpr int kMaxHalf = 512;  // dims <= 1024
+constexpr int kMaxHalf = 512;    // dims <= 1024
+constexpr int kArgInv = 128;     // inverse frequencies passed from the host when dims/2 <= this
+constexpr int kTableEntries = 1024;  // (cos, sin) pairs per block: tokens_per_block * dims/2
 
 struct RopeTensorDev {
     const void* x;
@@ -38,22 +46,30 @@ struct RopeArgs {
     const int32_t* pos;
     const float* ff;
     int64_t T, D;
-    int dims, neox, norm;
+    int dims, neox, norm, tpb;  // tpb: tokens per block
     float base, fs, af, eps;
+    int host_inv;              // inv[] holds base^(-2i/dims)*freq_scale, computed on the host in f64
+    double inv[kArgInv];
 };
 
-// The token's (cos, sin) table in LDS; every thread of the block must call it.
-__device__ __forceinline__ void build_table(const RopeArgs& a, int64_t t, float2* cs)
+// The block's (cos, sin) tables in LDS, one per token t0 .. t0+tpb-1; every thread must call it.
+// HOST_INV: the inverse frequencies are in a.inv (always so on the vector path).
+template <bool HOST_INV>
+__device__ __forceinline__ void build_table(const RopeArgs& a, int64_t t0, float2* cs)
 {
     const int half = a.dims / 2;
-    const double p = static_cast<double>(a.pos[t]);
-    for (int i = threadIdx.x; i < half; i += blockDim.x) {
-        double inv = pow(static_cast<double>(a.base), -2.0 * i / a.dims) * static_cast<double>(a.fs);
-        double theta = p * inv;
+    for (int e = threadIdx.x; e < a.tpb * half; e += blockDim.x) {
+        const int tl = e / half, i = e - tl * half;
+        const int64_t t = t0 + tl;
+        if (t >= a.T) continue;
+        const double inv = (HOST_INV || a.host_inv)
+                               ? a.inv[i]
+                               : pow(static_cast<double>(a.base), -2.0 * i / a.dims) * static_cast<double>(a.fs);
+        double theta = static_cast<double>(a.pos[t]) * inv;
         if (a.ff) theta /= static_cast<double>(a.ff[i]);
         double s, c;
-        sincos(theta, &s, &c);
-        cs[i] = make_float2(static_cast<float>(c) * a.af, static_cast<float>(s) * a.af);
+        sincos_f64(theta, &s, &c);
+        cs[e] = make_float2(static_cast<float>(c) * a.af, static_cast<float>(s) * a.af);
     }
     __syncthreads();
 }
@@ -67,28 +83,72 @@ __device__ __forceinline__ int tensor_of(const RopeArgs& a, int64_t gh)
     return k;
 }
 
+// Work item `idx` of the block: token t0 + idx / lpt, head (idx % lpt) / L, chunk idx % L.
+template <int DTI, int L>
+struct RopeItem {
+    int64_t t;
+    int tl, c, k;
+    int64_t h;
+    __device__ __forceinline__ RopeItem(const RopeArgs& a, int64_t t0, int idx)
+    {
+        const int lpt = static_cast<int>(a.total_heads) * L;
+        tl = idx / lpt;
+        const int rem = idx - tl * lpt;
+        const int64_t gh = rem / L;
+        c = rem - static_cast<int>(gh) * L;
+        t = t0 + tl;
+        k = tensor_of(a, gh);
+        h = gh - a.t[k].head0;
+    }
+};
+
 template <int DTI, int DTO, int L>
 __global__ __launch_bounds__(1024) void rope_vec(RopeArgs a)
 {
     using VI = Vec<DTI>;
     constexpr int V = VI::N;
-    __shared__ float2 cs[kMaxHalf];
-    const int64_t t = blockIdx.x;
-    build_table(a, t, cs);
-
-    const int c = threadIdx.x % L;  // chunk of the head row owned by this lane
+    __shared__ float2 cs[kTableEntries];
     const int half = a.dims / 2;
-    for (int64_t gh = threadIdx.x / L; gh < a.total_heads; gh += blockDim.x / L) {
-        const int k = tensor_of(a, gh);
-        const RopeTensorDev& tt = a.t[k];
-        const int64_t h = gh - tt.head0;
-        const char* xr = static_cast<const char*>(tt.x) + (t * tt.xst + h * tt.xsh) * VI::BYTES;
-        char* yr = static_cast<char*>(tt.y) + (t * tt.yst + h * tt.ysh) * Vec<DTO>::BYTES;
-        // element offsets of the two vectors: neox (cV, half + cV); normal (2cV, 2cV + V)
-        const int e0 = a.neox ? c * V : 2 * c * V;
-        const int e1 = a.neox ? half + c * V : 2 * c * V + V;
-        uint4 r0 = *reinterpret_cast<const uint4*>(xr + e0 * VI::BYTES);
-        uint4 r1 = *reinterpret_cast<const uint4*>(xr + e1 * VI::BYTES);
+    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * a.tpb;
+    const int items = a.tpb * static_cast<int>(a.total_heads) * L;
+
+    // element offsets of a lane's two vectors: neox (cV, half + cV); normal (2cV, 2cV + V)
+    auto offsets = [&](int c, int& e0, int& e1) {
+        e0 = a.neox ? c * V : 2 * c * V;
+        e1 = a.neox ? half + c * V : 2 * c * V + V;
+    };
+    auto in_row = [&](const RopeItem<DTI, L>& it) {
+        const RopeTensorDev& tt = a.t[it.k];
+        return static_cast<const char*>(tt.x) + (it.t * tt.xst + it.h * tt.xsh) * VI::BYTES;
+    };
+
+    // The first item's loads are issued before the table is built, so their latency overlaps the f64 work.
+    int idx = threadIdx.x;
+    uint4 r0 = make_uint4(0, 0, 0, 0), r1 = r0;
+    if (idx < items) {
+        RopeItem<DTI, L> it(a, t0, idx);
+        if (it.t < a.T) {
+            int e0, e1;
+            offsets(it.c, e0, e1);
+            const char* xr = in_row(it);
+            r0 = load_nt(xr + e0 * VI::BYTES);
+            r1 = load_nt(xr + e1 * VI::BYTES);
+        }
+    }
+    build_table<true>(a, t0, cs);
+
+    for (bool first = true; idx < items; idx += blockDim.x, first = false) {
+        RopeItem<DTI, L> it(a, t0, idx);
+        if (it.t >= a.T) continue;
+        const RopeTensorDev& tt = a.t[it.k];
+        int e0, e1;
+        offsets(it.c, e0, e1);
+        if (!first) {
+            const char* xr = in_row(it);
+            r0 = load_nt(xr + e0 * VI::BYTES);
+            r1 = load_nt(xr + e1 * VI::BYTES);
+        }
+        char* yr = static_cast<char*>(tt.y) + (it.t * tt.yst + it.h * tt.ysh) * Vec<DTO>::BYTES;
         float f[2 * V];
         VI::unpack(r0, f);
         VI::unpack(r1, f + V);
@@ -115,11 +175,12 @@ __global__ __launch_bounds__(1024) void rope_vec(RopeArgs a)
                 }
             }
         }
+        const float2* ct = cs + it.tl * half + it.c * V;
         float o[2 * V];
         if (a.neox) {
 #pragma unroll
             for (int e = 0; e < V; e++) {
-                const float2 cv = cs[c * V + e];
+                const float2 cv = ct[e];
                 const float x0 = f[e], x1 = f[V + e];
                 o[e] = x0 * cv.x - x1 * cv.y;
                 o[V + e] = x0 * cv.y + x1 * cv.x;
@@ -127,7 +188,7 @@ __global__ __launch_bounds__(1024) void rope_vec(RopeArgs a)
         } else {
 #pragma unroll
             for (int e = 0; e < V; e++) {
-                const float2 cv = cs[c * V + e];
+                const float2 cv = ct[e];
                 const float x0 = f[2 * e], x1 = f[2 * e + 1];
                 o[2 * e] = x0 * cv.x - x1 * cv.y;
                 o[2 * e + 1] = x0 * cv.y + x1 * cv.x;
@@ -142,9 +203,9 @@ __global__ __launch_bounds__(1024) void rope_vec(RopeArgs a)
 template <int DTI, int DTO>
 __global__ __launch_bounds__(256) void rope_scalar(RopeArgs a)
 {
-    __shared__ float2 cs[kMaxHalf];
-    const int64_t t = blockIdx.x;
-    build_table(a, t, cs);
+    __shared__ float2 cs[kTableEntries];
+    const int64_t t = blockIdx.x;  // one token per block (tpb == 1)
+    build_table<false>(a, t, cs);
     const int lane = threadIdx.x & 63;
     const int half = a.dims / 2;
     for (int64_t gh = threadIdx.x >> 6; gh < a.total_heads; gh += blockDim.x >> 6) {
@@ -182,28 +243,44 @@ __global__ __launch_bounds__(256) void rope_scalar(RopeArgs a)
     }
 }
 
+static int env_int(const char* name, int dflt)
+{
+    const char* s = getenv(name);
+    return s && *s ? atoi(s) : dflt;
+}
+
 template <int DTI, int DTO>
-static int dispatch(const RopeArgs& a, bool vec_ok, hipStream_t st)
+static int dispatch(RopeArgs a, bool vec_ok, hipStream_t st)
 {
     constexpr int V = Vec<DTI>::N;
     const int half = a.dims / 2;
-    dim3 grid(static_cast<unsigned>(a.T));
-    if (vec_ok && half % V == 0) {
+    if (vec_ok && a.host_inv && half % V == 0) {
         const int L = half / V;
-        int64_t lanes = a.total_heads * L;
-        int threads = static_cast<int>(lanes >= 1024 ? 1024 : ((lanes + 63) / 64) * 64);
-        switch (L) {
-        case 1: rope_vec<DTI, DTO, 1><<<grid, threads, 0, st>>>(a); return check_launch("rope_vec");
-        case 2: rope_vec<DTI, DTO, 2><<<grid, threads, 0, st>>>(a); return check_launch("rope_vec");
-        case 4: rope_vec<DTI, DTO, 4><<<grid, threads, 0, st>>>(a); return check_launch("rope_vec");
-        case 8: rope_vec<DTI, DTO, 8><<<grid, threads, 0, st>>>(a); return check_launch("rope_vec");
-        case 16: rope_vec<DTI, DTO, 16><<<grid, threads, 0, st>>>(a); return check_launch("rope_vec");
-        case 32: rope_vec<DTI, DTO, 32><<<grid, threads, 0, st>>>(a); return check_launch("rope_vec");
-        case 64: rope_vec<DTI, DTO, 64><<<grid, threads, 0, st>>>(a); return check_launch("rope_vec");
-        default: break;
+        if (L <= 64 && (L & (L - 1)) == 0) {
+            const int64_t lpt = a.total_heads * L;  // lanes per token
+            // Tokens per block: as many as keep the block at <= 512 lanes (>= 1), within the LDS table.
+            int tpb = lpt >= 512 ? 1 : static_cast<int>(512 / lpt);
+            int forced = env_int("SLHIP_ROPE_TPB", 0);
+            if (forced > 0) tpb = forced;
+            while (tpb > 1 && (tpb * half > kTableEntries || tpb * lpt > 1024)) tpb--;
+            a.tpb = tpb;
+            const int64_t lanes = tpb * lpt;
+            const int threads = static_cast<int>(lanes >= 1024 ? 1024 : ((lanes + 63) / 64) * 64);
+            dim3 grid(static_cast<unsigned>((a.T + tpb - 1) / tpb));
+            switch (L) {
+            case 1: rope_vec<DTI, DTO, 1><<<grid, threads, 0, st>>>(a); break;
+            case 2: rope_vec<DTI, DTO, 2><<<grid, threads, 0, st>>>(a); break;
+            case 4: rope_vec<DTI, DTO, 4><<<grid, threads, 0, st>>>(a); break;
+            case 8: rope_vec<DTI, DTO, 8><<<grid, threads, 0, st>>>(a); break;
+            case 16: rope_vec<DTI, DTO, 16><<<grid, threads, 0, st>>>(a); break;
+            case 32: rope_vec<DTI, DTO, 32><<<grid, threads, 0, st>>>(a); break;
+            default: rope_vec<DTI, DTO, 64><<<grid, threads, 0, st>>>(a); break;
+            }
+            return check_launch("rope_vec");
         }
     }
-    rope_scalar<DTI, DTO><<<grid, 256, 0, st>>>(a);
+    a.tpb = 1;
+    rope_scalar<DTI, DTO><<<dim3(static_cast<unsigned>(a.T)), 256, 0, st>>>(a);
     return check_launch("rope_scalar");
 }
 
@@ -241,6 +318,10 @@ extern "C" SLHIP_API int slhip_rope(int dtype_in, int dtype_out, const slhip_rop
     a.fs = cfg->freq_scale;
     a.af = cfg->attn_factor;
     a.eps = cfg->eps;
+    // Inverse frequencies in f64 on the host, as RopeOp's constructor computes them (RopeOp.cs:47-52).
+    a.host_inv = dims / 2 <= kArgInv;
+    if (a.host_inv)
+        for (int i = 0; i < dims / 2; i++) a.inv[i] = std::pow(static_cast<double>(a.base), -2.0 * i / dims) * static_cast<double>(a.fs);
     const int vin = dtype_in == SLHIP_F32 ? 4 : 8;
     const int bout = dtype_out == SLHIP_F32 ? 4 : 2;
     const int64_t oalign = vin * bout < 16 ? vin * bout : 16;
