@@ -11,12 +11,12 @@
 //   elements from dims to D are copied (normed when the norm is fused).
 // The angles are f64 because positions reach 32767 and more: an f32 argument would be off by ~1e-3 rad.
 //
-// Layout: one block per group of tokens. The block computes each token's dims/2 (cos, sin) pairs once
-// in LDS (f64 sincos of f64 angles; the inverse frequencies come from the host in f64), shared by every
-// head of every tensor; the first loads are issued before that work so their latency overlaps it. Each
-// head row is handled by L lanes (L = dims/2 / V, V = elements per 16-byte vector): lane c of a head
-// holds pairs [c*V, c*V + V) as two 16-byte vectors, so a wave covers 64/L whole heads with fully used
-// 16-byte loads and stores, and the fused norm is a butterfly over the L lanes of the head.
+// Layout (vector path): one block per token and one lane per (head, chunk) slot of it: L = dims/2 / V
+// lanes per head row (V = elements per 16-byte vector), lane c holding pairs [c*V, c*V + V) as two
+// 16-byte vectors, so a wave covers 64/L whole heads with fully used 16-byte loads and stores, and the
+// fused norm is a butterfly over the L lanes of a head. Each lane issues its loads (and its norm
+// weights') before the block computes the token's dims/2 (cos, sin) pairs into LDS -- one f64 angle
+// per thread, shared by every head of every tensor -- so the table work overlaps the HBM latency.
 #include "common.hpp"
 #include "rope_math.hpp"
 
@@ -27,9 +27,8 @@
 namespace slhip {
 
 constexpr int kMaxRopeTensors = 4;
-constexpr int kMaxHalf = 512;    // dims <= 1024
-constexpr int kArgInv = 128;     // inverse frequencies passed from the host when dims/2 <= this
-constexpr int kTableEntries = 1024;  // (cos, sin) pairs per block: tokens_per_block * dims/2
+constexpr int kMaxHalf = 512;  // dims <= 1024
+constexpr int kArgInv = 128;   // inverse frequencies carried in the kernel arguments up to dims = 256
 
 struct RopeTensorDev {
     const void* x;
@@ -46,32 +45,26 @@ struct RopeArgs {
     const int32_t* pos;
     const float* ff;
     int64_t T, D;
-    int dims, neox, norm, tpb;  // tpb: tokens per block
+    int dims, neox, norm;
     float base, fs, af, eps;
-    int host_inv;              // inv[] holds base^(-2i/dims)*freq_scale, computed on the host in f64
-    double inv[kArgInv];
+    int inv_in_args;         // inv[] holds the inverse frequencies (dims/2 <= kArgInv)
+    double l2b;              // log2(base) in f64, for dims/2 > kArgInv
+    double inv[kArgInv];     // base^(-2i/dims) * freq_scale in f64, computed on the host
 };
 
-// The block's (cos, sin) tables in LDS, one per token t0 .. t0+tpb-1; every thread must call it.
-// HOST_INV: the inverse frequencies are in a.inv (always so on the vector path).
-template <bool HOST_INV>
-__device__ __forceinline__ void build_table(const RopeArgs& a, int64_t t0, float2* cs)
+// Entry i of token t's table. The inverse frequencies come from the host in f64 (std::pow, as RopeOp's
+// Math.Pow) when dims/2 <= kArgInv; beyond that, exp2(log2(base) * (-2i/dims)) in f64 (within ~2e-15
+// relative of pow: < 1e-10 rad at position 32767, far below the f32 result's resolution).
+template <bool INV_ARGS>
+__device__ __forceinline__ float2 table_entry(const RopeArgs& a, int64_t t, int i)
 {
-    const int half = a.dims / 2;
-    for (int e = threadIdx.x; e < a.tpb * half; e += blockDim.x) {
-        const int tl = e / half, i = e - tl * half;
-        const int64_t t = t0 + tl;
-        if (t >= a.T) continue;
-        const double inv = (HOST_INV || a.host_inv)
-                               ? a.inv[i]
-                               : pow(static_cast<double>(a.base), -2.0 * i / a.dims) * static_cast<double>(a.fs);
-        double theta = static_cast<double>(a.pos[t]) * inv;
-        if (a.ff) theta /= static_cast<double>(a.ff[i]);
-        double s, c;
-        sincos_f64(theta, &s, &c);
-        cs[e] = make_float2(static_cast<float>(c) * a.af, static_cast<float>(s) * a.af);
-    }
-    __syncthreads();
+    const double inv = (INV_ARGS || a.inv_in_args) ? a.inv[i]
+                                                   : exp2(a.l2b * (-2.0 * i / a.dims)) * static_cast<double>(a.fs);
+    double theta = static_cast<double>(a.pos[t]) * inv;
+    if (a.ff) theta /= static_cast<double>(a.ff[i]);
+    double s, c;
+    sincos_f64(theta, &s, &c);
+    return make_float2(static_cast<float>(c) * a.af, static_cast<float>(s) * a.af);
 }
 
 __device__ __forceinline__ int tensor_of(const RopeArgs& a, int64_t gh)
@@ -83,22 +76,48 @@ __device__ __forceinline__ int tensor_of(const RopeArgs& a, int64_t gh)
     return k;
 }
 
-// Work item `idx` of the block: token t0 + idx / lpt, head (idx % lpt) / L, chunk idx % L.
-template <int DTI, int L>
-struct RopeItem {
-    int64_t t;
-    int tl, c, k;
-    int64_t h;
-    __device__ __forceinline__ RopeItem(const RopeArgs& a, int64_t t0, int idx)
+// One lane's slot: its head row's addresses at token 0, the token strides in bytes, the norm weight
+// pointer, and the element offsets of its two vectors -- neox (cV, half + cV), normal (2cV, 2cV + V).
+// The argument block's fields are read at constant indices and selected per lane: a per-lane dynamic
+// index into it would make every field a dependent memory load ahead of the data loads.
+template <int DTI, int DTO, int L>
+struct RopeSlot {
+    static constexpr int V = Vec<DTI>::N;
+    const char* x;
+    char* y;
+    const float* w;
+    int64_t xst, yst;
+    int c, e0, e1;
+    __device__ __forceinline__ RopeSlot(const RopeArgs& a, int slot)
     {
-        const int lpt = static_cast<int>(a.total_heads) * L;
-        tl = idx / lpt;
-        const int rem = idx - tl * lpt;
-        const int64_t gh = rem / L;
-        c = rem - static_cast<int>(gh) * L;
-        t = t0 + tl;
-        k = tensor_of(a, gh);
-        h = gh - a.t[k].head0;
+        const int64_t gh = slot / L;
+        c = slot - static_cast<int>(gh) * L;
+        const int k = tensor_of(a, gh);
+        const void* xp = a.t[0].x;
+        void* yp = a.t[0].y;
+        const float* wp = a.t[0].w;
+        int64_t h0 = a.t[0].head0, xs = a.t[0].xst, xh = a.t[0].xsh, ys = a.t[0].yst, yh = a.t[0].ysh;
+#pragma unroll
+        for (int j = 1; j < kMaxRopeTensors; j++) {
+            const bool s = k == j;
+            xp = s ? a.t[j].x : xp;
+            yp = s ? a.t[j].y : yp;
+            wp = s ? a.t[j].w : wp;
+            h0 = s ? a.t[j].head0 : h0;
+            xs = s ? a.t[j].xst : xs;
+            xh = s ? a.t[j].xsh : xh;
+            ys = s ? a.t[j].yst : ys;
+            yh = s ? a.t[j].ysh : yh;
+        }
+        const int64_t h = gh - h0;
+        x = static_cast<const char*>(xp) + h * xh * Vec<DTI>::BYTES;
+        y = static_cast<char*>(yp) + h * yh * Vec<DTO>::BYTES;
+        w = wp;
+        xst = xs * Vec<DTI>::BYTES;
+        yst = ys * Vec<DTO>::BYTES;
+        const int half = a.dims / 2;
+        e0 = a.neox ? c * V : 2 * c * V;
+        e1 = a.neox ? half + c * V : 2 * c * V + V;
     }
 };
 
@@ -107,110 +126,93 @@ __global__ __launch_bounds__(1024) void rope_vec(RopeArgs a)
 {
     using VI = Vec<DTI>;
     constexpr int V = VI::N;
-    __shared__ float2 cs[kTableEntries];
+    __shared__ float2 cs[kArgInv];
+    const int64_t t = blockIdx.x;
     const int half = a.dims / 2;
-    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * a.tpb;
-    const int items = a.tpb * static_cast<int>(a.total_heads) * L;
+    const int lpt = static_cast<int>(a.total_heads) * L;  // slots per token (<= blockDim.x)
+    const bool active = static_cast<int>(threadIdx.x) < lpt;
+    const RopeSlot<DTI, DTO, L> s(a, active ? static_cast<int>(threadIdx.x) : 0);
 
-    // element offsets of a lane's two vectors: neox (cV, half + cV); normal (2cV, 2cV + V)
-    auto offsets = [&](int c, int& e0, int& e1) {
-        e0 = a.neox ? c * V : 2 * c * V;
-        e1 = a.neox ? half + c * V : 2 * c * V + V;
-    };
-    auto in_row = [&](const RopeItem<DTI, L>& it) {
-        const RopeTensorDev& tt = a.t[it.k];
-        return static_cast<const char*>(tt.x) + (it.t * tt.xst + it.h * tt.xsh) * VI::BYTES;
-    };
-
-    // The first item's loads are issued before the table is built, so their latency overlaps the f64 work.
-    int idx = threadIdx.x;
+    // The row's loads and the norm weights are issued first, so their latency overlaps the table work.
     uint4 r0 = make_uint4(0, 0, 0, 0), r1 = r0;
-    if (idx < items) {
-        RopeItem<DTI, L> it(a, t0, idx);
-        if (it.t < a.T) {
-            int e0, e1;
-            offsets(it.c, e0, e1);
-            const char* xr = in_row(it);
-            r0 = load_nt(xr + e0 * VI::BYTES);
-            r1 = load_nt(xr + e1 * VI::BYTES);
-        }
-    }
-    build_table<true>(a, t0, cs);
-
-    for (bool first = true; idx < items; idx += blockDim.x, first = false) {
-        RopeItem<DTI, L> it(a, t0, idx);
-        if (it.t >= a.T) continue;
-        const RopeTensorDev& tt = a.t[it.k];
-        int e0, e1;
-        offsets(it.c, e0, e1);
-        if (!first) {
-            const char* xr = in_row(it);
-            r0 = load_nt(xr + e0 * VI::BYTES);
-            r1 = load_nt(xr + e1 * VI::BYTES);
-        }
-        char* yr = static_cast<char*>(tt.y) + (it.t * tt.yst + it.h * tt.ysh) * Vec<DTO>::BYTES;
-        float f[2 * V];
-        VI::unpack(r0, f);
-        VI::unpack(r1, f + V);
-        if (a.norm) {
-            float q = 0.f;
+    float w[2 * V];
+    const bool has_w = a.norm && s.w != nullptr;
+    if (active) {
+        const char* xr = s.x + t * s.xst;
+        r0 = load_nt(xr + s.e0 * VI::BYTES);
+        r1 = load_nt(xr + s.e1 * VI::BYTES);
+        if (has_w) {
 #pragma unroll
-            for (int e = 0; e < 2 * V; e++) q = fmaf(f[e], f[e], q);
-            q = group_sum<L>(q);
-            const float scale = 1.0f / sqrtf(q / static_cast<float>(a.D) + a.eps);
+            for (int hv = 0; hv < 2; hv++) {
+                const float4* wp = reinterpret_cast<const float4*>(s.w + (hv ? s.e1 : s.e0));
 #pragma unroll
-            for (int e = 0; e < 2 * V; e++) f[e] *= scale;
-            if (tt.w) {
-#pragma unroll
-                for (int hv = 0; hv < 2; hv++) {
-                    const float4* wp = reinterpret_cast<const float4*>(tt.w + (hv ? e1 : e0));
-#pragma unroll
-                    for (int q4 = 0; q4 < V / 4; q4++) {
-                        float4 w4 = wp[q4];
-                        f[hv * V + 4 * q4 + 0] *= w4.x;
-                        f[hv * V + 4 * q4 + 1] *= w4.y;
-                        f[hv * V + 4 * q4 + 2] *= w4.z;
-                        f[hv * V + 4 * q4 + 3] *= w4.w;
-                    }
+                for (int q4 = 0; q4 < V / 4; q4++) {
+                    const float4 w4 = wp[q4];
+                    w[hv * V + 4 * q4 + 0] = w4.x;
+                    w[hv * V + 4 * q4 + 1] = w4.y;
+                    w[hv * V + 4 * q4 + 2] = w4.z;
+                    w[hv * V + 4 * q4 + 3] = w4.w;
                 }
             }
         }
-        const float2* ct = cs + it.tl * half + it.c * V;
-        float o[2 * V];
-        if (a.neox) {
-#pragma unroll
-            for (int e = 0; e < V; e++) {
-                const float2 cv = ct[e];
-                const float x0 = f[e], x1 = f[V + e];
-                o[e] = x0 * cv.x - x1 * cv.y;
-                o[V + e] = x0 * cv.y + x1 * cv.x;
-            }
-        } else {
-#pragma unroll
-            for (int e = 0; e < V; e++) {
-                const float2 cv = ct[e];
-                const float x0 = f[2 * e], x1 = f[2 * e + 1];
-                o[2 * e] = x0 * cv.x - x1 * cv.y;
-                o[2 * e + 1] = x0 * cv.y + x1 * cv.x;
-            }
-        }
-        store_packed<DTO, V>(yr + e0 * Vec<DTO>::BYTES, o);
-        store_packed<DTO, V>(yr + e1 * Vec<DTO>::BYTES, o + V);
     }
+    for (int i = threadIdx.x; i < half; i += blockDim.x) cs[i] = table_entry<true>(a, t, i);
+    __syncthreads();
+    if (!active) return;
+
+    float f[2 * V];
+    VI::unpack(r0, f);
+    VI::unpack(r1, f + V);
+    if (a.norm) {
+        float q = 0.f;
+#pragma unroll
+        for (int e = 0; e < 2 * V; e++) q = fmaf(f[e], f[e], q);
+        q = group_sum<L>(q);
+        const float scale = 1.0f / sqrtf(q / static_cast<float>(a.D) + a.eps);
+#pragma unroll
+        for (int e = 0; e < 2 * V; e++) f[e] *= scale;
+        if (has_w) {
+#pragma unroll
+            for (int e = 0; e < 2 * V; e++) f[e] *= w[e];
+        }
+    }
+    const float2* ct = cs + s.c * V;
+    float o[2 * V];
+    if (a.neox) {
+#pragma unroll
+        for (int e = 0; e < V; e++) {
+            const float2 cv = ct[e];
+            const float x0 = f[e], x1 = f[V + e];
+            o[e] = x0 * cv.x - x1 * cv.y;
+            o[V + e] = x0 * cv.y + x1 * cv.x;
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < V; e++) {
+            const float2 cv = ct[e];
+            const float x0 = f[2 * e], x1 = f[2 * e + 1];
+            o[2 * e] = x0 * cv.x - x1 * cv.y;
+            o[2 * e + 1] = x0 * cv.y + x1 * cv.x;
+        }
+    }
+    char* yr = s.y + t * s.yst;
+    store_packed<DTO, V>(yr + s.e0 * Vec<DTO>::BYTES, o);
+    store_packed<DTO, V>(yr + s.e1 * Vec<DTO>::BYTES, o + V);
 }
 
-// General path (any D, dims <= D, strides, alignment): one wave per head row, scalar loads.
+// General path (any D, dims <= D, strides, alignment): one block per token, one wave per head row,
+// scalar loads.
 template <int DTI, int DTO>
 __global__ __launch_bounds__(256) void rope_scalar(RopeArgs a)
 {
-    __shared__ float2 cs[kTableEntries];
-    const int64_t t = blockIdx.x;  // one token per block (tpb == 1)
-    build_table<false>(a, t, cs);
-    const int lane = threadIdx.x & 63;
+    __shared__ float2 cs[kMaxHalf];
+    const int64_t t = blockIdx.x;
     const int half = a.dims / 2;
+    for (int i = threadIdx.x; i < half; i += blockDim.x) cs[i] = table_entry<false>(a, t, i);
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
     for (int64_t gh = threadIdx.x >> 6; gh < a.total_heads; gh += blockDim.x >> 6) {
-        const int k = tensor_of(a, gh);
-        const RopeTensorDev& tt = a.t[k];
+        const RopeTensorDev& tt = a.t[tensor_of(a, gh)];  // gh is wave-uniform: scalar loads
         const int64_t h = gh - tt.head0;
         const void* xr = static_cast<const char*>(tt.x) + (t * tt.xst + h * tt.xsh) * Vec<DTI>::BYTES;
         void* yr = static_cast<char*>(tt.y) + (t * tt.yst + h * tt.ysh) * Vec<DTO>::BYTES;
@@ -243,43 +245,32 @@ __global__ __launch_bounds__(256) void rope_scalar(RopeArgs a)
     }
 }
 
-static int env_int(const char* name, int dflt)
+template <int DTI, int DTO, int L>
+static int launch_vec(const RopeArgs& a, int threads, hipStream_t st)
 {
-    const char* s = getenv(name);
-    return s && *s ? atoi(s) : dflt;
+    rope_vec<DTI, DTO, L><<<dim3(static_cast<unsigned>(a.T)), threads, 0, st>>>(a);
+    return check_launch("rope_vec");
 }
 
 template <int DTI, int DTO>
-static int dispatch(RopeArgs a, bool vec_ok, hipStream_t st)
+static int dispatch(const RopeArgs& a, bool vec_ok, hipStream_t st)
 {
     constexpr int V = Vec<DTI>::N;
     const int half = a.dims / 2;
-    if (vec_ok && a.host_inv && half % V == 0) {
-        const int L = half / V;
-        if (L <= 64 && (L & (L - 1)) == 0) {
-            const int64_t lpt = a.total_heads * L;  // lanes per token
-            // Tokens per block: as many as keep the block at <= 512 lanes (>= 1), within the LDS table.
-            int tpb = lpt >= 512 ? 1 : static_cast<int>(512 / lpt);
-            int forced = env_int("SLHIP_ROPE_TPB", 0);
-            if (forced > 0) tpb = forced;
-            while (tpb > 1 && (tpb * half > kTableEntries || tpb * lpt > 1024)) tpb--;
-            a.tpb = tpb;
-            const int64_t lanes = tpb * lpt;
-            const int threads = static_cast<int>(lanes >= 1024 ? 1024 : ((lanes + 63) / 64) * 64);
-            dim3 grid(static_cast<unsigned>((a.T + tpb - 1) / tpb));
-            switch (L) {
-            case 1: rope_vec<DTI, DTO, 1><<<grid, threads, 0, st>>>(a); break;
-            case 2: rope_vec<DTI, DTO, 2><<<grid, threads, 0, st>>>(a); break;
-            case 4: rope_vec<DTI, DTO, 4><<<grid, threads, 0, st>>>(a); break;
-            case 8: rope_vec<DTI, DTO, 8><<<grid, threads, 0, st>>>(a); break;
-            case 16: rope_vec<DTI, DTO, 16><<<grid, threads, 0, st>>>(a); break;
-            case 32: rope_vec<DTI, DTO, 32><<<grid, threads, 0, st>>>(a); break;
-            default: rope_vec<DTI, DTO, 64><<<grid, threads, 0, st>>>(a); break;
-            }
-            return check_launch("rope_vec");
+    const int L = half % V == 0 ? half / V : 0;
+    const int64_t lpt = a.total_heads * L;
+    if (vec_ok && a.inv_in_args && L >= 1 && L <= 64 && (L & (L - 1)) == 0 && lpt <= 1024) {
+        const int threads = static_cast<int>(((lpt + 63) / 64) * 64);
+        switch (L) {
+        case 1: return launch_vec<DTI, DTO, 1>(a, threads, st);
+        case 2: return launch_vec<DTI, DTO, 2>(a, threads, st);
+        case 4: return launch_vec<DTI, DTO, 4>(a, threads, st);
+        case 8: return launch_vec<DTI, DTO, 8>(a, threads, st);
+        case 16: return launch_vec<DTI, DTO, 16>(a, threads, st);
+        case 32: return launch_vec<DTI, DTO, 32>(a, threads, st);
+        default: return launch_vec<DTI, DTO, 64>(a, threads, st);
         }
     }
-    a.tpb = 1;
     rope_scalar<DTI, DTO><<<dim3(static_cast<unsigned>(a.T)), 256, 0, st>>>(a);
     return check_launch("rope_scalar");
 }
@@ -304,6 +295,7 @@ extern "C" SLHIP_API int slhip_rope(int dtype_in, int dtype_out, const slhip_rop
     if (T > 0x7FFFFFFF) return fail(SLHIP_ERR_UNSUPPORTED, "rope: more than 2^31-1 tokens");
     if (!(dtype_in == SLHIP_F32 || dtype_in == SLHIP_BF16) || !(dtype_out == SLHIP_F32 || dtype_out == SLHIP_BF16))
         return fail(SLHIP_ERR_UNSUPPORTED, "rope: dtype pair (%d -> %d) not supported", dtype_in, dtype_out);
+    if (!(cfg->base > 0.0f)) return fail(SLHIP_ERR_INVALID, "rope: base must be positive");
 
     RopeArgs a{};
     a.nt = n_tensors;
@@ -318,10 +310,11 @@ extern "C" SLHIP_API int slhip_rope(int dtype_in, int dtype_out, const slhip_rop
     a.fs = cfg->freq_scale;
     a.af = cfg->attn_factor;
     a.eps = cfg->eps;
-    // Inverse frequencies in f64 on the host, as RopeOp's constructor computes them (RopeOp.cs:47-52).
-    a.host_inv = dims / 2 <= kArgInv;
-    if (a.host_inv)
-        for (int i = 0; i < dims / 2; i++) a.inv[i] = std::pow(static_cast<double>(a.base), -2.0 * i / dims) * static_cast<double>(a.fs);
+    a.l2b = std::log2(static_cast<double>(cfg->base));
+    a.inv_in_args = dims / 2 <= kArgInv;
+    if (a.inv_in_args)
+        for (int i = 0; i < dims / 2; i++)
+            a.inv[i] = std::pow(static_cast<double>(cfg->base), -2.0 * i / dims) * static_cast<double>(cfg->freq_scale);
     const int vin = dtype_in == SLHIP_F32 ? 4 : 8;
     const int bout = dtype_out == SLHIP_F32 ? 4 : 2;
     const int64_t oalign = vin * bout < 16 ? vin * bout : 16;
