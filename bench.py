@@ -185,6 +185,38 @@ class C5(Workload):
                       stream=stream)
 
 
+class CopyRef(Workload):
+    """A plain device copy (slhip_convert bf16 -> bf16 of 256 MiB: one 16-byte load and one 16-byte store per
+    lane, lanes contiguous): the practical HBM ceiling on this device, and the known-size kernel that
+    scales the rocprofv3 FETCH_SIZE / WRITE_SIZE counters."""
+    name = "copy_256MiB"
+
+    def __init__(self):
+        self.n = (256 << 20) // 2
+        self.desc = "plain copy, 256 MiB in + 256 MiB out"
+        self.bytes_per_step = 2 * 2 * self.n
+        R = copies_for(self.bytes_per_step)
+        self.x, self.y = Rot(None, 2 * self.n, R), Rot(None, 2 * self.n, R)
+        native.call("slhip_memset", self.x.buf.ptr, 0, self.x.buf.nbytes, None)
+        native.synchronize()
+
+    def launch(self, i, stream):
+        native.convert("bf16", "bf16", self.x.slot(i), self.y.slot(i), self.n, stream=stream)
+
+
+WORKLOADS = {
+    "c1_rmsnorm_f32": lambda: C1(),
+    "c2_add_rmsnorm_bf16": lambda: C2(),
+    "c3_swiglu_bf16": lambda: C3("silu"),
+    "c3_geglu_bf16": lambda: C3("gelu_tanh"),
+    "c4_qknorm_rope_bf16": lambda: C4(),
+    "c5_gather_q8_0": lambda: C5("q8_0"),
+    "c5_gather_q4_0": lambda: C5("q4_0"),
+    "c5_gather_f16": lambda: C5("f16"),
+    "copy_256MiB": lambda: CopyRef(),
+}
+
+
 def time_region(wl: Workload, steps: int, warmup: int, stream) -> tuple[float, float]:
     """Whole-region timing: (wall seconds between the two syncs, HIP-event milliseconds on the stream)."""
     for i in range(warmup):
@@ -326,6 +358,54 @@ def cpu_model() -> str:
 
 # ---- main ------------------------------------------------------------------------------------------------
 
+COPY_KERNEL = "convert_vec<2, 2>"  # the CopyRef kernel (bf16 -> bf16), as demangled by rocprofv3
+COPY_BYTES = 256 << 20              # bytes it reads, and writes, per launch
+
+
+def summarize(dbs: list[str]) -> None:
+    """Per-kernel summary of rocprofv3 rocpd databases: dispatch count and duration statistics from
+    kernel traces; mean FETCH_SIZE / WRITE_SIZE per dispatch from counter runs, and, when the copy
+    reference is in the same run, the counters scaled to bytes by the copy's known traffic."""
+    import sqlite3
+    from collections import defaultdict
+
+    def short(name):
+        return name.replace("void ", "").replace("slhip::", "").split("(")[0]
+
+    durs = defaultdict(list)
+    ctr = defaultdict(lambda: defaultdict(list))
+    for db in dbs:
+        c = sqlite3.connect(db)
+        tables = {r[0] for r in c.execute("select name from sqlite_master")}
+        counted = "pmc_events" in tables and c.execute("select count(*) from pmc_events").fetchone()[0] > 0
+        if "kernels" in tables and not counted:  # counter runs serialize dispatches: their durations are not used
+            for name, d in c.execute("select name, duration from kernels"):
+                durs[short(name)].append(d)
+        if "pmc_events" in tables:
+            for name, cn, v in c.execute("select name, counter_name, counter_value from pmc_events"):
+                ctr[short(name)][cn].append(v)
+    if durs:
+        print(f"{'kernel':58s} {'calls':>6s} {'avg us':>9s} {'min us':>9s} {'max us':>9s} {'total ms':>10s}")
+        for k, v in sorted(durs.items(), key=lambda kv: -sum(kv[1])):
+            a = np.array(v, dtype=np.float64) / 1e3
+            print(f"{k[:58]:58s} {len(a):6d} {a.mean():9.2f} {a.min():9.2f} {a.max():9.2f} {a.sum() / 1e3:10.3f}")
+    if ctr:
+        scale = {}
+        cp = ctr.get(COPY_KERNEL, {})
+        for cn in ("FETCH_SIZE", "WRITE_SIZE"):
+            if cp.get(cn):
+                scale[cn] = COPY_BYTES / (np.mean(cp[cn]) * 1024.0)
+        print()
+        print(f"{'kernel':58s} {'counter':>11s} {'dispatches':>10s} {'mean KiB':>12s} {'scaled MB':>10s}")
+        for k in sorted(ctr):
+            for cn, v in sorted(ctr[k].items()):
+                m = float(np.mean(v))
+                sc = f"{m * 1024 * scale[cn] / 1e6:10.2f}" if cn in scale else f"{'-':>10s}"
+                print(f"{k[:58]:58s} {cn:>11s} {len(v):10d} {m:12.1f} {sc}")
+        for cn, s in scale.items():
+            print(f"scale {cn}: {s:.4f} bytes per counted byte (copy reference: {COPY_BYTES} bytes per launch)")
+
+
 def load_traffic() -> dict:
     """HBM traffic per launch measured with rocprofv3 --pmc (FETCH_SIZE, WRITE_SIZE), recorded in
     profiles/traffic.json by the profiling run; {} when absent."""
@@ -348,7 +428,16 @@ def main():
     ap.add_argument("--launches", type=int, default=50, help="launches per graph in the ops table")
     ap.add_argument("--replays", type=int, default=10, help="graph replays per op in the ops table")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--profile", default="",
+                    help="profiling mode: run only this workload (and the copy reference) eagerly --steps times, "
+                         "for rocprofv3 --kernel-trace / --pmc; prints one summary line")
+    ap.add_argument("--summarize", nargs="+", metavar="DB",
+                    help="summarize rocprofv3 rocpd databases (kernel durations, FETCH_SIZE / WRITE_SIZE); no GPU")
     args = ap.parse_args()
+
+    if args.summarize:
+        summarize(args.summarize)
+        return
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the fused layer ops are row-independent and need no collective; "
@@ -361,6 +450,17 @@ def main():
     native.set_device(0)
     props = native.device_props(0)
     stream = native.Stream()
+
+    if args.profile:
+        out = {}
+        for name in (args.profile, "copy_256MiB"):
+            w = WORKLOADS[name]()
+            wall_s, ev_ms = time_region(w, args.steps, args.warmup, stream.handle)
+            out[name] = {"launches": args.steps, "avg_us": round(ev_ms * 1e3 / args.steps, 2),
+                         "bytes": w.bytes_per_step, "GB/s": round(w.bytes_per_step * args.steps / ev_ms / 1e6, 1)}
+            w.free()
+        print(json.dumps({"profile": out}), flush=True)
+        return
 
     # -- headline: config 2 --
     log("bench: preparing c2_add_rmsnorm_bf16")
@@ -386,10 +486,7 @@ def main():
     ops = {}
     which = set()
     if not args.no_ops:
-        builders = [("c1_rmsnorm_f32", C1), ("c2_add_rmsnorm_bf16", None), ("c3_swiglu_bf16", lambda: C3("silu")),
-                    ("c3_geglu_bf16", lambda: C3("gelu_tanh")), ("c4_qknorm_rope_bf16", C4),
-                    ("c5_gather_q8_0", lambda: C5("q8_0")), ("c5_gather_q4_0", lambda: C5("q4_0")),
-                    ("c5_gather_f16", lambda: C5("f16"))]
+        builders = [(n, None if n == "c2_add_rmsnorm_bf16" else mk) for n, mk in WORKLOADS.items()]
         only = [s for s in args.only.split(",") if s]
         for name, mk in builders:
             if only and not any(name.startswith(o) for o in only):

@@ -1,48 +1,72 @@
 // Element type conversion between f32, f16 and bf16 activations (the CPU provider's Cast of
 // activations; f32 -> bf16 rounding is Simd.FloatToBFloat, src/Sharplight.Cpu/Simd.cs:530-540).
-// Streaming kernel: 8 elements per lane per step (16-byte loads of the 2-byte types, 2x16-byte of f32).
+//
+// Layout: a wave converts 512 consecutive elements per step as two groups of 4 per lane -- elements
+// [4l, 4l+4) and [256+4l, 256+4l+4) -- so that every load and store instruction of the wave covers one
+// contiguous span (512 B or 1 KiB) whatever the two element sizes are. (Giving each lane 8 contiguous
+// elements instead would make the wider side's two 16-byte accesses per lane land 32 bytes apart, and a
+// store instruction would then half-fill every 64-byte segment it touches: measured 1.6x the write traffic
+// and 35% less bandwidth on MI355X.) A tail of fewer than 512 elements takes a per-element kernel.
 #include "common.hpp"
 
 namespace slhip {
 
-template <int DI, int DO>
-__device__ __forceinline__ void cvt8(const void* x, void* y, int64_t i8)
+// Loads / stores 4 consecutive elements of dtype DT (16 bytes for f32, 8 bytes for f16/bf16).
+template <int DT> __device__ __forceinline__ void load4(const char* p, float* f)
 {
-    float f[8];
-    if (DI == SLHIP_F32) {
-        const char* p = static_cast<const char*>(x) + 32 * i8;
+    if (DT == SLHIP_F32) {
         Vec<SLHIP_F32>::unpack(load_nt(p), f);
-        Vec<SLHIP_F32>::unpack(load_nt(p + 16), f + 4);
     } else {
-        Vec<DI>::unpack(load_nt(static_cast<const char*>(x) + 16 * i8), f);
+        const u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+        if (DT == SLHIP_BF16) {
+            f[0] = bf16_lo(v.x); f[1] = bf16_hi(v.x); f[2] = bf16_lo(v.y); f[3] = bf16_hi(v.y);
+        } else {
+            f[0] = f16_lo(v.x); f[1] = f16_hi(v.x); f[2] = f16_lo(v.y); f[3] = f16_hi(v.y);
+        }
     }
-    store_packed<DO, 8>(static_cast<char*>(y) + i8 * 8 * Vec<DO>::BYTES, f);
 }
 
 template <int DI, int DO>
-__global__ __launch_bounds__(256) void convert_vec(const void* x, void* y, int64_t n8)
+__global__ __launch_bounds__(256) void convert_vec(const void* x, void* y, int64_t chunks)
 {
-    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n8; i += static_cast<int64_t>(gridDim.x) * 256)
-        cvt8<DI, DO>(x, y, i);
+    const int64_t chunk = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);  // 512 elements each
+    if (chunk >= chunks) return;
+    const int lane = threadIdx.x & 63;
+    const int64_t e0 = chunk * 512 + 4 * lane;
+    float f0[4], f1[4];
+    load4<DI>(static_cast<const char*>(x) + e0 * Vec<DI>::BYTES, f0);
+    load4<DI>(static_cast<const char*>(x) + (e0 + 256) * Vec<DI>::BYTES, f1);
+    store_packed<DO, 4>(static_cast<char*>(y) + e0 * Vec<DO>::BYTES, f0);
+    store_packed<DO, 4>(static_cast<char*>(y) + (e0 + 256) * Vec<DO>::BYTES, f1);
 }
 
 template <int DI, int DO>
-__global__ __launch_bounds__(256) void convert_scalar(const void* x, void* y, int64_t n)
+__global__ __launch_bounds__(256) void convert_scalar(const void* x, void* y, int64_t begin, int64_t n)
 {
-    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += static_cast<int64_t>(gridDim.x) * 256)
+    for (int64_t i = begin + static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * 256)
         Vec<DO>::store1(y, i, Vec<DI>::load1(x, i));
 }
 
 template <int DI, int DO>
 static int run(const void* x, void* y, int64_t n, hipStream_t st)
 {
-    const bool vec = n % 8 == 0 && aligned16(x) && aligned16(y);
-    const int64_t work = vec ? n / 8 : n;
-    const int64_t blocks = (work + 255) / 256;
-    const unsigned grid = static_cast<unsigned>(blocks < 8192 ? blocks : 8192);
-    if (vec) convert_vec<DI, DO><<<grid, 256, 0, st>>>(x, y, n / 8);
-    else convert_scalar<DI, DO><<<grid, 256, 0, st>>>(x, y, n);
-    return check_launch("convert");
+    const bool vec = aligned16(x) && aligned16(y);
+    const int64_t chunks = vec ? n / 512 : 0;
+    if (chunks > 0) {
+        const int64_t blocks = (chunks + 3) / 4;
+        if (blocks > 0x7FFFFFFF) return fail(SLHIP_ERR_UNSUPPORTED, "convert: %lld elements", static_cast<long long>(n));
+        convert_vec<DI, DO><<<static_cast<unsigned>(blocks), 256, 0, st>>>(x, y, chunks);
+        int e = check_launch("convert_vec");
+        if (e) return e;
+    }
+    const int64_t done = chunks * 512;
+    if (done < n) {
+        const int64_t blocks = (n - done + 255) / 256;
+        convert_scalar<DI, DO><<<static_cast<unsigned>(blocks < 8192 ? blocks : 8192), 256, 0, st>>>(x, y, done, n);
+        return check_launch("convert_scalar");
+    }
+    return SLHIP_OK;
 }
 
 template <int DI>
