@@ -3,19 +3,23 @@
 Prints ONE JSON line. The headline workload (``value``) is BASELINE config 2 -- residual add + RMSNorm in
 bf16 at the Llama-3-8B shape x, res [8192, 4096] -- as whole-step HBM throughput: algorithmic bytes (each
 input read once, each output written once) per step / measured step time, with the inputs resident in HBM
-and rotated over enough copies (> 512 MB) that no step is served from the 256 MB Infinity Cache.
+and rotated over enough copies (> 512 MB) that no step is served from the 256 MB Infinity Cache. The K timed
+steps are recorded once in a HIP graph and launched as one, bracketed by stream synchronization.
 
 Also in the line:
 * ``roofline`` -- the dominant kernel (rownorm_vec on config 2) against the 8 TB/s HBM peak, its average
   launch duration taken from HIP events recorded on the launch stream around the timed region; ``traffic``
-  is the FETCH_SIZE + WRITE_SIZE bytes per launch measured with rocprofv3 (profiles/), scaled by the
-  counters' reading of a plain copy of known size, or null when no such measurement is recorded.
+  is the FETCH_SIZE + WRITE_SIZE bytes per launch measured with rocprofv3 (profiles/traffic.json), scaled by
+  the counters' reading of a plain copy of known size, or null when no such measurement is recorded.
 * ``cpu_baseline`` -- the reference CPU provider's arithmetic (the C oracle restating src/Sharplight.Cpu,
   threaded like CpuParallel) timed on this host on a bounded sample of the same workload.
-* ``ops`` -- every BASELINE config (C1..C5): median per-launch microseconds (HIP events), GB/s and % of peak
-  on the GPU, and the CPU oracle's time for the same op.
+* ``ops`` -- every BASELINE config (C1..C5) and a plain-copy reference: median per-launch microseconds
+  (graph replay of 50 rotated launches, HIP events), GB/s and % of peak on the GPU, and the CPU oracle's
+  time for the same op.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c2] [--no-cpu] [--no-ops]
+       python bench.py --profile OP --steps K      (one workload, eager launches, for rocprofv3)
+       python bench.py --summarize DB [DB ...]     (summarize rocprofv3 databases; no GPU)
 """
 from __future__ import annotations
 
@@ -233,6 +237,24 @@ def time_region(wl: Workload, steps: int, warmup: int, stream) -> tuple[float, f
     return t1 - t0, e0.elapsed_ms(e1)
 
 
+def time_region_graph(wl: Workload, steps: int, warmup: int, stream: native.Stream) -> tuple[float, float]:
+    """The headline timing: ``warmup`` untimed eager steps, then exactly ``steps`` steps -- recorded once in
+    a HIP graph and launched as one -- bracketed by stream synchronization on both sides. Returns (wall
+    seconds between the two syncs, HIP-event milliseconds recorded on the launch stream around the graph)."""
+    g = native.Graph(stream, lambda: [wl.launch(warmup + i, stream.handle) for i in range(steps)])
+    for i in range(warmup):
+        wl.launch(i, stream.handle)
+    native.synchronize(stream.handle)
+    e0, e1 = native.Event(), native.Event()
+    t0 = time.perf_counter()
+    e0.record(stream.handle)
+    g.launch(stream)
+    e1.record(stream.handle)
+    native.synchronize(stream.handle)
+    t1 = time.perf_counter()
+    return t1 - t0, e0.elapsed_ms(e1)
+
+
 def time_per_launch(wl: Workload, launches: int, replays: int, stream) -> np.ndarray:
     """Per-launch microseconds: ``launches`` launches (rotating through the copies) recorded once in a graph,
     the graph replayed ``replays`` times, each replay bracketed by HIP events on the stream; returns the
@@ -362,7 +384,7 @@ COPY_KERNEL = "convert_vec<2, 2>"  # the CopyRef kernel (bf16 -> bf16), as deman
 COPY_BYTES = 256 << 20              # bytes it reads, and writes, per launch
 
 
-def summarize(dbs: list[str]) -> None:
+def summarize(dbs: list[str], traffic_op: str = "") -> None:
     """Per-kernel summary of rocprofv3 rocpd databases: dispatch count and duration statistics from
     kernel traces; mean FETCH_SIZE / WRITE_SIZE per dispatch from counter runs, and, when the copy
     reference is in the same run, the counters scaled to bytes by the copy's known traffic."""
@@ -404,6 +426,26 @@ def summarize(dbs: list[str]) -> None:
                 print(f"{k[:58]:58s} {cn:>11s} {len(v):10d} {m:12.1f} {sc}")
         for cn, s in scale.items():
             print(f"scale {cn}: {s:.4f} bytes per counted byte (copy reference: {COPY_BYTES} bytes per launch)")
+        if traffic_op:
+            # The op's kernel is the run's kernel other than the copy reference and the runtime's own.
+            ks = [k for k in ctr if k != COPY_KERNEL and not k.startswith("__amd")]
+            if len(ks) != 1 or set(scale) != {"FETCH_SIZE", "WRITE_SIZE"}:
+                raise SystemExit(f"--traffic needs one op kernel and both counters with the copy reference: {ks}")
+            k = ks[0]
+            fetch = float(np.mean(ctr[k]["FETCH_SIZE"])) * 1024 * scale["FETCH_SIZE"]
+            write = float(np.mean(ctr[k]["WRITE_SIZE"])) * 1024 * scale["WRITE_SIZE"]
+            path = os.path.join(ROOT, "profiles", "traffic.json")
+            try:
+                with open(path) as f:
+                    data = json.load(f)
+            except (OSError, ValueError):
+                data = {}
+            data[traffic_op] = {"kernel": k, "fetch_bytes": round(fetch), "write_bytes": round(write),
+                                "bytes_per_launch": round(fetch + write),
+                                "scale": {cn: round(s, 4) for cn, s in scale.items()}}
+            with open(path, "w") as f:
+                json.dump(data, f, indent=1, sort_keys=True)
+            print(f"traffic {traffic_op}: {fetch / 1e6:.2f} MB fetched + {write / 1e6:.2f} MB written per launch -> {path}")
 
 
 def load_traffic() -> dict:
@@ -433,10 +475,13 @@ def main():
                          "for rocprofv3 --kernel-trace / --pmc; prints one summary line")
     ap.add_argument("--summarize", nargs="+", metavar="DB",
                     help="summarize rocprofv3 rocpd databases (kernel durations, FETCH_SIZE / WRITE_SIZE); no GPU")
+    ap.add_argument("--traffic", default="", metavar="OP",
+                    help="with --summarize of one op's FETCH_SIZE and WRITE_SIZE runs: record its scaled HBM traffic "
+                         "per launch in profiles/traffic.json")
     args = ap.parse_args()
 
     if args.summarize:
-        summarize(args.summarize)
+        summarize(args.summarize, args.traffic)
         return
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -465,7 +510,7 @@ def main():
     # -- headline: config 2 --
     log("bench: preparing c2_add_rmsnorm_bf16")
     wl = C2()
-    wall_s, ev_ms = time_region(wl, args.steps, args.warmup, stream.handle)
+    wall_s, ev_ms = time_region_graph(wl, args.steps, args.warmup, stream)
     per_launch_us = time_per_launch(wl, args.launches, args.replays, stream)
     bps = wl.bytes_per_step
     value = bps * args.steps / wall_s / 1e9
@@ -475,7 +520,7 @@ def main():
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / PEAK_GBS, 4),
                 "traffic": traffic.get("bytes_per_launch") if traffic else None,
-                "kernel": "rownorm_vec<bf16,bf16,NV=8,RES> (slhip_rownorm)",
+                "kernel": "rownorm_vec<bf16,bf16,NV=2,RES> x 4 waves per row (slhip_rownorm)",
                 "algorithmic_bytes": bps, "avg_launch_us": round(kernel_avg_s * 1e6, 2)}
     wl_desc = wl.desc
     rot = wl.x.R
