@@ -230,6 +230,48 @@ SLHIP_API int slhip_gather(int format, const void* table, int64_t V, int64_t D, 
  */
 SLHIP_API int slhip_convert(int dtype_in, int dtype_out, const void* x, void* y, int64_t n, slhip_stream stream);
 
+/* ---- provider / compiled segment (IExecutionProvider, IComputeDevice, ICompiledSegment) ----------------
+ *
+ * A graph segment arrives as text, one declaration per line ('#' starts a comment line):
+ *   value <id> <type> <dim> ...       type: f32 f16 bf16 i32 q8_0 q4_0 q4_1 q5_0 q5_1; a dim "T" is the
+ *                                     symbolic token count, bound at execute time (at most max_tokens)
+ *   input <id> | weight <id> | output <id>
+ *   node <Op> <in,ids> -> <out,ids> [key=value ...]
+ * with the StandardOps names and attributes of the reference (src/Sharplight.Core/Graph/StandardOps.cs):
+ *   Add, Mul (same-shape), Silu, GeluTanh, Gelu, RmsNorm (x[, w]; eps), L2Norm (x; eps),
+ *   LayerNorm (x[, w[, b]]; eps), Rope (x [T,H,D], pos i32 [T][, ff]; dims, base, style=neox|normal|gptj,
+ *   freq_scale, attn_factor), Gather (table [V, D...], ids i32 [N]), Cast.
+ * Compile applies the reference lowerer's fusions (Add+RmsNorm, act+Mul, RmsNorm inside Rope, q/k ropes
+ * in one launch); slhip_segment_launches lists the fused launches, one per line. Segments run on a stream
+ * of their own on the device current at compile time. */
+typedef void* slhip_segment;
+
+/* IExecutionProvider.CheckAvailability (IExecutionProvider.cs:30): SLHIP_OK when a device is usable, else a
+ * status and the reason (no device, no runtime). Never throws; cheap. */
+SLHIP_API int slhip_provider_check(char* reason, size_t reason_size);
+/* IComputeDevice.Supports(Node) (IComputeDevice.cs:30-31) for node `node_index` of a segment text:
+ * *supported = 1, or 0 with the reason (the node then goes to the placement fallback). */
+SLHIP_API int slhip_node_supports(const char* segment_ir, int node_index, int* supported, char* reason,
+                                  size_t reason_size);
+/* IComputeDevice.Compile (IComputeDevice.cs:33-38): allocates every value for max_tokens tokens
+ * (CompileOptions.MaxTokens). SLHIP_ERR_UNSUPPORTED for a node or pattern this provider cannot run. */
+SLHIP_API int slhip_segment_compile(const char* segment_ir, int64_t max_tokens, slhip_segment* segment);
+/* ICompiledSegment.SetInput (ICompiledSegment.cs:9-10): dense host bytes of an input or weight value. */
+SLHIP_API int slhip_segment_set_input(slhip_segment segment, int value, const void* data, size_t bytes);
+/* ICompiledSegment.Execute: runs the launches for `tokens` tokens; asynchronous until an output is read.
+ * A token count above the compiled bound fails like CpuCompiledSegment.Execute
+ * (src/Sharplight.Cpu/CpuCompiledSegment.cs:115-121). */
+SLHIP_API int slhip_segment_execute(slhip_segment segment, int64_t tokens);
+/* ICompiledSegment.GetOutput: waits for the segment, then copies the output's dense bytes for the last
+ * run's token count (the size must match). Reports a gather index error as SLHIP_ERR_INDEX. */
+SLHIP_API int slhip_segment_get_output(slhip_segment segment, int value, void* data, size_t bytes);
+/* ICompiledSegment.ResetState (no state is held by these ops) and DeviceMemoryBytes. */
+SLHIP_API int slhip_segment_reset_state(slhip_segment segment);
+SLHIP_API int slhip_segment_device_bytes(slhip_segment segment, int64_t* bytes);
+/* The fused launches of the compiled segment, one label per line (e.g. "fused[Add]+RmsNorm"). */
+SLHIP_API int slhip_segment_launches(slhip_segment segment, char* buf, size_t size);
+SLHIP_API int slhip_segment_destroy(slhip_segment segment);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,739 @@
+// The Sharplight.Hip execution provider's host side: a compiled graph segment over the fused-layer-op
+// kernels, mirroring the reference's provider contracts (src/Sharplight.Core/Runtime/IExecutionProvider.cs,
+// IComputeDevice.cs, ICompiledSegment.cs) for the ops on this path.
+//
+//   IExecutionProvider.CheckAvailability  -> slhip_provider_check
+//   IComputeDevice.Supports(Node)         -> slhip_node_supports / SegmentCompiler::supports
+//   IComputeDevice.Compile(segment, opts) -> slhip_segment_compile (opts.MaxTokens bounds the symbol T)
+//   ICompiledSegment.SetInput / Execute / GetOutput / ResetState / DeviceMemoryBytes
+//                                         -> slhip_segment_set_input / _execute / _get_output / ...
+//
+// Compile lowers the segment's nodes into fused units with the fusion rules of the reference's shared
+// lowerer (src/Sharplight.Shaders/Lowering/GraphLowerer.Fusion.cs):
+//   * Add followed by RmsNorm / L2Norm of its result (rank-1 f32 weight or none) -> one residual row-norm
+//     launch that also writes the sum when anything else reads it (FoldNormTails, :215-238);
+//   * Silu / GeluTanh / Gelu whose only consumer is a Mul -> one gated-activation launch (the fused
+//     elementwise unit, :89-142; IMlpActivation.ActivateGated, Architectures/IMlpActivation.cs:12);
+//   * RmsNorm with an f32 [D] weight whose only consumer is a Rope -> computed inside the rope launch
+//     (AbsorbIntoConsumers, :618-630); Rope launches that share positions and settings (q and k of a
+//     layer) are merged into one launch of up to four tensors;
+//   * RmsNorm, L2Norm, LayerNorm, Rope, Gather and Cast on their own.
+// An Add, Mul or activation that fits none of these patterns is not supported on this provider.
+//
+// The graph reaches the C ABI as a small line-based text form (one value, node, input, weight or output
+// per line; see slhip_segment_compile in include/sharplight_hip.h); the managed provider writes it from a
+// GraphSegment.
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <cmath>
+#include <map>
+#include <memory>
+#include <set>
+#include <sstream>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "common.hpp"
+
+namespace slhip {
+namespace {
+
+// ---- errors: the reference's exception types, as statuses --------------------------------------------
+
+struct Error : std::runtime_error {
+    int status;
+    Error(int s, const std::string& m) : std::runtime_error(m), status(s) {}
+};
+[[noreturn]] void invalid(const std::string& m) { throw Error(SLHIP_ERR_INVALID, m); }       // ArgumentException
+[[noreturn]] void unsupported(const std::string& m) { throw Error(SLHIP_ERR_UNSUPPORTED, m); }  // NotSupportedException
+void check(int st)
+{
+    if (st != SLHIP_OK) throw Error(st, slhip_last_error());
+}
+
+// ---- graph ---------------------------------------------------------------------------------------------
+
+enum class DType { F32, F16, BF16, I32, Q8_0, Q4_0, Q4_1, Q5_0, Q5_1 };
+
+struct TypeInfo {
+    const char* name;
+    DType t;
+    int block;      // values per block
+    int block_bytes;
+};
+const TypeInfo kTypes[] = {
+    {"f32", DType::F32, 1, 4},     {"f16", DType::F16, 1, 2},     {"bf16", DType::BF16, 1, 2},
+    {"i32", DType::I32, 1, 4},     {"q8_0", DType::Q8_0, 32, 34}, {"q4_0", DType::Q4_0, 32, 18},
+    {"q4_1", DType::Q4_1, 32, 20}, {"q5_0", DType::Q5_0, 32, 22}, {"q5_1", DType::Q5_1, 32, 24},
+};
+
+const TypeInfo& type_info(DType t)
+{
+    for (const auto& ti : kTypes)
+        if (ti.t == t) return ti;
+    invalid("unknown type");
+}
+
+bool is_activation(DType t) { return t == DType::F32 || t == DType::F16 || t == DType::BF16; }
+
+int act_code(DType t)
+{
+    switch (t) {
+    case DType::F32: return SLHIP_F32;
+    case DType::F16: return SLHIP_F16;
+    case DType::BF16: return SLHIP_BF16;
+    default: invalid("not an activation type");
+    }
+}
+
+int format_code(DType t)
+{
+    switch (t) {
+    case DType::F32: return SLHIP_FMT_F32;
+    case DType::F16: return SLHIP_FMT_F16;
+    case DType::BF16: return SLHIP_FMT_BF16;
+    case DType::Q8_0: return SLHIP_FMT_Q8_0;
+    case DType::Q4_0: return SLHIP_FMT_Q4_0;
+    case DType::Q4_1: return SLHIP_FMT_Q4_1;
+    case DType::Q5_0: return SLHIP_FMT_Q5_0;
+    case DType::Q5_1: return SLHIP_FMT_Q5_1;
+    default: unsupported("gather table type");
+    }
+}
+
+constexpr int64_t kSymT = -1;  // the symbolic token dimension T
+
+struct Value {
+    int id = -1;
+    DType type = DType::F32;
+    std::vector<int64_t> dims;  // dims[k] == kSymT: the token count of the run
+    bool input = false, weight = false, output = false;
+
+    int64_t elems(int64_t T) const
+    {
+        int64_t n = 1;
+        for (int64_t d : dims) n *= d == kSymT ? T : d;
+        return n;
+    }
+    int64_t bytes(int64_t T) const
+    {
+        const TypeInfo& ti = type_info(type);
+        return elems(T) / ti.block * ti.block_bytes;
+    }
+    int64_t last() const { return dims.empty() ? 1 : dims.back(); }
+    int64_t rows(int64_t T) const { return last() == 0 ? 0 : elems(T) / last(); }
+    bool symbolic() const
+    {
+        for (int64_t d : dims)
+            if (d == kSymT) return true;
+        return false;
+    }
+};
+
+struct Node {
+    std::string op;
+    std::vector<int> in, out;
+    std::map<std::string, std::string> attr;
+
+    float f(const char* k, float d) const
+    {
+        auto it = attr.find(k);
+        return it == attr.end() ? d : strtof(it->second.c_str(), nullptr);
+    }
+    long long i(const char* k, long long d) const
+    {
+        auto it = attr.find(k);
+        return it == attr.end() ? d : strtoll(it->second.c_str(), nullptr, 10);
+    }
+    std::string s(const char* k, const std::string& d) const
+    {
+        auto it = attr.find(k);
+        return it == attr.end() ? d : it->second;
+    }
+};
+
+struct Graph {
+    std::map<int, Value> values;
+    std::vector<Node> nodes;
+
+    Value& value(int id)
+    {
+        auto it = values.find(id);
+        if (it == values.end()) invalid("unknown value " + std::to_string(id));
+        return it->second;
+    }
+    const Value& value(int id) const { return const_cast<Graph*>(this)->value(id); }
+};
+
+std::vector<int> parse_ids(const std::string& s)
+{
+    std::vector<int> ids;
+    if (s == "-") return ids;
+    std::stringstream ss(s);
+    std::string tok;
+    while (std::getline(ss, tok, ',')) {
+        if (tok.empty()) invalid("empty value id in '" + s + "'");
+        ids.push_back(atoi(tok.c_str()));
+    }
+    return ids;
+}
+
+DType parse_type(const std::string& s)
+{
+    for (const auto& ti : kTypes)
+        if (s == ti.name) return ti.t;
+    invalid("unknown type '" + s + "'");
+}
+
+Node parse_node(std::istringstream& ls)
+{
+    Node n;
+    std::string ins, arrow, outs;
+    if (!(ls >> n.op >> ins >> arrow >> outs) || arrow != "->") invalid("node: expected '<op> <ins> -> <outs> [k=v...]'");
+    n.in = parse_ids(ins);
+    n.out = parse_ids(outs);
+    std::string kv;
+    while (ls >> kv) {
+        const size_t eq = kv.find('=');
+        if (eq == std::string::npos) invalid("node attribute '" + kv + "' is not key=value");
+        n.attr[kv.substr(0, eq)] = kv.substr(eq + 1);
+    }
+    return n;
+}
+
+Graph parse(const char* text)
+{
+    Graph g;
+    std::istringstream in(text ? text : "");
+    std::string line;
+    int ln = 0;
+    while (std::getline(in, line)) {
+        ln++;
+        std::istringstream ls(line);
+        std::string kw;
+        if (!(ls >> kw) || kw[0] == '#') continue;
+        try {
+            if (kw == "value") {
+                Value v;
+                std::string t, d;
+                if (!(ls >> v.id >> t)) invalid("value: expected '<id> <type> <dims...>'");
+                v.type = parse_type(t);
+                while (ls >> d) v.dims.push_back(d == "T" ? kSymT : strtoll(d.c_str(), nullptr, 10));
+                if (g.values.count(v.id)) invalid("value " + std::to_string(v.id) + " declared twice");
+                g.values[v.id] = v;
+            } else if (kw == "input" || kw == "weight" || kw == "output") {
+                int id;
+                if (!(ls >> id)) invalid(kw + ": expected a value id");
+                Value& v = g.value(id);
+                (kw == "input" ? v.input : kw == "weight" ? v.weight : v.output) = true;
+            } else if (kw == "node") {
+                Node n = parse_node(ls);
+                for (int id : n.in) g.value(id);
+                for (int id : n.out) g.value(id);
+                g.nodes.push_back(n);
+            } else {
+                invalid("unknown keyword '" + kw + "'");
+            }
+        } catch (const Error& e) {
+            throw Error(e.status, "line " + std::to_string(ln) + ": " + e.what());
+        }
+    }
+    return g;
+}
+
+// ---- op support (IComputeDevice.Supports) ----------------------------------------------------------
+
+struct Support {
+    bool ok;
+    std::string reason;
+};
+
+const std::set<std::string> kActs = {"Silu", "GeluTanh", "Gelu"};
+
+Support supports(const Graph& g, const Node& n)
+{
+    auto no = [](const std::string& r) { return Support{false, r}; };
+    auto act = [&](int id) { return is_activation(g.value(id).type); };
+    const std::string& op = n.op;
+    if (op == "Add" || op == "Mul") {
+        if (n.in.size() != 2 || n.out.size() != 1) return no(op + " takes two inputs");
+        if (!act(n.in[0]) || !act(n.in[1]) || !act(n.out[0])) return no(op + ": activation types only");
+        if (g.value(n.in[0]).dims != g.value(n.in[1]).dims) return no(op + ": broadcasting is not supported");
+        return {true, ""};
+    }
+    if (kActs.count(op)) {
+        if (n.in.size() != 1 || n.out.size() != 1 || !act(n.in[0])) return no(op + " takes one activation");
+        return {true, ""};
+    }
+    if (op == "RmsNorm" || op == "L2Norm" || op == "LayerNorm") {
+        const size_t maxin = op == "LayerNorm" ? 3 : op == "RmsNorm" ? 2 : 1;
+        if (n.in.empty() || n.in.size() > maxin || n.out.size() != 1) return no(op + ": wrong operand count");
+        const Value& x = g.value(n.in[0]);
+        if (!act(n.in[0]) || x.type == DType::F16) return no(op + ": f32 or bf16 rows");
+        for (size_t k = 1; k < n.in.size(); k++) {
+            const Value& w = g.value(n.in[k]);
+            if (w.type != DType::F32 || w.dims.size() != 1 || w.dims[0] != x.last())
+                return no(op + ": weights must be f32 [D]");  // the reference's fused norms require f32 weights
+        }
+        return {true, ""};
+    }
+    if (op == "Rope") {
+        if (n.in.size() < 2 || n.in.size() > 3 || n.out.size() != 1) return no("Rope takes x, positions[, freq factors]");
+        const Value& x = g.value(n.in[0]);
+        const Value& p = g.value(n.in[1]);
+        if (x.dims.size() != 3 || !act(n.in[0]) || x.type == DType::F16) return no("Rope: x must be f32/bf16 [T, H, D]");
+        if (p.type != DType::I32 || p.dims.empty() || p.dims[0] != x.dims[0]) return no("Rope: positions must be i32 [T]");
+        if (p.dims.size() > 2 || (p.dims.size() == 2 && p.dims[1] != 1))
+            return no("Rope: multi-axis positions (M-RoPE) are not supported");
+        if (!n.s("sections", "").empty() && n.s("sections", "0,0,0,0") != "0,0,0,0") return no("Rope: sections are not supported");
+        if (n.in.size() == 3 && g.value(n.in[2]).type != DType::F32) return no("Rope: frequency factors must be f32");
+        return {true, ""};
+    }
+    if (op == "Gather") {
+        if (n.in.size() != 2 || n.out.size() != 1) return no("Gather takes table, indices");
+        const Value& t = g.value(n.in[0]);
+        if (t.type == DType::I32) return no("Gather: integer tables are not supported");
+        if (g.value(n.in[1]).type != DType::I32) return no("Gather: indices must be i32");
+        const DType o = g.value(n.out[0]).type;
+        if (o != DType::F32 && o != DType::BF16) return no("Gather: f32 or bf16 output");
+        return {true, ""};
+    }
+    if (op == "Cast") {
+        if (n.in.size() != 1 || n.out.size() != 1 || !act(n.in[0]) || !act(n.out[0])) return no("Cast: activation types");
+        return {true, ""};
+    }
+    return no("op " + op + " is not on the fused-layer-op path of the HIP provider");
+}
+
+// ---- lowering into fused units -------------------------------------------------------------------------
+
+struct Unit {
+    enum Kind { RowNorm, Gated, Rope, Gather, Cast } kind;
+    std::string label;
+    // RowNorm
+    int norm = SLHIP_NORM_RMS;
+    int x = -1, res = -1, w = -1, b = -1, y = -1, h = -1;
+    float eps = 0.f;
+    // Gated
+    int act = SLHIP_ACT_SILU, gate = -1, up = -1;
+    // Rope: up to 4 tensors sharing positions and settings
+    struct RopeTensor {
+        int x, y, w;
+    };
+    std::vector<RopeTensor> rt;
+    int pos = -1, ff = -1;
+    slhip_rope_cfg cfg{};
+    // Gather
+    int table = -1, ids = -1;
+};
+
+class Segment {
+public:
+    Segment(Graph g, int64_t max_tokens) : g_(std::move(g)), max_t_(max_tokens)
+    {
+        if (max_t_ < 0) invalid("MaxTokens must not be negative");
+        for (const Node& n : g_.nodes) {
+            Support s = supports(g_, n);
+            if (!s.ok) unsupported(s.reason);
+        }
+        lower();
+        check(slhip_stream_create(&stream_));
+        allocate();
+    }
+
+    ~Segment()
+    {
+        for (auto& kv : mem_) slhip_free(kv.second);
+        if (stream_) slhip_stream_destroy(stream_);
+    }
+
+    void set_input(int id, const void* data, size_t bytes)
+    {
+        Value& v = g_.value(id);
+        if (!v.input && !v.weight) invalid("value " + std::to_string(id) + " is not an input or weight of the segment");
+        const int64_t cap = v.bytes(max_t_);
+        if (static_cast<int64_t>(bytes) > cap) invalid("input " + std::to_string(id) + ": " + std::to_string(bytes) +
+                                                       " bytes exceed the compiled size " + std::to_string(cap));
+        if (bytes && !data) invalid("input data is null");
+        check(slhip_memcpy_h2d(mem_.at(id), data, bytes, stream_));
+        check(slhip_stream_sync(stream_));
+    }
+
+    void execute(int64_t T)
+    {
+        if (T < 0) invalid("T must not be negative");
+        if (T > max_t_)  // CpuCompiledSegment.Execute (src/Sharplight.Cpu/CpuCompiledSegment.cs:115-121)
+            throw Error(SLHIP_ERR_INVALID, "Symbol 'T' = " + std::to_string(T) + " exceeds the compiled bound " +
+                                               std::to_string(max_t_) + ".");
+        t_ = T;
+        for (const Unit& u : units_) run(u, T);
+    }
+
+    void get_output(int id, void* data, size_t bytes)
+    {
+        const Value& v = g_.value(id);
+        if (!v.output) invalid("value " + std::to_string(id) + " is not an output of the segment");
+        const int64_t n = v.bytes(t_);
+        if (static_cast<int64_t>(bytes) != n)
+            invalid("output " + std::to_string(id) + " holds " + std::to_string(n) + " bytes, destination " + std::to_string(bytes));
+        check(slhip_stream_sync(stream_));  // raises a pending gather index error
+        if (n) check(slhip_memcpy_d2h(data, mem_.at(id), bytes, stream_));
+        check(slhip_stream_sync(stream_));
+    }
+
+    int64_t device_bytes() const { return device_bytes_; }
+
+    std::string launches() const
+    {
+        std::string s;
+        for (const Unit& u : units_) s += u.label + "\n";
+        return s;
+    }
+
+private:
+    Graph g_;
+    int64_t max_t_, t_ = 0;
+    std::vector<Unit> units_;
+    std::map<int, void*> mem_;
+    int64_t device_bytes_ = 0;
+    slhip_stream stream_ = nullptr;
+
+    std::map<int, std::vector<int>> consumers() const
+    {
+        std::map<int, std::vector<int>> c;
+        for (size_t k = 0; k < g_.nodes.size(); k++)
+            for (int id : g_.nodes[k].in) c[id].push_back(static_cast<int>(k));
+        return c;
+    }
+
+    static int norm_kind(const std::string& op)
+    {
+        return op == "RmsNorm" ? SLHIP_NORM_RMS : op == "L2Norm" ? SLHIP_NORM_L2 : SLHIP_NORM_LAYER;
+    }
+
+    Unit rownorm_unit(const Node& n)
+    {
+        Unit u{Unit::RowNorm};
+        u.norm = norm_kind(n.op);
+        u.x = n.in[0];
+        u.w = n.in.size() > 1 ? n.in[1] : -1;
+        u.b = n.in.size() > 2 ? n.in[2] : -1;
+        u.y = n.out[0];
+        u.eps = n.f("eps", n.op == "LayerNorm" ? 1e-5f : 1e-6f);
+        u.label = n.op;
+        return u;
+    }
+
+    void lower()
+    {
+        auto cons = consumers();
+        const size_t N = g_.nodes.size();
+        std::vector<bool> done(N, false);
+        auto single_use = [&](int id) { return !g_.value(id).output && cons[id].size() == 1; };
+        for (size_t k = 0; k < N; k++) {
+            if (done[k]) continue;
+            const Node& n = g_.nodes[k];
+            if (n.op == "Add" && k + 1 < N && !done[k + 1]) {
+                const Node& m = g_.nodes[k + 1];
+                if ((m.op == "RmsNorm" || m.op == "L2Norm") && m.in[0] == n.out[0]) {
+                    Unit u = rownorm_unit(m);
+                    u.x = n.in[0];
+                    u.res = n.in[1];
+                    // the sum is written only when something besides the norm reads it
+                    u.h = single_use(n.out[0]) ? -1 : n.out[0];
+                    u.label = std::string("fused[Add]+") + m.op;
+                    if (g_.value(n.in[0]).type != g_.value(n.out[0]).type ||
+                        g_.value(n.in[1]).type != g_.value(n.out[0]).type)
+                        unsupported("Add+" + m.op + ": the residual stream must keep one type");
+                    units_.push_back(u);
+                    done[k] = done[k + 1] = true;
+                    continue;
+                }
+            }
+            if (kActs.count(n.op) && single_use(n.out[0])) {
+                const int mk = cons[n.out[0]][0];
+                const Node& m = g_.nodes[mk];
+                if (m.op == "Mul" && !done[mk]) {
+                    Unit u{Unit::Gated};
+                    u.act = n.op == "Silu" ? SLHIP_ACT_SILU : n.op == "GeluTanh" ? SLHIP_ACT_GELU_TANH : SLHIP_ACT_GELU_ERF;
+                    u.gate = n.in[0];
+                    u.up = m.in[0] == n.out[0] ? m.in[1] : m.in[0];
+                    u.y = m.out[0];
+                    if (g_.value(u.gate).type != g_.value(u.up).type) unsupported("gated activation: gate and up types differ");
+                    u.label = "fused[" + n.op + ",Mul]";
+                    units_.push_back(u);
+                    done[k] = done[mk] = true;
+                    continue;
+                }
+            }
+            if (n.op == "RmsNorm" && n.in.size() == 2 && single_use(n.out[0])) {
+                const int rk = cons[n.out[0]][0];
+                const Node& r = g_.nodes[rk];
+                if (r.op == "Rope" && r.in[0] == n.out[0] && !done[rk] && rk > static_cast<int>(k)) {
+                    // computed inside the rope launch; marked here, emitted at the rope
+                    absorbed_norm_[rk] = static_cast<int>(k);
+                    done[k] = true;
+                    continue;
+                }
+            }
+            done[k] = true;
+            if (n.op == "RmsNorm" || n.op == "L2Norm" || n.op == "LayerNorm") {
+                units_.push_back(rownorm_unit(n));
+            } else if (n.op == "Rope") {
+                units_.push_back(rope_unit(static_cast<int>(k)));
+            } else if (n.op == "Gather") {
+                Unit u{Unit::Gather};
+                u.table = n.in[0];
+                u.ids = n.in[1];
+                u.y = n.out[0];
+                const Value& t = g_.value(u.table);
+                if (t.dims.size() < 2) invalid("Gather: table must be [V, ...]");
+                u.label = "Gather";
+                units_.push_back(u);
+            } else if (n.op == "Cast") {
+                Unit u{Unit::Cast};
+                u.x = n.in[0];
+                u.y = n.out[0];
+                u.label = "Cast";
+                units_.push_back(u);
+            } else {
+                unsupported("standalone " + n.op + ": the HIP provider runs " + n.op +
+                            " only fused (Add into a following RmsNorm/L2Norm, an activation into its Mul)");
+            }
+        }
+        merge_ropes();
+    }
+
+    std::map<int, int> absorbed_norm_;  // rope node -> RmsNorm node computed inside it
+
+    Unit rope_unit(int k)
+    {
+        const Node& r = g_.nodes[k];
+        Unit u{Unit::Rope};
+        int x = r.in[0], w = -1;
+        float eps = 0.f;
+        auto it = absorbed_norm_.find(k);
+        if (it != absorbed_norm_.end()) {
+            const Node& nn = g_.nodes[it->second];
+            x = nn.in[0];
+            w = nn.in[1];
+            eps = nn.f("eps", 1e-6f);
+        }
+        const Value& xv = g_.value(x);
+        u.rt.push_back({x, r.out[0], w});
+        u.pos = r.in[1];
+        u.ff = r.in.size() > 2 ? r.in[2] : -1;
+        const std::string style = r.s("style", "neox");
+        u.cfg.dims = static_cast<int32_t>(r.i("dims", 0));
+        u.cfg.neox = !(style == "gptj" || style == "normal");  // RopeOp.cs:43
+        u.cfg.base = r.f("base", 10000.f);
+        u.cfg.freq_scale = r.f("freq_scale", 1.f);
+        u.cfg.attn_factor = r.f("attn_factor", 1.f);
+        u.cfg.norm = w >= 0 ? 1 : 0;
+        u.cfg.eps = eps;
+        u.label = w >= 0 ? "rope+norm" : "rope";
+        if (xv.type != g_.value(r.out[0]).type && !(is_activation(g_.value(r.out[0]).type)))
+            unsupported("Rope output type");
+        return u;
+    }
+
+    // Consecutive rope units with the same positions, frequency factors, settings and types become one launch.
+    void merge_ropes()
+    {
+        std::vector<Unit> out;
+        for (Unit& u : units_) {
+            if (u.kind == Unit::Rope && !out.empty()) {
+                Unit& p = out.back();
+                const Value& a = g_.value(p.rt[0].x);
+                const Value& b = g_.value(u.rt[0].x);
+                const bool same = p.kind == Unit::Rope && p.pos == u.pos && p.ff == u.ff && p.rt.size() < 4 &&
+                                  memcmp(&p.cfg, &u.cfg, sizeof p.cfg) == 0 && a.type == b.type &&
+                                  g_.value(p.rt[0].y).type == g_.value(u.rt[0].y).type && a.dims[2] == b.dims[2] &&
+                                  a.dims[0] == b.dims[0];
+                if (same) {
+                    p.rt.push_back(u.rt[0]);
+                    p.label += "|" + u.label;
+                    continue;
+                }
+            }
+            out.push_back(u);
+        }
+        units_ = out;
+    }
+
+    void allocate()
+    {
+        for (auto& kv : g_.values) {
+            const int64_t n = kv.second.bytes(max_t_);
+            void* p = nullptr;
+            check(slhip_malloc(&p, static_cast<size_t>(n > 0 ? n : 0)));
+            mem_[kv.first] = p;
+            device_bytes_ += n;
+        }
+    }
+
+    void* ptr(int id) const { return id < 0 ? nullptr : mem_.at(id); }
+
+    void run(const Unit& u, int64_t T)
+    {
+        switch (u.kind) {
+        case Unit::RowNorm: {
+            const Value& x = g_.value(u.x);
+            const Value& y = g_.value(u.y);
+            const int64_t D = x.last(), rows = x.rows(T);
+            check(slhip_rownorm(u.norm, act_code(x.type), act_code(y.type), ptr(u.x), ptr(u.res),
+                                static_cast<const float*>(ptr(u.w)), static_cast<const float*>(ptr(u.b)), ptr(u.y),
+                                ptr(u.h), rows, D, D, D, D, D, u.eps, stream_));
+            break;
+        }
+        case Unit::Gated: {
+            const Value& gv = g_.value(u.gate);
+            const int64_t cols = gv.last(), rows = gv.rows(T);
+            check(slhip_gated_act(u.act, act_code(gv.type), act_code(g_.value(u.y).type), ptr(u.gate), ptr(u.up), ptr(u.y),
+                                  rows, cols, cols, cols, cols, stream_));
+            break;
+        }
+        case Unit::Rope: {
+            std::vector<slhip_rope_tensor> ts;
+            const Value& x0 = g_.value(u.rt[0].x);
+            const int64_t Tt = x0.dims[0] == kSymT ? T : x0.dims[0];
+            const int64_t D = x0.dims[2];
+            for (const auto& r : u.rt) {
+                const Value& xv = g_.value(r.x);
+                const int64_t H = xv.dims[1];
+                ts.push_back(slhip_rope_tensor{ptr(r.x), ptr(r.y), static_cast<const float*>(ptr(r.w)), H, H * D, D, H * D, D});
+            }
+            check(slhip_rope(act_code(x0.type), act_code(g_.value(u.rt[0].y).type), ts.data(), static_cast<int>(ts.size()),
+                             static_cast<const int32_t*>(ptr(u.pos)), static_cast<const float*>(ptr(u.ff)), Tt, D, &u.cfg,
+                             stream_));
+            break;
+        }
+        case Unit::Gather: {
+            const Value& t = g_.value(u.table);
+            const Value& ids = g_.value(u.ids);
+            int64_t D = 1;
+            for (size_t k = 1; k < t.dims.size(); k++) D *= t.dims[k];
+            const int64_t N = ids.elems(T);
+            check(slhip_gather(format_code(t.type), ptr(u.table), t.dims[0], D, static_cast<const int32_t*>(ptr(u.ids)), N,
+                               act_code(g_.value(u.y).type), ptr(u.y), D, stream_));
+            break;
+        }
+        case Unit::Cast: {
+            const Value& x = g_.value(u.x);
+            check(slhip_convert(act_code(x.type), act_code(g_.value(u.y).type), ptr(u.x), ptr(u.y), x.elems(T), stream_));
+            break;
+        }
+        }
+    }
+};
+
+template <typename F>
+int guarded(F&& f)
+{
+    try {
+        f();
+        return SLHIP_OK;
+    } catch (const Error& e) {
+        return fail(e.status, "%s", e.what());
+    } catch (const std::exception& e) {
+        return fail(SLHIP_ERR_INVALID, "%s", e.what());
+    }
+}
+
+}  // namespace
+}  // namespace slhip
+
+using namespace slhip;
+
+extern "C" {
+
+SLHIP_API int slhip_provider_check(char* reason, size_t reason_size)
+{
+    int n = 0;
+    int st = slhip_device_count(&n);
+    const char* why = st ? slhip_last_error() : n == 0 ? "no HIP device is visible" : "";
+    if (reason && reason_size) snprintf(reason, reason_size, "%s", why);
+    if (st) return st;
+    return n == 0 ? fail(SLHIP_ERR_NO_DEVICE, "%s", why) : SLHIP_OK;
+}
+
+SLHIP_API int slhip_node_supports(const char* segment_ir, int node_index, int* supported, char* reason,
+                                  size_t reason_size)
+{
+    return guarded([&] {
+        if (!supported) invalid("supported is null");
+        Graph g = parse(segment_ir);
+        if (node_index < 0 || node_index >= static_cast<int>(g.nodes.size())) invalid("node index out of range");
+        Support s = supports(g, g.nodes[node_index]);
+        *supported = s.ok ? 1 : 0;
+        if (reason && reason_size) snprintf(reason, reason_size, "%s", s.reason.c_str());
+    });
+}
+
+SLHIP_API int slhip_segment_compile(const char* segment_ir, int64_t max_tokens, slhip_segment* segment)
+{
+    return guarded([&] {
+        if (!segment) invalid("segment is null");
+        *segment = nullptr;
+        auto s = std::make_unique<Segment>(parse(segment_ir), max_tokens);
+        *segment = s.release();
+    });
+}
+
+SLHIP_API int slhip_segment_set_input(slhip_segment segment, int value, const void* data, size_t bytes)
+{
+    return guarded([&] {
+        if (!segment) invalid("segment is null");
+        static_cast<Segment*>(segment)->set_input(value, data, bytes);
+    });
+}
+
+SLHIP_API int slhip_segment_execute(slhip_segment segment, int64_t tokens)
+{
+    return guarded([&] {
+        if (!segment) invalid("segment is null");
+        static_cast<Segment*>(segment)->execute(tokens);
+    });
+}
+
+SLHIP_API int slhip_segment_get_output(slhip_segment segment, int value, void* data, size_t bytes)
+{
+    return guarded([&] {
+        if (!segment) invalid("segment is null");
+        static_cast<Segment*>(segment)->get_output(value, data, bytes);
+    });
+}
+
+SLHIP_API int slhip_segment_device_bytes(slhip_segment segment, int64_t* bytes)
+{
+    return guarded([&] {
+        if (!segment || !bytes) invalid("null argument");
+        *bytes = static_cast<Segment*>(segment)->device_bytes();
+    });
+}
+
+SLHIP_API int slhip_segment_launches(slhip_segment segment, char* buf, size_t size)
+{
+    return guarded([&] {
+        if (!segment || !buf || !size) invalid("null argument");
+        snprintf(buf, size, "%s", static_cast<Segment*>(segment)->launches().c_str());
+    });
+}
+
+SLHIP_API int slhip_segment_reset_state(slhip_segment segment)
+{
+    // The fused layer ops keep no state between steps (no KV cache or recurrent state lives here).
+    return guarded([&] {
+        if (!segment) invalid("segment is null");
+    });
+}
+
+SLHIP_API int slhip_segment_destroy(slhip_segment segment)
+{
+    return guarded([&] { delete static_cast<Segment*>(segment); });
+}
+
+}  // extern "C"

@@ -104,6 +104,16 @@ SIGNATURES = {
     "slhip_rope": (_I, [_I, _I, ctypes.POINTER(RopeTensor), _I, _P, _P, _I64, _I64, ctypes.POINTER(RopeCfg), _P]),
     "slhip_gather": (_I, [_I, _P, _I64, _I64, _P, _I64, _I, _P, _I64, _P]),
     "slhip_convert": (_I, [_I, _I, _P, _P, _I64, _P]),
+    "slhip_provider_check": (_I, [ctypes.c_char_p, _SZ]),
+    "slhip_node_supports": (_I, [ctypes.c_char_p, _I, ctypes.POINTER(_I), ctypes.c_char_p, _SZ]),
+    "slhip_segment_compile": (_I, [ctypes.c_char_p, _I64, ctypes.POINTER(_P)]),
+    "slhip_segment_set_input": (_I, [_P, _I, _P, _SZ]),
+    "slhip_segment_execute": (_I, [_P, _I64]),
+    "slhip_segment_get_output": (_I, [_P, _I, _P, _SZ]),
+    "slhip_segment_reset_state": (_I, [_P]),
+    "slhip_segment_device_bytes": (_I, [_P, ctypes.POINTER(_I64)]),
+    "slhip_segment_launches": (_I, [_P, ctypes.c_char_p, _SZ]),
+    "slhip_segment_destroy": (_I, [_P]),
 }
 
 _lib = None

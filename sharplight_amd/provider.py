@@ -1,0 +1,301 @@
+"""Host-side face of the Sharplight HIP execution provider, over libsharplight_hip's provider C ABI.
+
+Mirrors the reference's provider contracts for this path -- ``IExecutionProvider``
+(src/Sharplight.Core/Runtime/IExecutionProvider.cs:25-74), ``IComputeDevice`` (IComputeDevice.cs:6-67) and
+``ICompiledSegment`` (ICompiledSegment.cs:6-25) -- with the same names, argument meaning and error behaviour:
+``check_availability`` never raises, ``get_devices`` is empty when unavailable, ``open_device`` raises
+``ValueError`` for another provider's device and ``NotImplementedError`` when unavailable, ``supports``
+answers per node, ``compile`` raises ``NotImplementedError`` for what it cannot run, ``execute`` rejects a
+token count beyond the compiled bound. The lowering and fusion live in C++ (csrc/provider.hip); this module
+only builds the segment text and moves bytes.
+
+``GraphBuilder`` plays the part of the reference's GraphBuilder (src/Sharplight.Core/Graph/GraphBuilder.cs)
+for the ops on this path, so graph-level tests read like the reference's NormTests / FusionTests.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from . import native
+
+NP = {"f32": np.float32, "f16": np.float16, "bf16": np.uint16, "i32": np.int32}
+BLOCKS = {"q8_0": (32, 34), "q4_0": (32, 18), "q4_1": (32, 20), "q5_0": (32, 22), "q5_1": (32, 24)}
+ELEM_BYTES = {"f32": 4, "f16": 2, "bf16": 2, "i32": 4}
+
+
+@dataclass(frozen=True)
+class Value:
+    id: int
+    type: str
+    dims: tuple  # ints, or "T" for the symbolic token count
+
+    def shape(self, T: int) -> tuple:
+        return tuple(T if d == "T" else d for d in self.dims)
+
+    def nbytes(self, T: int) -> int:
+        n = int(np.prod(self.shape(T), dtype=np.int64)) if self.dims else 1
+        if self.type in BLOCKS:
+            bs, bb = BLOCKS[self.type]
+            return n // bs * bb
+        return n * ELEM_BYTES[self.type]
+
+
+@dataclass
+class Node:
+    op: str
+    inputs: list
+    outputs: list
+    attrs: dict = field(default_factory=dict)
+
+
+class GraphBuilder:
+    """Builds a graph segment for the provider (values, nodes, inputs, weights, outputs)."""
+
+    def __init__(self):
+        self.values: list[Value] = []
+        self.nodes: list[Node] = []
+        self.inputs: list[Value] = []
+        self.weights: list[Value] = []
+        self.outputs: list[Value] = []
+
+    def value(self, type: str, *dims) -> Value:
+        v = Value(len(self.values), type, tuple(dims))
+        self.values.append(v)
+        return v
+
+    def input(self, type: str, *dims) -> Value:
+        v = self.value(type, *dims)
+        self.inputs.append(v)
+        return v
+
+    def weight(self, type: str, *dims) -> Value:
+        v = self.value(type, *dims)
+        self.weights.append(v)
+        return v
+
+    def output(self, v: Value) -> Value:
+        self.outputs.append(v)
+        return v
+
+    def emit(self, op: str, inputs, out_type: str, out_dims, **attrs) -> Value:
+        y = self.value(out_type, *out_dims)
+        self.nodes.append(Node(op, [v for v in inputs if v is not None], [y], attrs))
+        return y
+
+    # the ops on this path (StandardOps names)
+    def add(self, a, b):
+        return self.emit("Add", [a, b], a.type, a.dims)
+
+    def mul(self, a, b):
+        return self.emit("Mul", [a, b], a.type, a.dims)
+
+    def silu(self, x):
+        return self.emit("Silu", [x], x.type, x.dims)
+
+    def gelu_tanh(self, x):
+        return self.emit("GeluTanh", [x], x.type, x.dims)
+
+    def gelu(self, x):
+        return self.emit("Gelu", [x], x.type, x.dims)
+
+    def rms_norm(self, x, w=None, eps=1e-6, out_type=None):
+        return self.emit("RmsNorm", [x, w], out_type or x.type, x.dims, eps=eps)
+
+    def l2_norm(self, x, eps=1e-6, out_type=None):
+        return self.emit("L2Norm", [x], out_type or x.type, x.dims, eps=eps)
+
+    def layer_norm(self, x, w=None, b=None, eps=1e-5, out_type=None):
+        if b is not None and w is None:
+            raise ValueError("LayerNorm bias without weight")
+        return self.emit("LayerNorm", [x, w, b], out_type or x.type, x.dims, eps=eps)
+
+    def rope(self, x, pos, ff=None, dims=0, base=10000.0, style="neox", freq_scale=1.0, attn_factor=1.0,
+             out_type=None):
+        return self.emit("Rope", [x, pos, ff], out_type or x.type, x.dims, dims=dims, base=base, style=style,
+                         freq_scale=freq_scale, attn_factor=attn_factor)
+
+    def gather(self, table, ids, out_type="f32"):
+        d = table.dims[1:]
+        return self.emit("Gather", [table, ids], out_type, (ids.dims[0],) + tuple(d))
+
+    def cast(self, x, to: str):
+        return self.emit("Cast", [x], to, x.dims)
+
+    def to_ir(self) -> str:
+        lines = []
+        for v in self.values:
+            lines.append(f"value {v.id} {v.type} " + " ".join(str(d) for d in v.dims))
+        for v in self.inputs:
+            lines.append(f"input {v.id}")
+        for v in self.weights:
+            lines.append(f"weight {v.id}")
+        for v in self.outputs:
+            lines.append(f"output {v.id}")
+        for n in self.nodes:
+            attrs = " ".join(f"{k}={_fmt(v)}" for k, v in n.attrs.items())
+            lines.append(f"node {n.op} {','.join(str(v.id) for v in n.inputs) or '-'} -> "
+                         f"{','.join(str(v.id) for v in n.outputs)} {attrs}".rstrip())
+        return "\n".join(lines) + "\n"
+
+
+def _fmt(v) -> str:
+    if isinstance(v, float):
+        return repr(float(v))
+    return str(v)
+
+
+@dataclass(frozen=True)
+class ProviderAvailability:
+    """ProviderAvailability (src/Sharplight.Core/Runtime/ProviderAvailability.cs)."""
+    is_available: bool
+    reason: str = ""
+
+
+@dataclass(frozen=True)
+class DeviceInfo:
+    """DeviceInfo (src/Sharplight.Core/Runtime/DeviceInfo.cs:4-50) for a HIP device."""
+    provider: str
+    index: int
+    name: str
+    kind: str
+    total_memory: int
+    vendor: str
+    driver: str
+    uuid: str
+    features: tuple
+    concurrent_workgroups: int
+
+
+@dataclass(frozen=True)
+class OpSupport:
+    is_supported: bool
+    reason: str = ""
+
+
+class HipExecutionProvider:
+    """IExecutionProvider for HIP devices. Cheap to construct; touches the runtime only in
+    check_availability / get_devices (IExecutionProvider.cs:3-6)."""
+
+    name = "hip"
+    portable_code_format = None  # kernels are prebuilt code objects: no portable stage
+
+    def check_availability(self) -> ProviderAvailability:
+        try:
+            buf = ctypes.create_string_buffer(512)
+            st = native.lib().slhip_provider_check(buf, len(buf))
+        except Exception as e:  # a missing or unloadable library means "unavailable", never an exception
+            return ProviderAvailability(False, str(e))
+        return ProviderAvailability(st == native.OK, "" if st == native.OK else buf.value.decode())
+
+    def get_devices(self) -> list[DeviceInfo]:
+        if not self.check_availability().is_available:
+            return []
+        out = []
+        for i in range(native.device_count()):
+            p = native.device_props(i)
+            out.append(DeviceInfo(self.name, i, p.name.decode() or p.arch.decode(), "DiscreteGpu", p.total_memory,
+                                  "AMD", "HIP", f"{p.pci_domain:04x}:{p.pci_bus:02x}:{p.pci_device:02x}",
+                                  ("bf16", "f16", "subgroup_ops"), p.compute_units))
+        return out
+
+    def open_device(self, device: DeviceInfo, options=None) -> "HipDevice":
+        if device.provider != self.name:
+            raise ValueError(f"Device of provider '{device.provider}' cannot be opened by '{self.name}'.")
+        avail = self.check_availability()
+        if not avail.is_available:
+            raise NotImplementedError(f"The HIP provider is unavailable: {avail.reason}")
+        return HipDevice(device)
+
+    def can_compile_for(self, profile) -> bool:
+        return False
+
+
+class HipDevice:
+    """IComputeDevice: supports() per node, compile() a segment; close() releases it."""
+
+    def __init__(self, info: DeviceInfo):
+        self.info = info
+        native.set_device(info.index)
+
+    @property
+    def available_memory(self) -> int:
+        free = ctypes.c_size_t(0)
+        native.call("slhip_mem_info", ctypes.byref(free), None)
+        return free.value
+
+    def supports(self, graph: GraphBuilder, node_index: int) -> OpSupport:
+        ok = ctypes.c_int(0)
+        buf = ctypes.create_string_buffer(512)
+        native.call("slhip_node_supports", graph.to_ir().encode(), node_index, ctypes.byref(ok), buf, len(buf))
+        return OpSupport(bool(ok.value), buf.value.decode())
+
+    def compile(self, graph: GraphBuilder, max_tokens: int = 512) -> "CompiledSegment":
+        native.set_device(self.info.index)
+        seg = ctypes.c_void_p(0)
+        native.call("slhip_segment_compile", graph.to_ir().encode(), max_tokens, ctypes.byref(seg))
+        return CompiledSegment(seg.value, graph)
+
+    def close(self):
+        pass
+
+
+class CompiledSegment:
+    """ICompiledSegment: set_input, execute (asynchronous until an output is read), get_output."""
+
+    def __init__(self, handle: int, graph: GraphBuilder):
+        self.handle = handle
+        self.graph = graph
+        self.tokens = 0
+
+    def set_input(self, value: Value, data: np.ndarray) -> None:
+        data = np.ascontiguousarray(data)
+        native.call("slhip_segment_set_input", self.handle, value.id, data.ctypes.data, data.nbytes)
+
+    def execute(self, T: int) -> None:
+        native.call("slhip_segment_execute", self.handle, T)
+        self.tokens = T
+
+    def get_output(self, value: Value) -> np.ndarray:
+        shape = value.shape(self.tokens)
+        if value.type in NP:
+            out = np.empty(shape, NP[value.type])
+        else:
+            out = np.empty(value.nbytes(self.tokens), np.uint8)
+        native.call("slhip_segment_get_output", self.handle, value.id, out.ctypes.data, out.nbytes)
+        return out
+
+    def reset_state(self) -> None:
+        native.call("slhip_segment_reset_state", self.handle)
+
+    @property
+    def device_memory_bytes(self) -> int:
+        n = ctypes.c_int64(0)
+        native.call("slhip_segment_device_bytes", self.handle, ctypes.byref(n))
+        return n.value
+
+    @property
+    def launches(self) -> list[str]:
+        buf = ctypes.create_string_buffer(8192)
+        native.call("slhip_segment_launches", self.handle, buf, len(buf))
+        return [s for s in buf.value.decode().split("\n") if s]
+
+    def close(self) -> None:
+        if self.handle:
+            native.call("slhip_segment_destroy", self.handle)
+            self.handle = 0
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            if self.handle and native._lib is not None:
+                native._lib.slhip_segment_destroy(self.handle)
+        except Exception:
+            pass

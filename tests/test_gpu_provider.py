@@ -1,0 +1,196 @@
+"""Graph segments through the HIP provider (discover -> open -> compile -> set inputs -> execute -> outputs),
+compared with the CPU oracle, in the manner of the reference's GPU-vs-CPU tests (tests/Sharplight.Vulkan.Tests:
+NormTests.cs, RowOpTests.cs, RopeTests.cs, GatherTests.cs, FusionTests.cs:18-26,59-67,142-157). The launch
+lists check that the fusions of the reference's lowerer happen."""
+import numpy as np
+import pytest
+
+import oracle
+from sharplight_amd import native, synth
+from sharplight_amd.provider import GraphBuilder, HipExecutionProvider
+from tests.devutil import log
+from tests.parity import assert_bf16_close, assert_bits_equal, assert_f32_close
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def dev(device):
+    p = HipExecutionProvider()
+    assert p.check_availability().is_available
+    devices = p.get_devices()
+    assert devices and devices[0].provider == "hip"
+    return p.open_device(devices[0])
+
+
+def test_norms_graph(dev):
+    """ViewAndNormTests.Norms / NormTests: RmsNorm with and without weight, L2Norm, LayerNorm (T=5, n=70)."""
+    T, n = 5, 70
+    g = GraphBuilder()
+    x = g.input("f32", "T", n)
+    w = g.weight("f32", n)
+    b = g.weight("f32", n)
+    rms = g.output(g.rms_norm(x, w, eps=1e-5))
+    rms0 = g.output(g.rms_norm(x, None, eps=1e-5))
+    l2 = g.output(g.l2_norm(x, eps=1e-6))
+    ln = g.output(g.layer_norm(x, w, b, eps=1e-5))
+    xs = synth.normal(1, 0, (T, n), std=3.0)
+    ws, bs = synth.normal(1, 1, (n,)), synth.normal(1, 2, (n,))
+    with dev.compile(g, max_tokens=16) as seg:
+        assert seg.launches == ["RmsNorm", "RmsNorm", "L2Norm", "LayerNorm"]
+        seg.set_input(x, xs)
+        seg.set_input(w, ws)
+        seg.set_input(b, bs)
+        log("provider norms")
+        seg.execute(T)
+        assert_f32_close(seg.get_output(rms), oracle.rmsnorm(xs, ws, 1e-5), what="rms")
+        assert_f32_close(seg.get_output(rms0), oracle.rmsnorm(xs, None, 1e-5), what="rms0")
+        assert_f32_close(seg.get_output(l2), oracle.rmsnorm(xs, None, 1e-6, mode=1), what="l2")
+        assert_f32_close(seg.get_output(ln), oracle.layernorm(xs, ws, bs, 1e-5), what="ln")
+
+
+@pytest.mark.parametrize("h_is_output", [True, False])
+def test_residual_add_rmsnorm_fuses(dev, h_is_output):
+    """FusionTests.cs:18-26: Add followed by RmsNorm is one launch; the sum is written only if read."""
+    T, D = 33, 4096
+    g = GraphBuilder()
+    x = g.input("bf16", "T", D)
+    r = g.input("bf16", "T", D)
+    w = g.weight("f32", D)
+    h = g.add(x, r)
+    if h_is_output:
+        g.output(h)
+    y = g.output(g.rms_norm(h, w, eps=1e-5))
+    c = synth.c2(rows=T, D=D)
+    with dev.compile(g, max_tokens=64) as seg:
+        assert seg.launches == ["fused[Add]+RmsNorm"]
+        seg.set_input(x, c["x"])
+        seg.set_input(r, c["res"])
+        seg.set_input(w, c["w"])
+        log(f"provider add+rmsnorm h_out={h_is_output}")
+        seg.execute(T)
+        yref, href = oracle.add_rmsnorm(c["x"], c["res"], c["w"], 1e-5, dtype="bf16")
+        assert_bf16_close(seg.get_output(y), yref, what="y")
+        if h_is_output:
+            assert_bf16_close(seg.get_output(h), href, ulp=0, what="h")
+
+
+@pytest.mark.parametrize("act,op", [("silu", "Silu"), ("gelu_tanh", "GeluTanh"), ("gelu_erf", "Gelu")])
+def test_gated_mlp_fuses(dev, act, op):
+    """IMlpActivation.ActivateGated: Mul(act(gate), up) is one launch (FusionTests.cs:59-67's epilogue)."""
+    T, F = 17, 14336
+    g = GraphBuilder()
+    gate = g.input("bf16", "T", F)
+    up = g.input("bf16", "T", F)
+    a = {"silu": g.silu, "gelu_tanh": g.gelu_tanh, "gelu_erf": g.gelu}[act](gate)
+    y = g.output(g.mul(up, a))  # operand order must not matter
+    c = synth.c3(rows=T, cols=F)
+    with dev.compile(g, max_tokens=32) as seg:
+        assert seg.launches == [f"fused[{op},Mul]"]
+        seg.set_input(gate, c["gate"])
+        seg.set_input(up, c["up"])
+        log(f"provider gated {act}")
+        seg.execute(T)
+        assert_bf16_close(seg.get_output(y), oracle.gated(act, c["gate"], c["up"], dtype="bf16"), what=act)
+
+
+def test_qwen3_qk_norm_rope_one_launch(dev):
+    """The Qwen3 attention prologue (DecoderGraphBuilder.Attention.cs:146-206): RmsNorm per head then neox rope
+    for q and k -- absorbed into rope (GraphLowerer.Fusion.cs:618-630) and merged into one launch."""
+    T = 64
+    g = GraphBuilder()
+    q = g.input("bf16", "T", 32, 128)
+    k = g.input("bf16", "T", 8, 128)
+    pos = g.input("i32", "T")
+    wq = g.weight("f32", 128)
+    wk = g.weight("f32", 128)
+    yq = g.output(g.rope(g.rms_norm(q, wq, eps=1e-6), pos, base=1e6, style="neox"))
+    yk = g.output(g.rope(g.rms_norm(k, wk, eps=1e-6), pos, base=1e6, style="neox"))
+    c = synth.c4(T=T)
+    with dev.compile(g, max_tokens=T) as seg:
+        assert seg.launches == ["rope+norm|rope+norm"]
+        for v, a in ((q, c["q"]), (k, c["k"]), (pos, c["pos"]), (wq, c["wq"]), (wk, c["wk"])):
+            seg.set_input(v, a)
+        log("provider qk-norm rope")
+        seg.execute(T)
+        assert_bf16_close(seg.get_output(yq), oracle.qk_norm_rope(c["q"], c["pos"], c["wq"], 1e-6, dtype="bf16", base=1e6),
+                          what="q")
+        assert_bf16_close(seg.get_output(yk), oracle.qk_norm_rope(c["k"], c["pos"], c["wk"], 1e-6, dtype="bf16", base=1e6),
+                          what="k")
+
+
+def test_rope_normal_style_with_freq_factors(dev):
+    """RopeTests.cs: the normal (gptj) style, frequency factors, partial dims, f32."""
+    T, H, D = 9, 3, 64
+    g = GraphBuilder()
+    x = g.input("f32", "T", H, D)
+    pos = g.input("i32", "T")
+    ff = g.weight("f32", 16)
+    y = g.output(g.rope(x, pos, ff, dims=32, base=1e4, style="gptj", freq_scale=0.5, attn_factor=1.25))
+    xs = synth.normal(5, 0, (T, H, D))
+    ps = synth.rng(5, 1).integers(0, 4000, T).astype(np.int32)
+    fs = synth.rng(5, 2).uniform(1, 4, 16).astype(np.float32)
+    with dev.compile(g, max_tokens=T) as seg:
+        assert seg.launches == ["rope"]
+        seg.set_input(x, xs)
+        seg.set_input(pos, ps)
+        seg.set_input(ff, fs)
+        seg.execute(T)
+        ref = oracle.rope(xs, ps, dims=32, neox=False, base=1e4, freq_scale=0.5, attn_factor=1.25, ff=fs)
+        assert_f32_close(seg.get_output(y), ref, what="gptj rope")
+
+
+@pytest.mark.parametrize("fmt", ["q8_0", "q4_0", "f16"])
+@pytest.mark.parametrize("out", ["f32", "bf16"])
+def test_gather_graph(dev, fmt, out):
+    """GatherTests.cs:147-163: token embedding from a quantized table; f32 output is the reference's default."""
+    V, D, N = 300, 4096, 40
+    g = GraphBuilder()
+    tbl = g.weight(fmt, V, D)
+    ids = g.input("i32", "T")
+    y = g.output(g.gather(tbl, ids, out_type=out))
+    table = synth.quant_table(fmt, V, D, seed=9)
+    idv = synth.rng(9, 1).integers(0, V, N).astype(np.int32)
+    with dev.compile(g, max_tokens=64) as seg:
+        seg.set_input(tbl, table)
+        seg.set_input(ids, idv)
+        seg.execute(N)
+        assert_bits_equal(seg.get_output(y), oracle.gather_as(fmt, table, V, D, idv, dtype=out), what=f"{fmt}->{out}")
+
+
+def test_symbol_bound_and_index_errors(dev):
+    """Execute beyond the compiled bound fails like CpuCompiledSegment.Execute; a bad id fails like GatherOp."""
+    V, D = 10, 64
+    g = GraphBuilder()
+    tbl = g.weight("f32", V, D)
+    ids = g.input("i32", "T")
+    y = g.output(g.gather(tbl, ids))
+    with dev.compile(g, max_tokens=4) as seg:
+        seg.set_input(tbl, np.zeros((V, D), np.float32))
+        with pytest.raises(ValueError, match="exceeds the compiled bound 4"):
+            seg.execute(5)
+        seg.set_input(ids, np.array([1, 11, 2], np.int32))
+        seg.execute(3)
+        with pytest.raises(IndexError, match="11"):
+            seg.get_output(y)
+        seg.set_input(ids, np.array([1, 2, 3], np.int32))
+        seg.execute(3)
+        assert seg.get_output(y).shape == (3, D)
+        assert seg.device_memory_bytes >= V * D * 4
+
+
+def test_symbolic_tokens_reuse_one_compilation(dev):
+    """One compiled segment runs any T up to its bound (decode T=1, prefill T=bound)."""
+    D = 1024
+    g = GraphBuilder()
+    x = g.input("f32", "T", D)
+    w = g.weight("f32", D)
+    y = g.output(g.rms_norm(x, w))
+    ws = synth.normal(3, 1, (D,), 1.0, 0.1)
+    with dev.compile(g, max_tokens=512) as seg:
+        seg.set_input(w, ws)
+        for T in (1, 7, 512, 3):
+            xs = synth.normal(T, 0, (T, D))
+            seg.set_input(x, xs)
+            seg.execute(T)
+            assert_f32_close(seg.get_output(y), oracle.rmsnorm(xs, ws, 1e-6), what=f"T={T}")
