@@ -652,12 +652,28 @@ extern "C" {
 
 SLHIP_API int slhip_provider_check(char* reason, size_t reason_size)
 {
+    // The library carries gfx950 code objects only: a device of another architecture cannot run them.
     int n = 0;
     int st = slhip_device_count(&n);
-    const char* why = st ? slhip_last_error() : n == 0 ? "no HIP device is visible" : "";
+    char why[256] = "";
+    if (st) {
+        snprintf(why, sizeof why, "%s", slhip_last_error());
+    } else if (n == 0) {
+        snprintf(why, sizeof why, "no HIP device is visible");
+    } else {
+        int usable = 0;
+        char seen[64] = "unknown";
+        for (int i = 0; i < n; ++i) {
+            slhip_device_props p;
+            if (slhip_device_props_get(i, &p) != SLHIP_OK) continue;
+            if (strncmp(p.arch, "gfx950", 6) == 0) ++usable;
+            else snprintf(seen, sizeof seen, "%s", p.arch);
+        }
+        if (!usable) snprintf(why, sizeof why, "no gfx950 device among %d visible (found %s)", n, seen);
+    }
     if (reason && reason_size) snprintf(reason, reason_size, "%s", why);
     if (st) return st;
-    return n == 0 ? fail(SLHIP_ERR_NO_DEVICE, "%s", why) : SLHIP_OK;
+    return why[0] ? fail(SLHIP_ERR_NO_DEVICE, "%s", why) : SLHIP_OK;
 }
 
 SLHIP_API int slhip_node_supports(const char* segment_ir, int node_index, int* supported, char* reason,

@@ -196,6 +196,8 @@ class HipExecutionProvider:
         out = []
         for i in range(native.device_count()):
             p = native.device_props(i)
+            if not p.arch.decode().startswith("gfx950"):
+                continue  # the library's code objects are gfx950 only
             out.append(DeviceInfo(self.name, i, p.name.decode() or p.arch.decode(), "DiscreteGpu", p.total_memory,
                                   "AMD", "HIP", f"{p.pci_domain:04x}:{p.pci_bus:02x}:{p.pci_device:02x}",
                                   ("bf16", "f16", "subgroup_ops"), p.compute_units))
