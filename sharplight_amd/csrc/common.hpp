@@ -63,18 +63,22 @@ __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w 
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
 
 // f32 -> bf16 with the reference's rounding (Simd.FloatToBFloat, src/Sharplight.Cpu/Simd.cs:530-540):
-// round to nearest even by adding 0x7FFF + lsb; a NaN keeps its top half with the quiet bit set.
+// round to nearest even (adding 0x7FFF + lsb); a NaN keeps its top half with the quiet bit set; f32
+// subnormals round like normals. gfx950's v_cvt_pk_bf16_f32 gives exactly these bits for every f32 input
+// (checked on all 2^16 top halves with tie, near-tie and NaN-payload low halves, and by the bit-exact
+// conversion tests), at one instruction per pair instead of about five per value.
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f)
 {
-    uint32_t b = __float_as_uint(f);
-    uint32_t r = (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
-    uint32_t q = (b >> 16) | 0x40u;
-    return (b & 0x7FFFFFFFu) > 0x7F800000u ? q : r;
+    return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
+
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi)
 {
-    return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+    const f32x2_t v = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
 __device__ __forceinline__ float f16_lo(uint32_t w)
@@ -208,5 +212,17 @@ template <int W> __device__ __forceinline__ float group_sum(float v)
 }
 
 __device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
+
+// Makes this wave's LDS writes visible to its own later LDS reads, for kernels whose waves work on
+// independent items and never wait for each other.
+__device__ __forceinline__ void wave_lds_sync()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// The index of the calling thread's wave in its block, as a wave-uniform (scalar) value.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
 }  // namespace slhip

@@ -129,15 +129,6 @@ __device__ __forceinline__ void store_vec(void* y, int64_t elem, const float* f)
     store_packed<DTO, VPL>(static_cast<char*>(y) + elem * Vec<DTO>::BYTES, f);
 }
 
-// Makes this wave's LDS writes visible to its own later LDS reads (the waves of a block work on
-// independent items and never wait for each other).
-__device__ __forceinline__ void wave_lds_sync()
-{
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 template <int FMT, int DTO, int CB, int WPB>
 __global__ __launch_bounds__(64 * WPB) void gather_quant(GatherArgs a)
 {

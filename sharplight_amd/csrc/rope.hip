@@ -11,12 +11,14 @@
 //   elements from dims to D are copied (normed when the norm is fused).
 // The angles are f64 because positions reach 32767 and more: an f32 argument would be off by ~1e-3 rad.
 //
-// Layout (vector path): one block per token and one lane per (head, chunk) slot of it: L = dims/2 / V
-// lanes per head row (V = elements per 16-byte vector), lane c holding pairs [c*V, c*V + V) as two
-// 16-byte vectors, so a wave covers 64/L whole heads with fully used 16-byte loads and stores, and the
-// fused norm is a butterfly over the L lanes of a head. Each lane issues its loads (and its norm
-// weights') before the block computes the token's dims/2 (cos, sin) pairs into LDS -- one f64 angle
-// per thread, shared by every head of every tensor -- so the table work overlaps the HBM latency.
+// Layout (vector path): a flat grid of independent waves. A wave owns one token and a group of 64/L
+// whole head rows of one tensor, L = dims/2 / V lanes per head row (V = elements per 16-byte vector);
+// lane c of a head holds pairs [c*V, c*V + V) as two 16-byte vectors, so loads and stores are fully
+// used 16-byte accesses and the fused norm is a butterfly over the L lanes of a head. Each wave issues
+// its loads and norm weights, then computes the token's dims/2 (cos, sin) pairs in f64 into its own LDS
+// slice (one angle per lane), and never waits for another wave: recomputing the table per wave costs
+// about one f64 sincos per lane, far less than a block-wide barrier that holds every wave of a token
+// until the table is ready.
 #include "common.hpp"
 #include "rope_math.hpp"
 
@@ -29,6 +31,7 @@ namespace slhip {
 constexpr int kMaxRopeTensors = 4;
 constexpr int kMaxHalf = 512;  // dims <= 1024
 constexpr int kArgInv = 128;   // inverse frequencies carried in the kernel arguments up to dims = 256
+constexpr int kRopeWpb = 4;    // waves per block of the vector path
 
 struct RopeTensorDev {
     const void* x;
@@ -42,6 +45,8 @@ struct RopeArgs {
     RopeTensorDev t[kMaxRopeTensors];
     int nt;
     int64_t total_heads;
+    int groups;                   // vector path: head groups per token, over all tensors
+    int goff[kMaxRopeTensors];    // vector path: first head group of each tensor
     const int32_t* pos;
     const float* ff;
     int64_t T, D;
@@ -67,6 +72,16 @@ __device__ __forceinline__ float2 table_entry(const RopeArgs& a, int64_t t, int 
     return make_float2(static_cast<float>(c) * a.af, static_cast<float>(s) * a.af);
 }
 
+// The same entry from inputs already in registers: theta = pos * inv (/ ff), all f64.
+__device__ __forceinline__ float2 table_value(const RopeArgs& a, double p, double inv, float ff)
+{
+    double theta = p * inv;
+    if (a.ff) theta /= static_cast<double>(ff);
+    double s, c;
+    sincos_f64(theta, &s, &c);
+    return make_float2(static_cast<float>(c) * a.af, static_cast<float>(s) * a.af);
+}
+
 __device__ __forceinline__ int tensor_of(const RopeArgs& a, int64_t gh)
 {
     int k = 0;
@@ -76,88 +91,101 @@ __device__ __forceinline__ int tensor_of(const RopeArgs& a, int64_t gh)
     return k;
 }
 
-// One lane's slot: its head row's addresses at token 0, the token strides in bytes, the norm weight
-// pointer, and the element offsets of its two vectors -- neox (cV, half + cV), normal (2cV, 2cV + V).
-// The argument block's fields are read at constant indices and selected per lane: a per-lane dynamic
-// index into it would make every field a dependent memory load ahead of the data loads.
-template <int DTI, int DTO, int L>
-struct RopeSlot {
-    static constexpr int V = Vec<DTI>::N;
-    const char* x;
-    char* y;
-    const float* w;
-    int64_t xst, yst;
-    int c, e0, e1;
-    __device__ __forceinline__ RopeSlot(const RopeArgs& a, int slot)
-    {
-        const int64_t gh = slot / L;
-        c = slot - static_cast<int>(gh) * L;
-        const int k = tensor_of(a, gh);
-        const void* xp = a.t[0].x;
-        void* yp = a.t[0].y;
-        const float* wp = a.t[0].w;
-        int64_t h0 = a.t[0].head0, xs = a.t[0].xst, xh = a.t[0].xsh, ys = a.t[0].yst, yh = a.t[0].ysh;
-#pragma unroll
-        for (int j = 1; j < kMaxRopeTensors; j++) {
-            const bool s = k == j;
-            xp = s ? a.t[j].x : xp;
-            yp = s ? a.t[j].y : yp;
-            wp = s ? a.t[j].w : wp;
-            h0 = s ? a.t[j].head0 : h0;
-            xs = s ? a.t[j].xst : xs;
-            xh = s ? a.t[j].xsh : xh;
-            ys = s ? a.t[j].yst : ys;
-            yh = s ? a.t[j].ysh : yh;
-        }
-        const int64_t h = gh - h0;
-        x = static_cast<const char*>(xp) + h * xh * Vec<DTI>::BYTES;
-        y = static_cast<char*>(yp) + h * yh * Vec<DTO>::BYTES;
-        w = wp;
-        xst = xs * Vec<DTI>::BYTES;
-        yst = ys * Vec<DTO>::BYTES;
-        const int half = a.dims / 2;
-        e0 = a.neox ? c * V : 2 * c * V;
-        e1 = a.neox ? half + c * V : 2 * c * V + V;
-    }
+typedef __attribute__((address_space(1))) float gfloat;
+
+// A row of ones standing in for an absent norm weight.
+struct OnesRow {
+    float v[2 * kArgInv];
 };
+constexpr OnesRow make_ones_row()
+{
+    OnesRow r{};
+    for (int i = 0; i < 2 * kArgInv; i++) r.v[i] = 1.0f;
+    return r;
+}
+__constant__ OnesRow kOnesRow = make_ones_row();
 
 template <int DTI, int DTO, int L>
-__global__ __launch_bounds__(1024) void rope_vec(RopeArgs a)
+__global__ __launch_bounds__(64 * kRopeWpb) void rope_vec(RopeArgs a)
 {
     using VI = Vec<DTI>;
     constexpr int V = VI::N;
-    __shared__ float2 cs[kArgInv];
-    const int64_t t = blockIdx.x;
-    const int half = a.dims / 2;
-    const int lpt = static_cast<int>(a.total_heads) * L;  // slots per token (<= blockDim.x)
-    const bool active = static_cast<int>(threadIdx.x) < lpt;
-    const RopeSlot<DTI, DTO, L> s(a, active ? static_cast<int>(threadIdx.x) : 0);
+    constexpr int HPW = 64 / L;             // head rows per wave
+    constexpr int HALF = L * V;             // dims / 2
+    constexpr int NE = (HALF + 63) / 64;    // table entries per lane
+    constexpr int NW = (2 * HALF + 63) / 64;  // norm-weight floats per lane
+    static_assert(HALF <= kArgInv, "the vector path takes its inverse frequencies from the arguments");
+    __shared__ float2 cs[kRopeWpb][kArgInv];
+    __shared__ float4 wsh[kRopeWpb][2 * kArgInv / 4];
+    // Grid: x = head group, y = block of kRopeWpb tokens. The group (and so the tensor) is uniform over
+    // the block, and the token needs no division: every wave issues few scalar instructions, which
+    // matters because a CU's scalar unit is shared by all of its waves. Blocks are dispatched x first,
+    // so the waves in flight cover whole tokens of contiguous memory.
+    const uint32_t t = blockIdx.y * kRopeWpb + wave_id();
+    if (t >= static_cast<uint32_t>(a.T)) return;
+    const int lane = threadIdx.x & 63;
+    const int wv = threadIdx.x >> 6;
+    const int gi = blockIdx.x;
+    int k = 0;
+#pragma unroll
+    for (int j = 1; j < kMaxRopeTensors; j++) k = (j < a.nt && gi >= a.goff[j]) ? j : k;
+    const RopeTensorDev& tt = a.t[k];
+    const void* xp = tt.x;
+    void* yp = tt.y;
+    const float* wp = tt.w;
+    const int64_t heads = tt.heads, xs = tt.xst, xh = tt.xsh, ys = tt.yst, yh = tt.ysh;
+    const int64_t h = static_cast<int64_t>(gi - a.goff[k]) * HPW + lane / L;
+    const int c = lane % L;
+    const bool active = h < heads;
+    const int e0 = a.neox ? c * V : 2 * c * V;
+    const int e1 = a.neox ? HALF + c * V : 2 * c * V + V;
+    // Lanes past the tensor's last head read that head (and store nothing), so every load below is
+    // unconditional: a load under a divergent branch makes the compiler wait for it at the join.
+    const int64_t hl = active ? h : heads - 1;
+    const char* xr = static_cast<const char*>(xp) + (static_cast<int64_t>(t) * xs + hl * xh) * VI::BYTES;
+    char* yr = static_cast<char*>(yp) + (static_cast<int64_t>(t) * ys + h * yh) * Vec<DTO>::BYTES;
 
-    // The row's loads and the norm weights are issued first, so their latency overlaps the table work.
-    uint4 r0 = make_uint4(0, 0, 0, 0), r1 = r0;
-    float w[2 * V];
-    const bool has_w = a.norm && s.w != nullptr;
-    if (active) {
-        const char* xr = s.x + t * s.xst;
-        r0 = load_nt(xr + s.e0 * VI::BYTES);
-        r1 = load_nt(xr + s.e1 * VI::BYTES);
-        if (has_w) {
+    // Table inputs first: entries lane (+ 64), NE per lane. Vector-memory loads complete in order, so a
+    // table input loaded after the row's data would make the f64 table wait for the HBM data instead of
+    // overlapping it; and the code stays free of branches up to the table, because the compiler waits
+    // for outstanding loads where divergent paths join. Without frequency factors the factor loads read
+    // tensor 0's first row (at least dims/2 floats long) and are not used.
+    // The head's norm-weight row (D = dims floats) is staged through LDS the same way, one or a few
+    // floats per lane instead of 2V floats per lane; a norm without weight reads a row of ones (exact).
+    const double p = static_cast<double>(a.pos[t]);
+    const float* ffp = a.ff ? a.ff : static_cast<const float*>(a.t[0].x);
+    // (Both candidates as global-address-space pointers: a generic pointer would make these flat
+    // loads, which also hold the LDS counter that the table's synchronization waits on.)
+    const gfloat* wsrc = (a.norm && wp) ? (const gfloat*)wp : (const gfloat*)kOnesRow.v;
+    int ie[NE];
+    double inv[NE];
+    float ffv[NE];
 #pragma unroll
-            for (int hv = 0; hv < 2; hv++) {
-                const float4* wp = reinterpret_cast<const float4*>(s.w + (hv ? s.e1 : s.e0));
-#pragma unroll
-                for (int q4 = 0; q4 < V / 4; q4++) {
-                    const float4 w4 = wp[q4];
-                    w[hv * V + 4 * q4 + 0] = w4.x;
-                    w[hv * V + 4 * q4 + 1] = w4.y;
-                    w[hv * V + 4 * q4 + 2] = w4.z;
-                    w[hv * V + 4 * q4 + 3] = w4.w;
-                }
-            }
-        }
+    for (int n = 0; n < NE; n++) {
+        ie[n] = lane + 64 * n < HALF ? lane + 64 * n : HALF - 1;
+        inv[n] = a.inv[ie[n]];
+        ffv[n] = ffp[ie[n]];
     }
-    for (int i = threadIdx.x; i < half; i += blockDim.x) cs[i] = table_entry<true>(a, t, i);
-    __syncthreads();
+    int iw[NW];
+    float wv_[NW];
+#pragma unroll
+    for (int n = 0; n < NW; n++) {
+        iw[n] = lane + 64 * n < 2 * HALF ? lane + 64 * n : 2 * HALF - 1;
+        wv_[n] = wsrc[iw[n]];
+    }
+    const uint4 r0 = load_nt(xr + e0 * VI::BYTES);
+    const uint4 r1 = load_nt(xr + e1 * VI::BYTES);
+    // Keeps the instruction scheduler from sinking the loads below the f64 work (it would, to save
+    // registers), which would leave the table's latency unhidden.
+    __builtin_amdgcn_sched_barrier(0);
+    // Lanes past dims/2 rewrite the last entry with the same value.
+    float2* ctab = cs[wv];
+#pragma unroll
+    for (int n = 0; n < NE; n++) ctab[ie[n]] = table_value(a, p, inv[n], ffv[n]);
+    float* wrow = reinterpret_cast<float*>(wsh[wv]);
+#pragma unroll
+    for (int n = 0; n < NW; n++) wrow[iw[n]] = wv_[n];
+    wave_lds_sync();
     if (!active) return;
 
     float f[2 * V];
@@ -171,12 +199,19 @@ __global__ __launch_bounds__(1024) void rope_vec(RopeArgs a)
         const float scale = 1.0f / sqrtf(q / static_cast<float>(a.D) + a.eps);
 #pragma unroll
         for (int e = 0; e < 2 * V; e++) f[e] *= scale;
-        if (has_w) {
 #pragma unroll
-            for (int e = 0; e < 2 * V; e++) f[e] *= w[e];
+        for (int hv = 0; hv < 2; hv++) {
+#pragma unroll
+            for (int q4 = 0; q4 < V / 4; q4++) {
+                const float4 w4 = wsh[wv][(hv ? e1 : e0) / 4 + q4];
+                f[hv * V + 4 * q4 + 0] *= w4.x;
+                f[hv * V + 4 * q4 + 1] *= w4.y;
+                f[hv * V + 4 * q4 + 2] *= w4.z;
+                f[hv * V + 4 * q4 + 3] *= w4.w;
+            }
         }
     }
-    const float2* ct = cs + s.c * V;
+    const float2* ct = ctab + c * V;
     float o[2 * V];
     if (a.neox) {
 #pragma unroll
@@ -195,9 +230,8 @@ __global__ __launch_bounds__(1024) void rope_vec(RopeArgs a)
             o[2 * e + 1] = x0 * cv.y + x1 * cv.x;
         }
     }
-    char* yr = s.y + t * s.yst;
-    store_packed<DTO, V>(yr + s.e0 * Vec<DTO>::BYTES, o);
-    store_packed<DTO, V>(yr + s.e1 * Vec<DTO>::BYTES, o + V);
+    store_packed<DTO, V>(yr + e0 * Vec<DTO>::BYTES, o);
+    store_packed<DTO, V>(yr + e1 * Vec<DTO>::BYTES, o + V);
 }
 
 // General path (any D, dims <= D, strides, alignment): one block per token, one wave per head row,
@@ -246,30 +280,43 @@ __global__ __launch_bounds__(256) void rope_scalar(RopeArgs a)
 }
 
 template <int DTI, int DTO, int L>
-static int launch_vec(const RopeArgs& a, int threads, hipStream_t st)
+static int launch_vec(RopeArgs& a, hipStream_t st)
 {
-    rope_vec<DTI, DTO, L><<<dim3(static_cast<unsigned>(a.T)), threads, 0, st>>>(a);
-    return check_launch("rope_vec");
+    if constexpr (L * Vec<DTI>::N > kArgInv) {
+        return 1;  // dims/2 beyond the argument table: the general path
+    } else {
+        constexpr int HPW = 64 / L;
+        int groups = 0;
+        for (int j = 0; j < a.nt; j++) {
+            a.goff[j] = groups;
+            groups += static_cast<int>((a.t[j].heads + HPW - 1) / HPW);
+        }
+        a.groups = groups;
+        const int64_t blocks = (a.T + kRopeWpb - 1) / kRopeWpb;
+        if (blocks > 65535) return 1;  // beyond the grid's y extent: the general path
+        rope_vec<DTI, DTO, L><<<dim3(static_cast<unsigned>(groups), static_cast<unsigned>(blocks)), 64 * kRopeWpb, 0, st>>>(a);
+        return check_launch("rope_vec");
+    }
 }
 
 template <int DTI, int DTO>
-static int dispatch(const RopeArgs& a, bool vec_ok, hipStream_t st)
+static int dispatch(RopeArgs& a, bool vec_ok, hipStream_t st)
 {
     constexpr int V = Vec<DTI>::N;
     const int half = a.dims / 2;
     const int L = half % V == 0 ? half / V : 0;
-    const int64_t lpt = a.total_heads * L;
-    if (vec_ok && a.inv_in_args && L >= 1 && L <= 64 && (L & (L - 1)) == 0 && lpt <= 1024) {
-        const int threads = static_cast<int>(((lpt + 63) / 64) * 64);
+    if (vec_ok && a.inv_in_args && L >= 1 && L <= 64 && (L & (L - 1)) == 0 && a.total_heads < (int64_t{1} << 30)) {
+        int st_vec;
         switch (L) {
-        case 1: return launch_vec<DTI, DTO, 1>(a, threads, st);
-        case 2: return launch_vec<DTI, DTO, 2>(a, threads, st);
-        case 4: return launch_vec<DTI, DTO, 4>(a, threads, st);
-        case 8: return launch_vec<DTI, DTO, 8>(a, threads, st);
-        case 16: return launch_vec<DTI, DTO, 16>(a, threads, st);
-        case 32: return launch_vec<DTI, DTO, 32>(a, threads, st);
-        default: return launch_vec<DTI, DTO, 64>(a, threads, st);
+        case 1: st_vec = launch_vec<DTI, DTO, 1>(a, st); break;
+        case 2: st_vec = launch_vec<DTI, DTO, 2>(a, st); break;
+        case 4: st_vec = launch_vec<DTI, DTO, 4>(a, st); break;
+        case 8: st_vec = launch_vec<DTI, DTO, 8>(a, st); break;
+        case 16: st_vec = launch_vec<DTI, DTO, 16>(a, st); break;
+        case 32: st_vec = launch_vec<DTI, DTO, 32>(a, st); break;
+        default: st_vec = launch_vec<DTI, DTO, 64>(a, st); break;
         }
+        if (st_vec != 1) return st_vec;
     }
     rope_scalar<DTI, DTO><<<dim3(static_cast<unsigned>(a.T)), 256, 0, st>>>(a);
     return check_launch("rope_scalar");
