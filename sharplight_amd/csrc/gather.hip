@@ -105,9 +105,15 @@ __device__ __forceinline__ void decode(const uint32_t* s, int j0, float* f)
     }
     uint32_t qh = 0;
     if (F::QH >= 0) qh = lds_u32(s, o + F::QH) >> k0;
+    // Four nibbles at once: rotating the word by the nibble shift and masking leaves one value per byte,
+    // which converts with a single byte-to-float instruction (the rotate keeps the compiler from folding
+    // the mask back into one bit-field extract per value).
+    uint32_t nib[2];
+#pragma unroll
+    for (int h = 0; h < N / 4; h++) nib[h] = __builtin_amdgcn_alignbit(b[h], b[h], shift) & 0x0F0F0F0Fu;
 #pragma unroll
     for (int e = 0; e < N; e++) {
-        uint32_t v = ((b[e >> 2] >> (8 * (e & 3) + shift)) & 15u);
+        uint32_t v = (nib[e >> 2] >> (8 * (e & 3))) & 0xFFu;
         if (F::QH >= 0) v |= ((qh >> e) & 1u) << 4;
         f[e] = __fmaf_rn(static_cast<float>(v), d, add);
     }
@@ -129,7 +135,16 @@ __device__ __forceinline__ void store_vec(void* y, int64_t elem, const float* f)
     store_packed<DTO, VPL>(static_cast<char*>(y) + elem * Vec<DTO>::BYTES, f);
 }
 
-template <int FMT, int DTO, int CB, int WPB>
+// One quantized work item of a wave: where its chunk comes from and goes to.
+struct QuantItem {
+    const uint8_t* src;
+    void* yrow;
+    int64_t id;
+    int nvec16, groups;
+    bool live, ok, first_chunk;
+};
+
+template <int FMT, int DTO, int CB, int WPB, int RPW>
 __global__ __launch_bounds__(64 * WPB) void gather_quant(GatherArgs a)
 {
     constexpr int BB = Fmt<FMT>::BB;
@@ -139,46 +154,86 @@ __global__ __launch_bounds__(64 * WPB) void gather_quant(GatherArgs a)
     constexpr int WORDS = CB * BB / 4 + 4;            // +pad for the 3-word reads at the end
     __shared__ __align__(16) uint32_t lds[WPB][WORDS];
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int64_t item = static_cast<int64_t>(blockIdx.x) * WPB + wave;
-    if (item >= a.N * a.chunks) return;
+    const int wave = wave_id();
+    const int64_t total = a.N * a.chunks;
+    const int64_t first = (static_cast<int64_t>(blockIdx.x) * WPB + wave) * RPW;
+    if (first >= total) return;
     uint32_t* s = lds[wave];
-    const int64_t row = item / a.chunks;
-    const int64_t chunk = item - row * a.chunks;
-    const int64_t b0 = chunk * CB;
     const int64_t nblocks = a.D / 32;
-    const int nb = static_cast<int>(nblocks - b0 < CB ? nblocks - b0 : CB);
-    const int nvec16 = nb * BB / 16;  // chunk starts and lengths are multiples of 16 bytes
-    const int groups = nb * 32 / VPL;
-    void* const yrow = static_cast<char*>(a.y) + (row * a.ys + b0 * 32) * Vec<DTO>::BYTES;
-    const int64_t id = a.ids[row];
-    if (static_cast<uint64_t>(id) >= static_cast<uint64_t>(a.V)) {
-        if (lane == 0 && chunk == 0) raise_index_error(a.err, id, a.V);
-        const float z[VPL] = {};
-        for (int g = lane; g < groups; g += 64) store_vec<DTO, VPL>(yrow, g * VPL, z);
-        return;
+
+    // The wave's RPW consecutive items; every id is fetched up front (wave-uniform scalar loads), so the
+    // dependent id latency is paid once per wave rather than once per item.
+    QuantItem it[RPW];
+#pragma unroll
+    for (int j = 0; j < RPW; j++) {
+        const int64_t item = first + j < total ? first + j : first;
+        const int64_t row = a.chunks == 1 ? item : item / a.chunks;
+        const int64_t chunk = item - row * a.chunks;
+        const int64_t b0 = chunk * CB;
+        const int nb = static_cast<int>(nblocks - b0 < CB ? nblocks - b0 : CB);
+        const int64_t id = a.ids[row];
+        it[j].live = first + j < total;
+        it[j].ok = static_cast<uint64_t>(id) < static_cast<uint64_t>(a.V);
+        it[j].first_chunk = chunk == 0;
+        it[j].id = id;
+        it[j].nvec16 = nb * BB / 16;  // chunk starts and lengths are multiples of 16 bytes
+        it[j].groups = nb * 32 / VPL;
+        it[j].src = a.table + (it[j].ok ? id : 0) * a.rb + b0 * BB;  // a bad id reads row 0, stores zeros
+        it[j].yrow = static_cast<char*>(a.y) + (row * a.ys + b0 * 32) * Vec<DTO>::BYTES;
     }
-    const uint8_t* src = a.table + id * a.rb + b0 * BB;
-    uint4 r[LOADS];
+
+    // Two-stage pipeline: item j + 1's loads are issued before item j is decoded and stored. Loads and
+    // LDS writes are branch-free (lanes past a chunk's end re-read and re-write its last 16 bytes): under
+    // a divergent branch the compiler could not prove the loads complete on every path and would wait
+    // for all outstanding memory operations -- the previous stores included -- before each later store.
+    uint4 cur[LOADS], nxt[LOADS];
+    int ic[LOADS];
 #pragma unroll
     for (int k = 0; k < LOADS; k++) {
-        const int i = lane + 64 * k;
-        if (i < nvec16) r[k] = load_nt(src + 16 * i);
+        const int i = lane + 64 * k < it[0].nvec16 ? lane + 64 * k : it[0].nvec16 - 1;
+        cur[k] = load_nt(it[0].src + 16 * i);
     }
 #pragma unroll
-    for (int k = 0; k < LOADS; k++) {
-        const int i = lane + 64 * k;
-        if (i < nvec16) reinterpret_cast<uint4*>(s)[i] = r[k];
-    }
-    wave_lds_sync();
+    for (int j = 0; j < RPW; j++) {
+        if (j + 1 < RPW) {
 #pragma unroll
-    for (int k = 0; k < STEPS; k++) {
-        const int g = lane + 64 * k;
-        if (g < groups) {
+            for (int k = 0; k < LOADS; k++) {
+                const int i = lane + 64 * k < it[j + 1].nvec16 ? lane + 64 * k : it[j + 1].nvec16 - 1;
+                nxt[k] = load_nt(it[j + 1].src + 16 * i);
+            }
+        }
+        // A bad id's chunk (row 0 was read in its place) becomes all-zero bytes: scale 0 and code 0,
+        // which every format decodes to +0.
+        // (A mask, not a select of vectors: the compiler lowers the latter to a stack array.)
+        const uint32_t keep = it[j].ok ? 0xFFFFFFFFu : 0u;
+#pragma unroll
+        for (int k = 0; k < LOADS; k++) {
+            ic[k] = lane + 64 * k < it[j].nvec16 ? lane + 64 * k : it[j].nvec16 - 1;
+            reinterpret_cast<uint4*>(s)[ic[k]] =
+                make_uint4(cur[k].x & keep, cur[k].y & keep, cur[k].z & keep, cur[k].w & keep);
+        }
+        wave_lds_sync();
+        // Every lane stores every step, so each item issues exactly STEPS stores on every path and the
+        // compiler can wait for the next item's loads without waiting for these stores. Lanes past a
+        // partial chunk's end (and a tail wave's dead item, which re-reads item 0) re-store identical
+        // bytes at the last vector.
+#pragma unroll
+        for (int k = 0; k < STEPS; k++) {
+            const int g = lane + 64 * k < it[j].groups ? lane + 64 * k : it[j].groups - 1;
             float f[VPL];
             decode<FMT, VPL>(s, g * VPL, f);
-            store_vec<DTO, VPL>(yrow, g * VPL, f);
+            store_vec<DTO, VPL>(it[j].live ? it[j].yrow : it[0].yrow, g * VPL, f);
         }
+        wave_lds_sync();
+        if (j + 1 < RPW) {
+#pragma unroll
+            for (int k = 0; k < LOADS; k++) cur[k] = nxt[k];
+        }
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int j = 0; j < RPW; j++)
+            if (it[j].live && !it[j].ok && it[j].first_chunk) raise_index_error(a.err, it[j].id, a.V);
     }
 }
 
@@ -206,31 +261,38 @@ __global__ __launch_bounds__(64 * WPB) void gather_plain(GatherArgs a)
         for (int g = lane; g < groups; g += 64) store_vec<DTO, VPL>(yrow, g * VPL, z);
         return;
     }
+    // Every load is issued before the first store, without branches (lanes past the chunk's end re-read
+    // its last vector): with a load under a divergent branch the compiler waits for all outstanding
+    // memory operations at each step, which serializes the loads behind the previous stores.
     const uint8_t* src = a.table + id * a.rb + c0 * IN_BYTES;
+    uint32_t w[STEPS][LB / 4];
+#pragma unroll
+    for (int k = 0; k < STEPS; k++) {
+        const int g = lane + 64 * k < groups ? lane + 64 * k : groups - 1;
+        if constexpr (LB == 16) {
+            const uint4 v = load_nt(src + 16 * g);
+            w[k][0] = v.x;
+            w[k][1] = v.y;
+            w[k][2] = v.z;
+            w[k][3] = v.w;
+        } else {
+            const u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(src + 8 * g));
+            w[k][0] = v.x;
+            w[k][1] = v.y;
+        }
+    }
+    const bool full = groups == 64 * STEPS;  // wave-uniform
 #pragma unroll
     for (int k = 0; k < STEPS; k++) {
         const int g = lane + 64 * k;
-        if (g >= groups) continue;
-        uint32_t w[LB / 4];
-        if constexpr (LB == 16) {
-            const uint4 v = load_nt(src + 16 * g);
-            w[0] = v.x;
-            w[1] = v.y;
-            w[2] = v.z;
-            w[3] = v.w;
-        } else {
-            const u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(src + 8 * g));
-            w[0] = v.x;
-            w[1] = v.y;
-        }
         float f[VPL];
 #pragma unroll
         for (int e = 0; e < VPL; e++) {
-            if (FMT == SLHIP_FMT_F32) f[e] = __uint_as_float(w[e]);
-            else if (FMT == SLHIP_FMT_F16) f[e] = (e & 1) ? f16_hi(w[e >> 1]) : f16_lo(w[e >> 1]);
-            else f[e] = (e & 1) ? bf16_hi(w[e >> 1]) : bf16_lo(w[e >> 1]);
+            if (FMT == SLHIP_FMT_F32) f[e] = __uint_as_float(w[k][e]);
+            else if (FMT == SLHIP_FMT_F16) f[e] = (e & 1) ? f16_hi(w[k][e >> 1]) : f16_lo(w[k][e >> 1]);
+            else f[e] = (e & 1) ? bf16_hi(w[k][e >> 1]) : bf16_lo(w[k][e >> 1]);
         }
-        store_vec<DTO, VPL>(yrow, g * VPL, f);
+        if (full || g < groups) store_vec<DTO, VPL>(yrow, g * VPL, f);
     }
 }
 
@@ -312,24 +374,28 @@ static int env_int(const char* name, int dflt)
 // Work-item size (SLHIP_GATHER_ITEM = 0: small, 1: large) and waves per block (SLHIP_GATHER_WPB = 1 or 4).
 // Default: large items (128 quantized blocks or 8 vectors per lane: 4096 values) in 4-wave blocks --
 // measured on MI355X at 16384 x 4096 from a 151936-row table, small items run the quantized formats
-// ~35% slower (each wave then pays a dependent id load for ~0.5 KiB of input).
+// ~35% slower (each wave then pays a dependent id load for ~0.5 KiB of input), and two items per wave
+// (SLHIP_GATHER_RPW = 2, the second item's loads issued before the first is decoded) 3-4% slower.
 struct GatherShape {
     bool large;
     int wpb;
+    int rpw;  // quantized work items per wave (SLHIP_GATHER_RPW = 1 or 2)
 };
 
 static GatherShape gather_shape()
 {
-    return GatherShape{env_int("SLHIP_GATHER_ITEM", 1) != 0, env_int("SLHIP_GATHER_WPB", 4) == 1 ? 1 : 4};
+    return GatherShape{env_int("SLHIP_GATHER_ITEM", 1) != 0, env_int("SLHIP_GATHER_WPB", 4) == 1 ? 1 : 4,
+                       env_int("SLHIP_GATHER_RPW", 1) == 2 ? 2 : 1};
 }
 
-template <int FMT, int DTO, int CB, int WPB>
+template <int FMT, int DTO, int CB, int WPB, int RPW>
 static int launch_quant_shape(GatherArgs a, hipStream_t st)
 {
     a.chunks = (a.D / 32 + CB - 1) / CB;
-    const int64_t blocks = (a.N * a.chunks + WPB - 1) / WPB;
+    const int64_t waves = (a.N * a.chunks + RPW - 1) / RPW;
+    const int64_t blocks = (waves + WPB - 1) / WPB;
     if (blocks > 0x7FFFFFFF) return fail(SLHIP_ERR_UNSUPPORTED, "gather: grid too large");
-    gather_quant<FMT, DTO, CB, WPB><<<static_cast<unsigned>(blocks), 64 * WPB, 0, st>>>(a);
+    gather_quant<FMT, DTO, CB, WPB, RPW><<<static_cast<unsigned>(blocks), 64 * WPB, 0, st>>>(a);
     return check_launch("gather_quant");
 }
 
@@ -337,8 +403,9 @@ template <int FMT, int DTO>
 static int launch_quant(const GatherArgs& a, hipStream_t st)
 {
     const GatherShape g = gather_shape();
-    if (g.large) return g.wpb == 1 ? launch_quant_shape<FMT, DTO, 128, 1>(a, st) : launch_quant_shape<FMT, DTO, 128, 4>(a, st);
-    return g.wpb == 1 ? launch_quant_shape<FMT, DTO, 16, 1>(a, st) : launch_quant_shape<FMT, DTO, 16, 4>(a, st);
+    if (!g.large) return g.wpb == 1 ? launch_quant_shape<FMT, DTO, 16, 1, 1>(a, st) : launch_quant_shape<FMT, DTO, 16, 4, 1>(a, st);
+    if (g.rpw == 2) return launch_quant_shape<FMT, DTO, 128, 4, 2>(a, st);
+    return g.wpb == 1 ? launch_quant_shape<FMT, DTO, 128, 1, 1>(a, st) : launch_quant_shape<FMT, DTO, 128, 4, 1>(a, st);
 }
 
 template <int FMT, int DTO, int STEPS, int WPB>

@@ -43,6 +43,12 @@ static constexpr int kMaxDevices = 64;
 static std::mutex g_err_mu;
 static uint32_t* g_err_word[kMaxDevices] = {};
 
+// The gather index-error word: {raised, id low, id high, V}. A file-scope device variable (zero at load),
+// so that no call -- including the first one under graph capture -- allocates; each device holds its own
+// copy, whose address is looked up once per device. In host code only that address is used: the
+// variable's name there is a host-side stand-in.
+__device__ __align__(16) uint32_t g_index_error[4];
+
 int index_error_word(uint32_t** word)
 {
     int dev = 0;
@@ -51,8 +57,7 @@ int index_error_word(uint32_t** word)
     std::lock_guard<std::mutex> lock(g_err_mu);
     if (!g_err_word[dev]) {
         void* p = nullptr;
-        SLHIP_CHECK_HIP(hipMalloc(&p, 16));
-        SLHIP_CHECK_HIP(hipMemset(p, 0, 16));
+        SLHIP_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(g_index_error)));
         g_err_word[dev] = static_cast<uint32_t*>(p);
     }
     *word = g_err_word[dev];
@@ -291,7 +296,7 @@ SLHIP_API int slhip_graph_end(slhip_stream stream, slhip_graph* graph)
     SLHIP_CHECK_HIP(hipStreamEndCapture(to_stream(stream), &g));
     hipGraphExec_t exec = nullptr;
     hipError_t e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
-    hipGraphDestroy(g);
+    (void)hipGraphDestroy(g);
     if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
     *graph = exec;
     return SLHIP_OK;

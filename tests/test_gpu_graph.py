@@ -45,3 +45,51 @@ def test_graph_replays_match_eager(device):
             assert_bf16_close(d.get(po, (64, 4096), np.uint16), oref, what=f"replay {rep} swiglu")
             assert_bits_equal(d.get(pe, (128, 4096), np.uint16), eref, what=f"replay {rep} gather")
         del g
+
+
+_FIRST_CALL_CAPTURED = r'''
+import sys
+import numpy as np
+sys.path.insert(0, sys.argv[1])
+from sharplight_amd import native, synth
+import oracle
+# No slhip_set_device and no eager gather before the capture: the gather inside the graph is the first
+# library call that needs the device's index-error word.
+c = synth.c5("q8_0", V=300, N=64)
+st = native.Stream()
+pt, pi = native.DeviceBuffer.from_numpy(c["table"]), native.DeviceBuffer.from_numpy(c["ids"])
+py = native.DeviceBuffer(64 * 4096 * 2)
+native.synchronize()
+g = native.Graph(st, lambda: native.gather("q8_0", pt, 300, 4096, pi, 64, "bf16", py, stream=st.handle))
+for _ in range(3):
+    g.launch(st)
+    st.sync()
+    got = py.download((64, 4096), np.uint16)
+    ref = oracle.gather_as("q8_0", c["table"], 300, 4096, c["ids"], dtype="bf16")
+    assert np.array_equal(got, ref)
+bad = c["ids"].copy()
+bad[5] = 300
+pi.upload(bad)
+native.synchronize()
+g.launch(st)
+try:
+    st.sync()
+    raise SystemExit("no index error")
+except IndexError as e:
+    assert "300" in str(e), e
+print("ok")
+'''
+
+
+def test_first_gather_under_capture_needs_no_allocation(device, tmp_path):
+    """The gather index-error word is a device variable: a gather captured before any other library call
+    on the device (so nothing could have allocated for it) records, replays and reports a bad id."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    script = tmp_path / "first_call.py"
+    script.write_text(_FIRST_CALL_CAPTURED)
+    log("subprocess: first gather under capture")
+    r = subprocess.run([sys.executable, str(script), root], capture_output=True, text=True, timeout=110)
+    assert r.returncode == 0 and r.stdout.strip().endswith("ok"), r.stdout + r.stderr
