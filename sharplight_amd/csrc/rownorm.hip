@@ -57,105 +57,107 @@ __global__ __launch_bounds__(1024) void rownorm_vec(RowNormArgs a, int wpr)
     __shared__ float red[4 * 16];
 
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = wave_id();
     const int group = wave / wpr;
     const int wig = wave - group * wpr;
     const int groups = blockDim.x / (64 * wpr);
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * groups + group;
-    const bool live = row < a.rows;
+    const int64_t row0 = static_cast<int64_t>(blockIdx.x) * groups + group;
     const int tpr = 64 * wpr;
     const int t = wig * 64 + lane;
     const int nvec = static_cast<int>(a.D / E);
 
-    float v[NV][E];
+    // Every load and store below is unconditional and each lane issues the same number of them: a lane
+    // past the row's end works on the row's last vector and a group past the last row on the last row,
+    // storing the same bytes as their owners, and masked values are kept out of the sums. (A memory
+    // operation under a divergent branch makes the compiler wait for all outstanding ones afterwards.)
+    const int64_t row = row0 < a.rows ? row0 : a.rows - 1;
+    int jv[NV];
+    bool own[NV];
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        const int j = t + k * tpr;
+        own[k] = j < nvec;
+        jv[k] = own[k] ? j : nvec - 1;
+    }
     const char* xr = static_cast<const char*>(a.x) + row * a.xs * VI::BYTES;
-    if (live) {
-        uint4 raw[NV];
+    uint4 raw[NV], rraw[NV];
+#pragma unroll
+    for (int k = 0; k < NV; k++) raw[k] = load_nt(xr + static_cast<int64_t>(jv[k]) * 16);
+    if (RES) {
+        const char* rr = static_cast<const char*>(a.res) + row * a.rs * VI::BYTES;
+#pragma unroll
+        for (int k = 0; k < NV; k++) rraw[k] = load_nt(rr + static_cast<int64_t>(jv[k]) * 16);
+    }
+    // The norm weight is read with the row data, ahead of the reduction, rather than after it.
+    float wv[NV][E];
+    const bool has_w = a.w != nullptr, has_b = a.b != nullptr;
+    if (has_w) {
 #pragma unroll
         for (int k = 0; k < NV; k++) {
-            int j = t + k * tpr;
-            if (j < nvec) raw[k] = load_nt(xr + static_cast<int64_t>(j) * 16);
+            const float4* wp = reinterpret_cast<const float4*>(a.w + static_cast<int64_t>(jv[k]) * E);
+#pragma unroll
+            for (int q4 = 0; q4 < E / 4; q4++) {
+                const float4 w4 = wp[q4];
+                wv[k][4 * q4 + 0] = w4.x;
+                wv[k][4 * q4 + 1] = w4.y;
+                wv[k][4 * q4 + 2] = w4.z;
+                wv[k][4 * q4 + 3] = w4.w;
+            }
         }
+    }
+
+    float v[NV][E];
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        VI::unpack(raw[k], v[k]);
         if (RES) {
-            const char* rr = static_cast<const char*>(a.res) + row * a.rs * VI::BYTES;
-            uint4 rraw[NV];
+            float rf[E];
+            VI::unpack(rraw[k], rf);
 #pragma unroll
-            for (int k = 0; k < NV; k++) {
-                int j = t + k * tpr;
-                if (j < nvec) rraw[k] = load_nt(rr + static_cast<int64_t>(j) * 16);
-            }
-#pragma unroll
-            for (int k = 0; k < NV; k++) {
-                int j = t + k * tpr;
-                if (j < nvec) {
-                    float xf[E], rf[E];
-                    VI::unpack(raw[k], xf);
-                    VI::unpack(rraw[k], rf);
-#pragma unroll
-                    for (int e = 0; e < E; e++) v[k][e] = xf[e] + rf[e];
-                }
-            }
-            if (a.h) {
-                char* hr = static_cast<char*>(a.h) + row * a.hs * VI::BYTES;
-#pragma unroll
-                for (int k = 0; k < NV; k++) {
-                    int j = t + k * tpr;
-                    if (j < nvec) store_nt(hr + static_cast<int64_t>(j) * 16, VI::pack(v[k]));
-                }
-            }
-        } else {
-#pragma unroll
-            for (int k = 0; k < NV; k++) {
-                int j = t + k * tpr;
-                if (j < nvec) VI::unpack(raw[k], v[k]);
-            }
+            for (int e = 0; e < E; e++) v[k][e] += rf[e];
         }
+    }
+    if (RES && a.h) {
+        char* hr = static_cast<char*>(a.h) + row * a.hs * VI::BYTES;
+#pragma unroll
+        for (int k = 0; k < NV; k++) store_nt(hr + static_cast<int64_t>(jv[k]) * 16, VI::pack(v[k]));
     }
 
     const float inv_d = 1.0f / static_cast<float>(a.D);
     float mean = 0.f, scale;
     if (a.kind == SLHIP_NORM_LAYER) {
         float s = 0.f;
-        if (live) {
 #pragma unroll
-            for (int k = 0; k < NV; k++)
-                if (t + k * tpr < nvec)
+        for (int k = 0; k < NV; k++)
 #pragma unroll
-                    for (int e = 0; e < E; e++) s += v[k][e];
-        }
+            for (int e = 0; e < E; e++) s += own[k] ? v[k][e] : 0.0f;
         mean = group_reduce<4>(s, wpr, group, wig, red) * inv_d;
         float q = 0.f;
-        if (live) {
 #pragma unroll
-            for (int k = 0; k < NV; k++)
-                if (t + k * tpr < nvec)
+        for (int k = 0; k < NV; k++)
 #pragma unroll
-                    for (int e = 0; e < E; e++) {
-                        float d = v[k][e] - mean;
-                        q = fmaf(d, d, q);
-                    }
-        }
-        float var = group_reduce<4>(q, wpr, group, wig, red) * inv_d;
+            for (int e = 0; e < E; e++) {
+                const float d = own[k] ? v[k][e] - mean : 0.0f;
+                q = fmaf(d, d, q);
+            }
+        const float var = group_reduce<4>(q, wpr, group, wig, red) * inv_d;
         scale = 1.0f / sqrtf(var + a.eps);
     } else {
         float q = 0.f;
-        if (live) {
 #pragma unroll
-            for (int k = 0; k < NV; k++)
-                if (t + k * tpr < nvec)
+        for (int k = 0; k < NV; k++)
 #pragma unroll
-                    for (int e = 0; e < E; e++) q = fmaf(v[k][e], v[k][e], q);
-        }
-        float ss = group_reduce<4>(q, wpr, group, wig, red);
+            for (int e = 0; e < E; e++) {
+                const float x = own[k] ? v[k][e] : 0.0f;
+                q = fmaf(x, x, q);
+            }
+        const float ss = group_reduce<4>(q, wpr, group, wig, red);
         scale = a.kind == SLHIP_NORM_RMS ? 1.0f / sqrtf(ss * inv_d + a.eps) : 1.0f / sqrtf(ss + a.eps);
     }
-    if (!live) return;
 
     char* yr = static_cast<char*>(a.y) + row * a.ys * Vec<DTO>::BYTES;
 #pragma unroll
     for (int k = 0; k < NV; k++) {
-        int j = t + k * tpr;
-        if (j >= nvec) continue;
         float o[E];
         if (a.kind == SLHIP_NORM_LAYER) {
 #pragma unroll
@@ -164,29 +166,22 @@ __global__ __launch_bounds__(1024) void rownorm_vec(RowNormArgs a, int wpr)
 #pragma unroll
             for (int e = 0; e < E; e++) o[e] = v[k][e] * scale;
         }
-        if (a.w) {
-            const float4* wp = reinterpret_cast<const float4*>(a.w + static_cast<int64_t>(j) * E);
+        if (has_w) {
 #pragma unroll
-            for (int q4 = 0; q4 < E / 4; q4++) {
-                float4 w4 = wp[q4];
-                o[4 * q4 + 0] *= w4.x;
-                o[4 * q4 + 1] *= w4.y;
-                o[4 * q4 + 2] *= w4.z;
-                o[4 * q4 + 3] *= w4.w;
-            }
+            for (int e = 0; e < E; e++) o[e] *= wv[k][e];
         }
-        if (a.b) {
-            const float4* bp = reinterpret_cast<const float4*>(a.b + static_cast<int64_t>(j) * E);
+        if (has_b) {  // LayerNorm only: the bias is read here, off the common path
+            const float4* bp = reinterpret_cast<const float4*>(a.b + static_cast<int64_t>(jv[k]) * E);
 #pragma unroll
             for (int q4 = 0; q4 < E / 4; q4++) {
-                float4 b4 = bp[q4];
+                const float4 b4 = bp[q4];
                 o[4 * q4 + 0] += b4.x;
                 o[4 * q4 + 1] += b4.y;
                 o[4 * q4 + 2] += b4.z;
                 o[4 * q4 + 3] += b4.w;
             }
         }
-        store_packed<DTO, E>(yr + static_cast<int64_t>(j) * E * Vec<DTO>::BYTES, o);
+        store_packed<DTO, E>(yr + static_cast<int64_t>(jv[k]) * E * Vec<DTO>::BYTES, o);
     }
 }
 
@@ -282,11 +277,11 @@ static int dispatch(const RowNormArgs& a, hipStream_t st)
                   (!a.w || aligned16(a.w)) && (!a.b || aligned16(a.b));
     int64_t nvec = a.D / E;
     if (vec_ok && nvec <= 8 * 64 * 16) {
-        // Row group sized for ~2 vectors (32 bytes) per lane and input: measured on MI355X at [8192, 4096]
-        // bf16 this beats one wave per row (8 vectors per lane) by ~7%, as the smaller register footprint
-        // keeps 8 waves per SIMD in flight. Widened further while the launch has fewer than ~4096 waves.
+        // Row group sized for ~4 vectors (64 bytes) per lane and input: measured on MI355X at [8192, 4096]
+        // bf16 (residual add) this beats 2 vectors per lane by ~2.5% and 8 vectors (one wave per row) by
+        // more. Widened further while the launch has fewer than ~4096 waves.
         int wpr = 1;
-        while (wpr < 16 && nvec > static_cast<int64_t>(2) * 64 * wpr) wpr *= 2;
+        while (wpr < 16 && nvec > static_cast<int64_t>(4) * 64 * wpr) wpr *= 2;
         while (wpr < 16 && a.rows * wpr < 4096 && nvec >= static_cast<int64_t>(64) * wpr * 2) wpr *= 2;
         int forced = env_int("SLHIP_ROWNORM_WPR", 0);
         if (forced == 1 || forced == 2 || forced == 4 || forced == 8 || forced == 16) {
