@@ -200,9 +200,10 @@ class CopyRef(Workload):
         self.desc = "plain copy, 256 MiB in + 256 MiB out"
         self.bytes_per_step = 2 * 2 * self.n
         R = copies_for(self.bytes_per_step)
-        self.x, self.y = Rot(None, 2 * self.n, R), Rot(None, 2 * self.n, R)
-        native.call("slhip_memset", self.x.buf.ptr, 0, self.x.buf.nbytes, None)
-        native.synchronize()
+        # Random values, like every workload's inputs: streaming zeros measured ~4% faster on MI355X
+        # (6715 vs 6467 GB/s for this copy), which would overstate the ceiling.
+        self.x = Rot(synth.normal(0, 7, (self.n,), dtype="bf16"), 2 * self.n, R)
+        self.y = Rot(None, 2 * self.n, R)
 
     def launch(self, i, stream):
         native.convert("bf16", "bf16", self.x.slot(i), self.y.slot(i), self.n, stream=stream)
@@ -520,7 +521,7 @@ def main():
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / PEAK_GBS, 4),
                 "traffic": traffic.get("bytes_per_launch") if traffic else None,
-                "kernel": "rownorm_vec<bf16,bf16,NV=2,RES> x 4 waves per row (slhip_rownorm)",
+                "kernel": (traffic or {}).get("kernel", "rownorm_vec") + " (slhip_rownorm)",
                 "algorithmic_bytes": bps, "avg_launch_us": round(kernel_avg_s * 1e6, 2)}
     wl_desc = wl.desc
     rot = wl.x.R
