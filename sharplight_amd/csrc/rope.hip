@@ -5,20 +5,21 @@
 // output of RowOp RmsNorm (RowOp.cs:63-77), which is what the Vulkan lowerer fuses into its rope kernel
 // (src/Sharplight.Shaders/Lowering/GraphLowerer.Fusion.cs:618-630, Kernels/rope.slang:150-195):
 //   inv_i = base^(-2i/dims) * freq_scale and theta = pos * inv_i (/ ff[i]) in f64;
-//   c = (float)cos(theta) * attn_factor, s = (float)sin(theta) * attn_factor;
+//   c = (float)cos(theta) * attn_factor, s = (float)sin(theta) * attn_factor (cos/sin within 1 f32 ulp);
 //   optional norm: x' = (x * (1/sqrt(sum(x^2)/D + eps))) * w;
 //   neox pairs (i, i + dims/2), normal pairs (2i, 2i+1): y0 = x0*c - x1*s, y1 = x0*s + x1*c;
 //   elements from dims to D are copied (normed when the norm is fused).
-// The angles are f64 because positions reach 32767 and more: an f32 argument would be off by ~1e-3 rad.
+// The angles and their reduction are f64 because positions reach 32767 and more: an f32 argument would
+// be off by ~1e-3 rad; sin/cos of the reduced angle (|r| <= pi/4) are evaluated in f32.
 //
 // Layout (vector path): a flat grid of independent waves. A wave owns one token and a group of 64/L
 // whole head rows of one tensor, L = dims/2 / V lanes per head row (V = elements per 16-byte vector);
 // lane c of a head holds pairs [c*V, c*V + V) as two 16-byte vectors, so loads and stores are fully
 // used 16-byte accesses and the fused norm is a butterfly over the L lanes of a head. Each wave issues
-// its loads and norm weights, then computes the token's dims/2 (cos, sin) pairs in f64 into its own LDS
-// slice (one angle per lane), and never waits for another wave: recomputing the table per wave costs
-// about one f64 sincos per lane, far less than a block-wide barrier that holds every wave of a token
-// until the table is ready.
+// its loads and norm weights, then computes the token's dims/2 (cos, sin) pairs (f64 angle and
+// reduction, f32 series) into its own LDS slice, one angle per lane, and never waits for another wave:
+// recomputing the table per wave costs about one sincos per lane, far less than a block-wide barrier
+// that holds every wave of a token until the table is ready.
 #include "common.hpp"
 #include "rope_math.hpp"
 
@@ -67,9 +68,9 @@ __device__ __forceinline__ float2 table_entry(const RopeArgs& a, int64_t t, int 
                                                    : exp2(a.l2b * (-2.0 * i / a.dims)) * static_cast<double>(a.fs);
     double theta = static_cast<double>(a.pos[t]) * inv;
     if (a.ff) theta /= static_cast<double>(a.ff[i]);
-    double s, c;
-    sincos_f64(theta, &s, &c);
-    return make_float2(static_cast<float>(c) * a.af, static_cast<float>(s) * a.af);
+    float s, c;
+    sincos_f64_to_f32(theta, &s, &c);
+    return make_float2(c * a.af, s * a.af);
 }
 
 // The same entry from inputs already in registers: theta = pos * inv (/ ff), all f64.
@@ -77,9 +78,9 @@ __device__ __forceinline__ float2 table_value(const RopeArgs& a, double p, doubl
 {
     double theta = p * inv;
     if (a.ff) theta /= static_cast<double>(ff);
-    double s, c;
-    sincos_f64(theta, &s, &c);
-    return make_float2(static_cast<float>(c) * a.af, static_cast<float>(s) * a.af);
+    float s, c;
+    sincos_f64_to_f32(theta, &s, &c);
+    return make_float2(c * a.af, s * a.af);
 }
 
 __device__ __forceinline__ int tensor_of(const RopeArgs& a, int64_t gh)
