@@ -14,8 +14,10 @@ Also in the line:
 * ``cpu_baseline`` -- the reference CPU provider's arithmetic (the C oracle restating src/Sharplight.Cpu,
   threaded like CpuParallel) timed on this host on a bounded sample of the same workload.
 * ``ops`` -- every BASELINE config (C1..C5) and a plain-copy reference: median per-launch microseconds
-  (graph replay of 50 rotated launches, HIP events), GB/s and % of peak on the GPU, and the CPU oracle's
-  time for the same op.
+  (graph replay of 50 rotated launches, HIP events), GB/s and % of peak on the GPU, a plain copy of the
+  same byte count with random data timed the same way (``copy_us_same_bytes``; ``pct_of_copy`` = the op's
+  speed relative to it: what a pure stream reaches at that size, where launch ramp and drain weigh more
+  than at the 256 MiB reference), and the CPU oracle's time for the same op.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c2] [--no-cpu] [--no-ops]
        python bench.py --profile OP --steps K      (one workload, eager launches, for rocprofv3)
@@ -203,6 +205,23 @@ class CopyRef(Workload):
         # Random values, like every workload's inputs: streaming zeros measured ~4% faster on MI355X
         # (6715 vs 6467 GB/s for this copy), which would overstate the ceiling.
         self.x = Rot(synth.normal(0, 7, (self.n,), dtype="bf16"), 2 * self.n, R)
+        self.y = Rot(None, 2 * self.n, R)
+
+    def launch(self, i, stream):
+        native.convert("bf16", "bf16", self.x.slot(i), self.y.slot(i), self.n, stream=stream)
+
+
+class SameBytesCopy(Workload):
+    """A plain copy moving the same number of bytes as an op (half read, half written), random data:
+    what a pure stream achieves at that size -- launch ramp and drain weigh more at small sizes."""
+
+    def __init__(self, nbytes: int):
+        self.n = max(nbytes // 4, 512)
+        self.name = f"copy_{nbytes}B"
+        self.bytes_per_step = 4 * self.n
+        R = copies_for(self.bytes_per_step)
+        bits = np.random.default_rng(11).integers(0, 1 << 16, size=self.n, dtype=np.uint16)
+        self.x = Rot(bits, 2 * self.n, R)
         self.y = Rot(None, 2 * self.n, R)
 
     def launch(self, i, stream):
@@ -468,6 +487,7 @@ def main():
     ap.add_argument("--only", default="", help="comma list of op names (prefixes) for the ops table")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-ops", action="store_true")
+    ap.add_argument("--no-ceiling", action="store_true", help="skip the same-bytes copy next to each op")
     ap.add_argument("--launches", type=int, default=50, help="launches per graph in the ops table")
     ap.add_argument("--replays", type=int, default=10, help="graph replays per op in the ops table")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -550,6 +570,12 @@ def main():
             med = float(np.median(us))
             ops[name] = {"us": round(med, 2), "us_min": round(float(us.min()), 2), "timing": "graph replay", "bytes": int(b),
                          "GB/s": round(b / med / 1e3, 1), "pct_peak": round(100 * b / med / 1e3 / PEAK_GBS, 1)}
+            if not args.no_ceiling and name != CopyRef.name:
+                cw = SameBytesCopy(int(b))
+                cus = float(np.median(time_per_launch(cw, args.launches, args.replays, stream)))
+                cw.free()
+                ops[name]["copy_us_same_bytes"] = round(cus, 2)
+                ops[name]["pct_of_copy"] = round(100 * cus / med, 1)
             log(f"bench: {name}: {med:.2f} us, {b / med / 1e3:.1f} GB/s")
 
     # -- CPU baseline --
