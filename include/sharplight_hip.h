@@ -9,7 +9,8 @@
  *  - Every function returns an int status: SLHIP_OK (0) or a negative slhip_status. The message of the
  *    last failure on the calling thread is slhip_last_error(). The managed side turns statuses into
  *    the exceptions the reference's providers throw: SLHIP_ERR_INVALID -> ArgumentException,
- *    SLHIP_ERR_UNSUPPORTED -> NotSupportedException, SLHIP_ERR_INDEX -> ArgumentOutOfRangeException.
+ *    SLHIP_ERR_UNSUPPORTED -> NotSupportedException, SLHIP_ERR_INDEX -> ArgumentOutOfRangeException,
+ *    SLHIP_ERR_CACHE -> InvalidOperationException.
  *  - Tensor pointers are device pointers (slhip_malloc). Sizes and strides are in ELEMENTS of the
  *    tensor's own dtype, rows are the leading dims flattened, the normalized/activated axis is last and
  *    dense.
@@ -17,8 +18,9 @@
  *    nothing is synchronous except slhip_stream_sync / slhip_event_synchronize / slhip_memcpy_*_sync.
  *  - Ops read inputs and write outputs only; outputs may alias an input of the same shape and layout
  *    (in-place) unless stated otherwise.
- *  - No op entry point allocates device memory, except slhip_gather's first call on a device, which
- *    allocates that device's 16-byte index-error word.
+ *  - No op entry point allocates device memory. Errors found by a kernel (a gather id outside the
+ *    table, a KV-cache row outside the cache) go to a per-device error word, a device variable of the
+ *    library, and are reported by the next slhip_stream_sync.
  */
 #ifndef SHARPLIGHT_HIP_H
 #define SHARPLIGHT_HIP_H
@@ -36,7 +38,7 @@ extern "C" {
 #define SLHIP_API __attribute__((visibility("default")))
 #endif
 
-#define SLHIP_ABI_VERSION 1
+#define SLHIP_ABI_VERSION 2
 
 typedef enum slhip_status {
     SLHIP_OK = 0,
@@ -44,7 +46,8 @@ typedef enum slhip_status {
     SLHIP_ERR_UNSUPPORTED = -2, /* valid request this library has no kernel for */
     SLHIP_ERR_HIP = -3,         /* the HIP runtime reported an error */
     SLHIP_ERR_INDEX = -4,       /* a gather index was outside [0, V) (reported by slhip_stream_sync) */
-    SLHIP_ERR_NO_DEVICE = -5    /* no usable device / driver */
+    SLHIP_ERR_NO_DEVICE = -5,   /* no usable device / driver */
+    SLHIP_ERR_CACHE = -6        /* a KV-cache row outside the cache or block table (at slhip_stream_sync) */
 } slhip_status;
 
 /* Element types of activations. */
@@ -175,8 +178,33 @@ SLHIP_API int slhip_gated_act(int act, int dtype_in, int dtype_out, const void* 
                               int64_t rows, int64_t cols, int64_t gate_stride, int64_t up_stride, int64_t out_stride,
                               slhip_stream stream);
 
+/* Destination rows of KV-cache writes (CacheWrite, src/Sharplight.Core/Graph/StandardOps.cs:310-319):
+ * token t of a launch goes to cache row
+ *   SLHIP_ROWS_PAST   n_past + t
+ *   SLHIP_ROWS_SEQ    slot * (ctx / slots) + position, from sequence rows seq[t] = (slot, position, ., .)
+ *   SLHIP_ROWS_PAGED  pages[slot, position / block_size] * block_size + position % block_size
+ * as src/Sharplight.Cpu/CacheWriteOp.cs:103-155 and KvPages.cs:28-49 map them. PAST overflow
+ * (n_past + T > ctx) is refused at the call; a SEQ/PAGED row outside the cache or block table is skipped
+ * and reported as SLHIP_ERR_CACHE by the next slhip_stream_sync (the other rows are written). */
+typedef enum slhip_rows_mode { SLHIP_ROWS_PAST = 0, SLHIP_ROWS_SEQ = 1, SLHIP_ROWS_PAGED = 2 } slhip_rows_mode;
+
+typedef struct slhip_cache_rows {
+    int32_t mode;
+    int32_t reserved;
+    int64_t ctx;              /* rows of the cache */
+    int64_t n_past;           /* PAST */
+    const int32_t* seq;       /* SEQ, PAGED: [T, 4] int32 */
+    int64_t slots;            /* SEQ: sequences sharing the cache in equal parts */
+    const int32_t* pages;     /* PAGED: block table [page_slots, blocks_per_slot] int32 */
+    int64_t page_slots, blocks_per_slot, block_size;
+} slhip_cache_rows;
+
 /* One tensor of a rope launch: x and y are [T, heads, D] with the given token/head strides
- * (innermost stride 1). norm_w: f32 [D] per-head RMSNorm weight, used when cfg->norm is set. */
+ * (innermost stride 1). norm_w: f32 [D] per-head RMSNorm weight, used when cfg->norm is set.
+ * rows: NULL, or y is a KV cache whose row t' = rows(t) receives token t (y_stride_t is then the cache
+ * row stride): the reference lowerer's Rope absorbed into its CacheWrite
+ * (src/Sharplight.Shaders/Lowering/GraphLowerer.Fusion.cs:633-648, Kernels/rope.slang:110-147).
+ * All tensors of one launch that have rows must describe the same rows. */
 typedef struct slhip_rope_tensor {
     const void* x;
     void* y;
@@ -184,6 +212,7 @@ typedef struct slhip_rope_tensor {
     int64_t heads;
     int64_t x_stride_t, x_stride_h;
     int64_t y_stride_t, y_stride_h;
+    const slhip_cache_rows* rows;
 } slhip_rope_tensor;
 
 typedef struct slhip_rope_cfg {
@@ -203,7 +232,8 @@ typedef struct slhip_rope_cfg {
  *   inv_i = base^(-2i/dims) * freq_scale (f64); theta = pos[t] * inv_i (/ ff[i]) (f64);
  *   c = (float)cos(theta) * attn_factor, s = (float)sin(theta) * attn_factor;
  *   y0 = x0*c - x1*s, y1 = x0*s + x1*c.
- * pos: int32 [T]; ff: f32 [dims/2] frequency divisors or NULL. dtype_in/dtype_out: F32 or BF16.
+ * pos: int32 [T]; ff: f32 [dims/2] frequency divisors or NULL. dtype_in: F32 or BF16; dtype_out: F32, F16
+ * (for f16 caches) or BF16.
  * Replaces: RopeOp (src/Sharplight.Cpu/RopeOp.cs:28-183) after RowOp RmsNorm, and the Vulkan rope kernels
  * with the absorbed norm (GraphLowerer.Fusion.cs:618-630, GraphLowerer.Transformer.cs:40, Kernels/rope.slang:150-195)
  * for the single-axis styles.
@@ -222,6 +252,14 @@ SLHIP_API int slhip_rope(int dtype_in, int dtype_out, const slhip_rope_tensor* t
  */
 SLHIP_API int slhip_gather(int format, const void* table, int64_t V, int64_t D, const int32_t* ids, int64_t N,
                            int dtype_out, void* y, int64_t y_stride, slhip_stream stream);
+
+/*
+ * KV-cache write (CacheWrite without an absorbed producer; src/Sharplight.Cpu/CacheWriteOp.cs:129-175):
+ * token t's `inner` values x[t*x_stride, +inner) go to cache[rows(t)*inner, +inner), converted from
+ * dtype_in (F32, BF16) to the cache's dtype (F32, F16 rounding to nearest even as .NET's (Half), BF16).
+ */
+SLHIP_API int slhip_cache_write(int dtype_in, int dtype_cache, const void* x, int64_t x_stride, int64_t T,
+                                int64_t inner, void* cache, const slhip_cache_rows* rows, slhip_stream stream);
 
 /*
  * Element type conversion y = cast(x) of n elements (F32, F16, BF16 in any direction); f32 -> bf16 rounds

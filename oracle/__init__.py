@@ -79,6 +79,9 @@ def _declare(L):
         "orc_unary_mt": (None, [_I, _P, _P, _I64]),
         "orc_rope_mt": (None, [_P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _F, _F, _F]),
         "orc_gather_mt": (_I, [_I, _P, _I64, _I64, _P, _I64, _P, ctypes.POINTER(_I64)]),
+        "orc_f32_to_f16_n": (None, [_P, _P, _I64]),
+        "orc_cache_rows": (_I, [_I, _I64, _I64, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, ctypes.c_char_p, _I64]),
+        "orc_cache_write": (None, [_I, _P, _I64, _P, _I64, _P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -262,3 +265,45 @@ def qk_norm_rope(x, pos, w=None, eps=1e-6, dtype="f32", **rope_kw):
 
 def gather_as(fmt, table, V, D, ids, dtype="f32"):
     return _out(gather(fmt, table, V, D, ids), dtype)
+
+
+# ---- KV cache writes -------------------------------------------------------------------------------
+
+ROWS = {"past": 0, "seq": 1, "paged": 2}
+
+
+class CacheOverflow(RuntimeError):
+    """The reference's CacheWriteOp / KvPages throw InvalidOperationException (CacheWriteOp.cs:103-127,
+    KvPages.cs:38-49)."""
+
+
+def to_f16(x):
+    x = _c(x, np.float32)
+    y = np.empty(x.shape, np.uint16)
+    lib().orc_f32_to_f16_n(_p(x), _p(y), x.size)
+    return y
+
+
+def cache_rows(mode, T, ctx, n_past=0, seq=None, slots=1, pages=None, block_size=16):
+    """Cache row of each token (CacheWriteOp's mapping); raises CacheOverflow like the reference."""
+    seq = _c(seq, np.int32)
+    pages = _c(pages, np.int32)
+    page_slots, bps = (pages.shape if pages is not None else (0, 0))
+    rows = np.empty(max(T, 1), np.int64)
+    err = ctypes.create_string_buffer(256)
+    st = lib().orc_cache_rows(ROWS[mode], T, ctx, n_past, _p(seq), slots, _p(pages), page_slots, bps, block_size,
+                              _p(rows), err, len(err))
+    if st:
+        raise CacheOverflow(err.value.decode())
+    return rows[:T]
+
+
+def cache_write(cache, x, rows, cache_type):
+    """CacheWriteOp.Body: x [T, inner] f32 into ``cache`` (numpy array: f32, or uint16 bits of f16/bf16)
+    at rows[t]; in place."""
+    x = _c(x, np.float32)
+    T = x.shape[0]
+    inner = x.size // max(T, 1)
+    rows = _c(rows, np.int64)
+    lib().orc_cache_write(FORMATS[cache_type], _p(cache), inner, _p(x), T, _p(rows))
+    return cache

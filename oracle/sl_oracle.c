@@ -14,6 +14,7 @@
 
 #include <math.h>
 #include <pthread.h>
+#include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -457,6 +458,111 @@ int orc_gather(int fmt, const uint8_t* table, int64_t V, int64_t D, const int32_
                int64_t* bad_index)
 {
     return gather_range(fmt, table, V, D, ids, 0, N, y, bad_index);
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* KV cache writes                                                                            */
+/* ------------------------------------------------------------------------------------------ */
+
+/* Simd.FloatToHalf (src/Sharplight.Cpu/Simd.cs:521-525) is .NET's (Half)f, in the .NET runtime rather
+ * than the reference: IEEE round to nearest even with gradual underflow and overflow to infinity; a NaN
+ * keeps its sign and the top 10 bits of its payload with the quiet bit set (sign | 0x7E00 | mant >> 13).
+ * The NaN rule is restated from the runtime's published source (parity unpinned for NaN payloads). */
+uint16_t orc_f32_to_f16(float f)
+{
+    uint32_t b = f2u(f);
+    uint32_t sign = (b >> 16) & 0x8000u;
+    uint32_t exp = (b >> 23) & 0xFFu;
+    uint32_t man = b & 0x7FFFFFu;
+    if (exp == 0xFF) return (uint16_t)(man ? (sign | 0x7E00u | (man >> 13)) : (sign | 0x7C00u));
+    int32_t e = (int32_t)exp - 127 + 15;  /* biased f16 exponent */
+    if (e >= 31) return (uint16_t)(sign | 0x7C00u);
+    uint32_t m = man | (exp ? 0x800000u : 0u);  /* 24-bit significand (f32 subnormals: no implicit 1) */
+    int shift;                                   /* bits dropped from m */
+    uint32_t base;
+    if (e >= 1) {
+        shift = 13;
+        base = ((uint32_t)e << 10);
+        m &= 0x7FFFFFu;  /* the implicit 1 is carried by the exponent field */
+    } else {
+        shift = 14 - e;  /* subnormal f16: value = m * 2^(exp-150) = q * 2^-24 */
+        if (!exp) shift = 200;  /* f32 subnormals are far below the smallest f16 subnormal */
+        base = 0;
+    }
+    if (shift > 31) return (uint16_t)sign;  /* rounds to zero (|f| < 2^-25 at most half an ulp) */
+    uint32_t q = m >> shift;
+    uint32_t rem = m & ((1u << shift) - 1u);
+    uint32_t half = 1u << (shift - 1);
+    if (rem > half || (rem == half && (q & 1u))) q++;  /* may carry into the exponent: still correct */
+    return (uint16_t)(sign | (base + q));
+}
+
+void orc_f32_to_f16_n(const float* x, uint16_t* y, int64_t n)
+{
+    for (int64_t i = 0; i < n; i++) y[i] = orc_f32_to_f16(x[i]);
+}
+
+/* Cache rows of tokens 0..T-1, as CacheWriteOp maps them (src/Sharplight.Cpu/CacheWriteOp.cs:103-155, no
+ * compression): ROWS_PAST row = n_past + t; ROWS_SEQ row = slot * (ctx / slots) + position from sequence
+ * rows seq[T, 4] = (slot, position, ., .); ROWS_PAGED row = table[slot, p / bs] * bs + p % bs
+ * (KvPages.Row, KvPages.cs:28-32). The checks run first, over every token, as CacheWriteOp.Run does
+ * (:103-127; KvPages.Check, KvPages.cs:38-49): 0, or -1 with the message the reference throws. */
+int orc_cache_rows(int mode, int64_t T, int64_t ctx, int64_t n_past, const int32_t* seq, int64_t slots,
+                   const int32_t* pages, int64_t page_slots, int64_t blocks_per_slot, int64_t block_size,
+                   int64_t* rows, char* err, int64_t err_size)
+{
+    if (mode == ORC_ROWS_PAST) {
+        if (n_past < 0 || n_past + T > ctx) {
+            snprintf(err, (size_t)err_size, "KV cache overflow: n_past %lld + T %lld > context %lld.",
+                     (long long)n_past, (long long)T, (long long)ctx);
+            return -1;
+        }
+        for (int64_t t = 0; t < T; t++) rows[t] = n_past + t;
+        return 0;
+    }
+    for (int64_t t = 0; t < T; t++) {
+        int32_t slot = seq[t * 4], p = seq[t * 4 + 1];
+        if (mode == ORC_ROWS_PAGED) {
+            if ((uint64_t)(int64_t)slot >= (uint64_t)page_slots || p < 0 || p >= blocks_per_slot * block_size) {
+                snprintf(err, (size_t)err_size, "Sequence slot %d / position %d outside the block table [%lld, %lld].",
+                         slot, p, (long long)page_slots, (long long)blocks_per_slot);
+                return -1;
+            }
+            int64_t block = pages[(int64_t)slot * blocks_per_slot + p / block_size];
+            if (block < 0 || (block + 1) * block_size > ctx) {
+                snprintf(err, (size_t)err_size, "Block %lld of slot %d (position %d) is outside the KV cache of %lld rows.",
+                         (long long)block, slot, p, (long long)ctx);
+                return -1;
+            }
+            rows[t] = block * block_size + p % block_size;
+        } else {
+            int64_t slot_ctx = ctx / (slots > 0 ? slots : 1);
+            if ((uint64_t)(int64_t)slot >= (uint64_t)slots || (uint64_t)(int64_t)p >= (uint64_t)slot_ctx) {
+                snprintf(err, (size_t)err_size, "KV cache overflow: sequence row %lld slot %d position %d (slot context %lld).",
+                         (long long)t, slot, p, (long long)slot_ctx);
+                return -1;
+            }
+            rows[t] = slot * slot_ctx + p;
+        }
+    }
+    return 0;
+}
+
+/* CacheWriteOp.Body (CacheWriteOp.cs:129-175): token t's `inner` f32 values go to cache row rows[t] as
+ * f32 (copied), f16 (FloatToHalf) or bf16 (FloatToBFloat). */
+void orc_cache_write(int cache_type, void* cache, int64_t inner, const float* x, int64_t T, const int64_t* rows)
+{
+    for (int64_t t = 0; t < T; t++) {
+        const float* src = x + t * inner;
+        int64_t d = rows[t] * inner;
+        if (cache_type == ORC_F32) {
+            memcpy((float*)cache + d, src, (size_t)inner * 4);
+        } else {
+            uint16_t* dst = (uint16_t*)cache + d;
+            for (int64_t i = 0; i < inner; i++)
+                dst[i] = cache_type == ORC_F16 ? orc_f32_to_f16(src[i]) : orc_f32_to_bf16(src[i]);
+        }
+    }
 }
 
 /* ------------------------------------------------------------------------------------------ */

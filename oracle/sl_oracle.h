@@ -58,6 +58,17 @@ int orc_dequant(int fmt, const uint8_t* src, int64_t count, float* dst);
 int orc_gather(int fmt, const uint8_t* table, int64_t V, int64_t D, const int32_t* ids, int64_t N, float* y,
                int64_t* bad_index);
 
+/* ---- KV cache writes (CacheWriteOp.cs, KvPages.cs) ---- */
+enum { ORC_ROWS_PAST = 0, ORC_ROWS_SEQ = 1, ORC_ROWS_PAGED = 2 };
+uint16_t orc_f32_to_f16(float f);
+void orc_f32_to_f16_n(const float* x, uint16_t* y, int64_t n);
+/* Cache row of every token (all checked first); 0, or -1 with the reference's message in err. */
+int orc_cache_rows(int mode, int64_t T, int64_t ctx, int64_t n_past, const int32_t* seq, int64_t slots,
+                   const int32_t* pages, int64_t page_slots, int64_t blocks_per_slot, int64_t block_size,
+                   int64_t* rows, char* err, int64_t err_size);
+/* x [T, inner] f32 -> cache rows[t] (cache_type ORC_F32 / ORC_F16 / ORC_BF16). */
+void orc_cache_write(int cache_type, void* cache, int64_t inner, const float* x, int64_t T, const int64_t* rows);
+
 /* ---- threaded variants for the CPU baseline (CpuParallel.cs:34-78) ---- */
 void orc_set_threads(int threads);
 int orc_get_threads(void);

@@ -23,9 +23,23 @@ int check_launch(const char* kernel);
         if (e_ != hipSuccess) return ::slhip::hip_fail(e_, #call);                                                     \
     } while (0)
 
-// Device word that gather kernels raise on an out-of-range id: [0] flag, [1] the id (low 32 bits),
-// [2] the id (high 32 bits). One per device, allocated on first use.
-int index_error_word(uint32_t** word);
+// The current device's error record, eight 32-bit words that kernels raise (raise_error) and
+// slhip_stream_sync reports: [0] code (0 = none), [1..6] the code's values. A device variable of the
+// library: nothing is allocated for it.
+int error_word(uint32_t** word);
+
+// KV-cache destination rows (slhip_cache_rows) as kernels take them.
+struct CacheRowsDev {
+    int mode;
+    int64_t ctx, n_past;
+    const int32_t* seq;
+    int64_t slots, slot_ctx;
+    const int32_t* pages;
+    int64_t page_slots, bps, bs;
+};
+// Validates `in` for a launch of T tokens (PAST overflow is refused here, as CacheWriteOp.Run throws for
+// it, src/Sharplight.Cpu/CacheWriteOp.cs:118-121) and fills `out`.
+int make_cache_rows(const slhip_cache_rows* in, int64_t T, CacheRowsDev* out);
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
@@ -212,6 +226,80 @@ template <int W> __device__ __forceinline__ float group_sum(float v)
 }
 
 __device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
+
+// ---- device side: errors raised by kernels -----------------------------------------------------------
+
+enum : uint32_t { kErrGatherIndex = 1, kErrCacheSeq = 2, kErrCachePageTable = 3, kErrCacheBlock = 4 };
+
+// Records an error in the device's error record unless one is already there (the first error wins).
+__device__ __forceinline__ void raise_error(uint32_t* err, uint32_t code, uint32_t a, uint32_t b, uint32_t c,
+                                            uint32_t d, uint32_t e, uint32_t f)
+{
+    if (atomicCAS(err, 0u, code) == 0u) {
+        err[1] = a;
+        err[2] = b;
+        err[3] = c;
+        err[4] = d;
+        err[5] = e;
+        err[6] = f;
+    }
+}
+
+// The cache row of token t (CacheWriteOp.Body, src/Sharplight.Cpu/CacheWriteOp.cs:129-155; KvPages.Row,
+// KvPages.cs:28-32), or row -1 with the error the reference would throw (CacheWriteOp.cs:103-117,
+// KvPages.Check, KvPages.cs:38-49) in code/values. Wave-uniform t: the sequence row and block table
+// entry are scalar loads.
+struct CacheRow {
+    int64_t row;
+    uint32_t code;
+    int32_t slot, pos;
+    int64_t v1, v2;
+};
+
+__device__ __forceinline__ CacheRow cache_row(const CacheRowsDev& r, int64_t t)
+{
+    CacheRow o{-1, 0, 0, 0, 0, 0};
+    if (r.mode == SLHIP_ROWS_PAST) {
+        o.row = r.n_past + t;  // checked against ctx on the host
+        return o;
+    }
+    const int32_t slot = r.seq[t * 4], pos = r.seq[t * 4 + 1];
+    o.slot = slot;
+    o.pos = pos;
+    if (r.mode == SLHIP_ROWS_SEQ) {
+        if (static_cast<uint64_t>(static_cast<int64_t>(slot)) >= static_cast<uint64_t>(r.slots) ||
+            static_cast<uint64_t>(static_cast<int64_t>(pos)) >= static_cast<uint64_t>(r.slot_ctx)) {
+            o.code = kErrCacheSeq;
+            o.v1 = r.slot_ctx;
+            return o;
+        }
+        o.row = slot * r.slot_ctx + pos;
+        return o;
+    }
+    if (static_cast<uint64_t>(static_cast<int64_t>(slot)) >= static_cast<uint64_t>(r.page_slots) || pos < 0 ||
+        pos >= r.bps * r.bs) {
+        o.code = kErrCachePageTable;
+        o.v1 = r.page_slots;
+        o.v2 = r.bps;
+        return o;
+    }
+    const int64_t block = r.pages[static_cast<int64_t>(slot) * r.bps + pos / r.bs];
+    if (block < 0 || (block + 1) * r.bs > r.ctx) {
+        o.code = kErrCacheBlock;
+        o.v1 = block;
+        o.v2 = r.ctx;
+        return o;
+    }
+    o.row = block * r.bs + pos % r.bs;
+    return o;
+}
+
+__device__ __forceinline__ void raise_cache_error(uint32_t* err, const CacheRow& c, int64_t t)
+{
+    raise_error(err, c.code, static_cast<uint32_t>(t), static_cast<uint32_t>(c.slot), static_cast<uint32_t>(c.pos),
+                static_cast<uint32_t>(static_cast<uint64_t>(c.v1)), static_cast<uint32_t>(static_cast<uint64_t>(c.v1) >> 32),
+                static_cast<uint32_t>(c.v2));
+}
 
 // Makes this wave's LDS writes visible to its own later LDS reads, for kernels whose waves work on
 // independent items and never wait for each other.

@@ -15,7 +15,7 @@
 // chunks (blocks of 34, 18, 20, 22 or 24 bytes: only 2-byte aligned) are loaded with 16-byte loads into
 // LDS, then each lane decodes VPL consecutive values per output vector, VPL = 16 bytes / output element
 // size (8 for bf16, 4 for f32), so every store instruction writes one contiguous span. An id outside
-// [0, V) zeroes its row and raises the device's index-error word, reported by slhip_stream_sync.
+// [0, V) zeroes its row and raises the device error record, reported by slhip_stream_sync.
 #include "common.hpp"
 
 #include <stdlib.h>
@@ -121,11 +121,8 @@ __device__ __forceinline__ void decode(const uint32_t* s, int j0, float* f)
 
 __device__ __forceinline__ void raise_index_error(uint32_t* err, int64_t id, int64_t V)
 {
-    if (atomicCAS(err, 0u, 1u) == 0u) {
-        err[1] = static_cast<uint32_t>(static_cast<uint64_t>(id));
-        err[2] = static_cast<uint32_t>(static_cast<uint64_t>(id) >> 32);
-        err[3] = static_cast<uint32_t>(V);
-    }
+    raise_error(err, kErrGatherIndex, static_cast<uint32_t>(static_cast<uint64_t>(id)),
+                static_cast<uint32_t>(static_cast<uint64_t>(id) >> 32), static_cast<uint32_t>(V), 0, 0, 0);
 }
 
 // One output vector: VPL values as dtype DTO (16 bytes).
@@ -473,7 +470,7 @@ extern "C" SLHIP_API int slhip_gather(int format, const void* table, int64_t V, 
     if (dtype_out != SLHIP_F32 && dtype_out != SLHIP_BF16)
         return fail(SLHIP_ERR_UNSUPPORTED, "gather: output dtype %d not supported", dtype_out);
     uint32_t* err = nullptr;
-    int stc = index_error_word(&err);
+    int stc = error_word(&err);
     if (stc) return stc;
     GatherArgs a{static_cast<const uint8_t*>(table), V, D, D / bs * bb, ids, N, y, N > 1 ? y_stride : D, err, 1};
     hipStream_t st = to_stream(stream);

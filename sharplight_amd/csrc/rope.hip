@@ -24,6 +24,7 @@
 #include "rope_math.hpp"
 
 #include <stdlib.h>
+#include <string.h>
 
 #include <cmath>
 
@@ -40,6 +41,7 @@ struct RopeTensorDev {
     const float* w;
     int64_t heads, head0;  // head count, and index of the first head in the launch's head numbering
     int64_t xst, xsh, yst, ysh;
+    int to_cache;          // y is a KV cache written at the rows of RopeArgs::rows
 };
 
 struct RopeArgs {
@@ -56,6 +58,8 @@ struct RopeArgs {
     int inv_in_args;         // inv[] holds the inverse frequencies (dims/2 <= kArgInv)
     double l2b;              // log2(base) in f64, for dims/2 > kArgInv
     double inv[kArgInv];     // base^(-2i/dims) * freq_scale in f64, computed on the host
+    CacheRowsDev rows;       // cache rows of the tensors with to_cache
+    uint32_t* err;           // the device error record (cache rows outside the cache)
 };
 
 // Entry i of token t's table. The inverse frequencies come from the host in f64 (std::pow, as RopeOp's
@@ -144,7 +148,6 @@ __global__ __launch_bounds__(64 * kRopeWpb) void rope_vec(RopeArgs a)
     // unconditional: a load under a divergent branch makes the compiler wait for it at the join.
     const int64_t hl = active ? h : heads - 1;
     const char* xr = static_cast<const char*>(xp) + (static_cast<int64_t>(t) * xs + hl * xh) * VI::BYTES;
-    char* yr = static_cast<char*>(yp) + (static_cast<int64_t>(t) * ys + h * yh) * Vec<DTO>::BYTES;
 
     // Table inputs first: entries lane (+ 64), NE per lane. Vector-memory loads complete in order, so a
     // table input loaded after the row's data would make the f64 table wait for the HBM data instead of
@@ -179,6 +182,11 @@ __global__ __launch_bounds__(64 * kRopeWpb) void rope_vec(RopeArgs a)
     // Keeps the instruction scheduler from sinking the loads below the f64 work (it would, to save
     // registers), which would leave the table's latency unhidden.
     __builtin_amdgcn_sched_barrier(0);
+    // The output row: the token itself, or its KV-cache row (scalar loads of its sequence row and block
+    // table entry, only needed by the stores).
+    CacheRow cr{static_cast<int64_t>(t), 0, 0, 0, 0, 0};
+    if (tt.to_cache) cr = cache_row(a.rows, t);
+    char* yr = static_cast<char*>(yp) + (cr.row * ys + h * yh) * Vec<DTO>::BYTES;
     // Lanes past dims/2 rewrite the last entry with the same value.
     float2* ctab = cs[wv];
 #pragma unroll
@@ -231,8 +239,12 @@ __global__ __launch_bounds__(64 * kRopeWpb) void rope_vec(RopeArgs a)
             o[2 * e + 1] = x0 * cv.y + x1 * cv.x;
         }
     }
-    store_packed<DTO, V>(yr + e0 * Vec<DTO>::BYTES, o);
-    store_packed<DTO, V>(yr + e1 * Vec<DTO>::BYTES, o + V);
+    if (cr.row >= 0) {  // wave-uniform: a row outside the cache is skipped and reported
+        store_packed<DTO, V>(yr + e0 * Vec<DTO>::BYTES, o);
+        store_packed<DTO, V>(yr + e1 * Vec<DTO>::BYTES, o + V);
+    } else if (lane == 0) {
+        raise_cache_error(a.err, cr, t);
+    }
 }
 
 // General path (any D, dims <= D, strides, alignment): one block per token, one wave per head row,
@@ -249,8 +261,17 @@ __global__ __launch_bounds__(256) void rope_scalar(RopeArgs a)
     for (int64_t gh = threadIdx.x >> 6; gh < a.total_heads; gh += blockDim.x >> 6) {
         const RopeTensorDev& tt = a.t[tensor_of(a, gh)];  // gh is wave-uniform: scalar loads
         const int64_t h = gh - tt.head0;
+        int64_t orow = t;
+        if (tt.to_cache) {
+            const CacheRow cr = cache_row(a.rows, t);
+            if (cr.row < 0) {  // skipped and reported, once per token and tensor
+                if (lane == 0 && h == 0) raise_cache_error(a.err, cr, t);
+                continue;
+            }
+            orow = cr.row;
+        }
         const void* xr = static_cast<const char*>(tt.x) + (t * tt.xst + h * tt.xsh) * Vec<DTI>::BYTES;
-        void* yr = static_cast<char*>(tt.y) + (t * tt.yst + h * tt.ysh) * Vec<DTO>::BYTES;
+        void* yr = static_cast<char*>(tt.y) + (orow * tt.yst + h * tt.ysh) * Vec<DTO>::BYTES;
         float scale = 1.0f;
         if (a.norm) {
             float q = 0.f;
@@ -341,7 +362,8 @@ extern "C" SLHIP_API int slhip_rope(int dtype_in, int dtype_out, const slhip_rop
     if (T == 0) return SLHIP_OK;
     if (!pos) return fail(SLHIP_ERR_INVALID, "rope: positions are required");
     if (T > 0x7FFFFFFF) return fail(SLHIP_ERR_UNSUPPORTED, "rope: more than 2^31-1 tokens");
-    if (!(dtype_in == SLHIP_F32 || dtype_in == SLHIP_BF16) || !(dtype_out == SLHIP_F32 || dtype_out == SLHIP_BF16))
+    if (!(dtype_in == SLHIP_F32 || dtype_in == SLHIP_BF16) ||
+        !(dtype_out == SLHIP_F32 || dtype_out == SLHIP_F16 || dtype_out == SLHIP_BF16))
         return fail(SLHIP_ERR_UNSUPPORTED, "rope: dtype pair (%d -> %d) not supported", dtype_in, dtype_out);
     if (!(cfg->base > 0.0f)) return fail(SLHIP_ERR_INVALID, "rope: base must be positive");
 
@@ -368,13 +390,26 @@ extern "C" SLHIP_API int slhip_rope(int dtype_in, int dtype_out, const slhip_rop
     const int64_t oalign = vin * bout < 16 ? vin * bout : 16;
     bool vec_ok = dims == D;
     int64_t heads = 0;
+    const slhip_cache_rows* rows = nullptr;
     for (int i = 0; i < n_tensors; i++) {
         const slhip_rope_tensor& s = tensors[i];
         if (!s.x || !s.y || s.heads < 0) return fail(SLHIP_ERR_INVALID, "rope: tensor %d is incomplete", i);
         if (s.heads > 1 && (s.x_stride_h < D || s.y_stride_h < D))
             return fail(SLHIP_ERR_INVALID, "rope: tensor %d head stride is smaller than D", i);
         if (cfg->norm == 0 && s.norm_w) return fail(SLHIP_ERR_INVALID, "rope: norm weight given without cfg->norm");
-        a.t[i] = RopeTensorDev{s.x, s.y, s.norm_w, s.heads, heads, s.x_stride_t, s.x_stride_h, s.y_stride_t, s.y_stride_h};
+        if (s.rows) {
+            if (rows && memcmp(rows, s.rows, sizeof *rows) != 0)
+                return fail(SLHIP_ERR_INVALID, "rope: the cache tensors of one launch must share their rows");
+            if (!rows) {
+                const int e = make_cache_rows(s.rows, T, &a.rows);
+                if (e) return e;
+                const int ee = error_word(&a.err);
+                if (ee) return ee;
+            }
+            rows = s.rows;
+        }
+        a.t[i] = RopeTensorDev{s.x, s.y, s.norm_w, s.heads, heads, s.x_stride_t, s.x_stride_h, s.y_stride_t, s.y_stride_h,
+                               s.rows ? 1 : 0};
         heads += s.heads;
         vec_ok = vec_ok && aligned16(s.x) && s.x_stride_t % vin == 0 && s.x_stride_h % vin == 0 &&
                  reinterpret_cast<uintptr_t>(s.y) % oalign == 0 && (s.y_stride_t * bout) % oalign == 0 &&
@@ -383,8 +418,12 @@ extern "C" SLHIP_API int slhip_rope(int dtype_in, int dtype_out, const slhip_rop
     a.total_heads = heads;
     if (heads == 0) return SLHIP_OK;
     hipStream_t st = to_stream(stream);
-    if (dtype_in == SLHIP_BF16 && dtype_out == SLHIP_BF16) return dispatch<SLHIP_BF16, SLHIP_BF16>(a, vec_ok, st);
-    if (dtype_in == SLHIP_F32 && dtype_out == SLHIP_F32) return dispatch<SLHIP_F32, SLHIP_F32>(a, vec_ok, st);
-    if (dtype_in == SLHIP_BF16 && dtype_out == SLHIP_F32) return dispatch<SLHIP_BF16, SLHIP_F32>(a, vec_ok, st);
-    return dispatch<SLHIP_F32, SLHIP_BF16>(a, vec_ok, st);
+    if (dtype_in == SLHIP_BF16) {
+        if (dtype_out == SLHIP_BF16) return dispatch<SLHIP_BF16, SLHIP_BF16>(a, vec_ok, st);
+        if (dtype_out == SLHIP_F16) return dispatch<SLHIP_BF16, SLHIP_F16>(a, vec_ok, st);
+        return dispatch<SLHIP_BF16, SLHIP_F32>(a, vec_ok, st);
+    }
+    if (dtype_out == SLHIP_BF16) return dispatch<SLHIP_F32, SLHIP_BF16>(a, vec_ok, st);
+    if (dtype_out == SLHIP_F16) return dispatch<SLHIP_F32, SLHIP_F16>(a, vec_ok, st);
+    return dispatch<SLHIP_F32, SLHIP_F32>(a, vec_ok, st);
 }

@@ -43,13 +43,13 @@ static constexpr int kMaxDevices = 64;
 static std::mutex g_err_mu;
 static uint32_t* g_err_word[kMaxDevices] = {};
 
-// The gather index-error word: {raised, id low, id high, V}. A file-scope device variable (zero at load),
-// so that no call -- including the first one under graph capture -- allocates; each device holds its own
-// copy, whose address is looked up once per device. In host code only that address is used: the
-// variable's name there is a host-side stand-in.
-__device__ __align__(16) uint32_t g_index_error[4];
+// The device error record (see error_word): a file-scope device variable (zero at load), so that no
+// call -- including a first one under graph capture -- allocates; each device holds its own copy, whose
+// address is looked up once per device. In host code only that address is used: the variable's name
+// there is a host-side stand-in.
+__device__ __align__(32) uint32_t g_device_error[8];
 
-int index_error_word(uint32_t** word)
+int error_word(uint32_t** word)
 {
     int dev = 0;
     SLHIP_CHECK_HIP(hipGetDevice(&dev));
@@ -57,15 +57,52 @@ int index_error_word(uint32_t** word)
     std::lock_guard<std::mutex> lock(g_err_mu);
     if (!g_err_word[dev]) {
         void* p = nullptr;
-        SLHIP_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(g_index_error)));
+        SLHIP_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(g_device_error)));
         g_err_word[dev] = static_cast<uint32_t*>(p);
     }
     *word = g_err_word[dev];
     return SLHIP_OK;
 }
 
-// Reads and clears the current device's index-error word after the stream drained.
-static int take_index_error()
+int make_cache_rows(const slhip_cache_rows* in, int64_t T, CacheRowsDev* out)
+{
+    if (!in) return fail(SLHIP_ERR_INVALID, "cache rows are null");
+    CacheRowsDev r{};
+    r.mode = in->mode;
+    r.ctx = in->ctx;
+    if (in->ctx < 0) return fail(SLHIP_ERR_INVALID, "cache rows: negative context");
+    switch (in->mode) {
+    case SLHIP_ROWS_PAST:
+        // CacheWriteOp.Run (src/Sharplight.Cpu/CacheWriteOp.cs:118-121)
+        if (in->n_past < 0 || in->n_past + T > in->ctx)
+            return fail(SLHIP_ERR_CACHE, "KV cache overflow: n_past %lld + T %lld > context %lld.",
+                        static_cast<long long>(in->n_past), static_cast<long long>(T), static_cast<long long>(in->ctx));
+        r.n_past = in->n_past;
+        break;
+    case SLHIP_ROWS_SEQ:
+        if (!in->seq || in->slots < 1) return fail(SLHIP_ERR_INVALID, "cache rows: SEQ needs seq and slots >= 1");
+        r.seq = in->seq;
+        r.slots = in->slots;
+        r.slot_ctx = in->ctx / in->slots;
+        break;
+    case SLHIP_ROWS_PAGED:
+        if (!in->seq || !in->pages || in->block_size < 1 || in->page_slots < 0 || in->blocks_per_slot < 0)
+            return fail(SLHIP_ERR_INVALID, "cache rows: PAGED needs seq, pages and block_size >= 1");
+        r.seq = in->seq;
+        r.pages = in->pages;
+        r.page_slots = in->page_slots;
+        r.bps = in->blocks_per_slot;
+        r.bs = in->block_size;
+        break;
+    default: return fail(SLHIP_ERR_INVALID, "cache rows: bad mode %d", in->mode);
+    }
+    *out = r;
+    return SLHIP_OK;
+}
+
+// Reads and clears the current device's error record after the stream drained; reports it as the
+// reference reports the same condition (GatherOp.cs:60-63, CacheWriteOp.cs:103-117, KvPages.cs:38-49).
+static int take_device_error()
 {
     int dev = 0;
     SLHIP_CHECK_HIP(hipGetDevice(&dev));
@@ -75,12 +112,28 @@ static int take_index_error()
         if (dev >= 0 && dev < kMaxDevices) w = g_err_word[dev];
     }
     if (!w) return SLHIP_OK;
-    uint32_t host[4] = {0, 0, 0, 0};
-    SLHIP_CHECK_HIP(hipMemcpy(host, w, 16, hipMemcpyDeviceToHost));
-    if (!host[0]) return SLHIP_OK;
-    SLHIP_CHECK_HIP(hipMemset(w, 0, 16));
-    int64_t id = static_cast<int64_t>(static_cast<uint64_t>(host[1]) | (static_cast<uint64_t>(host[2]) << 32));
-    return fail(SLHIP_ERR_INDEX, "Gather index %lld out of range [0,%u).", static_cast<long long>(id), host[3]);
+    uint32_t h[8] = {};
+    SLHIP_CHECK_HIP(hipMemcpy(h, w, sizeof h, hipMemcpyDeviceToHost));
+    if (!h[0]) return SLHIP_OK;
+    SLHIP_CHECK_HIP(hipMemset(w, 0, sizeof h));
+    const long long v1 = static_cast<long long>(static_cast<uint64_t>(h[4]) | (static_cast<uint64_t>(h[5]) << 32));
+    const int slot = static_cast<int>(h[2]), pos = static_cast<int>(h[3]);
+    switch (h[0]) {
+    case kErrGatherIndex: {
+        const long long id = static_cast<long long>(static_cast<uint64_t>(h[1]) | (static_cast<uint64_t>(h[2]) << 32));
+        return fail(SLHIP_ERR_INDEX, "Gather index %lld out of range [0,%u).", id, h[3]);
+    }
+    case kErrCacheSeq:
+        return fail(SLHIP_ERR_CACHE, "KV cache overflow: sequence row %u slot %d position %d (slot context %lld).",
+                    h[1], slot, pos, v1);
+    case kErrCachePageTable:
+        return fail(SLHIP_ERR_CACHE, "Sequence slot %d / position %d outside the block table [%lld, %u].", slot, pos,
+                    v1, h[6]);
+    case kErrCacheBlock:
+        return fail(SLHIP_ERR_CACHE, "Block %lld of slot %d (position %d) is outside the KV cache of %u rows.", v1,
+                    slot, pos, h[6]);
+    default: return fail(SLHIP_ERR_HIP, "device error record holds unknown code %u", h[0]);
+    }
 }
 
 }  // namespace slhip
@@ -140,7 +193,7 @@ SLHIP_API int slhip_set_device(int device)
     // The device's index-error word is allocated here, at open time, so that no later op call (possibly
     // under graph capture) allocates.
     uint32_t* w = nullptr;
-    return index_error_word(&w);
+    return error_word(&w);
 }
 
 SLHIP_API int slhip_get_device(int* device)
@@ -241,7 +294,7 @@ SLHIP_API int slhip_stream_destroy(slhip_stream stream)
 SLHIP_API int slhip_stream_sync(slhip_stream stream)
 {
     SLHIP_CHECK_HIP(hipStreamSynchronize(to_stream(stream)));
-    return take_index_error();
+    return take_device_error();
 }
 
 SLHIP_API int slhip_event_create(slhip_event* event)

@@ -16,7 +16,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libsharplight_hip.so")
 
-OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP, ERR_INDEX, ERR_NO_DEVICE = 0, -1, -2, -3, -4, -5
+OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP, ERR_INDEX, ERR_NO_DEVICE, ERR_CACHE = 0, -1, -2, -3, -4, -5, -6
 F32, F16, BF16 = 0, 1, 2
 DTYPES = {"f32": F32, "f16": F16, "bf16": BF16}
 NP_DTYPES = {F32: np.float32, F16: np.float16, BF16: np.uint16}  # bf16 travels as raw uint16 bits
@@ -45,6 +45,10 @@ class SlhipIndexError(IndexError):
     pass
 
 
+class SlhipCacheError(SlhipError):
+    """A KV-cache row outside the cache or block table (the reference throws InvalidOperationException)."""
+
+
 class DeviceProps(ctypes.Structure):
     _fields_ = [("name", ctypes.c_char * 256), ("arch", ctypes.c_char * 64), ("total_memory", ctypes.c_int64),
                 ("compute_units", ctypes.c_int32), ("wavefront_size", ctypes.c_int32),
@@ -53,10 +57,28 @@ class DeviceProps(ctypes.Structure):
                 ("max_threads_per_block", ctypes.c_int32), ("lds_bytes_per_block", ctypes.c_int32)]
 
 
+class CacheRows(ctypes.Structure):
+    """slhip_cache_rows: where token t of a cache write goes (ROWS_PAST / ROWS_SEQ / ROWS_PAGED)."""
+    _fields_ = [("mode", ctypes.c_int32), ("reserved", ctypes.c_int32), ("ctx", ctypes.c_int64),
+                ("n_past", ctypes.c_int64), ("seq", ctypes.c_void_p), ("slots", ctypes.c_int64),
+                ("pages", ctypes.c_void_p), ("page_slots", ctypes.c_int64), ("blocks_per_slot", ctypes.c_int64),
+                ("block_size", ctypes.c_int64)]
+
+
+ROWS = {"past": 0, "seq": 1, "paged": 2}
+
+
+def cache_rows(mode, ctx, *, n_past=0, seq=None, slots=1, pages=None, page_slots=0, blocks_per_slot=0,
+               block_size=16) -> CacheRows:
+    return CacheRows(ROWS.get(mode, mode), 0, ctx, n_past, ptr(seq), slots, ptr(pages), page_slots, blocks_per_slot,
+                     block_size)
+
+
 class RopeTensor(ctypes.Structure):
     _fields_ = [("x", ctypes.c_void_p), ("y", ctypes.c_void_p), ("norm_w", ctypes.c_void_p),
                 ("heads", ctypes.c_int64), ("x_stride_t", ctypes.c_int64), ("x_stride_h", ctypes.c_int64),
-                ("y_stride_t", ctypes.c_int64), ("y_stride_h", ctypes.c_int64)]
+                ("y_stride_t", ctypes.c_int64), ("y_stride_h", ctypes.c_int64),
+                ("rows", ctypes.POINTER(CacheRows))]
 
 
 class RopeCfg(ctypes.Structure):
@@ -104,6 +126,7 @@ SIGNATURES = {
     "slhip_rope": (_I, [_I, _I, ctypes.POINTER(RopeTensor), _I, _P, _P, _I64, _I64, ctypes.POINTER(RopeCfg), _P]),
     "slhip_gather": (_I, [_I, _P, _I64, _I64, _P, _I64, _I, _P, _I64, _P]),
     "slhip_convert": (_I, [_I, _I, _P, _P, _I64, _P]),
+    "slhip_cache_write": (_I, [_I, _I, _P, _I64, _I64, _I64, _P, ctypes.POINTER(CacheRows), _P]),
     "slhip_provider_check": (_I, [ctypes.c_char_p, _SZ]),
     "slhip_node_supports": (_I, [ctypes.c_char_p, _I, ctypes.POINTER(_I), ctypes.c_char_p, _SZ]),
     "slhip_segment_compile": (_I, [ctypes.c_char_p, _I64, ctypes.POINTER(_P)]),
@@ -148,6 +171,8 @@ def check(status: int) -> None:
         raise SlhipNotSupported(msg)
     if status == ERR_INDEX:
         raise SlhipIndexError(msg)
+    if status == ERR_CACHE:
+        raise SlhipCacheError(msg)
     raise SlhipError(f"status {status}: {msg}")
 
 
@@ -324,16 +349,24 @@ def gated_act(act, dtype_in, dtype_out, gate, up, out, rows, cols, *, gate_strid
 
 def rope(dtype_in, dtype_out, tensors, pos, T, D, *, dims=0, neox=True, base=10000.0, freq_scale=1.0,
          attn_factor=1.0, norm=False, eps=1e-6, ff=None, stream=None):
-    """tensors: list of dicts with x, y, heads and optional norm_w / strides (elements)."""
+    """tensors: list of dicts with x, y, heads and optional norm_w / strides (elements) / rows (a CacheRows:
+    y is then a KV cache [ctx, heads, D] written at those rows)."""
     arr = (RopeTensor * len(tensors))()
     for i, t in enumerate(tensors):
         H = t["heads"]
+        rows = t.get("rows")
         arr[i] = RopeTensor(ptr(t["x"]), ptr(t["y"]), ptr(t.get("norm_w")), H,
                             t.get("x_stride_t", H * D), t.get("x_stride_h", D),
-                            t.get("y_stride_t", H * D), t.get("y_stride_h", D))
+                            t.get("y_stride_t", H * D), t.get("y_stride_h", D),
+                            ctypes.pointer(rows) if rows is not None else None)
     cfg = RopeCfg(dims, 1 if neox else 0, base, freq_scale, attn_factor, 1 if norm else 0, eps, 0)
     call("slhip_rope", DTYPES.get(dtype_in, dtype_in), DTYPES.get(dtype_out, dtype_out), arr, len(tensors),
          ptr(pos), ptr(ff), T, D, ctypes.byref(cfg), stream)
+
+
+def cache_write(dtype_in, dtype_cache, x, T, inner, cache, rows: CacheRows, *, x_stride=None, stream=None):
+    call("slhip_cache_write", DTYPES.get(dtype_in, dtype_in), DTYPES.get(dtype_cache, dtype_cache), ptr(x),
+         inner if x_stride is None else x_stride, T, inner, ptr(cache), ctypes.byref(rows), stream)
 
 
 def gather(fmt, table, V, D, ids, N, dtype_out, y, *, y_stride=None, stream=None):

@@ -5,6 +5,7 @@
 * bf16 outputs: at most ``ulp`` (default 2) units in the last place from bf16_RNE(oracle f32 result),
   counted on the ordered integer line of bf16 codes (so -0 and +0 are 0 apart), with the f32 rule's
   absolute floor for results far below their row's scale (see assert_bf16_close).
+* f16 outputs (KV caches): the same rule on the f16 code line (assert_f16_close).
 * integer / byte / dequantized outputs: bit-exact.
 """
 from __future__ import annotations
@@ -29,6 +30,16 @@ def _bf16_f32(bits):
     return (np.asarray(bits, np.uint16).astype(np.uint32) << np.uint32(16)).view(np.float32)
 
 
+def _f16_f32(bits):
+    return np.asarray(bits, np.uint16).view(np.float16).astype(np.float32)
+
+
+def assert_f16_close(got, ref, ulp: int = BF16_ULP, what: str = "", atol_row: float | None = None):
+    """The bf16 rule (assert_bf16_close) on f16 codes: at most ``ulp`` f16 ulp from f16_RNE(oracle f32
+    result), with the same absolute floor."""
+    return _assert_half_close(got, ref, ulp, what, atol_row, _f16_f32, "f16")
+
+
 def assert_bf16_close(got, ref, ulp: int = BF16_ULP, what: str = "", atol_row: float | None = None):
     """At most ``ulp`` bf16 ulp from ``ref``. An element further away still passes when it is within the f32
     rule's absolute floor, ``atol_row`` (default 1e-5) x the RMS of its reference row: for results far below
@@ -36,6 +47,10 @@ def assert_bf16_close(got, ref, ulp: int = BF16_ULP, what: str = "", atol_row: f
     the result is finer than the f32 rounding of the terms that produced it, and the reference's own
     comparison (Diff.cs:206, ``atol + rtol*|ref|``) is absolute there too. ``ulp=0`` disables the floor
     (bit-exact comparison)."""
+    return _assert_half_close(got, ref, ulp, what, atol_row, _bf16_f32, "bf16")
+
+
+def _assert_half_close(got, ref, ulp, what, atol_row, to_f32, name):
     got = np.asarray(got, np.uint16)
     ref = np.asarray(ref, np.uint16)
     assert got.shape == ref.shape, (got.shape, ref.shape)
@@ -44,15 +59,15 @@ def assert_bf16_close(got, ref, ulp: int = BF16_ULP, what: str = "", atol_row: f
     d = bf16_ulp_diff(got, ref)
     over = d > ulp
     if over.any() and atol_row > 0:
-        rf = _bf16_f32(ref).astype(np.float64)
-        gf = _bf16_f32(got).astype(np.float64)
+        rf = to_f32(ref).astype(np.float64)
+        gf = to_f32(got).astype(np.float64)
         r2 = rf.reshape(-1, ref.shape[-1]) if ref.ndim else rf.reshape(1, 1)
         rms = np.sqrt(np.mean(r2 * r2, axis=1, keepdims=True))
         floor = np.broadcast_to(atol_row * rms, r2.shape).reshape(ref.shape)
         over &= ~(np.abs(gf - rf) <= floor)
     if over.any():
         i = np.unravel_index(np.argmax(np.where(over, d, -1)), d.shape)
-        raise AssertionError(f"{what}: {int(over.sum())} of {d.size} bf16 values beyond {ulp} ulp (and beyond the "
+        raise AssertionError(f"{what}: {int(over.sum())} of {d.size} {name} values beyond {ulp} ulp (and beyond the "
                              f"absolute floor); worst at {i}: got {got[i]:#06x} ref {ref[i]:#06x} ({int(d[i])} ulp)")
     return int(d.max()) if d.size else 0
 

@@ -60,4 +60,15 @@ def test_f32_to_f16_matches_numpy(device):
     x = x[np.isfinite(x)]
     x = x[: x.size - x.size % 8]
     y = _convert("f32", "f16", x)
-    assert np.array_equal(y.view(np.uint16), x.astype(np.float16).view(np.uint16))
+    with np.errstate(over="ignore"):  # values beyond f16's range round to infinity
+        ref = x.astype(np.float16).view(np.uint16)
+    assert np.array_equal(y.view(np.uint16), ref)
+
+
+def test_f32_to_f16_nans(device):
+    """NaN payloads through f32 -> f16 against the oracle's rule (the .NET runtime's (Half) conversion:
+    sign | 0x7E00 | mantissa >> 13)."""
+    nans = np.array([0x7F800001, 0x7FC00000, 0xFF800001, 0x7FBFFFFF, 0xFFFFFFFF, 0x7FA02000, 0xFFC12345,
+                     0x7F812000], np.uint32).view(np.float32)
+    y = _convert("f32", "f16", nans)
+    assert_bits_equal(y.view(np.uint16), oracle.to_f16(nans), what="f32->f16 NaN")

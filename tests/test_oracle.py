@@ -331,3 +331,89 @@ def test_qk_norm_rope_composition():
     got = oracle.qk_norm_rope(x, pos, w, 1e-6, base=1e6)
     ref = _rope_f64(_rms_f64(x, w, 1e-6).astype(np.float32), pos, 128, True, 1e6)
     np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-5)
+
+
+# ---- KV cache writes (CacheWriteOp.cs, KvPages.cs) ------------------------------------------------
+
+def test_f16_rounding_matches_numpy():
+    """FloatToHalf (.NET (Half)f): IEEE round to nearest even, gradual underflow, overflow to inf --
+    the same conversion numpy implements. Every finite f16 neighbourhood: the value itself, the midpoints
+    to its neighbours (ties) and the f32 values one ulp either side of each midpoint; plus 2M random f32
+    bit patterns over the whole exponent range."""
+    h = np.arange(0, 0x7C00, dtype=np.uint32).astype(np.uint16)  # every finite non-negative f16
+    v = h.view(np.float16).astype(np.float64)
+    with np.errstate(over="ignore"):  # the largest finite f16's neighbour is inf
+        nxt = np.nextafter(h.view(np.float16), np.float16(np.inf)).astype(np.float64)
+    mid = ((v + nxt) / 2).astype(np.float32)  # exact in f32
+    cand = np.concatenate([v.astype(np.float32), mid, np.nextafter(mid, np.float32(0)), np.nextafter(mid, np.float32(np.inf))])
+    rng = np.random.default_rng(3)
+    bits = rng.integers(0, 1 << 32, 2_000_000, dtype=np.uint64).astype(np.uint32)
+    bits = bits[(bits & 0x7F800000) != 0x7F800000]  # finite
+    cand = np.concatenate([cand, -cand, bits.view(np.float32), np.float32([0.0, -0.0, np.inf, -np.inf, 65504, 65520, -65520, 1e30])])
+    with np.errstate(over="ignore"):
+        ref = cand.astype(np.float16).view(np.uint16)
+    assert np.array_equal(oracle.to_f16(cand), ref)
+
+
+def test_f16_nan_keeps_sign_and_payload_top():
+    """The runtime's rule for NaN (parity unpinned: the .NET runtime is not part of the reference)."""
+    nans = np.array([0x7F800001, 0x7FC00000, 0xFF800001, 0x7FBFFFFF, 0xFFFFFFFF, 0x7FA02000], np.uint32)
+    got = oracle.to_f16(nans.view(np.float32))
+    want = ((nans >> 16) & 0x8000) | 0x7E00 | ((nans & 0x7FFFFF) >> 13)
+    assert np.array_equal(got, want.astype(np.uint16))
+    assert np.isnan(got.view(np.float16)).all()
+
+
+def test_cache_rows_past():
+    assert list(oracle.cache_rows("past", 4, 10, n_past=6)) == [6, 7, 8, 9]
+    assert list(oracle.cache_rows("past", 0, 10, n_past=10)) == []
+    with pytest.raises(oracle.CacheOverflow, match=r"n_past 7 \+ T 4 > context 10"):
+        oracle.cache_rows("past", 4, 10, n_past=7)
+
+
+def test_cache_rows_multi_sequence():
+    """Row = slot * (ctx / slots) + position (CacheWriteOp.Body, multi-sequence form)."""
+    rng = np.random.default_rng(4)
+    T, ctx, slots = 50, 96, 3
+    seq = np.zeros((T, 4), np.int32)
+    seq[:, 0] = rng.integers(0, slots, T)
+    seq[:, 1] = rng.integers(0, ctx // slots, T)
+    rows = oracle.cache_rows("seq", T, ctx, seq=seq, slots=slots)
+    assert np.array_equal(rows, seq[:, 0] * (ctx // slots) + seq[:, 1])
+    for bad in ((0, 32), (3, 0), (-1, 0), (1, -1)):
+        s2 = seq.copy()
+        s2[7, :2] = bad
+        with pytest.raises(oracle.CacheOverflow, match="KV cache overflow: sequence row 7"):
+            oracle.cache_rows("seq", T, ctx, seq=s2, slots=slots)
+
+
+def test_cache_rows_paged():
+    """Row = table[slot, p / bs] * bs + p % bs (KvPages.Row), brute force over every (slot, position)."""
+    rng = np.random.default_rng(5)
+    slots, bps, bs, ctx = 3, 4, 8, 12 * 8
+    table = rng.permutation(12)[: slots * bps].reshape(slots, bps).astype(np.int32)
+    seq = np.array([(s, p, 0, 0) for s in range(slots) for p in range(bps * bs)], np.int32)
+    rows = oracle.cache_rows("paged", len(seq), ctx, seq=seq, pages=table, block_size=bs)
+    want = [table[s, p // bs] * bs + p % bs for s, p, _, _ in seq]
+    assert np.array_equal(rows, want)
+    assert len(set(rows.tolist())) == len(rows)  # a permutation table maps positions to distinct rows
+    with pytest.raises(oracle.CacheOverflow, match="outside the block table"):
+        oracle.cache_rows("paged", 1, ctx, seq=np.int32([[0, bps * bs, 0, 0]]), pages=table, block_size=bs)
+    t2 = table.copy()
+    t2[1, 2] = 12  # past the cache's 12 blocks
+    with pytest.raises(oracle.CacheOverflow, match="Block 12 of slot 1"):
+        oracle.cache_rows("paged", 1, ctx, seq=np.int32([[1, 2 * bs + 3, 0, 0]]), pages=t2, block_size=bs)
+
+
+@pytest.mark.parametrize("ct", ["f32", "f16", "bf16"])
+def test_cache_write_converts_into_rows(ct):
+    rng = np.random.default_rng(6)
+    T, inner, ctx = 5, 24, 16
+    x = rng.standard_normal((T, inner)).astype(np.float32)
+    rows = np.int64([3, 9, 0, 15, 4])
+    cache = np.full((ctx, inner), 7, np.float32 if ct == "f32" else np.uint16)
+    oracle.cache_write(cache, x, rows, ct)
+    conv = {"f32": lambda a: a, "f16": oracle.to_f16, "bf16": oracle.to_bf16}[ct]
+    assert np.array_equal(cache[rows], conv(x))
+    untouched = np.setdiff1d(np.arange(ctx), rows)
+    assert (cache[untouched] == 7).all()
