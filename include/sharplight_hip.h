@@ -273,14 +273,18 @@ SLHIP_API int slhip_convert(int dtype_in, int dtype_out, const void* x, void* y,
  * A graph segment arrives as text, one declaration per line ('#' starts a comment line):
  *   value <id> <type> <dim> ...       type: f32 f16 bf16 i32 q8_0 q4_0 q4_1 q5_0 q5_1; a dim "T" is the
  *                                     symbolic token count, bound at execute time (at most max_tokens)
- *   input <id> | weight <id> | output <id>
+ *   input <id> | weight <id> | output <id> | state <id>    (a state -- a KV cache -- has fixed dims, persists
+ *                                     across runs, starts at zero and is zeroed again by reset_state)
  *   node <Op> <in,ids> -> <out,ids> [key=value ...]
  * with the StandardOps names and attributes of the reference (src/Sharplight.Core/Graph/StandardOps.cs):
  *   Add, Mul (same-shape), Silu, GeluTanh, Gelu, RmsNorm (x[, w]; eps), L2Norm (x; eps),
  *   LayerNorm (x[, w[, b]]; eps), Rope (x [T,H,D], pos i32 [T][, ff]; dims, base, style=neox|normal|gptj,
- *   freq_scale, attn_factor), Gather (table [V, D...], ids i32 [N]), Cast.
- * Compile applies the reference lowerer's fusions (Add+RmsNorm, act+Mul, RmsNorm inside Rope, q/k ropes
- * in one launch); slhip_segment_launches lists the fused launches, one per line. Segments run on a stream
+ *   freq_scale, attn_factor), Gather (table [V, D...], ids i32 [N]), Cast,
+ *   CacheWrite (state [ctx, ...], x [T, ...][, rows i32 [T,4][, pages i32 [slots, blocks]]]; offset=<scalar
+ *   name, default n_past>, slots, block_size): rows n_past + t, or the multi-sequence / paged rows.
+ * Compile applies the reference lowerer's fusions (Add+RmsNorm, act+Mul, RmsNorm inside Rope, a Rope whose
+ * only consumer is a CacheWrite stored into the cache, q/k ropes in one launch); slhip_segment_launches
+ * lists the fused launches, one per line. Segments run on a stream
  * of their own on the device current at compile time. */
 typedef void* slhip_segment;
 
@@ -301,10 +305,15 @@ SLHIP_API int slhip_segment_set_input(slhip_segment segment, int value, const vo
  * (src/Sharplight.Cpu/CpuCompiledSegment.cs:115-121). */
 SLHIP_API int slhip_segment_execute(slhip_segment segment, int64_t tokens);
 /* ICompiledSegment.GetOutput: waits for the segment, then copies the output's dense bytes for the last
- * run's token count (the size must match). Reports a gather index error as SLHIP_ERR_INDEX. */
+ * run's token count (the size must match); a state value reads back the whole state. Reports a gather
+ * index error as SLHIP_ERR_INDEX and a cache row outside the cache as SLHIP_ERR_CACHE. */
 SLHIP_API int slhip_segment_get_output(slhip_segment segment, int value, void* data, size_t bytes);
-/* ICompiledSegment.ResetState (no state is held by these ops) and DeviceMemoryBytes. */
+/* ICompiledSegment.ResetState: every state back to zero (CpuCompiledSegment.ResetState,
+ * src/Sharplight.Cpu/CpuCompiledSegment.cs:259-265); and DeviceMemoryBytes. */
 SLHIP_API int slhip_segment_reset_state(slhip_segment segment);
+/* A runtime scalar of the next runs (RunParameters.Scalars, src/Sharplight.Core/Runtime/RunParameters.cs:12),
+ * e.g. n_past for CacheWrite. A CacheWrite whose scalar was never set fails like CacheWriteOp.Run. */
+SLHIP_API int slhip_segment_set_scalar(slhip_segment segment, const char* name, int64_t value);
 SLHIP_API int slhip_segment_device_bytes(slhip_segment segment, int64_t* bytes);
 /* The fused launches of the compiled segment, one label per line (e.g. "fused[Add]+RmsNorm"). */
 SLHIP_API int slhip_segment_launches(slhip_segment segment, char* buf, size_t size);

@@ -27,6 +27,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <cmath>
 #include <map>
 #include <memory>
@@ -110,7 +111,7 @@ struct Value {
     int id = -1;
     DType type = DType::F32;
     std::vector<int64_t> dims;  // dims[k] == kSymT: the token count of the run
-    bool input = false, weight = false, output = false;
+    bool input = false, weight = false, output = false, state = false;
 
     int64_t elems(int64_t T) const
     {
@@ -175,7 +176,8 @@ std::vector<int> parse_ids(const std::string& s)
     std::stringstream ss(s);
     std::string tok;
     while (std::getline(ss, tok, ',')) {
-        if (tok.empty()) invalid("empty value id in '" + s + "'");
+        if (tok.empty() || tok.find_first_not_of("0123456789") != std::string::npos)
+            invalid("bad value id list '" + s + "' (ids, or '-' for none)");
         ids.push_back(atoi(tok.c_str()));
     }
     return ids;
@@ -224,11 +226,12 @@ Graph parse(const char* text)
                 while (ls >> d) v.dims.push_back(d == "T" ? kSymT : strtoll(d.c_str(), nullptr, 10));
                 if (g.values.count(v.id)) invalid("value " + std::to_string(v.id) + " declared twice");
                 g.values[v.id] = v;
-            } else if (kw == "input" || kw == "weight" || kw == "output") {
+            } else if (kw == "input" || kw == "weight" || kw == "output" || kw == "state") {
                 int id;
                 if (!(ls >> id)) invalid(kw + ": expected a value id");
                 Value& v = g.value(id);
-                (kw == "input" ? v.input : kw == "weight" ? v.weight : v.output) = true;
+                (kw == "input" ? v.input : kw == "weight" ? v.weight : kw == "output" ? v.output : v.state) = true;
+                if (v.state && v.symbolic()) invalid("state " + std::to_string(id) + " must have fixed dims");
             } else if (kw == "node") {
                 Node n = parse_node(ls);
                 for (int id : n.in) g.value(id);
@@ -301,6 +304,22 @@ Support supports(const Graph& g, const Node& n)
         if (o != DType::F32 && o != DType::BF16) return no("Gather: f32 or bf16 output");
         return {true, ""};
     }
+    if (op == "CacheWrite") {
+        // StandardOps.CacheWrite (src/Sharplight.Core/Graph/StandardOps.cs:310-319): state, x [, sequence rows
+        // [T, 4] (multi-sequence form) [, block table (paged form)]]; no outputs.
+        if (n.in.size() < 2 || n.in.size() > 4 || !n.out.empty()) return no("CacheWrite takes state, x[, rows[, pages]]");
+        const Value& st = g.value(n.in[0]);
+        const Value& x = g.value(n.in[1]);
+        if (!st.state) return no("CacheWrite: the first input must be a state");
+        if (!is_activation(st.type)) return no("CacheWrite: f32, f16 or bf16 caches (quantized caches are not supported)");
+        if (x.type != DType::F32 && x.type != DType::BF16) return no("CacheWrite: f32 or bf16 rows");
+        if (n.i("compression", 1) != 1) return no("CacheWrite: compressed caches are not supported");
+        if (st.dims.size() < 2 || x.dims.empty() || st.elems(0) / st.dims[0] != x.elems(1) / (x.dims[0] == kSymT ? 1 : x.dims[0]))
+            return no("CacheWrite: x rows must match the cache rows");
+        for (size_t k = 2; k < n.in.size(); k++)
+            if (g.value(n.in[k]).type != DType::I32) return no("CacheWrite: sequence rows and block table are i32");
+        return {true, ""};
+    }
     if (op == "Cast") {
         if (n.in.size() != 1 || n.out.size() != 1 || !act(n.in[0]) || !act(n.out[0])) return no("Cast: activation types");
         return {true, ""};
@@ -311,7 +330,7 @@ Support supports(const Graph& g, const Node& n)
 // ---- lowering into fused units -------------------------------------------------------------------------
 
 struct Unit {
-    enum Kind { RowNorm, Gated, Rope, Gather, Cast } kind;
+    enum Kind { RowNorm, Gated, Rope, Gather, Cast, CacheWrite } kind;
     std::string label;
     // RowNorm
     int norm = SLHIP_NORM_RMS;
@@ -322,12 +341,15 @@ struct Unit {
     // Rope: up to 4 tensors sharing positions and settings
     struct RopeTensor {
         int x, y, w;
+        int cache_node = -1;  // the CacheWrite this tensor's rows go through (y is its state)
     };
     std::vector<RopeTensor> rt;
     int pos = -1, ff = -1;
     slhip_rope_cfg cfg{};
     // Gather
     int table = -1, ids = -1;
+    // CacheWrite (standalone): x into the state y
+    int cache_node = -1;
 };
 
 class Segment {
@@ -342,6 +364,7 @@ public:
         lower();
         check(slhip_stream_create(&stream_));
         allocate();
+        reset_state();
     }
 
     ~Segment()
@@ -372,10 +395,22 @@ public:
         for (const Unit& u : units_) run(u, T);
     }
 
+    // Runtime scalars (RunParameters.Scalars, src/Sharplight.Core/Runtime/RunParameters.cs:12), e.g. n_past.
+    void set_scalar(const std::string& name, int64_t value) { scalars_[name] = value; }
+
+    // ICompiledSegment.ResetState: states (KV caches) back to zero, as CpuCompiledSegment.ResetState clears
+    // them (src/Sharplight.Cpu/CpuCompiledSegment.cs:259-265).
+    void reset_state()
+    {
+        for (auto& kv : g_.values)
+            if (kv.second.state) check(slhip_memset(mem_.at(kv.first), 0, static_cast<size_t>(kv.second.bytes(0)), stream_));
+        check(slhip_stream_sync(stream_));
+    }
+
     void get_output(int id, void* data, size_t bytes)
     {
         const Value& v = g_.value(id);
-        if (!v.output) invalid("value " + std::to_string(id) + " is not an output of the segment");
+        if (!v.output && !v.state) invalid("value " + std::to_string(id) + " is neither an output nor a state of the segment");
         const int64_t n = v.bytes(t_);
         if (static_cast<int64_t>(bytes) != n)
             invalid("output " + std::to_string(id) + " holds " + std::to_string(n) + " bytes, destination " + std::to_string(bytes));
@@ -398,6 +433,7 @@ private:
     int64_t max_t_, t_ = 0;
     std::vector<Unit> units_;
     std::map<int, void*> mem_;
+    std::map<std::string, int64_t> scalars_;
     int64_t device_bytes_ = 0;
     slhip_stream stream_ = nullptr;
 
@@ -483,7 +519,23 @@ private:
             if (n.op == "RmsNorm" || n.op == "L2Norm" || n.op == "LayerNorm") {
                 units_.push_back(rownorm_unit(n));
             } else if (n.op == "Rope") {
-                units_.push_back(rope_unit(static_cast<int>(k)));
+                Unit u = rope_unit(static_cast<int>(k));
+                // A rope whose only consumer is a cache write stores into the cache
+                // (GraphLowerer.Fusion.cs:633-648; f32/f16/bf16 caches, no compression).
+                if (single_use(n.out[0])) {
+                    const int mk = cons[n.out[0]][0];
+                    const Node& m = g_.nodes[mk];
+                    const Value& st = m.op == "CacheWrite" ? g_.value(m.in[0]) : g_.value(n.out[0]);
+                    const Value& rv = g_.value(n.out[0]);
+                    if (m.op == "CacheWrite" && !done[mk] && m.in[1] == n.out[0] && st.dims.size() == 3 &&
+                        rv.dims.size() == 3 && st.dims[1] == rv.dims[1] && st.dims[2] == rv.dims[2]) {
+                        u.rt[0].y = m.in[0];
+                        u.rt[0].cache_node = mk;
+                        u.label += "+cache";
+                        done[mk] = true;
+                    }
+                }
+                units_.push_back(u);
             } else if (n.op == "Gather") {
                 Unit u{Unit::Gather};
                 u.table = n.in[0];
@@ -498,6 +550,13 @@ private:
                 u.x = n.in[0];
                 u.y = n.out[0];
                 u.label = "Cast";
+                units_.push_back(u);
+            } else if (n.op == "CacheWrite") {
+                Unit u{Unit::CacheWrite};
+                u.x = n.in[1];
+                u.y = n.in[0];
+                u.cache_node = static_cast<int>(k);
+                u.label = "CacheWrite";
                 units_.push_back(u);
             } else {
                 unsupported("standalone " + n.op + ": the HIP provider runs " + n.op +
@@ -549,10 +608,14 @@ private:
                 Unit& p = out.back();
                 const Value& a = g_.value(p.rt[0].x);
                 const Value& b = g_.value(u.rt[0].x);
+                int pc = -1;  // the cache rows already in the launch, if any
+                for (const auto& t : p.rt)
+                    if (t.cache_node >= 0) pc = t.cache_node;
+                const int uc = u.rt[0].cache_node;
                 const bool same = p.kind == Unit::Rope && p.pos == u.pos && p.ff == u.ff && p.rt.size() < 4 &&
                                   memcmp(&p.cfg, &u.cfg, sizeof p.cfg) == 0 && a.type == b.type &&
                                   g_.value(p.rt[0].y).type == g_.value(u.rt[0].y).type && a.dims[2] == b.dims[2] &&
-                                  a.dims[0] == b.dims[0];
+                                  a.dims[0] == b.dims[0] && (pc < 0 || uc < 0 || same_rows(pc, uc));
                 if (same) {
                     p.rt.push_back(u.rt[0]);
                     p.label += "|" + u.label;
@@ -577,6 +640,51 @@ private:
 
     void* ptr(int id) const { return id < 0 ? nullptr : mem_.at(id); }
 
+    // Two cache writes that map tokens to the same rows (one launch may carry one row map).
+    bool same_rows(int a, int b) const
+    {
+        const Node& x = g_.nodes[a];
+        const Node& y = g_.nodes[b];
+        return x.in.size() == y.in.size() && std::equal(x.in.begin() + 2, x.in.end(), y.in.begin() + 2) &&
+               x.s("offset", "n_past") == y.s("offset", "n_past") && x.i("slots", 1) == y.i("slots", 1) &&
+               x.i("block_size", 16) == y.i("block_size", 16) && g_.value(x.in[0]).dims[0] == g_.value(y.in[0]).dims[0];
+    }
+
+    // The rows of cache write `node` for a run of T tokens: n_past + t from the offset scalar, or the
+    // multi-sequence rows [T, 4] (3rd input, attribute slots), or those through the block table (4th input,
+    // attribute block_size) -- the inputs the reference's MultiSequence rewrite appends
+    // (src/Sharplight.Core/Graph/MultiSequence.cs:201-233).
+    slhip_cache_rows rows_of(int node, int64_t T) const
+    {
+        const Node& n = g_.nodes[node];
+        const Value& st = g_.value(n.in[0]);
+        slhip_cache_rows r{};
+        r.ctx = st.dims[0];
+        if (n.in.size() == 2) {
+            const std::string name = n.s("offset", "n_past");
+            auto it = scalars_.find(name);
+            if (it == scalars_.end())  // CacheWriteOp.Run (src/Sharplight.Cpu/CacheWriteOp.cs:114-117)
+                throw Error(SLHIP_ERR_INVALID, "Runtime scalar '" + name + "' was not provided.");
+            r.mode = SLHIP_ROWS_PAST;
+            r.n_past = it->second;
+            return r;
+        }
+        r.seq = static_cast<const int32_t*>(ptr(n.in[2]));
+        if (n.in.size() == 3) {
+            r.mode = SLHIP_ROWS_SEQ;
+            r.slots = n.i("slots", 1);
+            return r;
+        }
+        const Value& pg = g_.value(n.in[3]);
+        r.mode = SLHIP_ROWS_PAGED;
+        r.pages = static_cast<const int32_t*>(ptr(n.in[3]));
+        r.page_slots = pg.dims.size() == 2 ? pg.dims[0] : 1;
+        r.blocks_per_slot = pg.dims.back();
+        r.block_size = n.i("block_size", 16);
+        (void)T;
+        return r;
+    }
+
     void run(const Unit& u, int64_t T)
     {
         switch (u.kind) {
@@ -598,13 +706,22 @@ private:
         }
         case Unit::Rope: {
             std::vector<slhip_rope_tensor> ts;
+            std::vector<slhip_cache_rows> rows;
+            rows.reserve(u.rt.size());  // the tensors point into it
             const Value& x0 = g_.value(u.rt[0].x);
             const int64_t Tt = x0.dims[0] == kSymT ? T : x0.dims[0];
             const int64_t D = x0.dims[2];
             for (const auto& r : u.rt) {
                 const Value& xv = g_.value(r.x);
                 const int64_t H = xv.dims[1];
-                ts.push_back(slhip_rope_tensor{ptr(r.x), ptr(r.y), static_cast<const float*>(ptr(r.w)), H, H * D, D, H * D, D});
+                slhip_rope_tensor t{ptr(r.x), ptr(r.y), static_cast<const float*>(ptr(r.w)), H, H * D, D, H * D, D, nullptr};
+                if (r.cache_node >= 0) {
+                    const Value& st = g_.value(r.y);
+                    rows.push_back(rows_of(r.cache_node, Tt));
+                    t.y_stride_t = st.dims[1] * st.dims[2];
+                    t.rows = &rows.back();
+                }
+                ts.push_back(t);
             }
             check(slhip_rope(act_code(x0.type), act_code(g_.value(u.rt[0].y).type), ts.data(), static_cast<int>(ts.size()),
                              static_cast<const int32_t*>(ptr(u.pos)), static_cast<const float*>(ptr(u.ff)), Tt, D, &u.cfg,
@@ -624,6 +741,15 @@ private:
         case Unit::Cast: {
             const Value& x = g_.value(u.x);
             check(slhip_convert(act_code(x.type), act_code(g_.value(u.y).type), ptr(u.x), ptr(u.y), x.elems(T), stream_));
+            break;
+        }
+        case Unit::CacheWrite: {
+            const Value& x = g_.value(u.x);
+            const Value& st = g_.value(u.y);
+            const int64_t Tt = x.dims[0] == kSymT ? T : x.dims[0];
+            const int64_t inner = st.elems(0) / st.dims[0];
+            const slhip_cache_rows r = rows_of(u.cache_node, Tt);
+            check(slhip_cache_write(act_code(x.type), act_code(st.type), ptr(u.x), inner, Tt, inner, ptr(u.y), &r, stream_));
             break;
         }
         }
@@ -741,9 +867,17 @@ SLHIP_API int slhip_segment_launches(slhip_segment segment, char* buf, size_t si
 
 SLHIP_API int slhip_segment_reset_state(slhip_segment segment)
 {
-    // The fused layer ops keep no state between steps (no KV cache or recurrent state lives here).
     return guarded([&] {
         if (!segment) invalid("segment is null");
+        static_cast<Segment*>(segment)->reset_state();
+    });
+}
+
+SLHIP_API int slhip_segment_set_scalar(slhip_segment segment, const char* name, int64_t value)
+{
+    return guarded([&] {
+        if (!segment || !name) invalid("segment and name are required");
+        static_cast<Segment*>(segment)->set_scalar(name, value);
     });
 }
 

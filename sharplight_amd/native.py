@@ -134,6 +134,7 @@ SIGNATURES = {
     "slhip_segment_execute": (_I, [_P, _I64]),
     "slhip_segment_get_output": (_I, [_P, _I, _P, _SZ]),
     "slhip_segment_reset_state": (_I, [_P]),
+    "slhip_segment_set_scalar": (_I, [_P, ctypes.c_char_p, _I64]),
     "slhip_segment_device_bytes": (_I, [_P, ctypes.POINTER(_I64)]),
     "slhip_segment_launches": (_I, [_P, ctypes.c_char_p, _SZ]),
     "slhip_segment_destroy": (_I, [_P]),

@@ -60,6 +60,7 @@ class GraphBuilder:
         self.inputs: list[Value] = []
         self.weights: list[Value] = []
         self.outputs: list[Value] = []
+        self.states: list[Value] = []
 
     def value(self, type: str, *dims) -> Value:
         v = Value(len(self.values), type, tuple(dims))
@@ -74,6 +75,12 @@ class GraphBuilder:
     def weight(self, type: str, *dims) -> Value:
         v = self.value(type, *dims)
         self.weights.append(v)
+        return v
+
+    def state(self, type: str, *dims) -> Value:
+        """A state (KV cache): fixed dims, persistent across runs, zero until written."""
+        v = self.value(type, *dims)
+        self.states.append(v)
         return v
 
     def output(self, v: Value) -> Value:
@@ -124,6 +131,16 @@ class GraphBuilder:
     def cast(self, x, to: str):
         return self.emit("Cast", [x], to, x.dims)
 
+    def cache_write(self, state, x, rows=None, pages=None, offset="n_past", slots=None, block_size=None):
+        """GraphBuilder.CacheWrite (src/Sharplight.Core/Graph/GraphBuilder.cs:330-336), with the inputs and
+        attributes the multi-sequence / paged rewrite adds (MultiSequence.cs:201-233)."""
+        attrs = {"offset": offset}
+        if slots is not None:
+            attrs["slots"] = slots
+        if block_size is not None:
+            attrs["block_size"] = block_size
+        self.nodes.append(Node("CacheWrite", [v for v in (state, x, rows, pages) if v is not None], [], attrs))
+
     def to_ir(self) -> str:
         lines = []
         for v in self.values:
@@ -134,10 +151,12 @@ class GraphBuilder:
             lines.append(f"weight {v.id}")
         for v in self.outputs:
             lines.append(f"output {v.id}")
+        for v in self.states:
+            lines.append(f"state {v.id}")
         for n in self.nodes:
             attrs = " ".join(f"{k}={_fmt(v)}" for k, v in n.attrs.items())
             lines.append(f"node {n.op} {','.join(str(v.id) for v in n.inputs) or '-'} -> "
-                         f"{','.join(str(v.id) for v in n.outputs)} {attrs}".rstrip())
+                         f"{','.join(str(v.id) for v in n.outputs) or '-'} {attrs}".rstrip())
         return "\n".join(lines) + "\n"
 
 
@@ -271,6 +290,10 @@ class CompiledSegment:
 
     def reset_state(self) -> None:
         native.call("slhip_segment_reset_state", self.handle)
+
+    def set_scalar(self, name: str, value: int) -> None:
+        """A runtime scalar of the next runs (RunParameters.Scalars), e.g. n_past."""
+        native.call("slhip_segment_set_scalar", self.handle, name.encode(), int(value))
 
     @property
     def device_memory_bytes(self) -> int:

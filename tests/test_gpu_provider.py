@@ -9,7 +9,7 @@ import oracle
 from sharplight_amd import native, synth
 from sharplight_amd.provider import GraphBuilder, HipExecutionProvider
 from tests.devutil import log
-from tests.parity import assert_bf16_close, assert_bits_equal, assert_f32_close
+from tests.parity import assert_bf16_close, assert_bits_equal, assert_f16_close, assert_f32_close
 
 pytestmark = pytest.mark.gpu
 
@@ -194,3 +194,86 @@ def test_symbolic_tokens_reuse_one_compilation(dev):
             seg.set_input(x, xs)
             seg.execute(T)
             assert_f32_close(seg.get_output(y), oracle.rmsnorm(xs, ws, 1e-6), what=f"T={T}")
+
+
+def _norm_rope_cache_graph(cache_type, D=128, Hq=4, Hkv=2, ctx=32, paged=False):
+    """FusionTests.NormRopeIntoCache (tests/Sharplight.Vulkan.Tests/FusionTests.cs:138-175) without the
+    attention read-out and with a single-axis rope: q and k RmsNorm then neox rope, k into the K cache,
+    v into the V cache; the caches are states read back after the steps."""
+    g = GraphBuilder()
+    q = g.input("bf16", "T", Hq, D)
+    k = g.input("bf16", "T", Hkv, D)
+    v = g.input("bf16", "T", Hkv, D)
+    pos = g.input("i32", "T")
+    wq, wk = g.weight("f32", D), g.weight("f32", D)
+    kc = g.state(cache_type, ctx, Hkv, D)
+    vc = g.state(cache_type, ctx, Hkv, D)
+    rows = pages = None
+    kw = {}
+    if paged:
+        rows = g.input("i32", "T", 4)
+        pages = g.weight("i32", 1, ctx // 8)
+        kw = dict(slots=1, block_size=8)
+    yq = g.output(g.rope(g.rms_norm(q, wq, eps=1e-6), pos, base=1e4, style="neox"))
+    g.cache_write(kc, g.rope(g.rms_norm(k, wk, eps=1e-6), pos, base=1e4, style="neox"), rows, pages, **kw)
+    g.cache_write(vc, v, rows, pages, **kw)
+    return g, dict(q=q, k=k, v=v, pos=pos, wq=wq, wk=wk, kc=kc, vc=vc, yq=yq, rows=rows, pages=pages)
+
+
+@pytest.mark.parametrize("cache_type,paged", [("bf16", False), ("f16", False), ("f16", True)])
+def test_norm_rope_into_cache_graph(dev, cache_type, paged):
+    D, Hq, Hkv, ctx = 128, 4, 2, 32
+    g, h = _norm_rope_cache_graph(cache_type, D, Hq, Hkv, ctx, paged)
+    wq, wk = synth.normal(7, 0, (D,), 1.0, 0.1), synth.normal(7, 1, (D,), 1.0, 0.1)
+    table = np.int32([[3, 0, 2, 1]])  # paged: positions 0-7 live in block 3, 8-15 in block 0, ...
+    chunks, past = [5, 1, 3, 1], 0
+    ref_k = np.zeros((ctx, Hkv, D), np.float32)
+    ref_v = np.zeros((ctx, Hkv, D), np.float32)
+    with dev.compile(g, max_tokens=8) as seg:
+        want = ["rope+norm|rope+norm+cache", "CacheWrite"] if cache_type == "bf16" else \
+               ["rope+norm", "rope+norm+cache", "CacheWrite"]
+        assert seg.launches == want
+        seg.set_input(h["wq"], wq)
+        seg.set_input(h["wk"], wk)
+        if paged:
+            seg.set_input(h["pages"], table)
+        for i, c in enumerate(chunks):
+            q = synth.normal(10 + i, 0, (c, Hq, D), dtype="bf16")
+            k = synth.normal(20 + i, 0, (c, Hkv, D), dtype="bf16")
+            v = synth.normal(30 + i, 0, (c, Hkv, D), dtype="bf16")
+            p = np.arange(past, past + c, dtype=np.int32)
+            for val, arr in ((h["q"], q), (h["k"], k), (h["v"], v), (h["pos"], p)):
+                seg.set_input(val, arr)
+            if paged:
+                seg.set_input(h["rows"], np.stack([np.zeros(c, np.int32), p, p, p], axis=1))
+            seg.set_scalar("n_past", past)
+            log(f"provider cache step {i}: T={c} past={past}")
+            seg.execute(c)
+            assert_bf16_close(seg.get_output(h["yq"]),
+                              oracle.qk_norm_rope(q, p, wq, 1e-6, dtype="bf16", base=1e4), what=f"q step {i}")
+            rows = p if not paged else table[0, p // 8] * 8 + p % 8
+            ref_k[rows] = oracle.rope(oracle.rmsnorm(oracle.from_bf16(k), wk, 1e-6), p, base=1e4)
+            ref_v[rows] = oracle.from_bf16(v)
+            past += c
+        conv = oracle.to_f16 if cache_type == "f16" else oracle.to_bf16
+        close = assert_f16_close if cache_type == "f16" else assert_bf16_close
+        got_k = seg.get_output(h["kc"]).view(np.uint16)
+        got_v = seg.get_output(h["vc"]).view(np.uint16)
+        close(got_k, conv(ref_k), what="k cache")
+        assert_bits_equal(got_v, conv(ref_v), what="v cache")
+        seg.reset_state()
+        assert not seg.get_output(h["kc"]).view(np.uint16).any()
+
+
+def test_cache_write_needs_its_scalar(dev):
+    g = GraphBuilder()
+    x = g.input("f32", "T", 64)
+    c = g.state("f32", 16, 64)
+    g.cache_write(c, x)
+    with dev.compile(g, max_tokens=4) as seg:
+        seg.set_input(x, np.ones((2, 64), np.float32))
+        with pytest.raises(ValueError, match="Runtime scalar 'n_past' was not provided"):
+            seg.execute(2)
+        seg.set_scalar("n_past", 15)
+        with pytest.raises(native.SlhipCacheError, match=r"n_past 15 \+ T 2 > context 16"):
+            seg.execute(2)

@@ -79,10 +79,11 @@ def test_unsupported_node_is_rejected_at_compile():
 
 def test_malformed_segment_text():
     seg = ctypes.c_void_p(0)
-    for bad in ["value 0 f99 4\n", "node Add 0,1 => 2\n", "output 7\n", "frobnicate\n"]:
+    for bad in ["value 0 f99 4\n", "node Add 0,1 => 2\n", "output 7\n", "frobnicate\n",
+                "value 0 f32 4\nstate 0\nnode CacheWrite 0,0 -> offset=n_past\n"]:
         st = native.lib().slhip_segment_compile(bad.encode(), 8, ctypes.byref(seg))
         assert st == native.ERR_INVALID, bad
-        assert "line 1" in native.last_error()
+        assert "line " in native.last_error()
 
 
 def test_availability_never_raises():
@@ -101,3 +102,30 @@ def test_open_device_of_other_provider():
     from sharplight_amd.provider import DeviceInfo
     with pytest.raises(ValueError):
         HipExecutionProvider().open_device(DeviceInfo("vulkan", 0, "x", "DiscreteGpu", 0, "", "", "", (), 0))
+
+
+def test_cache_write_text_and_support():
+    g = GraphBuilder()
+    k = g.input("bf16", "T", 2, 64)
+    pos = g.input("i32", "T")
+    kc = g.state("f16", 32, 2, 64)
+    g.cache_write(kc, g.rope(k, pos))
+    ir = g.to_ir()
+    assert "state 2" in ir and "node CacheWrite 2,3 -> - offset=n_past" in ir
+    assert _supports(g, 1) == (True, "")
+    q8 = g.state("q8_0", 32, 128)
+    x = g.input("f32", "T", 128)
+    g.cache_write(q8, x)
+    ok, why = _supports(g, 2)
+    assert not ok and "quantized" in why
+    g2 = GraphBuilder()
+    notstate = g2.input("f32", 32, 64)
+    g2.cache_write(notstate, g2.input("f32", "T", 64))
+    ok, why = _supports(g2, 0)
+    assert not ok and "state" in why
+
+
+def test_state_needs_fixed_dims():
+    seg = ctypes.c_void_p(0)
+    st = native.lib().slhip_segment_compile(b"value 0 f32 T 4\nstate 0\n", 8, ctypes.byref(seg))
+    assert st == native.ERR_INVALID and "fixed dims" in native.last_error()
