@@ -165,6 +165,69 @@ class C4(Workload):
                     self.pos.slot(i), self.T, 128, neox=True, base=self.base, norm=True, eps=self.eps, stream=stream)
 
 
+def _paged_rows(T: int, ctx: int, bs: int, seed: int):
+    """One sequence's T distinct positions in [0, ctx) (the C4 config draws positions from 0..32767) and a
+    shuffled block table: the sequence rows [T, 4] and the table [1, ctx / bs]."""
+    r = np.random.default_rng(seed)
+    pos = np.sort(r.permutation(ctx)[:T]).astype(np.int32)
+    seq = np.zeros((T, 4), np.int32)
+    seq[:, 1] = pos
+    table = r.permutation(ctx // bs).astype(np.int32).reshape(1, -1)
+    return pos, seq, table
+
+
+class C4Cache(Workload):
+    """C4 with k stored into a paged bf16 KV cache [32768, 8, 128] (block 16) in the same launch as q: the
+    rope absorbed into its CacheWrite (GraphLowerer.Fusion.cs:633-648). Same bytes as C4 plus the sequence
+    rows and block-table entries the launch reads."""
+    name = "c4_qk_rope_kv_bf16_paged"
+
+    def __init__(self, ctx=32768, bs=16):
+        c = synth.c4()
+        self.desc = "C4 shape, k rope+norm into a paged bf16 KV cache [32768, 8, 128], block 16"
+        self.T = c["pos"].size
+        self.eps, self.base = c["eps"], c["base"]
+        pos, seq, table = _paged_rows(self.T, ctx, bs, 1)
+        qb, kb = c["q"].nbytes, c["k"].nbytes
+        self.bytes_per_step = 2 * (qb + kb) + pos.nbytes + seq.nbytes + self.T * 4 + c["wq"].nbytes + c["wk"].nbytes
+        R = copies_for(self.bytes_per_step)
+        self.q, self.k = Rot(c["q"], qb, R), Rot(c["k"], kb, R)
+        self.yq = Rot(None, qb, R)
+        self.kc = Rot(None, ctx * 8 * 128 * 2, R)
+        self.pos, self.seq, self.pages = Rot(pos, pos.nbytes, 1), Rot(seq, seq.nbytes, 1), Rot(table, table.nbytes, 1)
+        self.rows = native.cache_rows("paged", ctx, seq=self.seq.slot(0), pages=self.pages.slot(0), page_slots=1,
+                                      blocks_per_slot=table.shape[1], block_size=bs)
+        self.wq, self.wk = Rot(c["wq"], 512, 1), Rot(c["wk"], 512, 1)
+
+    def launch(self, i, stream):
+        native.rope("bf16", "bf16",
+                    [dict(x=self.q.slot(i), y=self.yq.slot(i), heads=32, norm_w=self.wq.slot(0)),
+                     dict(x=self.k.slot(i), y=self.kc.slot(i), heads=8, norm_w=self.wk.slot(0), rows=self.rows)],
+                    self.pos.slot(0), self.T, 128, neox=True, base=self.base, norm=True, eps=self.eps, stream=stream)
+
+
+class VCache(Workload):
+    """V [4096, 8, 128] bf16 written into a paged f16 KV cache [32768, 8, 128] (block 16): CacheWrite
+    without an absorbed producer."""
+    name = "v_cache_write_f16_paged"
+
+    def __init__(self, ctx=32768, bs=16, T=4096):
+        self.desc = "V [4096, 8, 128] bf16 into a paged f16 KV cache [32768, 8, 128], block 16"
+        self.T, self.inner = T, 8 * 128
+        v = synth.normal(0, 5, (T, self.inner), dtype="bf16")
+        pos, seq, table = _paged_rows(T, ctx, bs, 2)
+        self.bytes_per_step = 2 * v.nbytes + seq.nbytes + T * 4
+        R = copies_for(self.bytes_per_step)
+        self.v = Rot(v, v.nbytes, R)
+        self.vc = Rot(None, ctx * self.inner * 2, R)
+        self.seq, self.pages = Rot(seq, seq.nbytes, 1), Rot(table, table.nbytes, 1)
+        self.rows = native.cache_rows("paged", ctx, seq=self.seq.slot(0), pages=self.pages.slot(0), page_slots=1,
+                                      blocks_per_slot=table.shape[1], block_size=bs)
+
+    def launch(self, i, stream):
+        native.cache_write("bf16", "f16", self.v.slot(i), self.T, self.inner, self.vc.slot(i), self.rows, stream=stream)
+
+
 class C5(Workload):
     def __init__(self, fmt):
         self.fmt = fmt
@@ -237,6 +300,8 @@ WORKLOADS = {
     "c5_gather_q8_0": lambda: C5("q8_0"),
     "c5_gather_q4_0": lambda: C5("q4_0"),
     "c5_gather_f16": lambda: C5("f16"),
+    "c4_qk_rope_kv_bf16_paged": lambda: C4Cache(),
+    "v_cache_write_f16_paged": lambda: VCache(),
     "copy_256MiB": lambda: CopyRef(),
 }
 
@@ -383,6 +448,31 @@ def cpu_baselines(budget_main: float, budget_op: float, which: set[str]) -> dict
         s, reps = cpu_time(lambda: L.orc_gather_mt(oracle.FORMATS[fmt], P(c["table"]), V, D, P(c["ids"]), N, P(y),
                                                    ctypes.byref(bad)), budget_op)
         res[name] = dict(s=s * 16384 / N, reps=reps, sample=f"{N} of 16384 ids, scaled x{16384 // N}, f32 output")
+    if "c4_qk_rope_kv_bf16_paged" in which or "v_cache_write_f16_paged" in which:
+        T, ctx = 1024, 32768
+        L, P = oracle.lib(), oracle._p
+        pos, seq, table = _paged_rows(T, ctx, 16, 1)
+        rows = oracle.cache_rows("paged", T, ctx, seq=seq, pages=table, block_size=16)
+        if "c4_qk_rope_kv_bf16_paged" in which:
+            c = synth.c4(T=T)
+            q, k = oracle.from_bf16(c["q"]), oracle.from_bf16(c["k"])
+            qn, kn, qo, ko = (np.empty_like(q), np.empty_like(k), np.empty_like(q), np.empty_like(k))
+            cache = np.zeros((ctx, 8 * 128), np.uint16)
+
+            def run():
+                L.orc_rmsnorm_mt(P(q), P(c["wq"]), P(qn), T * 32, 128, c["eps"], 0)
+                L.orc_rmsnorm_mt(P(k), P(c["wk"]), P(kn), T * 8, 128, c["eps"], 0)
+                L.orc_rope_mt(P(qn), P(pos), None, P(qo), T, 32, 128, 128, 1, c["base"], 1.0, 1.0)
+                L.orc_rope_mt(P(kn), P(pos), None, P(ko), T, 8, 128, 128, 1, c["base"], 1.0, 1.0)
+                L.orc_cache_write_mt(oracle.BF16, P(cache), 8 * 128, P(ko), T, P(rows))
+            s, reps = cpu_time(run, budget_op)
+            res["c4_qk_rope_kv_bf16_paged"] = dict(s=s * 4096 / T, reps=reps,
+                                                   sample=f"{T} of 4096 tokens, scaled x{4096 // T}; RmsNorm, Rope, CacheWrite")
+        if "v_cache_write_f16_paged" in which:
+            v = oracle.from_bf16(synth.normal(0, 5, (T, 8 * 128), dtype="bf16"))
+            cache = np.zeros((ctx, 8 * 128), np.uint16)
+            s, reps = cpu_time(lambda: L.orc_cache_write_mt(oracle.F16, P(cache), 8 * 128, P(v), T, P(rows)), budget_op)
+            res["v_cache_write_f16_paged"] = dict(s=s * 4096 / T, reps=reps, sample=f"{T} of 4096 tokens, scaled x{4096 // T}")
     for v in res.values():
         v["threads"] = threads
     return res

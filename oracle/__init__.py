@@ -82,6 +82,7 @@ def _declare(L):
         "orc_f32_to_f16_n": (None, [_P, _P, _I64]),
         "orc_cache_rows": (_I, [_I, _I64, _I64, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, ctypes.c_char_p, _I64]),
         "orc_cache_write": (None, [_I, _P, _I64, _P, _I64, _P]),
+        "orc_cache_write_mt": (None, [_I, _P, _I64, _P, _I64, _P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

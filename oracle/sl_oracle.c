@@ -780,3 +780,28 @@ int orc_gather_mt(int fmt, const uint8_t* table, int64_t V, int64_t D, const int
     if (g.status && bad_index) *bad_index = g.bad;
     return g.status;
 }
+
+typedef struct {
+    int type;
+    void* cache;
+    int64_t inner, T, per;
+    const float* x;
+    const int64_t* rows;
+} cache_ctx;
+
+static void cache_chunk(void* v, int64_t c)
+{
+    cache_ctx* k = (cache_ctx*)v;
+    int64_t s = c * k->per, e = s + k->per < k->T ? s + k->per : k->T;
+    if (s < e) orc_cache_write(k->type, k->cache, k->inner, k->x + s * k->inner, e - s, k->rows + s);
+}
+
+/* CacheWriteOp.Run (CacheWriteOp.cs:122-126): chunks = min(rows, Chunks(rows*rowLen, 8192)), over tokens. */
+void orc_cache_write_mt(int cache_type, void* cache, int64_t inner, const float* x, int64_t T, const int64_t* rows)
+{
+    if (T == 0) return;
+    int64_t ch = chunks_for(T * inner, 8192);
+    if (ch > T) ch = T;
+    cache_ctx k = {cache_type, cache, inner, T, (T + ch - 1) / ch, x, rows};
+    parallel_for(ch, cache_chunk, &k);
+}

@@ -79,6 +79,7 @@ void orc_mul_mt(const float* a, const float* b, float* y, int64_t n);
 void orc_unary_mt(int act, const float* x, float* y, int64_t n);
 void orc_rope_mt(const float* x, const int32_t* pos, const float* ff, float* y, int64_t T, int64_t H, int64_t D, int dims,
                  int neox, float base, float freq_scale, float attn_factor);
+void orc_cache_write_mt(int cache_type, void* cache, int64_t inner, const float* x, int64_t T, const int64_t* rows);
 int orc_gather_mt(int fmt, const uint8_t* table, int64_t V, int64_t D, const int32_t* ids, int64_t N, float* y,
                   int64_t* bad_index);
 
