@@ -83,6 +83,8 @@ def _declare(L):
         "orc_cache_rows": (_I, [_I, _I64, _I64, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, ctypes.c_char_p, _I64]),
         "orc_cache_write": (None, [_I, _P, _I64, _P, _I64, _P]),
         "orc_cache_write_mt": (None, [_I, _P, _I64, _P, _I64, _P]),
+        "orc_e4m3_code": (ctypes.c_uint8, [_F]),
+        "orc_quantize_fp8_rows": (None, [_P, _I64, _I64, _P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -308,3 +310,20 @@ def cache_write(cache, x, rows, cache_type):
     rows = _c(rows, np.int64)
     lib().orc_cache_write(FORMATS[cache_type], _p(cache), inner, _p(x), T, _p(rows))
     return cache
+
+
+# ---- E4M3 activation rows ---------------------------------------------------------------------------
+
+def e4m3_code(v: float) -> int:
+    return int(lib().orc_e4m3_code(float(v)))
+
+
+def quantize_fp8(x):
+    """quantize_fp8 (Kernels/gemm_fp8.slang:36-55): rows [R, K] f32 (K % 128 == 0) -> [R, K + K/32] bytes,
+    K E4M3 codes then K/128 f32 scales (amax / 448) per row."""
+    x = _c(x, np.float32)
+    K = x.shape[-1]
+    rows = x.size // K
+    out = np.empty((rows, K + K // 32), np.uint8)
+    lib().orc_quantize_fp8_rows(_p(x), rows, K, _p(out))
+    return out.reshape(x.shape[:-1] + (K + K // 32,))

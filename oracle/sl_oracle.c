@@ -805,3 +805,51 @@ void orc_cache_write_mt(int cache_type, void* cache, int64_t inner, const float*
     cache_ctx k = {cache_type, cache, inner, T, (T + ch - 1) / ch, x, rows};
     parallel_for(ch, cache_chunk, &k);
 }
+
+/* ------------------------------------------------------------------------------------------ */
+/* E4M3 activation rows (norm-written copies for the fp8 GEMM)                               */
+/* ------------------------------------------------------------------------------------------ */
+
+/* e4m3_code (src/Sharplight.Shaders/Kernels/e4m3.slang:5-23): the E4M3 code of |v| <= 448 rounded to
+ * nearest even; below 2^-6 a multiple of 2^-9 (round() of HLSL: halfway cases to even), above by adding
+ * 0x7FFFF + lsb at bit 20 of the f32 bits; saturated at code 0x7E (448); the sign in bit 7. */
+uint8_t orc_e4m3_code(float v)
+{
+    uint32_t sign = v < 0 ? 0x80u : 0u;
+    float a = fabsf(v);
+    uint32_t code;
+    if (a < 0.015625f) {
+        code = (uint32_t)nearbyintf(a * 512.0f); /* the default rounding mode: to nearest even */
+    } else {
+        uint32_t bits = f2u(a);
+        bits += 0x7FFFFu + ((bits >> 20) & 1u);
+        uint32_t c = (bits >> 20) - (120u << 3);
+        code = c < 0x7Eu ? c : 0x7Eu;
+    }
+    return (uint8_t)(sign | code);
+}
+
+/* quantize_fp8 (Kernels/gemm_fp8.slang:36-55) on one row of K values (K % 128 == 0): per 128-value group
+ * d = amax / 448 (e4m3_group_scale, e4m3.slang:25-31), codes of v * (d > 0 ? 1/d : 0) (e4m3_pack4,
+ * :33-38); out = [K codes][K/128 f32 scales], the activation row layout of the fp8 GEMM. */
+void orc_quantize_fp8_row(const float* x, int64_t K, uint8_t* out)
+{
+    float* scales = (float*)(out + K);
+    for (int64_t g = 0; g < K / 128; g++) {
+        const float* v = x + g * 128;
+        float amax = 0.0f;
+        for (int i = 0; i < 128; i++) {
+            float m = fabsf(v[i]);
+            if (m > amax) amax = m;
+        }
+        float d = amax / 448.0f;
+        float id = d > 0 ? 1.0f / d : 0.0f;
+        for (int i = 0; i < 128; i++) out[g * 128 + i] = orc_e4m3_code(v[i] * id);
+        memcpy(&scales[g], &d, 4);
+    }
+}
+
+void orc_quantize_fp8_rows(const float* x, int64_t rows, int64_t K, uint8_t* out)
+{
+    for (int64_t r = 0; r < rows; r++) orc_quantize_fp8_row(x + r * K, K, out + r * (K + K / 32));
+}

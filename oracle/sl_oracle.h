@@ -69,6 +69,11 @@ int orc_cache_rows(int mode, int64_t T, int64_t ctx, int64_t n_past, const int32
 /* x [T, inner] f32 -> cache rows[t] (cache_type ORC_F32 / ORC_F16 / ORC_BF16). */
 void orc_cache_write(int cache_type, void* cache, int64_t inner, const float* x, int64_t T, const int64_t* rows);
 
+/* ---- E4M3 activation rows (Kernels/e4m3.slang, Kernels/gemm_fp8.slang quantize_fp8) ---- */
+uint8_t orc_e4m3_code(float v);
+/* rows of K values (K % 128 == 0) -> rows of K + K/32 bytes: K codes, then K/128 f32 scales */
+void orc_quantize_fp8_rows(const float* x, int64_t rows, int64_t K, uint8_t* out);
+
 /* ---- threaded variants for the CPU baseline (CpuParallel.cs:34-78) ---- */
 void orc_set_threads(int threads);
 int orc_get_threads(void);

@@ -417,3 +417,53 @@ def test_cache_write_converts_into_rows(ct):
     assert np.array_equal(cache[rows], conv(x))
     untouched = np.setdiff1d(np.arange(ctx), rows)
     assert (cache[untouched] == 7).all()
+
+
+# ---- E4M3 activation rows (Kernels/e4m3.slang, Kernels/gemm_fp8.slang) ------------------------------
+
+def _e4m3_values():
+    """Every non-negative finite E4M3 code's value from the format's definition: bias 7, 3 mantissa bits,
+    subnormals m * 2^-9, largest finite code 0x7E = 448 (0x7F is NaN)."""
+    c = np.arange(0x7F)
+    e, m = c >> 3, c & 7
+    return np.where(e == 0, m * 2.0 ** -9, (1 + m / 8) * 2.0 ** (e - 7))
+
+
+def _e4m3_nearest(v):
+    """Brute force: the code whose value is nearest |v| (ties to the even code), saturated at 0x7E."""
+    vals = _e4m3_values()
+    a = np.minimum(np.abs(np.asarray(v, np.float64)), 448.0)
+    d = np.abs(a[:, None] - vals[None, :])
+    best = d.min(axis=1, keepdims=True)
+    cand = np.where(d == best, np.arange(0x7F)[None, :], 1 << 20)
+    even = np.where(cand % 2 == 0, cand, 1 << 20).min(axis=1)
+    code = np.where(even < (1 << 20), even, cand.min(axis=1))
+    return (code | np.where(np.asarray(v) < 0, 0x80, 0)).astype(np.uint8)
+
+
+def test_e4m3_code_is_nearest_even():
+    vals = _e4m3_values()
+    mids = (vals[:-1] + vals[1:]) / 2
+    f = np.float32
+    cand = np.concatenate([vals, mids, np.nextafter(mids.astype(f), f(0)), np.nextafter(mids.astype(f), f(1e9)),
+                           np.random.default_rng(8).uniform(0, 500, 20000), [448, 460, 464, 480, 1e6]]).astype(f)
+    cand = np.concatenate([cand, -cand])
+    got = np.array([oracle.e4m3_code(v) for v in cand], np.uint8)
+    assert np.array_equal(got, _e4m3_nearest(cand))
+
+
+def test_quantize_fp8_rows():
+    """Per 128 values: scale amax / 448, codes nearest to v / scale (computed as v * (1/scale) in f32)."""
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((3, 512)).astype(np.float32) * np.float32([[1], [1e-3], [300]])
+    x[1, 128:256] = 0  # an all-zero group: scale 0, codes 0
+    q = oracle.quantize_fp8(x)
+    assert q.shape == (3, 512 + 16)
+    for r in range(3):
+        d = q[r, 512:].view(np.float32)
+        for g in range(4):
+            v = x[r, 128 * g:128 * (g + 1)]
+            assert d[g] == np.float32(np.abs(v).max()) / np.float32(448)
+            inv = np.float32(1) / d[g] if d[g] > 0 else np.float32(0)
+            assert np.array_equal(q[r, 128 * g:128 * (g + 1)], _e4m3_nearest(v * inv))
+    assert not q[1, 128:256].any() and q[1, 512 + 4:512 + 8].view(np.float32)[0] == 0
