@@ -38,7 +38,7 @@ extern "C" {
 #define SLHIP_API __attribute__((visibility("default")))
 #endif
 
-#define SLHIP_ABI_VERSION 2
+#define SLHIP_ABI_VERSION 3
 
 typedef enum slhip_status {
     SLHIP_OK = 0,
@@ -162,6 +162,37 @@ SLHIP_API int slhip_graph_destroy(slhip_graph graph);
 SLHIP_API int slhip_rownorm(int kind, int dtype_in, int dtype_out, const void* x, const void* res, const float* w,
                             const float* b, void* y, void* h_out, int64_t rows, int64_t D, int64_t x_stride,
                             int64_t res_stride, int64_t y_stride, int64_t h_stride, float eps, slhip_stream stream);
+
+/*
+ * The GEMM activation copies a row norm can write beside (or instead of) y, from the same f32 values
+ * (the "nrm" of the reference's two-pass row norm kernel):
+ *   y16: f16 rows (round to nearest even; NaN keeps its payload top bits), row stride y16_stride elements;
+ *   yq:  E4M3 activation rows of the fp8 GEMM: per row D codes, then D/128 f32 scales; for each 128-value
+ *        group d = amax/448 and code = e4m3(v * (d > 0 ? 1/d : 0)) (quantize_fp8). Row stride yq_stride
+ *        bytes >= D + D/32 (the reference's dense rows are exactly that), D a multiple of 128,
+ *        4-byte aligned.
+ * Either may be NULL.
+ * Replaces: the f16 copy outputs and Fp8Output of RowNormKernelSource
+ * (src/Sharplight.Shaders/Lowering/RowNormKernelSource.cs:45-57,108-124,282-291; GraphLowerer.HalfCopies.cs:
+ * 36-40,106-151; GraphLowerer.Elementwise.cs:150-200), quantize_fp8 (Kernels/gemm_fp8.slang:36-55) and
+ * e4m3_code / e4m3_pack4 (Kernels/e4m3.slang:5-38).
+ */
+typedef struct slhip_norm_copies {
+    void* y16;
+    int64_t y16_stride;
+    void* yq;
+    int64_t yq_stride;
+} slhip_norm_copies;
+
+/*
+ * slhip_rownorm that also writes the copies in `copies` (NULL: none). y may be NULL when a copy is given:
+ * the reference's norm skips its f32 rows from prefill sizes when every reader takes the copy
+ * (GraphLowerer.Elementwise.cs:184-200).
+ */
+SLHIP_API int slhip_rownorm_copies(int kind, int dtype_in, int dtype_out, const void* x, const void* res,
+                                   const float* w, const float* b, void* y, void* h_out, int64_t rows, int64_t D,
+                                   int64_t x_stride, int64_t res_stride, int64_t y_stride, int64_t h_stride,
+                                   float eps, const slhip_norm_copies* copies, slhip_stream stream);
 
 /*
  * Gated activation out = act(gate) * up over [rows, cols] (IMlpActivation.ActivateGated,

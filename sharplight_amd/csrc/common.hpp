@@ -71,6 +71,8 @@ __device__ __forceinline__ void store_nt(void* p, const uint2& v)
     __builtin_nontemporal_store(t, static_cast<u32x2*>(p));
 }
 
+__device__ __forceinline__ void store_nt(void* p, uint32_t v) { __builtin_nontemporal_store(v, static_cast<uint32_t*>(p)); }
+
 // ---- device side: conversions ----------------------------------------------------------------------
 
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
@@ -226,6 +228,38 @@ template <int W> __device__ __forceinline__ float group_sum(float v)
 }
 
 __device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
+
+// Max over groups of W consecutive lanes; every lane of the group ends with the same value.
+template <int W> __device__ __forceinline__ float group_max(float v)
+{
+#pragma unroll
+    for (int o = W / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// ---- device side: E4M3 activation rows -------------------------------------------------------------
+
+// E4M3 code of v (|v| <= 448 expected) with the reference's rule (e4m3_code,
+// src/Sharplight.Shaders/Kernels/e4m3.slang:5-23): below 2^-6 the nearest multiple of 2^-9 (ties to
+// even), else round the f32 bits to 3 mantissa bits (ties to even) and rebias, saturating at code 0x7E
+// (448); the sign bit only for v < 0. Integer arithmetic, so every input -- NaN and infinities included --
+// gets the reference's code, which the hardware fp8 conversion would not (it yields 0x7F for NaN).
+__device__ __forceinline__ uint32_t e4m3_code(float v)
+{
+    const float a = fabsf(v);
+    const uint32_t sub = static_cast<uint32_t>(__builtin_rintf(a * 512.0f));
+    uint32_t bits = __float_as_uint(a);
+    bits += 0x7FFFFu + ((bits >> 20) & 1u);
+    const uint32_t nrm = min((bits >> 20) - (120u << 3), 0x7Eu);
+    return (v < 0.0f ? 0x80u : 0u) | (a < 0.015625f ? sub : nrm);
+}
+
+// The 4 codes of v[0..3] * id, packed little-endian (e4m3_pack4, e4m3.slang:33-38).
+__device__ __forceinline__ uint32_t e4m3_pack4(const float* v, float id)
+{
+    return e4m3_code(v[0] * id) | (e4m3_code(v[1] * id) << 8) | (e4m3_code(v[2] * id) << 16) |
+           (e4m3_code(v[3] * id) << 24);
+}
 
 // ---- device side: errors raised by kernels -----------------------------------------------------------
 

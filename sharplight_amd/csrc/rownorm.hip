@@ -14,7 +14,10 @@
 // instruction of a wave covers 1 KiB of consecutive bytes. The row stays in VGPRs between the
 // reduction and the scaling pass. Reductions are a butterfly within the wave, then (WPR > 1) one LDS
 // exchange between the group's waves. A block holds 256/(64*WPR) row groups (or one group of up to
-// 16 waves). Rows that do not fit the vector path (D not a multiple of the vector width, unaligned
+// 16 waves). The GEMM activation copies of the normalized row (f16 values; E4M3 codes with one f32
+// scale per 128 values) are written from the same f32 values as y: a 128-value group of the E4M3 rows is
+// the 16 (bf16 input) or 32 (f32 input) consecutive lanes holding it, so its amax is a butterfly max over
+// those lanes. Rows that do not fit the vector path (D not a multiple of the vector width, unaligned
 // pointers or strides, or D beyond 8*64*16 vectors) take a scalar block-per-row kernel.
 #include "common.hpp"
 
@@ -34,6 +37,10 @@ struct RowNormArgs {
     int64_t xs, rs, ys, hs;  // row strides in elements
     float eps;
     int kind;
+    void* y16;     // f16 copy of y, or null
+    int64_t y16s;  // its row stride in elements
+    void* yq;      // E4M3 rows (D codes, then D/128 f32 scales), or null
+    int64_t yqs;   // their row stride in bytes
 };
 
 template <int NG>  // number of row groups sharing the LDS exchange
@@ -49,11 +56,12 @@ __device__ __forceinline__ float group_reduce(float v, int wpr, int group, int w
     return s;
 }
 
-template <int DTI, int DTO, int NV, bool RES>
+template <int DTI, int DTO, int NV, bool RES, bool Q>
 __global__ __launch_bounds__(1024) void rownorm_vec(RowNormArgs a, int wpr)
 {
     using VI = Vec<DTI>;
     constexpr int E = VI::N;  // elements per 16-byte input vector
+    constexpr int G = 128 / E;  // lanes per 128-value E4M3 group
     __shared__ float red[4 * 16];
 
     const int lane = threadIdx.x & 63;
@@ -70,6 +78,8 @@ __global__ __launch_bounds__(1024) void rownorm_vec(RowNormArgs a, int wpr)
     // past the row's end works on the row's last vector and a group past the last row on the last row,
     // storing the same bytes as their owners, and masked values are kept out of the sums. (A memory
     // operation under a divergent branch makes the compiler wait for all outstanding ones afterwards.)
+    // With E4M3 rows (D a multiple of 128) a lane past the end takes its place in the row's last 128-value
+    // group instead, so that a whole group of such lanes repeats that group's codes and scale exactly.
     const int64_t row = row0 < a.rows ? row0 : a.rows - 1;
     int jv[NV];
     bool own[NV];
@@ -77,7 +87,7 @@ __global__ __launch_bounds__(1024) void rownorm_vec(RowNormArgs a, int wpr)
     for (int k = 0; k < NV; k++) {
         const int j = t + k * tpr;
         own[k] = j < nvec;
-        jv[k] = own[k] ? j : nvec - 1;
+        jv[k] = own[k] ? j : Q ? nvec - G + (j & (G - 1)) : nvec - 1;
     }
     const char* xr = static_cast<const char*>(a.x) + row * a.xs * VI::BYTES;
     uint4 raw[NV], rraw[NV];
@@ -156,6 +166,8 @@ __global__ __launch_bounds__(1024) void rownorm_vec(RowNormArgs a, int wpr)
     }
 
     char* yr = static_cast<char*>(a.y) + row * a.ys * Vec<DTO>::BYTES;
+    char* y16r = static_cast<char*>(a.y16) + row * a.y16s * 2;
+    char* qr = static_cast<char*>(a.yq) + row * a.yqs;
 #pragma unroll
     for (int k = 0; k < NV; k++) {
         float o[E];
@@ -181,7 +193,24 @@ __global__ __launch_bounds__(1024) void rownorm_vec(RowNormArgs a, int wpr)
                 o[4 * q4 + 3] += b4.w;
             }
         }
-        store_packed<DTO, E>(yr + static_cast<int64_t>(jv[k]) * E * Vec<DTO>::BYTES, o);
+        if (a.y) store_packed<DTO, E>(yr + static_cast<int64_t>(jv[k]) * E * Vec<DTO>::BYTES, o);
+        if (a.y16) store_packed<SLHIP_F16, E>(y16r + static_cast<int64_t>(jv[k]) * E * 2, o);
+        if (Q) {
+            // quantize_fp8 on the group (src/Sharplight.Shaders/Kernels/gemm_fp8.slang:36-55): d = amax/448,
+            // codes of o * (1/d); every lane of the group stores the same scale.
+            float m = 0.0f;
+#pragma unroll
+            for (int e = 0; e < E; e++) m = fmaxf(m, fabsf(o[e]));
+            m = group_max<G>(m);
+            const float d = m / 448.0f;
+            const float id = d > 0.0f ? 1.0f / d : 0.0f;
+            char* qp = qr + static_cast<int64_t>(jv[k]) * E;
+            if constexpr (E == 8)
+                store_nt(qp, make_uint2(e4m3_pack4(o, id), e4m3_pack4(o + 4, id)));
+            else
+                store_nt(qp, e4m3_pack4(o, id));
+            store_nt(qr + a.D + static_cast<int64_t>(jv[k] / G) * 4, __float_as_uint(d));
+        }
     }
 }
 
@@ -196,7 +225,9 @@ __global__ __launch_bounds__(256) void rownorm_scalar(RowNormArgs a)
     const void* xr = static_cast<const char*>(a.x) + row * a.xs * VI::BYTES;
     const void* rr = a.res ? static_cast<const char*>(a.res) + row * a.rs * VI::BYTES : nullptr;
     void* hr = (a.res && a.h) ? static_cast<char*>(a.h) + row * a.hs * VI::BYTES : nullptr;
-    void* yr = static_cast<char*>(a.y) + row * a.ys * Vec<DTO>::BYTES;
+    void* yr = a.y ? static_cast<char*>(a.y) + row * a.ys * Vec<DTO>::BYTES : nullptr;
+    void* y16r = a.y16 ? static_cast<char*>(a.y16) + row * a.y16s * 2 : nullptr;
+    char* qr = a.yq ? static_cast<char*>(a.yq) + row * a.yqs : nullptr;
     const int64_t D = a.D;
 
     auto reduce = [&](float s) {
@@ -232,13 +263,30 @@ __global__ __launch_bounds__(256) void rownorm_scalar(RowNormArgs a)
         float ss = reduce(q);
         scale = a.kind == SLHIP_NORM_RMS ? 1.0f / sqrtf(ss / static_cast<float>(D) + a.eps) : 1.0f / sqrtf(ss + a.eps);
     }
-    for (int64_t i = threadIdx.x; i < D; i += 256) {
-        float v = value(i);
-        if (hr) VI::store1(hr, i, v);
+    auto normed = [&](float v, int64_t i) {
         float o = a.kind == SLHIP_NORM_LAYER ? (v - mean) * scale : v * scale;
         if (a.w) o *= a.w[i];
         if (a.b) o += a.b[i];
-        Vec<DTO>::store1(yr, i, o);
+        return o;
+    };
+    for (int64_t i = threadIdx.x; i < D; i += 256) {
+        float v = value(i);
+        if (hr) VI::store1(hr, i, v);
+        const float o = normed(v, i);
+        if (yr) Vec<DTO>::store1(yr, i, o);
+        if (y16r) Vec<SLHIP_F16>::store1(y16r, i, o);
+    }
+    if (qr) {  // one wave per 128-value group, two values per lane
+        const int lane = threadIdx.x & 63;
+        for (int64_t g = threadIdx.x >> 6; g < D / 128; g += 4) {
+            const int64_t i0 = g * 128 + lane, i1 = i0 + 64;
+            const float o0 = normed(value(i0), i0), o1 = normed(value(i1), i1);
+            const float d = group_max<64>(fmaxf(fabsf(o0), fabsf(o1))) / 448.0f;
+            const float id = d > 0.0f ? 1.0f / d : 0.0f;
+            qr[i0] = static_cast<char>(e4m3_code(o0 * id));
+            qr[i1] = static_cast<char>(e4m3_code(o1 * id));
+            if (lane == 0) *reinterpret_cast<float*>(qr + D + g * 4) = d;
+        }
     }
 }
 
@@ -250,17 +298,17 @@ static int env_int(const char* name, int dflt)
     return s && *s ? atoi(s) : dflt;
 }
 
-template <int DTI, int DTO, bool RES>
+template <int DTI, int DTO, bool RES, bool Q>
 static int launch_vec(const RowNormArgs& a, int nv, int wpr, hipStream_t st)
 {
     int groups = wpr >= 4 ? 1 : 4 / wpr;
     int threads = 64 * wpr * groups;
     dim3 grid(static_cast<unsigned>((a.rows + groups - 1) / groups));
     switch (nv) {
-    case 1: rownorm_vec<DTI, DTO, 1, RES><<<grid, threads, 0, st>>>(a, wpr); break;
-    case 2: rownorm_vec<DTI, DTO, 2, RES><<<grid, threads, 0, st>>>(a, wpr); break;
-    case 4: rownorm_vec<DTI, DTO, 4, RES><<<grid, threads, 0, st>>>(a, wpr); break;
-    case 8: rownorm_vec<DTI, DTO, 8, RES><<<grid, threads, 0, st>>>(a, wpr); break;
+    case 1: rownorm_vec<DTI, DTO, 1, RES, Q><<<grid, threads, 0, st>>>(a, wpr); break;
+    case 2: rownorm_vec<DTI, DTO, 2, RES, Q><<<grid, threads, 0, st>>>(a, wpr); break;
+    case 4: rownorm_vec<DTI, DTO, 4, RES, Q><<<grid, threads, 0, st>>>(a, wpr); break;
+    case 8: rownorm_vec<DTI, DTO, 8, RES, Q><<<grid, threads, 0, st>>>(a, wpr); break;
     default: return fail(SLHIP_ERR_INVALID, "internal: bad vector count %d", nv);
     }
     return check_launch("rownorm_vec");
@@ -271,9 +319,12 @@ static int dispatch(const RowNormArgs& a, hipStream_t st)
 {
     constexpr int E = Vec<DTI>::N;
     constexpr int OA = E * Vec<DTO>::BYTES < 16 ? E * Vec<DTO>::BYTES : 16;  // output store alignment
+    constexpr int HA = E * 2;  // f16 copy store alignment (16 or 8 bytes)
     bool vec_ok = a.D % E == 0 && aligned16(a.x) && a.xs % E == 0 && (!a.res || (aligned16(a.res) && a.rs % E == 0)) &&
                   (!a.h || (aligned16(a.h) && a.hs % E == 0)) &&
                   reinterpret_cast<uintptr_t>(a.y) % OA == 0 && (a.ys * Vec<DTO>::BYTES) % OA == 0 &&
+                  reinterpret_cast<uintptr_t>(a.y16) % HA == 0 && (a.y16s * 2) % HA == 0 &&
+                  reinterpret_cast<uintptr_t>(a.yq) % E == 0 && a.yqs % E == 0 &&
                   (!a.w || aligned16(a.w)) && (!a.b || aligned16(a.b));
     int64_t nvec = a.D / E;
     if (vec_ok && nvec <= 8 * 64 * 16) {
@@ -289,7 +340,11 @@ static int dispatch(const RowNormArgs& a, hipStream_t st)
         }
         int64_t per = (nvec + 64 * wpr - 1) / (64 * wpr);
         int nv = per <= 1 ? 1 : per <= 2 ? 2 : per <= 4 ? 4 : 8;
-        return a.res ? launch_vec<DTI, DTO, true>(a, nv, wpr, st) : launch_vec<DTI, DTO, false>(a, nv, wpr, st);
+        if (a.yq)
+            return a.res ? launch_vec<DTI, DTO, true, true>(a, nv, wpr, st)
+                         : launch_vec<DTI, DTO, false, true>(a, nv, wpr, st);
+        return a.res ? launch_vec<DTI, DTO, true, false>(a, nv, wpr, st)
+                     : launch_vec<DTI, DTO, false, false>(a, nv, wpr, st);
     }
     rownorm_scalar<DTI, DTO><<<dim3(static_cast<unsigned>(a.rows)), 256, 0, st>>>(a);
     return check_launch("rownorm_scalar");
@@ -299,25 +354,49 @@ static int dispatch(const RowNormArgs& a, hipStream_t st)
 
 using namespace slhip;
 
-extern "C" SLHIP_API int slhip_rownorm(int kind, int dtype_in, int dtype_out, const void* x, const void* res,
-                                       const float* w, const float* b, void* y, void* h_out, int64_t rows, int64_t D,
-                                       int64_t x_stride, int64_t res_stride, int64_t y_stride, int64_t h_stride,
-                                       float eps, slhip_stream stream)
+extern "C" SLHIP_API int slhip_rownorm_copies(int kind, int dtype_in, int dtype_out, const void* x, const void* res,
+                                              const float* w, const float* b, void* y, void* h_out, int64_t rows,
+                                              int64_t D, int64_t x_stride, int64_t res_stride, int64_t y_stride,
+                                              int64_t h_stride, float eps, const slhip_norm_copies* copies,
+                                              slhip_stream stream)
 {
+    void* y16 = copies ? copies->y16 : nullptr;
+    void* yq = copies ? copies->yq : nullptr;
     if (kind < SLHIP_NORM_RMS || kind > SLHIP_NORM_LAYER) return fail(SLHIP_ERR_INVALID, "rownorm: bad kind %d", kind);
     if (rows < 0 || D < 0) return fail(SLHIP_ERR_INVALID, "rownorm: negative shape");
     if (rows == 0 || D == 0) return SLHIP_OK;
-    if (!x || !y) return fail(SLHIP_ERR_INVALID, "rownorm: x and y are required");
+    if (!x) return fail(SLHIP_ERR_INVALID, "rownorm: x is required");
+    if (!y && !y16 && !yq) return fail(SLHIP_ERR_INVALID, "rownorm: y or a copy of it is required");
     if (kind == SLHIP_NORM_L2 && w) return fail(SLHIP_ERR_INVALID, "rownorm: L2Norm takes no weight");
     if (kind != SLHIP_NORM_LAYER && b) return fail(SLHIP_ERR_INVALID, "rownorm: only LayerNorm takes a bias");
-    if (x_stride < D || y_stride < D || (res && res_stride < D) || (res && h_out && h_stride < D))
+    if (x_stride < D || (y && y_stride < D) || (res && res_stride < D) || (res && h_out && h_stride < D) ||
+        (y16 && copies->y16_stride < D))
         return fail(SLHIP_ERR_INVALID, "rownorm: a row stride is smaller than D");
+    if (yq && D % 128 != 0)
+        return fail(SLHIP_ERR_INVALID, "rownorm: E4M3 rows need a row length that is a multiple of 128 (D = %lld)",
+                    static_cast<long long>(D));
+    if (yq && copies->yq_stride < D + D / 32)
+        return fail(SLHIP_ERR_INVALID, "rownorm: E4M3 row stride %lld is below D + D/32 = %lld bytes",
+                    static_cast<long long>(copies->yq_stride), static_cast<long long>(D + D / 32));
+    if (yq && (reinterpret_cast<uintptr_t>(yq) % 4 != 0 || copies->yq_stride % 4 != 0))
+        return fail(SLHIP_ERR_INVALID, "rownorm: E4M3 rows must be 4-byte aligned (their f32 scales)");
     if (rows > 0x7FFFFFFF) return fail(SLHIP_ERR_UNSUPPORTED, "rownorm: more than 2^31-1 rows");
-    RowNormArgs a{x, res, w, b, y, res ? h_out : nullptr, rows, D, x_stride, res_stride, y_stride, h_stride, eps, kind};
+    RowNormArgs a{x, res, w, b, y, res ? h_out : nullptr, rows, D, x_stride, res_stride, y_stride, h_stride, eps, kind,
+                  y16, y16 ? copies->y16_stride : 0, yq, yq ? copies->yq_stride : 0};
     hipStream_t st = to_stream(stream);
     if (dtype_in == SLHIP_F32 && dtype_out == SLHIP_F32) return dispatch<SLHIP_F32, SLHIP_F32>(a, st);
     if (dtype_in == SLHIP_BF16 && dtype_out == SLHIP_BF16) return dispatch<SLHIP_BF16, SLHIP_BF16>(a, st);
     if (dtype_in == SLHIP_BF16 && dtype_out == SLHIP_F32) return dispatch<SLHIP_BF16, SLHIP_F32>(a, st);
     if (dtype_in == SLHIP_F32 && dtype_out == SLHIP_BF16) return dispatch<SLHIP_F32, SLHIP_BF16>(a, st);
     return fail(SLHIP_ERR_UNSUPPORTED, "rownorm: dtype pair (%d -> %d) not supported", dtype_in, dtype_out);
+}
+
+extern "C" SLHIP_API int slhip_rownorm(int kind, int dtype_in, int dtype_out, const void* x, const void* res,
+                                       const float* w, const float* b, void* y, void* h_out, int64_t rows, int64_t D,
+                                       int64_t x_stride, int64_t res_stride, int64_t y_stride, int64_t h_stride,
+                                       float eps, slhip_stream stream)
+{
+    if (!y && rows > 0 && D > 0) return fail(SLHIP_ERR_INVALID, "rownorm: x and y are required");
+    return slhip_rownorm_copies(kind, dtype_in, dtype_out, x, res, w, b, y, h_out, rows, D, x_stride, res_stride,
+                                y_stride, h_stride, eps, nullptr, stream);
 }

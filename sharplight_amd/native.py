@@ -65,6 +65,12 @@ class CacheRows(ctypes.Structure):
                 ("block_size", ctypes.c_int64)]
 
 
+class NormCopies(ctypes.Structure):
+    """slhip_norm_copies: the f16 and E4M3 GEMM activation copies a row norm writes (either may be NULL)."""
+    _fields_ = [("y16", ctypes.c_void_p), ("y16_stride", ctypes.c_int64), ("yq", ctypes.c_void_p),
+                ("yq_stride", ctypes.c_int64)]
+
+
 ROWS = {"past": 0, "seq": 1, "paged": 2}
 
 
@@ -122,6 +128,8 @@ SIGNATURES = {
     "slhip_graph_launch": (_I, [_P, _P]),
     "slhip_graph_destroy": (_I, [_P]),
     "slhip_rownorm": (_I, [_I, _I, _I, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P]),
+    "slhip_rownorm_copies": (_I, [_I, _I, _I, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F,
+                                  ctypes.POINTER(NormCopies), _P]),
     "slhip_gated_act": (_I, [_I, _I, _I, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P]),
     "slhip_rope": (_I, [_I, _I, ctypes.POINTER(RopeTensor), _I, _P, _P, _I64, _I64, ctypes.POINTER(RopeCfg), _P]),
     "slhip_gather": (_I, [_I, _P, _I64, _I64, _P, _I64, _I, _P, _I64, _P]),
@@ -334,11 +342,20 @@ class Graph:
 # ---- ops (device pointers in, nothing synchronous) -------------------------------------------------
 
 def rownorm(kind, dtype_in, dtype_out, x, y, rows, D, *, res=None, w=None, b=None, h_out=None, eps=1e-6,
-            x_stride=None, res_stride=None, y_stride=None, h_stride=None, stream=None):
-    call("slhip_rownorm", NORMS.get(kind, kind), DTYPES.get(dtype_in, dtype_in), DTYPES.get(dtype_out, dtype_out),
-         ptr(x), ptr(res), ptr(w), ptr(b), ptr(y), ptr(h_out), rows, D,
-         D if x_stride is None else x_stride, D if res_stride is None else res_stride,
-         D if y_stride is None else y_stride, D if h_stride is None else h_stride, eps, stream)
+            x_stride=None, res_stride=None, y_stride=None, h_stride=None, y16=None, y16_stride=None, yq=None,
+            yq_stride=None, stream=None):
+    """slhip_rownorm; with y16 (f16 rows) or yq (E4M3 rows: D codes then D/128 f32 scales) it calls
+    slhip_rownorm_copies, and y may then be None."""
+    args = (NORMS.get(kind, kind), DTYPES.get(dtype_in, dtype_in), DTYPES.get(dtype_out, dtype_out),
+            ptr(x), ptr(res), ptr(w), ptr(b), ptr(y), ptr(h_out), rows, D,
+            D if x_stride is None else x_stride, D if res_stride is None else res_stride,
+            D if y_stride is None else y_stride, D if h_stride is None else h_stride, eps)
+    if y16 is None and yq is None:
+        call("slhip_rownorm", *args, stream)
+        return
+    copies = NormCopies(ptr(y16), D if y16_stride is None else y16_stride, ptr(yq),
+                        D + D // 32 if yq_stride is None else yq_stride)
+    call("slhip_rownorm_copies", *args, ctypes.byref(copies), stream)
 
 
 def gated_act(act, dtype_in, dtype_out, gate, up, out, rows, cols, *, gate_stride=None, up_stride=None,

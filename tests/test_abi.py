@@ -45,6 +45,8 @@ int main(void) {
   printf("slhip_rope_tensor %zu\n", sizeof(slhip_rope_tensor));
   printf("slhip_rope_cfg %zu\n", sizeof(slhip_rope_cfg));
   printf("slhip_cache_rows %zu\n", sizeof(slhip_cache_rows));
+  printf("slhip_norm_copies %zu\n", sizeof(slhip_norm_copies));
+  P(slhip_norm_copies, y16_stride) P(slhip_norm_copies, yq) P(slhip_norm_copies, yq_stride)
   P(slhip_device_props, total_memory) P(slhip_device_props, l2_bytes) P(slhip_device_props, lds_bytes_per_block)
   P(slhip_rope_tensor, heads) P(slhip_rope_tensor, y_stride_h)
   P(slhip_rope_cfg, eps) P(slhip_rope_cfg, norm) P(slhip_rope_tensor, rows)
@@ -80,6 +82,9 @@ def test_struct_layouts_match_c():
     assert lay["slhip_rope_tensor.rows"] == native.RopeTensor.rows.offset
     for f in ("ctx", "n_past", "seq", "slots", "pages", "page_slots", "blocks_per_slot", "block_size"):
         assert lay[f"slhip_cache_rows.{f}"] == getattr(native.CacheRows, f).offset, f
+    assert lay["slhip_norm_copies"] == ctypes.sizeof(native.NormCopies)
+    for f in ("y16_stride", "yq", "yq_stride"):
+        assert lay[f"slhip_norm_copies.{f}"] == getattr(native.NormCopies, f).offset, f
 
 
 # ---- argument validation (returns before touching the device) ------------------------------------------
@@ -101,6 +106,20 @@ def test_rownorm_validation():
     with pytest.raises(native.SlhipNotSupported):
         native.rownorm("rms", "f16", "f32", FAKE, FAKE, 4, 8)
     native.rownorm("rms", "f32", "f32", None, None, 0, 8)  # empty: nothing to do, no pointers needed
+
+
+def test_rownorm_copies_validation():
+    with pytest.raises(native.SlhipArgumentError, match="y or a copy"):
+        native.call("slhip_rownorm_copies", 0, 0, 0, FAKE, None, None, None, None, None, 4, 128, 128, 128, 128, 128,
+                    1e-6, None, None)
+    with pytest.raises(native.SlhipArgumentError, match="multiple of 128"):
+        native.rownorm("rms", "f32", "f32", FAKE, None, 4, 96, yq=FAKE)
+    with pytest.raises(native.SlhipArgumentError, match=r"D \+ D/32 = 264"):
+        native.rownorm("rms", "bf16", "bf16", FAKE, None, 4, 256, yq=FAKE, yq_stride=260)
+    with pytest.raises(native.SlhipArgumentError, match="4-byte aligned"):
+        native.rownorm("rms", "bf16", "bf16", FAKE, None, 4, 256, yq=FAKE + 2)
+    with pytest.raises(native.SlhipArgumentError, match="stride"):
+        native.rownorm("rms", "f32", "f32", FAKE, None, 4, 128, y16=FAKE, y16_stride=64)
 
 
 def test_gated_validation():
