@@ -125,6 +125,32 @@ class C2(Workload):
                        w=self.w.slot(0), h_out=self.h.slot(i), eps=self.eps, stream=stream)
 
 
+class C2Copy(Workload):
+    """C2's Add+RmsNorm at a prefill size where every reader of the norm is a GEMM taking an activation copy:
+    the residual stream h (bf16) and the copy are written, the bf16 y is not (GraphLowerer.Elementwise.cs:
+    184-200). copy "e4m3": the fp8 GEMM's rows, 4096 codes + 32 f32 scales per row; "f16": f16 rows."""
+
+    def __init__(self, copy, rows=8192, D=4096):
+        c = synth.c2(rows=rows, D=D)
+        self.copy = copy
+        self.name = f"c2_add_rmsnorm_{copy}_copy_bf16"
+        self.desc = f"x + res -> h (bf16), RmsNorm -> {copy} copy only, [{rows}, {D}] bf16 in"
+        self.rows, self.D = rows, D
+        self.eps = c["eps"]
+        nb = c["x"].nbytes
+        self.qrow = D + D // 32 if copy == "e4m3" else 2 * D
+        self.bytes_per_step = 3 * nb + rows * self.qrow + c["w"].nbytes
+        R = copies_for(self.bytes_per_step)
+        self.x, self.r, self.h = Rot(c["x"], nb, R), Rot(c["res"], nb, R), Rot(None, nb, R)
+        self.q = Rot(None, rows * self.qrow, R)
+        self.w = Rot(c["w"], c["w"].nbytes, 1)
+
+    def launch(self, i, stream):
+        kw = dict(yq=self.q.slot(i)) if self.copy == "e4m3" else dict(y16=self.q.slot(i))
+        native.rownorm("rms", "bf16", "bf16", self.x.slot(i), None, self.rows, self.D, res=self.r.slot(i),
+                       w=self.w.slot(0), h_out=self.h.slot(i), eps=self.eps, stream=stream, **kw)
+
+
 class C3(Workload):
     def __init__(self, act):
         self.name = "c3_swiglu_bf16" if act == "silu" else "c3_geglu_bf16"
@@ -294,6 +320,8 @@ class SameBytesCopy(Workload):
 WORKLOADS = {
     "c1_rmsnorm_f32": lambda: C1(),
     "c2_add_rmsnorm_bf16": lambda: C2(),
+    "c2_add_rmsnorm_e4m3_copy_bf16": lambda: C2Copy("e4m3"),
+    "c2_add_rmsnorm_f16_copy_bf16": lambda: C2Copy("f16"),
     "c3_swiglu_bf16": lambda: C3("silu"),
     "c3_geglu_bf16": lambda: C3("gelu_tanh"),
     "c4_qknorm_rope_bf16": lambda: C4(),
@@ -400,6 +428,28 @@ def cpu_baselines(budget_main: float, budget_op: float, which: set[str]) -> dict
             L.orc_rmsnorm_mt(P(h), P(c["w"]), P(y), 8192, 4096, c["eps"], 0)
         s, reps = cpu_time(run, budget_main)
         res["c2_add_rmsnorm_bf16"] = dict(s=s, reps=reps, sample="full [8192,4096] shape, Add then RmsNorm in f32")
+    for copy in ("e4m3", "f16"):
+        name = f"c2_add_rmsnorm_{copy}_copy_bf16"
+        if name not in which:
+            continue
+        rows = 2048
+        c = synth.c2(rows=rows)
+        x, r = oracle.from_bf16(c["x"]), oracle.from_bf16(c["res"])
+        h, y = np.empty_like(x), np.empty_like(x)
+        q = np.empty((rows, 4096 + 128 if copy == "e4m3" else 4096), np.uint8 if copy == "e4m3" else np.uint16)
+        L, P = oracle.lib(), oracle._p
+        n = x.size
+
+        def run(copy=copy):
+            L.orc_add_mt(P(x), P(r), P(h), n)
+            L.orc_rmsnorm_mt(P(h), P(c["w"]), P(y), rows, 4096, c["eps"], 0)
+            if copy == "e4m3":
+                L.orc_quantize_fp8_rows_mt(P(y), rows, 4096, P(q))
+            else:
+                L.orc_f32_to_f16_mt(P(y), P(q), n)
+        s, reps = cpu_time(run, budget_op)
+        res[name] = dict(s=s * 8192 / rows, reps=reps,
+                         sample=f"{rows} of 8192 rows, scaled x{8192 // rows}; Add, RmsNorm, then the {copy} rows")
     if "c1_rmsnorm_f32" in which:
         c = synth.c1()
         y = np.empty_like(c["x"])

@@ -85,6 +85,8 @@ def _declare(L):
         "orc_cache_write_mt": (None, [_I, _P, _I64, _P, _I64, _P]),
         "orc_e4m3_code": (ctypes.c_uint8, [_F]),
         "orc_quantize_fp8_rows": (None, [_P, _I64, _I64, _P]),
+        "orc_quantize_fp8_rows_mt": (None, [_P, _I64, _I64, _P]),
+        "orc_f32_to_f16_mt": (None, [_P, _P, _I64]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

@@ -853,3 +853,49 @@ void orc_quantize_fp8_rows(const float* x, int64_t rows, int64_t K, uint8_t* out
 {
     for (int64_t r = 0; r < rows; r++) orc_quantize_fp8_row(x + r * K, K, out + r * (K + K / 32));
 }
+
+typedef struct {
+    const float* x;
+    uint8_t* out;
+    int64_t rows, K, per;
+} fp8_ctx;
+
+static void fp8_chunk(void* v, int64_t c)
+{
+    fp8_ctx* k = (fp8_ctx*)v;
+    int64_t s = c * k->per, e = s + k->per < k->rows ? s + k->per : k->rows;
+    if (s < e) orc_quantize_fp8_rows(k->x + s * k->K, e - s, k->K, k->out + s * (k->K + k->K / 32));
+}
+
+/* Row-chunked over the host threads, as the reference's CPU ops split rows (RowOp.cs chunking); only the
+ * timing of the CPU baseline uses it. */
+void orc_quantize_fp8_rows_mt(const float* x, int64_t rows, int64_t K, uint8_t* out)
+{
+    if (rows == 0) return;
+    int64_t ch = chunks_for(rows * K, 16384);
+    if (ch > rows) ch = rows;
+    fp8_ctx k = {x, out, rows, K, (rows + ch - 1) / ch};
+    parallel_for(ch, fp8_chunk, &k);
+}
+
+typedef struct {
+    const float* x;
+    uint16_t* y;
+    int64_t n, per;
+} f16_ctx;
+
+static void f16_chunk(void* v, int64_t c)
+{
+    f16_ctx* k = (f16_ctx*)v;
+    int64_t s = c * k->per, e = s + k->per < k->n ? s + k->per : k->n;
+    if (s < e) orc_f32_to_f16_n(k->x + s, k->y + s, e - s);
+}
+
+/* orc_f32_to_f16_n split over the host threads (the CPU baseline's timing only). */
+void orc_f32_to_f16_mt(const float* x, uint16_t* y, int64_t n)
+{
+    if (n == 0) return;
+    int64_t ch = chunks_for(n, 16384);
+    f16_ctx k = {x, y, n, (n + ch - 1) / ch};
+    parallel_for(ch, f16_chunk, &k);
+}

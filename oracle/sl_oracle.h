@@ -73,6 +73,8 @@ void orc_cache_write(int cache_type, void* cache, int64_t inner, const float* x,
 uint8_t orc_e4m3_code(float v);
 /* rows of K values (K % 128 == 0) -> rows of K + K/32 bytes: K codes, then K/128 f32 scales */
 void orc_quantize_fp8_rows(const float* x, int64_t rows, int64_t K, uint8_t* out);
+void orc_quantize_fp8_rows_mt(const float* x, int64_t rows, int64_t K, uint8_t* out);
+void orc_f32_to_f16_mt(const float* x, uint16_t* y, int64_t n);
 
 /* ---- threaded variants for the CPU baseline (CpuParallel.cs:34-78) ---- */
 void orc_set_threads(int threads);

@@ -16,6 +16,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libsharplight_hip.so")
+# GPU check programs of the test suite (sources under tests/, binaries beside them under tests/_bin/)
+TESTS = os.path.join(os.path.dirname(HERE), "tests")
+CHECKS = ["e4m3_exhaustive"]
 ARCH = os.environ.get("SLHIP_ARCH", "gfx950")
 
 # Packed-f32 VALU forms are disabled: hipcc -O3 would otherwise form them from plain float code.
@@ -50,6 +53,13 @@ def build(verbose: bool = False) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, LIB)
+    os.makedirs(os.path.join(TESTS, "_bin"), exist_ok=True)
+    for name in CHECKS:
+        exe = os.path.join(TESTS, "_bin", name)
+        r = subprocess.run([hipcc(), *[f for f in CFLAGS if f not in ("-fPIC", "-fvisibility=hidden")], "-o", exe,
+                            os.path.join(TESTS, name + ".hip")], capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"hipcc failed on tests/{name}.hip:\n{r.stdout}\n{r.stderr}")
     if verbose:
         print(f"built {LIB} from {len(sources)} sources")
     return LIB

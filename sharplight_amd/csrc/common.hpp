@@ -237,28 +237,93 @@ template <int W> __device__ __forceinline__ float group_max(float v)
     return v;
 }
 
+// Max over groups of W (2..32) consecutive lanes with DPP lane moves (no LDS round trip): swaps within
+// quads, then the mirror of each 8 and of each 16 lanes -- each step combines two disjoint halves, so
+// every lane ends with the group's max -- and one exchange across 16 lanes for W = 32.
+template <int CTRL> __device__ __forceinline__ float dpp_max_step(float v)
+{
+    return fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false)));
+}
+
+template <int W> __device__ __forceinline__ float group_max_dpp(float v)
+{
+    static_assert(W >= 2 && W <= 32 && (W & (W - 1)) == 0, "group of 2..32 lanes");
+    v = dpp_max_step<0xB1>(v);                       // quad_perm [1,0,3,2]
+    if constexpr (W >= 4) v = dpp_max_step<0x4E>(v);  // quad_perm [2,3,0,1]
+    if constexpr (W >= 8) v = dpp_max_step<0x141>(v);  // row_half_mirror
+    if constexpr (W >= 16) v = dpp_max_step<0x140>(v);  // row_mirror
+    if constexpr (W >= 32) v = fmaxf(v, __shfl_xor(v, 16, 64));
+    return v;
+}
+
+// Max over groups of W (2..32) consecutive lanes of non-negative, non-NaN floats, with DPP lane moves
+// (no LDS round trip): swaps within quads, then the mirror of each 8 and of each 16 lanes -- each step
+// combines two disjoint halves, so every lane ends with the group's max -- and one exchange across 16
+// lanes for W = 32. For such values the order of the bit patterns as unsigned integers is the order of
+// the values, so the steps are integer maxima (a float max would first quiet possible signalling NaNs).
+template <int CTRL> __device__ __forceinline__ uint32_t dpp_umax_step(uint32_t v)
+{
+    return max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xF, 0xF, false)));
+}
+
+template <int W> __device__ __forceinline__ float group_max_nonneg(float x)
+{
+    static_assert(W >= 2 && W <= 32 && (W & (W - 1)) == 0, "group of 2..32 lanes");
+    uint32_t v = __float_as_uint(x);
+    v = dpp_umax_step<0xB1>(v);                       // quad_perm [1,0,3,2]
+    if constexpr (W >= 4) v = dpp_umax_step<0x4E>(v);  // quad_perm [2,3,0,1]
+    if constexpr (W >= 8) v = dpp_umax_step<0x141>(v);  // row_half_mirror
+    if constexpr (W >= 16) v = dpp_umax_step<0x140>(v);  // row_mirror
+    if constexpr (W >= 32) v = max(v, static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), 16, 64)));
+    return __uint_as_float(v);
+}
+
 // ---- device side: E4M3 activation rows -------------------------------------------------------------
 
-// E4M3 code of v (|v| <= 448 expected) with the reference's rule (e4m3_code,
-// src/Sharplight.Shaders/Kernels/e4m3.slang:5-23): below 2^-6 the nearest multiple of 2^-9 (ties to
-// even), else round the f32 bits to 3 mantissa bits (ties to even) and rebias, saturating at code 0x7E
-// (448); the sign bit only for v < 0. Integer arithmetic, so every input -- NaN and infinities included --
-// gets the reference's code, which the hardware fp8 conversion would not (it yields 0x7F for NaN).
-__device__ __forceinline__ uint32_t e4m3_code(float v)
+// E4M3 codes with the reference's rule (e4m3_code, src/Sharplight.Shaders/Kernels/e4m3.slang:5-23): round
+// to nearest even on the E4M3 grid (multiples of 2^-9 below 2^-6), saturate at code 0x7E (448), and set
+// the sign bit only for v < 0 -- so -0 gives code 0x00, NaN 0x7E and +-inf 0x7E / 0xFE. gfx950's
+// v_cvt_pk_fp8_f32 (OCP E4M3, round to nearest even) returns these codes for every finite |v| <= 448
+// except -0. So the value is formed as fma(v, id, +0) -- v * id rounded once, with -0 turned into +0 --
+// and clamped to [-448, 448] (fminf first: it returns 448 for NaN). Over all 2^32 f32 inputs this equals
+// the integer rule bit for bit (tests/e4m3_exhaustive.hip).
+__device__ __forceinline__ float e4m3_operand(float v, float id)
 {
-    const float a = fabsf(v);
-    const uint32_t sub = static_cast<uint32_t>(__builtin_rintf(a * 512.0f));
-    uint32_t bits = __float_as_uint(a);
-    bits += 0x7FFFFu + ((bits >> 20) & 1u);
-    const uint32_t nrm = min((bits >> 20) - (120u << 3), 0x7Eu);
-    return (v < 0.0f ? 0x80u : 0u) | (a < 0.015625f ? sub : nrm);
+    return fmaxf(fminf(fmaf(v, id, 0.0f), 448.0f), -448.0f);
 }
 
 // The 4 codes of v[0..3] * id, packed little-endian (e4m3_pack4, e4m3.slang:33-38).
 __device__ __forceinline__ uint32_t e4m3_pack4(const float* v, float id)
 {
-    return e4m3_code(v[0] * id) | (e4m3_code(v[1] * id) << 8) | (e4m3_code(v[2] * id) << 16) |
-           (e4m3_code(v[3] * id) << 24);
+    int r = __builtin_amdgcn_cvt_pk_fp8_f32(e4m3_operand(v[0], id), e4m3_operand(v[1], id), 0, false);
+    r = __builtin_amdgcn_cvt_pk_fp8_f32(e4m3_operand(v[2], id), e4m3_operand(v[3], id), r, true);
+    return static_cast<uint32_t>(r);
+}
+
+__device__ __forceinline__ uint32_t e4m3_code(float v)
+{
+    return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(e4m3_operand(v, 1.0f), 0.0f, 0, false)) & 0xFFu;
+}
+
+// The group scale of quantize_fp8 from the group's amax m (>= 0, not NaN): d = m / 448 and
+// id = d > 0 ? 1 / d : 0 (e4m3_group_scale / e4m3_pack4, e4m3.slang:25-38), both correctly rounded. For
+// m = 0 and m in [2^-116, FLT_MAX] -- every amax of real activations -- a product with the rounded
+// reciprocal of 448 corrected by one fma gives d exactly, and the hardware reciprocal of d corrected by
+// one Newton step gives 1/d exactly (the division's results are normal there); elsewhere the lanes take
+// IEEE division. Checked against IEEE division for every non-negative f32 m (tests/e4m3_exhaustive.hip).
+__device__ __forceinline__ void e4m3_group_scale(float m, float& d, float& id)
+{
+    constexpr float kInv448 = 1.0f / 448.0f;
+    const float q = m * kInv448;
+    d = fmaf(fmaf(-q, 448.0f, m), kInv448, q);
+    const float y = __builtin_amdgcn_rcpf(d);
+    const float r = fmaf(fmaf(-d, y, 1.0f), y, y);
+    id = d > 0.0f ? r : 0.0f;
+    const uint32_t u = __float_as_uint(m);  // [2^-116, FLT_MAX] as bit patterns: [0x05800000, 0x7F7FFFFF]
+    if (u - 0x05800000u > 0x7F7FFFFFu - 0x05800000u && u != 0) {
+        d = m / 448.0f;
+        id = d > 0.0f ? 1.0f / d : 0.0f;
+    }
 }
 
 // ---- device side: errors raised by kernels -----------------------------------------------------------

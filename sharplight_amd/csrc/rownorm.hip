@@ -201,9 +201,9 @@ __global__ __launch_bounds__(1024) void rownorm_vec(RowNormArgs a, int wpr)
             float m = 0.0f;
 #pragma unroll
             for (int e = 0; e < E; e++) m = fmaxf(m, fabsf(o[e]));
-            m = group_max<G>(m);
-            const float d = m / 448.0f;
-            const float id = d > 0.0f ? 1.0f / d : 0.0f;
+            m = group_max_nonneg<G>(m);  // m is not NaN: the first fmaxf with 0 drops quiet NaNs
+            float d, id;
+            e4m3_group_scale(m, d, id);
             char* qp = qr + static_cast<int64_t>(jv[k]) * E;
             if constexpr (E == 8)
                 store_nt(qp, make_uint2(e4m3_pack4(o, id), e4m3_pack4(o + 4, id)));
@@ -282,7 +282,7 @@ __global__ __launch_bounds__(256) void rownorm_scalar(RowNormArgs a)
             const int64_t i0 = g * 128 + lane, i1 = i0 + 64;
             const float o0 = normed(value(i0), i0), o1 = normed(value(i1), i1);
             const float d = group_max<64>(fmaxf(fabsf(o0), fabsf(o1))) / 448.0f;
-            const float id = d > 0.0f ? 1.0f / d : 0.0f;
+            const float id = d > 0.0f ? 1.0f / d : 0.0f;  // the division itself: this path is not hot
             qr[i0] = static_cast<char>(e4m3_code(o0 * id));
             qr[i1] = static_cast<char>(e4m3_code(o1 * id));
             if (lane == 0) *reinterpret_cast<float*>(qr + D + g * 4) = d;

@@ -9,6 +9,8 @@ case also runs with f32 y: the oracle's f16 conversion and quantize_fp8 applied 
 copies bit for bit, and the copies must not depend on y's dtype or on whether y is written at all. The
 norm values themselves are held to the f32 tolerance against the oracle, and the E4M3 rows decode to
 within E4M3's half step of them."""
+import os
+import subprocess
 import zlib
 
 import numpy as np
@@ -20,6 +22,8 @@ from tests.devutil import Dev, log
 from tests.parity import assert_bits_equal, assert_f32_close
 
 pytestmark = pytest.mark.gpu
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 NP = {"f32": np.float32, "bf16": np.uint16}
 
@@ -142,3 +146,57 @@ def test_zero_group_has_zero_scale_and_codes(device):
     assert (yq[:, :128] == 0).all()
     assert (yq[:, D:D + 4].copy().view(np.float32) == 0).all()
     assert_bits_equal(yq, oracle.quantize_fp8(y32), what="E4M3 rows")
+
+
+def _code_grid():
+    """Every positive E4M3 value, every midpoint between neighbours (the ties), each midpoint one f32 ulp
+    either side, and the edges of the subnormal range: all within [0, 448], so that 448 stays each group's
+    amax."""
+    vals = _e4m3_value(np.arange(0x7F)).astype(np.float32)  # codes 0..0x7E
+    mids = ((vals[:-1].astype(np.float64) + vals[1:]) / 2).astype(np.float32)
+    grid = np.concatenate([vals, mids, np.nextafter(mids, np.float32(0)), np.nextafter(mids, np.float32(1000)),
+                           np.float32([2.0 ** -10, 2.0 ** -11, 2.0 ** -20, 1e-30, 0.015625 * (1 - 2 ** -24),
+                                       0.015625, 447.99997, 440.0, 447.0])])
+    return grid[(grid >= 0) & (grid <= 448)]
+
+
+@pytest.mark.parametrize("din", ["f32", "bf16"])
+def test_e4m3_code_grid_through_the_norm(device, din):
+    """RmsNorm with eps 0 of rows of +-1 has scale exactly 1, so y = +-w exactly; with 448 in every group
+    the E4M3 scale is 1 and the codes are e4m3_code(+-w) themselves: each code value, each tie (to even),
+    each tie +-1 ulp, on both signs, and -0 (code 0x00, v < 0 being false)."""
+    grid = _code_grid()
+    per = 127
+    n_groups = -(-grid.size // per)
+    w = np.zeros((n_groups, 128), np.float32)
+    w[:, 0] = 448.0
+    w.reshape(-1)[np.arange(grid.size) // per * 128 + 1 + np.arange(grid.size) % per] = grid
+    w = w.reshape(-1)
+    D = w.size
+    rows = np.ones((2, D), np.float32)
+    rows[1] = -1.0
+    wz = w.copy()
+    wz[2] = -0.0  # row 0: +1 * -0 = -0
+    x = oracle.to_bf16(rows) if din == "bf16" else rows
+    y32, _, yq = _run("rms", din, "f32", x, None, wz, 0.0, y=True, y16=False, yq=True)
+    assert np.array_equal(y32, rows * wz)
+    assert (yq[:, D:].copy().view(np.float32) == 1.0).all()
+    want = np.array([[oracle.e4m3_code(float(v)) for v in r] for r in (rows * wz)], np.uint8)
+    assert_bits_equal(yq[:, :D], want, what="E4M3 codes of the grid")
+    assert yq[0, 2] == 0x00 and yq[1, 2] == 0x00  # -0 (row 0) and +0 (row 1: -1 * -0)
+    assert_bits_equal(yq, oracle.quantize_fp8(y32), what="E4M3 rows")
+
+
+def test_e4m3_conversion_exhaustive(device):
+    """The kernels' E4M3 conversion against the reference's integer rule on all 2^32 f32 inputs, and their
+    group scale (d = amax/448, 1/d) against IEEE division for every non-negative amax (a check program
+    built beside the library: tests/e4m3_exhaustive.hip)."""
+    exe = os.path.join(ROOT, "tests", "_bin", "e4m3_exhaustive")
+    assert os.path.exists(exe), "tests/_bin/e4m3_exhaustive is not built: run the package build"
+    log("e4m3 exhaustive check program")
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=100)
+    out = r.stdout.split()
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert out[0] == "checked" and int(out[1]) == 1 << 32 and int(out[3]) == 0, r.stdout
+    assert int(out[7]) > 0, "the bare conversion must differ somewhere (-0, NaN, inf): the checker compared nothing"
+    assert out[8] == "scale_checked" and int(out[9]) == 0x7F800001 and int(out[11]) == 0, r.stdout

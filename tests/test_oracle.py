@@ -467,3 +467,17 @@ def test_quantize_fp8_rows():
             inv = np.float32(1) / d[g] if d[g] > 0 else np.float32(0)
             assert np.array_equal(q[r, 128 * g:128 * (g + 1)], _e4m3_nearest(v * inv))
     assert not q[1, 128:256].any() and q[1, 512 + 4:512 + 8].view(np.float32)[0] == 0
+
+
+def test_quantize_fp8_rows_threaded_matches():
+    x = np.random.default_rng(10).standard_normal((300, 1024)).astype(np.float32)
+    out = np.empty((300, 1024 + 32), np.uint8)
+    oracle.lib().orc_quantize_fp8_rows_mt(oracle._p(x), 300, 1024, oracle._p(out))
+    assert np.array_equal(out, oracle.quantize_fp8(x))
+
+
+def test_f16_threaded_matches():
+    x = np.random.default_rng(11).standard_normal(300_001).astype(np.float32)
+    y = np.empty(x.size, np.uint16)
+    oracle.lib().orc_f32_to_f16_mt(oracle._p(x), oracle._p(y), x.size)
+    assert np.array_equal(y, oracle.to_f16(x))
