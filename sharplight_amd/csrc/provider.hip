@@ -17,7 +17,10 @@
 //   * RmsNorm with an f32 [D] weight whose only consumer is a Rope -> computed inside the rope launch
 //     (AbsorbIntoConsumers, :618-630); Rope launches that share positions and settings (q and k of a
 //     layer) are merged into one launch of up to four tensors;
-//   * RmsNorm, L2Norm, LayerNorm, Rope, Gather and Cast on their own.
+//   * a Rope whose only consumer is a CacheWrite -> the rope stores into the cache rows (:633-648);
+//   * a Cast to f16 of a row norm's f32 output -> the f16 copy written by the norm launch, which then skips
+//     the f32 rows when nothing else reads them (GraphLowerer.HalfCopies.cs:106-151);
+//   * RmsNorm, L2Norm, LayerNorm, Rope, Gather, Cast and CacheWrite on their own.
 // An Add, Mul or activation that fits none of these patterns is not supported on this provider.
 //
 // The graph reaches the C ABI as a small line-based text form (one value, node, input, weight or output
@@ -335,6 +338,8 @@ struct Unit {
     // RowNorm
     int norm = SLHIP_NORM_RMS;
     int x = -1, res = -1, w = -1, b = -1, y = -1, h = -1;
+    int y16 = -1;         // f16 copy of y (an absorbed Cast), or -1
+    bool skip_y = false;  // y itself is read by nothing else: only the copy is written
     float eps = 0.f;
     // Gated
     int act = SLHIP_ACT_SILU, gate = -1, up = -1;
@@ -484,8 +489,9 @@ private:
                     if (g_.value(n.in[0]).type != g_.value(n.out[0]).type ||
                         g_.value(n.in[1]).type != g_.value(n.out[0]).type)
                         unsupported("Add+" + m.op + ": the residual stream must keep one type");
-                    units_.push_back(u);
                     done[k] = done[k + 1] = true;
+                    attach_half_copy(u, cons, done);
+                    units_.push_back(u);
                     continue;
                 }
             }
@@ -517,7 +523,9 @@ private:
             }
             done[k] = true;
             if (n.op == "RmsNorm" || n.op == "L2Norm" || n.op == "LayerNorm") {
-                units_.push_back(rownorm_unit(n));
+                Unit u = rownorm_unit(n);
+                attach_half_copy(u, cons, done);
+                units_.push_back(u);
             } else if (n.op == "Rope") {
                 Unit u = rope_unit(static_cast<int>(k));
                 // A rope whose only consumer is a cache write stores into the cache
@@ -567,6 +575,25 @@ private:
     }
 
     std::map<int, int> absorbed_norm_;  // rope node -> RmsNorm node computed inside it
+
+    // A Cast of an f32 norm output to f16 is the f16 copy the norm writes beside its rows: the norm's f32
+    // values rounded once, as the reference's row norm writes the half copy its GEMM readers take
+    // (GraphLowerer.HalfCopies.cs:106-151, RowNormKernelSource.cs:45-49). The f32 rows are then written only
+    // when something else reads them (GraphLowerer.Elementwise.cs:184-200).
+    void attach_half_copy(Unit& u, std::map<int, std::vector<int>>& cons, std::vector<bool>& done)
+    {
+        const Value& yv = g_.value(u.y);
+        if (yv.type != DType::F32) return;  // a bf16 y rounded again to f16 would differ from the copy
+        for (int c : cons[u.y]) {
+            const Node& m = g_.nodes[c];
+            if (m.op != "Cast" || done[c] || g_.value(m.out[0]).type != DType::F16) continue;
+            u.y16 = m.out[0];
+            done[c] = true;
+            u.skip_y = !yv.output && cons[u.y].size() == 1;
+            u.label += u.skip_y ? "+f16copy(no f32 rows)" : "+f16copy";
+            return;
+        }
+    }
 
     Unit rope_unit(int k)
     {
@@ -692,9 +719,11 @@ private:
             const Value& x = g_.value(u.x);
             const Value& y = g_.value(u.y);
             const int64_t D = x.last(), rows = x.rows(T);
-            check(slhip_rownorm(u.norm, act_code(x.type), act_code(y.type), ptr(u.x), ptr(u.res),
-                                static_cast<const float*>(ptr(u.w)), static_cast<const float*>(ptr(u.b)), ptr(u.y),
-                                ptr(u.h), rows, D, D, D, D, D, u.eps, stream_));
+            const slhip_norm_copies copies{ptr(u.y16), D, nullptr, 0};
+            check(slhip_rownorm_copies(u.norm, act_code(x.type), act_code(y.type), ptr(u.x), ptr(u.res),
+                                       static_cast<const float*>(ptr(u.w)), static_cast<const float*>(ptr(u.b)),
+                                       u.skip_y ? nullptr : ptr(u.y), ptr(u.h), rows, D, D, D, D, D, u.eps,
+                                       u.y16 >= 0 ? &copies : nullptr, stream_));
             break;
         }
         case Unit::Gated: {

@@ -75,6 +75,48 @@ def test_residual_add_rmsnorm_fuses(dev, h_is_output):
             assert_bf16_close(seg.get_output(h), href, ulp=0, what="h")
 
 
+@pytest.mark.parametrize("y_is_output", [True, False])
+def test_norm_writes_the_f16_copy(dev, y_is_output):
+    """NormHalfCopyTests (tests/Sharplight.Vulkan.Tests/NormHalfCopyTests.cs): a Cast to f16 of an f32 norm
+    output is the norm's own f16 copy -- one launch, the f32 values rounded once -- and the f32 rows are
+    written only when read."""
+    T, D = 40, 1024
+    g = GraphBuilder()
+    x = g.input("f32", "T", D)
+    r = g.input("f32", "T", D)
+    w = g.weight("f32", D)
+    y = g.rms_norm(g.add(x, r), w, eps=1e-6)
+    if y_is_output:
+        g.output(y)
+    y16 = g.output(g.cast(y, "f16"))
+    xs, rs = synth.normal(4, 0, (T, D)), synth.normal(4, 1, (T, D))
+    ws = synth.normal(4, 2, (D,), 1.0, 0.1)
+    with dev.compile(g, max_tokens=64) as seg:
+        assert seg.launches == ["fused[Add]+RmsNorm+f16copy" + ("" if y_is_output else "(no f32 rows)")]
+        seg.set_input(x, xs)
+        seg.set_input(r, rs)
+        seg.set_input(w, ws)
+        log(f"provider norm f16 copy y_out={y_is_output}")
+        seg.execute(T)
+        yref = oracle.rmsnorm(oracle.add(xs, rs), ws, 1e-6)
+        got16 = seg.get_output(y16)
+        assert_f16_close(got16.view(np.uint16), oracle.to_f16(yref), what="f16 copy")
+        if y_is_output:
+            y32 = seg.get_output(y)
+            assert_f32_close(y32, yref, what="y")
+            assert_bits_equal(got16.view(np.uint16), oracle.to_f16(y32), what="copy of y")
+
+
+def test_cast_of_a_bf16_norm_stays_separate(dev):
+    """The copy is the f32 value rounded once; a bf16 norm output cast to f16 is rounded twice, so it is not
+    absorbed."""
+    g = GraphBuilder()
+    x = g.input("bf16", "T", 256)
+    g.output(g.cast(g.rms_norm(x, None, out_type="bf16"), "f16"))
+    with dev.compile(g, max_tokens=8) as seg:
+        assert seg.launches == ["RmsNorm", "Cast"]
+
+
 @pytest.mark.parametrize("act,op", [("silu", "Silu"), ("gelu_tanh", "GeluTanh"), ("gelu_erf", "Gelu")])
 def test_gated_mlp_fuses(dev, act, op):
     """IMlpActivation.ActivateGated: Mul(act(gate), up) is one launch (FusionTests.cs:59-67's epilogue)."""
