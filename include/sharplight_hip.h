@@ -195,6 +195,25 @@ SLHIP_API int slhip_rownorm_copies(int kind, int dtype_in, int dtype_out, const 
                                    float eps, const slhip_norm_copies* copies, slhip_stream stream);
 
 /*
+ * Decode matvec y = x . W^T and the dual gate/up matvec y = act(x . Wg^T) * (x . Wu^T) for few activation
+ * rows (the decode FFN's gate/up projections with the gating epilogue).
+ *   x: [T, K] f32 or bf16 (dtype_x), row stride x_stride elements (a multiple of 4), 16-byte aligned rows;
+ *   W, Wg, Wu: N dense rows of K weights in `fmt` (F32, F16 or BF16; K a multiple of 8, or of 4 for F32),
+ *   16-byte aligned; y: [T, N] f32 or bf16 (dtype_y), row stride y_stride elements.
+ *   act: SLHIP_ACT_SILU / GELU_TANH / GELU_ERF, the same forms as slhip_gated_act.
+ * Products and sums in f32 (in another order than the CPU provider's, so equal to it within the rounding of
+ * a K-term f32 dot product); K <= 16384.
+ * Replaces: MatMulOp's float-row path (src/Sharplight.Cpu/MatMulOp.cs:376-465) followed by the activation and
+ * Mul, i.e. the reference's dual matvec unit (FoldDualMatMuls, src/Sharplight.Shaders/Lowering/
+ * GraphLowerer.Fusion.cs:286-353; tests/Sharplight.Vulkan.Tests/FusionTests.cs:59-80).
+ */
+SLHIP_API int slhip_matvec(int fmt, int dtype_x, int dtype_y, const void* x, int64_t x_stride, int64_t T, int64_t K,
+                           const void* w, int64_t N, void* y, int64_t y_stride, slhip_stream stream);
+SLHIP_API int slhip_dual_matvec(int act, int fmt, int dtype_x, int dtype_y, const void* x, int64_t x_stride, int64_t T,
+                                int64_t K, const void* w_gate, const void* w_up, int64_t N, void* y, int64_t y_stride,
+                                slhip_stream stream);
+
+/*
  * Gated activation out = act(gate) * up over [rows, cols] (IMlpActivation.ActivateGated,
  * src/Sharplight.Core/Architectures/IMlpActivation.cs:12; CPU: UnaryOp then BinaryOp Mul,
  * src/Sharplight.Cpu/ScalarMath.cs:552-641, BinaryOp.cs:8-103; Vulkan: the fused[Silu,Mul]

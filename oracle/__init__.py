@@ -87,6 +87,8 @@ def _declare(L):
         "orc_quantize_fp8_rows": (None, [_P, _I64, _I64, _P]),
         "orc_quantize_fp8_rows_mt": (None, [_P, _I64, _I64, _P]),
         "orc_f32_to_f16_mt": (None, [_P, _P, _I64]),
+        "orc_matvec": (ctypes.c_int, [ctypes.c_int, _P, _I64, _I64, _P, _I64, _P]),
+        "orc_matvec_mt": (ctypes.c_int, [ctypes.c_int, _P, _I64, _I64, _P, _I64, _P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -329,3 +331,24 @@ def quantize_fp8(x):
     out = np.empty((rows, K + K // 32), np.uint8)
     lib().orc_quantize_fp8_rows(_p(x), rows, K, _p(out))
     return out.reshape(x.shape[:-1] + (K + K // 32,))
+
+
+def matvec(fmt, w_raw, N, K, x, threads=None):
+    """MatMulOp's float-row path: y [T, N] f32 = x [T, K] f32 . W^T, W = N rows of the raw ``fmt`` bytes."""
+    x = _c(np.atleast_2d(x), np.float32)
+    w_raw = np.ascontiguousarray(w_raw).view(np.uint8)
+    T = x.shape[0]
+    y = np.empty((T, N), np.float32)
+    fn = lib().orc_matvec_mt if threads else lib().orc_matvec
+    if fn(FORMATS[fmt], _p(w_raw), N, K, _p(x), T, _p(y)):
+        raise ValueError(f"matvec: bad format/size {fmt} K={K}")
+    return y
+
+
+def dual_matvec(act, fmt, wg_raw, wu_raw, N, K, x, dtype="f32"):
+    """The unfused decode FFN the dual matvec replaces: act(x . Wg^T) * (x . Wu^T) as MatMul, MatMul, the
+    activation (UnaryOp) and Mul (BinaryOp), all f32; ``dtype`` "bf16" rounds the result."""
+    g = matvec(fmt, wg_raw, N, K, x)
+    u = matvec(fmt, wu_raw, N, K, x)
+    y = mul(unary(act, g), u)
+    return to_bf16(y) if dtype == "bf16" else y

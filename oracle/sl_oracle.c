@@ -899,3 +899,184 @@ void orc_f32_to_f16_mt(const float* x, uint16_t* y, int64_t n)
     f16_ctx k = {x, y, n, (n + ch - 1) / ch};
     parallel_for(ch, f16_chunk, &k);
 }
+
+/* ------------------------------------------------------------------------------------------ */
+/* Matvec: y = x . W^T for few activation rows (decode)                                       */
+/* ------------------------------------------------------------------------------------------ */
+
+/* Vector512.Sum: the runtime's horizontal add; restated as pairwise halving (lane i + lane i+8, then
+ * +4, +2, +1). The order of the runtime's reduction is not in the reference, so this level of rounding
+ * is parity unpinned; the matvec pins hold the results to the f64 dot within the f32 error bound. */
+static float sum16(const float* v)
+{
+    float s[16];
+    for (int i = 0; i < 16; i++) s[i] = v[i];
+    for (int w = 8; w > 0; w >>= 1)
+        for (int i = 0; i < w; i++) s[i] = s[i] + s[i + w];
+    return s[0];
+}
+
+/* Simd.Dot4 on the AVX-512 path (Simd.cs:91-133,161-175): two 16-lane accumulators (a over the first, b
+ * over the second half of each 32 elements, fma(w, x, acc)), a 16-element step into a, r = Sum(a + b),
+ * then a scalar tail r += w * x. */
+static void dot4(const float* x, const float* const* w, int64_t n, float* res)
+{
+    float a[4][16] = {{0}}, b[4][16] = {{0}};
+    int64_t i = 0;
+    for (; i + 32 <= n; i += 32)
+        for (int r = 0; r < 4; r++)
+            for (int l = 0; l < 16; l++) {
+                a[r][l] = fmaf(w[r][i + l], x[i + l], a[r][l]);
+                b[r][l] = fmaf(w[r][i + 16 + l], x[i + 16 + l], b[r][l]);
+            }
+    for (; i + 16 <= n; i += 16)
+        for (int r = 0; r < 4; r++)
+            for (int l = 0; l < 16; l++) a[r][l] = fmaf(w[r][i + l], x[i + l], a[r][l]);
+    for (int r = 0; r < 4; r++) {
+        float s[16];
+        for (int l = 0; l < 16; l++) s[l] = a[r][l] + b[r][l];
+        res[r] = sum16(s);
+    }
+    for (; i < n; i++)
+        for (int r = 0; r < 4; r++) res[r] = res[r] + w[r][i] * x[i];
+}
+
+/* Simd.Dot4x2 on the AVX-512 path (Simd.cs:176-270): one 16-lane accumulator per (token, row), then the
+ * scalar tail; res = [t0 r0..r3, t1 r0..r3]. */
+static void dot4x2(const float* x0, const float* x1, const float* const* w, int64_t n, float* res)
+{
+    float a[4][16] = {{0}}, c[4][16] = {{0}};
+    int64_t i = 0;
+    for (; i + 16 <= n; i += 16)
+        for (int r = 0; r < 4; r++)
+            for (int l = 0; l < 16; l++) {
+                a[r][l] = fmaf(w[r][i + l], x0[i + l], a[r][l]);
+                c[r][l] = fmaf(w[r][i + l], x1[i + l], c[r][l]);
+            }
+    for (int r = 0; r < 4; r++) {
+        res[r] = sum16(a[r]);
+        res[4 + r] = sum16(c[r]);
+    }
+    for (; i < n; i++)
+        for (int r = 0; r < 4; r++) {
+            res[r] = res[r] + w[r][i] * x0[i];
+            res[4 + r] = res[4 + r] + w[r][i] * x1[i];
+        }
+}
+
+/* Quant.DotQ8_0x4 / DotQ4_0x4 (Quant.cs:738-803), the fused one-row path for Q8_0 / Q4_0: per block and
+ * lane s = fma(q0, x0, q1 * x1) (Q4_0: fma(lo, x0, hi * x1) - 8 (x0 + x1)), acc = fma(s, d, acc); the
+ * rows' results are Sum(acc). */
+static float dot_fused_row(int fmt, const float* x, const uint8_t* row, int64_t nb)
+{
+    float acc[16] = {0};
+    for (int64_t b = 0; b < nb; b++) {
+        const float* x0 = x + b * 32;
+        const float* x1 = x0 + 16;
+        if (fmt == ORC_Q8_0) {
+            const uint8_t* p = row + b * 34;
+            const float d = rd_h(p);
+            for (int l = 0; l < 16; l++) {
+                const float s = fmaf((float)(int8_t)p[2 + l], x0[l], (float)(int8_t)p[18 + l] * x1[l]);
+                acc[l] = fmaf(s, d, acc[l]);
+            }
+        } else {
+            const uint8_t* p = row + b * 18;
+            const float d = rd_h(p);
+            for (int l = 0; l < 16; l++) {
+                const float x8 = (x0[l] + x1[l]) * 8.0f;
+                const float s = fmaf((float)(p[2 + l] & 15), x0[l], (float)(p[2 + l] >> 4) * x1[l]) - x8;
+                acc[l] = fmaf(s, d, acc[l]);
+            }
+        }
+    }
+    return sum16(acc);
+}
+
+/* MatMulOp's float-row path (MatMulOp.cs:376-465), as the CPU provider runs decode: rows of W in groups
+ * of four; with at most 4 activation rows and a fused kernel (Q8_0 / Q4_0) each row is one fused dot,
+ * otherwise K is walked in 1024-value chunks -- each chunk of the four rows dequantized (Quant.Dequantize)
+ * and dotted (Dot4x2 for pairs of rows when there are more than 4, Dot4 for the rest), the chunk results
+ * added into f32 accumulators. y is [T, N] f32; x is [T, K] f32; W is N rows of row_bytes(fmt, K). */
+static void matvec_groups(int fmt, const uint8_t* w, int64_t N, int64_t K, const float* x, int64_t T, float* y,
+                          int64_t g0, int64_t g1)
+{
+    const int64_t rb = orc_row_bytes(fmt, K);
+    const int fused = (fmt == ORC_Q8_0 || fmt == ORC_Q4_0) && T <= 4;
+    float* wbuf = (float*)malloc(4 * 1024 * sizeof(float));
+    float* acc = (float*)malloc((size_t)(T * 4 > 1 ? T * 4 : 1) * sizeof(float));
+    for (int64_t g = g0; g < g1; g++) {
+        const int64_t n0 = g * 4;
+        const int nr = N - n0 < 4 ? (int)(N - n0) : 4;
+        const uint8_t* rows[4];
+        for (int r = 0; r < 4; r++) rows[r] = w + (n0 + r < N ? n0 + r : N - 1) * rb;
+        if (fused) {
+            for (int64_t t = 0; t < T; t++)
+                for (int r = 0; r < nr; r++) y[t * N + n0 + r] = dot_fused_row(fmt, x + t * K, rows[r], K / 32);
+            continue;
+        }
+        for (int64_t i = 0; i < T * 4; i++) acc[i] = 0.0f;
+        for (int64_t kb = 0; kb < K; kb += 1024) {
+            const int64_t len = K - kb < 1024 ? K - kb : 1024;
+            const float* wp[4];
+            for (int r = 0; r < 4; r++) {
+                float* dst = wbuf + r * 1024;
+                const int64_t off = fmt == ORC_F32 ? kb * 4 : fmt == ORC_F16 || fmt == ORC_BF16 ? kb * 2
+                                                                     : kb / 32 * orc_row_bytes(fmt, 32);
+                orc_dequant(fmt, rows[r] + off, len, dst);
+                wp[r] = dst;
+            }
+            float res[8];
+            int64_t t = 0;
+            for (; T > 4 && t + 2 <= T; t += 2) {
+                dot4x2(x + t * K + kb, x + (t + 1) * K + kb, wp, len, res);
+                for (int r = 0; r < 4; r++) {
+                    acc[t * 4 + r] += res[r];
+                    acc[(t + 1) * 4 + r] += res[4 + r];
+                }
+            }
+            for (; t < T; t++) {
+                dot4(x + t * K + kb, wp, len, res);
+                for (int r = 0; r < 4; r++) acc[t * 4 + r] += res[r];
+            }
+        }
+        for (int64_t t = 0; t < T; t++)
+            for (int r = 0; r < nr; r++) y[t * N + n0 + r] = acc[t * 4 + r];
+    }
+    free(wbuf);
+    free(acc);
+}
+
+int orc_matvec(int fmt, const uint8_t* w, int64_t N, int64_t K, const float* x, int64_t T, float* y)
+{
+    if (orc_row_bytes(fmt, K) <= 0 || (fmt >= ORC_Q8_0 && K % 32)) return -1;
+    matvec_groups(fmt, w, N, K, x, T, y, 0, (N + 3) / 4);
+    return 0;
+}
+
+typedef struct {
+    int fmt;
+    const uint8_t* w;
+    int64_t N, K, T, groups, per;
+    const float* x;
+    float* y;
+} mv_ctx;
+
+static void mv_chunk(void* v, int64_t c)
+{
+    mv_ctx* k = (mv_ctx*)v;
+    int64_t g0 = c * k->per, g1 = g0 + k->per < k->groups ? g0 + k->per : k->groups;
+    if (g0 < g1) matvec_groups(k->fmt, k->w, k->N, k->K, k->x, k->T, k->y, g0, g1);
+}
+
+/* MatMulOp.Run's split (MatMulOp.cs:150-153): chunks = min(groups, threads * 8) over groups of 4 rows. */
+int orc_matvec_mt(int fmt, const uint8_t* w, int64_t N, int64_t K, const float* x, int64_t T, float* y)
+{
+    if (orc_row_bytes(fmt, K) <= 0 || (fmt >= ORC_Q8_0 && K % 32)) return -1;
+    const int64_t groups = (N + 3) / 4;
+    int64_t ch = groups < (int64_t)g_threads * 8 ? groups : (int64_t)g_threads * 8;
+    if (ch < 1) return 0;
+    mv_ctx k = {fmt, w, N, K, T, groups, (groups + ch - 1) / ch, x, y};
+    parallel_for(ch, mv_chunk, &k);
+    return 0;
+}

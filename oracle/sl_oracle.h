@@ -76,6 +76,10 @@ void orc_quantize_fp8_rows(const float* x, int64_t rows, int64_t K, uint8_t* out
 void orc_quantize_fp8_rows_mt(const float* x, int64_t rows, int64_t K, uint8_t* out);
 void orc_f32_to_f16_mt(const float* x, uint16_t* y, int64_t n);
 
+/* ---- Matvec y = x . W^T for few activation rows (MatMulOp's float-row path) ---- */
+int orc_matvec(int fmt, const uint8_t* w, int64_t N, int64_t K, const float* x, int64_t T, float* y);
+int orc_matvec_mt(int fmt, const uint8_t* w, int64_t N, int64_t K, const float* x, int64_t T, float* y);
+
 /* ---- threaded variants for the CPU baseline (CpuParallel.cs:34-78) ---- */
 void orc_set_threads(int threads);
 int orc_get_threads(void);

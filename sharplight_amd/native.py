@@ -130,6 +130,8 @@ SIGNATURES = {
     "slhip_rownorm": (_I, [_I, _I, _I, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P]),
     "slhip_rownorm_copies": (_I, [_I, _I, _I, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F,
                                   ctypes.POINTER(NormCopies), _P]),
+    "slhip_matvec": (_I, [_I, _I, _I, _P, _I64, _I64, _I64, _P, _I64, _P, _I64, _P]),
+    "slhip_dual_matvec": (_I, [_I, _I, _I, _I, _P, _I64, _I64, _I64, _P, _P, _I64, _P, _I64, _P]),
     "slhip_gated_act": (_I, [_I, _I, _I, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P]),
     "slhip_rope": (_I, [_I, _I, ctypes.POINTER(RopeTensor), _I, _P, _P, _I64, _I64, ctypes.POINTER(RopeCfg), _P]),
     "slhip_gather": (_I, [_I, _P, _I64, _I64, _P, _I64, _I, _P, _I64, _P]),
@@ -356,6 +358,20 @@ def rownorm(kind, dtype_in, dtype_out, x, y, rows, D, *, res=None, w=None, b=Non
     copies = NormCopies(ptr(y16), D if y16_stride is None else y16_stride, ptr(yq),
                         D + D // 32 if yq_stride is None else yq_stride)
     call("slhip_rownorm_copies", *args, ctypes.byref(copies), stream)
+
+
+def matvec(fmt, dtype_x, dtype_y, x, T, K, w, N, y, *, x_stride=None, y_stride=None, stream=None):
+    """y [T, N] = x [T, K] . W^T, W = N rows of K weights in ``fmt``."""
+    call("slhip_matvec", FORMATS.get(fmt, fmt), DTYPES.get(dtype_x, dtype_x), DTYPES.get(dtype_y, dtype_y), ptr(x),
+         K if x_stride is None else x_stride, T, K, ptr(w), N, ptr(y), N if y_stride is None else y_stride, stream)
+
+
+def dual_matvec(act, fmt, dtype_x, dtype_y, x, T, K, w_gate, w_up, N, y, *, x_stride=None, y_stride=None,
+                stream=None):
+    """y [T, N] = act(x . Wg^T) * (x . Wu^T)."""
+    call("slhip_dual_matvec", ACTS.get(act, act), FORMATS.get(fmt, fmt), DTYPES.get(dtype_x, dtype_x),
+         DTYPES.get(dtype_y, dtype_y), ptr(x), K if x_stride is None else x_stride, T, K, ptr(w_gate), ptr(w_up), N,
+         ptr(y), N if y_stride is None else y_stride, stream)
 
 
 def gated_act(act, dtype_in, dtype_out, gate, up, out, rows, cols, *, gate_stride=None, up_stride=None,

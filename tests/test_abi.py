@@ -170,3 +170,20 @@ def test_last_error_is_thread_local_and_never_null():
     th.join()
     assert seen == [""]
     assert "x and y" in native.last_error()
+
+
+def test_matvec_validation():
+    with pytest.raises(native.SlhipArgumentError, match="null"):
+        native.matvec("bf16", "f32", "f32", None, 1, 64, FAKE, 4, FAKE)
+    with pytest.raises(native.SlhipArgumentError, match="bad activation"):
+        native.dual_matvec(7, "bf16", "f32", "f32", FAKE, 1, 64, FAKE, FAKE, 4, FAKE)
+    with pytest.raises(native.SlhipNotSupported, match="weight format"):
+        native.matvec("q4_1", "f32", "f32", FAKE, 1, 64, FAKE, 4, FAKE)
+    with pytest.raises(native.SlhipNotSupported, match="multiple of 8"):
+        native.matvec("bf16", "f32", "f32", FAKE, 1, 60, FAKE, 4, FAKE)
+    with pytest.raises(native.SlhipNotSupported, match="16384"):
+        native.matvec("bf16", "f32", "f32", FAKE, 1, 16392, FAKE, 4, FAKE)
+    with pytest.raises(native.SlhipArgumentError, match="stride"):
+        native.matvec("bf16", "f32", "f32", FAKE, 1, 64, FAKE, 4, FAKE, x_stride=32)
+    with pytest.raises(native.SlhipNotSupported, match="f32 or bf16"):
+        native.matvec("bf16", "f16", "f32", FAKE, 1, 64, FAKE, 4, FAKE)

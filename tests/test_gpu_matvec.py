@@ -1,0 +1,174 @@
+"""GPU parity of the decode matvec and the dual gate/up matvec with the gating epilogue (slhip_matvec,
+slhip_dual_matvec) against the oracle's restatement of the CPU provider's MatMul float-row path followed by
+the activation and Mul -- the reference's FusionTests.SwiGluDualMatvec (tests/Sharplight.Vulkan.Tests/
+FusionTests.cs:59-80: the fused dual matvec against the CPU provider, T in 1..140, K 1024 and 256).
+
+Tolerance (f32 sums in a different order): for a dot product with terms x_k w_k the kernel and the oracle
+each stay within 2^-17 * sum_k |x_k w_k| of the exact value (the oracle's own pin), so they are held to
+2^-16 * S of each other; the dual epilogue propagates that through act(g) * u (first order, with act'
+evaluated in f64), plus 1e-5 relative for the activation itself. bf16 outputs: 2 bf16 ulp of the rounded
+reference on top. A one-hot x picks a weight column and must come out exactly."""
+import math
+import zlib
+
+import numpy as np
+import pytest
+
+import oracle
+from sharplight_amd import native, synth
+from tests.devutil import Dev, log
+from tests.parity import assert_bits_equal
+
+pytestmark = pytest.mark.gpu
+
+NP = {"f32": np.float32, "bf16": np.uint16}
+
+
+def _seed(*parts) -> int:
+    return zlib.crc32(repr(parts).encode())
+
+
+def _weights(fmt, N, K, seed, tid):
+    raw = synth.quant_table(fmt, N, K, seed=seed, tid=tid)
+    W = oracle.dequant(fmt, raw.reshape(-1), N * K).reshape(N, K)
+    return raw, W
+
+
+def _act64(act, g):
+    g = np.asarray(g, np.float64)
+    if act == "silu":
+        return g / (1.0 + np.exp(-g))
+    if act == "gelu_tanh":
+        return 0.5 * g * (1.0 + np.tanh(0.7978845608028654 * (g + 0.044715 * g ** 3)))
+    return 0.5 * g * (1.0 + np.vectorize(math.erf)(g / math.sqrt(2.0)))
+
+
+def _run(fmt, dx, dy, x, raws, N, K, *, act=None, x_stride=None, y_stride=None, pad=0):
+    T = x.shape[0]
+    xs = K if x_stride is None else x_stride
+    ys = N if y_stride is None else y_stride
+    xp = np.zeros((T, xs), x.dtype)
+    xp[:, :K] = x
+    with Dev() as d:
+        px = d.put(xp, pad)
+        pw = [d.put(r) for r in raws]
+        py = d.empty(max(T * ys * np.dtype(NP[dy]).itemsize, 4))
+        log(f"matvec {'dual ' + act if act else 'single'} fmt={fmt} x={dx} y={dy} T={T} K={K} N={N} "
+            f"xs={xs} ys={ys}")
+        if act:
+            native.dual_matvec(act, fmt, dx, dy, px, T, K, pw[0], pw[1], N, py, x_stride=xs, y_stride=ys)
+        else:
+            native.matvec(fmt, dx, dy, px, T, K, pw[0], N, py, x_stride=xs, y_stride=ys)
+        native.synchronize()
+        y = d.get(py, (T, ys), NP[dy])
+    return y[:, :N]
+
+
+def _x(dx, T, K, seed):
+    x = synth.normal(seed, 9, (T, K), dtype=dx)
+    return x, (oracle.from_bf16(x) if dx == "bf16" else x)
+
+
+def _check_single(got, dy, ref, S, what):
+    tol = 2.0 ** -16 * S + 1e-30
+    if dy == "bf16":
+        g = oracle.from_bf16(got).astype(np.float64)
+        r = oracle.from_bf16(oracle.to_bf16(ref)).astype(np.float64)
+        tol = tol + 2 * 2.0 ** -8 * np.abs(r)
+    else:
+        g, r = got.astype(np.float64), ref.astype(np.float64)
+    bad = np.abs(g - r) > tol
+    assert not bad.any(), f"{what}: {bad.sum()} of {bad.size} beyond the bound; first at {np.argwhere(bad)[0]}"
+
+
+SINGLE_CASES = [  # (fmt, x dtype, y dtype, T, K, N)
+    ("bf16", "f32", "f32", 1, 4096, 96),
+    ("bf16", "f32", "f32", 3, 1024, 96),
+    ("f16", "f32", "f32", 8, 1024, 37),
+    ("f32", "f32", "f32", 9, 256, 40),
+    ("bf16", "bf16", "bf16", 16, 4096, 70),
+    ("f16", "bf16", "f32", 20, 512, 33),
+    ("f32", "f32", "bf16", 2, 8, 5),        # one vector per row: most lanes clamp
+    ("bf16", "f32", "f32", 1, 14336, 24),   # K split over waves
+    ("f32", "f32", "f32", 1, 16384, 8),     # the largest staged K
+]
+
+
+@pytest.mark.parametrize("fmt,dx,dy,T,K,N", SINGLE_CASES)
+def test_matvec(device, fmt, dx, dy, T, K, N):
+    seed = _seed(fmt, dx, dy, T, K, N)
+    raw, W = _weights(fmt, N, K, seed, 1)
+    x, x32 = _x(dx, T, K, seed)
+    y = _run(fmt, dx, dy, x, [raw], N, K)
+    ref = oracle.matvec(fmt, raw, N, K, x32)
+    S = np.abs(x32).astype(np.float64) @ np.abs(W).astype(np.float64).T
+    _check_single(y, dy, ref, S, f"matvec {fmt}")
+
+
+@pytest.mark.parametrize("fmt", ["f32", "f16", "bf16"])
+def test_one_hot_rows_pick_columns_exactly(device, fmt):
+    N, K = 29, 2048
+    raw, W = _weights(fmt, N, K, 3, 1)
+    ks = [0, 7, 511, 512, 2047]
+    x = np.zeros((len(ks), K), np.float32)
+    x[np.arange(len(ks)), ks] = 1.0
+    y = _run(fmt, "f32", "f32", x, [raw], N, K)
+    assert_bits_equal(y, np.ascontiguousarray(W[:, ks].T), what="one-hot columns")
+
+
+DUAL_CASES = [  # (act, fmt, x dtype, y dtype, T, K, N): FusionTests.SwiGluDualMatvec's K/N plus decode shapes
+    ("silu", "bf16", "f32", "f32", 1, 1024, 96),
+    ("silu", "f16", "f32", "f32", 3, 1024, 96),
+    ("silu", "f32", "f32", "f32", 8, 1024, 96),
+    ("silu", "bf16", "f32", "f32", 9, 256, 40),
+    ("silu", "bf16", "f32", "bf16", 16, 1024, 96),
+    ("silu", "f16", "bf16", "bf16", 20, 256, 40),
+    ("silu", "bf16", "f32", "f32", 70, 1024, 96),
+    ("gelu_tanh", "bf16", "f32", "f32", 1, 4096, 64),
+    ("gelu_erf", "f16", "f32", "f32", 4, 4096, 64),
+    ("silu", "bf16", "bf16", "bf16", 1, 4096, 14336),  # the Llama-3-8B decode FFN (C3's model)
+]
+
+
+@pytest.mark.parametrize("act,fmt,dx,dy,T,K,N", DUAL_CASES)
+def test_dual_matvec(device, act, fmt, dx, dy, T, K, N):
+    seed = _seed(act, fmt, dx, dy, T, K, N)
+    rg, Wg = _weights(fmt, N, K, seed, 1)
+    ru, Wu = _weights(fmt, N, K, seed, 2)
+    x, x32 = _x(dx, T, K, seed)
+    y = _run(fmt, dx, dy, x, [rg, ru], N, K, act=act)
+    g = oracle.matvec(fmt, rg, N, K, x32)
+    u = oracle.matvec(fmt, ru, N, K, x32)
+    ref = oracle.mul(oracle.unary(act, g), u)
+    ax = np.abs(x32).astype(np.float64)
+    Sg = ax @ np.abs(Wg).astype(np.float64).T
+    Su = ax @ np.abs(Wu).astype(np.float64).T
+    g64 = g.astype(np.float64)
+    h = 1e-4 * np.maximum(1.0, np.abs(g64))
+    dact = (_act64(act, g64 + h) - _act64(act, g64 - h)) / (2 * h)
+    e = 2.0 ** -16
+    tol = np.abs(dact * u) * e * Sg + np.abs(_act64(act, g64)) * e * Su + 1e-5 * np.abs(ref) + 1e-30
+    if dy == "bf16":
+        got = oracle.from_bf16(y).astype(np.float64)
+        r = oracle.from_bf16(oracle.to_bf16(ref)).astype(np.float64)
+        tol = tol + 2 * 2.0 ** -8 * np.abs(r)
+    else:
+        got, r = y.astype(np.float64), ref.astype(np.float64)
+    bad = np.abs(got - r) > tol
+    assert not bad.any(), f"{bad.sum()} of {bad.size} beyond the bound; first at {np.argwhere(bad)[0]}"
+
+
+def test_strided_rows(device):
+    """x and y with row strides beyond the row (views of wider buffers): only the row's own values count
+    and only [T, N] of y is written."""
+    fmt, T, K, N = "bf16", 5, 1024, 50
+    raw, W = _weights(fmt, N, K, 4, 1)
+    x, x32 = _x("f32", T, K, 4)
+    y = _run(fmt, "f32", "f32", x, [raw], N, K, x_stride=K + 12, y_stride=N + 7)
+    S = np.abs(x32).astype(np.float64) @ np.abs(W).astype(np.float64).T
+    _check_single(y, "f32", oracle.matvec(fmt, raw, N, K, x32), S, "strided")
+
+
+def test_empty_shapes_are_noops(device):
+    native.matvec("bf16", "f32", "f32", None, 0, 64, None, 10, None)
+    native.dual_matvec("silu", "bf16", "f32", "f32", None, 3, 64, None, None, 0, None)

@@ -481,3 +481,54 @@ def test_f16_threaded_matches():
     y = np.empty(x.size, np.uint16)
     oracle.lib().orc_f32_to_f16_mt(oracle._p(x), oracle._p(y), x.size)
     assert np.array_equal(y, oracle.to_f16(x))
+
+
+# ---- matvec (MatMulOp's float-row path) ----------------------------------------------------------------
+
+MV_FORMATS = ["f32", "f16", "bf16", "q8_0", "q4_0", "q4_1", "q5_0", "q5_1"]
+
+
+def _deq_rows(fmt, raw, N, K):
+    return oracle.dequant(fmt, raw.reshape(-1), N * K).reshape(N, K)
+
+
+@pytest.mark.parametrize("fmt", MV_FORMATS)
+@pytest.mark.parametrize("T", [1, 3, 6])
+def test_matvec_one_hot_rows_pick_columns(fmt, T):
+    """x = e_k picks column k of the dequantized W exactly, on every path (fused, chunked, paired rows):
+    a transposed operand, a wrong block or chunk offset, or a dropped chunk cannot pass."""
+    N, K = 13, 2080  # N not a multiple of 4; K over two 1024-value chunks and a partial third
+    raw = synth.quant_table(fmt, N, K, seed=5, tid=1)
+    W = _deq_rows(fmt, raw, N, K)
+    ks = np.array([0, 31, 1023, 1024, 2079, 1500][:T])
+    x = np.zeros((T, K), np.float32)
+    x[np.arange(T), ks] = 1.0
+    y = oracle.matvec(fmt, raw, N, K, x)
+    assert np.array_equal(y, W[:, ks].T)
+
+
+@pytest.mark.parametrize("fmt", MV_FORMATS)
+@pytest.mark.parametrize("T", [1, 4, 5, 9])
+def test_matvec_matches_f64_within_the_f32_bound(fmt, T):
+    """Against the f64 dot of the dequantized rows: |y - y64| <= 2^-17 * sum_k |x_k w_k| (far below the
+    worst-case bound of f32 summation; a dropped or doubled term shows at ~1e-3 of the sum)."""
+    N, K = 37, 4096 if fmt != "f32" else 1536
+    raw = synth.quant_table(fmt, N, K, seed=6, tid=2)
+    W = _deq_rows(fmt, raw, N, K).astype(np.float64)
+    x = synth.normal(6, 3, (T, K))
+    y = oracle.matvec(fmt, raw, N, K, x)
+    y64 = x.astype(np.float64) @ W.T
+    bound = 2.0 ** -17 * (np.abs(x).astype(np.float64) @ np.abs(W).T)
+    assert (np.abs(y - y64) <= bound).all()
+
+
+def test_matvec_threaded_equals_plain():
+    N, K = 301, 1024
+    raw = synth.quant_table("q4_0", N, K, seed=7, tid=1)
+    x = synth.normal(7, 2, (2, K))
+    assert np.array_equal(oracle.matvec("q4_0", raw, N, K, x, threads=True), oracle.matvec("q4_0", raw, N, K, x))
+
+
+def test_matvec_rejects_ragged_quant_rows():
+    with pytest.raises(ValueError):
+        oracle.matvec("q8_0", np.zeros((2, 34), np.uint8), 2, 40, np.zeros((1, 40), np.float32))
