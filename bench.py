@@ -254,6 +254,27 @@ class VCache(Workload):
         native.cache_write("bf16", "f16", self.v.slot(i), self.T, self.inner, self.vc.slot(i), self.rows, stream=stream)
 
 
+class DualMatvec(Workload):
+    """The decode FFN's gate/up projections with the SiLU epilogue (Llama-3-8B, C3's model): x f32 [T, 4096],
+    Wg and Wu bf16 [14336, 4096], y f32 [T, 14336] -- weight-bandwidth-bound."""
+
+    def __init__(self, T=1, fmt="bf16", K=4096, N=14336):
+        self.name = f"dual_matvec_silu_{fmt}_T{T}"
+        self.desc = f"x f32 [{T}, {K}], Wg/Wu {fmt} [{N}, {K}], y = silu(x Wg^T) * (x Wu^T) f32 [{T}, {N}]"
+        self.T, self.K, self.N, self.fmt = T, K, N, fmt
+        wg = synth.quant_table(fmt, N, K, seed=0, tid=11)
+        wu = synth.quant_table(fmt, N, K, seed=0, tid=12)
+        x = synth.normal(0, 13, (T, K))
+        self.bytes_per_step = wg.nbytes + wu.nbytes + x.nbytes + T * N * 4
+        R = copies_for(self.bytes_per_step)
+        self.wg, self.wu = Rot(wg, wg.nbytes, R), Rot(wu, wu.nbytes, R)
+        self.x, self.y = Rot(x, x.nbytes, R), Rot(None, T * N * 4, R)
+
+    def launch(self, i, stream):
+        native.dual_matvec("silu", self.fmt, "f32", "f32", self.x.slot(i), self.T, self.K, self.wg.slot(i),
+                           self.wu.slot(i), self.N, self.y.slot(i), stream=stream)
+
+
 class C5(Workload):
     def __init__(self, fmt):
         self.fmt = fmt
@@ -330,6 +351,8 @@ WORKLOADS = {
     "c5_gather_f16": lambda: C5("f16"),
     "c4_qk_rope_kv_bf16_paged": lambda: C4Cache(),
     "v_cache_write_f16_paged": lambda: VCache(),
+    "dual_matvec_silu_bf16_T1": lambda: DualMatvec(1),
+    "dual_matvec_silu_bf16_T4": lambda: DualMatvec(4),
     "copy_256MiB": lambda: CopyRef(),
 }
 
@@ -450,6 +473,26 @@ def cpu_baselines(budget_main: float, budget_op: float, which: set[str]) -> dict
         s, reps = cpu_time(run, budget_op)
         res[name] = dict(s=s * 8192 / rows, reps=reps,
                          sample=f"{rows} of 8192 rows, scaled x{8192 // rows}; Add, RmsNorm, then the {copy} rows")
+    for T in (1, 4):
+        name = f"dual_matvec_silu_bf16_T{T}"
+        if name not in which:
+            continue
+        K, N = 4096, 14336
+        n_s = 3584  # a quarter of the rows: the op is row-independent
+        wg = synth.quant_table("bf16", n_s, K, seed=0, tid=11)
+        wu = synth.quant_table("bf16", n_s, K, seed=0, tid=12)
+        x = synth.normal(0, 13, (T, K))
+        L, P = oracle.lib(), oracle._p
+        g, u, a, yv = (np.empty((T, n_s), np.float32) for _ in range(4))
+
+        def run():
+            L.orc_matvec_mt(oracle.FORMATS["bf16"], P(wg), n_s, K, P(x), T, P(g))
+            L.orc_matvec_mt(oracle.FORMATS["bf16"], P(wu), n_s, K, P(x), T, P(u))
+            L.orc_unary_mt(oracle.ACTS["silu"], P(g), P(a), g.size)
+            L.orc_mul_mt(P(a), P(u), P(yv), g.size)
+        s, reps = cpu_time(run, budget_op)
+        res[name] = dict(s=s * N / n_s, reps=reps, sample=f"{n_s} of {N} weight rows, scaled x{N // n_s}; "
+                                                          "MatMul, MatMul, Silu, Mul in f32")
     if "c1_rmsnorm_f32" in which:
         c = synth.c1()
         y = np.empty_like(c["x"])

@@ -271,9 +271,9 @@ static int matvec_common(int fmt, int dtype_x, int dtype_y, const void* x, int64
     if ((dtype_x != SLHIP_F32 && dtype_x != SLHIP_BF16) || (dtype_y != SLHIP_F32 && dtype_y != SLHIP_BF16))
         return fail(SLHIP_ERR_UNSUPPORTED, "%s: activations and outputs are f32 or bf16", name);
     if (x_stride < K || y_stride < N) return fail(SLHIP_ERR_INVALID, "%s: a row stride is smaller than the row", name);
-    if (fmt != SLHIP_F32 && fmt != SLHIP_F16 && fmt != SLHIP_BF16)
+    if (fmt != SLHIP_FMT_F32 && fmt != SLHIP_FMT_F16 && fmt != SLHIP_FMT_BF16)
         return fail(SLHIP_ERR_UNSUPPORTED, "%s: weight format %d not supported", name, fmt);
-    const int E = fmt == SLHIP_F32 ? 4 : 8;
+    const int E = fmt == SLHIP_FMT_F32 ? 4 : 8;
     if (K % E != 0 || K % 4 != 0)
         return fail(SLHIP_ERR_UNSUPPORTED, "%s: K = %lld must be a multiple of %d for this weight format", name,
                     static_cast<long long>(K), E);
@@ -285,10 +285,10 @@ static int matvec_common(int fmt, int dtype_x, int dtype_y, const void* x, int64
                     static_cast<long long>(K));
     if (N > 0x7FFFFFFF || T > 0x7FFFFFFF) return fail(SLHIP_ERR_UNSUPPORTED, "%s: shape too large", name);
     MatvecArgs a{x, x_stride, static_cast<const char*>(wg), static_cast<const char*>(wu),
-                 K * (fmt == SLHIP_F32 ? 4 : 2), y, y_stride, T, K, N, 0, dtype_x, dtype_y, act};
+                 K * (fmt == SLHIP_FMT_F32 ? 4 : 2), y, y_stride, T, K, N, 0, dtype_x, dtype_y, act};
     hipStream_t st = to_stream(stream);
-    if (fmt == SLHIP_F32) return run_dense<SLHIP_F32>(a, dual, st);
-    if (fmt == SLHIP_F16) return run_dense<SLHIP_F16>(a, dual, st);
+    if (fmt == SLHIP_FMT_F32) return run_dense<SLHIP_F32>(a, dual, st);
+    if (fmt == SLHIP_FMT_F16) return run_dense<SLHIP_F16>(a, dual, st);
     return run_dense<SLHIP_BF16>(a, dual, st);
 }
 

@@ -20,7 +20,9 @@
 //   * a Rope whose only consumer is a CacheWrite -> the rope stores into the cache rows (:633-648);
 //   * a Cast to f16 of a row norm's f32 output -> the f16 copy written by the norm launch, which then skips
 //     the f32 rows when nothing else reads them (GraphLowerer.HalfCopies.cs:106-151);
-//   * RmsNorm, L2Norm, LayerNorm, Rope, Gather, Cast and CacheWrite on their own.
+//   * two MatMuls sharing x whose products feed act(gate) * up -> one dual matvec launch with the gating
+//     epilogue (FoldDualMatMuls, :286-353);
+//   * RmsNorm, L2Norm, LayerNorm, Rope, Gather, Cast, CacheWrite and MatMul (decode matvec) on their own.
 // An Add, Mul or activation that fits none of these patterns is not supported on this provider.
 //
 // The graph reaches the C ABI as a small line-based text form (one value, node, input, weight or output
@@ -327,13 +329,32 @@ Support supports(const Graph& g, const Node& n)
         if (n.in.size() != 1 || n.out.size() != 1 || !act(n.in[0]) || !act(n.out[0])) return no("Cast: activation types");
         return {true, ""};
     }
+    if (op == "MatMul") {
+        // StandardOps.MatMul (src/Sharplight.Core/Graph/StandardOps.cs:143-162): y = x . W^T, W a weight [N, K];
+        // run here as the decode matvec (few activation rows).
+        if (n.in.size() != 2 || n.out.size() != 1) return no("MatMul takes x, weight");
+        const Value& x = g.value(n.in[0]);
+        const Value& w = g.value(n.in[1]);
+        const Value& y = g.value(n.out[0]);
+        if (x.type != DType::F32 && x.type != DType::BF16) return no("MatMul: f32 or bf16 activations");
+        if (y.type != DType::F32 && y.type != DType::BF16) return no("MatMul: f32 or bf16 output");
+        if (!w.weight || w.dims.size() != 2) return no("MatMul: the second operand must be a weight [N, K]");
+        if (w.type != DType::F32 && w.type != DType::F16 && w.type != DType::BF16)
+            return no("MatMul: f32, f16 or bf16 weights on this provider");
+        if (x.dims.empty() || w.dims[1] != x.last()) return no("MatMul: K mismatch");
+        if (y.last() != w.dims[0]) return no("MatMul: output must be [.., N]");
+        const int64_t K = x.last();
+        if (K % (w.type == DType::F32 ? 4 : 8) != 0 || K > 16384)
+            return no("MatMul: K must be a multiple of 8 (4 for f32 weights) and at most 16384");
+        return {true, ""};
+    }
     return no("op " + op + " is not on the fused-layer-op path of the HIP provider");
 }
 
 // ---- lowering into fused units -------------------------------------------------------------------------
 
 struct Unit {
-    enum Kind { RowNorm, Gated, Rope, Gather, Cast, CacheWrite } kind;
+    enum Kind { RowNorm, Gated, Rope, Gather, Cast, CacheWrite, Matvec } kind;
     std::string label;
     // RowNorm
     int norm = SLHIP_NORM_RMS;
@@ -343,6 +364,8 @@ struct Unit {
     float eps = 0.f;
     // Gated
     int act = SLHIP_ACT_SILU, gate = -1, up = -1;
+    // Matvec: x . Wg^T, or act(x . Wg^T) * (x . Wu^T) when wu >= 0
+    int wg = -1, wu = -1;
     // Rope: up to 4 tensors sharing positions and settings
     struct RopeTensor {
         int x, y, w;
@@ -474,6 +497,7 @@ private:
         const size_t N = g_.nodes.size();
         std::vector<bool> done(N, false);
         auto single_use = [&](int id) { return !g_.value(id).output && cons[id].size() == 1; };
+        find_dual_matvecs(cons, single_use);
         for (size_t k = 0; k < N; k++) {
             if (done[k]) continue;
             const Node& n = g_.nodes[k];
@@ -494,6 +518,24 @@ private:
                     units_.push_back(u);
                     continue;
                 }
+            }
+            auto dual = dual_at_.find(static_cast<int>(k));
+            if (dual != dual_at_.end()) {  // the Mul closing act(x Wg^T) * (x Wu^T): one dual matvec launch
+                const DualPattern& d = dual->second;
+                Unit u{Unit::Matvec};
+                u.x = g_.nodes[d.mm_gate].in[0];
+                u.wg = g_.nodes[d.mm_gate].in[1];
+                u.wu = g_.nodes[d.mm_up].in[1];
+                u.act = d.act;
+                u.y = n.out[0];
+                u.label = "matvec2+fused[" + g_.nodes[d.act_node].op + ",Mul]";
+                units_.push_back(u);
+                done[k] = true;
+                continue;
+            }
+            if (absorbed_.count(static_cast<int>(k))) {  // a MatMul or activation of a dual matvec
+                done[k] = true;
+                continue;
             }
             if (kActs.count(n.op) && single_use(n.out[0])) {
                 const int mk = cons[n.out[0]][0];
@@ -559,6 +601,13 @@ private:
                 u.y = n.out[0];
                 u.label = "Cast";
                 units_.push_back(u);
+            } else if (n.op == "MatMul") {
+                Unit u{Unit::Matvec};
+                u.x = n.in[0];
+                u.wg = n.in[1];
+                u.y = n.out[0];
+                u.label = "matvec";
+                units_.push_back(u);
             } else if (n.op == "CacheWrite") {
                 Unit u{Unit::CacheWrite};
                 u.x = n.in[1];
@@ -575,6 +624,50 @@ private:
     }
 
     std::map<int, int> absorbed_norm_;  // rope node -> RmsNorm node computed inside it
+
+    // Gate/up matmul pairs sharing x that feed act(gate) * up (FoldDualMatMuls,
+    // src/Sharplight.Shaders/Lowering/GraphLowerer.Fusion.cs:286-353): both products read only by the
+    // pattern, weights of one type and shape, the activation's output read only by the Mul.
+    struct DualPattern {
+        int mm_gate, mm_up, act_node, act;
+    };
+    std::map<int, DualPattern> dual_at_;  // Mul node -> its pattern
+    std::set<int> absorbed_;              // MatMul and activation nodes inside a pattern
+
+    template <class F>
+    void find_dual_matvecs(std::map<int, std::vector<int>>& cons, F single_use)
+    {
+        std::map<int, int> producer;
+        for (size_t k = 0; k < g_.nodes.size(); k++)
+            for (int o : g_.nodes[k].out) producer[o] = static_cast<int>(k);
+        auto prod = [&](int id) { auto it = producer.find(id); return it == producer.end() ? -1 : it->second; };
+        for (size_t k = 0; k < g_.nodes.size(); k++) {
+            const Node& m = g_.nodes[k];
+            if (m.op != "Mul" || m.in.size() != 2) continue;
+            for (int side = 0; side < 2; side++) {
+                const int a = prod(m.in[side]), b = prod(m.in[1 - side]);
+                if (a < 0 || b < 0 || !kActs.count(g_.nodes[a].op)) continue;
+                const int ga = prod(g_.nodes[a].in[0]);
+                if (ga < 0 || g_.nodes[ga].op != "MatMul" || g_.nodes[b].op != "MatMul") continue;
+                const Node& mg = g_.nodes[ga];
+                const Node& mu = g_.nodes[b];
+                const Value& wg = g_.value(mg.in[1]);
+                const Value& wu = g_.value(mu.in[1]);
+                if (mg.in[0] != mu.in[0] || wg.type != wu.type || wg.dims != wu.dims) continue;
+                if (!single_use(mg.out[0]) || !single_use(mu.out[0]) || !single_use(g_.nodes[a].out[0])) continue;
+                if (g_.value(mg.out[0]).type != DType::F32 || g_.value(mu.out[0]).type != DType::F32 ||
+                    g_.value(g_.nodes[a].out[0]).type != DType::F32)
+                    continue;  // the unfused graph rounds nothing between the products and the Mul
+                const std::string& an = g_.nodes[a].op;
+                dual_at_[static_cast<int>(k)] = {ga, b, a, an == "Silu" ? SLHIP_ACT_SILU : an == "GeluTanh" ? SLHIP_ACT_GELU_TANH : SLHIP_ACT_GELU_ERF};
+                absorbed_.insert(ga);
+                absorbed_.insert(b);
+                absorbed_.insert(a);
+                break;
+            }
+        }
+        (void)cons;
+    }
 
     // A Cast of an f32 norm output to f16 is the f16 copy the norm writes beside its rows: the norm's f32
     // values rounded once, as the reference's row norm writes the half copy its GEMM readers take
@@ -724,6 +817,19 @@ private:
                                        static_cast<const float*>(ptr(u.w)), static_cast<const float*>(ptr(u.b)),
                                        u.skip_y ? nullptr : ptr(u.y), ptr(u.h), rows, D, D, D, D, D, u.eps,
                                        u.y16 >= 0 ? &copies : nullptr, stream_));
+            break;
+        }
+        case Unit::Matvec: {
+            const Value& xv = g_.value(u.x);
+            const Value& wv = g_.value(u.wg);
+            const int64_t K = xv.last(), rows = xv.rows(T), Nw = wv.dims[0];
+            const int fmt = wv.type == DType::F32 ? SLHIP_FMT_F32 : wv.type == DType::F16 ? SLHIP_FMT_F16 : SLHIP_FMT_BF16;
+            const int dy = act_code(g_.value(u.y).type);
+            if (u.wu >= 0)
+                check(slhip_dual_matvec(u.act, fmt, act_code(xv.type), dy, ptr(u.x), K, rows, K, ptr(u.wg), ptr(u.wu), Nw,
+                                        ptr(u.y), Nw, stream_));
+            else
+                check(slhip_matvec(fmt, act_code(xv.type), dy, ptr(u.x), K, rows, K, ptr(u.wg), Nw, ptr(u.y), Nw, stream_));
             break;
         }
         case Unit::Gated: {

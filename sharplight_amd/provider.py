@@ -128,6 +128,10 @@ class GraphBuilder:
         d = table.dims[1:]
         return self.emit("Gather", [table, ids], out_type, (ids.dims[0],) + tuple(d))
 
+    def matmul(self, x, w, out_type="f32"):
+        """StandardOps.MatMul: x [.., K] . W^T, W a weight [N, K] -> [.., N]."""
+        return self.emit("MatMul", [x, w], out_type, tuple(x.dims[:-1]) + (w.dims[0],))
+
     def cast(self, x, to: str):
         return self.emit("Cast", [x], to, x.dims)
 

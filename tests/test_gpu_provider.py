@@ -75,6 +75,57 @@ def test_residual_add_rmsnorm_fuses(dev, h_is_output):
             assert_bf16_close(seg.get_output(h), href, ulp=0, what="h")
 
 
+@pytest.mark.parametrize("fmt,T,swap", [("bf16", 1, False), ("f16", 3, True), ("f32", 9, False)])
+def test_swiglu_dual_matvec_fuses(dev, fmt, T, swap):
+    """FusionTests.SwiGluDualMatvec (FusionTests.cs:59-80): Mul(Silu(x Wg^T), x Wu^T) is one dual matvec launch
+    (in either operand order), within the f32 dot-product bound of the unfused CPU computation."""
+    K, N = 1024, 96
+    g = GraphBuilder()
+    x = g.input("f32", "T", K)
+    wg = g.weight(fmt, N, K)
+    wu = g.weight(fmt, N, K)
+    gate, up = g.matmul(x, wg), g.matmul(x, wu)
+    y = g.output(g.mul(up, g.silu(gate)) if swap else g.mul(g.silu(gate), up))
+    rg = synth.quant_table(fmt, N, K, seed=8, tid=1)
+    ru = synth.quant_table(fmt, N, K, seed=8, tid=2)
+    xs = synth.normal(8, 3, (T, K))
+    with dev.compile(g, max_tokens=16) as seg:
+        assert seg.launches == ["matvec2+fused[Silu,Mul]"]
+        seg.set_input(x, xs)
+        seg.set_input(wg, rg)
+        seg.set_input(wu, ru)
+        log(f"provider dual matvec {fmt} T={T}")
+        seg.execute(T)
+        got = seg.get_output(y).astype(np.float64)
+    gr, ur = oracle.matvec(fmt, rg, N, K, xs), oracle.matvec(fmt, ru, N, K, xs)
+    ref = oracle.mul(oracle.unary("silu", gr), ur).astype(np.float64)
+    Wg = oracle.dequant(fmt, rg.reshape(-1), N * K).reshape(N, K).astype(np.float64)
+    Wu = oracle.dequant(fmt, ru.reshape(-1), N * K).reshape(N, K).astype(np.float64)
+    ax = np.abs(xs).astype(np.float64)
+    # |d(silu)/dg| <= 1.1 everywhere: a first-order bound of the two products' rounding, plus the epilogue's
+    tol = 2.0 ** -16 * (1.1 * np.abs(ur) * (ax @ np.abs(Wg).T) + np.abs(gr) * (ax @ np.abs(Wu).T)) + 1e-5 * np.abs(ref)
+    assert (np.abs(got - ref) <= tol + 1e-30).all()
+
+
+def test_matmul_alone_is_a_matvec(dev):
+    K, N, T = 512, 40, 2
+    g = GraphBuilder()
+    x = g.input("f32", "T", K)
+    w = g.weight("bf16", N, K)
+    y = g.output(g.matmul(x, w))
+    raw = synth.quant_table("bf16", N, K, seed=9, tid=1)
+    xs = synth.normal(9, 2, (T, K))
+    with dev.compile(g, max_tokens=4) as seg:
+        assert seg.launches == ["matvec"]
+        seg.set_input(x, xs)
+        seg.set_input(w, raw)
+        seg.execute(T)
+        got = seg.get_output(y).astype(np.float64)
+    W = oracle.dequant("bf16", raw.reshape(-1), N * K).reshape(N, K).astype(np.float64)
+    S = np.abs(xs).astype(np.float64) @ np.abs(W).T
+    assert (np.abs(got - oracle.matvec("bf16", raw, N, K, xs)) <= 2.0 ** -16 * S).all()
+
+
 @pytest.mark.parametrize("y_is_output", [True, False])
 def test_norm_writes_the_f16_copy(dev, y_is_output):
     """NormHalfCopyTests (tests/Sharplight.Vulkan.Tests/NormHalfCopyTests.cs): a Cast to f16 of an f32 norm

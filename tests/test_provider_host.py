@@ -129,3 +129,21 @@ def test_state_needs_fixed_dims():
     seg = ctypes.c_void_p(0)
     st = native.lib().slhip_segment_compile(b"value 0 f32 T 4\nstate 0\n", 8, ctypes.byref(seg))
     assert st == native.ERR_INVALID and "fixed dims" in native.last_error()
+
+
+def test_matmul_support_answers():
+    g = GraphBuilder()
+    x = g.input("f32", "T", 64)
+    wq = g.weight("q8_0", 16, 64)
+    wb = g.weight("bf16", 16, 64)
+    w60 = g.weight("bf16", 16, 60)
+    x60 = g.input("f32", "T", 60)
+    g.matmul(x, wq)                          # 0: quantized weights -> no (not yet on this provider)
+    g.matmul(x, wb)                          # 1: yes
+    g.matmul(x60, w60)                       # 2: K not a multiple of 8 -> no
+    g.emit("MatMul", [x, x60], "f32", ("T", 64))  # 3: second operand not a weight [N, K] -> no
+    expect = [False, True, False, False]
+    for k, e in enumerate(expect):
+        ok, why = _supports(g, k)
+        assert ok == e, (k, why)
+        assert ok or why
