@@ -353,6 +353,8 @@ WORKLOADS = {
     "v_cache_write_f16_paged": lambda: VCache(),
     "dual_matvec_silu_bf16_T1": lambda: DualMatvec(1),
     "dual_matvec_silu_bf16_T4": lambda: DualMatvec(4),
+    "dual_matvec_silu_q8_0_T1": lambda: DualMatvec(1, "q8_0"),
+    "dual_matvec_silu_q4_0_T1": lambda: DualMatvec(1, "q4_0"),
     "copy_256MiB": lambda: CopyRef(),
 }
 
@@ -473,21 +475,21 @@ def cpu_baselines(budget_main: float, budget_op: float, which: set[str]) -> dict
         s, reps = cpu_time(run, budget_op)
         res[name] = dict(s=s * 8192 / rows, reps=reps,
                          sample=f"{rows} of 8192 rows, scaled x{8192 // rows}; Add, RmsNorm, then the {copy} rows")
-    for T in (1, 4):
-        name = f"dual_matvec_silu_bf16_T{T}"
+    for fmt, T in (("bf16", 1), ("bf16", 4), ("q8_0", 1), ("q4_0", 1)):
+        name = f"dual_matvec_silu_{fmt}_T{T}"
         if name not in which:
             continue
         K, N = 4096, 14336
         n_s = 3584  # a quarter of the rows: the op is row-independent
-        wg = synth.quant_table("bf16", n_s, K, seed=0, tid=11)
-        wu = synth.quant_table("bf16", n_s, K, seed=0, tid=12)
+        wg = synth.quant_table(fmt, n_s, K, seed=0, tid=11)
+        wu = synth.quant_table(fmt, n_s, K, seed=0, tid=12)
         x = synth.normal(0, 13, (T, K))
         L, P = oracle.lib(), oracle._p
         g, u, a, yv = (np.empty((T, n_s), np.float32) for _ in range(4))
 
-        def run():
-            L.orc_matvec_mt(oracle.FORMATS["bf16"], P(wg), n_s, K, P(x), T, P(g))
-            L.orc_matvec_mt(oracle.FORMATS["bf16"], P(wu), n_s, K, P(x), T, P(u))
+        def run(fmt=fmt, T=T, x=x, wg=wg, wu=wu, g=g, u=u, a=a, yv=yv):
+            L.orc_matvec_mt(oracle.FORMATS[fmt], P(wg), n_s, K, P(x), T, P(g))
+            L.orc_matvec_mt(oracle.FORMATS[fmt], P(wu), n_s, K, P(x), T, P(u))
             L.orc_unary_mt(oracle.ACTS["silu"], P(g), P(a), g.size)
             L.orc_mul_mt(P(a), P(u), P(yv), g.size)
         s, reps = cpu_time(run, budget_op)

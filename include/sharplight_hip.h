@@ -197,13 +197,16 @@ SLHIP_API int slhip_rownorm_copies(int kind, int dtype_in, int dtype_out, const 
 /*
  * Decode matvec y = x . W^T and the dual gate/up matvec y = act(x . Wg^T) * (x . Wu^T) for few activation
  * rows (the decode FFN's gate/up projections with the gating epilogue).
- *   x: [T, K] f32 or bf16 (dtype_x), row stride x_stride elements (a multiple of 4), 16-byte aligned rows;
- *   W, Wg, Wu: N dense rows of K weights in `fmt` (F32, F16 or BF16; K a multiple of 8, or of 4 for F32),
- *   16-byte aligned; y: [T, N] f32 or bf16 (dtype_y), row stride y_stride elements.
+ *   x: [T, K] f32 or bf16 (dtype_x), 16-byte aligned, row stride x_stride elements (a multiple of 8);
+ *   W, Wg, Wu: N rows of K weights in `fmt`, 16-byte aligned: dense F32/F16/BF16 (K a multiple of 8,
+ *   K <= 16384), or the GGUF block formats Q8_0/Q4_0/Q4_1/Q5_0/Q5_1 (rows of K/32 blocks, K a multiple of
+ *   256, the rows' block images fitting in LDS); y: [T, N] f32 or bf16 (dtype_y), row stride y_stride.
  *   act: SLHIP_ACT_SILU / GELU_TANH / GELU_ERF, the same forms as slhip_gated_act.
  * Products and sums in f32 (in another order than the CPU provider's, so equal to it within the rounding of
- * a K-term f32 dot product); K <= 16384.
- * Replaces: MatMulOp's float-row path (src/Sharplight.Cpu/MatMulOp.cs:376-465) followed by the activation and
+ * a K-term f32 dot product); block formats sum d * sum(x q) + a * sum(x) per block, as the reference's
+ * fused Q4_0 dot does.
+ * Replaces: MatMulOp's float-row path (src/Sharplight.Cpu/MatMulOp.cs:376-465; fused Q8_0/Q4_0 dots, Quant.cs:738-803)
+ * followed by the activation and
  * Mul, i.e. the reference's dual matvec unit (FoldDualMatMuls, src/Sharplight.Shaders/Lowering/
  * GraphLowerer.Fusion.cs:286-353; tests/Sharplight.Vulkan.Tests/FusionTests.cs:59-80).
  */

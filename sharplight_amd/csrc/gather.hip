@@ -17,11 +17,11 @@
 // size (8 for bf16, 4 for f32), so every store instruction writes one contiguous span. An id outside
 // [0, V) zeroes its row and raises the device error record, reported by slhip_stream_sync.
 #include "common.hpp"
+#include "quant.hpp"
 
 #include <stdlib.h>
 
 namespace slhip {
-
 
 struct GatherArgs {
     const uint8_t* table;
@@ -33,91 +33,6 @@ struct GatherArgs {
     uint32_t* err;
     int64_t chunks;  // chunks per row
 };
-
-template <int FMT> struct Fmt;
-template <> struct Fmt<SLHIP_FMT_Q8_0> { static constexpr int BB = 34, QS = 2, QH = -1; static constexpr bool M = false; static constexpr int OFF = 0; };
-template <> struct Fmt<SLHIP_FMT_Q4_0> { static constexpr int BB = 18, QS = 2, QH = -1; static constexpr bool M = false; static constexpr int OFF = -8; };
-template <> struct Fmt<SLHIP_FMT_Q4_1> { static constexpr int BB = 20, QS = 4, QH = -1; static constexpr bool M = true; static constexpr int OFF = 0; };
-template <> struct Fmt<SLHIP_FMT_Q5_0> { static constexpr int BB = 22, QS = 6, QH = 2; static constexpr bool M = false; static constexpr int OFF = -16; };
-template <> struct Fmt<SLHIP_FMT_Q5_1> { static constexpr int BB = 24, QS = 8, QH = 4; static constexpr bool M = true; static constexpr int OFF = 0; };
-
-__device__ __forceinline__ uint32_t lds_u16(const uint32_t* s, int off)
-{
-    uint32_t w = s[off >> 2];
-    return (off & 2) ? (w >> 16) : (w & 0xFFFFu);
-}
-
-// 4 bytes at an even LDS byte offset.
-__device__ __forceinline__ uint32_t lds_u32(const uint32_t* s, int off)
-{
-    const int i = off >> 2;
-    const uint32_t sh = (off & 3) * 8;
-    return __builtin_amdgcn_alignbit(s[i + 1], s[i], sh);
-}
-
-// 8 bytes at an even LDS byte offset, as two little-endian words.
-__device__ __forceinline__ uint2 lds_u64(const uint32_t* s, int off)
-{
-    const int i = off >> 2;
-    const uint32_t sh = (off & 3) * 8;
-    const uint32_t w0 = s[i], w1 = s[i + 1], w2 = s[i + 2];
-    return make_uint2(__builtin_amdgcn_alignbit(w1, w0, sh), __builtin_amdgcn_alignbit(w2, w1, sh));
-}
-
-__device__ __forceinline__ float half_at(const uint32_t* s, int off)
-{
-    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(lds_u16(s, off))));
-}
-
-// Decodes N (4 or 8) consecutive values starting at value j0 (a multiple of N) of the chunk in LDS.
-template <int FMT, int N>
-__device__ __forceinline__ void decode(const uint32_t* s, int j0, float* f)
-{
-    using F = Fmt<FMT>;
-    const int o = (j0 >> 5) * F::BB;  // the value's block
-    const int k0 = j0 & 31;           // first value index within the block
-    const float d = half_at(s, o);
-    uint32_t b[2];
-    if (FMT == SLHIP_FMT_Q8_0) {
-        if (N == 8) {
-            const uint2 q = lds_u64(s, o + F::QS + k0);
-            b[0] = q.x;
-            b[1] = q.y;
-        } else {
-            b[0] = lds_u32(s, o + F::QS + k0);
-        }
-#pragma unroll
-        for (int e = 0; e < N; e++)
-            f[e] = __fmaf_rn(static_cast<float>(static_cast<int8_t>(b[e >> 2] >> (8 * (e & 3)))), d, 0.0f);
-        return;
-    }
-    // Nibble blocks: value k < 16 is the low nibble of qs[k], k >= 16 the high nibble of qs[k - 16]; the
-    // 5-bit formats take bit k of the 32-bit qh as the fifth bit.
-    const float add = F::M ? half_at(s, o + 2) : static_cast<float>(F::OFF) * d;
-    const int kk = k0 & 15;
-    const int shift = k0 >= 16 ? 4 : 0;
-    if (N == 8) {
-        const uint2 q = lds_u64(s, o + F::QS + kk);
-        b[0] = q.x;
-        b[1] = q.y;
-    } else {
-        b[0] = lds_u32(s, o + F::QS + kk);
-    }
-    uint32_t qh = 0;
-    if (F::QH >= 0) qh = lds_u32(s, o + F::QH) >> k0;
-    // Four nibbles at once: rotating the word by the nibble shift and masking leaves one value per byte,
-    // which converts with a single byte-to-float instruction (the rotate keeps the compiler from folding
-    // the mask back into one bit-field extract per value).
-    uint32_t nib[2];
-#pragma unroll
-    for (int h = 0; h < N / 4; h++) nib[h] = __builtin_amdgcn_alignbit(b[h], b[h], shift) & 0x0F0F0F0Fu;
-#pragma unroll
-    for (int e = 0; e < N; e++) {
-        uint32_t v = (nib[e >> 2] >> (8 * (e & 3))) & 0xFFu;
-        if (F::QH >= 0) v |= ((qh >> e) & 1u) << 4;
-        f[e] = __fmaf_rn(static_cast<float>(v), d, add);
-    }
-}
 
 __device__ __forceinline__ void raise_index_error(uint32_t* err, int64_t id, int64_t V)
 {

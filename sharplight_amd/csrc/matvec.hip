@@ -17,12 +17,13 @@
 //     (their loads complete after the weights', which the in-order completion of vector loads enforces
 //     anyway); each lane then reads the x values of its own vectors from LDS;
 //   * per row and token, one f32 partial per lane -> wave butterfly -> (WPR > 1) one LDS exchange;
-//   * the epilogue (activation, product, output rounding) runs on the reduced sums; lane l stores token l.
+//   * the epilogue (activation, product, output rounding) runs on the reduced sums, one store per token.
 // Rows past N and lanes past the row end work on clamped indices and store the same values as their
 // owners, so every lane issues the same memory operations (a divergent branch around loads makes the
 // compiler wait for all outstanding ones).
 #include "act.hpp"
 #include "common.hpp"
+#include "quant.hpp"
 
 #include <stdlib.h>
 
@@ -43,6 +44,74 @@ struct MatvecArgs {
 };
 
 constexpr int kMvThreads = 512;
+
+// Stages activation rows t0 .. t0+TT-1 (rows past T repeat row T-1) into LDS as f32 [TT][K], up to four
+// 8-value groups per thread per pass; with XSUM also the sum of each 8-value group, [TT][K/8]. Slices wholly
+// past the end are skipped (a block-uniform test); in the last partial slice the spare lanes repeat the last
+// group (identical values; a duplicate LDS write of one address by many lanes would serialize).
+template <int TT, bool XSUM>
+__device__ __forceinline__ void stage_x(const MatvecArgs& a, float* xsh, float* xsum, int threads)
+{
+    const int per_row = static_cast<int>(a.K / 8);  // 8-value groups per row
+    const int units = TT * per_row;
+    for (int base = 0; base < units; base += 4 * threads) {
+        float v[4][8];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            if (base + q * threads >= units) break;
+            int u = base + q * threads + static_cast<int>(threadIdx.x);
+            u = u < units ? u : units - 1;
+            const int t = u / per_row;
+            const int c = u - t * per_row;
+            int64_t tok = a.t0 + t;
+            tok = tok < a.T ? tok : a.T - 1;
+            if (a.xt == SLHIP_F32) {
+                const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(a.x) + tok * a.xs + c * 8);
+                const float4 f0 = p[0], f1 = p[1];
+                v[q][0] = f0.x; v[q][1] = f0.y; v[q][2] = f0.z; v[q][3] = f0.w;
+                v[q][4] = f1.x; v[q][5] = f1.y; v[q][6] = f1.z; v[q][7] = f1.w;
+            } else {
+                const uint4 b = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.x) + tok * a.xs + c * 8);
+                Vec<SLHIP_BF16>::unpack(b, v[q]);
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            if (base + q * threads >= units) break;
+            int u = base + q * threads + static_cast<int>(threadIdx.x);
+            u = u < units ? u : units - 1;
+            float4* d = reinterpret_cast<float4*>(xsh) + 2 * u;
+            d[0] = make_float4(v[q][0], v[q][1], v[q][2], v[q][3]);
+            d[1] = make_float4(v[q][4], v[q][5], v[q][6], v[q][7]);
+            if (XSUM) xsum[u] = ((v[q][0] + v[q][1]) + (v[q][2] + v[q][3])) + ((v[q][4] + v[q][5]) + (v[q][6] + v[q][7]));
+        }
+    }
+}
+
+// The epilogue of a wave holding the reduced sums of row n for tokens t0 .. t0+TT-1 (every lane holds all of
+// them): act(g) * u for a dual matvec, else g, stored for each token by every lane (identical values to one
+// address; a per-lane choice of token would be a dynamically indexed register array, i.e. scratch memory).
+template <int TT, bool DUAL>
+__device__ __forceinline__ void store_row(const MatvecArgs& a, int64_t n, const float (&ag)[TT], const float (&au)[TT])
+{
+#pragma unroll
+    for (int t = 0; t < TT; t++) {
+        float out = ag[t];
+        if (DUAL) {
+            const float g = ag[t];
+            const float act = a.act == SLHIP_ACT_SILU        ? activate<SLHIP_ACT_SILU>(g)
+                              : a.act == SLHIP_ACT_GELU_TANH ? activate<SLHIP_ACT_GELU_TANH>(g)
+                                                             : activate<SLHIP_ACT_GELU_ERF>(g);
+            out = act * au[t];
+        }
+        int64_t tok = a.t0 + t;
+        tok = tok < a.T ? tok : a.T - 1;
+        if (a.yt == SLHIP_F32)
+            static_cast<float*>(a.y)[tok * a.ys + n] = out;
+        else
+            static_cast<uint16_t*>(a.y)[tok * a.ys + n] = static_cast<uint16_t>(f32_to_bf16_bits(out));
+    }
+}
 
 template <int WT, int TT, int NV, bool DUAL>
 __global__ __launch_bounds__(kMvThreads) void matvec_dense(MatvecArgs a, int wpr)
@@ -80,35 +149,7 @@ __global__ __launch_bounds__(kMvThreads) void matvec_dense(MatvecArgs a, int wpr
     }
     __builtin_amdgcn_sched_barrier(0);  // the weight loads go out before the staging loads
 
-    // Stage x rows t0 .. t0+TT-1 (rows past T repeat row T-1) as f32, eight 16-byte loads per lane per pass.
-    {
-        const int per_row = static_cast<int>(a.K / 4);  // float4 units per staged row
-        const int units = TT * per_row;
-        for (int base = 0; base < units; base += 8 * kMvThreads) {
-            float4 v[8];
-#pragma unroll
-            for (int q = 0; q < 8; q++) {
-                int u = base + q * kMvThreads + static_cast<int>(threadIdx.x);
-                u = u < units ? u : units - 1;
-                const int t = u / per_row;
-                const int c = u - t * per_row;
-                int64_t tok = a.t0 + t;
-                tok = tok < a.T ? tok : a.T - 1;
-                if (a.xt == SLHIP_F32) {
-                    v[q] = *reinterpret_cast<const float4*>(static_cast<const float*>(a.x) + tok * a.xs + c * 4);
-                } else {
-                    const uint2 b = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(a.x) + tok * a.xs + c * 4);
-                    v[q] = make_float4(bf16_lo(b.x), bf16_hi(b.x), bf16_lo(b.y), bf16_hi(b.y));
-                }
-            }
-#pragma unroll
-            for (int q = 0; q < 8; q++) {
-                int u = base + q * kMvThreads + static_cast<int>(threadIdx.x);
-                u = u < units ? u : units - 1;
-                reinterpret_cast<float4*>(xsh)[u] = v[q];
-            }
-        }
-    }
+    stage_x<TT, false>(a, xsh, nullptr, kMvThreads);
     __syncthreads();
 
     float ag[TT], au[TT];
@@ -169,27 +210,103 @@ __global__ __launch_bounds__(kMvThreads) void matvec_dense(MatvecArgs a, int wpr
     }
     if (wk != 0) return;  // wave-uniform
 
-    // Lane l stores token min(l, TT - 1), clamped to the last real token.
-    const int tl = lane < TT ? lane : TT - 1;
-    float g = ag[0], u = au[0];
+    store_row<TT, DUAL>(a, n, ag, au);
+}
+
+// Quantized weights (Q8_0, Q4_0, Q4_1, Q5_0, Q5_1): a block of 4 waves, one row (pair) per wave. Each wave
+// copies its rows' block images into LDS with 16-byte loads (the blocks are only 2-byte aligned), the block
+// stages x and the sum of every 8 x values, then each lane walks 8-value groups: with the block's scale d
+// and additive term (OFF * d or m), sum_k x_k (q_k d + add) = d * sum x q + add * sum x, the form of the
+// reference's fused Q4_0 dot (Quant.cs:770-803).
+constexpr int kMqThreads = 256;
+
+template <int FMT, int TT, int CH, bool DUAL>
+__global__ __launch_bounds__(kMqThreads) void matvec_quant(MatvecArgs a)
+{
+    using F = Fmt<FMT>;
+    extern __shared__ uint32_t smem[];
+    constexpr int R = DUAL ? 2 : 1;
+    const int lane = threadIdx.x & 63;
+    const int wave = wave_id();
+    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * (kMqThreads / 64) + wave;
+    const int64_t n = n0 < a.N ? n0 : a.N - 1;
+    const int nch = static_cast<int>(a.wrow / 16);  // 16-byte chunks per row
+    const int rbw = nch * 4;                         // words per row
+    uint32_t* rows = smem + wave * R * rbw;
+    float* xsh = reinterpret_cast<float*>(smem + (kMqThreads / 64) * R * rbw);
+    float* xsum = xsh + TT * a.K;
+
+    const int tot = R * nch;
+    auto load_batch = [&](int base, uint4* v) {
 #pragma unroll
-    for (int t = 1; t < TT; t++) {
-        g = tl == t ? ag[t] : g;
-        u = tl == t ? au[t] : u;
+        for (int c = 0; c < CH; c++) {
+            if (base + c * 64 >= tot) break;  // wave-uniform
+            int idx = base + c * 64 + lane;
+            idx = idx < tot ? idx : tot - 1;
+            const int r = idx >= nch ? 1 : 0;
+            const char* src = (r ? a.wu : a.wg) + n * a.wrow + static_cast<int64_t>(idx - r * nch) * 16;
+            v[c] = load_nt(src);
+        }
+    };
+    auto store_batch = [&](int base, const uint4* v) {
+#pragma unroll
+        for (int c = 0; c < CH; c++) {
+            if (base + c * 64 >= tot) break;  // wave-uniform
+            int idx = base + c * 64 + lane;
+            idx = idx < tot ? idx : tot - 1;
+            reinterpret_cast<uint4*>(rows)[idx] = v[c];
+        }
+    };
+    uint4 v[CH];
+    load_batch(0, v);
+    __builtin_amdgcn_sched_barrier(0);  // the weight loads go out before the staging loads
+    stage_x<TT, true>(a, xsh, xsum, kMqThreads);
+    store_batch(0, v);
+    for (int base = CH * 64; base < tot; base += CH * 64) {
+        load_batch(base, v);
+        store_batch(base, v);
     }
-    float out = g;
-    if (DUAL) {
-        const float act = a.act == SLHIP_ACT_SILU        ? activate<SLHIP_ACT_SILU>(g)
-                          : a.act == SLHIP_ACT_GELU_TANH ? activate<SLHIP_ACT_GELU_TANH>(g)
-                                                         : activate<SLHIP_ACT_GELU_ERF>(g);
-        out = act * u;
+    __syncthreads();
+
+    const int ng = static_cast<int>(a.K / 8);
+    const int per_row = ng;
+    float ag[TT], au[TT];
+#pragma unroll
+    for (int t = 0; t < TT; t++) ag[t] = au[t] = 0.0f;
+    for (int i = 0; i * 64 < ng; i++) {
+        int gi = lane + 64 * i;
+        const bool own = gi < ng;
+        gi = own ? gi : ng - 1;
+        float qg[8], qu[8], dg, addg, du = 0.0f, addu = 0.0f;
+        codes<FMT, 8>(rows, gi * 8, qg, dg, addg);
+        if (DUAL) codes<FMT, 8>(rows + rbw, gi * 8, qu, du, addu);
+#pragma unroll
+        for (int t = 0; t < TT; t++) {
+            const float4* xp = reinterpret_cast<const float4*>(xsh + t * a.K + gi * 8);
+            const float4 x0 = xp[0], x1 = xp[1];
+            const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            float sg = 0.0f, su = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                sg = fmaf(qg[e], xv[e], sg);
+                if (DUAL) su = fmaf(qu[e], xv[e], su);
+            }
+            float pg = dg * sg, pu = du * su;
+            if (FMT != SLHIP_FMT_Q8_0) {
+                const float xs = xsum[t * per_row + gi];
+                pg = fmaf(addg, xs, pg);
+                if (DUAL) pu = fmaf(addu, xs, pu);
+            }
+            ag[t] += own ? pg : 0.0f;
+            if (DUAL) au[t] += own ? pu : 0.0f;
+        }
     }
-    int64_t tok = a.t0 + tl;
-    tok = tok < a.T ? tok : a.T - 1;
-    if (a.yt == SLHIP_F32)
-        static_cast<float*>(a.y)[tok * a.ys + n] = out;
-    else
-        static_cast<uint16_t*>(a.y)[tok * a.ys + n] = static_cast<uint16_t>(f32_to_bf16_bits(out));
+#pragma unroll
+    for (int t = 0; t < TT; t++) {
+        ag[t] = wave_sum(ag[t]);
+        if (DUAL) au[t] = wave_sum(au[t]);
+    }
+    store_row<TT, DUAL>(a, n, ag, au);
 }
 
 // ---- host dispatch --------------------------------------------------------------------------------
@@ -257,6 +374,85 @@ static int run_dense(MatvecArgs a, bool dual, hipStream_t st)
     return SLHIP_OK;
 }
 
+static int quant_block_bytes(int fmt)
+{
+    switch (fmt) {
+    case SLHIP_FMT_Q8_0: return 34;
+    case SLHIP_FMT_Q4_0: return 18;
+    case SLHIP_FMT_Q4_1: return 20;
+    case SLHIP_FMT_Q5_0: return 22;
+    case SLHIP_FMT_Q5_1: return 24;
+    default: return 0;
+    }
+}
+
+constexpr size_t kMaxLds = 160 * 1024;  // gfx950 LDS per workgroup
+
+static size_t quant_lds(int tt, int64_t K, int64_t wrow, bool dual)
+{
+    return static_cast<size_t>(kMqThreads / 64) * (dual ? 2 : 1) * wrow + static_cast<size_t>(tt) * K * 4 +
+           static_cast<size_t>(tt) * (K / 8) * 4;
+}
+
+template <class Kern>
+static int allow_lds(Kern kernel, size_t lds)
+{
+    if (lds <= 65536) return SLHIP_OK;
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    return e == hipSuccess ? SLHIP_OK : fail(SLHIP_ERR_HIP, "matvec: %zu bytes of LDS refused: %s", lds, hipGetErrorString(e));
+}
+
+template <int FMT, int TT, int CH, bool DUAL>
+static int launch_quant(const MatvecArgs& a, hipStream_t st)
+{
+    const size_t lds = quant_lds(TT, a.K, a.wrow, DUAL);
+    auto kernel = matvec_quant<FMT, TT, CH, DUAL>;
+    const int r = allow_lds(kernel, lds);
+    if (r != SLHIP_OK) return r;
+    const dim3 grid(static_cast<unsigned>((a.N + kMqThreads / 64 - 1) / (kMqThreads / 64)));
+    kernel<<<grid, kMqThreads, lds, st>>>(a);
+    return check_launch("matvec_quant");
+}
+
+template <int FMT, int TT, bool DUAL>
+static int quant_ch(const MatvecArgs& a, int ch, hipStream_t st)
+{
+    switch (ch) {
+    case 4: return launch_quant<FMT, TT, 4, DUAL>(a, st);
+    case 8: return launch_quant<FMT, TT, 8, DUAL>(a, st);
+    default: return launch_quant<FMT, TT, 16, DUAL>(a, st);
+    }
+}
+
+template <int FMT, bool DUAL>
+static int quant_tt(const MatvecArgs& a, int tt, int ch, hipStream_t st)
+{
+    switch (tt) {
+    case 1: return quant_ch<FMT, 1, DUAL>(a, ch, st);
+    case 2: return quant_ch<FMT, 2, DUAL>(a, ch, st);
+    case 4: return quant_ch<FMT, 4, DUAL>(a, ch, st);
+    default: return quant_ch<FMT, 8, DUAL>(a, ch, st);
+    }
+}
+
+template <int FMT>
+static int run_quant(MatvecArgs a, bool dual, hipStream_t st)
+{
+    int tt = 8;
+    while (tt > 1 && (tt / 2 >= a.T || quant_lds(tt, a.K, a.wrow, dual) > kMaxLds)) tt /= 2;
+    if (quant_lds(tt, a.K, a.wrow, dual) > kMaxLds)
+        return fail(SLHIP_ERR_UNSUPPORTED, "matvec: K = %lld does not fit in LDS for this format", static_cast<long long>(a.K));
+    const int64_t per_lane = ((dual ? 2 : 1) * (a.wrow / 16) + 63) / 64;
+    const int ch = per_lane <= 4 ? 4 : per_lane <= 8 ? 8 : 16;
+    for (int64_t t0 = 0; t0 < a.T; t0 += tt) {
+        a.t0 = t0;
+        const int r = dual ? quant_tt<FMT, true>(a, tt, ch, st) : quant_tt<FMT, false>(a, tt, ch, st);
+        if (r != SLHIP_OK) return r;
+    }
+    return SLHIP_OK;
+}
+
 static int matvec_common(int fmt, int dtype_x, int dtype_y, const void* x, int64_t x_stride, int64_t T, int64_t K,
                          const void* wg, const void* wu, int64_t N, void* y, int64_t y_stride, int act, bool dual,
                          slhip_stream stream)
@@ -271,25 +467,33 @@ static int matvec_common(int fmt, int dtype_x, int dtype_y, const void* x, int64
     if ((dtype_x != SLHIP_F32 && dtype_x != SLHIP_BF16) || (dtype_y != SLHIP_F32 && dtype_y != SLHIP_BF16))
         return fail(SLHIP_ERR_UNSUPPORTED, "%s: activations and outputs are f32 or bf16", name);
     if (x_stride < K || y_stride < N) return fail(SLHIP_ERR_INVALID, "%s: a row stride is smaller than the row", name);
-    if (fmt != SLHIP_FMT_F32 && fmt != SLHIP_FMT_F16 && fmt != SLHIP_FMT_BF16)
-        return fail(SLHIP_ERR_UNSUPPORTED, "%s: weight format %d not supported", name, fmt);
-    const int E = fmt == SLHIP_FMT_F32 ? 4 : 8;
-    if (K % E != 0 || K % 4 != 0)
+    const bool dense = fmt == SLHIP_FMT_F32 || fmt == SLHIP_FMT_F16 || fmt == SLHIP_FMT_BF16;
+    const int bb = quant_block_bytes(fmt);
+    if (!dense && bb == 0) return fail(SLHIP_ERR_UNSUPPORTED, "%s: weight format %d not supported", name, fmt);
+    if (dense ? K % 8 != 0 : K % 256 != 0)
         return fail(SLHIP_ERR_UNSUPPORTED, "%s: K = %lld must be a multiple of %d for this weight format", name,
-                    static_cast<long long>(K), E);
-    if (!aligned16(wg) || (dual && !aligned16(wu)) || reinterpret_cast<uintptr_t>(x) % (dtype_x == SLHIP_F32 ? 16 : 8) ||
-        (x_stride % 4) != 0)
-        return fail(SLHIP_ERR_UNSUPPORTED, "%s: weights must be 16-byte aligned and x rows 4-element aligned", name);
-    if (static_cast<int64_t>(K) * 4 > 65536)
+                    static_cast<long long>(K), dense ? 8 : 256);
+    if (!aligned16(wg) || (dual && !aligned16(wu)) || !aligned16(x) || (x_stride % 8) != 0)
+        return fail(SLHIP_ERR_UNSUPPORTED, "%s: weights and x rows must be 16-byte aligned (x stride a multiple of 8)",
+                    name);
+    if (dense && static_cast<int64_t>(K) * 4 > 65536)
         return fail(SLHIP_ERR_UNSUPPORTED, "%s: K = %lld above the staged-activation limit 16384", name,
                     static_cast<long long>(K));
     if (N > 0x7FFFFFFF || T > 0x7FFFFFFF) return fail(SLHIP_ERR_UNSUPPORTED, "%s: shape too large", name);
-    MatvecArgs a{x, x_stride, static_cast<const char*>(wg), static_cast<const char*>(wu),
-                 K * (fmt == SLHIP_FMT_F32 ? 4 : 2), y, y_stride, T, K, N, 0, dtype_x, dtype_y, act};
+    const int64_t wrow = dense ? K * (fmt == SLHIP_FMT_F32 ? 4 : 2) : K / 32 * bb;
+    MatvecArgs a{x, x_stride, static_cast<const char*>(wg), static_cast<const char*>(wu), wrow, y, y_stride,
+                 T, K, N, 0, dtype_x, dtype_y, act};
     hipStream_t st = to_stream(stream);
-    if (fmt == SLHIP_FMT_F32) return run_dense<SLHIP_F32>(a, dual, st);
-    if (fmt == SLHIP_FMT_F16) return run_dense<SLHIP_F16>(a, dual, st);
-    return run_dense<SLHIP_BF16>(a, dual, st);
+    switch (fmt) {
+    case SLHIP_FMT_F32: return run_dense<SLHIP_F32>(a, dual, st);
+    case SLHIP_FMT_F16: return run_dense<SLHIP_F16>(a, dual, st);
+    case SLHIP_FMT_BF16: return run_dense<SLHIP_BF16>(a, dual, st);
+    case SLHIP_FMT_Q8_0: return run_quant<SLHIP_FMT_Q8_0>(a, dual, st);
+    case SLHIP_FMT_Q4_0: return run_quant<SLHIP_FMT_Q4_0>(a, dual, st);
+    case SLHIP_FMT_Q4_1: return run_quant<SLHIP_FMT_Q4_1>(a, dual, st);
+    case SLHIP_FMT_Q5_0: return run_quant<SLHIP_FMT_Q5_0>(a, dual, st);
+    default: return run_quant<SLHIP_FMT_Q5_1>(a, dual, st);
+    }
 }
 
 }  // namespace slhip

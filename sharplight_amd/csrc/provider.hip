@@ -339,13 +339,15 @@ Support supports(const Graph& g, const Node& n)
         if (x.type != DType::F32 && x.type != DType::BF16) return no("MatMul: f32 or bf16 activations");
         if (y.type != DType::F32 && y.type != DType::BF16) return no("MatMul: f32 or bf16 output");
         if (!w.weight || w.dims.size() != 2) return no("MatMul: the second operand must be a weight [N, K]");
-        if (w.type != DType::F32 && w.type != DType::F16 && w.type != DType::BF16)
-            return no("MatMul: f32, f16 or bf16 weights on this provider");
+        const bool dense = w.type == DType::F32 || w.type == DType::F16 || w.type == DType::BF16;
+        const bool blocks = w.type == DType::Q8_0 || w.type == DType::Q4_0 || w.type == DType::Q4_1 ||
+                            w.type == DType::Q5_0 || w.type == DType::Q5_1;
+        if (!dense && !blocks) return no("MatMul: f32, f16, bf16 or Q8_0/Q4_0/Q4_1/Q5_0/Q5_1 weights on this provider");
         if (x.dims.empty() || w.dims[1] != x.last()) return no("MatMul: K mismatch");
         if (y.last() != w.dims[0]) return no("MatMul: output must be [.., N]");
         const int64_t K = x.last();
-        if (K % (w.type == DType::F32 ? 4 : 8) != 0 || K > 16384)
-            return no("MatMul: K must be a multiple of 8 (4 for f32 weights) and at most 16384");
+        if (dense && (K % 8 != 0 || K > 16384)) return no("MatMul: K must be a multiple of 8 and at most 16384");
+        if (blocks && (K % 256 != 0 || K > 16384)) return no("MatMul: block-format K must be a multiple of 256, at most 16384");
         return {true, ""};
     }
     return no("op " + op + " is not on the fused-layer-op path of the HIP provider");
@@ -823,7 +825,7 @@ private:
             const Value& xv = g_.value(u.x);
             const Value& wv = g_.value(u.wg);
             const int64_t K = xv.last(), rows = xv.rows(T), Nw = wv.dims[0];
-            const int fmt = wv.type == DType::F32 ? SLHIP_FMT_F32 : wv.type == DType::F16 ? SLHIP_FMT_F16 : SLHIP_FMT_BF16;
+            const int fmt = format_code(wv.type);
             const int dy = act_code(g_.value(u.y).type);
             if (u.wu >= 0)
                 check(slhip_dual_matvec(u.act, fmt, act_code(xv.type), dy, ptr(u.x), K, rows, K, ptr(u.wg), ptr(u.wu), Nw,

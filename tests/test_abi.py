@@ -178,7 +178,9 @@ def test_matvec_validation():
     with pytest.raises(native.SlhipArgumentError, match="bad activation"):
         native.dual_matvec(7, "bf16", "f32", "f32", FAKE, 1, 64, FAKE, FAKE, 4, FAKE)
     with pytest.raises(native.SlhipNotSupported, match="weight format"):
-        native.matvec("q4_1", "f32", "f32", FAKE, 1, 64, FAKE, 4, FAKE)
+        native.matvec(42, "f32", "f32", FAKE, 1, 64, FAKE, 4, FAKE)
+    with pytest.raises(native.SlhipNotSupported, match="multiple of 256"):
+        native.matvec("q4_1", "f32", "f32", FAKE, 1, 128, FAKE, 4, FAKE)
     with pytest.raises(native.SlhipNotSupported, match="multiple of 8"):
         native.matvec("bf16", "f32", "f32", FAKE, 1, 60, FAKE, 4, FAKE)
     with pytest.raises(native.SlhipNotSupported, match="16384"):

@@ -4,8 +4,10 @@ the activation and Mul -- the reference's FusionTests.SwiGluDualMatvec (tests/Sh
 FusionTests.cs:59-80: the fused dual matvec against the CPU provider, T in 1..140, K 1024 and 256).
 
 Tolerance (f32 sums in a different order): for a dot product with terms x_k w_k the kernel and the oracle
-each stay within 2^-17 * sum_k |x_k w_k| of the exact value (the oracle's own pin), so they are held to
-2^-16 * S of each other; the dual epilogue propagates that through act(g) * u (first order, with act'
+each stay within 2^-17 * S of the exact value (the oracle's own pin), so they are held to 2^-16 * S of each
+other, with S = sum_k |x_k w_k| for dense and Q8_0 weights and, for the formats with an additive term
+(w = q d + a, summed as d * sum x q + a * sum x, the form of the reference's fused Q4_0 dot),
+S = sum_k |x_k| (|q_k d| + |a|); the dual epilogue propagates that through act(g) * u (first order, with act'
 evaluated in f64), plus 1e-5 relative for the activation itself. bf16 outputs: 2 bf16 ulp of the rounded
 reference on top. A one-hot x picks a weight column and must come out exactly."""
 import math
@@ -64,6 +66,22 @@ def _run(fmt, dx, dy, x, raws, N, K, *, act=None, x_stride=None, y_stride=None, 
     return y[:, :N]
 
 
+BLOCK_ADD = {"q4_0": -8, "q5_0": -16}  # additive term OFF * d; q4_1 / q5_1 carry m
+
+
+def _abs_terms(fmt, raw, W):
+    """|q d| + |a| per weight (= |w| for dense and Q8_0 weights): the magnitudes the kernel's sums add."""
+    if fmt in ("f32", "f16", "bf16", "q8_0"):
+        return np.abs(W).astype(np.float64)
+    N, K = W.shape
+    bb = {"q4_0": 18, "q4_1": 20, "q5_0": 22, "q5_1": 24}[fmt]
+    blocks = raw.reshape(N, K // 32, bb)
+    d = blocks[:, :, 0:2].copy().view(np.float16)[..., 0].astype(np.float64)
+    a = BLOCK_ADD[fmt] * d if fmt in BLOCK_ADD else blocks[:, :, 2:4].copy().view(np.float16)[..., 0].astype(np.float64)
+    A = np.repeat(a, 32, axis=1)
+    return np.abs(W.astype(np.float64) - A) + np.abs(A)
+
+
 def _x(dx, T, K, seed):
     x = synth.normal(seed, 9, (T, K), dtype=dx)
     return x, (oracle.from_bf16(x) if dx == "bf16" else x)
@@ -91,6 +109,12 @@ SINGLE_CASES = [  # (fmt, x dtype, y dtype, T, K, N)
     ("f32", "f32", "bf16", 2, 8, 5),        # one vector per row: most lanes clamp
     ("bf16", "f32", "f32", 1, 14336, 24),   # K split over waves
     ("f32", "f32", "f32", 1, 16384, 8),     # the largest staged K
+    ("q8_0", "f32", "f32", 1, 4096, 96),
+    ("q4_0", "f32", "f32", 3, 1024, 96),
+    ("q4_1", "bf16", "f32", 8, 1024, 37),
+    ("q5_0", "f32", "bf16", 9, 256, 40),
+    ("q5_1", "f32", "f32", 16, 4096, 33),
+    ("q8_0", "f32", "f32", 2, 14336, 20),   # a down projection's K: LDS beyond 64 KiB
 ]
 
 
@@ -101,12 +125,14 @@ def test_matvec(device, fmt, dx, dy, T, K, N):
     x, x32 = _x(dx, T, K, seed)
     y = _run(fmt, dx, dy, x, [raw], N, K)
     ref = oracle.matvec(fmt, raw, N, K, x32)
-    S = np.abs(x32).astype(np.float64) @ np.abs(W).astype(np.float64).T
+    S = np.abs(x32).astype(np.float64) @ _abs_terms(fmt, raw, W).T
     _check_single(y, dy, ref, S, f"matvec {fmt}")
 
 
-@pytest.mark.parametrize("fmt", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("fmt", ["f32", "f16", "bf16", "q8_0", "q4_0", "q4_1", "q5_0", "q5_1"])
 def test_one_hot_rows_pick_columns_exactly(device, fmt):
+    """x = e_k: every 8-value group but one sums to zero and the one holds q_k * 1 exactly, so y = d q_k + a
+    exactly -- the dequantized weight -- whatever the summation order."""
     N, K = 29, 2048
     raw, W = _weights(fmt, N, K, 3, 1)
     ks = [0, 7, 511, 512, 2047]
@@ -127,6 +153,12 @@ DUAL_CASES = [  # (act, fmt, x dtype, y dtype, T, K, N): FusionTests.SwiGluDualM
     ("gelu_tanh", "bf16", "f32", "f32", 1, 4096, 64),
     ("gelu_erf", "f16", "f32", "f32", 4, 4096, 64),
     ("silu", "bf16", "bf16", "bf16", 1, 4096, 14336),  # the Llama-3-8B decode FFN (C3's model)
+    ("silu", "q8_0", "f32", "f32", 1, 1024, 96),
+    ("silu", "q8_0", "f32", "f32", 9, 1024, 96),
+    ("silu", "q4_0", "f32", "f32", 1, 4096, 14336),
+    ("gelu_tanh", "q4_1", "f32", "bf16", 3, 1024, 96),
+    ("silu", "q5_0", "bf16", "f32", 20, 256, 40),
+    ("gelu_erf", "q5_1", "f32", "f32", 4, 2048, 64),
 ]
 
 
@@ -141,11 +173,18 @@ def test_dual_matvec(device, act, fmt, dx, dy, T, K, N):
     u = oracle.matvec(fmt, ru, N, K, x32)
     ref = oracle.mul(oracle.unary(act, g), u)
     ax = np.abs(x32).astype(np.float64)
-    Sg = ax @ np.abs(Wg).astype(np.float64).T
-    Su = ax @ np.abs(Wu).astype(np.float64).T
+    Sg = ax @ _abs_terms(fmt, rg, Wg).T
+    Su = ax @ _abs_terms(fmt, ru, Wu).T
     g64 = g.astype(np.float64)
     h = 1e-4 * np.maximum(1.0, np.abs(g64))
     dact = (_act64(act, g64 + h) - _act64(act, g64 - h)) / (2 * h)
+    # the slope of the implemented activation too: where the reference's erf rational is clamped (|g| > 5.4)
+    # 1 + erf(g) is a constant, so GELU-erf is linear in g there, unlike the exact function
+    h2 = 1e-3 * np.maximum(1.0, np.abs(g64))
+    gp, gm = (g64 + h2).astype(np.float32), (g64 - h2).astype(np.float32)
+    dimpl = (oracle.unary(act, gp).astype(np.float64) - oracle.unary(act, gm).astype(np.float64)) / (
+        gp.astype(np.float64) - gm.astype(np.float64))
+    dact = np.maximum(np.abs(dact), 1.5 * np.abs(dimpl))
     e = 2.0 ** -16
     tol = np.abs(dact * u) * e * Sg + np.abs(_act64(act, g64)) * e * Su + 1e-5 * np.abs(ref) + 1e-30
     if dy == "bf16":
@@ -155,7 +194,10 @@ def test_dual_matvec(device, act, fmt, dx, dy, T, K, N):
     else:
         got, r = y.astype(np.float64), ref.astype(np.float64)
     bad = np.abs(got - r) > tol
-    assert not bad.any(), f"{bad.sum()} of {bad.size} beyond the bound; first at {np.argwhere(bad)[0]}"
+    if bad.any():
+        i = tuple(np.argwhere(bad)[0])
+        raise AssertionError(f"{bad.sum()} of {bad.size} beyond the bound; first at {i}: got {got[i]!r} ref {r[i]!r} "
+                             f"tol {tol[i]!r} g {g[i]!r} u {u[i]!r} Sg {Sg[i]!r} Su {Su[i]!r}")
 
 
 def test_strided_rows(device):
@@ -164,7 +206,7 @@ def test_strided_rows(device):
     fmt, T, K, N = "bf16", 5, 1024, 50
     raw, W = _weights(fmt, N, K, 4, 1)
     x, x32 = _x("f32", T, K, 4)
-    y = _run(fmt, "f32", "f32", x, [raw], N, K, x_stride=K + 12, y_stride=N + 7)
+    y = _run(fmt, "f32", "f32", x, [raw], N, K, x_stride=K + 16, y_stride=N + 7)
     S = np.abs(x32).astype(np.float64) @ np.abs(W).astype(np.float64).T
     _check_single(y, "f32", oracle.matvec(fmt, raw, N, K, x32), S, "strided")
 

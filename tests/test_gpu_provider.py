@@ -75,7 +75,8 @@ def test_residual_add_rmsnorm_fuses(dev, h_is_output):
             assert_bf16_close(seg.get_output(h), href, ulp=0, what="h")
 
 
-@pytest.mark.parametrize("fmt,T,swap", [("bf16", 1, False), ("f16", 3, True), ("f32", 9, False)])
+@pytest.mark.parametrize("fmt,T,swap", [("bf16", 1, False), ("f16", 3, True), ("f32", 9, False), ("q8_0", 1, False),
+                                        ("q4_0", 3, True)])
 def test_swiglu_dual_matvec_fuses(dev, fmt, T, swap):
     """FusionTests.SwiGluDualMatvec (FusionTests.cs:59-80): Mul(Silu(x Wg^T), x Wu^T) is one dual matvec launch
     (in either operand order), within the f32 dot-product bound of the unfused CPU computation."""
@@ -99,11 +100,17 @@ def test_swiglu_dual_matvec_fuses(dev, fmt, T, swap):
         got = seg.get_output(y).astype(np.float64)
     gr, ur = oracle.matvec(fmt, rg, N, K, xs), oracle.matvec(fmt, ru, N, K, xs)
     ref = oracle.mul(oracle.unary("silu", gr), ur).astype(np.float64)
-    Wg = oracle.dequant(fmt, rg.reshape(-1), N * K).reshape(N, K).astype(np.float64)
-    Wu = oracle.dequant(fmt, ru.reshape(-1), N * K).reshape(N, K).astype(np.float64)
     ax = np.abs(xs).astype(np.float64)
-    # |d(silu)/dg| <= 1.1 everywhere: a first-order bound of the two products' rounding, plus the epilogue's
-    tol = 2.0 ** -16 * (1.1 * np.abs(ur) * (ax @ np.abs(Wg).T) + np.abs(gr) * (ax @ np.abs(Wu).T)) + 1e-5 * np.abs(ref)
+    # |d(silu)/dg| <= 1.1 everywhere: a first-order bound of the two products' rounding, plus the epilogue's;
+    # block formats with an additive term add |a| per weight to the magnitudes summed (Q4_0: 8 |d|)
+    def mags(raw):
+        W = oracle.dequant(fmt, raw.reshape(-1), N * K).reshape(N, K).astype(np.float64)
+        if fmt != "q4_0":
+            return np.abs(W)
+        d = raw.reshape(N, K // 32, 18)[:, :, 0:2].copy().view(np.float16)[..., 0].astype(np.float64)
+        A = np.repeat(-8.0 * d, 32, axis=1)
+        return np.abs(W - A) + np.abs(A)
+    tol = 2.0 ** -16 * (1.1 * np.abs(ur) * (ax @ mags(rg).T) + np.abs(gr) * (ax @ mags(ru).T)) + 1e-5 * np.abs(ref)
     assert (np.abs(got - ref) <= tol + 1e-30).all()
 
 

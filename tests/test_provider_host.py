@@ -138,11 +138,14 @@ def test_matmul_support_answers():
     wb = g.weight("bf16", 16, 64)
     w60 = g.weight("bf16", 16, 60)
     x60 = g.input("f32", "T", 60)
-    g.matmul(x, wq)                          # 0: quantized weights -> no (not yet on this provider)
+    g.matmul(x, wq)                          # 0: Q8_0 with K = 64 -> no (block formats need K % 256 == 0)
     g.matmul(x, wb)                          # 1: yes
     g.matmul(x60, w60)                       # 2: K not a multiple of 8 -> no
     g.emit("MatMul", [x, x60], "f32", ("T", 64))  # 3: second operand not a weight [N, K] -> no
-    expect = [False, True, False, False]
+    x256 = g.input("f32", "T", 256)
+    g.matmul(x256, g.weight("q4_0", 16, 256))     # 4: yes
+    g.matmul(x256, g.weight("i32", 16, 256))      # 5: integer weights -> no
+    expect = [False, True, False, False, True, False]
     for k, e in enumerate(expect):
         ok, why = _supports(g, k)
         assert ok == e, (k, why)
