@@ -88,6 +88,55 @@ __device__ __forceinline__ void stage_x(const MatvecArgs& a, float* xsh, float* 
     }
 }
 
+// Stages activation rows t0 .. t0+TT-1 for the block-format kernel: each 32-value block of x at a stride of
+// 36 floats ([TT][K/32][36] f32; the pad makes lanes that read consecutive blocks hit distinct LDS banks), and
+// the sum of each block, [TT][K/32]. Two blocks per thread per pass.
+template <int TT>
+__device__ __forceinline__ void stage_x_blocks(const MatvecArgs& a, float* xsh, float* xsum, int threads)
+{
+    const int per_row = static_cast<int>(a.K / 32);
+    const int units = TT * per_row;
+    for (int base = 0; base < units; base += 2 * threads) {
+        float v[2][32];
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            if (base + q * threads >= units) break;
+            int u = base + q * threads + static_cast<int>(threadIdx.x);
+            u = u < units ? u : units - 1;
+            const int t = u / per_row;
+            const int c = u - t * per_row;
+            int64_t tok = a.t0 + t;
+            tok = tok < a.T ? tok : a.T - 1;
+            if (a.xt == SLHIP_F32) {
+                const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(a.x) + tok * a.xs + c * 32);
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    const float4 f = p[k];
+                    v[q][4 * k] = f.x; v[q][4 * k + 1] = f.y; v[q][4 * k + 2] = f.z; v[q][4 * k + 3] = f.w;
+                }
+            } else {
+                const uint4* p = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.x) + tok * a.xs + c * 32);
+#pragma unroll
+                for (int k = 0; k < 4; k++) Vec<SLHIP_BF16>::unpack(p[k], v[q] + 8 * k);
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            if (base + q * threads >= units) break;
+            int u = base + q * threads + static_cast<int>(threadIdx.x);
+            u = u < units ? u : units - 1;
+            float4* d = reinterpret_cast<float4*>(xsh + u * 36);
+            float sum = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                d[k] = make_float4(v[q][4 * k], v[q][4 * k + 1], v[q][4 * k + 2], v[q][4 * k + 3]);
+                sum += (v[q][4 * k] + v[q][4 * k + 1]) + (v[q][4 * k + 2] + v[q][4 * k + 3]);
+            }
+            xsum[u] = sum;
+        }
+    }
+}
+
 // The epilogue of a wave holding the reduced sums of row n for tokens t0 .. t0+TT-1 (every lane holds all of
 // them): act(g) * u for a dual matvec, else g, stored for each token by every lane (identical values to one
 // address; a per-lane choice of token would be a dynamically indexed register array, i.e. scratch memory).
@@ -213,31 +262,31 @@ __global__ __launch_bounds__(kMvThreads) void matvec_dense(MatvecArgs a, int wpr
     store_row<TT, DUAL>(a, n, ag, au);
 }
 
-// Quantized weights (Q8_0, Q4_0, Q4_1, Q5_0, Q5_1): a block of 4 waves, one row (pair) per wave. Each wave
-// copies its rows' block images into LDS with 16-byte loads (the blocks are only 2-byte aligned), the block
-// stages x and the sum of every 8 x values, then each lane walks 8-value groups: with the block's scale d
-// and additive term (OFF * d or m), sum_k x_k (q_k d + add) = d * sum x q + add * sum x, the form of the
+// Quantized weights (Q8_0, Q4_0, Q4_1, Q5_0, Q5_1): persistent blocks of 4 waves; each wave walks row
+// (pairs) n, n + 4 * gridDim.x, ... . A row's block images go to the wave's own LDS region with 16-byte loads
+// (the blocks are only 2-byte aligned); the loads of the next row (pair) are issued before the current one
+// is computed, so their latency hides behind that work. The block stages x (32-value blocks padded to 36
+// floats) and the sum of every x block once. Each lane takes whole blocks: with the block's scale d and
+// additive term (OFF * d or m), sum_k x_k (q_k d + add) = d * sum x q + add * sum x, the form of the
 // reference's fused Q4_0 dot (Quant.cs:770-803).
 constexpr int kMqThreads = 256;
 
 template <int FMT, int TT, int CH, bool DUAL>
 __global__ __launch_bounds__(kMqThreads) void matvec_quant(MatvecArgs a)
 {
-    using F = Fmt<FMT>;
     extern __shared__ uint32_t smem[];
     constexpr int R = DUAL ? 2 : 1;
     const int lane = threadIdx.x & 63;
     const int wave = wave_id();
-    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * (kMqThreads / 64) + wave;
-    const int64_t n = n0 < a.N ? n0 : a.N - 1;
     const int nch = static_cast<int>(a.wrow / 16);  // 16-byte chunks per row
     const int rbw = nch * 4;                         // words per row
     uint32_t* rows = smem + wave * R * rbw;
     float* xsh = reinterpret_cast<float*>(smem + (kMqThreads / 64) * R * rbw);
-    float* xsum = xsh + TT * a.K;
+    const int nb = static_cast<int>(a.K / 32);  // blocks per row
+    float* xsum = xsh + TT * nb * 36;
 
     const int tot = R * nch;
-    auto load_batch = [&](int base, uint4* v) {
+    auto load_batch = [&](int64_t n, int base, uint4* v) {
 #pragma unroll
         for (int c = 0; c < CH; c++) {
             if (base + c * 64 >= tot) break;  // wave-uniform
@@ -257,56 +306,79 @@ __global__ __launch_bounds__(kMqThreads) void matvec_quant(MatvecArgs a)
             reinterpret_cast<uint4*>(rows)[idx] = v[c];
         }
     };
+    auto rest = [&](int64_t n, uint4* v) {  // batches after the first, loaded and stored in turn
+        for (int base = CH * 64; base < tot; base += CH * 64) {
+            load_batch(n, base, v);
+            store_batch(base, v);
+        }
+    };
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * (kMqThreads / 64);
+    int64_t n = static_cast<int64_t>(blockIdx.x) * (kMqThreads / 64) + wave;
+    const int64_t n_first = n < a.N ? n : a.N - 1;
     uint4 v[CH];
-    load_batch(0, v);
+    load_batch(n_first, 0, v);
     __builtin_amdgcn_sched_barrier(0);  // the weight loads go out before the staging loads
-    stage_x<TT, true>(a, xsh, xsum, kMqThreads);
+    stage_x_blocks<TT>(a, xsh, xsum, kMqThreads);
     store_batch(0, v);
-    for (int base = CH * 64; base < tot; base += CH * 64) {
-        load_batch(base, v);
-        store_batch(base, v);
-    }
+    rest(n_first, v);
     __syncthreads();
 
-    const int ng = static_cast<int>(a.K / 8);
-    const int per_row = ng;
-    float ag[TT], au[TT];
+    for (; n < a.N; n += stride) {  // wave-uniform
+        const int64_t next = n + stride;
+        const bool more = next < a.N;
+        if (more) load_batch(next, 0, v);
+        float ag[TT], au[TT];
 #pragma unroll
-    for (int t = 0; t < TT; t++) ag[t] = au[t] = 0.0f;
-    for (int i = 0; i * 64 < ng; i++) {
-        int gi = lane + 64 * i;
-        const bool own = gi < ng;
-        gi = own ? gi : ng - 1;
-        float qg[8], qu[8], dg, addg, du = 0.0f, addu = 0.0f;
-        codes<FMT, 8>(rows, gi * 8, qg, dg, addg);
-        if (DUAL) codes<FMT, 8>(rows + rbw, gi * 8, qu, du, addu);
+        for (int t = 0; t < TT; t++) ag[t] = au[t] = 0.0f;
+        // One block of both rows for every token; OWN false: a lane past the row's end adds nothing.
+        // One row's block for every token (Q8_0's 32 code bytes take 8 registers per row, so the rows of a
+        // pair go one after the other rather than side by side).
+        auto row_block = [&](const uint32_t* img, int b, bool own, float* acc) {
+            const BlockWords<FMT> bw = block_words<FMT>(img, b);
+            float sx[TT];
+#pragma unroll
+            for (int t = 0; t < TT; t++) sx[t] = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                float q[8];
+                block_codes8<FMT>(bw, j, q);
+#pragma unroll
+                for (int t = 0; t < TT; t++) {
+                    const float4* xp = reinterpret_cast<const float4*>(xsh + (t * nb + b) * 36 + 8 * j);
+                    const float4 x0 = xp[0], x1 = xp[1];
+                    const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+                    for (int e = 0; e < 8; e++) sx[t] = fmaf(q[e], xv[e], sx[t]);
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < TT; t++) {
+                float p = bw.d * sx[t];
+                if (FMT != SLHIP_FMT_Q8_0) p = fmaf(bw.add, xsum[t * nb + b], p);
+                acc[t] += own ? p : 0.0f;
+            }
+        };
+        auto block = [&](int b, bool own) {
+            row_block(rows, b, own, ag);
+            if (DUAL) row_block(rows + rbw, b, own, au);
+        };
+        const int full = nb / 64;  // iterations in which every lane has a block
+        for (int i = 0; i < full; i++) block(lane + 64 * i, true);
+        if (full * 64 < nb) {  // wave-uniform
+            const int b = lane + 64 * full;
+            block(b < nb ? b : nb - 1, b < nb);
+        }
 #pragma unroll
         for (int t = 0; t < TT; t++) {
-            const float4* xp = reinterpret_cast<const float4*>(xsh + t * a.K + gi * 8);
-            const float4 x0 = xp[0], x1 = xp[1];
-            const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-            float sg = 0.0f, su = 0.0f;
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                sg = fmaf(qg[e], xv[e], sg);
-                if (DUAL) su = fmaf(qu[e], xv[e], su);
-            }
-            float pg = dg * sg, pu = du * su;
-            if (FMT != SLHIP_FMT_Q8_0) {
-                const float xs = xsum[t * per_row + gi];
-                pg = fmaf(addg, xs, pg);
-                if (DUAL) pu = fmaf(addu, xs, pu);
-            }
-            ag[t] += own ? pg : 0.0f;
-            if (DUAL) au[t] += own ? pu : 0.0f;
+            ag[t] = wave_sum(ag[t]);
+            if (DUAL) au[t] = wave_sum(au[t]);
+        }
+        store_row<TT, DUAL>(a, n, ag, au);
+        if (more) {
+            store_batch(0, v);
+            rest(next, v);
         }
     }
-#pragma unroll
-    for (int t = 0; t < TT; t++) {
-        ag[t] = wave_sum(ag[t]);
-        if (DUAL) au[t] = wave_sum(au[t]);
-    }
-    store_row<TT, DUAL>(a, n, ag, au);
 }
 
 // ---- host dispatch --------------------------------------------------------------------------------
@@ -388,10 +460,22 @@ static int quant_block_bytes(int fmt)
 
 constexpr size_t kMaxLds = 160 * 1024;  // gfx950 LDS per workgroup
 
+static int device_cus()
+{
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            cus <= 0)
+            cus = 256;
+    }
+    return cus;
+}
+
 static size_t quant_lds(int tt, int64_t K, int64_t wrow, bool dual)
 {
-    return static_cast<size_t>(kMqThreads / 64) * (dual ? 2 : 1) * wrow + static_cast<size_t>(tt) * K * 4 +
-           static_cast<size_t>(tt) * (K / 8) * 4;
+    return static_cast<size_t>(kMqThreads / 64) * (dual ? 2 : 1) * wrow + static_cast<size_t>(tt) * (K / 32) * 36 * 4 +
+           static_cast<size_t>(tt) * (K / 32) * 4;
 }
 
 template <class Kern>
@@ -410,7 +494,12 @@ static int launch_quant(const MatvecArgs& a, hipStream_t st)
     auto kernel = matvec_quant<FMT, TT, CH, DUAL>;
     const int r = allow_lds(kernel, lds);
     if (r != SLHIP_OK) return r;
-    const dim3 grid(static_cast<unsigned>((a.N + kMqThreads / 64 - 1) / (kMqThreads / 64)));
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kMqThreads, lds) != hipSuccess || per_cu < 1)
+        per_cu = 1;
+    const int64_t blocks = (a.N + kMqThreads / 64 - 1) / (kMqThreads / 64);
+    const int64_t resident = static_cast<int64_t>(device_cus()) * per_cu;
+    const dim3 grid(static_cast<unsigned>(blocks < resident ? blocks : resident));
     kernel<<<grid, kMqThreads, lds, st>>>(a);
     return check_launch("matvec_quant");
 }
@@ -421,6 +510,7 @@ static int quant_ch(const MatvecArgs& a, int ch, hipStream_t st)
     switch (ch) {
     case 4: return launch_quant<FMT, TT, 4, DUAL>(a, st);
     case 8: return launch_quant<FMT, TT, 8, DUAL>(a, st);
+    case 12: return launch_quant<FMT, TT, 12, DUAL>(a, st);
     default: return launch_quant<FMT, TT, 16, DUAL>(a, st);
     }
 }
@@ -444,7 +534,7 @@ static int run_quant(MatvecArgs a, bool dual, hipStream_t st)
     if (quant_lds(tt, a.K, a.wrow, dual) > kMaxLds)
         return fail(SLHIP_ERR_UNSUPPORTED, "matvec: K = %lld does not fit in LDS for this format", static_cast<long long>(a.K));
     const int64_t per_lane = ((dual ? 2 : 1) * (a.wrow / 16) + 63) / 64;
-    const int ch = per_lane <= 4 ? 4 : per_lane <= 8 ? 8 : 16;
+    const int ch = per_lane <= 4 ? 4 : per_lane <= 8 ? 8 : per_lane <= 12 ? 12 : 16;
     for (int64_t t0 = 0; t0 < a.T; t0 += tt) {
         a.t0 = t0;
         const int r = dual ? quant_tt<FMT, true>(a, tt, ch, st) : quant_tt<FMT, false>(a, tt, ch, st);

@@ -46,6 +46,63 @@ __device__ __forceinline__ float half_at(const uint32_t* s, int off)
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(lds_u16(s, off))));
 }
 
+// A whole block of a row image in LDS for a dot product: its scale d, additive term (OFF * d, or m) and the
+// raw code words -- Q8_0: 8 words of int8 codes; Q4_x: 4 words of nibble pairs; Q5_x: the same plus the 32
+// fifth bits in hi.
+template <int FMT> struct BlockWords {
+    float d, add;
+    uint32_t w[FMT == SLHIP_FMT_Q8_0 ? 8 : 4];
+    uint32_t hi;
+};
+
+template <int FMT>
+__device__ __forceinline__ BlockWords<FMT> block_words(const uint32_t* s, int b)
+{
+    using F = Fmt<FMT>;
+    BlockWords<FMT> r;
+    const int o = b * F::BB;
+    r.d = half_at(s, o);
+    r.add = FMT == SLHIP_FMT_Q8_0 ? 0.0f : F::M ? half_at(s, o + 2) : static_cast<float>(F::OFF) * r.d;
+    constexpr int NW = FMT == SLHIP_FMT_Q8_0 ? 8 : 4;
+    // NW + 1 aligned words cover the NW words at the (even) byte offset o + QS
+    const int q0 = o + F::QS;
+    const int i0 = q0 >> 2;
+    const uint32_t sh = (q0 & 3) * 8;
+    uint32_t raw[NW + 1];
+#pragma unroll
+    for (int k = 0; k <= NW; k++) raw[k] = s[i0 + k];
+#pragma unroll
+    for (int k = 0; k < NW; k++) r.w[k] = __builtin_amdgcn_alignbit(raw[k + 1], raw[k], sh);
+    r.hi = F::QH >= 0 ? lds_u32(s, o + (F::QH >= 0 ? F::QH : 0)) : 0u;
+    return r;
+}
+
+// The codes of values 8j .. 8j+7 of a block as floats (j = 0..3).
+template <int FMT>
+__device__ __forceinline__ void block_codes8(const BlockWords<FMT>& bw, int j, float* q)
+{
+    using F = Fmt<FMT>;
+    if (FMT == SLHIP_FMT_Q8_0) {
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            q[e] = static_cast<float>(static_cast<int8_t>(bw.w[2 * j + (e >> 2)] >> (8 * (e & 3))));
+        return;
+    }
+    // value k < 16: low nibble of byte k; k >= 16: high nibble of byte k - 16
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const uint32_t word = bw.w[2 * (j & 1) + h];
+        uint32_t nib = (j >= 2 ? word >> 4 : word) & 0x0F0F0F0Fu;
+        if (F::QH < 0) asm("" : "+v"(nib));  // see codes(): keeps one byte conversion per value
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            uint32_t v = (nib >> (8 * e)) & 0xFFu;
+            if (F::QH >= 0) v |= ((bw.hi >> (8 * j + 4 * h + e)) & 1u) << 4;
+            q[4 * h + e] = static_cast<float>(v);
+        }
+    }
+}
+
 // Decodes N (4 or 8) consecutive values starting at value j0 (a multiple of N) of the chunk in LDS.
 // The codes of N (4 or 8) consecutive values starting at value j0 (a multiple of N) of the row image in LDS,
 // as floats, with their block's scale d and additive term (OFF * d, or m): value = fma(q, d, add).
@@ -87,9 +144,14 @@ __device__ __forceinline__ void codes(const uint32_t* s, int j0, float* q, float
     // Four nibbles at once: rotating the word by the nibble shift and masking leaves one value per byte,
     // which converts with a single byte-to-float instruction (the rotate keeps the compiler from folding
     // the mask back into one bit-field extract per value).
+    // The empty asm hides that the masked bytes' high nibbles are zero: knowing it, the compiler would turn
+    // each byte conversion back into a bit-field extract plus a conversion.
     uint32_t nib[2];
 #pragma unroll
-    for (int h = 0; h < N / 4; h++) nib[h] = __builtin_amdgcn_alignbit(b[h], b[h], shift) & 0x0F0F0F0Fu;
+    for (int h = 0; h < N / 4; h++) {
+        nib[h] = __builtin_amdgcn_alignbit(b[h], b[h], shift) & 0x0F0F0F0Fu;
+        if (F::QH < 0) asm("" : "+v"(nib[h]));
+    }
 #pragma unroll
     for (int e = 0; e < N; e++) {
         uint32_t v = (nib[e >> 2] >> (8 * (e & 3))) & 0xFFu;
