@@ -340,7 +340,11 @@ void orc_rope(const float* x, const int32_t* pos, const float* ff, float* y, int
 /* ------------------------------------------------------------------------------------------ */
 
 /* Quant.BlockSize / BlockBytes (src/Sharplight.Cpu/Quant.cs:181-216) for the formats here. */
-static int block_size(int fmt) { return fmt >= ORC_Q8_0 ? 32 : 1; }
+static int block_size(int fmt)
+{
+    if (fmt >= ORC_Q2_K && fmt != ORC_IQ4_NL) return 256;
+    return fmt >= ORC_Q8_0 ? 32 : 1;
+}
 static int block_bytes(int fmt)
 {
     switch (fmt) {
@@ -351,6 +355,13 @@ static int block_bytes(int fmt)
     case ORC_Q4_1: return 20;
     case ORC_Q5_0: return 22;
     case ORC_Q5_1: return 24;
+    case ORC_Q2_K: return 84;
+    case ORC_Q3_K: return 110;
+    case ORC_Q4_K: return 144;
+    case ORC_Q5_K: return 176;
+    case ORC_Q6_K: return 210;
+    case ORC_IQ4_NL: return 18;
+    case ORC_IQ4_XS: return 136;
     default: return -1;
     }
 }
@@ -363,6 +374,133 @@ int64_t orc_row_bytes(int fmt, int64_t d)
 }
 
 static inline float rd_h(const uint8_t* p) { return orc_f16_to_f32((uint16_t)(p[0] | (p[1] << 8))); }
+
+/* ---- K-quants and the 4-bit codebook formats ---- */
+
+/* Quant.ScaleMin (Quant.cs:502-516): the 6-bit scale and minimum j (0..7) of the 12 packed bytes q. */
+static void scale_min(int j, const uint8_t* q, int* sc, int* m)
+{
+    if (j < 4) {
+        *sc = q[j] & 63;
+        *m = q[j + 4] & 63;
+    } else {
+        *sc = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+        *m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+    }
+}
+
+/* The IQ4_NL / IQ4_XS codebook (Quant.cs:409), the values ggml's non-linear 4-bit formats define. */
+static const int8_t kIq4Values[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+
+/* One block of a K-quant or codebook format (256 values; IQ4_NL 32):
+ *  Q2_K  (Quant.KQuants.cs:36-66): {scales[16] (lo: scale, hi: min), qs[64], f16 d, f16 dmin};
+ *        value = q2 * (d * scale) - dmin * min, multiply and subtract unfused;
+ *  Q3_K  (:68-107): {hmask[32], qs[64], scales[12] (6-bit, packed), f16 d}; value = (q2 + 4 hbit - 4) *
+ *        (d * (scale - 32));
+ *  Q4_K  (Quant.cs:518-545): {f16 d, f16 dmin, scales[12], qs[128]}; value = fma(q4, d*sc, -(dmin*m));
+ *  Q5_K  (:547-582): {f16 d, f16 dmin, scales[12], qh[32], qs[128]}; the same with a fifth bit from qh;
+ *  Q6_K  (:584-624): {ql[128], qh[64], int8 scales[16], f16 d}; value = fma(q6, s, -32 s), s = d * scale;
+ *  IQ4_NL (:411-425): {f16 d, qs[16]}; value = d * codebook[nibble];
+ *  IQ4_XS (:427-446): {f16 d, u16 scales_h, scales_l[4], qs[128]}; value = (d * (ls - 32)) * codebook[nibble]. */
+static void kblock(int fmt, const uint8_t* p, float* dst)
+{
+    switch (fmt) {
+    case ORC_Q2_K: {
+        const float d = rd_h(p + 80), dmin = rd_h(p + 82);
+        for (int n = 0; n < 2; n++)
+            for (int j = 0; j < 4; j++)
+                for (int h = 0; h < 2; h++) {
+                    const int sc = p[n * 8 + 2 * j + h];
+                    const float dl = d * (float)(sc & 0xF), ml = dmin * (float)(sc >> 4);
+                    for (int i = 0; i < 16; i++) {
+                        const int q = (p[16 + 32 * n + 16 * h + i] >> (2 * j)) & 3;
+                        const float prod = (float)q * dl;
+                        dst[128 * n + 32 * j + 16 * h + i] = prod - ml;
+                    }
+                }
+        break;
+    }
+    case ORC_Q3_K: {
+        int8_t sc[16];
+        for (int s = 0; s < 16; s++) {
+            const int w = s / 4, b = s % 4;
+            const uint8_t a = p[96 + 4 * (w & 1) + b];
+            const int lo4 = w < 2 ? (a & 0xF) : (a >> 4);
+            const int hi2 = (p[104 + b] >> (2 * w)) & 3;
+            sc[s] = (int8_t)(lo4 | (hi2 << 4));
+        }
+        const float dall = rd_h(p + 108);
+        for (int n = 0; n < 2; n++)
+            for (int j = 0; j < 4; j++)
+                for (int h = 0; h < 2; h++) {
+                    const float dl = dall * (float)(sc[n * 8 + 2 * j + h] - 32);
+                    for (int i = 0; i < 16; i++) {
+                        const int low = (p[32 + 32 * n + 16 * h + i] >> (2 * j)) & 3;
+                        const int high = (p[16 * h + i] >> (4 * n + j)) & 1;
+                        const int v = low + 4 * high - 4;
+                        dst[128 * n + 32 * j + 16 * h + i] = (float)v * dl;
+                    }
+                }
+        break;
+    }
+    case ORC_Q4_K:
+    case ORC_Q5_K: {
+        const int k5 = fmt == ORC_Q5_K;
+        const float d = rd_h(p), dmin = rd_h(p + 2);
+        const uint8_t* scales = p + 4;
+        const uint8_t* qh = p + 16;
+        const uint8_t* qs = p + (k5 ? 48 : 16);
+        for (int j = 0; j < 4; j++)
+            for (int half = 0; half < 2; half++) {
+                int sc, m;
+                scale_min(2 * j + half, scales, &sc, &m);
+                const float dl = d * (float)sc, mm = dmin * (float)m;
+                for (int i = 0; i < 32; i++) {
+                    int q = (qs[32 * j + i] >> (4 * half)) & 15;
+                    if (k5) q |= ((qh[i] >> (2 * j + half)) & 1) << 4;
+                    dst[64 * j + 32 * half + i] = fmaf((float)q, dl, -mm);
+                }
+            }
+        break;
+    }
+    case ORC_Q6_K: {
+        const float d = rd_h(p + 208);
+        for (int n = 0; n < 2; n++)
+            for (int r = 0; r < 128; r++) {
+                const int qt = r / 32, i = r % 32, h = i / 16;
+                const uint8_t l = p[64 * n + (qt & 1 ? 32 : 0) + i];
+                const int lo = qt >= 2 ? l >> 4 : l & 15;
+                const int hi = (p[128 + 32 * n + i] >> (2 * qt)) & 3;
+                const float sc = d * (float)(int8_t)p[192 + 8 * n + h + 2 * qt];
+                dst[128 * n + r] = fmaf((float)(lo | (hi << 4)), sc, -32.0f * sc);
+            }
+        break;
+    }
+    case ORC_IQ4_NL: {
+        const float d = rd_h(p);
+        for (int j = 0; j < 16; j++) {
+            dst[j] = d * (float)kIq4Values[p[2 + j] & 0xF];
+            dst[j + 16] = d * (float)kIq4Values[p[2 + j] >> 4];
+        }
+        break;
+    }
+    case ORC_IQ4_XS: {
+        const float d = rd_h(p);
+        const unsigned sh = p[2] | ((unsigned)p[3] << 8);
+        for (int ib = 0; ib < 8; ib++) {
+            const int ls = ((p[4 + ib / 2] >> (4 * (ib % 2))) & 0xF) | (int)(((sh >> (2 * ib)) & 3) << 4);
+            const float dl = d * (float)(ls - 32);
+            const uint8_t* qs = p + 8 + 16 * ib;
+            for (int j = 0; j < 16; j++) {
+                dst[32 * ib + j] = dl * (float)kIq4Values[qs[j] & 0xF];
+                dst[32 * ib + j + 16] = dl * (float)kIq4Values[qs[j] >> 4];
+            }
+        }
+        break;
+    }
+    default: break;
+    }
+}
 
 /* Quant.Dequantize (Quant.cs:242-368) with the block decoders Q4_0/Q8_0 (:384-405),
  * Q4_1/Q5_0/Q5_1 (:449-500) and Simd.StoreI8x16/StoreU8x16 (Simd.cs:699-753): value =
@@ -378,6 +516,13 @@ int orc_dequant(int fmt, const uint8_t* p, int64_t count, float* dst)
         for (int64_t i = 0; i < count; i++) dst[i] = orc_bf16_to_f32((uint16_t)(p[2 * i] | (p[2 * i + 1] << 8)));
         return 0;
     default: break;
+    }
+    if (block_bytes(fmt) < 0) return -1;
+    if (block_size(fmt) == 256 || fmt == ORC_IQ4_NL) {
+        const int bs = block_size(fmt), bb = block_bytes(fmt);
+        if (count % bs) return -1;
+        for (int64_t b = 0; b < count / bs; b++) kblock(fmt, p + b * bb, dst + b * bs);
+        return 0;
     }
     if (count % 32) return -1;
     int64_t nb = count / 32;

@@ -44,7 +44,100 @@ def test_dequant_matches_ggml(quant_fx, fmt):
     assert float(np.sum((src - got) ** 2) / np.sum(src ** 2)) < 0.05  # the fixture is a real quantization
 
 
-@pytest.mark.parametrize("fmt", ["q8_0", "q4_0", "q4_1", "q5_0", "q5_1"])
+# ---- K-quants and the IQ4 codebook formats (GgmlDequantTests, tests/Sharplight.Cpu.Tests/GgmlDequantTests.cs) ----
+
+@pytest.fixture(scope="module")
+def quant_ext_fx():
+    return np.load(os.path.join(GOLDEN, "ggml_quant_ext.npz"))
+
+
+def _ext_records(fx, fmt):
+    return sorted({k[: -len("_shape")] for k in fx.files if k.startswith(fmt + "_") and k.endswith("_shape")})
+
+
+def _same_bits_or_both_nan(a, b):
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    return np.array_equal(a.view(np.uint32), b.view(np.uint32)) or (
+        np.array_equal(np.isnan(a), np.isnan(b)) and np.array_equal(a[~np.isnan(a)].view(np.uint32), b[~np.isnan(b)].view(np.uint32)))
+
+
+@pytest.mark.parametrize("fmt", ["q2_k", "q3_k", "iq4_nl", "iq4_xs"])
+def test_unfused_formats_match_ggml_bit_for_bit(quant_ext_fx, fmt):
+    """The reference decodes these as ggml does (separate multiply and subtract), so ggml's own output in
+    ggml_quant_ext.bin -- blocks quantized from gaussian data and random bytes -- must come out bit for bit
+    (GgmlDequantTests.DequantizeMatchesGgml)."""
+    recs = _ext_records(quant_ext_fx, fmt)
+    assert len(recs) == 2
+    for r in recs:
+        rows, cols = quant_ext_fx[f"{r}_shape"]
+        got = oracle.dequant(fmt, quant_ext_fx[f"{r}_blocks"].reshape(-1), rows * cols).reshape(rows, cols)
+        assert _same_bits_or_both_nan(got, quant_ext_fx[f"{r}_deq"]), r
+
+
+def _k_terms(fmt, blocks, rows, cols):
+    """Per value the magnitudes of the decoder's two terms, |q * scale| + |offset|, recomputed in f64 from the
+    block fields (an independent reading of the K-quant layouts)."""
+    nb = cols // 256
+    b = blocks.reshape(rows, nb, -1)
+    f16 = lambda a: a.copy().view(np.float16)[..., 0].astype(np.float64)
+    out = np.zeros((rows, nb, 256))
+    if fmt in ("q4_k", "q5_k"):
+        d, dmin, sc = f16(b[:, :, 0:2]), f16(b[:, :, 2:4]), b[:, :, 4:16].astype(np.int64)
+        qs = b[:, :, 48:176] if fmt == "q5_k" else b[:, :, 16:144]
+        for j in range(8):
+            if j < 4:
+                s_, m_ = sc[..., j] & 63, sc[..., j + 4] & 63
+            else:
+                s_ = (sc[..., j + 4] & 15) | ((sc[..., j - 4] >> 6) << 4)
+                m_ = (sc[..., j + 4] >> 4) | ((sc[..., j] >> 6) << 4)
+            g, half = j // 2, j % 2
+            q = (qs[:, :, 32 * g:32 * g + 32].astype(np.int64) >> (4 * half)) & 15
+            if fmt == "q5_k":
+                q |= ((b[:, :, 16:48].astype(np.int64) >> j) & 1) << 4
+            out[:, :, 32 * j:32 * j + 32] = np.abs(q * (d * s_)[..., None]) + np.abs((dmin * m_)[..., None])
+    else:  # q6_k
+        d = f16(b[:, :, 208:210])
+        for n in range(2):
+            for r in range(128):
+                qt, i = r // 32, r % 32
+                h = i // 16
+                lo = b[:, :, 64 * n + (32 if qt & 1 else 0) + i].astype(np.int64)
+                lo = lo >> 4 if qt >= 2 else lo & 15
+                hi = (b[:, :, 128 + 32 * n + i].astype(np.int64) >> (2 * qt)) & 3
+                s_ = d * b[:, :, 192 + 8 * n + h + 2 * qt].view(np.int8).astype(np.float64)
+                out[:, :, 128 * n + r] = np.abs((lo | (hi << 4)) * s_) + np.abs(32 * s_)
+    return out.reshape(rows, cols)
+
+
+@pytest.mark.parametrize("fmt", ["q4_k", "q5_k", "q6_k"])
+def test_fused_k_formats_match_ggml_within_one_rounding(quant_ext_fx, quant_fx, fmt):
+    """The reference fuses q * scale + offset (one rounding) where ggml multiplies, then subtracts (two), so the
+    values agree within one rounding of the larger term: |oracle - ggml| <= 2^-24 (|q scale| + |offset|) per
+    value -- far tighter than QuantTests' 1e-5 (QuantTests.cs:58) -- on ggml's blocks and on random bytes."""
+    cases = [(quant_ext_fx, r) for r in _ext_records(quant_ext_fx, fmt)] + [(quant_fx, fmt)]
+    for fx, r in cases:
+        rows, cols = fx[f"{r}_shape"]
+        blocks = fx[f"{r}_blocks"]
+        got = oracle.dequant(fmt, blocks.reshape(-1), rows * cols).reshape(rows, cols).astype(np.float64)
+        ref = fx[f"{r}_deq"].astype(np.float64)
+        fin = np.isfinite(ref)
+        assert np.array_equal(np.isfinite(got), fin), r
+        with np.errstate(invalid="ignore", over="ignore"):  # random-byte blocks hold inf / NaN scales
+            bound = 2.0 ** -24 * _k_terms(fmt, blocks, rows, cols)
+        assert (np.abs(got - ref)[fin] <= bound[fin] * (1 + 1e-12)).all(), r
+        # and most values are the same bits
+        assert np.mean(got[fin] == ref[fin]) > 0.5, r
+
+
+def test_k_quant_fixture_is_a_real_quantization(quant_fx):
+    for fmt in ("q4_k", "q5_k", "q6_k"):
+        rows, cols = quant_fx[f"{fmt}_shape"]
+        got = oracle.dequant(fmt, quant_fx[f"{fmt}_blocks"].reshape(-1), rows * cols).reshape(rows, cols)
+        src = quant_fx[f"{fmt}_src"]
+        assert float(np.sum((src - got) ** 2) / np.sum(src ** 2)) < 0.02, fmt
+
+
+@pytest.mark.parametrize("fmt", ["q8_0", "q4_0", "q4_1", "q5_0", "q5_1", "q4_k", "q5_k", "q6_k"])
 def test_gather_dequantizes_fixture_rows(quant_fx, fmt):
     """QuantTests.GatherDequantizes (QuantTests.cs:71-95): rows [3, 0, 2, 2] of the fixture table."""
     rows, cols = quant_fx[f"{fmt}_shape"]
