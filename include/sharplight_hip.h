@@ -63,7 +63,16 @@ typedef enum slhip_format {
     SLHIP_FMT_Q4_0 = 4, /* 18-byte blocks: f16 d, u8 qs[16] (nibbles)   -> (q-8)*d    */
     SLHIP_FMT_Q4_1 = 5, /* 20-byte blocks: f16 d, f16 m, u8 qs[16]      -> q*d + m    */
     SLHIP_FMT_Q5_0 = 6, /* 22-byte blocks: f16 d, u32 qh, u8 qs[16]     -> (q-16)*d   */
-    SLHIP_FMT_Q5_1 = 7  /* 24-byte blocks: f16 d, f16 m, u32 qh, qs[16] -> q*d + m    */
+    SLHIP_FMT_Q5_1 = 7, /* 24-byte blocks: f16 d, f16 m, u32 qh, qs[16] -> q*d + m    */
+    /* 256-value super-blocks (ggml's K-quants; src/Sharplight.Cpu/Quant.cs:500-624, Quant.KQuants.cs:36-107) */
+    SLHIP_FMT_Q2_K = 8,   /* 84 bytes: scales[16], qs[64], f16 d, f16 dmin   -> q*(d*sc) - dmin*m   */
+    SLHIP_FMT_Q3_K = 9,   /* 110 bytes: hmask[32], qs[64], scales[12], f16 d -> (q-4h)*(d*(sc-32))  */
+    SLHIP_FMT_Q4_K = 10,  /* 144 bytes: f16 d, f16 dmin, scales[12], qs[128] -> fma(q, d*sc, -dmin*m) */
+    SLHIP_FMT_Q5_K = 11,  /* 176 bytes: as Q4_K with qh[32] before qs         */
+    SLHIP_FMT_Q6_K = 12,  /* 210 bytes: ql[128], qh[64], int8 scales[16], f16 d -> fma(q, s, -32 s)   */
+    /* the 4-bit codebook formats (Quant.cs:407-446): value = scale * codebook[nibble] */
+    SLHIP_FMT_IQ4_NL = 13, /* 18-byte blocks of 32: f16 d, qs[16]          */
+    SLHIP_FMT_IQ4_XS = 14  /* 136 bytes per 256: f16 d, u16 scales_h, scales_l[4], qs[128] */
 } slhip_format;
 
 /* Row-norm kinds (StandardOps RmsNorm / L2Norm / LayerNorm). */
@@ -299,9 +308,11 @@ SLHIP_API int slhip_rope(int dtype_in, int dtype_out, const slhip_rope_tensor* t
  * Embedding gather y[i, :] = dequant(table[ids[i], :]) for i < N; table is the [V, row_bytes] image of a
  * [V, D] tensor in `format`. dtype_out: F32 or BF16 (f32 values rounded to nearest even). An id outside
  * [0, V) leaves its output row zero and raises SLHIP_ERR_INDEX at the next slhip_stream_sync.
+ * Formats: F32, F16, BF16, Q8_0, Q4_0, Q4_1, Q5_0, Q5_1 (D a multiple of 32), Q2_K..Q6_K and IQ4_XS (D a
+ * multiple of 256), IQ4_NL (32).
  * Replaces: GatherOp (src/Sharplight.Cpu/GatherOp.cs:22-75) with Quant.Dequantize
- * (src/Sharplight.Cpu/Quant.cs:242-405), and the Vulkan gather (GraphLowerer.Transformer.cs:133-179,
- * Kernels/data.slang:4-37).
+ * (src/Sharplight.Cpu/Quant.cs:242-446,500-624; Quant.KQuants.cs:36-107), and the Vulkan gather
+ * (GraphLowerer.Transformer.cs:133-179, Kernels/data.slang:4-37).
  */
 SLHIP_API int slhip_gather(int format, const void* table, int64_t V, int64_t D, const int32_t* ids, int64_t N,
                            int dtype_out, void* y, int64_t y_stride, slhip_stream stream);

@@ -5,6 +5,8 @@
 // src/Sharplight.Cpu/Simd.cs:699-753): value = fma(q, d, offset) with the block's f16 scale d and
 //   Q8_0: q int8, offset 0       Q4_0: q nibble, offset -8d    Q5_0: q 5-bit, offset -16d
 //   Q4_1: q nibble, offset m     Q5_1: q 5-bit, offset m       F16/BF16/F32: exact conversion
+// and the 256-value K-quants and the IQ4 codebook formats as decode_k (quant.hpp) restates them
+// (Quant.cs:407-446,500-624, Quant.KQuants.cs:36-107).
 // Every product is exact in f32, so the f32 result is bit-exact; a bf16 output is that value rounded
 // to nearest even (Simd.FloatToBFloat, Simd.cs:530-540). fma(q, d, 0) also fixes the sign of a zero
 // (+0 for q = 0), as the reference's FMA does.
@@ -20,6 +22,8 @@
 #include "quant.hpp"
 
 #include <stdlib.h>
+
+#include <type_traits>
 
 namespace slhip {
 
@@ -60,9 +64,10 @@ template <int FMT, int DTO, int CB, int WPB, int RPW>
 __global__ __launch_bounds__(64 * WPB) void gather_quant(GatherArgs a)
 {
     constexpr int BB = Fmt<FMT>::BB;
+    constexpr int BS = Fmt<FMT>::BS;                 // values per block
     constexpr int VPL = 16 / Vec<DTO>::BYTES;       // values per lane per output vector
     constexpr int LOADS = (CB * BB / 16 + 63) / 64;  // 16-byte loads per lane per chunk
-    constexpr int STEPS = (CB * 32 / VPL + 63) / 64;  // output vectors per lane per chunk
+    constexpr int STEPS = (CB * BS / VPL + 63) / 64;  // output vectors per lane per chunk
     constexpr int WORDS = CB * BB / 4 + 4;            // +pad for the 3-word reads at the end
     __shared__ __align__(16) uint32_t lds[WPB][WORDS];
     const int lane = threadIdx.x & 63;
@@ -71,7 +76,7 @@ __global__ __launch_bounds__(64 * WPB) void gather_quant(GatherArgs a)
     const int64_t first = (static_cast<int64_t>(blockIdx.x) * WPB + wave) * RPW;
     if (first >= total) return;
     uint32_t* s = lds[wave];
-    const int64_t nblocks = a.D / 32;
+    const int64_t nblocks = a.D / BS;
 
     // The wave's RPW consecutive items; every id is fetched up front (wave-uniform scalar loads), so the
     // dependent id latency is paid once per wave rather than once per item.
@@ -89,9 +94,9 @@ __global__ __launch_bounds__(64 * WPB) void gather_quant(GatherArgs a)
         it[j].first_chunk = chunk == 0;
         it[j].id = id;
         it[j].nvec16 = nb * BB / 16;  // chunk starts and lengths are multiples of 16 bytes
-        it[j].groups = nb * 32 / VPL;
+        it[j].groups = nb * BS / VPL;
         it[j].src = a.table + (it[j].ok ? id : 0) * a.rb + b0 * BB;  // a bad id reads row 0, stores zeros
-        it[j].yrow = static_cast<char*>(a.y) + (row * a.ys + b0 * 32) * Vec<DTO>::BYTES;
+        it[j].yrow = static_cast<char*>(a.y) + (row * a.ys + b0 * BS) * Vec<DTO>::BYTES;
     }
 
     // Two-stage pipeline: item j + 1's loads are issued before item j is decoded and stored. Loads and
@@ -227,7 +232,22 @@ __global__ __launch_bounds__(256) void gather_scalar(GatherArgs a, int fmt)
             };
             const int64_t blk = j / 32;
             const int k = static_cast<int>(j % 32);
+            auto kv = [&](auto fmt_tag) {  // one value of a K-quant or codebook block
+                constexpr int F = decltype(fmt_tag)::value;
+                const int64_t kb = j / Fmt<F>::BS;
+                const int kk = static_cast<int>(j % Fmt<F>::BS);
+                float f4[4];
+                decode_k<F, 4>(GlobalBytes{p + kb * Fmt<F>::BB}, 0, kk & ~3, f4);
+                return f4[kk & 3];
+            };
             switch (fmt) {
+            case SLHIP_FMT_Q2_K: v = kv(std::integral_constant<int, SLHIP_FMT_Q2_K>{}); break;
+            case SLHIP_FMT_Q3_K: v = kv(std::integral_constant<int, SLHIP_FMT_Q3_K>{}); break;
+            case SLHIP_FMT_Q4_K: v = kv(std::integral_constant<int, SLHIP_FMT_Q4_K>{}); break;
+            case SLHIP_FMT_Q5_K: v = kv(std::integral_constant<int, SLHIP_FMT_Q5_K>{}); break;
+            case SLHIP_FMT_Q6_K: v = kv(std::integral_constant<int, SLHIP_FMT_Q6_K>{}); break;
+            case SLHIP_FMT_IQ4_NL: v = kv(std::integral_constant<int, SLHIP_FMT_IQ4_NL>{}); break;
+            case SLHIP_FMT_IQ4_XS: v = kv(std::integral_constant<int, SLHIP_FMT_IQ4_XS>{}); break;
             case SLHIP_FMT_F32: {
                 uint32_t u = p[4 * j] | (p[4 * j + 1] << 8) | (p[4 * j + 2] << 16) | (static_cast<uint32_t>(p[4 * j + 3]) << 24);
                 v = __uint_as_float(u);
@@ -273,8 +293,21 @@ static int block_bytes(int fmt)
     case SLHIP_FMT_Q4_1: return 20;
     case SLHIP_FMT_Q5_0: return 22;
     case SLHIP_FMT_Q5_1: return 24;
+    case SLHIP_FMT_Q2_K: return 84;
+    case SLHIP_FMT_Q3_K: return 110;
+    case SLHIP_FMT_Q4_K: return 144;
+    case SLHIP_FMT_Q5_K: return 176;
+    case SLHIP_FMT_Q6_K: return 210;
+    case SLHIP_FMT_IQ4_NL: return 18;
+    case SLHIP_FMT_IQ4_XS: return 136;
     default: return -1;
     }
+}
+
+static int block_values(int fmt)
+{
+    if (fmt >= SLHIP_FMT_Q2_K && fmt != SLHIP_FMT_IQ4_NL) return 256;
+    return fmt >= SLHIP_FMT_Q8_0 ? 32 : 1;
 }
 
 static int env_int(const char* name, int dflt)
@@ -303,7 +336,7 @@ static GatherShape gather_shape()
 template <int FMT, int DTO, int CB, int WPB, int RPW>
 static int launch_quant_shape(GatherArgs a, hipStream_t st)
 {
-    a.chunks = (a.D / 32 + CB - 1) / CB;
+    a.chunks = (a.D / Fmt<FMT>::BS + CB - 1) / CB;
     const int64_t waves = (a.N * a.chunks + RPW - 1) / RPW;
     const int64_t blocks = (waves + WPB - 1) / WPB;
     if (blocks > 0x7FFFFFFF) return fail(SLHIP_ERR_UNSUPPORTED, "gather: grid too large");
@@ -311,13 +344,19 @@ static int launch_quant_shape(GatherArgs a, hipStream_t st)
     return check_launch("gather_quant");
 }
 
+// Chunks of 4096 values (large items) or 512 (small ones; only where the chunk is a whole number of
+// 16-byte vectors, which for 256-value blocks of 84, 110 or 210 bytes it is not).
 template <int FMT, int DTO>
 static int launch_quant(const GatherArgs& a, hipStream_t st)
 {
+    constexpr int CBL = 4096 / Fmt<FMT>::BS, CBS = 512 / Fmt<FMT>::BS;
     const GatherShape g = gather_shape();
-    if (!g.large) return g.wpb == 1 ? launch_quant_shape<FMT, DTO, 16, 1, 1>(a, st) : launch_quant_shape<FMT, DTO, 16, 4, 1>(a, st);
-    if (g.rpw == 2) return launch_quant_shape<FMT, DTO, 128, 4, 2>(a, st);
-    return g.wpb == 1 ? launch_quant_shape<FMT, DTO, 128, 1, 1>(a, st) : launch_quant_shape<FMT, DTO, 128, 4, 1>(a, st);
+    if constexpr ((CBS * Fmt<FMT>::BB) % 16 == 0) {
+        if (!g.large)
+            return g.wpb == 1 ? launch_quant_shape<FMT, DTO, CBS, 1, 1>(a, st) : launch_quant_shape<FMT, DTO, CBS, 4, 1>(a, st);
+    }
+    if (g.rpw == 2) return launch_quant_shape<FMT, DTO, CBL, 4, 2>(a, st);
+    return g.wpb == 1 ? launch_quant_shape<FMT, DTO, CBL, 1, 1>(a, st) : launch_quant_shape<FMT, DTO, CBL, 4, 1>(a, st);
 }
 
 template <int FMT, int DTO, int STEPS, int WPB>
@@ -355,6 +394,13 @@ static int dispatch(int fmt, GatherArgs a, hipStream_t st)
         case SLHIP_FMT_Q4_1: return launch_quant<SLHIP_FMT_Q4_1, DTO>(a, st);
         case SLHIP_FMT_Q5_0: return launch_quant<SLHIP_FMT_Q5_0, DTO>(a, st);
         case SLHIP_FMT_Q5_1: return launch_quant<SLHIP_FMT_Q5_1, DTO>(a, st);
+        case SLHIP_FMT_Q2_K: return launch_quant<SLHIP_FMT_Q2_K, DTO>(a, st);
+        case SLHIP_FMT_Q3_K: return launch_quant<SLHIP_FMT_Q3_K, DTO>(a, st);
+        case SLHIP_FMT_Q4_K: return launch_quant<SLHIP_FMT_Q4_K, DTO>(a, st);
+        case SLHIP_FMT_Q5_K: return launch_quant<SLHIP_FMT_Q5_K, DTO>(a, st);
+        case SLHIP_FMT_Q6_K: return launch_quant<SLHIP_FMT_Q6_K, DTO>(a, st);
+        case SLHIP_FMT_IQ4_NL: return launch_quant<SLHIP_FMT_IQ4_NL, DTO>(a, st);
+        case SLHIP_FMT_IQ4_XS: return launch_quant<SLHIP_FMT_IQ4_XS, DTO>(a, st);
         case SLHIP_FMT_F16: return launch_plain<SLHIP_FMT_F16, DTO>(a, st);
         case SLHIP_FMT_BF16: return launch_plain<SLHIP_FMT_BF16, DTO>(a, st);
         case SLHIP_FMT_F32: return launch_plain<SLHIP_FMT_F32, DTO>(a, st);
@@ -377,7 +423,7 @@ extern "C" SLHIP_API int slhip_gather(int format, const void* table, int64_t V, 
     const int bb = block_bytes(format);
     if (bb < 0) return fail(SLHIP_ERR_UNSUPPORTED, "gather: table format %d not supported", format);
     if (V < 0 || D < 0 || N < 0) return fail(SLHIP_ERR_INVALID, "gather: negative shape");
-    const int bs = format >= SLHIP_FMT_Q8_0 ? 32 : 1;
+    const int bs = block_values(format);
     if (D % bs != 0) return fail(SLHIP_ERR_INVALID, "gather: row length %lld is not a multiple of the block size %d", (long long)D, bs);
     if (N == 0 || D == 0) return SLHIP_OK;
     if (!table || !ids || !y) return fail(SLHIP_ERR_INVALID, "gather: null tensor");

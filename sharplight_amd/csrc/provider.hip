@@ -62,7 +62,7 @@ void check(int st)
 
 // ---- graph ---------------------------------------------------------------------------------------------
 
-enum class DType { F32, F16, BF16, I32, Q8_0, Q4_0, Q4_1, Q5_0, Q5_1 };
+enum class DType { F32, F16, BF16, I32, Q8_0, Q4_0, Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS };
 
 struct TypeInfo {
     const char* name;
@@ -74,6 +74,9 @@ const TypeInfo kTypes[] = {
     {"f32", DType::F32, 1, 4},     {"f16", DType::F16, 1, 2},     {"bf16", DType::BF16, 1, 2},
     {"i32", DType::I32, 1, 4},     {"q8_0", DType::Q8_0, 32, 34}, {"q4_0", DType::Q4_0, 32, 18},
     {"q4_1", DType::Q4_1, 32, 20}, {"q5_0", DType::Q5_0, 32, 22}, {"q5_1", DType::Q5_1, 32, 24},
+    {"q2_k", DType::Q2_K, 256, 84}, {"q3_k", DType::Q3_K, 256, 110}, {"q4_k", DType::Q4_K, 256, 144},
+    {"q5_k", DType::Q5_K, 256, 176}, {"q6_k", DType::Q6_K, 256, 210}, {"iq4_nl", DType::IQ4_NL, 32, 18},
+    {"iq4_xs", DType::IQ4_XS, 256, 136},
 };
 
 const TypeInfo& type_info(DType t)
@@ -106,6 +109,13 @@ int format_code(DType t)
     case DType::Q4_1: return SLHIP_FMT_Q4_1;
     case DType::Q5_0: return SLHIP_FMT_Q5_0;
     case DType::Q5_1: return SLHIP_FMT_Q5_1;
+    case DType::Q2_K: return SLHIP_FMT_Q2_K;
+    case DType::Q3_K: return SLHIP_FMT_Q3_K;
+    case DType::Q4_K: return SLHIP_FMT_Q4_K;
+    case DType::Q5_K: return SLHIP_FMT_Q5_K;
+    case DType::Q6_K: return SLHIP_FMT_Q6_K;
+    case DType::IQ4_NL: return SLHIP_FMT_IQ4_NL;
+    case DType::IQ4_XS: return SLHIP_FMT_IQ4_XS;
     default: unsupported("gather table type");
     }
 }

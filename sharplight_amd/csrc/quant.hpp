@@ -11,12 +11,21 @@
 
 namespace slhip {
 
+// BB: bytes per block; BS: values per block; QS / QH: byte offsets of the codes and of the fifth bits;
+// M: an f16 minimum follows d; OFF: the offset in units of d. K: the block is decoded by decode_k.
 template <int FMT> struct Fmt;
-template <> struct Fmt<SLHIP_FMT_Q8_0> { static constexpr int BB = 34, QS = 2, QH = -1; static constexpr bool M = false; static constexpr int OFF = 0; };
-template <> struct Fmt<SLHIP_FMT_Q4_0> { static constexpr int BB = 18, QS = 2, QH = -1; static constexpr bool M = false; static constexpr int OFF = -8; };
-template <> struct Fmt<SLHIP_FMT_Q4_1> { static constexpr int BB = 20, QS = 4, QH = -1; static constexpr bool M = true; static constexpr int OFF = 0; };
-template <> struct Fmt<SLHIP_FMT_Q5_0> { static constexpr int BB = 22, QS = 6, QH = 2; static constexpr bool M = false; static constexpr int OFF = -16; };
-template <> struct Fmt<SLHIP_FMT_Q5_1> { static constexpr int BB = 24, QS = 8, QH = 4; static constexpr bool M = true; static constexpr int OFF = 0; };
+template <> struct Fmt<SLHIP_FMT_Q8_0> { static constexpr int BB = 34, BS = 32, QS = 2, QH = -1; static constexpr bool M = false, K = false; static constexpr int OFF = 0; };
+template <> struct Fmt<SLHIP_FMT_Q4_0> { static constexpr int BB = 18, BS = 32, QS = 2, QH = -1; static constexpr bool M = false, K = false; static constexpr int OFF = -8; };
+template <> struct Fmt<SLHIP_FMT_Q4_1> { static constexpr int BB = 20, BS = 32, QS = 4, QH = -1; static constexpr bool M = true, K = false; static constexpr int OFF = 0; };
+template <> struct Fmt<SLHIP_FMT_Q5_0> { static constexpr int BB = 22, BS = 32, QS = 6, QH = 2; static constexpr bool M = false, K = false; static constexpr int OFF = -16; };
+template <> struct Fmt<SLHIP_FMT_Q5_1> { static constexpr int BB = 24, BS = 32, QS = 8, QH = 4; static constexpr bool M = true, K = false; static constexpr int OFF = 0; };
+template <> struct Fmt<SLHIP_FMT_Q2_K> { static constexpr int BB = 84, BS = 256, QS = 0, QH = -1; static constexpr bool M = false, K = true; static constexpr int OFF = 0; };
+template <> struct Fmt<SLHIP_FMT_Q3_K> { static constexpr int BB = 110, BS = 256, QS = 0, QH = -1; static constexpr bool M = false, K = true; static constexpr int OFF = 0; };
+template <> struct Fmt<SLHIP_FMT_Q4_K> { static constexpr int BB = 144, BS = 256, QS = 0, QH = -1; static constexpr bool M = false, K = true; static constexpr int OFF = 0; };
+template <> struct Fmt<SLHIP_FMT_Q5_K> { static constexpr int BB = 176, BS = 256, QS = 0, QH = -1; static constexpr bool M = false, K = true; static constexpr int OFF = 0; };
+template <> struct Fmt<SLHIP_FMT_Q6_K> { static constexpr int BB = 210, BS = 256, QS = 0, QH = -1; static constexpr bool M = false, K = true; static constexpr int OFF = 0; };
+template <> struct Fmt<SLHIP_FMT_IQ4_NL> { static constexpr int BB = 18, BS = 32, QS = 2, QH = -1; static constexpr bool M = false, K = true; static constexpr int OFF = 0; };
+template <> struct Fmt<SLHIP_FMT_IQ4_XS> { static constexpr int BB = 136, BS = 256, QS = 0, QH = -1; static constexpr bool M = false, K = true; static constexpr int OFF = 0; };
 
 __device__ __forceinline__ uint32_t lds_u16(const uint32_t* s, int off)
 {
@@ -160,14 +169,147 @@ __device__ __forceinline__ void codes(const uint32_t* s, int j0, float* q, float
     }
 }
 
+// Byte access to a block image: in LDS (words) or in global memory. Multi-byte reads are at even offsets.
+struct LdsBytes {
+    const uint32_t* s;
+    __device__ __forceinline__ uint32_t u8(int off) const { return (s[off >> 2] >> (8 * (off & 3))) & 0xFFu; }
+    __device__ __forceinline__ uint32_t u16(int off) const { return lds_u16(s, off); }
+    __device__ __forceinline__ uint32_t u32(int off) const { return lds_u32(s, off); }
+    __device__ __forceinline__ float h(int off) const { return half_at(s, off); }
+};
+
+struct GlobalBytes {
+    const uint8_t* p;
+    __device__ __forceinline__ uint32_t u8(int off) const { return p[off]; }
+    __device__ __forceinline__ uint32_t u16(int off) const { return p[off] | (static_cast<uint32_t>(p[off + 1]) << 8); }
+    __device__ __forceinline__ uint32_t u32(int off) const { return u16(off) | (u16(off + 2) << 16); }
+    __device__ __forceinline__ float h(int off) const
+    {
+        return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(u16(off))));
+    }
+};
+
+// The IQ4 codebook {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113}
+// (src/Sharplight.Cpu/Quant.cs:409) looked up for four nibble bytes at once: v_perm_b32 picks entries
+// 0..7 and 8..15 from the table held as four words, and bit 3 of each nibble selects between them.
+__device__ __forceinline__ uint32_t iq4_lookup4(uint32_t nib4)
+{
+    const uint32_t sel = nib4 & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(0xF6EADDCFu, 0xBFAD9881u, sel);
+    const uint32_t hi = __builtin_amdgcn_perm(0x71594535u, 0x26190D01u, sel);
+    const uint32_t m = ((nib4 >> 3) & 0x01010101u) * 0xFFu;
+    return (hi & m) | (lo & ~m);
+}
+
+// N (4 or 8) consecutive values k .. k+N-1 (k a multiple of N) of the K-quant or codebook block at byte
+// offset o, decoded with the reference's arithmetic (src/Sharplight.Cpu/Quant.cs:407-446,500-624,
+// Quant.KQuants.cs:36-107): the N values share one sub-block scale.
+template <int FMT, int N, class B>
+__device__ __forceinline__ void decode_k(const B& b, int o, int k, float* f)
+{
+    uint32_t w[N / 4];
+    auto words = [&](int off) {
+#pragma unroll
+        for (int h = 0; h < N / 4; h++) w[h] = b.u32(off + 4 * h);
+    };
+    auto byte_of = [&](const uint32_t* ws, int e) { return (ws[e >> 2] >> (8 * (e & 3))) & 0xFFu; };
+    if constexpr (FMT == SLHIP_FMT_Q4_K || FMT == SLHIP_FMT_Q5_K) {
+        const int g = k / 64, half = (k % 64) / 32, i = k % 32, j = 2 * g + half;
+        const int sb = o + 4;
+        uint32_t sc, m;
+        if (j < 4) {
+            sc = b.u8(sb + j) & 63u;
+            m = b.u8(sb + j + 4) & 63u;
+        } else {
+            sc = (b.u8(sb + j + 4) & 0xFu) | ((b.u8(sb + j - 4) >> 6) << 4);
+            m = (b.u8(sb + j + 4) >> 4) | ((b.u8(sb + j) >> 6) << 4);
+        }
+        const float dl = b.h(o) * static_cast<float>(sc), mm = b.h(o + 2) * static_cast<float>(m);
+        words(o + (FMT == SLHIP_FMT_Q5_K ? 48 : 16) + 32 * g + i);
+        uint32_t hw[N / 4];
+        if (FMT == SLHIP_FMT_Q5_K) {
+#pragma unroll
+            for (int h = 0; h < N / 4; h++) hw[h] = (b.u32(o + 16 + i + 4 * h) >> j) & 0x01010101u;
+        }
+#pragma unroll
+        for (int h = 0; h < N / 4; h++) {
+            w[h] = (w[h] >> (4 * half)) & 0x0F0F0F0Fu;
+            if (FMT == SLHIP_FMT_Q5_K) w[h] |= hw[h] << 4;
+        }
+#pragma unroll
+        for (int e = 0; e < N; e++) f[e] = __fmaf_rn(static_cast<float>(byte_of(w, e)), dl, -mm);
+    } else if constexpr (FMT == SLHIP_FMT_Q6_K) {
+        const int n = k / 128, r = k % 128, qt = r / 32, i = r % 32, h = i / 16;
+        words(o + 64 * n + (qt & 1 ? 32 : 0) + i);
+        uint32_t hw[N / 4];
+#pragma unroll
+        for (int x = 0; x < N / 4; x++) hw[x] = (b.u32(o + 128 + 32 * n + i + 4 * x) >> (2 * qt)) & 0x03030303u;
+#pragma unroll
+        for (int x = 0; x < N / 4; x++) w[x] = ((qt >= 2 ? w[x] >> 4 : w[x]) & 0x0F0F0F0Fu) | (hw[x] << 4);
+        const float s = b.h(o + 208) * static_cast<float>(static_cast<int8_t>(b.u8(o + 192 + 8 * n + h + 2 * qt)));
+#pragma unroll
+        for (int e = 0; e < N; e++) f[e] = __fmaf_rn(static_cast<float>(byte_of(w, e)), s, -32.0f * s);
+    } else if constexpr (FMT == SLHIP_FMT_Q2_K || FMT == SLHIP_FMT_Q3_K) {
+        const int n = k / 128, r = k % 128, j = r / 32, h = (r % 32) / 16, i = r % 16;
+        const int si = 8 * n + 2 * j + h;
+        if constexpr (FMT == SLHIP_FMT_Q2_K) {
+            words(o + 16 + 32 * n + 16 * h + i);
+            const uint32_t sc = b.u8(o + si);
+            const float dl = __fmul_rn(b.h(o + 80), static_cast<float>(sc & 0xFu));
+            const float ml = __fmul_rn(b.h(o + 82), static_cast<float>(sc >> 4));
+#pragma unroll
+            for (int x = 0; x < N / 4; x++) w[x] = (w[x] >> (2 * j)) & 0x03030303u;
+#pragma unroll
+            for (int e = 0; e < N; e++) f[e] = __fsub_rn(__fmul_rn(static_cast<float>(byte_of(w, e)), dl), ml);
+        } else {
+            const int ww = si / 4, bb = si % 4;
+            const uint32_t a = b.u8(o + 96 + 4 * (ww & 1) + bb);
+            const uint32_t sc = (ww < 2 ? (a & 0xFu) : (a >> 4)) | (((b.u8(o + 104 + bb) >> (2 * ww)) & 3u) << 4);
+            const float dl = __fmul_rn(b.h(o + 108), static_cast<float>(static_cast<int>(sc) - 32));
+            words(o + 32 + 32 * n + 16 * h + i);
+            uint32_t hw[N / 4];
+#pragma unroll
+            for (int x = 0; x < N / 4; x++) hw[x] = (b.u32(o + 16 * h + i + 4 * x) >> (4 * n + j)) & 0x01010101u;
+#pragma unroll
+            for (int e = 0; e < N; e++) {
+                const int v = static_cast<int>((byte_of(w, e) >> (2 * j)) & 3u) + 4 * static_cast<int>(byte_of(hw, e)) - 4;
+                f[e] = __fmul_rn(static_cast<float>(v), dl);
+            }
+        }
+    } else {  // IQ4_NL, IQ4_XS
+        float dl;
+        int qo, i;
+        if constexpr (FMT == SLHIP_FMT_IQ4_NL) {
+            dl = b.h(o);
+            i = k % 32;
+            qo = o + 2 + (i % 16);
+        } else {
+            const int ib = k / 32;
+            i = k % 32;
+            const uint32_t ls = ((b.u8(o + 4 + ib / 2) >> (4 * (ib % 2))) & 0xFu) | (((b.u16(o + 2) >> (2 * ib)) & 3u) << 4);
+            dl = __fmul_rn(b.h(o), static_cast<float>(static_cast<int>(ls) - 32));
+            qo = o + 8 + 16 * ib + (i % 16);
+        }
+        words(qo);
+#pragma unroll
+        for (int x = 0; x < N / 4; x++) w[x] = iq4_lookup4(((i >= 16) ? w[x] >> 4 : w[x]) & 0x0F0F0F0Fu);
+#pragma unroll
+        for (int e = 0; e < N; e++) f[e] = __fmul_rn(dl, static_cast<float>(static_cast<int8_t>(byte_of(w, e))));
+    }
+}
+
 // Decodes N (4 or 8) consecutive values starting at value j0 (a multiple of N) of the row image in LDS.
 template <int FMT, int N>
 __device__ __forceinline__ void decode(const uint32_t* s, int j0, float* f)
 {
-    float q[N], d, add;
-    codes<FMT, N>(s, j0, q, d, add);
+    if constexpr (Fmt<FMT>::K) {
+        decode_k<FMT, N>(LdsBytes{s}, (j0 / Fmt<FMT>::BS) * Fmt<FMT>::BB, j0 % Fmt<FMT>::BS, f);
+    } else {
+        float q[N], d, add;
+        codes<FMT, N>(s, j0, q, d, add);
 #pragma unroll
-    for (int e = 0; e < N; e++) f[e] = __fmaf_rn(q[e], d, add);
+        for (int e = 0; e < N; e++) f[e] = __fmaf_rn(q[e], d, add);
+    }
 }
 
 }  // namespace slhip

@@ -37,7 +37,14 @@ def normal(seed, tid, shape, mean=0.0, std=1.0, dtype="f32"):
     return bf16_bits(x) if dtype == "bf16" else x
 
 
-BLOCK = {"q8_0": 34, "q4_0": 18, "q4_1": 20, "q5_0": 22, "q5_1": 24}
+BLOCK = {"q8_0": 34, "q4_0": 18, "q4_1": 20, "q5_0": 22, "q5_1": 24, "iq4_nl": 18}
+# 256-value super-blocks: bytes per block, and the byte offsets of their f16 fields (d, dmin)
+KBLOCK = {"q2_k": (84, (80, 82)), "q3_k": (110, (108,)), "q4_k": (144, (0, 2)), "q5_k": (176, (0, 2)),
+          "q6_k": (210, (208,)), "iq4_xs": (136, (0,))}
+
+
+def block_values(fmt: str) -> int:
+    return 256 if fmt in KBLOCK else 32
 
 
 def row_bytes(fmt: str, D: int) -> int:
@@ -45,6 +52,9 @@ def row_bytes(fmt: str, D: int) -> int:
         return 4 * D
     if fmt in ("f16", "bf16"):
         return 2 * D
+    if fmt in KBLOCK:
+        assert D % 256 == 0
+        return D // 256 * KBLOCK[fmt][0]
     assert D % 32 == 0
     return D // 32 * BLOCK[fmt]
 
@@ -52,9 +62,18 @@ def row_bytes(fmt: str, D: int) -> int:
 def quant_table(fmt: str, V: int, D: int, seed: int = 0, tid: int = 0, scale_lo=0.001, scale_hi=0.02):
     """Raw [V, row_bytes] uint8 image of a table in ``fmt``.
 
-    q8_0: int8 codes ~ U{-127..127}; q4_*/q5_*: bytes ~ U{0..255} (so nibbles ~ U{0..15}); scales and
-    mins f16 ~ U[scale_lo, scale_hi]; f16: values N(0,1)*0.02; bf16 / f32: N(0,1)*0.02."""
+    q8_0: int8 codes ~ U{-127..127}; q4_*/q5_*/iq4_nl: bytes ~ U{0..255} (so nibbles ~ U{0..15}); scales and
+    mins f16 ~ U[scale_lo, scale_hi]; K-quants / iq4_xs: random bytes with their f16 fields ~ U[scale_lo,
+    scale_hi] (the packed sub-block scales are any bytes); f16: values N(0,1)*0.02; bf16 / f32: N(0,1)*0.02."""
     g = rng(seed, tid)
+    if fmt in KBLOCK:
+        bb, fields = KBLOCK[fmt]
+        nb = D // 256
+        t = g.integers(0, 256, size=(V, nb, bb), dtype=np.uint8)
+        for f in fields:
+            v = g.uniform(scale_lo, scale_hi, size=(V, nb)).astype(np.float16)
+            t[:, :, f:f + 2] = v.view(np.uint8).reshape(V, nb, 2)
+        return t.reshape(V, nb * bb)
     if fmt in ("f16", "bf16", "f32"):
         x = (g.standard_normal(size=(V, D), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
         if fmt == "f16":
@@ -96,6 +115,8 @@ CONFIGS = {
     "c5_gather_q8_0": Config("c5_gather_q8_0", "gather 16384 ids from Q8_0 [151936,4096] -> bf16"),
     "c5_gather_q4_0": Config("c5_gather_q4_0", "gather 16384 ids from Q4_0 [151936,4096] -> bf16"),
     "c5_gather_f16": Config("c5_gather_f16", "gather 16384 ids from F16 [151936,4096] -> bf16"),
+    "c5_gather_q4_k": Config("c5_gather_q4_k", "gather 16384 ids from Q4_K [151936,4096] -> bf16 (C5 shape, K-quant)"),
+    "c5_gather_q6_k": Config("c5_gather_q6_k", "gather 16384 ids from Q6_K [151936,4096] -> bf16 (C5 shape, K-quant)"),
 }
 
 

@@ -1,6 +1,6 @@
-"""GPU parity of slhip_gather (embedding rows with on-the-fly Q8_0 / Q4_0 / Q4_1 / Q5_0 / Q5_1 / F16 / BF16 /
-F32 dequantization): bit-exact against the oracle's GatherOp, mirroring the reference's GatherTests.cs:147-163
-and QuantTests.cs:49-97."""
+"""GPU parity of slhip_gather (embedding rows with on-the-fly Q8_0 / Q4_0 / Q4_1 / Q5_0 / Q5_1, K-quant
+Q2_K..Q6_K, IQ4_NL / IQ4_XS and F16 / BF16 / F32 dequantization): bit-exact against the oracle's GatherOp,
+mirroring the reference's GatherTests.cs:7-25,147-163, QuantTests.cs:49-97 and GgmlDequantTests."""
 import os
 
 import numpy as np
@@ -55,16 +55,44 @@ def test_ggml_fixture_rows(device, fmt, dout):
         np.testing.assert_array_equal(y, fx[f"{fmt}_deq"][ids])  # ggml's own values (+0 vs -0 aside)
 
 
-@pytest.mark.parametrize("fmt", ["f32", "f16", "bf16", "q8_0", "q4_0", "q4_1", "q5_0", "q5_1"])
+KFMTS = ["q2_k", "q3_k", "q4_k", "q5_k", "q6_k", "iq4_nl", "iq4_xs"]
+
+
+@pytest.mark.parametrize("fmt", ["f32", "f16", "bf16", "q8_0", "q4_0", "q4_1", "q5_0", "q5_1"] + KFMTS)
 @pytest.mark.parametrize("dout", ["f32", "bf16"])
 @pytest.mark.parametrize("D", [32, 256, 4096, 5120, 8192 + 32])
 def test_gather_formats(device, fmt, dout, D):
+    """Every format, both outputs: a single block, whole and partial 4096-value chunks, rows that are not
+    a whole number of 16-byte vectors (the general kernel). 256-value formats take D rounded to 256."""
+    if synth.block_values(fmt) == 256:
+        D = max(256, D // 256 * 256) + (256 if D == 8192 + 32 else 0)
     V, N = 300, 97
     t = synth.quant_table(fmt, V, D, seed=D, tid=0)
     ids = synth.rng(D, 1).integers(0, V, N).astype(np.int32)
     ids[:3] = [0, V - 1, 0]  # first, last, duplicate
     y = _run(fmt, t, V, D, ids, dout)
     assert_bits_equal(y, _ref(fmt, t, V, D, ids, dout), what=f"{fmt}->{dout} D={D}")
+
+
+@pytest.mark.parametrize("fmt", KFMTS)
+@pytest.mark.parametrize("dout", ["f32", "bf16"])
+def test_ggml_ext_fixture_rows(device, fmt, dout):
+    """ggml's own blocks and random bytes (ggml_quant_ext.bin, GgmlDequantTests): every row, bit-exact against
+    the oracle -- whose values are ggml's bit for bit (Q2_K, Q3_K, IQ4_*) or within one rounding (Q4_K..Q6_K)
+    -- including the NaN and infinite scales random bytes produce."""
+    fx = np.load(os.path.join(GOLDEN, "ggml_quant_ext.npz"))
+    for r in sorted({k[:-6] for k in fx.files if k.startswith(fmt + "_") and k.endswith("_shape")}):
+        rows, cols = (int(v) for v in fx[f"{r}_shape"])
+        ids = np.arange(rows, dtype=np.int32)[::-1].copy()
+        y = _run(fmt, fx[f"{r}_blocks"], rows, cols, ids, dout)
+        ref = _ref(fmt, fx[f"{r}_blocks"], rows, cols, ids, dout)
+        # NaNs compare as NaNs: a random-byte block with an infinite scale makes inf * 0 = NaN, whose sign is
+        # the platform's default NaN (negative on x86, where the reference runs; positive on the GPU)
+        yf = y if dout == "f32" else oracle.from_bf16(y)
+        rf = ref if dout == "f32" else oracle.from_bf16(ref)
+        nan = np.isnan(rf)
+        assert np.array_equal(np.isnan(yf), nan), r
+        assert np.array_equal(yf[~nan].view(np.uint32), rf[~nan].view(np.uint32)), r
 
 
 def test_gather_every_f16_code(device):

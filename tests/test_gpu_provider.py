@@ -240,10 +240,11 @@ def test_rope_normal_style_with_freq_factors(dev):
         assert_f32_close(seg.get_output(y), ref, what="gptj rope")
 
 
-@pytest.mark.parametrize("fmt", ["q8_0", "q4_0", "f16"])
+@pytest.mark.parametrize("fmt", ["q8_0", "q4_0", "f16", "q4_k", "q5_k", "q6_k"])
 @pytest.mark.parametrize("out", ["f32", "bf16"])
 def test_gather_graph(dev, fmt, out):
-    """GatherTests.cs:147-163: token embedding from a quantized table; f32 output is the reference's default."""
+    """GatherTests.cs:7-25,147-163: token embedding from a quantized table (the reference's Table cases include
+    q4_k, q5_k and q6_k); f32 output is the reference's default."""
     V, D, N = 300, 4096, 40
     g = GraphBuilder()
     tbl = g.weight(fmt, V, D)
