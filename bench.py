@@ -355,6 +355,7 @@ WORKLOADS = {
     "v_cache_write_f16_paged": lambda: VCache(),
     "dual_matvec_silu_bf16_T1": lambda: DualMatvec(1),
     "dual_matvec_silu_bf16_T4": lambda: DualMatvec(4),
+    "dual_matvec_silu_bf16_T16": lambda: DualMatvec(16),
     "dual_matvec_silu_q8_0_T1": lambda: DualMatvec(1, "q8_0"),
     "dual_matvec_silu_q4_0_T1": lambda: DualMatvec(1, "q4_0"),
     "copy_256MiB": lambda: CopyRef(),
@@ -477,7 +478,7 @@ def cpu_baselines(budget_main: float, budget_op: float, which: set[str]) -> dict
         s, reps = cpu_time(run, budget_op)
         res[name] = dict(s=s * 8192 / rows, reps=reps,
                          sample=f"{rows} of 8192 rows, scaled x{8192 // rows}; Add, RmsNorm, then the {copy} rows")
-    for fmt, T in (("bf16", 1), ("bf16", 4), ("q8_0", 1), ("q4_0", 1)):
+    for fmt, T in (("bf16", 1), ("bf16", 4), ("bf16", 16), ("q8_0", 1), ("q4_0", 1)):
         name = f"dual_matvec_silu_{fmt}_T{T}"
         if name not in which:
             continue

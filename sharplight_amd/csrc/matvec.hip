@@ -381,6 +381,168 @@ __global__ __launch_bounds__(kMqThreads) void matvec_quant(MatvecArgs a)
     }
 }
 
+// bf16 weights at several tokens on the matrix cores: v_mfma_f32_16x16x32_bf16 multiplies a 16-row weight
+// tile (A: lane l holds row l % 16, eight K values of group l / 16) by 16 tokens of x (B: lane l holds token
+// l % 16, the same K values) into a 16 x 16 f32 tile (lane l: rows 4 (l / 16) + i, token l % 16). f32 x is
+// split into three bf16 parts h + m + l = x exactly (each part the round-to-nearest-even of the remainder;
+// f32 has 24 significant bits, bf16 8), so every product w * part is exact and the sums stay f32: the
+// result has the error of f32 accumulation, like the VALU kernel. bf16 x is one part. A block of 8 waves
+// takes a 16-row tile (pair); the waves split K, each lane loading 2 x 16 bytes per row per 64 values (two
+// instructions covering 64 contiguous bytes of 16 rows each); partial tiles meet in LDS.
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(const uint4& v) { return __builtin_bit_cast(bf16x8_t, v); }
+
+// x[0..7] (f32) as three bf16 vectors with h + m + l == x; a non-finite x keeps only h (inf - inf would
+// otherwise make the remainders NaN).
+__device__ __forceinline__ void split3(const float* x, uint4& h, uint4& m, uint4& l)
+{
+    uint32_t hw[4], mw[4], lw[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float a0 = x[2 * i], a1 = x[2 * i + 1];
+        hw[i] = pack_bf16x2(a0, a1);
+        float r0 = a0 - bf16_lo(hw[i]), r1 = a1 - bf16_hi(hw[i]);
+        r0 = r0 == r0 ? r0 : 0.0f;
+        r1 = r1 == r1 ? r1 : 0.0f;
+        mw[i] = pack_bf16x2(r0, r1);
+        lw[i] = pack_bf16x2(r0 - bf16_lo(mw[i]), r1 - bf16_hi(mw[i]));
+    }
+    h = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+    m = make_uint4(mw[0], mw[1], mw[2], mw[3]);
+    l = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+}
+
+constexpr int kMmWaves = 8;
+
+template <bool DUAL, bool XF32>
+__global__ __launch_bounds__(64 * kMmWaves) void matvec_mfma(MatvecArgs a)
+{
+    __shared__ f32x4_t red[kMmWaves][2][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = wave_id();
+    const int r = lane & 15, g = lane >> 4;
+    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 16;
+    const int64_t row = n0 + r < a.N ? n0 + r : a.N - 1;
+    int64_t tok = a.t0 + r;
+    tok = tok < a.T ? tok : a.T - 1;
+    const int nc = static_cast<int>(a.K / 64);
+    const int c0 = wave * nc / kMmWaves, c1 = (wave + 1) * nc / kMmWaves;
+    const char* wg = a.wg + row * a.wrow;
+    const char* wu = DUAL ? a.wu + row * a.wrow : nullptr;
+    f32x4_t ag = {0.0f, 0.0f, 0.0f, 0.0f}, au = {0.0f, 0.0f, 0.0f, 0.0f};
+    // One chunk's operands as loaded: weights (gate, up: two 16-byte vectors each) and x (f32: four float4;
+    // bf16: two uint4 in xb). The next chunk's loads are issued before the current chunk is computed.
+    struct Ops {
+        uint4 A0, A1, U0, U1;
+        float4 xf[4];
+        uint4 xb[2];
+    };
+    auto load = [&](int c, Ops& o) {
+        const int64_t k0 = static_cast<int64_t>(c) * 64 + 8 * g;  // step 0: 64c + 8g + j; step 1: + 32
+        o.A0 = load_nt(wg + k0 * 2);
+        o.A1 = load_nt(wg + (k0 + 32) * 2);
+        if (DUAL) {
+            o.U0 = load_nt(wu + k0 * 2);
+            o.U1 = load_nt(wu + (k0 + 32) * 2);
+        }
+        if (XF32) {
+            const float* xr = static_cast<const float*>(a.x) + tok * a.xs + k0;
+            o.xf[0] = *reinterpret_cast<const float4*>(xr);
+            o.xf[1] = *reinterpret_cast<const float4*>(xr + 4);
+            o.xf[2] = *reinterpret_cast<const float4*>(xr + 32);
+            o.xf[3] = *reinterpret_cast<const float4*>(xr + 36);
+        } else {
+            const uint16_t* xr = static_cast<const uint16_t*>(a.x) + tok * a.xs + k0;
+            o.xb[0] = *reinterpret_cast<const uint4*>(xr);
+            o.xb[1] = *reinterpret_cast<const uint4*>(xr + 32);
+        }
+    };
+    auto compute = [&](const Ops& o) {
+        uint4 B[2][3];
+        int np = 1;
+        if (XF32) {
+#pragma unroll
+            for (int s2 = 0; s2 < 2; s2++) {
+                const float4 f0 = o.xf[2 * s2], f1 = o.xf[2 * s2 + 1];
+                const float xv[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
+                split3(xv, B[s2][0], B[s2][1], B[s2][2]);
+            }
+            np = 3;
+        } else {
+            B[0][0] = o.xb[0];
+            B[1][0] = o.xb[1];
+        }
+#pragma unroll
+        for (int p = 0; p < 3; p++) {
+            if (p >= np) break;
+            ag = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(o.A0), as_bf16x8(B[0][p]), ag, 0, 0, 0);
+            ag = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(o.A1), as_bf16x8(B[1][p]), ag, 0, 0, 0);
+            if (DUAL) {
+                au = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(o.U0), as_bf16x8(B[0][p]), au, 0, 0, 0);
+                au = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(o.U1), as_bf16x8(B[1][p]), au, 0, 0, 0);
+            }
+        }
+    };
+    // Two operand sets in alternation (a copy between them would wait for the loads): each chunk's loads are
+    // issued before the previous chunk is computed. The scheduling barriers keep them there -- left free, the
+    // scheduler sinks the loads below the MFMAs and every chunk waits for its own loads.
+    const int n = c1 - c0;
+    if (n > 0) {  // wave-uniform
+        Ops oa, ob;
+        load(c0, oa);
+        int i = 0;
+        for (; i + 2 < n; i += 2) {  // branch-free body: a merge would make the load counter waits exact-zero
+            load(c0 + i + 1, ob);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(oa);
+            __builtin_amdgcn_sched_barrier(0);
+            load(c0 + i + 2, oa);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(ob);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (i + 1 < n) {  // two chunks left
+            load(c0 + i + 1, ob);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(oa);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(ob);
+        } else {
+            compute(oa);
+        }
+    }
+    red[wave][0][lane] = ag;
+    if (DUAL) red[wave][1][lane] = au;
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int w = 1; w < kMmWaves; w++) {
+        ag += red[w][0][lane];
+        if (DUAL) au += red[w][1][lane];
+    }
+    // lane: token column r, rows 4g + i
+    const int64_t t = a.t0 + r;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int64_t n = n0 + 4 * g + i;
+        float out = ag[i];
+        if (DUAL) {
+            const float act = a.act == SLHIP_ACT_SILU        ? activate<SLHIP_ACT_SILU>(ag[i])
+                              : a.act == SLHIP_ACT_GELU_TANH ? activate<SLHIP_ACT_GELU_TANH>(ag[i])
+                                                             : activate<SLHIP_ACT_GELU_ERF>(ag[i]);
+            out = act * au[i];
+        }
+        if (t < a.T && n < a.N) {
+            if (a.yt == SLHIP_F32)
+                static_cast<float*>(a.y)[t * a.ys + n] = out;
+            else
+                static_cast<uint16_t*>(a.y)[t * a.ys + n] = static_cast<uint16_t>(f32_to_bf16_bits(out));
+        }
+    }
+}
+
 // ---- host dispatch --------------------------------------------------------------------------------
 
 static int env_int(const char* name, int dflt)
@@ -425,9 +587,35 @@ static int token_tile(int64_t T, int64_t K)
     return tt;
 }
 
+static int run_mfma(MatvecArgs a, bool dual, hipStream_t st)
+{
+    const dim3 grid(static_cast<unsigned>((a.N + 15) / 16));
+    for (int64_t t0 = 0; t0 < a.T; t0 += 16) {
+        a.t0 = t0;
+        if (a.xt == SLHIP_F32) {
+            if (dual) matvec_mfma<true, true><<<grid, 64 * kMmWaves, 0, st>>>(a);
+            else matvec_mfma<false, true><<<grid, 64 * kMmWaves, 0, st>>>(a);
+        } else {
+            if (dual) matvec_mfma<true, false><<<grid, 64 * kMmWaves, 0, st>>>(a);
+            else matvec_mfma<false, false><<<grid, 64 * kMmWaves, 0, st>>>(a);
+        }
+        const int r = check_launch("matvec_mfma");
+        if (r != SLHIP_OK) return r;
+    }
+    return SLHIP_OK;
+}
+
+// Tokens from which bf16 weights take the matrix cores (SLHIP_MATVEC_MFMA_MIN_T; 0 disables): below it the
+// VALU kernel is already at the HBM rate.
+static int mfma_min_tokens() { return env_int("SLHIP_MATVEC_MFMA_MIN_T", 5); }
+
 template <int WT>
 static int run_dense(MatvecArgs a, bool dual, hipStream_t st)
 {
+    if constexpr (WT == SLHIP_BF16) {
+        const int mt = mfma_min_tokens();
+        if (mt > 0 && a.T >= mt && a.K % 64 == 0) return run_mfma(a, dual, st);
+    }
     constexpr int E = Vec<WT>::N;
     const int64_t nvr = a.K / E;
     int wpr = 1;

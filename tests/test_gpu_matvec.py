@@ -214,3 +214,36 @@ def test_strided_rows(device):
 def test_empty_shapes_are_noops(device):
     native.matvec("bf16", "f32", "f32", None, 0, 64, None, 10, None)
     native.dual_matvec("silu", "bf16", "f32", "f32", None, 3, 64, None, None, 0, None)
+
+
+@pytest.mark.parametrize("min_t", ["0", "1"])  # 0: the VALU kernel for every T; 1: the matrix cores for every T
+@pytest.mark.parametrize("dual,dx,T,K,N", [
+    (False, "f32", 1, 1024, 48), (False, "f32", 4, 2048, 40), (True, "f32", 5, 4096, 64),
+    (True, "bf16", 17, 1024, 33), (False, "bf16", 33, 256, 17),
+])
+def test_bf16_paths_agree_with_oracle(device, monkeypatch, min_t, dual, dx, T, K, N):
+    """bf16 weights take the MFMA kernel from SLHIP_MATVEC_MFMA_MIN_T tokens on; both kernels meet the same
+    bound whichever T they are forced onto (ragged token and row tiles included)."""
+    monkeypatch.setenv("SLHIP_MATVEC_MFMA_MIN_T", min_t)
+    seed = _seed("paths", min_t, dual, dx, T, K, N)
+    rg, Wg = _weights("bf16", N, K, seed, 1)
+    x, x32 = _x(dx, T, K, seed)
+    if not dual:
+        y = _run("bf16", dx, "f32", x, [rg], N, K)
+        S = np.abs(x32).astype(np.float64) @ _abs_terms("bf16", rg, Wg).T
+        _check_single(y, "f32", oracle.matvec("bf16", rg, N, K, x32), S, f"bf16 min_t={min_t}")
+        return
+    ru, Wu = _weights("bf16", N, K, seed, 2)
+    y = _run("bf16", dx, "f32", x, [rg, ru], N, K, act="silu")
+    g = oracle.matvec("bf16", rg, N, K, x32)
+    u = oracle.matvec("bf16", ru, N, K, x32)
+    ref = oracle.mul(oracle.unary("silu", g), u).astype(np.float64)
+    ax = np.abs(x32).astype(np.float64)
+    Sg, Su = ax @ _abs_terms("bf16", rg, Wg).T, ax @ _abs_terms("bf16", ru, Wu).T
+    g64 = g.astype(np.float64)
+    s = 1 / (1 + np.exp(-g64))
+    dsilu = np.abs(s * (1 + g64 * (1 - s))) * 1.5 + 1e-3
+    e = 2.0 ** -16
+    tol = dsilu * np.abs(u) * e * Sg + np.abs(g64 * s) * e * Su + 1e-5 * np.abs(ref) + 1e-30
+    bad = np.abs(y.astype(np.float64) - ref) > tol
+    assert not bad.any(), f"dual min_t={min_t}: {bad.sum()} beyond the bound; first at {np.argwhere(bad)[0]}"
