@@ -415,6 +415,94 @@ def time_per_launch(wl: Workload, launches: int, replays: int, stream) -> np.nda
     return np.array(out)
 
 
+# ---- the on-disk -> device path ----------------------------------------------------------------------------
+
+PCIE_PEAK_GBS = 64.0  # PCIe 5.0 x16, one direction (32 GT/s x 16 lanes, 128b/130b)
+UPLOAD_NAME = "gguf_upload_q4_k"
+
+
+def bench_upload(stream, reps: int, cpu_seconds: float | None):
+    """A ~1.07 GB Q4_K tensor (token_embd-like [466034, 4096]) in a GGUF file in the page cache, uploaded to
+    HBM: the staged uploader (slhip_gguf_upload) against hipMemcpy from the same pageable mapping, and a
+    copy from pinned memory (the link's practical ceiling). Wall clock from the call to the stream's end."""
+    import tempfile
+    from sharplight_amd import gguf
+    rows, K = 466034, 4096
+    nbytes = rows * K // 256 * 144
+    d = tempfile.mkdtemp(prefix="slbench-")
+    path = os.path.join(d, "upload.gguf")
+    rng = np.random.default_rng(7)
+    w = gguf.GgufWriter().add_metadata("general.architecture", "bench")
+    w.add_tensor("token_embd.weight", 12, rng.integers(0, 256, nbytes, dtype=np.uint8).tobytes(), [rows, K])
+    w.write(path)
+    del w
+    out = {}
+    try:
+        f = gguf.GgufFile.open(path)
+        t = f.get_tensor("token_embd.weight")
+        dst = native.DeviceBuffer(nbytes)
+
+        def timed(fn):
+            ts = []
+            for _ in range(reps):
+                native.synchronize(stream.handle)
+                t0 = time.perf_counter()
+                fn()
+                native.synchronize(stream.handle)
+                ts.append(time.perf_counter() - t0)
+            return float(np.median(ts)), ts
+
+        t0 = time.perf_counter()
+        t.upload(dst.ptr, stream=stream.handle)  # first touch of the mapping's pages
+        native.synchronize(stream.handle)
+        cold = time.perf_counter() - t0
+        staged, _ = timed(lambda: t.upload(dst.ptr, stream=stream.handle))
+        src = t.pointer()
+        plain, _ = timed(lambda: native.call("slhip_memcpy_h2d", dst.ptr, src, nbytes, stream.handle))
+        pin = ctypes_pinned(nbytes)
+        pinned, _ = timed(lambda: native.call("slhip_memcpy_h2d", dst.ptr, pin[0], nbytes, stream.handle))
+        native.call("slhip_host_free", pin[0])
+        dst.free()
+        out = {"bytes": nbytes, "tensor": "q4_k [466034, 4096] in a GGUF file (page cache)",
+               "staged_GB/s": round(nbytes / staged / 1e9, 2), "staged_ms": round(staged * 1e3, 2),
+               "staged_first_touch_GB/s": round(nbytes / cold / 1e9, 2),
+               "hipMemcpy_pageable_GB/s": round(nbytes / plain / 1e9, 2),
+               "hipMemcpy_pinned_GB/s": round(nbytes / pinned / 1e9, 2),
+               "roofline": {"bound": "pcie", "achieved": round(nbytes / staged / 1e9, 2), "peak": PCIE_PEAK_GBS,
+                            "unit": "GB/s", "frac": round(nbytes / staged / 1e9 / PCIE_PEAK_GBS, 4)},
+               "staging": f"2 x {os.environ.get('SLHIP_UPLOAD_STAGING_MB', '64')} MiB pinned, "
+                          f"{os.environ.get('SLHIP_UPLOAD_THREADS', '8')} host threads", "reps": reps}
+        if cpu_seconds:
+            from oracle import gguf as og
+            with open(path, "rb") as fh:
+                import mmap
+                m = mmap.mmap(fh.fileno(), 0, access=mmap.ACCESS_READ)
+                info = og.parse_file(m)["tensors"][0]
+                n, t0 = 0, time.perf_counter()
+                while True:
+                    og.read_tensor(m, info)
+                    n += 1
+                    if time.perf_counter() - t0 > cpu_seconds:
+                        break
+                s = (time.perf_counter() - t0) / n
+                m.close()
+            out["cpu_baseline"] = {"value": round(nbytes / s / 1e9, 2), "unit": "GB/s", "cores": 1, "kind": "port",
+                                   "sample": f"oracle read of the whole tensor from the mapping into host memory, {n} reps"}
+        f.close()
+    finally:
+        os.unlink(path)
+        os.rmdir(d)
+    return out
+
+
+def ctypes_pinned(nbytes):
+    import ctypes
+    p = ctypes.c_void_p(0)
+    native.call("slhip_host_malloc", ctypes.byref(p), nbytes)
+    ctypes.memset(p.value, 0x5A, nbytes)
+    return (p.value,)
+
+
 # ---- CPU baseline (the oracle, on the host's cores) --------------------------------------------------------
 
 def cpu_threads() -> int:
@@ -675,6 +763,7 @@ def main():
     ap.add_argument("--only", default="", help="comma list of op names (prefixes) for the ops table")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-ops", action="store_true")
+    ap.add_argument("--no-upload", action="store_true", help="skip the GGUF file -> HBM upload measurement")
     ap.add_argument("--no-ceiling", action="store_true", help="skip the same-bytes copy next to each op")
     ap.add_argument("--launches", type=int, default=50, help="launches per graph in the ops table")
     ap.add_argument("--replays", type=int, default=10, help="graph replays per op in the ops table")
@@ -766,6 +855,14 @@ def main():
                 ops[name]["pct_of_copy"] = round(100 * cus / med, 1)
             log(f"bench: {name}: {med:.2f} us, {b / med / 1e3:.1f} GB/s")
 
+    # -- the on-disk -> device path --
+    upload = None
+    only = [o for o in args.only.split(",") if o]
+    if not args.no_upload and (not only or any(UPLOAD_NAME.startswith(o) for o in only)):
+        log("bench: GGUF upload")
+        upload = bench_upload(stream, 5, None if args.no_cpu else max(1.0, args.cpu_seconds / 8))
+        log(f"bench: upload {upload['staged_GB/s']} GB/s staged, {upload['hipMemcpy_pageable_GB/s']} GB/s hipMemcpy")
+
     # -- CPU baseline --
     cpu = None
     if not args.no_cpu:
@@ -801,6 +898,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "ops": ops,
+        "upload": upload,
     }
     print(json.dumps(line), flush=True)
 

@@ -10,7 +10,7 @@
  *    last failure on the calling thread is slhip_last_error(). The managed side turns statuses into
  *    the exceptions the reference's providers throw: SLHIP_ERR_INVALID -> ArgumentException,
  *    SLHIP_ERR_UNSUPPORTED -> NotSupportedException, SLHIP_ERR_INDEX -> ArgumentOutOfRangeException,
- *    SLHIP_ERR_CACHE -> InvalidOperationException.
+ *    SLHIP_ERR_CACHE -> InvalidOperationException, SLHIP_ERR_FORMAT -> InvalidDataException.
  *  - Tensor pointers are device pointers (slhip_malloc). Sizes and strides are in ELEMENTS of the
  *    tensor's own dtype, rows are the leading dims flattened, the normalized/activated axis is last and
  *    dense.
@@ -38,7 +38,7 @@ extern "C" {
 #define SLHIP_API __attribute__((visibility("default")))
 #endif
 
-#define SLHIP_ABI_VERSION 3
+#define SLHIP_ABI_VERSION 4
 
 typedef enum slhip_status {
     SLHIP_OK = 0,
@@ -47,7 +47,8 @@ typedef enum slhip_status {
     SLHIP_ERR_HIP = -3,         /* the HIP runtime reported an error */
     SLHIP_ERR_INDEX = -4,       /* a gather index was outside [0, V) (reported by slhip_stream_sync) */
     SLHIP_ERR_NO_DEVICE = -5,   /* no usable device / driver */
-    SLHIP_ERR_CACHE = -6        /* a KV-cache row outside the cache or block table (at slhip_stream_sync) */
+    SLHIP_ERR_CACHE = -6,       /* a KV-cache row outside the cache or block table (at slhip_stream_sync) */
+    SLHIP_ERR_FORMAT = -7       /* malformed file data: a truncated or inconsistent GGUF file */
 } slhip_status;
 
 /* Element types of activations. */
@@ -384,6 +385,110 @@ SLHIP_API int slhip_segment_device_bytes(slhip_segment segment, int64_t* bytes);
 /* The fused launches of the compiled segment, one label per line (e.g. "fused[Add]+RmsNorm"). */
 SLHIP_API int slhip_segment_launches(slhip_segment segment, char* buf, size_t size);
 SLHIP_API int slhip_segment_destroy(slhip_segment segment);
+
+/* ---- GGUF files and weight upload (the on-disk -> device path) --------------------------------
+ *
+ * A GGUF file (versions 2 and 3) memory-mapped read-only, its header, metadata and tensor table parsed
+ * with every read bounds-checked, so a truncated or hostile file fails with SLHIP_ERR_FORMAT instead of
+ * reading out of bounds. Replaces GgufFile.Open and its reader (src/Sharplight.Import.Gguf/GgufFile.cs:72-110,
+ * GgufReader.cs:1-175); the uploader replaces the Vulkan provider's staged weight upload
+ * (src/Sharplight.Vulkan/WeightUploader.cs:6-140). Strings returned by these functions live until
+ * slhip_gguf_close; host pointers into the mapping likewise. Parsing touches no device. */
+
+typedef struct slhip_gguf slhip_gguf; /* an open file, or a header prefix */
+
+/* GGUF metadata value types (gguf_metadata_value_type; GgufValueType.cs:4-19). */
+typedef enum slhip_gguf_vtype {
+    SLHIP_GGUF_UINT8 = 0, SLHIP_GGUF_INT8 = 1, SLHIP_GGUF_UINT16 = 2, SLHIP_GGUF_INT16 = 3,
+    SLHIP_GGUF_UINT32 = 4, SLHIP_GGUF_INT32 = 5, SLHIP_GGUF_FLOAT32 = 6, SLHIP_GGUF_BOOL = 7,
+    SLHIP_GGUF_STRING = 8, SLHIP_GGUF_ARRAY = 9, SLHIP_GGUF_UINT64 = 10, SLHIP_GGUF_INT64 = 11,
+    SLHIP_GGUF_FLOAT64 = 12
+} slhip_gguf_vtype;
+
+typedef struct slhip_gguf_info {
+    uint32_t version;        /* 2 or 3 (0 for a prefix that is not GGUF) */
+    uint32_t alignment;      /* general.alignment, default 32 */
+    int64_t n_tensors;       /* entries in the tensor table (0 for a prefix that does not hold it whole) */
+    int64_t n_kv;            /* metadata pairs read (a prefix: the pairs it holds whole) */
+    int64_t data_offset;     /* absolute offset of the tensor data section (-1 when unknown) */
+    int64_t file_length;     /* bytes mapped (a prefix: its length) */
+    int32_t has_data;        /* 1: opened from a file, tensor data readable; 0: a header prefix */
+    int32_t table_complete;  /* 1 when the whole tensor table was read */
+} slhip_gguf_info;
+
+/* One metadata value, a node of the value tree. Scalars: `u` (unsigned and bool), `i` (signed) or `f`
+ * (float32 widened exactly, float64). Strings: `data` -> `count` UTF-8 bytes (not NUL-terminated).
+ * Arrays: `elem_type` and `count`; numeric and bool elements are `count` packed little-endian values at
+ * `data` (unaligned); string and array elements are the nodes first_child .. first_child + count - 1. */
+typedef struct slhip_gguf_value {
+    uint32_t type;
+    uint32_t elem_type;
+    int64_t count;
+    uint64_t u;
+    int64_t i;
+    double f;
+    const void* data;
+    int64_t first_child;
+} slhip_gguf_value;
+
+/* A tensor of the table (GgufTensorInfo, GgufTensorInfo.cs:7-79). The element type is the one the file's
+ * ggml type id is read as (GgmlTypes.TryGetDataType, GgmlTypes.cs:94-119): the interleaved Q4_0 ids 31-33
+ * read as q4_0 rows, the narrow IQ1 ids 64-66 as iq1_s blocks, I2_S (36) as q2s_g128 blocks. */
+typedef struct slhip_gguf_tensor {
+    const char* name;
+    const char* type_name;   /* the reference's DataType name, e.g. "q4_k", "bf16" */
+    int32_t ggml_type;       /* the id stored in the file */
+    int32_t format;          /* the slhip_format this library's kernels read it as, or -1 */
+    int32_t block_size;      /* values per block (1 for plain element types) */
+    int32_t block_bytes;
+    int32_t n_dims;
+    int32_t reserved;
+    int64_t ne[8];           /* ggml dimensions, innermost first */
+    int64_t relative_offset; /* from the start of the data section */
+    int64_t offset;          /* absolute file offset (0 for a prefix) */
+    int64_t byte_size;       /* bytes as the element type above */
+    int64_t stored_bytes;    /* bytes the file holds for it */
+} slhip_gguf_tensor;
+
+/* Opens and maps `path` (GgufFile.Open). SLHIP_ERR_FORMAT: not GGUF, truncated, a tensor beyond the end
+ * of the file, a row length that is not a multiple of its type's block size; SLHIP_ERR_UNSUPPORTED: a
+ * GGUF version other than 2/3 or an unknown ggml type id; SLHIP_ERR_INVALID: the file cannot be opened. */
+SLHIP_API int slhip_gguf_open(const char* path, slhip_gguf** file);
+/* Parses the first `length` bytes of a GGUF file (copied; GgufHeaderProbe.ReadMetadata / ReadTensorTable,
+ * GgufHeaderProbe.cs:17-135): the pairs it holds whole, and the tensor table when it holds all of it
+ * (type ids unknown to this library are kept, with type_name "" and sizes 0). Never fails on content. */
+SLHIP_API int slhip_gguf_open_prefix(const void* bytes, size_t length, slhip_gguf** file);
+SLHIP_API int slhip_gguf_close(slhip_gguf* file);
+SLHIP_API int slhip_gguf_get_info(const slhip_gguf* file, slhip_gguf_info* info);
+/* Metadata pair `index` (file order): its key and the node of its value. */
+SLHIP_API int slhip_gguf_kv(const slhip_gguf* file, int64_t index, const char** key, int64_t* node);
+/* The pair of `key`, -1 when absent (the last one when a key repeats, as the reference's dictionary). */
+SLHIP_API int slhip_gguf_find_kv(const slhip_gguf* file, const char* key, int64_t* index);
+SLHIP_API int slhip_gguf_get_value(const slhip_gguf* file, int64_t node, slhip_gguf_value* value);
+SLHIP_API int slhip_gguf_tensor_info(const slhip_gguf* file, int64_t index, slhip_gguf_tensor* tensor);
+/* The tensor named `name`, -1 when absent (GgufFile.FindTensor). */
+SLHIP_API int slhip_gguf_find_tensor(const slhip_gguf* file, const char* name, int64_t* index);
+/* Describes a ggml type id as the tensor table would (name, block size and bytes, slhip_format);
+ * SLHIP_ERR_UNSUPPORTED for an unknown or removed id (GgmlTypes.GetDataType). */
+SLHIP_API int slhip_gguf_type(int ggml_type, slhip_gguf_tensor* type);
+/* Host read of bytes [offset, offset + bytes) of a tensor as its element type (IWeightSource.Read:
+ * GgufWeightSource.cs:9-19, GgufInterleavedQ4_0Source.cs:43-79, GgufI2sSource.cs:39-64): the interleaved
+ * Q4_0 rows de-interleaved, I2_S codes with the tensor's scale in front of every block. SLHIP_ERR_INDEX
+ * for a range outside the tensor; SLHIP_ERR_UNSUPPORTED for the narrow IQ1 types (widening not built). */
+SLHIP_API int slhip_gguf_read(const slhip_gguf* file, int64_t index, int64_t offset, void* dst, size_t bytes);
+/* The tensor's bytes in the mapping when they are its element type's bytes as stored (TryGetPointer),
+ * else NULL. */
+SLHIP_API int slhip_gguf_tensor_pointer(const slhip_gguf* file, int64_t index, const void** ptr);
+/* Uploads a whole tensor, as slhip_gguf_read returns it, to device memory `dst` of at least byte_size
+ * bytes, through the staging uploader below (WeightUploader.Upload). */
+SLHIP_API int slhip_gguf_upload(const slhip_gguf* file, int64_t index, void* dst, size_t dst_bytes,
+                                slhip_stream stream);
+/* Copies `bytes` of pageable host memory (a mapped file, say) to device memory through two pinned
+ * staging buffers of the current device: host threads fill one while the DMA engine drains the other.
+ * Returns once every source byte has been read; the device copies are ordered on `stream` (wait on it
+ * before reading dst). Calls on one device serialize on its uploader. Staging size
+ * SLHIP_UPLOAD_STAGING_MB (default 64 MiB per buffer), host threads SLHIP_UPLOAD_THREADS (default 8). */
+SLHIP_API int slhip_upload(void* dst, const void* src, size_t bytes, slhip_stream stream);
 
 #ifdef __cplusplus
 }

@@ -3,7 +3,8 @@
 This is the Python twin of the managed provider's ``[LibraryImport]`` declarations: one typed foreign
 function per C entry point, statuses turned into the exceptions the reference's providers throw
 (``ArgumentException`` -> ``ValueError``, ``NotSupportedException`` -> ``NotImplementedError``,
-``ArgumentOutOfRangeException`` -> ``IndexError``). There is no fallback: if the library is not built
+``ArgumentOutOfRangeException`` -> ``IndexError``, ``InvalidDataException`` -> ``SlhipFormatError``, a
+``ValueError``). There is no fallback: if the library is not built
 or cannot load, every call raises.
 """
 from __future__ import annotations
@@ -16,7 +17,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libsharplight_hip.so")
 
-OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP, ERR_INDEX, ERR_NO_DEVICE, ERR_CACHE = 0, -1, -2, -3, -4, -5, -6
+OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP, ERR_INDEX, ERR_NO_DEVICE, ERR_CACHE, ERR_FORMAT = 0, -1, -2, -3, -4, -5, -6, -7
 F32, F16, BF16 = 0, 1, 2
 DTYPES = {"f32": F32, "f16": F16, "bf16": BF16}
 NP_DTYPES = {F32: np.float32, F16: np.float16, BF16: np.uint16}  # bf16 travels as raw uint16 bits
@@ -47,6 +48,10 @@ class SlhipIndexError(IndexError):
     pass
 
 
+class SlhipFormatError(ValueError):
+    """Malformed file data (the reference throws InvalidDataException)."""
+
+
 class SlhipCacheError(SlhipError):
     """A KV-cache row outside the cache or block table (the reference throws InvalidOperationException)."""
 
@@ -71,6 +76,29 @@ class NormCopies(ctypes.Structure):
     """slhip_norm_copies: the f16 and E4M3 GEMM activation copies a row norm writes (either may be NULL)."""
     _fields_ = [("y16", ctypes.c_void_p), ("y16_stride", ctypes.c_int64), ("yq", ctypes.c_void_p),
                 ("yq_stride", ctypes.c_int64)]
+
+
+class GgufInfo(ctypes.Structure):
+    """slhip_gguf_info."""
+    _fields_ = [("version", ctypes.c_uint32), ("alignment", ctypes.c_uint32), ("n_tensors", ctypes.c_int64),
+                ("n_kv", ctypes.c_int64), ("data_offset", ctypes.c_int64), ("file_length", ctypes.c_int64),
+                ("has_data", ctypes.c_int32), ("table_complete", ctypes.c_int32)]
+
+
+class GgufValue(ctypes.Structure):
+    """slhip_gguf_value: one node of a metadata value tree."""
+    _fields_ = [("type", ctypes.c_uint32), ("elem_type", ctypes.c_uint32), ("count", ctypes.c_int64),
+                ("u", ctypes.c_uint64), ("i", ctypes.c_int64), ("f", ctypes.c_double), ("data", ctypes.c_void_p),
+                ("first_child", ctypes.c_int64)]
+
+
+class GgufTensor(ctypes.Structure):
+    """slhip_gguf_tensor."""
+    _fields_ = [("name", ctypes.c_char_p), ("type_name", ctypes.c_char_p), ("ggml_type", ctypes.c_int32),
+                ("format", ctypes.c_int32), ("block_size", ctypes.c_int32), ("block_bytes", ctypes.c_int32),
+                ("n_dims", ctypes.c_int32), ("reserved", ctypes.c_int32), ("ne", ctypes.c_int64 * 8),
+                ("relative_offset", ctypes.c_int64), ("offset", ctypes.c_int64), ("byte_size", ctypes.c_int64),
+                ("stored_bytes", ctypes.c_int64)]
 
 
 ROWS = {"past": 0, "seq": 1, "paged": 2}
@@ -150,6 +178,20 @@ SIGNATURES = {
     "slhip_segment_device_bytes": (_I, [_P, ctypes.POINTER(_I64)]),
     "slhip_segment_launches": (_I, [_P, ctypes.c_char_p, _SZ]),
     "slhip_segment_destroy": (_I, [_P]),
+    "slhip_gguf_open": (_I, [ctypes.c_char_p, ctypes.POINTER(_P)]),
+    "slhip_gguf_open_prefix": (_I, [_P, _SZ, ctypes.POINTER(_P)]),
+    "slhip_gguf_close": (_I, [_P]),
+    "slhip_gguf_get_info": (_I, [_P, ctypes.POINTER(GgufInfo)]),
+    "slhip_gguf_kv": (_I, [_P, _I64, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_I64)]),
+    "slhip_gguf_find_kv": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(_I64)]),
+    "slhip_gguf_get_value": (_I, [_P, _I64, ctypes.POINTER(GgufValue)]),
+    "slhip_gguf_tensor_info": (_I, [_P, _I64, ctypes.POINTER(GgufTensor)]),
+    "slhip_gguf_find_tensor": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(_I64)]),
+    "slhip_gguf_type": (_I, [_I, ctypes.POINTER(GgufTensor)]),
+    "slhip_gguf_read": (_I, [_P, _I64, _I64, _P, _SZ]),
+    "slhip_gguf_tensor_pointer": (_I, [_P, _I64, ctypes.POINTER(_P)]),
+    "slhip_gguf_upload": (_I, [_P, _I64, _P, _SZ, _P]),
+    "slhip_upload": (_I, [_P, _P, _SZ, _P]),
 }
 
 _lib = None
@@ -186,6 +228,8 @@ def check(status: int) -> None:
         raise SlhipIndexError(msg)
     if status == ERR_CACHE:
         raise SlhipCacheError(msg)
+    if status == ERR_FORMAT:
+        raise SlhipFormatError(msg)
     raise SlhipError(f"status {status}: {msg}")
 
 
