@@ -73,7 +73,12 @@ typedef enum slhip_format {
     SLHIP_FMT_Q6_K = 12,  /* 210 bytes: ql[128], qh[64], int8 scales[16], f16 d -> fma(q, s, -32 s)   */
     /* the 4-bit codebook formats (Quant.cs:407-446): value = scale * codebook[nibble] */
     SLHIP_FMT_IQ4_NL = 13, /* 18-byte blocks of 32: f16 d, qs[16]          */
-    SLHIP_FMT_IQ4_XS = 14  /* 136 bytes per 256: f16 d, u16 scales_h, scales_l[4], qs[128] */
+    SLHIP_FMT_IQ4_XS = 14, /* 136 bytes per 256: f16 d, u16 scales_h, scales_l[4], qs[128] */
+    /* ternary and 4-bit float formats (Quant.Ternary.cs:27-86, Quant.Fp4.cs:36-80): value = code * scale */
+    SLHIP_FMT_TQ1_0 = 15, /* 54 bytes per 256: qs[48] (5 base-3 digits per byte), qh[4], f16 d -> (t-1)*d */
+    SLHIP_FMT_TQ2_0 = 16, /* 66 bytes per 256: qs[64] (4 two-bit codes per byte), f16 d -> (q-1)*d         */
+    SLHIP_FMT_MXFP4 = 17, /* 17 bytes per 32: E8M0 e, qs[16] (E2M1 nibbles) -> fp4 * 2^(e-128)            */
+    SLHIP_FMT_NVFP4 = 18  /* 36 bytes per 64: UE4M3 d[4] (per 16), qs[32] (E2M1 nibbles) -> fp4 * d/2      */
 } slhip_format;
 
 /* Row-norm kinds (StandardOps RmsNorm / L2Norm / LayerNorm). */
@@ -311,8 +316,8 @@ SLHIP_API int slhip_rope(int dtype_in, int dtype_out, const slhip_rope_tensor* t
  * Embedding gather y[i, :] = dequant(table[ids[i], :]) for i < N; table is the [V, row_bytes] image of a
  * [V, D] tensor in `format`. dtype_out: F32 or BF16 (f32 values rounded to nearest even). An id outside
  * [0, V) leaves its output row zero and raises SLHIP_ERR_INDEX at the next slhip_stream_sync.
- * Formats: F32, F16, BF16, Q8_0, Q4_0, Q4_1, Q5_0, Q5_1 (D a multiple of 32), Q2_K..Q6_K and IQ4_XS (D a
- * multiple of 256), IQ4_NL (32).
+ * Formats: F32, F16, BF16, Q8_0, Q4_0, Q4_1, Q5_0, Q5_1 (D a multiple of 32), Q2_K..Q6_K, IQ4_XS, TQ1_0
+ * and TQ2_0 (D a multiple of 256), IQ4_NL and MXFP4 (32), NVFP4 (64).
  * Replaces: GatherOp (src/Sharplight.Cpu/GatherOp.cs:22-75) with Quant.Dequantize
  * (src/Sharplight.Cpu/Quant.cs:242-446,500-624; Quant.KQuants.cs:36-107), and the Vulkan gather
  * (GraphLowerer.Transformer.cs:133-179, Kernels/data.slang:4-37).

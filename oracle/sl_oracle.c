@@ -342,7 +342,9 @@ void orc_rope(const float* x, const int32_t* pos, const float* ff, float* y, int
 /* Quant.BlockSize / BlockBytes (src/Sharplight.Cpu/Quant.cs:181-216) for the formats here. */
 static int block_size(int fmt)
 {
-    if (fmt >= ORC_Q2_K && fmt != ORC_IQ4_NL) return 256;
+    if (fmt == ORC_IQ4_NL || fmt == ORC_MXFP4) return 32;
+    if (fmt == ORC_NVFP4) return 64;
+    if (fmt >= ORC_Q2_K) return 256;
     return fmt >= ORC_Q8_0 ? 32 : 1;
 }
 static int block_bytes(int fmt)
@@ -362,6 +364,10 @@ static int block_bytes(int fmt)
     case ORC_Q6_K: return 210;
     case ORC_IQ4_NL: return 18;
     case ORC_IQ4_XS: return 136;
+    case ORC_TQ1_0: return 54;
+    case ORC_TQ2_0: return 66;
+    case ORC_MXFP4: return 17;
+    case ORC_NVFP4: return 36;
     default: return -1;
     }
 }
@@ -391,6 +397,35 @@ static void scale_min(int j, const uint8_t* q, int* sc, int* m)
 
 /* The IQ4_NL / IQ4_XS codebook (Quant.cs:409), the values ggml's non-linear 4-bit formats define. */
 static const int8_t kIq4Values[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+
+/* Quant.s_fp4Values (Quant.Fp4.cs:10): the E2M1 magnitudes doubled, codes 8..15 negative. */
+static const int8_t kFp4Values[16] = {0, 1, 2, 3, 4, 6, 8, 12, 0, -1, -2, -3, -4, -6, -8, -12};
+
+/* Quant.E8M0Half (Quant.Fp4.cs:36-41): 2^(e-127) / 2, exponents 0 and 1 as f32 denormals. */
+static float e8m0_half(uint8_t e)
+{
+    uint32_t bits = e < 2 ? 0x00200000u << e : (uint32_t)(e - 1) << 23;
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+/* Quant.BuildUe4m3 (Quant.Fp4.cs:14-33): a UE4M3 byte (exponent bits 3-6, bias 7; mantissa bits 0-2; bit 7
+ * ignored) halved; 0 and 0x7F read as zero. */
+static float ue4m3_half(uint8_t x)
+{
+    if (x == 0 || x == 0x7F) return 0.0f;
+    const int e = (x >> 3) & 0xF, m = x & 7;
+    const float raw = e == 0 ? ldexpf((float)m, -9) : ldexpf(1.0f + (float)m / 8.0f, e - 7);
+    return raw * 0.5f;
+}
+
+/* Quant.BuildTrits (Quant.Ternary.cs:10-25): base-3 digit n of byte b, ((b * 3^n mod 256) * 3) >> 8, minus one. */
+static int trit(uint8_t b, int n)
+{
+    static const int p3[5] = {1, 3, 9, 27, 81};
+    return ((((int)b * p3[n]) & 0xFF) * 3 >> 8) - 1;
+}
 
 /* One block of a K-quant or codebook format (256 values; IQ4_NL 32):
  *  Q2_K  (Quant.KQuants.cs:36-66): {scales[16] (lo: scale, hi: min), qs[64], f16 d, f16 dmin};
@@ -498,6 +533,43 @@ static void kblock(int fmt, const uint8_t* p, float* dst)
         }
         break;
     }
+    case ORC_TQ1_0: {  /* Quant.TQ1_0 (Quant.Ternary.cs:27-64): {qs[48], qh[4], f16 d} */
+        const float d = rd_h(p + 52);
+        for (int n = 0; n < 5; n++) {
+            for (int m = 0; m < 32; m++) dst[n * 32 + m] = (float)trit(p[m], n) * d;
+            for (int m = 0; m < 16; m++) dst[160 + n * 16 + m] = (float)trit(p[32 + m], n) * d;
+        }
+        for (int n = 0; n < 4; n++)
+            for (int j = 0; j < 4; j++) dst[240 + n * 4 + j] = (float)trit(p[48 + j], n) * d;
+        break;
+    }
+    case ORC_TQ2_0: {  /* Quant.TQ2_0 (Quant.Ternary.cs:66-86): {qs[64], f16 d} */
+        const float d = rd_h(p + 64);
+        for (int j = 0; j < 2; j++)
+            for (int l = 0; l < 4; l++)
+                for (int m = 0; m < 32; m++)
+                    dst[128 * j + 32 * l + m] = (float)(((p[32 * j + m] >> (2 * l)) & 3) - 1) * d;
+        break;
+    }
+    case ORC_MXFP4: {  /* Quant.MXFP4 (Quant.Fp4.cs:43-58): {u8 e, qs[16]} */
+        const float d = e8m0_half(p[0]);
+        for (int j = 0; j < 16; j++) {
+            dst[j] = (float)kFp4Values[p[1 + j] & 0xF] * d;
+            dst[j + 16] = (float)kFp4Values[p[1 + j] >> 4] * d;
+        }
+        break;
+    }
+    case ORC_NVFP4: {  /* Quant.NVFP4 (Quant.Fp4.cs:60-80): {u8 d[4], qs[32]}, four 16-value sub-blocks */
+        for (int sb = 0; sb < 4; sb++) {
+            const float d = ue4m3_half(p[sb]);
+            const uint8_t* q = p + 4 + 8 * sb;
+            for (int j = 0; j < 8; j++) {
+                dst[16 * sb + j] = (float)kFp4Values[q[j] & 0xF] * d;
+                dst[16 * sb + j + 8] = (float)kFp4Values[q[j] >> 4] * d;
+            }
+        }
+        break;
+    }
     default: break;
     }
 }
@@ -518,7 +590,7 @@ int orc_dequant(int fmt, const uint8_t* p, int64_t count, float* dst)
     default: break;
     }
     if (block_bytes(fmt) < 0) return -1;
-    if (block_size(fmt) == 256 || fmt == ORC_IQ4_NL) {
+    if (fmt >= ORC_Q2_K) {
         const int bs = block_size(fmt), bb = block_bytes(fmt);
         if (count % bs) return -1;
         for (int64_t b = 0; b < count / bs; b++) kblock(fmt, p + b * bb, dst + b * bs);

@@ -248,6 +248,10 @@ __global__ __launch_bounds__(256) void gather_scalar(GatherArgs a, int fmt)
             case SLHIP_FMT_Q6_K: v = kv(std::integral_constant<int, SLHIP_FMT_Q6_K>{}); break;
             case SLHIP_FMT_IQ4_NL: v = kv(std::integral_constant<int, SLHIP_FMT_IQ4_NL>{}); break;
             case SLHIP_FMT_IQ4_XS: v = kv(std::integral_constant<int, SLHIP_FMT_IQ4_XS>{}); break;
+            case SLHIP_FMT_TQ1_0: v = kv(std::integral_constant<int, SLHIP_FMT_TQ1_0>{}); break;
+            case SLHIP_FMT_TQ2_0: v = kv(std::integral_constant<int, SLHIP_FMT_TQ2_0>{}); break;
+            case SLHIP_FMT_MXFP4: v = kv(std::integral_constant<int, SLHIP_FMT_MXFP4>{}); break;
+            case SLHIP_FMT_NVFP4: v = kv(std::integral_constant<int, SLHIP_FMT_NVFP4>{}); break;
             case SLHIP_FMT_F32: {
                 uint32_t u = p[4 * j] | (p[4 * j + 1] << 8) | (p[4 * j + 2] << 16) | (static_cast<uint32_t>(p[4 * j + 3]) << 24);
                 v = __uint_as_float(u);
@@ -300,14 +304,23 @@ static int block_bytes(int fmt)
     case SLHIP_FMT_Q6_K: return 210;
     case SLHIP_FMT_IQ4_NL: return 18;
     case SLHIP_FMT_IQ4_XS: return 136;
+    case SLHIP_FMT_TQ1_0: return 54;
+    case SLHIP_FMT_TQ2_0: return 66;
+    case SLHIP_FMT_MXFP4: return 17;
+    case SLHIP_FMT_NVFP4: return 36;
     default: return -1;
     }
 }
 
 static int block_values(int fmt)
 {
-    if (fmt >= SLHIP_FMT_Q2_K && fmt != SLHIP_FMT_IQ4_NL) return 256;
-    return fmt >= SLHIP_FMT_Q8_0 ? 32 : 1;
+    switch (fmt) {
+    case SLHIP_FMT_F32: case SLHIP_FMT_F16: case SLHIP_FMT_BF16: return 1;
+    case SLHIP_FMT_Q8_0: case SLHIP_FMT_Q4_0: case SLHIP_FMT_Q4_1: case SLHIP_FMT_Q5_0: case SLHIP_FMT_Q5_1:
+    case SLHIP_FMT_IQ4_NL: case SLHIP_FMT_MXFP4: return 32;
+    case SLHIP_FMT_NVFP4: return 64;
+    default: return 256;
+    }
 }
 
 static int env_int(const char* name, int dflt)
@@ -401,6 +414,10 @@ static int dispatch(int fmt, GatherArgs a, hipStream_t st)
         case SLHIP_FMT_Q6_K: return launch_quant<SLHIP_FMT_Q6_K, DTO>(a, st);
         case SLHIP_FMT_IQ4_NL: return launch_quant<SLHIP_FMT_IQ4_NL, DTO>(a, st);
         case SLHIP_FMT_IQ4_XS: return launch_quant<SLHIP_FMT_IQ4_XS, DTO>(a, st);
+        case SLHIP_FMT_TQ1_0: return launch_quant<SLHIP_FMT_TQ1_0, DTO>(a, st);
+        case SLHIP_FMT_TQ2_0: return launch_quant<SLHIP_FMT_TQ2_0, DTO>(a, st);
+        case SLHIP_FMT_MXFP4: return launch_quant<SLHIP_FMT_MXFP4, DTO>(a, st);
+        case SLHIP_FMT_NVFP4: return launch_quant<SLHIP_FMT_NVFP4, DTO>(a, st);
         case SLHIP_FMT_F16: return launch_plain<SLHIP_FMT_F16, DTO>(a, st);
         case SLHIP_FMT_BF16: return launch_plain<SLHIP_FMT_BF16, DTO>(a, st);
         case SLHIP_FMT_F32: return launch_plain<SLHIP_FMT_F32, DTO>(a, st);

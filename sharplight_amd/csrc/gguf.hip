@@ -116,15 +116,15 @@ TypeDesc type_desc(int id)
         d.chunk = id == 31 ? 4 : 8;
         return d;
     }
-    case 34: return t("tq1_0", 256, 54);
-    case 35: return t("tq2_0", 256, 66);
+    case 34: return t("tq1_0", 256, 54, SLHIP_FMT_TQ1_0);
+    case 35: return t("tq2_0", 256, 66, SLHIP_FMT_TQ2_0);
     case kI2S: {  // BitNet's I2_S: read as Q2S_G128 blocks (f32 scale + 32 code bytes)
         TypeDesc d = t("q2s_g128", 128, kI2sBlock);
         d.layout = Layout::I2S;
         return d;
     }
-    case 39: return t("mxfp4", 32, 17);
-    case 40: return t("nvfp4", 64, 36);
+    case 39: return t("mxfp4", 32, 17, SLHIP_FMT_MXFP4);
+    case 40: return t("nvfp4", 64, 36, SLHIP_FMT_NVFP4);
     case 41: return t("q1_0", 128, 18);
     case 42: return t("q2_0", 64, 18);
     case 43: return t("f8_e4m3", 1, 1);

@@ -62,7 +62,7 @@ void check(int st)
 
 // ---- graph ---------------------------------------------------------------------------------------------
 
-enum class DType { F32, F16, BF16, I32, Q8_0, Q4_0, Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS };
+enum class DType { F32, F16, BF16, I32, Q8_0, Q4_0, Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS, TQ1_0, TQ2_0, MXFP4, NVFP4 };
 
 struct TypeInfo {
     const char* name;
@@ -76,7 +76,8 @@ const TypeInfo kTypes[] = {
     {"q4_1", DType::Q4_1, 32, 20}, {"q5_0", DType::Q5_0, 32, 22}, {"q5_1", DType::Q5_1, 32, 24},
     {"q2_k", DType::Q2_K, 256, 84}, {"q3_k", DType::Q3_K, 256, 110}, {"q4_k", DType::Q4_K, 256, 144},
     {"q5_k", DType::Q5_K, 256, 176}, {"q6_k", DType::Q6_K, 256, 210}, {"iq4_nl", DType::IQ4_NL, 32, 18},
-    {"iq4_xs", DType::IQ4_XS, 256, 136},
+    {"iq4_xs", DType::IQ4_XS, 256, 136}, {"tq1_0", DType::TQ1_0, 256, 54}, {"tq2_0", DType::TQ2_0, 256, 66},
+    {"mxfp4", DType::MXFP4, 32, 17}, {"nvfp4", DType::NVFP4, 64, 36},
 };
 
 const TypeInfo& type_info(DType t)
@@ -116,6 +117,10 @@ int format_code(DType t)
     case DType::Q6_K: return SLHIP_FMT_Q6_K;
     case DType::IQ4_NL: return SLHIP_FMT_IQ4_NL;
     case DType::IQ4_XS: return SLHIP_FMT_IQ4_XS;
+    case DType::TQ1_0: return SLHIP_FMT_TQ1_0;
+    case DType::TQ2_0: return SLHIP_FMT_TQ2_0;
+    case DType::MXFP4: return SLHIP_FMT_MXFP4;
+    case DType::NVFP4: return SLHIP_FMT_NVFP4;
     default: unsupported("gather table type");
     }
 }

@@ -1,4 +1,4 @@
-// GGUF legacy block formats decoded from a row image staged in LDS (the embedding gather and the quantized
+// GGUF block formats decoded from a row image staged in LDS (the embedding gather and the quantized
 // matvec). Decoders as the reference CPU provider's (Quant.Dequantize, src/Sharplight.Cpu/Quant.cs:242-405;
 // Simd.StoreI8x16/StoreU8x16, Simd.cs:699-753): value = fma(q, d, offset) with the block's f16 scale d and
 //   Q8_0: q int8, offset 0       Q4_0: q nibble, offset -8d    Q5_0: q 5-bit, offset -16d
@@ -26,6 +26,10 @@ template <> struct Fmt<SLHIP_FMT_Q5_K> { static constexpr int BB = 176, BS = 256
 template <> struct Fmt<SLHIP_FMT_Q6_K> { static constexpr int BB = 210, BS = 256, QS = 0, QH = -1; static constexpr bool M = false, K = true; static constexpr int OFF = 0; };
 template <> struct Fmt<SLHIP_FMT_IQ4_NL> { static constexpr int BB = 18, BS = 32, QS = 2, QH = -1; static constexpr bool M = false, K = true; static constexpr int OFF = 0; };
 template <> struct Fmt<SLHIP_FMT_IQ4_XS> { static constexpr int BB = 136, BS = 256, QS = 0, QH = -1; static constexpr bool M = false, K = true; static constexpr int OFF = 0; };
+template <> struct Fmt<SLHIP_FMT_TQ1_0> { static constexpr int BB = 54, BS = 256, QS = 0, QH = -1; static constexpr bool M = false, K = true; static constexpr int OFF = 0; };
+template <> struct Fmt<SLHIP_FMT_TQ2_0> { static constexpr int BB = 66, BS = 256, QS = 0, QH = -1; static constexpr bool M = false, K = true; static constexpr int OFF = 0; };
+template <> struct Fmt<SLHIP_FMT_MXFP4> { static constexpr int BB = 17, BS = 32, QS = 0, QH = -1; static constexpr bool M = false, K = true; static constexpr int OFF = 0; };
+template <> struct Fmt<SLHIP_FMT_NVFP4> { static constexpr int BB = 36, BS = 64, QS = 0, QH = -1; static constexpr bool M = false, K = true; static constexpr int OFF = 0; };
 
 __device__ __forceinline__ uint32_t lds_u16(const uint32_t* s, int off)
 {
@@ -201,6 +205,41 @@ __device__ __forceinline__ uint32_t iq4_lookup4(uint32_t nib4)
     return (hi & m) | (lo & ~m);
 }
 
+// The E2M1 values doubled {0, 1, 2, 3, 4, 6, 8, 12, 0, -1, -2, -3, -4, -6, -8, -12} (src/Sharplight.Cpu/
+// Quant.Fp4.cs:10) as int8, looked up for four nibble bytes as iq4_lookup4 does.
+__device__ __forceinline__ uint32_t fp4_lookup4(uint32_t nib4)
+{
+    const uint32_t sel = nib4 & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(0x0C080604u, 0x03020100u, sel);
+    const uint32_t hi = __builtin_amdgcn_perm(0xF4F8FAFCu, 0xFDFEFF00u, sel);
+    const uint32_t m = ((nib4 >> 3) & 0x01010101u) * 0xFFu;
+    return (hi & m) | (lo & ~m);
+}
+
+// MXFP4's E8M0 scale halved (the stored E2M1 values are doubled): 2^(e - 128), the two smallest exponents
+// as f32 denormals (Quant.E8M0Half, Quant.Fp4.cs:36-41).
+__device__ __forceinline__ float e8m0_half(uint32_t e)
+{
+    return __uint_as_float(e < 2 ? 0x00200000u << e : (e - 1) << 23);
+}
+
+// NVFP4's UE4M3 scale byte halved: 4 exponent bits (bias 7) and 3 mantissa bits, the top bit ignored,
+// 0 and 0x7F read as zero (Quant.BuildUe4m3, Quant.Fp4.cs:14-33). Every value is exact in f32.
+__device__ __forceinline__ float ue4m3_half(uint32_t x)
+{
+    const int e = static_cast<int>((x >> 3) & 0xFu), m = static_cast<int>(x & 7u);
+    const float v = e == 0 ? __builtin_ldexpf(static_cast<float>(m), -10) : __builtin_ldexpf(static_cast<float>(8 + m), e - 11);
+    return (x == 0x7Fu) ? 0.0f : v;
+}
+
+// Base-3 digit n (0..4) of byte q, minus one: ((q * 3^n mod 256) * 3 >> 8) - 1 (Quant.BuildTrits,
+// Quant.Ternary.cs:10-25).
+__device__ __forceinline__ int trit(uint32_t q, int n)
+{
+    const uint32_t p3 = n == 0 ? 1u : n == 1 ? 3u : n == 2 ? 9u : n == 3 ? 27u : 81u;
+    return static_cast<int>((((q * p3) & 0xFFu) * 3u) >> 8) - 1;
+}
+
 // N (4 or 8) consecutive values k .. k+N-1 (k a multiple of N) of the K-quant or codebook block at byte
 // offset o, decoded with the reference's arithmetic (src/Sharplight.Cpu/Quant.cs:407-446,500-624,
 // Quant.KQuants.cs:36-107): the N values share one sub-block scale.
@@ -274,6 +313,53 @@ __device__ __forceinline__ void decode_k(const B& b, int o, int k, float* f)
             for (int e = 0; e < N; e++) {
                 const int v = static_cast<int>((byte_of(w, e) >> (2 * j)) & 3u) + 4 * static_cast<int>(byte_of(hw, e)) - 4;
                 f[e] = __fmul_rn(static_cast<float>(v), dl);
+            }
+        }
+    } else if constexpr (FMT == SLHIP_FMT_MXFP4) {
+        // {u8 e; u8 qs[16]}: value j < 16 the low nibble of qs[j], j >= 16 the high nibble of qs[j - 16]
+        // (Quant.MXFP4, Quant.Fp4.cs:43-58); value = fp4 * scale
+        const float d = e8m0_half(b.u8(o));
+        const int i = k % 32;
+        words(o + 1 + (i % 16));
+#pragma unroll
+        for (int x = 0; x < N / 4; x++) w[x] = fp4_lookup4(((i >= 16) ? w[x] >> 4 : w[x]) & 0x0F0F0F0Fu);
+#pragma unroll
+        for (int e = 0; e < N; e++) f[e] = __fmul_rn(static_cast<float>(static_cast<int8_t>(byte_of(w, e))), d);
+    } else if constexpr (FMT == SLHIP_FMT_NVFP4) {
+        // {u8 d[4]; u8 qs[32]}: four 16-value sub-blocks, each with a UE4M3 scale and 8 code bytes, low
+        // nibbles first (Quant.NVFP4, Quant.Fp4.cs:60-80)
+        const int sb = k / 16, i = k % 16;
+        const float d = ue4m3_half(b.u8(o + sb));
+        words(o + 4 + 8 * sb + (i % 8));
+#pragma unroll
+        for (int x = 0; x < N / 4; x++) w[x] = fp4_lookup4(((i >= 8) ? w[x] >> 4 : w[x]) & 0x0F0F0F0Fu);
+#pragma unroll
+        for (int e = 0; e < N; e++) f[e] = __fmul_rn(static_cast<float>(static_cast<int8_t>(byte_of(w, e))), d);
+    } else if constexpr (FMT == SLHIP_FMT_TQ2_0) {
+        // {u8 qs[64]; f16 d}: value (4j + l) * 32 + m = ((qs[32j + m] >> 2l) & 3) - 1, times d
+        // (Quant.TQ2_0, Quant.Ternary.cs:66-86)
+        const int j = k / 128, l = (k % 128) / 32, m = k % 32;
+        const float d = b.h(o + 64);
+        words(o + 32 * j + m);
+#pragma unroll
+        for (int e = 0; e < N; e++)
+            f[e] = __fmul_rn(static_cast<float>(static_cast<int>((byte_of(w, e) >> (2 * l)) & 3u) - 1), d);
+    } else if constexpr (FMT == SLHIP_FMT_TQ1_0) {
+        // {u8 qs[48]; u8 qh[4]; f16 d}: five base-3 digits per byte -- values n*32 + m from digit n of
+        // qs[m], 160 + n*16 + m from qs[32 + m], 240 + n*4 + j from qh[j] (Quant.TQ1_0, Quant.Ternary.cs:27-64)
+        const float d = b.h(o + 52);
+        if (k < 240) {  // N values of one digit of consecutive bytes
+            const bool a = k < 160;
+            const int n = a ? k / 32 : (k - 160) / 16;
+            words(o + (a ? k % 32 : 32 + (k - 160) % 16));
+#pragma unroll
+            for (int e = 0; e < N; e++) f[e] = __fmul_rn(static_cast<float>(trit(byte_of(w, e), n)), d);
+        } else {  // the last 16: digit n of qh[j] for value 240 + 4n + j
+            const uint32_t qh = b.u32(o + 48);
+#pragma unroll
+            for (int e = 0; e < N; e++) {
+                const int r = k - 240 + e;
+                f[e] = __fmul_rn(static_cast<float>(trit((qh >> (8 * (r % 4))) & 0xFFu, r / 4)), d);
             }
         }
     } else {  // IQ4_NL, IQ4_XS

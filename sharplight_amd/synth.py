@@ -40,10 +40,14 @@ def normal(seed, tid, shape, mean=0.0, std=1.0, dtype="f32"):
 BLOCK = {"q8_0": 34, "q4_0": 18, "q4_1": 20, "q5_0": 22, "q5_1": 24, "iq4_nl": 18}
 # 256-value super-blocks: bytes per block, and the byte offsets of their f16 fields (d, dmin)
 KBLOCK = {"q2_k": (84, (80, 82)), "q3_k": (110, (108,)), "q4_k": (144, (0, 2)), "q5_k": (176, (0, 2)),
-          "q6_k": (210, (208,)), "iq4_xs": (136, (0,))}
+          "q6_k": (210, (208,)), "iq4_xs": (136, (0,)), "tq1_0": (54, (52,)), "tq2_0": (66, (64,))}
+# 4-bit float blocks: bytes, values, and the scale bytes at the block start (E8M0 exponent / UE4M3 scales)
+FP4BLOCK = {"mxfp4": (17, 32, 1), "nvfp4": (36, 64, 4)}
 
 
 def block_values(fmt: str) -> int:
+    if fmt in FP4BLOCK:
+        return FP4BLOCK[fmt][1]
     return 256 if fmt in KBLOCK else 32
 
 
@@ -55,6 +59,10 @@ def row_bytes(fmt: str, D: int) -> int:
     if fmt in KBLOCK:
         assert D % 256 == 0
         return D // 256 * KBLOCK[fmt][0]
+    if fmt in FP4BLOCK:
+        bb, bs, _ = FP4BLOCK[fmt]
+        assert D % bs == 0
+        return D // bs * bb
     assert D % 32 == 0
     return D // 32 * BLOCK[fmt]
 
@@ -64,8 +72,17 @@ def quant_table(fmt: str, V: int, D: int, seed: int = 0, tid: int = 0, scale_lo=
 
     q8_0: int8 codes ~ U{-127..127}; q4_*/q5_*/iq4_nl: bytes ~ U{0..255} (so nibbles ~ U{0..15}); scales and
     mins f16 ~ U[scale_lo, scale_hi]; K-quants / iq4_xs: random bytes with their f16 fields ~ U[scale_lo,
-    scale_hi] (the packed sub-block scales are any bytes); f16: values N(0,1)*0.02; bf16 / f32: N(0,1)*0.02."""
+    scale_hi] (the packed sub-block scales are any bytes); tq1_0 / tq2_0 likewise; mxfp4: codes any bytes,
+    E8M0 exponents ~ U{118..126} (scales 2^-10..2^-2); nvfp4: codes any bytes, UE4M3 scales ~ U{0x20..0x3F}
+    (2^-4 .. 1.9); f16: values N(0,1)*0.02; bf16 / f32: N(0,1)*0.02."""
     g = rng(seed, tid)
+    if fmt in FP4BLOCK:
+        bb, bs, ns = FP4BLOCK[fmt]
+        nb = D // bs
+        t = g.integers(0, 256, size=(V, nb, bb), dtype=np.uint8)
+        lo, hi = (118, 127) if fmt == "mxfp4" else (0x20, 0x40)
+        t[:, :, :ns] = g.integers(lo, hi, size=(V, nb, ns), dtype=np.uint8)
+        return t.reshape(V, nb * bb)
     if fmt in KBLOCK:
         bb, fields = KBLOCK[fmt]
         nb = D // 256
@@ -117,6 +134,8 @@ CONFIGS = {
     "c5_gather_f16": Config("c5_gather_f16", "gather 16384 ids from F16 [151936,4096] -> bf16"),
     "c5_gather_q4_k": Config("c5_gather_q4_k", "gather 16384 ids from Q4_K [151936,4096] -> bf16 (C5 shape, K-quant)"),
     "c5_gather_q6_k": Config("c5_gather_q6_k", "gather 16384 ids from Q6_K [151936,4096] -> bf16 (C5 shape, K-quant)"),
+    "c5_gather_mxfp4": Config("c5_gather_mxfp4", "gather 16384 ids from MXFP4 [151936,4096] -> bf16 (C5 shape, 4-bit float)"),
+    "c5_gather_nvfp4": Config("c5_gather_nvfp4", "gather 16384 ids from NVFP4 [151936,4096] -> bf16 (C5 shape, 4-bit float)"),
 }
 
 

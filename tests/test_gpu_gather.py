@@ -55,7 +55,7 @@ def test_ggml_fixture_rows(device, fmt, dout):
         np.testing.assert_array_equal(y, fx[f"{fmt}_deq"][ids])  # ggml's own values (+0 vs -0 aside)
 
 
-KFMTS = ["q2_k", "q3_k", "q4_k", "q5_k", "q6_k", "iq4_nl", "iq4_xs"]
+KFMTS = ["q2_k", "q3_k", "q4_k", "q5_k", "q6_k", "iq4_nl", "iq4_xs", "tq1_0", "tq2_0", "mxfp4", "nvfp4"]
 
 
 @pytest.mark.parametrize("fmt", ["f32", "f16", "bf16", "q8_0", "q4_0", "q4_1", "q5_0", "q5_1"] + KFMTS)
@@ -63,9 +63,11 @@ KFMTS = ["q2_k", "q3_k", "q4_k", "q5_k", "q6_k", "iq4_nl", "iq4_xs"]
 @pytest.mark.parametrize("D", [32, 256, 4096, 5120, 8192 + 32])
 def test_gather_formats(device, fmt, dout, D):
     """Every format, both outputs: a single block, whole and partial 4096-value chunks, rows that are not
-    a whole number of 16-byte vectors (the general kernel). 256-value formats take D rounded to 256."""
-    if synth.block_values(fmt) == 256:
-        D = max(256, D // 256 * 256) + (256 if D == 8192 + 32 else 0)
+    a whole number of 16-byte vectors (the general kernel). Formats with larger blocks take D rounded to
+    their block size."""
+    bs = synth.block_values(fmt)
+    if bs > 32:  # D rounded to the block size; the ragged case keeps one extra block past 8192
+        D = max(bs, D // bs * bs) + (bs if D == 8192 + 32 else 0)
     V, N = 300, 97
     t = synth.quant_table(fmt, V, D, seed=D, tid=0)
     ids = synth.rng(D, 1).integers(0, V, N).astype(np.int32)

@@ -61,7 +61,7 @@ def _same_bits_or_both_nan(a, b):
         np.array_equal(np.isnan(a), np.isnan(b)) and np.array_equal(a[~np.isnan(a)].view(np.uint32), b[~np.isnan(b)].view(np.uint32)))
 
 
-@pytest.mark.parametrize("fmt", ["q2_k", "q3_k", "iq4_nl", "iq4_xs"])
+@pytest.mark.parametrize("fmt", ["q2_k", "q3_k", "iq4_nl", "iq4_xs", "tq1_0", "tq2_0", "mxfp4", "nvfp4"])
 def test_unfused_formats_match_ggml_bit_for_bit(quant_ext_fx, fmt):
     """The reference decodes these as ggml does (separate multiply and subtract), so ggml's own output in
     ggml_quant_ext.bin -- blocks quantized from gaussian data and random bytes -- must come out bit for bit
@@ -625,3 +625,48 @@ def test_matvec_threaded_equals_plain():
 def test_matvec_rejects_ragged_quant_rows():
     with pytest.raises(ValueError):
         oracle.matvec("q8_0", np.zeros((2, 34), np.uint8), 2, 40, np.zeros((1, 40), np.float32))
+
+
+def test_fp4_scales_and_codes_closed_forms():
+    """MXFP4: every E8M0 byte e gives 2^(e-128) times the doubled E2M1 value of every code; NVFP4: every
+    UE4M3 byte gives (m/8 + 1) 2^(e-7) / 2 (e > 0) or m 2^-9 / 2 (e = 0), bit 7 ignored, 0x7F -> 0."""
+    e2m1 = np.array([0, 0.5, 1, 1.5, 2, 3, 4, 6], np.float64)
+    code_vals = np.concatenate([2 * e2m1, -2 * e2m1])  # doubled, codes 8..15 negative
+    # MXFP4: block = e, then 16 bytes holding codes j (low nibble) and 15 - j (high nibble)
+    blocks = np.zeros((256, 17), np.uint8)
+    blocks[:, 0] = np.arange(256)
+    blocks[:, 1:] = (np.arange(16) | ((15 - np.arange(16)) << 4)).astype(np.uint8)
+    got = oracle.dequant("mxfp4", blocks.reshape(-1), 256 * 32).reshape(256, 32).astype(np.float64)
+    codes = np.concatenate([np.arange(16), 15 - np.arange(16)])
+    want = np.ldexp(1.0, np.arange(256) - 128)[:, None] * code_vals[codes][None, :]
+    assert np.array_equal(got, want.astype(np.float32).astype(np.float64))
+    # NVFP4: four scales per block, code 2 (value 2) everywhere -> 2 * scale
+    x = np.arange(256)
+    e, m = (x >> 3) & 15, x & 7
+    scale = np.where(e == 0, m * 2.0 ** -9, (1 + m / 8) * np.ldexp(1.0, e - 7)) / 2
+    scale[(x == 0) | (x == 0x7F)] = 0
+    blocks = np.zeros((64, 36), np.uint8)
+    blocks[:, :4] = x.reshape(64, 4)
+    blocks[:, 4:] = 0x22
+    got = oracle.dequant("nvfp4", blocks.reshape(-1), 64 * 64).reshape(64, 4, 16).astype(np.float64)
+    assert np.array_equal(got, np.broadcast_to(2 * scale.reshape(64, 4)[..., None], got.shape))
+
+
+def test_tq1_trits_invert_the_ggml_packing():
+    """Five ternary digits t0..t4 (t0 most significant) pack as q = ceil(v * 256 / 243), v = sum t_i 3^(4-i)
+    (ggml's quantize_row_tq1_0); every byte of every TQ1_0 region must decode back to t_n - 1."""
+    v = np.arange(243)
+    q = (v * 256 + 242) // 243
+    digits = np.stack([(v // 3 ** (4 - n)) % 3 for n in range(5)], 1)  # [243, 5]
+    blocks = np.zeros((243, 54), np.uint8)
+    blocks[:, :48] = q[:, None]
+    blocks[:, 48:52] = q[:, None]
+    blocks[:, 52:54] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    got = oracle.dequant("tq1_0", blocks.reshape(-1), 243 * 256).reshape(243, 256)
+    want = np.empty((243, 256))
+    for n in range(5):
+        want[:, n * 32:(n + 1) * 32] = digits[:, n:n + 1] - 1
+        want[:, 160 + n * 16:160 + (n + 1) * 16] = digits[:, n:n + 1] - 1
+    for n in range(4):
+        want[:, 240 + 4 * n:244 + 4 * n] = digits[:, n:n + 1] - 1
+    assert np.array_equal(got, want)
