@@ -353,6 +353,8 @@ WORKLOADS = {
     "c5_gather_q6_k": lambda: C5("q6_k"),
     "c5_gather_mxfp4": lambda: C5("mxfp4"),
     "c5_gather_nvfp4": lambda: C5("nvfp4"),
+    "c5_gather_iq2_xxs": lambda: C5("iq2_xxs"),
+    "c5_gather_iq3_s": lambda: C5("iq3_s"),
     "c4_qk_rope_kv_bf16_paged": lambda: C4Cache(),
     "v_cache_write_f16_paged": lambda: VCache(),
     "dual_matvec_silu_bf16_T1": lambda: DualMatvec(1),
@@ -623,7 +625,7 @@ def cpu_baselines(budget_main: float, budget_op: float, which: set[str]) -> dict
             L.orc_rope_mt(P(kn), P(c["pos"]), None, P(ko), T, 8, 128, 128, 1, c["base"], 1.0, 1.0)
         s, reps = cpu_time(run, budget_op)
         res["c4_qknorm_rope_bf16"] = dict(s=s * 4096 / T, reps=reps, sample=f"{T} of 4096 tokens, scaled x{4096 // T}")
-    for fmt in ("q8_0", "q4_0", "f16", "q4_k", "q6_k", "mxfp4", "nvfp4"):
+    for fmt in ("q8_0", "q4_0", "f16", "q4_k", "q6_k", "mxfp4", "nvfp4", "iq2_xxs", "iq3_s"):
         name = f"c5_gather_{fmt}"
         if name not in which:
             continue

@@ -78,7 +78,16 @@ typedef enum slhip_format {
     SLHIP_FMT_TQ1_0 = 15, /* 54 bytes per 256: qs[48] (5 base-3 digits per byte), qh[4], f16 d -> (t-1)*d */
     SLHIP_FMT_TQ2_0 = 16, /* 66 bytes per 256: qs[64] (4 two-bit codes per byte), f16 d -> (q-1)*d         */
     SLHIP_FMT_MXFP4 = 17, /* 17 bytes per 32: E8M0 e, qs[16] (E2M1 nibbles) -> fp4 * 2^(e-128)            */
-    SLHIP_FMT_NVFP4 = 18  /* 36 bytes per 64: UE4M3 d[4] (per 16), qs[32] (E2M1 nibbles) -> fp4 * d/2      */
+    SLHIP_FMT_NVFP4 = 18, /* 36 bytes per 64: UE4M3 d[4] (per 16), qs[32] (E2M1 nibbles) -> fp4 * d/2      */
+    /* ggml's grid IQ formats (Quant.Iq.cs:113-306), 256 values per block: groups of 8 values index a
+     * lattice table, with sign patterns and small scales */
+    SLHIP_FMT_IQ2_XXS = 19, /* 66 bytes  */
+    SLHIP_FMT_IQ2_XS = 20,  /* 74 bytes  */
+    SLHIP_FMT_IQ2_S = 21,   /* 82 bytes  */
+    SLHIP_FMT_IQ3_XXS = 22, /* 98 bytes  */
+    SLHIP_FMT_IQ3_S = 23,   /* 110 bytes */
+    SLHIP_FMT_IQ1_S = 24,   /* 50 bytes  */
+    SLHIP_FMT_IQ1_M = 25    /* 56 bytes  */
 } slhip_format;
 
 /* Row-norm kinds (StandardOps RmsNorm / L2Norm / LayerNorm). */
@@ -317,7 +326,7 @@ SLHIP_API int slhip_rope(int dtype_in, int dtype_out, const slhip_rope_tensor* t
  * [V, D] tensor in `format`. dtype_out: F32 or BF16 (f32 values rounded to nearest even). An id outside
  * [0, V) leaves its output row zero and raises SLHIP_ERR_INDEX at the next slhip_stream_sync.
  * Formats: F32, F16, BF16, Q8_0, Q4_0, Q4_1, Q5_0, Q5_1 (D a multiple of 32), Q2_K..Q6_K, IQ4_XS, TQ1_0
- * and TQ2_0 (D a multiple of 256), IQ4_NL and MXFP4 (32), NVFP4 (64).
+ * and TQ2_0 and the grid IQ formats IQ2_XXS..IQ1_M (D a multiple of 256), IQ4_NL and MXFP4 (32), NVFP4 (64).
  * Replaces: GatherOp (src/Sharplight.Cpu/GatherOp.cs:22-75) with Quant.Dequantize
  * (src/Sharplight.Cpu/Quant.cs:242-446,500-624; Quant.KQuants.cs:36-107), and the Vulkan gather
  * (GraphLowerer.Transformer.cs:133-179, Kernels/data.slang:4-37).

@@ -22,10 +22,12 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "liboracle.so")
 
 (F32, F16, BF16, Q8_0, Q4_0, Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS, TQ1_0, TQ2_0, MXFP4,
- NVFP4) = range(19)
+ NVFP4, IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_S, IQ1_M) = range(26)
 FORMATS = {"f32": F32, "f16": F16, "bf16": BF16, "q8_0": Q8_0, "q4_0": Q4_0, "q4_1": Q4_1, "q5_0": Q5_0,
            "q5_1": Q5_1, "q2_k": Q2_K, "q3_k": Q3_K, "q4_k": Q4_K, "q5_k": Q5_K, "q6_k": Q6_K, "iq4_nl": IQ4_NL,
-           "iq4_xs": IQ4_XS, "tq1_0": TQ1_0, "tq2_0": TQ2_0, "mxfp4": MXFP4, "nvfp4": NVFP4}
+           "iq4_xs": IQ4_XS, "tq1_0": TQ1_0, "tq2_0": TQ2_0, "mxfp4": MXFP4, "nvfp4": NVFP4,
+           "iq2_xxs": IQ2_XXS, "iq2_xs": IQ2_XS, "iq2_s": IQ2_S, "iq3_xxs": IQ3_XXS, "iq3_s": IQ3_S, "iq1_s": IQ1_S,
+           "iq1_m": IQ1_M}
 ACTS = {"silu": 0, "gelu_tanh": 1, "gelu_erf": 2}
 
 _lib = None

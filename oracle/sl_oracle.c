@@ -13,6 +13,8 @@
 #include "sl_oracle.h"
 
 #include <math.h>
+
+#include "../sharplight_amd/csrc/iq_grids.h" /* ggml's lattice tables: data of the grid IQ formats */
 #include <pthread.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -368,6 +370,13 @@ static int block_bytes(int fmt)
     case ORC_TQ2_0: return 66;
     case ORC_MXFP4: return 17;
     case ORC_NVFP4: return 36;
+    case ORC_IQ2_XXS: return 66;
+    case ORC_IQ2_XS: return 74;
+    case ORC_IQ2_S: return 82;
+    case ORC_IQ3_XXS: return 98;
+    case ORC_IQ3_S: return 110;
+    case ORC_IQ1_S: return 50;
+    case ORC_IQ1_M: return 56;
     default: return -1;
     }
 }
@@ -425,6 +434,131 @@ static int trit(uint8_t b, int n)
 {
     static const int p3[5] = {1, 3, 9, 27, 81};
     return ((((int)b * p3[n]) & 0xFF) * 3 >> 8) - 1;
+}
+
+/* ksigns_iq2xs (IqSigns.cs): a 7-bit index i selects the signs of eight values, bit j set = value j
+ * negative, the eighth sign the parity of the other seven: i | parity(i) << 7. */
+static int ksign(uint32_t i) { return (int)(i | ((uint32_t)__builtin_parity(i) << 7)); }
+static inline uint32_t rd_u32(const uint8_t* p) { uint32_t v; memcpy(&v, p, 4); return v; }
+static inline uint32_t rd_u16(const uint8_t* p) { return (uint32_t)p[0] | ((uint32_t)p[1] << 8); }
+
+/* Quant.StoreSigned8 / StoreSigned4x2 (Quant.Iq.cs:99-111): (grid byte * (+-1)) * scale, one rounding. */
+static void signed8(const uint8_t* g8, int signs, float scale, float* dst)
+{
+    for (int j = 0; j < 8; j++) dst[j] = ((float)g8[j] * ((signs >> j) & 1 ? -1.0f : 1.0f)) * scale;
+}
+
+/* The grid IQ formats (Quant.Iq.cs:113-306), 256 values per block. */
+static void iq_block(int fmt, const uint8_t* p, float* dst)
+{
+    uint8_t g[8];
+    switch (fmt) {
+    case ORC_IQ2_XXS: { /* {f16 d; u16 qs[32]}: per 32 values 4 grid indices, then 4 sign indices + scale */
+        const float d = rd_h(p);
+        for (int ib = 0; ib < 8; ib++, dst += 32) {
+            const uint32_t idx = rd_u32(p + 2 + 8 * ib), ss = rd_u32(p + 6 + 8 * ib);
+            const float db = d * (0.5f + (float)(ss >> 28)) * 0.25f;
+            for (int l = 0; l < 4; l++) {
+                memcpy(g, &kIq2xxsGrid[(idx >> (8 * l)) & 0xFF], 8);
+                signed8(g, ksign((ss >> (7 * l)) & 127), db, dst + 8 * l);
+            }
+        }
+        break;
+    }
+    case ORC_IQ2_XS: { /* {f16 d; u16 qs[32]; u8 scales[8]}: 9-bit grid index + 7-bit sign index */
+        const float d = rd_h(p);
+        for (int ib = 0; ib < 8; ib++, dst += 32) {
+            const int sc = p[66 + ib];
+            const float db0 = d * (0.5f + (float)(sc & 0xF)) * 0.25f, db1 = d * (0.5f + (float)(sc >> 4)) * 0.25f;
+            for (int l = 0; l < 4; l++) {
+                const uint32_t q = rd_u16(p + 2 + 2 * (4 * ib + l));
+                memcpy(g, &kIq2xsGrid[q & 511], 8);
+                signed8(g, ksign(q >> 9), l < 2 ? db0 : db1, dst + 8 * l);
+            }
+        }
+        break;
+    }
+    case ORC_IQ2_S: { /* {f16 d; qs[64] (low index bits, then sign bytes); qh[8]; scales[8]} */
+        const float d = rd_h(p);
+        for (int ib = 0; ib < 8; ib++, dst += 32) {
+            const int sc = p[74 + ib];
+            const float db0 = d * (0.5f + (float)(sc & 0xF)) * 0.25f, db1 = d * (0.5f + (float)(sc >> 4)) * 0.25f;
+            for (int l = 0; l < 4; l++) {
+                const int index = p[2 + 4 * ib + l] | ((p[66 + ib] << (8 - 2 * l)) & 0x300);
+                memcpy(g, &kIq2sGrid[index], 8);
+                signed8(g, p[34 + 4 * ib + l], l < 2 ? db0 : db1, dst + 8 * l);
+            }
+        }
+        break;
+    }
+    case ORC_IQ3_XXS: { /* {f16 d; qs[64] (8-bit indices of 4-value entries); 8 words: 4 sign indices + scale} */
+        const float d = rd_h(p);
+        for (int ib = 0; ib < 8; ib++, dst += 32) {
+            const uint32_t w = rd_u32(p + 66 + 4 * ib);
+            const float db = d * (0.5f + (float)(w >> 28)) * 0.5f;
+            for (int l = 0; l < 4; l++) {
+                memcpy(g, &kIq3xxsGrid[p[2 + 8 * ib + 2 * l]], 4);
+                memcpy(g + 4, &kIq3xxsGrid[p[2 + 8 * ib + 2 * l + 1]], 4);
+                signed8(g, ksign((w >> (7 * l)) & 127), db, dst + 8 * l);
+            }
+        }
+        break;
+    }
+    case ORC_IQ3_S: { /* {f16 d; qs[64]; qh[8]; signs[32]; scales[4]}: 9-bit indices, scales 1 + 2s */
+        const float d = rd_h(p);
+        for (int ib = 0; ib < 8; ib++, dst += 32) {
+            const int s4 = p[106 + ib / 2];
+            const float db = d * (float)(1 + 2 * (ib % 2 == 0 ? (s4 & 0xF) : (s4 >> 4)));
+            const int high = p[66 + ib];
+            for (int l = 0; l < 4; l++) {
+                const int lo = p[2 + 8 * ib + 2 * l] | ((high << (8 - 2 * l)) & 256);
+                const int hi = p[2 + 8 * ib + 2 * l + 1] | ((high << (7 - 2 * l)) & 256);
+                memcpy(g, &kIq3sGrid[lo], 4);
+                memcpy(g + 4, &kIq3sGrid[hi], 4);
+                signed8(g, p[74 + 4 * ib + l], db, dst + 8 * l);
+            }
+        }
+        break;
+    }
+    case ORC_IQ1_S:
+    case ORC_IQ1_M: {
+        /* Quant.StoreIq1 (Quant.Iq.cs:246-251): (grid + delta) * scale, delta +-1/8 */
+        int8_t e[8];
+        if (fmt == ORC_IQ1_S) { /* {f16 d; qs[32]; u16 qh[8]} */
+            const float d = rd_h(p);
+            for (int ib = 0; ib < 8; ib++, dst += 32) {
+                const uint32_t qh = rd_u16(p + 34 + 2 * ib);
+                const float dl = d * (float)(2 * ((qh >> 12) & 7) + 1);
+                const float delta = (qh & 0x8000) ? -0.125f : 0.125f;
+                for (int l = 0; l < 4; l++) {
+                    memcpy(e, &kIq1sGrid[p[2 + 4 * ib + l] | (((qh >> (3 * l)) & 7) << 8)], 8);
+                    for (int j = 0; j < 8; j++) dst[8 * l + j] = ((float)e[j] + delta) * dl;
+                }
+            }
+        } else { /* {qs[32]; qh[16]; u16 scales[4]}, the f16 super-scale in the scales' top nibbles */
+            uint32_t sc[4];
+            for (int i = 0; i < 4; i++) sc[i] = rd_u16(p + 48 + 2 * i);
+            const uint32_t bits = (sc[0] >> 12) | ((sc[1] >> 8) & 0x00F0) | ((sc[2] >> 4) & 0x0F00) | (sc[3] & 0xF000);
+            const float d = orc_f16_to_f32((uint16_t)bits);
+            for (int ib = 0; ib < 8; ib++, dst += 32) {
+                const float dl1 = d * (float)(2 * ((sc[ib / 2] >> (6 * (ib % 2))) & 7) + 1);
+                const float dl2 = d * (float)(2 * ((sc[ib / 2] >> (6 * (ib % 2) + 3)) & 7) + 1);
+                const uint8_t* qs = p + 4 * ib;
+                const uint8_t* qh = p + 32 + 2 * ib;
+                const int idx[4] = {qs[0] | ((qh[0] << 8) & 0x700), qs[1] | ((qh[0] << 4) & 0x700),
+                                    qs[2] | ((qh[1] << 8) & 0x700), qs[3] | ((qh[1] << 4) & 0x700)};
+                const int neg[4] = {qh[0] & 0x08, qh[0] & 0x80, qh[1] & 0x08, qh[1] & 0x80};
+                for (int l = 0; l < 4; l++) {
+                    memcpy(e, &kIq1sGrid[idx[l]], 8);
+                    const float delta = neg[l] ? -0.125f : 0.125f, dl = l < 2 ? dl1 : dl2;
+                    for (int j = 0; j < 8; j++) dst[8 * l + j] = ((float)e[j] + delta) * dl;
+                }
+            }
+        }
+        break;
+    }
+    default: break;
+    }
 }
 
 /* One block of a K-quant or codebook format (256 values; IQ4_NL 32):
@@ -533,6 +667,10 @@ static void kblock(int fmt, const uint8_t* p, float* dst)
         }
         break;
     }
+    case ORC_IQ2_XXS: case ORC_IQ2_XS: case ORC_IQ2_S: case ORC_IQ3_XXS: case ORC_IQ3_S: case ORC_IQ1_S:
+    case ORC_IQ1_M:
+        iq_block(fmt, p, dst);
+        break;
     case ORC_TQ1_0: {  /* Quant.TQ1_0 (Quant.Ternary.cs:27-64): {qs[48], qh[4], f16 d} */
         const float d = rd_h(p + 52);
         for (int n = 0; n < 5; n++) {

@@ -23,7 +23,8 @@ extern "C" {
 /* Table formats, numbered like the C ABI's slhip_format (include/sharplight_hip.h). */
 enum { ORC_F32 = 0, ORC_F16 = 1, ORC_BF16 = 2, ORC_Q8_0 = 3, ORC_Q4_0 = 4, ORC_Q4_1 = 5, ORC_Q5_0 = 6, ORC_Q5_1 = 7,
        ORC_Q2_K = 8, ORC_Q3_K = 9, ORC_Q4_K = 10, ORC_Q5_K = 11, ORC_Q6_K = 12, ORC_IQ4_NL = 13, ORC_IQ4_XS = 14,
-       ORC_TQ1_0 = 15, ORC_TQ2_0 = 16, ORC_MXFP4 = 17, ORC_NVFP4 = 18 };
+       ORC_TQ1_0 = 15, ORC_TQ2_0 = 16, ORC_MXFP4 = 17, ORC_NVFP4 = 18, ORC_IQ2_XXS = 19, ORC_IQ2_XS = 20,
+       ORC_IQ2_S = 21, ORC_IQ3_XXS = 22, ORC_IQ3_S = 23, ORC_IQ1_S = 24, ORC_IQ1_M = 25 };
 
 /* ---- scalar conversions (Simd.cs:518-540, Quant.cs:371-381) ---- */
 uint16_t orc_f32_to_bf16(float f);

@@ -252,6 +252,13 @@ __global__ __launch_bounds__(256) void gather_scalar(GatherArgs a, int fmt)
             case SLHIP_FMT_TQ2_0: v = kv(std::integral_constant<int, SLHIP_FMT_TQ2_0>{}); break;
             case SLHIP_FMT_MXFP4: v = kv(std::integral_constant<int, SLHIP_FMT_MXFP4>{}); break;
             case SLHIP_FMT_NVFP4: v = kv(std::integral_constant<int, SLHIP_FMT_NVFP4>{}); break;
+            case SLHIP_FMT_IQ2_XXS: v = kv(std::integral_constant<int, SLHIP_FMT_IQ2_XXS>{}); break;
+            case SLHIP_FMT_IQ2_XS: v = kv(std::integral_constant<int, SLHIP_FMT_IQ2_XS>{}); break;
+            case SLHIP_FMT_IQ2_S: v = kv(std::integral_constant<int, SLHIP_FMT_IQ2_S>{}); break;
+            case SLHIP_FMT_IQ3_XXS: v = kv(std::integral_constant<int, SLHIP_FMT_IQ3_XXS>{}); break;
+            case SLHIP_FMT_IQ3_S: v = kv(std::integral_constant<int, SLHIP_FMT_IQ3_S>{}); break;
+            case SLHIP_FMT_IQ1_S: v = kv(std::integral_constant<int, SLHIP_FMT_IQ1_S>{}); break;
+            case SLHIP_FMT_IQ1_M: v = kv(std::integral_constant<int, SLHIP_FMT_IQ1_M>{}); break;
             case SLHIP_FMT_F32: {
                 uint32_t u = p[4 * j] | (p[4 * j + 1] << 8) | (p[4 * j + 2] << 16) | (static_cast<uint32_t>(p[4 * j + 3]) << 24);
                 v = __uint_as_float(u);
@@ -308,6 +315,13 @@ static int block_bytes(int fmt)
     case SLHIP_FMT_TQ2_0: return 66;
     case SLHIP_FMT_MXFP4: return 17;
     case SLHIP_FMT_NVFP4: return 36;
+    case SLHIP_FMT_IQ2_XXS: return 66;
+    case SLHIP_FMT_IQ2_XS: return 74;
+    case SLHIP_FMT_IQ2_S: return 82;
+    case SLHIP_FMT_IQ3_XXS: return 98;
+    case SLHIP_FMT_IQ3_S: return 110;
+    case SLHIP_FMT_IQ1_S: return 50;
+    case SLHIP_FMT_IQ1_M: return 56;
     default: return -1;
     }
 }
@@ -418,6 +432,13 @@ static int dispatch(int fmt, GatherArgs a, hipStream_t st)
         case SLHIP_FMT_TQ2_0: return launch_quant<SLHIP_FMT_TQ2_0, DTO>(a, st);
         case SLHIP_FMT_MXFP4: return launch_quant<SLHIP_FMT_MXFP4, DTO>(a, st);
         case SLHIP_FMT_NVFP4: return launch_quant<SLHIP_FMT_NVFP4, DTO>(a, st);
+        case SLHIP_FMT_IQ2_XXS: return launch_quant<SLHIP_FMT_IQ2_XXS, DTO>(a, st);
+        case SLHIP_FMT_IQ2_XS: return launch_quant<SLHIP_FMT_IQ2_XS, DTO>(a, st);
+        case SLHIP_FMT_IQ2_S: return launch_quant<SLHIP_FMT_IQ2_S, DTO>(a, st);
+        case SLHIP_FMT_IQ3_XXS: return launch_quant<SLHIP_FMT_IQ3_XXS, DTO>(a, st);
+        case SLHIP_FMT_IQ3_S: return launch_quant<SLHIP_FMT_IQ3_S, DTO>(a, st);
+        case SLHIP_FMT_IQ1_S: return launch_quant<SLHIP_FMT_IQ1_S, DTO>(a, st);
+        case SLHIP_FMT_IQ1_M: return launch_quant<SLHIP_FMT_IQ1_M, DTO>(a, st);
         case SLHIP_FMT_F16: return launch_plain<SLHIP_FMT_F16, DTO>(a, st);
         case SLHIP_FMT_BF16: return launch_plain<SLHIP_FMT_BF16, DTO>(a, st);
         case SLHIP_FMT_F32: return launch_plain<SLHIP_FMT_F32, DTO>(a, st);

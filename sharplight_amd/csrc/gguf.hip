@@ -94,20 +94,20 @@ TypeDesc type_desc(int id)
     case 13: return t("q5_k", 256, 176, SLHIP_FMT_Q5_K);
     case 14: return t("q6_k", 256, 210, SLHIP_FMT_Q6_K);
     case 15: return t("q8_k", 256, 292);
-    case 16: return t("iq2_xxs", 256, 66);
-    case 17: return t("iq2_xs", 256, 74);
-    case 18: return t("iq3_xxs", 256, 98);
-    case 19: return t("iq1_s", 256, 50);
+    case 16: return t("iq2_xxs", 256, 66, SLHIP_FMT_IQ2_XXS);
+    case 17: return t("iq2_xs", 256, 74, SLHIP_FMT_IQ2_XS);
+    case 18: return t("iq3_xxs", 256, 98, SLHIP_FMT_IQ3_XXS);
+    case 19: return t("iq1_s", 256, 50, SLHIP_FMT_IQ1_S);
     case 20: return t("iq4_nl", 32, 18, SLHIP_FMT_IQ4_NL);
-    case 21: return t("iq3_s", 256, 110);
-    case 22: return t("iq2_s", 256, 82);
+    case 21: return t("iq3_s", 256, 110, SLHIP_FMT_IQ3_S);
+    case 22: return t("iq2_s", 256, 82, SLHIP_FMT_IQ2_S);
     case 23: return t("iq4_xs", 256, 136, SLHIP_FMT_IQ4_XS);
     case 24: return t("i8", 1, 1);
     case 25: return t("i16", 1, 2);
     case 26: return t("i32", 1, 4);
     case 27: return t("i64", 1, 8);
     case 28: return t("f64", 1, 8);
-    case 29: return t("iq1_m", 256, 56);
+    case 29: return t("iq1_m", 256, 56, SLHIP_FMT_IQ1_M);
     case 30: return t("bf16", 1, 2, SLHIP_FMT_BF16);
     case 31: case 32: case 33: {  // Q4_0_4_4, Q4_0_4_8, Q4_0_8_8: read as Q4_0 rows
         TypeDesc d = t("q4_0", 32, 18, SLHIP_FMT_Q4_0);

@@ -62,7 +62,8 @@ void check(int st)
 
 // ---- graph ---------------------------------------------------------------------------------------------
 
-enum class DType { F32, F16, BF16, I32, Q8_0, Q4_0, Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS, TQ1_0, TQ2_0, MXFP4, NVFP4 };
+enum class DType { F32, F16, BF16, I32, Q8_0, Q4_0, Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS, TQ1_0, TQ2_0, MXFP4, NVFP4,
+                   IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_S, IQ1_M };
 
 struct TypeInfo {
     const char* name;
@@ -77,7 +78,9 @@ const TypeInfo kTypes[] = {
     {"q2_k", DType::Q2_K, 256, 84}, {"q3_k", DType::Q3_K, 256, 110}, {"q4_k", DType::Q4_K, 256, 144},
     {"q5_k", DType::Q5_K, 256, 176}, {"q6_k", DType::Q6_K, 256, 210}, {"iq4_nl", DType::IQ4_NL, 32, 18},
     {"iq4_xs", DType::IQ4_XS, 256, 136}, {"tq1_0", DType::TQ1_0, 256, 54}, {"tq2_0", DType::TQ2_0, 256, 66},
-    {"mxfp4", DType::MXFP4, 32, 17}, {"nvfp4", DType::NVFP4, 64, 36},
+    {"mxfp4", DType::MXFP4, 32, 17}, {"nvfp4", DType::NVFP4, 64, 36}, {"iq2_xxs", DType::IQ2_XXS, 256, 66},
+    {"iq2_xs", DType::IQ2_XS, 256, 74}, {"iq2_s", DType::IQ2_S, 256, 82}, {"iq3_xxs", DType::IQ3_XXS, 256, 98},
+    {"iq3_s", DType::IQ3_S, 256, 110}, {"iq1_s", DType::IQ1_S, 256, 50}, {"iq1_m", DType::IQ1_M, 256, 56},
 };
 
 const TypeInfo& type_info(DType t)
@@ -121,6 +124,13 @@ int format_code(DType t)
     case DType::TQ2_0: return SLHIP_FMT_TQ2_0;
     case DType::MXFP4: return SLHIP_FMT_MXFP4;
     case DType::NVFP4: return SLHIP_FMT_NVFP4;
+    case DType::IQ2_XXS: return SLHIP_FMT_IQ2_XXS;
+    case DType::IQ2_XS: return SLHIP_FMT_IQ2_XS;
+    case DType::IQ2_S: return SLHIP_FMT_IQ2_S;
+    case DType::IQ3_XXS: return SLHIP_FMT_IQ3_XXS;
+    case DType::IQ3_S: return SLHIP_FMT_IQ3_S;
+    case DType::IQ1_S: return SLHIP_FMT_IQ1_S;
+    case DType::IQ1_M: return SLHIP_FMT_IQ1_M;
     default: unsupported("gather table type");
     }
 }

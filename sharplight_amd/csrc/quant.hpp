@@ -9,6 +9,10 @@
 
 #include "common.hpp"
 
+// plain device globals: as constant-address-space arrays, per-lane lookups were turned into scalar loads
+#define SLHIP_GRID_QUAL static __device__
+#include "iq_grids.h"
+
 namespace slhip {
 
 // BB: bytes per block; BS: values per block; QS / QH: byte offsets of the codes and of the fifth bits;
@@ -30,6 +34,19 @@ template <> struct Fmt<SLHIP_FMT_TQ1_0> { static constexpr int BB = 54, BS = 256
 template <> struct Fmt<SLHIP_FMT_TQ2_0> { static constexpr int BB = 66, BS = 256, QS = 0, QH = -1; static constexpr bool M = false, K = true; static constexpr int OFF = 0; };
 template <> struct Fmt<SLHIP_FMT_MXFP4> { static constexpr int BB = 17, BS = 32, QS = 0, QH = -1; static constexpr bool M = false, K = true; static constexpr int OFF = 0; };
 template <> struct Fmt<SLHIP_FMT_NVFP4> { static constexpr int BB = 36, BS = 64, QS = 0, QH = -1; static constexpr bool M = false, K = true; static constexpr int OFF = 0; };
+template <> struct Fmt<SLHIP_FMT_IQ2_XXS> { static constexpr int BB = 66, BS = 256, QS = 0, QH = -1; static constexpr bool M = false, K = true; static constexpr int OFF = 0; };
+template <> struct Fmt<SLHIP_FMT_IQ2_XS> { static constexpr int BB = 74, BS = 256, QS = 0, QH = -1; static constexpr bool M = false, K = true; static constexpr int OFF = 0; };
+template <> struct Fmt<SLHIP_FMT_IQ2_S> { static constexpr int BB = 82, BS = 256, QS = 0, QH = -1; static constexpr bool M = false, K = true; static constexpr int OFF = 0; };
+template <> struct Fmt<SLHIP_FMT_IQ3_XXS> { static constexpr int BB = 98, BS = 256, QS = 0, QH = -1; static constexpr bool M = false, K = true; static constexpr int OFF = 0; };
+template <> struct Fmt<SLHIP_FMT_IQ3_S> { static constexpr int BB = 110, BS = 256, QS = 0, QH = -1; static constexpr bool M = false, K = true; static constexpr int OFF = 0; };
+template <> struct Fmt<SLHIP_FMT_IQ1_S> { static constexpr int BB = 50, BS = 256, QS = 0, QH = -1; static constexpr bool M = false, K = true; static constexpr int OFF = 0; };
+template <> struct Fmt<SLHIP_FMT_IQ1_M> { static constexpr int BB = 56, BS = 256, QS = 0, QH = -1; static constexpr bool M = false, K = true; static constexpr int OFF = 0; };
+
+constexpr bool is_grid_iq(int f)
+{
+    return f == SLHIP_FMT_IQ2_XXS || f == SLHIP_FMT_IQ2_XS || f == SLHIP_FMT_IQ2_S || f == SLHIP_FMT_IQ3_XXS ||
+           f == SLHIP_FMT_IQ3_S || f == SLHIP_FMT_IQ1_S || f == SLHIP_FMT_IQ1_M;
+}
 
 __device__ __forceinline__ uint32_t lds_u16(const uint32_t* s, int off)
 {
@@ -240,6 +257,72 @@ __device__ __forceinline__ int trit(uint32_t q, int n)
     return static_cast<int>((((q * p3) & 0xFFu) * 3u) >> 8) - 1;
 }
 
+// ksigns_iq2xs: the 7-bit index i with its parity as the eighth sign bit (bit j set: value j negative).
+__device__ __forceinline__ uint32_t ksign(uint32_t i) { return i | ((__popc(i) & 1u) << 7); }
+
+// One 8-value group g (0..31) of a grid IQ block at byte offset o (Quant.Iq.cs:113-306): the eight grid
+// bytes (two 4-byte entries for the IQ3 formats), the sign bits and the group's scale; the IQ1 formats
+// give the delta (+-1/8) instead of signs. The scales keep the reference's order of f32 operations.
+template <int FMT, class B>
+__device__ __forceinline__ void iq_group(const B& b, int o, int g, uint2& gv, uint32_t& signs, float& scale, float& delta)
+{
+    const int ib = g / 4, l = g % 4;
+    signs = 0;
+    delta = 0.0f;
+    if constexpr (FMT == SLHIP_FMT_IQ2_XXS) {
+        const uint32_t idx = b.u32(o + 2 + 8 * ib), ss = b.u32(o + 6 + 8 * ib);
+        scale = __fmul_rn(__fmul_rn(b.h(o), 0.5f + static_cast<float>(ss >> 28)), 0.25f);
+        const uint64_t e = kIq2xxsGrid[(idx >> (8 * l)) & 0xFFu];
+        gv = make_uint2(static_cast<uint32_t>(e), static_cast<uint32_t>(e >> 32));
+        signs = ksign((ss >> (7 * l)) & 127u);
+    } else if constexpr (FMT == SLHIP_FMT_IQ2_XS || FMT == SLHIP_FMT_IQ2_S) {
+        const uint32_t sc = b.u8(o + (FMT == SLHIP_FMT_IQ2_XS ? 66 : 74) + ib);
+        scale = __fmul_rn(__fmul_rn(b.h(o), 0.5f + static_cast<float>(l < 2 ? (sc & 0xFu) : (sc >> 4))), 0.25f);
+        uint64_t e;
+        if constexpr (FMT == SLHIP_FMT_IQ2_XS) {
+            const uint32_t q = b.u16(o + 2 + 2 * (4 * ib + l));
+            e = kIq2xsGrid[q & 511u];
+            signs = ksign(q >> 9);
+        } else {
+            const uint32_t index = b.u8(o + 2 + 4 * ib + l) | ((b.u8(o + 66 + ib) << (8 - 2 * l)) & 0x300u);
+            e = kIq2sGrid[index];
+            signs = b.u8(o + 34 + 4 * ib + l);
+        }
+        gv = make_uint2(static_cast<uint32_t>(e), static_cast<uint32_t>(e >> 32));
+    } else if constexpr (FMT == SLHIP_FMT_IQ3_XXS) {
+        const uint32_t w = b.u32(o + 66 + 4 * ib);
+        scale = __fmul_rn(__fmul_rn(b.h(o), 0.5f + static_cast<float>(w >> 28)), 0.5f);
+        gv = make_uint2(kIq3xxsGrid[b.u8(o + 2 + 8 * ib + 2 * l)], kIq3xxsGrid[b.u8(o + 2 + 8 * ib + 2 * l + 1)]);
+        signs = ksign((w >> (7 * l)) & 127u);
+    } else if constexpr (FMT == SLHIP_FMT_IQ3_S) {
+        const uint32_t s4 = b.u8(o + 106 + ib / 2);
+        scale = __fmul_rn(b.h(o), static_cast<float>(1 + 2 * static_cast<int>(ib % 2 == 0 ? (s4 & 0xFu) : (s4 >> 4))));
+        const uint32_t high = b.u8(o + 66 + ib);
+        const uint32_t lo = b.u8(o + 2 + 8 * ib + 2 * l) | ((high << (8 - 2 * l)) & 256u);
+        const uint32_t hi = b.u8(o + 2 + 8 * ib + 2 * l + 1) | ((high << (7 - 2 * l)) & 256u);
+        gv = make_uint2(kIq3sGrid[lo], kIq3sGrid[hi]);
+        signs = b.u8(o + 74 + 4 * ib + l);
+    } else if constexpr (FMT == SLHIP_FMT_IQ1_S) {
+        const uint32_t qh = b.u16(o + 34 + 2 * ib);
+        scale = __fmul_rn(b.h(o), static_cast<float>(2 * static_cast<int>((qh >> 12) & 7u) + 1));
+        delta = (qh & 0x8000u) ? -0.125f : 0.125f;
+        const uint64_t e = kIq1sGrid[b.u8(o + 2 + 4 * ib + l) | (((qh >> (3 * l)) & 7u) << 8)];
+        gv = make_uint2(static_cast<uint32_t>(e), static_cast<uint32_t>(e >> 32));
+    } else {  // IQ1_M
+        const uint32_t s0 = b.u16(o + 48), s1 = b.u16(o + 50), s2 = b.u16(o + 52), s3 = b.u16(o + 54);
+        const uint32_t bits = (s0 >> 12) | ((s1 >> 8) & 0x00F0u) | ((s2 >> 4) & 0x0F00u) | (s3 & 0xF000u);
+        const float d = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
+        const uint32_t sw = b.u16(o + 48 + 2 * (ib / 2));
+        const int sh = 6 * (ib % 2) + (l < 2 ? 0 : 3);
+        scale = __fmul_rn(d, static_cast<float>(2 * static_cast<int>((sw >> sh) & 7u) + 1));
+        const uint32_t qh = b.u8(o + 32 + 2 * ib + l / 2);
+        const uint32_t index = b.u8(o + 4 * ib + l) | ((l % 2 == 0 ? (qh << 8) : (qh << 4)) & 0x700u);
+        delta = (qh & (l % 2 == 0 ? 0x08u : 0x80u)) ? -0.125f : 0.125f;
+        const uint64_t e = kIq1sGrid[index];
+        gv = make_uint2(static_cast<uint32_t>(e), static_cast<uint32_t>(e >> 32));
+    }
+}
+
 // N (4 or 8) consecutive values k .. k+N-1 (k a multiple of N) of the K-quant or codebook block at byte
 // offset o, decoded with the reference's arithmetic (src/Sharplight.Cpu/Quant.cs:407-446,500-624,
 // Quant.KQuants.cs:36-107): the N values share one sub-block scale.
@@ -313,6 +396,28 @@ __device__ __forceinline__ void decode_k(const B& b, int o, int k, float* f)
             for (int e = 0; e < N; e++) {
                 const int v = static_cast<int>((byte_of(w, e) >> (2 * j)) & 3u) + 4 * static_cast<int>(byte_of(hw, e)) - 4;
                 f[e] = __fmul_rn(static_cast<float>(v), dl);
+            }
+        }
+    } else if constexpr (is_grid_iq(FMT)) {
+        // (grid byte * (+-1)) * scale for IQ2/IQ3 (Quant.StoreSigned8/4x2), (grid + delta) * scale for IQ1
+        // (Quant.StoreIq1): one rounding per value
+        uint2 gv;
+        uint32_t signs;
+        float scale, delta;
+        iq_group<FMT>(b, o, k / 8, gv, signs, scale, delta);
+        const int j0 = k % 8;  // 0, or 4 when N = 4
+        // The word is chosen by a select: indexed as a two-entry array with the runtime j0, the compiler
+        // folded the index into the table address and loaded it as if it were the same for every lane.
+        const uint32_t w_lo = N == 8 ? gv.x : (j0 == 0 ? gv.x : gv.y);
+#pragma unroll
+        for (int e = 0; e < N; e++) {
+            const int j = j0 + e;
+            const uint32_t byte = ((e < 4 ? w_lo : gv.y) >> (8 * (e & 3))) & 0xFFu;
+            if constexpr (FMT == SLHIP_FMT_IQ1_S || FMT == SLHIP_FMT_IQ1_M) {
+                f[e] = __fmul_rn(static_cast<float>(static_cast<int8_t>(byte)) + delta, scale);
+            } else {
+                const float v = static_cast<float>(byte);
+                f[e] = __fmul_rn((signs >> j) & 1u ? -v : v, scale);
             }
         }
     } else if constexpr (FMT == SLHIP_FMT_MXFP4) {

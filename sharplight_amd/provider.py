@@ -25,7 +25,8 @@ NP = {"f32": np.float32, "f16": np.float16, "bf16": np.uint16, "i32": np.int32}
 BLOCKS = {"q8_0": (32, 34), "q4_0": (32, 18), "q4_1": (32, 20), "q5_0": (32, 22), "q5_1": (32, 24),
           "q2_k": (256, 84), "q3_k": (256, 110), "q4_k": (256, 144), "q5_k": (256, 176), "q6_k": (256, 210),
           "iq4_nl": (32, 18), "iq4_xs": (256, 136), "tq1_0": (256, 54), "tq2_0": (256, 66), "mxfp4": (32, 17),
-          "nvfp4": (64, 36)}
+          "nvfp4": (64, 36), "iq2_xxs": (256, 66), "iq2_xs": (256, 74), "iq2_s": (256, 82), "iq3_xxs": (256, 98),
+          "iq3_s": (256, 110), "iq1_s": (256, 50), "iq1_m": (256, 56)}
 ELEM_BYTES = {"f32": 4, "f16": 2, "bf16": 2, "i32": 4}
 
 

@@ -40,7 +40,9 @@ def normal(seed, tid, shape, mean=0.0, std=1.0, dtype="f32"):
 BLOCK = {"q8_0": 34, "q4_0": 18, "q4_1": 20, "q5_0": 22, "q5_1": 24, "iq4_nl": 18}
 # 256-value super-blocks: bytes per block, and the byte offsets of their f16 fields (d, dmin)
 KBLOCK = {"q2_k": (84, (80, 82)), "q3_k": (110, (108,)), "q4_k": (144, (0, 2)), "q5_k": (176, (0, 2)),
-          "q6_k": (210, (208,)), "iq4_xs": (136, (0,)), "tq1_0": (54, (52,)), "tq2_0": (66, (64,))}
+          "q6_k": (210, (208,)), "iq4_xs": (136, (0,)), "tq1_0": (54, (52,)), "tq2_0": (66, (64,)),
+          "iq2_xxs": (66, (0,)), "iq2_xs": (74, (0,)), "iq2_s": (82, (0,)), "iq3_xxs": (98, (0,)), "iq3_s": (110, (0,)),
+          "iq1_s": (50, (0,)), "iq1_m": (56, ())}
 # 4-bit float blocks: bytes, values, and the scale bytes at the block start (E8M0 exponent / UE4M3 scales)
 FP4BLOCK = {"mxfp4": (17, 32, 1), "nvfp4": (36, 64, 4)}
 
@@ -90,6 +92,12 @@ def quant_table(fmt: str, V: int, D: int, seed: int = 0, tid: int = 0, scale_lo=
         for f in fields:
             v = g.uniform(scale_lo, scale_hi, size=(V, nb)).astype(np.float16)
             t[:, :, f:f + 2] = v.view(np.uint8).reshape(V, nb, 2)
+        if fmt == "iq1_m":  # the f16 scale lives in the top nibbles of the four u16 scale words
+            bits = g.uniform(scale_lo, scale_hi, size=(V, nb)).astype(np.float16).view(np.uint16).astype(np.uint32)
+            w = t[:, :, 48:56].copy().view(np.uint16).astype(np.uint32)
+            for i in range(4):
+                w[..., i] = (w[..., i] & 0x0FFF) | (((bits >> (4 * i)) & 0xF) << 12)
+            t[:, :, 48:56] = w.astype(np.uint16).view(np.uint8).reshape(V, nb, 8)
         return t.reshape(V, nb * bb)
     if fmt in ("f16", "bf16", "f32"):
         x = (g.standard_normal(size=(V, D), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
@@ -136,6 +144,8 @@ CONFIGS = {
     "c5_gather_q6_k": Config("c5_gather_q6_k", "gather 16384 ids from Q6_K [151936,4096] -> bf16 (C5 shape, K-quant)"),
     "c5_gather_mxfp4": Config("c5_gather_mxfp4", "gather 16384 ids from MXFP4 [151936,4096] -> bf16 (C5 shape, 4-bit float)"),
     "c5_gather_nvfp4": Config("c5_gather_nvfp4", "gather 16384 ids from NVFP4 [151936,4096] -> bf16 (C5 shape, 4-bit float)"),
+    "c5_gather_iq2_xxs": Config("c5_gather_iq2_xxs", "gather 16384 ids from IQ2_XXS [151936,4096] -> bf16 (C5 shape, grid IQ)"),
+    "c5_gather_iq3_s": Config("c5_gather_iq3_s", "gather 16384 ids from IQ3_S [151936,4096] -> bf16 (C5 shape, grid IQ)"),
 }
 
 

@@ -55,7 +55,8 @@ def test_ggml_fixture_rows(device, fmt, dout):
         np.testing.assert_array_equal(y, fx[f"{fmt}_deq"][ids])  # ggml's own values (+0 vs -0 aside)
 
 
-KFMTS = ["q2_k", "q3_k", "q4_k", "q5_k", "q6_k", "iq4_nl", "iq4_xs", "tq1_0", "tq2_0", "mxfp4", "nvfp4"]
+KFMTS = ["q2_k", "q3_k", "q4_k", "q5_k", "q6_k", "iq4_nl", "iq4_xs", "tq1_0", "tq2_0", "mxfp4", "nvfp4", "iq2_xxs",
+         "iq2_xs", "iq2_s", "iq3_xxs", "iq3_s", "iq1_s", "iq1_m"]
 
 
 @pytest.mark.parametrize("fmt", ["f32", "f16", "bf16", "q8_0", "q4_0", "q4_1", "q5_0", "q5_1"] + KFMTS)

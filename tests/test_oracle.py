@@ -61,7 +61,8 @@ def _same_bits_or_both_nan(a, b):
         np.array_equal(np.isnan(a), np.isnan(b)) and np.array_equal(a[~np.isnan(a)].view(np.uint32), b[~np.isnan(b)].view(np.uint32)))
 
 
-@pytest.mark.parametrize("fmt", ["q2_k", "q3_k", "iq4_nl", "iq4_xs", "tq1_0", "tq2_0", "mxfp4", "nvfp4"])
+@pytest.mark.parametrize("fmt", ["q2_k", "q3_k", "iq4_nl", "iq4_xs", "tq1_0", "tq2_0", "mxfp4", "nvfp4", "iq2_xxs",
+                                 "iq2_xs", "iq2_s", "iq3_xxs", "iq3_s", "iq1_s", "iq1_m"])
 def test_unfused_formats_match_ggml_bit_for_bit(quant_ext_fx, fmt):
     """The reference decodes these as ggml does (separate multiply and subtract), so ggml's own output in
     ggml_quant_ext.bin -- blocks quantized from gaussian data and random bytes -- must come out bit for bit
@@ -670,3 +671,35 @@ def test_tq1_trits_invert_the_ggml_packing():
     for n in range(4):
         want[:, 240 + 4 * n:244 + 4 * n] = digits[:, n:n + 1] - 1
     assert np.array_equal(got, want)
+
+
+def _grid(name, n, width):
+    """A table of iq_grids.h as an [n, width] byte array."""
+    import re
+    text = open(os.path.join(os.path.dirname(__file__), "..", "sharplight_amd", "csrc", "iq_grids.h")).read()
+    body = text[text.index(name + "["):]
+    body = body[body.index("{") + 1:body.index("}")]
+    vals = [int(v.rstrip("ul"), 16) for v in re.findall(r"0x[0-9a-f]+u?l*", body)]
+    assert len(vals) == n
+    dt = np.uint64 if width == 8 else np.uint32
+    return np.array(vals, dt).view(np.uint8).reshape(n, width), np.array(vals, dt)
+
+
+def test_iq_grid_tables_have_the_lattice_structure():
+    """ggml's lattice tables: IQ2 entries take the values {8, 25, 43}, IQ3 entries {4, 12, ..., 52, 62}, IQ1
+    entries {-1, 0, 1}; entries are distinct and ascending as ggml lists them (the IQ1 entries as base-3
+    numbers), with the table sizes the
+    index widths imply. A corrupted or shifted entry breaks one of these; the fixture records above pin the
+    entries their blocks use bit for bit."""
+    for name, n, w, allowed in [("kIq2xxsGrid", 256, 8, {8, 25, 43}), ("kIq2xsGrid", 512, 8, {8, 25, 43}),
+                                ("kIq2sGrid", 1024, 8, {8, 25, 43}),
+                                ("kIq3xxsGrid", 256, 4, {4, 12, 20, 28, 36, 44, 52, 62}),
+                                ("kIq3sGrid", 512, 4, {1, 3, 5, 7, 9, 11, 13, 15}),
+                                ("kIq1sGrid", 2048, 8, {0xFF, 0, 1})]:
+        b, v = _grid(name, n, w)
+        assert set(np.unique(b).tolist()) <= allowed, name
+        if name == "kIq1sGrid":  # ascending as base-3 numbers, byte 7 the most significant digit
+            key = ((b.view(np.int8)[:, ::-1].astype(np.int64) + 1) * 3 ** np.arange(7, -1, -1)).sum(1)
+        else:
+            key = v
+        assert np.all(key[1:] > key[:-1]), name
