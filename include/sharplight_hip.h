@@ -228,7 +228,7 @@ SLHIP_API int slhip_rownorm_copies(int kind, int dtype_in, int dtype_out, const 
  *   act: SLHIP_ACT_SILU / GELU_TANH / GELU_ERF, the same forms as slhip_gated_act.
  * Products and sums in f32 (in another order than the CPU provider's, so equal to it within the rounding of
  * a K-term f32 dot product); block formats sum d * sum(x q) + a * sum(x) per block, as the reference's
- * fused Q4_0 dot does. BF16 weights with T >= SLHIP_MATVEC_MFMA_MIN_T (environment, default 5; 0 keeps the
+ * fused Q4_0 dot does. BF16 weights with T >= SLHIP_MATVEC_MFMA_MIN_T (environment, default 3; 0 keeps the
  * VALU kernel) and K a multiple of 64 go to the matrix cores with f32 x split exactly into three bf16 parts:
  * the same products, summed in another order, under the same bound.
  * Replaces: MatMulOp's float-row path (src/Sharplight.Cpu/MatMulOp.cs:376-465; fused Q8_0/Q4_0 dots, Quant.cs:738-803)

@@ -543,6 +543,169 @@ __global__ __launch_bounds__(64 * kMmWaves) void matvec_mfma(MatvecArgs a)
     }
 }
 
+// The same product with the weights staged row by row: reading a 16-row tile straight into MFMA operands
+// puts 16 rows x 64 bytes in every load instruction, a pattern HBM serves at ~5.0 TB/s, while 1 KiB of one
+// or two rows per instruction streams at ~6.4 TB/s. So per stage of SK values, the block loads the tile's
+// rows contiguously into LDS (row pitch SK*2 + 16 bytes: the 16 rows of an A fragment fall 4 banks apart),
+// and each wave reads its A fragments from there. Stages are double-buffered: the next stage's rows (and
+// this wave's x) are in flight while the current one is multiplied, one barrier per stage.
+template <bool DUAL, bool XF32, int SK, int NT>
+__global__ __launch_bounds__(64 * kMmWaves) void matvec_mfma_lds(MatvecArgs a)
+{
+    constexpr int NM = DUAL ? 2 : 1;
+    constexpr int ROWS = 16 * NT;               // rows per block: NT tiles share each x fragment
+    constexpr int RB = SK * 2;                  // bytes of one row per stage
+    constexpr int PITCH = RB + 16;
+    constexpr int RPI = 1024 / RB;              // rows per 1 KiB load instruction
+    constexpr int LPR = 64 / RPI;               // lanes per row in one instruction
+    constexpr int UNITS = NM * ROWS / RPI;      // load instructions per stage
+    constexpr int UPW = UNITS / kMmWaves;       // ... per wave
+    constexpr int KPW = SK / 32 / kMmWaves;     // MFMA k-steps per wave per stage
+    static_assert(UNITS % kMmWaves == 0 && UPW >= 1 && KPW >= 1, "stage shape");
+    __shared__ __align__(16) uint8_t stage[2][NM][ROWS][PITCH];
+    const int lane = threadIdx.x & 63;
+    const int wave = wave_id();
+    const int r = lane & 15, g = lane >> 4;
+    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * ROWS;
+    int64_t tok = a.t0 + r;
+    tok = tok < a.T ? tok : a.T - 1;
+    const int ns = static_cast<int>(a.K / SK);
+
+    // this lane's 16 bytes of each of the wave's load instructions
+    const char* src[UPW];
+    int dst[UPW];
+#pragma unroll
+    for (int i = 0; i < UPW; i++) {
+        const int u = wave + kMmWaves * i;
+        const int m = u / (ROWS / RPI), rr = (u % (ROWS / RPI)) * RPI + lane / LPR;
+        const int byte = (lane % LPR) * 16;
+        int64_t row = n0 + rr;
+        row = row < a.N ? row : a.N - 1;
+        src[i] = (m == 0 ? a.wg : a.wu) + row * a.wrow + byte;
+        dst[i] = (m * ROWS + rr) * PITCH + byte;
+    }
+    // Weight rows two stages ahead, in two register sets (the LDS holds the current and the next stage):
+    // stage s + 2 is loaded while s is multiplied, and s + 1 is written to LDS at the end of stage s.
+    uint4 pa[UPW], pb[UPW];
+    auto fetch_w = [&](uint4* pw, int s) {
+#pragma unroll
+        for (int i = 0; i < UPW; i++) pw[i] = load_nt(src[i] + static_cast<int64_t>(s) * RB);
+    };
+    auto put_w = [&](const uint4* pw, int b) {
+#pragma unroll
+        for (int i = 0; i < UPW; i++) *reinterpret_cast<uint4*>(&stage[b][0][0][0] + dst[i]) = pw[i];
+    };
+    // x of this wave's k-steps: f32 two float4, bf16 one uint4 per k-step (one stage ahead)
+    float4 xf[KPW][2];
+    uint4 xb[KPW];
+    auto fetch_x = [&](int s) {
+#pragma unroll
+        for (int q = 0; q < KPW; q++) {
+            const int64_t k0 = static_cast<int64_t>(s) * SK + (wave * KPW + q) * 32 + 8 * g;
+            if (XF32) {
+                const float* xr = static_cast<const float*>(a.x) + tok * a.xs + k0;
+                xf[q][0] = *reinterpret_cast<const float4*>(xr);
+                xf[q][1] = *reinterpret_cast<const float4*>(xr + 4);
+            } else {
+                xb[q] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.x) + tok * a.xs + k0);
+            }
+        }
+    };
+    f32x4_t ag[NT], au[NT];
+#pragma unroll
+    for (int tt = 0; tt < NT; tt++) ag[tt] = au[tt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    // Stage s from LDS buffer s & 1. Issue order matters for the in-order load counter: x(s + 1) before
+    // w(s + 2), so that waiting for x at the next stage leaves w(s + 2) in flight.
+    auto run_stage = [&](int s, uint4* wnext, uint4* wfree) {
+        const int b = s & 1;
+        uint4 B[KPW][3];
+        uint4 Ag[KPW][NT], Au[KPW][NT];
+#pragma unroll
+        for (int q = 0; q < KPW; q++) {
+            if (XF32) {
+                const float v[8] = {xf[q][0].x, xf[q][0].y, xf[q][0].z, xf[q][0].w,
+                                    xf[q][1].x, xf[q][1].y, xf[q][1].z, xf[q][1].w};
+                split3(v, B[q][0], B[q][1], B[q][2]);
+            } else {
+                B[q][0] = xb[q];
+            }
+            const int kb = ((wave * KPW + q) * 32 + 8 * g) * 2;
+#pragma unroll
+            for (int tt = 0; tt < NT; tt++) {
+                Ag[q][tt] = *reinterpret_cast<const uint4*>(&stage[b][0][16 * tt + r][kb]);
+                if (DUAL) Au[q][tt] = *reinterpret_cast<const uint4*>(&stage[b][NM - 1][16 * tt + r][kb]);
+            }
+        }
+        if (s + 1 < ns) fetch_x(s + 1);        // block-uniform conditions
+        if (s + 2 < ns) fetch_w(wfree, s + 2);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int q = 0; q < KPW; q++) {
+#pragma unroll
+            for (int p = 0; p < (XF32 ? 3 : 1); p++) {
+#pragma unroll
+                for (int tt = 0; tt < NT; tt++) {
+                    ag[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(Ag[q][tt]), as_bf16x8(B[q][p]), ag[tt], 0, 0, 0);
+                    if (DUAL)
+                        au[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(Au[q][tt]), as_bf16x8(B[q][p]), au[tt], 0, 0, 0);
+                }
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (s + 1 < ns) put_w(wnext, b ^ 1);
+        __syncthreads();
+    };
+    fetch_x(0);
+    fetch_w(pa, 0);
+    if (ns > 1) fetch_w(pb, 1);
+    put_w(pa, 0);
+    __syncthreads();
+    // stage s: the next stage's rows are in pb (s even) or pa (s odd); the other set is free
+    int s = 0;
+    for (; s + 1 < ns; s += 2) {
+        run_stage(s, pb, pa);
+        run_stage(s + 1, pa, pb);
+    }
+    if (s < ns) run_stage(s, pb, pa);
+    // partial tiles meet in the (now idle) stage memory: [wave][tile][matrix][lane]
+    f32x4_t* red = reinterpret_cast<f32x4_t*>(&stage[0][0][0][0]);
+    static_assert(sizeof(stage) >= sizeof(f32x4_t) * kMmWaves * NM * NT * 64, "reduction space");
+#pragma unroll
+    for (int tt = 0; tt < NT; tt++) {
+        red[((wave * NT + tt) * NM) * 64 + lane] = ag[tt];
+        if (DUAL) red[((wave * NT + tt) * NM + 1) * 64 + lane] = au[tt];
+    }
+    __syncthreads();
+    // wave tt < NT finishes tile tt
+    if (wave >= NT) return;
+    const int tt = wave;
+    f32x4_t sg = red[(tt * NM) * 64 + lane], su = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    if (DUAL) su = red[(tt * NM + 1) * 64 + lane];
+#pragma unroll
+    for (int w = 1; w < kMmWaves; w++) {
+        sg += red[((w * NT + tt) * NM) * 64 + lane];
+        if (DUAL) su += red[((w * NT + tt) * NM + 1) * 64 + lane];
+    }
+    const int64_t t = a.t0 + r;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int64_t n = n0 + 16 * tt + 4 * g + i;
+        float out = sg[i];
+        if (DUAL) {
+            const float act = a.act == SLHIP_ACT_SILU        ? activate<SLHIP_ACT_SILU>(sg[i])
+                              : a.act == SLHIP_ACT_GELU_TANH ? activate<SLHIP_ACT_GELU_TANH>(sg[i])
+                                                             : activate<SLHIP_ACT_GELU_ERF>(sg[i]);
+            out = act * su[i];
+        }
+        if (t < a.T && n < a.N) {
+            if (a.yt == SLHIP_F32)
+                static_cast<float*>(a.y)[t * a.ys + n] = out;
+            else
+                static_cast<uint16_t*>(a.y)[t * a.ys + n] = static_cast<uint16_t>(f32_to_bf16_bits(out));
+        }
+    }
+}
+
 // ---- host dispatch --------------------------------------------------------------------------------
 
 static int env_int(const char* name, int dflt)
@@ -587,12 +750,42 @@ static int token_tile(int64_t T, int64_t K)
     return tt;
 }
 
+template <int SK, int NT>
+static void launch_mfma_lds(const MatvecArgs& a, bool dual, hipStream_t st)
+{
+    const dim3 grid(static_cast<unsigned>((a.N + 16 * NT - 1) / (16 * NT)));
+    if (a.xt == SLHIP_F32) {
+        if (dual) matvec_mfma_lds<true, true, SK, NT><<<grid, 64 * kMmWaves, 0, st>>>(a);
+        else matvec_mfma_lds<false, true, SK, NT><<<grid, 64 * kMmWaves, 0, st>>>(a);
+    } else {
+        if (dual) matvec_mfma_lds<true, false, SK, NT><<<grid, 64 * kMmWaves, 0, st>>>(a);
+        else matvec_mfma_lds<false, false, SK, NT><<<grid, 64 * kMmWaves, 0, st>>>(a);
+    }
+}
+
+// Weight stage of the LDS-staged MFMA kernel (SLHIP_MATVEC_MFMA_SK: 256 or 512 values; 0 = operands
+// loaded straight from global memory, also used when K is not a multiple of the stage) and 16-row tiles
+// per block (SLHIP_MATVEC_MFMA_NT: 1 or 2; one with the 512-value stage).
+static int mfma_stage() { return env_int("SLHIP_MATVEC_MFMA_SK", 256); }
+// Default: one tile up to 8 tokens (finer blocks spread the 16-row tiles more evenly over the CUs), two
+// above (each x fragment then feeds twice the weights; measured at 14336 x 4096: 51 vs 57 us at T = 16).
+static int mfma_tiles(int64_t T)
+{
+    const int nt = env_int("SLHIP_MATVEC_MFMA_NT", 0);
+    return nt == 1 || nt == 2 ? nt : (T > 8 ? 2 : 1);
+}
+
 static int run_mfma(MatvecArgs a, bool dual, hipStream_t st)
 {
     const dim3 grid(static_cast<unsigned>((a.N + 15) / 16));
+    const int sk = mfma_stage(), nt = mfma_tiles(a.T);
     for (int64_t t0 = 0; t0 < a.T; t0 += 16) {
         a.t0 = t0;
-        if (a.xt == SLHIP_F32) {
+        if (sk == 512 && a.K % 512 == 0) {
+            launch_mfma_lds<512, 1>(a, dual, st);  // two tiles would take 133 KB of LDS per block
+        } else if (sk == 256 && a.K % 256 == 0) {
+            nt == 2 ? launch_mfma_lds<256, 2>(a, dual, st) : launch_mfma_lds<256, 1>(a, dual, st);
+        } else if (a.xt == SLHIP_F32) {
             if (dual) matvec_mfma<true, true><<<grid, 64 * kMmWaves, 0, st>>>(a);
             else matvec_mfma<false, true><<<grid, 64 * kMmWaves, 0, st>>>(a);
         } else {
@@ -607,7 +800,7 @@ static int run_mfma(MatvecArgs a, bool dual, hipStream_t st)
 
 // Tokens from which bf16 weights take the matrix cores (SLHIP_MATVEC_MFMA_MIN_T; 0 disables): below it the
 // VALU kernel is already at the HBM rate.
-static int mfma_min_tokens() { return env_int("SLHIP_MATVEC_MFMA_MIN_T", 5); }
+static int mfma_min_tokens() { return env_int("SLHIP_MATVEC_MFMA_MIN_T", 3); }
 
 template <int WT>
 static int run_dense(MatvecArgs a, bool dual, hipStream_t st)

@@ -220,10 +220,12 @@ def test_empty_shapes_are_noops(device):
 @pytest.mark.parametrize("dual,dx,T,K,N", [
     (False, "f32", 1, 1024, 48), (False, "f32", 4, 2048, 40), (True, "f32", 5, 4096, 64),
     (True, "bf16", 17, 1024, 33), (False, "bf16", 33, 256, 17),
+    (True, "f32", 9, 320, 40),  # K not a multiple of the 256-value stage: operands loaded directly
 ])
 def test_bf16_paths_agree_with_oracle(device, monkeypatch, min_t, dual, dx, T, K, N):
-    """bf16 weights take the MFMA kernel from SLHIP_MATVEC_MFMA_MIN_T tokens on; both kernels meet the same
-    bound whichever T they are forced onto (ragged token and row tiles included)."""
+    """bf16 weights take the MFMA kernels from SLHIP_MATVEC_MFMA_MIN_T tokens on; every kernel meets the same
+    bound whichever T it is forced onto (ragged token and row tiles, one and two 16-row tiles per block, the
+    LDS-staged kernel and, for K off its stage size, the directly loaded one)."""
     monkeypatch.setenv("SLHIP_MATVEC_MFMA_MIN_T", min_t)
     seed = _seed("paths", min_t, dual, dx, T, K, N)
     rg, Wg = _weights("bf16", N, K, seed, 1)
