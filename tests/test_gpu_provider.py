@@ -240,7 +240,8 @@ def test_rope_normal_style_with_freq_factors(dev):
         assert_f32_close(seg.get_output(y), ref, what="gptj rope")
 
 
-@pytest.mark.parametrize("fmt", ["q8_0", "q4_0", "f16", "q4_k", "q5_k", "q6_k"])
+@pytest.mark.parametrize("fmt", ["q8_0", "q4_0", "f16", "q4_k", "q5_k", "q6_k", "iq4_xs", "tq2_0", "mxfp4", "nvfp4",
+                                 "iq2_xxs", "iq3_s", "iq1_m"])
 @pytest.mark.parametrize("out", ["f32", "bf16"])
 def test_gather_graph(dev, fmt, out):
     """GatherTests.cs:7-25,147-163: token embedding from a quantized table (the reference's Table cases include
