@@ -487,8 +487,8 @@ SLHIP_API int slhip_gguf_find_tensor(const slhip_gguf* file, const char* name, i
 SLHIP_API int slhip_gguf_type(int ggml_type, slhip_gguf_tensor* type);
 /* Host read of bytes [offset, offset + bytes) of a tensor as its element type (IWeightSource.Read:
  * GgufWeightSource.cs:9-19, GgufInterleavedQ4_0Source.cs:43-79, GgufI2sSource.cs:39-64): the interleaved
- * Q4_0 rows de-interleaved, I2_S codes with the tensor's scale in front of every block. SLHIP_ERR_INDEX
- * for a range outside the tensor; SLHIP_ERR_UNSUPPORTED for the narrow IQ1 types (widening not built). */
+ * Q4_0 rows de-interleaved, I2_S codes with the tensor's scale in front of every block, the narrow IQ1
+ * blocks widened to IQ1_S (GgmlNarrowIq1.cs:55-86). SLHIP_ERR_INDEX for a range outside the tensor. */
 SLHIP_API int slhip_gguf_read(const slhip_gguf* file, int64_t index, int64_t offset, void* dst, size_t bytes);
 /* The tensor's bytes in the mapping when they are its element type's bytes as stored (TryGetPointer),
  * else NULL. */

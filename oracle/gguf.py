@@ -10,8 +10,8 @@ Follows:
 - ``GgmlTypes.cs:52-119``: ggml type ids and what each is read as, with the block geometry of
   ``src/Sharplight.Core/Tensors/DataType.cs:76-244``.
 - ``GgufHeaderProbe.cs:17-135``: metadata and tensor table from a prefix of a file.
-- ``GgufInterleavedQ4_0Source.cs:43-79`` and ``GgufI2sSource.cs:11-64``: the types read in another
-  layout than they are stored in.
+- ``GgufInterleavedQ4_0Source.cs:43-79``, ``GgufI2sSource.cs:11-64`` and ``GgmlNarrowIq1.cs:55-86``: the
+  types read in another layout than they are stored in.
 
 Metadata values come back typed as the reference's CLR values are: numpy scalars of the exact width
 for numbers, ``bool``, ``str``; numpy arrays for numeric and bool arrays, ``list`` of ``str`` for string
@@ -291,8 +291,49 @@ def read_tensor(data, t):
         out[:, 4:] = np.frombuffer(raw[:blocks * 32], np.uint8).reshape(blocks, 32)
         return out.tobytes()
     if g in NARROW_IQ1:
-        raise GgufUnsupported("narrow IQ1 widening")
+        sb = NARROW_IQ1[g]
+        return b"".join(widen_narrow_iq1(g, raw[b * sb:(b + 1) * sb]) for b in range(t["byte_size"] // 50))
     return raw
+
+
+_NARROW_GRIDS = {}
+
+
+def _narrow_grid(g):
+    """The narrow type's codebook as IQ1_S grid positions, from the library's generated table header
+    (sharplight_amd/csrc/narrow_iq1_grids.h: data of the format, pinned by the fork's decoded fixture)."""
+    if not _NARROW_GRIDS:
+        import os
+        import re
+        text = open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "..", "sharplight_amd", "csrc",
+                                 "narrow_iq1_grids.h")).read()
+        for gid, name in ((64, "kNarrowIq1Xs"), (65, "kNarrowIq1Xxs"), (66, "kNarrowIq1Xxxs")):
+            body = text[text.index(name + "["):]
+            body = body[body.index("{") + 1:body.index("}")]
+            _NARROW_GRIDS[gid] = [int(v) for v in re.findall(r"\d+", body)]
+    return _NARROW_GRIDS[g]
+
+
+def widen_narrow_iq1(g, narrow: bytes) -> bytes:
+    """GgmlNarrowIq1.Widen (src/Sharplight.Import.Gguf/GgmlNarrowIq1.cs:55-86): one narrow block (46, 42 or 38
+    bytes) as the 50-byte IQ1_S block with the same values."""
+    grid = _narrow_grid(g)
+    wide = bytearray(50)
+    wide[0:2] = narrow[0:2]
+    qs, tail = narrow[2:34], narrow[34:]
+    for ib in range(8):
+        if g == 65:
+            ss = tail[ib] >> 4
+        else:
+            ss = (tail[8 + ib // 2 if g == 64 else ib // 2] >> (4 * (ib & 1))) & 0xF
+        qh = (ss & 7) << 12 | (ss >> 3) << 15
+        for l in range(4):
+            high = (tail[ib] >> (2 * l)) & 3 if g == 64 else ((tail[ib] >> l) & 1 if g == 65 else 0)
+            index = grid[qs[4 * ib + l] | high << 8]
+            wide[2 + 4 * ib + l] = index & 0xFF
+            qh |= (index >> 8) << (3 * l)
+        wide[34 + 2 * ib:36 + 2 * ib] = struct.pack("<H", qh)
+    return bytes(wide)
 
 
 def deinterleave_q4_0(raw, blocks_per_row, rows, chunk):

@@ -4,7 +4,8 @@
 // Reader: src/Sharplight.Import.Gguf/GgufFile.cs:72-245 (open, header, metadata, tensor table, sizes and
 // bounds), GgufReader.cs:1-175 (bounds-checked cursor, value types, array guards), GgmlTypes.cs:52-119
 // (type ids), GgufHeaderProbe.cs:17-135 (header prefixes), GgufInterleavedQ4_0Source.cs:43-79 and
-// GgufI2sSource.cs:39-64 (types read in another layout than stored).
+// GgufI2sSource.cs:39-64, GgufNarrowIq1Source.cs and GgmlNarrowIq1.cs:55-86 (types read in another layout
+// than stored).
 // Uploader: src/Sharplight.Vulkan/WeightUploader.cs:6-140 (two staging buffers, one filled by the host
 // while the other is copied).
 //
@@ -12,6 +13,7 @@
 // whose numeric arrays and strings point into the mapping (a prefix is copied first, so they point into
 // the copy).
 #include "common.hpp"
+#include "narrow_iq1_grids.h"
 
 #include <fcntl.h>
 #include <sys/mman.h>
@@ -129,7 +131,7 @@ TypeDesc type_desc(int id)
     case 42: return t("q2_0", 64, 18);
     case 43: return t("f8_e4m3", 1, 1);
     case 64: case 65: case 66: {  // unsloth's narrow IQ1 types: read as IQ1_S blocks
-        TypeDesc d = t("iq1_s", 256, kWideIq1Bytes);
+        TypeDesc d = t("iq1_s", 256, kWideIq1Bytes, SLHIP_FMT_IQ1_S);
         d.layout = Layout::NarrowIq1;
         d.stored_block = id == 64 ? 46 : id == 65 ? 42 : 38;
         return d;
@@ -480,6 +482,34 @@ void fill_tensor(const Tensor& t, slhip_gguf_tensor* o)
     o->stored_bytes = t.stored;
 }
 
+// One narrow IQ1 block (46, 42 or 38 bytes) as the IQ1_S block (50 bytes) with the same values
+// (GgmlNarrowIq1.Widen, GgmlNarrowIq1.cs:55-86): the f16 scale and the 32 low index bytes carry over with
+// each group's index replaced by its IQ1_S grid position; per 32 values the u16 qh holds the three high
+// position bits of each group, the 3-bit scale (bits 12-14) and the delta sign (bit 15).
+//   IQ1_XS  (64): f16 d, qs[32], qh[8] (group l's two high index bits at 2l), sc[4] (a nibble per 32 values)
+//   IQ1_XXS (65): f16 d, qs[32], qh[8] (bit l: group l's ninth index bit; bits 4-7: scale and sign)
+//   IQ1_XXXS(66): f16 d, qs[32] (whole 8-bit indices), sc[4]
+void widen_narrow_iq1(int ggml, const uint8_t* narrow, uint8_t* wide)
+{
+    const uint16_t* grid = ggml == 64 ? kNarrowIq1Xs : ggml == 65 ? kNarrowIq1Xxs : kNarrowIq1Xxxs;
+    wide[0] = narrow[0];
+    wide[1] = narrow[1];
+    const uint8_t* qs = narrow + 2;
+    const uint8_t* tail = narrow + 34;
+    for (int ib = 0; ib < 8; ib++) {
+        const int ss = ggml == 65 ? tail[ib] >> 4 : (tail[ggml == 64 ? 8 + ib / 2 : ib / 2] >> (4 * (ib & 1))) & 0xF;
+        int qh = (ss & 7) << 12 | (ss >> 3) << 15;
+        for (int l = 0; l < 4; l++) {
+            const int high = ggml == 64 ? (tail[ib] >> (2 * l)) & 3 : ggml == 65 ? (tail[ib] >> l) & 1 : 0;
+            const int index = grid[qs[4 * ib + l] | high << 8];
+            wide[2 + 4 * ib + l] = static_cast<uint8_t>(index);
+            qh |= (index >> 8) << (3 * l);
+        }
+        wide[34 + 2 * ib] = static_cast<uint8_t>(qh);
+        wide[35 + 2 * ib] = static_cast<uint8_t>(qh >> 8);
+    }
+}
+
 // IWeightSource.Read of [off, off + n) of tensor t into dst. The range was checked by the caller.
 void read_range(const slhip_gguf& g, const Tensor& t, int64_t off, uint8_t* dst, int64_t n)
 {
@@ -526,7 +556,18 @@ void read_range(const slhip_gguf& g, const Tensor& t, int64_t off, uint8_t* dst,
         }
         return;
     }
-    case Layout::NarrowIq1: return;  // rejected by the callers
+    case Layout::NarrowIq1: {  // GgufNarrowIq1Source: each stored block widened to IQ1_S
+        const int sb = t.desc.stored_block;
+        uint8_t block[kWideIq1Bytes];
+        const int64_t end = off + n;
+        for (int64_t b = off / kWideIq1Bytes; b * kWideIq1Bytes < end; b++) {
+            widen_narrow_iq1(t.ggml, data + b * sb, block);
+            const int64_t bs = b * kWideIq1Bytes;
+            const int64_t from = std::max<int64_t>(0, off - bs), to = std::min<int64_t>(kWideIq1Bytes, end - bs);
+            std::memcpy(dst + (bs + from - off), block + from, static_cast<size_t>(to - from));
+        }
+        return;
+    }
     }
 }
 
@@ -542,8 +583,6 @@ int check_tensor(const slhip_gguf* g, int64_t index, const Tensor** t)
 int check_readable(const slhip_gguf* g, const Tensor& t)
 {
     if (!g->has_data) return fail(SLHIP_ERR_INVALID, "tensor '%s': a header prefix holds no tensor data", t.name.c_str());
-    if (t.desc.layout == Layout::NarrowIq1)
-        return fail(SLHIP_ERR_UNSUPPORTED, "tensor '%s': ggml type %d (narrow IQ1) is not read by this library", t.name.c_str(), t.ggml);
     return SLHIP_OK;
 }
 

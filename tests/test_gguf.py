@@ -435,13 +435,51 @@ def test_i2s_reads_as_scaled_blocks(tmp_path):
     assert np.array_equal(got * scale[:, None], want * np.float32(1.7))
 
 
-def test_narrow_iq1_is_described_but_not_read(tmp_path):
+def _narrow_records():
+    import oracle  # noqa: F401  (the C oracle decodes the widened IQ1_S blocks)
+    fx = np.load(os.path.join(os.path.dirname(__file__), "golden", "ggml_narrow_iq1.npz"))
+    n = len([k for k in fx.files if k.endswith("_type")])
+    return [(int(fx[f"r{i}_type"][0]), int(fx[f"r{i}_type"][1]), int(fx[f"r{i}_type"][2]), fx[f"r{i}_blocks"].tobytes(),
+             fx[f"r{i}_deq"]) for i in range(n)]
+
+
+def test_narrow_iq1_widening_decodes_like_the_fork():
+    """NarrowIq1Tests.WidenedBlocks_DecodeLikeTheFork: blocks of the three narrow types (gaussian data and random
+    bytes), widened to IQ1_S, decode to the fork's own floats -- here bit for bit (the reference allows 1e-6)."""
+    import oracle
+    recs = _narrow_records()
+    assert sorted({r[0] for r in recs}) == [64, 65, 66]
+    for g, rows, cols, blocks, want in recs:
+        sb = og.NARROW_IQ1[g]
+        wide = b"".join(og.widen_narrow_iq1(g, blocks[k * sb:(k + 1) * sb]) for k in range(rows * cols // 256))
+        got = oracle.dequant("iq1_s", np.frombuffer(wide, np.uint8), rows * cols).reshape(rows, cols)
+        nan = np.isnan(want)
+        assert np.array_equal(np.isnan(got), nan)
+        assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32)), g
+
+
+def test_narrow_iq1_reads_widened_at_any_offset(tmp_path):
+    """NarrowIq1Tests.Source_ReadsWidenedBlocksAtAnyOffset, for every narrow type and fixture record: the
+    native reader returns the oracle's widened blocks, whole and from a range inside blocks."""
+    for i, (g, rows, cols, blocks, _) in enumerate(_narrow_records()):
+        hdr = struct.pack("<IIQQ", 0x46554747, 3, 1, 0) + struct.pack("<Q", 1) + b"w"
+        hdr += struct.pack("<IQQIQ", 2, cols, rows, g, 0)
+        blob = hdr + bytes((len(hdr) + 31) // 32 * 32 - len(hdr)) + blocks
+        p = tmp_path / f"n{i}.gguf"
+        p.write_bytes(blob)
+        want = og.read_tensor(blob, og.parse_file(blob)["tensors"][0])
+        with gguf.GgufFile.open(p) as f:
+            t = f.tensors[0]
+            assert (t.data_type, t.format, t.byte_size, t.stored_bytes) == ("iq1_s", "iq1_s", len(want), len(blocks))
+            assert t.read() == want and t.read(37, 61) == want[37:98]
+            assert t.pointer() == 0
+
+
+def test_narrow_iq1_header_prefix_has_no_data():
     data = _fx("Kimi-K3-UD-TQ1_0")
-    table = gguf.read_tensor_table(data)
-    assert any(t[1] == 65 for t in table)
     with gguf.GgufFile.from_prefix(data) as f:
         t = next(t for t in f.tensors if t.ggml_type == 65)
-        assert (t.data_type, t.block_bytes) == ("iq1_s", 50)
+        assert (t.data_type, t.block_bytes, t.format) == ("iq1_s", 50, "iq1_s")
         assert t.stored_bytes == t.byte_size // 50 * 42
         with pytest.raises(native.SlhipArgumentError, match="header prefix"):
             t.read(0, 1)

@@ -140,3 +140,32 @@ def test_embedding_table_from_file_gathers_like_oracle(device, tmp_path, staging
         got = Dev.get(y, (ids.size, D), np.float32)
     want = oracle.gather(fmt, table, V, D, ids)
     assert got.tobytes() == want.tobytes()
+
+
+def test_narrow_iq1_upload_gathers_like_the_fork(device, tmp_path, staging):
+    """Narrow IQ1 tensors (GGUF ids 64-66) uploaded -- widened to IQ1_S on the way -- and gathered: the fork's
+    own decoded floats (ggml_narrow_iq1.bin), bit for bit."""
+    import os
+    staging(1, 3)
+    fx = np.load(os.path.join(os.path.dirname(__file__), "golden", "ggml_narrow_iq1.npz"))
+    for i in range(len([k for k in fx.files if k.endswith("_type")])):
+        g, rows, cols = (int(v) for v in fx[f"r{i}_type"])
+        blocks, want = fx[f"r{i}_blocks"].tobytes(), fx[f"r{i}_deq"]
+        hdr = struct.pack("<IIQQ", 0x46554747, 3, 1, 0) + struct.pack("<Q", 1) + b"w"
+        hdr += struct.pack("<IQQIQ", 2, cols, rows, g, 0)
+        p = tmp_path / f"n{i}.gguf"
+        p.write_bytes(hdr + bytes((len(hdr) + 31) // 32 * 32 - len(hdr)) + blocks)
+        with gguf.GgufFile.open(p) as f, Dev() as d:
+            t = f.tensors[0]
+            log(f"narrow IQ1 upload + gather type {g} [{rows}, {cols}]")
+            tab = d.empty(t.byte_size)
+            t.upload(tab)
+            ids = np.arange(rows, dtype=np.int32)
+            pid = d.put(ids)
+            y = d.empty(rows * cols * 4)
+            native.gather("iq1_s", tab, rows, cols, pid, rows, "f32", y)
+            native.synchronize()
+            got = Dev.get(y, (rows, cols), np.float32)
+        nan = np.isnan(want)
+        assert np.array_equal(np.isnan(got), nan)
+        assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32)), (i, g)
