@@ -1377,7 +1377,7 @@ static void matvec_groups(int fmt, const uint8_t* w, int64_t N, int64_t K, const
             for (int r = 0; r < 4; r++) {
                 float* dst = wbuf + r * 1024;
                 const int64_t off = fmt == ORC_F32 ? kb * 4 : fmt == ORC_F16 || fmt == ORC_BF16 ? kb * 2
-                                                                     : kb / 32 * orc_row_bytes(fmt, 32);
+                                                                     : kb / block_size(fmt) * block_bytes(fmt);
                 orc_dequant(fmt, rows[r] + off, len, dst);
                 wp[r] = dst;
             }

@@ -262,13 +262,69 @@ __global__ __launch_bounds__(kMvThreads) void matvec_dense(MatvecArgs a, int wpr
     store_row<TT, DUAL>(a, n, ag, au);
 }
 
-// Quantized weights (Q8_0, Q4_0, Q4_1, Q5_0, Q5_1): persistent blocks of 4 waves; each wave walks row
+// Quantized weights (Q8_0, Q4_0, Q4_1, Q5_0, Q5_1; Q4_K, Q5_K, Q6_K by 32-value sub-blocks): persistent
+// blocks of 4 waves; each wave walks row
 // (pairs) n, n + 4 * gridDim.x, ... . A row's block images go to the wave's own LDS region with 16-byte loads
 // (the blocks are only 2-byte aligned); the loads of the next row (pair) are issued before the current one
 // is computed, so their latency hides behind that work. The block stages x (32-value blocks padded to 36
 // floats) and the sum of every x block once. Each lane takes whole blocks: with the block's scale d and
 // additive term (OFF * d or m), sum_k x_k (q_k d + add) = d * sum x q + add * sum x, the form of the
 // reference's fused Q4_0 dot (Quant.cs:770-803).
+// A K-quant row image in LDS, 32-value sub-block b (of super-block b / 8): its scale terms and 32 codes, one
+// per byte of w (Quant.cs:518-624). Q4_K / Q5_K: value = fma(q, d0, -m), d0 = d * sc, m = dmin * mn; Q6_K:
+// value = (q - 32) * s per 16 values, s = d * scale (d0 for values 0-15, d1 for 16-31); codes 0..63 here.
+struct KSub {
+    float d0, d1, m;
+    uint32_t w[8];
+};
+
+template <int FMT>
+__device__ __forceinline__ KSub ksub(const uint32_t* s, int b)
+{
+    KSub r;
+    const int sb = b >> 3, j = b & 7;
+    const LdsBytes B{s};
+    if constexpr (FMT == SLHIP_FMT_Q4_K || FMT == SLHIP_FMT_Q5_K) {
+        constexpr bool K5 = FMT == SLHIP_FMT_Q5_K;
+        const int o = sb * (K5 ? 176 : 144);  // super-blocks of 144 / 176 bytes: 16-byte aligned
+        uint32_t sc, mn;
+        if (j < 4) {
+            sc = B.u8(o + 4 + j) & 63u;
+            mn = B.u8(o + 8 + j) & 63u;
+        } else {
+            sc = (B.u8(o + 8 + j) & 0xFu) | ((B.u8(o + j) >> 6) << 4);
+            mn = (B.u8(o + 8 + j) >> 4) | ((B.u8(o + 4 + j) >> 6) << 4);
+        }
+        r.d0 = __fmul_rn(half_at(s, o), static_cast<float>(sc));
+        r.d1 = r.d0;
+        r.m = __fmul_rn(half_at(s, o + 2), static_cast<float>(mn));
+        const uint32_t* q = s + (o + (K5 ? 48 : 16) + 32 * (j >> 1)) / 4;
+        const uint32_t* qh = s + (o + 16) / 4;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            uint32_t w = (q[k] >> (4 * (j & 1))) & 0x0F0F0F0Fu;
+            if (K5) w |= ((qh[k] >> j) & 0x01010101u) << 4;
+            asm("" : "+v"(w));  // hides the zero high bits: each byte then converts with one v_cvt_f32_ubyte
+            r.w[k] = w;
+        }
+    } else {  // Q6_K: {ql[128], qh[64], int8 scales[16], f16 d}, 210 bytes (2-byte aligned)
+        const int o = sb * 210, n = j >> 2, qt = j & 3;
+        const float d = half_at(s, o + 208);
+        r.d0 = __fmul_rn(d, static_cast<float>(static_cast<int8_t>(B.u8(o + 192 + 8 * n + 2 * qt))));
+        r.d1 = __fmul_rn(d, static_cast<float>(static_cast<int8_t>(B.u8(o + 193 + 8 * n + 2 * qt))));
+        r.m = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const uint32_t l = lds_u32(s, o + 64 * n + 32 * (qt & 1) + 4 * k);
+            const uint32_t h = lds_u32(s, o + 128 + 32 * n + 4 * k);
+            uint32_t w = ((qt >= 2 ? l >> 4 : l) & 0x0F0F0F0Fu) | (((h >> (2 * qt)) & 0x03030303u) << 4);
+            asm("" : "+v"(w));
+            r.w[k] = w;
+        }
+    }
+    return r;
+}
+
 constexpr int kMqThreads = 256;
 
 template <int FMT, int TT, int CH, bool DUAL>
@@ -334,6 +390,39 @@ __global__ __launch_bounds__(kMqThreads) void matvec_quant(MatvecArgs a)
         // One row's block for every token (Q8_0's 32 code bytes take 8 registers per row, so the rows of a
         // pair go one after the other rather than side by side).
         auto row_block = [&](const uint32_t* img, int b, bool own, float* acc) {
+            if constexpr (Fmt<FMT>::K) {
+                // K-quants: sum x q over the sub-block (Q6_K: x (q - 32) per 16-value half), then
+                // d0 * sum - m * sum x (Q4_K, Q5_K) or d0 * half0 + d1 * half1 (Q6_K)
+                const KSub ks = ksub<FMT>(img, b);
+                float s0[TT], s1[TT];
+#pragma unroll
+                for (int t = 0; t < TT; t++) s0[t] = s1[t] = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    float q[8];
+#pragma unroll
+                    for (int e = 0; e < 8; e++) {
+                        q[e] = static_cast<float>((ks.w[2 * j + (e >> 2)] >> (8 * (e & 3))) & 0xFFu);
+                        if (FMT == SLHIP_FMT_Q6_K) q[e] -= 32.0f;
+                    }
+#pragma unroll
+                    for (int t = 0; t < TT; t++) {
+                        const float4* xp = reinterpret_cast<const float4*>(xsh + (t * nb + b) * 36 + 8 * j);
+                        const float4 x0 = xp[0], x1 = xp[1];
+                        const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+                        float& acc_h = (FMT == SLHIP_FMT_Q6_K && j >= 2) ? s1[t] : s0[t];
+#pragma unroll
+                        for (int e = 0; e < 8; e++) acc_h = fmaf(q[e], xv[e], acc_h);
+                    }
+                }
+#pragma unroll
+                for (int t = 0; t < TT; t++) {
+                    const float p = FMT == SLHIP_FMT_Q6_K ? fmaf(ks.d1, s1[t], ks.d0 * s0[t])
+                                                          : fmaf(-ks.m, xsum[t * nb + b], ks.d0 * s0[t]);
+                    acc[t] += own ? p : 0.0f;
+                }
+                return;
+            }
             const BlockWords<FMT> bw = block_words<FMT>(img, b);
             float sx[TT];
 #pragma unroll
@@ -827,15 +916,22 @@ static int run_dense(MatvecArgs a, bool dual, hipStream_t st)
     return SLHIP_OK;
 }
 
-static int quant_block_bytes(int fmt)
+// Values and bytes per block of the quantized weight formats; {0, 0} for the others.
+struct QGeom {
+    int bs, bb;
+};
+static QGeom quant_geom(int fmt)
 {
     switch (fmt) {
-    case SLHIP_FMT_Q8_0: return 34;
-    case SLHIP_FMT_Q4_0: return 18;
-    case SLHIP_FMT_Q4_1: return 20;
-    case SLHIP_FMT_Q5_0: return 22;
-    case SLHIP_FMT_Q5_1: return 24;
-    default: return 0;
+    case SLHIP_FMT_Q8_0: return {32, 34};
+    case SLHIP_FMT_Q4_0: return {32, 18};
+    case SLHIP_FMT_Q4_1: return {32, 20};
+    case SLHIP_FMT_Q5_0: return {32, 22};
+    case SLHIP_FMT_Q5_1: return {32, 24};
+    case SLHIP_FMT_Q4_K: return {256, 144};
+    case SLHIP_FMT_Q5_K: return {256, 176};
+    case SLHIP_FMT_Q6_K: return {256, 210};
+    default: return {0, 0};
     }
 }
 
@@ -910,7 +1006,7 @@ static int quant_tt(const MatvecArgs& a, int tt, int ch, hipStream_t st)
 template <int FMT>
 static int run_quant(MatvecArgs a, bool dual, hipStream_t st)
 {
-    int tt = 8;
+    int tt = Fmt<FMT>::K && dual ? 4 : 8;  // the K-quant sub-block decode at 8 tokens of a pair spills
     while (tt > 1 && (tt / 2 >= a.T || quant_lds(tt, a.K, a.wrow, dual) > kMaxLds)) tt /= 2;
     if (quant_lds(tt, a.K, a.wrow, dual) > kMaxLds)
         return fail(SLHIP_ERR_UNSUPPORTED, "matvec: K = %lld does not fit in LDS for this format", static_cast<long long>(a.K));
@@ -939,8 +1035,8 @@ static int matvec_common(int fmt, int dtype_x, int dtype_y, const void* x, int64
         return fail(SLHIP_ERR_UNSUPPORTED, "%s: activations and outputs are f32 or bf16", name);
     if (x_stride < K || y_stride < N) return fail(SLHIP_ERR_INVALID, "%s: a row stride is smaller than the row", name);
     const bool dense = fmt == SLHIP_FMT_F32 || fmt == SLHIP_FMT_F16 || fmt == SLHIP_FMT_BF16;
-    const int bb = quant_block_bytes(fmt);
-    if (!dense && bb == 0) return fail(SLHIP_ERR_UNSUPPORTED, "%s: weight format %d not supported", name, fmt);
+    const QGeom qg = quant_geom(fmt);
+    if (!dense && qg.bs == 0) return fail(SLHIP_ERR_UNSUPPORTED, "%s: weight format %d not supported", name, fmt);
     if (dense ? K % 8 != 0 : K % 256 != 0)
         return fail(SLHIP_ERR_UNSUPPORTED, "%s: K = %lld must be a multiple of %d for this weight format", name,
                     static_cast<long long>(K), dense ? 8 : 256);
@@ -951,7 +1047,10 @@ static int matvec_common(int fmt, int dtype_x, int dtype_y, const void* x, int64
         return fail(SLHIP_ERR_UNSUPPORTED, "%s: K = %lld above the staged-activation limit 16384", name,
                     static_cast<long long>(K));
     if (N > 0x7FFFFFFF || T > 0x7FFFFFFF) return fail(SLHIP_ERR_UNSUPPORTED, "%s: shape too large", name);
-    const int64_t wrow = dense ? K * (fmt == SLHIP_FMT_F32 ? 4 : 2) : K / 32 * bb;
+    const int64_t wrow = dense ? K * (fmt == SLHIP_FMT_F32 ? 4 : 2) : K / qg.bs * qg.bb;
+    if (wrow % 16 != 0)  // the block kernel stages rows with 16-byte loads (Q6_K: K a multiple of 2048)
+        return fail(SLHIP_ERR_UNSUPPORTED, "%s: rows of %lld bytes are not a multiple of 16 for this weight format",
+                    name, static_cast<long long>(wrow));
     MatvecArgs a{x, x_stride, static_cast<const char*>(wg), static_cast<const char*>(wu), wrow, y, y_stride,
                  T, K, N, 0, dtype_x, dtype_y, act};
     hipStream_t st = to_stream(stream);
@@ -963,7 +1062,10 @@ static int matvec_common(int fmt, int dtype_x, int dtype_y, const void* x, int64
     case SLHIP_FMT_Q4_0: return run_quant<SLHIP_FMT_Q4_0>(a, dual, st);
     case SLHIP_FMT_Q4_1: return run_quant<SLHIP_FMT_Q4_1>(a, dual, st);
     case SLHIP_FMT_Q5_0: return run_quant<SLHIP_FMT_Q5_0>(a, dual, st);
-    default: return run_quant<SLHIP_FMT_Q5_1>(a, dual, st);
+    case SLHIP_FMT_Q5_1: return run_quant<SLHIP_FMT_Q5_1>(a, dual, st);
+    case SLHIP_FMT_Q4_K: return run_quant<SLHIP_FMT_Q4_K>(a, dual, st);
+    case SLHIP_FMT_Q5_K: return run_quant<SLHIP_FMT_Q5_K>(a, dual, st);
+    default: return run_quant<SLHIP_FMT_Q6_K>(a, dual, st);
     }
 }
 

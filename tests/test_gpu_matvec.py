@@ -39,7 +39,8 @@ def _weights(fmt, N, K, seed, tid):
 def _act64(act, g):
     g = np.asarray(g, np.float64)
     if act == "silu":
-        return g / (1.0 + np.exp(-g))
+        with np.errstate(over="ignore"):  # exp(-g) = inf for very negative g: g / inf = -0, as wanted
+            return g / (1.0 + np.exp(-g))
     if act == "gelu_tanh":
         return 0.5 * g * (1.0 + np.tanh(0.7978845608028654 * (g + 0.044715 * g ** 3)))
     return 0.5 * g * (1.0 + np.vectorize(math.erf)(g / math.sqrt(2.0)))
@@ -73,6 +74,10 @@ def _abs_terms(fmt, raw, W):
     """|q d| + |a| per weight (= |w| for dense and Q8_0 weights): the magnitudes the kernel's sums add."""
     if fmt in ("f32", "f16", "bf16", "q8_0"):
         return np.abs(W).astype(np.float64)
+    if fmt in ("q4_k", "q5_k", "q6_k"):  # |q * scale| + |offset| per value, from the block fields
+        from tests.test_oracle import _k_terms
+        N, K = W.shape
+        return _k_terms(fmt, raw.reshape(-1), N, K).reshape(N, K)
     N, K = W.shape
     bb = {"q4_0": 18, "q4_1": 20, "q5_0": 22, "q5_1": 24}[fmt]
     blocks = raw.reshape(N, K // 32, bb)
@@ -115,6 +120,11 @@ SINGLE_CASES = [  # (fmt, x dtype, y dtype, T, K, N)
     ("q5_0", "f32", "bf16", 9, 256, 40),
     ("q5_1", "f32", "f32", 16, 4096, 33),
     ("q8_0", "f32", "f32", 2, 14336, 20),   # a down projection's K: LDS beyond 64 KiB
+    ("q4_k", "f32", "f32", 1, 4096, 96),
+    ("q5_k", "bf16", "f32", 3, 2048, 37),
+    ("q6_k", "f32", "bf16", 9, 4096, 40),
+    ("q4_k", "f32", "f32", 2, 14336, 20),
+    ("q6_k", "f32", "f32", 1, 14336, 24),
 ]
 
 
@@ -129,7 +139,7 @@ def test_matvec(device, fmt, dx, dy, T, K, N):
     _check_single(y, dy, ref, S, f"matvec {fmt}")
 
 
-@pytest.mark.parametrize("fmt", ["f32", "f16", "bf16", "q8_0", "q4_0", "q4_1", "q5_0", "q5_1"])
+@pytest.mark.parametrize("fmt", ["f32", "f16", "bf16", "q8_0", "q4_0", "q4_1", "q5_0", "q5_1", "q6_k"])
 def test_one_hot_rows_pick_columns_exactly(device, fmt):
     """x = e_k: every 8-value group but one sums to zero and the one holds q_k * 1 exactly, so y = d q_k + a
     exactly -- the dequantized weight -- whatever the summation order."""
@@ -159,6 +169,11 @@ DUAL_CASES = [  # (act, fmt, x dtype, y dtype, T, K, N): FusionTests.SwiGluDualM
     ("gelu_tanh", "q4_1", "f32", "bf16", 3, 1024, 96),
     ("silu", "q5_0", "bf16", "f32", 20, 256, 40),
     ("gelu_erf", "q5_1", "f32", "f32", 4, 2048, 64),
+    ("silu", "q4_k", "f32", "f32", 1, 4096, 14336),   # a Q4_K_M decode FFN (Mistral-7B / Llama-3-8B shapes)
+    ("silu", "q6_k", "f32", "f32", 1, 4096, 14336),
+    ("silu", "q5_k", "f32", "bf16", 5, 4096, 96),
+    ("gelu_tanh", "q4_k", "bf16", "f32", 9, 2048, 40),
+    ("silu", "q6_k", "f32", "f32", 12, 2048, 33),
 ]
 
 

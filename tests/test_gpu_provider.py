@@ -76,7 +76,7 @@ def test_residual_add_rmsnorm_fuses(dev, h_is_output):
 
 
 @pytest.mark.parametrize("fmt,T,swap", [("bf16", 1, False), ("f16", 3, True), ("f32", 9, False), ("q8_0", 1, False),
-                                        ("q4_0", 3, True)])
+                                        ("q4_0", 3, True), ("q4_k", 1, False), ("q5_k", 3, True)])
 def test_swiglu_dual_matvec_fuses(dev, fmt, T, swap):
     """FusionTests.SwiGluDualMatvec (FusionTests.cs:59-80): Mul(Silu(x Wg^T), x Wu^T) is one dual matvec launch
     (in either operand order), within the f32 dot-product bound of the unfused CPU computation."""
@@ -105,6 +105,9 @@ def test_swiglu_dual_matvec_fuses(dev, fmt, T, swap):
     # block formats with an additive term add |a| per weight to the magnitudes summed (Q4_0: 8 |d|)
     def mags(raw):
         W = oracle.dequant(fmt, raw.reshape(-1), N * K).reshape(N, K).astype(np.float64)
+        if fmt in ("q4_k", "q5_k"):  # |q * scale| + |min| per value
+            from tests.test_oracle import _k_terms
+            return _k_terms(fmt, raw.reshape(-1), N, K).reshape(N, K)
         if fmt != "q4_0":
             return np.abs(W)
         d = raw.reshape(N, K // 32, 18)[:, :, 0:2].copy().view(np.float16)[..., 0].astype(np.float64)
