@@ -326,6 +326,7 @@ __device__ __forceinline__ KSub ksub(const uint32_t* s, int b)
 }
 
 constexpr int kMqThreads = 256;
+constexpr bool PAIR = true;  // both rows of a dual pair per x read (every block format but Q8_0)
 
 template <int FMT, int TT, int CH, bool DUAL>
 __global__ __launch_bounds__(kMqThreads) void matvec_quant(MatvecArgs a)
@@ -447,9 +448,77 @@ __global__ __launch_bounds__(kMqThreads) void matvec_quant(MatvecArgs a)
                 acc[t] += own ? p : 0.0f;
             }
         };
+        // Both rows of a pair at once (not Q8_0, whose codes take 8 registers per row): each x vector is read
+        // from LDS once for the gate and the up row.
+        auto pair_block = [&](int b, bool own) {
+            float g0[TT], g1[TT], u0[TT], u1[TT];
+#pragma unroll
+            for (int t = 0; t < TT; t++) g0[t] = g1[t] = u0[t] = u1[t] = 0.0f;
+            auto dot8 = [&](const float* qg, const float* qu, int j, bool second) {
+#pragma unroll
+                for (int t = 0; t < TT; t++) {
+                    const float4* xp = reinterpret_cast<const float4*>(xsh + (t * nb + b) * 36 + 8 * j);
+                    const float4 x0 = xp[0], x1 = xp[1];
+                    const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+                    float& ag_h = second ? g1[t] : g0[t];
+                    float& au_h = second ? u1[t] : u0[t];
+#pragma unroll
+                    for (int e = 0; e < 8; e++) {
+                        ag_h = fmaf(qg[e], xv[e], ag_h);
+                        au_h = fmaf(qu[e], xv[e], au_h);
+                    }
+                }
+            };
+            if constexpr (Fmt<FMT>::K) {
+                const KSub kg = ksub<FMT>(rows, b), ku = ksub<FMT>(rows + rbw, b);
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    float qg[8], qu[8];
+#pragma unroll
+                    for (int e = 0; e < 8; e++) {
+                        qg[e] = static_cast<float>((kg.w[2 * j + (e >> 2)] >> (8 * (e & 3))) & 0xFFu);
+                        qu[e] = static_cast<float>((ku.w[2 * j + (e >> 2)] >> (8 * (e & 3))) & 0xFFu);
+                        if (FMT == SLHIP_FMT_Q6_K) {
+                            qg[e] -= 32.0f;
+                            qu[e] -= 32.0f;
+                        }
+                    }
+                    dot8(qg, qu, j, FMT == SLHIP_FMT_Q6_K && j >= 2);
+                }
+#pragma unroll
+                for (int t = 0; t < TT; t++) {
+                    const float pg = FMT == SLHIP_FMT_Q6_K ? fmaf(kg.d1, g1[t], kg.d0 * g0[t])
+                                                           : fmaf(-kg.m, xsum[t * nb + b], kg.d0 * g0[t]);
+                    const float pu = FMT == SLHIP_FMT_Q6_K ? fmaf(ku.d1, u1[t], ku.d0 * u0[t])
+                                                           : fmaf(-ku.m, xsum[t * nb + b], ku.d0 * u0[t]);
+                    ag[t] += own ? pg : 0.0f;
+                    au[t] += own ? pu : 0.0f;
+                }
+            } else {
+                const BlockWords<FMT> bg = block_words<FMT>(rows, b), bu = block_words<FMT>(rows + rbw, b);
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    float qg[8], qu[8];
+                    block_codes8<FMT>(bg, j, qg);
+                    block_codes8<FMT>(bu, j, qu);
+                    dot8(qg, qu, j, false);
+                }
+#pragma unroll
+                for (int t = 0; t < TT; t++) {
+                    const float pg = fmaf(bg.add, xsum[t * nb + b], bg.d * g0[t]);
+                    const float pu = fmaf(bu.add, xsum[t * nb + b], bu.d * u0[t]);
+                    ag[t] += own ? pg : 0.0f;
+                    au[t] += own ? pu : 0.0f;
+                }
+            }
+        };
         auto block = [&](int b, bool own) {
-            row_block(rows, b, own, ag);
-            if (DUAL) row_block(rows + rbw, b, own, au);
+            if constexpr (DUAL && FMT != SLHIP_FMT_Q8_0 && PAIR) {
+                pair_block(b, own);
+            } else {
+                row_block(rows, b, own, ag);
+                if (DUAL) row_block(rows + rbw, b, own, au);
+            }
         };
         const int full = nb / 64;  // iterations in which every lane has a block
         for (int i = 0; i < full; i++) block(lane + 64 * i, true);
