@@ -174,6 +174,12 @@ DUAL_CASES = [  # (act, fmt, x dtype, y dtype, T, K, N): FusionTests.SwiGluDualM
     ("silu", "q5_k", "f32", "bf16", 5, 4096, 96),
     ("gelu_tanh", "q4_k", "bf16", "f32", 9, 2048, 40),
     ("silu", "q6_k", "f32", "f32", 12, 2048, 33),
+    # one token, a gate/up pair per x read, each block format
+    ("silu", "q4_1", "f32", "f32", 1, 2048, 64),
+    ("gelu_erf", "q5_0", "bf16", "f32", 1, 1024, 96),
+    ("silu", "q5_1", "f32", "bf16", 1, 4096, 40),
+    ("silu", "q5_k", "f32", "f32", 1, 2048, 33),
+    ("gelu_tanh", "q4_k", "bf16", "bf16", 1, 14336, 24),
 ]
 
 
