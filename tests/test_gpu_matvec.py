@@ -121,6 +121,8 @@ SINGLE_CASES = [  # (fmt, x dtype, y dtype, T, K, N)
     ("q5_1", "f32", "f32", 16, 4096, 33),
     ("q8_0", "f32", "f32", 2, 14336, 20),   # a down projection's K: LDS beyond 64 KiB
     ("q4_k", "f32", "f32", 1, 4096, 96),
+    ("q4_0", "f32", "f32", 1, 4096, 90),    # one token
+    ("q4_0", "bf16", "bf16", 1, 14336, 33),
     ("q5_k", "bf16", "f32", 3, 2048, 37),
     ("q6_k", "f32", "bf16", 9, 4096, 40),
     ("q4_k", "f32", "f32", 2, 14336, 20),
