@@ -89,8 +89,9 @@ __device__ __forceinline__ void stage_x(const MatvecArgs& a, float* xsh, float* 
 }
 
 // Stages activation rows t0 .. t0+TT-1 for the block-format kernel: each 32-value block of x at a stride of
-// 36 floats ([TT][K/32][36] f32; the pad makes lanes that read consecutive blocks hit distinct LDS banks), and
-// the sum of each block, [TT][K/32]. Two blocks per thread per pass.
+// 36 floats ([TT][K/32][36] f32; the pad makes lanes that read consecutive blocks hit distinct LDS banks; its
+// first two floats hold the sums of the block's 16-value halves), and the sum of each block, [TT][K/32]. Two
+// blocks per thread per pass.
 template <int TT>
 __device__ __forceinline__ void stage_x_blocks(const MatvecArgs& a, float* xsh, float* xsum, int threads)
 {
@@ -126,13 +127,17 @@ __device__ __forceinline__ void stage_x_blocks(const MatvecArgs& a, float* xsh, 
             int u = base + q * threads + static_cast<int>(threadIdx.x);
             u = u < units ? u : units - 1;
             float4* d = reinterpret_cast<float4*>(xsh + u * 36);
-            float sum = 0.0f;
+            float sum = 0.0f, half[2] = {0.0f, 0.0f};
 #pragma unroll
             for (int k = 0; k < 8; k++) {
                 d[k] = make_float4(v[q][4 * k], v[q][4 * k + 1], v[q][4 * k + 2], v[q][4 * k + 3]);
-                sum += (v[q][4 * k] + v[q][4 * k + 1]) + (v[q][4 * k + 2] + v[q][4 * k + 3]);
+                const float p = (v[q][4 * k] + v[q][4 * k + 1]) + (v[q][4 * k + 2] + v[q][4 * k + 3]);
+                sum += p;
+                half[k >> 2] += p;
             }
             xsum[u] = sum;
+            xsh[u * 36 + 32] = half[0];  // the pad holds the sums of the two 16-value halves (Q6_K)
+            xsh[u * 36 + 33] = half[1];
         }
     }
 }
@@ -272,7 +277,8 @@ __global__ __launch_bounds__(kMvThreads) void matvec_dense(MatvecArgs a, int wpr
 // reference's fused Q4_0 dot (Quant.cs:770-803).
 // A K-quant row image in LDS, 32-value sub-block b (of super-block b / 8): its scale terms and 32 codes, one
 // per byte of w (Quant.cs:518-624). Q4_K / Q5_K: value = fma(q, d0, -m), d0 = d * sc, m = dmin * mn; Q6_K:
-// value = (q - 32) * s per 16 values, s = d * scale (d0 for values 0-15, d1 for 16-31); codes 0..63 here.
+// value = (q - 32) * s per 16 values, s = d * scale (d0 for values 0-15, d1 for 16-31); codes 0..63 here,
+// the -32 applied to the halves' sums of x.
 struct KSub {
     float d0, d1, m;
     uint32_t w[8];
@@ -323,6 +329,13 @@ __device__ __forceinline__ KSub ksub(const uint32_t* s, int b)
         }
     }
     return r;
+}
+
+// A Q6_K sub-block's share from the halves' sums of x q (codes 0..63) and of x (hx[0], hx[1]):
+// s0 (sum x q - 32 sum x) + s1 (...): the -32 of every value applied once per half.
+__device__ __forceinline__ float q6_terms(const KSub& k, float sq0, float sq1, const float* hx)
+{
+    return fmaf(k.d1, fmaf(-32.0f, hx[1], sq1), k.d0 * fmaf(-32.0f, hx[0], sq0));
 }
 
 constexpr int kMqThreads = 256;
@@ -392,8 +405,8 @@ __global__ __launch_bounds__(kMqThreads) void matvec_quant(MatvecArgs a)
         // pair go one after the other rather than side by side).
         auto row_block = [&](const uint32_t* img, int b, bool own, float* acc) {
             if constexpr (Fmt<FMT>::K) {
-                // K-quants: sum x q over the sub-block (Q6_K: x (q - 32) per 16-value half), then
-                // d0 * sum - m * sum x (Q4_K, Q5_K) or d0 * half0 + d1 * half1 (Q6_K)
+                // K-quants: sum x q over the sub-block (Q6_K: per 16-value half), then
+                // d0 * sum - m * sum x (Q4_K, Q5_K) or the halves' (sum x q - 32 sum x) scaled (Q6_K)
                 const KSub ks = ksub<FMT>(img, b);
                 float s0[TT], s1[TT];
 #pragma unroll
@@ -404,7 +417,6 @@ __global__ __launch_bounds__(kMqThreads) void matvec_quant(MatvecArgs a)
 #pragma unroll
                     for (int e = 0; e < 8; e++) {
                         q[e] = static_cast<float>((ks.w[2 * j + (e >> 2)] >> (8 * (e & 3))) & 0xFFu);
-                        if (FMT == SLHIP_FMT_Q6_K) q[e] -= 32.0f;
                     }
 #pragma unroll
                     for (int t = 0; t < TT; t++) {
@@ -418,7 +430,8 @@ __global__ __launch_bounds__(kMqThreads) void matvec_quant(MatvecArgs a)
                 }
 #pragma unroll
                 for (int t = 0; t < TT; t++) {
-                    const float p = FMT == SLHIP_FMT_Q6_K ? fmaf(ks.d1, s1[t], ks.d0 * s0[t])
+                    const float* hx = xsh + (t * nb + b) * 36 + 32;
+                    const float p = FMT == SLHIP_FMT_Q6_K ? q6_terms(ks, s0[t], s1[t], hx)
                                                           : fmaf(-ks.m, xsum[t * nb + b], ks.d0 * s0[t]);
                     acc[t] += own ? p : 0.0f;
                 }
@@ -478,18 +491,15 @@ __global__ __launch_bounds__(kMqThreads) void matvec_quant(MatvecArgs a)
                     for (int e = 0; e < 8; e++) {
                         qg[e] = static_cast<float>((kg.w[2 * j + (e >> 2)] >> (8 * (e & 3))) & 0xFFu);
                         qu[e] = static_cast<float>((ku.w[2 * j + (e >> 2)] >> (8 * (e & 3))) & 0xFFu);
-                        if (FMT == SLHIP_FMT_Q6_K) {
-                            qg[e] -= 32.0f;
-                            qu[e] -= 32.0f;
-                        }
                     }
                     dot8(qg, qu, j, FMT == SLHIP_FMT_Q6_K && j >= 2);
                 }
 #pragma unroll
                 for (int t = 0; t < TT; t++) {
-                    const float pg = FMT == SLHIP_FMT_Q6_K ? fmaf(kg.d1, g1[t], kg.d0 * g0[t])
+                    const float* hx = xsh + (t * nb + b) * 36 + 32;
+                    const float pg = FMT == SLHIP_FMT_Q6_K ? q6_terms(kg, g0[t], g1[t], hx)
                                                            : fmaf(-kg.m, xsum[t * nb + b], kg.d0 * g0[t]);
-                    const float pu = FMT == SLHIP_FMT_Q6_K ? fmaf(ku.d1, u1[t], ku.d0 * u0[t])
+                    const float pu = FMT == SLHIP_FMT_Q6_K ? q6_terms(ku, u0[t], u1[t], hx)
                                                            : fmaf(-ku.m, xsum[t * nb + b], ku.d0 * u0[t]);
                     ag[t] += own ? pg : 0.0f;
                     au[t] += own ? pu : 0.0f;
