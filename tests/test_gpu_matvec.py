@@ -272,3 +272,38 @@ def test_bf16_paths_agree_with_oracle(device, monkeypatch, min_t, dual, dx, T, K
     tol = dsilu * np.abs(u) * e * Sg + np.abs(g64 * s) * e * Su + 1e-5 * np.abs(ref) + 1e-30
     bad = np.abs(y.astype(np.float64) - ref) > tol
     assert not bad.any(), f"dual min_t={min_t}: {bad.sum()} beyond the bound; first at {np.argwhere(bad)[0]}"
+
+
+@pytest.mark.parametrize("dual", [False, True])
+def test_q6k_codes_near_32_with_offset_x(device, dual):
+    """Q6_K's -32 is applied to the sums of x over each 16-value half (sum x q - 32 sum x, the decomposition of
+    the reference's integer dot, IntDot.Decode.cs:216-221): codes 32..34 and x of mean 4 make sum x q about 33
+    times the result. Checked against the strict bound 2^-16 * sum |x| |w| (|w| itself, not the code and
+    offset terms): an f32 emulation of the kernel's order stays below 2^-21 of it."""
+    N, K, T = 48, 4096, 3
+    rng = np.random.default_rng(17)
+    raws = []
+    for tid in (1, 2):
+        raw, _ = _weights("q6_k", N, K, 5, tid)
+        b = raw.reshape(-1, 210).copy()
+        nib = rng.integers(0, 3, (b.shape[0], 128, 2))
+        b[:, 0:128] = (nib[..., 0] | (nib[..., 1] << 4)).astype(np.uint8)  # low nibbles 0..2
+        b[:, 128:192] = 0xAA                                               # every 2-bit high field 2
+        b[:, 208:210] = np.frombuffer(np.float16(0.0123).tobytes(), np.uint8)
+        raws.append(b.reshape(raw.shape))
+    x = (4.0 + 0.25 * rng.standard_normal((T, K))).astype(np.float32)
+    W = [oracle.dequant("q6_k", r.reshape(-1), N * K).reshape(N, K).astype(np.float64) for r in raws]
+    if not dual:
+        y = _run("q6_k", "f32", "f32", x, raws[:1], N, K)
+        ref = oracle.matvec("q6_k", raws[0], N, K, x)
+        _check_single(y, "f32", ref, np.abs(x).astype(np.float64) @ np.abs(W[0]).T, "q6_k near 32")
+        return
+    y = _run("q6_k", "f32", "f32", x, raws, N, K, act="silu").astype(np.float64)
+    g = x.astype(np.float64) @ W[0].T
+    u = x.astype(np.float64) @ W[1].T
+    Sg = np.abs(x).astype(np.float64) @ np.abs(W[0]).T
+    Su = np.abs(x).astype(np.float64) @ np.abs(W[1]).T
+    # |d(silu(g) u)| <= |silu'(g)| |dg| |u| + |silu(g)| |du| with |silu'| <= 1.1; plus one f32 rounding
+    ref = _act64("silu", g) * u
+    tol = 1.1 * 2.0 ** -16 * Sg * np.abs(u) + 2.0 ** -16 * Su * np.abs(_act64("silu", g)) + 2.0 ** -23 * np.abs(ref)
+    assert (np.abs(y - ref) <= tol).all()
