@@ -307,3 +307,34 @@ def test_q6k_codes_near_32_with_offset_x(device, dual):
     ref = _act64("silu", g) * u
     tol = 1.1 * 2.0 ** -16 * Sg * np.abs(u) + 2.0 ** -16 * Su * np.abs(_act64("silu", g)) + 2.0 ** -23 * np.abs(ref)
     assert (np.abs(y - ref) <= tol).all()
+
+
+@pytest.mark.parametrize("dual", [False, True])
+def test_q8_0_codes_near_0_with_offset_x(device, dual):
+    """Codes -2..2 and x of mean 4, against the strict bound 2^-16 * sum |x| |w|: a guard for any rewrite that
+    sums offset codes q + 128 and applies -128 d to the sum of x (the reference's integer-dot form,
+    IntDot.Decode.cs:75-81), which would cancel about 128-fold here (f32 emulation: 2^-20 of the bound)."""
+    N, K, T = 40, 4096, 3
+    rng = np.random.default_rng(23)
+    raws = []
+    for tid in (1, 2):
+        raw, _ = _weights("q8_0", N, K, 5, tid)
+        b = raw.reshape(-1, 34).copy()
+        b[:, 2:34] = rng.integers(-2, 3, (b.shape[0], 32)).astype(np.int8).view(np.uint8)
+        b[:, 0:2] = np.frombuffer(np.float16(0.0123).tobytes(), np.uint8)
+        raws.append(b.reshape(raw.shape))
+    x = (4.0 + 0.25 * rng.standard_normal((T, K))).astype(np.float32)
+    W = [oracle.dequant("q8_0", r.reshape(-1), N * K).reshape(N, K).astype(np.float64) for r in raws]
+    if not dual:
+        y = _run("q8_0", "f32", "f32", x, raws[:1], N, K)
+        ref = oracle.matvec("q8_0", raws[0], N, K, x)
+        _check_single(y, "f32", ref, np.abs(x).astype(np.float64) @ np.abs(W[0]).T, "q8_0 near 0")
+        return
+    y = _run("q8_0", "f32", "f32", x, raws, N, K, act="silu").astype(np.float64)
+    g = x.astype(np.float64) @ W[0].T
+    u = x.astype(np.float64) @ W[1].T
+    Sg = np.abs(x).astype(np.float64) @ np.abs(W[0]).T
+    Su = np.abs(x).astype(np.float64) @ np.abs(W[1]).T
+    ref = _act64("silu", g) * u
+    tol = 1.1 * 2.0 ** -16 * Sg * np.abs(u) + 2.0 ** -16 * Su * np.abs(_act64("silu", g)) + 2.0 ** -23 * np.abs(ref)
+    assert (np.abs(y - ref) <= tol).all()
