@@ -261,9 +261,9 @@ def add_layernorm(x, res, w, b, eps, dtype="f32"):
     return _out(y, dtype), (_out(h, dtype) if res is not None else None)
 
 
-def gated(act, gate, up, dtype="f32"):
+def gated(act, gate, up, dtype="f32", threads=None):
     """Mul(act(gate), up) as two ops (IMlpActivation.cs:12)."""
-    return _out(mul(unary(act, _as_f32(gate, dtype)), _as_f32(up, dtype)), dtype)
+    return _out(mul(unary(act, _as_f32(gate, dtype), threads=threads), _as_f32(up, dtype), threads=threads), dtype)
 
 
 def qk_norm_rope(x, pos, w=None, eps=1e-6, dtype="f32", **rope_kw):

@@ -127,11 +127,20 @@ __global__ __launch_bounds__(1024) void rownorm_vec(RowNormArgs a, int wpr)
             for (int e = 0; e < E; e++) v[k][e] += rf[e];
         }
     }
-    if (RES && a.h) {
-        char* hr = static_cast<char*>(a.h) + row * a.hs * VI::BYTES;
+    // In-place calls (y over x, h over res) are safe because no store is issued before every wave of the
+    // block holds all of its loaded data: the first reduction consumes every loaded value of the wave (and,
+    // with WPR > 1, ends in a block barrier), and every store comes after it. Lanes past the row's end then
+    // store the bytes their owners store, computed from the same unmodified inputs. A group past the last
+    // row (possible only with one wave per row, where no barrier orders it against the owning wave) stores
+    // nothing: its test is wave-uniform, so the branch is scalar.
+    const bool store_row = row0 < a.rows;
+    auto store_h = [&]() {
+        if (RES && a.h && store_row) {
+            char* hr = static_cast<char*>(a.h) + row * a.hs * VI::BYTES;
 #pragma unroll
-        for (int k = 0; k < NV; k++) store_nt(hr + static_cast<int64_t>(jv[k]) * 16, VI::pack(v[k]));
-    }
+            for (int k = 0; k < NV; k++) store_nt(hr + static_cast<int64_t>(jv[k]) * 16, VI::pack(v[k]));
+        }
+    };
 
     const float inv_d = 1.0f / static_cast<float>(a.D);
     float mean = 0.f, scale;
@@ -142,6 +151,7 @@ __global__ __launch_bounds__(1024) void rownorm_vec(RowNormArgs a, int wpr)
 #pragma unroll
             for (int e = 0; e < E; e++) s += own[k] ? v[k][e] : 0.0f;
         mean = group_reduce<4>(s, wpr, group, wig, red) * inv_d;
+        store_h();
         float q = 0.f;
 #pragma unroll
         for (int k = 0; k < NV; k++)
@@ -162,9 +172,11 @@ __global__ __launch_bounds__(1024) void rownorm_vec(RowNormArgs a, int wpr)
                 q = fmaf(x, x, q);
             }
         const float ss = group_reduce<4>(q, wpr, group, wig, red);
+        store_h();
         scale = a.kind == SLHIP_NORM_RMS ? 1.0f / sqrtf(ss * inv_d + a.eps) : 1.0f / sqrtf(ss + a.eps);
     }
 
+    if (!store_row) return;
     char* yr = static_cast<char*>(a.y) + row * a.ys * Vec<DTO>::BYTES;
     char* y16r = static_cast<char*>(a.y16) + row * a.y16s * 2;
     char* qr = static_cast<char*>(a.yq) + row * a.yqs;
@@ -269,13 +281,8 @@ __global__ __launch_bounds__(256) void rownorm_scalar(RowNormArgs a)
         if (a.b) o += a.b[i];
         return o;
     };
-    for (int64_t i = threadIdx.x; i < D; i += 256) {
-        float v = value(i);
-        if (hr) VI::store1(hr, i, v);
-        const float o = normed(v, i);
-        if (yr) Vec<DTO>::store1(yr, i, o);
-        if (y16r) Vec<SLHIP_F16>::store1(y16r, i, o);
-    }
+    // The E4M3 rows re-read the inputs, so they are written first and a barrier separates them from the
+    // stores of y and h, which may overwrite x and res (in-place calls).
     if (qr) {  // one wave per 128-value group, two values per lane
         const int lane = threadIdx.x & 63;
         for (int64_t g = threadIdx.x >> 6; g < D / 128; g += 4) {
@@ -287,6 +294,14 @@ __global__ __launch_bounds__(256) void rownorm_scalar(RowNormArgs a)
             qr[i1] = static_cast<char>(e4m3_code(o1 * id));
             if (lane == 0) *reinterpret_cast<float*>(qr + D + g * 4) = d;
         }
+    }
+    if (qr) __syncthreads();
+    for (int64_t i = threadIdx.x; i < D; i += 256) {
+        float v = value(i);
+        if (hr) VI::store1(hr, i, v);
+        const float o = normed(v, i);
+        if (yr) Vec<DTO>::store1(yr, i, o);
+        if (y16r) Vec<SLHIP_F16>::store1(y16r, i, o);
     }
 }
 

@@ -26,16 +26,14 @@ def _run(act, din, dout, g, u, *, gs=None, us=None, os_=None, pad=0):
         return d.get(po, (rows, ocols), NP[dout])
 
 
-@pytest.mark.parametrize("act", ["silu", "gelu_tanh"])
+@pytest.mark.parametrize("act", ["silu", "gelu_tanh", "gelu_erf"])
 def test_c3_full_shape(device, act):
-    """BASELINE config 3 at [8192, 14336] bf16 (SwiGLU and GeGLU); 512 sampled rows checked in full
-    against the oracle, and the whole output for sign/finiteness against silu's closed-form properties."""
+    """BASELINE config 3 at [8192, 14336] bf16 (SwiGLU, GeGLU, and the GELU-erf gate at the same shape): every
+    element against the oracle's threaded Unary-then-Mul, within 2 bf16 ulp."""
     c = synth.c3()
     y = _run(act, "bf16", "bf16", c["gate"], c["up"])
-    rows = np.unique(np.concatenate([[0, 8191], np.random.default_rng(0).integers(0, 8192, 510)]))
-    yref = oracle.gated(act, c["gate"][rows], c["up"][rows], dtype="bf16")
-    assert_bf16_close(y[rows], yref, what=f"C3 {act}")
-    assert np.isfinite(synth.bf16_to_f32(y[::97])).all()
+    yref = oracle.gated(act, c["gate"], c["up"], dtype="bf16", threads=16)
+    assert_bf16_close(y, yref, what=f"C3 {act}")
 
 
 @pytest.mark.parametrize("act", ["silu", "gelu_tanh", "gelu_erf"])

@@ -154,6 +154,45 @@ def test_rownorm_in_place_residual(device):
     assert_bf16_close(h, href, ulp=0, what="in-place h")
 
 
+IN_PLACE = [
+    # kind, dtype, rows, D, residual, forced row-group width (0: the dispatcher's choice)
+    ("rms", "f32", 4097, 1024, False, 0),   # one wave per row, 4 rows per block: 3 surplus groups
+    ("rms", "bf16", 4099, 512, True, 0),    # one wave per row with a residual; 3 surplus groups
+    ("rms", "bf16", 37, 896, True, 0),      # 112 vectors: surplus lanes of the same wave
+    ("rms", "bf16", 37, 896, True, 2),      # surplus lanes in the second wave of a two-wave group
+    ("rms", "bf16", 4099, 896, True, 2),    # two-wave groups, two groups per block, one surplus group
+    ("rms", "f32", 5, 1000, True, 4),       # 250 vectors over 256 lanes: surplus lanes in the fourth wave
+    ("layer", "bf16", 4099, 512, True, 0),  # LayerNorm's two reductions with one wave per row
+    ("layer", "f32", 37, 1000, True, 2),
+    ("rms", "bf16", 9, 4100, True, 0),      # D % 8 != 0: the scalar kernel
+]
+
+
+@pytest.mark.parametrize("kind,din,rows,D,with_res,wpr", IN_PLACE)
+def test_rownorm_in_place_shapes(device, monkeypatch, kind, din, rows, D, with_res, wpr):
+    """y written over x and h over res at shapes whose launch has lanes past the row's end or row groups past
+    the last row, which re-read the row's last vector or last row: those must not observe the owner's
+    stores (every value compared with the oracle on the unmodified inputs)."""
+    if wpr:
+        monkeypatch.setenv("SLHIP_ROWNORM_WPR", str(wpr))
+    x, r, w, b = _inputs(rows, D, din, seed=rows + D, scale=2.0)
+    b = b if kind == "layer" else None
+    with Dev() as d:
+        px = d.put(x)
+        pr = d.put(r) if with_res else None
+        log(f"rownorm in-place kind={kind} {din} [{rows},{D}] res={with_res} wpr={wpr}")
+        native.rownorm(kind, din, din, px, px, rows, D, res=pr, w=d.put(w), b=d.put(b) if b is not None else None,
+                       h_out=pr, eps=1e-5)
+        native.synchronize()
+        y = d.get(px, (rows, D), NP[din])
+        h = d.get(pr, (rows, D), NP[din]) if with_res else None
+    yref, href, _ = _reference(kind, din, din, x, r, w, b, 1e-5, with_res)
+    _check(din, y, yref, f"in-place y {kind} [{rows},{D}]")
+    if with_res:
+        assert np.array_equal(h.view(np.uint16 if din == "bf16" else np.uint32),
+                              href.view(np.uint16 if din == "bf16" else np.uint32)), "in-place h"
+
+
 def test_rownorm_zero_rows_is_noop(device):
     native.rownorm("rms", "f32", "f32", None, None, 0, 1024)
     native.synchronize()
