@@ -351,6 +351,58 @@ SLHIP_API int slhip_cache_write(int dtype_in, int dtype_cache, const void* x, in
  */
 SLHIP_API int slhip_convert(int dtype_in, int dtype_out, const void* x, void* y, int64_t n, slhip_stream stream);
 
+/* ---- standalone elementwise ops ------------------------------------------------------------------ */
+
+/* Two-operand ops, in the order of the reference's BinaryKind (src/Sharplight.Cpu/BinaryKind.cs:4);
+ * SLHIP_BIN_FMOD is Mod with the attribute fmod=true (C fmod: the sign of the dividend). Comparisons and
+ * logic ops give 1.0 / 0.0. */
+typedef enum slhip_binary_op {
+    SLHIP_BIN_ADD = 0, SLHIP_BIN_SUB, SLHIP_BIN_MUL, SLHIP_BIN_DIV, SLHIP_BIN_MAX, SLHIP_BIN_MIN, SLHIP_BIN_POW,
+    SLHIP_BIN_MOD, SLHIP_BIN_PRELU, SLHIP_BIN_EQUAL, SLHIP_BIN_NOT_EQUAL, SLHIP_BIN_LESS, SLHIP_BIN_LESS_EQUAL,
+    SLHIP_BIN_GREATER, SLHIP_BIN_GREATER_EQUAL, SLHIP_BIN_AND, SLHIP_BIN_OR, SLHIP_BIN_XOR, SLHIP_BIN_ATAN2,
+    SLHIP_BIN_FMOD
+} slhip_binary_op;
+
+/* One-operand ops, in the order of the reference's UnaryKind (src/Sharplight.Cpu/UnaryKind.cs:4-6). p0/p1
+ * are its two parameters: Scale (scale, bias), Clip (min, max), HardSigmoid (alpha, beta), Elu/Celu/
+ * ThresholdedRelu/LeakyRelu (alpha), Selu (alpha, gamma)
+ * (CpuCompiledSegment.LowerElementwise.cs:31-39). */
+typedef enum slhip_unary_op {
+    SLHIP_UN_NEG = 0, SLHIP_UN_EXP, SLHIP_UN_LOG, SLHIP_UN_SQRT, SLHIP_UN_RSQRT, SLHIP_UN_SIGMOID, SLHIP_UN_SILU,
+    SLHIP_UN_GELU, SLHIP_UN_GELU_TANH, SLHIP_UN_TANH, SLHIP_UN_SOFTPLUS, SLHIP_UN_RELU, SLHIP_UN_ABS,
+    SLHIP_UN_SQUARE, SLHIP_UN_RECIP, SLHIP_UN_SCALE, SLHIP_UN_ERF, SLHIP_UN_HARD_SWISH, SLHIP_UN_HARD_SIGMOID,
+    SLHIP_UN_CLIP, SLHIP_UN_SIN, SLHIP_UN_COS, SLHIP_UN_TAN, SLHIP_UN_ASIN, SLHIP_UN_ACOS, SLHIP_UN_ATAN,
+    SLHIP_UN_SINH, SLHIP_UN_COSH, SLHIP_UN_ASINH, SLHIP_UN_ACOSH, SLHIP_UN_ATANH, SLHIP_UN_FLOOR, SLHIP_UN_CEIL,
+    SLHIP_UN_ROUND, SLHIP_UN_SIGN, SLHIP_UN_SOFTSIGN, SLHIP_UN_MISH, SLHIP_UN_ELU, SLHIP_UN_CELU, SLHIP_UN_SELU,
+    SLHIP_UN_LEAKY_RELU, SLHIP_UN_THRESHOLDED_RELU, SLHIP_UN_NOT, SLHIP_UN_IS_NAN, SLHIP_UN_IS_INF
+} slhip_unary_op;
+
+/*
+ * y = op(a, b) with numpy-style broadcasting, y dense [dims] (rank <= 8). a_strides / b_strides: element
+ * strides of a and b aligned to y's rank, 0 along a dim the operand broadcasts (extent 1, or missing in
+ * front) -- BinaryOp's Align (src/Sharplight.Cpu/BinaryOp.cs:37-58); NULL means dense [dims].
+ * dtype_a: F32, F16 or BF16; dtype_b: dtype_a or F32 (a bias or scale kept in f32); dtype_out: any.
+ * Arithmetic in f32 as BinaryOp (BinaryOp.cs:60-357): Max/Min propagate NaN and order -0 below +0; Pow
+ * with an exponent that is one value along y's innermost dim takes BinaryOp.Apply's forms for 2, 1, 0.5
+ * and 3. y may alias a or b when it has that operand's shape and layout.
+ * Replaces: BinaryOp and the Vulkan lowerer's generated elementwise kernels
+ * (src/Sharplight.Shaders/Lowering/GraphLowerer.Elementwise.cs:60-200).
+ */
+SLHIP_API int slhip_binary(int op, int dtype_a, int dtype_b, int dtype_out, const void* a, const int64_t* a_strides,
+                           const void* b, const int64_t* b_strides, void* y, const int64_t* dims, int rank,
+                           slhip_stream stream);
+
+/*
+ * y = op(x) over [rows, cols] with row strides (elements). dtype_in, dtype_out: F32, F16 or BF16.
+ * The forms are ScalarMath.Unary's vector forms (src/Sharplight.Cpu/ScalarMath.cs:100-650): Scale and
+ * HardSigmoid/HardSwish fused multiply-adds, Gelu with the f64 rational erf (as slhip_gated_act),
+ * GeluTanh as v / (1 + exp(-u)), Softplus in f64; exp, tanh, log and the trigonometric functions to
+ * within 2 f32 ulp of the correctly rounded value.
+ * Replaces: UnaryOp (src/Sharplight.Cpu/UnaryOp.cs:30-75) and the lowerer's lone-activation kernels.
+ */
+SLHIP_API int slhip_unary(int op, int dtype_in, int dtype_out, const void* x, void* y, int64_t rows, int64_t cols,
+                          int64_t x_stride, int64_t y_stride, float p0, float p1, slhip_stream stream);
+
 /* ---- provider / compiled segment (IExecutionProvider, IComputeDevice, ICompiledSegment) ----------------
  *
  * A graph segment arrives as text, one declaration per line ('#' starts a comment line):
@@ -360,7 +412,10 @@ SLHIP_API int slhip_convert(int dtype_in, int dtype_out, const void* x, void* y,
  *                                     across runs, starts at zero and is zeroed again by reset_state)
  *   node <Op> <in,ids> -> <out,ids> [key=value ...]
  * with the StandardOps names and attributes of the reference (src/Sharplight.Core/Graph/StandardOps.cs):
- *   Add, Mul (same-shape), Silu, GeluTanh, Gelu, RmsNorm (x[, w]; eps), L2Norm (x; eps),
+ *   the binary ops Add, Sub, Mul, Div, Max, Min, Pow, Mod (fmod), PRelu, the comparisons and logic ops,
+ *   Atan2 (numpy broadcasting), the one-operand ops of slhip_unary_op by name, Scale (scale, bias), Clip
+ *   (min, max), HardSigmoid (alpha, beta), Elu/Celu/LeakyRelu/ThresholdedRelu (alpha), Selu (alpha, gamma),
+ *   RmsNorm (x[, w]; eps), L2Norm (x; eps),
  *   LayerNorm (x[, w[, b]]; eps), Rope (x [T,H,D], pos i32 [T][, ff]; dims, base, style=neox|normal|gptj,
  *   freq_scale, attn_factor), Gather (table [V, D...], ids i32 [N]), Cast,
  *   CacheWrite (state [ctx, ...], x [T, ...][, rows i32 [T,4][, pages i32 [slots, blocks]]]; offset=<scalar
@@ -400,6 +455,10 @@ SLHIP_API int slhip_segment_set_scalar(slhip_segment segment, const char* name, 
 SLHIP_API int slhip_segment_device_bytes(slhip_segment segment, int64_t* bytes);
 /* The fused launches of the compiled segment, one label per line (e.g. "fused[Add]+RmsNorm"). */
 SLHIP_API int slhip_segment_launches(slhip_segment segment, char* buf, size_t size);
+/* The launches slhip_segment_compile would create for a segment text, one label per line, decided without
+ * touching a device: the lowerer's plan (GraphLowerer.Lower, src/Sharplight.Shaders/Lowering/GraphLowerer.cs:
+ * 64-71, without the buffers). Fails as compile would for a node or pattern this provider cannot run. */
+SLHIP_API int slhip_segment_plan(const char* segment_ir, char* buf, size_t size);
 SLHIP_API int slhip_segment_destroy(slhip_segment segment);
 
 /* ---- GGUF files and weight upload (the on-disk -> device path) --------------------------------

@@ -69,6 +69,9 @@ def _declare(L):
         "orc_mul": (None, [_P, _P, _P, _I64]),
         "orc_unary": (None, [_I, _P, _P, _I64]),
         "orc_erf": (ctypes.c_double, [ctypes.c_double]),
+        "orc_unary_kind": (None, [_I, _P, _P, _I64, _F, _F]),
+        "orc_binary": (None, [_I, _P, _P, _P, _P, _P, _P, _I]),
+        "orc_align": (None, [_P, _I, _I, _P]),
         "orc_erf_rational": (_F, [_F]),
         "orc_rope": (None, [_P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _F, _F, _F]),
         "orc_row_bytes": (_I64, [_I, _I64]),
@@ -194,6 +197,47 @@ def unary(act, x, threads=None):
     x = _c(x, np.float32)
     y = np.empty_like(x)
     (lib().orc_unary_mt if threads else lib().orc_unary)(ACTS[act], _p(x), _p(y), x.size)
+    return y
+
+
+# The reference's UnaryKind and BinaryKind, by name (src/Sharplight.Cpu/UnaryKind.cs:4-6, BinaryKind.cs:4).
+UNARY_KINDS = ["Neg", "Exp", "Log", "Sqrt", "Rsqrt", "Sigmoid", "Silu", "Gelu", "GeluTanh", "Tanh", "Softplus", "Relu",
+               "Abs", "Square", "Recip", "Scale", "Erf", "HardSwish", "HardSigmoid", "Clip", "Sin", "Cos", "Tan",
+               "Asin", "Acos", "Atan", "Sinh", "Cosh", "Asinh", "Acosh", "Atanh", "Floor", "Ceil", "Round", "Sign",
+               "Softsign", "Mish", "Elu", "Celu", "Selu", "LeakyRelu", "ThresholdedRelu", "Not", "IsNaN", "IsInf"]
+BINARY_KINDS = ["Add", "Sub", "Mul", "Div", "Max", "Min", "Pow", "Mod", "PRelu", "Equal", "NotEqual", "Less",
+                "LessEqual", "Greater", "GreaterEqual", "And", "Or", "Xor", "Atan2", "FMod"]
+
+
+def unary_kind(kind, x, p0=1.0, p1=0.0):
+    """ScalarMath.Unary of one contiguous range (vector forms on whole groups of 8, then the tail form)."""
+    x = _c(x, np.float32)
+    y = np.empty(x.shape, np.float32)
+    lib().orc_unary_kind(UNARY_KINDS.index(kind), _p(x), _p(y), x.size, p0, p1)
+    return y
+
+
+def align(a_shape, y_rank):
+    """BinaryOp.Align: element strides of a dense operand of a_shape against an output of rank y_rank."""
+    d = np.asarray(a_shape, np.int64)
+    s = np.empty(max(y_rank, 1), np.int64)
+    lib().orc_align(_p(d), len(a_shape), y_rank, _p(s))
+    return s[:y_rank]
+
+
+def binary(kind, a, b):
+    """BinaryOp on dense f32 operands with numpy broadcasting; returns y of the broadcast shape."""
+    sha, shb = np.shape(a), np.shape(b)
+    a = _c(a, np.float32)  # (a 0-d operand becomes 1-d here; its shape is kept above)
+    b = _c(b, np.float32)
+    shape = np.broadcast_shapes(sha, shb)
+    r = len(shape)
+    y = np.empty(shape, np.float32)
+    dims = np.asarray(shape if r else [1], np.int64)
+    sa, sb = align(sha, r), align(shb, r)
+    if r == 0:
+        sa = sb = np.zeros(1, np.int64)
+    lib().orc_binary(BINARY_KINDS.index(kind), _p(a), _p(sa), _p(b), _p(sb), _p(y), _p(dims), r)
     return y
 
 

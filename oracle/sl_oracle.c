@@ -290,6 +290,222 @@ static void unary_range(int act, const float* x, float* y, int64_t n)
 
 void orc_unary(int act, const float* x, float* y, int64_t n) { unary_range(act, x, y, n); }
 
+/* The reference's UnaryKind (src/Sharplight.Cpu/UnaryKind.cs:4-6), numbered as declared there. */
+enum { U_NEG, U_EXP, U_LOG, U_SQRT, U_RSQRT, U_SIGMOID, U_SILU, U_GELU, U_GELU_TANH, U_TANH, U_SOFTPLUS, U_RELU,
+       U_ABS, U_SQUARE, U_RECIP, U_SCALE, U_ERF, U_HARD_SWISH, U_HARD_SIGMOID, U_CLIP, U_SIN, U_COS, U_TAN, U_ASIN,
+       U_ACOS, U_ATAN, U_SINH, U_COSH, U_ASINH, U_ACOSH, U_ATANH, U_FLOOR, U_CEIL, U_ROUND, U_SIGN, U_SOFTSIGN,
+       U_MISH, U_ELU, U_CELU, U_SELU, U_LEAKY_RELU, U_THRESHOLDED_RELU, U_NOT, U_IS_NAN, U_IS_INF };
+
+/* MathF.Max / MathF.Min and the Vector*.Max/Min of .NET (IEEE 754-2019 maximum/minimum): NaN if
+ * either operand is NaN, +0 above -0. */
+static float net_max(float a, float b)
+{
+    if (a != a) return a;
+    if (b != b) return b;
+    if (a == b) return signbit(a) ? b : a;
+    return a > b ? a : b;
+}
+static float net_min(float a, float b)
+{
+    if (a != a) return a;
+    if (b != b) return b;
+    if (a == b) return signbit(a) ? a : b;
+    return a < b ? a : b;
+}
+
+/* Softplus (ScalarMath.cs:643-650) and the Mish term (:279-284): log(1 + exp(v)) in f64 up to 20. */
+static float softplus(float v) { return v > 20.0f ? v : (float)log(1.0 + exp((double)v)); }
+
+/* ScalarMath.Unary (src/Sharplight.Cpu/ScalarMath.cs:173-650) on one contiguous range, AVX2 tier
+ * (CpuIsa.Use256): the kinds with a Vector256 loop take its form on whole groups of 8 from the start of
+ * the range and the scalar form on the rest; the others are scalar throughout. Forms that differ:
+ *   HardSwish   (349-370): vector v*min(max(fma(v, 1/6, 0.5), 0), 1); tail v*clamp(v*(1/6) + 0.5, 0, 1)
+ *   HardSigmoid (371-387): vector min(max(fma(v, a, b), 0), 1);       tail clamp(v*a + b, 0, 1)
+ *   Scale       (460-484): vector fma(v, s, b);                       tail v*s + b
+ *   GeluTanh, Gelu as unary_range above; Silu, Sigmoid and Exp have one form (.NET's Vector Exp against
+ *   MathF.Exp: libm stands in for both). */
+void orc_unary_kind(int kind, const float* x, float* y, int64_t n, float p0, float p1)
+{
+    const int64_t vec = n - n % 8;
+    int64_t i = 0;
+    switch (kind) {
+    case U_SILU: unary_range(0, x, y, n); return;
+    case U_GELU_TANH: unary_range(1, x, y, n); return;
+    case U_GELU: unary_range(2, x, y, n); return;
+    case U_HARD_SWISH:
+        for (; i < vec; i++) y[i] = x[i] * net_min(net_max(fmaf(x[i], 1.0f / 6.0f, 0.5f), 0.0f), 1.0f);
+        for (; i < n; i++) {
+            float c = x[i] * (1.0f / 6.0f) + 0.5f;  /* Math.Clamp(v, 0, 1): v < 0 -> 0, v > 1 -> 1, else v */
+            y[i] = x[i] * (c < 0.0f ? 0.0f : c > 1.0f ? 1.0f : c);
+        }
+        return;
+    case U_HARD_SIGMOID:
+        for (; i < vec; i++) y[i] = net_min(net_max(fmaf(x[i], p0, p1), 0.0f), 1.0f);
+        for (; i < n; i++) {
+            float c = x[i] * p0 + p1;
+            y[i] = c < 0.0f ? 0.0f : c > 1.0f ? 1.0f : c;
+        }
+        return;
+    case U_SCALE:
+        for (; i < vec; i++) y[i] = fmaf(x[i], p0, p1);
+        for (; i < n; i++) y[i] = x[i] * p0 + p1;
+        return;
+    case U_ERF: /* vector: the f64 rational (ErfV); tail ErfF, the same rational with separate mul/add */
+        for (; i < vec; i++) y[i] = orc_erf_rational(x[i]);
+        for (; i < n; i++) {
+            const double A1 = -1.60960333262415e-02, A3 = -2.95459980854025e-03, A5 = -7.34990630326855e-04,
+                         A7 = -5.69250639462346e-05, A9 = -2.10102402082508e-06, A11 = 2.77068142495902e-08,
+                         A13 = -2.72614225801306e-10, B0 = -1.42647390514189e-02, B2 = -7.37332916720468e-03,
+                         B4 = -1.68282697438203e-03, B6 = -2.13374055278905e-04, B8 = -1.45660718464996e-05;
+            const double c = (double)3.832506856900711f;
+            double v = x[i];
+            v = v < -c ? -c : v > c ? c : v;
+            double x2 = v * v;
+            double pp = ((((((A13 * x2 + A11) * x2 + A9) * x2 + A7) * x2 + A5) * x2 + A3) * x2 + A1) * v;
+            double q = ((((B8 * x2 + B6) * x2 + B4) * x2 + B2) * x2 + B0);
+            y[i] = (float)(pp / q);
+        }
+        return;
+    default: break;
+    }
+    for (; i < n; i++) {
+        const float v = x[i];
+        float r;
+        switch (kind) {
+        case U_NEG: r = -v; break;
+        case U_EXP: r = expf(v); break;
+        case U_LOG: r = logf(v); break;
+        case U_SQRT: r = sqrtf(v); break;
+        case U_RSQRT: r = 1.0f / sqrtf(v); break;
+        case U_SIGMOID: r = 1.0f / (1.0f + expf(-v)); break;
+        case U_TANH: r = tanhf(v); break;
+        case U_SOFTPLUS: r = softplus(v); break;
+        case U_RELU: r = v > 0 ? v : 0.0f; break;
+        case U_ABS: r = fabsf(v); break;
+        case U_SQUARE: r = v * v; break;
+        case U_RECIP: r = 1.0f / v; break;
+        case U_CLIP: r = net_min(net_max(v, p0), p1); break; /* Vector256.Min(Max(v, lo), hi) (:388-410) */
+        case U_SIN: r = sinf(v); break;
+        case U_COS: r = cosf(v); break;
+        case U_TAN: r = tanf(v); break;
+        case U_ASIN: r = asinf(v); break;
+        case U_ACOS: r = acosf(v); break;
+        case U_ATAN: r = atanf(v); break;
+        case U_SINH: r = sinhf(v); break;
+        case U_COSH: r = coshf(v); break;
+        case U_ASINH: r = asinhf(v); break;
+        case U_ACOSH: r = acoshf(v); break;
+        case U_ATANH: r = atanhf(v); break;
+        case U_FLOOR: r = floorf(v); break;
+        case U_CEIL: r = ceilf(v); break;
+        case U_ROUND: r = rintf(v); break; /* MidpointRounding.ToEven under the default rounding mode */
+        case U_SIGN: r = v > 0 ? 1.0f : v < 0 ? -1.0f : v; break;
+        case U_SOFTSIGN: r = v / (1.0f + fabsf(v)); break;
+        case U_MISH: r = v * tanhf(softplus(v)); break;
+        case U_ELU: r = v >= 0 ? v : p0 * (expf(v) - 1.0f); break;
+        case U_CELU: r = net_max(0.0f, v) + net_min(0.0f, p0 * (expf(v / p0) - 1.0f)); break;
+        case U_SELU: r = v > 0 ? p1 * v : p1 * p0 * (expf(v) - 1.0f); break;
+        case U_LEAKY_RELU: r = v >= 0 ? v : p0 * v; break;
+        case U_THRESHOLDED_RELU: r = v > p0 ? v : 0.0f; break;
+        case U_NOT: r = v != 0 ? 0.0f : 1.0f; break;
+        case U_IS_NAN: r = v != v ? 1.0f : 0.0f; break;
+        default: r = isinf(v) ? 1.0f : 0.0f; break;
+        }
+        y[i] = r;
+    }
+}
+
+/* BinaryKind (src/Sharplight.Cpu/BinaryKind.cs:4), then Mod with fmod = true. */
+enum { B_ADD, B_SUB, B_MUL, B_DIV, B_MAX, B_MIN, B_POW, B_MOD, B_PRELU, B_EQ, B_NE, B_LT, B_LE, B_GT, B_GE, B_AND,
+       B_OR, B_XOR, B_ATAN2, B_FMOD };
+
+/* BinaryOp.OpS / OpS2 (BinaryOp.cs:309-357). */
+static float binary_scalar(int k, float a, float b)
+{
+    switch (k) {
+    case B_ADD: return a + b;
+    case B_SUB: return a - b;
+    case B_MUL: return a * b;
+    case B_DIV: return a / b;
+    case B_MAX: return net_max(a, b);
+    case B_MIN: return net_min(a, b);
+    case B_POW: return powf(a, b);
+    case B_MOD:
+    case B_FMOD: {
+        float r = fmodf(a, b);
+        if (k == B_MOD && r != 0 && (r < 0) != (b < 0)) r += b;
+        return r;
+    }
+    case B_PRELU: return a < 0 ? a * b : a;
+    case B_EQ: return a == b ? 1.0f : 0.0f;
+    case B_NE: return a != b ? 1.0f : 0.0f;
+    case B_LT: return a < b ? 1.0f : 0.0f;
+    case B_LE: return a <= b ? 1.0f : 0.0f;
+    case B_GT: return a > b ? 1.0f : 0.0f;
+    case B_GE: return a >= b ? 1.0f : 0.0f;
+    case B_AND: return a != 0 && b != 0 ? 1.0f : 0.0f;
+    case B_OR: return a != 0 || b != 0 ? 1.0f : 0.0f;
+    case B_XOR: return (a != 0) != (b != 0) ? 1.0f : 0.0f;
+    default: return atan2f(a, b);
+    }
+}
+
+/* BinaryOp.Apply (BinaryOp.cs:141-275) on one row of n outputs: Pow with a row-constant exponent (sb == 0)
+ * takes the forms for 2, 1, 0.5 and 3 (:153-196); the vector loops compute what the scalar ops do. */
+static void binary_row(int k, const float* a, int64_t sa, const float* b, int64_t sb, float* y, int64_t n)
+{
+    if (k == B_POW && sb == 0) {
+        const float e = *b;
+        for (int64_t i = 0; i < n; i++) {
+            const float v = a[i * sa];
+            y[i] = e == 2.0f ? v * v : e == 1.0f ? v : e == 0.5f ? sqrtf(v) : e == 3.0f ? v * v * v : powf(v, e);
+        }
+        return;
+    }
+    for (int64_t i = 0; i < n; i++) y[i] = binary_scalar(k, a[i * sa], b[i * sb]);
+}
+
+/* BinaryOp.Align (BinaryOp.cs:37-58): a's strides against y's rank; a dim of extent 1 or a missing
+ * leading dim gets stride 0. a_dims/a_rank describe a dense operand. */
+void orc_align(const int64_t* a_dims, int a_rank, int y_rank, int64_t* strides)
+{
+    int64_t dense[16];
+    int64_t acc = 1;
+    for (int k = a_rank - 1; k >= 0; k--) {
+        dense[k] = acc;
+        acc *= a_dims[k];
+    }
+    for (int k = 0; k < y_rank; k++) {
+        const int ik = k - (y_rank - a_rank);
+        strides[k] = ik < 0 || a_dims[ik] == 1 ? 0 : dense[ik];
+    }
+}
+
+/* BinaryOp.Run + Body (BinaryOp.cs:60-139): y dense [dims], a and b by aligned strides. Rows of the
+ * innermost dim (the trailing merge changes only the loop bounds, not the values); rank 0 is one element. */
+void orc_binary(int k, const float* a, const int64_t* sa, const float* b, const int64_t* sb, float* y,
+                const int64_t* dims, int rank)
+{
+    if (rank == 0) {
+        binary_row(k, a, 0, b, 0, y, 1);
+        return;
+    }
+    int64_t total = 1;
+    for (int d = 0; d < rank; d++) total *= dims[d];
+    if (total == 0) return;
+    const int64_t l = dims[rank - 1];
+    for (int64_t r = 0; r < total / l; r++) {
+        int64_t ao = 0, bo = 0, rr = r;
+        for (int d = rank - 2; d >= 0; d--) {
+            const int64_t q = rr / dims[d], ix = rr - q * dims[d];
+            rr = q;
+            ao += ix * sa[d];
+            bo += ix * sb[d];
+        }
+        binary_row(k, a + ao, sa[rank - 1], b + bo, sb[rank - 1], y + r * l, l);
+    }
+}
+
 /* ------------------------------------------------------------------------------------------ */
 /* rope                                                                                       */
 /* ------------------------------------------------------------------------------------------ */

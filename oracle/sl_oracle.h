@@ -47,6 +47,12 @@ void orc_add(const float* a, const float* b, float* y, int64_t n);
 void orc_mul(const float* a, const float* b, float* y, int64_t n);
 /* act: 0 = Silu, 1 = GeluTanh, 2 = Gelu (erf) */
 void orc_unary(int act, const float* x, float* y, int64_t n);
+/* kind: the reference's UnaryKind number (Neg = 0 ... IsInf = 44); p0/p1 its two parameters */
+void orc_unary_kind(int kind, const float* x, float* y, int64_t n, float p0, float p1);
+/* kind: BinaryKind number (Add = 0 ... Atan2 = 18), 19 = Mod with fmod; y dense [dims], a/b aligned strides */
+void orc_binary(int kind, const float* a, const int64_t* sa, const float* b, const int64_t* sb, float* y,
+                const int64_t* dims, int rank);
+void orc_align(const int64_t* a_dims, int a_rank, int y_rank, int64_t* strides);
 double orc_erf(double x);
 float orc_erf_rational(float x);
 

@@ -28,6 +28,9 @@ int check_launch(const char* kernel);
 // library: nothing is allocated for it.
 int error_word(uint32_t** word);
 
+// Whether slhip_matvec / slhip_dual_matvec can stage rows of K values of `fmt` (matvec.hip).
+bool matvec_fits(int fmt, int64_t K, bool dual);
+
 // KV-cache destination rows (slhip_cache_rows) as kernels take them.
 struct CacheRowsDev {
     int mode;

@@ -1099,6 +1099,16 @@ static int run_quant(MatvecArgs a, bool dual, hipStream_t st)
     return SLHIP_OK;
 }
 
+// Whether a (dual) matvec over rows of K values of `fmt` can run: for the block formats, whether one token's
+// staged x and the row images of a block's waves fit in LDS.
+bool matvec_fits(int fmt, int64_t K, bool dual)
+{
+    const QGeom qg = quant_geom(fmt);
+    if (qg.bs == 0) return true;
+    if (K % qg.bs != 0) return false;
+    return quant_lds(1, K, K / qg.bs * qg.bb, dual) <= kMaxLds;
+}
+
 static int matvec_common(int fmt, int dtype_x, int dtype_y, const void* x, int64_t x_stride, int64_t T, int64_t K,
                          const void* wg, const void* wu, int64_t N, void* y, int64_t y_stride, int act, bool dual,
                          slhip_stream stream)

@@ -22,8 +22,10 @@
 //     the f32 rows when nothing else reads them (GraphLowerer.HalfCopies.cs:106-151);
 //   * two MatMuls sharing x whose products feed act(gate) * up -> one dual matvec launch with the gating
 //     epilogue (FoldDualMatMuls, :286-353);
-//   * RmsNorm, L2Norm, LayerNorm, Rope, Gather, Cast, CacheWrite and MatMul (decode matvec) on their own.
-// An Add, Mul or activation that fits none of these patterns is not supported on this provider.
+//   * RmsNorm, L2Norm, LayerNorm, Rope, Gather, Cast, CacheWrite and MatMul (decode matvec) on their own;
+//   * every other elementwise node -- the binary ops with numpy broadcasting (a bias add, a scalar Mul),
+//     the one-operand ops, Scale and Clip -- as one standalone elementwise launch (the CPU provider's
+//     BinaryOp / UnaryOp, src/Sharplight.Cpu/CpuCompiledSegment.LowerElementwise.cs:8-72).
 //
 // The graph reaches the C ABI as a small line-based text form (one value, node, input, weight or output
 // per line; see slhip_segment_compile in include/sharplight_hip.h); the managed provider writes it from a
@@ -34,6 +36,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <tuple>
 #include <map>
 #include <memory>
 #include <set>
@@ -286,19 +289,88 @@ struct Support {
 
 const std::set<std::string> kActs = {"Silu", "GeluTanh", "Gelu"};
 
+// StandardOps.BinaryNames (src/Sharplight.Core/Graph/StandardOps.cs:39-45) -> slhip_binary_op.
+const std::map<std::string, int> kBinaryOps = {
+    {"Add", SLHIP_BIN_ADD}, {"Sub", SLHIP_BIN_SUB}, {"Mul", SLHIP_BIN_MUL}, {"Div", SLHIP_BIN_DIV},
+    {"Max", SLHIP_BIN_MAX}, {"Min", SLHIP_BIN_MIN}, {"Pow", SLHIP_BIN_POW}, {"Mod", SLHIP_BIN_MOD},
+    {"PRelu", SLHIP_BIN_PRELU}, {"Equal", SLHIP_BIN_EQUAL}, {"NotEqual", SLHIP_BIN_NOT_EQUAL},
+    {"Less", SLHIP_BIN_LESS}, {"LessEqual", SLHIP_BIN_LESS_EQUAL}, {"Greater", SLHIP_BIN_GREATER},
+    {"GreaterEqual", SLHIP_BIN_GREATER_EQUAL}, {"And", SLHIP_BIN_AND}, {"Or", SLHIP_BIN_OR}, {"Xor", SLHIP_BIN_XOR},
+    {"Atan2", SLHIP_BIN_ATAN2}};
+// Commutative ops: an f32 a with a bf16/f16 b runs as op(b, a) (slhip_binary takes b as a's type or f32).
+const std::set<int> kCommutative = {SLHIP_BIN_ADD, SLHIP_BIN_MUL, SLHIP_BIN_MAX, SLHIP_BIN_MIN, SLHIP_BIN_EQUAL,
+                                    SLHIP_BIN_NOT_EQUAL, SLHIP_BIN_AND, SLHIP_BIN_OR, SLHIP_BIN_XOR};
+
+// StandardOps.UnaryNames (StandardOps.cs:25-33), Scale (:48) and Clip (StandardOps.Spatial.cs:12) ->
+// slhip_unary_op (the reference's UnaryKind order).
+const std::map<std::string, int> kUnaryOps = {
+    {"Neg", SLHIP_UN_NEG}, {"Exp", SLHIP_UN_EXP}, {"Log", SLHIP_UN_LOG}, {"Sqrt", SLHIP_UN_SQRT},
+    {"Rsqrt", SLHIP_UN_RSQRT}, {"Sigmoid", SLHIP_UN_SIGMOID}, {"Silu", SLHIP_UN_SILU}, {"Gelu", SLHIP_UN_GELU},
+    {"GeluTanh", SLHIP_UN_GELU_TANH}, {"Tanh", SLHIP_UN_TANH}, {"Softplus", SLHIP_UN_SOFTPLUS},
+    {"Relu", SLHIP_UN_RELU}, {"Abs", SLHIP_UN_ABS}, {"Square", SLHIP_UN_SQUARE}, {"Recip", SLHIP_UN_RECIP},
+    {"Scale", SLHIP_UN_SCALE}, {"Erf", SLHIP_UN_ERF}, {"HardSwish", SLHIP_UN_HARD_SWISH},
+    {"HardSigmoid", SLHIP_UN_HARD_SIGMOID}, {"Clip", SLHIP_UN_CLIP}, {"Sin", SLHIP_UN_SIN}, {"Cos", SLHIP_UN_COS},
+    {"Tan", SLHIP_UN_TAN}, {"Asin", SLHIP_UN_ASIN}, {"Acos", SLHIP_UN_ACOS}, {"Atan", SLHIP_UN_ATAN},
+    {"Sinh", SLHIP_UN_SINH}, {"Cosh", SLHIP_UN_COSH}, {"Asinh", SLHIP_UN_ASINH}, {"Acosh", SLHIP_UN_ACOSH},
+    {"Atanh", SLHIP_UN_ATANH}, {"Floor", SLHIP_UN_FLOOR}, {"Ceil", SLHIP_UN_CEIL}, {"Round", SLHIP_UN_ROUND},
+    {"Sign", SLHIP_UN_SIGN}, {"Softsign", SLHIP_UN_SOFTSIGN}, {"Mish", SLHIP_UN_MISH}, {"Elu", SLHIP_UN_ELU},
+    {"Celu", SLHIP_UN_CELU}, {"Selu", SLHIP_UN_SELU}, {"LeakyRelu", SLHIP_UN_LEAKY_RELU},
+    {"ThresholdedRelu", SLHIP_UN_THRESHOLDED_RELU}, {"Not", SLHIP_UN_NOT}, {"IsNaN", SLHIP_UN_IS_NAN},
+    {"IsInf", SLHIP_UN_IS_INF}};
+
+// numpy broadcasting of two dim lists (the symbolic T broadcasts against T or 1 only); false if they clash.
+bool broadcast_dims(const std::vector<int64_t>& a, const std::vector<int64_t>& b, std::vector<int64_t>& out)
+{
+    const size_t r = std::max(a.size(), b.size());
+    out.assign(r, 1);
+    for (size_t k = 0; k < r; k++) {
+        const int64_t da = k < r - a.size() ? 1 : a[k - (r - a.size())];
+        const int64_t db = k < r - b.size() ? 1 : b[k - (r - b.size())];
+        if (da == db) out[k] = da;
+        else if (da == 1) out[k] = db;
+        else if (db == 1) out[k] = da;
+        else return false;
+    }
+    return true;
+}
+
+// The two UnaryOp parameters of a node (CpuCompiledSegment.LowerElementwise.cs:31-50).
+std::pair<float, float> unary_params(int code, const Node& n)
+{
+    const float inf = INFINITY;
+    switch (code) {
+    case SLHIP_UN_SCALE: return {n.f("scale", 1.f), n.f("bias", 0.f)};
+    case SLHIP_UN_HARD_SIGMOID: return {n.f("alpha", 0.2f), n.f("beta", 0.5f)};
+    case SLHIP_UN_ELU:
+    case SLHIP_UN_CELU:
+    case SLHIP_UN_THRESHOLDED_RELU: return {n.f("alpha", 1.f), 0.f};
+    case SLHIP_UN_SELU: return {n.f("alpha", 1.67326319217681884765625f), n.f("gamma", 1.05070102214813232421875f)};
+    case SLHIP_UN_LEAKY_RELU: return {n.f("alpha", 0.01f), 0.f};
+    case SLHIP_UN_CLIP: return {n.f("min", -inf), n.f("max", inf)};
+    default: return {1.f, 0.f};
+    }
+}
+
 Support supports(const Graph& g, const Node& n)
 {
     auto no = [](const std::string& r) { return Support{false, r}; };
     auto act = [&](int id) { return is_activation(g.value(id).type); };
     const std::string& op = n.op;
-    if (op == "Add" || op == "Mul") {
+    if (kBinaryOps.count(op)) {
         if (n.in.size() != 2 || n.out.size() != 1) return no(op + " takes two inputs");
-        if (!act(n.in[0]) || !act(n.in[1]) || !act(n.out[0])) return no(op + ": activation types only");
-        if (g.value(n.in[0]).dims != g.value(n.in[1]).dims) return no(op + ": broadcasting is not supported");
+        if (!act(n.in[0]) || !act(n.in[1]) || !act(n.out[0])) return no(op + ": f32, f16 or bf16 operands");
+        const DType ta = g.value(n.in[0]).type, tb = g.value(n.in[1]).type;
+        const bool swap = ta == DType::F32 && tb != DType::F32 && kCommutative.count(kBinaryOps.at(op));
+        if (tb != ta && tb != DType::F32 && !swap) return no(op + ": b must have a's type or be f32");
+        std::vector<int64_t> bd;
+        if (!broadcast_dims(g.value(n.in[0]).dims, g.value(n.in[1]).dims, bd)) return no(op + ": shapes do not broadcast");
+        if (bd != g.value(n.out[0]).dims) return no(op + ": output shape is not the broadcast shape");
+        if (bd.size() > 8) return no(op + ": rank above 8");
         return {true, ""};
     }
-    if (kActs.count(op)) {
-        if (n.in.size() != 1 || n.out.size() != 1 || !act(n.in[0])) return no(op + " takes one activation");
+    if (kUnaryOps.count(op)) {
+        if (n.in.size() != 1 || n.out.size() != 1 || !act(n.in[0]) || !act(n.out[0])) return no(op + " takes one activation");
+        if (g.value(n.in[0]).dims != g.value(n.out[0]).dims) return no(op + ": output shape differs from the input's");
         return {true, ""};
     }
     if (op == "RmsNorm" || op == "L2Norm" || op == "LayerNorm") {
@@ -376,6 +448,7 @@ Support supports(const Graph& g, const Node& n)
         if (dense && (K % 8 != 0 || K > 16384)) return no("MatMul: K must be a multiple of 8 and at most 16384");
         if (blocks && (K % 256 != 0 || K > 16384)) return no("MatMul: block-format K must be a multiple of 256, at most 16384");
         if (w.type == DType::Q6_K && K % 2048 != 0) return no("MatMul: Q6_K rows need K a multiple of 2048 (16-byte rows)");
+        if (!matvec_fits(format_code(w.type), K, false)) return no("MatMul: the weight rows do not fit the matvec's LDS staging");
         return {true, ""};
     }
     return no("op " + op + " is not on the fused-layer-op path of the HIP provider");
@@ -384,7 +457,7 @@ Support supports(const Graph& g, const Node& n)
 // ---- lowering into fused units -------------------------------------------------------------------------
 
 struct Unit {
-    enum Kind { RowNorm, Gated, Rope, Gather, Cast, CacheWrite, Matvec } kind;
+    enum Kind { RowNorm, Gated, Rope, Gather, Cast, CacheWrite, Matvec, Binary, Unary } kind;
     std::string label;
     // RowNorm
     int norm = SLHIP_NORM_RMS;
@@ -408,11 +481,15 @@ struct Unit {
     int table = -1, ids = -1;
     // CacheWrite (standalone): x into the state y
     int cache_node = -1;
+    // Binary: y = op(x, up) with broadcasting; Unary: y = op(x) with parameters p0, p1
+    int op = 0;
+    float p0 = 0.f, p1 = 0.f;
 };
 
 class Segment {
 public:
-    Segment(Graph g, int64_t max_tokens) : g_(std::move(g)), max_t_(max_tokens)
+    // plan_only: lower the nodes into launches and stop (no stream, no device memory).
+    Segment(Graph g, int64_t max_tokens, bool plan_only = false) : g_(std::move(g)), max_t_(max_tokens)
     {
         if (max_t_ < 0) invalid("MaxTokens must not be negative");
         for (const Node& n : g_.nodes) {
@@ -420,6 +497,7 @@ public:
             if (!s.ok) unsupported(s.reason);
         }
         lower();
+        if (plan_only) return;
         check(slhip_stream_create(&stream_));
         allocate();
         reset_state();
@@ -533,7 +611,9 @@ private:
             const Node& n = g_.nodes[k];
             if (n.op == "Add" && k + 1 < N && !done[k + 1]) {
                 const Node& m = g_.nodes[k + 1];
-                if ((m.op == "RmsNorm" || m.op == "L2Norm") && m.in[0] == n.out[0]) {
+                const auto& od = g_.value(n.out[0]).dims;
+                if ((m.op == "RmsNorm" || m.op == "L2Norm") && m.in[0] == n.out[0] && g_.value(n.in[0]).dims == od &&
+                    g_.value(n.in[1]).dims == od) {
                     Unit u = rownorm_unit(m);
                     u.x = n.in[0];
                     u.res = n.in[1];
@@ -570,7 +650,12 @@ private:
             if (kActs.count(n.op) && single_use(n.out[0])) {
                 const int mk = cons[n.out[0]][0];
                 const Node& m = g_.nodes[mk];
-                if (m.op == "Mul" && !done[mk]) {
+                const int up = m.in.size() == 2 ? (m.in[0] == n.out[0] ? m.in[1] : m.in[0]) : -1;
+                // The unit is emitted here, at the activation, so `up` must already exist: made by an earlier
+                // node (or an input). Same shapes only: a broadcast Mul runs as its own launch.
+                const bool ready = up >= 0 && producer_before(up, static_cast<int>(k));
+                if (m.op == "Mul" && !done[mk] && ready && g_.value(up).dims == g_.value(n.in[0]).dims &&
+                    g_.value(m.out[0]).dims == g_.value(n.in[0]).dims) {
                     Unit u{Unit::Gated};
                     u.act = n.op == "Silu" ? SLHIP_ACT_SILU : n.op == "GeluTanh" ? SLHIP_ACT_GELU_TANH : SLHIP_ACT_GELU_ERF;
                     u.gate = n.in[0];
@@ -645,15 +730,63 @@ private:
                 u.cache_node = static_cast<int>(k);
                 u.label = "CacheWrite";
                 units_.push_back(u);
+            } else if (kBinaryOps.count(n.op)) {
+                Unit u{Unit::Binary};
+                u.op = kBinaryOps.at(n.op);
+                if (u.op == SLHIP_BIN_MOD && (n.s("fmod", "false") == "true" || n.s("fmod", "0") == "1")) u.op = SLHIP_BIN_FMOD;
+                u.x = n.in[0];
+                u.up = n.in[1];
+                if (g_.value(u.x).type == DType::F32 && g_.value(u.up).type != DType::F32) std::swap(u.x, u.up);  // commutative
+                u.y = n.out[0];
+                u.label = n.op;
+                units_.push_back(u);
+            } else if (kUnaryOps.count(n.op)) {
+                Unit u{Unit::Unary};
+                u.op = kUnaryOps.at(n.op);
+                std::tie(u.p0, u.p1) = unary_params(u.op, n);
+                u.x = n.in[0];
+                u.y = n.out[0];
+                u.label = n.op;
+                units_.push_back(u);
             } else {
-                unsupported("standalone " + n.op + ": the HIP provider runs " + n.op +
-                            " only fused (Add into a following RmsNorm/L2Norm, an activation into its Mul)");
+                unsupported("op " + n.op + " has no lowering on the HIP provider");
             }
         }
         merge_ropes();
     }
 
     std::map<int, int> absorbed_norm_;  // rope node -> RmsNorm node computed inside it
+
+    // Whether value `id` is a segment input/weight/state or is produced by a node before node k.
+    bool producer_before(int id, int k) const
+    {
+        for (int j = 0; j < static_cast<int>(g_.nodes.size()); j++)
+            for (int o : g_.nodes[j].out)
+                if (o == id) return j < k;
+        return true;
+    }
+
+    std::vector<int64_t> dims_at(int id, int64_t T) const
+    {
+        std::vector<int64_t> d = g_.value(id).dims;
+        for (auto& x : d)
+            if (x == kSymT) x = T;
+        return d;
+    }
+
+    // BinaryOp.Align (src/Sharplight.Cpu/BinaryOp.cs:37-58) for a dense operand: its strides against y's rank,
+    // 0 along a dim it lacks or holds once.
+    static std::vector<int64_t> align(const std::vector<int64_t>& d, size_t rank)
+    {
+        std::vector<int64_t> s(rank, 0);
+        int64_t acc = 1;
+        for (size_t i = d.size(); i-- > 0;) {
+            const size_t k = i + (rank - d.size());
+            s[k] = d[i] == 1 ? 0 : acc;
+            acc *= d[i];
+        }
+        return s;
+    }
 
     // Gate/up matmul pairs sharing x that feed act(gate) * up (FoldDualMatMuls,
     // src/Sharplight.Shaders/Lowering/GraphLowerer.Fusion.cs:286-353): both products read only by the
@@ -685,6 +818,7 @@ private:
                 const Value& wu = g_.value(mu.in[1]);
                 if (mg.in[0] != mu.in[0] || wg.type != wu.type || wg.dims != wu.dims) continue;
                 if (!single_use(mg.out[0]) || !single_use(mu.out[0]) || !single_use(g_.nodes[a].out[0])) continue;
+                if (!matvec_fits(format_code(wg.type), wg.dims[1], true)) continue;  // two matvecs + the gated unit
                 if (g_.value(mg.out[0]).type != DType::F32 || g_.value(mu.out[0]).type != DType::F32 ||
                     g_.value(g_.nodes[a].out[0]).type != DType::F32)
                     continue;  // the unfused graph rounds nothing between the products and the Mul
@@ -908,6 +1042,21 @@ private:
             check(slhip_convert(act_code(x.type), act_code(g_.value(u.y).type), ptr(u.x), ptr(u.y), x.elems(T), stream_));
             break;
         }
+        case Unit::Binary: {
+            const std::vector<int64_t> yd = dims_at(u.y, T);
+            const std::vector<int64_t> sa = align(dims_at(u.x, T), yd.size()), sb = align(dims_at(u.up, T), yd.size());
+            check(slhip_binary(u.op, act_code(g_.value(u.x).type), act_code(g_.value(u.up).type), act_code(g_.value(u.y).type),
+                               ptr(u.x), sa.data(), ptr(u.up), sb.data(), ptr(u.y), yd.data(), static_cast<int>(yd.size()),
+                               stream_));
+            break;
+        }
+        case Unit::Unary: {
+            const Value& x = g_.value(u.x);
+            const int64_t cols = x.last(), rows = x.rows(T);
+            check(slhip_unary(u.op, act_code(x.type), act_code(g_.value(u.y).type), ptr(u.x), ptr(u.y), rows, cols, cols, cols,
+                              u.p0, u.p1, stream_));
+            break;
+        }
         case Unit::CacheWrite: {
             const Value& x = g_.value(u.x);
             const Value& st = g_.value(u.y);
@@ -987,6 +1136,15 @@ SLHIP_API int slhip_segment_compile(const char* segment_ir, int64_t max_tokens, 
         *segment = nullptr;
         auto s = std::make_unique<Segment>(parse(segment_ir), max_tokens);
         *segment = s.release();
+    });
+}
+
+SLHIP_API int slhip_segment_plan(const char* segment_ir, char* buf, size_t size)
+{
+    return guarded([&] {
+        if (!buf || !size) invalid("null argument");
+        Segment s(parse(segment_ir), 0, true);
+        snprintf(buf, size, "%s", s.launches().c_str());
     });
 }
 

@@ -34,6 +34,15 @@ NORM_RMS, NORM_L2, NORM_LAYER = 0, 1, 2
 NORMS = {"rms": NORM_RMS, "l2": NORM_L2, "layer": NORM_LAYER}
 ACT_SILU, ACT_GELU_TANH, ACT_GELU_ERF = 0, 1, 2
 ACTS = {"silu": ACT_SILU, "gelu_tanh": ACT_GELU_TANH, "gelu_erf": ACT_GELU_ERF}
+# slhip_unary_op / slhip_binary_op: the reference's UnaryKind and BinaryKind order, by StandardOps name
+UNARY_OPS = {n: i for i, n in enumerate(
+    ["Neg", "Exp", "Log", "Sqrt", "Rsqrt", "Sigmoid", "Silu", "Gelu", "GeluTanh", "Tanh", "Softplus", "Relu", "Abs",
+     "Square", "Recip", "Scale", "Erf", "HardSwish", "HardSigmoid", "Clip", "Sin", "Cos", "Tan", "Asin", "Acos",
+     "Atan", "Sinh", "Cosh", "Asinh", "Acosh", "Atanh", "Floor", "Ceil", "Round", "Sign", "Softsign", "Mish", "Elu",
+     "Celu", "Selu", "LeakyRelu", "ThresholdedRelu", "Not", "IsNaN", "IsInf"])}
+BINARY_OPS = {n: i for i, n in enumerate(
+    ["Add", "Sub", "Mul", "Div", "Max", "Min", "Pow", "Mod", "PRelu", "Equal", "NotEqual", "Less", "LessEqual",
+     "Greater", "GreaterEqual", "And", "Or", "Xor", "Atan2", "FMod"])}
 
 
 class SlhipError(RuntimeError):
@@ -170,6 +179,8 @@ SIGNATURES = {
     "slhip_rope": (_I, [_I, _I, ctypes.POINTER(RopeTensor), _I, _P, _P, _I64, _I64, ctypes.POINTER(RopeCfg), _P]),
     "slhip_gather": (_I, [_I, _P, _I64, _I64, _P, _I64, _I, _P, _I64, _P]),
     "slhip_convert": (_I, [_I, _I, _P, _P, _I64, _P]),
+    "slhip_binary": (_I, [_I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _I, _P]),
+    "slhip_unary": (_I, [_I, _I, _I, _P, _P, _I64, _I64, _I64, _I64, _F, _F, _P]),
     "slhip_cache_write": (_I, [_I, _I, _P, _I64, _I64, _I64, _P, ctypes.POINTER(CacheRows), _P]),
     "slhip_provider_check": (_I, [ctypes.c_char_p, _SZ]),
     "slhip_node_supports": (_I, [ctypes.c_char_p, _I, ctypes.POINTER(_I), ctypes.c_char_p, _SZ]),
@@ -181,6 +192,7 @@ SIGNATURES = {
     "slhip_segment_set_scalar": (_I, [_P, ctypes.c_char_p, _I64]),
     "slhip_segment_device_bytes": (_I, [_P, ctypes.POINTER(_I64)]),
     "slhip_segment_launches": (_I, [_P, ctypes.c_char_p, _SZ]),
+    "slhip_segment_plan": (_I, [ctypes.c_char_p, ctypes.c_char_p, _SZ]),
     "slhip_segment_destroy": (_I, [_P]),
     "slhip_gguf_open": (_I, [ctypes.c_char_p, ctypes.POINTER(_P)]),
     "slhip_gguf_open_prefix": (_I, [_P, _SZ, ctypes.POINTER(_P)]),
@@ -429,6 +441,23 @@ def gated_act(act, dtype_in, dtype_out, gate, up, out, rows, cols, *, gate_strid
     call("slhip_gated_act", ACTS.get(act, act), DTYPES.get(dtype_in, dtype_in), DTYPES.get(dtype_out, dtype_out),
          ptr(gate), ptr(up), ptr(out), rows, cols, cols if gate_stride is None else gate_stride,
          cols if up_stride is None else up_stride, cols if out_stride is None else out_stride, stream)
+
+
+def binary(op, dtype_a, dtype_b, dtype_out, a, b, y, dims, *, a_strides=None, b_strides=None, stream=None):
+    """y [dims] = op(a, b); a_strides / b_strides: element strides aligned to y's rank (0 where broadcast),
+    None for dense [dims]."""
+    rank = len(dims)
+    arr = lambda v: None if v is None else (_I64 * max(rank, 1))(*v) if rank else (_I64 * 1)(0)
+    call("slhip_binary", BINARY_OPS.get(op, op), DTYPES.get(dtype_a, dtype_a), DTYPES.get(dtype_b, dtype_b),
+         DTYPES.get(dtype_out, dtype_out), ptr(a), arr(a_strides), ptr(b), arr(b_strides), ptr(y),
+         (_I64 * max(rank, 1))(*dims) if rank else None, rank, stream)
+
+
+def unary(op, dtype_in, dtype_out, x, y, rows, cols, *, x_stride=None, y_stride=None, p0=1.0, p1=0.0, stream=None):
+    """y [rows, cols] = op(x) with the reference's two unary parameters p0, p1."""
+    call("slhip_unary", UNARY_OPS.get(op, op), DTYPES.get(dtype_in, dtype_in), DTYPES.get(dtype_out, dtype_out),
+         ptr(x), ptr(y), rows, cols, cols if x_stride is None else x_stride, cols if y_stride is None else y_stride,
+         p0, p1, stream)
 
 
 def rope(dtype_in, dtype_out, tensors, pos, T, D, *, dims=0, neox=True, base=10000.0, freq_scale=1.0,

@@ -97,11 +97,24 @@ class GraphBuilder:
         return y
 
     # the ops on this path (StandardOps names)
+    def binary(self, op, a, b, out_type=None, **attrs):
+        """A StandardOps binary op with numpy broadcasting (the symbolic "T" broadcasts against T or 1)."""
+        return self.emit(op, [a, b], out_type or a.type, broadcast(a.dims, b.dims), **attrs)
+
+    def unary(self, op, x, out_type=None, **attrs):
+        return self.emit(op, [x], out_type or x.type, x.dims, **attrs)
+
     def add(self, a, b):
-        return self.emit("Add", [a, b], a.type, a.dims)
+        return self.binary("Add", a, b)
 
     def mul(self, a, b):
-        return self.emit("Mul", [a, b], a.type, a.dims)
+        return self.binary("Mul", a, b)
+
+    def scale(self, x, scale=1.0, bias=0.0):
+        return self.unary("Scale", x, scale=scale, bias=bias)
+
+    def clip(self, x, min=float("-inf"), max=float("inf")):
+        return self.unary("Clip", x, min=min, max=max)
 
     def silu(self, x):
         return self.emit("Silu", [x], x.type, x.dims)
@@ -166,6 +179,29 @@ class GraphBuilder:
             lines.append(f"node {n.op} {','.join(str(v.id) for v in n.inputs) or '-'} -> "
                          f"{','.join(str(v.id) for v in n.outputs) or '-'} {attrs}".rstrip())
         return "\n".join(lines) + "\n"
+
+
+def broadcast(a: tuple, b: tuple) -> tuple:
+    """numpy broadcasting of two dim tuples whose entries are ints or "T"."""
+    r = max(len(a), len(b))
+    a = (1,) * (r - len(a)) + tuple(a)
+    b = (1,) * (r - len(b)) + tuple(b)
+    out = []
+    for x, y in zip(a, b):
+        if x == y or y == 1:
+            out.append(x)
+        elif x == 1:
+            out.append(y)
+        else:
+            raise ValueError(f"shapes {a} and {b} do not broadcast")
+    return tuple(out)
+
+
+def plan(graph: "GraphBuilder") -> list[str]:
+    """The launches compile() would create for ``graph``, decided without a device (slhip_segment_plan)."""
+    buf = ctypes.create_string_buffer(8192)
+    native.call("slhip_segment_plan", graph.to_ir().encode(), buf, len(buf))
+    return [s for s in buf.value.decode().split("\n") if s]
 
 
 def _fmt(v) -> str:

@@ -78,11 +78,11 @@ def assert_f32_close(got, ref, rtol=F32_RTOL, atol_row=F32_ATOL_ROW, what: str =
     assert got.shape == ref.shape, (got.shape, ref.shape)
     if ref.size == 0:
         return 0.0
-    r2 = ref.reshape(-1, ref.shape[-1]).astype(np.float64)
+    r2 = (ref.reshape(-1, ref.shape[-1]) if ref.ndim else ref.reshape(1, 1)).astype(np.float64)
     rms = np.sqrt(np.mean(r2 * r2, axis=1, keepdims=True))
     atol = atol_row * np.broadcast_to(rms, r2.shape).reshape(ref.shape)
     d = np.abs(got.astype(np.float64) - ref.astype(np.float64))
-    bad = ~(d <= atol + rtol * np.abs(ref.astype(np.float64)))
+    bad = ~(d <= atol + rtol * np.abs(ref.astype(np.float64))) & ~(got == ref)  # equal infinities match
     if bad.any():
         i = np.unravel_index(np.argmax(bad), bad.shape)
         raise AssertionError(f"{what}: {int(bad.sum())} of {bad.size} f32 values out of tolerance; first at {i}: "

@@ -382,3 +382,33 @@ def test_cache_write_needs_its_scalar(dev):
         seg.set_scalar("n_past", 15)
         with pytest.raises(native.SlhipCacheError, match=r"n_past 15 \+ T 2 > context 16"):
             seg.execute(2)
+
+
+def test_standalone_elementwise_graph(dev):
+    """A bias add over bf16 rows (f32 bias), a scalar Mul, a lone Silu and a Scale in one segment, each its
+    own launch, against the oracle's BinaryOp/UnaryOp on the same widened values."""
+    T, D = 19, 1000
+    g = GraphBuilder()
+    x = g.input("bf16", "T", D)
+    bias = g.weight("f32", D)
+    s = g.weight("f32", 1)
+    h = g.add(x, bias)
+    m = g.mul(h, s)
+    a = g.output(g.silu(m))
+    z = g.output(g.scale(a, scale=0.5, bias=-1.0))
+    xs = oracle.to_bf16(synth.normal(5, 0, (T, D), std=2.0))
+    bs = synth.normal(5, 1, (D,))
+    ss = np.array([1.75], np.float32)
+    with dev.compile(g, max_tokens=32) as seg:
+        assert seg.launches == ["Add", "Mul", "Silu", "Scale"]
+        seg.set_input(x, xs)
+        seg.set_input(bias, bs)
+        seg.set_input(s, ss)
+        log("provider standalone elementwise")
+        seg.execute(T)
+        h32 = oracle.from_bf16(oracle.to_bf16(oracle.binary("Add", oracle.from_bf16(xs), bs)))
+        m32 = oracle.from_bf16(oracle.to_bf16(oracle.binary("Mul", h32, ss)))
+        a16 = oracle.to_bf16(oracle.unary_kind("Silu", m32))
+        assert_bf16_close(seg.get_output(a), a16, what="silu")
+        z16 = oracle.to_bf16(oracle.unary_kind("Scale", oracle.from_bf16(seg.get_output(a)).ravel(), 0.5, -1.0))
+        assert_bf16_close(seg.get_output(z), z16.reshape(T, D), ulp=0, what="scale")

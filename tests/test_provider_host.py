@@ -5,7 +5,7 @@ import ctypes
 import pytest
 
 from sharplight_amd import native
-from sharplight_amd.provider import GraphBuilder, HipExecutionProvider
+from sharplight_amd.provider import GraphBuilder, HipExecutionProvider, plan
 
 
 def _supports(g: GraphBuilder, k: int):
@@ -44,7 +44,7 @@ def test_supports_answers():
     w16 = g.weight("f16", 64)
     g.rms_norm(x, w16)                       # 0: f16 norm weight -> no (f32 weights only)
     g.rope(x, pos)                           # 1: yes
-    g.emit("MatMul", [x, x], "f32", ("T", 4, 64))  # 2: not on this path
+    g.emit("Softmax", [x], "f32", ("T", 4, 64))  # 2: not on this path
     xh = g.input("f16", "T", 64)
     g.rms_norm(xh)                           # 3: f16 rows -> no
     tbl = g.weight("q8_0", 100, 64)
@@ -60,13 +60,84 @@ def test_supports_answers():
         assert ok or why
 
 
-def test_standalone_elementwise_is_rejected_at_compile():
+def test_standalone_elementwise_lowers_to_its_own_launch():
+    """An Add with nothing to fuse into, a bias add, a scalar Mul and a lone Silu each become one elementwise
+    launch of the same segment (no split to the CPU)."""
     g = GraphBuilder()
     a = g.input("f32", "T", 64)
     b = g.input("f32", "T", 64)
-    g.output(g.add(a, b))  # no norm follows: nothing to fuse it into
-    st, msg = _compile_error(g)
-    assert st == native.ERR_UNSUPPORTED and "standalone Add" in msg
+    bias = g.weight("f32", 64)
+    s = g.weight("f32", 1)
+    y = g.add(g.add(a, b), bias)
+    y = g.mul(y, s)
+    g.output(g.silu(y))
+    assert plan(g) == ["Add", "Add", "Mul", "Silu"]
+    for k in range(4):
+        assert _supports(g, k)[0]
+
+
+def test_broadcast_support_answers():
+    g = GraphBuilder()
+    x = g.input("bf16", "T", 8, 64)
+    g.binary("Add", x, g.weight("f32", 64))             # 0: bf16 + f32 bias -> yes
+    g.binary("Mul", g.weight("f32", 64), x)             # 1: f32 * bf16 commutes -> yes
+    g.binary("Sub", g.weight("f32", 64), x, "bf16")      # 2: f32 - bf16 does not commute -> no
+    g.emit("Add", [x, g.input("f32", "T", 7, 64)], "bf16", ("T", 8, 64))  # 3: 8 vs 7 -> no
+    g.emit("Add", [x, g.input("bf16", 5, 8, 64)], "bf16", ("T", 8, 64))   # 4: T vs 5 -> no
+    g.unary("Scale", x, scale=2.0, bias=1.0)            # 5: yes
+    g.unary("Clip", x, min=-1.0, max=1.0)               # 6: yes
+    g.emit("Relu", [x], "bf16", ("T", 64))              # 7: output shape differs -> no
+    expect = [True, True, False, False, False, True, True, False]
+    for k, e in enumerate(expect):
+        ok, why = _supports(g, k)
+        assert ok == e, (k, why)
+
+
+def test_gated_unit_waits_for_up():
+    """Gate MatMul (bf16 out: no dual matvec) -> Silu -> up MatMul -> Mul: the activation comes before up's
+    producer, so act and Mul must not be fused at the activation (it would read up before it is written)."""
+    g = GraphBuilder()
+    x = g.input("bf16", "T", 256)
+    wg = g.weight("bf16", 512, 256)
+    wu = g.weight("bf16", 512, 256)
+    gate = g.matmul(x, wg, out_type="bf16")
+    act = g.silu(gate)
+    up = g.matmul(x, wu, out_type="bf16")
+    g.output(g.mul(act, up))
+    assert plan(g) == ["matvec", "Silu", "matvec", "Mul"]
+    # the usual order (both products first) still fuses
+    g2 = GraphBuilder()
+    x = g2.input("bf16", "T", 256)
+    gate = g2.matmul(x, g2.weight("bf16", 512, 256), out_type="bf16")
+    up = g2.matmul(x, g2.weight("bf16", 512, 256), out_type="bf16")
+    g2.output(g2.mul(g2.silu(gate), up))
+    assert plan(g2) == ["matvec", "matvec", "fused[Silu,Mul]"]
+
+
+def test_dual_matvec_falls_back_when_rows_do_not_fit_lds():
+    """A Q8_0 gate/up pair at K = 16384 does not fit the dual kernel's LDS staging: two matvecs plus the
+    gated unit instead (a single Q8_0 matvec at that K fits)."""
+    def build(K):
+        g = GraphBuilder()
+        x = g.input("f32", "T", K)
+        gate = g.matmul(x, g.weight("q8_0", 256, K))
+        up = g.matmul(x, g.weight("q8_0", 256, K))
+        g.output(g.mul(g.silu(gate), up))
+        return g
+    assert plan(build(4096)) == ["matvec2+fused[Silu,Mul]"]
+    assert plan(build(16384)) == ["matvec", "matvec", "fused[Silu,Mul]"]
+
+
+def test_residual_add_with_broadcast_is_not_fused_into_the_norm():
+    g = GraphBuilder()
+    x = g.input("f32", "T", 64)
+    b = g.weight("f32", 64)
+    g.output(g.rms_norm(g.add(x, b), g.weight("f32", 64)))
+    assert plan(g) == ["Add", "RmsNorm"]
+    g = GraphBuilder()
+    x = g.input("f32", "T", 64)
+    g.output(g.rms_norm(g.add(x, g.input("f32", "T", 64)), g.weight("f32", 64)))
+    assert plan(g) == ["fused[Add]+RmsNorm"]
 
 
 def test_unsupported_node_is_rejected_at_compile():
