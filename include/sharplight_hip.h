@@ -38,7 +38,7 @@ extern "C" {
 #define SLHIP_API __attribute__((visibility("default")))
 #endif
 
-#define SLHIP_ABI_VERSION 4
+#define SLHIP_ABI_VERSION 5
 
 typedef enum slhip_status {
     SLHIP_OK = 0,
@@ -304,7 +304,19 @@ typedef struct slhip_rope_cfg {
     float attn_factor; /* multiplies cos and sin */
     int32_t norm;      /* 1: per-head RMSNorm (norm_w, eps) before the rotation */
     float eps;
-    int32_t reserved;
+    int32_t pos_axes;  /* A: positions are int32 [T, A], 1..4 (0 means 1) */
+    /* Multi-axis rope (M-RoPE; StandardOps.Rope's sections / interleaved / sections_per_element,
+     * src/Sharplight.Core/Graph/StandardOps.cs:182-192; RopeOp.AxisOf, src/Sharplight.Cpu/RopeOp.cs:54-106):
+     * pair section i takes position axis
+     *   sector = i % (s0+s1+s2+s3); sectioned: 0 below s0, 1 below s0+s1, 2 below s0+s1+s2, else 3;
+     *   interleaved: 1 if sector % 3 == 1 and sector < 3*s1, 2 if % 3 == 2 and < 3*s2, 0 if % 3 == 0 and
+     *   < 3*s0, else 3;
+     * with per_element the elements are sectioned two by two (element e takes pair section e/2), so the two
+     * elements of a neox pair may rotate by different axes' angles: y0 = x0*c1 - x1*s1, y1 = x0*s2 + x1*c2.
+     * An axis beyond A reads axis 0 when A == 1, else position 0. All of s0..s2 zero: one axis. */
+    int32_t sections[4];
+    int32_t interleaved;
+    int32_t per_element;
 } slhip_rope_cfg;
 
 /*
@@ -313,11 +325,11 @@ typedef struct slhip_rope_cfg {
  *   inv_i = base^(-2i/dims) * freq_scale (f64); theta = pos[t] * inv_i (/ ff[i]) (f64);
  *   c = (float)cos(theta) * attn_factor, s = (float)sin(theta) * attn_factor;
  *   y0 = x0*c - x1*s, y1 = x0*s + x1*c.
- * pos: int32 [T]; ff: f32 [dims/2] frequency divisors or NULL. dtype_in: F32 or BF16; dtype_out: F32, F16
+ * pos: int32 [T, cfg->pos_axes]; ff: f32 [dims/2] frequency divisors or NULL. dtype_in: F32 or BF16; dtype_out: F32, F16
  * (for f16 caches) or BF16.
  * Replaces: RopeOp (src/Sharplight.Cpu/RopeOp.cs:28-183) after RowOp RmsNorm, and the Vulkan rope kernels
- * with the absorbed norm (GraphLowerer.Fusion.cs:618-630, GraphLowerer.Transformer.cs:40, Kernels/rope.slang:150-195)
- * for the single-axis styles.
+ * with the absorbed norm (GraphLowerer.Fusion.cs:618-630, GraphLowerer.Transformer.cs:40, Kernels/rope.slang:5-30,150-195),
+ * single-axis and multi-axis.
  */
 SLHIP_API int slhip_rope(int dtype_in, int dtype_out, const slhip_rope_tensor* tensors, int n_tensors,
                          const int32_t* pos, const float* ff, int64_t T, int64_t D, const slhip_rope_cfg* cfg,
@@ -416,8 +428,9 @@ SLHIP_API int slhip_unary(int op, int dtype_in, int dtype_out, const void* x, vo
  *   Atan2 (numpy broadcasting), the one-operand ops of slhip_unary_op by name, Scale (scale, bias), Clip
  *   (min, max), HardSigmoid (alpha, beta), Elu/Celu/LeakyRelu/ThresholdedRelu (alpha), Selu (alpha, gamma),
  *   RmsNorm (x[, w]; eps), L2Norm (x; eps),
- *   LayerNorm (x[, w[, b]]; eps), Rope (x [T,H,D], pos i32 [T][, ff]; dims, base, style=neox|normal|gptj,
- *   freq_scale, attn_factor), Gather (table [V, D...], ids i32 [N]), Cast,
+ *   LayerNorm (x[, w[, b]]; eps), Rope (x [T,H,D], pos i32 [T] or [T,A<=4][, ff]; dims, base,
+ *   style=neox|normal|gptj, freq_scale, attn_factor, sections=s0,s1,s2,s3, interleaved, sections_per_element),
+ *   Gather (table [V, D...], ids i32 [N]), Cast,
  *   CacheWrite (state [ctx, ...], x [T, ...][, rows i32 [T,4][, pages i32 [slots, blocks]]]; offset=<scalar
  *   name, default n_past>, slots, block_size): rows n_past + t, or the multi-sequence / paged rows.
  * Compile applies the reference lowerer's fusions (Add+RmsNorm, act+Mul, RmsNorm inside Rope, a Rope whose

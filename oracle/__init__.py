@@ -74,6 +74,8 @@ def _declare(L):
         "orc_align": (None, [_P, _I, _I, _P]),
         "orc_erf_rational": (_F, [_F]),
         "orc_rope": (None, [_P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _F, _F, _F]),
+        "orc_rope_multi": (None, [_P, _P, _I, _P, _I, _I, _P, _P, _I64, _I64, _I64, _I, _I, _F, _F, _F]),
+        "orc_rope_axis_of": (_I, [_I, _P, _I]),
         "orc_row_bytes": (_I64, [_I, _I64]),
         "orc_dequant": (_I, [_I, _P, _I64, _P]),
         "orc_gather": (_I, [_I, _P, _I64, _I64, _P, _I64, _P, ctypes.POINTER(_I64)]),
@@ -253,6 +255,26 @@ def rope(x, pos, dims=None, neox=True, base=10000.0, freq_scale=1.0, attn_factor
     fn = lib().orc_rope_mt if threads else lib().orc_rope
     fn(_p(x), _p(pos), _p(ff), _p(y), T, H, D, dims, int(bool(neox)), base, freq_scale, attn_factor)
     return y
+
+
+def rope_multi(x, pos, sections=None, interleaved=False, per_element=False, dims=None, neox=True, base=10000.0,
+               freq_scale=1.0, attn_factor=1.0, ff=None):
+    """Multi-axis RopeOp: x [T, H, D] f32, positions int32 [T, A] (A <= 4), sections of 4 entries or None."""
+    x = _c(x, np.float32)
+    T, H, D = x.shape
+    pos = _c(pos, np.int32).reshape(T, -1)
+    sec = None if sections is None else _c(sections, np.int32)
+    ff = _c(ff, np.float32)
+    dims = D if not dims else dims
+    y = np.empty_like(x)
+    lib().orc_rope_multi(_p(x), _p(pos), pos.shape[1], _p(sec), int(bool(interleaved)), int(bool(per_element)),
+                         _p(ff), _p(y), T, H, D, dims, int(bool(neox)), base, freq_scale, attn_factor)
+    return y
+
+
+def rope_axis_of(i, sections, interleaved=False):
+    sec = _c(sections, np.int32)
+    return int(lib().orc_rope_axis_of(i, _p(sec), int(bool(interleaved))))
 
 
 def row_bytes(fmt, d):

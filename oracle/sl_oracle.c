@@ -510,24 +510,58 @@ void orc_binary(int k, const float* a, const int64_t* sa, const float* b, const 
 /* rope                                                                                       */
 /* ------------------------------------------------------------------------------------------ */
 
-/* RopeOp (src/Sharplight.Cpu/RopeOp.cs): inverse frequencies in f64 (ctor, :47-52), per token
- * theta = pos * invFreq (/ ff[i]) in f64, cos/sin narrowed to f32 then times attn_factor
- * (:133-150); neox pairs (i, i+half), normal pairs (2i, 2i+1) (:151-176); elements from dims to
- * D are copied (:177-180). Single position axis. */
-static void rope_tokens(const float* x, const int32_t* pos, const float* ff, float* y, int64_t t0, int64_t t1,
-                        int64_t H, int64_t D, int dims, int neox, float base, float freq_scale, float attn_factor)
+/* RopeOp.AxisOf (src/Sharplight.Cpu/RopeOp.cs:70-106): the position axis of pair section i under llama.cpp's
+ * M-RoPE sector rules; 0 without sections (all of sections[0..2] zero). */
+int orc_rope_axis_of(int i, const int32_t* sec, int interleaved)
+{
+    if (!sec || !(sec[0] > 0 || sec[1] > 0 || sec[2] > 0)) return 0;
+    int sect_dims = sec[0] + sec[1] + sec[2] + sec[3];
+    int sector = i % sect_dims;
+    if (interleaved) {
+        if (sector % 3 == 1 && sector < 3 * sec[1]) return 1;
+        if (sector % 3 == 2 && sector < 3 * sec[2]) return 2;
+        return sector % 3 == 0 && sector < 3 * sec[0] ? 0 : 3;
+    }
+    if (sector < sec[0]) return 0;
+    if (sector < sec[0] + sec[1]) return 1;
+    return sector < sec[0] + sec[1] + sec[2] ? 2 : 3;
+}
+
+/* RopeOp (src/Sharplight.Cpu/RopeOp.cs): inverse frequencies in f64 (ctor, :47-52); per pair the axes of its
+ * first and second element (:54-66: with per-element sections element e takes the axis of pair section e/2);
+ * per token the positions of 4 axes, a missing axis taking axis 0 when there is one axis, else 0 (:133-139);
+ * theta = pos[axis] * invFreq (/ ff[i]) in f64, cos/sin narrowed to f32 then times attn_factor (:141-154);
+ * neox pairs (i, i+half), normal pairs (2i, 2i+1): y0 = x0*c1 - x1*s1, y1 = x0*s2 + x1*c2 (:155-176);
+ * elements from dims to D are copied (:177-180). pos [T, axes] dense. */
+static void rope_tokens(const float* x, const int32_t* pos, int axes, const int32_t* sec, int interleaved,
+                        int per_element, const float* ff, float* y, int64_t t0, int64_t t1, int64_t H, int64_t D,
+                        int dims, int neox, float base, float freq_scale, float attn_factor)
 {
     int half = dims / 2;
-    double* inv = (double*)malloc(sizeof(double) * (size_t)(half > 0 ? half : 1));
-    float* cs = (float*)malloc(sizeof(float) * (size_t)(half > 0 ? half : 1) * 2);
-    for (int i = 0; i < half; i++) inv[i] = pow((double)base, -2.0 * i / dims) * (double)freq_scale;
+    size_t hn = (size_t)(half > 0 ? half : 1);
+    double* inv = (double*)malloc(sizeof(double) * hn);
+    float* cs = (float*)malloc(sizeof(float) * hn * 4);
+    int* ax1 = (int*)malloc(sizeof(int) * hn);
+    int* ax2 = (int*)malloc(sizeof(int) * hn);
+    for (int i = 0; i < half; i++) {
+        inv[i] = pow((double)base, -2.0 * i / dims) * (double)freq_scale;
+        int first = neox ? i : 2 * i, second = neox ? i + half : 2 * i + 1;
+        ax1[i] = orc_rope_axis_of(per_element ? first / 2 : i, sec, interleaved);
+        ax2[i] = orc_rope_axis_of(per_element ? second / 2 : i, sec, interleaved);
+    }
     for (int64_t t = t0; t < t1; t++) {
-        double p = (double)pos[t];
+        double pp[4];
+        for (int a = 0; a < 4; a++) pp[a] = a < axes ? (double)pos[t * axes + a] : (axes == 1 ? (double)pos[t * axes] : 0.0);
         for (int i = 0; i < half; i++) {
-            double theta = p * inv[i];
-            if (ff) theta /= (double)ff[i];
-            cs[2 * i] = (float)cos(theta) * attn_factor;
-            cs[2 * i + 1] = (float)sin(theta) * attn_factor;
+            double theta = pp[ax1[i]] * inv[i], theta2 = pp[ax2[i]] * inv[i];
+            if (ff) {
+                theta /= (double)ff[i];
+                theta2 /= (double)ff[i];
+            }
+            cs[4 * i] = (float)cos(theta) * attn_factor;
+            cs[4 * i + 1] = (float)sin(theta) * attn_factor;
+            cs[4 * i + 2] = (float)cos(theta2) * attn_factor;
+            cs[4 * i + 3] = (float)sin(theta2) * attn_factor;
         }
         for (int64_t h = 0; h < H; h++) {
             const float* xr = x + (t * H + h) * D;
@@ -536,21 +570,30 @@ static void rope_tokens(const float* x, const int32_t* pos, const float* ff, flo
                 int i0 = neox ? i : 2 * i;
                 int i1 = neox ? i + half : 2 * i + 1;
                 float x0 = xr[i0], x1 = xr[i1];
-                float c = cs[2 * i], s = cs[2 * i + 1];
-                yr[i0] = x0 * c - x1 * s;
-                yr[i1] = x0 * s + x1 * c;
+                yr[i0] = x0 * cs[4 * i] - x1 * cs[4 * i + 1];
+                yr[i1] = x0 * cs[4 * i + 3] + x1 * cs[4 * i + 2];
             }
             for (int64_t i = dims; i < D; i++) yr[i] = xr[i];
         }
     }
     free(inv);
     free(cs);
+    free(ax1);
+    free(ax2);
 }
 
 void orc_rope(const float* x, const int32_t* pos, const float* ff, float* y, int64_t T, int64_t H, int64_t D, int dims,
               int neox, float base, float freq_scale, float attn_factor)
 {
-    rope_tokens(x, pos, ff, y, 0, T, H, D, dims, neox, base, freq_scale, attn_factor);
+    rope_tokens(x, pos, 1, NULL, 0, 0, ff, y, 0, T, H, D, dims, neox, base, freq_scale, attn_factor);
+}
+
+void orc_rope_multi(const float* x, const int32_t* pos, int axes, const int32_t* sections, int interleaved,
+                    int per_element, const float* ff, float* y, int64_t T, int64_t H, int64_t D, int dims, int neox,
+                    float base, float freq_scale, float attn_factor)
+{
+    rope_tokens(x, pos, axes, sections, interleaved, per_element, ff, y, 0, T, H, D, dims, neox, base, freq_scale,
+                attn_factor);
 }
 
 /* ------------------------------------------------------------------------------------------ */
@@ -1286,7 +1329,7 @@ static void rope_chunk(void* v, int64_t c)
 {
     rope_ctx* r = (rope_ctx*)v;
     int64_t s = c * r->per, e = s + r->per < r->T ? s + r->per : r->T;
-    if (s < e) rope_tokens(r->x, r->pos, r->ff, r->y, s, e, r->H, r->D, r->dims, r->neox, r->base, r->fs, r->af);
+    if (s < e) rope_tokens(r->x, r->pos, 1, NULL, 0, 0, r->ff, r->y, s, e, r->H, r->D, r->dims, r->neox, r->base, r->fs, r->af);
 }
 
 /* RopeOp.Run (RopeOp.cs:108-119): chunks = min(T, Chunks(T*H*D, 16384)). */

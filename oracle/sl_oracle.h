@@ -60,6 +60,13 @@ float orc_erf_rational(float x);
 void orc_rope(const float* x, const int32_t* pos, const float* ff, float* y, int64_t T, int64_t H, int64_t D, int dims,
               int neox, float base, float freq_scale, float attn_factor);
 
+/* Multi-axis rope: pos [T, axes] (axes 1..4), sections[4] (NULL or all of [0..2] zero: one axis),
+ * interleaved (Qwen3-VL sectors), per_element (XD-RoPE: element e takes the axis of pair section e/2). */
+void orc_rope_multi(const float* x, const int32_t* pos, int axes, const int32_t* sections, int interleaved,
+                    int per_element, const float* ff, float* y, int64_t T, int64_t H, int64_t D, int dims, int neox,
+                    float base, float freq_scale, float attn_factor);
+int orc_rope_axis_of(int i, const int32_t* sections, int interleaved);
+
 /* ---- dequant / gather (Quant.cs:242-405, GatherOp.cs:22-75) ---- */
 int64_t orc_row_bytes(int fmt, int64_t d);
 int orc_dequant(int fmt, const uint8_t* src, int64_t count, float* dst);

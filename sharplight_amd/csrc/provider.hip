@@ -351,6 +351,27 @@ std::pair<float, float> unary_params(int code, const Node& n)
     }
 }
 
+// Rope's `sections` attribute: empty, or four comma-separated non-negative integers.
+bool parse_sections(const std::string& text, std::vector<int>& sec)
+{
+    sec.assign(4, 0);
+    if (text.empty()) return true;
+    std::stringstream ss(text);
+    std::string tok;
+    int k = 0;
+    while (std::getline(ss, tok, ',')) {
+        if (k == 4 || tok.empty() || tok.find_first_not_of("0123456789") != std::string::npos) return false;
+        sec[k++] = atoi(tok.c_str());
+    }
+    return k == 4;
+}
+
+bool flag(const Node& n, const char* key)
+{
+    const std::string v = n.s(key, "false");
+    return v == "true" || v == "True" || v == "1";
+}
+
 Support supports(const Graph& g, const Node& n)
 {
     auto no = [](const std::string& r) { return Support{false, r}; };
@@ -391,9 +412,10 @@ Support supports(const Graph& g, const Node& n)
         const Value& p = g.value(n.in[1]);
         if (x.dims.size() != 3 || !act(n.in[0]) || x.type == DType::F16) return no("Rope: x must be f32/bf16 [T, H, D]");
         if (p.type != DType::I32 || p.dims.empty() || p.dims[0] != x.dims[0]) return no("Rope: positions must be i32 [T]");
-        if (p.dims.size() > 2 || (p.dims.size() == 2 && p.dims[1] != 1))
-            return no("Rope: multi-axis positions (M-RoPE) are not supported");
-        if (!n.s("sections", "").empty() && n.s("sections", "0,0,0,0") != "0,0,0,0") return no("Rope: sections are not supported");
+        if (p.dims.size() > 2 || (p.dims.size() == 2 && (p.dims[1] < 1 || p.dims[1] > 4)))
+            return no("Rope: positions must be i32 [T] or [T, A] with A <= 4 axes");
+        std::vector<int> sec;
+        if (!parse_sections(n.s("sections", ""), sec)) return no("Rope: sections must be four non-negative integers");
         if (n.in.size() == 3 && g.value(n.in[2]).type != DType::F32) return no("Rope: frequency factors must be f32");
         return {true, ""};
     }
@@ -733,7 +755,7 @@ private:
             } else if (kBinaryOps.count(n.op)) {
                 Unit u{Unit::Binary};
                 u.op = kBinaryOps.at(n.op);
-                if (u.op == SLHIP_BIN_MOD && (n.s("fmod", "false") == "true" || n.s("fmod", "0") == "1")) u.op = SLHIP_BIN_FMOD;
+                if (u.op == SLHIP_BIN_MOD && flag(n, "fmod")) u.op = SLHIP_BIN_FMOD;
                 u.x = n.in[0];
                 u.up = n.in[1];
                 if (g_.value(u.x).type == DType::F32 && g_.value(u.up).type != DType::F32) std::swap(u.x, u.up);  // commutative
@@ -877,6 +899,14 @@ private:
         u.cfg.attn_factor = r.f("attn_factor", 1.f);
         u.cfg.norm = w >= 0 ? 1 : 0;
         u.cfg.eps = eps;
+        // multi-axis positions [T, A] and the M-RoPE sections (StandardOps.cs:182-192)
+        const Value& pv = g_.value(r.in[1]);
+        u.cfg.pos_axes = pv.dims.size() == 2 ? static_cast<int32_t>(pv.dims[1]) : 1;
+        std::vector<int> sec;
+        parse_sections(r.s("sections", ""), sec);
+        for (int q = 0; q < 4; q++) u.cfg.sections[q] = sec[q];
+        u.cfg.interleaved = flag(r, "interleaved") ? 1 : 0;
+        u.cfg.per_element = flag(r, "sections_per_element") ? 1 : 0;
         u.label = w >= 0 ? "rope+norm" : "rope";
         if (xv.type != g_.value(r.out[0]).type && !(is_activation(g_.value(r.out[0]).type)))
             unsupported("Rope output type");

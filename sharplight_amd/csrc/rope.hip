@@ -60,21 +60,64 @@ struct RopeArgs {
     double inv[kArgInv];     // base^(-2i/dims) * freq_scale in f64, computed on the host
     CacheRowsDev rows;       // cache rows of the tensors with to_cache
     uint32_t* err;           // the device error record (cache rows outside the cache)
+    int axes;                // position axes per token (positions [T, axes])
+    int multi;               // sections in use: pairs (or elements) take their own axis
+    int sec[4], interleaved, per_element;
 };
 
-// Entry i of token t's table. The inverse frequencies come from the host in f64 (std::pow, as RopeOp's
-// Math.Pow) when dims/2 <= kArgInv; beyond that, exp2(log2(base) * (-2i/dims)) in f64 (within ~2e-15
-// relative of pow: < 1e-10 rad at position 32767, far below the f32 result's resolution).
-template <bool INV_ARGS>
-__device__ __forceinline__ float2 table_entry(const RopeArgs& a, int64_t t, int i)
+// RopeOp.AxisOf (src/Sharplight.Cpu/RopeOp.cs:70-106) / rope.slang's axis_for_pair (Kernels/rope.slang:20-40).
+__device__ __forceinline__ int axis_of(const RopeArgs& a, int i)
 {
-    const double inv = (INV_ARGS || a.inv_in_args) ? a.inv[i]
-                                                   : exp2(a.l2b * (-2.0 * i / a.dims)) * static_cast<double>(a.fs);
-    double theta = static_cast<double>(a.pos[t]) * inv;
+    const int sd = a.sec[0] + a.sec[1] + a.sec[2] + a.sec[3];
+    const int sector = i % sd;
+    if (a.interleaved) {
+        if (sector % 3 == 1 && sector < 3 * a.sec[1]) return 1;
+        if (sector % 3 == 2 && sector < 3 * a.sec[2]) return 2;
+        return sector % 3 == 0 && sector < 3 * a.sec[0] ? 0 : 3;
+    }
+    if (sector < a.sec[0]) return 0;
+    if (sector < a.sec[0] + a.sec[1]) return 1;
+    return sector < a.sec[0] + a.sec[1] + a.sec[2] ? 2 : 3;
+}
+
+// The axes of pair i's first and second element (RopeOp.cs:54-66).
+__device__ __forceinline__ int2 pair_axes(const RopeArgs& a, int i)
+{
+    if (!a.multi) return make_int2(0, 0);
+    const int half = a.dims / 2;
+    const int first = a.neox ? i : 2 * i, second = a.neox ? i + half : 2 * i + 1;
+    return make_int2(axis_of(a, a.per_element ? first / 2 : i), axis_of(a, a.per_element ? second / 2 : i));
+}
+
+// Token t's positions of the four axes: an axis beyond the given ones reads axis 0 when there is one axis,
+// else position 0 (RopeOp.cs:133-139).
+__device__ __forceinline__ void token_positions(const RopeArgs& a, int64_t t, double* pp)
+{
+#pragma unroll
+    for (int ax = 0; ax < 4; ax++)
+        pp[ax] = ax < a.axes ? static_cast<double>(a.pos[t * a.axes + ax]) : a.axes == 1 ? static_cast<double>(a.pos[t * a.axes]) : 0.0;
+}
+
+// Entry i of token t's table: (c1, s1, c2, s2), the second pair for the pair's second element (the same
+// angle unless per-element sections give it another axis). The inverse frequencies come from the host in
+// f64 (std::pow, as RopeOp's Math.Pow) when dims/2 <= kArgInv; beyond that, exp2(log2(base) * (-2i/dims))
+// in f64 (within ~2e-15 relative of pow: < 1e-10 rad at position 32767, far below the f32 result's
+// resolution).
+__device__ __forceinline__ float4 table_entry(const RopeArgs& a, const double* pp, int i)
+{
+    const double inv = a.inv_in_args ? a.inv[i] : exp2(a.l2b * (-2.0 * i / a.dims)) * static_cast<double>(a.fs);
+    const int2 ax = pair_axes(a, i);
+    double theta = pp[ax.x] * inv;
     if (a.ff) theta /= static_cast<double>(a.ff[i]);
     float s, c;
     sincos_f64_to_f32(theta, &s, &c);
-    return make_float2(c * a.af, s * a.af);
+    float s2 = s, c2 = c;
+    if (ax.y != ax.x) {
+        double theta2 = pp[ax.y] * inv;
+        if (a.ff) theta2 /= static_cast<double>(a.ff[i]);
+        sincos_f64_to_f32(theta2, &s2, &c2);
+    }
+    return make_float4(c * a.af, s * a.af, c2 * a.af, s2 * a.af);
 }
 
 // The same entry from inputs already in registers: theta = pos * inv (/ ff), all f64.
@@ -110,7 +153,7 @@ constexpr OnesRow make_ones_row()
 }
 __constant__ OnesRow kOnesRow = make_ones_row();
 
-template <int DTI, int DTO, int L>
+template <int DTI, int DTO, int L, bool MULTI>
 __global__ __launch_bounds__(64 * kRopeWpb) void rope_vec(RopeArgs a)
 {
     using VI = Vec<DTI>;
@@ -120,7 +163,8 @@ __global__ __launch_bounds__(64 * kRopeWpb) void rope_vec(RopeArgs a)
     constexpr int NE = (HALF + 63) / 64;    // table entries per lane
     constexpr int NW = (2 * HALF + 63) / 64;  // norm-weight floats per lane
     static_assert(HALF <= kArgInv, "the vector path takes its inverse frequencies from the arguments");
-    __shared__ float2 cs[kRopeWpb][kArgInv];
+    __shared__ float2 cs[MULTI ? 1 : kRopeWpb][kArgInv];
+    __shared__ float4 cs4[MULTI ? kRopeWpb : 1][MULTI ? kArgInv : 1];  // multi-axis: (c1, s1, c2, s2)
     __shared__ float4 wsh[kRopeWpb][2 * kArgInv / 4];
     // Grid: x = head group, y = block of kRopeWpb tokens. The group (and so the tensor) is uniform over
     // the block, and the token needs no division: every wave issues few scalar instructions, which
@@ -156,7 +200,11 @@ __global__ __launch_bounds__(64 * kRopeWpb) void rope_vec(RopeArgs a)
     // tensor 0's first row (at least dims/2 floats long) and are not used.
     // The head's norm-weight row (D = dims floats) is staged through LDS the same way, one or a few
     // floats per lane instead of 2V floats per lane; a norm without weight reads a row of ones (exact).
-    const double p = static_cast<double>(a.pos[t]);
+    double p = 0.0, pp[4];
+    if constexpr (MULTI)
+        token_positions(a, t, pp);
+    else
+        p = static_cast<double>(a.pos[t]);
     const float* ffp = a.ff ? a.ff : static_cast<const float*>(a.t[0].x);
     // (Both candidates as global-address-space pointers: a generic pointer would make these flat
     // loads, which also hold the LDS counter that the table's synchronization waits on.)
@@ -188,9 +236,19 @@ __global__ __launch_bounds__(64 * kRopeWpb) void rope_vec(RopeArgs a)
     if (tt.to_cache) cr = cache_row(a.rows, t);
     char* yr = static_cast<char*>(yp) + (cr.row * ys + h * yh) * Vec<DTO>::BYTES;
     // Lanes past dims/2 rewrite the last entry with the same value.
-    float2* ctab = cs[wv];
+    float2* ctab = cs[MULTI ? 0 : wv];
+    float4* ctab4 = cs4[MULTI ? wv : 0];
 #pragma unroll
-    for (int n = 0; n < NE; n++) ctab[ie[n]] = table_value(a, p, inv[n], ffv[n]);
+    for (int n = 0; n < NE; n++) {
+        if constexpr (MULTI) {
+            const int2 ax = pair_axes(a, ie[n]);
+            const float2 v1 = table_value(a, pp[ax.x], inv[n], ffv[n]);
+            const float2 v2 = ax.y == ax.x ? v1 : table_value(a, pp[ax.y], inv[n], ffv[n]);
+            ctab4[ie[n]] = make_float4(v1.x, v1.y, v2.x, v2.y);
+        } else {
+            ctab[ie[n]] = table_value(a, p, inv[n], ffv[n]);
+        }
+    }
     float* wrow = reinterpret_cast<float*>(wsh[wv]);
 #pragma unroll
     for (int n = 0; n < NW; n++) wrow[iw[n]] = wv_[n];
@@ -220,23 +278,35 @@ __global__ __launch_bounds__(64 * kRopeWpb) void rope_vec(RopeArgs a)
             }
         }
     }
-    const float2* ct = ctab + c * V;
     float o[2 * V];
-    if (a.neox) {
+    if constexpr (MULTI) {
+        const float4* ct = ctab4 + c * V;
 #pragma unroll
         for (int e = 0; e < V; e++) {
-            const float2 cv = ct[e];
-            const float x0 = f[e], x1 = f[V + e];
-            o[e] = x0 * cv.x - x1 * cv.y;
-            o[V + e] = x0 * cv.y + x1 * cv.x;
+            const float4 cv = ct[e];
+            const int j0 = a.neox ? e : 2 * e, j1 = a.neox ? V + e : 2 * e + 1;
+            const float x0 = f[j0], x1 = f[j1];
+            o[j0] = x0 * cv.x - x1 * cv.y;
+            o[j1] = x0 * cv.w + x1 * cv.z;
         }
     } else {
+        const float2* ct = ctab + c * V;
+        if (a.neox) {
 #pragma unroll
-        for (int e = 0; e < V; e++) {
-            const float2 cv = ct[e];
-            const float x0 = f[2 * e], x1 = f[2 * e + 1];
-            o[2 * e] = x0 * cv.x - x1 * cv.y;
-            o[2 * e + 1] = x0 * cv.y + x1 * cv.x;
+            for (int e = 0; e < V; e++) {
+                const float2 cv = ct[e];
+                const float x0 = f[e], x1 = f[V + e];
+                o[e] = x0 * cv.x - x1 * cv.y;
+                o[V + e] = x0 * cv.y + x1 * cv.x;
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < V; e++) {
+                const float2 cv = ct[e];
+                const float x0 = f[2 * e], x1 = f[2 * e + 1];
+                o[2 * e] = x0 * cv.x - x1 * cv.y;
+                o[2 * e + 1] = x0 * cv.y + x1 * cv.x;
+            }
         }
     }
     if (cr.row >= 0) {  // wave-uniform: a row outside the cache is skipped and reported
@@ -252,10 +322,12 @@ __global__ __launch_bounds__(64 * kRopeWpb) void rope_vec(RopeArgs a)
 template <int DTI, int DTO>
 __global__ __launch_bounds__(256) void rope_scalar(RopeArgs a)
 {
-    __shared__ float2 cs[kMaxHalf];
+    __shared__ float4 cs[kMaxHalf];
     const int64_t t = blockIdx.x;
     const int half = a.dims / 2;
-    for (int i = threadIdx.x; i < half; i += blockDim.x) cs[i] = table_entry<false>(a, t, i);
+    double pp[4];
+    token_positions(a, t, pp);
+    for (int i = threadIdx.x; i < half; i += blockDim.x) cs[i] = table_entry(a, pp, i);
     __syncthreads();
     const int lane = threadIdx.x & 63;
     for (int64_t gh = threadIdx.x >> 6; gh < a.total_heads; gh += blockDim.x >> 6) {
@@ -293,9 +365,9 @@ __global__ __launch_bounds__(256) void rope_scalar(RopeArgs a)
             const int i0 = a.neox ? i : 2 * i;
             const int i1 = a.neox ? i + half : 2 * i + 1;
             const float x0 = val(i0), x1 = val(i1);
-            const float2 cv = cs[i];
+            const float4 cv = cs[i];
             Vec<DTO>::store1(yr, i0, x0 * cv.x - x1 * cv.y);
-            Vec<DTO>::store1(yr, i1, x0 * cv.y + x1 * cv.x);
+            Vec<DTO>::store1(yr, i1, x0 * cv.w + x1 * cv.z);
         }
         for (int64_t i = a.dims + lane; i < a.D; i += 64) Vec<DTO>::store1(yr, i, val(i));
     }
@@ -316,7 +388,11 @@ static int launch_vec(RopeArgs& a, hipStream_t st)
         a.groups = groups;
         const int64_t blocks = (a.T + kRopeWpb - 1) / kRopeWpb;
         if (blocks > 65535) return 1;  // beyond the grid's y extent: the general path
-        rope_vec<DTI, DTO, L><<<dim3(static_cast<unsigned>(groups), static_cast<unsigned>(blocks)), 64 * kRopeWpb, 0, st>>>(a);
+        const dim3 grid(static_cast<unsigned>(groups), static_cast<unsigned>(blocks));
+        if (a.multi || a.axes > 1)
+            rope_vec<DTI, DTO, L, true><<<grid, 64 * kRopeWpb, 0, st>>>(a);
+        else
+            rope_vec<DTI, DTO, L, false><<<grid, 64 * kRopeWpb, 0, st>>>(a);
         return check_launch("rope_vec");
     }
 }
@@ -381,6 +457,15 @@ extern "C" SLHIP_API int slhip_rope(int dtype_in, int dtype_out, const slhip_rop
     a.af = cfg->attn_factor;
     a.eps = cfg->eps;
     a.l2b = std::log2(static_cast<double>(cfg->base));
+    a.axes = cfg->pos_axes <= 0 ? 1 : cfg->pos_axes;
+    if (a.axes > 4) return fail(SLHIP_ERR_INVALID, "rope: at most 4 position axes (got %d)", a.axes);
+    for (int k = 0; k < 4; k++) {
+        if (cfg->sections[k] < 0) return fail(SLHIP_ERR_INVALID, "rope: negative section");
+        a.sec[k] = cfg->sections[k];
+    }
+    a.multi = a.sec[0] > 0 || a.sec[1] > 0 || a.sec[2] > 0;
+    a.interleaved = cfg->interleaved ? 1 : 0;
+    a.per_element = cfg->per_element ? 1 : 0;
     a.inv_in_args = dims / 2 <= kArgInv;
     if (a.inv_in_args)
         for (int i = 0; i < dims / 2; i++)

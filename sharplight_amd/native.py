@@ -133,7 +133,8 @@ class RopeTensor(ctypes.Structure):
 class RopeCfg(ctypes.Structure):
     _fields_ = [("dims", ctypes.c_int32), ("neox", ctypes.c_int32), ("base", ctypes.c_float),
                 ("freq_scale", ctypes.c_float), ("attn_factor", ctypes.c_float), ("norm", ctypes.c_int32),
-                ("eps", ctypes.c_float), ("reserved", ctypes.c_int32)]
+                ("eps", ctypes.c_float), ("pos_axes", ctypes.c_int32), ("sections", ctypes.c_int32 * 4),
+                ("interleaved", ctypes.c_int32), ("per_element", ctypes.c_int32)]
 
 
 _P = ctypes.c_void_p
@@ -461,7 +462,8 @@ def unary(op, dtype_in, dtype_out, x, y, rows, cols, *, x_stride=None, y_stride=
 
 
 def rope(dtype_in, dtype_out, tensors, pos, T, D, *, dims=0, neox=True, base=10000.0, freq_scale=1.0,
-         attn_factor=1.0, norm=False, eps=1e-6, ff=None, stream=None):
+         attn_factor=1.0, norm=False, eps=1e-6, ff=None, pos_axes=1, sections=None, interleaved=False,
+         per_element=False, stream=None):
     """tensors: list of dicts with x, y, heads and optional norm_w / strides (elements) / rows (a CacheRows:
     y is then a KV cache [ctx, heads, D] written at those rows)."""
     arr = (RopeTensor * len(tensors))()
@@ -472,7 +474,8 @@ def rope(dtype_in, dtype_out, tensors, pos, T, D, *, dims=0, neox=True, base=100
                             t.get("x_stride_t", H * D), t.get("x_stride_h", D),
                             t.get("y_stride_t", H * D), t.get("y_stride_h", D),
                             ctypes.pointer(rows) if rows is not None else None)
-    cfg = RopeCfg(dims, 1 if neox else 0, base, freq_scale, attn_factor, 1 if norm else 0, eps, 0)
+    cfg = RopeCfg(dims, 1 if neox else 0, base, freq_scale, attn_factor, 1 if norm else 0, eps, pos_axes,
+                  (ctypes.c_int32 * 4)(*(sections or (0, 0, 0, 0))), 1 if interleaved else 0, 1 if per_element else 0)
     call("slhip_rope", DTYPES.get(dtype_in, dtype_in), DTYPES.get(dtype_out, dtype_out), arr, len(tensors),
          ptr(pos), ptr(ff), T, D, ctypes.byref(cfg), stream)
 

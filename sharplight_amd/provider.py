@@ -137,9 +137,16 @@ class GraphBuilder:
         return self.emit("LayerNorm", [x, w, b], out_type or x.type, x.dims, eps=eps)
 
     def rope(self, x, pos, ff=None, dims=0, base=10000.0, style="neox", freq_scale=1.0, attn_factor=1.0,
-             out_type=None):
-        return self.emit("Rope", [x, pos, ff], out_type or x.type, x.dims, dims=dims, base=base, style=style,
-                         freq_scale=freq_scale, attn_factor=attn_factor)
+             out_type=None, sections=None, interleaved=False, sections_per_element=False):
+        """StandardOps.Rope; pos i32 [T] or [T, A] (multi-axis, with `sections` of four entries)."""
+        attrs = dict(dims=dims, base=base, style=style, freq_scale=freq_scale, attn_factor=attn_factor)
+        if sections is not None:
+            attrs["sections"] = ",".join(str(int(v)) for v in sections)
+        if interleaved:
+            attrs["interleaved"] = "true"
+        if sections_per_element:
+            attrs["sections_per_element"] = "true"
+        return self.emit("Rope", [x, pos, ff], out_type or x.type, x.dims, **attrs)
 
     def gather(self, table, ids, out_type="f32"):
         d = table.dims[1:]

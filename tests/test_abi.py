@@ -49,7 +49,8 @@ int main(void) {
   P(slhip_norm_copies, y16_stride) P(slhip_norm_copies, yq) P(slhip_norm_copies, yq_stride)
   P(slhip_device_props, total_memory) P(slhip_device_props, l2_bytes) P(slhip_device_props, lds_bytes_per_block)
   P(slhip_rope_tensor, heads) P(slhip_rope_tensor, y_stride_h)
-  P(slhip_rope_cfg, eps) P(slhip_rope_cfg, norm) P(slhip_rope_tensor, rows)
+  P(slhip_rope_cfg, eps) P(slhip_rope_cfg, norm) P(slhip_rope_cfg, sections) P(slhip_rope_cfg, per_element)
+  P(slhip_rope_tensor, rows)
   P(slhip_cache_rows, ctx) P(slhip_cache_rows, n_past) P(slhip_cache_rows, seq) P(slhip_cache_rows, slots)
   P(slhip_cache_rows, pages) P(slhip_cache_rows, page_slots) P(slhip_cache_rows, blocks_per_slot)
   P(slhip_cache_rows, block_size)
@@ -78,6 +79,8 @@ def test_struct_layouts_match_c():
     assert lay["slhip_rope_tensor.y_stride_h"] == native.RopeTensor.y_stride_h.offset
     assert lay["slhip_rope_cfg.eps"] == native.RopeCfg.eps.offset
     assert lay["slhip_rope_cfg.norm"] == native.RopeCfg.norm.offset
+    assert lay["slhip_rope_cfg.sections"] == native.RopeCfg.sections.offset
+    assert lay["slhip_rope_cfg.per_element"] == native.RopeCfg.per_element.offset
     assert lay["slhip_cache_rows"] == ctypes.sizeof(native.CacheRows)
     assert lay["slhip_rope_tensor.rows"] == native.RopeTensor.rows.offset
     for f in ("ctx", "n_past", "seq", "slots", "pages", "page_slots", "blocks_per_slot", "block_size"):

@@ -412,3 +412,34 @@ def test_standalone_elementwise_graph(dev):
         assert_bf16_close(seg.get_output(a), a16, what="silu")
         z16 = oracle.to_bf16(oracle.unary_kind("Scale", oracle.from_bf16(seg.get_output(a)).ravel(), 0.5, -1.0))
         assert_bf16_close(seg.get_output(z), z16.reshape(T, D), ulp=0, what="scale")
+
+
+def test_mrope_graph_one_launch(dev):
+    """A Qwen3-VL attention prologue: per-head RmsNorm then interleaved M-RoPE over [T, 3] positions for q
+    and k -- absorbed and merged into one launch like the single-axis form."""
+    T = 40
+    g = GraphBuilder()
+    q = g.input("bf16", "T", 8, 128)
+    k = g.input("bf16", "T", 2, 128)
+    pos = g.input("i32", "T", 3)
+    wq = g.weight("f32", 128)
+    wk = g.weight("f32", 128)
+    kw = dict(base=5e6, style="neox", sections=(24, 20, 20, 0), interleaved=True)
+    yq = g.output(g.rope(g.rms_norm(q, wq, eps=1e-6), pos, **kw))
+    yk = g.output(g.rope(g.rms_norm(k, wk, eps=1e-6), pos, **kw))
+    rng = np.random.default_rng(4)
+    qs = oracle.to_bf16(rng.standard_normal((T, 8, 128)).astype(np.float32))
+    ks = oracle.to_bf16(rng.standard_normal((T, 2, 128)).astype(np.float32))
+    ps = rng.integers(0, 9000, (T, 3)).astype(np.int32)
+    wqs = (1 + 0.1 * rng.standard_normal(128)).astype(np.float32)
+    wks = (1 + 0.1 * rng.standard_normal(128)).astype(np.float32)
+    with dev.compile(g, max_tokens=T) as seg:
+        assert seg.launches == ["rope+norm|rope+norm"]
+        for v, a in ((q, qs), (k, ks), (pos, ps), (wq, wqs), (wk, wks)):
+            seg.set_input(v, a)
+        log("provider mrope")
+        seg.execute(T)
+        for y, x, w in ((yq, qs, wqs), (yk, ks, wks)):
+            xn = oracle.rmsnorm(oracle.from_bf16(x).reshape(-1, 128), w, 1e-6).reshape(x.shape)
+            ref = oracle.to_bf16(oracle.rope_multi(xn, ps, [24, 20, 20, 0], interleaved=True, base=5e6))
+            assert_bf16_close(seg.get_output(y), ref, what="mrope")

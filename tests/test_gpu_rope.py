@@ -142,3 +142,61 @@ def test_rope_position_zero_is_identity(device):
 def test_rope_empty(device):
     native.rope("bf16", "bf16", [dict(x=16, y=16, heads=4)], 16, 0, 128)
     native.synchronize()
+
+
+# ---- multi-axis rope (M-RoPE, interleaved, per-element sections) ----------------------------------------
+
+def test_rope_multi_axis_matches_ggml(device):
+    """GgmlCrossCheckTests.RopeMatchesGgml's seven cases through slhip_rope (f32): the four-axis positions
+    with sections for modes 8 (M-RoPE) and 40 (interleaved), against ggml's output at the reference's 2e-4
+    and against the oracle within the f32 tolerance."""
+    fx = np.load(os.path.join(GOLDEN, "ggml_rope.npz"))
+    for k in range(7):
+        mode, dims, T, H, D = (int(v) for v in fx[f"case{k}_meta"])
+        multi = mode >= 8
+        x = fx[f"case{k}_x"]
+        pos = fx[f"case{k}_pos"] if multi else np.ascontiguousarray(fx[f"case{k}_pos"][:, 0])
+        sec = [int(v) for v in fx[f"case{k}_sections"]] if multi else None
+        fs = float(fx[f"case{k}_freq_scale"][0])
+        (y,) = _run("f32", "f32", [(x, None)], pos, D, dims=dims, neox=mode != 0, base=10000.0, freq_scale=fs,
+                    pos_axes=4 if multi else 1, sections=sec, interleaved=mode == 40)
+        np.testing.assert_allclose(y, fx[f"case{k}_y"], rtol=2e-4, atol=2e-4)
+        ref = oracle.rope_multi(x, pos, sec, interleaved=mode == 40, dims=dims, neox=mode != 0, freq_scale=fs)
+        assert_f32_close(y, ref, what=f"ggml case {k}")
+
+
+@pytest.mark.parametrize("interleaved,per_element,neox", [(False, False, True), (True, False, True),
+                                                          (False, True, True), (True, True, False)])
+def test_rope_multi_axis_qk_norm_bf16(device, interleaved, per_element, neox):
+    """A Qwen3-VL-style prologue: q [256, 16, 128] and k [256, 4, 128] bf16 with the per-head RMSNorm fused,
+    three position axes (t, h, w) with sections [24, 20, 20, 0], theta 5e6 -- the vector kernel's
+    multi-axis variant, against the oracle's RmsNorm then multi-axis RopeOp."""
+    rng = np.random.default_rng(31)
+    T = 256
+    q = oracle.to_bf16(rng.standard_normal((T, 16, 128)).astype(np.float32))
+    k = oracle.to_bf16(rng.standard_normal((T, 4, 128)).astype(np.float32))
+    wq = (1 + 0.1 * rng.standard_normal(128)).astype(np.float32)
+    wk = (1 + 0.1 * rng.standard_normal(128)).astype(np.float32)
+    pos = rng.integers(0, 32768, (T, 3)).astype(np.int32)
+    sec = [24, 20, 20, 0]
+    yq, yk = _run("bf16", "bf16", [(q, wq), (k, wk)], pos, 128, neox=neox, base=5e6, norm=True, eps=1e-6,
+                  pos_axes=3, sections=sec, interleaved=interleaved, per_element=per_element)
+    for y, x, w, name in ((yq, q, wq, "q"), (yk, k, wk, "k")):
+        xn = oracle.rmsnorm(oracle.from_bf16(x).reshape(-1, 128), w, 1e-6).reshape(x.shape)
+        ref = oracle.to_bf16(oracle.rope_multi(xn, pos, sec, interleaved=interleaved, per_element=per_element,
+                                               neox=neox, base=5e6))
+        assert_bf16_close(y, ref, what=f"{name} il={interleaved} pe={per_element}")
+
+
+def test_rope_multi_axis_general_path(device):
+    """Partial dims (48 of D 72) and a single position axis broadcast to the sections: the general kernel."""
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((9, 3, 72)).astype(np.float32)
+    p = rng.integers(0, 20000, 9).astype(np.int32)
+    pos4 = rng.integers(0, 20000, (9, 4)).astype(np.int32)
+    (y1,) = _run("f32", "f32", [(x, None)], p, 72, dims=48, neox=True, base=1e4, sections=[4, 8, 8, 4])
+    assert_f32_close(y1, oracle.rope_multi(x, p[:, None], [4, 8, 8, 4], dims=48, base=1e4), what="one axis")
+    (y4,) = _run("f32", "f32", [(x, None)], pos4, 72, dims=48, neox=True, base=1e4, pos_axes=4,
+                 sections=[4, 8, 8, 4], per_element=True)
+    assert_f32_close(y4, oracle.rope_multi(x, pos4, [4, 8, 8, 4], per_element=True, dims=48, base=1e4),
+                     what="four axes, per element")

@@ -362,16 +362,74 @@ def test_erf_implementations():
 # ---- rope ---------------------------------------------------------------------------------------------
 
 def test_rope_matches_ggml(rope_fx):
-    """GgmlCrossCheckTests.RopeMatchesGgml (GgmlCrossCheckTests.cs:75-98), single-axis cases: normal (mode
-    0), neox (mode 2), neox with partial dims and freq_scale 0.5. Reference tolerance 2e-4."""
-    for k in range(3):
+    """GgmlCrossCheckTests.RopeMatchesGgml (GgmlCrossCheckTests.cs:75-98), all seven cases: normal (mode 0),
+    neox (mode 2), neox with partial dims and freq_scale 0.5, M-RoPE (mode 8, sections 2,3,3,0) and
+    interleaved M-RoPE (mode 40, three section sets, one with dims 32 of D 64). Positions [T, 4] for the
+    multi-axis modes, axis 0 otherwise, as the reference test passes them. Reference tolerance 2e-4."""
+    for k in range(7):
         mode, dims, T, H, D = (int(v) for v in rope_fx[f"case{k}_meta"])
-        assert mode in (0, 2)
-        got = oracle.rope(rope_fx[f"case{k}_x"], rope_fx[f"case{k}_pos"][:, 0], dims=dims, neox=mode == 2,
-                          base=10000.0, freq_scale=float(rope_fx[f"case{k}_freq_scale"][0]))
+        fs = float(rope_fx[f"case{k}_freq_scale"][0])
+        if mode >= 8:
+            got = oracle.rope_multi(rope_fx[f"case{k}_x"], rope_fx[f"case{k}_pos"], rope_fx[f"case{k}_sections"],
+                                    interleaved=mode == 40, dims=dims, neox=True, base=10000.0, freq_scale=fs)
+        else:
+            got = oracle.rope(rope_fx[f"case{k}_x"], rope_fx[f"case{k}_pos"][:, 0], dims=dims, neox=mode == 2,
+                              base=10000.0, freq_scale=fs)
         ref = rope_fx[f"case{k}_y"]
         np.testing.assert_allclose(got, ref, rtol=2e-4, atol=2e-4)
-        assert np.abs(got - ref).max() < 1e-5
+        assert np.abs(got - ref).max() < 1e-5, k
+
+
+def test_rope_axis_of_sector_rules():
+    """RopeOp.AxisOf by hand: sectioned [2,3,3,0] and interleaved [3,2,2,1] over two periods; no sections
+    -> axis 0."""
+    sec = [oracle.rope_axis_of(i, [2, 3, 3, 0]) for i in range(10)]
+    assert sec == [0, 0, 1, 1, 1, 2, 2, 2, 0, 0]
+    il = [oracle.rope_axis_of(i, [3, 2, 2, 1], interleaved=True) for i in range(16)]
+    assert il == [0, 1, 2, 0, 1, 2, 0, 3] * 2
+    assert [oracle.rope_axis_of(i, [0, 0, 0, 5]) for i in range(3)] == [0, 0, 0]
+
+
+def _rope_axes_f64(x, pos, ax1, ax2, dims, neox, base=10000.0):
+    """f64 closed form with given axes per pair for the first and the second element."""
+    T, H, D = x.shape
+    half = dims // 2
+    inv = base ** (-2.0 * np.arange(half) / dims)
+    th1 = pos.astype(np.float64)[:, ax1] * inv[None, :]
+    th2 = pos.astype(np.float64)[:, ax2] * inv[None, :]
+    i0 = np.arange(half) if neox else 2 * np.arange(half)
+    i1 = i0 + half if neox else i0 + 1
+    y = x.astype(np.float64).copy()
+    x0, x1 = x[:, :, i0].astype(np.float64), x[:, :, i1].astype(np.float64)
+    y[:, :, i0] = x0 * np.cos(th1)[:, None, :] - x1 * np.sin(th1)[:, None, :]
+    y[:, :, i1] = x0 * np.sin(th2)[:, None, :] + x1 * np.cos(th2)[:, None, :]
+    return y
+
+
+def test_rope_per_element_sections():
+    """XD-RoPE: dims 8, sections [1,1,1,1], neox: pair i's first element i takes section i//2 and its second
+    element i+4 section (i+4)//2, so the axes are (0,2), (0,2), (1,3), (1,3) -- worked by hand. With gptj
+    pairs (2i, 2i+1) both elements take section i: per-element sections change nothing."""
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((5, 3, 8)).astype(np.float32)
+    pos = rng.integers(0, 3000, (5, 4)).astype(np.int32)
+    got = oracle.rope_multi(x, pos, [1, 1, 1, 1], per_element=True, neox=True)
+    want = _rope_axes_f64(x, pos, [0, 0, 1, 1], [2, 2, 3, 3], 8, True)
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-5)
+    plain = oracle.rope_multi(x, pos, [1, 1, 1, 1], neox=False)
+    assert np.array_equal(oracle.rope_multi(x, pos, [1, 1, 1, 1], per_element=True, neox=False), plain)
+    np.testing.assert_allclose(plain, _rope_axes_f64(x, pos, [0, 1, 2, 3], [0, 1, 2, 3], 8, False), rtol=1e-5, atol=1e-5)
+
+
+def test_rope_multi_axis_with_equal_axes_is_plain_rope():
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((6, 2, 16)).astype(np.float32)
+    p = rng.integers(0, 30000, 6).astype(np.int32)
+    pos = np.repeat(p[:, None], 4, axis=1)
+    for sec, il in (([2, 3, 3, 0], False), ([3, 2, 2, 1], True)):
+        assert np.array_equal(oracle.rope_multi(x, pos, sec, interleaved=il), oracle.rope(x, p))
+    # one position axis broadcast to all four (RopeOp.cs:133-139)
+    assert np.array_equal(oracle.rope_multi(x, p[:, None], [2, 3, 3, 0]), oracle.rope(x, p))
 
 
 def _rope_f64(x, pos, dims, neox, base, fs=1.0, af=1.0, ff=None):

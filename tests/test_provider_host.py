@@ -52,8 +52,11 @@ def test_supports_answers():
     g.gather(tbl, ids, out_type="bf16")      # 4: yes
     g.gather(tbl, ids, out_type="f16")       # 5: f16 output -> no
     pos2 = g.input("i32", "T", 4)
-    g.rope(x, pos2)                          # 6: multi-axis positions -> no
-    expect = [False, True, False, False, True, False, False]
+    g.rope(x, pos2, sections=(8, 12, 12, 0))  # 6: multi-axis positions (M-RoPE) -> yes
+    pos5 = g.input("i32", "T", 5)
+    g.rope(x, pos5)                          # 7: five axes -> no
+    g.emit("Rope", [x, pos2], "f32", x.dims, sections="1,2,3")  # 8: three sections -> no
+    expect = [False, True, False, False, True, False, True, False, False]
     for k, e in enumerate(expect):
         ok, why = _supports(g, k)
         assert ok == e, (k, why)
