@@ -18,7 +18,7 @@ BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libsharplight_hip.so")
 # GPU check programs of the test suite (sources under tests/, binaries beside them under tests/_bin/)
 TESTS = os.path.join(os.path.dirname(HERE), "tests")
-CHECKS = ["e4m3_exhaustive"]
+CHECKS = ["e4m3_exhaustive", "recip_exhaustive"]
 ARCH = os.environ.get("SLHIP_ARCH", "gfx950")
 
 # Packed-f32 VALU forms are disabled: hipcc -O3 would otherwise form them from plain float code.
@@ -33,8 +33,18 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found")
 
 
-def _compile(src: str) -> str:
+def _stale(src: str, obj: str) -> bool:
+    """Whether obj is older than src or than any header under csrc/ or include/."""
+    if not os.path.exists(obj):
+        return True
+    deps = [src] + glob.glob(os.path.join(CSRC, "*.h")) + glob.glob(os.path.join(CSRC, "*.hpp")) + glob.glob(os.path.join(os.path.dirname(HERE), "include", "*.h"))
+    return max(os.path.getmtime(d) for d in deps) > os.path.getmtime(obj)
+
+
+def _compile(src: str, incremental: bool = False) -> str:
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
+    if incremental and not _stale(src, obj):
+        return obj
     cmd = [hipcc(), *CFLAGS, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
@@ -42,11 +52,12 @@ def _compile(src: str) -> str:
     return obj
 
 
-def build(verbose: bool = False) -> str:
+def build(verbose: bool = False, incremental: bool = False) -> str:
+    """Compiles every source (incremental: only those whose object is older than the source or a header)."""
     os.makedirs(BUILD, exist_ok=True)
     sources = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
     with ThreadPoolExecutor(max_workers=min(8, len(sources))) as ex:
-        objs = list(ex.map(_compile, sources))
+        objs = list(ex.map(lambda src: _compile(src, incremental), sources))
     tmp = LIB + ".tmp"
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -56,6 +67,8 @@ def build(verbose: bool = False) -> str:
     os.makedirs(os.path.join(TESTS, "_bin"), exist_ok=True)
     for name in CHECKS:
         exe = os.path.join(TESTS, "_bin", name)
+        if incremental and not _stale(os.path.join(TESTS, name + ".hip"), exe):
+            continue
         r = subprocess.run([hipcc(), *[f for f in CFLAGS if f not in ("-fPIC", "-fvisibility=hidden")], "-o", exe,
                             os.path.join(TESTS, name + ".hip")], capture_output=True, text=True)
         if r.returncode != 0:
@@ -66,5 +79,5 @@ def build(verbose: bool = False) -> str:
 
 
 if __name__ == "__main__":
-    build(verbose=True)
+    build(verbose=True, incremental="--incremental" in sys.argv)
     sys.exit(0)

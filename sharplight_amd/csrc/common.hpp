@@ -221,16 +221,55 @@ template <> __device__ __forceinline__ void store_packed<SLHIP_F16, 4>(void* p, 
 
 // ---- device side: wavefront reductions ------------------------------------------------------------
 
-// Butterfly sum over groups of W consecutive lanes (W a power of two <= 64); every lane of the group
-// ends with the same value, summed in the same order.
+template <int CTRL> __device__ __forceinline__ float dpp_f32(float v)
+{
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over groups of W consecutive lanes (W a power of two <= 64); every lane of the group ends with the
+// same value (the same pairs, quads, ... summed in the same order for every lane). Within a 16-lane row the
+// steps are DPP moves (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror: once the
+// lanes of a quad (of 8 lanes) agree, the mirror pairs each with the other quad (half)), with no LDS round
+// trip; across rows a lane exchange.
 template <int W> __device__ __forceinline__ float group_sum(float v)
 {
-#pragma unroll
-    for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    static_assert(W >= 1 && W <= 64 && (W & (W - 1)) == 0, "group of 1..64 lanes");
+    if constexpr (W >= 2) v += dpp_f32<0xB1>(v);
+    if constexpr (W >= 4) v += dpp_f32<0x4E>(v);
+    if constexpr (W >= 8) v += dpp_f32<0x141>(v);
+    if constexpr (W >= 16) v += dpp_f32<0x140>(v);
+    if constexpr (W >= 32) v += __shfl_xor(v, 16, 64);
+    if constexpr (W >= 64) v += __shfl_xor(v, 32, 64);
     return v;
 }
 
-__device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
+// The hardware reciprocal with one Newton step: r = fma(fma(-s, y, 1), y, y), y = rcp(s).
+__device__ __forceinline__ float recip_nr(float s)
+{
+    const float y = __builtin_amdgcn_rcpf(s);
+    return fmaf(fmaf(-s, y, 1.0f), y, y);
+}
+
+// 1/s rounded as IEEE division: recip_nr where it equals the quotient -- s in [2^-125, 2^125], checked for
+// every f32 there on the device by tests/recip_exhaustive.hip -- and the division elsewhere.
+__device__ __forceinline__ float recip_ieee(float s)
+{
+    const float r = recip_nr(s);
+    return (s >= 0x1p-125f && s <= 0x1p125f) ? r : 1.0f / s;
+}
+
+// Sum over the whole wave, returned wave-uniform: the row sums by DPP as above, then row_bcast:15 and
+// row_bcast:31 carry rows 0..2 into row 3, whose last lane holds the total ((r0 + r1) + (r2 + r3)).
+__device__ __forceinline__ float wave_sum(float v)
+{
+    v += dpp_f32<0xB1>(v);
+    v += dpp_f32<0x4E>(v);
+    v += dpp_f32<0x141>(v);
+    v += dpp_f32<0x140>(v);
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xA, 0xF, false));  // row_bcast:15
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x143, 0xC, 0xF, false));  // row_bcast:31
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
 
 // Max over groups of W consecutive lanes; every lane of the group ends with the same value.
 template <int W> __device__ __forceinline__ float group_max(float v)

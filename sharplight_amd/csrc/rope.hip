@@ -30,6 +30,7 @@
 
 namespace slhip {
 
+
 constexpr int kMaxRopeTensors = 4;
 constexpr int kMaxHalf = 512;  // dims <= 1024
 constexpr int kArgInv = 128;   // inverse frequencies carried in the kernel arguments up to dims = 256
@@ -55,6 +56,7 @@ struct RopeArgs {
     int64_t T, D;
     int dims, neox, norm;
     float base, fs, af, eps;
+    float inv_d;             // 1/D when D is a power of two (then q * inv_d == q / D exactly), else 0
     int inv_in_args;         // inv[] holds the inverse frequencies (dims/2 <= kArgInv)
     double l2b;              // log2(base) in f64, for dims/2 > kArgInv
     double inv[kArgInv];     // base^(-2i/dims) * freq_scale in f64, computed on the host
@@ -120,14 +122,15 @@ __device__ __forceinline__ float4 table_entry(const RopeArgs& a, const double* p
     return make_float4(c * a.af, s * a.af, c2 * a.af, s2 * a.af);
 }
 
-// The same entry from inputs already in registers: theta = pos * inv (/ ff), all f64.
-__device__ __forceinline__ float2 table_value(const RopeArgs& a, double p, double inv, float ff)
+// sin/cos of theta = p * inv (/ ff, only when the launch has frequency factors: FF) in f64, narrowed to f32.
+template <bool FF>
+__device__ __forceinline__ float2 angle_cs(double p, double inv, float ff)
 {
     double theta = p * inv;
-    if (a.ff) theta /= static_cast<double>(ff);
+    if constexpr (FF) theta /= static_cast<double>(ff);
     float s, c;
     sincos_f64_to_f32(theta, &s, &c);
-    return make_float2(c * a.af, s * a.af);
+    return make_float2(c, s);
 }
 
 __device__ __forceinline__ int tensor_of(const RopeArgs& a, int64_t gh)
@@ -153,7 +156,44 @@ constexpr OnesRow make_ones_row()
 }
 __constant__ OnesRow kOnesRow = make_ones_row();
 
-template <int DTI, int DTO, int L, bool MULTI>
+// Sum of squares of 2V values held as V/2 packed bf16 words per vector: each v_dot2 adds two exact products.
+template <int DTI, int V>
+__device__ __forceinline__ float sum_squares(const uint4& r0, const uint4& r1, const float* f)
+{
+    float q = 0.f;
+    if constexpr (DTI == SLHIP_BF16) {
+        const uint32_t w[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
+        float q1 = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; i += 2) {
+            q = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w[i]), __builtin_bit_cast(bf16x2_t, w[i]), q, false);
+            q1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w[i + 1]), __builtin_bit_cast(bf16x2_t, w[i + 1]), q1, false);
+        }
+        q += q1;
+    } else {
+        float q1 = 0.f;
+#pragma unroll
+        for (int e = 0; e < 2 * V; e += 2) {
+            q = fmaf(f[e], f[e], q);
+            q1 = fmaf(f[e + 1], f[e + 1], q1);
+        }
+        q += q1;
+    }
+    return q;
+}
+
+// Vector path. Grid: x = head group, y = block of kRopeWpb tokens. The group (and so the tensor) is uniform
+// over the block, and the token needs no division: every wave issues few scalar instructions, which matters
+// because a CU's scalar unit is shared by all of its waves. Blocks are dispatched x first, so the waves in
+// flight cover whole tokens of contiguous memory.
+//
+// The wave's table holds, per rotation pair i of its token, (c1 w0, s1 w1, s2 w0, c2 w1) with w0, w1 the norm
+// weights of the pair's two elements (1 without a weight) and (c2, s2) the angle of the second element's
+// axis (the first's unless per-element sections differ): the norm's weight multiply is folded into the
+// table, so a lane applies y0 = f0 T.x - f1 T.y, y1 = f0 T.z + f1 T.w to its scaled values f = x * scale.
+// (The CPU provider rounds x*scale*w before the rotation; folding changes the rounding of each product by
+// at most an f32 ulp, well inside the parity tolerance.)
+template <int DTI, int DTO, int L, bool MULTI, bool FF>
 __global__ __launch_bounds__(64 * kRopeWpb) void rope_vec(RopeArgs a)
 {
     using VI = Vec<DTI>;
@@ -161,15 +201,8 @@ __global__ __launch_bounds__(64 * kRopeWpb) void rope_vec(RopeArgs a)
     constexpr int HPW = 64 / L;             // head rows per wave
     constexpr int HALF = L * V;             // dims / 2
     constexpr int NE = (HALF + 63) / 64;    // table entries per lane
-    constexpr int NW = (2 * HALF + 63) / 64;  // norm-weight floats per lane
     static_assert(HALF <= kArgInv, "the vector path takes its inverse frequencies from the arguments");
-    __shared__ float2 cs[MULTI ? 1 : kRopeWpb][kArgInv];
-    __shared__ float4 cs4[MULTI ? kRopeWpb : 1][MULTI ? kArgInv : 1];  // multi-axis: (c1, s1, c2, s2)
-    __shared__ float4 wsh[kRopeWpb][2 * kArgInv / 4];
-    // Grid: x = head group, y = block of kRopeWpb tokens. The group (and so the tensor) is uniform over
-    // the block, and the token needs no division: every wave issues few scalar instructions, which
-    // matters because a CU's scalar unit is shared by all of its waves. Blocks are dispatched x first,
-    // so the waves in flight cover whole tokens of contiguous memory.
+    __shared__ float4 cs[kRopeWpb][kArgInv];
     const uint32_t t = blockIdx.y * kRopeWpb + wave_id();
     if (t >= static_cast<uint32_t>(a.T)) return;
     const int lane = threadIdx.x & 63;
@@ -191,42 +224,38 @@ __global__ __launch_bounds__(64 * kRopeWpb) void rope_vec(RopeArgs a)
     // Lanes past the tensor's last head read that head (and store nothing), so every load below is
     // unconditional: a load under a divergent branch makes the compiler wait for it at the join.
     const int64_t hl = active ? h : heads - 1;
-    const char* xr = static_cast<const char*>(xp) + (static_cast<int64_t>(t) * xs + hl * xh) * VI::BYTES;
+    const char* xrow = static_cast<const char*>(xp) + static_cast<int64_t>(t) * xs * VI::BYTES;  // wave-uniform
+    const uint32_t xo0 = static_cast<uint32_t>((hl * xh + e0) * VI::BYTES);
+    const uint32_t xo1 = static_cast<uint32_t>((hl * xh + e1) * VI::BYTES);
 
-    // Table inputs first: entries lane (+ 64), NE per lane. Vector-memory loads complete in order, so a
-    // table input loaded after the row's data would make the f64 table wait for the HBM data instead of
-    // overlapping it; and the code stays free of branches up to the table, because the compiler waits
-    // for outstanding loads where divergent paths join. Without frequency factors the factor loads read
-    // tensor 0's first row (at least dims/2 floats long) and are not used.
-    // The head's norm-weight row (D = dims floats) is staged through LDS the same way, one or a few
-    // floats per lane instead of 2V floats per lane; a norm without weight reads a row of ones (exact).
+    // Table inputs first: entries lane (+ 64), NE per lane. Vector-memory loads complete in order, so a table
+    // input loaded after the row's data would make the f64 table wait for the HBM data instead of overlapping
+    // it; and the code stays free of branches up to the table, because the compiler waits for outstanding
+    // loads where divergent paths join. A norm without weight reads a row of ones (exact).
     double p = 0.0, pp[4];
     if constexpr (MULTI)
         token_positions(a, t, pp);
     else
         p = static_cast<double>(a.pos[t]);
-    const float* ffp = a.ff ? a.ff : static_cast<const float*>(a.t[0].x);
-    // (Both candidates as global-address-space pointers: a generic pointer would make these flat
-    // loads, which also hold the LDS counter that the table's synchronization waits on.)
+    // (Global-address-space pointers: a generic pointer would make these flat loads, which also hold the
+    // LDS counter that the table's synchronization waits on.)
     const gfloat* wsrc = (a.norm && wp) ? (const gfloat*)wp : (const gfloat*)kOnesRow.v;
+    const gfloat* ffp = (const gfloat*)(FF ? a.ff : kOnesRow.v);
     int ie[NE];
     double inv[NE];
-    float ffv[NE];
+    float ffv[NE], w0[NE], w1[NE];
 #pragma unroll
     for (int n = 0; n < NE; n++) {
         ie[n] = lane + 64 * n < HALF ? lane + 64 * n : HALF - 1;
         inv[n] = a.inv[ie[n]];
         ffv[n] = ffp[ie[n]];
+        const int j0 = a.neox ? ie[n] : 2 * ie[n];
+        const int j1 = a.neox ? ie[n] + HALF : 2 * ie[n] + 1;
+        w0[n] = wsrc[j0];
+        w1[n] = wsrc[j1];
     }
-    int iw[NW];
-    float wv_[NW];
-#pragma unroll
-    for (int n = 0; n < NW; n++) {
-        iw[n] = lane + 64 * n < 2 * HALF ? lane + 64 * n : 2 * HALF - 1;
-        wv_[n] = wsrc[iw[n]];
-    }
-    const uint4 r0 = load_nt(xr + e0 * VI::BYTES);
-    const uint4 r1 = load_nt(xr + e1 * VI::BYTES);
+    const uint4 r0 = load_nt(xrow + xo0);
+    const uint4 r1 = load_nt(xrow + xo1);
     // Keeps the instruction scheduler from sinking the loads below the f64 work (it would, to save
     // registers), which would leave the table's latency unhidden.
     __builtin_amdgcn_sched_barrier(0);
@@ -234,24 +263,20 @@ __global__ __launch_bounds__(64 * kRopeWpb) void rope_vec(RopeArgs a)
     // table entry, only needed by the stores).
     CacheRow cr{static_cast<int64_t>(t), 0, 0, 0, 0, 0};
     if (tt.to_cache) cr = cache_row(a.rows, t);
-    char* yr = static_cast<char*>(yp) + (cr.row * ys + h * yh) * Vec<DTO>::BYTES;
     // Lanes past dims/2 rewrite the last entry with the same value.
-    float2* ctab = cs[MULTI ? 0 : wv];
-    float4* ctab4 = cs4[MULTI ? wv : 0];
 #pragma unroll
     for (int n = 0; n < NE; n++) {
+        float2 v1, v2;
         if constexpr (MULTI) {
             const int2 ax = pair_axes(a, ie[n]);
-            const float2 v1 = table_value(a, pp[ax.x], inv[n], ffv[n]);
-            const float2 v2 = ax.y == ax.x ? v1 : table_value(a, pp[ax.y], inv[n], ffv[n]);
-            ctab4[ie[n]] = make_float4(v1.x, v1.y, v2.x, v2.y);
+            v1 = angle_cs<FF>(pp[ax.x], inv[n], ffv[n]);
+            v2 = ax.y == ax.x ? v1 : angle_cs<FF>(pp[ax.y], inv[n], ffv[n]);
         } else {
-            ctab[ie[n]] = table_value(a, p, inv[n], ffv[n]);
+            v1 = v2 = angle_cs<FF>(p, inv[n], ffv[n]);
         }
+        const float cf = a.af;
+        cs[wv][ie[n]] = make_float4((v1.x * cf) * w0[n], (v1.y * cf) * w1[n], (v2.y * cf) * w0[n], (v2.x * cf) * w1[n]);
     }
-    float* wrow = reinterpret_cast<float*>(wsh[wv]);
-#pragma unroll
-    for (int n = 0; n < NW; n++) wrow[iw[n]] = wv_[n];
     wave_lds_sync();
     if (!active) return;
 
@@ -259,57 +284,38 @@ __global__ __launch_bounds__(64 * kRopeWpb) void rope_vec(RopeArgs a)
     VI::unpack(r0, f);
     VI::unpack(r1, f + V);
     if (a.norm) {
-        float q = 0.f;
-#pragma unroll
-        for (int e = 0; e < 2 * V; e++) q = fmaf(f[e], f[e], q);
-        q = group_sum<L>(q);
-        const float scale = 1.0f / sqrtf(q / static_cast<float>(a.D) + a.eps);
+        const float q = group_sum<L>(sum_squares<DTI, V>(r0, r1, f));
+        const float m = a.inv_d > 0.f ? q * a.inv_d : q / static_cast<float>(a.D);
+        const float sq = sqrtf(m + a.eps);
+        float scale = recip_nr(sq);
+        // recip_nr equals 1/sq on [2^-125, 2^125]; outside it (a zero, infinite or extreme sum) the division.
+        // The test is wave-uniform, so the division is not evaluated on the common path.
+        const bool in_range = sq >= 0x1p-125f && sq <= 0x1p125f;
+        if (__builtin_amdgcn_ballot_w64(!in_range) != 0) {
+            if (!in_range) scale = 1.0f / sq;
+        }
 #pragma unroll
         for (int e = 0; e < 2 * V; e++) f[e] *= scale;
-#pragma unroll
-        for (int hv = 0; hv < 2; hv++) {
-#pragma unroll
-            for (int q4 = 0; q4 < V / 4; q4++) {
-                const float4 w4 = wsh[wv][(hv ? e1 : e0) / 4 + q4];
-                f[hv * V + 4 * q4 + 0] *= w4.x;
-                f[hv * V + 4 * q4 + 1] *= w4.y;
-                f[hv * V + 4 * q4 + 2] *= w4.z;
-                f[hv * V + 4 * q4 + 3] *= w4.w;
-            }
-        }
     }
+    const float4* ct = &cs[wv][c * V];
     float o[2 * V];
-    if constexpr (MULTI) {
-        const float4* ct = ctab4 + c * V;
+    if (a.neox) {  // wave-uniform: one loop per pair layout, no per-element selects
 #pragma unroll
         for (int e = 0; e < V; e++) {
             const float4 cv = ct[e];
-            const int j0 = a.neox ? e : 2 * e, j1 = a.neox ? V + e : 2 * e + 1;
-            const float x0 = f[j0], x1 = f[j1];
-            o[j0] = x0 * cv.x - x1 * cv.y;
-            o[j1] = x0 * cv.w + x1 * cv.z;
+            o[e] = f[e] * cv.x - f[V + e] * cv.y;
+            o[V + e] = f[e] * cv.z + f[V + e] * cv.w;
         }
     } else {
-        const float2* ct = ctab + c * V;
-        if (a.neox) {
 #pragma unroll
-            for (int e = 0; e < V; e++) {
-                const float2 cv = ct[e];
-                const float x0 = f[e], x1 = f[V + e];
-                o[e] = x0 * cv.x - x1 * cv.y;
-                o[V + e] = x0 * cv.y + x1 * cv.x;
-            }
-        } else {
-#pragma unroll
-            for (int e = 0; e < V; e++) {
-                const float2 cv = ct[e];
-                const float x0 = f[2 * e], x1 = f[2 * e + 1];
-                o[2 * e] = x0 * cv.x - x1 * cv.y;
-                o[2 * e + 1] = x0 * cv.y + x1 * cv.x;
-            }
+        for (int e = 0; e < V; e++) {
+            const float4 cv = ct[e];
+            o[2 * e] = f[2 * e] * cv.x - f[2 * e + 1] * cv.y;
+            o[2 * e + 1] = f[2 * e] * cv.z + f[2 * e + 1] * cv.w;
         }
     }
     if (cr.row >= 0) {  // wave-uniform: a row outside the cache is skipped and reported
+        char* yr = static_cast<char*>(yp) + (cr.row * ys + h * yh) * Vec<DTO>::BYTES;
         store_packed<DTO, V>(yr + e0 * Vec<DTO>::BYTES, o);
         store_packed<DTO, V>(yr + e1 * Vec<DTO>::BYTES, o + V);
     } else if (lane == 0) {
@@ -389,10 +395,14 @@ static int launch_vec(RopeArgs& a, hipStream_t st)
         const int64_t blocks = (a.T + kRopeWpb - 1) / kRopeWpb;
         if (blocks > 65535) return 1;  // beyond the grid's y extent: the general path
         const dim3 grid(static_cast<unsigned>(groups), static_cast<unsigned>(blocks));
-        if (a.multi || a.axes > 1)
-            rope_vec<DTI, DTO, L, true><<<grid, 64 * kRopeWpb, 0, st>>>(a);
-        else
-            rope_vec<DTI, DTO, L, false><<<grid, 64 * kRopeWpb, 0, st>>>(a);
+        const bool multi = a.multi || a.axes > 1;
+        if (a.ff) {
+            if (multi) rope_vec<DTI, DTO, L, true, true><<<grid, 64 * kRopeWpb, 0, st>>>(a);
+            else rope_vec<DTI, DTO, L, false, true><<<grid, 64 * kRopeWpb, 0, st>>>(a);
+        } else {
+            if (multi) rope_vec<DTI, DTO, L, true, false><<<grid, 64 * kRopeWpb, 0, st>>>(a);
+            else rope_vec<DTI, DTO, L, false, false><<<grid, 64 * kRopeWpb, 0, st>>>(a);
+        }
         return check_launch("rope_vec");
     }
 }
@@ -456,6 +466,7 @@ extern "C" SLHIP_API int slhip_rope(int dtype_in, int dtype_out, const slhip_rop
     a.fs = cfg->freq_scale;
     a.af = cfg->attn_factor;
     a.eps = cfg->eps;
+    a.inv_d = (D & (D - 1)) == 0 ? 1.0f / static_cast<float>(D) : 0.0f;
     a.l2b = std::log2(static_cast<double>(cfg->base));
     a.axes = cfg->pos_axes <= 0 ? 1 : cfg->pos_axes;
     if (a.axes > 4) return fail(SLHIP_ERR_INVALID, "rope: at most 4 position axes (got %d)", a.axes);

@@ -200,3 +200,19 @@ def test_rope_multi_axis_general_path(device):
                  sections=[4, 8, 8, 4], per_element=True)
     assert_f32_close(y4, oracle.rope_multi(x, pos4, [4, 8, 8, 4], per_element=True, dims=48, base=1e4),
                      what="four axes, per element")
+
+
+def test_recip_exhaustive(device):
+    """The reciprocal behind the fused q/k-norm scale (hardware reciprocal + one Newton step, division outside
+    [2^-125, 2^125]) equals IEEE 1.0f / s on all 2^32 f32 inputs, and the bare hardware reciprocal does not
+    (a check program built beside the library: tests/recip_exhaustive.hip)."""
+    import subprocess
+    exe = os.path.join(os.path.dirname(GOLDEN), "_bin", "recip_exhaustive")
+    assert os.path.exists(exe), "tests/_bin/recip_exhaustive is not built: run the package build"
+    log("recip exhaustive check program")
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=100)
+    out = r.stdout.split()
+    assert out[0] == "checked" and int(out[1]) == 1 << 32, r.stdout + r.stderr
+    assert int(out[3]) == 0 and int(out[5]) == 0, r.stdout
+    assert int(out[7]) > 0, "the bare reciprocal must differ somewhere: the checker compared nothing"
+    assert r.returncode == 0, r.stdout + r.stderr
