@@ -12,7 +12,7 @@
 // (+0 for q = 0), as the reference's FMA does.
 //
 // Layout: a flat grid of work items, one wavefront each: an item is a chunk of one output row -- CB
-// quantized blocks or STEPS output vectors per lane of a plain table (4096 values by default) -- and each
+// quantized blocks or STEPS output vectors per lane of a plain table (for the quantized formats about 1 KiB of block image, for the plain ones 4096 values) -- and each
 // wave streams its item and exits; the waves of a block never synchronize with each other. Quantized
 // chunks (blocks of 34, 18, 20, 22 or 24 bytes: only 2-byte aligned) are loaded with 16-byte loads into
 // LDS, then each lane decodes VPL consecutive values per output vector, VPL = 16 bytes / output element
@@ -344,10 +344,9 @@ static int env_int(const char* name, int dflt)
 }
 
 // Work-item size (SLHIP_GATHER_ITEM = 0: small, 1: large) and waves per block (SLHIP_GATHER_WPB = 1 or 4).
-// Default: large items (128 quantized blocks or 8 vectors per lane: 4096 values) in 4-wave blocks --
-// measured on MI355X at 16384 x 4096 from a 151936-row table, small items run the quantized formats
-// ~35% slower (each wave then pays a dependent id load for ~0.5 KiB of input), and two items per wave
-// (SLHIP_GATHER_RPW = 2, the second item's loads issued before the first is decoded) 3-4% slower.
+// Default: large items (item_values() for the quantized formats, 8 vectors per lane of a plain table) in
+// 4-wave blocks; two items per wave (SLHIP_GATHER_RPW = 2, the second item's loads issued before the first
+// is decoded) measured 3-4% slower.
 struct GatherShape {
     bool large;
     int wpb;
@@ -371,19 +370,31 @@ static int launch_quant_shape(GatherArgs a, hipStream_t st)
     return check_launch("gather_quant");
 }
 
-// Chunks of 4096 values (large items) or 512 (small ones; only where the chunk is a whole number of
-// 16-byte vectors, which for 256-value blocks of 84, 110 or 210 bytes it is not).
+// Values per work item for a format: the smallest of 1024, 2048 and 4096 values whose block image is at least
+// 1 KiB and a whole number of 16-byte vectors (4096 otherwise). Measured on MI355X at 16384 x 4096 from a
+// 151936-row table: ~1 KiB of random row bytes per wave beats 2 and 4 KiB by 1-3% (Q8_0 at 1024 values:
+// 36.4 against 37.4 us at 4096; Q4_0 at 2048: 31.3-31.6 against 31.8), while smaller items lose (~0.5 KiB:
+// Q4_0 at 1024 values 31.9 us, and 512-value items ~35% slower: each wave pays a dependent id load).
+template <int FMT>
+constexpr int item_values()
+{
+    constexpr int BS = Fmt<FMT>::BS, BB = Fmt<FMT>::BB;
+    for (int v = 1024; v < 4096; v *= 2)
+        if (v % BS == 0 && (v / BS * BB) % 16 == 0 && v / BS * BB >= 1024) return v;
+    return 4096;
+}
+
 template <int FMT, int DTO>
 static int launch_quant(const GatherArgs& a, hipStream_t st)
 {
-    constexpr int CBL = 4096 / Fmt<FMT>::BS, CBS = 512 / Fmt<FMT>::BS;
+    constexpr int CB = item_values<FMT>() / Fmt<FMT>::BS, CBS = 512 / Fmt<FMT>::BS;
     const GatherShape g = gather_shape();
     if constexpr ((CBS * Fmt<FMT>::BB) % 16 == 0) {
         if (!g.large)
             return g.wpb == 1 ? launch_quant_shape<FMT, DTO, CBS, 1, 1>(a, st) : launch_quant_shape<FMT, DTO, CBS, 4, 1>(a, st);
     }
-    if (g.rpw == 2) return launch_quant_shape<FMT, DTO, CBL, 4, 2>(a, st);
-    return g.wpb == 1 ? launch_quant_shape<FMT, DTO, CBL, 1, 1>(a, st) : launch_quant_shape<FMT, DTO, CBL, 4, 1>(a, st);
+    if (g.rpw == 2) return launch_quant_shape<FMT, DTO, CB, 4, 2>(a, st);
+    return g.wpb == 1 ? launch_quant_shape<FMT, DTO, CB, 1, 1>(a, st) : launch_quant_shape<FMT, DTO, CB, 4, 1>(a, st);
 }
 
 template <int FMT, int DTO, int STEPS, int WPB>
