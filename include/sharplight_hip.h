@@ -87,7 +87,26 @@ typedef enum slhip_format {
     SLHIP_FMT_IQ3_XXS = 22, /* 98 bytes  */
     SLHIP_FMT_IQ3_S = 23,   /* 110 bytes */
     SLHIP_FMT_IQ1_S = 24,   /* 50 bytes  */
-    SLHIP_FMT_IQ1_M = 25    /* 56 bytes  */
+    SLHIP_FMT_IQ1_M = 25,   /* 56 bytes  */
+    /* The reference's own formats (src/Sharplight.Core/Tensors/DataType.cs:154-244; decoders Quant.cs:656-718,
+     * Quant.Grouped.cs, Quant.Absmax.cs, Quant.Fp4.cs:86-107, Quant.Fp8.cs): */
+    SLHIP_FMT_Q1_0 = 26,       /* 128 values, 18 bytes: f16 d, u8 bits[16]; bit i of byte j -> value 8j+i = +-d */
+    SLHIP_FMT_Q2_0 = 27,       /* 64 values, 18 bytes: f16 d, u8 qs[16]; 2-bit code i of byte j -> (c-1)*d      */
+    SLHIP_FMT_Q2_0_G128 = 28,  /* 128 values, 34 bytes: the Q2_0 code with one scale per 128                 */
+    SLHIP_FMT_TERN1_G128 = 29, /* 128 values, 28 bytes: base-3 digits in bytes 0..25, f16 d at 26 -> t*d      */
+    SLHIP_FMT_NVFP4_GS = 30,   /* 64 values, 40 bytes: f32 g, UE4M3 d[4], qs[32] -> fp4 * (d*g)              */
+    SLHIP_FMT_Q4Z_G32 = 31,    /* 32 values, 20 bytes: f16 d, f16 z, nibbles -> (q - z)*d                   */
+    SLHIP_FMT_Q4Z_G128 = 32,   /* 128 values, 68 bytes: the same, four 32-value runs                        */
+    SLHIP_FMT_Q8Z_G32 = 33,    /* 32 values, 36 bytes: f16 d, f16 z, u8 q[32] -> (q - z)*d                  */
+    SLHIP_FMT_Q8Z_G128 = 34,   /* 128 values, 132 bytes                                                     */
+    SLHIP_FMT_NF4_B64 = 35,    /* 64 values, 36 bytes: f32 d, nibbles -> NF4[q]*d                           */
+    SLHIP_FMT_FP4_B64 = 36,    /* 64 values, 36 bytes: f32 d, nibbles -> FP4[q]*d                           */
+    SLHIP_FMT_Q8A_G32 = 37,    /* 32 values, 36 bytes: f32 d, i8 q[32] -> q*d*(1/127)                       */
+    SLHIP_FMT_Q2S_G128 = 38,   /* 128 values, 36 bytes: f32 d, u8 qs[32]; byte j: values j, 32+j, 64+j, 96+j */
+    SLHIP_FMT_F8E4M3 = 39,     /* OCP E4M3FN bytes                                                          */
+    SLHIP_FMT_F8E5M2 = 40,     /* E5M2 bytes (the top byte of an IEEE half)                                 */
+    SLHIP_FMT_F8E4M3_B32 = 41, /* 32 values, 36 bytes: f32 d, E4M3 q[32] -> e4m3(q)*d                       */
+    SLHIP_FMT_F8E4M3_B128 = 42 /* 128 values, 132 bytes                                                     */
 } slhip_format;
 
 /* Row-norm kinds (StandardOps RmsNorm / L2Norm / LayerNorm). */
@@ -340,7 +359,8 @@ SLHIP_API int slhip_rope(int dtype_in, int dtype_out, const slhip_rope_tensor* t
  * [V, D] tensor in `format`. dtype_out: F32 or BF16 (f32 values rounded to nearest even). An id outside
  * [0, V) leaves its output row zero and raises SLHIP_ERR_INDEX at the next slhip_stream_sync.
  * Formats: F32, F16, BF16, Q8_0, Q4_0, Q4_1, Q5_0, Q5_1 (D a multiple of 32), Q2_K..Q6_K, IQ4_XS, TQ1_0
- * and TQ2_0 and the grid IQ formats IQ2_XXS..IQ1_M (D a multiple of 256), IQ4_NL and MXFP4 (32), NVFP4 (64).
+ * and TQ2_0 and the grid IQ formats IQ2_XXS..IQ1_M (D a multiple of 256), IQ4_NL and MXFP4 (32), NVFP4 (64),
+ * and the reference's formats Q1_0 .. F8E4M3_B128 (D a multiple of their block size).
  * Replaces: GatherOp (src/Sharplight.Cpu/GatherOp.cs:22-75) with Quant.Dequantize
  * (src/Sharplight.Cpu/Quant.cs:242-446,500-624; Quant.KQuants.cs:36-107), and the Vulkan gather
  * (GraphLowerer.Transformer.cs:133-179, Kernels/data.slang:4-37).

@@ -23,11 +23,14 @@ _LIB_PATH = os.path.join(_HERE, "liboracle.so")
 
 (F32, F16, BF16, Q8_0, Q4_0, Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS, TQ1_0, TQ2_0, MXFP4,
  NVFP4, IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_S, IQ1_M) = range(26)
+# the reference's own formats, numbered like the C ABI
+REF_FORMATS = ["q1_0", "q2_0", "q2_0_g128", "tern1_g128", "nvfp4_gs", "q4z_g32", "q4z_g128", "q8z_g32", "q8z_g128",
+               "nf4_b64", "fp4_b64", "q8a_g32", "q2s_g128", "f8e4m3", "f8e5m2", "f8e4m3_b32", "f8e4m3_b128"]
 FORMATS = {"f32": F32, "f16": F16, "bf16": BF16, "q8_0": Q8_0, "q4_0": Q4_0, "q4_1": Q4_1, "q5_0": Q5_0,
            "q5_1": Q5_1, "q2_k": Q2_K, "q3_k": Q3_K, "q4_k": Q4_K, "q5_k": Q5_K, "q6_k": Q6_K, "iq4_nl": IQ4_NL,
            "iq4_xs": IQ4_XS, "tq1_0": TQ1_0, "tq2_0": TQ2_0, "mxfp4": MXFP4, "nvfp4": NVFP4,
            "iq2_xxs": IQ2_XXS, "iq2_xs": IQ2_XS, "iq2_s": IQ2_S, "iq3_xxs": IQ3_XXS, "iq3_s": IQ3_S, "iq1_s": IQ1_S,
-           "iq1_m": IQ1_M}
+           "iq1_m": IQ1_M, **{n: 26 + i for i, n in enumerate(REF_FORMATS)}}
 ACTS = {"silu": 0, "gelu_tanh": 1, "gelu_erf": 2}
 
 _lib = None
@@ -69,6 +72,8 @@ def _declare(L):
         "orc_mul": (None, [_P, _P, _P, _I64]),
         "orc_unary": (None, [_I, _P, _P, _I64]),
         "orc_erf": (ctypes.c_double, [ctypes.c_double]),
+        "orc_e4m3_value": (_F, [ctypes.c_uint8]),
+        "orc_e5m2_value": (_F, [ctypes.c_uint8]),
         "orc_unary_kind": (None, [_I, _P, _P, _I64, _F, _F]),
         "orc_binary": (None, [_I, _P, _P, _P, _P, _P, _P, _I]),
         "orc_align": (None, [_P, _I, _I, _P]),

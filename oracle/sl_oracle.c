@@ -603,6 +603,14 @@ void orc_rope_multi(const float* x, const int32_t* pos, int axes, const int32_t*
 /* Quant.BlockSize / BlockBytes (src/Sharplight.Cpu/Quant.cs:181-216) for the formats here. */
 static int block_size(int fmt)
 {
+    switch (fmt) {  /* the reference's own formats (Quant.BlockSize, Quant.cs:181-198) */
+    case ORC_Q1_0: case ORC_Q2_0_G128: case ORC_TERN1_G128: case ORC_Q2S_G128: case ORC_Q4Z_G128: case ORC_Q8Z_G128:
+    case ORC_F8E4M3_B128: return 128;
+    case ORC_Q2_0: case ORC_NVFP4_GS: case ORC_NF4_B64: case ORC_FP4_B64: return 64;
+    case ORC_Q4Z_G32: case ORC_Q8Z_G32: case ORC_Q8A_G32: case ORC_F8E4M3_B32: return 32;
+    case ORC_F8E4M3: case ORC_F8E5M2: return 1;
+    default: break;
+    }
     if (fmt == ORC_IQ4_NL || fmt == ORC_MXFP4) return 32;
     if (fmt == ORC_NVFP4) return 64;
     if (fmt >= ORC_Q2_K) return 256;
@@ -636,6 +644,16 @@ static int block_bytes(int fmt)
     case ORC_IQ3_S: return 110;
     case ORC_IQ1_S: return 50;
     case ORC_IQ1_M: return 56;
+    /* Quant.BlockBytes (Quant.cs:200-238) */
+    case ORC_Q1_0: case ORC_Q2_0: return 18;
+    case ORC_Q2_0_G128: return 34;
+    case ORC_TERN1_G128: return 28;
+    case ORC_NVFP4_GS: return 40;
+    case ORC_Q4Z_G32: return 20;
+    case ORC_Q4Z_G128: return 68;
+    case ORC_Q8Z_G32: case ORC_NF4_B64: case ORC_FP4_B64: case ORC_Q8A_G32: case ORC_Q2S_G128: case ORC_F8E4M3_B32: return 36;
+    case ORC_Q8Z_G128: case ORC_F8E4M3_B128: return 132;
+    case ORC_F8E4M3: case ORC_F8E5M2: return 1;
     default: return -1;
     }
 }
@@ -830,6 +848,125 @@ static void iq_block(int fmt, const uint8_t* p, float* dst)
  *  Q6_K  (:584-624): {ql[128], qh[64], int8 scales[16], f16 d}; value = fma(q6, s, -32 s), s = d * scale;
  *  IQ4_NL (:411-425): {f16 d, qs[16]}; value = d * codebook[nibble];
  *  IQ4_XS (:427-446): {f16 d, u16 scales_h, scales_l[4], qs[128]}; value = (d * (ls - 32)) * codebook[nibble]. */
+/* Quant.E4m3ToFloat (Quant.Fp8.cs:37-49): bias 7, exponent 0 subnormal (m * 2^-9), exponent 15 with
+ * mantissa 7 NaN (.NET's float.NaN, then negated for a set sign bit), no infinity. */
+float orc_e4m3_value(uint8_t x)
+{
+    const int exp = (x >> 3) & 0xF, man = x & 7;
+    float mag;
+    if (exp == 0xF && man == 7) mag = u2f(0xFFC00000u);  /* float.NaN */
+    else mag = exp == 0 ? ldexpf((float)man, -9) : ldexpf(1.0f + (float)man / 8.0f, exp - 7);
+    return (x & 0x80) ? -mag : mag;
+}
+
+/* Quant.BuildE5m2 (Quant.Fp8.cs:62-72): the byte as the top half of an IEEE half. */
+float orc_e5m2_value(uint8_t x) { return orc_f16_to_f32((uint16_t)(x << 8)); }
+
+/* Nf4CodeBook / Fp4CodeBook (src/Sharplight.Core/Tensors/Grids/Nf4CodeBook.cs, Fp4CodeBook.cs): format data. */
+static const float kNf4Book[16] = {
+    -1.0f, -0.6961928009986877f, -0.5250730514526367f, -0.39491748809814453f, -0.28444138169288635f, -0.18477343022823334f,
+    -0.09105003625154495f, 0.0f, 0.07958029955625534f, 0.16093020141124725f, 0.24611230194568634f, 0.33791524171829224f,
+    0.44070982933044434f, 0.5626170039176941f, 0.7229568362236023f, 1.0f};
+static const float kFp4Book[16] = {
+    0.0f, 0.0052083334885537624f, 0.6666666865348816f, 1.0f, 0.3333333432674408f, 0.5f, 0.1666666716337204f, 0.25f,
+    0.0f, -0.0052083334885537624f, -0.6666666865348816f, -1.0f, -0.3333333432674408f, -0.5f, -0.1666666716337204f, -0.25f};
+
+static float rd_f32(const uint8_t* p) { float f; memcpy(&f, p, 4); return f; }
+
+/* One block of the reference's own formats, restated from its decoders in their loop order. */
+static void refblock(int fmt, const uint8_t* p, float* dst)
+{
+    switch (fmt) {
+    case ORC_Q1_0: {  /* Quant.Q1_0 (Quant.cs:656-669): lut[byte][i] = bit i ? +1 : -1, times d */
+        const float d = rd_h(p);
+        for (int j = 0; j < 16; j++)
+            for (int i = 0; i < 8; i++) dst[j * 8 + i] = (((p[2 + j] >> i) & 1) ? 1.0f : -1.0f) * d;
+        break;
+    }
+    case ORC_Q2_0: case ORC_Q2_0_G128: {  /* Quant.Q2_0 (Quant.cs:673-686): lut[byte][i] = ((byte >> 2i) & 3) - 1 */
+        const int qb = fmt == ORC_Q2_0 ? 16 : 32;
+        const float d = rd_h(p);
+        for (int j = 0; j < qb; j++)
+            for (int i = 0; i < 4; i++) dst[j * 4 + i] = (float)(((p[2 + j] >> (2 * i)) & 3) - 1) * d;
+        break;
+    }
+    case ORC_TERN1_G128: {  /* Quant.Tern1 (Quant.cs:689-718) */
+        const float d = rd_h(p + 26);
+        for (int m = 0; m < 16; m++)
+            for (int n = 0; n < 5; n++) dst[n * 16 + m] = (float)trit(p[m], n) * d;
+        for (int m = 0; m < 8; m++)
+            for (int n = 0; n < 5; n++) dst[80 + n * 8 + m] = (float)trit(p[16 + m], n) * d;
+        for (int h = 0; h < 2; h++)
+            for (int n = 0; n < 4; n++) dst[120 + n * 2 + h] = (float)trit(p[24 + h], n) * d;
+        break;
+    }
+    case ORC_NVFP4_GS: {  /* Quant.NVFP4_GS (Quant.Fp4.cs:86-107): d = ue4m3 * g, then fp4 * d */
+        const float g = rd_f32(p);
+        for (int sb = 0; sb < 4; sb++) {
+            const float d = ue4m3_half(p[4 + sb]) * g;
+            const uint8_t* q = p + 8 + 8 * sb;
+            for (int j = 0; j < 8; j++) {
+                dst[16 * sb + j] = (float)kFp4Values[q[j] & 0xF] * d;
+                dst[16 * sb + j + 8] = (float)kFp4Values[q[j] >> 4] * d;
+            }
+        }
+        break;
+    }
+    case ORC_Q4Z_G32: case ORC_Q4Z_G128: {  /* Quant.Q4Z (Quant.Grouped.cs:66-83), StoreU8x16Zeroed: (q - z) * d */
+        const int group = fmt == ORC_Q4Z_G32 ? 32 : 128;
+        const float d = rd_h(p), z = rd_h(p + 2);
+        for (int run = 0; run < group / 32; run++)
+            for (int j = 0; j < 16; j++) {
+                const uint8_t q = p[4 + 16 * run + j];
+                dst[32 * run + j] = ((float)(q & 0xF) - z) * d;
+                dst[32 * run + 16 + j] = ((float)(q >> 4) - z) * d;
+            }
+        break;
+    }
+    case ORC_Q8Z_G32: case ORC_Q8Z_G128: {  /* Quant.Q8Z (Quant.Grouped.cs:86-98) */
+        const int group = fmt == ORC_Q8Z_G32 ? 32 : 128;
+        const float d = rd_h(p), z = rd_h(p + 2);
+        for (int j = 0; j < group; j++) dst[j] = ((float)p[4 + j] - z) * d;
+        break;
+    }
+    case ORC_NF4_B64: case ORC_FP4_B64: {  /* Quant.LookupB64 (Quant.Grouped.cs:107-127) */
+        const float* book = fmt == ORC_NF4_B64 ? kNf4Book : kFp4Book;
+        const float d = rd_f32(p);
+        for (int run = 0; run < 2; run++)
+            for (int j = 0; j < 16; j++) {
+                const uint8_t q = p[4 + 16 * run + j];
+                dst[32 * run + j] = book[q & 0xF] * d;
+                dst[32 * run + j + 16] = book[q >> 4] * d;
+            }
+        break;
+    }
+    case ORC_Q8A_G32: {  /* Quant.Q8A_G32 (Quant.Absmax.cs:29-40): q * d * (1/127), left to right */
+        const float d = rd_f32(p);
+        for (int j = 0; j < 32; j++) dst[j] = (float)(int8_t)p[4 + j] * d * 7.874015718698502e-3f;
+        break;
+    }
+    case ORC_Q2S_G128: {  /* Quant.Q2S_G128 (Quant.Absmax.cs:43-57) */
+        const float d = rd_f32(p);
+        for (int j = 0; j < 32; j++) {
+            dst[j] = (float)(((p[4 + j] >> 6) & 3) - 1) * d;
+            dst[32 + j] = (float)(((p[4 + j] >> 4) & 3) - 1) * d;
+            dst[64 + j] = (float)(((p[4 + j] >> 2) & 3) - 1) * d;
+            dst[96 + j] = (float)((p[4 + j] & 3) - 1) * d;
+        }
+        break;
+    }
+    case ORC_F8E4M3: dst[0] = orc_e4m3_value(p[0]) * 1.0f; break;  /* Quant.Lookup with scale 1 (Quant.Fp8.cs:125-137) */
+    case ORC_F8E5M2: dst[0] = orc_e5m2_value(p[0]) * 1.0f; break;
+    case ORC_F8E4M3_B32: case ORC_F8E4M3_B128: {  /* Quant.ScaledE4m3Blocks (Quant.Fp8.cs:112-122) */
+        const int block = fmt == ORC_F8E4M3_B32 ? 32 : 128;
+        const float d = rd_f32(p);
+        for (int j = 0; j < block; j++) dst[j] = orc_e4m3_value(p[4 + j]) * d;
+        break;
+    }
+    default: break;
+    }
+}
+
 static void kblock(int fmt, const uint8_t* p, float* dst)
 {
     switch (fmt) {
@@ -967,7 +1104,9 @@ static void kblock(int fmt, const uint8_t* p, float* dst)
         }
         break;
     }
-    default: break;
+    default:
+        refblock(fmt, p, dst);
+        break;
     }
 }
 

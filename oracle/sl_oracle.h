@@ -24,7 +24,14 @@ extern "C" {
 enum { ORC_F32 = 0, ORC_F16 = 1, ORC_BF16 = 2, ORC_Q8_0 = 3, ORC_Q4_0 = 4, ORC_Q4_1 = 5, ORC_Q5_0 = 6, ORC_Q5_1 = 7,
        ORC_Q2_K = 8, ORC_Q3_K = 9, ORC_Q4_K = 10, ORC_Q5_K = 11, ORC_Q6_K = 12, ORC_IQ4_NL = 13, ORC_IQ4_XS = 14,
        ORC_TQ1_0 = 15, ORC_TQ2_0 = 16, ORC_MXFP4 = 17, ORC_NVFP4 = 18, ORC_IQ2_XXS = 19, ORC_IQ2_XS = 20,
-       ORC_IQ2_S = 21, ORC_IQ3_XXS = 22, ORC_IQ3_S = 23, ORC_IQ1_S = 24, ORC_IQ1_M = 25 };
+       ORC_IQ2_S = 21, ORC_IQ3_XXS = 22, ORC_IQ3_S = 23, ORC_IQ1_S = 24, ORC_IQ1_M = 25,
+       /* the reference's own formats */
+       ORC_Q1_0 = 26, ORC_Q2_0 = 27, ORC_Q2_0_G128 = 28, ORC_TERN1_G128 = 29, ORC_NVFP4_GS = 30, ORC_Q4Z_G32 = 31,
+       ORC_Q4Z_G128 = 32, ORC_Q8Z_G32 = 33, ORC_Q8Z_G128 = 34, ORC_NF4_B64 = 35, ORC_FP4_B64 = 36, ORC_Q8A_G32 = 37,
+       ORC_Q2S_G128 = 38, ORC_F8E4M3 = 39, ORC_F8E5M2 = 40, ORC_F8E4M3_B32 = 41, ORC_F8E4M3_B128 = 42 };
+/* E4M3FN / E5M2 byte -> f32 (Quant.E4m3ToFloat, Quant.BuildE5m2) */
+float orc_e4m3_value(uint8_t x);
+float orc_e5m2_value(uint8_t x);
 
 /* ---- scalar conversions (Simd.cs:518-540, Quant.cs:371-381) ---- */
 uint16_t orc_f32_to_bf16(float f);

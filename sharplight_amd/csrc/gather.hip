@@ -234,6 +234,8 @@ __global__ __launch_bounds__(256) void gather_scalar(GatherArgs a, int fmt)
             const int k = static_cast<int>(j % 32);
             auto kv = [&](auto fmt_tag) {  // one value of a K-quant or codebook block
                 constexpr int F = decltype(fmt_tag)::value;
+                if constexpr (F == SLHIP_FMT_F8E4M3) return e4m3_value(p[j]);  // one byte per value: no 4-byte group
+                if constexpr (F == SLHIP_FMT_F8E5M2) return e5m2_value(p[j]);
                 const int64_t kb = j / Fmt<F>::BS;
                 const int kk = static_cast<int>(j % Fmt<F>::BS);
                 float f4[4];
@@ -259,6 +261,23 @@ __global__ __launch_bounds__(256) void gather_scalar(GatherArgs a, int fmt)
             case SLHIP_FMT_IQ3_S: v = kv(std::integral_constant<int, SLHIP_FMT_IQ3_S>{}); break;
             case SLHIP_FMT_IQ1_S: v = kv(std::integral_constant<int, SLHIP_FMT_IQ1_S>{}); break;
             case SLHIP_FMT_IQ1_M: v = kv(std::integral_constant<int, SLHIP_FMT_IQ1_M>{}); break;
+            case SLHIP_FMT_Q1_0: v = kv(std::integral_constant<int, SLHIP_FMT_Q1_0>{}); break;
+            case SLHIP_FMT_Q2_0: v = kv(std::integral_constant<int, SLHIP_FMT_Q2_0>{}); break;
+            case SLHIP_FMT_Q2_0_G128: v = kv(std::integral_constant<int, SLHIP_FMT_Q2_0_G128>{}); break;
+            case SLHIP_FMT_TERN1_G128: v = kv(std::integral_constant<int, SLHIP_FMT_TERN1_G128>{}); break;
+            case SLHIP_FMT_NVFP4_GS: v = kv(std::integral_constant<int, SLHIP_FMT_NVFP4_GS>{}); break;
+            case SLHIP_FMT_Q4Z_G32: v = kv(std::integral_constant<int, SLHIP_FMT_Q4Z_G32>{}); break;
+            case SLHIP_FMT_Q4Z_G128: v = kv(std::integral_constant<int, SLHIP_FMT_Q4Z_G128>{}); break;
+            case SLHIP_FMT_Q8Z_G32: v = kv(std::integral_constant<int, SLHIP_FMT_Q8Z_G32>{}); break;
+            case SLHIP_FMT_Q8Z_G128: v = kv(std::integral_constant<int, SLHIP_FMT_Q8Z_G128>{}); break;
+            case SLHIP_FMT_NF4_B64: v = kv(std::integral_constant<int, SLHIP_FMT_NF4_B64>{}); break;
+            case SLHIP_FMT_FP4_B64: v = kv(std::integral_constant<int, SLHIP_FMT_FP4_B64>{}); break;
+            case SLHIP_FMT_Q8A_G32: v = kv(std::integral_constant<int, SLHIP_FMT_Q8A_G32>{}); break;
+            case SLHIP_FMT_Q2S_G128: v = kv(std::integral_constant<int, SLHIP_FMT_Q2S_G128>{}); break;
+            case SLHIP_FMT_F8E4M3: v = kv(std::integral_constant<int, SLHIP_FMT_F8E4M3>{}); break;
+            case SLHIP_FMT_F8E5M2: v = kv(std::integral_constant<int, SLHIP_FMT_F8E5M2>{}); break;
+            case SLHIP_FMT_F8E4M3_B32: v = kv(std::integral_constant<int, SLHIP_FMT_F8E4M3_B32>{}); break;
+            case SLHIP_FMT_F8E4M3_B128: v = kv(std::integral_constant<int, SLHIP_FMT_F8E4M3_B128>{}); break;
             case SLHIP_FMT_F32: {
                 uint32_t u = p[4 * j] | (p[4 * j + 1] << 8) | (p[4 * j + 2] << 16) | (static_cast<uint32_t>(p[4 * j + 3]) << 24);
                 v = __uint_as_float(u);
@@ -322,6 +341,23 @@ static int block_bytes(int fmt)
     case SLHIP_FMT_IQ3_S: return 110;
     case SLHIP_FMT_IQ1_S: return 50;
     case SLHIP_FMT_IQ1_M: return 56;
+    case SLHIP_FMT_Q1_0: return 18;
+    case SLHIP_FMT_Q2_0: return 18;
+    case SLHIP_FMT_Q2_0_G128: return 34;
+    case SLHIP_FMT_TERN1_G128: return 28;
+    case SLHIP_FMT_NVFP4_GS: return 40;
+    case SLHIP_FMT_Q4Z_G32: return 20;
+    case SLHIP_FMT_Q4Z_G128: return 68;
+    case SLHIP_FMT_Q8Z_G32: return 36;
+    case SLHIP_FMT_Q8Z_G128: return 132;
+    case SLHIP_FMT_NF4_B64: return 36;
+    case SLHIP_FMT_FP4_B64: return 36;
+    case SLHIP_FMT_Q8A_G32: return 36;
+    case SLHIP_FMT_Q2S_G128: return 36;
+    case SLHIP_FMT_F8E4M3: return 1;
+    case SLHIP_FMT_F8E5M2: return 1;
+    case SLHIP_FMT_F8E4M3_B32: return 36;
+    case SLHIP_FMT_F8E4M3_B128: return 132;
     default: return -1;
     }
 }
@@ -333,6 +369,10 @@ static int block_values(int fmt)
     case SLHIP_FMT_Q8_0: case SLHIP_FMT_Q4_0: case SLHIP_FMT_Q4_1: case SLHIP_FMT_Q5_0: case SLHIP_FMT_Q5_1:
     case SLHIP_FMT_IQ4_NL: case SLHIP_FMT_MXFP4: return 32;
     case SLHIP_FMT_NVFP4: return 64;
+    case SLHIP_FMT_Q1_0: case SLHIP_FMT_Q2_0_G128: case SLHIP_FMT_TERN1_G128: case SLHIP_FMT_Q4Z_G128: case SLHIP_FMT_Q8Z_G128: case SLHIP_FMT_Q2S_G128: case SLHIP_FMT_F8E4M3_B128: return 128;
+    case SLHIP_FMT_Q2_0: case SLHIP_FMT_NVFP4_GS: case SLHIP_FMT_NF4_B64: case SLHIP_FMT_FP4_B64: return 64;
+    case SLHIP_FMT_Q4Z_G32: case SLHIP_FMT_Q8Z_G32: case SLHIP_FMT_Q8A_G32: case SLHIP_FMT_F8E4M3_B32: return 32;
+    case SLHIP_FMT_F8E4M3: case SLHIP_FMT_F8E5M2: return 1;
     default: return 256;
     }
 }
@@ -450,6 +490,23 @@ static int dispatch(int fmt, GatherArgs a, hipStream_t st)
         case SLHIP_FMT_IQ3_S: return launch_quant<SLHIP_FMT_IQ3_S, DTO>(a, st);
         case SLHIP_FMT_IQ1_S: return launch_quant<SLHIP_FMT_IQ1_S, DTO>(a, st);
         case SLHIP_FMT_IQ1_M: return launch_quant<SLHIP_FMT_IQ1_M, DTO>(a, st);
+        case SLHIP_FMT_Q1_0: return launch_quant<SLHIP_FMT_Q1_0, DTO>(a, st);
+        case SLHIP_FMT_Q2_0: return launch_quant<SLHIP_FMT_Q2_0, DTO>(a, st);
+        case SLHIP_FMT_Q2_0_G128: return launch_quant<SLHIP_FMT_Q2_0_G128, DTO>(a, st);
+        case SLHIP_FMT_TERN1_G128: return launch_quant<SLHIP_FMT_TERN1_G128, DTO>(a, st);
+        case SLHIP_FMT_NVFP4_GS: return launch_quant<SLHIP_FMT_NVFP4_GS, DTO>(a, st);
+        case SLHIP_FMT_Q4Z_G32: return launch_quant<SLHIP_FMT_Q4Z_G32, DTO>(a, st);
+        case SLHIP_FMT_Q4Z_G128: return launch_quant<SLHIP_FMT_Q4Z_G128, DTO>(a, st);
+        case SLHIP_FMT_Q8Z_G32: return launch_quant<SLHIP_FMT_Q8Z_G32, DTO>(a, st);
+        case SLHIP_FMT_Q8Z_G128: return launch_quant<SLHIP_FMT_Q8Z_G128, DTO>(a, st);
+        case SLHIP_FMT_NF4_B64: return launch_quant<SLHIP_FMT_NF4_B64, DTO>(a, st);
+        case SLHIP_FMT_FP4_B64: return launch_quant<SLHIP_FMT_FP4_B64, DTO>(a, st);
+        case SLHIP_FMT_Q8A_G32: return launch_quant<SLHIP_FMT_Q8A_G32, DTO>(a, st);
+        case SLHIP_FMT_Q2S_G128: return launch_quant<SLHIP_FMT_Q2S_G128, DTO>(a, st);
+        case SLHIP_FMT_F8E4M3: return launch_quant<SLHIP_FMT_F8E4M3, DTO>(a, st);
+        case SLHIP_FMT_F8E5M2: return launch_quant<SLHIP_FMT_F8E5M2, DTO>(a, st);
+        case SLHIP_FMT_F8E4M3_B32: return launch_quant<SLHIP_FMT_F8E4M3_B32, DTO>(a, st);
+        case SLHIP_FMT_F8E4M3_B128: return launch_quant<SLHIP_FMT_F8E4M3_B128, DTO>(a, st);
         case SLHIP_FMT_F16: return launch_plain<SLHIP_FMT_F16, DTO>(a, st);
         case SLHIP_FMT_BF16: return launch_plain<SLHIP_FMT_BF16, DTO>(a, st);
         case SLHIP_FMT_F32: return launch_plain<SLHIP_FMT_F32, DTO>(a, st);

@@ -121,23 +121,23 @@ TypeDesc type_desc(int id)
     case 34: return t("tq1_0", 256, 54, SLHIP_FMT_TQ1_0);
     case 35: return t("tq2_0", 256, 66, SLHIP_FMT_TQ2_0);
     case kI2S: {  // BitNet's I2_S: read as Q2S_G128 blocks (f32 scale + 32 code bytes)
-        TypeDesc d = t("q2s_g128", 128, kI2sBlock);
+        TypeDesc d = t("q2s_g128", 128, kI2sBlock, SLHIP_FMT_Q2S_G128);
         d.layout = Layout::I2S;
         return d;
     }
     case 39: return t("mxfp4", 32, 17, SLHIP_FMT_MXFP4);
     case 40: return t("nvfp4", 64, 36, SLHIP_FMT_NVFP4);
-    case 41: return t("q1_0", 128, 18);
-    case 42: return t("q2_0", 64, 18);
-    case 43: return t("f8_e4m3", 1, 1);
+    case 41: return t("q1_0", 128, 18, SLHIP_FMT_Q1_0);
+    case 42: return t("q2_0", 64, 18, SLHIP_FMT_Q2_0);
+    case 43: return t("f8_e4m3", 1, 1, SLHIP_FMT_F8E4M3);
     case 64: case 65: case 66: {  // unsloth's narrow IQ1 types: read as IQ1_S blocks
         TypeDesc d = t("iq1_s", 256, kWideIq1Bytes, SLHIP_FMT_IQ1_S);
         d.layout = Layout::NarrowIq1;
         d.stored_block = id == 64 ? 46 : id == 65 ? 42 : 38;
         return d;
     }
-    case 142: return t("q2_0_g128", 128, 34);   // PrismML PQ2_0
-    case 143: return t("tern1_g128", 128, 28);  // PrismML PTQ1_0
+    case 142: return t("q2_0_g128", 128, 34, SLHIP_FMT_Q2_0_G128);   // PrismML PQ2_0
+    case 143: return t("tern1_g128", 128, 28, SLHIP_FMT_TERN1_G128);  // PrismML PTQ1_0
     case 144: return t("trellis_v4k8_g128", 128, 34);
     case 145: return t("trellis_v4k6_g128", 128, 26);
     case 146: return t("trellis_v4k7_g128", 128, 30);

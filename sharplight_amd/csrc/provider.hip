@@ -66,7 +66,7 @@ void check(int st)
 // ---- graph ---------------------------------------------------------------------------------------------
 
 enum class DType { F32, F16, BF16, I32, Q8_0, Q4_0, Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS, TQ1_0, TQ2_0, MXFP4, NVFP4,
-                   IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_S, IQ1_M };
+                   IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_S, IQ1_M, Q1_0, Q2_0, Q2_0_G128, TERN1_G128, NVFP4_GS, Q4Z_G32, Q4Z_G128, Q8Z_G32, Q8Z_G128, NF4_B64, FP4_B64, Q8A_G32, Q2S_G128, F8E4M3, F8E5M2, F8E4M3_B32, F8E4M3_B128 };
 
 struct TypeInfo {
     const char* name;
@@ -84,6 +84,24 @@ const TypeInfo kTypes[] = {
     {"mxfp4", DType::MXFP4, 32, 17}, {"nvfp4", DType::NVFP4, 64, 36}, {"iq2_xxs", DType::IQ2_XXS, 256, 66},
     {"iq2_xs", DType::IQ2_XS, 256, 74}, {"iq2_s", DType::IQ2_S, 256, 82}, {"iq3_xxs", DType::IQ3_XXS, 256, 98},
     {"iq3_s", DType::IQ3_S, 256, 110}, {"iq1_s", DType::IQ1_S, 256, 50}, {"iq1_m", DType::IQ1_M, 256, 56},
+    // the reference's own formats (src/Sharplight.Core/Tensors/DataType.cs:154-244)
+    {"q1_0", DType::Q1_0, 128, 18},
+    {"q2_0", DType::Q2_0, 64, 18},
+    {"q2_0_g128", DType::Q2_0_G128, 128, 34},
+    {"tern1_g128", DType::TERN1_G128, 128, 28},
+    {"nvfp4_gs", DType::NVFP4_GS, 64, 40},
+    {"q4z_g32", DType::Q4Z_G32, 32, 20},
+    {"q4z_g128", DType::Q4Z_G128, 128, 68},
+    {"q8z_g32", DType::Q8Z_G32, 32, 36},
+    {"q8z_g128", DType::Q8Z_G128, 128, 132},
+    {"nf4_b64", DType::NF4_B64, 64, 36},
+    {"fp4_b64", DType::FP4_B64, 64, 36},
+    {"q8a_g32", DType::Q8A_G32, 32, 36},
+    {"q2s_g128", DType::Q2S_G128, 128, 36},
+    {"f8e4m3", DType::F8E4M3, 1, 1},
+    {"f8e5m2", DType::F8E5M2, 1, 1},
+    {"f8e4m3_b32", DType::F8E4M3_B32, 32, 36},
+    {"f8e4m3_b128", DType::F8E4M3_B128, 128, 132},
 };
 
 const TypeInfo& type_info(DType t)
@@ -134,6 +152,23 @@ int format_code(DType t)
     case DType::IQ3_S: return SLHIP_FMT_IQ3_S;
     case DType::IQ1_S: return SLHIP_FMT_IQ1_S;
     case DType::IQ1_M: return SLHIP_FMT_IQ1_M;
+    case DType::Q1_0: return SLHIP_FMT_Q1_0;
+    case DType::Q2_0: return SLHIP_FMT_Q2_0;
+    case DType::Q2_0_G128: return SLHIP_FMT_Q2_0_G128;
+    case DType::TERN1_G128: return SLHIP_FMT_TERN1_G128;
+    case DType::NVFP4_GS: return SLHIP_FMT_NVFP4_GS;
+    case DType::Q4Z_G32: return SLHIP_FMT_Q4Z_G32;
+    case DType::Q4Z_G128: return SLHIP_FMT_Q4Z_G128;
+    case DType::Q8Z_G32: return SLHIP_FMT_Q8Z_G32;
+    case DType::Q8Z_G128: return SLHIP_FMT_Q8Z_G128;
+    case DType::NF4_B64: return SLHIP_FMT_NF4_B64;
+    case DType::FP4_B64: return SLHIP_FMT_FP4_B64;
+    case DType::Q8A_G32: return SLHIP_FMT_Q8A_G32;
+    case DType::Q2S_G128: return SLHIP_FMT_Q2S_G128;
+    case DType::F8E4M3: return SLHIP_FMT_F8E4M3;
+    case DType::F8E5M2: return SLHIP_FMT_F8E5M2;
+    case DType::F8E4M3_B32: return SLHIP_FMT_F8E4M3_B32;
+    case DType::F8E4M3_B128: return SLHIP_FMT_F8E4M3_B128;
     default: unsupported("gather table type");
     }
 }

@@ -41,6 +41,56 @@ template <> struct Fmt<SLHIP_FMT_IQ3_XXS> { static constexpr int BB = 98, BS = 2
 template <> struct Fmt<SLHIP_FMT_IQ3_S> { static constexpr int BB = 110, BS = 256, QS = 0, QH = -1; static constexpr bool M = false, K = true; static constexpr int OFF = 0; };
 template <> struct Fmt<SLHIP_FMT_IQ1_S> { static constexpr int BB = 50, BS = 256, QS = 0, QH = -1; static constexpr bool M = false, K = true; static constexpr int OFF = 0; };
 template <> struct Fmt<SLHIP_FMT_IQ1_M> { static constexpr int BB = 56, BS = 256, QS = 0, QH = -1; static constexpr bool M = false, K = true; static constexpr int OFF = 0; };
+// The reference's own formats (src/Sharplight.Core/Tensors/DataType.cs:154-244), all decoded by decode_k.
+#define SLHIP_KFMT(F, bb, bs) \
+    template <> struct Fmt<F> { static constexpr int BB = bb, BS = bs, QS = 0, QH = -1; static constexpr bool M = false, K = true; static constexpr int OFF = 0; };
+SLHIP_KFMT(SLHIP_FMT_Q1_0, 18, 128)
+SLHIP_KFMT(SLHIP_FMT_Q2_0, 18, 64)
+SLHIP_KFMT(SLHIP_FMT_Q2_0_G128, 34, 128)
+SLHIP_KFMT(SLHIP_FMT_TERN1_G128, 28, 128)
+SLHIP_KFMT(SLHIP_FMT_NVFP4_GS, 40, 64)
+SLHIP_KFMT(SLHIP_FMT_Q4Z_G32, 20, 32)
+SLHIP_KFMT(SLHIP_FMT_Q4Z_G128, 68, 128)
+SLHIP_KFMT(SLHIP_FMT_Q8Z_G32, 36, 32)
+SLHIP_KFMT(SLHIP_FMT_Q8Z_G128, 132, 128)
+SLHIP_KFMT(SLHIP_FMT_NF4_B64, 36, 64)
+SLHIP_KFMT(SLHIP_FMT_FP4_B64, 36, 64)
+SLHIP_KFMT(SLHIP_FMT_Q8A_G32, 36, 32)
+SLHIP_KFMT(SLHIP_FMT_Q2S_G128, 36, 128)
+SLHIP_KFMT(SLHIP_FMT_F8E4M3, 1, 1)
+SLHIP_KFMT(SLHIP_FMT_F8E5M2, 1, 1)
+SLHIP_KFMT(SLHIP_FMT_F8E4M3_B32, 36, 32)
+SLHIP_KFMT(SLHIP_FMT_F8E4M3_B128, 132, 128)
+#undef SLHIP_KFMT
+
+// The 16-entry code books of NF4_B64 and FP4_B64 (the f32 values bitsandbytes stores as quant_map, as the
+// reference lists them: src/Sharplight.Core/Tensors/Grids/Nf4CodeBook.cs, Fp4CodeBook.cs). Format data;
+// plain device globals, per-lane loads (see iq_grids.h).
+SLHIP_GRID_QUAL const float kNf4Values[16] = {
+    -1.0f, -0.6961928009986877f, -0.5250730514526367f, -0.39491748809814453f, -0.28444138169288635f, -0.18477343022823334f,
+    -0.09105003625154495f, 0.0f, 0.07958029955625534f, 0.16093020141124725f, 0.24611230194568634f, 0.33791524171829224f,
+    0.44070982933044434f, 0.5626170039176941f, 0.7229568362236023f, 1.0f};
+SLHIP_GRID_QUAL const float kFp4Values[16] = {
+    0.0f, 0.0052083334885537624f, 0.6666666865348816f, 1.0f, 0.3333333432674408f, 0.5f, 0.1666666716337204f, 0.25f,
+    0.0f, -0.0052083334885537624f, -0.6666666865348816f, -1.0f, -0.3333333432674408f, -0.5f, -0.1666666716337204f, -0.25f};
+
+constexpr bool is_reference_fmt(int f) { return f >= SLHIP_FMT_Q1_0 && f <= SLHIP_FMT_F8E4M3_B128; }
+
+// An OCP E4M3FN byte as f32 (exact): bias 7, exponent 0 subnormal (m * 2^-9), 0x7F and 0xFF NaN, no infinity
+// (Quant.E4m3ToFloat, src/Sharplight.Cpu/Quant.Fp8.cs:37-49).
+__device__ __forceinline__ float e4m3_value(uint32_t x)
+{
+    const uint32_t e = (x >> 3) & 0xFu, m = x & 7u, sign = (x & 0x80u) << 24;
+    if (e == 0xFu && m == 7u) return __uint_as_float(0x7FC00000u | sign);
+    const uint32_t mag = e == 0 ? __float_as_uint(static_cast<float>(m) * 0x1p-9f) : ((e + 120u) << 23) | (m << 20);
+    return __uint_as_float(mag | sign);
+}
+
+// An E5M2 byte: the top byte of an IEEE half (Quant.BuildE5m2, Quant.Fp8.cs:62-72).
+__device__ __forceinline__ float e5m2_value(uint32_t x)
+{
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(x << 8)));
+}
 
 constexpr bool is_grid_iq(int f)
 {
@@ -323,6 +373,123 @@ __device__ __forceinline__ void iq_group(const B& b, int o, int g, uint2& gv, ui
     }
 }
 
+// N (4 or 8) consecutive values k .. k+N-1 (k a multiple of N) of a block of the reference's own formats at
+// byte offset o, in the reference's arithmetic (one f32 rounding per product, subtractions not fused).
+template <int FMT, int N, class B>
+__device__ __forceinline__ void decode_ref(const B& b, int o, int k, float* f)
+{
+    auto byte_at = [&](int off) { return b.u8(off); };
+    if constexpr (FMT == SLHIP_FMT_Q1_0) {
+        // bit i of byte j is value 8j + i: +d when set, -d when clear (Quant.Q1_0, Quant.cs:656-669)
+        const float d = b.h(o);
+        const uint32_t bits = byte_at(o + 2 + k / 8) >> (k % 8);
+#pragma unroll
+        for (int e = 0; e < N; e++) f[e] = __fmul_rn((bits >> e) & 1u ? 1.0f : -1.0f, d);
+    } else if constexpr (FMT == SLHIP_FMT_Q2_0 || FMT == SLHIP_FMT_Q2_0_G128) {
+        // byte j holds values 4j .. 4j+3, value 4j+i in bits 2i, 2i+1; (code - 1) * d (Quant.Q2_0, Quant.cs:673-686)
+        const float d = b.h(o);
+        const uint32_t w = N == 8 ? b.u16(o + 2 + k / 4) : byte_at(o + 2 + k / 4);
+#pragma unroll
+        for (int e = 0; e < N; e++) f[e] = __fmul_rn(static_cast<float>(static_cast<int>((w >> (2 * e)) & 3u) - 1), d);
+    } else if constexpr (FMT == SLHIP_FMT_TERN1_G128) {
+        // digit n of byte m: values n*16 + m (bytes 0..15), 80 + n*8 + m (bytes 16..23), 120 + 2n + h (bytes 24, 25);
+        // digit times d (Quant.Tern1, Quant.cs:689-718)
+        const float d = b.h(o + 26);
+        if (k < 120) {
+            const bool a = k < 80;
+            const int n = a ? k / 16 : (k - 80) / 8;
+            const int m = a ? k % 16 : 16 + (k - 80) % 8;
+#pragma unroll
+            for (int e = 0; e < N; e++) f[e] = __fmul_rn(static_cast<float>(trit(byte_at(o + m + e), n)), d);
+        } else {
+#pragma unroll
+            for (int e = 0; e < N; e++) {
+                const int r = k - 120 + e;
+                f[e] = __fmul_rn(static_cast<float>(trit(byte_at(o + 24 + r % 2), r / 2)), d);
+            }
+        }
+    } else if constexpr (FMT == SLHIP_FMT_NVFP4_GS) {
+        // {f32 g; u8 d[4]; u8 qs[32]}: the sub-block multiplier UE4M3 * g rounded once, then times the doubled
+        // E2M1 code, as NVFP4 (Quant.NVFP4_GS, Quant.Fp4.cs:86-107)
+        const int sb = k / 16, i = k % 16;
+        const float d = __fmul_rn(ue4m3_half(byte_at(o + 4 + sb)), __uint_as_float(b.u32(o)));
+        uint32_t w[N / 4];
+#pragma unroll
+        for (int x = 0; x < N / 4; x++) w[x] = fp4_lookup4(((i >= 8 ? b.u32(o + 8 + 8 * sb + i % 8 + 4 * x) >> 4 : b.u32(o + 8 + 8 * sb + i % 8 + 4 * x))) & 0x0F0F0F0Fu);
+#pragma unroll
+        for (int e = 0; e < N; e++) f[e] = __fmul_rn(static_cast<float>(static_cast<int8_t>((w[e >> 2] >> (8 * (e & 3))) & 0xFFu)), d);
+    } else if constexpr (FMT == SLHIP_FMT_Q4Z_G32 || FMT == SLHIP_FMT_Q4Z_G128 || FMT == SLHIP_FMT_NF4_B64 ||
+                         FMT == SLHIP_FMT_FP4_B64) {
+        // 32-value runs of 16 code bytes: value j the low nibble of byte j, j + 16 the high nibble.
+        // Q4Z: {f16 d; f16 z; codes} -> (q - z) * d (Quant.Q4Z, Quant.Grouped.cs:66-83; Quant.StoreU8x16Zeroed,
+        // Quant.Absmax.cs:13-23); NF4/FP4: {f32 d; codes} -> book[q] * d (Quant.LookupB64, Quant.Grouped.cs:107-127)
+        constexpr bool Z = FMT == SLHIP_FMT_Q4Z_G32 || FMT == SLHIP_FMT_Q4Z_G128;
+        const int run = k / 32, i = k % 32;
+        const int qo = o + 4 + 16 * run + i % 16;
+#pragma unroll
+        for (int x = 0; x < N / 4; x++) {
+            const uint32_t w = (i >= 16 ? b.u32(qo + 4 * x) >> 4 : b.u32(qo + 4 * x)) & 0x0F0F0F0Fu;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const uint32_t q = (w >> (8 * e)) & 0xFFu;
+                if constexpr (Z) {
+                    f[4 * x + e] = __fmul_rn(__fsub_rn(static_cast<float>(q), b.h(o + 2)), b.h(o));
+                } else {
+                    const float book = FMT == SLHIP_FMT_NF4_B64 ? kNf4Values[q] : kFp4Values[q];
+                    f[4 * x + e] = __fmul_rn(book, __uint_as_float(b.u32(o)));
+                }
+            }
+        }
+    } else if constexpr (FMT == SLHIP_FMT_Q8Z_G32 || FMT == SLHIP_FMT_Q8Z_G128) {
+        // {f16 d; f16 z; u8 q[group]} -> (q - z) * d (Quant.Q8Z, Quant.Grouped.cs:86-98)
+        const float d = b.h(o), z = b.h(o + 2);
+#pragma unroll
+        for (int x = 0; x < N / 4; x++) {
+            const uint32_t w = b.u32(o + 4 + k + 4 * x);
+#pragma unroll
+            for (int e = 0; e < 4; e++) f[4 * x + e] = __fmul_rn(__fsub_rn(static_cast<float>((w >> (8 * e)) & 0xFFu), z), d);
+        }
+    } else if constexpr (FMT == SLHIP_FMT_Q8A_G32) {
+        // {f32 d; i8 q[32]} -> (q * d) * (1/127 as f32) (Quant.Q8A_G32, Quant.Absmax.cs:29-40)
+        const float d = __uint_as_float(b.u32(o));
+#pragma unroll
+        for (int x = 0; x < N / 4; x++) {
+            const uint32_t w = b.u32(o + 4 + k + 4 * x);
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                f[4 * x + e] = __fmul_rn(__fmul_rn(static_cast<float>(static_cast<int8_t>((w >> (8 * e)) & 0xFFu)), d),
+                                         7.874015718698502e-3f);
+        }
+    } else if constexpr (FMT == SLHIP_FMT_Q2S_G128) {
+        // {f32 d; u8 qs[32]}: byte j holds values j, 32 + j, 64 + j, 96 + j in bits 6, 4, 2, 0 -> (code - 1) * d
+        // (Quant.Q2S_G128, Quant.Absmax.cs:43-57)
+        const float d = __uint_as_float(b.u32(o));
+        const int sh = 6 - 2 * (k / 32);
+#pragma unroll
+        for (int x = 0; x < N / 4; x++) {
+            const uint32_t w = b.u32(o + 4 + k % 32 + 4 * x);
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                f[4 * x + e] = __fmul_rn(static_cast<float>(static_cast<int>((w >> (8 * e + sh)) & 3u) - 1), d);
+        }
+    } else {
+        // FP8: plain E4M3 / E5M2 bytes (times 1), or {f32 d; E4M3 q[block]} -> e4m3(q) * d
+        // (Quant.DequantizeFp8 / ScaledE4m3Blocks / Lookup, Quant.Fp8.cs:78-137)
+        constexpr bool SCALED = FMT == SLHIP_FMT_F8E4M3_B32 || FMT == SLHIP_FMT_F8E4M3_B128;
+        const float d = SCALED ? __uint_as_float(b.u32(o)) : 1.0f;
+        const int qo = SCALED ? o + 4 + k : o + k;
+#pragma unroll
+        for (int x = 0; x < N / 4; x++) {
+            const uint32_t w = b.u32(qo + 4 * x);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const uint32_t q = (w >> (8 * e)) & 0xFFu;
+                f[4 * x + e] = __fmul_rn(FMT == SLHIP_FMT_F8E5M2 ? e5m2_value(q) : e4m3_value(q), d);
+            }
+        }
+    }
+}
+
 // N (4 or 8) consecutive values k .. k+N-1 (k a multiple of N) of the K-quant or codebook block at byte
 // offset o, decoded with the reference's arithmetic (src/Sharplight.Cpu/Quant.cs:407-446,500-624,
 // Quant.KQuants.cs:36-107): the N values share one sub-block scale.
@@ -467,6 +634,8 @@ __device__ __forceinline__ void decode_k(const B& b, int o, int k, float* f)
                 f[e] = __fmul_rn(static_cast<float>(trit((qh >> (8 * (r % 4))) & 0xFFu, r / 4)), d);
             }
         }
+    } else if constexpr (is_reference_fmt(FMT)) {
+        decode_ref<FMT, N>(b, o, k, f);
     } else {  // IQ4_NL, IQ4_XS
         float dl;
         int qo, i;

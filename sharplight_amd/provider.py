@@ -26,7 +26,11 @@ BLOCKS = {"q8_0": (32, 34), "q4_0": (32, 18), "q4_1": (32, 20), "q5_0": (32, 22)
           "q2_k": (256, 84), "q3_k": (256, 110), "q4_k": (256, 144), "q5_k": (256, 176), "q6_k": (256, 210),
           "iq4_nl": (32, 18), "iq4_xs": (256, 136), "tq1_0": (256, 54), "tq2_0": (256, 66), "mxfp4": (32, 17),
           "nvfp4": (64, 36), "iq2_xxs": (256, 66), "iq2_xs": (256, 74), "iq2_s": (256, 82), "iq3_xxs": (256, 98),
-          "iq3_s": (256, 110), "iq1_s": (256, 50), "iq1_m": (256, 56)}
+          "iq3_s": (256, 110), "iq1_s": (256, 50), "iq1_m": (256, 56),
+          "q1_0": (128, 18), "q2_0": (64, 18), "q2_0_g128": (128, 34), "tern1_g128": (128, 28), "nvfp4_gs": (64, 40),
+          "q4z_g32": (32, 20), "q4z_g128": (128, 68), "q8z_g32": (32, 36), "q8z_g128": (128, 132), "nf4_b64": (64, 36),
+          "fp4_b64": (64, 36), "q8a_g32": (32, 36), "q2s_g128": (128, 36), "f8e4m3": (1, 1), "f8e5m2": (1, 1),
+          "f8e4m3_b32": (32, 36), "f8e4m3_b128": (128, 132)}
 ELEM_BYTES = {"f32": 4, "f16": 2, "bf16": 2, "i32": 4}
 
 

@@ -45,15 +45,30 @@ KBLOCK = {"q2_k": (84, (80, 82)), "q3_k": (110, (108,)), "q4_k": (144, (0, 2)), 
           "iq1_s": (50, (0,)), "iq1_m": (56, ())}
 # 4-bit float blocks: bytes, values, and the scale bytes at the block start (E8M0 exponent / UE4M3 scales)
 FP4BLOCK = {"mxfp4": (17, 32, 1), "nvfp4": (36, 64, 4)}
+# The reference's own formats: bytes, values, and the scale fields ("h" f16 at an offset, "f" f32 at an offset,
+# "ue" UE4M3 bytes at 4..7) -- every other byte random.
+REFBLOCK = {"q1_0": (18, 128, (("h", 0),)), "q2_0": (18, 64, (("h", 0),)), "q2_0_g128": (34, 128, (("h", 0),)),
+            "tern1_g128": (28, 128, (("h", 26),)), "nvfp4_gs": (40, 64, (("f", 0), ("ue", 4))),
+            "q4z_g32": (20, 32, (("h", 0), ("z", 2))), "q4z_g128": (68, 128, (("h", 0), ("z", 2))),
+            "q8z_g32": (36, 32, (("h", 0), ("z8", 2))), "q8z_g128": (132, 128, (("h", 0), ("z8", 2))),
+            "nf4_b64": (36, 64, (("f", 0),)), "fp4_b64": (36, 64, (("f", 0),)), "q8a_g32": (36, 32, (("f", 0),)),
+            "q2s_g128": (36, 128, (("f", 0),)), "f8e4m3": (1, 1, ()), "f8e5m2": (1, 1, ()),
+            "f8e4m3_b32": (36, 32, (("f", 0),)), "f8e4m3_b128": (132, 128, (("f", 0),))}
 
 
 def block_values(fmt: str) -> int:
+    if fmt in REFBLOCK:
+        return REFBLOCK[fmt][1]
     if fmt in FP4BLOCK:
         return FP4BLOCK[fmt][1]
     return 256 if fmt in KBLOCK else 32
 
 
 def row_bytes(fmt: str, D: int) -> int:
+    if fmt in REFBLOCK:
+        bb, bs, _ = REFBLOCK[fmt]
+        assert D % bs == 0
+        return D // bs * bb
     if fmt == "f32":
         return 4 * D
     if fmt in ("f16", "bf16"):
@@ -78,6 +93,26 @@ def quant_table(fmt: str, V: int, D: int, seed: int = 0, tid: int = 0, scale_lo=
     E8M0 exponents ~ U{118..126} (scales 2^-10..2^-2); nvfp4: codes any bytes, UE4M3 scales ~ U{0x20..0x3F}
     (2^-4 .. 1.9); f16: values N(0,1)*0.02; bf16 / f32: N(0,1)*0.02."""
     g = rng(seed, tid)
+    if fmt in REFBLOCK:  # random code bytes; scales ~ U[scale_lo, scale_hi] (f32 ones x 64: their codes are small)
+        bb, bs, fields = REFBLOCK[fmt]
+        nb = D // bs
+        t = g.integers(0, 256, size=(V, nb, bb), dtype=np.uint8)
+        if fmt == "f8e4m3":  # no NaN codes (0x7F, 0xFF) in the synthetic table
+            t[t & 0x7F == 0x7F] = 0x7E
+        for kind, off in fields:
+            if kind == "h":
+                t[:, :, off:off + 2] = g.uniform(scale_lo, scale_hi, size=(V, nb)).astype(np.float16).view(np.uint8).reshape(V, nb, 2)
+            elif kind in ("z", "z8"):  # a zero point near the code range's middle
+                mid = 8.0 if kind == "z" else 128.0
+                t[:, :, off:off + 2] = g.uniform(mid - 2, mid + 2, size=(V, nb)).astype(np.float16).view(np.uint8).reshape(V, nb, 2)
+            elif kind == "f":
+                t[:, :, off:off + 4] = (g.uniform(scale_lo, scale_hi, size=(V, nb)) * 64).astype(np.float32).view(np.uint8).reshape(V, nb, 4)
+            elif kind == "ue":
+                t[:, :, off:off + 4] = g.integers(0x20, 0x40, size=(V, nb, 4), dtype=np.uint8)
+        if fmt == "f8e4m3_b32" or fmt == "f8e4m3_b128":
+            c = t[:, :, 4:]
+            c[c & 0x7F == 0x7F] = 0x7E
+        return t.reshape(V, nb * bb)
     if fmt in FP4BLOCK:
         bb, bs, ns = FP4BLOCK[fmt]
         nb = D // bs

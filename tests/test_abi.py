@@ -153,7 +153,7 @@ def test_rope_validation():
 
 def test_gather_validation():
     with pytest.raises(native.SlhipNotSupported, match="format"):
-        native.gather(42, FAKE, 10, 32, FAKE, 4, "bf16", FAKE)
+        native.gather(99, FAKE, 10, 32, FAKE, 4, "bf16", FAKE)
     with pytest.raises(native.SlhipArgumentError, match="block size"):
         native.gather("q8_0", FAKE, 10, 40, FAKE, 4, "bf16", FAKE)
     with pytest.raises(native.SlhipArgumentError, match="null"):

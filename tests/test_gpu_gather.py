@@ -162,3 +162,53 @@ def test_gather_out_of_range_raises_on_sync(device):
 def test_gather_empty(device):
     native.gather("q8_0", None, 10, 4096, None, 0, "bf16", None)
     native.synchronize()
+
+
+def _nan_aware_equal(y, ref, dout, what):
+    yf = y if dout == "f32" else oracle.from_bf16(y)
+    rf = ref if dout == "f32" else oracle.from_bf16(ref)
+    nan = np.isnan(rf)
+    assert np.array_equal(np.isnan(yf), nan), what
+    assert np.array_equal(yf[~nan].view(np.uint32), rf[~nan].view(np.uint32)), what
+
+
+@pytest.mark.parametrize("fmt", oracle.REF_FORMATS)
+@pytest.mark.parametrize("dout", ["f32", "bf16"])
+@pytest.mark.parametrize("D", [128, 4096, 5120 + 128])
+def test_gather_reference_formats(device, fmt, dout, D):
+    """The reference's own formats (Q1_0 .. F8E4M3_B128, src/Sharplight.Cpu/Quant.cs:287-362): random code
+    bytes with sane scales, bit-exact against the oracle's restatement of each decoder (NaNs -- from E5M2's
+    NaN codes -- compared as NaNs), on a single block, whole work items and a partial last item."""
+    bs = synth.block_values(fmt)
+    D = max(bs, D // bs * bs)
+    V, N = 257, 61
+    t = synth.quant_table(fmt, V, D, seed=D + 7, tid=len(fmt))
+    ids = synth.rng(D, 3).integers(0, V, N).astype(np.int32)
+    ids[:3] = [0, V - 1, 0]
+    y = _run(fmt, t, V, D, ids, dout)
+    _nan_aware_equal(y, _ref(fmt, t, V, D, ids, dout), dout, f"{fmt}->{dout} D={D}")
+
+
+@pytest.mark.parametrize("fmt", ["f8e4m3", "f8e5m2"])
+def test_gather_every_fp8_code(device, fmt):
+    """All 256 codes of the plain FP8 tables to f32, exact (NaN codes as NaN)."""
+    t = np.tile(np.arange(256, dtype=np.uint8), 16).reshape(1, 4096)
+    y = _run(fmt, t, 1, 4096, np.zeros(1, np.int32), "f32")
+    _nan_aware_equal(y, _ref(fmt, t, 1, 4096, np.zeros(1, np.int32), "f32"), "f32", fmt)
+
+
+@pytest.mark.parametrize("fmt", ["nvfp4_gs", "q4z_g32", "q8z_g128", "nf4_b64", "q8a_g32", "f8e4m3_b32"])
+def test_gather_reference_formats_unaligned(device, fmt):
+    """A table 2 bytes off 16-byte alignment: the general kernel, same bits."""
+    bs = synth.block_values(fmt)
+    V, D = 9, 2 * max(bs, 64)
+    t = synth.quant_table(fmt, V, D, seed=3, tid=1)
+    ids = np.array([3, 0, 8, 3], np.int32)
+    with Dev() as d:
+        pt = d.put(t, 2)
+        py = d.empty(4 * D * 4)
+        log(f"gather unaligned {fmt}")
+        native.gather(fmt, pt, V, D, d.put(ids), 4, "f32", py)
+        native.synchronize()
+        y = d.get(py, (4, D), np.float32)
+    _nan_aware_equal(y, _ref(fmt, t, V, D, ids, "f32"), "f32", fmt)
