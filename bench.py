@@ -151,9 +151,48 @@ class C2Copy(Workload):
                        w=self.w.slot(0), h_out=self.h.slot(i), eps=self.eps, stream=stream, **kw)
 
 
+class LayerNorm(Workload):
+    """slhip_rownorm kind LAYER with gamma and beta: the reference's ViT figure (197 x 768 f32,
+    docs/benchmarks.md:2869) and the C2 shape in bf16."""
+
+    def __init__(self, rows, D, dtype):
+        self.name = "layernorm_vit_f32" if dtype == "f32" else "layernorm_bf16"
+        self.desc = synth.CONFIGS[self.name].description
+        c = synth.layernorm(rows=rows, D=D, dtype=dtype)
+        self.rows, self.D, self.dtype, self.eps = rows, D, dtype, c["eps"]
+        nb = c["x"].nbytes
+        self.bytes_per_step = 2 * nb + c["w"].nbytes + c["b"].nbytes
+        R = copies_for(self.bytes_per_step)
+        self.x, self.y = Rot(c["x"], nb, R), Rot(None, nb, R)
+        self.w, self.b = Rot(c["w"], c["w"].nbytes, 1), Rot(c["b"], c["b"].nbytes, 1)
+
+    def launch(self, i, stream):
+        native.rownorm("layer", self.dtype, self.dtype, self.x.slot(i), self.y.slot(i), self.rows, self.D,
+                       w=self.w.slot(0), b=self.b.slot(0), eps=self.eps, stream=stream)
+
+
+class BiasAdd(Workload):
+    """A lone broadcast Add (slhip_binary): x [8192, 4096] bf16 + bias [4096] bf16 -> bf16."""
+    name = "bias_add_bf16"
+
+    def __init__(self, rows=8192, D=4096):
+        self.desc = synth.CONFIGS[self.name].description
+        self.rows, self.D = rows, D
+        x = synth.normal(0, 0, (rows, D), dtype="bf16")
+        bias = synth.normal(0, 1, (D,), dtype="bf16")
+        nb = x.nbytes
+        self.bytes_per_step = 2 * nb + bias.nbytes
+        R = copies_for(self.bytes_per_step)
+        self.x, self.y, self.b = Rot(x, nb, R), Rot(None, nb, R), Rot(bias, bias.nbytes, 1)
+
+    def launch(self, i, stream):
+        native.binary("Add", "bf16", "bf16", "bf16", self.x.slot(i), self.b.slot(0), self.y.slot(i),
+                      [self.rows, self.D], a_strides=[self.D, 1], b_strides=[0, 1], stream=stream)
+
+
 class C3(Workload):
     def __init__(self, act):
-        self.name = "c3_swiglu_bf16" if act == "silu" else "c3_geglu_bf16"
+        self.name = {"silu": "c3_swiglu_bf16", "gelu_tanh": "c3_geglu_bf16", "gelu_erf": "c3_geglu_erf_bf16"}[act]
         self.act = act
         self.desc = synth.CONFIGS[self.name].description
         c = synth.c3()
@@ -345,6 +384,10 @@ WORKLOADS = {
     "c2_add_rmsnorm_f16_copy_bf16": lambda: C2Copy("f16"),
     "c3_swiglu_bf16": lambda: C3("silu"),
     "c3_geglu_bf16": lambda: C3("gelu_tanh"),
+    "c3_geglu_erf_bf16": lambda: C3("gelu_erf"),
+    "layernorm_vit_f32": lambda: LayerNorm(197, 768, "f32"),
+    "layernorm_bf16": lambda: LayerNorm(8192, 4096, "bf16"),
+    "bias_add_bf16": lambda: BiasAdd(),
     "c4_qknorm_rope_bf16": lambda: C4(),
     "c5_gather_q8_0": lambda: C5("q8_0"),
     "c5_gather_q4_0": lambda: C5("q4_0"),
@@ -400,6 +443,27 @@ def time_region_graph(wl: Workload, steps: int, warmup: int, stream: native.Stre
     native.synchronize(stream.handle)
     t1 = time.perf_counter()
     return t1 - t0, e0.elapsed_ms(e1)
+
+
+def time_eager(wl: Workload, launches: int, stream) -> np.ndarray:
+    """Per-launch microseconds of single eager launches: each launch alone between two HIP events on the
+    stream, the stream synchronized before the next, so every figure holds one dispatch's start-up and
+    drain (what a caller that launches one op and waits sees, without host submission time)."""
+    for i in range(3):
+        wl.launch(i, stream)
+    native.synchronize(stream)
+    out = []
+    e0, e1 = native.Event(), native.Event()
+    for i in range(launches):
+        e0.record(stream)
+        wl.launch(i, stream)
+        e1.record(stream)
+        native.synchronize(stream)
+        out.append(e0.elapsed_ms(e1) * 1e3)
+    return np.array(out)
+
+
+EAGER_OPS = ("c1_rmsnorm_f32", "layernorm_vit_f32")  # small ops whose per-launch figure differs from replay
 
 
 def time_per_launch(wl: Workload, launches: int, replays: int, stream) -> np.ndarray:
@@ -598,7 +662,26 @@ def cpu_baselines(budget_main: float, budget_op: float, which: set[str]) -> dict
         L, P = oracle.lib(), oracle._p
         s, reps = cpu_time(lambda: L.orc_rmsnorm_mt(P(c["x"]), P(c["w"]), P(y), 512, 1024, c["eps"], 0), budget_op)
         res["c1_rmsnorm_f32"] = dict(s=s, reps=reps, sample="full [512,1024]")
-    for act, name in (("silu", "c3_swiglu_bf16"), ("gelu_tanh", "c3_geglu_bf16")):
+    for name, rows, D, dtype in (("layernorm_vit_f32", 197, 768, "f32"), ("layernorm_bf16", 1024, 4096, "bf16")):
+        if name not in which:
+            continue
+        c = synth.layernorm(rows=rows, D=D, dtype=dtype)
+        x = c["x"] if dtype == "f32" else oracle.from_bf16(c["x"])
+        y = np.empty_like(x)
+        L, P = oracle.lib(), oracle._p
+        s, reps = cpu_time(lambda: L.orc_layernorm_mt(P(x), P(c["w"]), P(c["b"]), P(y), rows, D, c["eps"]), budget_op)
+        full = 197 if dtype == "f32" else 8192
+        res[name] = dict(s=s * full / rows, reps=reps,
+                         sample=f"full [197,768]" if full == rows else f"{rows} of {full} rows, scaled x{full // rows}")
+    if "bias_add_bf16" in which:
+        rows = 512
+        x = oracle.from_bf16(synth.normal(0, 0, (rows, 4096), dtype="bf16"))
+        bias = oracle.from_bf16(synth.normal(0, 1, (4096,), dtype="bf16"))
+        s, reps = cpu_time(lambda: oracle.binary("Add", x, bias), budget_op)
+        res["bias_add_bf16"] = dict(s=s * 8192 / rows, reps=reps, threads=1,
+                                    sample=f"{rows} of 8192 rows, scaled x{8192 // rows}; one thread (the oracle's "
+                                           "broadcast Add is single-threaded)")
+    for act, name in (("silu", "c3_swiglu_bf16"), ("gelu_tanh", "c3_geglu_bf16"), ("gelu_erf", "c3_geglu_erf_bf16")):
         if name not in which:
             continue
         rows = 1024  # 1/8 of the rows: the op is row-independent, time scales linearly
@@ -666,7 +749,7 @@ def cpu_baselines(budget_main: float, budget_op: float, which: set[str]) -> dict
             s, reps = cpu_time(lambda: L.orc_cache_write_mt(oracle.F16, P(cache), 8 * 128, P(v), T, P(rows)), budget_op)
             res["v_cache_write_f16_paged"] = dict(s=s * 4096 / T, reps=reps, sample=f"{T} of 4096 tokens, scaled x{4096 // T}")
     for v in res.values():
-        v["threads"] = threads
+        v.setdefault("threads", threads)
     return res
 
 
@@ -849,10 +932,16 @@ def main():
                 w = mk()
                 us = time_per_launch(w, args.launches, args.replays, stream)
                 b = w.bytes_per_step
+                eager = time_eager(w, args.launches, stream.handle) if name in EAGER_OPS else None
                 w.free()
             med = float(np.median(us))
             ops[name] = {"us": round(med, 2), "us_min": round(float(us.min()), 2), "timing": "graph replay", "bytes": int(b),
                          "GB/s": round(b / med / 1e3, 1), "pct_peak": round(100 * b / med / 1e3 / PEAK_GBS, 1)}
+            if name != "c2_add_rmsnorm_bf16" and eager is not None:
+                em = float(np.median(eager))
+                ops[name]["eager_us"] = round(em, 2)
+                ops[name]["eager_timing"] = "one eager launch between two HIP events, synchronized each time"
+                ops[name]["eager_GB/s"] = round(b / em / 1e3, 1)
             if not args.no_ceiling and name != CopyRef.name:
                 cw = SameBytesCopy(int(b))
                 cus = float(np.median(time_per_launch(cw, args.launches, args.replays, stream)))
@@ -884,10 +973,14 @@ def main():
                 ops[name]["cpu_us"] = round(v["s"] * 1e6, 1)
                 ops[name]["cpu_GB/s"] = round(ops[name]["bytes"] / v["s"] / 1e9, 2)
                 ops[name]["cpu_sample"] = v["sample"]
+                ops[name]["cpu_threads"] = v["threads"]
 
     line = {
         "metric": "achieved HBM GB/s (% of MI355X peak) per fused op; us per op at config shape",
         "value": round(value, 1),
+        "value_clock": f"host wall clock between the stream syncs around one HIP graph of {args.steps} C2 launches "
+                       "(roofline.achieved: HIP events on the launch stream around the same graph; ops: per-launch "
+                       "averages of graph replays)",
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,

@@ -124,7 +124,7 @@ __device__ __forceinline__ float unary_op(int op, float v, float p0, float p1)
     case SLHIP_UN_SQUARE: return v * v;
     case SLHIP_UN_RECIP: return 1.0f / v;
     case SLHIP_UN_SCALE: return fmaf(v, p0, p1);
-    case SLHIP_UN_ERF: return erf_rational(v);
+    case SLHIP_UN_ERF: return v != v ? v : erf_rational(v);
     case SLHIP_UN_HARD_SWISH: return v * ieee_min(ieee_max(fmaf(v, 1.0f / 6.0f, 0.5f), 0.0f), 1.0f);
     case SLHIP_UN_HARD_SIGMOID: return ieee_min(ieee_max(fmaf(v, p0, p1), 0.0f), 1.0f);
     case SLHIP_UN_CLIP: return ieee_min(ieee_max(v, p0), p1);

@@ -41,6 +41,7 @@ constexpr int64_t kHeaderBytes = 24;
 constexpr uint32_t kMaxDims = 8;
 constexpr int64_t kMinStringBytes = 8;   // a string's length prefix
 constexpr int64_t kMinArrayBytes = 12;   // a nested array's element type and count
+constexpr int kMaxArrayDepth = 64;      // nesting limit of arrays of arrays
 constexpr int64_t kIntMax = 2147483647;
 
 // A malformed file (SLHIP_ERR_FORMAT) or a valid file this library does not read (SLHIP_ERR_UNSUPPORTED).
@@ -262,7 +263,7 @@ struct slhip_gguf {
     }
 
     // GgufReader.ReadValue / ReadArray (GgufReader.cs:72-144). Fills nodes[id]; children are appended.
-    void read_value(Cursor& c, uint32_t type, int64_t id)
+    void read_value(Cursor& c, uint32_t type, int64_t id, int depth = 0)
     {
         Node n;
         n.type = type;
@@ -283,6 +284,9 @@ struct slhip_gguf {
             const uint32_t elem = c.read<uint32_t>();
             const int64_t count = c.read_len();
             if (count > kIntMax) format_error("Array too large.");
+            // arrays of arrays recurse on the native stack: a crafted file of a few MB could nest deep
+            // enough to overflow it, so nesting beyond kMaxArrayDepth is a format error
+            if (depth >= kMaxArrayDepth) format_error("Arrays nested deeper than " + std::to_string(kMaxArrayDepth) + ".");
             n.elem = elem;
             n.count = count;
             static const int kSize[13] = {1, 1, 2, 2, 4, 4, 4, 1, 0, 0, 8, 8, 8};
@@ -301,7 +305,7 @@ struct slhip_gguf {
                         read_string(c, s);
                         nodes[first + k] = s;
                     } else {
-                        read_value(c, SLHIP_GGUF_ARRAY, first + k);
+                        read_value(c, SLHIP_GGUF_ARRAY, first + k, depth + 1);
                     }
                 }
                 n.first_child = first;

@@ -101,7 +101,8 @@ __global__ __launch_bounds__(1024) void rownorm_vec(RowNormArgs a, int wpr)
     // The norm weight is read with the row data, ahead of the reduction, rather than after it.
     float wv[NV][E];
     const bool has_w = a.w != nullptr, has_b = a.b != nullptr;
-    if (has_w) {
+    constexpr bool W_EARLY = RES || DTI == SLHIP_F32;  // a packed row reads it after the reductions
+    if (W_EARLY && has_w) {
 #pragma unroll
         for (int k = 0; k < NV; k++) {
             const float4* wp = reinterpret_cast<const float4*>(a.w + static_cast<int64_t>(jv[k]) * E);
@@ -116,6 +117,18 @@ __global__ __launch_bounds__(1024) void rownorm_vec(RowNormArgs a, int wpr)
         }
     }
 
+    // Without a residual the row stays in registers as loaded (a 2-byte row in half the registers of its
+    // f32 values) and is widened again in each pass; the empty asm statements stop the compiler from
+    // keeping the widened values alive across the reductions instead. The registers saved double the
+    // waves resident per SIMD, i.e. the bytes in flight, which is what a 2-stream norm lacks.
+    constexpr bool PACKED = !RES && DTI != SLHIP_F32;
+    auto launder = [&]() {
+        if constexpr (PACKED) {
+#pragma unroll
+            for (int k = 0; k < NV; k++)
+                asm volatile("" : "+v"(raw[k].x), "+v"(raw[k].y), "+v"(raw[k].z), "+v"(raw[k].w));
+        }
+    };
     float v[NV][E];
 #pragma unroll
     for (int k = 0; k < NV; k++) {
@@ -152,14 +165,17 @@ __global__ __launch_bounds__(1024) void rownorm_vec(RowNormArgs a, int wpr)
             for (int e = 0; e < E; e++) s += own[k] ? v[k][e] : 0.0f;
         mean = group_reduce<4>(s, wpr, group, wig, red) * inv_d;
         store_h();
+        launder();
         float q = 0.f;
 #pragma unroll
-        for (int k = 0; k < NV; k++)
+        for (int k = 0; k < NV; k++) {
+            if constexpr (PACKED) VI::unpack(raw[k], v[k]);
 #pragma unroll
             for (int e = 0; e < E; e++) {
                 const float d = own[k] ? v[k][e] - mean : 0.0f;
                 q = fmaf(d, d, q);
             }
+        }
         const float var = group_reduce<4>(q, wpr, group, wig, red) * inv_d;
         scale = 1.0f / sqrtf(var + a.eps);
     } else {
@@ -177,11 +193,13 @@ __global__ __launch_bounds__(1024) void rownorm_vec(RowNormArgs a, int wpr)
     }
 
     if (!store_row) return;
+    launder();
     char* yr = static_cast<char*>(a.y) + row * a.ys * Vec<DTO>::BYTES;
     char* y16r = static_cast<char*>(a.y16) + row * a.y16s * 2;
     char* qr = static_cast<char*>(a.yq) + row * a.yqs;
 #pragma unroll
     for (int k = 0; k < NV; k++) {
+        if constexpr (PACKED) VI::unpack(raw[k], v[k]);
         float o[E];
         if (a.kind == SLHIP_NORM_LAYER) {
 #pragma unroll
@@ -191,6 +209,17 @@ __global__ __launch_bounds__(1024) void rownorm_vec(RowNormArgs a, int wpr)
             for (int e = 0; e < E; e++) o[e] = v[k][e] * scale;
         }
         if (has_w) {
+            if constexpr (!W_EARLY) {
+                const float4* wp = reinterpret_cast<const float4*>(a.w + static_cast<int64_t>(jv[k]) * E);
+#pragma unroll
+                for (int q4 = 0; q4 < E / 4; q4++) {
+                    const float4 w4 = wp[q4];
+                    wv[k][4 * q4 + 0] = w4.x;
+                    wv[k][4 * q4 + 1] = w4.y;
+                    wv[k][4 * q4 + 2] = w4.z;
+                    wv[k][4 * q4 + 3] = w4.w;
+                }
+            }
 #pragma unroll
             for (int e = 0; e < E; e++) o[e] *= wv[k][e];
         }

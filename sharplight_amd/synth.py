@@ -170,6 +170,10 @@ CONFIGS = {
                                   "residual add + RMSNorm bf16 x,res[8192,4096], gamma f32, eps 1e-5 (Llama-3-8B)"),
     "c3_swiglu_bf16": Config("c3_swiglu_bf16", "SwiGLU bf16 gate,up[8192,14336] (Llama-3-8B FFN)"),
     "c3_geglu_bf16": Config("c3_geglu_bf16", "GeGLU (tanh GELU) bf16 gate,up[8192,14336]"),
+    "c3_geglu_erf_bf16": Config("c3_geglu_erf_bf16", "GeGLU (erf GELU) bf16 gate,up[8192,14336]"),
+    "layernorm_vit_f32": Config("layernorm_vit_f32", "LayerNorm f32 x[197,768], gamma/beta, eps 1e-6 (ViT-B/16)"),
+    "layernorm_bf16": Config("layernorm_bf16", "LayerNorm bf16 x[8192,4096], f32 gamma/beta, eps 1e-5 (C2 shape)"),
+    "bias_add_bf16": Config("bias_add_bf16", "Add bf16 x[8192,4096] + bias[4096] (broadcast) -> bf16"),
     "c4_qknorm_rope_bf16": Config("c4_qknorm_rope_bf16",
                                   "q[4096,32,128], k[4096,8,128] bf16: per-head RMSNorm + neox RoPE theta 1e6 (Qwen3-8B)"),
     "c5_gather_q8_0": Config("c5_gather_q8_0", "gather 16384 ids from Q8_0 [151936,4096] -> bf16"),
@@ -191,6 +195,11 @@ def c1(seed=0, rows=512, D=1024):
 def c2(seed=0, rows=8192, D=4096):
     return dict(x=normal(seed, 0, (rows, D), dtype="bf16"), res=normal(seed, 1, (rows, D), dtype="bf16"),
                 w=normal(seed, 2, (D,), 1.0, 0.1), eps=1e-5)
+
+
+def layernorm(seed=0, rows=197, D=768, dtype="f32"):
+    return dict(x=normal(seed, 0, (rows, D), dtype=dtype), w=normal(seed, 1, (D,), 1.0, 0.1),
+                b=normal(seed, 2, (D,), 0.0, 0.1), eps=1e-6 if dtype == "f32" else 1e-5)
 
 
 def c3(seed=0, rows=8192, cols=14336):

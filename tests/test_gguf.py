@@ -361,6 +361,24 @@ def test_malformed_tables_and_values():
         _both_raise(blob, exc, oexc, match)
 
 
+def test_deeply_nested_arrays_fail_without_recursing_away():
+    """Arrays of arrays nest at most 64 deep; deeper nesting is a format error, not a stack overflow.
+
+    The reference recurses without a limit in managed code; a native reader must not, since a file of
+    a few MB could nest 10^5 deep. 64 levels still open."""
+    def nested(depth):
+        key = struct.pack("<Q", 1) + b"k"
+        body = struct.pack("<I", 9) + struct.pack("<IQ", 9, 1) * (depth - 1) + struct.pack("<IQ", 4, 1) + \
+            struct.pack("<I", 7)
+        return struct.pack("<IIQQ", 0x46554747, 3, 0, 1) + key + body + bytes(64)
+    f = _native_from_bytes(nested(64))
+    assert f is not None
+    with pytest.raises(native.SlhipFormatError, match="nested deeper than 64"):
+        _native_from_bytes(nested(65))
+    with pytest.raises(native.SlhipFormatError, match="nested deeper than 64"):
+        _native_from_bytes(nested(200000))
+
+
 def test_closed_file_refuses_reads(tmp_path):
     """GgufRoundTripTests.Dispose_InvalidatesSources."""
     p = tmp_path / "d.gguf"

@@ -141,7 +141,7 @@ def test_binary_rejects_mixed_input_types(device):
 
 UNARY_EXACT = {"Neg", "Sqrt", "Rsqrt", "Relu", "Abs", "Square", "Recip", "Scale", "HardSwish", "HardSigmoid", "Clip",
                "Floor", "Ceil", "Round", "Sign", "Softsign", "LeakyRelu", "ThresholdedRelu", "Not", "IsNaN", "IsInf",
-               "Gelu", "Erf", "Softplus"}
+               "Softplus"}
 PARAMS = {"Scale": (1.25, -0.5), "HardSigmoid": (0.2, 0.5), "Clip": (-1.5, 2.0), "Elu": (1.0, 0.0),
           "Celu": (1.3, 0.0), "Selu": (1.6732632, 1.050701), "LeakyRelu": (0.01, 0.0), "ThresholdedRelu": (1.0, 0.0)}
 DOMAIN = {"Log": (0.01, 8), "Sqrt": (0, 8), "Rsqrt": (0.01, 8), "Asin": (-0.99, 0.99), "Acos": (-0.99, 0.99),
@@ -167,6 +167,34 @@ def test_unary_kinds(device, op, dt):
         y = d.get(py, (37, 1000), NP[dt])
     ref = oracle.unary_kind(op, _f32(x, dt), p0, p1)
     _check(y, ref, dt, op in UNARY_EXACT, f"{op} {dt}")
+
+
+def test_erf_dense_grid_error_bound(device):
+    """Erf and Gelu evaluate the reference's f64 rational (ScalarMath.cs:51-98) in f32: over 2^24 points of
+    [-6, 6] (beyond the clamp at 3.8325 on both sides) erf stays within 4e-7 absolute and 8 ulp of the f64
+    evaluation narrowed to f32, and Gelu within 0.5|x| times that; erf(NaN) is NaN."""
+    n = 1 << 24
+    x = np.linspace(-6, 6, n, dtype=np.float32).reshape(1024, n // 1024)
+    x[0, :3] = [np.nan, np.inf, -np.inf]
+    out = {}
+    with Dev() as d:
+        px, py = d.put(x), d.empty(x.nbytes)
+        for op in ("Erf", "Gelu"):
+            log(f"unary {op} dense grid")
+            native.unary(op, "f32", "f32", px, py, x.shape[0], x.shape[1])
+            native.synchronize()
+            out[op] = d.get(py, x.shape, np.float32)
+    ref = oracle.unary_kind("Erf", x)
+    got = out["Erf"]
+    assert np.isnan(got[0, 0])
+    f = ~np.isnan(x)  # +-inf clamp like any |x| > 3.8325
+    err = np.abs(got[f].astype(np.float64) - ref[f])
+    ulp = np.abs(got[f].view(np.int32).astype(np.int64) - ref[f].view(np.int32))
+    assert err.max() <= 4e-7 and ulp.max() <= 8, (err.max(), ulp.max())
+    gref = oracle.unary_kind("Gelu", x)
+    f = np.isfinite(x)
+    gerr = np.abs(out["Gelu"][f].astype(np.float64) - gref[f])
+    assert np.all(gerr <= 0.5 * np.abs(x[f]) * 4.2e-7 + 1e-7 * np.abs(gref[f])), gerr.max()
 
 
 def test_unary_ragged_strided_and_special_values(device):

@@ -6,7 +6,7 @@ import pytest
 import oracle
 from sharplight_amd import native, synth
 from tests.devutil import Dev, log
-from tests.parity import assert_bf16_close, assert_bits_equal, assert_f32_close
+from tests.parity import assert_bf16_close, assert_f32_close
 
 pytestmark = pytest.mark.gpu
 
@@ -51,8 +51,10 @@ def test_gated_dtypes(device, act, din, dout):
     else:
         assert_f32_close(y, yf, what=f"{act} {din}->{dout}")
     if act == "gelu_erf" and dout == "f32":
-        # same f64 rational, same f32 steps as the reference's vector form: bit-identical
-        assert_bits_equal(y, yf, what="gelu_erf bits")
+        # the reference's rational evaluated in f32 rather than f64: erf within 4e-7 absolute, so the
+        # result within 0.5 |g| |u| 4e-7 (+ the f32 roundings of the product)
+        bound = 0.5 * np.abs(gf) * np.abs(uf) * 4.2e-7 + 2e-7 * np.abs(yf)
+        assert np.all(np.abs(y.astype(np.float64) - yf) <= bound), "gelu_erf beyond the erf error bound"
 
 
 def test_gated_extreme_inputs(device):

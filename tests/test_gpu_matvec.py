@@ -210,6 +210,8 @@ def test_dual_matvec(device, act, fmt, dx, dy, T, K, N):
     dact = np.maximum(np.abs(dact), 1.5 * np.abs(dimpl))
     e = 2.0 ** -16
     tol = np.abs(dact * u) * e * Sg + np.abs(_act64(act, g64)) * e * Su + 1e-5 * np.abs(ref) + 1e-30
+    if act == "gelu_erf":  # the erf rational evaluated in f32: within 4e-7 of the f64 evaluation
+        tol = tol + 0.5 * np.abs(g64 * u) * 4.2e-7
     if dy == "bf16":
         got = oracle.from_bf16(y).astype(np.float64)
         r = oracle.from_bf16(oracle.to_bf16(ref)).astype(np.float64)
