@@ -438,8 +438,10 @@ SLHIP_API int slhip_unary(int op, int dtype_in, int dtype_out, const void* x, vo
 /* ---- provider / compiled segment (IExecutionProvider, IComputeDevice, ICompiledSegment) ----------------
  *
  * A graph segment arrives as text, one declaration per line ('#' starts a comment line):
- *   value <id> <type> <dim> ...       type: f32 f16 bf16 i32 q8_0 q4_0 q4_1 q5_0 q5_1; a dim "T" is the
- *                                     symbolic token count, bound at execute time (at most max_tokens)
+ *   value <id> <type> <dim> ...       type: a DataType name of the reference (f32 f16 bf16 i32, and the
+ *                                     block formats slhip_format lists: q8_0 q4_k iq2_xxs nf4_b64 ...); a dim
+ *                                     is a size, or "T", the symbolic token count bound at execute time (at
+ *                                     most max_tokens); other symbols are refused
  *   input <id> | weight <id> | output <id> | state <id>    (a state -- a KV cache -- has fixed dims, persists
  *                                     across runs, starts at zero and is zeroed again by reset_state)
  *   node <Op> <in,ids> -> <out,ids> [key=value ...]
@@ -492,6 +494,10 @@ SLHIP_API int slhip_segment_launches(slhip_segment segment, char* buf, size_t si
  * touching a device: the lowerer's plan (GraphLowerer.Lower, src/Sharplight.Shaders/Lowering/GraphLowerer.cs:
  * 64-71, without the buffers). Fails as compile would for a node or pattern this provider cannot run. */
 SLHIP_API int slhip_segment_plan(const char* segment_ir, char* buf, size_t size);
+/* The segment text as the provider read it, in canonical form: value lines by id, then the input, weight,
+ * output and state lines by id, then the node lines in order with their attributes sorted by key. No device
+ * is touched; malformed text fails as compile would. A buffer too small fails (nothing is truncated). */
+SLHIP_API int slhip_segment_describe(const char* segment_ir, char* buf, size_t size);
 SLHIP_API int slhip_segment_destroy(slhip_segment segment);
 
 /* ---- GGUF files and weight upload (the on-disk -> device path) --------------------------------

@@ -291,7 +291,16 @@ Graph parse(const char* text)
                 std::string t, d;
                 if (!(ls >> v.id >> t)) invalid("value: expected '<id> <type> <dims...>'");
                 v.type = parse_type(t);
-                while (ls >> d) v.dims.push_back(d == "T" ? kSymT : strtoll(d.c_str(), nullptr, 10));
+                while (ls >> d) {
+                    if (d == "T") {
+                        v.dims.push_back(kSymT);
+                        continue;
+                    }
+                    if (d.find_first_not_of("0123456789") != std::string::npos)
+                        invalid("dimension '" + d + "' is neither a size nor the token count T (other symbols and "
+                                "symbolic expressions are not supported)");
+                    v.dims.push_back(strtoll(d.c_str(), nullptr, 10));
+                }
                 if (g.values.count(v.id)) invalid("value " + std::to_string(v.id) + " declared twice");
                 g.values[v.id] = v;
             } else if (kw == "input" || kw == "weight" || kw == "output" || kw == "state") {
@@ -1204,12 +1213,50 @@ SLHIP_API int slhip_segment_compile(const char* segment_ir, int64_t max_tokens, 
     });
 }
 
+// Copies text into a caller's buffer, failing (not truncating) when it does not fit.
+static void put_text(const std::string& text, char* buf, size_t size)
+{
+    if (!buf || !size) invalid("null argument");
+    if (text.size() + 1 > size) invalid("buffer of " + std::to_string(size) + " bytes too small for " +
+                                        std::to_string(text.size() + 1));
+    memcpy(buf, text.c_str(), text.size() + 1);
+}
+
 SLHIP_API int slhip_segment_plan(const char* segment_ir, char* buf, size_t size)
 {
     return guarded([&] {
-        if (!buf || !size) invalid("null argument");
         Segment s(parse(segment_ir), 0, true);
-        snprintf(buf, size, "%s", s.launches().c_str());
+        put_text(s.launches(), buf, size);
+    });
+}
+
+SLHIP_API int slhip_segment_describe(const char* segment_ir, char* buf, size_t size)
+{
+    return guarded([&] {
+        const Graph g = parse(segment_ir);
+        std::string out;
+        for (const auto& [id, v] : g.values) {
+            out += "value " + std::to_string(id) + " " + type_info(v.type).name;
+            for (int64_t d : v.dims) out += " " + (d == kSymT ? std::string("T") : std::to_string(d));
+            out += "\n";
+        }
+        const char* roles[4] = {"input", "weight", "output", "state"};
+        for (int r = 0; r < 4; r++)
+            for (const auto& [id, v] : g.values)
+                if ((r == 0 && v.input) || (r == 1 && v.weight) || (r == 2 && v.output) || (r == 3 && v.state))
+                    out += std::string(roles[r]) + " " + std::to_string(id) + "\n";
+        auto ids = [](const std::vector<int>& l) {
+            if (l.empty()) return std::string("-");
+            std::string t;
+            for (size_t k = 0; k < l.size(); k++) t += (k ? "," : "") + std::to_string(l[k]);
+            return t;
+        };
+        for (const Node& n : g.nodes) {
+            out += "node " + n.op + " " + ids(n.in) + " -> " + ids(n.out);
+            for (const auto& [k, v] : n.attr) out += " " + k + "=" + v;  // std::map: sorted by key
+            out += "\n";
+        }
+        put_text(out, buf, size);
     });
 }
 

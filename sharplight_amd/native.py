@@ -197,6 +197,7 @@ SIGNATURES = {
     "slhip_segment_device_bytes": (_I, [_P, ctypes.POINTER(_I64)]),
     "slhip_segment_launches": (_I, [_P, ctypes.c_char_p, _SZ]),
     "slhip_segment_plan": (_I, [ctypes.c_char_p, ctypes.c_char_p, _SZ]),
+    "slhip_segment_describe": (_I, [ctypes.c_char_p, ctypes.c_char_p, _SZ]),
     "slhip_segment_destroy": (_I, [_P]),
     "slhip_gguf_open": (_I, [ctypes.c_char_p, ctypes.POINTER(_P)]),
     "slhip_gguf_open_prefix": (_I, [_P, _SZ, ctypes.POINTER(_P)]),

@@ -215,10 +215,25 @@ def plan(graph: "GraphBuilder") -> list[str]:
     return [s for s in buf.value.decode().split("\n") if s]
 
 
+def describe(text: str) -> str:
+    """The segment text as the provider parsed it, in canonical form (slhip_segment_describe)."""
+    buf = ctypes.create_string_buffer(1 << 16)
+    native.call("slhip_segment_describe", text.encode(), buf, len(buf))
+    return buf.value.decode()
+
+
 def _fmt(v) -> str:
+    """An attribute value as segment text: floats round-trip (repr), booleans true/false, lists comma-joined."""
+    if isinstance(v, bool):
+        return "true" if v else "false"
     if isinstance(v, float):
         return repr(float(v))
-    return str(v)
+    if isinstance(v, (list, tuple)):
+        return ",".join(_fmt(x) for x in v)
+    s = str(v)
+    if not s or any(c.isspace() for c in s):
+        raise ValueError(f"attribute value {v!r} cannot be written as one token")
+    return s
 
 
 @dataclass(frozen=True)

@@ -5,7 +5,7 @@ import ctypes
 import pytest
 
 from sharplight_amd import native
-from sharplight_amd.provider import GraphBuilder, HipExecutionProvider, plan
+from sharplight_amd.provider import GraphBuilder, HipExecutionProvider, _fmt, describe, plan
 
 
 def _supports(g: GraphBuilder, k: int):
@@ -35,6 +35,63 @@ def test_segment_text():
     assert "node Add 0,1 -> 3" in ir
     assert "node RmsNorm 3,2 -> 4 eps=1e-05" in ir
     assert "weight 2" in ir and "output 3" in ir and "output 4" in ir
+
+
+def _canonical(g: GraphBuilder) -> str:
+    """The builder's own objects written in the provider's canonical order (independent of to_ir)."""
+    out = [f"value {v.id} {v.type}" + "".join(f" {d}" for d in v.dims) for v in sorted(g.values, key=lambda v: v.id)]
+    for role, vals in (("input", g.inputs), ("weight", g.weights), ("output", g.outputs), ("state", g.states)):
+        out += [f"{role} {i}" for i in sorted({v.id for v in vals})]
+    for n in g.nodes:
+        ids = lambda l: ",".join(str(v.id) for v in l) or "-"
+        out.append(f"node {n.op} {ids(n.inputs)} -> {ids(n.outputs)}" +
+                   "".join(f" {k}={_fmt(n.attrs[k])}" for k in sorted(n.attrs)))
+    return "\n".join(out) + "\n"
+
+
+def test_segment_text_round_trip():
+    """to_ir() parses back (slhip_segment_describe) to the same values, roles, nodes and attributes, over
+    every statement kind, the block types, the symbolic T, states, empty lists and the attribute spellings
+    (floats incl. +-inf, booleans, section lists, scalar names)."""
+    g = GraphBuilder()
+    x = g.input("bf16", "T", 4096)
+    r = g.input("f32", "T", 4096)
+    pos = g.input("i32", "T", 4)
+    ids = g.input("i32", "T")
+    cache = g.state("f16", 32768, 8, 128)
+    w = g.weight("f32", 4096)
+    b = g.weight("f32", 4096)
+    ff = g.weight("f32", 64)
+    emb = {t: g.weight(t, 1024, 4096) for t in ("q8_0", "q4_k", "iq2_xxs", "nf4_b64", "q2_0_g128", "f8e4m3_b128")}
+    h = g.add(x, r)
+    y = g.rms_norm(h, w, eps=1e-6)
+    g.layer_norm(y, w, b, eps=1e-5, out_type="bf16")
+    q = g.value("bf16", "T", 32, 128)
+    g.nodes.append(type(g.nodes[0])("Reshape", [y], [q], {}))
+    k = g.rope(q, pos, ff, dims=128, base=1e6, style="normal", freq_scale=0.25, attn_factor=1.5,
+               sections=[16, 24, 24, 0], interleaved=True, sections_per_element=True)
+    g.cache_write(cache, k, offset="n_past", slots=2, block_size=16)
+    g.output(g.clip(g.scale(y, scale=0.125, bias=-3.0), min=float("-inf"), max=6.0))
+    g.output(g.binary("Mod", y, w, fmod=True))
+    for t, e in emb.items():
+        g.output(g.gather(e, ids, out_type="bf16"))
+    g.output(g.matmul(y, emb["q4_k"], out_type="f32"))
+    g.output(g.cast(y, "f16"))
+    g.output(g.unary("LeakyRelu", y, alpha=0.01))
+    ir = g.to_ir()
+    assert describe(ir) == _canonical(g)
+    # the canonical text is a fixed point
+    assert describe(describe(ir)) == describe(ir)
+
+
+def test_segment_text_refuses_other_symbols_and_small_buffers():
+    with pytest.raises(native.SlhipArgumentError, match="neither a size nor the token count T"):
+        describe("value 0 f32 N 64\n")
+    with pytest.raises(native.SlhipArgumentError, match="too small"):
+        buf = ctypes.create_string_buffer(8)
+        native.call("slhip_segment_describe", b"value 0 f32 T 64\n", buf, len(buf))
+    with pytest.raises(ValueError):
+        _fmt("two words")
 
 
 def test_supports_answers():
