@@ -106,7 +106,15 @@ typedef enum slhip_format {
     SLHIP_FMT_F8E4M3 = 39,     /* OCP E4M3FN bytes                                                          */
     SLHIP_FMT_F8E5M2 = 40,     /* E5M2 bytes (the top byte of an IEEE half)                                 */
     SLHIP_FMT_F8E4M3_B32 = 41, /* 32 values, 36 bytes: f32 d, E4M3 q[32] -> e4m3(q)*d                       */
-    SLHIP_FMT_F8E4M3_B128 = 42 /* 128 values, 132 bytes                                                     */
+    SLHIP_FMT_F8E4M3_B128 = 42, /* 128 values, 132 bytes                                                    */
+    /* Trellis-coded, 128 values: f16 d, then the path bytes of N steps of V values and K new bits each; step t's
+     * 16-bit state hashes to codebook points, value = d * point (src/Sharplight.Core/Tensors/TrellisBlocks.cs) */
+    SLHIP_FMT_TRELLIS_V4K8_G128 = 43, /* 34 bytes: V = 4, K = 8 (states from byte pairs)                     */
+    SLHIP_FMT_TRELLIS_V4K6_G128 = 44, /* 26 bytes: V = 4, K = 6 (states from a circular bit stream)          */
+    SLHIP_FMT_TRELLIS_V4K7_G128 = 45, /* 30 bytes: V = 4, K = 7                                              */
+    SLHIP_FMT_TRELLIS_V2K5_G128 = 46, /* 42 bytes: V = 2, K = 5                                              */
+    SLHIP_FMT_TRELLIS_V2K6_G128 = 47, /* 50 bytes: V = 2, K = 6                                              */
+    SLHIP_FMT_TRELLIS_V2K7_G128 = 48  /* 58 bytes: V = 2, K = 7                                              */
 } slhip_format;
 
 /* Row-norm kinds (StandardOps RmsNorm / L2Norm / LayerNorm). */
@@ -360,7 +368,7 @@ SLHIP_API int slhip_rope(int dtype_in, int dtype_out, const slhip_rope_tensor* t
  * [0, V) leaves its output row zero and raises SLHIP_ERR_INDEX at the next slhip_stream_sync.
  * Formats: F32, F16, BF16, Q8_0, Q4_0, Q4_1, Q5_0, Q5_1 (D a multiple of 32), Q2_K..Q6_K, IQ4_XS, TQ1_0
  * and TQ2_0 and the grid IQ formats IQ2_XXS..IQ1_M (D a multiple of 256), IQ4_NL and MXFP4 (32), NVFP4 (64),
- * and the reference's formats Q1_0 .. F8E4M3_B128 (D a multiple of their block size).
+ * and the reference's formats Q1_0 .. F8E4M3_B128 and the trellis formats (D a multiple of their block size).
  * Replaces: GatherOp (src/Sharplight.Cpu/GatherOp.cs:22-75) with Quant.Dequantize
  * (src/Sharplight.Cpu/Quant.cs:242-446,500-624; Quant.KQuants.cs:36-107), and the Vulkan gather
  * (GraphLowerer.Transformer.cs:133-179, Kernels/data.slang:4-37).

@@ -25,7 +25,8 @@ _LIB_PATH = os.path.join(_HERE, "liboracle.so")
  NVFP4, IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_S, IQ1_M) = range(26)
 # the reference's own formats, numbered like the C ABI
 REF_FORMATS = ["q1_0", "q2_0", "q2_0_g128", "tern1_g128", "nvfp4_gs", "q4z_g32", "q4z_g128", "q8z_g32", "q8z_g128",
-               "nf4_b64", "fp4_b64", "q8a_g32", "q2s_g128", "f8e4m3", "f8e5m2", "f8e4m3_b32", "f8e4m3_b128"]
+               "nf4_b64", "fp4_b64", "q8a_g32", "q2s_g128", "f8e4m3", "f8e5m2", "f8e4m3_b32", "f8e4m3_b128",
+               "trellis_v4k8_g128", "trellis_v4k6_g128", "trellis_v4k7_g128", "trellis_v2k5_g128", "trellis_v2k6_g128", "trellis_v2k7_g128"]
 FORMATS = {"f32": F32, "f16": F16, "bf16": BF16, "q8_0": Q8_0, "q4_0": Q4_0, "q4_1": Q4_1, "q5_0": Q5_0,
            "q5_1": Q5_1, "q2_k": Q2_K, "q3_k": Q3_K, "q4_k": Q4_K, "q5_k": Q5_K, "q6_k": Q6_K, "iq4_nl": IQ4_NL,
            "iq4_xs": IQ4_XS, "tq1_0": TQ1_0, "tq2_0": TQ2_0, "mxfp4": MXFP4, "nvfp4": NVFP4,

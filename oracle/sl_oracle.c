@@ -15,6 +15,7 @@
 #include <math.h>
 
 #include "../sharplight_amd/csrc/iq_grids.h" /* ggml's lattice tables: data of the grid IQ formats */
+#include "../sharplight_amd/csrc/trellis_codebook.h" /* the trellis formats' codebook: data of the formats */
 #include <pthread.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -606,6 +607,8 @@ static int block_size(int fmt)
     switch (fmt) {  /* the reference's own formats (Quant.BlockSize, Quant.cs:181-198) */
     case ORC_Q1_0: case ORC_Q2_0_G128: case ORC_TERN1_G128: case ORC_Q2S_G128: case ORC_Q4Z_G128: case ORC_Q8Z_G128:
     case ORC_F8E4M3_B128: return 128;
+    case ORC_TRELLIS_V4K8: case ORC_TRELLIS_V4K6: case ORC_TRELLIS_V4K7: case ORC_TRELLIS_V2K5: case ORC_TRELLIS_V2K6:
+    case ORC_TRELLIS_V2K7: return 128;
     case ORC_Q2_0: case ORC_NVFP4_GS: case ORC_NF4_B64: case ORC_FP4_B64: return 64;
     case ORC_Q4Z_G32: case ORC_Q8Z_G32: case ORC_Q8A_G32: case ORC_F8E4M3_B32: return 32;
     case ORC_F8E4M3: case ORC_F8E5M2: return 1;
@@ -654,6 +657,13 @@ static int block_bytes(int fmt)
     case ORC_Q8Z_G32: case ORC_NF4_B64: case ORC_FP4_B64: case ORC_Q8A_G32: case ORC_Q2S_G128: case ORC_F8E4M3_B32: return 36;
     case ORC_Q8Z_G128: case ORC_F8E4M3_B128: return 132;
     case ORC_F8E4M3: case ORC_F8E5M2: return 1;
+    /* DataType.TrellisV4K8_G128 .. TrellisV2K7_G128 (DataType.cs:212-223): 2 + steps * bits / 8 */
+    case ORC_TRELLIS_V4K8: return 34;
+    case ORC_TRELLIS_V4K6: return 26;
+    case ORC_TRELLIS_V4K7: return 30;
+    case ORC_TRELLIS_V2K5: return 42;
+    case ORC_TRELLIS_V2K6: return 50;
+    case ORC_TRELLIS_V2K7: return 58;
     default: return -1;
     }
 }
@@ -874,9 +884,44 @@ static const float kFp4Book[16] = {
 static float rd_f32(const uint8_t* p) { float f; memcpy(&f, p, 4); return f; }
 
 /* One block of the reference's own formats, restated from its decoders in their loop order. */
+/* TrellisBlocks.State (src/Sharplight.Core/Tensors/TrellisBlocks.cs:61-73): step t's 16-bit state */
+static uint32_t trellis_state(const uint8_t* qs, int v, int k, int t)
+{
+    const int steps = 128 / v;
+    if (k == 8) return (uint32_t)qs[(t + steps - 1) % steps] << 8 | qs[t];
+    const int bytes = steps * k / 8, off = (steps - 1 - t) * k, i0 = off >> 3;
+    const uint32_t w = qs[i0] | (uint32_t)qs[(i0 + 1) % bytes] << 8 | (uint32_t)qs[(i0 + 2) % bytes] << 16;
+    return (w >> (off & 7)) & 0xffffu;
+}
+
+/* TrellisBlocks.DecodeBlock (TrellisBlocks.cs:80-102): the state's low 15 bits times 0x9e3779b1 (mod 2^32);
+ * point x >> 21 (and, 4 values per step, point (x >> 10) & 2047) of the f16 codebook, each value d * point */
+static void trellis_block(int v, int k, const uint8_t* p, float* dst)
+{
+    const float d = rd_h(p);
+    int o = 0;
+    for (int t = 0; t < 128 / v; t++) {
+        const uint32_t x = (trellis_state(p + 2, v, k, t) & 0x7fffu) * 0x9e3779b1u;
+        uint32_t pt = x >> 21;
+        dst[o++] = d * orc_f16_to_f32(kTrellisCodebook[2 * pt]);
+        dst[o++] = d * orc_f16_to_f32(kTrellisCodebook[2 * pt + 1]);
+        if (v == 4) {
+            pt = (x >> 10) & 2047u;
+            dst[o++] = d * orc_f16_to_f32(kTrellisCodebook[2 * pt]);
+            dst[o++] = d * orc_f16_to_f32(kTrellisCodebook[2 * pt + 1]);
+        }
+    }
+}
+
 static void refblock(int fmt, const uint8_t* p, float* dst)
 {
     switch (fmt) {
+    case ORC_TRELLIS_V4K8: trellis_block(4, 8, p, dst); break;
+    case ORC_TRELLIS_V4K6: trellis_block(4, 6, p, dst); break;
+    case ORC_TRELLIS_V4K7: trellis_block(4, 7, p, dst); break;
+    case ORC_TRELLIS_V2K5: trellis_block(2, 5, p, dst); break;
+    case ORC_TRELLIS_V2K6: trellis_block(2, 6, p, dst); break;
+    case ORC_TRELLIS_V2K7: trellis_block(2, 7, p, dst); break;
     case ORC_Q1_0: {  /* Quant.Q1_0 (Quant.cs:656-669): lut[byte][i] = bit i ? +1 : -1, times d */
         const float d = rd_h(p);
         for (int j = 0; j < 16; j++)

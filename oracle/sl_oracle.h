@@ -28,7 +28,10 @@ enum { ORC_F32 = 0, ORC_F16 = 1, ORC_BF16 = 2, ORC_Q8_0 = 3, ORC_Q4_0 = 4, ORC_Q
        /* the reference's own formats */
        ORC_Q1_0 = 26, ORC_Q2_0 = 27, ORC_Q2_0_G128 = 28, ORC_TERN1_G128 = 29, ORC_NVFP4_GS = 30, ORC_Q4Z_G32 = 31,
        ORC_Q4Z_G128 = 32, ORC_Q8Z_G32 = 33, ORC_Q8Z_G128 = 34, ORC_NF4_B64 = 35, ORC_FP4_B64 = 36, ORC_Q8A_G32 = 37,
-       ORC_Q2S_G128 = 38, ORC_F8E4M3 = 39, ORC_F8E5M2 = 40, ORC_F8E4M3_B32 = 41, ORC_F8E4M3_B128 = 42 };
+       ORC_Q2S_G128 = 38, ORC_F8E4M3 = 39, ORC_F8E5M2 = 40, ORC_F8E4M3_B32 = 41, ORC_F8E4M3_B128 = 42,
+       /* trellis-coded (TrellisBlocks.cs), 128 values per block */
+       ORC_TRELLIS_V4K8 = 43, ORC_TRELLIS_V4K6 = 44, ORC_TRELLIS_V4K7 = 45, ORC_TRELLIS_V2K5 = 46,
+       ORC_TRELLIS_V2K6 = 47, ORC_TRELLIS_V2K7 = 48 };
 /* E4M3FN / E5M2 byte -> f32 (Quant.E4m3ToFloat, Quant.BuildE5m2) */
 float orc_e4m3_value(uint8_t x);
 float orc_e5m2_value(uint8_t x);

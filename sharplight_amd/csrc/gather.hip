@@ -278,6 +278,12 @@ __global__ __launch_bounds__(256) void gather_scalar(GatherArgs a, int fmt)
             case SLHIP_FMT_F8E5M2: v = kv(std::integral_constant<int, SLHIP_FMT_F8E5M2>{}); break;
             case SLHIP_FMT_F8E4M3_B32: v = kv(std::integral_constant<int, SLHIP_FMT_F8E4M3_B32>{}); break;
             case SLHIP_FMT_F8E4M3_B128: v = kv(std::integral_constant<int, SLHIP_FMT_F8E4M3_B128>{}); break;
+            case SLHIP_FMT_TRELLIS_V4K8_G128: v = kv(std::integral_constant<int, SLHIP_FMT_TRELLIS_V4K8_G128>{}); break;
+            case SLHIP_FMT_TRELLIS_V4K6_G128: v = kv(std::integral_constant<int, SLHIP_FMT_TRELLIS_V4K6_G128>{}); break;
+            case SLHIP_FMT_TRELLIS_V4K7_G128: v = kv(std::integral_constant<int, SLHIP_FMT_TRELLIS_V4K7_G128>{}); break;
+            case SLHIP_FMT_TRELLIS_V2K5_G128: v = kv(std::integral_constant<int, SLHIP_FMT_TRELLIS_V2K5_G128>{}); break;
+            case SLHIP_FMT_TRELLIS_V2K6_G128: v = kv(std::integral_constant<int, SLHIP_FMT_TRELLIS_V2K6_G128>{}); break;
+            case SLHIP_FMT_TRELLIS_V2K7_G128: v = kv(std::integral_constant<int, SLHIP_FMT_TRELLIS_V2K7_G128>{}); break;
             case SLHIP_FMT_F32: {
                 uint32_t u = p[4 * j] | (p[4 * j + 1] << 8) | (p[4 * j + 2] << 16) | (static_cast<uint32_t>(p[4 * j + 3]) << 24);
                 v = __uint_as_float(u);
@@ -358,6 +364,12 @@ static int block_bytes(int fmt)
     case SLHIP_FMT_F8E5M2: return 1;
     case SLHIP_FMT_F8E4M3_B32: return 36;
     case SLHIP_FMT_F8E4M3_B128: return 132;
+    case SLHIP_FMT_TRELLIS_V4K8_G128: return 34;
+    case SLHIP_FMT_TRELLIS_V4K6_G128: return 26;
+    case SLHIP_FMT_TRELLIS_V4K7_G128: return 30;
+    case SLHIP_FMT_TRELLIS_V2K5_G128: return 42;
+    case SLHIP_FMT_TRELLIS_V2K6_G128: return 50;
+    case SLHIP_FMT_TRELLIS_V2K7_G128: return 58;
     default: return -1;
     }
 }
@@ -369,7 +381,9 @@ static int block_values(int fmt)
     case SLHIP_FMT_Q8_0: case SLHIP_FMT_Q4_0: case SLHIP_FMT_Q4_1: case SLHIP_FMT_Q5_0: case SLHIP_FMT_Q5_1:
     case SLHIP_FMT_IQ4_NL: case SLHIP_FMT_MXFP4: return 32;
     case SLHIP_FMT_NVFP4: return 64;
-    case SLHIP_FMT_Q1_0: case SLHIP_FMT_Q2_0_G128: case SLHIP_FMT_TERN1_G128: case SLHIP_FMT_Q4Z_G128: case SLHIP_FMT_Q8Z_G128: case SLHIP_FMT_Q2S_G128: case SLHIP_FMT_F8E4M3_B128: return 128;
+    case SLHIP_FMT_Q1_0: case SLHIP_FMT_Q2_0_G128: case SLHIP_FMT_TERN1_G128: case SLHIP_FMT_Q4Z_G128: case SLHIP_FMT_Q8Z_G128: case SLHIP_FMT_Q2S_G128: case SLHIP_FMT_F8E4M3_B128:
+    case SLHIP_FMT_TRELLIS_V4K8_G128: case SLHIP_FMT_TRELLIS_V4K6_G128: case SLHIP_FMT_TRELLIS_V4K7_G128:
+    case SLHIP_FMT_TRELLIS_V2K5_G128: case SLHIP_FMT_TRELLIS_V2K6_G128: case SLHIP_FMT_TRELLIS_V2K7_G128: return 128;
     case SLHIP_FMT_Q2_0: case SLHIP_FMT_NVFP4_GS: case SLHIP_FMT_NF4_B64: case SLHIP_FMT_FP4_B64: return 64;
     case SLHIP_FMT_Q4Z_G32: case SLHIP_FMT_Q8Z_G32: case SLHIP_FMT_Q8A_G32: case SLHIP_FMT_F8E4M3_B32: return 32;
     case SLHIP_FMT_F8E4M3: case SLHIP_FMT_F8E5M2: return 1;
@@ -507,6 +521,12 @@ static int dispatch(int fmt, GatherArgs a, hipStream_t st)
         case SLHIP_FMT_F8E5M2: return launch_quant<SLHIP_FMT_F8E5M2, DTO>(a, st);
         case SLHIP_FMT_F8E4M3_B32: return launch_quant<SLHIP_FMT_F8E4M3_B32, DTO>(a, st);
         case SLHIP_FMT_F8E4M3_B128: return launch_quant<SLHIP_FMT_F8E4M3_B128, DTO>(a, st);
+        case SLHIP_FMT_TRELLIS_V4K8_G128: return launch_quant<SLHIP_FMT_TRELLIS_V4K8_G128, DTO>(a, st);
+        case SLHIP_FMT_TRELLIS_V4K6_G128: return launch_quant<SLHIP_FMT_TRELLIS_V4K6_G128, DTO>(a, st);
+        case SLHIP_FMT_TRELLIS_V4K7_G128: return launch_quant<SLHIP_FMT_TRELLIS_V4K7_G128, DTO>(a, st);
+        case SLHIP_FMT_TRELLIS_V2K5_G128: return launch_quant<SLHIP_FMT_TRELLIS_V2K5_G128, DTO>(a, st);
+        case SLHIP_FMT_TRELLIS_V2K6_G128: return launch_quant<SLHIP_FMT_TRELLIS_V2K6_G128, DTO>(a, st);
+        case SLHIP_FMT_TRELLIS_V2K7_G128: return launch_quant<SLHIP_FMT_TRELLIS_V2K7_G128, DTO>(a, st);
         case SLHIP_FMT_F16: return launch_plain<SLHIP_FMT_F16, DTO>(a, st);
         case SLHIP_FMT_BF16: return launch_plain<SLHIP_FMT_BF16, DTO>(a, st);
         case SLHIP_FMT_F32: return launch_plain<SLHIP_FMT_F32, DTO>(a, st);

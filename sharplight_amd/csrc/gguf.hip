@@ -139,12 +139,12 @@ TypeDesc type_desc(int id)
     }
     case 142: return t("q2_0_g128", 128, 34, SLHIP_FMT_Q2_0_G128);   // PrismML PQ2_0
     case 143: return t("tern1_g128", 128, 28, SLHIP_FMT_TERN1_G128);  // PrismML PTQ1_0
-    case 144: return t("trellis_v4k8_g128", 128, 34);
-    case 145: return t("trellis_v4k6_g128", 128, 26);
-    case 146: return t("trellis_v4k7_g128", 128, 30);
-    case 147: return t("trellis_v2k5_g128", 128, 42);
-    case 148: return t("trellis_v2k6_g128", 128, 50);
-    case 149: return t("trellis_v2k7_g128", 128, 58);
+    case 144: return t("trellis_v4k8_g128", 128, 34, SLHIP_FMT_TRELLIS_V4K8_G128);
+    case 145: return t("trellis_v4k6_g128", 128, 26, SLHIP_FMT_TRELLIS_V4K6_G128);
+    case 146: return t("trellis_v4k7_g128", 128, 30, SLHIP_FMT_TRELLIS_V4K7_G128);
+    case 147: return t("trellis_v2k5_g128", 128, 42, SLHIP_FMT_TRELLIS_V2K5_G128);
+    case 148: return t("trellis_v2k6_g128", 128, 50, SLHIP_FMT_TRELLIS_V2K6_G128);
+    case 149: return t("trellis_v2k7_g128", 128, 58, SLHIP_FMT_TRELLIS_V2K7_G128);
     default: return TypeDesc{};
     }
 }

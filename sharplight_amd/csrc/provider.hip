@@ -66,7 +66,7 @@ void check(int st)
 // ---- graph ---------------------------------------------------------------------------------------------
 
 enum class DType { F32, F16, BF16, I32, Q8_0, Q4_0, Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS, TQ1_0, TQ2_0, MXFP4, NVFP4,
-                   IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_S, IQ1_M, Q1_0, Q2_0, Q2_0_G128, TERN1_G128, NVFP4_GS, Q4Z_G32, Q4Z_G128, Q8Z_G32, Q8Z_G128, NF4_B64, FP4_B64, Q8A_G32, Q2S_G128, F8E4M3, F8E5M2, F8E4M3_B32, F8E4M3_B128 };
+                   IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_S, IQ1_M, Q1_0, Q2_0, Q2_0_G128, TERN1_G128, NVFP4_GS, Q4Z_G32, Q4Z_G128, Q8Z_G32, Q8Z_G128, NF4_B64, FP4_B64, Q8A_G32, Q2S_G128, F8E4M3, F8E5M2, F8E4M3_B32, F8E4M3_B128, TRELLIS_V4K8_G128, TRELLIS_V4K6_G128, TRELLIS_V4K7_G128, TRELLIS_V2K5_G128, TRELLIS_V2K6_G128, TRELLIS_V2K7_G128 };
 
 struct TypeInfo {
     const char* name;
@@ -102,6 +102,12 @@ const TypeInfo kTypes[] = {
     {"f8e5m2", DType::F8E5M2, 1, 1},
     {"f8e4m3_b32", DType::F8E4M3_B32, 32, 36},
     {"f8e4m3_b128", DType::F8E4M3_B128, 128, 132},
+    {"trellis_v4k8_g128", DType::TRELLIS_V4K8_G128, 128, 34},
+    {"trellis_v4k6_g128", DType::TRELLIS_V4K6_G128, 128, 26},
+    {"trellis_v4k7_g128", DType::TRELLIS_V4K7_G128, 128, 30},
+    {"trellis_v2k5_g128", DType::TRELLIS_V2K5_G128, 128, 42},
+    {"trellis_v2k6_g128", DType::TRELLIS_V2K6_G128, 128, 50},
+    {"trellis_v2k7_g128", DType::TRELLIS_V2K7_G128, 128, 58},
 };
 
 const TypeInfo& type_info(DType t)
@@ -169,6 +175,12 @@ int format_code(DType t)
     case DType::F8E5M2: return SLHIP_FMT_F8E5M2;
     case DType::F8E4M3_B32: return SLHIP_FMT_F8E4M3_B32;
     case DType::F8E4M3_B128: return SLHIP_FMT_F8E4M3_B128;
+    case DType::TRELLIS_V4K8_G128: return SLHIP_FMT_TRELLIS_V4K8_G128;
+    case DType::TRELLIS_V4K6_G128: return SLHIP_FMT_TRELLIS_V4K6_G128;
+    case DType::TRELLIS_V4K7_G128: return SLHIP_FMT_TRELLIS_V4K7_G128;
+    case DType::TRELLIS_V2K5_G128: return SLHIP_FMT_TRELLIS_V2K5_G128;
+    case DType::TRELLIS_V2K6_G128: return SLHIP_FMT_TRELLIS_V2K6_G128;
+    case DType::TRELLIS_V2K7_G128: return SLHIP_FMT_TRELLIS_V2K7_G128;
     default: unsupported("gather table type");
     }
 }

@@ -10,8 +10,9 @@
 #include "common.hpp"
 
 // plain device globals: as constant-address-space arrays, per-lane lookups were turned into scalar loads
-#define SLHIP_GRID_QUAL static __device__
+#define SLHIP_GRID_QUAL static __device__ __attribute__((aligned(16)))
 #include "iq_grids.h"
+#include "trellis_codebook.h"
 
 namespace slhip {
 
@@ -61,6 +62,12 @@ SLHIP_KFMT(SLHIP_FMT_F8E4M3, 1, 1)
 SLHIP_KFMT(SLHIP_FMT_F8E5M2, 1, 1)
 SLHIP_KFMT(SLHIP_FMT_F8E4M3_B32, 36, 32)
 SLHIP_KFMT(SLHIP_FMT_F8E4M3_B128, 132, 128)
+SLHIP_KFMT(SLHIP_FMT_TRELLIS_V4K8_G128, 34, 128)
+SLHIP_KFMT(SLHIP_FMT_TRELLIS_V4K6_G128, 26, 128)
+SLHIP_KFMT(SLHIP_FMT_TRELLIS_V4K7_G128, 30, 128)
+SLHIP_KFMT(SLHIP_FMT_TRELLIS_V2K5_G128, 42, 128)
+SLHIP_KFMT(SLHIP_FMT_TRELLIS_V2K6_G128, 50, 128)
+SLHIP_KFMT(SLHIP_FMT_TRELLIS_V2K7_G128, 58, 128)
 #undef SLHIP_KFMT
 
 // The 16-entry code books of NF4_B64 and FP4_B64 (the f32 values bitsandbytes stores as quant_map, as the
@@ -74,7 +81,14 @@ SLHIP_GRID_QUAL const float kFp4Values[16] = {
     0.0f, 0.0052083334885537624f, 0.6666666865348816f, 1.0f, 0.3333333432674408f, 0.5f, 0.1666666716337204f, 0.25f,
     0.0f, -0.0052083334885537624f, -0.6666666865348816f, -1.0f, -0.3333333432674408f, -0.5f, -0.1666666716337204f, -0.25f};
 
-constexpr bool is_reference_fmt(int f) { return f >= SLHIP_FMT_Q1_0 && f <= SLHIP_FMT_F8E4M3_B128; }
+constexpr bool is_reference_fmt(int f) { return f >= SLHIP_FMT_Q1_0 && f <= SLHIP_FMT_TRELLIS_V2K7_G128; }
+constexpr bool is_trellis_fmt(int f) { return f >= SLHIP_FMT_TRELLIS_V4K8_G128 && f <= SLHIP_FMT_TRELLIS_V2K7_G128; }
+
+// Trellis codebook point p: its two f16 values as one word (the table is 16-byte aligned).
+__device__ __forceinline__ uint32_t trellis_point(uint32_t p)
+{
+    return reinterpret_cast<const uint32_t*>(kTrellisCodebook)[p];
+}
 
 // An OCP E4M3FN byte as f32 (exact): bias 7, exponent 0 subnormal (m * 2^-9), 0x7F and 0xFF NaN, no infinity
 // (Quant.E4m3ToFloat, src/Sharplight.Cpu/Quant.Fp8.cs:37-49).
@@ -471,6 +485,41 @@ __device__ __forceinline__ void decode_ref(const B& b, int o, int k, float* f)
 #pragma unroll
             for (int e = 0; e < 4; e++)
                 f[4 * x + e] = __fmul_rn(static_cast<float>(static_cast<int>((w >> (8 * e + sh)) & 3u) - 1), d);
+        }
+    } else if constexpr (is_trellis_fmt(FMT)) {
+        // {f16 d; path bytes}: step t (V values) has a 16-bit state, for K = 8 the bytes t-1 (mod steps) and t,
+        // otherwise the 16 bits at bit (steps-1-t)*K of the circular K*steps-bit stream, LSB first; the low 15
+        // bits hash to x = s * 0x9e3779b1 (mod 2^32), codebook point x >> 21 gives values 0-1 of the step and
+        // (V = 4) point (x >> 10) & 2047 values 2-3; value = d * point (TrellisBlocks.State / DecodeBlock,
+        // src/Sharplight.Core/Tensors/TrellisBlocks.cs:61-102)
+        constexpr int V = FMT <= SLHIP_FMT_TRELLIS_V4K7_G128 ? 4 : 2;
+        constexpr int KB = FMT == SLHIP_FMT_TRELLIS_V4K8_G128 ? 8 : FMT == SLHIP_FMT_TRELLIS_V4K6_G128 ? 6
+                         : FMT == SLHIP_FMT_TRELLIS_V4K7_G128 ? 7 : FMT == SLHIP_FMT_TRELLIS_V2K5_G128 ? 5
+                         : FMT == SLHIP_FMT_TRELLIS_V2K6_G128 ? 6 : 7;
+        constexpr int STEPS = 128 / V, BYTES = STEPS * KB / 8;
+        const float d = b.h(o);
+        const int qs = o + 2;
+#pragma unroll
+        for (int s = 0; s < N / V; s++) {
+            const int t = k / V + s;
+            uint32_t st;
+            if constexpr (KB == 8) {
+                st = (byte_at(qs + (t + STEPS - 1) % STEPS) << 8) | byte_at(qs + t);
+            } else {
+                const int off = (STEPS - 1 - t) * KB, i0 = off >> 3;
+                const uint32_t w = byte_at(qs + i0) | (byte_at(qs + (i0 + 1) % BYTES) << 8) |
+                                   (byte_at(qs + (i0 + 2) % BYTES) << 16);
+                st = (w >> (off & 7)) & 0xFFFFu;
+            }
+            const uint32_t x = (st & 0x7FFFu) * 0x9E3779B1u;
+            const uint32_t p0 = trellis_point(x >> 21);
+            f[V * s + 0] = __fmul_rn(d, f16_lo(p0));
+            f[V * s + 1] = __fmul_rn(d, f16_hi(p0));
+            if constexpr (V == 4) {
+                const uint32_t p1 = trellis_point((x >> 10) & 2047u);
+                f[V * s + 2] = __fmul_rn(d, f16_lo(p1));
+                f[V * s + 3] = __fmul_rn(d, f16_hi(p1));
+            }
         }
     } else {
         // FP8: plain E4M3 / E5M2 bytes (times 1), or {f32 d; E4M3 q[block]} -> e4m3(q) * d

@@ -24,9 +24,10 @@ NP_DTYPES = {F32: np.float32, F16: np.float16, BF16: np.uint16}  # bf16 travels 
 (FMT_F32, FMT_F16, FMT_BF16, FMT_Q8_0, FMT_Q4_0, FMT_Q4_1, FMT_Q5_0, FMT_Q5_1, FMT_Q2_K, FMT_Q3_K, FMT_Q4_K,
  FMT_Q5_K, FMT_Q6_K, FMT_IQ4_NL, FMT_IQ4_XS, FMT_TQ1_0, FMT_TQ2_0, FMT_MXFP4, FMT_NVFP4, FMT_IQ2_XXS, FMT_IQ2_XS,
  FMT_IQ2_S, FMT_IQ3_XXS, FMT_IQ3_S, FMT_IQ1_S, FMT_IQ1_M) = range(26)
-# the reference's own formats (slhip_format 26..42)
+# the reference's own formats (slhip_format 26..48, the trellis formats last)
 REF_FORMATS = ["q1_0", "q2_0", "q2_0_g128", "tern1_g128", "nvfp4_gs", "q4z_g32", "q4z_g128", "q8z_g32", "q8z_g128",
-               "nf4_b64", "fp4_b64", "q8a_g32", "q2s_g128", "f8e4m3", "f8e5m2", "f8e4m3_b32", "f8e4m3_b128"]
+               "nf4_b64", "fp4_b64", "q8a_g32", "q2s_g128", "f8e4m3", "f8e5m2", "f8e4m3_b32", "f8e4m3_b128",
+               "trellis_v4k8_g128", "trellis_v4k6_g128", "trellis_v4k7_g128", "trellis_v2k5_g128", "trellis_v2k6_g128", "trellis_v2k7_g128"]
 FORMATS = {"f32": FMT_F32, "f16": FMT_F16, "bf16": FMT_BF16, "q8_0": FMT_Q8_0, "q4_0": FMT_Q4_0,
            "q4_1": FMT_Q4_1, "q5_0": FMT_Q5_0, "q5_1": FMT_Q5_1, "q2_k": FMT_Q2_K, "q3_k": FMT_Q3_K,
            "q4_k": FMT_Q4_K, "q5_k": FMT_Q5_K, "q6_k": FMT_Q6_K, "iq4_nl": FMT_IQ4_NL, "iq4_xs": FMT_IQ4_XS,

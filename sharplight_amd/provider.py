@@ -30,7 +30,9 @@ BLOCKS = {"q8_0": (32, 34), "q4_0": (32, 18), "q4_1": (32, 20), "q5_0": (32, 22)
           "q1_0": (128, 18), "q2_0": (64, 18), "q2_0_g128": (128, 34), "tern1_g128": (128, 28), "nvfp4_gs": (64, 40),
           "q4z_g32": (32, 20), "q4z_g128": (128, 68), "q8z_g32": (32, 36), "q8z_g128": (128, 132), "nf4_b64": (64, 36),
           "fp4_b64": (64, 36), "q8a_g32": (32, 36), "q2s_g128": (128, 36), "f8e4m3": (1, 1), "f8e5m2": (1, 1),
-          "f8e4m3_b32": (32, 36), "f8e4m3_b128": (128, 132)}
+          "f8e4m3_b32": (32, 36), "f8e4m3_b128": (128, 132), "trellis_v4k8_g128": (128, 34),
+          "trellis_v4k6_g128": (128, 26), "trellis_v4k7_g128": (128, 30), "trellis_v2k5_g128": (128, 42),
+          "trellis_v2k6_g128": (128, 50), "trellis_v2k7_g128": (128, 58)}
 ELEM_BYTES = {"f32": 4, "f16": 2, "bf16": 2, "i32": 4}
 
 

@@ -53,7 +53,10 @@ REFBLOCK = {"q1_0": (18, 128, (("h", 0),)), "q2_0": (18, 64, (("h", 0),)), "q2_0
             "q8z_g32": (36, 32, (("h", 0), ("z8", 2))), "q8z_g128": (132, 128, (("h", 0), ("z8", 2))),
             "nf4_b64": (36, 64, (("f", 0),)), "fp4_b64": (36, 64, (("f", 0),)), "q8a_g32": (36, 32, (("f", 0),)),
             "q2s_g128": (36, 128, (("f", 0),)), "f8e4m3": (1, 1, ()), "f8e5m2": (1, 1, ()),
-            "f8e4m3_b32": (36, 32, (("f", 0),)), "f8e4m3_b128": (132, 128, (("f", 0),))}
+            "f8e4m3_b32": (36, 32, (("f", 0),)), "f8e4m3_b128": (132, 128, (("f", 0),)),
+            "trellis_v4k8_g128": (34, 128, (("h", 0),)), "trellis_v4k6_g128": (26, 128, (("h", 0),)),
+            "trellis_v4k7_g128": (30, 128, (("h", 0),)), "trellis_v2k5_g128": (42, 128, (("h", 0),)),
+            "trellis_v2k6_g128": (50, 128, (("h", 0),)), "trellis_v2k7_g128": (58, 128, (("h", 0),))}
 
 
 def block_values(fmt: str) -> int:

@@ -189,6 +189,16 @@ def test_gather_reference_formats(device, fmt, dout, D):
     _nan_aware_equal(y, _ref(fmt, t, V, D, ids, dout), dout, f"{fmt}->{dout} D={D}")
 
 
+def test_gather_trellis_reference_fixture(device):
+    """The reference's trellis fixture (tests/golden/trellis_ref.bin: the fork's decoders' values) gathered on
+    the GPU, every row of every record, bit for bit against the fixture itself."""
+    from tests.test_oracle_formats import trellis_fixture
+    for fmt, rows, cols, blocks, expected in trellis_fixture():
+        ids = np.arange(rows, dtype=np.int32)[::-1].copy()
+        y = _run(fmt, np.ascontiguousarray(blocks), rows, cols, ids, "f32")
+        assert np.array_equal(y.view(np.uint32), expected[ids].view(np.uint32)), fmt
+
+
 @pytest.mark.parametrize("fmt", ["f8e4m3", "f8e5m2"])
 def test_gather_every_fp8_code(device, fmt):
     """All 256 codes of the plain FP8 tables to f32, exact (NaN codes as NaN)."""
@@ -197,7 +207,8 @@ def test_gather_every_fp8_code(device, fmt):
     _nan_aware_equal(y, _ref(fmt, t, 1, 4096, np.zeros(1, np.int32), "f32"), "f32", fmt)
 
 
-@pytest.mark.parametrize("fmt", ["nvfp4_gs", "q4z_g32", "q8z_g128", "nf4_b64", "q8a_g32", "f8e4m3_b32"])
+@pytest.mark.parametrize("fmt", ["nvfp4_gs", "q4z_g32", "q8z_g128", "nf4_b64", "q8a_g32", "f8e4m3_b32",
+                                 "trellis_v4k6_g128", "trellis_v2k5_g128"])
 def test_gather_reference_formats_unaligned(device, fmt):
     """A table 2 bytes off 16-byte alignment: the general kernel, same bits."""
     bs = synth.block_values(fmt)

@@ -226,3 +226,65 @@ def test_scaled_e4m3_blocks(fmt, block):
     e4 = np.array([oracle.lib().orc_e4m3_value(int(c)) for c in range(256)], F32)
     want = (e4[blocks[:, 4:]] * d[:, None]).astype(F32)
     assert np.array_equal(got, want, equal_nan=True)
+
+
+TRELLIS_IDS = {144: "trellis_v4k8_g128", 145: "trellis_v4k6_g128", 146: "trellis_v4k7_g128",
+               147: "trellis_v2k5_g128", 148: "trellis_v2k6_g128", 149: "trellis_v2k7_g128"}
+
+
+def trellis_fixture():
+    """tests/golden/trellis_ref.bin, a data file of the reference's tests (tests/Sharplight.Cpu.Tests/Fixtures,
+    read by TrellisDequantTests.cs:49-69): random blocks of each trellis format (ggml ids 144-149 of the
+    fork that introduced them) with the values the fork's decoders give, as (format, rows, cols, block bytes,
+    expected f32 values)."""
+    import os
+    import struct
+    from sharplight_amd import synth
+    b = open(os.path.join(os.path.dirname(__file__), "golden", "trellis_ref.bin"), "rb").read()
+    n, o = struct.unpack_from("<i", b, 0)[0], 4
+    out = []
+    for _ in range(n):
+        t, rows, cols = struct.unpack_from("<iii", b, o)
+        o += 12
+        fmt = TRELLIS_IDS[t]
+        nb = rows * synth.row_bytes(fmt, cols)
+        blocks = np.frombuffer(b, np.uint8, nb, o).reshape(rows, -1)
+        o += nb
+        expected = np.frombuffer(b, np.float32, rows * cols, o).reshape(rows, cols)
+        o += 4 * rows * cols
+        out.append((fmt, rows, cols, blocks, expected))
+    assert o == len(b)
+    return out
+
+
+def test_trellis_matches_the_reference_fixture_bit_for_bit():
+    """TrellisDequantTests.EveryFormat_DequantizesLikeTheReference: every format, every value, same bits."""
+    seen = set()
+    for fmt, rows, cols, blocks, expected in trellis_fixture():
+        got = _deq(fmt, blocks, rows * cols).reshape(rows, cols)
+        assert np.array_equal(got.view(np.uint32), expected.view(np.uint32)), fmt
+        seen.add(fmt)
+    assert seen == set(TRELLIS_IDS.values())
+
+
+@pytest.mark.parametrize("fmt", list(TRELLIS_IDS.values()))
+def test_trellis_scale_is_a_plain_factor(fmt):
+    """value = d * point: with d a power of two every value scales exactly, and d = 0 gives zeros (+-0);
+    the path bytes alone select the points (a block's values with d = 1 are codebook entries)."""
+    from sharplight_amd import synth
+    t = synth.quant_table(fmt, 4, 512, seed=5, tid=9)
+    bb = synth.row_bytes(fmt, 128)
+    blocks = t.reshape(-1, bb).copy()
+    blocks[:, 0:2] = _h(1.0)
+    one = _deq(fmt, blocks, blocks.shape[0] * 128)
+    import os
+    import re
+    text = open(os.path.join(os.path.dirname(__file__), "..", "sharplight_amd", "csrc", "trellis_codebook.h")).read()
+    book = np.array([int(v, 16) for v in re.findall(r"0x[0-9a-f]+", text.split("{", 1)[1])], np.uint16)
+    assert book.size == 4096
+    assert np.isin(one, book.view(np.float16).astype(F32)).all()
+    for k in (-3, 0, 5):
+        blocks[:, 0:2] = _h(2.0 ** k)
+        assert np.array_equal(_deq(fmt, blocks, blocks.shape[0] * 128), one * F32(2.0 ** k))
+    blocks[:, 0:2] = _h(0.0)
+    assert not np.any(_deq(fmt, blocks, blocks.shape[0] * 128))
