@@ -874,6 +874,366 @@ __global__ __launch_bounds__(64 * kMmWaves) void matvec_mfma_lds(MatvecArgs a)
     }
 }
 
+// ---- K-quant weights at one token on the matrix cores (integer MFMA) -------------------------------------
+//
+// The VALU kernel above spends ~4 lane instructions per Q4_K weight (code extraction, conversion, FMA), which
+// holds a decode dual matvec at ~38% of the HBM peak. Here the products run on v_mfma_i32_16x16x64_i8, exact
+// in integers, and the VALU keeps the code masking and the per-sub-block scaling:
+//   * x is written as four 7-bit digits per value against its 32-value block's exponent e:
+//     x = 2^(e-6) (d1 + d2 2^-7 + d3 2^-14 + d4 2^-21) to within 2^(e-28), far below f32 accumulation error
+//     (kq_digits).
+//   * B (64 K x 16 N) is 16 weight rows: lane l holds row l % 16 and 16 codes (bytes, as masked) of its
+//     K-group l / 16. A (16 M x 64 K) holds "slots": K-group g's values appear in slots 4g .. 4g+3 as the four
+//     digit planes, every other slot zero. Output slot 4g + p (lane l holds slots 4 (l / 16) + 0..3 of row
+//     l % 16) is then the exact integer sum S_p of the lane's own codes times digit p.
+//   * After a group's MFMA a lane forms sum q x = 2^(e-6) (S1 + 2^-7 (S2 + 2^-7 (S3 + 2^-7 S4))) and scales
+//     it by its group's scale: Q4_K d0 (that) - m X (X the f32 sum of the block's x), Q6_K d sc (that) with
+//     S_p - 32 sum d_p for the code offset. Rows of zero weights contribute exactly 0 (Q6_K: codes 32) or
+//     exactly -m X (Q4_K: codes 0).
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ i32x4_t as_i32x4(const uint4& v) { return __builtin_bit_cast(i32x4_t, v); }
+
+// Q4_K sub-block j (0..7, runtime) of a super-block header {f16 d, f16 dmin, u8 scales[12]}: d0 = d * sc,
+// m = dmin * mn with the 6-bit sc, mn of Quant.cs:518-545.
+__device__ __forceinline__ void q4k_scales(const uint4& hdr, int j, float& d0, float& m)
+{
+    const int sh = 8 * (j & 3);
+    const uint32_t by = (hdr.y >> sh) & 0xFFu, bz = (hdr.z >> sh) & 0xFFu, bw = (hdr.w >> sh) & 0xFFu;
+    // both forms, then a select by mask (a lane-dependent ternary would become a branch)
+    const uint32_t hi = j < 4 ? 0u : ~0u;
+    const uint32_t sc = ((by & 63u) & ~hi) | (((bw & 15u) | ((by >> 6) << 4)) & hi);
+    const uint32_t mn = ((bz & 63u) & ~hi) | (((bw >> 4) | ((bz >> 6) << 4)) & hi);
+    d0 = __fmul_rn(f16_lo(hdr.x), static_cast<float>(sc));
+    m = __fmul_rn(f16_hi(hdr.x), static_cast<float>(mn));
+}
+
+// sum q x of a lane's sub-block from the digit-plane sums S (slots 0..3) and the block's 2^(e-6)
+__device__ __forceinline__ float digits_dot(const i32x4_t& S, float xs)
+{
+    float f = static_cast<float>(S[3]);
+    f = fmaf(f, 0.0078125f, static_cast<float>(S[2]));
+    f = fmaf(f, 0.0078125f, static_cast<float>(S[1]));
+    f = fmaf(f, 0.0078125f, static_cast<float>(S[0]));
+    return f * xs;
+}
+
+// Digits of x for the integer MFMA: per 32-value block (eight lanes) its exponent e (max |x| = f 2^e, f in [0.5, 1)), its f32
+// sum, and the digit planes of X = rint(x 2^(27-e)) (|X| < 2^27): X = d1 2^21 + d2 2^14 + d3 2^7 + d4 with
+// d2..d4 in 0..127 and d1 = X >> 21 in -64..63, so x = 2^(e-6) (d1 + d2 2^-7 + d3 2^-14 + d4 2^-21) to
+// within 2^(e-28). Four values per lane (eight lanes per block): the four plane words (byte k = value k),
+// 2^(e-6) and the block's sum.
+__device__ __forceinline__ void kq_digits(const float (&xv)[4], uint32_t (&pl)[4], float& down, float& sm)
+{
+    float mx = fmaxf(fmaxf(fabsf(xv[0]), fabsf(xv[1])), fmaxf(fabsf(xv[2]), fabsf(xv[3])));
+    sm = (xv[0] + xv[1]) + (xv[2] + xv[3]);
+#pragma unroll
+    for (int o = 1; o < 8; o <<= 1) {  // the 8 lanes of the block (consecutive lanes)
+        mx = fmaxf(mx, __shfl_xor(mx, o));
+        sm += __shfl_xor(sm, o);
+    }
+    int e;
+    frexpf(mx, &e);  // 0 for mx = 0
+    const bool finite = mx <= 3.4028234663852886e38f;
+    // 2^(27-e) as two factors, each finite even for a block of subnormals (e down to -148)
+    const int sh = 27 - e, sh1 = sh < 100 ? sh : 100;
+    const float up1 = ldexpf(1.0f, sh1), up2 = ldexpf(1.0f, sh - sh1);
+    down = finite ? ldexpf(1.0f, e - 6) : __builtin_nanf("");
+    uint32_t y[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int X = finite ? static_cast<int>(rintf((xv[k] * up1) * up2)) : 0;
+        const uint32_t u = static_cast<uint32_t>(X);
+        // bytes d4, d3, d2, d1 (the 7-bit fields moved to byte boundaries, d1 with its sign bits)
+        y[k] = (u & 0x7Fu) | ((u << 1) & 0x7F00u) | ((u << 2) & 0x7F0000u) | ((u << 3) & 0xFF000000u);
+    }
+    // transpose: plane p (d1 .. d4) holds byte 3 - p of y[0..3]
+    const uint32_t lo01 = __builtin_amdgcn_perm(y[1], y[0], 0x05010400u);  // y0.b0 y1.b0 y0.b1 y1.b1
+    const uint32_t hi01 = __builtin_amdgcn_perm(y[1], y[0], 0x07030602u);  // y0.b2 y1.b2 y0.b3 y1.b3
+    const uint32_t lo23 = __builtin_amdgcn_perm(y[3], y[2], 0x05010400u);
+    const uint32_t hi23 = __builtin_amdgcn_perm(y[3], y[2], 0x07030602u);
+    pl[0] = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);  // d1: byte 3 of y0..y3
+    pl[1] = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u);  // d2: byte 2
+    pl[2] = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u);  // d3: byte 1
+    pl[3] = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u);  // d4: byte 0
+}
+
+// The wave's four x values of super-block sb (values sb * 256 + 4 lane ..)
+__device__ __forceinline__ void kq_load_x(const MatvecArgs& a, int sb, float (&xv)[4])
+{
+    const int v4 = sb * 64 + (threadIdx.x & 63);
+    if (a.xt == SLHIP_F32) {
+        const float4 t = reinterpret_cast<const float4*>(a.x)[v4];
+        xv[0] = t.x; xv[1] = t.y; xv[2] = t.z; xv[3] = t.w;
+    } else {
+        const uint2 t = reinterpret_cast<const uint2*>(a.x)[v4];
+        xv[0] = bf16_lo(t.x); xv[1] = bf16_hi(t.x); xv[2] = bf16_lo(t.y); xv[3] = bf16_hi(t.y);
+    }
+}
+
+// A tile of 16 weight rows streamed through LDS by a persistent block of 16 waves. An item is one matrix's
+// K segment of the tile (dual: the gate segment, then the up segment): wave w copies row w's segment -- one
+// contiguous run -- with direct global -> LDS loads (no registers held), two items in flight while a third is
+// computed (three LDS buffers). Long runs per wave read HBM at the rate of a linear stream; 16 rows read side
+// by side in short pieces measured ~30% slower. Once an item has landed, every wave computes its share for
+// all 16 rows on the matrix cores: Q4_K one super-block per wave (16 per segment), Q6_K one half super-block
+// (8 per segment). x is digitized once per block for the whole K. A block takes tiles b, b + grid, ...; a
+// tile's items in order, its sums kept in registers.
+constexpr int kKqTileWaves = 16;
+constexpr int kKqBufs = 3;  // item buffers in LDS (two landing while one is computed)
+
+template <int FMT> struct KqGeom;
+template <> struct KqGeom<SLHIP_FMT_Q4_K> {
+    static constexpr int BB = 144, SEG_SB = 16;
+    static constexpr int ROW = SEG_SB * BB + 16;  // LDS stride of a row's segment (padded: 580 words, banks 4n)
+};
+template <> struct KqGeom<SLHIP_FMT_Q6_K> {
+    static constexpr int BB = 210, SEG_SB = 8;
+    static constexpr int ROW = SEG_SB * BB;  // 420 words: rows start on banks 36n mod 64, distinct for n < 16
+};
+
+// LDS: x digit planes [4][K], 16 zero bytes, per 32-value block 2^(e-6) and sum, (Q6_K) per 16-value group
+// the four digit-plane sums [K/16][4], the waves' sums [2][waves][16], the item buffers.
+template <int FMT>
+static size_t kq_tile_lds(int64_t K)
+{
+    return static_cast<size_t>(K) * 4 + 16 + static_cast<size_t>(K / 32) * 8 +
+           (FMT == SLHIP_FMT_Q6_K ? static_cast<size_t>(K) : 0) + 2 * kKqTileWaves * 16 * 4 +
+           static_cast<size_t>(kKqBufs) * kKqTileWaves * KqGeom<FMT>::ROW;
+}
+
+// A direct global -> LDS load of 16 bytes per lane: lane i's bytes land at lds_base + 16 i (lds_base
+// wave-uniform, an LDS byte address). Written as inline assembly so that the compiler does not treat the
+// loads as pending LDS writes, which makes it wait for every outstanding load before any LDS read or barrier;
+// the kernel waits for them itself (wait_vmcnt), knowing which buffer each load fills.
+__device__ __forceinline__ void lds_dma16(const void* src, uint32_t lds_base)
+{
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_base) : "m0", "memory");
+}
+
+// s_waitcnt with only a vmcnt limit (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt and lgkmcnt at max)
+template <int V>
+__device__ __forceinline__ void wait_vmcnt()
+{
+    __builtin_amdgcn_s_waitcnt((V & 0xF) | ((V >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// 16 bytes at LDS byte address p, which is 2-byte aligned and misaligned by mis = p % 16 (wave-uniform):
+// two aligned 16-byte reads and a funnel shift.
+__device__ __forceinline__ uint4 lds_read16_mis(const char* p, int mis)
+{
+    const uint4* b = reinterpret_cast<const uint4*>(p - mis);
+    const uint4 lo = b[0], hi = b[1];
+    uint32_t w[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+    if (mis & 8) {  // wave-uniform selects
+#pragma unroll
+        for (int i = 0; i < 6; i++) w[i] = w[i + 2];
+    }
+    if (mis & 4) {
+#pragma unroll
+        for (int i = 0; i < 5; i++) w[i] = w[i + 1];
+    }
+    const uint32_t sh = 8u * static_cast<uint32_t>(mis & 3);
+    return make_uint4(__builtin_amdgcn_alignbyte(w[1], w[0], sh >> 3), __builtin_amdgcn_alignbyte(w[2], w[1], sh >> 3),
+                      __builtin_amdgcn_alignbyte(w[3], w[2], sh >> 3), __builtin_amdgcn_alignbyte(w[4], w[3], sh >> 3));
+}
+
+template <int FMT, bool DUAL>
+__global__ __launch_bounds__(64 * kKqTileWaves) void matvec_kq_tile(MatvecArgs a, int nseg)
+{
+    using G = KqGeom<FMT>;
+    constexpr bool Q6 = FMT == SLHIP_FMT_Q6_K;
+    constexpr int SEG = G::SEG_SB * G::BB;         // bytes of a row's segment
+    constexpr int UNITS = SEG / 16;                // 16-byte units of it
+    constexpr int LOADS = (UNITS + 63) / 64;       // load instructions per item and wave
+    extern __shared__ uint32_t smem[];
+    const int K = static_cast<int>(a.K);
+    char* lds = reinterpret_cast<char*>(smem);
+    const uint32_t zero_off = 4u * static_cast<uint32_t>(K);                 // 16 zero bytes after the planes
+    float* xscale = reinterpret_cast<float*>(lds + zero_off + 16);            // [K / 32] 2^(e-6)
+    float* xsum = xscale + K / 32;                                             // [K / 32]
+    int* dsum = reinterpret_cast<int*>(xsum + K / 32);                         // Q6_K: [K / 16][4]
+    float* red = reinterpret_cast<float*>(dsum + (Q6 ? K / 4 : 0));           // [2][waves][16]
+    char* wbuf = reinterpret_cast<char*>(red + 2 * kKqTileWaves * 16);        // [bufs][waves][G::ROW]
+    const int lane = threadIdx.x & 63, wave = wave_id();
+    const int n = lane & 15, q = lane >> 4;
+    const int64_t tiles = (a.N + 15) / 16;
+
+    // item (tile t, segment s) -> LDS buffer: wave w's row segment, 16-byte units on consecutive lanes
+    auto issue = [&](int64_t t, int s, int buf) {
+        const int64_t row0 = t * 16 + wave;
+        const int64_t row = row0 < a.N ? row0 : a.N - 1;
+        const bool up = DUAL && (s & 1);
+        const int64_t off = row * a.wrow + static_cast<int64_t>(DUAL ? s >> 1 : s) * SEG;
+        char* dst = wbuf + (buf * kKqTileWaves + wave) * G::ROW;
+#pragma unroll
+        for (int i = 0; i < LOADS; i++) {
+            const int u = lane + 64 * i;
+            if (64 * i + 64 > UNITS && u >= UNITS) continue;  // the last instruction's spare lanes
+            lds_dma16((up ? a.wu : a.wg) + off + 16 * u,
+                      __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(dst + 1024 * i))));
+        }
+    };
+    auto next_item = [&](int64_t& t, int& s) {
+        if (++s == nseg) {
+            s = 0;
+            t += gridDim.x;
+        }
+    };
+
+    int64_t lt = blockIdx.x;  // the item whose loads go out next
+    int ls = 0;
+    for (int b = 0; b < kKqBufs - 1; b++) {  // prologue: the first two items (past the end: the last tile again)
+        issue(lt < tiles ? lt : tiles - 1, lt < tiles ? ls : 0, b);
+        next_item(lt, ls);
+    }
+    // x digitized once: per 32-value block its exponent, sum and digit planes [4][K]; Q6_K also the digit
+    // sums of every 16-value group (its codes are stored + 32: sum (q - 32) d = sum q d - 32 sum d, exact)
+    for (int v4 = threadIdx.x; v4 < K / 4; v4 += 64 * kKqTileWaves) {  // whole waves (K % 256 == 0)
+        float xv[4];
+        kq_load_x(a, v4 / 64, xv);  // the lane's four values (v4 == 64 sb + lane)
+        uint32_t pl[4];
+        float down, sm;
+        kq_digits(xv, pl, down, sm);
+#pragma unroll
+        for (int p = 0; p < 4; p++) reinterpret_cast<uint32_t*>(lds + p * K)[v4] = pl[p];
+        if ((lane & 7) == 0) {
+            xscale[v4 / 8] = down;
+            xsum[v4 / 8] = sm;
+        }
+        if (Q6) {
+            int ds[4];
+#pragma unroll
+            for (int p = 0; p < 4; p++) {
+                const uint32_t w = pl[p];
+                // bytes as signed (d1) or unsigned (d2..d4) digits
+                int t = p == 0 ? (static_cast<int>(w << 24) >> 24) + (static_cast<int>(w << 16) >> 24) +
+                                     (static_cast<int>(w << 8) >> 24) + (static_cast<int>(w) >> 24)
+                               : static_cast<int>((w & 0xFFu) + ((w >> 8) & 0xFFu) + ((w >> 16) & 0xFFu) + (w >> 24));
+                t += __shfl_xor(t, 1);
+                t += __shfl_xor(t, 2);
+                ds[p] = t;
+            }
+            if ((lane & 3) == 0) *reinterpret_cast<int4*>(dsum + 4 * (v4 / 4)) = make_int4(ds[0], ds[1], ds[2], ds[3]);
+        }
+    }
+    if (threadIdx.x < 4) smem[zero_off / 4 + threadIdx.x] = 0u;
+
+    const int plane = n - 4 * q;  // this lane's slot n is digit plane `plane` of K-group q, or a zero slot
+    const bool has_plane = plane >= 0 && plane < 4;
+    const uint32_t a_base = has_plane ? static_cast<uint32_t>(plane * K) : zero_off;
+    const uint32_t a_step = has_plane ? 1u : 0u;
+    auto a_op = [&](int v) {  // A operand: 16 digits of plane `plane` from value v (or zeros)
+        return as_i32x4(*reinterpret_cast<const uint4*>(lds + a_base + static_cast<uint32_t>(v) * a_step));
+    };
+    float accg = 0.0f, accu = 0.0f;
+
+    // Q4_K: super-block `wave` of the segment. Lane group q holds code group q (sub-blocks 2q, 2q + 1: low and
+    // high nibbles) of row n; two MFMAs per sub-block.
+    auto compute_q4k = [&](const char* bufp, int seg, float& acc) {
+        const int sb = seg * G::SEG_SB + wave;
+        const char* row = bufp + n * G::ROW + wave * G::BB;
+        const uint4 h = *reinterpret_cast<const uint4*>(row);
+        const uint4 c0 = *reinterpret_cast<const uint4*>(row + 16 + 32 * q);
+        const uint4 c1 = *reinterpret_cast<const uint4*>(row + 32 + 32 * q);
+#pragma unroll
+        for (int hi = 0; hi < 2; hi++) {
+            i32x4_t c = {0, 0, 0, 0};
+#pragma unroll
+            for (int i = 0; i < 2; i++) {  // the sub-block's values 0-15, 16-31
+                const uint4& w = i ? c1 : c0;
+                const uint32_t S = hi ? 4 : 0;
+                const uint4 b = make_uint4((w.x >> S) & 0x0F0F0F0Fu, (w.y >> S) & 0x0F0F0F0Fu,
+                                           (w.z >> S) & 0x0F0F0F0Fu, (w.w >> S) & 0x0F0F0F0Fu);
+                c = __builtin_amdgcn_mfma_i32_16x16x64_i8(a_op(sb * 256 + 64 * q + 32 * hi + 16 * i), as_i32x4(b), c,
+                                                          0, 0, 0);
+            }
+            const int j = 2 * q + hi;
+            float d0, m;
+            q4k_scales(h, j, d0, m);
+            acc = fmaf(d0, digits_dot(c, xscale[sb * 8 + j]), acc);
+            acc = fmaf(-m, xsum[sb * 8 + j], acc);
+        }
+    };
+    // Q6_K: half `hf` of super-block `wave / 2` (values 128 hf .. +127). In MFMA m lane group q takes the 16
+    // values 128 hf + 32 k + 16 lh + 0..15, k = 2m + (q >> 1), lh = q & 1: low (k < 2) or high nibbles of
+    // ql[64 hf + 32 (k & 1) + 16 lh ..] with bits 2k of qh[128 + 32 hf + 16 lh ..]; scale sc[8 hf + 2k + lh].
+    auto compute_q6k = [&](const char* bufp, int seg, float& acc) {
+        const int sbl = wave >> 1, hf = wave & 1, lh = q & 1;
+        const int sb = seg * G::SEG_SB + sbl;
+        const char* row = bufp + n * G::ROW + sbl * G::BB;
+        const int mis = (sbl * G::BB) & 15;  // the super-block's offset from 16-byte alignment (rows are aligned)
+        const uint4 ql = lds_read16_mis(row + 64 * hf + 32 * (q >> 1) + 16 * lh, mis);
+        const uint4 qh = lds_read16_mis(row + 128 + 32 * hf + 16 * lh, mis);
+        const float d = static_cast<float>(*reinterpret_cast<const _Float16*>(row + 208));
+#pragma unroll
+        for (int m = 0; m < 2; m++) {
+            const int k = 2 * m + (q >> 1);
+            const uint32_t hs = 2u * static_cast<uint32_t>(k);
+            auto code = [&](uint32_t l, uint32_t h) {
+                return ((m ? l >> 4 : l) & 0x0F0F0F0Fu) | (((h >> hs) & 0x03030303u) << 4);
+            };
+            const uint4 b = make_uint4(code(ql.x, qh.x), code(ql.y, qh.y), code(ql.z, qh.z), code(ql.w, qh.w));
+            const int v = sb * 256 + 128 * hf + 32 * k + 16 * lh;
+            i32x4_t c = {0, 0, 0, 0};
+            c = __builtin_amdgcn_mfma_i32_16x16x64_i8(a_op(v), as_i32x4(b), c, 0, 0, 0);
+            const int4 ds = *reinterpret_cast<const int4*>(dsum + 4 * (v / 16));
+            c[0] -= 32 * ds.x;
+            c[1] -= 32 * ds.y;
+            c[2] -= 32 * ds.z;
+            c[3] -= 32 * ds.w;
+            const float sc = static_cast<float>(*reinterpret_cast<const int8_t*>(row + 192 + 8 * hf + 2 * k + lh));
+            acc = fmaf(__fmul_rn(d, sc), digits_dot(c, xscale[v / 32]), acc);
+        }
+    };
+
+    int64_t t = blockIdx.x;
+    int s = 0, buf = 0;
+    while (t < tiles) {  // block-uniform
+        // this item's loads went out two items ago; the next item's may stay out
+        wait_vmcnt<LOADS>();
+        __syncthreads();  // the item is in LDS (every wave's row), and every wave is done with the buffer of
+                          // the previous item, which now takes the item two ahead
+        {
+            const int pb = buf == 0 ? kKqBufs - 1 : buf - 1;
+            issue(lt < tiles ? lt : tiles - 1, lt < tiles ? ls : 0, pb);
+            next_item(lt, ls);
+        }
+        const char* bufp = wbuf + buf * kKqTileWaves * G::ROW;
+        const int seg = DUAL ? s >> 1 : s;
+        float& acc = DUAL && (s & 1) ? accu : accg;
+        if (Q6)
+            compute_q6k(bufp, seg, acc);
+        else
+            compute_q4k(bufp, seg, acc);
+        if (s + 1 == nseg) {  // the tile is complete: the four lane groups of a row, then the waves
+            float g = accg, u = accu;
+            g += __shfl_xor(g, 16);
+            g += __shfl_xor(g, 32);
+            u += __shfl_xor(u, 16);
+            u += __shfl_xor(u, 32);
+            if (q == 0) {
+                red[wave * 16 + n] = g;
+                red[(kKqTileWaves + wave) * 16 + n] = u;
+            }
+            __syncthreads();
+            const int64_t n0 = t * 16;
+            if (wave == 0 && lane < 16 && n0 + n < a.N) {
+                float ag[1] = {0.0f}, au[1] = {0.0f};
+                for (int w = 0; w < kKqTileWaves; w++) {
+                    ag[0] += red[w * 16 + n];
+                    au[0] += red[(kKqTileWaves + w) * 16 + n];
+                }
+                store_row<1, DUAL>(a, n0 + n, ag, au);
+            }
+            accg = accu = 0.0f;
+        }
+        next_item(t, s);
+        buf = buf + 1 == kKqBufs ? 0 : buf + 1;
+    }
+    wait_vmcnt<0>();  // no load may still be landing in LDS when the block ends
+}
+
 // ---- host dispatch --------------------------------------------------------------------------------
 
 static int env_int(const char* name, int dflt)
@@ -1082,9 +1442,29 @@ static int quant_tt(const MatvecArgs& a, int tt, int ch, hipStream_t st)
     }
 }
 
+template <int FMT, bool DUAL>
+static int launch_kq_tile(const MatvecArgs& a, hipStream_t st)
+{
+    const size_t lds = kq_tile_lds<FMT>(a.K);
+    auto kernel = matvec_kq_tile<FMT, DUAL>;
+    const int r = allow_lds(kernel, lds);
+    if (r != SLHIP_OK) return r;
+    const int nseg = static_cast<int>(a.K / 256) / KqGeom<FMT>::SEG_SB * (DUAL ? 2 : 1);
+    const int64_t tiles = (a.N + 15) / 16;
+    const int64_t grid = tiles < device_cus() ? tiles : device_cus();
+    kernel<<<dim3(static_cast<unsigned>(grid)), 64 * kKqTileWaves, lds, st>>>(a, nseg);
+    return check_launch("matvec_kq_tile");
+}
+
 template <int FMT>
 static int run_quant(MatvecArgs a, bool dual, hipStream_t st)
 {
+    if constexpr (FMT == SLHIP_FMT_Q4_K || FMT == SLHIP_FMT_Q6_K) {
+        // one token: the matrix-core kernel, when K splits into whole segments and its LDS fits
+        if (a.T == 1 && a.K % (256 * KqGeom<FMT>::SEG_SB) == 0 && kq_tile_lds<FMT>(a.K) <= kMaxLds &&
+            env_int("SLHIP_KQ_MFMA", 1))
+            return dual ? launch_kq_tile<FMT, true>(a, st) : launch_kq_tile<FMT, false>(a, st);
+    }
     int tt = Fmt<FMT>::K && dual ? 4 : 8;  // the K-quant sub-block decode at 8 tokens of a pair spills
     while (tt > 1 && (tt / 2 >= a.T || quant_lds(tt, a.K, a.wrow, dual) > kMaxLds)) tt /= 2;
     if (quant_lds(tt, a.K, a.wrow, dual) > kMaxLds)

@@ -127,6 +127,11 @@ SINGLE_CASES = [  # (fmt, x dtype, y dtype, T, K, N)
     ("q6_k", "f32", "bf16", 9, 4096, 40),
     ("q4_k", "f32", "f32", 2, 14336, 20),
     ("q6_k", "f32", "f32", 1, 14336, 24),
+    ("q4_k", "bf16", "f32", 1, 256, 33),    # one token on the matrix cores: one super-block, a partial tile
+    ("q4_k", "f32", "bf16", 1, 2048, 17),
+    ("q4_k", "bf16", "bf16", 1, 14336, 40),
+    ("q6_k", "bf16", "f32", 1, 2048, 33),    # one token on the matrix cores: one segment, a partial tile
+    ("q6_k", "f32", "bf16", 1, 4096, 17),
 ]
 
 
@@ -276,13 +281,58 @@ def test_bf16_paths_agree_with_oracle(device, monkeypatch, min_t, dual, dx, T, K
     assert not bad.any(), f"dual min_t={min_t}: {bad.sum()} beyond the bound; first at {np.argwhere(bad)[0]}"
 
 
+def test_q6k_one_token_rows_of_code_32_give_exactly_zero(device):
+    """At one token (the integer matrix-core kernel) a Q6_K row whose codes are all 32 -- zero weights, as in
+    padded or pruned rows -- gives exactly 0: its sum is formed as sum q d - 32 sum d in integers. Other rows
+    of the same tile stay within the f32 bound."""
+    N, K = 40, 4096
+    raw, _ = _weights("q6_k", N, K, 23, 1)
+    b = raw.reshape(N, K // 256, 210)
+    b[0:5, :, 0:128] = 0x00          # low nibbles 0
+    b[0:5, :, 128:192] = 0xAA        # high 2-bit fields 2: every code 32
+    W = oracle.dequant("q6_k", raw.reshape(-1), N * K).reshape(N, K)
+    assert not np.any(W[0:5])
+    x = synth.normal(3, 9, (1, K)) * 5 + 2
+    y = _run("q6_k", "f32", "f32", x, [raw], N, K)
+    assert np.all(y[0, 0:5] == 0.0), y[0, 0:5]
+    S = np.abs(x).astype(np.float64) @ _abs_terms("q6_k", raw, W).T
+    _check_single(y, "f32", oracle.matvec("q6_k", raw, N, K, x), S, "q6_k one token")
+
+
+def test_q4k_one_token_wide_range_and_zero_rows(device):
+    """The one-token Q4_K kernel (integer matrix cores, x as four 7-bit digits per value against its 32-value
+    block's exponent): x spanning 2^-20 .. 2^12 inside each block, exact zeros and a huge outlier stay within
+    the f32 bound; rows whose codes and minima are all zero give exactly 0, and so do rows whose codes are
+    zero with a minimum, exactly -m * sum(x) per sub-block (checked against the oracle's value)."""
+    N, K = 48, 2048
+    raw, W = _weights("q4_k", N, K, 17, 1)
+    blocks = raw.reshape(N, K // 256, 144)
+    blocks[0:8, :, 16:] = 0          # codes 0
+    blocks[0:4, :, 2:4] = 0          # and dmin 0: the row's weights are exactly 0
+    W = oracle.dequant("q4_k", raw.reshape(-1), N * K).reshape(N, K)
+    r = synth.rng(5, 5)
+    x = (r.standard_normal((1, K)) * 2.0 ** r.integers(-20, 13, (1, K))).astype(np.float32)
+    x[0, ::37] = 0.0
+    x[0, 100] = 3.0e4
+    for dual in (False, True):
+        y = _run("q4_k", "f32", "f32", x, [raw, raw] if dual else [raw], N, K, act="silu" if dual else None)
+        g = oracle.matvec("q4_k", raw, N, K, x)
+        if dual:
+            assert np.all(y[0, 0:4] == 0.0)  # silu(0) * 0
+            continue
+        assert np.all(y[0, 0:4] == 0.0), y[0, 0:4]
+        S = np.abs(x).astype(np.float64) @ _abs_terms("q4_k", raw, W).T
+        _check_single(y, "f32", g, S, "q4_k one token, wide x")
+
+
+@pytest.mark.parametrize("T", [1, 3])
 @pytest.mark.parametrize("dual", [False, True])
-def test_q6k_codes_near_32_with_offset_x(device, dual):
+def test_q6k_codes_near_32_with_offset_x(device, dual, T):
     """Q6_K's -32 is applied to the sums of x over each 16-value half (sum x q - 32 sum x, the decomposition of
     the reference's integer dot, IntDot.Decode.cs:216-221): codes 32..34 and x of mean 4 make sum x q about 33
     times the result. Checked against the strict bound 2^-16 * sum |x| |w| (|w| itself, not the code and
     offset terms): an f32 emulation of the kernel's order stays below 2^-21 of it."""
-    N, K, T = 48, 4096, 3
+    N, K = 48, 4096
     rng = np.random.default_rng(17)
     raws = []
     for tid in (1, 2):
