@@ -251,15 +251,16 @@ SLHIP_API int slhip_rownorm_copies(int kind, int dtype_in, int dtype_out, const 
  *   x: [T, K] f32 or bf16 (dtype_x), 16-byte aligned, row stride x_stride elements (a multiple of 8);
  *   W, Wg, Wu: N rows of K weights in `fmt`, 16-byte aligned: dense F32/F16/BF16 (K a multiple of 8,
  *   K <= 16384), or the GGUF block formats Q8_0/Q4_0/Q4_1/Q5_0/Q5_1 and Q4_K/Q5_K/Q6_K (K a multiple of
- *   256, rows a multiple of 16 bytes -- Q6_K: K a multiple of 2048 -- and the rows' block images fitting in
- *   LDS); y: [T, N] f32 or bf16 (dtype_y), row stride y_stride.
+ *   256 and the rows' block images fitting in LDS); y: [T, N] f32 or bf16 (dtype_y), row stride y_stride.
  *   act: SLHIP_ACT_SILU / GELU_TANH / GELU_ERF, the same forms as slhip_gated_act.
  * Products and sums in f32 (in another order than the CPU provider's, so equal to it within the rounding of
  * a K-term f32 dot product); block formats sum d * sum(x q) + a * sum(x) per block, as the reference's
  * fused Q4_0 dot does (the K-quants per 32-value sub-block: d0 * sum(x q) - m * sum(x); Q6_K
  * s * sum(x (q - 32)) per 16 values). BF16 weights with T >= SLHIP_MATVEC_MFMA_MIN_T (environment, default 3; 0 keeps the
  * VALU kernel) and K a multiple of 64 go to the matrix cores with f32 x split exactly into three bf16 parts:
- * the same products, summed in another order, under the same bound.
+ * the same products, summed in another order, under the same bound. Q4_K and Q6_K at T = 1 (K a multiple of
+ * 4096 for Q4_K, 2048 for Q6_K) go to the integer matrix cores: x represented to 2^(e-28) of its 32-value
+ * block's largest power of two, the code sums exact, under the same bound.
  * Replaces: MatMulOp's float-row path (src/Sharplight.Cpu/MatMulOp.cs:376-465; fused Q8_0/Q4_0 dots, Quant.cs:738-803)
  * followed by the activation and
  * Mul, i.e. the reference's dual matvec unit (FoldDualMatMuls, src/Sharplight.Shaders/Lowering/

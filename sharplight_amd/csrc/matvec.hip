@@ -341,14 +341,45 @@ __device__ __forceinline__ float q6_terms(const KSub& k, float sq0, float sq1, c
 constexpr int kMqThreads = 256;
 constexpr bool PAIR = true;  // both rows of a dual pair per x read (every block format but Q8_0)
 
-template <int FMT, int TT, int CH, bool DUAL>
+// U: the width of the staging loads, 16 bytes unless the rows are not 16-byte multiples (Q6_K rows of K not
+// a multiple of 2048: 210 (K / 256) bytes, aligned to the largest power of two dividing them); a row's
+// 16-byte chunk is then read as 16 / U loads, the pieces past the row's end repeating its last unit (their
+// bytes land in the row image's padding).
+template <int U>
+__device__ __forceinline__ uint4 load16_as(const char* row, int64_t off, int64_t wrow)
+{
+    if constexpr (U == 16) {
+        return load_nt(row + off);
+    } else {
+        uint32_t w[4];
+#pragma unroll
+        for (int k = 0; k < 16 / U; k++) {
+            int64_t o = off + k * U;
+            o = o < wrow ? o : wrow - U;
+            if constexpr (U == 8) {
+                const uint2 t = *reinterpret_cast<const uint2*>(row + o);
+                w[2 * k] = t.x;
+                w[2 * k + 1] = t.y;
+            } else if constexpr (U == 4) {
+                w[k] = *reinterpret_cast<const uint32_t*>(row + o);
+            } else {
+                const uint32_t h = *reinterpret_cast<const uint16_t*>(row + o);
+                if (k & 1) w[k / 2] |= h << 16;
+                else w[k / 2] = h;
+            }
+        }
+        return make_uint4(w[0], w[1], w[2], w[3]);
+    }
+}
+
+template <int FMT, int TT, int CH, bool DUAL, int U = 16>
 __global__ __launch_bounds__(kMqThreads) void matvec_quant(MatvecArgs a)
 {
     extern __shared__ uint32_t smem[];
     constexpr int R = DUAL ? 2 : 1;
     const int lane = threadIdx.x & 63;
     const int wave = wave_id();
-    const int nch = static_cast<int>(a.wrow / 16);  // 16-byte chunks per row
+    const int nch = static_cast<int>((a.wrow + 15) / 16);  // 16-byte chunks per row (the last may be partial)
     const int rbw = nch * 4;                         // words per row
     uint32_t* rows = smem + wave * R * rbw;
     float* xsh = reinterpret_cast<float*>(smem + (kMqThreads / 64) * R * rbw);
@@ -363,8 +394,7 @@ __global__ __launch_bounds__(kMqThreads) void matvec_quant(MatvecArgs a)
             int idx = base + c * 64 + lane;
             idx = idx < tot ? idx : tot - 1;
             const int r = idx >= nch ? 1 : 0;
-            const char* src = (r ? a.wu : a.wg) + n * a.wrow + static_cast<int64_t>(idx - r * nch) * 16;
-            v[c] = load_nt(src);
+            v[c] = load16_as<U>((r ? a.wu : a.wg) + n * a.wrow, static_cast<int64_t>(idx - r * nch) * 16, a.wrow);
         }
     };
     auto store_batch = [&](int base, const uint4* v) {
@@ -1390,7 +1420,8 @@ static int device_cus()
 
 static size_t quant_lds(int tt, int64_t K, int64_t wrow, bool dual)
 {
-    return static_cast<size_t>(kMqThreads / 64) * (dual ? 2 : 1) * wrow + static_cast<size_t>(tt) * (K / 32) * 36 * 4 +
+    const int64_t rowb = (wrow + 15) / 16 * 16;  // a row image, padded to whole 16-byte chunks
+    return static_cast<size_t>(kMqThreads / 64) * (dual ? 2 : 1) * rowb + static_cast<size_t>(tt) * (K / 32) * 36 * 4 +
            static_cast<size_t>(tt) * (K / 32) * 4;
 }
 
@@ -1403,11 +1434,11 @@ static int allow_lds(Kern kernel, size_t lds)
     return e == hipSuccess ? SLHIP_OK : fail(SLHIP_ERR_HIP, "matvec: %zu bytes of LDS refused: %s", lds, hipGetErrorString(e));
 }
 
-template <int FMT, int TT, int CH, bool DUAL>
+template <int FMT, int TT, int CH, bool DUAL, int U = 16>
 static int launch_quant(const MatvecArgs& a, hipStream_t st)
 {
     const size_t lds = quant_lds(TT, a.K, a.wrow, DUAL);
-    auto kernel = matvec_quant<FMT, TT, CH, DUAL>;
+    auto kernel = matvec_quant<FMT, TT, CH, DUAL, U>;
     const int r = allow_lds(kernel, lds);
     if (r != SLHIP_OK) return r;
     int per_cu = 0;
@@ -1423,6 +1454,13 @@ static int launch_quant(const MatvecArgs& a, hipStream_t st)
 template <int FMT, int TT, bool DUAL>
 static int quant_ch(const MatvecArgs& a, int ch, hipStream_t st)
 {
+    if constexpr (FMT == SLHIP_FMT_Q6_K) {  // rows not 16-byte multiples: narrower staging loads
+        if (a.wrow % 16 != 0) {
+            return a.wrow % 8 == 0   ? launch_quant<FMT, TT, 8, DUAL, 8>(a, st)
+                   : a.wrow % 4 == 0 ? launch_quant<FMT, TT, 8, DUAL, 4>(a, st)
+                                     : launch_quant<FMT, TT, 8, DUAL, 2>(a, st);
+        }
+    }
     switch (ch) {
     case 4: return launch_quant<FMT, TT, 4, DUAL>(a, st);
     case 8: return launch_quant<FMT, TT, 8, DUAL>(a, st);
@@ -1517,7 +1555,7 @@ static int matvec_common(int fmt, int dtype_x, int dtype_y, const void* x, int64
                     static_cast<long long>(K));
     if (N > 0x7FFFFFFF || T > 0x7FFFFFFF) return fail(SLHIP_ERR_UNSUPPORTED, "%s: shape too large", name);
     const int64_t wrow = dense ? K * (fmt == SLHIP_FMT_F32 ? 4 : 2) : K / qg.bs * qg.bb;
-    if (wrow % 16 != 0)  // the block kernel stages rows with 16-byte loads (Q6_K: K a multiple of 2048)
+    if (wrow % 16 != 0 && fmt != SLHIP_FMT_Q6_K)  // (only Q6_K rows can be: 210 bytes per 256 values)
         return fail(SLHIP_ERR_UNSUPPORTED, "%s: rows of %lld bytes are not a multiple of 16 for this weight format",
                     name, static_cast<long long>(wrow));
     MatvecArgs a{x, x_stride, static_cast<const char*>(wg), static_cast<const char*>(wu), wrow, y, y_stride,

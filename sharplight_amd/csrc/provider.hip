@@ -525,7 +525,6 @@ Support supports(const Graph& g, const Node& n)
         const int64_t K = x.last();
         if (dense && (K % 8 != 0 || K > 16384)) return no("MatMul: K must be a multiple of 8 and at most 16384");
         if (blocks && (K % 256 != 0 || K > 16384)) return no("MatMul: block-format K must be a multiple of 256, at most 16384");
-        if (w.type == DType::Q6_K && K % 2048 != 0) return no("MatMul: Q6_K rows need K a multiple of 2048 (16-byte rows)");
         if (!matvec_fits(format_code(w.type), K, false)) return no("MatMul: the weight rows do not fit the matvec's LDS staging");
         return {true, ""};
     }

@@ -132,6 +132,10 @@ SINGLE_CASES = [  # (fmt, x dtype, y dtype, T, K, N)
     ("q4_k", "bf16", "bf16", 1, 14336, 40),
     ("q6_k", "bf16", "f32", 1, 2048, 33),    # one token on the matrix cores: one segment, a partial tile
     ("q6_k", "f32", "bf16", 1, 4096, 17),
+    ("q6_k", "f32", "f32", 1, 3072, 40),     # rows of 2520 bytes: 8-byte staging loads
+    ("q6_k", "f32", "f32", 2, 2560, 33),     # 2100 bytes: 4-byte loads
+    ("q6_k", "bf16", "f32", 1, 768, 24),     # 630 bytes: 2-byte loads
+    ("q6_k", "f32", "bf16", 5, 5120, 19),    # 4200 bytes
 ]
 
 
@@ -187,6 +191,8 @@ DUAL_CASES = [  # (act, fmt, x dtype, y dtype, T, K, N): FusionTests.SwiGluDualM
     ("silu", "q5_1", "f32", "bf16", 1, 4096, 40),
     ("silu", "q5_k", "f32", "f32", 1, 2048, 33),
     ("gelu_tanh", "q4_k", "bf16", "bf16", 1, 14336, 24),
+    ("silu", "q6_k", "f32", "f32", 1, 3072, 40),          # Q6_K rows not 16-byte multiples
+    ("gelu_erf", "q6_k", "bf16", "f32", 3, 768, 33),
 ]
 
 

@@ -277,11 +277,11 @@ def test_matmul_support_answers():
     g.matmul(x256, g.weight("q4_0", 16, 256))     # 4: yes
     g.matmul(x256, g.weight("i32", 16, 256))      # 5: integer weights -> no
     g.matmul(x256, g.weight("q4_k", 16, 256))     # 6: yes
-    g.matmul(x256, g.weight("q6_k", 16, 256))     # 7: Q6_K rows of 210 bytes -> no (K % 2048)
+    g.matmul(x256, g.weight("q6_k", 16, 256))     # 7: Q6_K rows of 210 bytes -> yes (2-byte staging loads)
     x2048 = g.input("f32", "T", 2048)
     g.matmul(x2048, g.weight("q6_k", 16, 2048))   # 8: yes
     g.matmul(x2048, g.weight("iq4_xs", 16, 2048))  # 9: no matvec for this format
-    expect = [False, True, False, False, True, False, True, False, True, False]
+    expect = [False, True, False, False, True, False, True, True, True, False]
     for k, e in enumerate(expect):
         ok, why = _supports(g, k)
         assert ok == e, (k, why)
