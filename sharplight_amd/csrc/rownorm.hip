@@ -17,8 +17,9 @@
 // 16 waves). The GEMM activation copies of the normalized row (f16 values; E4M3 codes with one f32
 // scale per 128 values) are written from the same f32 values as y: a 128-value group of the E4M3 rows is
 // the 16 (bf16 input) or 32 (f32 input) consecutive lanes holding it, so its amax is a butterfly max over
-// those lanes. Rows that do not fit the vector path (D not a multiple of the vector width, unaligned
-// pointers or strides, or D beyond 8*64*16 vectors) take a scalar block-per-row kernel.
+// those lanes. 2-byte rows whose length is a multiple of 4 but not of 8 use the same kernel with 8-byte
+// vectors. Rows that fit neither (odd lengths, unaligned pointers or strides, or D beyond 8*64*16
+// vectors) take a scalar block-per-row kernel.
 #include "common.hpp"
 
 #include <stdlib.h>
@@ -56,11 +57,50 @@ __device__ __forceinline__ float group_reduce(float v, int wpr, int group, int w
     return s;
 }
 
-template <int DTI, int DTO, int NV, bool RES, bool Q>
+// The raw input vector of a lane: 16 bytes, or 8 bytes (four 2-byte values) for rows whose length is a
+// multiple of 4 but not of 8.
+template <int VB> struct RawVec;
+template <> struct RawVec<16> {
+    using T = uint4;
+    __device__ static __forceinline__ T load(const void* p) { return load_nt(p); }
+    __device__ static __forceinline__ void launder(T& r)
+    {
+        asm volatile("" : "+v"(r.x), "+v"(r.y), "+v"(r.z), "+v"(r.w));
+    }
+    template <int DT> __device__ static __forceinline__ void unpack(const T& r, float* f) { Vec<DT>::unpack(r, f); }
+    template <int DT> __device__ static __forceinline__ T pack(const float* f) { return Vec<DT>::pack(f); }
+};
+template <> struct RawVec<8> {
+    using T = uint2;
+    __device__ static __forceinline__ T load(const void* p)
+    {
+        const u32x2 v = __builtin_nontemporal_load(static_cast<const u32x2*>(p));
+        return make_uint2(v.x, v.y);
+    }
+    __device__ static __forceinline__ void launder(T& r) { asm volatile("" : "+v"(r.x), "+v"(r.y)); }
+    template <int DT> __device__ static __forceinline__ void unpack(const T& r, float* f)
+    {
+        static_assert(Vec<DT>::BYTES == 2, "8-byte vectors hold 2-byte values");
+        float t[8];
+        Vec<DT>::unpack(make_uint4(r.x, r.y, 0u, 0u), t);
+#pragma unroll
+        for (int e = 0; e < 4; e++) f[e] = t[e];
+    }
+    template <int DT> __device__ static __forceinline__ T pack(const float* f)
+    {
+        const float t[8] = {f[0], f[1], f[2], f[3], 0.f, 0.f, 0.f, 0.f};
+        const uint4 v = Vec<DT>::pack(t);
+        return make_uint2(v.x, v.y);
+    }
+};
+
+template <int DTI, int DTO, int NV, bool RES, bool Q, int VB>
 __global__ __launch_bounds__(1024) void rownorm_vec(RowNormArgs a, int wpr)
 {
     using VI = Vec<DTI>;
-    constexpr int E = VI::N;  // elements per 16-byte input vector
+    using RV = RawVec<VB>;
+    static_assert(VB == 16 || (VB == 8 && VI::BYTES == 2 && !Q), "8-byte vectors: 2-byte rows, no E4M3 copy");
+    constexpr int E = VB / VI::BYTES;  // elements per input vector
     constexpr int G = 128 / E;  // lanes per 128-value E4M3 group
     __shared__ float red[4 * 16];
 
@@ -90,13 +130,13 @@ __global__ __launch_bounds__(1024) void rownorm_vec(RowNormArgs a, int wpr)
         jv[k] = own[k] ? j : Q ? nvec - G + (j & (G - 1)) : nvec - 1;
     }
     const char* xr = static_cast<const char*>(a.x) + row * a.xs * VI::BYTES;
-    uint4 raw[NV], rraw[NV];
+    typename RV::T raw[NV], rraw[NV];
 #pragma unroll
-    for (int k = 0; k < NV; k++) raw[k] = load_nt(xr + static_cast<int64_t>(jv[k]) * 16);
+    for (int k = 0; k < NV; k++) raw[k] = RV::load(xr + static_cast<int64_t>(jv[k]) * VB);
     if (RES) {
         const char* rr = static_cast<const char*>(a.res) + row * a.rs * VI::BYTES;
 #pragma unroll
-        for (int k = 0; k < NV; k++) rraw[k] = load_nt(rr + static_cast<int64_t>(jv[k]) * 16);
+        for (int k = 0; k < NV; k++) rraw[k] = RV::load(rr + static_cast<int64_t>(jv[k]) * VB);
     }
     // The norm weight is read with the row data, ahead of the reduction, rather than after it.
     float wv[NV][E];
@@ -125,17 +165,16 @@ __global__ __launch_bounds__(1024) void rownorm_vec(RowNormArgs a, int wpr)
     auto launder = [&]() {
         if constexpr (PACKED) {
 #pragma unroll
-            for (int k = 0; k < NV; k++)
-                asm volatile("" : "+v"(raw[k].x), "+v"(raw[k].y), "+v"(raw[k].z), "+v"(raw[k].w));
+            for (int k = 0; k < NV; k++) RV::launder(raw[k]);
         }
     };
     float v[NV][E];
 #pragma unroll
     for (int k = 0; k < NV; k++) {
-        VI::unpack(raw[k], v[k]);
+        RV::template unpack<DTI>(raw[k], v[k]);
         if (RES) {
             float rf[E];
-            VI::unpack(rraw[k], rf);
+            RV::template unpack<DTI>(rraw[k], rf);
 #pragma unroll
             for (int e = 0; e < E; e++) v[k][e] += rf[e];
         }
@@ -151,7 +190,7 @@ __global__ __launch_bounds__(1024) void rownorm_vec(RowNormArgs a, int wpr)
         if (RES && a.h && store_row) {
             char* hr = static_cast<char*>(a.h) + row * a.hs * VI::BYTES;
 #pragma unroll
-            for (int k = 0; k < NV; k++) store_nt(hr + static_cast<int64_t>(jv[k]) * 16, VI::pack(v[k]));
+            for (int k = 0; k < NV; k++) store_nt(hr + static_cast<int64_t>(jv[k]) * VB, RV::template pack<DTI>(v[k]));
         }
     };
 
@@ -169,7 +208,7 @@ __global__ __launch_bounds__(1024) void rownorm_vec(RowNormArgs a, int wpr)
         float q = 0.f;
 #pragma unroll
         for (int k = 0; k < NV; k++) {
-            if constexpr (PACKED) VI::unpack(raw[k], v[k]);
+            if constexpr (PACKED) RV::template unpack<DTI>(raw[k], v[k]);
 #pragma unroll
             for (int e = 0; e < E; e++) {
                 const float d = own[k] ? v[k][e] - mean : 0.0f;
@@ -199,7 +238,7 @@ __global__ __launch_bounds__(1024) void rownorm_vec(RowNormArgs a, int wpr)
     char* qr = static_cast<char*>(a.yq) + row * a.yqs;
 #pragma unroll
     for (int k = 0; k < NV; k++) {
-        if constexpr (PACKED) VI::unpack(raw[k], v[k]);
+        if constexpr (PACKED) RV::template unpack<DTI>(raw[k], v[k]);
         float o[E];
         if (a.kind == SLHIP_NORM_LAYER) {
 #pragma unroll
@@ -342,53 +381,80 @@ static int env_int(const char* name, int dflt)
     return s && *s ? atoi(s) : dflt;
 }
 
-template <int DTI, int DTO, bool RES, bool Q>
+template <int DTI, int DTO, bool RES, bool Q, int VB>
 static int launch_vec(const RowNormArgs& a, int nv, int wpr, hipStream_t st)
 {
     int groups = wpr >= 4 ? 1 : 4 / wpr;
     int threads = 64 * wpr * groups;
     dim3 grid(static_cast<unsigned>((a.rows + groups - 1) / groups));
     switch (nv) {
-    case 1: rownorm_vec<DTI, DTO, 1, RES, Q><<<grid, threads, 0, st>>>(a, wpr); break;
-    case 2: rownorm_vec<DTI, DTO, 2, RES, Q><<<grid, threads, 0, st>>>(a, wpr); break;
-    case 4: rownorm_vec<DTI, DTO, 4, RES, Q><<<grid, threads, 0, st>>>(a, wpr); break;
-    case 8: rownorm_vec<DTI, DTO, 8, RES, Q><<<grid, threads, 0, st>>>(a, wpr); break;
+    case 1: rownorm_vec<DTI, DTO, 1, RES, Q, VB><<<grid, threads, 0, st>>>(a, wpr); break;
+    case 2: rownorm_vec<DTI, DTO, 2, RES, Q, VB><<<grid, threads, 0, st>>>(a, wpr); break;
+    case 3: rownorm_vec<DTI, DTO, 3, RES, Q, VB><<<grid, threads, 0, st>>>(a, wpr); break;
+    case 4: rownorm_vec<DTI, DTO, 4, RES, Q, VB><<<grid, threads, 0, st>>>(a, wpr); break;
+    case 5: rownorm_vec<DTI, DTO, 5, RES, Q, VB><<<grid, threads, 0, st>>>(a, wpr); break;
+    case 6: rownorm_vec<DTI, DTO, 6, RES, Q, VB><<<grid, threads, 0, st>>>(a, wpr); break;
+    case 8: rownorm_vec<DTI, DTO, 8, RES, Q, VB><<<grid, threads, 0, st>>>(a, wpr); break;
     default: return fail(SLHIP_ERR_INVALID, "internal: bad vector count %d", nv);
     }
     return check_launch("rownorm_vec");
 }
 
+static bool aligned_to(const void* p, int n) { return reinterpret_cast<uintptr_t>(p) % n == 0; }
+
+// Whether the rows fit the vector kernel with VB-byte input vectors: D a multiple of the vector's values,
+// every pointer and row stride aligned to the accesses the kernel makes (inputs and h: VB bytes; y and the
+// f16 copy: the values of one vector at the output width, at most 16 bytes; w and b: 16-byte loads), and
+// at most 8 vectors per lane of a 16-wave row group.
+template <int DTI, int DTO, int VB>
+static bool vec_fits(const RowNormArgs& a)
+{
+    constexpr int E = VB / Vec<DTI>::BYTES;
+    constexpr int OA = E * Vec<DTO>::BYTES < 16 ? E * Vec<DTO>::BYTES : 16;
+    constexpr int HA = E * 2 < 16 ? E * 2 : 16;
+    return a.D % E == 0 && a.D / E <= 8 * 64 * 16 && aligned_to(a.x, VB) && a.xs % E == 0 &&
+           (!a.res || (aligned_to(a.res, VB) && a.rs % E == 0)) && (!a.h || (aligned_to(a.h, VB) && a.hs % E == 0)) &&
+           aligned_to(a.y, OA) && (a.ys * Vec<DTO>::BYTES) % OA == 0 && aligned_to(a.y16, HA) &&
+           (a.y16s * 2) % HA == 0 && aligned_to(a.yq, E) && a.yqs % E == 0 && (!a.w || aligned16(a.w)) &&
+           (!a.b || aligned16(a.b));
+}
+
+template <int DTI, int DTO, int VB>
+static int launch_fitting(const RowNormArgs& a, hipStream_t st)
+{
+    const int64_t nvec = a.D / (VB / Vec<DTI>::BYTES);
+    // Row group sized for at most 64 bytes per lane and input (4 vectors of 16 bytes, 8 of 8): measured on
+    // MI355X at [8192, 4096] bf16 (residual add) 4 vectors of 16 bytes beat 2 by ~2.5% and 8 (one wave per
+    // row) by more; at [8192, 4100] five 8-byte vectors over four waves beat three over eight by 7%.
+    // Widened further while the launch has fewer than ~4096 waves. Lanes take 1-6 or 8 vectors, so that a
+    // row just beyond a power of two leaves fewer lanes idle.
+    constexpr int LANE_VECS = 64 / VB;
+    int wpr = 1;
+    while (wpr < 16 && nvec > static_cast<int64_t>(LANE_VECS) * 64 * wpr) wpr *= 2;
+    while (wpr < 16 && a.rows * wpr < 4096 && nvec >= static_cast<int64_t>(64) * wpr * 2) wpr *= 2;
+    int forced = env_int("SLHIP_ROWNORM_WPR", 0);
+    if (forced == 1 || forced == 2 || forced == 4 || forced == 8 || forced == 16) {
+        if (nvec <= static_cast<int64_t>(8) * 64 * forced) wpr = forced;
+    }
+    int64_t per = (nvec + 64 * wpr - 1) / (64 * wpr);
+    int nv = per == 7 ? 8 : static_cast<int>(per);
+    if constexpr (VB == 16) {
+        if (a.yq)
+            return a.res ? launch_vec<DTI, DTO, true, true, VB>(a, nv, wpr, st)
+                         : launch_vec<DTI, DTO, false, true, VB>(a, nv, wpr, st);
+    }
+    return a.res ? launch_vec<DTI, DTO, true, false, VB>(a, nv, wpr, st)
+                 : launch_vec<DTI, DTO, false, false, VB>(a, nv, wpr, st);
+}
+
 template <int DTI, int DTO>
 static int dispatch(const RowNormArgs& a, hipStream_t st)
 {
-    constexpr int E = Vec<DTI>::N;
-    constexpr int OA = E * Vec<DTO>::BYTES < 16 ? E * Vec<DTO>::BYTES : 16;  // output store alignment
-    constexpr int HA = E * 2;  // f16 copy store alignment (16 or 8 bytes)
-    bool vec_ok = a.D % E == 0 && aligned16(a.x) && a.xs % E == 0 && (!a.res || (aligned16(a.res) && a.rs % E == 0)) &&
-                  (!a.h || (aligned16(a.h) && a.hs % E == 0)) &&
-                  reinterpret_cast<uintptr_t>(a.y) % OA == 0 && (a.ys * Vec<DTO>::BYTES) % OA == 0 &&
-                  reinterpret_cast<uintptr_t>(a.y16) % HA == 0 && (a.y16s * 2) % HA == 0 &&
-                  reinterpret_cast<uintptr_t>(a.yq) % E == 0 && a.yqs % E == 0 &&
-                  (!a.w || aligned16(a.w)) && (!a.b || aligned16(a.b));
-    int64_t nvec = a.D / E;
-    if (vec_ok && nvec <= 8 * 64 * 16) {
-        // Row group sized for ~4 vectors (64 bytes) per lane and input: measured on MI355X at [8192, 4096]
-        // bf16 (residual add) this beats 2 vectors per lane by ~2.5% and 8 vectors (one wave per row) by
-        // more. Widened further while the launch has fewer than ~4096 waves.
-        int wpr = 1;
-        while (wpr < 16 && nvec > static_cast<int64_t>(4) * 64 * wpr) wpr *= 2;
-        while (wpr < 16 && a.rows * wpr < 4096 && nvec >= static_cast<int64_t>(64) * wpr * 2) wpr *= 2;
-        int forced = env_int("SLHIP_ROWNORM_WPR", 0);
-        if (forced == 1 || forced == 2 || forced == 4 || forced == 8 || forced == 16) {
-            if (nvec <= static_cast<int64_t>(8) * 64 * forced) wpr = forced;
-        }
-        int64_t per = (nvec + 64 * wpr - 1) / (64 * wpr);
-        int nv = per <= 1 ? 1 : per <= 2 ? 2 : per <= 4 ? 4 : 8;
-        if (a.yq)
-            return a.res ? launch_vec<DTI, DTO, true, true>(a, nv, wpr, st)
-                         : launch_vec<DTI, DTO, false, true>(a, nv, wpr, st);
-        return a.res ? launch_vec<DTI, DTO, true, false>(a, nv, wpr, st)
-                     : launch_vec<DTI, DTO, false, false>(a, nv, wpr, st);
+    if (vec_fits<DTI, DTO, 16>(a)) return launch_fitting<DTI, DTO, 16>(a, st);
+    // 2-byte rows of a length that is a multiple of 4 but not 8 (e.g. D = 4100) take 8-byte vectors; the
+    // E4M3 copy needs D % 128 == 0 and so always fits 16-byte vectors when its pointers do.
+    if constexpr (Vec<DTI>::BYTES == 2) {
+        if (!a.yq && vec_fits<DTI, DTO, 8>(a)) return launch_fitting<DTI, DTO, 8>(a, st);
     }
     rownorm_scalar<DTI, DTO><<<dim3(static_cast<unsigned>(a.rows)), 256, 0, st>>>(a);
     return check_launch("rownorm_scalar");

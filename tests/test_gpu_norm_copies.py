@@ -123,6 +123,23 @@ def test_scalar_path_copies(device, din):
     assert_bits_equal(yq, oracle.quantize_fp8(y32), what="E4M3 rows")
 
 
+@pytest.mark.parametrize("din,D,res", [("bf16", 1004, True), ("bf16", 4100, False)])
+def test_f16_copy_of_rows_with_8_byte_vectors(device, din, D, res):
+    """2-byte rows of a length that is a multiple of 4 but not of 8 (8-byte vectors): the f16 copy follows
+    the kernel's f32 values as on the 16-byte path (no E4M3 rows: they need D % 128 == 0)."""
+    rows = 13
+    seed = _seed("vec8", din, D, res)
+    x = synth.normal(seed, 0, (rows, D), dtype=din)
+    r = synth.normal(seed, 1, (rows, D), dtype=din) if res else None
+    w = synth.normal(seed, 2, (D,), 1.0, 0.1)
+    y32, y16, _ = _run("rms", din, "f32", x, r, w, 1e-6, y=True, y16=True, yq=False)
+    assert_f32_close(y32, _oracle_norm("rms", din, x, r, w, 1e-6), what="norm values")
+    assert_bits_equal(y16, oracle.to_f16(y32), what="f16 copy")
+    y_bf, y16b, _ = _run("rms", din, "bf16", x, r, w, 1e-6, y=True, y16=True, yq=False)
+    assert_bits_equal(y_bf, oracle.to_bf16(y32), what="bf16 y of the same values")
+    assert_bits_equal(y16b, y16, what="f16 copy beside bf16 y")
+
+
 def test_strided_copies_leave_the_padding(device):
     """Row strides beyond the row: the copies land at their rows and the bytes between stay untouched."""
     rows, D = 11, 512

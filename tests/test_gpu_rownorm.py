@@ -99,7 +99,14 @@ CASES = [
     ("rms", "bf16", "bf16", 1, 40960),
     ("rms", "f32", "f32", 2, 70000),   # beyond the vector path: scalar kernel
     ("l2", "f32", "f32", 6, 256),
-    ("l2", "bf16", "bf16", 6, 4100),   # D % 8 != 0: scalar kernel
+    ("l2", "bf16", "bf16", 6, 4100),   # D % 8 == 4: 8-byte vectors
+    ("rms", "bf16", "bf16", 5, 4100),
+    ("rms", "bf16", "f32", 9, 1004),
+    ("layer", "bf16", "bf16", 3, 1004),
+    ("layer", "bf16", "f32", 2, 12),
+    ("rms", "bf16", "bf16", 2, 32764),  # 8191 vectors of 8 bytes: one 16-wave group, 8 vectors per lane
+    ("rms", "bf16", "bf16", 4, 4102),   # D % 4 == 2: scalar kernel
+    ("layer", "bf16", "bf16", 3, 1001),
     ("layer", "f32", "f32", 5, 70),
     ("layer", "f32", "f32", 197, 768),
     ("layer", "f32", "f32", 4, 5000),
@@ -164,7 +171,11 @@ IN_PLACE = [
     ("rms", "f32", 5, 1000, True, 4),       # 250 vectors over 256 lanes: surplus lanes in the fourth wave
     ("layer", "bf16", 4099, 512, True, 0),  # LayerNorm's two reductions with one wave per row
     ("layer", "f32", 37, 1000, True, 2),
-    ("rms", "bf16", 9, 4100, True, 0),      # D % 8 != 0: the scalar kernel
+    ("rms", "bf16", 9, 4100, True, 0),      # D % 8 == 4: 8-byte vectors, surplus lanes
+    ("layer", "bf16", 4099, 1004, True, 0),  # 8-byte vectors, one wave per row, surplus groups
+    ("rms", "bf16", 4099, 1004, False, 1),
+    ("rms", "bf16", 37, 1004, True, 4),
+    ("rms", "bf16", 9, 4102, True, 0),      # D % 4 == 2: the scalar kernel
 ]
 
 
