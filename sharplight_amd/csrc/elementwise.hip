@@ -5,14 +5,15 @@
 // Semantics follow the reference CPU provider: BinaryOp (src/Sharplight.Cpu/BinaryOp.cs:8-350) with
 // numpy-style broadcasting by aligned strides (Align, :37-58: a dim of extent 1, or one the operand lacks,
 // gets stride 0), and ScalarMath.Unary (src/Sharplight.Cpu/ScalarMath.cs:100-641) in the forms its vector
-// loops compute (fused multiply-adds where they fuse, Gelu's f64 rational erf, GeluTanh through exp).
+// loops compute (fused multiply-adds where they fuse, Gelu's rational erf, GeluTanh through exp).
 // Arithmetic in f32; inputs and outputs f32, f16 or bf16.
 //
 // Layout: the host merges adjacent dims along which every operand stays linear (BinaryOp.Run's trailing
 // merge, :84-99, applied to every dim) and drops extent-1 dims, leaving "rows" of L contiguous output
 // elements under at most 7 outer dims. When L is a multiple of 8 and the output is 16-byte aligned, each
-// wave takes a 512-element span of one row: its row offsets are wave-uniform (scalar registers), each lane
-// one 8-element vector. Per operand the inner access is a 16-byte vector load (contiguous and aligned), one
+// wave takes a 512-element span of one row: its row offsets are wave-uniform (scalar registers, divided out
+// in 32 bits while the indices fit), each lane one 8-element vector; both operands' loads are issued before
+// either is used. Per operand the inner access is a 16-byte vector load (contiguous and aligned), one
 // value per wave (broadcast along the row: a bias per row, a scalar), or 8 element loads (strided or
 // unaligned). Lanes past the row's end redo its last vector and store the bytes its owner stores. Anything
 // else runs a one-thread-per-element kernel over the full index.
@@ -20,6 +21,7 @@
 #include "common.hpp"
 
 #include <math.h>
+#include <stdlib.h>
 
 namespace slhip {
 
@@ -38,7 +40,8 @@ struct EwArgs {
     int64_t sa_in, sb_in;  // innermost strides of a and b (0: broadcast along the row)
     int mode_a, mode_b;    // 0: 16-byte vectors, 1: one value per row, 2: element loads
     int64_t rows;          // product of the outer dims
-    int64_t spans;         // 512-element spans per row
+    int64_t spans;         // 512-element spans per row (one per wave)
+    int idx32;             // rows * spans < 2^32: the row index decomposes in 32-bit arithmetic
 };
 
 // ---- arithmetic ------------------------------------------------------------------------------------
@@ -158,21 +161,44 @@ __device__ __forceinline__ float unary_op(int op, float v, float p0, float p1)
 
 // ---- kernels ----------------------------------------------------------------------------------------
 
+// Eight values of an operand at row offset `off`, columns c .. c + 7, in two steps: fetch8 issues the loads
+// (a 16-byte vector, one value per row, or eight element loads), unpack8 turns them into f32. A kernel
+// fetches both operands before it unpacks either, so that their loads are in flight together (a load whose
+// result is used inside the mode branch makes the compiler wait for it before the next operand's loads).
+template <int DT> struct Fetch8 {
+    uint4 r[Vec<DT>::N == 4 ? 2 : 1];
+    float v[8];
+};
+
 template <int DT>
-__device__ __forceinline__ void load8(const void* base, int64_t off, int mode, int64_t s_in, int64_t c, float* v)
+__device__ __forceinline__ void fetch8(const void* base, int64_t off, int mode, int64_t s_in, int64_t c, Fetch8<DT>& f)
 {
     using V = Vec<DT>;
     if (mode == 0) {
         const char* p = static_cast<const char*>(base) + (off + c) * V::BYTES;
-        V::unpack(load_nt(p), v);
-        if constexpr (V::N == 4) V::unpack(load_nt(p + 16), v + 4);
+        f.r[0] = load_nt(p);
+        if constexpr (V::N == 4) f.r[1] = load_nt(p + 16);
     } else if (mode == 1) {
-        const float s = V::load1(base, off);
-#pragma unroll
-        for (int e = 0; e < 8; e++) v[e] = s;
+        f.v[0] = V::load1(base, off);
     } else {
 #pragma unroll
-        for (int e = 0; e < 8; e++) v[e] = V::load1(base, off + (c + e) * s_in);
+        for (int e = 0; e < 8; e++) f.v[e] = V::load1(base, off + (c + e) * s_in);
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ void unpack8(int mode, const Fetch8<DT>& f, float* v)
+{
+    using V = Vec<DT>;
+    if (mode == 0) {
+        V::unpack(f.r[0], v);
+        if constexpr (V::N == 4) V::unpack(f.r[1], v + 4);
+    } else if (mode == 1) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) v[e] = f.v[0];
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; e++) v[e] = f.v[e];
     }
 }
 
@@ -181,24 +207,42 @@ __global__ __launch_bounds__(256) void ew_vec(EwArgs a)
 {
     const int64_t w = static_cast<int64_t>(blockIdx.x) * 4 + wave_id();
     if (w >= a.rows * a.spans) return;  // wave-uniform: whole waves past the end
-    int64_t r = w / a.spans;
-    const int64_t span = w - r * a.spans;
-    int64_t ao = 0, bo = 0, yo = 0;
-    for (int k = a.nd - 1; k >= 0; k--) {  // wave-uniform row offsets
-        const int64_t q = r / a.dims[k];
-        const int64_t ix = r - q * a.dims[k];
-        r = q;
-        ao += ix * a.sa[k];
-        bo += ix * a.sb[k];
-        yo += ix * a.sy[k];
+    int64_t span, ao = 0, bo = 0, yo = 0;
+    if (a.idx32) {  // wave-uniform row offsets; 32-bit divisions while the indices fit
+        uint32_t r = static_cast<uint32_t>(w) / static_cast<uint32_t>(a.spans);
+        span = static_cast<uint32_t>(w) - r * static_cast<uint32_t>(a.spans);
+        for (int k = a.nd - 1; k >= 0; k--) {
+            const uint32_t d = static_cast<uint32_t>(a.dims[k]);
+            const uint32_t q = r / d;
+            const int64_t ix = r - q * d;
+            r = q;
+            ao += ix * a.sa[k];
+            bo += ix * a.sb[k];
+            yo += ix * a.sy[k];
+        }
+    } else {
+        int64_t r = w / a.spans;
+        span = w - r * a.spans;
+        for (int k = a.nd - 1; k >= 0; k--) {
+            const int64_t q = r / a.dims[k];
+            const int64_t ix = r - q * a.dims[k];
+            r = q;
+            ao += ix * a.sa[k];
+            bo += ix * a.sb[k];
+            yo += ix * a.sy[k];
+        }
     }
     int64_t c = span * 512 + (threadIdx.x & 63) * 8;
     c = c < a.L - 8 ? c : a.L - 8;
     float x[8], o[8];
-    load8<DA>(a.a, ao, a.mode_a, a.sa_in, c, x);
+    Fetch8<DA> fa;
+    Fetch8<DB> fb;
+    fetch8<DA>(a.a, ao, a.mode_a, a.sa_in, c, fa);
+    if constexpr (BIN) fetch8<DB>(a.b, bo, a.mode_b, a.sb_in, c, fb);
+    unpack8<DA>(a.mode_a, fa, x);
     if constexpr (BIN) {
         float z[8];
-        load8<DB>(a.b, bo, a.mode_b, a.sb_in, c, z);
+        unpack8<DB>(a.mode_b, fb, z);
         switch (a.op) {  // the common ops get a loop of their own; the rest one switch per element
         case SLHIP_BIN_ADD:
 #pragma unroll
@@ -310,6 +354,12 @@ static int launch(EwArgs& a, bool vec, hipStream_t st)
         const int64_t waves = a.rows * a.spans;
         const int64_t blocks = (waves + 3) / 4;
         if (blocks > 0x7FFFFFFF) return fail(SLHIP_ERR_UNSUPPORTED, "elementwise: tensor too large");
+        // (SLHIP_EW_INDEX64=1 takes the 64-bit form at any size, so that tests reach it)
+        static const bool force64 = [] {
+            const char* e = getenv("SLHIP_EW_INDEX64");
+            return e && *e == '1';
+        }();
+        a.idx32 = waves <= 0xFFFFFFFFll && !force64 ? 1 : 0;
         ew_vec<DA, DB, DO, BIN><<<dim3(static_cast<unsigned>(blocks)), 256, 0, st>>>(a);
         return check_launch("ew_vec");
     }

@@ -2,6 +2,8 @@
 UnaryKind) against the oracle's BinaryOp / ScalarMath.Unary restatement -- the reference's ElementwiseTests
 pattern (GPU vs CPU provider), with the reference's broadcast shapes (a bias over rows, one value per row,
 a scalar, outer-product shapes)."""
+import os
+
 import numpy as np
 import pytest
 
@@ -11,6 +13,7 @@ from tests.devutil import Dev, log
 from tests.parity import assert_bf16_close, assert_f32_close
 
 pytestmark = pytest.mark.gpu
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 NP = {"f32": np.float32, "bf16": np.uint16, "f16": np.float16}
 RNG = np.random.default_rng(77)
@@ -113,6 +116,36 @@ def test_bias_add_at_prefill_size(device):
     a = oracle.to_bf16(a32)
     y = _binary("Add", "bf16", "f32", "bf16", a, b)
     assert_bf16_close(y, oracle.to_bf16(oracle.binary("Add", oracle.from_bf16(a), b)), ulp=0, what="bias add")
+
+
+def test_binary_index_forms_agree(device):
+    """The row index of a wave divided out in 32 bits (every size a launch can take today) and in 64 bits
+    (the form for more than 2^32 waves, forced at start-up by SLHIP_EW_INDEX64 in a child process) give the
+    same outputs over the broadcast shapes."""
+    import json
+    import subprocess
+    import sys
+    cases = [(sa, sb) for sa, sb in SHAPES if np.prod(sa, dtype=int) >= 8]
+    script = (
+        "import json, sys, numpy as np\n"
+        "sys.path.insert(0, %r)\n"
+        "from tests.test_gpu_elementwise import _binary, SHAPES\n"
+        "from sharplight_amd import native\n"
+        "native.set_device(0)\n"
+        "rng = np.random.default_rng(5)\n"
+        "out = []\n"
+        "for sa, sb in %r:\n"
+        "    a = rng.uniform(-4, 4, sa).astype(np.float32); b = rng.uniform(-4, 4, sb).astype(np.float32)\n"
+        "    out.append(_binary('Add', 'f32', 'f32', 'f32', a, b).tobytes().hex())\n"
+        "print(json.dumps(out))\n") % (ROOT, [(list(a), list(b)) for a, b in cases])
+    res = []
+    for force in ("0", "1"):
+        env = dict(os.environ, SLHIP_EW_INDEX64=force)
+        log(f"elementwise index form, SLHIP_EW_INDEX64={force} (child process)")
+        r = subprocess.run([sys.executable, "-c", script], capture_output=True, text=True, timeout=100, env=env)
+        assert r.returncode == 0, r.stderr[-2000:]
+        res.append(json.loads(r.stdout.strip().splitlines()[-1]))
+    assert res[0] == res[1]
 
 
 def test_binary_strided_and_unaligned(device):
