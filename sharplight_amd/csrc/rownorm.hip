@@ -235,8 +235,9 @@ __global__ __launch_bounds__(1024) void rownorm_vec(RowNormArgs a, int wpr)
     launder();
     // Unpacked rows (f32, or with a residual) load the LayerNorm bias for every vector here, ahead of the
     // stores (a load used inside its own branch is waited for before the next vector's loads go out:
-    // [197, 768] f32 3.40 -> 3.23 us); a packed row loads weight and bias per vector, as the registers of
-    // all of them would cost the packed row its occupancy ([8192, 4096] bf16: 29.4 -> 30.6 us).
+    // [197, 768] f32 3.40 -> 3.23 us); a packed row loads weight and bias per vector (both before either is
+    // used), as the registers of all of them would cost the packed row its occupancy ([8192, 4096] bf16:
+    // 29.4 -> 30.6 us).
     float bv[NV][E];
     if (!PACKED && has_b) {
 #pragma unroll
@@ -257,17 +258,9 @@ __global__ __launch_bounds__(1024) void rownorm_vec(RowNormArgs a, int wpr)
     char* qr = static_cast<char*>(a.yq) + row * a.yqs;
 #pragma unroll
     for (int k = 0; k < NV; k++) {
-        if constexpr (PACKED) RV::template unpack<DTI>(raw[k], v[k]);
-        float o[E];
-        if (a.kind == SLHIP_NORM_LAYER) {
-#pragma unroll
-            for (int e = 0; e < E; e++) o[e] = (v[k][e] - mean) * scale;
-        } else {
-#pragma unroll
-            for (int e = 0; e < E; e++) o[e] = v[k][e] * scale;
-        }
-        if (has_w) {
-            if constexpr (!W_EARLY) {
+        // a packed row's weight and bias for this vector, both loads out before either is used
+        if constexpr (!W_EARLY) {
+            if (has_w) {
                 const float4* wp = reinterpret_cast<const float4*>(a.w + static_cast<int64_t>(jv[k]) * E);
 #pragma unroll
                 for (int q4 = 0; q4 < E / 4; q4++) {
@@ -278,11 +271,9 @@ __global__ __launch_bounds__(1024) void rownorm_vec(RowNormArgs a, int wpr)
                     wv[k][4 * q4 + 3] = w4.w;
                 }
             }
-#pragma unroll
-            for (int e = 0; e < E; e++) o[e] *= wv[k][e];
         }
-        if (has_b) {
-            if constexpr (PACKED) {
+        if constexpr (PACKED) {
+            if (has_b) {
                 const float4* bp = reinterpret_cast<const float4*>(a.b + static_cast<int64_t>(jv[k]) * E);
 #pragma unroll
                 for (int q4 = 0; q4 < E / 4; q4++) {
@@ -293,6 +284,21 @@ __global__ __launch_bounds__(1024) void rownorm_vec(RowNormArgs a, int wpr)
                     bv[k][4 * q4 + 3] = b4.w;
                 }
             }
+        }
+        if constexpr (PACKED) RV::template unpack<DTI>(raw[k], v[k]);
+        float o[E];
+        if (a.kind == SLHIP_NORM_LAYER) {
+#pragma unroll
+            for (int e = 0; e < E; e++) o[e] = (v[k][e] - mean) * scale;
+        } else {
+#pragma unroll
+            for (int e = 0; e < E; e++) o[e] = v[k][e] * scale;
+        }
+        if (has_w) {
+#pragma unroll
+            for (int e = 0; e < E; e++) o[e] *= wv[k][e];
+        }
+        if (has_b) {
 #pragma unroll
             for (int e = 0; e < E; e++) o[e] += bv[k][e];
         }
