@@ -136,6 +136,8 @@ SINGLE_CASES = [  # (fmt, x dtype, y dtype, T, K, N)
     ("q6_k", "f32", "f32", 2, 2560, 33),     # 2100 bytes: 4-byte loads
     ("q6_k", "bf16", "f32", 1, 768, 24),     # 630 bytes: 2-byte loads
     ("q6_k", "f32", "bf16", 5, 5120, 19),    # 4200 bytes
+    ("q4_0", "bf16", "f32", 1, 8192, 17),    # one token, a partial block of rows
+    ("q4_0", "f32", "bf16", 1, 4096, 1),     # a single row
 ]
 
 
@@ -303,6 +305,34 @@ def test_q6k_one_token_rows_of_code_32_give_exactly_zero(device):
     assert np.all(y[0, 0:5] == 0.0), y[0, 0:5]
     S = np.abs(x).astype(np.float64) @ _abs_terms("q6_k", raw, W).T
     _check_single(y, "f32", oracle.matvec("q6_k", raw, N, K, x), S, "q6_k one token")
+
+
+def test_q40_one_token_rows_of_code_8_and_wide_range(device):
+    """Q4_0 at one token: rows whose codes are all 8 (zero weights), blocks with d = 0 or a large d among
+    ordinary ones, and x spanning 2^-20 .. 2^12 with zeros and an outlier stay within the f32 bound, single and
+    dual. (The kernel folds the offset as d (sum q x - 8 sum x) per block, so a zero row gives a residual of
+    f32 rounding size, ~2^-24 8 d sum |x| per block, not an exact 0; the bound's |a| term covers it.)"""
+    N, K = 40, 4096
+    raw, _ = _weights("q4_0", N, K, 29, 1)
+    b = raw.reshape(N, K // 32, 18)
+    b[0:5, :, 2:] = 0x88             # every code 8
+    b[6, ::3, 0:2] = 0               # d = +0 on every third block of row 6
+    b[7, 5, 0:2] = np.frombuffer(np.float16(6.0e4).tobytes(), np.uint8)
+    W = oracle.dequant("q4_0", raw.reshape(-1), N * K).reshape(N, K)
+    assert not np.any(W[0:5])
+    r = synth.rng(7, 7)
+    x = (r.standard_normal((1, K)) * 2.0 ** r.integers(-20, 13, (1, K))).astype(np.float32)
+    x[0, ::41] = 0.0
+    x[0, 300] = -2.5e4
+    y = _run("q4_0", "f32", "f32", x, [raw], N, K)
+    S = np.abs(x).astype(np.float64) @ _abs_terms("q4_0", raw, W).T
+    _check_single(y, "f32", oracle.matvec("q4_0", raw, N, K, x), S, "q4_0 one token")
+    assert np.all(np.abs(y[0, 0:5]) <= 2.0 ** -16 * S[0, 0:5])
+    g = oracle.matvec("q4_0", raw, N, K, x)
+    y2 = _run("q4_0", "f32", "f32", x, [raw, raw], N, K, act="silu")
+    sig = 1.0 / (1.0 + np.exp(-g.astype(np.float64)))
+    ref = g * sig * g
+    assert np.all(np.abs(y2 - ref) <= 2.0 ** -14 * (S * (np.abs(g) + S) + 1e-30)), "dual q4_0 one token"
 
 
 def test_q4k_one_token_wide_range_and_zero_rows(device):
