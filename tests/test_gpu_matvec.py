@@ -330,7 +330,7 @@ def test_q40_one_token_rows_of_code_8_and_wide_range(device):
     assert np.all(np.abs(y[0, 0:5]) <= 2.0 ** -16 * S[0, 0:5])
     g = oracle.matvec("q4_0", raw, N, K, x)
     y2 = _run("q4_0", "f32", "f32", x, [raw, raw], N, K, act="silu")
-    sig = 1.0 / (1.0 + np.exp(-g.astype(np.float64)))
+    sig = 0.5 * (1.0 + np.tanh(0.5 * g.astype(np.float64)))  # the logistic function, without overflow
     ref = g * sig * g
     assert np.all(np.abs(y2 - ref) <= 2.0 ** -14 * (S * (np.abs(g) + S) + 1e-30)), "dual q4_0 one token"
 
