@@ -917,9 +917,9 @@ __global__ __launch_bounds__(64 * kMmWaves) void matvec_mfma_lds(MatvecArgs a)
 //     digit planes, every other slot zero. Output slot 4g + p (lane l holds slots 4 (l / 16) + 0..3 of row
 //     l % 16) is then the exact integer sum S_p of the lane's own codes times digit p.
 //   * After a group's MFMA a lane forms sum q x = 2^(e-6) (S1 + 2^-7 (S2 + 2^-7 (S3 + 2^-7 S4))) and scales
-//     it by its group's scale: Q4_K d0 (that) - m X (X the f32 sum of the block's x), Q6_K d sc (that) with
-//     S_p - 32 sum d_p for the code offset. Rows of zero weights contribute exactly 0 (Q6_K: codes 32) or
-//     exactly -m X (Q4_K: codes 0).
+//     it by its group's scale: Q4_K d0 (that) - m X (X the f32 sum of the block's x), Q6_K d sc (that), its
+//     codes entering B as the signed bytes q - 32. Rows of zero weights contribute exactly 0 (Q6_K: codes 32)
+//     or exactly -m X (Q4_K: codes 0).
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ i32x4_t as_i32x4(const uint4& v) { return __builtin_bit_cast(i32x4_t, v); }
@@ -1022,13 +1022,12 @@ template <> struct KqGeom<SLHIP_FMT_Q6_K> {
     static constexpr int ROW = SEG_SB * BB;  // 420 words: rows start on banks 36n mod 64, distinct for n < 16
 };
 
-// LDS: x digit planes [4][K], 16 zero bytes, per 32-value block 2^(e-6) and sum, (Q6_K) per 16-value group
-// the four digit-plane sums [K/16][4], the waves' sums [2][waves][16], the item buffers.
+// LDS: x digit planes [4][K], 16 zero bytes, per 32-value block 2^(e-6) and sum, the waves' sums
+// [2][waves][16], the item buffers.
 template <int FMT>
 static size_t kq_tile_lds(int64_t K)
 {
-    return static_cast<size_t>(K) * 4 + 16 + static_cast<size_t>(K / 32) * 8 +
-           (FMT == SLHIP_FMT_Q6_K ? static_cast<size_t>(K) : 0) + 2 * kKqTileWaves * 16 * 4 +
+    return static_cast<size_t>(K) * 4 + 16 + static_cast<size_t>(K / 32) * 8 + 2 * kKqTileWaves * 16 * 4 +
            static_cast<size_t>(kKqBufs) * kKqTileWaves * KqGeom<FMT>::ROW;
 }
 
@@ -1082,8 +1081,7 @@ __global__ __launch_bounds__(64 * kKqTileWaves) void matvec_kq_tile(MatvecArgs a
     const uint32_t zero_off = 4u * static_cast<uint32_t>(K);                 // 16 zero bytes after the planes
     float* xscale = reinterpret_cast<float*>(lds + zero_off + 16);            // [K / 32] 2^(e-6)
     float* xsum = xscale + K / 32;                                             // [K / 32]
-    int* dsum = reinterpret_cast<int*>(xsum + K / 32);                         // Q6_K: [K / 16][4]
-    float* red = reinterpret_cast<float*>(dsum + (Q6 ? K / 4 : 0));           // [2][waves][16]
+    float* red = xsum + K / 32;                                                // [2][waves][16]
     char* wbuf = reinterpret_cast<char*>(red + 2 * kKqTileWaves * 16);        // [bufs][waves][G::ROW]
     const int lane = threadIdx.x & 63, wave = wave_id();
     const int n = lane & 15, q = lane >> 4;
@@ -1117,8 +1115,7 @@ __global__ __launch_bounds__(64 * kKqTileWaves) void matvec_kq_tile(MatvecArgs a
         issue(lt < tiles ? lt : tiles - 1, lt < tiles ? ls : 0, b);
         next_item(lt, ls);
     }
-    // x digitized once: per 32-value block its exponent, sum and digit planes [4][K]; Q6_K also the digit
-    // sums of every 16-value group (its codes are stored + 32: sum (q - 32) d = sum q d - 32 sum d, exact)
+    // x digitized once: per 32-value block its exponent, sum and digit planes [4][K]
     for (int v4 = threadIdx.x; v4 < K / 4; v4 += 64 * kKqTileWaves) {  // whole waves (K % 256 == 0)
         float xv[4];
         kq_load_x(a, v4 / 64, xv);  // the lane's four values (v4 == 64 sb + lane)
@@ -1130,21 +1127,6 @@ __global__ __launch_bounds__(64 * kKqTileWaves) void matvec_kq_tile(MatvecArgs a
         if ((lane & 7) == 0) {
             xscale[v4 / 8] = down;
             xsum[v4 / 8] = sm;
-        }
-        if (Q6) {
-            int ds[4];
-#pragma unroll
-            for (int p = 0; p < 4; p++) {
-                const uint32_t w = pl[p];
-                // bytes as signed (d1) or unsigned (d2..d4) digits
-                int t = p == 0 ? (static_cast<int>(w << 24) >> 24) + (static_cast<int>(w << 16) >> 24) +
-                                     (static_cast<int>(w << 8) >> 24) + (static_cast<int>(w) >> 24)
-                               : static_cast<int>((w & 0xFFu) + ((w >> 8) & 0xFFu) + ((w >> 16) & 0xFFu) + (w >> 24));
-                t += __shfl_xor(t, 1);
-                t += __shfl_xor(t, 2);
-                ds[p] = t;
-            }
-            if ((lane & 3) == 0) *reinterpret_cast<int4*>(dsum + 4 * (v4 / 4)) = make_int4(ds[0], ds[1], ds[2], ds[3]);
         }
     }
     if (threadIdx.x < 4) smem[zero_off / 4 + threadIdx.x] = 0u;
@@ -1200,18 +1182,15 @@ __global__ __launch_bounds__(64 * kKqTileWaves) void matvec_kq_tile(MatvecArgs a
         for (int m = 0; m < 2; m++) {
             const int k = 2 * m + (q >> 1);
             const uint32_t hs = 2u * static_cast<uint32_t>(k);
+            // q - 32 as a signed byte: (q + 128) - 32 cannot borrow across bytes, then the top bit flipped back
             auto code = [&](uint32_t l, uint32_t h) {
-                return ((m ? l >> 4 : l) & 0x0F0F0F0Fu) | (((h >> hs) & 0x03030303u) << 4);
+                const uint32_t q = ((m ? l >> 4 : l) & 0x0F0F0F0Fu) | (((h >> hs) & 0x03030303u) << 4);
+                return ((q | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
             };
             const uint4 b = make_uint4(code(ql.x, qh.x), code(ql.y, qh.y), code(ql.z, qh.z), code(ql.w, qh.w));
             const int v = sb * 256 + 128 * hf + 32 * k + 16 * lh;
             i32x4_t c = {0, 0, 0, 0};
             c = __builtin_amdgcn_mfma_i32_16x16x64_i8(a_op(v), as_i32x4(b), c, 0, 0, 0);
-            const int4 ds = *reinterpret_cast<const int4*>(dsum + 4 * (v / 16));
-            c[0] -= 32 * ds.x;
-            c[1] -= 32 * ds.y;
-            c[2] -= 32 * ds.z;
-            c[3] -= 32 * ds.w;
             const float sc = static_cast<float>(*reinterpret_cast<const int8_t*>(row + 192 + 8 * hf + 2 * k + lh));
             acc = fmaf(__fmul_rn(d, sc), digits_dot(c, xscale[v / 32]), acc);
         }
