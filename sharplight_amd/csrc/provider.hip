@@ -205,6 +205,13 @@ struct Value {
         return elems(T) / ti.block * ti.block_bytes;
     }
     int64_t last() const { return dims.empty() ? 1 : dims.back(); }
+    // elements per entry of the first dimension (T counted as 1 past it)
+    int64_t inner() const
+    {
+        int64_t n = 1;
+        for (size_t k = 1; k < dims.size(); k++) n *= dims[k] == kSymT ? 1 : dims[k];
+        return n;
+    }
     int64_t rows(int64_t T) const { return last() == 0 ? 0 : elems(T) / last(); }
     bool symbolic() const
     {
@@ -311,8 +318,16 @@ Graph parse(const char* text)
                     if (d.find_first_not_of("0123456789") != std::string::npos)
                         invalid("dimension '" + d + "' is neither a size nor the token count T (other symbols and "
                                 "symbolic expressions are not supported)");
+                    // sizes up to 2^40 each and 2^46 elements without T: the byte counts of every launch stay
+                    // far inside int64 for any token count the segment accepts
+                    if (d.size() > 13 || strtoll(d.c_str(), nullptr, 10) > (int64_t{1} << 40))
+                        invalid("dimension " + d + " is above 2^40");
                     v.dims.push_back(strtoll(d.c_str(), nullptr, 10));
                 }
+                int64_t fixed = 1;
+                for (int64_t dd : v.dims)
+                    if (dd != kSymT && (__builtin_mul_overflow(fixed, dd, &fixed) || fixed > (int64_t{1} << 46)))
+                        invalid("value " + std::to_string(v.id) + " has more than 2^46 elements");
                 if (g.values.count(v.id)) invalid("value " + std::to_string(v.id) + " declared twice");
                 g.values[v.id] = v;
             } else if (kw == "input" || kw == "weight" || kw == "output" || kw == "state") {
@@ -494,7 +509,7 @@ Support supports(const Graph& g, const Node& n)
         if (!is_activation(st.type)) return no("CacheWrite: f32, f16 or bf16 caches (quantized caches are not supported)");
         if (x.type != DType::F32 && x.type != DType::BF16) return no("CacheWrite: f32 or bf16 rows");
         if (n.i("compression", 1) != 1) return no("CacheWrite: compressed caches are not supported");
-        if (st.dims.size() < 2 || x.dims.empty() || st.elems(0) / st.dims[0] != x.elems(1) / (x.dims[0] == kSymT ? 1 : x.dims[0]))
+        if (st.dims.size() < 2 || x.dims.empty() || st.inner() != x.inner())
             return no("CacheWrite: x rows must match the cache rows");
         for (size_t k = 2; k < n.in.size(); k++)
             if (g.value(n.in[k]).type != DType::I32) return no("CacheWrite: sequence rows and block table are i32");
@@ -569,6 +584,7 @@ public:
     Segment(Graph g, int64_t max_tokens, bool plan_only = false) : g_(std::move(g)), max_t_(max_tokens)
     {
         if (max_t_ < 0) invalid("MaxTokens must not be negative");
+        if (max_t_ > (int64_t{1} << 20)) invalid("MaxTokens above 2^20 is not supported");
         for (const Node& n : g_.nodes) {
             Support s = supports(g_, n);
             if (!s.ok) unsupported(s.reason);
@@ -1146,7 +1162,7 @@ private:
             const Value& x = g_.value(u.x);
             const Value& st = g_.value(u.y);
             const int64_t Tt = x.dims[0] == kSymT ? T : x.dims[0];
-            const int64_t inner = st.elems(0) / st.dims[0];
+            const int64_t inner = st.inner();
             const slhip_cache_rows r = rows_of(u.cache_node, Tt);
             check(slhip_cache_write(act_code(x.type), act_code(st.type), ptr(u.x), inner, Tt, inner, ptr(u.y), &r, stream_));
             break;

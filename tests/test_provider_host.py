@@ -286,3 +286,27 @@ def test_matmul_support_answers():
         ok, why = _supports(g, k)
         assert ok == e, (k, why)
         assert ok or why
+
+
+def test_zero_and_oversized_dimensions_are_answered_not_crashed():
+    """A cache write against a state or rows with a zero extent is answered (no division by the extent), and
+    sizes the provider could not address are refused at parse time: a dimension above 2^40, more than 2^46
+    elements without T, a token bound above 2^20. (Found by fuzzing the segment text under AddressSanitizer.)"""
+    text = ("value 0 f16 0 8 128\nvalue 1 bf16 T 8 128\nvalue 2 f16 4 0 128\nstate 0\nstate 2\ninput 1\n"
+            "node CacheWrite 0,1 -> -\nnode CacheWrite 2,1 -> -\n")
+    answers = []
+    for k in (0, 1):
+        ok = ctypes.c_int(1)
+        buf = ctypes.create_string_buffer(512)
+        native.call("slhip_node_supports", text.encode(), k, ctypes.byref(ok), buf, len(buf))
+        answers.append((ok.value, buf.value.decode()))
+    assert answers[0] == (1, "")  # rows of 8 x 128 into a cache of zero slots: a shape match (the write itself
+    #                                is refused at run time, every position being past the cache's end)
+    assert answers[1][0] == 0 and "cache rows" in answers[1][1]
+    for bad, msg in (("value 0 f32 T 1099511627777\n", "above 2"), ("value 0 f32 262144 262144 4096\n", "2\\^46"),
+                     ("value 0 f32 T 99999999999999999999\n", "above 2")):
+        with pytest.raises(native.SlhipArgumentError, match=msg):
+            describe(bad)
+    seg = ctypes.c_void_p(0)
+    assert native.lib().slhip_segment_compile(b"value 0 f32 T 64\ninput 0\n", (1 << 20) + 1, ctypes.byref(seg)) != native.OK
+    assert "2^20" in native.last_error()
