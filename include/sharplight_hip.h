@@ -449,8 +449,9 @@ SLHIP_API int slhip_unary(int op, int dtype_in, int dtype_out, const void* x, vo
  * A graph segment arrives as text, one declaration per line ('#' starts a comment line):
  *   value <id> <type> <dim> ...       type: a DataType name of the reference (f32 f16 bf16 i32, and the
  *                                     block formats slhip_format lists: q8_0 q4_k iq2_xxs nf4_b64 ...); a dim
- *                                     is a size, or "T", the symbolic token count bound at execute time (at
- *                                     most max_tokens); other symbols are refused
+ *                                     is a size (at most 2^40; at most 2^46 elements per value without T), or
+ *                                     "T", the symbolic token count bound at execute time (at most
+ *                                     max_tokens); other symbols are refused
  *   input <id> | weight <id> | output <id> | state <id>    (a state -- a KV cache -- has fixed dims, persists
  *                                     across runs, starts at zero and is zeroed again by reset_state)
  *   node <Op> <in,ids> -> <out,ids> [key=value ...]
@@ -478,7 +479,7 @@ SLHIP_API int slhip_provider_check(char* reason, size_t reason_size);
 SLHIP_API int slhip_node_supports(const char* segment_ir, int node_index, int* supported, char* reason,
                                   size_t reason_size);
 /* IComputeDevice.Compile (IComputeDevice.cs:33-38): allocates every value for max_tokens tokens
- * (CompileOptions.MaxTokens). SLHIP_ERR_UNSUPPORTED for a node or pattern this provider cannot run. */
+ * (CompileOptions.MaxTokens, 0 .. 2^20). SLHIP_ERR_UNSUPPORTED for a node or pattern this provider cannot run. */
 SLHIP_API int slhip_segment_compile(const char* segment_ir, int64_t max_tokens, slhip_segment* segment);
 /* ICompiledSegment.SetInput (ICompiledSegment.cs:9-10): dense host bytes of an input or weight value. */
 SLHIP_API int slhip_segment_set_input(slhip_segment segment, int value, const void* data, size_t bytes);
