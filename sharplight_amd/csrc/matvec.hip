@@ -1304,18 +1304,20 @@ static void launch_mfma_lds(const MatvecArgs& a, bool dual, hipStream_t st)
 // loaded straight from global memory, also used when K is not a multiple of the stage) and 16-row tiles
 // per block (SLHIP_MATVEC_MFMA_NT: 1 or 2; one with the 512-value stage).
 static int mfma_stage() { return env_int("SLHIP_MATVEC_MFMA_SK", 256); }
-// Default: one tile up to 8 tokens (finer blocks spread the 16-row tiles more evenly over the CUs), two
-// above (each x fragment then feeds twice the weights; measured at 14336 x 4096: 51 vs 57 us at T = 16).
-static int mfma_tiles(int64_t T)
+// Default: one tile (finer blocks spread the 16-row tiles more evenly over the CUs), two only for f32 x above
+// 12 tokens, where each x fragment's three-way bf16 split then feeds twice the weights. Measured at
+// 14336 x 4096 (dual, us, one tile / two): f32 x T = 8 46.3 / 48.4, T = 12 47.7 / 48.9, T = 16 51.1 / 50.0;
+// bf16 x T = 8 39.8 / 47.0, T = 16 42.1 / 47.7.
+static int mfma_tiles(int64_t T, int xt)
 {
     const int nt = env_int("SLHIP_MATVEC_MFMA_NT", 0);
-    return nt == 1 || nt == 2 ? nt : (T > 8 ? 2 : 1);
+    return nt == 1 || nt == 2 ? nt : (xt == SLHIP_F32 && T > 12 ? 2 : 1);
 }
 
 static int run_mfma(MatvecArgs a, bool dual, hipStream_t st)
 {
     const dim3 grid(static_cast<unsigned>((a.N + 15) / 16));
-    const int sk = mfma_stage(), nt = mfma_tiles(a.T);
+    const int sk = mfma_stage(), nt = mfma_tiles(a.T, a.xt);
     for (int64_t t0 = 0; t0 < a.T; t0 += 16) {
         a.t0 = t0;
         if (sk == 512 && a.K % 512 == 0) {
