@@ -1338,14 +1338,15 @@ static int run_mfma(MatvecArgs a, bool dual, hipStream_t st)
 }
 
 // Tokens from which bf16 weights take the matrix cores (SLHIP_MATVEC_MFMA_MIN_T; 0 disables): below it the
-// VALU kernel is already at the HBM rate.
-static int mfma_min_tokens() { return env_int("SLHIP_MATVEC_MFMA_MIN_T", 3); }
+// VALU kernel is already at the HBM rate. Measured at 14336 x 4096 (dual, us, VALU / matrix cores) at T = 2:
+// f32 x 41.6 / 44.3, bf16 x 45.1 / 40.0; at T = 3: f32 x 51.5 / 43.6.
+static int mfma_min_tokens(int xt) { return env_int("SLHIP_MATVEC_MFMA_MIN_T", xt == SLHIP_BF16 ? 2 : 3); }
 
 template <int WT>
 static int run_dense(MatvecArgs a, bool dual, hipStream_t st)
 {
     if constexpr (WT == SLHIP_BF16) {
-        const int mt = mfma_min_tokens();
+        const int mt = mfma_min_tokens(a.xt);
         if (mt > 0 && a.T >= mt && a.K % 64 == 0) return run_mfma(a, dual, st);
     }
     constexpr int E = Vec<WT>::N;

@@ -136,6 +136,7 @@ SINGLE_CASES = [  # (fmt, x dtype, y dtype, T, K, N)
     ("q6_k", "f32", "f32", 2, 2560, 33),     # 2100 bytes: 4-byte loads
     ("q6_k", "bf16", "f32", 1, 768, 24),     # 630 bytes: 2-byte loads
     ("q6_k", "f32", "bf16", 5, 5120, 19),    # 4200 bytes
+    ("bf16", "bf16", "f32", 2, 2048, 40),    # bf16 x at two tokens: the matrix cores
     ("q4_0", "bf16", "f32", 1, 8192, 17),    # one token, a partial block of rows
     ("q4_0", "f32", "bf16", 1, 4096, 1),     # a single row
 ]
@@ -176,6 +177,9 @@ DUAL_CASES = [  # (act, fmt, x dtype, y dtype, T, K, N): FusionTests.SwiGluDualM
     ("gelu_tanh", "bf16", "f32", "f32", 1, 4096, 64),
     ("gelu_erf", "f16", "f32", "f32", 4, 4096, 64),
     ("silu", "bf16", "bf16", "bf16", 1, 4096, 14336),  # the Llama-3-8B decode FFN (C3's model)
+    ("silu", "bf16", "bf16", "f32", 2, 4096, 72),      # bf16 x at two tokens: the matrix cores
+    ("gelu_tanh", "bf16", "bf16", "bf16", 16, 1024, 40),  # bf16 x at 16 tokens: one tile per block
+    ("silu", "bf16", "f32", "f32", 13, 1024, 72),      # f32 x above 12 tokens: two tiles per block
     ("silu", "q8_0", "f32", "f32", 1, 1024, 96),
     ("silu", "q8_0", "f32", "f32", 9, 1024, 96),
     ("silu", "q4_0", "f32", "f32", 1, 4096, 14336),
