@@ -904,6 +904,227 @@ __global__ __launch_bounds__(64 * kMmWaves) void matvec_mfma_lds(MatvecArgs a)
     }
 }
 
+// ---- 32-value block formats at several tokens on the matrix cores ---------------------------------------
+//
+// The VALU kernel decodes every weight once per group of tokens, so its time grows with T (Q4_0 dual at
+// [14336, 4096]: 18 us at T = 1, 57 at 4, 218 at 16). Here a 16-row tile's blocks are staged raw in LDS and
+// each code is decoded once into a bf16 A fragment that serves all 16 token columns of
+// v_mfma_f32_16x16x32_bf16: a 32-value block is one MFMA k-step, so each block's sums (16 rows x 16 tokens)
+// come out of one short MFMA chain and take the block scale d on the VALU (acc += d * sum). The codes enter
+// exactly (Q4_0: q - 8, Q8_0: q; small integers are exact in bf16); f32 x enters as two bf16 parts h + m
+// (h = bf16(x), m = bf16(x - h): |x - h - m| <= 2^-18 |x|, inside the matvec bound), bf16 x as it is. A block
+// of 8 waves takes one tile; the waves split each stage's blocks; the stage's row bytes are loaded two stages
+// ahead into registers and written to LDS one stage ahead (as the bf16 kernel above); partial sums meet in
+// LDS at the end.
+template <int FMT> struct MqGeom;
+constexpr int kMqWaves = 8;
+template <> struct MqGeom<SLHIP_FMT_Q4_0> { static constexpr int SKB = 32; };  // blocks per stage: 576-byte rows
+template <> struct MqGeom<SLHIP_FMT_Q8_0> { static constexpr int SKB = 16; };  // 544-byte rows
+
+// Eight codes of lane group g (values 8g .. 8g + 7 of the block) as four bf16 pairs; row: the row's stage
+// bytes (4-byte aligned), off: the block's first byte in it.
+template <int FMT>
+__device__ __forceinline__ uint4 mq_codes(const uint8_t* row, int off, int g)
+{
+    // the eight code bytes at off + 2 + (Q4_0: 8 (g & 1); Q8_0: 8 g), 2-byte aligned: three aligned words
+    // and a funnel shift (the row pointer is used as it is, so the reads stay LDS reads)
+    const int q = off + 2 + (FMT == SLHIP_FMT_Q4_0 ? 8 * (g & 1) : 8 * g);
+    const uint32_t* w = reinterpret_cast<const uint32_t*>(row) + (q >> 2);
+    const uint32_t sh = static_cast<uint32_t>(q & 3) * 8;
+    const uint32_t w0 = w[0], w1 = w[1], w2 = w[2];
+    uint32_t lo = __builtin_amdgcn_alignbit(w1, w0, sh), hi = __builtin_amdgcn_alignbit(w2, w1, sh);
+    float f[8];
+    if constexpr (FMT == SLHIP_FMT_Q4_0) {  // low nibbles (g < 2: values 0-15) or high (values 16-31)
+        const uint32_t s = 4 * static_cast<uint32_t>(g >> 1);
+        lo = (lo >> s) & 0x0F0F0F0Fu;
+        hi = (hi >> s) & 0x0F0F0F0Fu;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            f[e] = static_cast<float>((lo >> (8 * e)) & 0xFFu) - 8.0f;
+            f[4 + e] = static_cast<float>((hi >> (8 * e)) & 0xFFu) - 8.0f;
+        }
+    } else {  // int8 codes: q + 128 as an unsigned byte, then exact f32 arithmetic
+        lo ^= 0x80808080u;
+        hi ^= 0x80808080u;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            f[e] = static_cast<float>((lo >> (8 * e)) & 0xFFu) - 128.0f;
+            f[4 + e] = static_cast<float>((hi >> (8 * e)) & 0xFFu) - 128.0f;
+        }
+    }
+    return make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]), pack_bf16x2(f[6], f[7]));
+}
+
+// x[0..7] (f32) as two bf16 vectors h + m: h = bf16(x), m = bf16(x - h); a non-finite x keeps only h.
+__device__ __forceinline__ void split2(const float* x, uint4& h, uint4& m)
+{
+    uint32_t hw[4], mw[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float a0 = x[2 * i], a1 = x[2 * i + 1];
+        hw[i] = pack_bf16x2(a0, a1);
+        float r0 = a0 - bf16_lo(hw[i]), r1 = a1 - bf16_hi(hw[i]);
+        r0 = r0 == r0 ? r0 : 0.0f;
+        r1 = r1 == r1 ? r1 : 0.0f;
+        mw[i] = pack_bf16x2(r0, r1);
+    }
+    h = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+    m = make_uint4(mw[0], mw[1], mw[2], mw[3]);
+}
+
+template <int FMT, bool DUAL, bool XF32>
+__global__ __launch_bounds__(64 * kMqWaves) void matvec_mfma_q(MatvecArgs a)
+{
+    constexpr int BB = Fmt<FMT>::BB;
+    constexpr int NM = DUAL ? 2 : 1;
+    constexpr int SKB = MqGeom<FMT>::SKB;
+    constexpr int RB = SKB * BB;  // bytes of one row per stage
+    constexpr int PITCH = RB + 16;
+    constexpr int UPR = RB / 16;  // 16-byte units of a row per stage
+    constexpr int UNITS = NM * 16 * UPR;
+    constexpr int UPL = (UNITS + 64 * kMqWaves - 1) / (64 * kMqWaves);
+    constexpr int BPW = SKB / kMqWaves;  // blocks per wave and stage
+    static_assert(RB % 16 == 0 && SKB % kMqWaves == 0, "stage shape");
+    __shared__ __align__(16) uint8_t stage[2][NM][16][PITCH];
+    const int lane = threadIdx.x & 63;
+    const int wave = wave_id();
+    const int r = lane & 15, g = lane >> 4;
+    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 16;
+    int64_t tok = a.t0 + r;
+    tok = tok < a.T ? tok : a.T - 1;
+    const int ns = static_cast<int>(a.K / (SKB * 32));
+
+    // this thread's 16-byte units of the stage (threads past the last unit repeat it)
+    const char* src[UPL];
+    int dst[UPL];
+#pragma unroll
+    for (int i = 0; i < UPL; i++) {
+        int u = static_cast<int>(threadIdx.x) + 64 * kMqWaves * i;
+        u = u < UNITS ? u : UNITS - 1;
+        const int m = u / (16 * UPR), rem = u - m * (16 * UPR), rr = rem / UPR, c = rem - rr * UPR;
+        int64_t row = n0 + rr;
+        row = row < a.N ? row : a.N - 1;
+        src[i] = (m == 0 ? a.wg : a.wu) + row * a.wrow + 16 * c;
+        dst[i] = (m * 16 + rr) * PITCH + 16 * c;
+    }
+    uint4 pa[UPL], pb[UPL];
+    auto fetch_w = [&](uint4* pw, int s) {
+#pragma unroll
+        for (int i = 0; i < UPL; i++) pw[i] = load_nt(src[i] + static_cast<int64_t>(s) * RB);
+    };
+    auto put_w = [&](const uint4* pw, int b) {
+#pragma unroll
+        for (int i = 0; i < UPL; i++) *reinterpret_cast<uint4*>(&stage[b][0][0][0] + dst[i]) = pw[i];
+    };
+    // x of the wave's blocks, one stage ahead in two register sets: lane (g, token r) holds values 8g .. 8g + 7
+    struct Xs {
+        float4 f[BPW][2];
+        uint4 b[BPW];
+    };
+    auto fetch_x = [&](Xs& x, int s) {
+#pragma unroll
+        for (int j = 0; j < BPW; j++) {
+            const int64_t k0 = (static_cast<int64_t>(s) * SKB + wave * BPW + j) * 32 + 8 * g;
+            if (XF32) {
+                const float* xr = static_cast<const float*>(a.x) + tok * a.xs + k0;
+                x.f[j][0] = *reinterpret_cast<const float4*>(xr);
+                x.f[j][1] = *reinterpret_cast<const float4*>(xr + 4);
+            } else {
+                x.b[j] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.x) + tok * a.xs + k0);
+            }
+        }
+    };
+    f32x4_t ag = {0.0f, 0.0f, 0.0f, 0.0f}, au = {0.0f, 0.0f, 0.0f, 0.0f};
+    // Stage s from LDS buffer s & 1 with x in xc; the next stage's x (into xn) and the weights two ahead go
+    // out first, then each block in turn: its codes and scales from LDS, x split, the MFMAs, the scaling.
+    auto run_stage = [&](int s, const Xs& xc, Xs& xn, uint4* wnext, uint4* wfree) {
+        const int b = s & 1;
+        if (s + 1 < ns) fetch_x(xn, s + 1);  // block-uniform conditions
+        if (s + 2 < ns) fetch_w(wfree, s + 2);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < BPW; j++) {
+            const int off = (wave * BPW + j) * BB;
+            const uint4 Ag = mq_codes<FMT>(&stage[b][0][r][0], off, g);
+            uint4 Au = Ag;
+            if (DUAL) Au = mq_codes<FMT>(&stage[b][NM - 1][r][0], off, g);
+            float dg[4], du[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {  // the scales of the rows this lane's sums belong to (4g .. 4g + 3)
+                dg[i] = static_cast<float>(*reinterpret_cast<const _Float16*>(&stage[b][0][4 * g + i][off]));
+                du[i] = DUAL ? static_cast<float>(*reinterpret_cast<const _Float16*>(&stage[b][NM - 1][4 * g + i][off]))
+                             : 0.0f;
+            }
+            uint4 Bh, Bm;
+            if (XF32) {
+                const float v[8] = {xc.f[j][0].x, xc.f[j][0].y, xc.f[j][0].z, xc.f[j][0].w,
+                                    xc.f[j][1].x, xc.f[j][1].y, xc.f[j][1].z, xc.f[j][1].w};
+                split2(v, Bh, Bm);
+            } else {
+                Bh = xc.b[j];
+            }
+            f32x4_t cg = {0.0f, 0.0f, 0.0f, 0.0f}, cu = {0.0f, 0.0f, 0.0f, 0.0f};
+            cg = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(Ag), as_bf16x8(Bh), cg, 0, 0, 0);
+            if (XF32) cg = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(Ag), as_bf16x8(Bm), cg, 0, 0, 0);
+            if (DUAL) {
+                cu = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(Au), as_bf16x8(Bh), cu, 0, 0, 0);
+                if (XF32) cu = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(Au), as_bf16x8(Bm), cu, 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                ag[i] = fmaf(dg[i], cg[i], ag[i]);
+                if (DUAL) au[i] = fmaf(du[i], cu[i], au[i]);
+            }
+        }
+        if (s + 1 < ns) put_w(wnext, b ^ 1);
+        __syncthreads();
+    };
+    Xs xa, xb;
+    fetch_x(xa, 0);
+    fetch_w(pa, 0);
+    if (ns > 1) fetch_w(pb, 1);
+    put_w(pa, 0);
+    __syncthreads();
+    int s = 0;
+    for (; s + 1 < ns; s += 2) {
+        run_stage(s, xa, xb, pb, pa);
+        run_stage(s + 1, xb, xa, pa, pb);
+    }
+    if (s < ns) run_stage(s, xa, xb, pb, pa);
+    // the waves' partial sums meet in the (now idle) stage memory: [wave][matrix][lane]
+    f32x4_t* red = reinterpret_cast<f32x4_t*>(&stage[0][0][0][0]);
+    static_assert(sizeof(stage) >= sizeof(f32x4_t) * kMqWaves * NM * 64, "reduction space");
+    red[(wave * NM) * 64 + lane] = ag;
+    if (DUAL) red[(wave * NM + 1) * 64 + lane] = au;
+    __syncthreads();
+    if (wave != 0) return;
+    f32x4_t sg = red[lane], su = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    if (DUAL) su = red[64 + lane];
+#pragma unroll
+    for (int w = 1; w < kMqWaves; w++) {
+        sg += red[(w * NM) * 64 + lane];
+        if (DUAL) su += red[(w * NM + 1) * 64 + lane];
+    }
+    const int64_t t = a.t0 + r;  // lane: token column r, rows 4g + i
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int64_t n = n0 + 4 * g + i;
+        float out = sg[i];
+        if (DUAL) {
+            const float act = a.act == SLHIP_ACT_SILU        ? activate<SLHIP_ACT_SILU>(sg[i])
+                              : a.act == SLHIP_ACT_GELU_TANH ? activate<SLHIP_ACT_GELU_TANH>(sg[i])
+                                                             : activate<SLHIP_ACT_GELU_ERF>(sg[i]);
+            out = act * su[i];
+        }
+        if (t < a.T && n < a.N) {
+            if (a.yt == SLHIP_F32)
+                static_cast<float*>(a.y)[t * a.ys + n] = out;
+            else
+                static_cast<uint16_t*>(a.y)[t * a.ys + n] = static_cast<uint16_t>(f32_to_bf16_bits(out));
+        }
+    }
+}
+
 // ---- K-quant weights at one token on the matrix cores (integer MFMA) -------------------------------------
 //
 // The VALU kernel above spends ~4 lane instructions per Q4_K weight (code extraction, conversion, FMA), which
@@ -1476,9 +1697,39 @@ static int launch_kq_tile(const MatvecArgs& a, hipStream_t st)
     return check_launch("matvec_kq_tile");
 }
 
+// Tokens from which the 32-value block formats (Q4_0, Q8_0) take the matrix cores (SLHIP_MATVEC_MQ_MIN_T; 0
+// disables). Measured at [14336, 4096] (dual, us, VALU / matrix cores; f32 x, bf16 x): Q4_0 T = 2 26.7 /
+// 52.1, 25.7 / 39.7; T = 3 57.2 / 52.7, 55.6 / 40.3; T = 16 218 / 58, - / 42; Q8_0 T = 3 58.3 / 57.4,
+// 56.6 / 45.7; T = 16 223 / 64.
+static int mq_min_tokens() { return env_int("SLHIP_MATVEC_MQ_MIN_T", 3); }
+
+template <int FMT>
+static int run_mfma_q(MatvecArgs a, bool dual, hipStream_t st)
+{
+    const dim3 grid(static_cast<unsigned>((a.N + 15) / 16));
+    for (int64_t t0 = 0; t0 < a.T; t0 += 16) {
+        a.t0 = t0;
+        if (a.xt == SLHIP_F32) {
+            if (dual) matvec_mfma_q<FMT, true, true><<<grid, 64 * kMqWaves, 0, st>>>(a);
+            else matvec_mfma_q<FMT, false, true><<<grid, 64 * kMqWaves, 0, st>>>(a);
+        } else {
+            if (dual) matvec_mfma_q<FMT, true, false><<<grid, 64 * kMqWaves, 0, st>>>(a);
+            else matvec_mfma_q<FMT, false, false><<<grid, 64 * kMqWaves, 0, st>>>(a);
+        }
+        const int r = check_launch("matvec_mfma_q");
+        if (r != SLHIP_OK) return r;
+    }
+    return SLHIP_OK;
+}
+
 template <int FMT>
 static int run_quant(MatvecArgs a, bool dual, hipStream_t st)
 {
+    if constexpr (FMT == SLHIP_FMT_Q4_0 || FMT == SLHIP_FMT_Q8_0) {
+        // several tokens: the matrix-core kernel, when K splits into whole stages
+        const int mt = mq_min_tokens();
+        if (mt > 0 && a.T >= mt && a.K % (MqGeom<FMT>::SKB * 32) == 0) return run_mfma_q<FMT>(a, dual, st);
+    }
     if constexpr (FMT == SLHIP_FMT_Q4_K || FMT == SLHIP_FMT_Q6_K) {
         // one token: the matrix-core kernel, when K splits into whole segments and its LDS fits
         if (a.T == 1 && a.K % (256 * KqGeom<FMT>::SEG_SB) == 0 && kq_tile_lds<FMT>(a.K) <= kMaxLds &&

@@ -137,6 +137,11 @@ SINGLE_CASES = [  # (fmt, x dtype, y dtype, T, K, N)
     ("q6_k", "bf16", "f32", 1, 768, 24),     # 630 bytes: 2-byte loads
     ("q6_k", "f32", "bf16", 5, 5120, 19),    # 4200 bytes
     ("bf16", "bf16", "f32", 2, 2048, 40),    # bf16 x at two tokens: the matrix cores
+    ("q4_0", "bf16", "bf16", 16, 4096, 50),  # block formats from three tokens on the matrix cores
+    ("q8_0", "bf16", "f32", 3, 1024, 33),
+    ("q4_0", "f32", "f32", 2, 2048, 33),     # two tokens: the VALU kernel
+    ("q8_0", "f32", "bf16", 17, 2048, 40),   # two token groups, the second of one token
+    ("q4_0", "f32", "f32", 5, 1536, 24),     # K not a whole number of 1024-value stages: the VALU kernel
     ("q4_0", "bf16", "f32", 1, 8192, 17),    # one token, a partial block of rows
     ("q4_0", "f32", "bf16", 1, 4096, 1),     # a single row
 ]
@@ -183,6 +188,8 @@ DUAL_CASES = [  # (act, fmt, x dtype, y dtype, T, K, N): FusionTests.SwiGluDualM
     ("silu", "q8_0", "f32", "f32", 1, 1024, 96),
     ("silu", "q8_0", "f32", "f32", 9, 1024, 96),
     ("silu", "q4_0", "f32", "f32", 1, 4096, 14336),
+    ("silu", "q4_0", "f32", "f32", 16, 4096, 14336),  # batched decode on the matrix cores
+    ("gelu_erf", "q8_0", "bf16", "bf16", 4, 2048, 72),
     ("gelu_tanh", "q4_1", "f32", "bf16", 3, 1024, 96),
     ("silu", "q5_0", "bf16", "f32", 20, 256, 40),
     ("gelu_erf", "q5_1", "f32", "f32", 4, 2048, 64),
