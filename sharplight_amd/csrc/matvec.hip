@@ -912,14 +912,20 @@ __global__ __launch_bounds__(64 * kMmWaves) void matvec_mfma_lds(MatvecArgs a)
 // v_mfma_f32_16x16x32_bf16: a 32-value block is one MFMA k-step, so each block's sums (16 rows x 16 tokens)
 // come out of one short MFMA chain and take the block scale d on the VALU (acc += d * sum). The codes enter
 // exactly (Q4_0: q - 8, Q8_0: q; small integers are exact in bf16); f32 x enters as two bf16 parts h + m
-// (h = bf16(x), m = bf16(x - h): |x - h - m| <= 2^-18 |x|, inside the matvec bound), bf16 x as it is. A block
+// (h = bf16(x), m = bf16(x - h): |x - h - m| <= 2^-18 |x|, inside the matvec bound), bf16 x as it is. Q4_K
+// takes the same path with its 32-value sub-blocks as the blocks (a stage is 4 super-blocks, 576 bytes of a
+// row, and a wave half a super-block): codes q enter as they are, and the sub-block's d0 = d sc and minimum
+// m = dmin mn are applied on the VALU as acc += d0 sum(q x) - m sum(x), sum(x) of the lane's token summed
+// across its four lane groups (Quant.cs:518-545's value d0 q - m). A block
 // of 8 waves takes one tile; the waves split each stage's blocks; the stage's row bytes are loaded two stages
 // ahead into registers and written to LDS one stage ahead (as the bf16 kernel above); partial sums meet in
 // LDS at the end.
 template <int FMT> struct MqGeom;
 constexpr int kMqWaves = 8;
-template <> struct MqGeom<SLHIP_FMT_Q4_0> { static constexpr int SKB = 32; };  // blocks per stage: 576-byte rows
-template <> struct MqGeom<SLHIP_FMT_Q8_0> { static constexpr int SKB = 16; };  // 544-byte rows
+// SKB: 32-value blocks per stage, RB: bytes of one row per stage
+template <> struct MqGeom<SLHIP_FMT_Q4_0> { static constexpr int SKB = 32, RB = 32 * 18; };
+template <> struct MqGeom<SLHIP_FMT_Q8_0> { static constexpr int SKB = 16, RB = 16 * 34; };
+template <> struct MqGeom<SLHIP_FMT_Q4_K> { static constexpr int SKB = 32, RB = 4 * 144; };  // 4 super-blocks
 
 // Eight codes of lane group g (values 8g .. 8g + 7 of the block) as four bf16 pairs; row: the row's stage
 // bytes (4-byte aligned), off: the block's first byte in it.
@@ -955,6 +961,23 @@ __device__ __forceinline__ uint4 mq_codes(const uint8_t* row, int off, int g)
     return make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]), pack_bf16x2(f[6], f[7]));
 }
 
+// Eight Q4_K codes of lane group g (values 8g .. 8g + 7 of sub-block j: the low (j even) or high nibbles of
+// bytes 32 (j / 2) + 8g .. of the super-block's 128 code bytes, Quant.cs:518-545) as four bf16 pairs; sbo: the
+// super-block's first byte in the staged row (a multiple of 16), so the eight bytes are one aligned 8-byte read.
+__device__ __forceinline__ uint4 q4k_codes(const uint8_t* row, int sbo, int j, int g)
+{
+    const uint2 w = *reinterpret_cast<const uint2*>(row + sbo + 16 + 32 * (j >> 1) + 8 * g);
+    const uint32_t sh = 4 * static_cast<uint32_t>(j & 1);
+    const uint32_t lo = (w.x >> sh) & 0x0F0F0F0Fu, hi = (w.y >> sh) & 0x0F0F0F0Fu;
+    float f[8];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        f[e] = static_cast<float>((lo >> (8 * e)) & 0xFFu);
+        f[4 + e] = static_cast<float>((hi >> (8 * e)) & 0xFFu);
+    }
+    return make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]), pack_bf16x2(f[6], f[7]));
+}
+
 // x[0..7] (f32) as two bf16 vectors h + m: h = bf16(x), m = bf16(x - h); a non-finite x keeps only h.
 __device__ __forceinline__ void split2(const float* x, uint4& h, uint4& m)
 {
@@ -972,19 +995,23 @@ __device__ __forceinline__ void split2(const float* x, uint4& h, uint4& m)
     m = make_uint4(mw[0], mw[1], mw[2], mw[3]);
 }
 
+__device__ __forceinline__ void q4k_scales(const uint4& hdr, int j, float& d0, float& m);  // defined below
+
 template <int FMT, bool DUAL, bool XF32>
 __global__ __launch_bounds__(64 * kMqWaves) void matvec_mfma_q(MatvecArgs a)
 {
     constexpr int BB = Fmt<FMT>::BB;
     constexpr int NM = DUAL ? 2 : 1;
     constexpr int SKB = MqGeom<FMT>::SKB;
-    constexpr int RB = SKB * BB;  // bytes of one row per stage
+    constexpr bool KQ = FMT == SLHIP_FMT_Q4_K;
+    constexpr int RB = MqGeom<FMT>::RB;  // bytes of one row per stage
     constexpr int PITCH = RB + 16;
     constexpr int UPR = RB / 16;  // 16-byte units of a row per stage
     constexpr int UNITS = NM * 16 * UPR;
     constexpr int UPL = (UNITS + 64 * kMqWaves - 1) / (64 * kMqWaves);
     constexpr int BPW = SKB / kMqWaves;  // blocks per wave and stage
     static_assert(RB % 16 == 0 && SKB % kMqWaves == 0, "stage shape");
+    static_assert(!KQ || BPW == 4, "a Q4_K wave takes half a super-block per stage");
     __shared__ __align__(16) uint8_t stage[2][NM][16][PITCH];
     const int lane = threadIdx.x & 63;
     const int wave = wave_id();
@@ -992,7 +1019,7 @@ __global__ __launch_bounds__(64 * kMqWaves) void matvec_mfma_q(MatvecArgs a)
     const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 16;
     int64_t tok = a.t0 + r;
     tok = tok < a.T ? tok : a.T - 1;
-    const int ns = static_cast<int>(a.K / (SKB * 32));
+    const int ns = static_cast<int>(a.K / (SKB * 32));  // stages (each SKB * 32 values of the row)
 
     // this thread's 16-byte units of the stage (threads past the last unit repeat it)
     const char* src[UPL];
@@ -1042,26 +1069,60 @@ __global__ __launch_bounds__(64 * kMqWaves) void matvec_mfma_q(MatvecArgs a)
         if (s + 1 < ns) fetch_x(xn, s + 1);  // block-uniform conditions
         if (s + 2 < ns) fetch_w(wfree, s + 2);
         __builtin_amdgcn_sched_barrier(0);
+        // Q4_K: the wave's half super-block (sub-blocks 4 (wave & 1) ..) and the headers of the rows its sums
+        // belong to (4g .. 4g + 3), read once per stage. (Decoding the (d0, m) pairs once per wave into an LDS
+        // table instead cost a block of residency per CU: 82 -> 116 us at 16 tokens.)
+        const int sbo = KQ ? (wave >> 1) * 144 : 0;
+        uint4 hg[4], hu[4];
+        if constexpr (KQ) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                hg[i] = *reinterpret_cast<const uint4*>(&stage[b][0][4 * g + i][sbo]);
+                hu[i] = DUAL ? *reinterpret_cast<const uint4*>(&stage[b][NM - 1][4 * g + i][sbo]) : hg[i];
+            }
+        }
 #pragma unroll
         for (int j = 0; j < BPW; j++) {
             const int off = (wave * BPW + j) * BB;
-            const uint4 Ag = mq_codes<FMT>(&stage[b][0][r][0], off, g);
-            uint4 Au = Ag;
-            if (DUAL) Au = mq_codes<FMT>(&stage[b][NM - 1][r][0], off, g);
-            float dg[4], du[4];
+            const int sj = KQ ? 4 * (wave & 1) + j : 0;  // Q4_K sub-block
+            uint4 Ag, Au;
+            if constexpr (KQ) {
+                Ag = q4k_codes(&stage[b][0][r][0], sbo, sj, g);
+                Au = DUAL ? q4k_codes(&stage[b][NM - 1][r][0], sbo, sj, g) : Ag;
+            } else {
+                Ag = mq_codes<FMT>(&stage[b][0][r][0], off, g);
+                Au = DUAL ? mq_codes<FMT>(&stage[b][NM - 1][r][0], off, g) : Ag;
+            }
+            float dg[4], du[4], mg[4], mu[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) {  // the scales of the rows this lane's sums belong to (4g .. 4g + 3)
-                dg[i] = static_cast<float>(*reinterpret_cast<const _Float16*>(&stage[b][0][4 * g + i][off]));
-                du[i] = DUAL ? static_cast<float>(*reinterpret_cast<const _Float16*>(&stage[b][NM - 1][4 * g + i][off]))
-                             : 0.0f;
+                if constexpr (KQ) {
+                    q4k_scales(hg[i], sj, dg[i], mg[i]);
+                    if (DUAL) q4k_scales(hu[i], sj, du[i], mu[i]);
+                } else {
+                    dg[i] = static_cast<float>(*reinterpret_cast<const _Float16*>(&stage[b][0][4 * g + i][off]));
+                    du[i] = DUAL ? static_cast<float>(*reinterpret_cast<const _Float16*>(&stage[b][NM - 1][4 * g + i][off]))
+                                 : 0.0f;
+                }
             }
             uint4 Bh, Bm;
+            float xsum = 0.0f;  // Q4_K: the sub-block's x sum of this lane's token (the min term)
             if (XF32) {
                 const float v[8] = {xc.f[j][0].x, xc.f[j][0].y, xc.f[j][0].z, xc.f[j][0].w,
                                     xc.f[j][1].x, xc.f[j][1].y, xc.f[j][1].z, xc.f[j][1].w};
                 split2(v, Bh, Bm);
+                if constexpr (KQ) xsum = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
             } else {
                 Bh = xc.b[j];
+                if constexpr (KQ) {
+                    const uint4& w = xc.b[j];
+                    xsum = ((bf16_lo(w.x) + bf16_hi(w.x)) + (bf16_lo(w.y) + bf16_hi(w.y))) +
+                           ((bf16_lo(w.z) + bf16_hi(w.z)) + (bf16_lo(w.w) + bf16_hi(w.w)));
+                }
+            }
+            if constexpr (KQ) {  // the four lane groups of the token hold the sub-block's four 8-value parts
+                xsum += __shfl_xor(xsum, 16);
+                xsum += __shfl_xor(xsum, 32);
             }
             f32x4_t cg = {0.0f, 0.0f, 0.0f, 0.0f}, cu = {0.0f, 0.0f, 0.0f, 0.0f};
             cg = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(Ag), as_bf16x8(Bh), cg, 0, 0, 0);
@@ -1074,6 +1135,10 @@ __global__ __launch_bounds__(64 * kMqWaves) void matvec_mfma_q(MatvecArgs a)
             for (int i = 0; i < 4; i++) {
                 ag[i] = fmaf(dg[i], cg[i], ag[i]);
                 if (DUAL) au[i] = fmaf(du[i], cu[i], au[i]);
+                if constexpr (KQ) {  // Q4_K: d0 sum(q x) - m sum(x)
+                    ag[i] = fmaf(-mg[i], xsum, ag[i]);
+                    if (DUAL) au[i] = fmaf(-mu[i], xsum, au[i]);
+                }
             }
         }
         if (s + 1 < ns) put_w(wnext, b ^ 1);
@@ -1702,6 +1767,10 @@ static int launch_kq_tile(const MatvecArgs& a, hipStream_t st)
 // 52.1, 25.7 / 39.7; T = 3 57.2 / 52.7, 55.6 / 40.3; T = 16 218 / 58, - / 42; Q8_0 T = 3 58.3 / 57.4,
 // 56.6 / 45.7; T = 16 223 / 64.
 static int mq_min_tokens() { return env_int("SLHIP_MATVEC_MQ_MIN_T", 3); }
+// The same for Q4_K (SLHIP_MATVEC_KQ_MIN_T): its VALU kernel takes four tokens per pass, so the matrix cores
+// pay from five. Measured dual at [14336, 4096], f32 x (us, VALU / matrix cores): T = 4 57.6 / 75.2;
+// T = 16 229 / 82.
+static int kq_min_tokens() { return env_int("SLHIP_MATVEC_KQ_MIN_T", 5); }
 
 template <int FMT>
 static int run_mfma_q(MatvecArgs a, bool dual, hipStream_t st)
@@ -1725,9 +1794,9 @@ static int run_mfma_q(MatvecArgs a, bool dual, hipStream_t st)
 template <int FMT>
 static int run_quant(MatvecArgs a, bool dual, hipStream_t st)
 {
-    if constexpr (FMT == SLHIP_FMT_Q4_0 || FMT == SLHIP_FMT_Q8_0) {
+    if constexpr (FMT == SLHIP_FMT_Q4_0 || FMT == SLHIP_FMT_Q8_0 || FMT == SLHIP_FMT_Q4_K) {
         // several tokens: the matrix-core kernel, when K splits into whole stages
-        const int mt = mq_min_tokens();
+        const int mt = FMT == SLHIP_FMT_Q4_K ? kq_min_tokens() : mq_min_tokens();
         if (mt > 0 && a.T >= mt && a.K % (MqGeom<FMT>::SKB * 32) == 0) return run_mfma_q<FMT>(a, dual, st);
     }
     if constexpr (FMT == SLHIP_FMT_Q4_K || FMT == SLHIP_FMT_Q6_K) {

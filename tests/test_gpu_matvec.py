@@ -144,6 +144,10 @@ SINGLE_CASES = [  # (fmt, x dtype, y dtype, T, K, N)
     ("q4_0", "f32", "f32", 5, 1536, 24),     # K not a whole number of 1024-value stages: the VALU kernel
     ("q4_0", "bf16", "f32", 1, 8192, 17),    # one token, a partial block of rows
     ("q4_0", "f32", "bf16", 1, 4096, 1),     # a single row
+    ("q4_k", "f32", "f32", 5, 1024, 33),     # Q4_K from five tokens on the matrix cores: one stage
+    ("q4_k", "bf16", "bf16", 16, 4096, 50),
+    ("q4_k", "f32", "bf16", 17, 2048, 40),   # two token groups, the second of one token
+    ("q4_k", "f32", "f32", 4, 1280, 24),     # K not a whole number of 1024-value stages: the VALU kernel
 ]
 
 
@@ -206,6 +210,9 @@ DUAL_CASES = [  # (act, fmt, x dtype, y dtype, T, K, N): FusionTests.SwiGluDualM
     ("gelu_tanh", "q4_k", "bf16", "bf16", 1, 14336, 24),
     ("silu", "q6_k", "f32", "f32", 1, 3072, 40),          # Q6_K rows not 16-byte multiples
     ("gelu_erf", "q6_k", "bf16", "f32", 3, 768, 33),
+    ("silu", "q4_k", "f32", "f32", 16, 4096, 14336),  # batched Q4_K_M decode FFN on the matrix cores
+    ("gelu_erf", "q4_k", "bf16", "bf16", 6, 1024, 72),
+    ("silu", "q4_k", "f32", "f32", 4, 1024, 40),       # four tokens: still the VALU kernel
 ]
 
 
@@ -370,6 +377,26 @@ def test_q4k_one_token_wide_range_and_zero_rows(device):
         assert np.all(y[0, 0:4] == 0.0), y[0, 0:4]
         S = np.abs(x).astype(np.float64) @ _abs_terms("q4_k", raw, W).T
         _check_single(y, "f32", g, S, "q4_k one token, wide x")
+
+
+def test_q4k_several_tokens_wide_range_and_zero_rows(device):
+    """The several-token Q4_K kernel (bf16 codes on the matrix cores, f32 x as two bf16 parts, the minimum
+    applied as -m * sum(x) per sub-block on the VALU): x spanning 2^-20 .. 2^12 within a block, exact zeros and
+    an outlier stay within the f32 bound per token; rows whose codes and minima are all zero give exactly 0."""
+    N, K, T = 40, 2048, 5
+    raw, W = _weights("q4_k", N, K, 23, 1)
+    blocks = raw.reshape(N, K // 256, 144)
+    blocks[0:8, :, 16:] = 0          # codes 0
+    blocks[0:4, :, 2:4] = 0          # and dmin 0: the row's weights are exactly 0
+    W = oracle.dequant("q4_k", raw.reshape(-1), N * K).reshape(N, K)
+    r = synth.rng(6, 6)
+    x = (r.standard_normal((T, K)) * 2.0 ** r.integers(-20, 13, (T, K))).astype(np.float32)
+    x[:, ::37] = 0.0
+    x[1, 100] = 3.0e4
+    y = _run("q4_k", "f32", "f32", x, [raw], N, K)
+    assert np.all(y[:, 0:4] == 0.0), y[:, 0:4]
+    S = np.abs(x).astype(np.float64) @ _abs_terms("q4_k", raw, W).T
+    _check_single(y, "f32", oracle.matvec("q4_k", raw, N, K, x), S, "q4_k several tokens, wide x")
 
 
 @pytest.mark.parametrize("T", [1, 3])
