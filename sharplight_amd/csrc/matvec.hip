@@ -27,6 +27,8 @@
 
 #include <stdlib.h>
 
+#include <type_traits>
+
 namespace slhip {
 
 struct MatvecArgs {
@@ -922,10 +924,11 @@ __global__ __launch_bounds__(64 * kMmWaves) void matvec_mfma_lds(MatvecArgs a)
 // LDS at the end.
 template <int FMT> struct MqGeom;
 constexpr int kMqWaves = 8;
-// SKB: 32-value blocks per stage, RB: bytes of one row per stage
-template <> struct MqGeom<SLHIP_FMT_Q4_0> { static constexpr int SKB = 32, RB = 32 * 18; };
-template <> struct MqGeom<SLHIP_FMT_Q8_0> { static constexpr int SKB = 16, RB = 16 * 34; };
-template <> struct MqGeom<SLHIP_FMT_Q4_K> { static constexpr int SKB = 32, RB = 4 * 144; };  // 4 super-blocks
+// SKB: 32-value blocks per stage, RB: bytes of one row per stage, UB: bytes per staging load
+template <> struct MqGeom<SLHIP_FMT_Q4_0> { static constexpr int SKB = 32, RB = 32 * 18, UB = 16; };
+template <> struct MqGeom<SLHIP_FMT_Q8_0> { static constexpr int SKB = 16, RB = 16 * 34, UB = 16; };
+template <> struct MqGeom<SLHIP_FMT_Q4_K> { static constexpr int SKB = 32, RB = 4 * 144, UB = 16; };  // 4 super-blocks
+template <> struct MqGeom<SLHIP_FMT_Q6_K> { static constexpr int SKB = 32, RB = 4 * 210, UB = 8; };   // 840 bytes
 
 // Eight codes of lane group g (values 8g .. 8g + 7 of the block) as four bf16 pairs; row: the row's stage
 // bytes (4-byte aligned), off: the block's first byte in it.
@@ -978,6 +981,34 @@ __device__ __forceinline__ uint4 q4k_codes(const uint8_t* row, int sbo, int j, i
     return make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]), pack_bf16x2(f[6], f[7]));
 }
 
+// Eight Q6_K codes q - 32 of lane group g: values l = 8g .. 8g + 7 of the 32-value block u = 4 hf + k of a
+// super-block {ql[128], qh[64], sc[16], f16 d}: q = (low (k < 2) or high nibble of ql[64 hf + 32 (k & 1) + l]) |
+// (bits 2k, 2k + 1 of qh[32 hf + l]) << 4 (ggml's Q6_K layout, Quant.KQuants.cs:36-107), as four bf16 pairs
+// (exact: -32 .. 31). sbo: the super-block's first byte in the staged row (2-byte aligned), so each 8-byte
+// run is three aligned words and a funnel shift.
+__device__ __forceinline__ uint4 q6k_codes(const uint8_t* row, int sbo, int u, int g)
+{
+    const int hf = u >> 2, k = u & 3;
+    auto bytes8 = [&](int q) {
+        const uint32_t* w = reinterpret_cast<const uint32_t*>(row) + (q >> 2);
+        const uint32_t sh = static_cast<uint32_t>(q & 3) * 8;
+        const uint32_t w0 = w[0], w1 = w[1], w2 = w[2];
+        return make_uint2(__builtin_amdgcn_alignbit(w1, w0, sh), __builtin_amdgcn_alignbit(w2, w1, sh));
+    };
+    const uint2 l = bytes8(sbo + 64 * hf + 32 * (k & 1) + 8 * g);
+    const uint2 h = bytes8(sbo + 128 + 32 * hf + 8 * g);
+    const uint32_t ls = 4 * static_cast<uint32_t>(k >> 1), hs = 2 * static_cast<uint32_t>(k);
+    const uint32_t q0 = ((l.x >> ls) & 0x0F0F0F0Fu) | (((h.x >> hs) & 0x03030303u) << 4);
+    const uint32_t q1 = ((l.y >> ls) & 0x0F0F0F0Fu) | (((h.y >> hs) & 0x03030303u) << 4);
+    float f[8];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        f[e] = static_cast<float>((q0 >> (8 * e)) & 0xFFu) - 32.0f;
+        f[4 + e] = static_cast<float>((q1 >> (8 * e)) & 0xFFu) - 32.0f;
+    }
+    return make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]), pack_bf16x2(f[6], f[7]));
+}
+
 // x[0..7] (f32) as two bf16 vectors h + m: h = bf16(x), m = bf16(x - h); a non-finite x keeps only h.
 __device__ __forceinline__ void split2(const float* x, uint4& h, uint4& m)
 {
@@ -1004,14 +1035,17 @@ __global__ __launch_bounds__(64 * kMqWaves) void matvec_mfma_q(MatvecArgs a)
     constexpr int NM = DUAL ? 2 : 1;
     constexpr int SKB = MqGeom<FMT>::SKB;
     constexpr bool KQ = FMT == SLHIP_FMT_Q4_K;
+    constexpr bool K6 = FMT == SLHIP_FMT_Q6_K;
     constexpr int RB = MqGeom<FMT>::RB;  // bytes of one row per stage
+    constexpr int UB = MqGeom<FMT>::UB;  // bytes per staging load
+    using WU = std::conditional_t<UB == 16, uint4, uint2>;
     constexpr int PITCH = RB + 16;
-    constexpr int UPR = RB / 16;  // 16-byte units of a row per stage
+    constexpr int UPR = RB / UB;  // staging units of a row per stage
     constexpr int UNITS = NM * 16 * UPR;
     constexpr int UPL = (UNITS + 64 * kMqWaves - 1) / (64 * kMqWaves);
     constexpr int BPW = SKB / kMqWaves;  // blocks per wave and stage
-    static_assert(RB % 16 == 0 && SKB % kMqWaves == 0, "stage shape");
-    static_assert(!KQ || BPW == 4, "a Q4_K wave takes half a super-block per stage");
+    static_assert(RB % UB == 0 && PITCH % 8 == 0 && SKB % kMqWaves == 0, "stage shape");
+    static_assert(!(KQ || K6) || BPW == 4, "a K-quant wave takes half a super-block per stage");
     __shared__ __align__(16) uint8_t stage[2][NM][16][PITCH];
     const int lane = threadIdx.x & 63;
     const int wave = wave_id();
@@ -1031,17 +1065,25 @@ __global__ __launch_bounds__(64 * kMqWaves) void matvec_mfma_q(MatvecArgs a)
         const int m = u / (16 * UPR), rem = u - m * (16 * UPR), rr = rem / UPR, c = rem - rr * UPR;
         int64_t row = n0 + rr;
         row = row < a.N ? row : a.N - 1;
-        src[i] = (m == 0 ? a.wg : a.wu) + row * a.wrow + 16 * c;
-        dst[i] = (m * 16 + rr) * PITCH + 16 * c;
+        src[i] = (m == 0 ? a.wg : a.wu) + row * a.wrow + UB * c;
+        dst[i] = (m * 16 + rr) * PITCH + UB * c;
     }
-    uint4 pa[UPL], pb[UPL];
-    auto fetch_w = [&](uint4* pw, int s) {
+    WU pa[UPL], pb[UPL];
+    auto fetch_w = [&](WU* pw, int s) {
 #pragma unroll
-        for (int i = 0; i < UPL; i++) pw[i] = load_nt(src[i] + static_cast<int64_t>(s) * RB);
+        for (int i = 0; i < UPL; i++) {
+            const char* p = src[i] + static_cast<int64_t>(s) * RB;
+            if constexpr (UB == 16) {
+                pw[i] = load_nt(p);
+            } else {
+                const u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+                pw[i] = make_uint2(v.x, v.y);
+            }
+        }
     };
-    auto put_w = [&](const uint4* pw, int b) {
+    auto put_w = [&](const WU* pw, int b) {
 #pragma unroll
-        for (int i = 0; i < UPL; i++) *reinterpret_cast<uint4*>(&stage[b][0][0][0] + dst[i]) = pw[i];
+        for (int i = 0; i < UPL; i++) *reinterpret_cast<WU*>(&stage[b][0][0][0] + dst[i]) = pw[i];
     };
     // x of the wave's blocks, one stage ahead in two register sets: lane (g, token r) holds values 8g .. 8g + 7
     struct Xs {
@@ -1064,7 +1106,7 @@ __global__ __launch_bounds__(64 * kMqWaves) void matvec_mfma_q(MatvecArgs a)
     f32x4_t ag = {0.0f, 0.0f, 0.0f, 0.0f}, au = {0.0f, 0.0f, 0.0f, 0.0f};
     // Stage s from LDS buffer s & 1 with x in xc; the next stage's x (into xn) and the weights two ahead go
     // out first, then each block in turn: its codes and scales from LDS, x split, the MFMAs, the scaling.
-    auto run_stage = [&](int s, const Xs& xc, Xs& xn, uint4* wnext, uint4* wfree) {
+    auto run_stage = [&](int s, const Xs& xc, Xs& xn, WU* wnext, WU* wfree) {
         const int b = s & 1;
         if (s + 1 < ns) fetch_x(xn, s + 1);  // block-uniform conditions
         if (s + 2 < ns) fetch_w(wfree, s + 2);
@@ -1072,8 +1114,17 @@ __global__ __launch_bounds__(64 * kMqWaves) void matvec_mfma_q(MatvecArgs a)
         // Q4_K: the wave's half super-block (sub-blocks 4 (wave & 1) ..) and the headers of the rows its sums
         // belong to (4g .. 4g + 3), read once per stage. (Decoding the (d0, m) pairs once per wave into an LDS
         // table instead cost a block of residency per CU: 82 -> 116 us at 16 tokens.)
-        const int sbo = KQ ? (wave >> 1) * 144 : 0;
+        const int sbo = KQ ? (wave >> 1) * 144 : K6 ? (wave >> 1) * 210 : 0;
         uint4 hg[4], hu[4];
+        float d6g[4], d6u[4];  // Q6_K: the super-block scale d of the rows 4g + i
+        if constexpr (K6) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                d6g[i] = static_cast<float>(*reinterpret_cast<const _Float16*>(&stage[b][0][4 * g + i][sbo + 208]));
+                d6u[i] = DUAL ? static_cast<float>(*reinterpret_cast<const _Float16*>(&stage[b][NM - 1][4 * g + i][sbo + 208]))
+                              : 0.0f;
+            }
+        }
         if constexpr (KQ) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
@@ -1089,6 +1140,9 @@ __global__ __launch_bounds__(64 * kMqWaves) void matvec_mfma_q(MatvecArgs a)
             if constexpr (KQ) {
                 Ag = q4k_codes(&stage[b][0][r][0], sbo, sj, g);
                 Au = DUAL ? q4k_codes(&stage[b][NM - 1][r][0], sbo, sj, g) : Ag;
+            } else if constexpr (K6) {
+                Ag = q6k_codes(&stage[b][0][r][0], sbo, 4 * (wave & 1) + j, g);
+                Au = DUAL ? q6k_codes(&stage[b][NM - 1][r][0], sbo, 4 * (wave & 1) + j, g) : Ag;
             } else {
                 Ag = mq_codes<FMT>(&stage[b][0][r][0], off, g);
                 Au = DUAL ? mq_codes<FMT>(&stage[b][NM - 1][r][0], off, g) : Ag;
@@ -1099,6 +1153,17 @@ __global__ __launch_bounds__(64 * kMqWaves) void matvec_mfma_q(MatvecArgs a)
                 if constexpr (KQ) {
                     q4k_scales(hg[i], sj, dg[i], mg[i]);
                     if (DUAL) q4k_scales(hu[i], sj, du[i], mu[i]);
+                } else if constexpr (K6) {
+                    // the block's two 16-value scales sc[8 hf + 2k + 0..1] (2-byte aligned): d sc as (dg, mg)
+                    const int so = sbo + 192 + 2 * (4 * (wave & 1) + j);
+                    const uint32_t sg = *reinterpret_cast<const uint16_t*>(&stage[b][0][4 * g + i][so]);
+                    dg[i] = __fmul_rn(d6g[i], static_cast<float>(static_cast<int8_t>(sg & 0xFFu)));
+                    mg[i] = __fmul_rn(d6g[i], static_cast<float>(static_cast<int8_t>(sg >> 8)));
+                    if (DUAL) {
+                        const uint32_t su = *reinterpret_cast<const uint16_t*>(&stage[b][NM - 1][4 * g + i][so]);
+                        du[i] = __fmul_rn(d6u[i], static_cast<float>(static_cast<int8_t>(su & 0xFFu)));
+                        mu[i] = __fmul_rn(d6u[i], static_cast<float>(static_cast<int8_t>(su >> 8)));
+                    }
                 } else {
                     dg[i] = static_cast<float>(*reinterpret_cast<const _Float16*>(&stage[b][0][4 * g + i][off]));
                     du[i] = DUAL ? static_cast<float>(*reinterpret_cast<const _Float16*>(&stage[b][NM - 1][4 * g + i][off]))
@@ -1123,6 +1188,31 @@ __global__ __launch_bounds__(64 * kMqWaves) void matvec_mfma_q(MatvecArgs a)
             if constexpr (KQ) {  // the four lane groups of the token hold the sub-block's four 8-value parts
                 xsum += __shfl_xor(xsum, 16);
                 xsum += __shfl_xor(xsum, 32);
+            }
+            if constexpr (K6) {
+                // Q6_K: lane groups 0-1 hold the block's first 16 values (scale dg), 2-3 the second (scale mg):
+                // one MFMA chain per half, the other half's codes masked to zero (a mask, not a select of
+                // vectors, which the compiler would lower to a stack array)
+                const uint32_t keep = g < 2 ? ~0u : 0u;
+                auto half = [&](const uint4& A, uint32_t k) { return make_uint4(A.x & k, A.y & k, A.z & k, A.w & k); };
+                const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int m = 0; m < NM; m++) {
+                    const uint4& A = m == 0 ? Ag : Au;
+                    const uint4 A0 = half(A, keep), A1 = half(A, ~keep);
+                    f32x4_t c0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(A0), as_bf16x8(Bh), zero, 0, 0, 0);
+                    f32x4_t c1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(A1), as_bf16x8(Bh), zero, 0, 0, 0);
+                    if (XF32) {
+                        c0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(A0), as_bf16x8(Bm), c0, 0, 0, 0);
+                        c1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(A1), as_bf16x8(Bm), c1, 0, 0, 0);
+                    }
+                    f32x4_t& acc = m == 0 ? ag : au;
+                    const float* s0 = m == 0 ? dg : du;
+                    const float* s1 = m == 0 ? mg : mu;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) acc[i] = fmaf(s1[i], c1[i], fmaf(s0[i], c0[i], acc[i]));
+                }
+                continue;
             }
             f32x4_t cg = {0.0f, 0.0f, 0.0f, 0.0f}, cu = {0.0f, 0.0f, 0.0f, 0.0f};
             cg = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(Ag), as_bf16x8(Bh), cg, 0, 0, 0);
@@ -1767,8 +1857,8 @@ static int launch_kq_tile(const MatvecArgs& a, hipStream_t st)
 // 52.1, 25.7 / 39.7; T = 3 57.2 / 52.7, 55.6 / 40.3; T = 16 218 / 58, - / 42; Q8_0 T = 3 58.3 / 57.4,
 // 56.6 / 45.7; T = 16 223 / 64.
 static int mq_min_tokens() { return env_int("SLHIP_MATVEC_MQ_MIN_T", 3); }
-// The same for Q4_K (SLHIP_MATVEC_KQ_MIN_T): its VALU kernel takes four tokens per pass, so the matrix cores
-// pay from five. Measured dual at [14336, 4096], f32 x (us, VALU / matrix cores): T = 4 57.6 / 75.2;
+// The same for Q4_K and Q6_K (SLHIP_MATVEC_KQ_MIN_T): their VALU kernel takes four tokens per pass, so the
+// matrix cores pay from five. Measured dual at [14336, 4096], f32 x (us, VALU / matrix cores): T = 4 57.6 / 75.2;
 // T = 16 229 / 82.
 static int kq_min_tokens() { return env_int("SLHIP_MATVEC_KQ_MIN_T", 5); }
 
@@ -1794,10 +1884,12 @@ static int run_mfma_q(MatvecArgs a, bool dual, hipStream_t st)
 template <int FMT>
 static int run_quant(MatvecArgs a, bool dual, hipStream_t st)
 {
-    if constexpr (FMT == SLHIP_FMT_Q4_0 || FMT == SLHIP_FMT_Q8_0 || FMT == SLHIP_FMT_Q4_K) {
-        // several tokens: the matrix-core kernel, when K splits into whole stages
-        const int mt = FMT == SLHIP_FMT_Q4_K ? kq_min_tokens() : mq_min_tokens();
-        if (mt > 0 && a.T >= mt && a.K % (MqGeom<FMT>::SKB * 32) == 0) return run_mfma_q<FMT>(a, dual, st);
+    if constexpr (FMT == SLHIP_FMT_Q4_0 || FMT == SLHIP_FMT_Q8_0 || FMT == SLHIP_FMT_Q4_K || FMT == SLHIP_FMT_Q6_K) {
+        // several tokens: the matrix-core kernel, when K splits into whole stages (and the rows into its loads)
+        const int mt = Fmt<FMT>::K ? kq_min_tokens() : mq_min_tokens();
+        const uintptr_t al = reinterpret_cast<uintptr_t>(a.wg) | reinterpret_cast<uintptr_t>(a.wu);
+        if (mt > 0 && a.T >= mt && a.K % (MqGeom<FMT>::SKB * 32) == 0 && al % MqGeom<FMT>::UB == 0)
+            return run_mfma_q<FMT>(a, dual, st);
     }
     if constexpr (FMT == SLHIP_FMT_Q4_K || FMT == SLHIP_FMT_Q6_K) {
         // one token: the matrix-core kernel, when K splits into whole segments and its LDS fits

@@ -148,6 +148,9 @@ SINGLE_CASES = [  # (fmt, x dtype, y dtype, T, K, N)
     ("q4_k", "bf16", "bf16", 16, 4096, 50),
     ("q4_k", "f32", "bf16", 17, 2048, 40),   # two token groups, the second of one token
     ("q4_k", "f32", "f32", 4, 1280, 24),     # K not a whole number of 1024-value stages: the VALU kernel
+    ("q6_k", "f32", "f32", 5, 1024, 33),     # Q6_K from five tokens on the matrix cores: one 840-byte stage
+    ("q6_k", "bf16", "bf16", 16, 4096, 50),
+    ("q6_k", "f32", "bf16", 17, 3072, 40),   # two token groups, the second of one token; three stages
 ]
 
 
@@ -213,6 +216,8 @@ DUAL_CASES = [  # (act, fmt, x dtype, y dtype, T, K, N): FusionTests.SwiGluDualM
     ("silu", "q4_k", "f32", "f32", 16, 4096, 14336),  # batched Q4_K_M decode FFN on the matrix cores
     ("gelu_erf", "q4_k", "bf16", "bf16", 6, 1024, 72),
     ("silu", "q4_k", "f32", "f32", 4, 1024, 40),       # four tokens: still the VALU kernel
+    ("silu", "q6_k", "f32", "f32", 16, 4096, 14336),  # batched decode with Q6_K weights on the matrix cores
+    ("gelu_tanh", "q6_k", "bf16", "f32", 8, 2048, 40),
 ]
 
 
@@ -399,7 +404,7 @@ def test_q4k_several_tokens_wide_range_and_zero_rows(device):
     _check_single(y, "f32", oracle.matvec("q4_k", raw, N, K, x), S, "q4_k several tokens, wide x")
 
 
-@pytest.mark.parametrize("T", [1, 3])
+@pytest.mark.parametrize("T", [1, 3, 6])
 @pytest.mark.parametrize("dual", [False, True])
 def test_q6k_codes_near_32_with_offset_x(device, dual, T):
     """Q6_K's -32 is applied to the sums of x over each 16-value half (sum x q - 32 sum x, the decomposition of
