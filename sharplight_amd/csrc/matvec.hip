@@ -918,7 +918,10 @@ __global__ __launch_bounds__(64 * kMmWaves) void matvec_mfma_lds(MatvecArgs a)
 // takes the same path with its 32-value sub-blocks as the blocks (a stage is 4 super-blocks, 576 bytes of a
 // row, and a wave half a super-block): codes q enter as they are, and the sub-block's d0 = d sc and minimum
 // m = dmin mn are applied on the VALU as acc += d0 sum(q x) - m sum(x), sum(x) of the lane's token summed
-// across its four lane groups (Quant.cs:518-545's value d0 q - m). A block
+// across its four lane groups (Quant.cs:518-545's value d0 q - m). Q6_K too (a stage is 2 super-blocks, 420
+// bytes staged with 4-byte loads, and a wave a quarter super-block): codes enter as q - 32, and since a
+// 32-value block holds two 16-value scale groups, each block takes two MFMA chains, lane groups 0-1 (the
+// first group's values) in one and 2-3 in the other, the other half's codes masked to zero. A block
 // of 8 waves takes one tile; the waves split each stage's blocks; the stage's row bytes are loaded two stages
 // ahead into registers and written to LDS one stage ahead (as the bf16 kernel above); partial sums meet in
 // LDS at the end.
@@ -928,7 +931,7 @@ constexpr int kMqWaves = 8;
 template <> struct MqGeom<SLHIP_FMT_Q4_0> { static constexpr int SKB = 32, RB = 32 * 18, UB = 16; };
 template <> struct MqGeom<SLHIP_FMT_Q8_0> { static constexpr int SKB = 16, RB = 16 * 34, UB = 16; };
 template <> struct MqGeom<SLHIP_FMT_Q4_K> { static constexpr int SKB = 32, RB = 4 * 144, UB = 16; };  // 4 super-blocks
-template <> struct MqGeom<SLHIP_FMT_Q6_K> { static constexpr int SKB = 32, RB = 4 * 210, UB = 8; };   // 840 bytes
+template <> struct MqGeom<SLHIP_FMT_Q6_K> { static constexpr int SKB = 16, RB = 2 * 210, UB = 4; };   // 420 bytes
 
 // Eight codes of lane group g (values 8g .. 8g + 7 of the block) as four bf16 pairs; row: the row's stage
 // bytes (4-byte aligned), off: the block's first byte in it.
@@ -1038,14 +1041,15 @@ __global__ __launch_bounds__(64 * kMqWaves) void matvec_mfma_q(MatvecArgs a)
     constexpr bool K6 = FMT == SLHIP_FMT_Q6_K;
     constexpr int RB = MqGeom<FMT>::RB;  // bytes of one row per stage
     constexpr int UB = MqGeom<FMT>::UB;  // bytes per staging load
-    using WU = std::conditional_t<UB == 16, uint4, uint2>;
+    using WU = std::conditional_t<UB == 16, uint4, std::conditional_t<UB == 8, uint2, uint32_t>>;
     constexpr int PITCH = RB + 16;
     constexpr int UPR = RB / UB;  // staging units of a row per stage
     constexpr int UNITS = NM * 16 * UPR;
     constexpr int UPL = (UNITS + 64 * kMqWaves - 1) / (64 * kMqWaves);
     constexpr int BPW = SKB / kMqWaves;  // blocks per wave and stage
-    static_assert(RB % UB == 0 && PITCH % 8 == 0 && SKB % kMqWaves == 0, "stage shape");
-    static_assert(!(KQ || K6) || BPW == 4, "a K-quant wave takes half a super-block per stage");
+    static_assert(RB % UB == 0 && PITCH % UB == 0 && SKB % kMqWaves == 0, "stage shape");
+    static_assert(!(KQ || K6) || 8 % BPW == 0, "a K-quant wave takes whole blocks of one super-block");
+    static_assert(!KQ || BPW == 4, "a Q4_K wave takes the four sub-blocks of one packed scale word");
     __shared__ __align__(16) uint8_t stage[2][NM][16][PITCH];
     const int lane = threadIdx.x & 63;
     const int wave = wave_id();
@@ -1075,9 +1079,11 @@ __global__ __launch_bounds__(64 * kMqWaves) void matvec_mfma_q(MatvecArgs a)
             const char* p = src[i] + static_cast<int64_t>(s) * RB;
             if constexpr (UB == 16) {
                 pw[i] = load_nt(p);
-            } else {
+            } else if constexpr (UB == 8) {
                 const u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
                 pw[i] = make_uint2(v.x, v.y);
+            } else {
+                pw[i] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
             }
         }
     };
@@ -1111,11 +1117,17 @@ __global__ __launch_bounds__(64 * kMqWaves) void matvec_mfma_q(MatvecArgs a)
         if (s + 1 < ns) fetch_x(xn, s + 1);  // block-uniform conditions
         if (s + 2 < ns) fetch_w(wfree, s + 2);
         __builtin_amdgcn_sched_barrier(0);
-        // Q4_K: the wave's half super-block (sub-blocks 4 (wave & 1) ..) and the headers of the rows its sums
-        // belong to (4g .. 4g + 3), read once per stage. (Decoding the (d0, m) pairs once per wave into an LDS
-        // table instead cost a block of residency per CU: 82 -> 116 us at 16 tokens.)
-        const int sbo = KQ ? (wave >> 1) * 144 : K6 ? (wave >> 1) * 210 : 0;
-        uint4 hg[4], hu[4];
+        // Q4_K: the wave's half super-block (sub-blocks 4 (wave & 1) ..); the headers of the rows its sums
+        // belong to (4g .. 4g + 3) are read once per stage. (Decoding the (d0, m) pairs once per wave into an
+        // LDS table instead cost a block of residency per CU: 82 -> 116 us at 16 tokens.)
+        // K-quants: the wave's blocks u0 .. u0 + BPW - 1 of the stage's super-block (wave BPW) / 8
+        const int u0 = (wave * BPW) & 7;
+        const int sbo = KQ ? ((wave * BPW) >> 3) * 144 : K6 ? ((wave * BPW) >> 3) * 210 : 0;
+        // Q4_K: per row 4g + i its d, dmin and the packed 6-bit scales and minima of the wave's four sub-blocks
+        // (byte j of scw / mnw: sub-block u0 + j; Quant.cs:518-545's packing), so that a sub-block's d0 and m
+        // are one byte conversion and one multiply each
+        float kdg[4], kmg[4], kdu[4], kmu[4];
+        uint32_t scg[4], mng[4], scu[4], mnu[4];
         float d6g[4], d6u[4];  // Q6_K: the super-block scale d of the rows 4g + i
         if constexpr (K6) {
 #pragma unroll
@@ -1126,23 +1138,35 @@ __global__ __launch_bounds__(64 * kMqWaves) void matvec_mfma_q(MatvecArgs a)
             }
         }
         if constexpr (KQ) {
+            auto words = [&](const uint4& h, float& d, float& dm, uint32_t& sc, uint32_t& mn) {
+                d = f16_lo(h.x);
+                dm = f16_hi(h.x);
+                if (u0 < 4) {  // sub-blocks 0-3: the low 6 bits of bytes 4..7 (scales) and 8..11 (minima)
+                    sc = h.y & 0x3F3F3F3Fu;
+                    mn = h.z & 0x3F3F3F3Fu;
+                } else {  // 4-7: low / high nibbles of bytes 12..15, top two bits of bytes 4..11
+                    sc = (h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u);
+                    mn = ((h.w >> 4) & 0x0F0F0F0Fu) | ((h.z >> 2) & 0x30303030u);
+                }
+            };
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                hg[i] = *reinterpret_cast<const uint4*>(&stage[b][0][4 * g + i][sbo]);
-                hu[i] = DUAL ? *reinterpret_cast<const uint4*>(&stage[b][NM - 1][4 * g + i][sbo]) : hg[i];
+                words(*reinterpret_cast<const uint4*>(&stage[b][0][4 * g + i][sbo]), kdg[i], kmg[i], scg[i], mng[i]);
+                if (DUAL)
+                    words(*reinterpret_cast<const uint4*>(&stage[b][NM - 1][4 * g + i][sbo]), kdu[i], kmu[i], scu[i], mnu[i]);
             }
         }
 #pragma unroll
         for (int j = 0; j < BPW; j++) {
             const int off = (wave * BPW + j) * BB;
-            const int sj = KQ ? 4 * (wave & 1) + j : 0;  // Q4_K sub-block
+            const int sj = u0 + j;  // K-quant block (Q4_K sub-block, Q6_K 32-value quarter-half) in its super-block
             uint4 Ag, Au;
             if constexpr (KQ) {
                 Ag = q4k_codes(&stage[b][0][r][0], sbo, sj, g);
                 Au = DUAL ? q4k_codes(&stage[b][NM - 1][r][0], sbo, sj, g) : Ag;
             } else if constexpr (K6) {
-                Ag = q6k_codes(&stage[b][0][r][0], sbo, 4 * (wave & 1) + j, g);
-                Au = DUAL ? q6k_codes(&stage[b][NM - 1][r][0], sbo, 4 * (wave & 1) + j, g) : Ag;
+                Ag = q6k_codes(&stage[b][0][r][0], sbo, sj, g);
+                Au = DUAL ? q6k_codes(&stage[b][NM - 1][r][0], sbo, sj, g) : Ag;
             } else {
                 Ag = mq_codes<FMT>(&stage[b][0][r][0], off, g);
                 Au = DUAL ? mq_codes<FMT>(&stage[b][NM - 1][r][0], off, g) : Ag;
@@ -1151,11 +1175,16 @@ __global__ __launch_bounds__(64 * kMqWaves) void matvec_mfma_q(MatvecArgs a)
 #pragma unroll
             for (int i = 0; i < 4; i++) {  // the scales of the rows this lane's sums belong to (4g .. 4g + 3)
                 if constexpr (KQ) {
-                    q4k_scales(hg[i], sj, dg[i], mg[i]);
-                    if (DUAL) q4k_scales(hu[i], sj, du[i], mu[i]);
+                    const uint32_t sh = 8 * static_cast<uint32_t>(j);  // byte j: sub-block u0 + j
+                    dg[i] = __fmul_rn(kdg[i], static_cast<float>((scg[i] >> sh) & 0xFFu));
+                    mg[i] = __fmul_rn(kmg[i], static_cast<float>((mng[i] >> sh) & 0xFFu));
+                    if (DUAL) {
+                        du[i] = __fmul_rn(kdu[i], static_cast<float>((scu[i] >> sh) & 0xFFu));
+                        mu[i] = __fmul_rn(kmu[i], static_cast<float>((mnu[i] >> sh) & 0xFFu));
+                    }
                 } else if constexpr (K6) {
                     // the block's two 16-value scales sc[8 hf + 2k + 0..1] (2-byte aligned): d sc as (dg, mg)
-                    const int so = sbo + 192 + 2 * (4 * (wave & 1) + j);
+                    const int so = sbo + 192 + 2 * sj;
                     const uint32_t sg = *reinterpret_cast<const uint16_t*>(&stage[b][0][4 * g + i][so]);
                     dg[i] = __fmul_rn(d6g[i], static_cast<float>(static_cast<int8_t>(sg & 0xFFu)));
                     mg[i] = __fmul_rn(d6g[i], static_cast<float>(static_cast<int8_t>(sg >> 8)));
