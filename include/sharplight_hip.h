@@ -260,8 +260,8 @@ SLHIP_API int slhip_rownorm_copies(int kind, int dtype_in, int dtype_out, const 
  * VALU kernel) and K a multiple of 64 go to the matrix cores with f32 x split exactly into three bf16 parts:
  * the same products, summed in another order, under the same bound. Q4_K and Q6_K at T = 1 (K a multiple of
  * 4096 for Q4_K, 2048 for Q6_K) go to the integer matrix cores: x represented to 2^(e-28) of its 32-value
- * block's largest power of two, the code sums exact, under the same bound. Q4_0 and Q8_0 from
- * SLHIP_MATVEC_MQ_MIN_T tokens (default 3), Q4_K and Q6_K from SLHIP_MATVEC_KQ_MIN_T (default 5), with K a
+ * block's largest power of two, the code sums exact, under the same bound. Q8_0/Q4_0/Q4_1/Q5_0/Q5_1 from
+ * SLHIP_MATVEC_MQ_MIN_T tokens (default 3), Q4_K/Q5_K/Q6_K from SLHIP_MATVEC_KQ_MIN_T (default 5), with K a
  * multiple of 1024 (Q6_K: 512), go to the matrix cores as exact bf16 codes (Q4_0 q - 8, Q6_K q - 32) against
  * x in two bf16 parts (|x - h - m| <= 2^-18 |x|), 16 tokens per launch, block scales (and the K-quants'
  * minima, scales per 16 values) applied per block in f32: the same bound.

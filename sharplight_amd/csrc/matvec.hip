@@ -930,30 +930,55 @@ constexpr int kMqWaves = 8;
 // SKB: 32-value blocks per stage, RB: bytes of one row per stage, UB: bytes per staging load
 template <> struct MqGeom<SLHIP_FMT_Q4_0> { static constexpr int SKB = 32, RB = 32 * 18, UB = 16; };
 template <> struct MqGeom<SLHIP_FMT_Q8_0> { static constexpr int SKB = 16, RB = 16 * 34, UB = 16; };
+template <> struct MqGeom<SLHIP_FMT_Q4_1> { static constexpr int SKB = 32, RB = 32 * 20, UB = 16; };
+template <> struct MqGeom<SLHIP_FMT_Q5_0> { static constexpr int SKB = 32, RB = 32 * 22, UB = 16; };
+template <> struct MqGeom<SLHIP_FMT_Q5_1> { static constexpr int SKB = 32, RB = 32 * 24, UB = 16; };
 template <> struct MqGeom<SLHIP_FMT_Q4_K> { static constexpr int SKB = 32, RB = 4 * 144, UB = 16; };  // 4 super-blocks
+template <> struct MqGeom<SLHIP_FMT_Q5_K> { static constexpr int SKB = 32, RB = 4 * 176, UB = 16; };
 template <> struct MqGeom<SLHIP_FMT_Q6_K> { static constexpr int SKB = 16, RB = 2 * 210, UB = 4; };   // 420 bytes
 
-// Eight codes of lane group g (values 8g .. 8g + 7 of the block) as four bf16 pairs; row: the row's stage
-// bytes (4-byte aligned), off: the block's first byte in it.
+// Eight codes of lane group g (values 8g .. 8g + 7 of the block) as four bf16 pairs, the format's offset
+// applied (Q4_0 q - 8, Q5_0 q - 16: exact); row: the row's stage bytes (4-byte aligned), off: the block's
+// first byte in it. Layouts of Quant.cs:242-405: {f16 d, [f16 m], [u32 qh], qs}, value v the low (v < 16) or
+// high nibble of qs[v % 16], plus 16 when bit v of qh is set (Q5_0, Q5_1); Q8_0 int8 codes.
 template <int FMT>
 __device__ __forceinline__ uint4 mq_codes(const uint8_t* row, int off, int g)
 {
-    // the eight code bytes at off + 2 + (Q4_0: 8 (g & 1); Q8_0: 8 g), 2-byte aligned: three aligned words
-    // and a funnel shift (the row pointer is used as it is, so the reads stay LDS reads)
-    const int q = off + 2 + (FMT == SLHIP_FMT_Q4_0 ? 8 * (g & 1) : 8 * g);
-    const uint32_t* w = reinterpret_cast<const uint32_t*>(row) + (q >> 2);
-    const uint32_t sh = static_cast<uint32_t>(q & 3) * 8;
-    const uint32_t w0 = w[0], w1 = w[1], w2 = w[2];
-    uint32_t lo = __builtin_amdgcn_alignbit(w1, w0, sh), hi = __builtin_amdgcn_alignbit(w2, w1, sh);
+    using F = Fmt<FMT>;
+    constexpr bool NIB = FMT != SLHIP_FMT_Q8_0;
+    // the eight code bytes at off + QS + (nibble formats: 8 (g & 1); Q8_0: 8 g), 2-byte aligned: three
+    // aligned words and a funnel shift (the row pointer is used as it is, so the reads stay LDS reads)
+    const int q = off + F::QS + (NIB ? 8 * (g & 1) : 8 * g);
+    auto words = [&](int p, uint32_t& a, uint32_t& b) {
+        const uint32_t* w = reinterpret_cast<const uint32_t*>(row) + (p >> 2);
+        const uint32_t sh = static_cast<uint32_t>(p & 3) * 8;
+        const uint32_t w0 = w[0], w1 = w[1], w2 = w[2];
+        a = __builtin_amdgcn_alignbit(w1, w0, sh);
+        b = __builtin_amdgcn_alignbit(w2, w1, sh);
+    };
+    uint32_t lo, hi;
+    words(q, lo, hi);
     float f[8];
-    if constexpr (FMT == SLHIP_FMT_Q4_0) {  // low nibbles (g < 2: values 0-15) or high (values 16-31)
+    if constexpr (NIB) {  // low nibbles (g < 2: values 0-15) or high (values 16-31)
         const uint32_t s = 4 * static_cast<uint32_t>(g >> 1);
         lo = (lo >> s) & 0x0F0F0F0Fu;
         hi = (hi >> s) & 0x0F0F0F0Fu;
+        if constexpr (F::QH >= 0) {  // bits 8g .. 8g + 7 of qh, one per value, to bit 4 of its byte
+            uint32_t qh, unused;
+            words(off + F::QH, qh, unused);
+            const uint32_t hb = (qh >> (8 * g)) & 0xFFu;
+            // spread the 8 bits to bit 4 of 8 bytes: bit e -> byte e
+            const uint32_t b0 = hb & 0x0Fu, b1 = hb >> 4;
+            auto spread = [](uint32_t n) {  // 4 bits -> bit 4 of 4 bytes
+                return ((n & 1u) << 4) | ((n & 2u) << 11) | ((n & 4u) << 18) | ((n & 8u) << 25);
+            };
+            lo |= spread(b0);
+            hi |= spread(b1);
+        }
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            f[e] = static_cast<float>((lo >> (8 * e)) & 0xFFu) - 8.0f;
-            f[4 + e] = static_cast<float>((hi >> (8 * e)) & 0xFFu) - 8.0f;
+            f[e] = static_cast<float>((lo >> (8 * e)) & 0xFFu) + static_cast<float>(F::OFF);
+            f[4 + e] = static_cast<float>((hi >> (8 * e)) & 0xFFu) + static_cast<float>(F::OFF);
         }
     } else {  // int8 codes: q + 128 as an unsigned byte, then exact f32 arithmetic
         lo ^= 0x80808080u;
@@ -970,11 +995,19 @@ __device__ __forceinline__ uint4 mq_codes(const uint8_t* row, int off, int g)
 // Eight Q4_K codes of lane group g (values 8g .. 8g + 7 of sub-block j: the low (j even) or high nibbles of
 // bytes 32 (j / 2) + 8g .. of the super-block's 128 code bytes, Quant.cs:518-545) as four bf16 pairs; sbo: the
 // super-block's first byte in the staged row (a multiple of 16), so the eight bytes are one aligned 8-byte read.
+// Q5_K (FIVE): the codes after a 32-byte qh at byte 16, and value l of sub-block j adds 16 when bit j of qh[l]
+// is set (ggml's Q5_K layout, the same scale packing as Q4_K).
+template <bool FIVE = false>
 __device__ __forceinline__ uint4 q4k_codes(const uint8_t* row, int sbo, int j, int g)
 {
-    const uint2 w = *reinterpret_cast<const uint2*>(row + sbo + 16 + 32 * (j >> 1) + 8 * g);
+    const uint2 w = *reinterpret_cast<const uint2*>(row + sbo + (FIVE ? 48 : 16) + 32 * (j >> 1) + 8 * g);
     const uint32_t sh = 4 * static_cast<uint32_t>(j & 1);
-    const uint32_t lo = (w.x >> sh) & 0x0F0F0F0Fu, hi = (w.y >> sh) & 0x0F0F0F0Fu;
+    uint32_t lo = (w.x >> sh) & 0x0F0F0F0Fu, hi = (w.y >> sh) & 0x0F0F0F0Fu;
+    if constexpr (FIVE) {
+        const uint2 h = *reinterpret_cast<const uint2*>(row + sbo + 16 + 8 * g);
+        lo |= ((h.x >> j) & 0x01010101u) << 4;
+        hi |= ((h.y >> j) & 0x01010101u) << 4;
+    }
     float f[8];
 #pragma unroll
     for (int e = 0; e < 4; e++) {
@@ -1037,8 +1070,10 @@ __global__ __launch_bounds__(64 * kMqWaves) void matvec_mfma_q(MatvecArgs a)
     constexpr int BB = Fmt<FMT>::BB;
     constexpr int NM = DUAL ? 2 : 1;
     constexpr int SKB = MqGeom<FMT>::SKB;
-    constexpr bool KQ = FMT == SLHIP_FMT_Q4_K;
+    constexpr bool KQ = FMT == SLHIP_FMT_Q4_K || FMT == SLHIP_FMT_Q5_K;  // 8 sub-blocks, d0 q - m
     constexpr bool K6 = FMT == SLHIP_FMT_Q6_K;
+    constexpr bool MB = Fmt<FMT>::M && !Fmt<FMT>::K;  // Q4_1, Q5_1: d q + m per 32-value block
+    constexpr int SBB = KQ ? Fmt<FMT>::BB : 210;       // K-quant super-block bytes
     constexpr int RB = MqGeom<FMT>::RB;  // bytes of one row per stage
     constexpr int UB = MqGeom<FMT>::UB;  // bytes per staging load
     using WU = std::conditional_t<UB == 16, uint4, std::conditional_t<UB == 8, uint2, uint32_t>>;
@@ -1122,7 +1157,7 @@ __global__ __launch_bounds__(64 * kMqWaves) void matvec_mfma_q(MatvecArgs a)
         // LDS table instead cost a block of residency per CU: 82 -> 116 us at 16 tokens.)
         // K-quants: the wave's blocks u0 .. u0 + BPW - 1 of the stage's super-block (wave BPW) / 8
         const int u0 = (wave * BPW) & 7;
-        const int sbo = KQ ? ((wave * BPW) >> 3) * 144 : K6 ? ((wave * BPW) >> 3) * 210 : 0;
+        const int sbo = (KQ || K6) ? ((wave * BPW) >> 3) * SBB : 0;
         // Q4_K: per row 4g + i its d, dmin and the packed 6-bit scales and minima of the wave's four sub-blocks
         // (byte j of scw / mnw: sub-block u0 + j; Quant.cs:518-545's packing), so that a sub-block's d0 and m
         // are one byte conversion and one multiply each
@@ -1162,8 +1197,9 @@ __global__ __launch_bounds__(64 * kMqWaves) void matvec_mfma_q(MatvecArgs a)
             const int sj = u0 + j;  // K-quant block (Q4_K sub-block, Q6_K 32-value quarter-half) in its super-block
             uint4 Ag, Au;
             if constexpr (KQ) {
-                Ag = q4k_codes(&stage[b][0][r][0], sbo, sj, g);
-                Au = DUAL ? q4k_codes(&stage[b][NM - 1][r][0], sbo, sj, g) : Ag;
+                constexpr bool FIVE = FMT == SLHIP_FMT_Q5_K;
+                Ag = q4k_codes<FIVE>(&stage[b][0][r][0], sbo, sj, g);
+                Au = DUAL ? q4k_codes<FIVE>(&stage[b][NM - 1][r][0], sbo, sj, g) : Ag;
             } else if constexpr (K6) {
                 Ag = q6k_codes(&stage[b][0][r][0], sbo, sj, g);
                 Au = DUAL ? q6k_codes(&stage[b][NM - 1][r][0], sbo, sj, g) : Ag;
@@ -1197,6 +1233,11 @@ __global__ __launch_bounds__(64 * kMqWaves) void matvec_mfma_q(MatvecArgs a)
                     dg[i] = static_cast<float>(*reinterpret_cast<const _Float16*>(&stage[b][0][4 * g + i][off]));
                     du[i] = DUAL ? static_cast<float>(*reinterpret_cast<const _Float16*>(&stage[b][NM - 1][4 * g + i][off]))
                                  : 0.0f;
+                    if constexpr (MB) {  // the block minimum m (f16 after d)
+                        mg[i] = static_cast<float>(*reinterpret_cast<const _Float16*>(&stage[b][0][4 * g + i][off + 2]));
+                        mu[i] = DUAL ? static_cast<float>(*reinterpret_cast<const _Float16*>(&stage[b][NM - 1][4 * g + i][off + 2]))
+                                     : 0.0f;
+                    }
                 }
             }
             uint4 Bh, Bm;
@@ -1205,16 +1246,16 @@ __global__ __launch_bounds__(64 * kMqWaves) void matvec_mfma_q(MatvecArgs a)
                 const float v[8] = {xc.f[j][0].x, xc.f[j][0].y, xc.f[j][0].z, xc.f[j][0].w,
                                     xc.f[j][1].x, xc.f[j][1].y, xc.f[j][1].z, xc.f[j][1].w};
                 split2(v, Bh, Bm);
-                if constexpr (KQ) xsum = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+                if constexpr (KQ || MB) xsum = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
             } else {
                 Bh = xc.b[j];
-                if constexpr (KQ) {
+                if constexpr (KQ || MB) {
                     const uint4& w = xc.b[j];
                     xsum = ((bf16_lo(w.x) + bf16_hi(w.x)) + (bf16_lo(w.y) + bf16_hi(w.y))) +
                            ((bf16_lo(w.z) + bf16_hi(w.z)) + (bf16_lo(w.w) + bf16_hi(w.w)));
                 }
             }
-            if constexpr (KQ) {  // the four lane groups of the token hold the sub-block's four 8-value parts
+            if constexpr (KQ || MB) {  // the four lane groups of the token hold the block's four 8-value parts
                 xsum += __shfl_xor(xsum, 16);
                 xsum += __shfl_xor(xsum, 32);
             }
@@ -1254,9 +1295,13 @@ __global__ __launch_bounds__(64 * kMqWaves) void matvec_mfma_q(MatvecArgs a)
             for (int i = 0; i < 4; i++) {
                 ag[i] = fmaf(dg[i], cg[i], ag[i]);
                 if (DUAL) au[i] = fmaf(du[i], cu[i], au[i]);
-                if constexpr (KQ) {  // Q4_K: d0 sum(q x) - m sum(x)
+                if constexpr (KQ) {  // Q4_K, Q5_K: d0 sum(q x) - m sum(x)
                     ag[i] = fmaf(-mg[i], xsum, ag[i]);
                     if (DUAL) au[i] = fmaf(-mu[i], xsum, au[i]);
+                }
+                if constexpr (MB) {  // Q4_1, Q5_1: d sum(q x) + m sum(x)
+                    ag[i] = fmaf(mg[i], xsum, ag[i]);
+                    if (DUAL) au[i] = fmaf(mu[i], xsum, au[i]);
                 }
             }
         }
@@ -1886,8 +1931,8 @@ static int launch_kq_tile(const MatvecArgs& a, hipStream_t st)
 // 52.1, 25.7 / 39.7; T = 3 57.2 / 52.7, 55.6 / 40.3; T = 16 218 / 58, - / 42; Q8_0 T = 3 58.3 / 57.4,
 // 56.6 / 45.7; T = 16 223 / 64.
 static int mq_min_tokens() { return env_int("SLHIP_MATVEC_MQ_MIN_T", 3); }
-// The same for Q4_K and Q6_K (SLHIP_MATVEC_KQ_MIN_T): their VALU kernel takes four tokens per pass, so the
-// matrix cores pay from five. Measured dual at [14336, 4096], f32 x (us, VALU / matrix cores): T = 4 57.6 / 75.2;
+// The same for Q4_K, Q5_K and Q6_K (SLHIP_MATVEC_KQ_MIN_T): their VALU kernel takes four tokens per pass, so
+// the matrix cores pay from five. (Q4_1, Q5_0 and Q5_1 follow Q4_0's SLHIP_MATVEC_MQ_MIN_T.) Measured dual at [14336, 4096], f32 x (us, VALU / matrix cores): T = 4 57.6 / 75.2;
 // T = 16 229 / 82.
 static int kq_min_tokens() { return env_int("SLHIP_MATVEC_KQ_MIN_T", 5); }
 
@@ -1913,7 +1958,8 @@ static int run_mfma_q(MatvecArgs a, bool dual, hipStream_t st)
 template <int FMT>
 static int run_quant(MatvecArgs a, bool dual, hipStream_t st)
 {
-    if constexpr (FMT == SLHIP_FMT_Q4_0 || FMT == SLHIP_FMT_Q8_0 || FMT == SLHIP_FMT_Q4_K || FMT == SLHIP_FMT_Q6_K) {
+    if constexpr (FMT == SLHIP_FMT_Q4_0 || FMT == SLHIP_FMT_Q8_0 || FMT == SLHIP_FMT_Q4_1 || FMT == SLHIP_FMT_Q5_0 ||
+                  FMT == SLHIP_FMT_Q5_1 || FMT == SLHIP_FMT_Q4_K || FMT == SLHIP_FMT_Q5_K || FMT == SLHIP_FMT_Q6_K) {
         // several tokens: the matrix-core kernel, when K splits into whole stages (and the rows into its loads)
         const int mt = Fmt<FMT>::K ? kq_min_tokens() : mq_min_tokens();
         const uintptr_t al = reinterpret_cast<uintptr_t>(a.wg) | reinterpret_cast<uintptr_t>(a.wu);

@@ -151,6 +151,11 @@ SINGLE_CASES = [  # (fmt, x dtype, y dtype, T, K, N)
     ("q6_k", "f32", "f32", 5, 1024, 33),     # Q6_K from five tokens on the matrix cores: one 840-byte stage
     ("q6_k", "bf16", "bf16", 16, 4096, 50),
     ("q6_k", "f32", "bf16", 17, 3072, 40),   # two token groups, the second of one token; three stages
+    ("q5_0", "f32", "f32", 6, 2048, 33),     # the other block formats on the matrix cores (Q5: qh bits)
+    ("q4_1", "bf16", "f32", 16, 1024, 40),
+    ("q5_1", "f32", "bf16", 3, 3072, 24),
+    ("q5_k", "f32", "f32", 16, 4096, 40),
+    ("q5_k", "bf16", "bf16", 7, 1024, 17),
 ]
 
 
@@ -218,6 +223,9 @@ DUAL_CASES = [  # (act, fmt, x dtype, y dtype, T, K, N): FusionTests.SwiGluDualM
     ("silu", "q4_k", "f32", "f32", 4, 1024, 40),       # four tokens: still the VALU kernel
     ("silu", "q6_k", "f32", "f32", 16, 4096, 14336),  # batched decode with Q6_K weights on the matrix cores
     ("gelu_tanh", "q6_k", "bf16", "f32", 8, 2048, 40),
+    ("silu", "q5_k", "f32", "f32", 16, 4096, 14336),  # a Q5_K_M decode FFN at 16 tokens
+    ("silu", "q5_0", "f32", "f32", 16, 1024, 64),
+    ("gelu_erf", "q4_1", "bf16", "bf16", 5, 2048, 33),
 ]
 
 
