@@ -251,7 +251,8 @@ SLHIP_API int slhip_rownorm_copies(int kind, int dtype_in, int dtype_out, const 
  *   x: [T, K] f32 or bf16 (dtype_x), 16-byte aligned, row stride x_stride elements (a multiple of 8);
  *   W, Wg, Wu: N rows of K weights in `fmt`, 16-byte aligned: dense F32/F16/BF16 (K a multiple of 8,
  *   K <= 16384), or the GGUF block formats Q8_0/Q4_0/Q4_1/Q5_0/Q5_1 and Q4_K/Q5_K/Q6_K (K a multiple of
- *   256 and the rows' block images fitting in LDS); y: [T, N] f32 or bf16 (dtype_y), row stride y_stride.
+ *   256 and the rows' block images fitting in LDS), or Q2_K / Q3_K (K a multiple of 1024; the matrix cores
+ *   at every T); y: [T, N] f32 or bf16 (dtype_y), row stride y_stride.
  *   act: SLHIP_ACT_SILU / GELU_TANH / GELU_ERF, the same forms as slhip_gated_act.
  * Products and sums in f32 (in another order than the CPU provider's, so equal to it within the rounding of
  * a K-term f32 dot product); block formats sum d * sum(x q) + a * sum(x) per block, as the reference's

@@ -936,6 +936,8 @@ template <> struct MqGeom<SLHIP_FMT_Q5_1> { static constexpr int SKB = 32, RB = 
 template <> struct MqGeom<SLHIP_FMT_Q4_K> { static constexpr int SKB = 32, RB = 4 * 144, UB = 16; };  // 4 super-blocks
 template <> struct MqGeom<SLHIP_FMT_Q5_K> { static constexpr int SKB = 32, RB = 4 * 176, UB = 16; };
 template <> struct MqGeom<SLHIP_FMT_Q6_K> { static constexpr int SKB = 16, RB = 2 * 210, UB = 4; };   // 420 bytes
+template <> struct MqGeom<SLHIP_FMT_Q2_K> { static constexpr int SKB = 32, RB = 4 * 84, UB = 16; };   // 336 bytes
+template <> struct MqGeom<SLHIP_FMT_Q3_K> { static constexpr int SKB = 32, RB = 4 * 110, UB = 8; };   // 440 bytes
 
 // Eight codes of lane group g (values 8g .. 8g + 7 of the block) as four bf16 pairs, the format's offset
 // applied (Q4_0 q - 8, Q5_0 q - 16: exact); row: the row's stage bytes (4-byte aligned), off: the block's
@@ -1017,6 +1019,42 @@ __device__ __forceinline__ uint4 q4k_codes(const uint8_t* row, int sbo, int j, i
     return make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]), pack_bf16x2(f[6], f[7]));
 }
 
+// Eight bytes at LDS byte q of a 4-byte aligned row, q 2-byte aligned: three aligned words and a funnel shift.
+__device__ __forceinline__ uint2 lds_bytes8(const uint8_t* row, int q)
+{
+    const uint32_t* w = reinterpret_cast<const uint32_t*>(row) + (q >> 2);
+    const uint32_t sh = static_cast<uint32_t>(q & 3) * 8;
+    const uint32_t w0 = w[0], w1 = w[1], w2 = w[2];
+    return make_uint2(__builtin_amdgcn_alignbit(w1, w0, sh), __builtin_amdgcn_alignbit(w2, w1, sh));
+}
+
+// Eight Q2_K / Q3_K codes of lane group g for the 32-value block u = 4n + j of a super-block, as four bf16
+// pairs (Quant.KQuants.cs:36-107, ggml's layouts): value 128n + 32j + 8g + e has the 2-bit field 2j of byte
+// 32n + 8g + e of qs (Q2_K: qs at 16; Q3_K: qs at 32, plus 4 when bit 4n + j of hmask byte 8g + e is set,
+// minus 4). Lane groups 0-1 hold the block's first 16-value scale group, 2-3 the second.
+template <bool Q3>
+__device__ __forceinline__ uint4 q23k_codes(const uint8_t* row, int sbo, int u, int g)
+{
+    const int n = u >> 2, j = u & 3;
+    const uint2 l = lds_bytes8(row, sbo + (Q3 ? 32 : 16) + 32 * n + 8 * g);
+    const uint32_t sh = 2 * static_cast<uint32_t>(j);
+    uint32_t q0 = (l.x >> sh) & 0x03030303u, q1 = (l.y >> sh) & 0x03030303u;
+    if constexpr (Q3) {
+        const uint2 h = lds_bytes8(row, sbo + 8 * g);
+        const uint32_t hs = static_cast<uint32_t>(4 * n + j);
+        q0 |= ((h.x >> hs) & 0x01010101u) << 2;
+        q1 |= ((h.y >> hs) & 0x01010101u) << 2;
+    }
+    constexpr float OFF = Q3 ? -4.0f : 0.0f;
+    float f[8];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        f[e] = static_cast<float>((q0 >> (8 * e)) & 0xFFu) + OFF;
+        f[4 + e] = static_cast<float>((q1 >> (8 * e)) & 0xFFu) + OFF;
+    }
+    return make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]), pack_bf16x2(f[6], f[7]));
+}
+
 // Eight Q6_K codes q - 32 of lane group g: values l = 8g .. 8g + 7 of the 32-value block u = 4 hf + k of a
 // super-block {ql[128], qh[64], sc[16], f16 d}: q = (low (k < 2) or high nibble of ql[64 hf + 32 (k & 1) + l]) |
 // (bits 2k, 2k + 1 of qh[32 hf + l]) << 4 (ggml's Q6_K layout, Quant.KQuants.cs:36-107), as four bf16 pairs
@@ -1071,9 +1109,10 @@ __global__ __launch_bounds__(64 * kMqWaves) void matvec_mfma_q(MatvecArgs a)
     constexpr int NM = DUAL ? 2 : 1;
     constexpr int SKB = MqGeom<FMT>::SKB;
     constexpr bool KQ = FMT == SLHIP_FMT_Q4_K || FMT == SLHIP_FMT_Q5_K;  // 8 sub-blocks, d0 q - m
-    constexpr bool K6 = FMT == SLHIP_FMT_Q6_K;
+    constexpr bool Q2K = FMT == SLHIP_FMT_Q2_K, Q3K = FMT == SLHIP_FMT_Q3_K;
+    constexpr bool K6 = FMT == SLHIP_FMT_Q6_K || Q2K || Q3K;  // two 16-value scale groups per 32-value block
     constexpr bool MB = Fmt<FMT>::M && !Fmt<FMT>::K;  // Q4_1, Q5_1: d q + m per 32-value block
-    constexpr int SBB = KQ ? Fmt<FMT>::BB : 210;       // K-quant super-block bytes
+    constexpr int SBB = Fmt<FMT>::BB;                  // K-quant super-block bytes
     constexpr int RB = MqGeom<FMT>::RB;  // bytes of one row per stage
     constexpr int UB = MqGeom<FMT>::UB;  // bytes per staging load
     using WU = std::conditional_t<UB == 16, uint4, std::conditional_t<UB == 8, uint2, uint32_t>>;
@@ -1163,13 +1202,20 @@ __global__ __launch_bounds__(64 * kMqWaves) void matvec_mfma_q(MatvecArgs a)
         // are one byte conversion and one multiply each
         float kdg[4], kmg[4], kdu[4], kmu[4];
         uint32_t scg[4], mng[4], scu[4], mnu[4];
-        float d6g[4], d6u[4];  // Q6_K: the super-block scale d of the rows 4g + i
+        // Q6_K / Q3_K / Q2_K: the super-block scale d (Q2_K: and dmin) of the rows 4g + i
+        float d6g[4], d6u[4], n6g[4], n6u[4];
         if constexpr (K6) {
+            constexpr int DO = Q2K ? 80 : Q3K ? 108 : 208;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                d6g[i] = static_cast<float>(*reinterpret_cast<const _Float16*>(&stage[b][0][4 * g + i][sbo + 208]));
-                d6u[i] = DUAL ? static_cast<float>(*reinterpret_cast<const _Float16*>(&stage[b][NM - 1][4 * g + i][sbo + 208]))
+                d6g[i] = static_cast<float>(*reinterpret_cast<const _Float16*>(&stage[b][0][4 * g + i][sbo + DO]));
+                d6u[i] = DUAL ? static_cast<float>(*reinterpret_cast<const _Float16*>(&stage[b][NM - 1][4 * g + i][sbo + DO]))
                               : 0.0f;
+                if constexpr (Q2K) {
+                    n6g[i] = static_cast<float>(*reinterpret_cast<const _Float16*>(&stage[b][0][4 * g + i][sbo + 82]));
+                    n6u[i] = DUAL ? static_cast<float>(*reinterpret_cast<const _Float16*>(&stage[b][NM - 1][4 * g + i][sbo + 82]))
+                                  : 0.0f;
+                }
             }
         }
         if constexpr (KQ) {
@@ -1200,6 +1246,9 @@ __global__ __launch_bounds__(64 * kMqWaves) void matvec_mfma_q(MatvecArgs a)
                 constexpr bool FIVE = FMT == SLHIP_FMT_Q5_K;
                 Ag = q4k_codes<FIVE>(&stage[b][0][r][0], sbo, sj, g);
                 Au = DUAL ? q4k_codes<FIVE>(&stage[b][NM - 1][r][0], sbo, sj, g) : Ag;
+            } else if constexpr (Q2K || Q3K) {
+                Ag = q23k_codes<Q3K>(&stage[b][0][r][0], sbo, sj, g);
+                Au = DUAL ? q23k_codes<Q3K>(&stage[b][NM - 1][r][0], sbo, sj, g) : Ag;
             } else if constexpr (K6) {
                 Ag = q6k_codes(&stage[b][0][r][0], sbo, sj, g);
                 Au = DUAL ? q6k_codes(&stage[b][NM - 1][r][0], sbo, sj, g) : Ag;
@@ -1208,9 +1257,35 @@ __global__ __launch_bounds__(64 * kMqWaves) void matvec_mfma_q(MatvecArgs a)
                 Au = DUAL ? mq_codes<FMT>(&stage[b][NM - 1][r][0], off, g) : Ag;
             }
             float dg[4], du[4], mg[4], mu[4];
+            float ng0[4], ng1[4], nu0[4], nu1[4];  // Q2_K: the two halves' minima dmin * m
 #pragma unroll
             for (int i = 0; i < 4; i++) {  // the scales of the rows this lane's sums belong to (4g .. 4g + 3)
-                if constexpr (KQ) {
+                if constexpr (Q2K) {
+                    // scale bytes 8n + 2j + 0..1 (the block's two halves): d (low nibble), dmin (high nibble)
+                    auto sc2 = [&](const uint8_t* row, float d, float dm, float& s0, float& s1, float& m0, float& m1) {
+                        const uint32_t v = *reinterpret_cast<const uint16_t*>(row + sbo + 2 * sj);
+                        s0 = __fmul_rn(d, static_cast<float>(v & 0xFu));
+                        s1 = __fmul_rn(d, static_cast<float>((v >> 8) & 0xFu));
+                        m0 = __fmul_rn(dm, static_cast<float>((v >> 4) & 0xFu));
+                        m1 = __fmul_rn(dm, static_cast<float>(v >> 12));
+                    };
+                    sc2(&stage[b][0][4 * g + i][0], d6g[i], n6g[i], dg[i], mg[i], ng0[i], ng1[i]);
+                    if (DUAL) sc2(&stage[b][NM - 1][4 * g + i][0], d6u[i], n6u[i], du[i], mu[i], nu0[i], nu1[i]);
+                } else if constexpr (Q3K) {
+                    // 6-bit scales s = 8n + 2j + 0..1: low 4 bits from bytes 96 + 4 (w & 1) + b (the low nibble
+                    // for w < 2), high 2 from bits 2w of bytes 104 + b, w = s / 4, b = s % 4; d (s - 32)
+                    const int s0 = 2 * sj, w = s0 >> 2, b0 = s0 & 3;
+                    auto sc3 = [&](const uint8_t* row, float d, float& o0, float& o1) {
+                        const uint32_t a = *reinterpret_cast<const uint16_t*>(row + sbo + 96 + 4 * (w & 1) + b0);
+                        const uint32_t h = *reinterpret_cast<const uint16_t*>(row + sbo + 104 + b0);
+                        const uint32_t lo = w < 2 ? (a & 0x0F0Fu) : ((a >> 4) & 0x0F0Fu);
+                        const uint32_t sc = lo | (((h >> (2 * w)) & 0x0303u) << 4);
+                        o0 = __fmul_rn(d, static_cast<float>(static_cast<int>(sc & 0xFFu) - 32));
+                        o1 = __fmul_rn(d, static_cast<float>(static_cast<int>(sc >> 8) - 32));
+                    };
+                    sc3(&stage[b][0][4 * g + i][0], d6g[i], dg[i], mg[i]);
+                    if (DUAL) sc3(&stage[b][NM - 1][4 * g + i][0], d6u[i], du[i], mu[i]);
+                } else if constexpr (KQ) {
                     const uint32_t sh = 8 * static_cast<uint32_t>(j);  // byte j: sub-block u0 + j
                     dg[i] = __fmul_rn(kdg[i], static_cast<float>((scg[i] >> sh) & 0xFFu));
                     mg[i] = __fmul_rn(kmg[i], static_cast<float>((mng[i] >> sh) & 0xFFu));
@@ -1246,10 +1321,10 @@ __global__ __launch_bounds__(64 * kMqWaves) void matvec_mfma_q(MatvecArgs a)
                 const float v[8] = {xc.f[j][0].x, xc.f[j][0].y, xc.f[j][0].z, xc.f[j][0].w,
                                     xc.f[j][1].x, xc.f[j][1].y, xc.f[j][1].z, xc.f[j][1].w};
                 split2(v, Bh, Bm);
-                if constexpr (KQ || MB) xsum = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+                if constexpr (KQ || MB || Q2K) xsum = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
             } else {
                 Bh = xc.b[j];
-                if constexpr (KQ || MB) {
+                if constexpr (KQ || MB || Q2K) {
                     const uint4& w = xc.b[j];
                     xsum = ((bf16_lo(w.x) + bf16_hi(w.x)) + (bf16_lo(w.y) + bf16_hi(w.y))) +
                            ((bf16_lo(w.z) + bf16_hi(w.z)) + (bf16_lo(w.w) + bf16_hi(w.w)));
@@ -1259,8 +1334,15 @@ __global__ __launch_bounds__(64 * kMqWaves) void matvec_mfma_q(MatvecArgs a)
                 xsum += __shfl_xor(xsum, 16);
                 xsum += __shfl_xor(xsum, 32);
             }
+            float xh0 = 0.0f, xh1 = 0.0f;  // Q2_K: the token's x sums over the block's two 16-value halves
+            if constexpr (Q2K) {
+                const float p01 = xsum + __shfl_xor(xsum, 16);  // lane groups {0, 1} or {2, 3}
+                const float other = __shfl_xor(p01, 32);
+                xh0 = g < 2 ? p01 : other;
+                xh1 = g < 2 ? other : p01;
+            }
             if constexpr (K6) {
-                // Q6_K: lane groups 0-1 hold the block's first 16 values (scale dg), 2-3 the second (scale mg):
+                // Q6_K, Q3_K, Q2_K: lane groups 0-1 hold the block's first 16 values (scale dg), 2-3 the second (scale mg):
                 // one MFMA chain per half, the other half's codes masked to zero (a mask, not a select of
                 // vectors, which the compiler would lower to a stack array)
                 const uint32_t keep = g < 2 ? ~0u : 0u;
@@ -1281,6 +1363,12 @@ __global__ __launch_bounds__(64 * kMqWaves) void matvec_mfma_q(MatvecArgs a)
                     const float* s1 = m == 0 ? mg : mu;
 #pragma unroll
                     for (int i = 0; i < 4; i++) acc[i] = fmaf(s1[i], c1[i], fmaf(s0[i], c0[i], acc[i]));
+                    if constexpr (Q2K) {  // - dmin m per half times the half's x sum
+                        const float* n0 = m == 0 ? ng0 : nu0;
+                        const float* n1 = m == 0 ? ng1 : nu1;
+#pragma unroll
+                        for (int i = 0; i < 4; i++) acc[i] = fmaf(-n1[i], xh1, fmaf(-n0[i], xh0, acc[i]));
+                    }
                 }
                 continue;
             }
@@ -1832,6 +1920,8 @@ static QGeom quant_geom(int fmt)
     case SLHIP_FMT_Q4_K: return {256, 144};
     case SLHIP_FMT_Q5_K: return {256, 176};
     case SLHIP_FMT_Q6_K: return {256, 210};
+    case SLHIP_FMT_Q2_K: return {256, 84};
+    case SLHIP_FMT_Q3_K: return {256, 110};
     default: return {0, 0};
     }
 }
@@ -1986,6 +2076,18 @@ static int run_quant(MatvecArgs a, bool dual, hipStream_t st)
     return SLHIP_OK;
 }
 
+// Q2_K and Q3_K have no VALU kernel: every token count takes the matrix cores (K a multiple of 1024 and the
+// weights aligned to the stage's loads).
+template <int FMT>
+static int run_mfma_only(MatvecArgs a, bool dual, hipStream_t st)
+{
+    const uintptr_t al = reinterpret_cast<uintptr_t>(a.wg) | reinterpret_cast<uintptr_t>(a.wu);
+    if (a.K % (MqGeom<FMT>::SKB * 32) != 0 || al % MqGeom<FMT>::UB != 0)
+        return fail(SLHIP_ERR_UNSUPPORTED, "matvec: Q2_K / Q3_K weights need K a multiple of %d (K = %lld)",
+                    MqGeom<FMT>::SKB * 32, static_cast<long long>(a.K));
+    return run_mfma_q<FMT>(a, dual, st);
+}
+
 // Whether a (dual) matvec over rows of K values of `fmt` can run: for the block formats, whether one token's
 // staged x and the row images of a block's waves fit in LDS.
 bool matvec_fits(int fmt, int64_t K, bool dual)
@@ -1993,6 +2095,8 @@ bool matvec_fits(int fmt, int64_t K, bool dual)
     const QGeom qg = quant_geom(fmt);
     if (qg.bs == 0) return true;
     if (K % qg.bs != 0) return false;
+    if (fmt == SLHIP_FMT_Q2_K) return K % (MqGeom<SLHIP_FMT_Q2_K>::SKB * 32) == 0;  // matrix cores only
+    if (fmt == SLHIP_FMT_Q3_K) return K % (MqGeom<SLHIP_FMT_Q3_K>::SKB * 32) == 0;
     return quant_lds(1, K, K / qg.bs * qg.bb, dual) <= kMaxLds;
 }
 
@@ -2024,7 +2128,8 @@ static int matvec_common(int fmt, int dtype_x, int dtype_y, const void* x, int64
                     static_cast<long long>(K));
     if (N > 0x7FFFFFFF || T > 0x7FFFFFFF) return fail(SLHIP_ERR_UNSUPPORTED, "%s: shape too large", name);
     const int64_t wrow = dense ? K * (fmt == SLHIP_FMT_F32 ? 4 : 2) : K / qg.bs * qg.bb;
-    if (wrow % 16 != 0 && fmt != SLHIP_FMT_Q6_K)  // (only Q6_K rows can be: 210 bytes per 256 values)
+    if (wrow % 16 != 0 && fmt != SLHIP_FMT_Q6_K && fmt != SLHIP_FMT_Q2_K && fmt != SLHIP_FMT_Q3_K)
+        // (only the K-quants of 210, 84 and 110 bytes per 256 values can be)
         return fail(SLHIP_ERR_UNSUPPORTED, "%s: rows of %lld bytes are not a multiple of 16 for this weight format",
                     name, static_cast<long long>(wrow));
     MatvecArgs a{x, x_stride, static_cast<const char*>(wg), static_cast<const char*>(wu), wrow, y, y_stride,
@@ -2041,6 +2146,8 @@ static int matvec_common(int fmt, int dtype_x, int dtype_y, const void* x, int64
     case SLHIP_FMT_Q5_1: return run_quant<SLHIP_FMT_Q5_1>(a, dual, st);
     case SLHIP_FMT_Q4_K: return run_quant<SLHIP_FMT_Q4_K>(a, dual, st);
     case SLHIP_FMT_Q5_K: return run_quant<SLHIP_FMT_Q5_K>(a, dual, st);
+    case SLHIP_FMT_Q2_K: return run_mfma_only<SLHIP_FMT_Q2_K>(a, dual, st);
+    case SLHIP_FMT_Q3_K: return run_mfma_only<SLHIP_FMT_Q3_K>(a, dual, st);
     default: return run_quant<SLHIP_FMT_Q6_K>(a, dual, st);
     }
 }

@@ -530,17 +530,19 @@ Support supports(const Graph& g, const Node& n)
         if (y.type != DType::F32 && y.type != DType::BF16) return no("MatMul: f32 or bf16 output");
         if (!w.weight || w.dims.size() != 2) return no("MatMul: the second operand must be a weight [N, K]");
         const bool dense = w.type == DType::F32 || w.type == DType::F16 || w.type == DType::BF16;
-        const bool kq = w.type == DType::Q4_K || w.type == DType::Q5_K || w.type == DType::Q6_K;
+        const bool kq = w.type == DType::Q4_K || w.type == DType::Q5_K || w.type == DType::Q6_K ||
+                        w.type == DType::Q2_K || w.type == DType::Q3_K;
         const bool blocks = w.type == DType::Q8_0 || w.type == DType::Q4_0 || w.type == DType::Q4_1 ||
                             w.type == DType::Q5_0 || w.type == DType::Q5_1 || kq;
         if (!dense && !blocks)
-            return no("MatMul: f32, f16, bf16, Q8_0/Q4_0/Q4_1/Q5_0/Q5_1 or Q4_K/Q5_K/Q6_K weights on this provider");
+            return no("MatMul: f32, f16, bf16, Q8_0/Q4_0/Q4_1/Q5_0/Q5_1 or Q2_K/Q3_K/Q4_K/Q5_K/Q6_K weights on this provider");
         if (x.dims.empty() || w.dims[1] != x.last()) return no("MatMul: K mismatch");
         if (y.last() != w.dims[0]) return no("MatMul: output must be [.., N]");
         const int64_t K = x.last();
         if (dense && (K % 8 != 0 || K > 16384)) return no("MatMul: K must be a multiple of 8 and at most 16384");
         if (blocks && (K % 256 != 0 || K > 16384)) return no("MatMul: block-format K must be a multiple of 256, at most 16384");
-        if (!matvec_fits(format_code(w.type), K, false)) return no("MatMul: the weight rows do not fit the matvec's LDS staging");
+        if (!matvec_fits(format_code(w.type), K, false))
+            return no("MatMul: the weight rows do not fit the matvec's staging (Q2_K, Q3_K: K a multiple of 1024)");
         return {true, ""};
     }
     return no("op " + op + " is not on the fused-layer-op path of the HIP provider");

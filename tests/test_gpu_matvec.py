@@ -74,6 +74,22 @@ def _abs_terms(fmt, raw, W):
     """|q d| + |a| per weight (= |w| for dense and Q8_0 weights): the magnitudes the kernel's sums add."""
     if fmt in ("f32", "f16", "bf16", "q8_0"):
         return np.abs(W).astype(np.float64)
+    if fmt == "q3_k":  # d (s - 32) (q - 4): one term per value
+        return np.abs(W).astype(np.float64)
+    if fmt == "q2_k":  # |q d sc| + |dmin m| per value (ggml's Q2_K layout)
+        N, K = W.shape
+        b = raw.reshape(N, K // 256, 84)
+        f16 = lambda a: a.copy().view(np.float16)[..., 0].astype(np.float64)
+        d, dmin = f16(b[:, :, 80:82]), f16(b[:, :, 82:84])
+        out = np.zeros((N, K // 256, 256))
+        for n in range(2):
+            for j in range(4):
+                for h in range(2):
+                    sc = b[:, :, 8 * n + 2 * j + h].astype(np.int64)
+                    q = (b[:, :, 16 + 32 * n + 16 * h:16 + 32 * n + 16 * h + 16].astype(np.int64) >> (2 * j)) & 3
+                    v0 = 128 * n + 32 * j + 16 * h
+                    out[:, :, v0:v0 + 16] = np.abs(q * (d * (sc & 15))[..., None]) + np.abs((dmin * (sc >> 4))[..., None])
+        return out.reshape(N, K)
     if fmt in ("q4_k", "q5_k", "q6_k"):  # |q * scale| + |offset| per value, from the block fields
         from tests.test_oracle import _k_terms
         N, K = W.shape
@@ -156,6 +172,10 @@ SINGLE_CASES = [  # (fmt, x dtype, y dtype, T, K, N)
     ("q5_1", "f32", "bf16", 3, 3072, 24),
     ("q5_k", "f32", "f32", 16, 4096, 40),
     ("q5_k", "bf16", "bf16", 7, 1024, 17),
+    ("q2_k", "f32", "f32", 1, 4096, 40),     # Q2_K and Q3_K: the matrix cores at every token count
+    ("q3_k", "bf16", "bf16", 3, 2048, 33),
+    ("q2_k", "f32", "bf16", 16, 1024, 17),
+    ("q3_k", "f32", "f32", 17, 1024, 24),
 ]
 
 
@@ -170,7 +190,7 @@ def test_matvec(device, fmt, dx, dy, T, K, N):
     _check_single(y, dy, ref, S, f"matvec {fmt}")
 
 
-@pytest.mark.parametrize("fmt", ["f32", "f16", "bf16", "q8_0", "q4_0", "q4_1", "q5_0", "q5_1", "q6_k"])
+@pytest.mark.parametrize("fmt", ["f32", "f16", "bf16", "q8_0", "q4_0", "q4_1", "q5_0", "q5_1", "q6_k", "q2_k", "q3_k"])
 def test_one_hot_rows_pick_columns_exactly(device, fmt):
     """x = e_k: every 8-value group but one sums to zero and the one holds q_k * 1 exactly, so y = d q_k + a
     exactly -- the dequantized weight -- whatever the summation order."""
@@ -180,7 +200,9 @@ def test_one_hot_rows_pick_columns_exactly(device, fmt):
     x = np.zeros((len(ks), K), np.float32)
     x[np.arange(len(ks)), ks] = 1.0
     y = _run(fmt, "f32", "f32", x, [raw], N, K)
-    assert_bits_equal(y, np.ascontiguousarray(W[:, ks].T), what="one-hot columns")
+    # + 0.0 makes -0 +0: a dot product that starts from +0 (the CPU MatMul's) turns a -0 weight (Q3_K's
+    # (q - 4) d s with q = 4 and a negative scale) into +0
+    assert_bits_equal(y + np.float32(0.0), np.ascontiguousarray(W[:, ks].T) + np.float32(0.0), what="one-hot columns")
 
 
 DUAL_CASES = [  # (act, fmt, x dtype, y dtype, T, K, N): FusionTests.SwiGluDualMatvec's K/N plus decode shapes
@@ -226,6 +248,8 @@ DUAL_CASES = [  # (act, fmt, x dtype, y dtype, T, K, N): FusionTests.SwiGluDualM
     ("silu", "q5_k", "f32", "f32", 16, 4096, 14336),  # a Q5_K_M decode FFN at 16 tokens
     ("silu", "q5_0", "f32", "f32", 16, 1024, 64),
     ("gelu_erf", "q4_1", "bf16", "bf16", 5, 2048, 33),
+    ("silu", "q3_k", "f32", "f32", 1, 4096, 1024),    # a Q3_K_M decode FFN's gate/up
+    ("gelu_tanh", "q2_k", "bf16", "f32", 8, 2048, 40),
 ]
 
 

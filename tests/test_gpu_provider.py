@@ -77,7 +77,8 @@ def test_residual_add_rmsnorm_fuses(dev, h_is_output):
 
 @pytest.mark.parametrize("fmt,T,swap", [("bf16", 1, False), ("f16", 3, True), ("f32", 9, False), ("q8_0", 1, False),
                                         ("q4_0", 3, True), ("q4_k", 1, False), ("q5_k", 3, True),
-                                        ("q4_k", 8, False), ("q6_k", 16, True)])  # several-token matrix cores
+                                        ("q4_k", 8, False), ("q6_k", 16, True),   # several-token matrix cores
+                                        ("q3_k", 2, False)])                      # Q3_K: matrix cores always
 def test_swiglu_dual_matvec_fuses(dev, fmt, T, swap):
     """FusionTests.SwiGluDualMatvec (FusionTests.cs:59-80): Mul(Silu(x Wg^T), x Wu^T) is one dual matvec launch
     (in either operand order), within the f32 dot-product bound of the unfused CPU computation."""
