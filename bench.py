@@ -413,6 +413,8 @@ WORKLOADS = {
     "dual_matvec_silu_q4_k_T16": lambda: DualMatvec(16, "q4_k"),
     "dual_matvec_silu_q6_k_T16": lambda: DualMatvec(16, "q6_k"),
     "dual_matvec_silu_q5_k_T16": lambda: DualMatvec(16, "q5_k"),
+    "dual_matvec_silu_q3_k_T1": lambda: DualMatvec(1, "q3_k"),
+    "dual_matvec_silu_q3_k_T16": lambda: DualMatvec(16, "q3_k"),
     "copy_256MiB": lambda: CopyRef(),
 }
 
@@ -643,7 +645,8 @@ def cpu_baselines(budget_main: float, budget_op: float, which: set[str]) -> dict
         res[name] = dict(s=s * 8192 / rows, reps=reps,
                          sample=f"{rows} of 8192 rows, scaled x{8192 // rows}; Add, RmsNorm, then the {copy} rows")
     for fmt, T in (("bf16", 1), ("bf16", 4), ("bf16", 16), ("q8_0", 1), ("q4_0", 1), ("q4_k", 1), ("q6_k", 1),
-                   ("q4_0", 16), ("q8_0", 16), ("q4_k", 4), ("q4_k", 16), ("q6_k", 16), ("q5_k", 16)):
+                   ("q4_0", 16), ("q8_0", 16), ("q4_k", 4), ("q4_k", 16), ("q6_k", 16), ("q5_k", 16),
+                   ("q3_k", 1), ("q3_k", 16)):
         name = f"dual_matvec_silu_{fmt}_T{T}"
         if name not in which:
             continue
