@@ -906,7 +906,7 @@ __global__ __launch_bounds__(64 * kMmWaves) void matvec_mfma_lds(MatvecArgs a)
     }
 }
 
-// ---- 32-value block formats at several tokens on the matrix cores ---------------------------------------
+// ---- block formats at several tokens on the matrix cores -------------------------------------------------
 //
 // The VALU kernel decodes every weight once per group of tokens, so its time grows with T (Q4_0 dual at
 // [14336, 4096]: 18 us at T = 1, 57 at 4, 218 at 16). Here a 16-row tile's blocks are staged raw in LDS and
@@ -921,8 +921,11 @@ __global__ __launch_bounds__(64 * kMmWaves) void matvec_mfma_lds(MatvecArgs a)
 // across its four lane groups (Quant.cs:518-545's value d0 q - m). Q6_K too (a stage is 2 super-blocks, 420
 // bytes staged with 4-byte loads, and a wave a quarter super-block): codes enter as q - 32, and since a
 // 32-value block holds two 16-value scale groups, each block takes two MFMA chains, lane groups 0-1 (the
-// first group's values) in one and 2-3 in the other, the other half's codes masked to zero. A block
-// of 8 waves takes one tile; the waves split each stage's blocks; the stage's row bytes are loaded two stages
+// first group's values) in one and 2-3 in the other, the other half's codes masked to zero. The other block
+// formats follow the same pattern: Q4_1 and Q5_1 add m sum(x) per block, Q5_0 and Q5_1 take the 17th code
+// bit from their qh word, Q5_K is Q4_K with qh bit j of byte l, and Q2_K / Q3_K (16-value scale groups, as
+// Q6_K; Q3_K's codes q + 4h - 4, Q2_K's per-half minimum dmin m sum(x) over each half) have no VALU kernel
+// and take this one at every token count. A block of 8 waves takes one tile; the waves split each stage's blocks; the stage's row bytes are loaded two stages
 // ahead into registers and written to LDS one stage ahead (as the bf16 kernel above); partial sums meet in
 // LDS at the end.
 template <int FMT> struct MqGeom;
@@ -1240,7 +1243,7 @@ __global__ __launch_bounds__(64 * kMqWaves) void matvec_mfma_q(MatvecArgs a)
 #pragma unroll
         for (int j = 0; j < BPW; j++) {
             const int off = (wave * BPW + j) * BB;
-            const int sj = u0 + j;  // K-quant block (Q4_K sub-block, Q6_K 32-value quarter-half) in its super-block
+            const int sj = u0 + j;  // K-quant 32-value block (0..7) in its super-block
             uint4 Ag, Au;
             if constexpr (KQ) {
                 constexpr bool FIVE = FMT == SLHIP_FMT_Q5_K;
