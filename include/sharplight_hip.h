@@ -251,8 +251,7 @@ SLHIP_API int slhip_rownorm_copies(int kind, int dtype_in, int dtype_out, const 
  *   x: [T, K] f32 or bf16 (dtype_x), 16-byte aligned, row stride x_stride elements (a multiple of 8);
  *   W, Wg, Wu: N rows of K weights in `fmt`, 16-byte aligned: dense F32/F16/BF16 (K a multiple of 8,
  *   K <= 16384), or the GGUF block formats Q8_0/Q4_0/Q4_1/Q5_0/Q5_1 and Q4_K/Q5_K/Q6_K (K a multiple of
- *   256 and the rows' block images fitting in LDS), or Q2_K / Q3_K (K a multiple of 1024; the matrix cores
- *   at every T); y: [T, N] f32 or bf16 (dtype_y), row stride y_stride.
+ *   256 and the rows' block images fitting in LDS), or Q2_K / Q3_K (K a multiple of 1024); y: [T, N] f32 or bf16 (dtype_y), row stride y_stride.
  *   act: SLHIP_ACT_SILU / GELU_TANH / GELU_ERF, the same forms as slhip_gated_act.
  * Products and sums in f32 (in another order than the CPU provider's, so equal to it within the rounding of
  * a K-term f32 dot product); block formats sum d * sum(x q) + a * sum(x) per block, as the reference's
@@ -262,7 +261,7 @@ SLHIP_API int slhip_rownorm_copies(int kind, int dtype_in, int dtype_out, const 
  * the same products, summed in another order, under the same bound. Q4_K and Q6_K at T = 1 (K a multiple of
  * 4096 for Q4_K, 2048 for Q6_K) go to the integer matrix cores: x represented to 2^(e-28) of its 32-value
  * block's largest power of two, the code sums exact, under the same bound. Q8_0/Q4_0/Q4_1/Q5_0/Q5_1 from
- * SLHIP_MATVEC_MQ_MIN_T tokens (default 3), Q4_K/Q5_K/Q6_K from SLHIP_MATVEC_KQ_MIN_T (default 5), with K a
+ * SLHIP_MATVEC_MQ_MIN_T tokens (default 3), Q2_K..Q6_K from SLHIP_MATVEC_KQ_MIN_T (default 5), with K a
  * multiple of 1024 (Q6_K: 512), go to the matrix cores as exact bf16 codes (Q4_0 q - 8, Q6_K q - 32) against
  * x in two bf16 parts (|x - h - m| <= 2^-18 |x|), 16 tokens per launch, block scales (and the K-quants'
  * minima, scales per 16 values) applied per block in f32: the same bound.

@@ -269,7 +269,7 @@ __global__ __launch_bounds__(kMvThreads) void matvec_dense(MatvecArgs a, int wpr
     store_row<TT, DUAL>(a, n, ag, au);
 }
 
-// Quantized weights (Q8_0, Q4_0, Q4_1, Q5_0, Q5_1; Q4_K, Q5_K, Q6_K by 32-value sub-blocks): persistent
+// Quantized weights (Q8_0, Q4_0, Q4_1, Q5_0, Q5_1; Q2_K, Q3_K, Q4_K, Q5_K, Q6_K by 32-value sub-blocks): persistent
 // blocks of 4 waves; each wave walks row
 // (pairs) n, n + 4 * gridDim.x, ... . A row's block images go to the wave's own LDS region with 16-byte loads
 // (the blocks are only 2-byte aligned); the loads of the next row (pair) are issued before the current one
@@ -280,11 +280,17 @@ __global__ __launch_bounds__(kMvThreads) void matvec_dense(MatvecArgs a, int wpr
 // A K-quant row image in LDS, 32-value sub-block b (of super-block b / 8): its scale terms and 32 codes, one
 // per byte of w (Quant.cs:518-624). Q4_K / Q5_K: value = fma(q, d0, -m), d0 = d * sc, m = dmin * mn; Q6_K:
 // value = (q - 32) * s per 16 values, s = d * scale (d0 for values 0-15, d1 for 16-31); codes 0..63 here,
-// the -32 applied to the halves' sums of x.
+// the -32 applied to the halves' sums of x. Q3_K: value = (q - 4) * s per 16 values (q = 2 low bits + 4 * the
+// hmask bit; s = d (sc - 32) with the 6-bit packed scales), the -4 applied like Q6_K's -32; Q2_K: value =
+// q * d0 - m per 16 values (d0 = d * (sc & 15), m = dmin * (sc >> 4); second half d1, m1).
 struct KSub {
-    float d0, d1, m;
+    float d0, d1, m, m1;
     uint32_t w[8];
 };
+
+// Formats whose 32-value sub-block holds two 16-value scale groups.
+template <int FMT>
+constexpr bool kHalves = FMT == SLHIP_FMT_Q6_K || FMT == SLHIP_FMT_Q3_K || FMT == SLHIP_FMT_Q2_K;
 
 template <int FMT>
 __device__ __forceinline__ KSub ksub(const uint32_t* s, int b)
@@ -306,6 +312,7 @@ __device__ __forceinline__ KSub ksub(const uint32_t* s, int b)
         r.d0 = __fmul_rn(half_at(s, o), static_cast<float>(sc));
         r.d1 = r.d0;
         r.m = __fmul_rn(half_at(s, o + 2), static_cast<float>(mn));
+        r.m1 = r.m;
         const uint32_t* q = s + (o + (K5 ? 48 : 16) + 32 * (j >> 1)) / 4;
         const uint32_t* qh = s + (o + 16) / 4;
 #pragma unroll
@@ -315,12 +322,48 @@ __device__ __forceinline__ KSub ksub(const uint32_t* s, int b)
             asm("" : "+v"(w));  // hides the zero high bits: each byte then converts with one v_cvt_f32_ubyte
             r.w[k] = w;
         }
+    } else if constexpr (FMT == SLHIP_FMT_Q2_K) {  // {scales[16], qs[64], f16 d, f16 dmin}, 84 bytes
+        const int o = sb * 84, n = j >> 2, jj = j & 3;
+        const float d = half_at(s, o + 80), dm = half_at(s, o + 82);
+        const uint32_t c0 = B.u8(o + 8 * n + 2 * jj), c1 = B.u8(o + 8 * n + 2 * jj + 1);
+        r.d0 = __fmul_rn(d, static_cast<float>(c0 & 15u));
+        r.d1 = __fmul_rn(d, static_cast<float>(c1 & 15u));
+        r.m = __fmul_rn(dm, static_cast<float>(c0 >> 4));
+        r.m1 = __fmul_rn(dm, static_cast<float>(c1 >> 4));
+#pragma unroll
+        for (int k = 0; k < 8; k++) {  // values 4k .. 4k + 3 of the sub-block: 2-bit field 2jj of qs[32n + v]
+            uint32_t w = (lds_u32(s, o + 16 + 32 * n + 4 * k) >> (2 * jj)) & 0x03030303u;
+            asm("" : "+v"(w));
+            r.w[k] = w;
+        }
+    } else if constexpr (FMT == SLHIP_FMT_Q3_K) {  // {hmask[32], qs[64], scales[12], f16 d}, 110 bytes
+        const int o = sb * 110, n = j >> 2, jj = j & 3;
+        const float d = half_at(s, o + 108);
+        // 6-bit scales s = 8n + 2jj + 0..1: low 4 bits from byte 96 + 4 (w & 1) + b (low nibble for w < 2),
+        // high 2 bits from bits 2w of byte 104 + b, w = s / 4, b = s % 4
+        auto scale = [&](int sidx) {
+            const int w = sidx >> 2, b = sidx & 3;
+            const uint32_t a = B.u8(o + 96 + 4 * (w & 1) + b);
+            const uint32_t lo = w < 2 ? (a & 15u) : (a >> 4);
+            const uint32_t hi = (B.u8(o + 104 + b) >> (2 * w)) & 3u;
+            return static_cast<float>(static_cast<int>(lo | (hi << 4)) - 32);
+        };
+        r.d0 = __fmul_rn(d, scale(8 * n + 2 * jj));
+        r.d1 = __fmul_rn(d, scale(8 * n + 2 * jj + 1));
+        r.m = r.m1 = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {  // 2-bit field 2jj of qs[32n + v], plus 4 with bit 4n + jj of hmask[v]
+            const uint32_t l = lds_u32(s, o + 32 + 32 * n + 4 * k), h = lds_u32(s, o + 4 * k);
+            uint32_t w = ((l >> (2 * jj)) & 0x03030303u) | (((h >> (4 * n + jj)) & 0x01010101u) << 2);
+            asm("" : "+v"(w));
+            r.w[k] = w;
+        }
     } else {  // Q6_K: {ql[128], qh[64], int8 scales[16], f16 d}, 210 bytes (2-byte aligned)
         const int o = sb * 210, n = j >> 2, qt = j & 3;
         const float d = half_at(s, o + 208);
         r.d0 = __fmul_rn(d, static_cast<float>(static_cast<int8_t>(B.u8(o + 192 + 8 * n + 2 * qt))));
         r.d1 = __fmul_rn(d, static_cast<float>(static_cast<int8_t>(B.u8(o + 193 + 8 * n + 2 * qt))));
-        r.m = 0.0f;
+        r.m = r.m1 = 0.0f;
 #pragma unroll
         for (int k = 0; k < 8; k++) {
             const uint32_t l = lds_u32(s, o + 64 * n + 32 * (qt & 1) + 4 * k);
@@ -333,11 +376,18 @@ __device__ __forceinline__ KSub ksub(const uint32_t* s, int b)
     return r;
 }
 
-// A Q6_K sub-block's share from the halves' sums of x q (codes 0..63) and of x (hx[0], hx[1]):
-// s0 (sum x q - 32 sum x) + s1 (...): the -32 of every value applied once per half.
-__device__ __forceinline__ float q6_terms(const KSub& k, float sq0, float sq1, const float* hx)
+// A two-half sub-block's share from the halves' sums of x q and of x (hx[0], hx[1]): Q6_K and Q3_K
+// s0 (sum x q + OFF sum x) + s1 (...), their offset (-32, -4) applied once per half; Q2_K
+// d0 sum x q - m sum x + d1 (...) - m1 (...).
+template <int FMT>
+__device__ __forceinline__ float half_terms(const KSub& k, float sq0, float sq1, const float* hx)
 {
-    return fmaf(k.d1, fmaf(-32.0f, hx[1], sq1), k.d0 * fmaf(-32.0f, hx[0], sq0));
+    if constexpr (FMT == SLHIP_FMT_Q2_K) {
+        return fmaf(k.d1, sq1, fmaf(-k.m1, hx[1], fmaf(k.d0, sq0, -k.m * hx[0])));
+    } else {
+        constexpr float OFF = FMT == SLHIP_FMT_Q3_K ? -4.0f : -32.0f;
+        return fmaf(k.d1, fmaf(OFF, hx[1], sq1), k.d0 * fmaf(OFF, hx[0], sq0));
+    }
 }
 
 constexpr int kMqThreads = 256;
@@ -455,7 +505,7 @@ __global__ __launch_bounds__(kMqThreads) void matvec_quant(MatvecArgs a)
                         const float4* xp = reinterpret_cast<const float4*>(xsh + (t * nb + b) * 36 + 8 * j);
                         const float4 x0 = xp[0], x1 = xp[1];
                         const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-                        float& acc_h = (FMT == SLHIP_FMT_Q6_K && j >= 2) ? s1[t] : s0[t];
+                        float& acc_h = (kHalves<FMT> && j >= 2) ? s1[t] : s0[t];
 #pragma unroll
                         for (int e = 0; e < 8; e++) acc_h = fmaf(q[e], xv[e], acc_h);
                     }
@@ -463,7 +513,7 @@ __global__ __launch_bounds__(kMqThreads) void matvec_quant(MatvecArgs a)
 #pragma unroll
                 for (int t = 0; t < TT; t++) {
                     const float* hx = xsh + (t * nb + b) * 36 + 32;
-                    const float p = FMT == SLHIP_FMT_Q6_K ? q6_terms(ks, s0[t], s1[t], hx)
+                    const float p = kHalves<FMT> ? half_terms<FMT>(ks, s0[t], s1[t], hx)
                                                           : fmaf(-ks.m, xsum[t * nb + b], ks.d0 * s0[t]);
                     acc[t] += own ? p : 0.0f;
                 }
@@ -524,14 +574,14 @@ __global__ __launch_bounds__(kMqThreads) void matvec_quant(MatvecArgs a)
                         qg[e] = static_cast<float>((kg.w[2 * j + (e >> 2)] >> (8 * (e & 3))) & 0xFFu);
                         qu[e] = static_cast<float>((ku.w[2 * j + (e >> 2)] >> (8 * (e & 3))) & 0xFFu);
                     }
-                    dot8(qg, qu, j, FMT == SLHIP_FMT_Q6_K && j >= 2);
+                    dot8(qg, qu, j, kHalves<FMT> && j >= 2);
                 }
 #pragma unroll
                 for (int t = 0; t < TT; t++) {
                     const float* hx = xsh + (t * nb + b) * 36 + 32;
-                    const float pg = FMT == SLHIP_FMT_Q6_K ? q6_terms(kg, g0[t], g1[t], hx)
+                    const float pg = kHalves<FMT> ? half_terms<FMT>(kg, g0[t], g1[t], hx)
                                                            : fmaf(-kg.m, xsum[t * nb + b], kg.d0 * g0[t]);
-                    const float pu = FMT == SLHIP_FMT_Q6_K ? q6_terms(ku, u0[t], u1[t], hx)
+                    const float pu = kHalves<FMT> ? half_terms<FMT>(ku, u0[t], u1[t], hx)
                                                            : fmaf(-ku.m, xsum[t * nb + b], ku.d0 * u0[t]);
                     ag[t] += own ? pg : 0.0f;
                     au[t] += own ? pu : 0.0f;
@@ -924,8 +974,8 @@ __global__ __launch_bounds__(64 * kMmWaves) void matvec_mfma_lds(MatvecArgs a)
 // first group's values) in one and 2-3 in the other, the other half's codes masked to zero. The other block
 // formats follow the same pattern: Q4_1 and Q5_1 add m sum(x) per block, Q5_0 and Q5_1 take the 17th code
 // bit from their qh word, Q5_K is Q4_K with qh bit j of byte l, and Q2_K / Q3_K (16-value scale groups, as
-// Q6_K; Q3_K's codes q + 4h - 4, Q2_K's per-half minimum dmin m sum(x) over each half) have no VALU kernel
-// and take this one at every token count. A block of 8 waves takes one tile; the waves split each stage's blocks; the stage's row bytes are loaded two stages
+// Q6_K; Q3_K's codes q + 4h - 4, Q2_K's per-half minimum dmin m sum(x) over each half). A block of 8 waves
+// takes one tile; the waves split each stage's blocks; the stage's row bytes are loaded two stages
 // ahead into registers and written to LDS one stage ahead (as the bf16 kernel above); partial sums meet in
 // LDS at the end.
 template <int FMT> struct MqGeom;
@@ -1979,7 +2029,7 @@ static int launch_quant(const MatvecArgs& a, hipStream_t st)
 template <int FMT, int TT, bool DUAL>
 static int quant_ch(const MatvecArgs& a, int ch, hipStream_t st)
 {
-    if constexpr (FMT == SLHIP_FMT_Q6_K) {  // rows not 16-byte multiples: narrower staging loads
+    if constexpr (FMT == SLHIP_FMT_Q6_K || FMT == SLHIP_FMT_Q3_K) {  // rows not 16-byte multiples: narrower staging loads
         if (a.wrow % 16 != 0) {
             return a.wrow % 8 == 0   ? launch_quant<FMT, TT, 8, DUAL, 8>(a, st)
                    : a.wrow % 4 == 0 ? launch_quant<FMT, TT, 8, DUAL, 4>(a, st)
@@ -2024,8 +2074,8 @@ static int launch_kq_tile(const MatvecArgs& a, hipStream_t st)
 // 52.1, 25.7 / 39.7; T = 3 57.2 / 52.7, 55.6 / 40.3; T = 16 218 / 58, - / 42; Q8_0 T = 3 58.3 / 57.4,
 // 56.6 / 45.7; T = 16 223 / 64.
 static int mq_min_tokens() { return env_int("SLHIP_MATVEC_MQ_MIN_T", 3); }
-// The same for Q4_K, Q5_K and Q6_K (SLHIP_MATVEC_KQ_MIN_T): their VALU kernel takes four tokens per pass, so
-// the matrix cores pay from five. (Q4_1, Q5_0 and Q5_1 follow Q4_0's SLHIP_MATVEC_MQ_MIN_T.) Measured dual at [14336, 4096], f32 x (us, VALU / matrix cores): T = 4 57.6 / 75.2;
+// The same for the K-quants (SLHIP_MATVEC_KQ_MIN_T): their VALU kernel takes four tokens per pass, so the
+// matrix cores pay from five. (Q4_1, Q5_0 and Q5_1 follow Q4_0's SLHIP_MATVEC_MQ_MIN_T.) Measured dual at [14336, 4096], f32 x (us, VALU / matrix cores): T = 4 57.6 / 75.2;
 // T = 16 229 / 82.
 static int kq_min_tokens() { return env_int("SLHIP_MATVEC_KQ_MIN_T", 5); }
 
@@ -2052,7 +2102,8 @@ template <int FMT>
 static int run_quant(MatvecArgs a, bool dual, hipStream_t st)
 {
     if constexpr (FMT == SLHIP_FMT_Q4_0 || FMT == SLHIP_FMT_Q8_0 || FMT == SLHIP_FMT_Q4_1 || FMT == SLHIP_FMT_Q5_0 ||
-                  FMT == SLHIP_FMT_Q5_1 || FMT == SLHIP_FMT_Q4_K || FMT == SLHIP_FMT_Q5_K || FMT == SLHIP_FMT_Q6_K) {
+                  FMT == SLHIP_FMT_Q5_1 || FMT == SLHIP_FMT_Q4_K || FMT == SLHIP_FMT_Q5_K || FMT == SLHIP_FMT_Q6_K ||
+                  FMT == SLHIP_FMT_Q2_K || FMT == SLHIP_FMT_Q3_K) {
         // several tokens: the matrix-core kernel, when K splits into whole stages (and the rows into its loads)
         const int mt = Fmt<FMT>::K ? kq_min_tokens() : mq_min_tokens();
         const uintptr_t al = reinterpret_cast<uintptr_t>(a.wg) | reinterpret_cast<uintptr_t>(a.wu);
@@ -2077,18 +2128,6 @@ static int run_quant(MatvecArgs a, bool dual, hipStream_t st)
         if (r != SLHIP_OK) return r;
     }
     return SLHIP_OK;
-}
-
-// Q2_K and Q3_K have no VALU kernel: every token count takes the matrix cores (K a multiple of 1024 and the
-// weights aligned to the stage's loads).
-template <int FMT>
-static int run_mfma_only(MatvecArgs a, bool dual, hipStream_t st)
-{
-    const uintptr_t al = reinterpret_cast<uintptr_t>(a.wg) | reinterpret_cast<uintptr_t>(a.wu);
-    if (a.K % (MqGeom<FMT>::SKB * 32) != 0 || al % MqGeom<FMT>::UB != 0)
-        return fail(SLHIP_ERR_UNSUPPORTED, "matvec: Q2_K / Q3_K weights need K a multiple of %d (K = %lld)",
-                    MqGeom<FMT>::SKB * 32, static_cast<long long>(a.K));
-    return run_mfma_q<FMT>(a, dual, st);
 }
 
 // Whether a (dual) matvec over rows of K values of `fmt` can run: for the block formats, whether one token's
@@ -2149,8 +2188,8 @@ static int matvec_common(int fmt, int dtype_x, int dtype_y, const void* x, int64
     case SLHIP_FMT_Q5_1: return run_quant<SLHIP_FMT_Q5_1>(a, dual, st);
     case SLHIP_FMT_Q4_K: return run_quant<SLHIP_FMT_Q4_K>(a, dual, st);
     case SLHIP_FMT_Q5_K: return run_quant<SLHIP_FMT_Q5_K>(a, dual, st);
-    case SLHIP_FMT_Q2_K: return run_mfma_only<SLHIP_FMT_Q2_K>(a, dual, st);
-    case SLHIP_FMT_Q3_K: return run_mfma_only<SLHIP_FMT_Q3_K>(a, dual, st);
+    case SLHIP_FMT_Q2_K: return run_quant<SLHIP_FMT_Q2_K>(a, dual, st);
+    case SLHIP_FMT_Q3_K: return run_quant<SLHIP_FMT_Q3_K>(a, dual, st);
     default: return run_quant<SLHIP_FMT_Q6_K>(a, dual, st);
     }
 }

@@ -172,7 +172,9 @@ SINGLE_CASES = [  # (fmt, x dtype, y dtype, T, K, N)
     ("q5_1", "f32", "bf16", 3, 3072, 24),
     ("q5_k", "f32", "f32", 16, 4096, 40),
     ("q5_k", "bf16", "bf16", 7, 1024, 17),
-    ("q2_k", "f32", "f32", 1, 4096, 40),     # Q2_K and Q3_K: the matrix cores at every token count
+    ("q2_k", "f32", "f32", 1, 4096, 40),     # Q2_K and Q3_K: the VALU kernel below five tokens
+    ("q2_k", "bf16", "f32", 4, 2048, 24),
+    ("q3_k", "f32", "bf16", 2, 3072, 33),    # rows of 1320 bytes: 8-byte staging loads
     ("q3_k", "bf16", "bf16", 3, 2048, 33),
     ("q2_k", "f32", "bf16", 16, 1024, 17),
     ("q3_k", "f32", "f32", 17, 1024, 24),
@@ -202,6 +204,19 @@ def test_one_hot_rows_pick_columns_exactly(device, fmt):
     y = _run(fmt, "f32", "f32", x, [raw], N, K)
     # + 0.0 makes -0 +0: a dot product that starts from +0 (the CPU MatMul's) turns a -0 weight (Q3_K's
     # (q - 4) d s with q = 4 and a negative scale) into +0
+    assert_bits_equal(y + np.float32(0.0), np.ascontiguousarray(W[:, ks].T) + np.float32(0.0), what="one-hot columns")
+
+
+@pytest.mark.parametrize("fmt", ["q2_k", "q3_k"])
+def test_one_hot_columns_below_five_tokens(device, fmt):
+    """The same exactness on the VALU kernel (two tokens): each half's terms d0 sum(x q) - m sum(x) (Q2_K) or
+    d0 (sum(x q) - 4 sum(x)) (Q3_K) give the dequantized weight with one rounding."""
+    N, K = 21, 2048
+    raw, W = _weights(fmt, N, K, 4, 1)
+    ks = [3, 1553]
+    x = np.zeros((len(ks), K), np.float32)
+    x[np.arange(len(ks)), ks] = 1.0
+    y = _run(fmt, "f32", "f32", x, [raw], N, K)
     assert_bits_equal(y + np.float32(0.0), np.ascontiguousarray(W[:, ks].T) + np.float32(0.0), what="one-hot columns")
 
 
