@@ -414,6 +414,7 @@ WORKLOADS = {
     "dual_matvec_silu_q6_k_T16": lambda: DualMatvec(16, "q6_k"),
     "dual_matvec_silu_q5_k_T16": lambda: DualMatvec(16, "q5_k"),
     "dual_matvec_silu_q3_k_T1": lambda: DualMatvec(1, "q3_k"),
+    "dual_matvec_silu_q3_k_T8": lambda: DualMatvec(8, "q3_k"),
     "dual_matvec_silu_q3_k_T16": lambda: DualMatvec(16, "q3_k"),
     "copy_256MiB": lambda: CopyRef(),
 }
