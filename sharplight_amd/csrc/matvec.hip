@@ -2029,7 +2029,8 @@ static int launch_quant(const MatvecArgs& a, hipStream_t st)
 template <int FMT, int TT, bool DUAL>
 static int quant_ch(const MatvecArgs& a, int ch, hipStream_t st)
 {
-    if constexpr (FMT == SLHIP_FMT_Q6_K || FMT == SLHIP_FMT_Q3_K) {  // rows not 16-byte multiples: narrower staging loads
+    if constexpr (FMT == SLHIP_FMT_Q6_K || FMT == SLHIP_FMT_Q3_K || FMT == SLHIP_FMT_Q2_K) {
+        // rows not 16-byte multiples (210, 110 or 84 bytes per 256 values): narrower staging loads
         if (a.wrow % 16 != 0) {
             return a.wrow % 8 == 0   ? launch_quant<FMT, TT, 8, DUAL, 8>(a, st)
                    : a.wrow % 4 == 0 ? launch_quant<FMT, TT, 8, DUAL, 4>(a, st)
@@ -2137,8 +2138,6 @@ bool matvec_fits(int fmt, int64_t K, bool dual)
     const QGeom qg = quant_geom(fmt);
     if (qg.bs == 0) return true;
     if (K % qg.bs != 0) return false;
-    if (fmt == SLHIP_FMT_Q2_K) return K % (MqGeom<SLHIP_FMT_Q2_K>::SKB * 32) == 0;  // matrix cores only
-    if (fmt == SLHIP_FMT_Q3_K) return K % (MqGeom<SLHIP_FMT_Q3_K>::SKB * 32) == 0;
     return quant_lds(1, K, K / qg.bs * qg.bb, dual) <= kMaxLds;
 }
 

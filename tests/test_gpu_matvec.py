@@ -178,6 +178,9 @@ SINGLE_CASES = [  # (fmt, x dtype, y dtype, T, K, N)
     ("q3_k", "bf16", "bf16", 3, 2048, 33),
     ("q2_k", "f32", "bf16", 16, 1024, 17),
     ("q3_k", "f32", "f32", 17, 1024, 24),
+    ("q2_k", "f32", "f32", 1, 1280, 33),     # rows of 420 bytes (not 16-byte multiples): 4-byte staging loads
+    ("q2_k", "bf16", "bf16", 3, 512, 17),    # 168 bytes
+    ("q2_k", "f32", "f32", 6, 1280, 19),     # five tokens or more, K not a multiple of 1024: the VALU kernel
 ]
 
 
@@ -265,6 +268,8 @@ DUAL_CASES = [  # (act, fmt, x dtype, y dtype, T, K, N): FusionTests.SwiGluDualM
     ("gelu_erf", "q4_1", "bf16", "bf16", 5, 2048, 33),
     ("silu", "q3_k", "f32", "f32", 1, 4096, 1024),    # a Q3_K_M decode FFN's gate/up
     ("gelu_tanh", "q2_k", "bf16", "f32", 8, 2048, 40),
+    ("silu", "q2_k", "f32", "f32", 1, 1280, 40),          # Q2_K rows of 420 bytes: 4-byte staging loads
+    ("silu", "q2_k", "bf16", "bf16", 2, 768, 24),         # 252 bytes
 ]
 
 

@@ -281,11 +281,11 @@ def test_matmul_support_answers():
     x2048 = g.input("f32", "T", 2048)
     g.matmul(x2048, g.weight("q6_k", 16, 2048))   # 8: yes
     g.matmul(x2048, g.weight("iq4_xs", 16, 2048))  # 9: no matvec for this format
-    g.matmul(x2048, g.weight("q2_k", 16, 2048))   # 10: Q2_K on the matrix cores: K a multiple of 1024 -> yes
-    g.matmul(x256, g.weight("q3_k", 16, 256))     # 11: Q3_K with K = 256 -> no
+    g.matmul(x2048, g.weight("q2_k", 16, 2048))   # 10: yes
+    g.matmul(x256, g.weight("q3_k", 16, 256))     # 11: Q3_K with K = 256 -> yes (the VALU kernel at any T)
     x1024 = g.input("f32", "T", 1024)
     g.matmul(x1024, g.weight("q3_k", 16, 1024))   # 12: yes
-    expect = [False, True, False, False, True, False, True, True, True, False, True, False, True]
+    expect = [False, True, False, False, True, False, True, True, True, False, True, True, True]
     for k, e in enumerate(expect):
         ok, why = _supports(g, k)
         assert ok == e, (k, why)
