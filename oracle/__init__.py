@@ -104,6 +104,12 @@ def _declare(L):
         "orc_f32_to_f16_mt": (None, [_P, _P, _I64]),
         "orc_matvec": (ctypes.c_int, [ctypes.c_int, _P, _I64, _I64, _P, _I64, _P]),
         "orc_matvec_mt": (ctypes.c_int, [ctypes.c_int, _P, _I64, _I64, _P, _I64, _P]),
+        "orc_q8_quantize": (_I, [_P, _I64, _I64, _P, _P, _P]),
+        "orc_intdot_decode": (_I, [_I, _P, _I64, _P, _P, _P]),
+        "orc_intdot_dot": (_F, [_P, _P, _P, _P, _P, _P, _I64]),
+        "orc_intdot_supported": (_I, [_I]),
+        "orc_matvec_q8": (_I, [_I, _P, _I64, _I64, _P, _I64, _P, _P]),
+        "orc_matvec_q8_mt": (_I, [_I, _P, _I64, _I64, _P, _I64, _P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -428,3 +434,56 @@ def dual_matvec(act, fmt, wg_raw, wu_raw, N, K, x, dtype="f32"):
     u = matvec(fmt, wu_raw, N, K, x)
     y = mul(unary(act, g), u)
     return to_bf16(y) if dtype == "bf16" else y
+
+
+# ---- integer-dot matvec (q8 activations) ---------------------------------------------------------------
+
+INTDOT_FORMATS = ("q8_0", "q4_0", "q4_1", "q5_0", "q5_1", "q4_k", "q5_k", "q6_k", "iq4_nl", "iq4_xs", "mxfp4")
+
+
+def q8_quantize(x):
+    """IntDot.Quantize per row: x [rows, K] f32 -> (q int8 [rows, K], d f32 [rows, K/32], gs f32 [rows, K/16])."""
+    x = _c(np.atleast_2d(x), np.float32)
+    rows, K = x.shape
+    q = np.empty((rows, K), np.int8)
+    d = np.empty((rows, K // 32), np.float32)
+    gs = np.empty((rows, K // 16), np.float32)
+    if lib().orc_q8_quantize(_p(x), rows, K, _p(q), _p(d), _p(gs)):
+        raise ValueError(f"q8_quantize: K={K} is not a multiple of 32")
+    return q, d, gs
+
+
+def intdot_decode(fmt, row_raw, K):
+    """IntDot.Decode of one weight row: (u uint8 [K], a f32 [K/16], b f32 [K/16]), value = a u + b."""
+    row_raw = np.ascontiguousarray(row_raw).view(np.uint8)
+    u = np.empty(K, np.uint8)
+    a = np.empty(K // 16, np.float32)
+    b = np.empty(K // 16, np.float32)
+    if lib().orc_intdot_decode(FORMATS[fmt], _p(row_raw), K, _p(u), _p(a), _p(b)):
+        raise ValueError(f"intdot_decode: {fmt} has no integer-dot decoder")
+    return u, a, b
+
+
+def intdot_dot(u, a, b, q, d, gs):
+    """IntDot.DotScalar: one decoded weight row with one quantized activation row."""
+    u, a, b = _c(u, np.uint8), _c(a, np.float32), _c(b, np.float32)
+    q, d, gs = _c(q, np.int8), _c(d, np.float32), _c(gs, np.float32)
+    return float(lib().orc_intdot_dot(_p(u), _p(a), _p(b), _p(q), _p(d), _p(gs), u.size))
+
+
+def matvec_q8(fmt, w_raw, N, K, x, threads=None, with_abs=False):
+    """MatMulOp's integer-dot path: x [T, K] quantized per 32 values, y [T, N] f32. with_abs: also the
+    per-output sum of |a d s| + |b gs| (f64), the magnitude bound of the f32 accumulation."""
+    x = _c(np.atleast_2d(x), np.float32)
+    w_raw = np.ascontiguousarray(w_raw).view(np.uint8)
+    T = x.shape[0]
+    y = np.empty((T, N), np.float32)
+    if threads:
+        r = lib().orc_matvec_q8_mt(FORMATS[fmt], _p(w_raw), N, K, _p(x), T, _p(y))
+        yabs = None
+    else:
+        yabs = np.empty((T, N), np.float64) if with_abs else None
+        r = lib().orc_matvec_q8(FORMATS[fmt], _p(w_raw), N, K, _p(x), T, _p(y), _p(yabs))
+    if r:
+        raise ValueError(f"matvec_q8: {fmt} K={K} not supported")
+    return (y, yabs) if with_abs else y

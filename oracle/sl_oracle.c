@@ -1878,3 +1878,286 @@ int orc_matvec_mt(int fmt, const uint8_t* w, int64_t N, int64_t K, const float* 
     parallel_for(ch, mv_chunk, &k);
     return 0;
 }
+
+/* ==== Integer-dot matmul: q8 activations x decoded weight codes (IntDot.cs, IntDot.Decode.cs, IntDot.Kernels.cs)
+ * The CPU provider's few-row MatMul when integer dots are enabled (MatMulOp.cs:144-146, 173-213). A quantized
+ * activation row here is three arrays: q int8 [K], d f32 [K/32] (one block scale per 32 values, the values of
+ * Q8Row.LaneScales without their fourfold repetition) and gs f32 [K/16] (Q8Row.GroupSums: d * sum(q) per 16). */
+
+/* .NET's saturating float -> int conversion (NaN -> 0), the cast of IntDot.QuantizeBlockScalar. */
+static int32_t sat_i32(float v)
+{
+    if (v != v) return 0;
+    if (v >= 2147483648.0f) return INT32_MAX;
+    if (v <= -2147483648.0f) return INT32_MIN;
+    return (int32_t)v;
+}
+
+/* IntDot.QuantizeBlockScalar (IntDot.cs:92-126), one 32-value block: amax by MathF.Max (NaN-propagating),
+ * d = amax / 127, id = 1 / d (0 for d == 0), q = (int)(x * id + copysign(0.5, x * id)) -- round half away from
+ * zero through an f32 addition, so x * id = 0.49999997 rounds to 1 -- and the two 16-value group sums d * s. */
+static void q8_block(const float* x, int8_t* q, float* d, float* gs)
+{
+    float amax = 0.0f;
+    for (int i = 0; i < 32; i++) {
+        const float a = fabsf(x[i]);
+        amax = (a != a || amax != amax) ? NAN : (a > amax ? a : amax);
+    }
+    const float dd = amax / 127.0f;
+    const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
+    int s0 = 0, s1 = 0;
+    for (int i = 0; i < 32; i++) {
+        const float v = x[i] * id;
+        const int32_t r = sat_i32(v + copysignf(0.5f, v));
+        q[i] = (int8_t)(uint8_t)(uint32_t)r;
+        if (i < 16) s0 += r;
+        else s1 += r;
+    }
+    *d = dd;
+    gs[0] = dd * (float)s0;
+    gs[1] = dd * (float)s1;
+}
+
+int orc_q8_quantize(const float* x, int64_t rows, int64_t K, int8_t* q, float* d, float* gs)
+{
+    if (K % 32) return -1;
+    for (int64_t r = 0; r < rows; r++)
+        for (int64_t b = 0; b < K / 32; b++)
+            q8_block(x + r * K + 32 * b, q + r * K + 32 * b, d + r * (K / 32) + b, gs + r * (K / 16) + 2 * b);
+    return 0;
+}
+
+/* IntDot.Decode (IntDot.Decode.cs:17-293): K values of a weight row -> unsigned codes u [K] and a multiplier a
+ * and an offset b per 16 values, value = a * u + b. Formats: IntDot.Supports (IntDot.cs:36-38). */
+int orc_intdot_decode(int fmt, const uint8_t* p, int64_t K, uint8_t* u, float* a, float* b)
+{
+    static const uint8_t iq4u[16] = {1, 24, 45, 63, 79, 93, 106, 118, 129, 141, 153, 166, 181, 197, 217, 241};
+    static const uint8_t fp4u[16] = {16, 17, 18, 19, 20, 22, 24, 28, 16, 15, 14, 13, 12, 10, 8, 4};
+#define SETB(g, m, o) (a[2 * (g)] = a[2 * (g) + 1] = (m), b[2 * (g)] = b[2 * (g) + 1] = (o))
+    switch (fmt) {
+    case ORC_Q8_0:
+        for (int64_t blk = 0; blk < K / 32; blk++, p += 34) {
+            const float dd = rd_h(p);
+            for (int i = 0; i < 32; i++) u[32 * blk + i] = (uint8_t)(p[2 + i] ^ 0x80);
+            SETB(blk, dd, -128.0f * dd);
+        }
+        return 0;
+    case ORC_Q4_0:
+    case ORC_Q4_1: {
+        const int m = fmt == ORC_Q4_1, bytes = m ? 20 : 18, qo = m ? 4 : 2;
+        for (int64_t blk = 0; blk < K / 32; blk++, p += bytes) {
+            const float dd = rd_h(p);
+            for (int i = 0; i < 16; i++) {
+                u[32 * blk + i] = p[qo + i] & 0xF;
+                u[32 * blk + 16 + i] = p[qo + i] >> 4;
+            }
+            SETB(blk, dd, m ? rd_h(p + 2) : -8.0f * dd);
+        }
+        return 0;
+    }
+    case ORC_Q5_0:
+    case ORC_Q5_1: {
+        const int m = fmt == ORC_Q5_1, bytes = m ? 24 : 22, ho = m ? 4 : 2;
+        for (int64_t blk = 0; blk < K / 32; blk++, p += bytes) {
+            const float dd = rd_h(p);
+            const uint32_t qh = (uint32_t)p[ho] | ((uint32_t)p[ho + 1] << 8) | ((uint32_t)p[ho + 2] << 16) |
+                                ((uint32_t)p[ho + 3] << 24);
+            for (int i = 0; i < 16; i++) {
+                u[32 * blk + i] = (uint8_t)((p[ho + 4 + i] & 0xF) | (((qh >> i) & 1) << 4));
+                u[32 * blk + 16 + i] = (uint8_t)((p[ho + 4 + i] >> 4) | (((qh >> (16 + i)) & 1) << 4));
+            }
+            SETB(blk, dd, m ? rd_h(p + 2) : -16.0f * dd);
+        }
+        return 0;
+    }
+    case ORC_Q4_K:
+    case ORC_Q5_K: {
+        const int five = fmt == ORC_Q5_K, bytes = five ? 176 : 144;
+        for (int64_t blk = 0; blk < K / 256; blk++, p += bytes) {
+            const float dd = rd_h(p), dmin = rd_h(p + 2);
+            const uint8_t* qs = p + (five ? 48 : 16);
+            uint8_t* ub = u + 256 * blk;
+            for (int j = 0; j < 4; j++)
+                for (int i = 0; i < 32; i++) {
+                    const uint8_t c = qs[32 * j + i];
+                    int lo = c & 0xF, hi = c >> 4;
+                    if (five) {
+                        const uint8_t h = p[16 + i];
+                        lo |= ((h >> (2 * j)) & 1) << 4;
+                        hi |= ((h >> (2 * j + 1)) & 1) << 4;
+                    }
+                    ub[64 * j + i] = (uint8_t)lo;
+                    ub[64 * j + 32 + i] = (uint8_t)hi;
+                }
+            for (int j = 0; j < 8; j++) {
+                int sc, mn;
+                scale_min(j, p + 4, &sc, &mn);
+                SETB(8 * blk + j, dd * (float)sc, -dmin * (float)mn);
+            }
+        }
+        return 0;
+    }
+    case ORC_Q6_K:
+        for (int64_t blk = 0; blk < K / 256; blk++, p += 210) {
+            const float dd = rd_h(p + 208);
+            uint8_t* ub = u + 256 * blk;
+            for (int n = 0; n < 2; n++) {
+                const uint8_t* ql = p + 64 * n;
+                const uint8_t* qh = p + 128 + 32 * n;
+                for (int i = 0; i < 32; i++) {
+                    ub[128 * n + i] = (uint8_t)((ql[i] & 0xF) | ((qh[i] & 3) << 4));
+                    ub[128 * n + 32 + i] = (uint8_t)((ql[32 + i] & 0xF) | (((qh[i] >> 2) & 3) << 4));
+                    ub[128 * n + 64 + i] = (uint8_t)((ql[i] >> 4) | (((qh[i] >> 4) & 3) << 4));
+                    ub[128 * n + 96 + i] = (uint8_t)((ql[32 + i] >> 4) | (((qh[i] >> 6) & 3) << 4));
+                }
+            }
+            for (int g = 0; g < 16; g++) {
+                const float s = dd * (float)(int8_t)p[192 + g];
+                a[16 * blk + g] = s;
+                b[16 * blk + g] = -32.0f * s;
+            }
+        }
+        return 0;
+    case ORC_IQ4_NL:
+        for (int64_t blk = 0; blk < K / 32; blk++, p += 18) {
+            const float dd = rd_h(p);
+            for (int i = 0; i < 16; i++) {
+                u[32 * blk + i] = iq4u[p[2 + i] & 0xF];
+                u[32 * blk + 16 + i] = iq4u[p[2 + i] >> 4];
+            }
+            SETB(blk, dd, -128.0f * dd);
+        }
+        return 0;
+    case ORC_IQ4_XS:
+        for (int64_t blk = 0; blk < K / 256; blk++, p += 136) {
+            const float dd = rd_h(p);
+            const uint32_t sh = (uint32_t)p[2] | ((uint32_t)p[3] << 8);
+            for (int ib = 0; ib < 8; ib++) {
+                const int ls = ((p[4 + ib / 2] >> (4 * (ib % 2))) & 0xF) | (int)(((sh >> (2 * ib)) & 3) << 4);
+                const float dl = dd * (float)(ls - 32);
+                for (int i = 0; i < 16; i++) {
+                    u[256 * blk + 32 * ib + i] = iq4u[p[8 + 16 * ib + i] & 0xF];
+                    u[256 * blk + 32 * ib + 16 + i] = iq4u[p[8 + 16 * ib + i] >> 4];
+                }
+                SETB(8 * blk + ib, dl, -128.0f * dl);
+            }
+        }
+        return 0;
+    case ORC_MXFP4:
+        for (int64_t blk = 0; blk < K / 32; blk++, p += 17) {
+            const float dd = e8m0_half(p[0]);
+            for (int i = 0; i < 16; i++) {
+                u[32 * blk + i] = fp4u[p[1 + i] & 0xF];
+                u[32 * blk + 16 + i] = fp4u[p[1 + i] >> 4];
+            }
+            SETB(blk, dd, -16.0f * dd);
+        }
+        return 0;
+    default:
+        return -1;
+    }
+#undef SETB
+}
+
+/* IntDot.DotScalar (IntDot.Kernels.cs:12-29): per 16 values the exact integer sum s = sum(u q), then
+ * acc += a * d * s + b * gs in f32, group by group. */
+float orc_intdot_dot(const uint8_t* u, const float* a, const float* b, const int8_t* q, const float* d, const float* gs,
+                     int64_t K)
+{
+    float acc = 0.0f;
+    for (int64_t g = 0; g < K / 16; g++) {
+        int32_t s = 0;
+        for (int i = 0; i < 16; i++) s += (int32_t)u[16 * g + i] * (int32_t)q[16 * g + i];
+        const float t1 = (a[g] * d[g / 2]) * (float)s;
+        const float t2 = b[g] * gs[g];
+        acc += t1 + t2;
+    }
+    return acc;
+}
+
+/* sum over groups of |a d s| + |b gs|: the magnitude of what the dot adds, for tolerance bounds */
+static double intdot_abs(const uint8_t* u, const float* a, const float* b, const int8_t* q, const float* d,
+                         const float* gs, int64_t K)
+{
+    double acc = 0.0;
+    for (int64_t g = 0; g < K / 16; g++) {
+        int64_t s = 0;
+        for (int i = 0; i < 16; i++) s += (int64_t)u[16 * g + i] * (int64_t)q[16 * g + i];
+        acc += fabs((double)a[g] * (double)d[g / 2] * (double)s) + fabs((double)b[g] * (double)gs[g]);
+    }
+    return acc;
+}
+
+int orc_intdot_supported(int fmt)
+{
+    return fmt == ORC_Q8_0 || fmt == ORC_Q4_0 || fmt == ORC_Q4_1 || fmt == ORC_Q5_0 || fmt == ORC_Q5_1 ||
+           fmt == ORC_Q4_K || fmt == ORC_Q5_K || fmt == ORC_Q6_K || fmt == ORC_IQ4_NL || fmt == ORC_IQ4_XS ||
+           fmt == ORC_MXFP4;
+}
+
+typedef struct {
+    int fmt;
+    const uint8_t* w;
+    int64_t N, K, T, per, rowb;
+    const int8_t* q;
+    const float *d, *gs;
+    float* y;
+    double* yabs;
+} iv_ctx;
+
+static void iv_rows(void* v, int64_t c)
+{
+    iv_ctx* k = (iv_ctx*)v;
+    const int64_t n0 = c * k->per, n1 = n0 + k->per < k->N ? n0 + k->per : k->N;
+    if (n0 >= n1) return;
+    uint8_t* u = (uint8_t*)malloc((size_t)k->K);
+    float* a = (float*)malloc((size_t)(k->K / 16) * 4);
+    float* b = (float*)malloc((size_t)(k->K / 16) * 4);
+    for (int64_t n = n0; n < n1; n++) {
+        orc_intdot_decode(k->fmt, k->w + n * k->rowb, k->K, u, a, b);
+        for (int64_t t = 0; t < k->T; t++) {
+            const int8_t* q = k->q + t * k->K;
+            const float* d = k->d + t * (k->K / 32);
+            const float* gs = k->gs + t * (k->K / 16);
+            if (k->y) k->y[t * k->N + n] = orc_intdot_dot(u, a, b, q, d, gs, k->K);
+            if (k->yabs) k->yabs[t * k->N + n] = intdot_abs(u, a, b, q, d, gs, k->K);
+        }
+    }
+    free(u);
+    free(a);
+    free(b);
+}
+
+/* MatMulOp.RunIntDot (MatMulOp.cs:173-213): quantize the T activation rows, then every weight row decoded once
+ * and dotted with each of them; threaded over chunks = clamp(N / 16, 1, threads * 4) row ranges. yabs (may be
+ * null): sum |a d s| + |b gs| per output. y may be null when only yabs is wanted. */
+static int matvec_q8_impl(int fmt, const uint8_t* w, int64_t N, int64_t K, const float* x, int64_t T, float* y,
+                          double* yabs, int threaded)
+{
+    const int super = fmt == ORC_Q4_K || fmt == ORC_Q5_K || fmt == ORC_Q6_K || fmt == ORC_IQ4_XS;
+    if (!orc_intdot_supported(fmt) || K % (super ? 256 : 32)) return -1;
+    int8_t* q = (int8_t*)malloc((size_t)(T * K) + 1);
+    float* d = (float*)malloc((size_t)(T * (K / 32)) * 4 + 4);
+    float* gs = (float*)malloc((size_t)(T * (K / 16)) * 4 + 4);
+    orc_q8_quantize(x, T, K, q, d, gs);
+    int64_t chunks = threaded ? N / 16 : 1;
+    if (chunks < 1) chunks = 1;
+    if (threaded && chunks > (int64_t)g_threads * 4) chunks = (int64_t)g_threads * 4;
+    iv_ctx k = {fmt, w, N, K, T, (N + chunks - 1) / chunks, orc_row_bytes(fmt, K), q, d, gs, y, yabs};
+    if (threaded) parallel_for(chunks, iv_rows, &k);
+    else iv_rows(&k, 0);
+    free(q);
+    free(d);
+    free(gs);
+    return 0;
+}
+
+int orc_matvec_q8(int fmt, const uint8_t* w, int64_t N, int64_t K, const float* x, int64_t T, float* y, double* yabs)
+{
+    return matvec_q8_impl(fmt, w, N, K, x, T, y, yabs, 0);
+}
+
+int orc_matvec_q8_mt(int fmt, const uint8_t* w, int64_t N, int64_t K, const float* x, int64_t T, float* y)
+{
+    return matvec_q8_impl(fmt, w, N, K, x, T, y, NULL, 1);
+}

@@ -106,6 +106,18 @@ void orc_f32_to_f16_mt(const float* x, uint16_t* y, int64_t n);
 int orc_matvec(int fmt, const uint8_t* w, int64_t N, int64_t K, const float* x, int64_t T, float* y);
 int orc_matvec_mt(int fmt, const uint8_t* w, int64_t N, int64_t K, const float* x, int64_t T, float* y);
 
+/* ---- Integer-dot matvec: q8 activations (MatMulOp's IntDot path, IntDot.cs) ----
+ * quantized rows: q int8 [rows][K], d f32 [rows][K/32] (block scales), gs f32 [rows][K/16] (d * sum q per 16) */
+int orc_q8_quantize(const float* x, int64_t rows, int64_t K, int8_t* q, float* d, float* gs);
+/* weight row -> codes u [K], multiplier a and offset b per 16 values (value = a u + b) */
+int orc_intdot_decode(int fmt, const uint8_t* row, int64_t K, uint8_t* u, float* a, float* b);
+float orc_intdot_dot(const uint8_t* u, const float* a, const float* b, const int8_t* q, const float* d, const float* gs,
+                     int64_t K);
+int orc_intdot_supported(int fmt);
+/* y [T, N] (may be null); yabs [T, N] (may be null): sum |a d s| + |b gs| per output */
+int orc_matvec_q8(int fmt, const uint8_t* w, int64_t N, int64_t K, const float* x, int64_t T, float* y, double* yabs);
+int orc_matvec_q8_mt(int fmt, const uint8_t* w, int64_t N, int64_t K, const float* x, int64_t T, float* y);
+
 /* ---- threaded variants for the CPU baseline (CpuParallel.cs:34-78) ---- */
 void orc_set_threads(int threads);
 int orc_get_threads(void);
