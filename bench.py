@@ -314,6 +314,32 @@ class DualMatvec(Workload):
                            self.wu.slot(i), self.N, self.y.slot(i), stream=stream)
 
 
+class DualMatvecQ8(Workload):
+    """The same decode FFN with the reference's default activation numerics: x quantized to q8 per 32 values
+    (one launch), then the integer-dot dual matvec with the SiLU epilogue (the lowerer's "x->q8" and
+    "matmul2 ... int-dot" launches). Bytes counted as for the f32 form (weights, x f32, y f32): the q8 copy's
+    write and read are not algorithmic."""
+
+    def __init__(self, T=1, fmt="q4_k", K=4096, N=14336):
+        self.name = f"dual_matvec_int8_silu_{fmt}_T{T}"
+        self.desc = (f"x f32 [{T}, {K}] -> q8, Wg/Wu {fmt} [{N}, {K}], y = silu(x Wg^T) * (x Wu^T) f32 [{T}, {N}] "
+                     "(two launches)")
+        self.T, self.K, self.N, self.fmt = T, K, N, fmt
+        wg = synth.quant_table(fmt, N, K, seed=0, tid=11)
+        wu = synth.quant_table(fmt, N, K, seed=0, tid=12)
+        x = synth.normal(0, 13, (T, K))
+        self.bytes_per_step = wg.nbytes + wu.nbytes + x.nbytes + T * N * 4
+        R = copies_for(self.bytes_per_step)
+        self.wg, self.wu = Rot(wg, wg.nbytes, R), Rot(wu, wu.nbytes, R)
+        self.x, self.y = Rot(x, x.nbytes, R), Rot(None, T * N * 4, R)
+        self.xq = Rot(None, T * native.q8_row_bytes(K), R)
+
+    def launch(self, i, stream):
+        native.quantize_q8("f32", self.x.slot(i), self.T, self.K, self.xq.slot(i), stream=stream)
+        native.dual_matvec_q8("silu", self.fmt, "f32", self.xq.slot(i), self.T, self.K, self.wg.slot(i),
+                              self.wu.slot(i), self.N, self.y.slot(i), stream=stream)
+
+
 class C5(Workload):
     def __init__(self, fmt):
         self.fmt = fmt
@@ -416,6 +442,9 @@ WORKLOADS = {
     "dual_matvec_silu_q3_k_T1": lambda: DualMatvec(1, "q3_k"),
     "dual_matvec_silu_q3_k_T8": lambda: DualMatvec(8, "q3_k"),
     "dual_matvec_silu_q3_k_T16": lambda: DualMatvec(16, "q3_k"),
+    **{f"dual_matvec_int8_silu_{f}_T{t}": (lambda f=f, t=t: DualMatvecQ8(t, f))
+       for f, t in (("q4_k", 1), ("q6_k", 1), ("q4_0", 1), ("q8_0", 2), ("q5_k", 1), ("iq4_nl", 1), ("mxfp4", 1),
+                    ("q4_k", 4), ("q4_k", 8), ("q6_k", 8), ("q8_0", 16))},
     "copy_256MiB": lambda: CopyRef(),
 }
 
@@ -667,6 +696,27 @@ def cpu_baselines(budget_main: float, budget_op: float, which: set[str]) -> dict
         s, reps = cpu_time(run, budget_op)
         res[name] = dict(s=s * N / n_s, reps=reps, sample=f"{n_s} of {N} weight rows, scaled x{N // n_s}; "
                                                           "MatMul, MatMul, Silu, Mul in f32")
+    for fmt, T in (("q4_k", 1), ("q6_k", 1), ("q4_0", 1), ("q8_0", 2), ("q5_k", 1), ("iq4_nl", 1), ("mxfp4", 1),
+                   ("q4_k", 4), ("q4_k", 8), ("q6_k", 8), ("q8_0", 16)):
+        name = f"dual_matvec_int8_silu_{fmt}_T{T}"
+        if name not in which:
+            continue
+        K, N = 4096, 14336
+        n_s = 3584  # a quarter of the rows: the op is row-independent
+        wg = synth.quant_table(fmt, n_s, K, seed=0, tid=11)
+        wu = synth.quant_table(fmt, n_s, K, seed=0, tid=12)
+        x = synth.normal(0, 13, (T, K))
+        L, P = oracle.lib(), oracle._p
+        g, u, a, yv = (np.empty((T, n_s), np.float32) for _ in range(4))
+
+        def run(fmt=fmt, T=T, x=x, wg=wg, wu=wu, g=g, u=u, a=a, yv=yv):
+            L.orc_matvec_q8_mt(oracle.FORMATS[fmt], P(wg), n_s, K, P(x), T, P(g))
+            L.orc_matvec_q8_mt(oracle.FORMATS[fmt], P(wu), n_s, K, P(x), T, P(u))
+            L.orc_unary_mt(oracle.ACTS["silu"], P(g), P(a), g.size)
+            L.orc_mul_mt(P(a), P(u), P(yv), g.size)
+        s, reps = cpu_time(run, budget_op)
+        res[name] = dict(s=s * N / n_s, reps=reps, sample=f"{n_s} of {N} weight rows, scaled x{N // n_s}; "
+                                                          "MatMul (q8 activations, integer dots) twice, Silu, Mul")
     if "c1_rmsnorm_f32" in which:
         c = synth.c1()
         y = np.empty_like(c["x"])

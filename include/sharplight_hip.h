@@ -251,7 +251,8 @@ SLHIP_API int slhip_rownorm_copies(int kind, int dtype_in, int dtype_out, const 
  *   x: [T, K] f32 or bf16 (dtype_x), 16-byte aligned, row stride x_stride elements (a multiple of 8);
  *   W, Wg, Wu: N rows of K weights in `fmt`, 16-byte aligned: dense F32/F16/BF16 (K a multiple of 8,
  *   K <= 16384), or the GGUF block formats Q8_0/Q4_0/Q4_1/Q5_0/Q5_1 and Q4_K/Q5_K/Q6_K (K a multiple of
- *   256 and the rows' block images fitting in LDS), or Q2_K / Q3_K (K a multiple of 1024); y: [T, N] f32 or bf16 (dtype_y), row stride y_stride.
+ *   256 and the rows' block images fitting in LDS), or Q2_K / Q3_K (K a multiple of 256); y: [T, N] f32 or bf16
+ *   (dtype_y), row stride y_stride.
  *   act: SLHIP_ACT_SILU / GELU_TANH / GELU_ERF, the same forms as slhip_gated_act.
  * Products and sums in f32 (in another order than the CPU provider's, so equal to it within the rounding of
  * a K-term f32 dot product); block formats sum d * sum(x q) + a * sum(x) per block, as the reference's
@@ -275,6 +276,39 @@ SLHIP_API int slhip_matvec(int fmt, int dtype_x, int dtype_y, const void* x, int
 SLHIP_API int slhip_dual_matvec(int act, int fmt, int dtype_x, int dtype_y, const void* x, int64_t x_stride, int64_t T,
                                 int64_t K, const void* w_gate, const void* w_up, int64_t N, void* y, int64_t y_stride,
                                 slhip_stream stream);
+/* slhip_matvec followed by y += bias (bias [N] f32, NULL for none) in the same launch: the reference's matmul
+ * whose only reader adds a constant row vector (FoldMatMulBiases, src/Sharplight.Shaders/Lowering/
+ * GraphLowerer.Fusion.cs:355-408; LowerMatMulBias, GraphLowerer.MatMul.cs:205-245: the same f32 sum as the Add). */
+SLHIP_API int slhip_matvec_bias(int fmt, int dtype_x, int dtype_y, const void* x, int64_t x_stride, int64_t T,
+                                int64_t K, const void* w, int64_t N, const float* bias, void* y, int64_t y_stride,
+                                slhip_stream stream);
+
+/*
+ * Integer-dot decode matvec: the reference's few-row MatMul on quantized weights when activations may be
+ * quantized (src/Sharplight.Cpu/MatMulOp.cs:144-146,173-213 with IntDot.cs; the Vulkan lowerer's int-dot matvec,
+ * src/Sharplight.Shaders/Lowering/GraphLowerer.IntDot.cs:52-117 and Kernels/mmvq.slang). Two steps, so that
+ * several matmuls reading the same x share one quantized copy (GraphLowerer.IntDot.cs:119-220):
+ *
+ * slhip_quantize_q8: x [T, K] f32 or bf16 (row stride x_stride elements, a multiple of 4; x and xq 16-byte
+ *   aligned; K a multiple of 32) -> xq, T rows of slhip_q8_row_bytes(K) = 1.5 K bytes each:
+ *     int8 q[K], then per 32-value block f32 {d, d * sum(q[0..15]), d * sum(q[16..31]), 0},
+ *   with d = amax / 127 and q = (int)(x / d rounded half away from zero through an f32 addition), bit for bit
+ *   IntDot.QuantizeBlockScalar (IntDot.cs:92-126; NaN in a block: d NaN, codes 0).
+ * slhip_matvec_q8 / slhip_dual_matvec_q8: y [T, N] (f32 or bf16, row stride y_stride) = xq . W^T (+ bias[N] f32,
+ *   single form, may be NULL), or act(xq . Wg^T) * (xq . Wu^T). Weights: Q8_0, Q4_0, Q4_1, Q5_0, Q5_1, IQ4_NL,
+ *   MXFP4 (K a multiple of 32, rows of an even number of bytes), Q4_K, Q5_K, Q6_K, IQ4_XS (K a multiple of 256)
+ *   (IntDot.Supports, IntDot.cs:36-38), 16-byte aligned. Per 16 values the
+ *   integer sum s of codes times q is exact; y sums a * d * s + b * gs (w = a * code + b, IntDot.Decode) in f32, in
+ *   another order than IntDot.DotScalar, so within f32 accumulation of those terms of the CPU provider's result.
+ */
+SLHIP_API int64_t slhip_q8_row_bytes(int64_t K);
+SLHIP_API int slhip_quantize_q8(int dtype_x, const void* x, int64_t x_stride, int64_t T, int64_t K, void* xq,
+                                slhip_stream stream);
+SLHIP_API int slhip_matvec_q8(int fmt, int dtype_y, const void* xq, int64_t T, int64_t K, const void* w, int64_t N,
+                              void* y, int64_t y_stride, const float* bias, slhip_stream stream);
+SLHIP_API int slhip_dual_matvec_q8(int act, int fmt, int dtype_y, const void* xq, int64_t T, int64_t K,
+                                   const void* w_gate, const void* w_up, int64_t N, void* y, int64_t y_stride,
+                                   slhip_stream stream);
 
 /*
  * Gated activation out = act(gate) * up over [rows, cols] (IMlpActivation.ActivateGated,
@@ -459,6 +493,8 @@ SLHIP_API int slhip_unary(int op, int dtype_in, int dtype_out, const void* x, vo
  *   input <id> | weight <id> | output <id> | state <id>    (a state -- a KV cache -- has fixed dims, persists
  *                                     across runs, starts at zero and is zeroed again by reset_state)
  *   node <Op> <in,ids> -> <out,ids> [key=value ...]
+ *   option <key>=<value> ...         compile options: reduced_precision=0|1 (CompileOptions.
+ *                                     AllowReducedPrecision), int_dot=lowerer|cpu|off (below)
  * with the StandardOps names and attributes of the reference (src/Sharplight.Core/Graph/StandardOps.cs):
  *   the binary ops Add, Sub, Mul, Div, Max, Min, Pow, Mod (fmod), PRelu, the comparisons and logic ops,
  *   Atan2 (numpy broadcasting), the one-operand ops of slhip_unary_op by name, Scale (scale, bias), Clip
@@ -468,7 +504,16 @@ SLHIP_API int slhip_unary(int op, int dtype_in, int dtype_out, const void* x, vo
  *   style=neox|normal|gptj, freq_scale, attn_factor, sections=s0,s1,s2,s3, interleaved, sections_per_element),
  *   Gather (table [V, D...], ids i32 [N]), Cast,
  *   CacheWrite (state [ctx, ...], x [T, ...][, rows i32 [T,4][, pages i32 [slots, blocks]]]; offset=<scalar
- *   name, default n_past>, slots, block_size): rows n_past + t, or the multi-sequence / paged rows.
+ *   name, default n_past>, slots, block_size): rows n_past + t, or the multi-sequence / paged rows,
+ *   MatMul (x [.., K] f32/bf16, a weight [N, K]; f32_activations): the decode matvec.
+ * A MatMul quantizes x to q8 and runs the integer-dot matvec (slhip_quantize_q8 + slhip_matvec_q8, one q8 copy
+ * per x and row range shared by the matmuls that read it) unless it carries f32_activations=1 and the
+ * compile does not allow reduced precision (GraphLowerer.IntDot.cs:61-62), for the activation row counts of
+ * the rule int_dot names: "lowerer" (default; GraphLowerer.IntDot.cs:18-19,52-75): Q8_0 2..16 rows,
+ * Q4_K/Q5_K/Q6_K and Q4_0/Q5_0/IQ4_NL/MXFP4 1..8 rows; "cpu" (MatMulOp.cs:104,138-147): every format of
+ * IntDot.Supports, 1..31 rows; "off": never. Other row counts take the f32 matvec (IQ4_NL, IQ4_XS and MXFP4
+ * have no f32 matvec: such a run fails with SLHIP_ERR_UNSUPPORTED). A MatMul whose product only feeds an Add
+ * of a constant f32 [N] weight folds the Add into its launch (FoldMatMulBiases).
  * Compile applies the reference lowerer's fusions (Add+RmsNorm, act+Mul, RmsNorm inside Rope, a Rope whose
  * only consumer is a CacheWrite stored into the cache, q/k ropes in one launch); slhip_segment_launches
  * lists the fused launches, one per line. Segments run on a stream
@@ -504,6 +549,9 @@ SLHIP_API int slhip_segment_set_scalar(slhip_segment segment, const char* name, 
 SLHIP_API int slhip_segment_device_bytes(slhip_segment segment, int64_t* bytes);
 /* The fused launches of the compiled segment, one label per line (e.g. "fused[Add]+RmsNorm"). */
 SLHIP_API int slhip_segment_launches(slhip_segment segment, char* buf, size_t size);
+/* The launches a run of `tokens` tokens makes, one per line: the units whose row-count condition holds, each
+ * matvec labelled with the path it takes (" int-dot" or " f32"), a quantization as "x->q8". */
+SLHIP_API int slhip_segment_launches_at(slhip_segment segment, int64_t tokens, char* buf, size_t size);
 /* The launches slhip_segment_compile would create for a segment text, one label per line, decided without
  * touching a device: the lowerer's plan (GraphLowerer.Lower, src/Sharplight.Shaders/Lowering/GraphLowerer.cs:
  * 64-71, without the buffers). Fails as compile would for a node or pattern this provider cannot run. */

@@ -33,11 +33,29 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found")
 
 
+def _includes(path: str, seen: set) -> None:
+    """Adds the csrc/ and include/ headers that path includes, transitively, to seen."""
+    import re
+    try:
+        text = open(path).read()
+    except OSError:
+        return
+    for name in re.findall(r'#include\s+"([^"]+)"', text):
+        for base in (os.path.dirname(path), CSRC, os.path.join(os.path.dirname(HERE), "include")):
+            cand = os.path.normpath(os.path.join(base, name))
+            if os.path.exists(cand):
+                if cand not in seen:
+                    seen.add(cand)
+                    _includes(cand, seen)
+                break
+
+
 def _stale(src: str, obj: str) -> bool:
-    """Whether obj is older than src or than any header under csrc/ or include/."""
+    """Whether obj is older than src or than any header src includes (directly or through other headers)."""
     if not os.path.exists(obj):
         return True
-    deps = [src] + glob.glob(os.path.join(CSRC, "*.h")) + glob.glob(os.path.join(CSRC, "*.hpp")) + glob.glob(os.path.join(os.path.dirname(HERE), "include", "*.h"))
+    deps = {src}
+    _includes(src, deps)
     return max(os.path.getmtime(d) for d in deps) > os.path.getmtime(obj)
 
 

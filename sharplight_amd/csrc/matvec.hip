@@ -43,6 +43,7 @@ struct MatvecArgs {
     int64_t t0;  // first activation row of this launch
     int xt, yt;  // SLHIP_F32 / SLHIP_BF16
     int act;     // dual: SLHIP_ACT_*
+    const float* bias;  // single matvec: [N] f32 added to each output row (FoldMatMulBiases), or null
 };
 
 constexpr int kMvThreads = 512;
@@ -159,6 +160,8 @@ __device__ __forceinline__ void store_row(const MatvecArgs& a, int64_t n, const 
                               : a.act == SLHIP_ACT_GELU_TANH ? activate<SLHIP_ACT_GELU_TANH>(g)
                                                              : activate<SLHIP_ACT_GELU_ERF>(g);
             out = act * au[t];
+        } else if (a.bias) {
+            out = out + a.bias[n];
         }
         int64_t tok = a.t0 + t;
         tok = tok < a.T ? tok : a.T - 1;
@@ -785,6 +788,7 @@ __global__ __launch_bounds__(64 * kMmWaves) void matvec_mfma(MatvecArgs a)
             out = act * au[i];
         }
         if (t < a.T && n < a.N) {
+            if (!DUAL && a.bias) out = out + a.bias[n];
             if (a.yt == SLHIP_F32)
                 static_cast<float*>(a.y)[t * a.ys + n] = out;
             else
@@ -948,6 +952,7 @@ __global__ __launch_bounds__(64 * kMmWaves) void matvec_mfma_lds(MatvecArgs a)
             out = act * su[i];
         }
         if (t < a.T && n < a.N) {
+            if (!DUAL && a.bias) out = out + a.bias[n];
             if (a.yt == SLHIP_F32)
                 static_cast<float*>(a.y)[t * a.ys + n] = out;
             else
@@ -1487,6 +1492,7 @@ __global__ __launch_bounds__(64 * kMqWaves) void matvec_mfma_q(MatvecArgs a)
             out = act * su[i];
         }
         if (t < a.T && n < a.N) {
+            if (!DUAL && a.bias) out = out + a.bias[n];
             if (a.yt == SLHIP_F32)
                 static_cast<float*>(a.y)[t * a.ys + n] = out;
             else
@@ -2143,7 +2149,7 @@ bool matvec_fits(int fmt, int64_t K, bool dual)
 
 static int matvec_common(int fmt, int dtype_x, int dtype_y, const void* x, int64_t x_stride, int64_t T, int64_t K,
                          const void* wg, const void* wu, int64_t N, void* y, int64_t y_stride, int act, bool dual,
-                         slhip_stream stream)
+                         slhip_stream stream, const float* bias = nullptr)
 {
     const char* name = dual ? "dual_matvec" : "matvec";
     if (T < 0 || K < 0 || N < 0) return fail(SLHIP_ERR_INVALID, "%s: negative shape", name);
@@ -2174,7 +2180,7 @@ static int matvec_common(int fmt, int dtype_x, int dtype_y, const void* x, int64
         return fail(SLHIP_ERR_UNSUPPORTED, "%s: rows of %lld bytes are not a multiple of 16 for this weight format",
                     name, static_cast<long long>(wrow));
     MatvecArgs a{x, x_stride, static_cast<const char*>(wg), static_cast<const char*>(wu), wrow, y, y_stride,
-                 T, K, N, 0, dtype_x, dtype_y, act};
+                 T, K, N, 0, dtype_x, dtype_y, act, dual ? nullptr : bias};
     hipStream_t st = to_stream(stream);
     switch (fmt) {
     case SLHIP_FMT_F32: return run_dense<SLHIP_F32>(a, dual, st);
@@ -2202,6 +2208,13 @@ extern "C" SLHIP_API int slhip_matvec(int fmt, int dtype_x, int dtype_y, const v
                                       slhip_stream stream)
 {
     return matvec_common(fmt, dtype_x, dtype_y, x, x_stride, T, K, w, nullptr, N, y, y_stride, 0, false, stream);
+}
+
+extern "C" SLHIP_API int slhip_matvec_bias(int fmt, int dtype_x, int dtype_y, const void* x, int64_t x_stride, int64_t T,
+                                           int64_t K, const void* w, int64_t N, const float* bias, void* y,
+                                           int64_t y_stride, slhip_stream stream)
+{
+    return matvec_common(fmt, dtype_x, dtype_y, x, x_stride, T, K, w, nullptr, N, y, y_stride, 0, false, stream, bias);
 }
 
 extern "C" SLHIP_API int slhip_dual_matvec(int act, int fmt, int dtype_x, int dtype_y, const void* x, int64_t x_stride,

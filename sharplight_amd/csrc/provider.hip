@@ -246,6 +246,10 @@ struct Node {
 struct Graph {
     std::map<int, Value> values;
     std::vector<Node> nodes;
+    // Compile options (`option key=value` lines): reduced_precision (CompileOptions.AllowReducedPrecision,
+    // src/Sharplight.Core/Runtime/CompileOptions.cs:23) and int_dot, the rule that picks the integer-dot matvec
+    // (see IntDotPolicy).
+    std::map<std::string, std::string> options;
 
     Value& value(int id)
     {
@@ -336,6 +340,21 @@ Graph parse(const char* text)
                 Value& v = g.value(id);
                 (kw == "input" ? v.input : kw == "weight" ? v.weight : kw == "output" ? v.output : v.state) = true;
                 if (v.state && v.symbolic()) invalid("state " + std::to_string(id) + " must have fixed dims");
+            } else if (kw == "option") {
+                std::string kv;
+                while (ls >> kv) {
+                    const size_t eq = kv.find('=');
+                    if (eq == std::string::npos) invalid("option '" + kv + "' is not key=value");
+                    const std::string k = kv.substr(0, eq), v = kv.substr(eq + 1);
+                    if (k == "reduced_precision") {
+                        if (v != "0" && v != "1" && v != "true" && v != "false") invalid("reduced_precision is 0 or 1");
+                    } else if (k == "int_dot") {
+                        if (v != "lowerer" && v != "cpu" && v != "off") invalid("int_dot is lowerer, cpu or off");
+                    } else {
+                        invalid("unknown option '" + k + "'");
+                    }
+                    g.options[k] = v;
+                }
             } else if (kw == "node") {
                 Node n = parse_node(ls);
                 for (int id : n.in) g.value(id);
@@ -443,6 +462,68 @@ bool flag(const Node& n, const char* key)
     return v == "true" || v == "True" || v == "1";
 }
 
+}  // namespace
+bool matvec_q8_fits(int fmt, int64_t K, bool dual);  // matvec_i8.hip
+namespace {
+
+// When a MatMul quantizes its activations to q8 and takes the integer-dot matvec, and for which activation
+// row counts. The node may not when it carries f32_activations, unless the compile allows reduced precision
+// (QuantizedActivationsAllowed, src/Sharplight.Shaders/Lowering/GraphLowerer.IntDot.cs:61-62;
+// CpuCompiledSegment.LowerLinear.cs:39). Rules (option int_dot):
+//   lowerer (default) -- the Vulkan lowerer's UseIntDotMatvec (GraphLowerer.IntDot.cs:52-55,68-75; IntDotMaxRows
+//     :18-19; IntDotFirstRow, GraphLowerer.RowInvariance.cs:21-25): Q8_0 from 2 to 16 rows, Q4_K/Q5_K/Q6_K (K a
+//     multiple of 256) and the 32-value block formats Q4_0/Q5_0/IQ4_NL/MXFP4 (SHARPLIGHT_MMVQ_BLOCK, on by
+//     default) from 1 to 8 rows;
+//   cpu -- the CPU provider's MatMulOp (MatMulOp.cs:104,138-147): every IntDot.Supports format (IntDot.cs:36-38)
+//     below IntDotGemmMinRows (32) rows;
+//   off -- never (a device without DeviceFeatures.IntDot).
+struct IntDotRange {
+    int64_t lo = 0, hi = -1;  // rows lo..hi take the integer-dot matvec; empty when hi < lo
+    bool any() const { return hi >= lo; }
+    bool covers(int64_t r) const { return r >= lo && r <= hi; }
+};
+
+IntDotRange int_dot_range(const Graph& g, const Node& mm, DType w, int64_t K)
+{
+    IntDotRange r;
+    auto opt = [&](const char* k, const char* d) {
+        auto it = g.options.find(k);
+        return it == g.options.end() ? std::string(d) : it->second;
+    };
+    const std::string policy = opt("int_dot", "lowerer");
+    const std::string rp = opt("reduced_precision", "0");
+    const bool reduced = rp == "1" || rp == "true";
+    if (policy == "off" || (!reduced && flag(mm, "f32_activations"))) return r;
+    const bool candidate = w == DType::Q8_0 || w == DType::Q4_0 || w == DType::Q4_1 || w == DType::Q5_0 ||
+                           w == DType::Q5_1 || w == DType::Q4_K || w == DType::Q5_K || w == DType::Q6_K ||
+                           w == DType::IQ4_NL || w == DType::IQ4_XS || w == DType::MXFP4;
+    if (!candidate) return r;
+    const int fmt = format_code(w);
+    if (!matvec_q8_fits(fmt, K, false)) return r;
+    const bool kq = w == DType::Q4_K || w == DType::Q5_K || w == DType::Q6_K;
+    if (policy == "cpu") {
+        r.lo = 1;
+        r.hi = 31;
+        return r;
+    }
+    if (w == DType::Q8_0) {
+        r.lo = 2;
+        r.hi = 16;
+    } else if ((kq && K % 256 == 0) || w == DType::Q4_0 || w == DType::Q5_0 || w == DType::IQ4_NL || w == DType::MXFP4) {
+        r.lo = 1;
+        r.hi = 8;
+    }
+    return r;
+}
+
+// Weight formats the f32-activation matvec reads (slhip_matvec); the others run on the integer-dot path only.
+bool float_matvec_format(DType t)
+{
+    return t == DType::F32 || t == DType::F16 || t == DType::BF16 || t == DType::Q8_0 || t == DType::Q4_0 ||
+           t == DType::Q4_1 || t == DType::Q5_0 || t == DType::Q5_1 || t == DType::Q2_K || t == DType::Q3_K ||
+           t == DType::Q4_K || t == DType::Q5_K || t == DType::Q6_K;
+}
+
 Support supports(const Graph& g, const Node& n)
 {
     auto no = [](const std::string& r) { return Support{false, r}; };
@@ -529,21 +610,23 @@ Support supports(const Graph& g, const Node& n)
         if (x.type != DType::F32 && x.type != DType::BF16) return no("MatMul: f32 or bf16 activations");
         if (y.type != DType::F32 && y.type != DType::BF16) return no("MatMul: f32 or bf16 output");
         if (!w.weight || w.dims.size() != 2) return no("MatMul: the second operand must be a weight [N, K]");
-        const bool dense = w.type == DType::F32 || w.type == DType::F16 || w.type == DType::BF16;
-        const bool kq = w.type == DType::Q4_K || w.type == DType::Q5_K || w.type == DType::Q6_K ||
-                        w.type == DType::Q2_K || w.type == DType::Q3_K;
-        const bool blocks = w.type == DType::Q8_0 || w.type == DType::Q4_0 || w.type == DType::Q4_1 ||
-                            w.type == DType::Q5_0 || w.type == DType::Q5_1 || kq;
-        if (!dense && !blocks)
-            return no("MatMul: f32, f16, bf16, Q8_0/Q4_0/Q4_1/Q5_0/Q5_1 or Q2_K/Q3_K/Q4_K/Q5_K/Q6_K weights on this provider");
         if (x.dims.empty() || w.dims[1] != x.last()) return no("MatMul: K mismatch");
         if (y.last() != w.dims[0]) return no("MatMul: output must be [.., N]");
         const int64_t K = x.last();
-        if (dense && (K % 8 != 0 || K > 16384)) return no("MatMul: K must be a multiple of 8 and at most 16384");
-        if (blocks && (K % 256 != 0 || K > 16384)) return no("MatMul: block-format K must be a multiple of 256, at most 16384");
-        if (!matvec_fits(format_code(w.type), K, false))
-            return no("MatMul: the weight rows do not fit the matvec's staging (Q2_K, Q3_K: K a multiple of 1024)");
-        return {true, ""};
+        const bool dense = w.type == DType::F32 || w.type == DType::F16 || w.type == DType::BF16;
+        const IntDotRange id = int_dot_range(g, n, w.type, K);
+        if (float_matvec_format(w.type)) {
+            if (dense && (K % 8 != 0 || K > 16384)) return no("MatMul: K must be a multiple of 8 and at most 16384");
+            if (!dense && (K % 256 != 0 || K > 16384)) return no("MatMul: block-format K must be a multiple of 256, at most 16384");
+            if (!matvec_fits(format_code(w.type), K, false))
+                return no("MatMul: the weight rows do not fit the matvec's staging");
+            return {true, ""};
+        }
+        // no f32 matvec for the format: the integer-dot path must serve every row count from one (compile
+        // refuses a token bound whose row count passes the range's end)
+        if (id.any() && id.lo == 1) return {true, ""};
+        return no("MatMul: f32, f16, bf16, Q8_0/Q4_0/Q4_1/Q5_0/Q5_1 or Q2_K..Q6_K weights (IQ4_NL, IQ4_XS and MXFP4 "
+                  "only with quantized activations, the integer-dot matvec) on this provider");
     }
     return no("op " + op + " is not on the fused-layer-op path of the HIP provider");
 }
@@ -551,7 +634,7 @@ Support supports(const Graph& g, const Node& n)
 // ---- lowering into fused units -------------------------------------------------------------------------
 
 struct Unit {
-    enum Kind { RowNorm, Gated, Rope, Gather, Cast, CacheWrite, Matvec, Binary, Unary } kind;
+    enum Kind { RowNorm, Gated, Rope, Gather, Cast, CacheWrite, Matvec, Binary, Unary, QuantizeQ8 } kind;
     std::string label;
     // RowNorm
     int norm = SLHIP_NORM_RMS;
@@ -561,8 +644,12 @@ struct Unit {
     float eps = 0.f;
     // Gated
     int act = SLHIP_ACT_SILU, gate = -1, up = -1;
-    // Matvec: x . Wg^T, or act(x . Wg^T) * (x . Wu^T) when wu >= 0
+    // Matvec: x . Wg^T (+ bias), or act(x . Wg^T) * (x . Wu^T) when wu >= 0
     int wg = -1, wu = -1;
+    int mm_node = -1;   // the (gate) MatMul node
+    int bias = -1;      // an absorbed Add of a constant f32 row vector [N] (FoldMatMulBiases)
+    IntDotRange q8;     // Matvec / QuantizeQ8: the activation rows that take the integer-dot path
+    int q8buf = -1;     // the quantized copy of x (scratch buffer index) the integer-dot path reads
     // Rope: up to 4 tensors sharing positions and settings
     struct RopeTensor {
         int x, y, w;
@@ -592,6 +679,7 @@ public:
             if (!s.ok) unsupported(s.reason);
         }
         lower();
+        assign_q8();
         if (plan_only) return;
         check(slhip_stream_create(&stream_));
         allocate();
@@ -601,6 +689,7 @@ public:
     ~Segment()
     {
         for (auto& kv : mem_) slhip_free(kv.second);
+        for (void* p : scratch_) slhip_free(p);
         if (stream_) slhip_stream_destroy(stream_);
     }
 
@@ -659,11 +748,35 @@ public:
         return s;
     }
 
+    // The launches a run of T tokens makes: the units whose row-count condition holds, each matvec with the
+    // path it takes at that count.
+    std::string launches_at(int64_t T) const
+    {
+        std::string s;
+        for (const Unit& u : units_) {
+            if (u.kind == Unit::QuantizeQ8 || u.kind == Unit::Matvec) {
+                const int64_t rows = g_.value(u.x).rows(T);
+                if (rows == 0) continue;
+                if (u.kind == Unit::QuantizeQ8) {
+                    if (u.q8.covers(rows)) s += "x->q8\n";
+                    continue;
+                }
+                std::string l = u.label.substr(0, u.label.find(" (int-dot"));
+                s += l + (u.q8.covers(rows) ? " int-dot\n" : " f32\n");
+                continue;
+            }
+            s += u.label + "\n";
+        }
+        return s;
+    }
+
 private:
     Graph g_;
     int64_t max_t_, t_ = 0;
     std::vector<Unit> units_;
     std::map<int, void*> mem_;
+    std::vector<int64_t> scratch_bytes_;  // the quantized activation copies (assign_q8)
+    std::vector<void*> scratch_;
     std::map<std::string, int64_t> scalars_;
     int64_t device_bytes_ = 0;
     slhip_stream stream_ = nullptr;
@@ -733,6 +846,7 @@ private:
                 u.wu = g_.nodes[d.mm_up].in[1];
                 u.act = d.act;
                 u.y = n.out[0];
+                u.mm_node = d.mm_gate;
                 u.label = "matvec2+fused[" + g_.nodes[d.act_node].op + ",Mul]";
                 units_.push_back(u);
                 done[k] = true;
@@ -816,7 +930,9 @@ private:
                 u.x = n.in[0];
                 u.wg = n.in[1];
                 u.y = n.out[0];
+                u.mm_node = static_cast<int>(k);
                 u.label = "matvec";
+                fold_bias(u, cons, done, single_use);
                 units_.push_back(u);
             } else if (n.op == "CacheWrite") {
                 Unit u{Unit::CacheWrite};
@@ -913,7 +1029,11 @@ private:
                 const Value& wu = g_.value(mu.in[1]);
                 if (mg.in[0] != mu.in[0] || wg.type != wu.type || wg.dims != wu.dims) continue;
                 if (!single_use(mg.out[0]) || !single_use(mu.out[0]) || !single_use(g_.nodes[a].out[0])) continue;
-                if (!matvec_fits(format_code(wg.type), wg.dims[1], true)) continue;  // two matvecs + the gated unit
+                // two matvecs + the gated unit when neither path fits the pair
+                const bool fits_f32 = float_matvec_format(wg.type) && matvec_fits(format_code(wg.type), wg.dims[1], true);
+                if (!fits_f32 && !(int_dot_range(g_, mg, wg.type, wg.dims[1]).any() &&
+                                   matvec_q8_fits(format_code(wg.type), wg.dims[1], true)))
+                    continue;
                 if (g_.value(mg.out[0]).type != DType::F32 || g_.value(mu.out[0]).type != DType::F32 ||
                     g_.value(g_.nodes[a].out[0]).type != DType::F32)
                     continue;  // the unfused graph rounds nothing between the products and the Mul
@@ -926,6 +1046,69 @@ private:
             }
         }
         (void)cons;
+    }
+
+    // A MatMul whose product is read only by an Add of a constant f32 row vector [N] (a weight) with an f32
+    // result of the product's shape: the Add joins the matvec launch (FoldMatMulBiases,
+    // src/Sharplight.Shaders/Lowering/GraphLowerer.Fusion.cs:355-408; LowerMatMulBias, GraphLowerer.MatMul.cs:205-245).
+    template <class F>
+    void fold_bias(Unit& u, std::map<int, std::vector<int>>& cons, std::vector<bool>& done, F single_use)
+    {
+        const int prod = u.y;
+        if (!single_use(prod) || g_.value(prod).type != DType::F32) return;
+        const int c = cons[prod][0];
+        const Node& a = g_.nodes[c];
+        if (a.op != "Add" || a.in.size() != 2 || done[c] || a.in[0] == a.in[1]) return;
+        const int b = a.in[0] == prod ? a.in[1] : a.in[0];
+        const Value& bv = g_.value(b);
+        const Value& wv = g_.value(u.wg);
+        const Value& ov = g_.value(a.out[0]);
+        if (!bv.weight || bv.type != DType::F32 || bv.dims.size() != 1 || bv.dims[0] != wv.dims[0] ||
+            ov.type != DType::F32 || ov.dims != g_.value(prod).dims)
+            return;
+        u.bias = b;
+        u.y = a.out[0];
+        u.label += "+bias";
+        done[c] = true;
+    }
+
+    // The integer-dot range of every matvec unit, and the quantized copies of x they read: one per (x, row
+    // range), made by a quantization launch placed before the first matvec that reads it and run for the row
+    // counts of that range -- the lowerer's shared q8 copies (QuantizedActivations, GraphLowerer.IntDot.cs:119-220).
+    void assign_q8()
+    {
+        std::map<std::tuple<int, int64_t, int64_t>, int> bufs;
+        std::vector<Unit> out;
+        for (Unit& u : units_) {
+            if (u.kind == Unit::Matvec) {
+                const Value& wv = g_.value(u.wg);
+                u.q8 = int_dot_range(g_, g_.nodes[u.mm_node], wv.type, wv.dims[1]);
+                const int64_t max_rows = g_.value(u.x).rows(max_t_);
+                if (!float_matvec_format(wv.type) && max_rows > u.q8.hi)
+                    unsupported(std::string("MatMul of ") + type_info(wv.type).name + " weights runs on the integer-dot "
+                                "matvec only, up to " + std::to_string(u.q8.hi) + " activation rows; the segment may "
+                                "run " + std::to_string(max_rows));
+                if (u.q8.any()) {
+                    const auto key = std::make_tuple(u.x, u.q8.lo, u.q8.hi);
+                    auto it = bufs.find(key);
+                    if (it == bufs.end()) {
+                        Unit q{Unit::QuantizeQ8};
+                        q.x = u.x;
+                        q.q8 = u.q8;
+                        q.q8buf = static_cast<int>(scratch_bytes_.size());
+                        const Value& xv = g_.value(u.x);
+                        scratch_bytes_.push_back(xv.rows(max_t_) * slhip_q8_row_bytes(xv.last()));
+                        q.label = "x->q8 rows " + std::to_string(q.q8.lo) + ".." + std::to_string(q.q8.hi);
+                        it = bufs.emplace(key, q.q8buf).first;
+                        out.push_back(q);
+                    }
+                    u.q8buf = it->second;
+                    u.label += " (int-dot rows " + std::to_string(u.q8.lo) + ".." + std::to_string(u.q8.hi) + ")";
+                }
+            }
+            out.push_back(u);
+        }
+        units_.swap(out);
     }
 
     // A Cast of an f32 norm output to f16 is the f16 copy the norm writes beside its rows: the norm's f32
@@ -1023,6 +1206,12 @@ private:
             mem_[kv.first] = p;
             device_bytes_ += n;
         }
+        for (int64_t n : scratch_bytes_) {
+            void* p = nullptr;
+            check(slhip_malloc(&p, static_cast<size_t>(n > 0 ? n : 0)));
+            scratch_.push_back(p);
+            device_bytes_ += n;
+        }
     }
 
     void* ptr(int id) const { return id < 0 ? nullptr : mem_.at(id); }
@@ -1086,17 +1275,40 @@ private:
                                        u.y16 >= 0 ? &copies : nullptr, stream_));
             break;
         }
+        case Unit::QuantizeQ8: {
+            const Value& xv = g_.value(u.x);
+            const int64_t K = xv.last(), rows = xv.rows(T);
+            if (u.q8.covers(rows))
+                check(slhip_quantize_q8(act_code(xv.type), ptr(u.x), K, rows, K, scratch_.at(u.q8buf), stream_));
+            break;
+        }
         case Unit::Matvec: {
             const Value& xv = g_.value(u.x);
             const Value& wv = g_.value(u.wg);
             const int64_t K = xv.last(), rows = xv.rows(T), Nw = wv.dims[0];
             const int fmt = format_code(wv.type);
             const int dy = act_code(g_.value(u.y).type);
+            const float* bias = static_cast<const float*>(ptr(u.bias));
+            if (rows == 0) break;
+            if (u.q8.covers(rows)) {
+                void* xq = scratch_.at(u.q8buf);
+                if (u.wu >= 0)
+                    check(slhip_dual_matvec_q8(u.act, fmt, dy, xq, rows, K, ptr(u.wg), ptr(u.wu), Nw, ptr(u.y), Nw, stream_));
+                else
+                    check(slhip_matvec_q8(fmt, dy, xq, rows, K, ptr(u.wg), Nw, ptr(u.y), Nw, bias, stream_));
+                break;
+            }
+            if (!float_matvec_format(wv.type))  // refused at compile; kept as a guard
+                unsupported(std::string("MatMul of ") + type_info(wv.type).name + " weights [" + std::to_string(Nw) +
+                            ", " + std::to_string(K) + "] runs on the integer-dot matvec only, for " +
+                            std::to_string(u.q8.lo) + ".." + std::to_string(u.q8.hi) + " activation rows; this run has " +
+                            std::to_string(rows));
             if (u.wu >= 0)
                 check(slhip_dual_matvec(u.act, fmt, act_code(xv.type), dy, ptr(u.x), K, rows, K, ptr(u.wg), ptr(u.wu), Nw,
                                         ptr(u.y), Nw, stream_));
             else
-                check(slhip_matvec(fmt, act_code(xv.type), dy, ptr(u.x), K, rows, K, ptr(u.wg), Nw, ptr(u.y), Nw, stream_));
+                check(slhip_matvec_bias(fmt, act_code(xv.type), dy, ptr(u.x), K, rows, K, ptr(u.wg), Nw, bias, ptr(u.y), Nw,
+                                        stream_));
             break;
         }
         case Unit::Gated: {
@@ -1264,6 +1476,7 @@ SLHIP_API int slhip_segment_describe(const char* segment_ir, char* buf, size_t s
     return guarded([&] {
         const Graph g = parse(segment_ir);
         std::string out;
+        for (const auto& [k, v] : g.options) out += "option " + k + "=" + v + "\n";
         for (const auto& [id, v] : g.values) {
             out += "value " + std::to_string(id) + " " + type_info(v.type).name;
             for (int64_t d : v.dims) out += " " + (d == kSymT ? std::string("T") : std::to_string(d));
@@ -1326,6 +1539,15 @@ SLHIP_API int slhip_segment_launches(slhip_segment segment, char* buf, size_t si
     return guarded([&] {
         if (!segment || !buf || !size) invalid("null argument");
         snprintf(buf, size, "%s", static_cast<Segment*>(segment)->launches().c_str());
+    });
+}
+
+SLHIP_API int slhip_segment_launches_at(slhip_segment segment, int64_t tokens, char* buf, size_t size)
+{
+    return guarded([&] {
+        if (!segment || !buf || !size) invalid("null argument");
+        if (tokens < 0) invalid("T must not be negative");
+        put_text(static_cast<Segment*>(segment)->launches_at(tokens), buf, size);
     });
 }
 

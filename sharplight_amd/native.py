@@ -180,6 +180,11 @@ SIGNATURES = {
                                   ctypes.POINTER(NormCopies), _P]),
     "slhip_matvec": (_I, [_I, _I, _I, _P, _I64, _I64, _I64, _P, _I64, _P, _I64, _P]),
     "slhip_dual_matvec": (_I, [_I, _I, _I, _I, _P, _I64, _I64, _I64, _P, _P, _I64, _P, _I64, _P]),
+    "slhip_matvec_bias": (_I, [_I, _I, _I, _P, _I64, _I64, _I64, _P, _I64, _P, _P, _I64, _P]),
+    "slhip_q8_row_bytes": (_I64, [_I64]),
+    "slhip_quantize_q8": (_I, [_I, _P, _I64, _I64, _I64, _P, _P]),
+    "slhip_matvec_q8": (_I, [_I, _I, _P, _I64, _I64, _P, _I64, _P, _I64, _P, _P]),
+    "slhip_dual_matvec_q8": (_I, [_I, _I, _I, _P, _I64, _I64, _P, _P, _I64, _P, _I64, _P]),
     "slhip_gated_act": (_I, [_I, _I, _I, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P]),
     "slhip_rope": (_I, [_I, _I, ctypes.POINTER(RopeTensor), _I, _P, _P, _I64, _I64, ctypes.POINTER(RopeCfg), _P]),
     "slhip_gather": (_I, [_I, _P, _I64, _I64, _P, _I64, _I, _P, _I64, _P]),
@@ -197,6 +202,7 @@ SIGNATURES = {
     "slhip_segment_set_scalar": (_I, [_P, ctypes.c_char_p, _I64]),
     "slhip_segment_device_bytes": (_I, [_P, ctypes.POINTER(_I64)]),
     "slhip_segment_launches": (_I, [_P, ctypes.c_char_p, _SZ]),
+    "slhip_segment_launches_at": (_I, [_P, _I64, ctypes.c_char_p, _SZ]),
     "slhip_segment_plan": (_I, [ctypes.c_char_p, ctypes.c_char_p, _SZ]),
     "slhip_segment_describe": (_I, [ctypes.c_char_p, ctypes.c_char_p, _SZ]),
     "slhip_segment_destroy": (_I, [_P]),
@@ -434,12 +440,42 @@ def matvec(fmt, dtype_x, dtype_y, x, T, K, w, N, y, *, x_stride=None, y_stride=N
          K if x_stride is None else x_stride, T, K, ptr(w), N, ptr(y), N if y_stride is None else y_stride, stream)
 
 
+def matvec_bias(fmt, dtype_x, dtype_y, x, T, K, w, N, bias, y, *, x_stride=None, y_stride=None, stream=None):
+    """y [T, N] = x [T, K] . W^T + bias[N] (one launch)."""
+    call("slhip_matvec_bias", FORMATS.get(fmt, fmt), DTYPES.get(dtype_x, dtype_x), DTYPES.get(dtype_y, dtype_y),
+         ptr(x), K if x_stride is None else x_stride, T, K, ptr(w), N, ptr(bias), ptr(y),
+         N if y_stride is None else y_stride, stream)
+
+
 def dual_matvec(act, fmt, dtype_x, dtype_y, x, T, K, w_gate, w_up, N, y, *, x_stride=None, y_stride=None,
                 stream=None):
     """y [T, N] = act(x . Wg^T) * (x . Wu^T)."""
     call("slhip_dual_matvec", ACTS.get(act, act), FORMATS.get(fmt, fmt), DTYPES.get(dtype_x, dtype_x),
          DTYPES.get(dtype_y, dtype_y), ptr(x), K if x_stride is None else x_stride, T, K, ptr(w_gate), ptr(w_up), N,
          ptr(y), N if y_stride is None else y_stride, stream)
+
+
+def q8_row_bytes(K) -> int:
+    """Bytes of one quantized activation row of K values (slhip_quantize_q8's layout)."""
+    return int(lib().slhip_q8_row_bytes(K))
+
+
+def quantize_q8(dtype_x, x, T, K, xq, *, x_stride=None, stream=None):
+    """x [T, K] (f32 / bf16) -> the int-dot matvec's quantized rows at xq ([T, q8_row_bytes(K)] bytes)."""
+    call("slhip_quantize_q8", DTYPES.get(dtype_x, dtype_x), ptr(x), K if x_stride is None else x_stride, T, K,
+         ptr(xq), stream)
+
+
+def matvec_q8(fmt, dtype_y, xq, T, K, w, N, y, *, y_stride=None, bias=None, stream=None):
+    """y [T, N] = x . W^T + bias on the quantized rows xq (integer dots)."""
+    call("slhip_matvec_q8", FORMATS.get(fmt, fmt), DTYPES.get(dtype_y, dtype_y), ptr(xq), T, K, ptr(w), N, ptr(y),
+         N if y_stride is None else y_stride, ptr(bias), stream)
+
+
+def dual_matvec_q8(act, fmt, dtype_y, xq, T, K, w_gate, w_up, N, y, *, y_stride=None, stream=None):
+    """y [T, N] = act(x . Wg^T) * (x . Wu^T) on the quantized rows xq (integer dots)."""
+    call("slhip_dual_matvec_q8", ACTS.get(act, act), FORMATS.get(fmt, fmt), DTYPES.get(dtype_y, dtype_y), ptr(xq), T,
+         K, ptr(w_gate), ptr(w_up), N, ptr(y), N if y_stride is None else y_stride, stream)
 
 
 def gated_act(act, dtype_in, dtype_out, gate, up, out, rows, cols, *, gate_stride=None, up_stride=None,

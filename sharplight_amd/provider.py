@@ -71,6 +71,9 @@ class GraphBuilder:
         self.weights: list[Value] = []
         self.outputs: list[Value] = []
         self.states: list[Value] = []
+        # compile options: reduced_precision (CompileOptions.AllowReducedPrecision) and int_dot
+        # ("lowerer" | "cpu" | "off": which rule picks the integer-dot matvec)
+        self.options: dict = {}
 
     def value(self, type: str, *dims) -> Value:
         v = Value(len(self.values), type, tuple(dims))
@@ -158,9 +161,11 @@ class GraphBuilder:
         d = table.dims[1:]
         return self.emit("Gather", [table, ids], out_type, (ids.dims[0],) + tuple(d))
 
-    def matmul(self, x, w, out_type="f32"):
-        """StandardOps.MatMul: x [.., K] . W^T, W a weight [N, K] -> [.., N]."""
-        return self.emit("MatMul", [x, w], out_type, tuple(x.dims[:-1]) + (w.dims[0],))
+    def matmul(self, x, w, out_type="f32", f32_activations=None):
+        """StandardOps.MatMul: x [.., K] . W^T, W a weight [N, K] -> [.., N]; f32_activations=True keeps x
+        unquantized (StandardOps.F32ActivationsAttribute, src/Sharplight.Core/Graph/StandardOps.cs:135)."""
+        attrs = {} if f32_activations is None else {"f32_activations": f32_activations}
+        return self.emit("MatMul", [x, w], out_type, tuple(x.dims[:-1]) + (w.dims[0],), **attrs)
 
     def cast(self, x, to: str):
         return self.emit("Cast", [x], to, x.dims)
@@ -176,7 +181,7 @@ class GraphBuilder:
         self.nodes.append(Node("CacheWrite", [v for v in (state, x, rows, pages) if v is not None], [], attrs))
 
     def to_ir(self) -> str:
-        lines = []
+        lines = [f"option {k}={_fmt(v)}" for k, v in self.options.items()]
         for v in self.values:
             lines.append(f"value {v.id} {v.type} " + " ".join(str(d) for d in v.dims))
         for v in self.inputs:
@@ -377,6 +382,12 @@ class CompiledSegment:
     def launches(self) -> list[str]:
         buf = ctypes.create_string_buffer(8192)
         native.call("slhip_segment_launches", self.handle, buf, len(buf))
+        return [s for s in buf.value.decode().split("\n") if s]
+
+    def launches_at(self, tokens: int) -> list[str]:
+        """The launches a run of ``tokens`` tokens makes (each matvec with the path it takes)."""
+        buf = ctypes.create_string_buffer(8192)
+        native.call("slhip_segment_launches_at", self.handle, tokens, buf, len(buf))
         return [s for s in buf.value.decode().split("\n") if s]
 
     def close(self) -> None:

@@ -81,13 +81,14 @@ def test_residual_add_rmsnorm_fuses(dev, h_is_output):
                                         ("q3_k", 2, False)])                      # Q3_K: matrix cores always
 def test_swiglu_dual_matvec_fuses(dev, fmt, T, swap):
     """FusionTests.SwiGluDualMatvec (FusionTests.cs:59-80): Mul(Silu(x Wg^T), x Wu^T) is one dual matvec launch
-    (in either operand order), within the f32 dot-product bound of the unfused CPU computation."""
+    (in either operand order), within the f32 dot-product bound of the unfused CPU computation. The matmuls
+    carry f32_activations, so x stays f32 (the float-row path); the integer-dot form is tested below."""
     K, N = 1024, 96
     g = GraphBuilder()
     x = g.input("f32", "T", K)
     wg = g.weight(fmt, N, K)
     wu = g.weight(fmt, N, K)
-    gate, up = g.matmul(x, wg), g.matmul(x, wu)
+    gate, up = g.matmul(x, wg, f32_activations=True), g.matmul(x, wu, f32_activations=True)
     y = g.output(g.mul(up, g.silu(gate)) if swap else g.mul(g.silu(gate), up))
     rg = synth.quant_table(fmt, N, K, seed=8, tid=1)
     ru = synth.quant_table(fmt, N, K, seed=8, tid=2)
@@ -445,3 +446,109 @@ def test_mrope_graph_one_launch(dev):
             xn = oracle.rmsnorm(oracle.from_bf16(x).reshape(-1, 128), w, 1e-6).reshape(x.shape)
             ref = oracle.to_bf16(oracle.rope_multi(xn, ps, [24, 20, 20, 0], interleaved=True, base=5e6))
             assert_bf16_close(seg.get_output(y), ref, what="mrope")
+
+
+@pytest.mark.parametrize("fmt,T", [("q4_k", 1), ("q4_k", 8), ("q4_k", 9), ("q6_k", 3), ("q8_0", 1), ("q8_0", 2),
+                                   ("mxfp4", 4), ("q4_0", 5)])
+def test_swiglu_dual_matvec_int_dot(dev, fmt, T):
+    """The decode FFN's gate/up pair by default (the lowerer's rule): x quantized once to q8, one dual int-dot
+    launch for the row counts of the format's range (Q4_K/Q6_K/Q4_0/MXFP4 1..8, Q8_0 2..16), the f32 dual matvec
+    outside it (GraphLowerer.MatMul.cs:150-158; GraphLowerer.IntDot.cs:18-19,52-75). Parity: against the oracle's
+    integer-dot restatement inside the range, the float-row path outside."""
+    K, N = 2048, 96
+    g = GraphBuilder()
+    x = g.input("f32", "T", K)
+    wg = g.weight(fmt, N, K)
+    wu = g.weight(fmt, N, K)
+    y = g.output(g.mul(g.silu(g.matmul(x, wg)), g.matmul(x, wu)))
+    rg = synth.quant_table(fmt, N, K, seed=12, tid=1)
+    ru = synth.quant_table(fmt, N, K, seed=12, tid=2)
+    xs = synth.normal(12, 3, (T, K))
+    lo, hi = (2, 16) if fmt == "q8_0" else (1, 8)
+    int_dot = lo <= T <= hi
+    with dev.compile(g, max_tokens=8 if fmt == "mxfp4" else 16) as seg:
+        assert seg.launches == [f"x->q8 rows {lo}..{hi}", f"matvec2+fused[Silu,Mul] (int-dot rows {lo}..{hi})"]
+        assert seg.launches_at(T) == (["x->q8", "matvec2+fused[Silu,Mul] int-dot"] if int_dot
+                                      else ["matvec2+fused[Silu,Mul] f32"])
+        seg.set_input(x, xs)
+        seg.set_input(wg, rg)
+        seg.set_input(wu, ru)
+        log(f"provider dual int-dot matvec {fmt} T={T}")
+        seg.execute(T)
+        got = seg.get_output(y).astype(np.float64)
+    if int_dot:
+        gr, Sg = oracle.matvec_q8(fmt, rg, N, K, xs, with_abs=True)
+        ur, Su = oracle.matvec_q8(fmt, ru, N, K, xs, with_abs=True)
+    else:
+        gr, ur = oracle.matvec(fmt, rg, N, K, xs), oracle.matvec(fmt, ru, N, K, xs)
+        from tests.test_gpu_matvec import _abs_terms
+        ax = np.abs(xs).astype(np.float64)
+        Wg = oracle.dequant(fmt, rg.reshape(-1), N * K).reshape(N, K)
+        Wu = oracle.dequant(fmt, ru.reshape(-1), N * K).reshape(N, K)
+        Sg, Su = ax @ _abs_terms(fmt, rg, Wg).T, ax @ _abs_terms(fmt, ru, Wu).T
+    ref = oracle.mul(oracle.unary("silu", gr), ur).astype(np.float64)
+    tol = 2.0 ** -16 * (1.1 * np.abs(ur) * Sg + np.abs(gr) * Su) + 1e-5 * np.abs(ref)
+    assert (np.abs(got - ref) <= tol + 1e-30).all()
+
+
+def test_qkv_projections_share_one_q8_copy_and_fold_biases(dev):
+    """Three biased projections of one x (a Qwen2-style attention input): one quantization, three int-dot
+    launches with the biases folded in (FoldMatMulBiases), and a Q8_0 projection of the same x with its own
+    copy for its own row range."""
+    K = 1024
+    Ns = [128, 64, 64]
+    g = GraphBuilder()
+    x = g.input("f32", "T", K)
+    ws = [g.weight("q4_k", n, K) for n in Ns]
+    bs = [g.weight("f32", n) for n in Ns]
+    ys = [g.output(g.add(g.matmul(x, w), b)) for w, b in zip(ws, bs)]
+    w8 = g.weight("q8_0", 32, K)
+    y8 = g.output(g.matmul(x, w8))
+    raws = [synth.quant_table("q4_k", n, K, seed=30, tid=i) for i, n in enumerate(Ns)]
+    biases = [synth.normal(30, 10 + i, (n,)) for i, n in enumerate(Ns)]
+    raw8 = synth.quant_table("q8_0", 32, K, seed=30, tid=9)
+    T = 3
+    xs = synth.normal(30, 20, (T, K))
+    with dev.compile(g, max_tokens=16) as seg:
+        assert seg.launches == ["x->q8 rows 1..8"] + ["matvec+bias (int-dot rows 1..8)"] * 3 + [
+            "x->q8 rows 2..16", "matvec (int-dot rows 2..16)"]
+        assert seg.launches_at(1) == ["x->q8"] + ["matvec+bias int-dot"] * 3 + ["matvec f32"]
+        seg.set_input(x, xs)
+        for w, r in zip(ws, raws):
+            seg.set_input(w, r)
+        for b, v in zip(bs, biases):
+            seg.set_input(b, v)
+        seg.set_input(w8, raw8)
+        log("provider qkv int-dot + bias")
+        seg.execute(T)
+        for y, r, v, n in zip(ys, raws, biases, Ns):
+            ref, S = oracle.matvec_q8("q4_k", r, n, K, xs, with_abs=True)
+            ref = oracle.add(ref, np.broadcast_to(v, ref.shape).copy()).astype(np.float64)
+            got = seg.get_output(y).astype(np.float64)
+            assert (np.abs(got - ref) <= 2.0 ** -16 * S + 2.0 ** -24 * np.abs(ref) + 1e-30).all()
+        ref, S = oracle.matvec_q8("q8_0", raw8, 32, K, xs, with_abs=True)
+        assert (np.abs(seg.get_output(y8).astype(np.float64) - ref) <= 2.0 ** -16 * S + 1e-30).all()
+
+
+def test_f32_activations_keep_x_unquantized(dev):
+    K, N, T = 1024, 40, 2
+    for f32_act, reduced in [(True, False), (True, True), (False, False)]:
+        g = GraphBuilder()
+        if reduced:
+            g.options["reduced_precision"] = True
+        x = g.input("f32", "T", K)
+        w = g.weight("q4_k", N, K)
+        y = g.output(g.matmul(x, w, f32_activations=f32_act))
+        raw = synth.quant_table("q4_k", N, K, seed=31, tid=1)
+        xs = synth.normal(31, 2, (T, K))
+        with dev.compile(g, max_tokens=4) as seg:
+            seg.set_input(x, xs)
+            seg.set_input(w, raw)
+            log(f"provider f32_activations={f32_act} reduced={reduced}")
+            seg.execute(T)
+            got = seg.get_output(y)
+        q8 = not f32_act or reduced
+        ref = oracle.matvec_q8("q4_k", raw, N, K, xs) if q8 else oracle.matvec("q4_k", raw, N, K, xs)
+        other = oracle.matvec("q4_k", raw, N, K, xs) if q8 else oracle.matvec_q8("q4_k", raw, N, K, xs)
+        # the two numerics differ visibly at this size; the result is the one the rule picks
+        assert np.abs(got - ref).max() < 0.1 * np.abs(got - other).max()

@@ -180,8 +180,8 @@ def test_dual_matvec_falls_back_when_rows_do_not_fit_lds():
     def build(K):
         g = GraphBuilder()
         x = g.input("f32", "T", K)
-        gate = g.matmul(x, g.weight("q8_0", 256, K))
-        up = g.matmul(x, g.weight("q8_0", 256, K))
+        gate = g.matmul(x, g.weight("q8_0", 256, K), f32_activations=True)
+        up = g.matmul(x, g.weight("q8_0", 256, K), f32_activations=True)
         g.output(g.mul(g.silu(gate), up))
         return g
     assert plan(build(4096)) == ["matvec2+fused[Silu,Mul]"]
@@ -314,3 +314,103 @@ def test_zero_and_oversized_dimensions_are_answered_not_crashed():
     seg = ctypes.c_void_p(0)
     assert native.lib().slhip_segment_compile(b"value 0 f32 T 64\ninput 0\n", (1 << 20) + 1, ctypes.byref(seg)) != native.OK
     assert "2^20" in native.last_error()
+
+
+# ---- the integer-dot matvec: which MatMuls quantize x, and the shared q8 copies ---------------------------
+
+def _qkv(fmts, **opts):
+    g = GraphBuilder()
+    g.options.update(opts)
+    x = g.input("f32", "T", 1024)
+    for f in fmts:
+        g.output(g.matmul(x, g.weight(f, 64, 1024)))
+    return g
+
+
+def test_int_dot_plan_shares_one_q8_copy_per_x_and_range():
+    """GraphLowerer.IntDot.cs:119-220: matmuls reading the same rows share one quantized copy per row range
+    (Q4_K and Q6_K: 1..8 rows; Q8_0: 2..16 rows, IntDotMinRows / IntDotMaxRows :18-19,75)."""
+    assert plan(_qkv(["q4_k", "q6_k", "q4_k"])) == [
+        "x->q8 rows 1..8", "matvec (int-dot rows 1..8)", "matvec (int-dot rows 1..8)", "matvec (int-dot rows 1..8)"]
+    assert plan(_qkv(["q4_k", "q8_0"])) == [
+        "x->q8 rows 1..8", "matvec (int-dot rows 1..8)", "x->q8 rows 2..16", "matvec (int-dot rows 2..16)"]
+    # the lowerer's rule: the 32-value block formats Q4_0 / Q5_0 (SHARPLIGHT_MMVQ_BLOCK on by default), not Q4_1,
+    # Q5_1 or dense weights
+    assert plan(_qkv(["q4_0", "q5_0"])) == [
+        "x->q8 rows 1..8", "matvec (int-dot rows 1..8)", "matvec (int-dot rows 1..8)"]
+    assert plan(_qkv(["q4_1", "q5_1", "bf16", "q2_k", "q3_k"])) == ["matvec"] * 5
+
+
+def test_int_dot_rules_and_f32_activations():
+    # the CPU provider's rule: every IntDot.Supports format below 32 rows (MatMulOp.cs:104,138-147)
+    assert plan(_qkv(["q4_1", "q8_0", "bf16", "q2_k"], int_dot="cpu")) == [
+        "x->q8 rows 1..31", "matvec (int-dot rows 1..31)", "matvec (int-dot rows 1..31)", "matvec", "matvec"]
+    assert plan(_qkv(["q4_k", "q8_0"], int_dot="off")) == ["matvec", "matvec"]
+    # f32_activations keeps x unquantized unless the compile allows reduced precision (GraphLowerer.IntDot.cs:61-62)
+    def one(**kw):
+        g = GraphBuilder()
+        g.options.update(kw.pop("opts", {}))
+        x = g.input("f32", "T", 1024)
+        g.output(g.matmul(x, g.weight("q4_k", 64, 1024), **kw))
+        return g
+    assert plan(one(f32_activations=True)) == ["matvec"]
+    assert plan(one(f32_activations=False)) == ["x->q8 rows 1..8", "matvec (int-dot rows 1..8)"]
+    assert plan(one(f32_activations=True, opts={"reduced_precision": True})) == ["x->q8 rows 1..8",
+                                                                                 "matvec (int-dot rows 1..8)"]
+
+
+def test_int_dot_options_are_checked_and_described():
+    g = _qkv(["q4_k"], int_dot="cpu", reduced_precision=True)
+    text = describe(g.to_ir())
+    assert "option int_dot=cpu\n" in text and "option reduced_precision=true\n" in text
+    for bad in ("option int_dot=gpu\n", "option speed=3\n", "option reduced_precision=2\n", "option x\n"):
+        seg = ctypes.c_void_p(0)
+        st = native.lib().slhip_segment_compile((bad + g.to_ir()).encode(), 4, ctypes.byref(seg))
+        assert st == native.ERR_INVALID, bad
+
+
+def test_int_dot_only_formats():
+    """IQ4_NL, IQ4_XS and MXFP4 have no f32 matvec here: supported when the integer-dot path serves every row
+    count from one, and compile refuses a token bound beyond the range's end."""
+    def g_of(fmt, K=1024, **opts):
+        g = GraphBuilder()
+        g.options.update(opts)
+        x = g.input("f32", "T", K)
+        g.output(g.matmul(x, g.weight(fmt, 64, K)))
+        return g
+    for fmt in ("iq4_nl", "mxfp4"):
+        assert _supports(g_of(fmt), 0)[0]
+        assert plan(g_of(fmt)) == ["x->q8 rows 1..8", "matvec (int-dot rows 1..8)"]
+        seg = ctypes.c_void_p(0)
+        st = native.lib().slhip_segment_compile(g_of(fmt).to_ir().encode(), 9, ctypes.byref(seg))
+        assert st == native.ERR_UNSUPPORTED and "up to 8 activation rows" in native.last_error()
+    assert not _supports(g_of("iq4_xs"), 0)[0]           # not in the lowerer's int-dot set
+    assert _supports(g_of("iq4_xs", int_dot="cpu"), 0)[0]  # the CPU provider's
+    assert not _supports(g_of("mxfp4", int_dot="off"), 0)[0]
+    # gpt-oss's K = 2880 (not a multiple of 256): MXFP4 yes (integer dots only), Q4_0 no (no f32 path at that K)
+    assert _supports(g_of("mxfp4", K=2880), 0)[0]
+    assert not _supports(g_of("q4_0", K=2880), 0)[0]
+
+
+def test_matmul_bias_folds_into_the_matvec():
+    """FoldMatMulBiases (GraphLowerer.Fusion.cs:355-408): an Add of a constant f32 row vector [N] that is the
+    product's only reader joins the matvec launch; other Adds stay their own launch."""
+    def g_of(bias_kind):
+        g = GraphBuilder()
+        x = g.input("f32", "T", 1024)
+        p = g.matmul(x, g.weight("bf16", 64, 1024))
+        b = g.input("f32", 64) if bias_kind == "input" else g.weight("f32", 64)
+        g.output(g.add(b, p) if bias_kind == "swapped" else g.add(p, b))
+        return g
+    assert plan(g_of("weight")) == ["matvec+bias"]
+    assert plan(g_of("swapped")) == ["matvec+bias"]
+    assert plan(g_of("input")) == ["matvec", "Add"]
+    g = GraphBuilder()
+    x = g.input("f32", "T", 1024)
+    p = g.output(g.matmul(x, g.weight("q4_k", 64, 1024)))  # the product is also an output: not folded
+    g.output(g.add(p, g.weight("f32", 64)))
+    assert plan(g) == ["x->q8 rows 1..8", "matvec (int-dot rows 1..8)", "Add"]
+    g = GraphBuilder()
+    x = g.input("f32", "T", 1024)
+    g.output(g.add(g.matmul(x, g.weight("q4_k", 64, 1024)), g.weight("f32", 64)))
+    assert plan(g) == ["x->q8 rows 1..8", "matvec+bias (int-dot rows 1..8)"]
