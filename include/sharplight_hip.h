@@ -482,6 +482,62 @@ SLHIP_API int slhip_binary(int op, int dtype_a, int dtype_b, int dtype_out, cons
 SLHIP_API int slhip_unary(int op, int dtype_in, int dtype_out, const void* x, void* y, int64_t rows, int64_t cols,
                           int64_t x_stride, int64_t y_stride, float p0, float p1, slhip_stream stream);
 
+/*
+ * A fused elementwise group (the lowerer's generated elementwise kernel, src/Sharplight.Shaders/Lowering/
+ * GraphLowerer.Fusion.cs:88-205), optionally with the row norm before it (FoldNormHeads, :240-284) or after it
+ * (FoldNormTails, :211-238), over an output of [rows, cols] (cols a multiple of 4):
+ *   registers 0 .. n_inputs-1 are loaded with the inputs, each FULL ([rows, cols]), ROW (one value per
+ *   column: [cols]), COL (one value per row: [rows]) or SCALAR (one value); f32 / bf16 / f16, FULL and ROW
+ *   inputs 16-byte (f32) or 8-byte aligned; then the ops run in order, op k (kind BINARY: slhip_binary_op of
+ *   registers a, b; UNARY: slhip_unary_op of register a with p0, p1) writing register dst in f32, rounded to
+ *   `round` (the node's output type); SLHIP_EW_MAX_REGS registers;
+ *   each output stores one register ([rows, cols], f32 / bf16 / f16).
+ *   head (kind SLHIP_EWN_RMS / SLHIP_EWN_L2, SLHIP_EWN_NONE for none): input register `reg` is replaced by
+ *   round(norm(input) * w) (w [cols] f32 or NULL; round to dtype_y) before the ops;
+ *   tail: y [rows, cols] (dtype_y) = norm(register reg) * w after the ops; at most one of head and tail.
+ * The arithmetic is that of slhip_binary / slhip_unary / slhip_rownorm per node, so the group equals the
+ * nodes run one by one. */
+#define SLHIP_EW_MAX_INPUTS 8
+#define SLHIP_EW_MAX_OPS 16
+#define SLHIP_EW_MAX_OUTPUTS 4
+#define SLHIP_EW_MAX_REGS 16
+typedef enum slhip_ew_input_mode { SLHIP_EWI_FULL = 0, SLHIP_EWI_ROW = 1, SLHIP_EWI_COL = 2, SLHIP_EWI_SCALAR = 3 } slhip_ew_input_mode;
+typedef enum slhip_ew_op_kind { SLHIP_EWK_BINARY = 0, SLHIP_EWK_UNARY = 1 } slhip_ew_op_kind;
+typedef enum slhip_ew_norm_kind { SLHIP_EWN_NONE = 0, SLHIP_EWN_RMS = 1, SLHIP_EWN_L2 = 2 } slhip_ew_norm_kind;
+typedef struct slhip_ew_input {
+    const void* data;
+    int dtype;
+    int mode;
+} slhip_ew_input;
+typedef struct slhip_ew_op {
+    int kind, op;
+    int a, b;   /* source registers */
+    int dst;    /* destination register */
+    int round;  /* SLHIP_F32 (none), SLHIP_BF16 or SLHIP_F16 */
+    float p0, p1;
+} slhip_ew_op;
+typedef struct slhip_ew_output {
+    void* data;
+    int dtype;
+    int reg;
+} slhip_ew_output;
+typedef struct slhip_ew_norm {
+    int kind;     /* slhip_ew_norm_kind */
+    int reg;
+    const float* w;
+    float eps;
+    void* y;      /* tail only */
+    int dtype_y;
+} slhip_ew_norm;
+typedef struct slhip_ew_program {
+    int n_inputs, n_ops, n_outputs;
+    slhip_ew_input inputs[SLHIP_EW_MAX_INPUTS];
+    slhip_ew_op ops[SLHIP_EW_MAX_OPS];
+    slhip_ew_output outputs[SLHIP_EW_MAX_OUTPUTS];
+    slhip_ew_norm head, tail;
+} slhip_ew_program;
+SLHIP_API int slhip_ew_program_run(const slhip_ew_program* prog, int64_t rows, int64_t cols, slhip_stream stream);
+
 /* ---- provider / compiled segment (IExecutionProvider, IComputeDevice, ICompiledSegment) ----------------
  *
  * A graph segment arrives as text, one declaration per line ('#' starts a comment line):

@@ -634,7 +634,7 @@ Support supports(const Graph& g, const Node& n)
 // ---- lowering into fused units -------------------------------------------------------------------------
 
 struct Unit {
-    enum Kind { RowNorm, Gated, Rope, Gather, Cast, CacheWrite, Matvec, Binary, Unary, QuantizeQ8 } kind;
+    enum Kind { RowNorm, Gated, Rope, Gather, Cast, CacheWrite, Matvec, Binary, Unary, QuantizeQ8, EwGroup } kind;
     std::string label;
     // RowNorm
     int norm = SLHIP_NORM_RMS;
@@ -665,6 +665,12 @@ struct Unit {
     // Binary: y = op(x, up) with broadcasting; Unary: y = op(x) with parameters p0, p1
     int op = 0;
     float p0 = 0.f, p1 = 0.f;
+    // EwGroup: the program of a fused elementwise group (value ids in place of the device pointers), the value
+    // whose shape is the group's, and the folded norms (node indices, -1 for none)
+    std::vector<int> ew_in, ew_mode;
+    std::vector<slhip_ew_op> ew_ops;
+    std::vector<std::pair<int, int>> ew_out;  // (value, register)
+    int shape_of = -1, head_node = -1, tail_node = -1, norm_reg = -1;
 };
 
 class Segment {
@@ -814,10 +820,21 @@ private:
         std::vector<bool> done(N, false);
         auto single_use = [&](int id) { return !g_.value(id).output && cons[id].size() == 1; };
         find_dual_matvecs(cons, single_use);
+        form_groups(cons);
         for (size_t k = 0; k < N; k++) {
             if (done[k]) continue;
             const Node& n = g_.nodes[k];
-            if (n.op == "Add" && k + 1 < N && !done[k + 1]) {
+            if (group_of_[k] >= 0) {  // a fused group, emitted at its last node
+                done[k] = true;
+                const EwGroup& G = groups_[group_of_[k]];
+                if (static_cast<int>(k) == G.nodes.back()) emit_group(G, cons, done);
+                continue;
+            }
+            if (folded_norms_.count(static_cast<int>(k))) {
+                done[k] = true;
+                continue;
+            }
+            if (n.op == "Add" && k + 1 < N && !done[k + 1] && !folded_norms_.count(static_cast<int>(k) + 1)) {
                 const Node& m = g_.nodes[k + 1];
                 const auto& od = g_.value(n.out[0]).dims;
                 if ((m.op == "RmsNorm" || m.op == "L2Norm") && m.in[0] == n.out[0] && g_.value(n.in[0]).dims == od &&
@@ -941,24 +958,8 @@ private:
                 u.cache_node = static_cast<int>(k);
                 u.label = "CacheWrite";
                 units_.push_back(u);
-            } else if (kBinaryOps.count(n.op)) {
-                Unit u{Unit::Binary};
-                u.op = kBinaryOps.at(n.op);
-                if (u.op == SLHIP_BIN_MOD && flag(n, "fmod")) u.op = SLHIP_BIN_FMOD;
-                u.x = n.in[0];
-                u.up = n.in[1];
-                if (g_.value(u.x).type == DType::F32 && g_.value(u.up).type != DType::F32) std::swap(u.x, u.up);  // commutative
-                u.y = n.out[0];
-                u.label = n.op;
-                units_.push_back(u);
-            } else if (kUnaryOps.count(n.op)) {
-                Unit u{Unit::Unary};
-                u.op = kUnaryOps.at(n.op);
-                std::tie(u.p0, u.p1) = unary_params(u.op, n);
-                u.x = n.in[0];
-                u.y = n.out[0];
-                u.label = n.op;
-                units_.push_back(u);
+            } else if (kBinaryOps.count(n.op) || kUnaryOps.count(n.op)) {
+                units_.push_back(elementwise_unit(static_cast<int>(k)));
             } else {
                 unsupported("op " + n.op + " has no lowering on the HIP provider");
             }
@@ -997,6 +998,351 @@ private:
             acc *= d[i];
         }
         return s;
+    }
+
+    // ---- fused elementwise groups (GraphLowerer.Fusion.cs:88-285) -------------------------------------------
+
+    struct EwGroup {
+        std::vector<int> nodes;
+        int head = -1, tail = -1;  // folded row norms
+        bool dead = false;
+    };
+    std::vector<EwGroup> groups_;
+    std::vector<int> group_of_;    // node -> its group, or -1
+    std::set<int> folded_norms_;   // norm nodes folded into a group
+
+    // How an input of dims `in` feeds an output of dims `out` in a group program, or -1 when no mode fits.
+    static int input_mode(const std::vector<int64_t>& in, const std::vector<int64_t>& out)
+    {
+        const size_t r = out.size();
+        if (in.size() > r) return -1;
+        std::vector<int64_t> a(r - in.size(), 1);
+        a.insert(a.end(), in.begin(), in.end());
+        if (a == out) return SLHIP_EWI_FULL;
+        bool lead_one = true, lead_same = true;
+        for (size_t k = 0; k + 1 < r; k++) {
+            lead_one = lead_one && a[k] == 1;
+            lead_same = lead_same && a[k] == out[k];
+        }
+        if (lead_one && a[r - 1] == 1) return SLHIP_EWI_SCALAR;
+        if (lead_one && a[r - 1] == out[r - 1]) return SLHIP_EWI_ROW;
+        if (lead_same && a[r - 1] == 1) return SLHIP_EWI_COL;
+        return -1;
+    }
+
+    // IsFusable (GraphLowerer.Fusion.cs:9-11): an elementwise op with an f32 output and activation inputs; here also
+    // inputs whose broadcast the group program can express and rows of a multiple of 4 values.
+    bool fusable(int k) const
+    {
+        const Node& n = g_.nodes[k];
+        if (absorbed_.count(k) || dual_at_.count(k)) return false;
+        if (!kBinaryOps.count(n.op) && !kUnaryOps.count(n.op)) return false;
+        if (n.out.size() != 1) return false;
+        const Value& y = g_.value(n.out[0]);
+        if (y.type != DType::F32 || y.dims.empty() || y.dims.back() == kSymT || y.dims.back() % 4 != 0) return false;
+        for (int id : n.in) {
+            const Value& v = g_.value(id);
+            if (!is_activation(v.type) || input_mode(v.dims, y.dims) < 0) return false;
+        }
+        return true;
+    }
+
+    int ext_inputs(const std::vector<int>& nodes) const
+    {
+        std::set<int> produced, ext;
+        for (int k : nodes) produced.insert(g_.nodes[k].out[0]);
+        for (int k : nodes)
+            for (int id : g_.nodes[k].in)
+                if (!produced.count(id)) ext.insert(id);
+        return static_cast<int>(ext.size());
+    }
+
+    static bool norm_weight_fusable(const Graph& g, const Node& norm)
+    {
+        return norm.in.size() <= 1 || (g.value(norm.in[1]).type == DType::F32 && g.value(norm.in[1]).dims.size() == 1);
+    }
+
+    // The values of group `G` that the launch stores: read by a node outside the unit, or segment outputs.
+    std::vector<int> group_outputs(const EwGroup& G, std::map<int, std::vector<int>>& cons) const
+    {
+        std::set<int> in(G.nodes.begin(), G.nodes.end());
+        std::vector<int> outs;
+        for (int k : G.nodes) {
+            const int v = g_.nodes[k].out[0];
+            bool esc = g_.value(v).output;
+            for (int c : cons[v]) esc = esc || (!in.count(c) && c != G.tail);
+            if (esc) outs.push_back(v);
+        }
+        return outs;
+    }
+
+    // GroupElementwiseChains, MergeElementwiseGroups, FoldNormTails and FoldNormHeads (GraphLowerer.Fusion.cs:
+    // 88-284) over the nodes not taken by a dual matvec.
+    void form_groups(std::map<int, std::vector<int>>& cons)
+    {
+        const int N = static_cast<int>(g_.nodes.size());
+        constexpr int kMaxIn = SLHIP_EW_MAX_INPUTS - 1;  // a register kept for a norm head's input
+        struct URef {
+            int group, node;
+        };
+        std::vector<URef> us;
+        int open = -1;
+        std::set<int> open_vals;
+        auto dims_of = [&](const EwGroup& G) { return g_.value(g_.nodes[G.nodes[0]].out[0]).dims; };
+        for (int k = 0; k < N; k++) {
+            if (fusable(k)) {
+                const Node& n = g_.nodes[k];
+                bool joins = false;
+                if (open >= 0) {
+                    EwGroup& G = groups_[open];
+                    std::vector<int> with = G.nodes;
+                    with.push_back(k);
+                    bool reads = false;
+                    for (int id : n.in) reads = reads || open_vals.count(id);
+                    joins = reads && g_.value(n.out[0]).dims == dims_of(G) && ext_inputs(with) <= kMaxIn &&
+                            static_cast<int>(with.size()) <= SLHIP_EW_MAX_OPS;
+                }
+                if (!joins) {
+                    groups_.push_back(EwGroup{});
+                    open = static_cast<int>(groups_.size()) - 1;
+                    open_vals.clear();
+                    us.push_back({open, -1});
+                }
+                groups_[open].nodes.push_back(k);
+                open_vals.insert(n.out[0]);
+                continue;
+            }
+            open = -1;
+            us.push_back({-1, k});
+        }
+        // merge along data flow: a group reading an earlier group's output takes its nodes when nothing in
+        // between reads those outputs or writes a state
+        for (int j = 0; j < static_cast<int>(us.size()); j++) {
+            if (us[j].group < 0) continue;
+            for (int i = j - 1; i >= std::max(0, j - 16); i--) {
+                if (us[i].group < 0) continue;
+                EwGroup& E = groups_[us[i].group];
+                EwGroup& L = groups_[us[j].group];
+                if (dims_of(E) != dims_of(L)) continue;
+                std::set<int> outs;
+                for (int k : E.nodes) outs.insert(g_.nodes[k].out[0]);
+                bool reads = false;
+                for (int k : L.nodes)
+                    for (int id : g_.nodes[k].in) reads = reads || outs.count(id);
+                std::vector<int> both = E.nodes;
+                both.insert(both.end(), L.nodes.begin(), L.nodes.end());
+                if (!reads || ext_inputs(both) > kMaxIn || static_cast<int>(both.size()) > SLHIP_EW_MAX_OPS) continue;
+                bool blocked = false;
+                for (int u = i + 1; u < j && !blocked; u++) {
+                    std::vector<int> un = us[u].group >= 0 ? groups_[us[u].group].nodes : std::vector<int>{us[u].node};
+                    for (int k : un) {
+                        const Node& n = g_.nodes[k];
+                        if (n.op == "CacheWrite") blocked = true;
+                        for (int id : n.in) blocked = blocked || outs.count(id);
+                    }
+                }
+                if (blocked) continue;
+                L.nodes = both;
+                E.dead = true;
+                us.erase(us.begin() + i);
+                j--;
+            }
+        }
+        // a row norm right after a group, of one of its values (FoldNormTails, :211-238)
+        for (int i = 0; i + 1 < static_cast<int>(us.size()); i++) {
+            if (us[i].group < 0 || us[i + 1].node < 0) continue;
+            const Node& nm = g_.nodes[us[i + 1].node];
+            if (nm.op != "RmsNorm" && nm.op != "L2Norm") continue;
+            EwGroup& G = groups_[us[i].group];
+            bool made = false;
+            for (int k : G.nodes) made = made || g_.nodes[k].out[0] == nm.in[0];
+            if (!made || g_.value(nm.in[0]).dims != dims_of(G) || !norm_weight_fusable(g_, nm)) continue;
+            G.tail = us[i + 1].node;
+            us.erase(us.begin() + i + 1);
+        }
+        // a row norm whose output only the next group reads (FoldNormHeads, :240-284)
+        for (int i = 0; i + 1 < static_cast<int>(us.size()); i++) {
+            if (us[i].node < 0 || us[i + 1].group < 0) continue;
+            const Node& nm = g_.nodes[us[i].node];
+            if (nm.op != "RmsNorm" && nm.op != "L2Norm") continue;
+            EwGroup& G = groups_[us[i + 1].group];
+            const int y = nm.out[0];
+            if (G.tail >= 0 || G.head >= 0 || g_.value(y).output || g_.value(y).dims != dims_of(G) ||
+                !norm_weight_fusable(g_, nm) || !is_activation(g_.value(y).type))
+                continue;
+            bool only = !cons[y].empty();
+            for (int c : cons[y]) only = only && std::find(G.nodes.begin(), G.nodes.end(), c) != G.nodes.end();
+            if (!only) continue;
+            G.head = us[i].node;
+            us.erase(us.begin() + i);
+            i--;
+        }
+        group_of_.assign(N, -1);
+        for (size_t gi = 0; gi < groups_.size(); gi++) {
+            EwGroup& G = groups_[gi];
+            if (G.dead) continue;
+            if (group_outputs(G, cons).size() > SLHIP_EW_MAX_OUTPUTS) {  // too many stores: unfused
+                G.dead = true;
+                continue;
+            }
+            for (int k : G.nodes) group_of_[k] = static_cast<int>(gi);
+            if (G.head >= 0) folded_norms_.insert(G.head);
+            if (G.tail >= 0) folded_norms_.insert(G.tail);
+        }
+    }
+
+    Unit elementwise_unit(int k)
+    {
+        const Node& n = g_.nodes[k];
+        if (kBinaryOps.count(n.op)) {
+            Unit u{Unit::Binary};
+            u.op = kBinaryOps.at(n.op);
+            if (u.op == SLHIP_BIN_MOD && flag(n, "fmod")) u.op = SLHIP_BIN_FMOD;
+            u.x = n.in[0];
+            u.up = n.in[1];
+            if (g_.value(u.x).type == DType::F32 && g_.value(u.up).type != DType::F32) std::swap(u.x, u.up);  // commutative
+            u.y = n.out[0];
+            u.label = n.op;
+            return u;
+        }
+        Unit u{Unit::Unary};
+        u.op = kUnaryOps.at(n.op);
+        std::tie(u.p0, u.p1) = unary_params(u.op, n);
+        u.x = n.in[0];
+        u.y = n.out[0];
+        u.label = n.op;
+        return u;
+    }
+
+    // A group whose program does not fit: its head norm, its nodes and its tail norm as their own launches.
+    void emit_unfused(const EwGroup& G, std::map<int, std::vector<int>>& cons, std::vector<bool>& done)
+    {
+        if (G.head >= 0) units_.push_back(rownorm_unit(g_.nodes[G.head]));
+        for (int k : G.nodes) units_.push_back(elementwise_unit(k));
+        if (G.tail >= 0) {
+            Unit u = rownorm_unit(g_.nodes[G.tail]);
+            attach_half_copy(u, cons, done);
+            units_.push_back(u);
+        }
+    }
+
+    // The launch of a group: the row-norm kernel for [Add] + norm of two same-shape operands, the gated kernel
+    // for [act, Mul], a standalone launch for a lone node, else the group program.
+    void emit_group(const EwGroup& G, std::map<int, std::vector<int>>& cons, std::vector<bool>& done)
+    {
+        const Node& n0 = g_.nodes[G.nodes[0]];
+        const std::vector<int> outs = group_outputs(G, cons);
+        if (G.nodes.size() == 1 && G.head < 0 && G.tail < 0) {
+            units_.push_back(elementwise_unit(G.nodes[0]));
+            return;
+        }
+        if (G.nodes.size() == 1 && G.tail >= 0 && G.head < 0 && n0.op == "Add") {
+            const auto& od = g_.value(n0.out[0]).dims;
+            if (g_.value(n0.in[0]).dims == od && g_.value(n0.in[1]).dims == od &&
+                g_.value(n0.in[0]).type == DType::F32 && g_.value(n0.in[1]).type == DType::F32) {
+                const Node& m = g_.nodes[G.tail];
+                Unit u = rownorm_unit(m);
+                u.x = n0.in[0];
+                u.res = n0.in[1];
+                u.h = outs.empty() ? -1 : n0.out[0];
+                u.label = std::string("fused[Add]+") + m.op;
+                attach_half_copy(u, cons, done);
+                units_.push_back(u);
+                return;
+            }
+        }
+        if (G.nodes.size() == 2 && G.head < 0 && G.tail < 0 && kActs.count(n0.op) && g_.nodes[G.nodes[1]].op == "Mul") {
+            const Node& m = g_.nodes[G.nodes[1]];
+            const int a = n0.out[0];
+            const int up = m.in[0] == a ? m.in[1] : m.in[0];
+            if ((m.in[0] == a) != (m.in[1] == a) && outs.size() == 1 && outs[0] == m.out[0] &&
+                g_.value(up).dims == g_.value(n0.in[0]).dims && g_.value(m.out[0]).dims == g_.value(n0.in[0]).dims &&
+                g_.value(up).type == g_.value(n0.in[0]).type) {
+                Unit u{Unit::Gated};
+                u.act = n0.op == "Silu" ? SLHIP_ACT_SILU : n0.op == "GeluTanh" ? SLHIP_ACT_GELU_TANH : SLHIP_ACT_GELU_ERF;
+                u.gate = n0.in[0];
+                u.up = up;
+                u.y = m.out[0];
+                u.label = "fused[" + n0.op + ",Mul]";
+                units_.push_back(u);
+                return;
+            }
+        }
+        Unit u{Unit::EwGroup};
+        u.shape_of = n0.out[0];
+        u.head_node = G.head;
+        u.tail_node = G.tail;
+        std::map<int, int> reg;
+        auto input = [&](int id) {
+            auto it = reg.find(id);
+            if (it != reg.end()) return it->second;
+            const int r = static_cast<int>(u.ew_in.size());
+            u.ew_in.push_back(id);
+            u.ew_mode.push_back(input_mode(g_.value(id).dims, g_.value(u.shape_of).dims));
+            reg[id] = r;
+            return r;
+        };
+        if (G.head >= 0) {  // the head's input takes register 0; the norm's output is that register once normed
+            const Node& h = g_.nodes[G.head];
+            u.ew_in.push_back(h.in[0]);
+            u.ew_mode.push_back(SLHIP_EWI_FULL);
+            reg[h.out[0]] = 0;
+            u.norm_reg = 0;
+        }
+        for (int k : G.nodes)  // every external input first: registers 0 .. n_inputs-1
+            for (int id : g_.nodes[k].in) {
+                bool produced = false;
+                for (int j : G.nodes) produced = produced || g_.nodes[j].out[0] == id;
+                if (!produced) input(id);
+            }
+        // registers: the inputs 0 .. n-1, then each op's result in a register whose value is dead (linear scan;
+        // the stored values and the tail's operand live to the end)
+        const int nin = static_cast<int>(u.ew_in.size());
+        std::map<int, int> last;  // value -> index of the last op reading it (a large index: live to the end)
+        constexpr int kEnd = 1 << 20;
+        for (size_t i = 0; i < G.nodes.size(); i++)
+            for (int id : g_.nodes[G.nodes[i]].in) last[id] = static_cast<int>(i);
+        for (int v : outs) last[v] = kEnd;
+        if (G.tail >= 0) last[g_.nodes[G.tail].in[0]] = kEnd;
+        std::vector<bool> busy(SLHIP_EW_MAX_REGS, false);
+        for (int r = 0; r < nin; r++) busy[r] = true;
+        std::string label;
+        for (size_t i = 0; i < G.nodes.size(); i++) {
+            const Node& n = g_.nodes[G.nodes[i]];
+            slhip_ew_op o{};
+            o.round = SLHIP_F32;
+            if (kBinaryOps.count(n.op)) {
+                o.kind = SLHIP_EWK_BINARY;
+                o.op = kBinaryOps.at(n.op);
+                if (o.op == SLHIP_BIN_MOD && flag(n, "fmod")) o.op = SLHIP_BIN_FMOD;
+                o.a = reg.at(n.in[0]);
+                o.b = reg.at(n.in[1]);
+            } else {
+                o.kind = SLHIP_EWK_UNARY;
+                o.op = kUnaryOps.at(n.op);
+                std::tie(o.p0, o.p1) = unary_params(o.op, n);
+                o.a = reg.at(n.in[0]);
+            }
+            for (int id : n.in)  // operands read for the last time free their registers (read before the write)
+                if (last.at(id) == static_cast<int>(i)) busy[reg.at(id)] = false;
+            int dst = -1;
+            for (int r = 0; r < SLHIP_EW_MAX_REGS && dst < 0; r++)
+                if (!busy[r]) dst = r;
+            if (dst < 0) {  // more live values than registers: the nodes run one by one
+                emit_unfused(G, cons, done);
+                return;
+            }
+            busy[dst] = true;
+            o.dst = dst;
+            u.ew_ops.push_back(o);
+            reg[n.out[0]] = dst;
+            label += (i ? "," : "") + n.op;
+        }
+        for (int v : outs) u.ew_out.push_back({v, reg.at(v)});
+        if (G.tail >= 0) u.norm_reg = reg.at(g_.nodes[G.tail].in[0]);
+        u.label = (G.head >= 0 ? g_.nodes[G.head].op + "+" : std::string()) + "fused[" + label + "]" +
+                  (G.tail >= 0 ? "+" + g_.nodes[G.tail].op : std::string());
+        units_.push_back(u);
     }
 
     // Gate/up matmul pairs sharing x that feed act(gate) * up (FoldDualMatMuls,
@@ -1059,6 +1405,10 @@ private:
         const int c = cons[prod][0];
         const Node& a = g_.nodes[c];
         if (a.op != "Add" || a.in.size() != 2 || done[c] || a.in[0] == a.in[1]) return;
+        if (group_of_[c] >= 0) {  // a single-node Add group only (FoldMatMulBiases)
+            const EwGroup& G = groups_[group_of_[c]];
+            if (G.nodes.size() != 1 || G.head >= 0 || G.tail >= 0) return;
+        }
         const int b = a.in[0] == prod ? a.in[1] : a.in[0];
         const Value& bv = g_.value(b);
         const Value& wv = g_.value(u.wg);
@@ -1070,6 +1420,10 @@ private:
         u.y = a.out[0];
         u.label += "+bias";
         done[c] = true;
+        if (group_of_[c] >= 0) {
+            groups_[group_of_[c]].dead = true;
+            group_of_[c] = -1;
+        }
     }
 
     // The integer-dot range of every matvec unit, and the quantized copies of x they read: one per (x, row
@@ -1363,6 +1717,33 @@ private:
             check(slhip_binary(u.op, act_code(g_.value(u.x).type), act_code(g_.value(u.up).type), act_code(g_.value(u.y).type),
                                ptr(u.x), sa.data(), ptr(u.up), sb.data(), ptr(u.y), yd.data(), static_cast<int>(yd.size()),
                                stream_));
+            break;
+        }
+        case Unit::EwGroup: {
+            slhip_ew_program p{};
+            p.n_inputs = static_cast<int>(u.ew_in.size());
+            p.n_ops = static_cast<int>(u.ew_ops.size());
+            p.n_outputs = static_cast<int>(u.ew_out.size());
+            for (int i = 0; i < p.n_inputs; i++)
+                p.inputs[i] = slhip_ew_input{ptr(u.ew_in[i]), act_code(g_.value(u.ew_in[i]).type), u.ew_mode[i]};
+            for (int k = 0; k < p.n_ops; k++) p.ops[k] = u.ew_ops[k];
+            for (int j = 0; j < p.n_outputs; j++)
+                p.outputs[j] = slhip_ew_output{ptr(u.ew_out[j].first), act_code(g_.value(u.ew_out[j].first).type), u.ew_out[j].second};
+            auto norm_of = [&](int node, bool tail) {
+                const Node& nm = g_.nodes[node];
+                slhip_ew_norm r{};
+                r.kind = nm.op == "L2Norm" ? SLHIP_EWN_L2 : SLHIP_EWN_RMS;
+                r.reg = u.norm_reg;
+                r.w = nm.in.size() > 1 ? static_cast<const float*>(ptr(nm.in[1])) : nullptr;
+                r.eps = nm.f("eps", 1e-6f);
+                r.y = tail ? ptr(nm.out[0]) : nullptr;
+                r.dtype_y = act_code(g_.value(nm.out[0]).type);
+                return r;
+            };
+            if (u.head_node >= 0) p.head = norm_of(u.head_node, false);
+            if (u.tail_node >= 0) p.tail = norm_of(u.tail_node, true);
+            const Value& sv = g_.value(u.shape_of);
+            check(slhip_ew_program_run(&p, sv.rows(T), sv.last(), stream_));
             break;
         }
         case Unit::Unary: {

@@ -95,6 +95,37 @@ class NormCopies(ctypes.Structure):
                 ("yq_stride", ctypes.c_int64)]
 
 
+EW_MAX_INPUTS, EW_MAX_OPS, EW_MAX_OUTPUTS, EW_MAX_REGS = 8, 16, 4, 16
+EWI_FULL, EWI_ROW, EWI_COL, EWI_SCALAR = 0, 1, 2, 3
+EWK_BINARY, EWK_UNARY = 0, 1
+EW_NORMS = {"rms": 1, "l2": 2}
+
+
+class EwInput(ctypes.Structure):
+    _fields_ = [("data", ctypes.c_void_p), ("dtype", ctypes.c_int), ("mode", ctypes.c_int)]
+
+
+class EwOp(ctypes.Structure):
+    _fields_ = [("kind", ctypes.c_int), ("op", ctypes.c_int), ("a", ctypes.c_int), ("b", ctypes.c_int),
+                ("dst", ctypes.c_int), ("round", ctypes.c_int), ("p0", ctypes.c_float), ("p1", ctypes.c_float)]
+
+
+class EwOutput(ctypes.Structure):
+    _fields_ = [("data", ctypes.c_void_p), ("dtype", ctypes.c_int), ("reg", ctypes.c_int)]
+
+
+class EwNorm(ctypes.Structure):
+    _fields_ = [("kind", ctypes.c_int), ("reg", ctypes.c_int), ("w", ctypes.c_void_p), ("eps", ctypes.c_float),
+                ("y", ctypes.c_void_p), ("dtype_y", ctypes.c_int)]
+
+
+class EwProgram(ctypes.Structure):
+    """slhip_ew_program: a fused elementwise group with an optional norm head or tail."""
+    _fields_ = [("n_inputs", ctypes.c_int), ("n_ops", ctypes.c_int), ("n_outputs", ctypes.c_int),
+                ("inputs", EwInput * EW_MAX_INPUTS), ("ops", EwOp * EW_MAX_OPS),
+                ("outputs", EwOutput * EW_MAX_OUTPUTS), ("head", EwNorm), ("tail", EwNorm)]
+
+
 class GgufInfo(ctypes.Structure):
     """slhip_gguf_info."""
     _fields_ = [("version", ctypes.c_uint32), ("alignment", ctypes.c_uint32), ("n_tensors", ctypes.c_int64),
@@ -182,6 +213,7 @@ SIGNATURES = {
     "slhip_dual_matvec": (_I, [_I, _I, _I, _I, _P, _I64, _I64, _I64, _P, _P, _I64, _P, _I64, _P]),
     "slhip_matvec_bias": (_I, [_I, _I, _I, _P, _I64, _I64, _I64, _P, _I64, _P, _P, _I64, _P]),
     "slhip_q8_row_bytes": (_I64, [_I64]),
+    "slhip_ew_program_run": (_I, [ctypes.POINTER(EwProgram), _I64, _I64, _P]),
     "slhip_quantize_q8": (_I, [_I, _P, _I64, _I64, _I64, _P, _P]),
     "slhip_matvec_q8": (_I, [_I, _I, _P, _I64, _I64, _P, _I64, _P, _I64, _P, _P]),
     "slhip_dual_matvec_q8": (_I, [_I, _I, _I, _P, _I64, _I64, _P, _P, _I64, _P, _I64, _P]),
@@ -453,6 +485,26 @@ def dual_matvec(act, fmt, dtype_x, dtype_y, x, T, K, w_gate, w_up, N, y, *, x_st
     call("slhip_dual_matvec", ACTS.get(act, act), FORMATS.get(fmt, fmt), DTYPES.get(dtype_x, dtype_x),
          DTYPES.get(dtype_y, dtype_y), ptr(x), K if x_stride is None else x_stride, T, K, ptr(w_gate), ptr(w_up), N,
          ptr(y), N if y_stride is None else y_stride, stream)
+
+
+def ew_program(inputs, ops, outputs, rows, cols, *, head=None, tail=None, stream=None):
+    """A fused elementwise group (slhip_ew_program_run). inputs: [(ptr, dtype, mode)]; ops: [(kind, op, a, b,
+    round dtype, p0, p1)] with kind "binary"/"unary" and op a BINARY_OPS / UNARY_OPS name; outputs:
+    [(ptr, dtype, reg)]; head / tail: dict(kind="rms"|"l2", reg, w, eps, y, dtype_y)."""
+    p = EwProgram()
+    p.n_inputs, p.n_ops, p.n_outputs = len(inputs), len(ops), len(outputs)
+    for i, (d, dt, mode) in enumerate(inputs):
+        p.inputs[i] = EwInput(ptr(d), DTYPES.get(dt, dt), mode)
+    for k, (kind, op, a, b, dst, rnd, p0, p1) in enumerate(ops):
+        code = BINARY_OPS[op] if kind == "binary" else UNARY_OPS[op]
+        p.ops[k] = EwOp(EWK_BINARY if kind == "binary" else EWK_UNARY, code, a, b, dst, DTYPES.get(rnd, rnd), p0, p1)
+    for j, (d, dt, reg) in enumerate(outputs):
+        p.outputs[j] = EwOutput(ptr(d), DTYPES.get(dt, dt), reg)
+    for name, nm in (("head", head), ("tail", tail)):
+        if nm:
+            setattr(p, name, EwNorm(EW_NORMS[nm["kind"]], nm["reg"], ptr(nm.get("w")), nm.get("eps", 1e-6),
+                                    ptr(nm.get("y")), DTYPES.get(nm.get("dtype_y", "f32"), nm.get("dtype_y", "f32"))))
+    call("slhip_ew_program_run", ctypes.byref(p), rows, cols, stream)
 
 
 def q8_row_bytes(K) -> int:

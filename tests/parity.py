@@ -34,23 +34,29 @@ def _f16_f32(bits):
     return np.asarray(bits, np.uint16).view(np.float16).astype(np.float32)
 
 
-def assert_f16_close(got, ref, ulp: int = BF16_ULP, what: str = "", atol_row: float | None = None):
+def assert_f16_close(got, ref, ulp: int = BF16_ULP, what: str = "", atol_row: float | None = None,
+                     max_floor_only: int | None = None):
     """The bf16 rule (assert_bf16_close) on f16 codes: at most ``ulp`` f16 ulp from f16_RNE(oracle f32
     result), with the same absolute floor."""
-    return _assert_half_close(got, ref, ulp, what, atol_row, _f16_f32, "f16")
+    return _assert_half_close(got, ref, ulp, what, atol_row, _f16_f32, "f16", max_floor_only)
 
 
-def assert_bf16_close(got, ref, ulp: int = BF16_ULP, what: str = "", atol_row: float | None = None):
+def assert_bf16_close(got, ref, ulp: int = BF16_ULP, what: str = "", atol_row: float | None = None,
+                      max_floor_only: int | None = None):
     """At most ``ulp`` bf16 ulp from ``ref``. An element further away still passes when it is within the f32
     rule's absolute floor, ``atol_row`` (default 1e-5) x the RMS of its reference row: for results far below
     the row's scale -- the cancellation in a rotated pair, exp() underflowing into subnormals -- the ulp of
     the result is finer than the f32 rounding of the terms that produced it, and the reference's own
     comparison (Diff.cs:206, ``atol + rtol*|ref|``) is absolute there too. ``ulp=0`` disables the floor
-    (bit-exact comparison)."""
-    return _assert_half_close(got, ref, ulp, what, atol_row, _bf16_f32, "bf16")
+    (bit-exact comparison). The elements that pass only through the floor are counted (FLOOR_ONLY[what]);
+    ``max_floor_only`` bounds that count, so a regression that moves many elements there fails."""
+    return _assert_half_close(got, ref, ulp, what, atol_row, _bf16_f32, "bf16", max_floor_only)
 
 
-def _assert_half_close(got, ref, ulp, what, atol_row, to_f32, name):
+FLOOR_ONLY: dict = {}  # what -> (elements beyond ulp that passed through the absolute floor, elements compared)
+
+
+def _assert_half_close(got, ref, ulp, what, atol_row, to_f32, name, max_floor_only=None):
     got = np.asarray(got, np.uint16)
     ref = np.asarray(ref, np.uint16)
     assert got.shape == ref.shape, (got.shape, ref.shape)
@@ -58,6 +64,7 @@ def _assert_half_close(got, ref, ulp, what, atol_row, to_f32, name):
         atol_row = 0.0 if ulp == 0 else F32_ATOL_ROW
     d = bf16_ulp_diff(got, ref)
     over = d > ulp
+    beyond = int(over.sum())
     if over.any() and atol_row > 0:
         rf = to_f32(ref).astype(np.float64)
         gf = to_f32(got).astype(np.float64)
@@ -65,6 +72,11 @@ def _assert_half_close(got, ref, ulp, what, atol_row, to_f32, name):
         rms = np.sqrt(np.mean(r2 * r2, axis=1, keepdims=True))
         floor = np.broadcast_to(atol_row * rms, r2.shape).reshape(ref.shape)
         over &= ~(np.abs(gf - rf) <= floor)
+    floor_only = beyond - int(over.sum())
+    FLOOR_ONLY[what] = (floor_only, int(d.size))
+    if max_floor_only is not None and floor_only > max_floor_only:
+        raise AssertionError(f"{what}: {floor_only} of {d.size} {name} values pass only through the absolute floor "
+                             f"(at most {max_floor_only} allowed)")
     if over.any():
         i = np.unravel_index(np.argmax(np.where(over, d, -1)), d.shape)
         raise AssertionError(f"{what}: {int(over.sum())} of {d.size} {name} values beyond {ulp} ulp (and beyond the "

@@ -6,7 +6,7 @@ import pytest
 import oracle
 from sharplight_amd import native, synth
 from tests.devutil import Dev, log
-from tests.parity import assert_bf16_close, assert_f32_close
+from tests.parity import FLOOR_ONLY, assert_bf16_close, assert_f32_close
 
 pytestmark = pytest.mark.gpu
 
@@ -26,6 +26,11 @@ def _run(act, din, dout, g, u, *, gs=None, us=None, os_=None, pad=0):
         return d.get(po, (rows, ocols), NP[dout])
 
 
+# elements of C3 that may pass only through the bf16 rule's absolute floor, about twice the MI355X count:
+# SiLU and GELU-tanh none; GELU-erf 204 of 117M (0.5 g (1 + erf(g / sqrt 2)) cancels for very negative g)
+C3_FLOOR_ONLY = {"silu": 0, "gelu_tanh": 0, "gelu_erf": 400}
+
+
 @pytest.mark.parametrize("act", ["silu", "gelu_tanh", "gelu_erf"])
 def test_c3_full_shape(device, act):
     """BASELINE config 3 at [8192, 14336] bf16 (SwiGLU, GeGLU, and the GELU-erf gate at the same shape): every
@@ -33,7 +38,8 @@ def test_c3_full_shape(device, act):
     c = synth.c3()
     y = _run(act, "bf16", "bf16", c["gate"], c["up"])
     yref = oracle.gated(act, c["gate"], c["up"], dtype="bf16", threads=16)
-    assert_bf16_close(y, yref, what=f"C3 {act}")
+    assert_bf16_close(y, yref, what=f"C3 {act}", max_floor_only=C3_FLOOR_ONLY[act])
+    log(f"C3 {act}: {FLOOR_ONLY[f'C3 {act}'][0]} of {FLOOR_ONLY[f'C3 {act}'][1]} pass only through the absolute floor")
 
 
 @pytest.mark.parametrize("act", ["silu", "gelu_tanh", "gelu_erf"])

@@ -9,7 +9,7 @@ import pytest
 import oracle
 from sharplight_amd import native, synth
 from tests.devutil import Dev, log
-from tests.parity import assert_bf16_close, assert_f32_close
+from tests.parity import FLOOR_ONLY, assert_bf16_close, assert_f32_close
 
 pytestmark = pytest.mark.gpu
 
@@ -53,6 +53,12 @@ def _check(dout, y, ref, what):
         assert_f32_close(y, ref, what=what)
 
 
+# elements of C4 (q, k) that may pass only through the bf16 rule's absolute floor, about twice the MI355X
+# count (13 of 16.8M for q, 6 of 4.2M for k): the rotation's x0 c - x1 s cancels for a few pairs, whose
+# result then sits far below its row's scale
+C4_FLOOR_ONLY = (26, 12)
+
+
 def test_c4_qk_norm_rope(device):
     """Qwen3-8B attention prologue, q [4096,32,128] and k [4096,8,128] bf16 in one launch:
     per-head RMSNorm (eps 1e-6) then neox RoPE, theta 1e6, positions ~ U{0..32767}."""
@@ -60,9 +66,11 @@ def test_c4_qk_norm_rope(device):
     yq, yk = _run("bf16", "bf16", [(c["q"], c["wq"]), (c["k"], c["wk"])], c["pos"], 128, neox=True, base=c["base"],
                   norm=True, eps=c["eps"])
     assert_bf16_close(yq, oracle.qk_norm_rope(c["q"], c["pos"], c["wq"], c["eps"], dtype="bf16", base=c["base"]),
-                      what="C4 q")
+                      what="C4 q", max_floor_only=C4_FLOOR_ONLY[0])
     assert_bf16_close(yk, oracle.qk_norm_rope(c["k"], c["pos"], c["wk"], c["eps"], dtype="bf16", base=c["base"]),
-                      what="C4 k")
+                      what="C4 k", max_floor_only=C4_FLOOR_ONLY[1])
+    for w in ("C4 q", "C4 k"):
+        log(f"{w}: {FLOOR_ONLY[w][0]} of {FLOOR_ONLY[w][1]} pass only through the absolute floor")
 
 
 def test_rope_matches_ggml_fixture(device):

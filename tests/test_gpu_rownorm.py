@@ -7,7 +7,7 @@ import pytest
 import oracle
 from sharplight_amd import native, synth
 from tests.devutil import Dev, log
-from tests.parity import assert_bf16_close, assert_f32_close
+from tests.parity import FLOOR_ONLY, assert_bf16_close, assert_f32_close
 
 pytestmark = pytest.mark.gpu
 
@@ -78,13 +78,19 @@ def test_c1_rmsnorm_f32(device):
     assert rel < 1e-5
 
 
+# elements of the full-shape configs that may pass only through the bf16 rule's absolute floor (measured on
+# MI355X; the norm's outputs are products, nothing cancels)
+C2_FLOOR_ONLY = 0
+
+
 def test_c2_add_rmsnorm_bf16(device):
     """residual add + RMSNorm bf16 [8192, 4096], gamma f32, eps 1e-5; y and h both bf16."""
     c = synth.c2()
     y, h = _run("rms", "bf16", "bf16", c["x"], c["res"], c["w"], None, c["eps"], with_res=True, with_h=True)
     yref, href, _ = _reference("rms", "bf16", "bf16", c["x"], c["res"], c["w"], None, c["eps"], True)
     assert_bf16_close(h, href, ulp=0, what="C2 h (x+res rounded once: exact)")
-    assert_bf16_close(y, yref, what="C2 y")
+    assert_bf16_close(y, yref, what="C2 y", max_floor_only=C2_FLOOR_ONLY)
+    log(f"C2 y: {FLOOR_ONLY['C2 y'][0]} of {FLOOR_ONLY['C2 y'][1]} pass only through the absolute floor")
 
 
 CASES = [

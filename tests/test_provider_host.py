@@ -120,9 +120,10 @@ def test_supports_answers():
         assert ok or why
 
 
-def test_standalone_elementwise_lowers_to_its_own_launch():
-    """An Add with nothing to fuse into, a bias add, a scalar Mul and a lone Silu each become one elementwise
-    launch of the same segment (no split to the CPU)."""
+def test_elementwise_chain_is_one_group():
+    """GroupElementwiseChains (GraphLowerer.Fusion.cs:88-142): consecutive f32 elementwise nodes of one output
+    shape, each reading the open group, are one generated kernel -- an Add, a bias add, a scalar Mul and a
+    Silu here; a lone node is its own standalone launch; bf16 outputs are not fusable (IsFusable, :9-11)."""
     g = GraphBuilder()
     a = g.input("f32", "T", 64)
     b = g.input("f32", "T", 64)
@@ -131,9 +132,16 @@ def test_standalone_elementwise_lowers_to_its_own_launch():
     y = g.add(g.add(a, b), bias)
     y = g.mul(y, s)
     g.output(g.silu(y))
-    assert plan(g) == ["Add", "Add", "Mul", "Silu"]
+    assert plan(g) == ["fused[Add,Add,Mul,Silu]"]
     for k in range(4):
         assert _supports(g, k)[0]
+    g = GraphBuilder()
+    g.output(g.add(g.input("f32", "T", 64), g.weight("f32", 64)))
+    assert plan(g) == ["Add"]
+    g = GraphBuilder()
+    x = g.input("bf16", "T", 64)
+    g.output(g.silu(g.add(x, g.input("bf16", "T", 64))))
+    assert plan(g) == ["Add", "Silu"]
 
 
 def test_broadcast_support_answers():
@@ -188,12 +196,14 @@ def test_dual_matvec_falls_back_when_rows_do_not_fit_lds():
     assert plan(build(16384)) == ["matvec", "matvec", "fused[Silu,Mul]"]
 
 
-def test_residual_add_with_broadcast_is_not_fused_into_the_norm():
+def test_add_before_a_norm_folds_into_it():
+    """FoldNormTails (GraphLowerer.Fusion.cs:211-238): a broadcast Add before a norm joins the norm's launch
+    (the group program); two same-shape operands take the residual row-norm kernel."""
     g = GraphBuilder()
     x = g.input("f32", "T", 64)
     b = g.weight("f32", 64)
     g.output(g.rms_norm(g.add(x, b), g.weight("f32", 64)))
-    assert plan(g) == ["Add", "RmsNorm"]
+    assert plan(g) == ["fused[Add]+RmsNorm"]
     g = GraphBuilder()
     x = g.input("f32", "T", 64)
     g.output(g.rms_norm(g.add(x, g.input("f32", "T", 64)), g.weight("f32", 64)))
@@ -414,3 +424,62 @@ def test_matmul_bias_folds_into_the_matvec():
     x = g.input("f32", "T", 1024)
     g.output(g.add(g.matmul(x, g.weight("q4_k", 64, 1024)), g.weight("f32", 64)))
     assert plan(g) == ["x->q8 rows 1..8", "matvec+bias (int-dot rows 1..8)"]
+
+
+# ---- fused elementwise groups (GraphLowerer.Fusion.cs:88-285) -----------------------------------------------
+
+def test_bias_residual_norm_is_one_launch():
+    """Add(bias) + Add(residual) + RmsNorm: one group with the norm as its tail; the sum is stored only when
+    something else reads it."""
+    g = GraphBuilder()
+    x = g.input("f32", "T", 256)
+    r = g.input("f32", "T", 256)
+    h = g.add(g.add(x, g.weight("f32", 256)), r)
+    g.output(g.rms_norm(h, g.weight("f32", 256), eps=1e-6))
+    assert plan(g) == ["fused[Add,Add]+RmsNorm"]
+
+
+def test_norm_head_and_scale():
+    """FoldNormHeads (:240-284): RmsNorm -> Mul(w) -> Scale, the norm read only by the group: one launch; a norm
+    that is also a segment output stays its own launch."""
+    g = GraphBuilder()
+    x = g.input("f32", "T", 128)
+    n = g.rms_norm(x, None, eps=1e-6)
+    g.output(g.scale(g.mul(n, g.weight("f32", 128)), scale=0.5, bias=0.25))
+    assert plan(g) == ["RmsNorm+fused[Mul,Scale]"]
+    g = GraphBuilder()
+    x = g.input("f32", "T", 128)
+    n = g.output(g.rms_norm(x, None, eps=1e-6))
+    g.output(g.scale(g.mul(n, g.weight("f32", 128)), scale=0.5))
+    assert plan(g) == ["RmsNorm", "fused[Mul,Scale]"]
+
+
+def _gpt_oss_swiglu(K=256, N=512, alpha=1.702, limit=7.0):
+    """gpt-oss's clamped SwiGLU with the projections' biases (the model's MLP: gate and up products, their bias
+    adds, gate clamped above, up clamped both ways, gate * sigmoid(alpha gate) * (up + 1))."""
+    g = GraphBuilder()
+    x = g.input("f32", "T", K)
+    gate = g.add(g.matmul(x, g.weight("bf16", N, K)), g.weight("f32", N))
+    up = g.add(g.matmul(x, g.weight("bf16", N, K)), g.weight("f32", N))
+    gc = g.clip(gate, max=limit)
+    uc = g.clip(up, min=-limit, max=limit)
+    glu = g.mul(gc, g.unary("Sigmoid", g.scale(gc, scale=alpha)))
+    g.output(g.mul(g.scale(uc, bias=1.0), glu))
+    return g
+
+
+def test_gpt_oss_clamped_swiglu_merges_into_one_group():
+    """MergeElementwiseGroups (:160-205): the groups split by the up projection join along data flow, so the
+    bias adds, clamps and gating are one kernel after the two matvecs (the Add groups are not single-node, so
+    FoldMatMulBiases leaves them in the group, as the reference does)."""
+    assert plan(_gpt_oss_swiglu()) == ["matvec", "matvec",
+                                       "fused[Add,Clip,Add,Clip,Scale,Sigmoid,Mul,Scale,Mul]"]
+
+
+def test_group_merge_is_blocked_by_a_reader_in_between():
+    g = GraphBuilder()
+    x = g.input("f32", "T", 64)
+    a = g.scale(x, scale=2.0)                      # group 1
+    m = g.output(g.matmul(a, g.weight("bf16", 64, 64)))  # reads group 1's output: blocks the merge
+    g.output(g.add(a, m))                          # group 2 reads group 1's output
+    assert plan(g) == ["Scale", "matvec", "Add"]
