@@ -309,6 +309,12 @@ SLHIP_API int slhip_matvec_q8(int fmt, int dtype_y, const void* xq, int64_t T, i
 SLHIP_API int slhip_dual_matvec_q8(int act, int fmt, int dtype_y, const void* xq, int64_t T, int64_t K,
                                    const void* w_gate, const void* w_up, int64_t N, void* y, int64_t y_stride,
                                    slhip_stream stream);
+/* The decode FFN's gate/up pair in one call: slhip_quantize_q8 of x into `work` (work_bytes >= T *
+ * slhip_q8_row_bytes(K), 16-byte aligned), then slhip_dual_matvec_q8 -- the lowerer's "x->q8" and int-dot
+ * launches (GraphLowerer.IntDot.cs:82-117,226-249). SLHIP_ERR_INVALID when the workspace is too small. */
+SLHIP_API int slhip_dual_matvec_int8(int act, int fmt, int dtype_x, int dtype_y, const void* x, int64_t x_stride,
+                                     int64_t T, int64_t K, const void* w_gate, const void* w_up, int64_t N, void* y,
+                                     int64_t y_stride, void* work, int64_t work_bytes, slhip_stream stream);
 
 /*
  * Gated activation out = act(gate) * up over [rows, cols] (IMlpActivation.ActivateGated,

@@ -81,6 +81,11 @@ def build(verbose: bool = False, incremental: bool = False) -> str:
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
+    # a host pass that drops a kernel's launch stub still exits 0: refuse a library with undefined own symbols
+    nm = subprocess.run(["nm", "-D", "--undefined-only", tmp], capture_output=True, text=True)
+    missing = [l.split()[-1] for l in nm.stdout.splitlines() if "slhip" in l]
+    if missing:
+        raise RuntimeError(f"link left symbols of this library undefined: {missing[:5]}")
     os.replace(tmp, LIB)
     os.makedirs(os.path.join(TESTS, "_bin"), exist_ok=True)
     for name in CHECKS:

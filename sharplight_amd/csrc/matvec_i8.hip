@@ -161,9 +161,35 @@ int matvec_q8_common(int fmt, int dtype_y, const void* xq, int64_t T, int64_t K,
     }
 }
 
+// The decode FFN's gate/up projections in one call: x quantized into `work` (at least T q8 rows), then the
+// dual integer-dot matvec.
+int dual_int8_common(int act, int fmt, int dtype_x, int dtype_y, const void* x, int64_t x_stride, int64_t T, int64_t K,
+                     const void* wg, const void* wu, int64_t N, void* y, int64_t y_stride, void* work, int64_t work_bytes,
+                     hipStream_t st)
+{
+    if (T < 0 || K < 0) return fail(SLHIP_ERR_INVALID, "dual_matvec_int8: negative shape");
+    if (T == 0 || N == 0) return SLHIP_OK;
+    const int64_t need = T * (K + K / 2);
+    if (!work || work_bytes < need)
+        return fail(SLHIP_ERR_INVALID, "dual_matvec_int8: the workspace holds %lld bytes, %lld needed",
+                    static_cast<long long>(work ? work_bytes : 0), static_cast<long long>(need));
+    const int r = quantize_q8_common(dtype_x, x, x_stride, T, K, work, st);
+    if (r != SLHIP_OK) return r;
+    return matvec_q8_common(fmt, dtype_y, work, T, K, wg, wu, N, y, y_stride, nullptr, act, true, st);
+}
+
 }  // namespace slhip
 
 using namespace slhip;
+
+extern "C" SLHIP_API int slhip_dual_matvec_int8(int act, int fmt, int dtype_x, int dtype_y, const void* x,
+                                                int64_t x_stride, int64_t T, int64_t K, const void* w_gate,
+                                                const void* w_up, int64_t N, void* y, int64_t y_stride, void* work,
+                                                int64_t work_bytes, slhip_stream stream)
+{
+    return dual_int8_common(act, fmt, dtype_x, dtype_y, x, x_stride, T, K, w_gate, w_up, N, y, y_stride, work,
+                            work_bytes, to_stream(stream));
+}
 
 extern "C" SLHIP_API int64_t slhip_q8_row_bytes(int64_t K) { return K < 0 ? 0 : K + K / 2; }
 

@@ -7,6 +7,9 @@
 #include "quant.hpp"
 
 #include <limits.h>
+#include <stdlib.h>
+
+#include <type_traits>
 
 namespace slhip {
 
@@ -172,6 +175,320 @@ __device__ __forceinline__ float unit_dot(const I8Unit& u, const uint4& x0, cons
         const float p = __fmul_rn(u.a0, __fmul_rn(sc.x, static_cast<float>(s)));
         if constexpr (form == kScale32Off) return fmaf(u.b0, sc.y + sc.z, p);
         else return p;
+    }
+}
+
+// ---- several tokens on the integer matrix cores ----------------------------------------------------------
+//
+// v_mfma_i32_16x16x32_i8 multiplies 16 tokens' q8 values of one 32-value unit (A: lane l holds token l % 16,
+// values 8 (l / 16) .. + 7) with a 16-row tile's codes of the unit (B: lane l holds row l % 16, the same values)
+// into exact int32 sums (lane l: tokens 4 (l / 16) + i, row l % 16, so each lane decodes its own row's
+// multiplier and offset once per unit), so each unit's sums for 16 rows x 16 tokens take one
+// instruction and the scaling a (d s) + b gs per output runs on the VALU. Q6_K's two 16-value scale groups take
+// two instructions, each with the other half's codes masked to zero. A block of 8 waves takes a tile (a gate/up
+// pair of tiles); stages of 1024 values of the 16 rows go through LDS, double-buffered: the next stage's rows and
+// q8 scales move from HBM straight into LDS (global_load_lds, no registers) while the current one is computed;
+// each wave takes 4 units of a stage; the waves' partial sums meet in LDS at the end.
+
+// Bytes of one row per 1024-value stage and the width of the staging loads.
+template <int FMT> struct I8Stage;
+template <> struct I8Stage<SLHIP_FMT_Q8_0> { static constexpr int RB = 32 * 34, UB = 16; };
+template <> struct I8Stage<SLHIP_FMT_Q4_0> { static constexpr int RB = 32 * 18, UB = 16; };
+template <> struct I8Stage<SLHIP_FMT_Q4_1> { static constexpr int RB = 32 * 20, UB = 16; };
+template <> struct I8Stage<SLHIP_FMT_Q5_0> { static constexpr int RB = 32 * 22, UB = 16; };
+template <> struct I8Stage<SLHIP_FMT_Q5_1> { static constexpr int RB = 32 * 24, UB = 16; };
+template <> struct I8Stage<SLHIP_FMT_IQ4_NL> { static constexpr int RB = 32 * 18, UB = 16; };
+template <> struct I8Stage<SLHIP_FMT_MXFP4> { static constexpr int RB = 32 * 17, UB = 16; };
+template <> struct I8Stage<SLHIP_FMT_Q4_K> { static constexpr int RB = 4 * 144, UB = 16; };
+template <> struct I8Stage<SLHIP_FMT_Q5_K> { static constexpr int RB = 4 * 176, UB = 16; };
+template <> struct I8Stage<SLHIP_FMT_Q6_K> { static constexpr int RB = 4 * 210, UB = 4; };
+template <> struct I8Stage<SLHIP_FMT_IQ4_XS> { static constexpr int RB = 4 * 136, UB = 16; };
+
+constexpr int kI8MfWaves = 8;
+
+// The 8 codes of values 8 g .. 8 g + 7 of unit b of a row image (the bytes i8_unit's c[2 g], c[2 g + 1] hold).
+template <int FMT>
+__device__ __forceinline__ uint2 i8_codes8(const uint32_t* s, int b, int g)
+{
+    const LdsBytes B{s};
+    if constexpr (FMT == SLHIP_FMT_Q8_0) {
+        return lds_u64(s, b * 34 + 2 + 8 * g);
+    } else if constexpr (FMT == SLHIP_FMT_Q4_0 || FMT == SLHIP_FMT_Q4_1 || FMT == SLHIP_FMT_IQ4_NL ||
+                         FMT == SLHIP_FMT_Q5_0 || FMT == SLHIP_FMT_Q5_1 || FMT == SLHIP_FMT_MXFP4) {
+        constexpr int BB = FMT == SLHIP_FMT_MXFP4 ? 17 : Fmt<FMT>::BB;
+        constexpr int QS = FMT == SLHIP_FMT_MXFP4 ? 1 : Fmt<FMT>::QS;
+        const int o = b * BB;
+        const uint2 w = lds_u64(s, o + QS + 8 * (g & 1));
+        const uint32_t sh = g >= 2 ? 4u : 0u;
+        uint32_t lo = (w.x >> sh) & 0x0F0F0F0Fu, hi = (w.y >> sh) & 0x0F0F0F0Fu;
+        if constexpr (FMT == SLHIP_FMT_Q5_0 || FMT == SLHIP_FMT_Q5_1) {  // bit v of qh for value v
+            const uint32_t qh = lds_u32(s, o + Fmt<FMT>::QH) >> (8 * g);
+            lo |= ((((qh & 0xFu) * 0x00204081u) & 0x01010101u) << 4);
+            hi |= (((((qh >> 4) & 0xFu) * 0x00204081u) & 0x01010101u) << 4);
+        }
+        if constexpr (FMT == SLHIP_FMT_IQ4_NL) {
+            lo = iq4_lookup4(lo);
+            hi = iq4_lookup4(hi);
+        }
+        if constexpr (FMT == SLHIP_FMT_MXFP4) {
+            lo = fp4_lookup4(lo);
+            hi = fp4_lookup4(hi);
+        }
+        return make_uint2(lo, hi);
+    } else if constexpr (FMT == SLHIP_FMT_Q4_K || FMT == SLHIP_FMT_Q5_K) {
+        constexpr bool K5 = FMT == SLHIP_FMT_Q5_K;
+        const int sb = b >> 3, j = b & 7;
+        const int o = sb * (K5 ? 176 : 144);
+        const uint32_t* q = s + (o + (K5 ? 48 : 16) + 32 * (j >> 1) + 8 * g) / 4;
+        uint32_t lo = (q[0] >> (4 * (j & 1))) & 0x0F0F0F0Fu, hi = (q[1] >> (4 * (j & 1))) & 0x0F0F0F0Fu;
+        if constexpr (K5) {
+            const uint32_t* qh = s + (o + 16 + 8 * g) / 4;
+            lo |= ((qh[0] >> j) & 0x01010101u) << 4;
+            hi |= ((qh[1] >> j) & 0x01010101u) << 4;
+        }
+        return make_uint2(lo, hi);
+    } else if constexpr (FMT == SLHIP_FMT_Q6_K) {
+        const int sb = b >> 3, j = b & 7, n = j >> 2, qt = j & 3;
+        const int o = sb * 210;
+        const uint2 l = lds_u64(s, o + 64 * n + 32 * (qt & 1) + 8 * g);
+        const uint2 h = lds_u64(s, o + 128 + 32 * n + 8 * g);
+        const uint32_t ls = qt >= 2 ? 4u : 0u, hs = 2u * static_cast<uint32_t>(qt);
+        return make_uint2(((l.x >> ls) & 0x0F0F0F0Fu) | (((h.x >> hs) & 0x03030303u) << 4),
+                          ((l.y >> ls) & 0x0F0F0F0Fu) | (((h.y >> hs) & 0x03030303u) << 4));
+    } else {  // IQ4_XS
+        const int sb = b >> 3, ib = b & 7;
+        const uint2 w = lds_u64(s, sb * 136 + 8 + 16 * ib + 8 * (g & 1));
+        const uint32_t sh = g >= 2 ? 4u : 0u;
+        return make_uint2(iq4_lookup4((w.x >> sh) & 0x0F0F0F0Fu), iq4_lookup4((w.y >> sh) & 0x0F0F0F0Fu));
+    }
+    (void)B;
+}
+
+// The multipliers and offsets of unit b of a row image (i8_unit's scales without the codes).
+template <int FMT>
+__device__ __forceinline__ float4 i8_scales(const uint32_t* s, int b)
+{
+    const LdsBytes B{s};
+    if constexpr (FMT == SLHIP_FMT_Q8_0) {
+        const float d = half_at(s, b * 34);
+        return make_float4(d, d, 0.0f, 0.0f);
+    } else if constexpr (FMT == SLHIP_FMT_Q4_0 || FMT == SLHIP_FMT_Q4_1 || FMT == SLHIP_FMT_IQ4_NL ||
+                         FMT == SLHIP_FMT_Q5_0 || FMT == SLHIP_FMT_Q5_1) {
+        using F = Fmt<FMT>;
+        const int o = b * F::BB;
+        const float d = half_at(s, o);
+        const float off = FMT == SLHIP_FMT_IQ4_NL ? 0.0f : F::M ? half_at(s, o + 2) : static_cast<float>(F::OFF) * d;
+        return make_float4(d, d, off, off);
+    } else if constexpr (FMT == SLHIP_FMT_MXFP4) {
+        const float d = e8m0_half(B.u8(b * 17));
+        return make_float4(d, d, 0.0f, 0.0f);
+    } else if constexpr (FMT == SLHIP_FMT_Q4_K || FMT == SLHIP_FMT_Q5_K) {
+        const int sb = b >> 3, j = b & 7;
+        const int o = sb * (FMT == SLHIP_FMT_Q5_K ? 176 : 144);
+        uint32_t sc, mn;
+        if (j < 4) {
+            sc = B.u8(o + 4 + j) & 63u;
+            mn = B.u8(o + 8 + j) & 63u;
+        } else {
+            sc = (B.u8(o + 8 + j) & 0xFu) | ((B.u8(o + j) >> 6) << 4);
+            mn = (B.u8(o + 8 + j) >> 4) | ((B.u8(o + 4 + j) >> 6) << 4);
+        }
+        const float a = __fmul_rn(half_at(s, o), static_cast<float>(sc));
+        const float m = -__fmul_rn(half_at(s, o + 2), static_cast<float>(mn));
+        return make_float4(a, a, m, m);
+    } else if constexpr (FMT == SLHIP_FMT_Q6_K) {
+        const int sb = b >> 3, j = b & 7, n = j >> 2, qt = j & 3;
+        const int o = sb * 210;
+        const float d = half_at(s, o + 208);
+        const float a0 = __fmul_rn(d, static_cast<float>(static_cast<int8_t>(B.u8(o + 192 + 8 * n + 2 * qt))));
+        const float a1 = __fmul_rn(d, static_cast<float>(static_cast<int8_t>(B.u8(o + 193 + 8 * n + 2 * qt))));
+        return make_float4(a0, a1, -32.0f * a0, -32.0f * a1);
+    } else {
+        const int sb = b >> 3, ib = b & 7;
+        const int o = sb * 136;
+        const uint32_t sh = lds_u16(s, o + 2);
+        const int ls = static_cast<int>(((B.u8(o + 4 + ib / 2) >> (4 * (ib & 1))) & 0xFu) | (((sh >> (2 * ib)) & 3u) << 4));
+        const float a = __fmul_rn(half_at(s, o), static_cast<float>(ls - 32));
+        return make_float4(a, a, 0.0f, 0.0f);
+    }
+}
+
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+// global_load_lds of N bytes per lane: lane l's N bytes from src land at lds + N l (lds wave-uniform).
+template <int N>
+__device__ __forceinline__ void load_to_lds(const void* src, void* lds)
+{
+    static_assert(N == 4 || N == 16, "load width");
+    if constexpr (N == 16)
+        __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0);
+    else
+        __builtin_amdgcn_global_load_lds(src, lds, 4, 0, 0);
+}
+
+template <int FMT, bool DUAL>
+__global__ __launch_bounds__(64 * kI8MfWaves) void matvec_i8_mfma(I8Args a)
+{
+    constexpr int NM = DUAL ? 2 : 1;
+    constexpr int RB = I8Stage<FMT>::RB, UB = I8Stage<FMT>::UB;
+    constexpr int PITCH = RB + 16;  // bytes per staged row (rows of a tile land on different banks)
+    constexpr int SPR = PITCH / UB;  // load slots per staged row; the last 16 / UB of them are padding
+    constexpr int SLOTS = NM * 16 * SPR;
+    constexpr int NT = 64 * kI8MfWaves;
+    constexpr int LPT = (SLOTS + NT - 1) / NT;  // loads per thread and stage
+    constexpr int BPW = 32 / kI8MfWaves;  // units per wave and stage
+    constexpr bool H16 = kUnitForm<FMT> == kScale16Off;
+    static_assert(RB % UB == 0 && (UB == 16 || UB == 4), "stage shape");
+    static_assert(NT == 16 * 32, "one thread per token and unit of a stage stages the q8 scales");
+    static_assert(sizeof(uint32_t) * 2 * NM * 16 * (PITCH / 4) >= sizeof(float) * kI8MfWaves * NM * 4 * 64,
+                  "the cross-wave reduction reuses the weight stage");
+    __shared__ __align__(16) uint32_t stage[2][NM][16][PITCH / 4];
+    __shared__ float4 xsc[2][16][32];  // the q8 scales {d, d s_lo, d s_hi, 0} of [token][unit] of a stage
+    const int lane = threadIdx.x & 63;
+    const int wave = wave_id();
+    const int r = lane & 15, g = lane >> 4;
+    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 16;
+    const int K = static_cast<int>(a.K);
+    const int ns = K / 1024;
+    const int64_t xstride = K + K / 2;
+    int64_t tok = a.t0 + r;
+    tok = tok < a.T ? tok : a.T - 1;
+    const uint8_t* xrow = a.xq + tok * xstride;
+    // the scale this thread stages: token threadIdx / 32 of the pass, unit threadIdx % 32 of each stage
+    int64_t stok = a.t0 + (threadIdx.x >> 5);
+    stok = stok < a.T ? stok : a.T - 1;
+    const float4* xs_src = reinterpret_cast<const float4*>(a.xq + stok * xstride + K) + (threadIdx.x & 31);
+
+    // Load slot q = threadIdx + NT i is byte UB q of the stage: row (m, rr), slot c of SPR; a padding slot loads
+    // the row's last real piece again (the LDS image is contiguous, so the lanes of a wave fill one run).
+    const char* src[LPT];
+#pragma unroll
+    for (int i = 0; i < LPT; i++) {
+        int q = static_cast<int>(threadIdx.x) + NT * i;
+        q = q < SLOTS ? q : SLOTS - 1;
+        const int m = q / (16 * SPR), rem = q - m * (16 * SPR), rr = rem / SPR;
+        int c = rem - rr * SPR;
+        c = c < RB / UB ? c : RB / UB - 1;
+        int64_t row = n0 + rr;
+        row = row < a.N ? row : a.N - 1;
+        src[i] = (m == 0 ? a.wg : a.wu) + row * a.wrow + UB * c;
+    }
+    auto fetch = [&](int b, int s) {
+#pragma unroll
+        for (int i = 0; i < LPT; i++) {
+            if (NT * i + 64 * wave >= SLOTS) break;  // wave-uniform: the LDS run of a wave starts in the stage
+            if (NT * (i + 1) > SLOTS && static_cast<int>(threadIdx.x) + NT * i >= SLOTS) continue;
+            char* base = reinterpret_cast<char*>(&stage[b][0][0][0]) + UB * (NT * i + 64 * wave);
+            load_to_lds<UB>(src[i] + static_cast<int64_t>(s) * RB, base);
+        }
+        load_to_lds<16>(xs_src + 32 * s, &xsc[b][0][0] + 64 * wave);
+    };
+    struct Xs {
+        uint2 q[BPW];
+    };
+    auto fetch_x = [&](Xs& x, int s) {
+#pragma unroll
+        for (int j = 0; j < BPW; j++) x.q[j] = *reinterpret_cast<const uint2*>(xrow + (s * 32 + wave * BPW + j) * 32 + 8 * g);
+    };
+    // acc[m][i]: weight row n0 + r of matrix m, token t0 + 4 g + i (the MFMA's A operand is the q8 tokens, B the
+    // weight codes, so each lane decodes the multipliers of its own row once per unit)
+    float acc[NM][4];
+#pragma unroll
+    for (int m = 0; m < NM; m++)
+        for (int i = 0; i < 4; i++) acc[m][i] = 0.0f;
+    auto compute = [&](int b, const Xs& x) {
+#pragma unroll
+        for (int j = 0; j < BPW; j++) {
+            const int u = wave * BPW + j;
+            const long xb = static_cast<long>(__builtin_bit_cast(uint64_t, x.q[j]));
+            float4 xs[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) xs[i] = xsc[b][4 * g + i][u];
+#pragma unroll
+            for (int m = 0; m < NM; m++) {
+                const uint2 c = i8_codes8<FMT>(stage[b][m][r], u, g);
+                const float4 sc = i8_scales<FMT>(stage[b][m][r], u);
+                const i32x4_t z = {0, 0, 0, 0};
+                if constexpr (H16) {
+                    const bool first = g < 2;
+                    const long c0 = first ? static_cast<long>(__builtin_bit_cast(uint64_t, c)) : 0;
+                    const long c1 = first ? 0 : static_cast<long>(__builtin_bit_cast(uint64_t, c));
+                    const i32x4_t S0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(xb, c0, z, 0, 0, 0);
+                    const i32x4_t S1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(xb, c1, z, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        acc[m][i] += fmaf(sc.x, __fmul_rn(xs[i].x, static_cast<float>(S0[i])),
+                                          fmaf(sc.y, __fmul_rn(xs[i].x, static_cast<float>(S1[i])),
+                                               fmaf(sc.z, xs[i].y, __fmul_rn(sc.w, xs[i].z))));
+                } else {
+                    const i32x4_t S = __builtin_amdgcn_mfma_i32_16x16x32_i8(xb, static_cast<long>(__builtin_bit_cast(uint64_t, c)), z, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const float p = __fmul_rn(sc.x, __fmul_rn(xs[i].x, static_cast<float>(S[i])));
+                        acc[m][i] += kUnitForm<FMT> == kScale32Off ? fmaf(sc.z, xs[i].y + xs[i].z, p) : p;
+                    }
+                }
+            }
+        }
+    };
+    // vmcnt(0): the stage's LDS writes by global_load_lds (and the q8 codes in registers) have landed
+    constexpr int kWaitLoads = 0x0F70;
+    Xs xa, xb2;
+    fetch(0, 0);
+    fetch_x(xa, 0);
+    __builtin_amdgcn_s_waitcnt(kWaitLoads);
+    __syncthreads();
+    for (int s = 0; s < ns; s += 2) {  // two stages per iteration: the code register sets alternate statically
+        if (s + 1 < ns) {
+            fetch(1, s + 1);
+            fetch_x(xb2, s + 1);
+        }
+        compute(0, xa);
+        __builtin_amdgcn_s_waitcnt(kWaitLoads);
+        __syncthreads();
+        if (s + 1 >= ns) break;
+        if (s + 2 < ns) {
+            fetch(0, s + 2);
+            fetch_x(xa, s + 2);
+        }
+        compute(1, xb2);
+        __builtin_amdgcn_s_waitcnt(kWaitLoads);
+        __syncthreads();
+    }
+    // every wave is past its last read of the stage (the loop ends on a barrier): reuse it for the reduction
+    float* red = reinterpret_cast<float*>(&stage[0][0][0][0]);  // [wave][m][i][lane]
+#pragma unroll
+    for (int m = 0; m < NM; m++)
+        for (int i = 0; i < 4; i++) red[((wave * NM + m) * 4 + i) * 64 + lane] = acc[m][i];
+    __syncthreads();
+    if (wave == 0) {
+        float v[NM][4];
+#pragma unroll
+        for (int m = 0; m < NM; m++)
+            for (int i = 0; i < 4; i++) {
+                float t = 0.0f;
+                for (int w = 0; w < kI8MfWaves; w++) t += red[((w * NM + m) * 4 + i) * 64 + lane];
+                v[m][i] = t;
+            }
+        const int64_t n = n0 + r;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int64_t tt = a.t0 + 4 * g + i;
+            float out = v[0][i];
+            if constexpr (DUAL) {
+                const float act = a.act == SLHIP_ACT_SILU        ? activate<SLHIP_ACT_SILU>(out)
+                                  : a.act == SLHIP_ACT_GELU_TANH ? activate<SLHIP_ACT_GELU_TANH>(out)
+                                                                 : activate<SLHIP_ACT_GELU_ERF>(out);
+                out = act * v[NM - 1][i];
+            }
+            if (tt < a.T && n < a.N) {
+                if (!DUAL && a.bias) out = out + a.bias[n];
+                if (a.yt == SLHIP_F32)
+                    static_cast<float*>(a.y)[tt * a.ys + n] = out;
+                else
+                    static_cast<uint16_t*>(a.y)[tt * a.ys + n] = static_cast<uint16_t>(f32_to_bf16_bits(out));
+            }
+        }
     }
 }
 
@@ -405,9 +722,37 @@ static int i8_tt(const I8Args& a, int tt, hipStream_t st)
     }
 }
 
+// Tokens from which the integer-dot matvec takes the matrix cores (SLHIP_MATVEC_I8_MFMA_MIN_T; 0 disables), when
+// K is a multiple of 1024 (whole stages).
+inline int i8_mfma_min_tokens()
+{
+    static int v = -1;
+    if (v < 0) {
+        const char* e = getenv("SLHIP_MATVEC_I8_MFMA_MIN_T");
+        v = e ? atoi(e) : 9;
+    }
+    return v;
+}
+
+template <int FMT>
+int run_i8_mfma(I8Args a, bool dual, hipStream_t st)
+{
+    const dim3 grid(static_cast<unsigned>((a.N + 15) / 16));
+    for (int64_t t0 = 0; t0 < a.T; t0 += 16) {
+        a.t0 = t0;
+        if (dual) matvec_i8_mfma<FMT, true><<<grid, 64 * kI8MfWaves, 0, st>>>(a);
+        else matvec_i8_mfma<FMT, false><<<grid, 64 * kI8MfWaves, 0, st>>>(a);
+        const int r = check_launch("matvec_i8_mfma");
+        if (r != SLHIP_OK) return r;
+    }
+    return SLHIP_OK;
+}
+
 template <int FMT>
 int run_i8(I8Args a, bool dual, hipStream_t st)
 {
+    const int mt = i8_mfma_min_tokens();
+    if (mt > 0 && a.T >= mt && a.K % 1024 == 0 && a.wrow % I8Stage<FMT>::UB == 0) return run_i8_mfma<FMT>(a, dual, st);
     int tt = 8;
     while (tt > 1 && (tt / 2 >= a.T || i8_lds(tt, a.K, a.wrow, dual) > kI8MaxLds)) tt /= 2;
     if (i8_lds(tt, a.K, a.wrow, dual) > kI8MaxLds)

@@ -152,6 +152,12 @@ SINGLE_CASES = [  # (fmt, x dtype, y dtype, T, K, N)
     ("q8_0", "bf16", "f32", 1, 1056, 33),    # 1122 bytes
     ("q5_1", "f32", "bf16", 3, 2080, 24),    # 1560 bytes: 8-byte loads
     ("iq4_nl", "f32", "f32", 4, 96, 17),     # three blocks
+    # from nine tokens with K a multiple of 1024: the integer matrix cores (16-row tiles, 1024-value stages)
+    *[(f, "f32", "bf16", 9, 1024, 40) for f in FORMATS],      # one stage, a partial tile
+    ("q4_k", "bf16", "f32", 16, 3072, 48),   # three stages (an odd count)
+    ("q6_k", "f32", "f32", 20, 2048, 33),    # a full 16-token pass and a 4-token one
+    ("q8_0", "f32", "f32", 9, 14336, 16),    # fourteen stages, one tile
+    ("q4_0", "f32", "f32", 10, 1280, 24),    # K not whole stages: the VALU kernel
 ]
 
 
@@ -204,6 +210,10 @@ DUAL_CASES = [  # (act, fmt, x dtype, y dtype, T, K, N)
     ("silu", "iq4_xs", "f32", "f32", 1, 1280, 40),
     ("silu", "mxfp4", "f32", "f32", 5, 2880, 33),       # gpt-oss's hidden size (rows of 1530 bytes)
     ("silu", "q6_k", "f32", "f32", 16, 3072, 17),
+    ("gelu_erf", "q5_k", "bf16", "bf16", 12, 4096, 100),   # matrix cores, dual
+    ("silu", "iq4_xs", "f32", "f32", 11, 2048, 64),
+    ("gelu_tanh", "mxfp4", "f32", "bf16", 9, 1024, 16),
+    ("silu", "q8_0", "f32", "f32", 16, 4096, 14336),        # the lowerer's largest Q8_0 int-dot batch
 ]
 
 
@@ -225,6 +235,29 @@ def test_dual_matvec_q8(device, act, fmt, dx, dy, T, K, N):
     if act == "gelu_erf":
         tol = tol + 0.5 * np.abs(g64 * u) * 4.2e-7
     _compare(y, dy, ref, tol, f"dual_matvec_q8 {act} {fmt}")
+
+
+@pytest.mark.parametrize("fmt,dx,T,K,N", [("q4_k", "f32", 3, 4096, 200), ("q8_0", "bf16", 12, 2048, 64)])
+def test_dual_matvec_int8_one_call(device, fmt, dx, T, K, N):
+    """slhip_dual_matvec_int8 (quantize into the caller's workspace, then the dual matvec) equals the two calls
+    bit for bit; a workspace below T q8 rows is refused."""
+    seed = _seed("one_call", fmt, dx, T)
+    rg = synth.quant_table(fmt, N, K, seed=seed, tid=1)
+    ru = synth.quant_table(fmt, N, K, seed=seed, tid=2)
+    x, _ = _x(dx, T, K, seed)
+    two = _run(fmt, dx, "f32", x, [rg, ru], N, K, act="silu")
+    with Dev() as d:
+        px, pg, pu = d.put(x), d.put(rg), d.put(ru)
+        py = d.empty(T * N * 4)
+        wb = T * native.q8_row_bytes(K)
+        work = d.empty(wb)
+        log(f"dual_matvec_int8 fmt={fmt} x={dx} T={T} K={K} N={N}")
+        native.dual_matvec_int8("silu", fmt, dx, "f32", px, T, K, pg, pu, N, py, work, wb)
+        native.synchronize()
+        one = d.get(py, (T, N), np.float32)
+        with pytest.raises(native.SlhipArgumentError, match="workspace"):
+            native.dual_matvec_int8("silu", fmt, dx, "f32", px, T, K, pg, pu, N, py, work, wb - 1)
+    assert np.array_equal(one.view(np.uint32), two.view(np.uint32))
 
 
 def test_refusals(device):
