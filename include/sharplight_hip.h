@@ -315,6 +315,15 @@ SLHIP_API int slhip_dual_matvec_q8(int act, int fmt, int dtype_y, const void* xq
 SLHIP_API int slhip_dual_matvec_int8(int act, int fmt, int dtype_x, int dtype_y, const void* x, int64_t x_stride,
                                      int64_t T, int64_t K, const void* w_gate, const void* w_up, int64_t N, void* y,
                                      int64_t y_stride, void* work, int64_t work_bytes, slhip_stream stream);
+/* slhip_dual_matvec_int8 without a workspace argument and without allocating: no counterpart in the reference;
+ * for callers that cannot allocate device memory (code under HIP graph capture, tight serving loops). The
+ * quantized rows go to a static 1 MiB array per device (T * 1.5 K <= 1048576 bytes, else SLHIP_ERR_UNSUPPORTED),
+ * which every call on that device shares: calls that overlap on one GPU (several streams, several host threads)
+ * race on it. The same kernels and results as slhip_dual_matvec_int8. */
+SLHIP_API int slhip_dual_matvec_int8_noalloc(int act, int fmt, int dtype_x, int dtype_y, const void* x,
+                                             int64_t x_stride, int64_t T, int64_t K, const void* w_gate,
+                                             const void* w_up, int64_t N, void* y, int64_t y_stride,
+                                             slhip_stream stream);
 
 /*
  * Gated activation out = act(gate) * up over [rows, cols] (IMlpActivation.ActivateGated,

@@ -28,6 +28,8 @@
 
 #include <stdlib.h>
 
+#include <mutex>
+
 namespace slhip {
 
 __device__ __forceinline__ int32_t sat_i32(float v)
@@ -162,7 +164,8 @@ int matvec_q8_common(int fmt, int dtype_y, const void* xq, int64_t T, int64_t K,
 }
 
 // The decode FFN's gate/up projections in one call: x quantized into `work` (at least T q8 rows), then the
-// dual integer-dot matvec.
+// dual integer-dot matvec. The no-allocation variant below runs the same two kernels on a file-scope device
+// array instead of `work`.
 int dual_int8_common(int act, int fmt, int dtype_x, int dtype_y, const void* x, int64_t x_stride, int64_t T, int64_t K,
                      const void* wg, const void* wu, int64_t N, void* y, int64_t y_stride, void* work, int64_t work_bytes,
                      hipStream_t st)
@@ -178,6 +181,32 @@ int dual_int8_common(int act, int fmt, int dtype_x, int dtype_y, const void* x, 
     return matvec_q8_common(fmt, dtype_y, work, T, K, wg, wu, N, y, y_stride, nullptr, act, true, st);
 }
 
+// The no-allocation variant's workspace: 1 MiB per device (T * 1.5 K bytes, e.g. 32 rows of K = 16384 or 170 of
+// K = 4096), held by every GPU the library runs on until the process ends. Host code reaches it only through the
+// device address hipGetSymbolAddress gives, once per device.
+constexpr int64_t kStaticWorkBytes = int64_t{1} << 20;
+static __device__ __align__(256) uint8_t scratch[kStaticWorkBytes];
+
+constexpr int kMaxDevices = 64;
+static void* g_scratch_ptr[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+static int static_work(void** out)
+{
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+        return fail(SLHIP_ERR_HIP, "dual_matvec_int8_noalloc: no current device");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) return fail(SLHIP_ERR_HIP, "dual_matvec_int8_noalloc: workspace address: %s", hipGetErrorString(e));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return SLHIP_OK;
+}
+
 }  // namespace slhip
 
 using namespace slhip;
@@ -189,6 +218,26 @@ extern "C" SLHIP_API int slhip_dual_matvec_int8(int act, int fmt, int dtype_x, i
 {
     return dual_int8_common(act, fmt, dtype_x, dtype_y, x, x_stride, T, K, w_gate, w_up, N, y, y_stride, work,
                             work_bytes, to_stream(stream));
+}
+
+extern "C" SLHIP_API int slhip_dual_matvec_int8_noalloc(int act, int fmt, int dtype_x, int dtype_y, const void* x,
+                                                        int64_t x_stride, int64_t T, int64_t K, const void* w_gate,
+                                                        const void* w_up, int64_t N, void* y, int64_t y_stride,
+                                                        slhip_stream stream)
+{
+    if (T > 0 && K > 0 && T * (K + K / 2) > kStaticWorkBytes)
+        return fail(SLHIP_ERR_UNSUPPORTED,
+                    "dual_matvec_int8_noalloc: %lld rows of K = %lld need %lld bytes of workspace, above the static %lld",
+                    static_cast<long long>(T), static_cast<long long>(K), static_cast<long long>(T * (K + K / 2)),
+                    static_cast<long long>(kStaticWorkBytes));
+    if (T <= 0 || N <= 0)  // the shape checks (and the empty no-op) of the workspace form
+        return dual_int8_common(act, fmt, dtype_x, dtype_y, x, x_stride, T, K, w_gate, w_up, N, y, y_stride, nullptr, 0,
+                                to_stream(stream));
+    void* work = nullptr;
+    const int r = static_work(&work);
+    if (r != SLHIP_OK) return r;
+    return dual_int8_common(act, fmt, dtype_x, dtype_y, x, x_stride, T, K, w_gate, w_up, N, y, y_stride, work,
+                            kStaticWorkBytes, to_stream(stream));
 }
 
 extern "C" SLHIP_API int64_t slhip_q8_row_bytes(int64_t K) { return K < 0 ? 0 : K + K / 2; }

@@ -215,6 +215,7 @@ SIGNATURES = {
     "slhip_q8_row_bytes": (_I64, [_I64]),
     "slhip_ew_program_run": (_I, [ctypes.POINTER(EwProgram), _I64, _I64, _P]),
     "slhip_dual_matvec_int8": (_I, [_I, _I, _I, _I, _P, _I64, _I64, _I64, _P, _P, _I64, _P, _I64, _P, _I64, _P]),
+    "slhip_dual_matvec_int8_noalloc": (_I, [_I, _I, _I, _I, _P, _I64, _I64, _I64, _P, _P, _I64, _P, _I64, _P]),
     "slhip_quantize_q8": (_I, [_I, _P, _I64, _I64, _I64, _P, _P]),
     "slhip_matvec_q8": (_I, [_I, _I, _P, _I64, _I64, _P, _I64, _P, _I64, _P, _P]),
     "slhip_dual_matvec_q8": (_I, [_I, _I, _I, _P, _I64, _I64, _P, _P, _I64, _P, _I64, _P]),
@@ -537,6 +538,14 @@ def dual_matvec_int8(act, fmt, dtype_x, dtype_y, x, T, K, w_gate, w_up, N, y, wo
     call("slhip_dual_matvec_int8", ACTS.get(act, act), FORMATS.get(fmt, fmt), DTYPES.get(dtype_x, dtype_x),
          DTYPES.get(dtype_y, dtype_y), ptr(x), K if x_stride is None else x_stride, T, K, ptr(w_gate), ptr(w_up), N,
          ptr(y), N if y_stride is None else y_stride, ptr(work), work_bytes, stream)
+
+
+def dual_matvec_int8_noalloc(act, fmt, dtype_x, dtype_y, x, T, K, w_gate, w_up, N, y, *, x_stride=None,
+                             y_stride=None, stream=None):
+    """dual_matvec_int8 on the library's static per-device workspace (allocates nothing)."""
+    call("slhip_dual_matvec_int8_noalloc", ACTS.get(act, act), FORMATS.get(fmt, fmt), DTYPES.get(dtype_x, dtype_x),
+         DTYPES.get(dtype_y, dtype_y), ptr(x), K if x_stride is None else x_stride, T, K, ptr(w_gate), ptr(w_up), N,
+         ptr(y), N if y_stride is None else y_stride, stream)
 
 
 def gated_act(act, dtype_in, dtype_out, gate, up, out, rows, cols, *, gate_stride=None, up_stride=None,
