@@ -171,6 +171,21 @@ class LayerNorm(Workload):
                        w=self.w.slot(0), b=self.b.slot(0), eps=self.eps, stream=stream)
 
 
+class RmsNormPlain(LayerNorm):
+    """RMSNorm with gamma at LayerNorm's C2-shape workload (no residual, no bias): the same two streams, for
+    comparing the two kinds' kernels."""
+
+    def __init__(self):
+        super().__init__(8192, 4096, "bf16")
+        self.name = "rmsnorm_bf16"
+        self.desc = "x bf16 [8192, 4096], gamma f32 [4096] -> y bf16 (RMSNorm, no residual)"
+        self.bytes_per_step -= self.D * 4
+
+    def launch(self, i, stream):
+        native.rownorm("rms", self.dtype, self.dtype, self.x.slot(i), self.y.slot(i), self.rows, self.D,
+                       w=self.w.slot(0), eps=self.eps, stream=stream)
+
+
 class BiasAdd(Workload):
     """A lone broadcast Add (slhip_binary): x [8192, 4096] bf16 + bias [4096] bf16 -> bf16."""
     name = "bias_add_bf16"
@@ -413,6 +428,7 @@ WORKLOADS = {
     "c3_geglu_erf_bf16": lambda: C3("gelu_erf"),
     "layernorm_vit_f32": lambda: LayerNorm(197, 768, "f32"),
     "layernorm_bf16": lambda: LayerNorm(8192, 4096, "bf16"),
+    "rmsnorm_bf16": lambda: RmsNormPlain(),
     "bias_add_bf16": lambda: BiasAdd(),
     "c4_qknorm_rope_bf16": lambda: C4(),
     "c5_gather_q8_0": lambda: C5("q8_0"),

@@ -323,6 +323,195 @@ __global__ __launch_bounds__(1024) void rownorm_vec(RowNormArgs a, int wpr)
     }
 }
 
+// Sums of R rows over their row groups at once: the same butterfly and the same LDS order per row as
+// group_reduce, with one pair of barriers for all R.
+template <int R>
+__device__ __forceinline__ void group_reduce_rows(float* v, int wpr, int group, int wave_in_group, float* red)
+{
+#pragma unroll
+    for (int i = 0; i < R; i++) v[i] = wave_sum(v[i]);
+    if (wpr == 1) return;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) {
+#pragma unroll
+        for (int i = 0; i < R; i++) red[(group * 16 + wave_in_group) * R + i] = v[i];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < R; i++) {
+        float s = 0.f;
+        for (int w = 0; w < wpr; w++) s += red[(group * 16 + w) * R + i];
+        v[i] = s;
+    }
+}
+
+// Two-byte rows without a residual or copies, R rows per row group: the group loads all R rows, reduces
+// them together and then, per vector, reads the norm weight and bias once for the R rows. Each row's
+// arithmetic (and so its result) is that of rownorm_vec; what changes is that the f32 weight and bias,
+// which are 4x the row's bytes between them for a bf16 LayerNorm and come from the L2 for every row, are
+// read once per R rows, and the block barriers of the reductions are shared by the R rows.
+template <int DTI, int DTO, int NV, int R>
+__global__ __launch_bounds__(1024) void rownorm_rows(RowNormArgs a, int wpr)
+{
+    using VI = Vec<DTI>;
+    using RV = RawVec<16>;
+    static_assert(VI::BYTES == 2, "rows of 2-byte values");
+    constexpr int E = 16 / VI::BYTES;
+    __shared__ float red[4 * 16 * R];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = wave_id();
+    const int group = wave / wpr;
+    const int wig = wave - group * wpr;
+    const int groups = blockDim.x / (64 * wpr);
+    const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * groups + group) * R;
+    const int tpr = 64 * wpr;
+    const int t = wig * 64 + lane;
+    const int nvec = static_cast<int>(a.D / E);
+
+    // As in rownorm_vec: unconditional loads and stores, lanes past the row's end on its last vector, rows
+    // past the last row on the last row (and storing nothing).
+    int jv[NV];
+    bool own[NV];
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        const int j = t + k * tpr;
+        own[k] = j < nvec;
+        jv[k] = own[k] ? j : nvec - 1;
+    }
+    int64_t row[R];
+    RV::T raw[R][NV];
+#pragma unroll
+    for (int i = 0; i < R; i++) {
+        row[i] = row0 + i < a.rows ? row0 + i : a.rows - 1;
+        const char* xr = static_cast<const char*>(a.x) + row[i] * a.xs * VI::BYTES;
+#pragma unroll
+        for (int k = 0; k < NV; k++) raw[i][k] = RV::load(xr + static_cast<int64_t>(jv[k]) * 16);
+    }
+    const bool has_w = a.w != nullptr, has_b = a.b != nullptr;
+    // the weight and bias of a vector are loaded once for the R rows (loading the next vector's ahead, or the
+    // first one's with the rows, measured ~6% slower: the registers cost a wave per SIMD)
+    auto load_wb = [&](int k, float* w8, float* b8) {
+        if (has_w) {
+            const float4* wp = reinterpret_cast<const float4*>(a.w + static_cast<int64_t>(jv[k]) * E);
+#pragma unroll
+            for (int q4 = 0; q4 < E / 4; q4++) {
+                const float4 w4 = wp[q4];
+                w8[4 * q4 + 0] = w4.x;
+                w8[4 * q4 + 1] = w4.y;
+                w8[4 * q4 + 2] = w4.z;
+                w8[4 * q4 + 3] = w4.w;
+            }
+        }
+        if (has_b) {
+            const float4* bp = reinterpret_cast<const float4*>(a.b + static_cast<int64_t>(jv[k]) * E);
+#pragma unroll
+            for (int q4 = 0; q4 < E / 4; q4++) {
+                const float4 b4 = bp[q4];
+                b8[4 * q4 + 0] = b4.x;
+                b8[4 * q4 + 1] = b4.y;
+                b8[4 * q4 + 2] = b4.z;
+                b8[4 * q4 + 3] = b4.w;
+            }
+        }
+    };
+    auto launder = [&]() {
+#pragma unroll
+        for (int i = 0; i < R; i++)
+#pragma unroll
+            for (int k = 0; k < NV; k++) RV::launder(raw[i][k]);
+    };
+
+    const float inv_d = 1.0f / static_cast<float>(a.D);
+    float mean[R], scale[R];
+    if (a.kind == SLHIP_NORM_LAYER) {
+        float s[R];
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            s[i] = 0.f;
+#pragma unroll
+            for (int k = 0; k < NV; k++) {
+                float v[E];
+                RV::template unpack<DTI>(raw[i][k], v);
+#pragma unroll
+                for (int e = 0; e < E; e++) s[i] += own[k] ? v[e] : 0.0f;
+            }
+        }
+        group_reduce_rows<R>(s, wpr, group, wig, red);
+        launder();
+        float q[R];
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            mean[i] = s[i] * inv_d;
+            q[i] = 0.f;
+#pragma unroll
+            for (int k = 0; k < NV; k++) {
+                float v[E];
+                RV::template unpack<DTI>(raw[i][k], v);
+#pragma unroll
+                for (int e = 0; e < E; e++) {
+                    const float d = own[k] ? v[e] - mean[i] : 0.0f;
+                    q[i] = fmaf(d, d, q[i]);
+                }
+            }
+        }
+        group_reduce_rows<R>(q, wpr, group, wig, red);
+#pragma unroll
+        for (int i = 0; i < R; i++) scale[i] = 1.0f / sqrtf(q[i] * inv_d + a.eps);
+    } else {
+        float q[R];
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            mean[i] = 0.f;
+            q[i] = 0.f;
+#pragma unroll
+            for (int k = 0; k < NV; k++) {
+                float v[E];
+                RV::template unpack<DTI>(raw[i][k], v);
+#pragma unroll
+                for (int e = 0; e < E; e++) {
+                    const float x = own[k] ? v[e] : 0.0f;
+                    q[i] = fmaf(x, x, q[i]);
+                }
+            }
+        }
+        group_reduce_rows<R>(q, wpr, group, wig, red);
+#pragma unroll
+        for (int i = 0; i < R; i++)
+            scale[i] = a.kind == SLHIP_NORM_RMS ? 1.0f / sqrtf(q[i] * inv_d + a.eps) : 1.0f / sqrtf(q[i] + a.eps);
+    }
+    if (row0 >= a.rows) return;
+    launder();
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        float w8[E], b8[E];
+        load_wb(k, w8, b8);
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            if (row0 + i >= a.rows) break;  // wave-uniform
+            float v[E], o[E];
+            RV::template unpack<DTI>(raw[i][k], v);
+            if (a.kind == SLHIP_NORM_LAYER) {
+#pragma unroll
+                for (int e = 0; e < E; e++) o[e] = (v[e] - mean[i]) * scale[i];
+            } else {
+#pragma unroll
+                for (int e = 0; e < E; e++) o[e] = v[e] * scale[i];
+            }
+            if (has_w) {
+#pragma unroll
+                for (int e = 0; e < E; e++) o[e] *= w8[e];
+            }
+            if (has_b) {
+#pragma unroll
+                for (int e = 0; e < E; e++) o[e] += b8[e];
+            }
+            char* yr = static_cast<char*>(a.y) + row[i] * a.ys * Vec<DTO>::BYTES;
+            store_packed<DTO, E>(yr + static_cast<int64_t>(jv[k]) * E * Vec<DTO>::BYTES, o);
+        }
+    }
+}
+
 // Scalar fallback: one 256-thread block per row, re-reading the row from global memory (cache-resident)
 // for each pass.
 template <int DTI, int DTO>
@@ -429,6 +618,22 @@ static int launch_vec(const RowNormArgs& a, int nv, int wpr, hipStream_t st)
     return check_launch("rownorm_vec");
 }
 
+template <int DTI, int DTO, int R>
+static int launch_rows(const RowNormArgs& a, int nv, int wpr, hipStream_t st)
+{
+    int groups = wpr >= 4 ? 1 : 4 / wpr;
+    int threads = 64 * wpr * groups;
+    dim3 grid(static_cast<unsigned>((a.rows + groups * R - 1) / (groups * R)));
+    switch (nv) {
+    case 1: rownorm_rows<DTI, DTO, 1, R><<<grid, threads, 0, st>>>(a, wpr); break;
+    case 2: rownorm_rows<DTI, DTO, 2, R><<<grid, threads, 0, st>>>(a, wpr); break;
+    case 3: rownorm_rows<DTI, DTO, 3, R><<<grid, threads, 0, st>>>(a, wpr); break;
+    case 4: rownorm_rows<DTI, DTO, 4, R><<<grid, threads, 0, st>>>(a, wpr); break;
+    default: return fail(SLHIP_ERR_INVALID, "internal: bad vector count %d", nv);
+    }
+    return check_launch("rownorm_rows");
+}
+
 static bool aligned_to(const void* p, int n) { return reinterpret_cast<uintptr_t>(p) % n == 0; }
 
 // Whether the rows fit the vector kernel with VB-byte input vectors: D a multiple of the vector's values,
@@ -467,6 +672,12 @@ static int launch_fitting(const RowNormArgs& a, hipStream_t st)
     }
     int64_t per = (nvec + 64 * wpr - 1) / (64 * wpr);
     int nv = per == 7 ? 8 : static_cast<int>(per);
+    if constexpr (VB == 16 && Vec<DTI>::BYTES == 2) {
+        // two-byte rows without a residual or copies: R rows per row group (SLHIP_ROWNORM_ROWS, 1 or 2), up to
+        // 4 vectors per lane (beyond that two rows' registers spill at 1024-thread blocks)
+        const int r = env_int("SLHIP_ROWNORM_ROWS", 2);
+        if (!a.res && !a.yq && !a.y16 && a.y && r == 2 && nv <= 4) return launch_rows<DTI, DTO, 2>(a, nv, wpr, st);
+    }
     if constexpr (VB == 16) {
         if (a.yq)
             return a.res ? launch_vec<DTI, DTO, true, true, VB>(a, nv, wpr, st)
