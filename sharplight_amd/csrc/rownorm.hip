@@ -44,12 +44,13 @@ struct RowNormArgs {
     int64_t yqs;   // their row stride in bytes
 };
 
+// Sum over a row group: a wave butterfly, then (several waves) one LDS exchange. Each call of a kernel passes
+// its own LDS region, so no barrier is needed ahead of the writes.
 template <int NG>  // number of row groups sharing the LDS exchange
 __device__ __forceinline__ float group_reduce(float v, int wpr, int group, int wave_in_group, float* red)
 {
     v = wave_sum(v);
     if (wpr == 1) return v;
-    __syncthreads();
     if ((threadIdx.x & 63) == 0) red[group * 16 + wave_in_group] = v;
     __syncthreads();
     float s = 0.f;
@@ -102,7 +103,7 @@ __global__ __launch_bounds__(1024) void rownorm_vec(RowNormArgs a, int wpr)
     static_assert(VB == 16 || (VB == 8 && VI::BYTES == 2 && !Q), "8-byte vectors: 2-byte rows, no E4M3 copy");
     constexpr int E = VB / VI::BYTES;  // elements per input vector
     constexpr int G = 128 / E;  // lanes per 128-value E4M3 group
-    __shared__ float red[4 * 16];
+    __shared__ float red[2][4 * 16];  // one region per reduction
 
     const int lane = threadIdx.x & 63;
     const int wave = wave_id();
@@ -202,7 +203,7 @@ __global__ __launch_bounds__(1024) void rownorm_vec(RowNormArgs a, int wpr)
         for (int k = 0; k < NV; k++)
 #pragma unroll
             for (int e = 0; e < E; e++) s += own[k] ? v[k][e] : 0.0f;
-        mean = group_reduce<4>(s, wpr, group, wig, red) * inv_d;
+        mean = group_reduce<4>(s, wpr, group, wig, red[0]) * inv_d;
         store_h();
         launder();
         float q = 0.f;
@@ -215,7 +216,7 @@ __global__ __launch_bounds__(1024) void rownorm_vec(RowNormArgs a, int wpr)
                 q = fmaf(d, d, q);
             }
         }
-        const float var = group_reduce<4>(q, wpr, group, wig, red) * inv_d;
+        const float var = group_reduce<4>(q, wpr, group, wig, red[1]) * inv_d;
         scale = 1.0f / sqrtf(var + a.eps);
     } else {
         float q = 0.f;
@@ -226,7 +227,7 @@ __global__ __launch_bounds__(1024) void rownorm_vec(RowNormArgs a, int wpr)
                 const float x = own[k] ? v[k][e] : 0.0f;
                 q = fmaf(x, x, q);
             }
-        const float ss = group_reduce<4>(q, wpr, group, wig, red);
+        const float ss = group_reduce<4>(q, wpr, group, wig, red[1]);
         store_h();
         scale = a.kind == SLHIP_NORM_RMS ? 1.0f / sqrtf(ss * inv_d + a.eps) : 1.0f / sqrtf(ss + a.eps);
     }
@@ -324,14 +325,14 @@ __global__ __launch_bounds__(1024) void rownorm_vec(RowNormArgs a, int wpr)
 }
 
 // Sums of R rows over their row groups at once: the same butterfly and the same LDS order per row as
-// group_reduce, with one pair of barriers for all R.
+// group_reduce, with one barrier for all R. Each call of a kernel passes its own LDS region, so no barrier
+// is needed ahead of the writes.
 template <int R>
 __device__ __forceinline__ void group_reduce_rows(float* v, int wpr, int group, int wave_in_group, float* red)
 {
 #pragma unroll
     for (int i = 0; i < R; i++) v[i] = wave_sum(v[i]);
     if (wpr == 1) return;
-    __syncthreads();
     if ((threadIdx.x & 63) == 0) {
 #pragma unroll
         for (int i = 0; i < R; i++) red[(group * 16 + wave_in_group) * R + i] = v[i];
@@ -357,7 +358,7 @@ __global__ __launch_bounds__(1024) void rownorm_rows(RowNormArgs a, int wpr)
     using RV = RawVec<16>;
     static_assert(VI::BYTES == 2, "rows of 2-byte values");
     constexpr int E = 16 / VI::BYTES;
-    __shared__ float red[4 * 16 * R];
+    __shared__ float red[2][4 * 16 * R];  // one region per reduction
 
     const int lane = threadIdx.x & 63;
     const int wave = wave_id();
@@ -437,7 +438,7 @@ __global__ __launch_bounds__(1024) void rownorm_rows(RowNormArgs a, int wpr)
                 for (int e = 0; e < E; e++) s[i] += own[k] ? v[e] : 0.0f;
             }
         }
-        group_reduce_rows<R>(s, wpr, group, wig, red);
+        group_reduce_rows<R>(s, wpr, group, wig, red[0]);
         launder();
         float q[R];
 #pragma unroll
@@ -455,7 +456,7 @@ __global__ __launch_bounds__(1024) void rownorm_rows(RowNormArgs a, int wpr)
                 }
             }
         }
-        group_reduce_rows<R>(q, wpr, group, wig, red);
+        group_reduce_rows<R>(q, wpr, group, wig, red[1]);
 #pragma unroll
         for (int i = 0; i < R; i++) scale[i] = 1.0f / sqrtf(q[i] * inv_d + a.eps);
     } else {
@@ -475,7 +476,7 @@ __global__ __launch_bounds__(1024) void rownorm_rows(RowNormArgs a, int wpr)
                 }
             }
         }
-        group_reduce_rows<R>(q, wpr, group, wig, red);
+        group_reduce_rows<R>(q, wpr, group, wig, red[1]);
 #pragma unroll
         for (int i = 0; i < R; i++)
             scale[i] = a.kind == SLHIP_NORM_RMS ? 1.0f / sqrtf(q[i] * inv_d + a.eps) : 1.0f / sqrtf(q[i] + a.eps);
