@@ -190,19 +190,20 @@ __device__ __forceinline__ float unit_dot(const I8Unit& u, const uint4& x0, cons
 // q8 scales move from HBM straight into LDS (global_load_lds, no registers) while the current one is computed;
 // each wave takes 4 units of a stage; the waves' partial sums meet in LDS at the end.
 
-// Bytes of one row per 1024-value stage and the width of the staging loads.
+// Bytes of one row per 1024-value stage, the width of the staging loads, and whether the multipliers go
+// through a per-wave table (below).
 template <int FMT> struct I8Stage;
-template <> struct I8Stage<SLHIP_FMT_Q8_0> { static constexpr int RB = 32 * 34, UB = 16; };
-template <> struct I8Stage<SLHIP_FMT_Q4_0> { static constexpr int RB = 32 * 18, UB = 16; };
-template <> struct I8Stage<SLHIP_FMT_Q4_1> { static constexpr int RB = 32 * 20, UB = 16; };
-template <> struct I8Stage<SLHIP_FMT_Q5_0> { static constexpr int RB = 32 * 22, UB = 16; };
-template <> struct I8Stage<SLHIP_FMT_Q5_1> { static constexpr int RB = 32 * 24, UB = 16; };
-template <> struct I8Stage<SLHIP_FMT_IQ4_NL> { static constexpr int RB = 32 * 18, UB = 16; };
-template <> struct I8Stage<SLHIP_FMT_MXFP4> { static constexpr int RB = 32 * 17, UB = 16; };
-template <> struct I8Stage<SLHIP_FMT_Q4_K> { static constexpr int RB = 4 * 144, UB = 16; };
-template <> struct I8Stage<SLHIP_FMT_Q5_K> { static constexpr int RB = 4 * 176, UB = 16; };
-template <> struct I8Stage<SLHIP_FMT_Q6_K> { static constexpr int RB = 4 * 210, UB = 4; };
-template <> struct I8Stage<SLHIP_FMT_IQ4_XS> { static constexpr int RB = 4 * 136, UB = 16; };
+template <> struct I8Stage<SLHIP_FMT_Q8_0> { static constexpr int RB = 32 * 34, UB = 16; static constexpr bool TABLE = false; };
+template <> struct I8Stage<SLHIP_FMT_Q4_0> { static constexpr int RB = 32 * 18, UB = 16; static constexpr bool TABLE = false; };
+template <> struct I8Stage<SLHIP_FMT_Q4_1> { static constexpr int RB = 32 * 20, UB = 16; static constexpr bool TABLE = false; };
+template <> struct I8Stage<SLHIP_FMT_Q5_0> { static constexpr int RB = 32 * 22, UB = 16; static constexpr bool TABLE = false; };
+template <> struct I8Stage<SLHIP_FMT_Q5_1> { static constexpr int RB = 32 * 24, UB = 16; static constexpr bool TABLE = false; };
+template <> struct I8Stage<SLHIP_FMT_IQ4_NL> { static constexpr int RB = 32 * 18, UB = 16; static constexpr bool TABLE = false; };
+template <> struct I8Stage<SLHIP_FMT_MXFP4> { static constexpr int RB = 32 * 17, UB = 16; static constexpr bool TABLE = false; };
+template <> struct I8Stage<SLHIP_FMT_Q4_K> { static constexpr int RB = 4 * 144, UB = 16; static constexpr bool TABLE = true; };
+template <> struct I8Stage<SLHIP_FMT_Q5_K> { static constexpr int RB = 4 * 176, UB = 16; static constexpr bool TABLE = true; };
+template <> struct I8Stage<SLHIP_FMT_Q6_K> { static constexpr int RB = 4 * 210, UB = 4; static constexpr bool TABLE = false; };
+template <> struct I8Stage<SLHIP_FMT_IQ4_XS> { static constexpr int RB = 4 * 136, UB = 16; static constexpr bool TABLE = true; };
 
 constexpr int kI8MfWaves = 8;
 
@@ -313,17 +314,63 @@ __device__ __forceinline__ float4 i8_scales(const uint32_t* s, int b)
     }
 }
 
-typedef int i32x4_t __attribute__((ext_vector_type(4)));
+// The multiplier and offset (a, b) of unit 4 h + j (j < 4) of a super-block from its first 16 bytes held in
+// registers (Q4_K / Q5_K: d, dmin, the 12 packed 6-bit scale and min bytes; IQ4_XS: d, scales_h, scales_l),
+// the same arithmetic as i8_scales on the LDS image.
+template <int FMT>
+__device__ __forceinline__ float2 hdr_scales(const uint4& q, int h, int j)
+{
+    auto byte = [](uint32_t w, int k) { return (w >> (8 * k)) & 0xFFu; };
+    const float d = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(q.x & 0xFFFFu)));
+    if constexpr (FMT == SLHIP_FMT_Q4_K || FMT == SLHIP_FMT_Q5_K) {
+        const float dmin = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(q.x >> 16)));
+        uint32_t sc, mn;
+        if (h == 0) {  // units 0..3: bytes 4 + j and 8 + j, low 6 bits
+            sc = byte(q.y, j) & 63u;
+            mn = byte(q.z, j) & 63u;
+        } else {  // units 4..7: low nibbles of bytes 12 + j with the top bits of bytes j + 4, j + 8 (units 0..3's)
+            sc = (byte(q.w, j) & 0xFu) | ((byte(q.y, j) >> 6) << 4);
+            mn = (byte(q.w, j) >> 4) | ((byte(q.z, j) >> 6) << 4);
+        }
+        return make_float2(__fmul_rn(d, static_cast<float>(sc)), -__fmul_rn(dmin, static_cast<float>(mn)));
+    } else {  // IQ4_XS: ib = 4 h + j; ls = 4 bits of scales_l[ib / 2] | 2 bits of scales_h << 4
+        const int ib = 4 * h + j;
+        const uint32_t sh = q.x >> 16;
+        const uint32_t lo = (byte(q.y, ib >> 1) >> (4 * (ib & 1))) & 0xFu;
+        const int ls = static_cast<int>(lo | (((sh >> (2 * ib)) & 3u) << 4));
+        return make_float2(__fmul_rn(d, static_cast<float>(ls - 32)), 0.0f);
+    }
+}
 
-// global_load_lds of N bytes per lane: lane l's N bytes from src land at lds + N l (lds wave-uniform).
+// Bytes per staged row of the matrix-core kernel: at least 16 past the row (lds_u64 reads up to 12 bytes beyond
+// a piece), a whole number of staging loads, and 32 mod 64 bytes, so that the 16 rows a wave reads at once start
+// in 8 different 32-byte bank groups.
+constexpr int i8_pitch(int rb, int ub)
+{
+    int p = rb + 16;
+    while (p % ub != 0 || p % 64 != 32) p += 4;
+    return p;
+}
+
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// global_load_lds of N bytes per lane: lane l's N bytes from base + off land at lds + N l (base and lds
+// wave-uniform). Written as inline assembly so that the compiler, which would otherwise treat every later LDS
+// read as possibly reading these bytes and wait for the loads (vmcnt(0)) before it -- serializing the next
+// stage's loads with this stage's arithmetic -- leaves the wait to the caller: an explicit vmcnt(0) ahead of
+// the barrier that publishes the stage. (The compiler's own waits for other loads stay correct: memory
+// operations complete in order, so loads it does not count only make its waits longer.)
 template <int N>
-__device__ __forceinline__ void load_to_lds(const void* src, void* lds)
+__device__ __forceinline__ void load_to_lds(const void* base, uint32_t off, void* lds)
 {
     static_assert(N == 4 || N == 16, "load width");
+    typedef __attribute__((address_space(3))) char lds_char;
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_char*)lds)));
     if constexpr (N == 16)
-        __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0);
+        asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(m0) : "memory", "m0");
     else
-        __builtin_amdgcn_global_load_lds(src, lds, 4, 0, 0);
+        asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(m0) : "memory", "m0");
 }
 
 template <int FMT, bool DUAL>
@@ -331,19 +378,23 @@ __global__ __launch_bounds__(64 * kI8MfWaves) void matvec_i8_mfma(I8Args a)
 {
     constexpr int NM = DUAL ? 2 : 1;
     constexpr int RB = I8Stage<FMT>::RB, UB = I8Stage<FMT>::UB;
-    constexpr int PITCH = RB + 16;  // bytes per staged row (rows of a tile land on different banks)
-    constexpr int SPR = PITCH / UB;  // load slots per staged row; the last 16 / UB of them are padding
-    constexpr int SLOTS = NM * 16 * SPR;
+    constexpr int PITCH = i8_pitch(RB, UB);
+    constexpr int SPR = PITCH / UB;  // load slots per staged row; those past RB / UB are padding
+    constexpr int MS = (16 * SPR + 63) / 64 * 64;  // slots per matrix: whole waves, so a wave's run is in one
+    constexpr int SLOTS = NM * MS;
     constexpr int NT = 64 * kI8MfWaves;
     constexpr int LPT = (SLOTS + NT - 1) / NT;  // loads per thread and stage
     constexpr int BPW = 32 / kI8MfWaves;  // units per wave and stage
     constexpr bool H16 = kUnitForm<FMT> == kScale16Off;
     static_assert(RB % UB == 0 && (UB == 16 || UB == 4), "stage shape");
     static_assert(NT == 16 * 32, "one thread per token and unit of a stage stages the q8 scales");
-    static_assert(sizeof(uint32_t) * 2 * NM * 16 * (PITCH / 4) >= sizeof(float) * kI8MfWaves * NM * 4 * 64,
+    static_assert(2 * SLOTS * UB >= static_cast<int>(sizeof(float)) * kI8MfWaves * NM * 4 * 64,
                   "the cross-wave reduction reuses the weight stage");
-    __shared__ __align__(16) uint32_t stage[2][NM][16][PITCH / 4];
-    __shared__ float4 xsc[2][16][32];  // the q8 scales {d, d s_lo, d s_hi, 0} of [token][unit] of a stage
+    __shared__ __align__(16) uint32_t stage[2][SLOTS * UB / 4];  // [matrix: 16 rows of PITCH bytes, padding]
+    auto rowp = [&](int b, int m, int rr) -> const uint32_t* { return &stage[b][(m * MS * UB + rr * PITCH) / 4]; };
+    // the q8 scales {d, d s_lo, d s_hi, 0} of [unit][token] of a stage (the 4 tokens a lane group reads at
+    // once are 64 bytes apart: different banks)
+    __shared__ float4 xsc[2][32][16];
     const int lane = threadIdx.x & 63;
     const int wave = wave_id();
     const int r = lane & 15, g = lane >> 4;
@@ -354,41 +405,63 @@ __global__ __launch_bounds__(64 * kI8MfWaves) void matvec_i8_mfma(I8Args a)
     int64_t tok = a.t0 + r;
     tok = tok < a.T ? tok : a.T - 1;
     const uint8_t* xrow = a.xq + tok * xstride;
-    // the scale this thread stages: token threadIdx / 32 of the pass, unit threadIdx % 32 of each stage
-    int64_t stok = a.t0 + (threadIdx.x >> 5);
+    // the scale this thread stages: token threadIdx % 16 of the pass, unit threadIdx / 16 of each stage
+    int64_t stok = a.t0 + (threadIdx.x & 15);
     stok = stok < a.T ? stok : a.T - 1;
-    const float4* xs_src = reinterpret_cast<const float4*>(a.xq + stok * xstride + K) + (threadIdx.x & 31);
+    // (offset from the pass's first q8 row: 16 rows, below 2^31 bytes)
+    const uint8_t* xs_base = a.xq + a.t0 * xstride + K;
+    const uint32_t xs_off = static_cast<uint32_t>((stok - a.t0) * xstride + 16 * (threadIdx.x >> 4));
 
-    // Load slot q = threadIdx + NT i is byte UB q of the stage: row (m, rr), slot c of SPR; a padding slot loads
-    // the row's last real piece again (the LDS image is contiguous, so the lanes of a wave fill one run).
-    const char* src[LPT];
+    // Load slot q = threadIdx + NT i is byte UB q of the stage: matrix q / MS, row rr, slot c of SPR; a padding
+    // slot (the row's last 16 bytes, or the matrix's tail) loads a real piece again (the LDS image is
+    // contiguous, so the lanes of a wave fill one run, and a wave's run lies in one matrix). src: the byte
+    // offset from the matrix start (below 2^31), so that the address is a scalar base plus one register.
+    uint32_t src[LPT];
 #pragma unroll
     for (int i = 0; i < LPT; i++) {
         int q = static_cast<int>(threadIdx.x) + NT * i;
         q = q < SLOTS ? q : SLOTS - 1;
-        const int m = q / (16 * SPR), rem = q - m * (16 * SPR), rr = rem / SPR;
-        int c = rem - rr * SPR;
+        const int m = q / MS, rem = q - m * MS;
+        int rr = rem / SPR, c = rem - rr * SPR;
+        if (rr > 15) {
+            rr = 15;
+            c = 0;
+        }
         c = c < RB / UB ? c : RB / UB - 1;
         int64_t row = n0 + rr;
         row = row < a.N ? row : a.N - 1;
-        src[i] = (m == 0 ? a.wg : a.wu) + row * a.wrow + UB * c;
+        src[i] = static_cast<uint32_t>(row * a.wrow + UB * c);
     }
     auto fetch = [&](int b, int s) {
 #pragma unroll
         for (int i = 0; i < LPT; i++) {
             if (NT * i + 64 * wave >= SLOTS) break;  // wave-uniform: the LDS run of a wave starts in the stage
             if (NT * (i + 1) > SLOTS && static_cast<int>(threadIdx.x) + NT * i >= SLOTS) continue;
-            char* base = reinterpret_cast<char*>(&stage[b][0][0][0]) + UB * (NT * i + 64 * wave);
-            load_to_lds<UB>(src[i] + static_cast<int64_t>(s) * RB, base);
+            char* base = reinterpret_cast<char*>(&stage[b][0]) + UB * (NT * i + 64 * wave);
+            const char* mat = ((NT * i + 64 * wave) / MS ? a.wu : a.wg) + static_cast<int64_t>(s) * RB;
+            load_to_lds<UB>(mat, src[i], base);
         }
-        load_to_lds<16>(xs_src + 32 * s, &xsc[b][0][0] + 64 * wave);
+        load_to_lds<16>(xs_base + static_cast<int64_t>(s) * 512, xs_off, &xsc[b][0][0] + 64 * wave);
     };
+    constexpr bool TABLE = I8Stage<FMT>::TABLE;
+    constexpr int SBB = FMT == SLHIP_FMT_Q4_K ? 144 : FMT == SLHIP_FMT_Q5_K ? 176 : 136;  // super-block bytes
+    // (TABLE formats) the super-block header of the wave's units for row lane % (16 NM): its first 16 bytes,
+    // loaded from HBM with the stage (the same lines the stage moves into LDS)
+    const char* hdr_src = nullptr;
+    if constexpr (TABLE) {
+        const int rr = lane % (NM * 16);
+        int64_t row = n0 + rr % 16;
+        row = row < a.N ? row : a.N - 1;
+        hdr_src = (rr >= 16 ? a.wu : a.wg) + row * a.wrow + (wave * BPW / 8) * SBB;
+    }
     struct Xs {
         uint2 q[BPW];
+        uint4 hdr;
     };
     auto fetch_x = [&](Xs& x, int s) {
 #pragma unroll
         for (int j = 0; j < BPW; j++) x.q[j] = *reinterpret_cast<const uint2*>(xrow + (s * 32 + wave * BPW + j) * 32 + 8 * g);
+        if constexpr (TABLE) x.hdr = *reinterpret_cast<const uint4*>(hdr_src + static_cast<int64_t>(s) * (1024 / 256) * SBB);
     };
     // acc[m][i]: weight row n0 + r of matrix m, token t0 + 4 g + i (the MFMA's A operand is the q8 tokens, B the
     // weight codes, so each lane decodes the multipliers of its own row once per unit)
@@ -396,18 +469,62 @@ __global__ __launch_bounds__(64 * kI8MfWaves) void matvec_i8_mfma(I8Args a)
 #pragma unroll
     for (int m = 0; m < NM; m++)
         for (int i = 0; i < 4; i++) acc[m][i] = 0.0f;
+    constexpr bool OFF = kUnitForm<FMT> == kScale32Off;  // formats with one offset per unit
+    f32x4_t acc_off[NM];
+#pragma unroll
+    for (int m = 0; m < NM; m++) acc_off[m] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    // The K-quants' and IQ4_XS's multipliers and offsets (6-bit fields spread over the super-block header) for
+    // the wave's units and the tile's rows are decoded once each, by the lane holding the row's header, into
+    // the wave's own LDS table, and read there by the 4 lanes of a row; the other formats' (one f16 or e8m0
+    // field) are read from the stage directly.
+    constexpr int NENT = NM * 16 * BPW;
+    static_assert(BPW == 4, "a wave's units are one half of a super-block");
+    __shared__ __align__(16) float2 wsc[TABLE ? kI8MfWaves : 1][TABLE ? NENT : 1];
+    float2* my = wsc[TABLE ? wave : 0];
     auto compute = [&](int b, const Xs& x) {
+        if constexpr (TABLE) {
+            static_assert(!H16, "the table holds one multiplier and offset per unit");
+            const int h = (wave * BPW / 4) & 1;  // which half of the super-block the wave's units are
+            if (lane < NM * 16) {
+#pragma unroll
+                for (int j = 0; j < BPW; j++) my[j * NM * 16 + lane] = hdr_scales<FMT>(x.hdr, h, j);
+            }
+            wave_lds_sync();
+        }
+        // The offset terms b gs of the wave's 4 units are a 16 x 16 x 4 product (tokens x units . units x rows):
+        // one f32 matrix-core instruction per matrix, accumulated over the stages in acc_off; lane (r, g)
+        // supplies token r's q8 sum of unit g and row r's offset of unit g. (Q6_K's offsets, one per 16-value
+        // half, are added with its products.)
+        if constexpr (OFF) {
+            const float4 xo = xsc[b][wave * BPW + g][r];
+#pragma unroll
+            for (int m = 0; m < NM; m++) {
+                float4 so;
+                if constexpr (TABLE) {
+                    const float2 s2 = my[g * NM * 16 + m * 16 + r];
+                    so = make_float4(s2.x, s2.x, s2.y, s2.y);
+                } else {
+                    so = i8_scales<FMT>(rowp(b, m, r), wave * BPW + g);
+                }
+                acc_off[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(xo.y + xo.z, so.z, acc_off[m], 0, 0, 0);
+            }
+        }
 #pragma unroll
         for (int j = 0; j < BPW; j++) {
             const int u = wave * BPW + j;
             const long xb = static_cast<long>(__builtin_bit_cast(uint64_t, x.q[j]));
-            float4 xs[4];
+            float d[4];
 #pragma unroll
-            for (int i = 0; i < 4; i++) xs[i] = xsc[b][4 * g + i][u];
+            for (int i = 0; i < 4; i++) d[i] = xsc[b][u][4 * g + i].x;
 #pragma unroll
             for (int m = 0; m < NM; m++) {
-                const uint2 c = i8_codes8<FMT>(stage[b][m][r], u, g);
-                const float4 sc = i8_scales<FMT>(stage[b][m][r], u);
+                const uint2 c = i8_codes8<FMT>(rowp(b, m, r), u, g);
+                float4 sc;
+                if constexpr (TABLE) {
+                    sc.x = my[j * NM * 16 + m * 16 + r].x;
+                } else {
+                    sc = i8_scales<FMT>(rowp(b, m, r), u);
+                }
                 const i32x4_t z = {0, 0, 0, 0};
                 if constexpr (H16) {
                     const bool first = g < 2;
@@ -416,17 +533,16 @@ __global__ __launch_bounds__(64 * kI8MfWaves) void matvec_i8_mfma(I8Args a)
                     const i32x4_t S0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(xb, c0, z, 0, 0, 0);
                     const i32x4_t S1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(xb, c1, z, 0, 0, 0);
 #pragma unroll
-                    for (int i = 0; i < 4; i++)
-                        acc[m][i] += fmaf(sc.x, __fmul_rn(xs[i].x, static_cast<float>(S0[i])),
-                                          fmaf(sc.y, __fmul_rn(xs[i].x, static_cast<float>(S1[i])),
-                                               fmaf(sc.z, xs[i].y, __fmul_rn(sc.w, xs[i].z))));
+                    for (int i = 0; i < 4; i++) {
+                        const float4 xs = xsc[b][u][4 * g + i];
+                        acc[m][i] += fmaf(sc.x, __fmul_rn(xs.x, static_cast<float>(S0[i])),
+                                          fmaf(sc.y, __fmul_rn(xs.x, static_cast<float>(S1[i])),
+                                               fmaf(sc.z, xs.y, __fmul_rn(sc.w, xs.z))));
+                    }
                 } else {
                     const i32x4_t S = __builtin_amdgcn_mfma_i32_16x16x32_i8(xb, static_cast<long>(__builtin_bit_cast(uint64_t, c)), z, 0, 0, 0);
 #pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const float p = __fmul_rn(sc.x, __fmul_rn(xs[i].x, static_cast<float>(S[i])));
-                        acc[m][i] += kUnitForm<FMT> == kScale32Off ? fmaf(sc.z, xs[i].y + xs[i].z, p) : p;
-                    }
+                    for (int i = 0; i < 4; i++) acc[m][i] = fmaf(__fmul_rn(sc.x, d[i]), static_cast<float>(S[i]), acc[m][i]);
                 }
             }
         }
@@ -455,8 +571,13 @@ __global__ __launch_bounds__(64 * kI8MfWaves) void matvec_i8_mfma(I8Args a)
         __builtin_amdgcn_s_waitcnt(kWaitLoads);
         __syncthreads();
     }
+    if constexpr (OFF) {
+#pragma unroll
+        for (int m = 0; m < NM; m++)
+            for (int i = 0; i < 4; i++) acc[m][i] += acc_off[m][i];
+    }
     // every wave is past its last read of the stage (the loop ends on a barrier): reuse it for the reduction
-    float* red = reinterpret_cast<float*>(&stage[0][0][0][0]);  // [wave][m][i][lane]
+    float* red = reinterpret_cast<float*>(&stage[0][0]);  // [wave][m][i][lane]
 #pragma unroll
     for (int m = 0; m < NM; m++)
         for (int i = 0; i < 4; i++) red[((wave * NM + m) * 4 + i) * 64 + lane] = acc[m][i];
@@ -722,14 +843,17 @@ static int i8_tt(const I8Args& a, int tt, hipStream_t st)
     }
 }
 
-// Tokens from which the integer-dot matvec takes the matrix cores (SLHIP_MATVEC_I8_MFMA_MIN_T; 0 disables), when
-// K is a multiple of 1024 (whole stages).
+// Tokens from which the integer-dot matvec takes the matrix cores, when K is a multiple of 1024 (whole
+// stages): 5 (measured on MI355X, [14336, 4096] gate/up pairs: at 4 tokens the VALU kernel's one 4-token pass
+// is level with the matrix cores or ahead for every format, from 5 it takes an 8-token pass and falls 1.6-1.9x
+// behind); SLHIP_MATVEC_I8_MFMA_MIN_T overrides it (0 disables).
+template <int FMT>
 inline int i8_mfma_min_tokens()
 {
-    static int v = -1;
-    if (v < 0) {
+    static int v = -2;
+    if (v == -2) {
         const char* e = getenv("SLHIP_MATVEC_I8_MFMA_MIN_T");
-        v = e ? atoi(e) : 9;
+        v = e ? atoi(e) : 5;
     }
     return v;
 }
@@ -751,8 +875,9 @@ int run_i8_mfma(I8Args a, bool dual, hipStream_t st)
 template <int FMT>
 int run_i8(I8Args a, bool dual, hipStream_t st)
 {
-    const int mt = i8_mfma_min_tokens();
-    if (mt > 0 && a.T >= mt && a.K % 1024 == 0 && a.wrow % I8Stage<FMT>::UB == 0) return run_i8_mfma<FMT>(a, dual, st);
+    const int mt = i8_mfma_min_tokens<FMT>();
+    if (mt > 0 && a.T >= mt && a.K % 1024 == 0 && a.wrow % I8Stage<FMT>::UB == 0 && a.N * a.wrow < (int64_t{1} << 31))
+        return run_i8_mfma<FMT>(a, dual, st);
     int tt = 8;
     while (tt > 1 && (tt / 2 >= a.T || i8_lds(tt, a.K, a.wrow, dual) > kI8MaxLds)) tt /= 2;
     if (i8_lds(tt, a.K, a.wrow, dual) > kI8MaxLds)

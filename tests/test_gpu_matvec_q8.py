@@ -152,7 +152,7 @@ SINGLE_CASES = [  # (fmt, x dtype, y dtype, T, K, N)
     ("q8_0", "bf16", "f32", 1, 1056, 33),    # 1122 bytes
     ("q5_1", "f32", "bf16", 3, 2080, 24),    # 1560 bytes: 8-byte loads
     ("iq4_nl", "f32", "f32", 4, 96, 17),     # three blocks
-    # from nine tokens with K a multiple of 1024: the integer matrix cores (16-row tiles, 1024-value stages)
+    # from five tokens with K a multiple of 1024: the integer matrix cores (16-row tiles, 1024-value stages)
     *[(f, "f32", "bf16", 9, 1024, 40) for f in FORMATS],      # one stage, a partial tile
     ("q4_k", "bf16", "f32", 16, 3072, 48),   # three stages (an odd count)
     ("q6_k", "f32", "f32", 20, 2048, 33),    # a full 16-token pass and a 4-token one
