@@ -186,6 +186,67 @@ class RmsNormPlain(LayerNorm):
                        w=self.w.slot(0), eps=self.eps, stream=stream)
 
 
+class EwGroupNormTail(Workload):
+    """A fused elementwise group with its norm tail (slhip_ew_program_run): h = (x + bias) + res, y = RmsNorm(h) * w,
+    f32 [8192, 4096] (the provider's launch for Add(bias) + Add(residual) + RmsNorm, FoldNormTails)."""
+    name = "ewg_bias_residual_rmsnorm_f32"
+
+    def __init__(self, rows=8192, D=4096):
+        self.desc = "x, res f32 [8192, 4096], bias, w f32 [4096] -> h, y f32 (one fused-group launch)"
+        self.rows, self.D = rows, D
+        x = synth.normal(0, 30, (rows, D))
+        r = synth.normal(0, 31, (rows, D))
+        b = synth.normal(0, 32, (D,))
+        w = synth.normal(0, 33, (D,), 1.0, 0.1)
+        nb = x.nbytes
+        self.bytes_per_step = 4 * nb + b.nbytes + w.nbytes
+        R = copies_for(self.bytes_per_step)
+        self.x, self.r, self.h, self.y = Rot(x, nb, R), Rot(r, nb, R), Rot(None, nb, R), Rot(None, nb, R)
+        self.b, self.w = Rot(b, b.nbytes, 1), Rot(w, w.nbytes, 1)
+        self.launch(0, None)  # an uncaptured first run makes the group's generated kernel
+        native.synchronize()
+
+    def launch(self, i, stream):
+        native.ew_program([(self.x.slot(i), "f32", native.EWI_FULL), (self.b.slot(0), "f32", native.EWI_ROW),
+                           (self.r.slot(i), "f32", native.EWI_FULL)],
+                          [("binary", "Add", 0, 1, 3, "f32", 0, 0), ("binary", "Add", 3, 2, 3, "f32", 0, 0)],
+                          [(self.h.slot(i), "f32", 3)], self.rows, self.D,
+                          tail=dict(kind="rms", reg=3, w=self.w.slot(0), eps=1e-6, y=self.y.slot(i), dtype_y="f32"),
+                          stream=stream)
+
+
+class EwGroupSwiglu(Workload):
+    """gpt-oss's clamped SwiGLU with its bias adds as one fused-group launch (nine nodes, four inputs), f32
+    [8192, 2880]: y = (clip(u + bu, -7, 7) + 1) * g' * sigmoid(1.702 g'), g' = clip(g + bg, max 7)."""
+    name = "ewg_gpt_oss_swiglu_f32"
+
+    def __init__(self, rows=8192, D=2880):
+        self.desc = "gate, up f32 [8192, 2880], biases f32 [2880] -> y f32 (one fused-group launch)"
+        self.rows, self.D = rows, D
+        g = synth.normal(0, 34, (rows, D), std=4.0)
+        u = synth.normal(0, 35, (rows, D), std=4.0)
+        bg = synth.normal(0, 36, (D,))
+        bu = synth.normal(0, 37, (D,))
+        nb = g.nbytes
+        self.bytes_per_step = 3 * nb + bg.nbytes + bu.nbytes
+        R = copies_for(self.bytes_per_step)
+        self.g, self.u, self.y = Rot(g, nb, R), Rot(u, nb, R), Rot(None, nb, R)
+        self.bg, self.bu = Rot(bg, bg.nbytes, 1), Rot(bu, bu.nbytes, 1)
+        self.launch(0, None)  # an uncaptured first run makes the group's generated kernel
+        native.synchronize()
+
+    def launch(self, i, stream):
+        inf = float("inf")
+        native.ew_program([(self.g.slot(i), "f32", native.EWI_FULL), (self.u.slot(i), "f32", native.EWI_FULL),
+                           (self.bg.slot(0), "f32", native.EWI_ROW), (self.bu.slot(0), "f32", native.EWI_ROW)],
+                          [("binary", "Add", 0, 2, 4, "f32", 0, 0), ("unary", "Clip", 4, 0, 4, "f32", -inf, 7.0),
+                           ("binary", "Add", 1, 3, 5, "f32", 0, 0), ("unary", "Clip", 5, 0, 5, "f32", -7.0, 7.0),
+                           ("unary", "Scale", 4, 0, 6, "f32", 1.702, 0.0), ("unary", "Sigmoid", 6, 0, 6, "f32", 0, 0),
+                           ("binary", "Mul", 4, 6, 6, "f32", 0, 0), ("unary", "Scale", 5, 0, 5, "f32", 1.0, 1.0),
+                           ("binary", "Mul", 5, 6, 7, "f32", 0, 0)],
+                          [(self.y.slot(i), "f32", 7)], self.rows, self.D, stream=stream)
+
+
 class BiasAdd(Workload):
     """A lone broadcast Add (slhip_binary): x [8192, 4096] bf16 + bias [4096] bf16 -> bf16."""
     name = "bias_add_bf16"
@@ -428,6 +489,8 @@ WORKLOADS = {
     "c3_geglu_erf_bf16": lambda: C3("gelu_erf"),
     "layernorm_vit_f32": lambda: LayerNorm(197, 768, "f32"),
     "layernorm_bf16": lambda: LayerNorm(8192, 4096, "bf16"),
+    "ewg_bias_residual_rmsnorm_f32": lambda: EwGroupNormTail(),
+    "ewg_gpt_oss_swiglu_f32": lambda: EwGroupSwiglu(),
     "rmsnorm_bf16": lambda: RmsNormPlain(),
     "bias_add_bf16": lambda: BiasAdd(),
     "c4_qknorm_rope_bf16": lambda: C4(),

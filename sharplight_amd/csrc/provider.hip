@@ -463,6 +463,7 @@ bool flag(const Node& n, const char* key)
 }
 
 }  // namespace
+int ew_program_prepare(const slhip_ew_program* prog, int64_t cols);  // ewgroup.hip
 bool matvec_q8_fits(int fmt, int64_t K, bool dual);  // matvec_i8.hip
 namespace {
 
@@ -689,6 +690,7 @@ public:
         if (plan_only) return;
         check(slhip_stream_create(&stream_));
         allocate();
+        prepare_groups();
         reset_state();
     }
 
@@ -1568,6 +1570,45 @@ private:
         }
     }
 
+    // The fused group's program (slhip_ew_program) on the segment's buffers.
+    slhip_ew_program ew_program_of(const Unit& u) const
+    {
+        slhip_ew_program p{};
+        p.n_inputs = static_cast<int>(u.ew_in.size());
+        p.n_ops = static_cast<int>(u.ew_ops.size());
+        p.n_outputs = static_cast<int>(u.ew_out.size());
+        for (int i = 0; i < p.n_inputs; i++)
+            p.inputs[i] = slhip_ew_input{ptr(u.ew_in[i]), act_code(g_.value(u.ew_in[i]).type), u.ew_mode[i]};
+        for (int k = 0; k < p.n_ops; k++) p.ops[k] = u.ew_ops[k];
+        for (int j = 0; j < p.n_outputs; j++)
+            p.outputs[j] = slhip_ew_output{ptr(u.ew_out[j].first), act_code(g_.value(u.ew_out[j].first).type), u.ew_out[j].second};
+        auto norm_of = [&](int node, bool tail) {
+            const Node& nm = g_.nodes[node];
+            slhip_ew_norm r{};
+            r.kind = nm.op == "L2Norm" ? SLHIP_EWN_L2 : SLHIP_EWN_RMS;
+            r.reg = u.norm_reg;
+            r.w = nm.in.size() > 1 ? static_cast<const float*>(ptr(nm.in[1])) : nullptr;
+            r.eps = nm.f("eps", 1e-6f);
+            r.y = tail ? ptr(nm.out[0]) : nullptr;
+            r.dtype_y = act_code(g_.value(nm.out[0]).type);
+            return r;
+        };
+        if (u.head_node >= 0) p.head = norm_of(u.head_node, false);
+        if (u.tail_node >= 0) p.tail = norm_of(u.tail_node, true);
+        return p;
+    }
+
+    // The fused groups' generated kernels are made at compile time, so that the first Execute (or a graph
+    // recorded from it) launches them rather than the interpreter.
+    void prepare_groups()
+    {
+        for (const Unit& u : units_) {
+            if (u.kind != Unit::EwGroup) continue;
+            const slhip_ew_program p = ew_program_of(u);
+            check(ew_program_prepare(&p, g_.value(u.shape_of).last()));
+        }
+    }
+
     void* ptr(int id) const { return id < 0 ? nullptr : mem_.at(id); }
 
     // Two cache writes that map tokens to the same rows (one launch may carry one row map).
@@ -1720,28 +1761,7 @@ private:
             break;
         }
         case Unit::EwGroup: {
-            slhip_ew_program p{};
-            p.n_inputs = static_cast<int>(u.ew_in.size());
-            p.n_ops = static_cast<int>(u.ew_ops.size());
-            p.n_outputs = static_cast<int>(u.ew_out.size());
-            for (int i = 0; i < p.n_inputs; i++)
-                p.inputs[i] = slhip_ew_input{ptr(u.ew_in[i]), act_code(g_.value(u.ew_in[i]).type), u.ew_mode[i]};
-            for (int k = 0; k < p.n_ops; k++) p.ops[k] = u.ew_ops[k];
-            for (int j = 0; j < p.n_outputs; j++)
-                p.outputs[j] = slhip_ew_output{ptr(u.ew_out[j].first), act_code(g_.value(u.ew_out[j].first).type), u.ew_out[j].second};
-            auto norm_of = [&](int node, bool tail) {
-                const Node& nm = g_.nodes[node];
-                slhip_ew_norm r{};
-                r.kind = nm.op == "L2Norm" ? SLHIP_EWN_L2 : SLHIP_EWN_RMS;
-                r.reg = u.norm_reg;
-                r.w = nm.in.size() > 1 ? static_cast<const float*>(ptr(nm.in[1])) : nullptr;
-                r.eps = nm.f("eps", 1e-6f);
-                r.y = tail ? ptr(nm.out[0]) : nullptr;
-                r.dtype_y = act_code(g_.value(nm.out[0]).type);
-                return r;
-            };
-            if (u.head_node >= 0) p.head = norm_of(u.head_node, false);
-            if (u.tail_node >= 0) p.tail = norm_of(u.tail_node, true);
+            const slhip_ew_program p = ew_program_of(u);
             const Value& sv = g_.value(u.shape_of);
             check(slhip_ew_program_run(&p, sv.rows(T), sv.last(), stream_));
             break;

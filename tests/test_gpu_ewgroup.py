@@ -2,6 +2,8 @@
 (GraphLowerer.Fusion.cs:88-285: GroupElementwiseChains, MergeElementwiseGroups, FoldNormTails, FoldNormHeads)
 against the oracle's node-by-node CPU arithmetic (BinaryOp, ScalarMath.Unary, RowOp), f32 at 1e-5 relative
 (the parity rule of tests/parity.py), bf16 outputs within 2 ulp, stored intermediates included."""
+import os
+
 import numpy as np
 import pytest
 
@@ -14,7 +16,20 @@ from tests.parity import assert_bf16_close, assert_f32_close
 pytestmark = pytest.mark.gpu
 
 
-def test_program_every_input_mode(device):
+@pytest.fixture(params=["generated", "interpreter"])
+def path(request, device):
+    """Both forms of a group's kernel: the one generated for the program (default) and the op-code interpreter
+    (SLHIP_EWG_JIT=0, read at every run)."""
+    old = os.environ.get("SLHIP_EWG_JIT")
+    os.environ["SLHIP_EWG_JIT"] = "1" if request.param == "generated" else "0"
+    yield request.param
+    if old is None:
+        del os.environ["SLHIP_EWG_JIT"]
+    else:
+        os.environ["SLHIP_EWG_JIT"] = old
+
+
+def test_program_every_input_mode(path):
     rows, cols = 37, 1024
     x = synth.normal(40, 0, (rows, cols))
     b = synth.normal(40, 1, (cols,), dtype="bf16")
@@ -24,7 +39,7 @@ def test_program_every_input_mode(device):
         px, pb, ps, pc = d.put(x), d.put(b), d.put(s), d.put(c)
         p1 = d.empty(rows * cols * 4)
         p3 = d.empty(rows * cols * 2)
-        log("ew_program modes")
+        log(f"ew_program modes {path}")
         # r4 = x + b; r5 = r4 * s; r4 = silu(r5); r6 = r4 - c  (registers reused)
         native.ew_program([(px, "f32", native.EWI_FULL), (pb, "bf16", native.EWI_ROW), (ps, "f32", native.EWI_SCALAR),
                            (pc, "f32", native.EWI_COL)],
@@ -40,10 +55,11 @@ def test_program_every_input_mode(device):
     assert_bf16_close(y3, oracle.to_bf16(r3), what="bf16 output")
 
 
-@pytest.mark.parametrize("dty", ["f32", "bf16"])
-def test_program_norm_tail(device, dty):
-    """Add(bias) + Add(residual) + RmsNorm: h stored, y = RmsNorm(h) * w."""
-    rows, cols = 64, 4096
+@pytest.mark.parametrize("dty,cols", [("f32", 4096), ("bf16", 4096), ("f32", 5000)])
+def test_program_norm_tail(path, dty, cols):
+    """Add(bias) + Add(residual) + RmsNorm: h stored, y = RmsNorm(h) * w (5000 columns: beyond the generated
+    kernel's registers, a second pass over the row)."""
+    rows = 64
     x = synth.normal(41, 0, (rows, cols))
     r = synth.normal(41, 1, (rows, cols))
     bias = synth.normal(41, 2, (cols,))
@@ -52,7 +68,7 @@ def test_program_norm_tail(device, dty):
         px, pr, pbias, pw = d.put(x), d.put(r), d.put(bias), d.put(w)
         ph = d.empty(rows * cols * 4)
         py = d.empty(rows * cols * (4 if dty == "f32" else 2))
-        log(f"ew_program norm tail y={dty}")
+        log(f"ew_program norm tail y={dty} cols={cols} {path}")
         native.ew_program([(px, "f32", native.EWI_FULL), (pbias, "f32", native.EWI_ROW), (pr, "f32", native.EWI_FULL)],
                           [("binary", "Add", 0, 1, 3, "f32", 0, 0), ("binary", "Add", 3, 2, 3, "f32", 0, 0)],
                           [(ph, "f32", 3)], rows, cols,
@@ -69,15 +85,16 @@ def test_program_norm_tail(device, dty):
         assert_bf16_close(y, oracle.to_bf16(yref), what="y")
 
 
-def test_program_norm_head(device):
+@pytest.mark.parametrize("cols", [2048, 4100])
+def test_program_norm_head(path, cols):
     """RmsNorm (no weight) read only by Mul(w2) -> Scale: the norm computed in the group's launch."""
-    rows, cols = 50, 2048
+    rows = 50
     x = synth.normal(42, 0, (rows, cols), std=3.0)
     w2 = synth.normal(42, 1, (cols,))
     with Dev() as d:
         px, pw2 = d.put(x), d.put(w2)
         py = d.empty(rows * cols * 4)
-        log("ew_program norm head")
+        log(f"ew_program norm head cols={cols} {path}")
         native.ew_program([(px, "f32", native.EWI_FULL), (pw2, "f32", native.EWI_ROW)],
                           [("binary", "Mul", 0, 1, 2, "f32", 0, 0), ("unary", "Scale", 2, 0, 2, "f32", 0.5, 0.25)],
                           [(py, "f32", 2)], rows, cols, head=dict(kind="rms", reg=0, eps=1e-6, dtype_y="f32"))
