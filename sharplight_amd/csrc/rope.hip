@@ -275,7 +275,10 @@ __global__ __launch_bounds__(64 * kRopeWpb) void rope_vec(RopeArgs a)
             v1 = v2 = angle_cs<FF>(p, inv[n], ffv[n]);
         }
         const float cf = a.af;
-        cs[wv][ie[n]] = make_float4((v1.x * cf) * w0[n], (v1.y * cf) * w1[n], (v2.y * cf) * w0[n], (v2.x * cf) * w1[n]);
+        // entry c V + e at e L + c: the L lanes of a head read one vector of entries each step, L
+        // consecutive 16-byte entries (no bank conflicts; entry-major the L reads were 16 V bytes apart)
+        const int slot = (ie[n] % V) * L + ie[n] / V;
+        cs[wv][slot] = make_float4((v1.x * cf) * w0[n], (v1.y * cf) * w1[n], (v2.y * cf) * w0[n], (v2.x * cf) * w1[n]);
     }
     wave_lds_sync();
     if (!active) return;
@@ -297,19 +300,19 @@ __global__ __launch_bounds__(64 * kRopeWpb) void rope_vec(RopeArgs a)
 #pragma unroll
         for (int e = 0; e < 2 * V; e++) f[e] *= scale;
     }
-    const float4* ct = &cs[wv][c * V];
+    const float4* ct = &cs[wv][c];  // entry c V + e at e L + c
     float o[2 * V];
     if (a.neox) {  // wave-uniform: one loop per pair layout, no per-element selects
 #pragma unroll
         for (int e = 0; e < V; e++) {
-            const float4 cv = ct[e];
+            const float4 cv = ct[e * L];
             o[e] = f[e] * cv.x - f[V + e] * cv.y;
             o[V + e] = f[e] * cv.z + f[V + e] * cv.w;
         }
     } else {
 #pragma unroll
         for (int e = 0; e < V; e++) {
-            const float4 cv = ct[e];
+            const float4 cv = ct[e * L];
             o[2 * e] = f[2 * e] * cv.x - f[2 * e + 1] * cv.y;
             o[2 * e + 1] = f[2 * e] * cv.z + f[2 * e + 1] * cv.w;
         }
