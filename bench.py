@@ -777,7 +777,7 @@ def cpu_baselines(budget_main: float, budget_op: float, which: set[str]) -> dict
         res[name] = dict(s=s * N / n_s, reps=reps, sample=f"{n_s} of {N} weight rows, scaled x{N // n_s}; "
                                                           "MatMul, MatMul, Silu, Mul in f32")
     for fmt, T in (("q4_k", 1), ("q6_k", 1), ("q4_0", 1), ("q8_0", 2), ("q5_k", 1), ("iq4_nl", 1), ("mxfp4", 1),
-                   ("q4_k", 4), ("q4_k", 8), ("q6_k", 8), ("q8_0", 16)):
+                   ("q4_k", 4), ("q4_k", 8), ("q6_k", 8), ("q8_0", 16), ("q4_k", 16), ("q6_k", 16), ("q4_0", 16)):
         name = f"dual_matvec_int8_silu_{fmt}_T{T}"
         if name not in which:
             continue
@@ -814,6 +814,45 @@ def cpu_baselines(budget_main: float, budget_op: float, which: set[str]) -> dict
         full = 197 if dtype == "f32" else 8192
         res[name] = dict(s=s * full / rows, reps=reps,
                          sample=f"full [197,768]" if full == rows else f"{rows} of {full} rows, scaled x{full // rows}")
+    if "rmsnorm_bf16" in which:
+        rows = 1024
+        c = synth.layernorm(rows=rows, D=4096, dtype="bf16")
+        x = oracle.from_bf16(c["x"])
+        y = np.empty_like(x)
+        L, P = oracle.lib(), oracle._p
+        s, reps = cpu_time(lambda: L.orc_rmsnorm_mt(P(x), P(c["w"]), P(y), rows, 4096, c["eps"], 0), budget_op)
+        res["rmsnorm_bf16"] = dict(s=s * 8192 / rows, reps=reps, sample=f"{rows} of 8192 rows, scaled x{8192 // rows}")
+    if "ewg_bias_residual_rmsnorm_f32" in which:
+        rows = 1024
+        x, r = synth.normal(0, 30, (rows, 4096)), synth.normal(0, 31, (rows, 4096))
+        b, w = synth.normal(0, 32, (4096,)), synth.normal(0, 33, (4096,), 1.0, 0.1)
+        bb = np.broadcast_to(b, x.shape).copy()
+        h1, h, y = np.empty_like(x), np.empty_like(x), np.empty_like(x)
+        L, P = oracle.lib(), oracle._p
+
+        def run():
+            L.orc_add_mt(P(x), P(bb), P(h1), x.size)
+            L.orc_add_mt(P(h1), P(r), P(h), x.size)
+            L.orc_rmsnorm_mt(P(h), P(w), P(y), rows, 4096, 1e-6, 0)
+        s, reps = cpu_time(run, budget_op)
+        res["ewg_bias_residual_rmsnorm_f32"] = dict(s=s * 8192 / rows, reps=reps,
+                                                    sample=f"{rows} of 8192 rows, scaled x{8192 // rows}; Add, Add, "
+                                                           "RmsNorm node by node (the bias broadcast made outside)")
+    if "ewg_gpt_oss_swiglu_f32" in which:
+        rows = 256
+        g, u = synth.normal(0, 34, (rows, 2880), std=4.0), synth.normal(0, 35, (rows, 2880), std=4.0)
+        bg, bu = synth.normal(0, 36, (2880,)), synth.normal(0, 37, (2880,))
+        inf = float("inf")
+
+        def run():
+            gc = oracle.unary_kind("Clip", oracle.binary("Add", g, bg), -inf, 7.0)
+            uc = oracle.unary_kind("Clip", oracle.binary("Add", u, bu), -7.0, 7.0)
+            glu = oracle.binary("Mul", gc, oracle.unary_kind("Sigmoid", oracle.unary_kind("Scale", gc, 1.702, 0.0)))
+            oracle.binary("Mul", oracle.unary_kind("Scale", uc, 1.0, 1.0), glu)
+        s, reps = cpu_time(run, budget_op)
+        res["ewg_gpt_oss_swiglu_f32"] = dict(s=s * 8192 / rows, reps=reps, threads=1,
+                                             sample=f"{rows} of 8192 rows, scaled x{8192 // rows}; the nine nodes one "
+                                                    "by one, one thread (the oracle's elementwise ops are single-threaded)")
     if "bias_add_bf16" in which:
         rows = 512
         x = oracle.from_bf16(synth.normal(0, 0, (rows, 4096), dtype="bf16"))
