@@ -55,6 +55,30 @@ def test_program_every_input_mode(path):
     assert_bf16_close(y3, oracle.to_bf16(r3), what="bf16 output")
 
 
+def test_program_rounding_and_f16(path):
+    """A node whose output type is bf16 or f16 (the value rounded where the unfused graph stores it), an f16 input
+    and an f16 output."""
+    rows, cols = 19, 768
+    x = synth.normal(46, 0, (rows, cols))
+    h = synth.normal(46, 1, (rows, cols)).astype(np.float16)
+    with Dev() as d:
+        px, ph = d.put(x), d.put(h)
+        py = d.empty(rows * cols * 2)
+        log(f"ew_program rounding f16 {path}")
+        # r2 = bf16(x * 3) ; r3 = f16(r2 + h) ; r2 = tanh(r3) -> f16 output
+        native.ew_program([(px, "f32", native.EWI_FULL), (ph, "f16", native.EWI_FULL)],
+                          [("unary", "Scale", 0, 0, 2, "bf16", 3.0, 0.0), ("binary", "Add", 2, 1, 3, "f16", 0, 0),
+                           ("unary", "Tanh", 3, 0, 2, "f32", 0, 0)],
+                          [(py, "f16", 2)], rows, cols)
+        native.synchronize()
+        y = d.get(py, (rows, cols), np.float16)
+    r2 = oracle.from_bf16(oracle.to_bf16(oracle.unary_kind("Scale", x, 3.0, 0.0)))
+    r3 = oracle.binary("Add", r2, h.astype(np.float32)).astype(np.float16).astype(np.float32)
+    ref = oracle.unary_kind("Tanh", r3).astype(np.float16)
+    bad = np.abs(y.astype(np.float64) - ref.astype(np.float64)) > 2.0 ** -10 * np.abs(ref.astype(np.float64)) + 1e-7
+    assert not bad.any(), (np.argwhere(bad)[:3], y[bad][:3], ref[bad][:3])
+
+
 @pytest.mark.parametrize("dty,cols", [("f32", 4096), ("bf16", 4096), ("f32", 5000)])
 def test_program_norm_tail(path, dty, cols):
     """Add(bias) + Add(residual) + RmsNorm: h stored, y = RmsNorm(h) * w (5000 columns: beyond the generated

@@ -171,11 +171,13 @@ def test_matvec_q8(device, fmt, dx, dy, T, K, N):
     _compare(y, dy, ref, 2.0 ** -16 * S + 1e-30, f"matvec_q8 {fmt}")
 
 
-@pytest.mark.parametrize("fmt", ["q4_0", "q4_k", "q6_k", "iq4_nl"])
-def test_matvec_q8_bias_and_spread(device, fmt):
-    """The bias epilogue (FoldMatMulBiases: y + b in f32 after the product) and x blocks spread over 2^-20..2^12."""
-    T, K, N = 3, 2048, 50
-    seed = _seed("bias", fmt)
+@pytest.mark.parametrize("fmt,T", [("q4_0", 3), ("q4_k", 3), ("q6_k", 3), ("iq4_nl", 3), ("q4_k", 12), ("q8_0", 7),
+                                   ("q6_k", 16), ("mxfp4", 5)])
+def test_matvec_q8_bias_and_spread(device, fmt, T):
+    """The bias epilogue (FoldMatMulBiases: y + b in f32 after the product) and x blocks spread over 2^-20..2^12,
+    on the VALU kernel (T <= 4) and the matrix cores."""
+    K, N = 2048, 50
+    seed = _seed("bias", fmt, T)
     raw = synth.quant_table(fmt, N, K, seed=seed, tid=1)
     x, x32 = _x("f32", T, K, seed, spread=True)
     b = synth.normal(seed, 4, (N,), dtype="f32")

@@ -491,6 +491,34 @@ def test_swiglu_dual_matvec_int_dot(dev, fmt, T):
     assert (np.abs(got - ref) <= tol + 1e-30).all()
 
 
+@pytest.mark.parametrize("fmt,T", [("q4_k", 20), ("iq4_xs", 31), ("q5_0", 6)])
+def test_int_dot_cpu_rule_many_rows(dev, fmt, T):
+    """The CPU provider's rule (option int_dot=cpu: every IntDot format, 1..31 rows, MatMulOp.cs:104,138-147) at
+    row counts the integer matrix cores take in 16-token passes (20 = 16 + 4, 31 = 16 + 15)."""
+    K, N = 1024, 80
+    g = GraphBuilder()
+    g.options["int_dot"] = "cpu"
+    x = g.input("f32", "T", K)
+    wg, wu = g.weight(fmt, N, K), g.weight(fmt, N, K)
+    y = g.output(g.mul(g.silu(g.matmul(x, wg)), g.matmul(x, wu)))
+    rg = synth.quant_table(fmt, N, K, seed=14, tid=1)
+    ru = synth.quant_table(fmt, N, K, seed=14, tid=2)
+    xs = synth.normal(14, 3, (T, K))
+    with dev.compile(g, max_tokens=31) as seg:  # IQ4_XS has no f32 matvec: the bound stays in the rule's range
+        assert seg.launches_at(T) == ["x->q8", "matvec2+fused[Silu,Mul] int-dot"]
+        seg.set_input(x, xs)
+        seg.set_input(wg, rg)
+        seg.set_input(wu, ru)
+        log(f"provider int-dot cpu rule {fmt} T={T}")
+        seg.execute(T)
+        got = seg.get_output(y).astype(np.float64)
+    gr, Sg = oracle.matvec_q8(fmt, rg, N, K, xs, with_abs=True)
+    ur, Su = oracle.matvec_q8(fmt, ru, N, K, xs, with_abs=True)
+    ref = oracle.mul(oracle.unary("silu", gr), ur).astype(np.float64)
+    tol = 2.0 ** -16 * (1.1 * np.abs(ur) * Sg + np.abs(gr) * Su) + 1e-5 * np.abs(ref)
+    assert (np.abs(got - ref) <= tol + 1e-30).all()
+
+
 def test_qkv_projections_share_one_q8_copy_and_fold_biases(dev):
     """Three biased projections of one x (a Qwen2-style attention input): one quantization, three int-dot
     launches with the biases folded in (FoldMatMulBiases), and a Q8_0 projection of the same x with its own
