@@ -1862,15 +1862,14 @@ static int launch_kq_tile(const MatvecArgs& a, hipStream_t st)
     return check_launch("matvec_kq_tile");
 }
 
-// Tokens from which the 32-value block formats (Q4_0, Q8_0) take the matrix cores (SLHIP_MATVEC_MQ_MIN_T; 0
-// disables). Measured at [14336, 4096] (dual, us, VALU / matrix cores; f32 x, bf16 x): Q4_0 T = 2 26.7 /
-// 52.1, 25.7 / 39.7; T = 3 57.2 / 52.7, 55.6 / 40.3; T = 16 218 / 58, - / 42; Q8_0 T = 3 58.3 / 57.4,
-// 56.6 / 45.7; T = 16 223 / 64.
+// Tokens from which the 32-value block formats (Q4_0, Q8_0, Q4_1, Q5_0, Q5_1) take the matrix cores
+// (SLHIP_MATVEC_MQ_MIN_T; 0 disables). Measured with matvec_mq2 at [14336, 4096] (dual, f32 x, us, VALU /
+// matrix cores): Q4_0 T = 2 28.1 / 44.1, T = 3 56.8 / 45.0; Q8_0 T = 2 32.5 / 46.2, T = 3 58.0 / 48.1.
 static int mq_min_tokens() { return env_int("SLHIP_MATVEC_MQ_MIN_T", 3); }
-// The same for the K-quants (SLHIP_MATVEC_KQ_MIN_T): their VALU kernel takes four tokens per pass, so the
-// matrix cores pay from five. (Q4_1, Q5_0 and Q5_1 follow Q4_0's SLHIP_MATVEC_MQ_MIN_T.) Measured dual at [14336, 4096], f32 x (us, VALU / matrix cores): T = 4 57.6 / 75.2;
-// T = 16 229 / 82.
-static int kq_min_tokens() { return env_int("SLHIP_MATVEC_KQ_MIN_T", 5); }
+// The same for the K-quants (SLHIP_MATVEC_KQ_MIN_T). With matvec_mq2, measured dual at [14336, 4096], f32 x
+// (us, VALU / matrix cores): Q4_K T = 2 30.6 / 46.5, T = 3 60.6 / 49.0; Q6_K T = 3 94.2 / 62.5; Q3_K T = 3
+// 78.0 / 61.2 (the VALU kernel's passes hold 2 and then 4 tokens): from three tokens.
+static int kq_min_tokens() { return env_int("SLHIP_MATVEC_KQ_MIN_T", 3); }
 
 // The several-token kernel with the stage moved straight to LDS and each lane scaling its own row
 // (matvec_mq.hpp, matvec_mq_*.hip); SLHIP_MATVEC_MQ2=0 keeps matvec_mfma_q below, which also takes the
