@@ -196,13 +196,19 @@ __global__ __launch_bounds__(64 * kMq2Waves) void matvec_mq2(MatvecArgs a)
             if constexpr (XF32) {
                 v[0] = x.f[j][0].x; v[1] = x.f[j][0].y; v[2] = x.f[j][0].z; v[3] = x.f[j][0].w;
                 v[4] = x.f[j][1].x; v[5] = x.f[j][1].y; v[6] = x.f[j][1].z; v[7] = x.f[j][1].w;
-                split3(v, P[0], P[1], P[NP - 1]);
             } else {
                 P[0] = x.b[j];
                 Vec<SLHIP_BF16>::unpack(x.b[j], v);
             }
+            const float ps8 = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+            if constexpr (XF32) {
+                // the split's guard against non-finite x (whose remainders would be NaN) only when some lane's
+                // eight values have a non-finite (or overflowing) sum: a wave-uniform test
+                if (__builtin_amdgcn_ballot_w64(!(fabsf(ps8) <= 3.4028235e38f)) == 0) split3_finite(v, P[0], P[1], P[NP - 1]);
+                else split3(v, P[0], P[1], P[NP - 1]);
+            }
             if constexpr (MIN) {
-                float ps = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+                float ps = ps8;
                 if constexpr (Q2K) {  // per 16-value half: lane groups {0, 1} and {2, 3}
                     const float p01 = ps + __shfl_xor(ps, 16);
                     const float other = __shfl_xor(p01, 32);

@@ -30,6 +30,23 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(const uint4& v) { return __builtin_bit_cast(bf16x8_t, v); }
 
+// split3 for finite x: the same parts without the guard.
+__device__ __forceinline__ void split3_finite(const float* x, uint4& h, uint4& m, uint4& l)
+{
+    uint32_t hw[4], mw[4], lw[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float a0 = x[2 * i], a1 = x[2 * i + 1];
+        hw[i] = pack_bf16x2(a0, a1);
+        const float r0 = a0 - bf16_lo(hw[i]), r1 = a1 - bf16_hi(hw[i]);
+        mw[i] = pack_bf16x2(r0, r1);
+        lw[i] = pack_bf16x2(r0 - bf16_lo(mw[i]), r1 - bf16_hi(mw[i]));
+    }
+    h = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+    m = make_uint4(mw[0], mw[1], mw[2], mw[3]);
+    l = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+}
+
 // x[0..7] (f32) as three bf16 vectors with h + m + l == x; a non-finite x keeps only h (inf - inf would
 // otherwise make the remainders NaN).
 __device__ __forceinline__ void split3(const float* x, uint4& h, uint4& m, uint4& l)
