@@ -195,6 +195,29 @@ def test_matvec(device, fmt, dx, dy, T, K, N):
     _check_single(y, dy, ref, S, f"matvec {fmt}")
 
 
+@pytest.mark.parametrize("fmt,dx,T", [("bf16", "f32", 1), ("bf16", "f32", 5), ("q4_k", "f32", 1), ("q4_k", "f32", 4),
+                                    ("q4_k", "bf16", 16), ("q6_k", "f32", 7), ("q4_0", "f32", 3), ("q8_0", "bf16", 12),
+                                    ("q3_k", "f32", 9), ("q5_1", "f32", 2)])
+def test_matvec_bias(device, fmt, dx, T):
+    """slhip_matvec_bias: y = x . W^T + bias in the matvec's launch (FoldMatMulBiases: the f32 sum, then the Add
+    of the f32 row vector), on every path (one token, the VALU kernels, the matrix cores)."""
+    K, N = 2048, 56
+    seed = _seed("bias", fmt, dx, T)
+    raw, W = _weights(fmt, N, K, seed, 1)
+    x, x32 = _x(dx, T, K, seed)
+    b = synth.normal(seed, 5, (N,))
+    with Dev() as d:
+        px, pw, pb = d.put(x), d.put(raw), d.put(b)
+        py = d.empty(T * N * 4)
+        log(f"matvec_bias fmt={fmt} x={dx} T={T}")
+        native.matvec_bias(fmt, dx, "f32", px, T, K, pw, N, pb, py)
+        native.synchronize()
+        y = d.get(py, (T, N), np.float32)
+    ref = oracle.add(oracle.matvec(fmt, raw, N, K, x32), np.broadcast_to(b, (T, N)).copy())
+    S = np.abs(x32).astype(np.float64) @ _abs_terms(fmt, raw, W).T
+    _check_single(y, "f32", ref, S + 2.0 ** -8 * np.abs(ref.astype(np.float64)), f"matvec_bias {fmt}")
+
+
 @pytest.mark.parametrize("fmt", ["f32", "f16", "bf16", "q8_0", "q4_0", "q4_1", "q5_0", "q5_1", "q6_k", "q2_k", "q3_k"])
 def test_one_hot_rows_pick_columns_exactly(device, fmt):
     """x = e_k: every 8-value group but one sums to zero and the one holds q_k * 1 exactly, so y = d q_k + a
