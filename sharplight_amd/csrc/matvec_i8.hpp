@@ -179,6 +179,8 @@ __device__ __forceinline__ float unit_dot(const I8Unit& u, const uint4& x0, cons
     }
 }
 
+#include "matvec_i8_reg.hpp"
+
 // ---- several tokens on the integer matrix cores ----------------------------------------------------------
 //
 // v_mfma_i32_16x16x32_i8 multiplies 16 tokens' q8 values of one 32-value unit (A: lane l holds token l % 16,
@@ -632,25 +634,45 @@ __global__ __launch_bounds__(kI8Threads) void matvec_i8(I8Args a)
     uint8_t* xs = reinterpret_cast<uint8_t*>(smem + (kI8Threads / 64) * R * rbw);
     const int nb = K / 32;  // units per row
 
-    const int tot = R * nch;
+    // 16-byte rows: each matrix's chunks are padded to whole groups of 64, so a group of 64 chunks (one load
+    // per lane) lies in one matrix and reads from a wave-uniform row base (no per-lane address arithmetic);
+    // lanes past the row's end load nothing and store nothing. Other rows: one run over both rows' chunks,
+    // clamped to the last one.
+    const int ncp = U == 16 ? (nch + 63) / 64 * 64 : nch;
+    const int tot = R * ncp;
     auto load_batch = [&](int64_t n, int base, uint4* v) {
 #pragma unroll
         for (int c = 0; c < CH; c++) {
-            if (base + c * 64 >= tot) break;  // wave-uniform
-            int idx = base + c * 64 + lane;
-            idx = idx < tot ? idx : tot - 1;
-            const int r = idx >= nch ? 1 : 0;
-            v[c] = load_chunk<U>((r ? a.wu : a.wg) + n * a.wrow, static_cast<int64_t>(idx - r * nch) * 16, a.wrow);
+            const int g0 = base + c * 64;
+            if (g0 >= tot) break;  // wave-uniform
+            if constexpr (U == 16) {
+                const int r = g0 >= ncp ? 1 : 0;  // wave-uniform
+                const int w = g0 - r * ncp + lane;
+                const char* row = (r ? a.wu : a.wg) + n * a.wrow;
+                if (w < nch) v[c] = load_nt(row + static_cast<uint32_t>(w) * 16u);
+            } else {
+                int idx = g0 + lane;
+                idx = idx < tot ? idx : tot - 1;
+                const int r = idx >= nch ? 1 : 0;
+                v[c] = load_chunk<U>((r ? a.wu : a.wg) + n * a.wrow, static_cast<int64_t>(idx - r * nch) * 16, a.wrow);
+            }
         }
     };
     auto store_batch = [&](int base, const uint4* v) {
 #pragma unroll
         for (int c = 0; c < CH; c++) {
-            if (base + c * 64 >= tot) break;  // wave-uniform
-            int idx = base + c * 64 + lane;
-            idx = idx < tot ? idx : tot - 1;
-            const int r = idx >= nch ? 1 : 0;
-            reinterpret_cast<uint4*>(rows + r * rbw)[idx - r * nch] = v[c];
+            const int g0 = base + c * 64;
+            if (g0 >= tot) break;  // wave-uniform
+            if constexpr (U == 16) {
+                const int r = g0 >= ncp ? 1 : 0;
+                const int w = g0 - r * ncp + lane;
+                if (w < nch) reinterpret_cast<uint4*>(rows + r * rbw)[w] = v[c];
+            } else {
+                int idx = g0 + lane;
+                idx = idx < tot ? idx : tot - 1;
+                const int r = idx >= nch ? 1 : 0;
+                reinterpret_cast<uint4*>(rows + r * rbw)[idx - r * nch] = v[c];
+            }
         }
     };
     auto rest = [&](int64_t n, uint4* v) {  // batches after the first, loaded and stored in turn
@@ -702,11 +724,48 @@ __global__ __launch_bounds__(kI8Threads) void matvec_i8(I8Args a)
                 }
             }
         };
-        const int full = nb / 64;  // iterations in which every lane has a unit
-        for (int i = 0; i < full; i++) unit(lane + 64 * i, true);
-        if (full * 64 < nb) {  // wave-uniform
-            const int b = lane + 64 * full;
-            unit(b < nb ? b : nb - 1, b < nb);
+        if constexpr (kLdsPiece<FMT>) {
+            // a 64-value slice per lane, its bytes read from the row images as aligned 16-byte words
+            const int nsl = K / 64;
+            auto slice = [&](int sl, bool own) {
+                using P = RegPiece<FMT>;
+                uint4 wg[P::NW], wu[P::NW];
+                P::lds_load(wg, rows, sl);
+                if constexpr (DUAL) P::lds_load(wu, rows + rbw, sl);
+                I8Unit g0, g1, u0, u1;
+                int j0, j1;
+                P::units(wg, sl, g0, g1, j0, j1);
+                if constexpr (DUAL) P::units(wu, sl, u0, u1, j0, j1);
+#pragma unroll
+                for (int t = 0; t < TT; t++) {
+                    const uint8_t* xt = xs + t * xrow;
+                    const uint4 x00 = *reinterpret_cast<const uint4*>(xt + 32 * j0);
+                    const uint4 x01 = *reinterpret_cast<const uint4*>(xt + 32 * j0 + 16);
+                    const uint4 x10 = *reinterpret_cast<const uint4*>(xt + 32 * j1);
+                    const uint4 x11 = *reinterpret_cast<const uint4*>(xt + 32 * j1 + 16);
+                    const float4 sc0 = *reinterpret_cast<const float4*>(xt + K + 16 * j0);
+                    const float4 sc1 = *reinterpret_cast<const float4*>(xt + K + 16 * j1);
+                    const float pg = unit_dot<FMT>(g0, x00, x01, sc0) + unit_dot<FMT>(g1, x10, x11, sc1);
+                    ag[t] += own ? pg : 0.0f;
+                    if constexpr (DUAL) {
+                        const float pu = unit_dot<FMT>(u0, x00, x01, sc0) + unit_dot<FMT>(u1, x10, x11, sc1);
+                        au[t] += own ? pu : 0.0f;
+                    }
+                }
+            };
+            const int full = nsl / 64;
+            for (int i = 0; i < full; i++) slice(lane + 64 * i, true);
+            if (full * 64 < nsl) {  // wave-uniform
+                const int sl = lane + 64 * full;
+                slice(sl < nsl ? sl : nsl - 1, sl < nsl);
+            }
+        } else {
+            const int full = nb / 64;  // iterations in which every lane has a unit
+            for (int i = 0; i < full; i++) unit(lane + 64 * i, true);
+            if (full * 64 < nb) {  // wave-uniform
+                const int b = lane + 64 * full;
+                unit(b < nb ? b : nb - 1, b < nb);
+            }
         }
 #pragma unroll
         for (int t = 0; t < TT; t++) {
@@ -807,6 +866,56 @@ static int i8_ch(const I8Args& a, hipStream_t st)
     return launch_i8<FMT, TT, 8, DUAL, 16>(a, st);
 }
 
+// The register-piece kernel: a persistent grid of as many waves as fit, trimmed so that every wave gets the
+// same number of rows.
+template <int FMT, int TT, bool DUAL, int D>
+static int launch_i8_reg(const I8Args& a, hipStream_t st)
+{
+    const size_t lds = static_cast<size_t>(TT) * static_cast<size_t>(a.K + a.K / 2);
+    auto kernel = matvec_i8_reg<FMT, TT, DUAL, D>;
+    if (lds > 65536) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+        if (e != hipSuccess) return fail(SLHIP_ERR_HIP, "matvec_q8: %zu bytes of LDS refused: %s", lds, hipGetErrorString(e));
+    }
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kI8RegThreads, lds) != hipSuccess || per_cu < 1)
+        per_cu = 1;
+    constexpr int wpb = kI8RegThreads / 64;
+    const int64_t resident = static_cast<int64_t>(device_cus_i8()) * per_cu * wpb;
+    const int64_t per_wave = (a.N + resident - 1) / resident;
+    const int64_t waves = (a.N + per_wave - 1) / per_wave;
+    kernel<<<dim3(static_cast<unsigned>((waves + wpb - 1) / wpb)), kI8RegThreads, lds, st>>>(a);
+    return check_launch("matvec_i8_reg");
+}
+
+// Whether the register-piece kernel takes T tokens: for its formats at one to four tokens with K a multiple of
+// 64 (SLHIP_MATVEC_I8_REG=0 turns it off).
+template <int FMT>
+inline bool i8_reg_takes(const I8Args& a)
+{
+    static int v = -1;
+    if (v == -1) {
+        const char* e = getenv("SLHIP_MATVEC_I8_REG");
+        v = e ? atoi(e) : 1;
+    }
+    return v != 0 && kRegPieceKernel<FMT> && a.T <= 4 && a.K % 64 == 0 && 4 * (a.K + a.K / 2) <= static_cast<int64_t>(kI8MaxLds);
+}
+
+template <int FMT, bool DUAL>
+static int run_i8_reg(I8Args a, hipStream_t st)
+{
+    const int tt = a.T <= 1 ? 1 : a.T <= 2 ? 2 : 4;
+    for (int64_t t0 = 0; t0 < a.T; t0 += tt) {
+        a.t0 = t0;
+        // two register sets (one item in flight while one is computed): three measured slower
+        const int r = tt == 1 ? launch_i8_reg<FMT, 1, DUAL, 2>(a, st) : tt == 2 ? launch_i8_reg<FMT, 2, DUAL, 2>(a, st)
+                                                                         : launch_i8_reg<FMT, 4, DUAL, 2>(a, st);
+        if (r != SLHIP_OK) return r;
+    }
+    return SLHIP_OK;
+}
+
 template <int FMT, bool DUAL>
 static int i8_tt(const I8Args& a, int tt, hipStream_t st)
 {
@@ -853,6 +962,8 @@ int run_i8(I8Args a, bool dual, hipStream_t st)
     const int mt = i8_mfma_min_tokens<FMT>();
     if (mt > 0 && a.T >= mt && a.K % 1024 == 0 && a.wrow % I8Stage<FMT>::UB == 0 && a.N * a.wrow < (int64_t{1} << 31))
         return run_i8_mfma<FMT>(a, dual, st);
+    if constexpr (kRegPieceKernel<FMT>)
+        if (i8_reg_takes<FMT>(a)) return dual ? run_i8_reg<FMT, true>(a, st) : run_i8_reg<FMT, false>(a, st);
     int tt = 8;
     while (tt > 1 && (tt / 2 >= a.T || i8_lds(tt, a.K, a.wrow, dual) > kI8MaxLds)) tt /= 2;
     if (i8_lds(tt, a.K, a.wrow, dual) > kI8MaxLds)

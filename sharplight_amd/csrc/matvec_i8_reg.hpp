@@ -1,0 +1,307 @@
+#pragma once
+// The integer-dot matvec's 64-value slices (included by matvec_i8.hpp inside namespace slhip, after unit_dot).
+//
+// A slice is two 32-value units of a row together with the bytes of their block or super-block scales;
+// RegPiece<FMT> decodes a slice from a few 16-byte words into two I8Units (codes, multipliers, offsets), so
+// that each lane decodes only its own scales, with word-wide arithmetic.
+//   * Q4_K / Q5_K: the LDS-staged kernel (matvec_i8) reads each lane's slice out of the row images as aligned
+//     16-byte words (lds_load).
+//   * Q6_K / IQ4_XS: the register-piece kernel below loads each lane's slice from HBM straight into
+//     registers (unaligned loads: their blocks are only 2- or 8-byte aligned), with no row image in LDS, no
+//     LDS store and no per-chunk address arithmetic. A wave takes rows n, n + W, ... (W waves in the grid,
+//     sized so that each wave gets the same number of rows), one (row, group of 64 slices) item at a time:
+//     the next D - 1 items' loads are in flight while one is computed (D register sets in rotation). The
+//     block's quantized activation rows sit in LDS; a row's output is the wave sum of its lanes' unit terms
+//     (unit_dot, the same per-unit arithmetic as the LDS-staged kernel).
+
+typedef uint32_t u32x4_a2 __attribute__((ext_vector_type(4), aligned(2)));
+typedef uint32_t u32_a2 __attribute__((aligned(2)));
+
+__device__ __forceinline__ uint4 ldw16(const char* p)
+{
+    const u32x4_a2 v = *reinterpret_cast<const u32x4_a2*>(p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint32_t ldw4(const char* p) { return *reinterpret_cast<const u32_a2*>(p); }
+__device__ __forceinline__ uint32_t ldw2(const char* p) { return *reinterpret_cast<const uint16_t*>(p); }
+
+__device__ __forceinline__ uint32_t word_of(const uint4& v, int k) { return k == 0 ? v.x : k == 1 ? v.y : k == 2 ? v.z : v.w; }
+
+// A lane's raw bytes for slice s of a row (NW 16-byte registers), and the two units they hold with the unit
+// index (32-value units from the row's start) of each; field layouts as in i8_unit.
+template <int FMT> struct RegPiece;
+
+// Q4_K / Q5_K sub-blocks jj, jj + 1 (jj = 2 (p & 1), p = the slice's quarter of its super-block) of the 6-bit
+// scales and minimums from the header words (scales[0..3], [4..7], [8..11]): two bytes at a time.
+__device__ __forceinline__ void k_scales2(const uint4& h, int p, uint32_t& sc, uint32_t& mn)
+{
+    const int sh = 16 * (p & 1);
+    const uint32_t Y = h.y >> sh, Z = h.z >> sh, W = h.w >> sh;
+    if (p >= 2) {
+        sc = (W & 0x0F0Fu) | ((Y >> 2) & 0x3030u);
+        mn = ((W >> 4) & 0x0F0Fu) | ((Z >> 2) & 0x3030u);
+    } else {
+        sc = Y & 0x3F3Fu;
+        mn = Z & 0x3F3Fu;
+    }
+}
+
+template <int FMT> struct RegPieceK45 {  // {f16 d, f16 dmin, u8 scales[12], [u8 qh[32]], u8 qs[128]}
+    static constexpr bool K5 = FMT == SLHIP_FMT_Q5_K;
+    static constexpr int NW = K5 ? 5 : 3;
+    // a slice's header and code words from a row image in LDS (super-blocks and their code runs are 16-byte
+    // aligned there); with Q5_K, the 32 bytes of fifth bits
+    static __device__ __forceinline__ void lds_load(uint4* w, const uint32_t* img, int s)
+    {
+        const uint4* b = reinterpret_cast<const uint4*>(img) + (K5 ? 11 : 9) * (s >> 2);
+        w[0] = b[0];
+        const uint4* q = b + (K5 ? 3 : 1) + 2 * (s & 3);
+        w[1] = q[0];
+        w[2] = q[1];
+        if constexpr (K5) {
+            w[3] = b[1];
+            w[4] = b[2];
+        }
+    }
+    static __device__ __forceinline__ void units(const uint4* w, int s, I8Unit& u0, I8Unit& u1, int& j0, int& j1)
+    {
+        const int p = s & 3;
+        j0 = 2 * s;
+        j1 = j0 + 1;
+        uint32_t sc, mn;
+        k_scales2(w[0], p, sc, mn);
+        const float d = f16_lo(w[0].x), dm = f16_hi(w[0].x);
+        u0.a0 = u0.a1 = __fmul_rn(d, static_cast<float>(sc & 0xFFu));
+        u1.a0 = u1.a1 = __fmul_rn(d, static_cast<float>(sc >> 8));
+        u0.b0 = u0.b1 = -__fmul_rn(dm, static_cast<float>(mn & 0xFFu));
+        u1.b0 = u1.b1 = -__fmul_rn(dm, static_cast<float>(mn >> 8));
+        const int jj = 2 * p;  // sub-block of the super-block (bit of qh)
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const uint32_t q = word_of(w[1 + k / 4], k % 4);
+            uint32_t lo = q & 0x0F0F0F0Fu, hi = (q >> 4) & 0x0F0F0F0Fu;
+            if constexpr (K5) {
+                const uint32_t qh = word_of(w[3 + k / 4], k % 4);
+                lo |= ((qh >> jj) & 0x01010101u) << 4;
+                hi |= ((qh >> (jj + 1)) & 0x01010101u) << 4;
+            }
+            u0.c[k] = lo;
+            u1.c[k] = hi;
+        }
+    }
+};
+template <> struct RegPiece<SLHIP_FMT_Q4_K> : RegPieceK45<SLHIP_FMT_Q4_K> {};
+template <> struct RegPiece<SLHIP_FMT_Q5_K> : RegPieceK45<SLHIP_FMT_Q5_K> {};
+
+template <> struct RegPiece<SLHIP_FMT_IQ4_XS> {  // {f16 d, u16 scales_h, u8 scales_l[4], u8 qs[128]}
+    static constexpr int NW = 3;
+    static __device__ __forceinline__ void load(uint4* w, const char* row, int s)
+    {
+        const char* b = row + 136 * (s >> 2);
+        w[0].x = ldw4(b);
+        w[0].y = ldw4(b + 4);
+        w[1] = ldw16(b + 8 + 32 * (s & 3));
+        w[2] = ldw16(b + 24 + 32 * (s & 3));
+    }
+    static __device__ __forceinline__ void units(const uint4* w, int s, I8Unit& u0, I8Unit& u1, int& j0, int& j1)
+    {
+        const int p = s & 3;
+        j0 = 2 * s;
+        j1 = j0 + 1;
+        const float d = f16_lo(w[0].x);
+        const uint32_t sh = (w[0].x >> (16 + 4 * p)) & 0xFu;  // the high bits of sub-blocks 2p and 2p + 1
+        const uint32_t sl = (w[0].y >> (8 * p)) & 0xFFu;
+        const int ls0 = static_cast<int>((sl & 0xFu) | ((sh & 3u) << 4));
+        const int ls1 = static_cast<int>((sl >> 4) | ((sh >> 2) << 4));
+        u0.a0 = u0.a1 = __fmul_rn(d, static_cast<float>(ls0 - 32));
+        u1.a0 = u1.a1 = __fmul_rn(d, static_cast<float>(ls1 - 32));
+        u0.b0 = u0.b1 = u1.b0 = u1.b1 = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint32_t q0 = word_of(w[1], k), q1 = word_of(w[2], k);
+            u0.c[k] = iq4_lookup4(q0 & 0x0F0F0F0Fu);
+            u0.c[4 + k] = iq4_lookup4((q0 >> 4) & 0x0F0F0F0Fu);
+            u1.c[k] = iq4_lookup4(q1 & 0x0F0F0F0Fu);
+            u1.c[4 + k] = iq4_lookup4((q1 >> 4) & 0x0F0F0F0Fu);
+        }
+    }
+};
+
+template <> struct RegPiece<SLHIP_FMT_Q6_K> {  // {ql[128], qh[64], i8 scales[16], f16 d}
+    // slice quarter p: ql[32 p .. + 31] holds quarters qt = p & 1 (low nibbles) and qt + 2 (high nibbles) of
+    // half n = p / 2, whose two high bits are in qh[32 n ..]: units 4 n + qt and 4 n + qt + 2 of the super-block
+    static constexpr int NW = 5;
+    static __device__ __forceinline__ void load(uint4* w, const char* row, int s)
+    {
+        const int p = s & 3, n = p >> 1;
+        const char* b = row + 210 * (s >> 2);
+        w[0] = ldw16(b + 32 * p);
+        w[1] = ldw16(b + 32 * p + 16);
+        w[2] = ldw16(b + 128 + 32 * n);
+        w[3] = ldw16(b + 144 + 32 * n);
+        w[4].x = ldw4(b + 192 + 8 * n);
+        w[4].y = ldw4(b + 196 + 8 * n);
+        w[4].z = ldw2(b + 208);
+    }
+    static __device__ __forceinline__ void units(const uint4* w, int s, I8Unit& u0, I8Unit& u1, int& j0, int& j1)
+    {
+        const int p = s & 3, n = p >> 1, qt = p & 1;
+        j0 = 8 * (s >> 2) + 4 * n + qt;
+        j1 = j0 + 2;
+        const float d = f16_lo(w[4].z);
+        const uint32_t s0 = w[4].x >> (16 * qt), s1 = w[4].y >> (16 * qt);
+        u0.a0 = __fmul_rn(d, static_cast<float>(static_cast<int8_t>(s0 & 0xFFu)));
+        u0.a1 = __fmul_rn(d, static_cast<float>(static_cast<int8_t>((s0 >> 8) & 0xFFu)));
+        u1.a0 = __fmul_rn(d, static_cast<float>(static_cast<int8_t>(s1 & 0xFFu)));
+        u1.a1 = __fmul_rn(d, static_cast<float>(static_cast<int8_t>((s1 >> 8) & 0xFFu)));
+        u0.b0 = -32.0f * u0.a0;
+        u0.b1 = -32.0f * u0.a1;
+        u1.b0 = -32.0f * u1.a0;
+        u1.b1 = -32.0f * u1.a1;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const uint32_t l = word_of(w[k / 4], k % 4), h = word_of(w[2 + k / 4], k % 4);
+            u0.c[k] = (l & 0x0F0F0F0Fu) | (((h >> (2 * qt)) & 0x03030303u) << 4);
+            u1.c[k] = ((l >> 4) & 0x0F0F0F0Fu) | (((h >> (2 * qt + 4)) & 0x03030303u) << 4);
+        }
+    }
+};
+
+// Formats whose slices the LDS-staged kernel reads as aligned 16-byte words.
+template <int FMT> constexpr bool kLdsPiece = FMT == SLHIP_FMT_Q4_K || FMT == SLHIP_FMT_Q5_K;
+
+// Formats the register-piece kernel takes (measured against the LDS-staged kernel on [14336, 4096] gate/up
+// pairs at one to four tokens: Q6_K 30.0 / 32.7 / 38.9 us against 30.3 / 35.7 / 49.6, IQ4_XS ~10% ahead; for
+// the 32-value block formats the scattered 16-byte pieces cost more L1 accesses than they save, and Q4_K /
+// Q5_K run faster as slices of the LDS row images).
+template <int FMT> constexpr bool kRegPieceKernel = FMT == SLHIP_FMT_Q6_K || FMT == SLHIP_FMT_IQ4_XS;
+
+constexpr int kI8RegThreads = 256;
+
+template <int FMT, int TT, bool DUAL, int D>
+__global__ __launch_bounds__(kI8RegThreads) void matvec_i8_reg(I8Args a)
+{
+    using P = RegPiece<FMT>;
+    constexpr int R = DUAL ? 2 : 1;
+    extern __shared__ uint4 xsm[];
+    const int lane = threadIdx.x & 63;
+    const int wave = wave_id();
+    const int K = static_cast<int>(a.K);
+    const int xrow = K + K / 2;
+    const int ns = K / 64;             // 64-value slices per row
+    const int ni = (ns + 63) / 64;     // items (one slice per lane) per row
+    {  // the block's TT quantized rows (rows past T repeat row T - 1)
+        const int per = xrow / 16;
+        for (int u = threadIdx.x; u < TT * per; u += kI8RegThreads) {
+            const int t = u / per;
+            int64_t tok = a.t0 + t;
+            tok = tok < a.T ? tok : a.T - 1;
+            xsm[u] = reinterpret_cast<const uint4*>(a.xq + tok * xrow)[u - t * per];
+        }
+    }
+    __syncthreads();
+    const char* xs = reinterpret_cast<const char*>(xsm);
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * (kI8RegThreads / 64);
+    int64_t n = static_cast<int64_t>(blockIdx.x) * (kI8RegThreads / 64) + wave;
+    if (n >= a.N) return;  // wave-uniform; no barrier follows
+
+    float ag[TT], au[TT];
+#pragma unroll
+    for (int t = 0; t < TT; t++) ag[t] = au[t] = 0.0f;
+
+    // loads of item (row, it) into a register set; rows past N read row N - 1 (their results are dropped)
+    auto load = [&](uint4 (&w)[R][P::NW], int64_t row, int it) {
+        const int64_t rr = row < a.N ? row : a.N - 1;
+        int s = it * 64 + lane;
+        s = s < ns ? s : ns - 1;
+        P::load(w[0], a.wg + rr * a.wrow, s);
+        if constexpr (DUAL) P::load(w[1], a.wu + rr * a.wrow, s);
+    };
+    auto compute = [&](const uint4 (&w)[R][P::NW], int it) {
+        const int s0 = it * 64 + lane;
+        const bool own = s0 < ns;
+        const int s = own ? s0 : ns - 1;
+        I8Unit g0, g1, u0, u1;
+        int j0, j1;
+        P::units(w[0], s, g0, g1, j0, j1);
+        if constexpr (DUAL) P::units(w[1], s, u0, u1, j0, j1);
+#pragma unroll
+        for (int t = 0; t < TT; t++) {
+            const char* xt = xs + t * xrow;
+            const uint4 x00 = *reinterpret_cast<const uint4*>(xt + 32 * j0);
+            const uint4 x01 = *reinterpret_cast<const uint4*>(xt + 32 * j0 + 16);
+            const uint4 x10 = *reinterpret_cast<const uint4*>(xt + 32 * j1);
+            const uint4 x11 = *reinterpret_cast<const uint4*>(xt + 32 * j1 + 16);
+            const float4 sc0 = *reinterpret_cast<const float4*>(xt + K + 16 * j0);
+            const float4 sc1 = *reinterpret_cast<const float4*>(xt + K + 16 * j1);
+            const float pg = unit_dot<FMT>(g0, x00, x01, sc0) + unit_dot<FMT>(g1, x10, x11, sc1);
+            ag[t] += own ? pg : 0.0f;
+            if constexpr (DUAL) {
+                const float pu = unit_dot<FMT>(u0, x00, x01, sc0) + unit_dot<FMT>(u1, x10, x11, sc1);
+                au[t] += own ? pu : 0.0f;
+            }
+        }
+    };
+    auto finish = [&](int64_t row) {
+#pragma unroll
+        for (int t = 0; t < TT; t++) {
+            float out = wave_sum(ag[t]);
+            if constexpr (DUAL) {
+                const float u = wave_sum(au[t]);
+                const float g = out;
+                const float act = a.act == SLHIP_ACT_SILU        ? activate<SLHIP_ACT_SILU>(g)
+                                  : a.act == SLHIP_ACT_GELU_TANH ? activate<SLHIP_ACT_GELU_TANH>(g)
+                                                                 : activate<SLHIP_ACT_GELU_ERF>(g);
+                out = act * u;
+            } else if (a.bias) {
+                out = out + a.bias[row];
+            }
+            const int64_t tok = a.t0 + t;
+            if (tok < a.T && lane == 0) {
+                if (a.yt == SLHIP_F32)
+                    static_cast<float*>(a.y)[tok * a.ys + row] = out;
+                else
+                    static_cast<uint16_t*>(a.y)[tok * a.ys + row] = static_cast<uint16_t>(f32_to_bf16_bits(out));
+            }
+            ag[t] = au[t] = 0.0f;
+        }
+    };
+
+    // D register sets in rotation: set k holds item (rn[k], ri[k]); while one is computed the next D - 1
+    // items' loads are in flight. Loads past the last item read the clamped row N - 1 (cache hits), so the
+    // wait counts stay exact.
+    uint4 S[D][R][P::NW];
+    int64_t rn[D];
+    int ri[D];
+    auto next = [&](int k, int from) {
+        rn[k] = rn[from];
+        ri[k] = ri[from] + 1;
+        if (ri[k] == ni) {
+            ri[k] = 0;
+            rn[k] += stride;
+        }
+    };
+    rn[0] = n;
+    ri[0] = 0;
+    load(S[0], rn[0], ri[0]);
+#pragma unroll
+    for (int k = 1; k < D - 1; k++) {
+        next(k, k - 1);
+        load(S[k], rn[k], ri[k]);
+    }
+    bool more = true;
+    while (more) {
+#pragma unroll
+        for (int k = 0; k < D; k++) {
+            if (more) {
+                const int kl = (k + D - 1) % D, kp = (k + D - 2) % D;
+                next(kl, kp);
+                load(S[kl], rn[kl], ri[kl]);
+                compute(S[k], ri[k]);
+                if (ri[k] == ni - 1) finish(rn[k]);
+                more = rn[(k + 1) % D] < a.N;
+            }
+        }
+    }
+}
+

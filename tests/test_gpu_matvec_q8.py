@@ -158,6 +158,13 @@ SINGLE_CASES = [  # (fmt, x dtype, y dtype, T, K, N)
     ("q6_k", "f32", "f32", 20, 2048, 33),    # a full 16-token pass and a 4-token one
     ("q8_0", "f32", "f32", 9, 14336, 16),    # fourteen stages, one tile
     ("q4_0", "f32", "f32", 10, 1280, 24),    # K not whole stages: the VALU kernel
+    # 64-value slices: Q6_K / IQ4_XS loaded straight into registers, Q4_K / Q5_K read from the row images;
+    # K = 14336 is four slice groups per row (the last one half full), T = 3 pads a four-token pass
+    ("q6_k", "f32", "f32", 2, 14336, 20),
+    ("iq4_xs", "bf16", "f32", 3, 14336, 17),
+    ("q4_k", "f32", "bf16", 3, 14336, 21),
+    ("q5_k", "f32", "f32", 1, 14336, 19),
+    ("q6_k", "f32", "bf16", 4, 256, 700),    # one slice group, many rows per wave
 ]
 
 
