@@ -189,24 +189,27 @@ __device__ __forceinline__ float unit_dot(const I8Unit& u, const uint4& x0, cons
 // multiplier and offset once per unit), so each unit's sums for 16 rows x 16 tokens take one
 // instruction and the scaling a (d s) + b gs per output runs on the VALU. Q6_K's two 16-value scale groups take
 // two instructions, each with the other half's codes masked to zero. A block of 8 waves takes a tile (a gate/up
-// pair of tiles); stages of 1024 values of the 16 rows go through LDS, double-buffered: the next stage's rows and
-// q8 scales move from HBM straight into LDS (global_load_lds, no registers) while the current one is computed;
-// each wave takes 4 units of a stage; the waves' partial sums meet in LDS at the end.
+// pair of tiles); stages of SU units (1024 values; 512 for Q8_0) of the 16 rows go through LDS, double-buffered:
+// the next stage's rows and q8 scales move from HBM straight into LDS (global_load_lds, no registers) while the
+// current one is computed; each wave takes SU / 8 units of a stage; the waves' partial sums meet in LDS at the
+// end.
 
-// Bytes of one row per 1024-value stage, the width of the staging loads, and whether the multipliers go
-// through a per-wave table (below).
+// Bytes of one row per 1024 values, the width of the staging loads, the 32-value units per stage (SU: Q8_0's
+// large rows take 512-value stages, which fit more blocks per CU -- [14336, 4096] pairs at 16 tokens 51.8 ->
+// 44 us; every other format measured slower so), and whether the multipliers go through a per-wave table
+// (below).
 template <int FMT> struct I8Stage;
-template <> struct I8Stage<SLHIP_FMT_Q8_0> { static constexpr int RB = 32 * 34, UB = 16; static constexpr bool TABLE = false; };
-template <> struct I8Stage<SLHIP_FMT_Q4_0> { static constexpr int RB = 32 * 18, UB = 16; static constexpr bool TABLE = false; };
-template <> struct I8Stage<SLHIP_FMT_Q4_1> { static constexpr int RB = 32 * 20, UB = 16; static constexpr bool TABLE = false; };
-template <> struct I8Stage<SLHIP_FMT_Q5_0> { static constexpr int RB = 32 * 22, UB = 16; static constexpr bool TABLE = false; };
-template <> struct I8Stage<SLHIP_FMT_Q5_1> { static constexpr int RB = 32 * 24, UB = 16; static constexpr bool TABLE = false; };
-template <> struct I8Stage<SLHIP_FMT_IQ4_NL> { static constexpr int RB = 32 * 18, UB = 16; static constexpr bool TABLE = false; };
-template <> struct I8Stage<SLHIP_FMT_MXFP4> { static constexpr int RB = 32 * 17, UB = 16; static constexpr bool TABLE = false; };
-template <> struct I8Stage<SLHIP_FMT_Q4_K> { static constexpr int RB = 4 * 144, UB = 16; static constexpr bool TABLE = true; };
-template <> struct I8Stage<SLHIP_FMT_Q5_K> { static constexpr int RB = 4 * 176, UB = 16; static constexpr bool TABLE = true; };
-template <> struct I8Stage<SLHIP_FMT_Q6_K> { static constexpr int RB = 4 * 210, UB = 4; static constexpr bool TABLE = false; };
-template <> struct I8Stage<SLHIP_FMT_IQ4_XS> { static constexpr int RB = 4 * 136, UB = 16; static constexpr bool TABLE = true; };
+template <> struct I8Stage<SLHIP_FMT_Q8_0> { static constexpr int RB = 32 * 34, UB = 16, SU = 16; static constexpr bool TABLE = false; };
+template <> struct I8Stage<SLHIP_FMT_Q4_0> { static constexpr int RB = 32 * 18, UB = 16, SU = 32; static constexpr bool TABLE = false; };
+template <> struct I8Stage<SLHIP_FMT_Q4_1> { static constexpr int RB = 32 * 20, UB = 16, SU = 32; static constexpr bool TABLE = false; };
+template <> struct I8Stage<SLHIP_FMT_Q5_0> { static constexpr int RB = 32 * 22, UB = 16, SU = 32; static constexpr bool TABLE = false; };
+template <> struct I8Stage<SLHIP_FMT_Q5_1> { static constexpr int RB = 32 * 24, UB = 16, SU = 32; static constexpr bool TABLE = false; };
+template <> struct I8Stage<SLHIP_FMT_IQ4_NL> { static constexpr int RB = 32 * 18, UB = 16, SU = 32; static constexpr bool TABLE = false; };
+template <> struct I8Stage<SLHIP_FMT_MXFP4> { static constexpr int RB = 32 * 17, UB = 16, SU = 32; static constexpr bool TABLE = false; };
+template <> struct I8Stage<SLHIP_FMT_Q4_K> { static constexpr int RB = 4 * 144, UB = 16, SU = 32; static constexpr bool TABLE = true; };
+template <> struct I8Stage<SLHIP_FMT_Q5_K> { static constexpr int RB = 4 * 176, UB = 16, SU = 32; static constexpr bool TABLE = true; };
+template <> struct I8Stage<SLHIP_FMT_Q6_K> { static constexpr int RB = 4 * 210, UB = 4, SU = 32; static constexpr bool TABLE = false; };
+template <> struct I8Stage<SLHIP_FMT_IQ4_XS> { static constexpr int RB = 4 * 136, UB = 16, SU = 32; static constexpr bool TABLE = true; };
 
 constexpr int kI8MfWaves = 8;
 
@@ -350,34 +353,34 @@ typedef int i32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 
-template <int FMT, bool DUAL>
-__global__ __launch_bounds__(64 * kI8MfWaves) void matvec_i8_mfma(I8Args a)
+template <int FMT, bool DUAL, int SU>
+__global__ __launch_bounds__(64 * kI8MfWaves) __attribute__((amdgpu_waves_per_eu(SU == 16 ? 6 : 1))) void matvec_i8_mfma(I8Args a)
 {
     constexpr int NM = DUAL ? 2 : 1;
-    constexpr int RB = I8Stage<FMT>::RB, UB = I8Stage<FMT>::UB;
+    constexpr int RB = I8Stage<FMT>::RB * SU / 32, UB = I8Stage<FMT>::UB;  // SU 32-value units per stage
     constexpr int PITCH = stage_pitch(RB, UB);
     constexpr int SPR = PITCH / UB;  // load slots per staged row; those past RB / UB are padding
     constexpr int MS = (16 * SPR + 63) / 64 * 64;  // slots per matrix: whole waves, so a wave's run is in one
     constexpr int SLOTS = NM * MS;
     constexpr int NT = 64 * kI8MfWaves;
     constexpr int LPT = (SLOTS + NT - 1) / NT;  // loads per thread and stage
-    constexpr int BPW = 32 / kI8MfWaves;  // units per wave and stage
+    constexpr int BPW = SU / kI8MfWaves;  // units per wave and stage
     constexpr bool H16 = kUnitForm<FMT> == kScale16Off;
     static_assert(RB % UB == 0 && (UB == 16 || UB == 4), "stage shape");
-    static_assert(NT == 16 * 32, "one thread per token and unit of a stage stages the q8 scales");
+    static_assert(NT >= 16 * SU && (SU == 16 || SU == 32), "one thread per token and unit of a stage stages the q8 scales");
     static_assert(2 * SLOTS * UB >= static_cast<int>(sizeof(float)) * kI8MfWaves * NM * 4 * 64,
                   "the cross-wave reduction reuses the weight stage");
     __shared__ __align__(16) uint32_t stage[2][SLOTS * UB / 4];  // [matrix: 16 rows of PITCH bytes, padding]
     auto rowp = [&](int b, int m, int rr) -> const uint32_t* { return &stage[b][(m * MS * UB + rr * PITCH) / 4]; };
     // the q8 scales {d, d s_lo, d s_hi, 0} of [unit][token] of a stage (the 4 tokens a lane group reads at
     // once are 64 bytes apart: different banks)
-    __shared__ float4 xsc[2][32][16];
+    __shared__ float4 xsc[2][SU][16];
     const int lane = threadIdx.x & 63;
     const int wave = wave_id();
     const int r = lane & 15, g = lane >> 4;
     const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 16;
     const int K = static_cast<int>(a.K);
-    const int ns = K / 1024;
+    const int ns = K / (32 * SU);
     const int64_t xstride = K + K / 2;
     int64_t tok = a.t0 + r;
     tok = tok < a.T ? tok : a.T - 1;
@@ -418,7 +421,14 @@ __global__ __launch_bounds__(64 * kI8MfWaves) void matvec_i8_mfma(I8Args a)
             const char* mat = ((NT * i + 64 * wave) / MS ? a.wu : a.wg) + static_cast<int64_t>(s) * RB;
             load_to_lds<UB>(mat, src[i], base);
         }
-        load_to_lds<16>(xs_base + static_cast<int64_t>(s) * 512, xs_off, &xsc[b][0][0] + 64 * wave);
+        if (64 * wave < 16 * SU) {  // wave-uniform; the base made visibly uniform for the scalar operand
+            const uint64_t xb = reinterpret_cast<uint64_t>(xs_base + static_cast<int64_t>(s) * (16 * SU));
+            // (readfirstlane returns int: each half goes through uint32_t, or the low half would sign-extend)
+            const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(xb)));
+            const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(xb >> 32)));
+            const uint64_t xbu = (static_cast<uint64_t>(hi) << 32) | lo;
+            load_to_lds<16>(reinterpret_cast<const void*>(xbu), xs_off, &xsc[b][0][0] + 64 * wave);
+        }
     };
     constexpr bool TABLE = I8Stage<FMT>::TABLE;
     constexpr int SBB = FMT == SLHIP_FMT_Q4_K ? 144 : FMT == SLHIP_FMT_Q5_K ? 176 : 136;  // super-block bytes
@@ -437,8 +447,8 @@ __global__ __launch_bounds__(64 * kI8MfWaves) void matvec_i8_mfma(I8Args a)
     };
     auto fetch_x = [&](Xs& x, int s) {
 #pragma unroll
-        for (int j = 0; j < BPW; j++) x.q[j] = *reinterpret_cast<const uint2*>(xrow + (s * 32 + wave * BPW + j) * 32 + 8 * g);
-        if constexpr (TABLE) x.hdr = *reinterpret_cast<const uint4*>(hdr_src + static_cast<int64_t>(s) * (1024 / 256) * SBB);
+        for (int j = 0; j < BPW; j++) x.q[j] = *reinterpret_cast<const uint2*>(xrow + (s * SU + wave * BPW + j) * 32 + 8 * g);
+        if constexpr (TABLE) x.hdr = *reinterpret_cast<const uint4*>(hdr_src + static_cast<int64_t>(s) * (SU / 8) * SBB);
     };
     // acc[m][i]: weight row n0 + r of matrix m, token t0 + 4 g + i (the MFMA's A operand is the q8 tokens, B the
     // weight codes, so each lane decodes the multipliers of its own row once per unit)
@@ -455,35 +465,40 @@ __global__ __launch_bounds__(64 * kI8MfWaves) void matvec_i8_mfma(I8Args a)
     // the wave's own LDS table, and read there by the 4 lanes of a row; the other formats' (one f16 or e8m0
     // field) are read from the stage directly.
     constexpr int NENT = NM * 16 * BPW;
-    static_assert(BPW == 4, "a wave's units are one half of a super-block");
+    static_assert(8 % BPW == 0, "a wave's units lie in one super-block");
     __shared__ __align__(16) float2 wsc[TABLE ? kI8MfWaves : 1][TABLE ? NENT : 1];
     float2* my = wsc[TABLE ? wave : 0];
     auto compute = [&](int b, const Xs& x) {
         if constexpr (TABLE) {
             static_assert(!H16, "the table holds one multiplier and offset per unit");
-            const int h = (wave * BPW / 4) & 1;  // which half of the super-block the wave's units are
             if (lane < NM * 16) {
 #pragma unroll
-                for (int j = 0; j < BPW; j++) my[j * NM * 16 + lane] = hdr_scales<FMT>(x.hdr, h, j);
+                for (int j = 0; j < BPW; j++) {
+                    const int u8 = (wave * BPW + j) & 7;  // the unit's place in its super-block
+                    my[j * NM * 16 + lane] = hdr_scales<FMT>(x.hdr, u8 >> 2, u8 & 3);
+                }
             }
             wave_lds_sync();
         }
-        // The offset terms b gs of the wave's 4 units are a 16 x 16 x 4 product (tokens x units . units x rows):
+        // The offset terms b gs of the wave's units are a 16 x 16 x 4 product (tokens x units . units x rows):
         // one f32 matrix-core instruction per matrix, accumulated over the stages in acc_off; lane (r, g)
         // supplies token r's q8 sum of unit g and row r's offset of unit g. (Q6_K's offsets, one per 16-value
         // half, are added with its products.)
         if constexpr (OFF) {
-            const float4 xo = xsc[b][wave * BPW + g][r];
+            // (with two units per wave, lane groups 2 and 3 supply zeros for the instruction's other two)
+            const int gu = g < BPW ? g : 0;
+            const float4 xo = xsc[b][wave * BPW + gu][r];
+            const float xg = g < BPW ? xo.y + xo.z : 0.0f;
 #pragma unroll
             for (int m = 0; m < NM; m++) {
                 float4 so;
                 if constexpr (TABLE) {
-                    const float2 s2 = my[g * NM * 16 + m * 16 + r];
+                    const float2 s2 = my[gu * NM * 16 + m * 16 + r];
                     so = make_float4(s2.x, s2.x, s2.y, s2.y);
                 } else {
-                    so = i8_scales<FMT>(rowp(b, m, r), wave * BPW + g);
+                    so = i8_scales<FMT>(rowp(b, m, r), wave * BPW + gu);
                 }
-                acc_off[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(xo.y + xo.z, so.z, acc_off[m], 0, 0, 0);
+                acc_off[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(xg, so.z, acc_off[m], 0, 0, 0);
             }
         }
 #pragma unroll
@@ -927,7 +942,7 @@ static int i8_tt(const I8Args& a, int tt, hipStream_t st)
     }
 }
 
-// Tokens from which the integer-dot matvec takes the matrix cores, when K is a multiple of 1024 (whole
+// Tokens from which the integer-dot matvec takes the matrix cores, when K is a multiple of the stage (whole
 // stages): 5 (measured on MI355X, [14336, 4096] gate/up pairs: at 4 tokens the VALU kernel's one 4-token pass
 // is level with the matrix cores or ahead for every format, from 5 it takes an 8-token pass and falls 1.6-1.9x
 // behind); SLHIP_MATVEC_I8_MFMA_MIN_T overrides it (0 disables).
@@ -946,10 +961,11 @@ template <int FMT>
 int run_i8_mfma(I8Args a, bool dual, hipStream_t st)
 {
     const dim3 grid(static_cast<unsigned>((a.N + 15) / 16));
+    constexpr int SU = I8Stage<FMT>::SU;
     for (int64_t t0 = 0; t0 < a.T; t0 += 16) {
         a.t0 = t0;
-        if (dual) matvec_i8_mfma<FMT, true><<<grid, 64 * kI8MfWaves, 0, st>>>(a);
-        else matvec_i8_mfma<FMT, false><<<grid, 64 * kI8MfWaves, 0, st>>>(a);
+        if (dual) matvec_i8_mfma<FMT, true, SU><<<grid, 64 * kI8MfWaves, 0, st>>>(a);
+        else matvec_i8_mfma<FMT, false, SU><<<grid, 64 * kI8MfWaves, 0, st>>>(a);
         const int r = check_launch("matvec_i8_mfma");
         if (r != SLHIP_OK) return r;
     }
@@ -960,7 +976,7 @@ template <int FMT>
 int run_i8(I8Args a, bool dual, hipStream_t st)
 {
     const int mt = i8_mfma_min_tokens<FMT>();
-    if (mt > 0 && a.T >= mt && a.K % 1024 == 0 && a.wrow % I8Stage<FMT>::UB == 0 && a.N * a.wrow < (int64_t{1} << 31))
+    if (mt > 0 && a.T >= mt && a.K % (32 * I8Stage<FMT>::SU) == 0 && a.wrow % I8Stage<FMT>::UB == 0 && a.N * a.wrow < (int64_t{1} << 31))
         return run_i8_mfma<FMT>(a, dual, st);
     if constexpr (kRegPieceKernel<FMT>)
         if (i8_reg_takes<FMT>(a)) return dual ? run_i8_reg<FMT, true>(a, st) : run_i8_reg<FMT, false>(a, st);

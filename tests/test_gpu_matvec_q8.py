@@ -165,6 +165,7 @@ SINGLE_CASES = [  # (fmt, x dtype, y dtype, T, K, N)
     ("q4_k", "f32", "bf16", 3, 14336, 21),
     ("q5_k", "f32", "f32", 1, 14336, 19),
     ("q6_k", "f32", "bf16", 4, 256, 700),    # one slice group, many rows per wave
+    ("q8_0", "f32", "f32", 6, 1536, 33),     # Q8_0's 512-value stages: three of them (K not a multiple of 1024)
 ]
 
 
