@@ -513,6 +513,170 @@ __global__ __launch_bounds__(1024) void rownorm_rows(RowNormArgs a, int wpr)
     }
 }
 
+// Two-byte rows without a residual or copies, persistent: a block is one row group of wpr waves that keeps
+// its lanes' weight and bias vectors in registers for the whole launch (read from L2 once per block, where
+// rownorm_rows reads them per row pair) and walks row pairs b, b + B, ... (B blocks, each with the same
+// count `per`); the next pair's rows are loaded before the current pair is reduced and stored. The
+// arithmetic per row is rownorm_rows's.
+template <int DTI, int DTO, int NV>
+__global__ __launch_bounds__(1024) void rownorm_rows_p(RowNormArgs a, int wpr, int64_t per)
+{
+    using VI = Vec<DTI>;
+    using RV = RawVec<16>;
+    static_assert(VI::BYTES == 2, "rows of 2-byte values");
+    constexpr int E = 16 / VI::BYTES;
+    constexpr int R = 2;
+    __shared__ float red[2][16 * R];  // one region per reduction
+
+    const int lane = threadIdx.x & 63;
+    const int wave = wave_id();
+    const int t = wave * 64 + lane;
+    const int tpr = 64 * wpr;
+    const int nvec = static_cast<int>(a.D / E);
+    int jv[NV];
+    bool own[NV];
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        const int j = t + k * tpr;
+        own[k] = j < nvec;
+        jv[k] = own[k] ? j : nvec - 1;
+    }
+    const bool has_w = a.w != nullptr, has_b = a.b != nullptr;
+    float w[NV][E], b[NV][E];
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+#pragma unroll
+        for (int q4 = 0; q4 < E / 4; q4++) {
+            const float4 w4 = has_w ? reinterpret_cast<const float4*>(a.w + static_cast<int64_t>(jv[k]) * E)[q4] : make_float4(1.f, 1.f, 1.f, 1.f);
+            const float4 b4 = has_b ? reinterpret_cast<const float4*>(a.b + static_cast<int64_t>(jv[k]) * E)[q4] : make_float4(0.f, 0.f, 0.f, 0.f);
+            w[k][4 * q4 + 0] = w4.x;
+            w[k][4 * q4 + 1] = w4.y;
+            w[k][4 * q4 + 2] = w4.z;
+            w[k][4 * q4 + 3] = w4.w;
+            b[k][4 * q4 + 0] = b4.x;
+            b[k][4 * q4 + 1] = b4.y;
+            b[k][4 * q4 + 2] = b4.z;
+            b[k][4 * q4 + 3] = b4.w;
+        }
+    }
+    const int64_t B = gridDim.x;
+    const float inv_d = 1.0f / static_cast<float>(a.D);
+    // rows past the last are loaded as the last row and not stored
+    auto clamp_row = [&](int64_t r) { return r < a.rows ? r : a.rows - 1; };
+    auto load_pair = [&](RV::T (&raw)[R][NV], int64_t pair) {
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            const char* xr = static_cast<const char*>(a.x) + clamp_row(pair * R + i) * a.xs * VI::BYTES;
+#pragma unroll
+            for (int k = 0; k < NV; k++) raw[i][k] = RV::load(xr + static_cast<int64_t>(jv[k]) * 16);
+        }
+    };
+    auto process = [&](RV::T (&raw)[R][NV], int64_t pair) {
+        auto launder = [&]() {
+#pragma unroll
+            for (int i = 0; i < R; i++)
+#pragma unroll
+                for (int k = 0; k < NV; k++) RV::launder(raw[i][k]);
+        };
+        float mean[R], scale[R];
+        if (a.kind == SLHIP_NORM_LAYER) {
+            float s[R];
+#pragma unroll
+            for (int i = 0; i < R; i++) {
+                s[i] = 0.f;
+#pragma unroll
+                for (int k = 0; k < NV; k++) {
+                    float v[E];
+                    RV::template unpack<DTI>(raw[i][k], v);
+#pragma unroll
+                    for (int e = 0; e < E; e++) s[i] += own[k] ? v[e] : 0.0f;
+                }
+            }
+            group_reduce_rows<R>(s, wpr, 0, wave, red[0]);
+            launder();
+            float q[R];
+#pragma unroll
+            for (int i = 0; i < R; i++) {
+                mean[i] = s[i] * inv_d;
+                q[i] = 0.f;
+#pragma unroll
+                for (int k = 0; k < NV; k++) {
+                    float v[E];
+                    RV::template unpack<DTI>(raw[i][k], v);
+#pragma unroll
+                    for (int e = 0; e < E; e++) {
+                        const float d = own[k] ? v[e] - mean[i] : 0.0f;
+                        q[i] = fmaf(d, d, q[i]);
+                    }
+                }
+            }
+            group_reduce_rows<R>(q, wpr, 0, wave, red[1]);
+#pragma unroll
+            for (int i = 0; i < R; i++) scale[i] = 1.0f / sqrtf(q[i] * inv_d + a.eps);
+        } else {
+            float q[R];
+#pragma unroll
+            for (int i = 0; i < R; i++) {
+                mean[i] = 0.f;
+                q[i] = 0.f;
+#pragma unroll
+                for (int k = 0; k < NV; k++) {
+                    float v[E];
+                    RV::template unpack<DTI>(raw[i][k], v);
+#pragma unroll
+                    for (int e = 0; e < E; e++) {
+                        const float x = own[k] ? v[e] : 0.0f;
+                        q[i] = fmaf(x, x, q[i]);
+                    }
+                }
+            }
+            group_reduce_rows<R>(q, wpr, 0, wave, red[1]);
+#pragma unroll
+            for (int i = 0; i < R; i++)
+                scale[i] = a.kind == SLHIP_NORM_RMS ? 1.0f / sqrtf(q[i] * inv_d + a.eps) : 1.0f / sqrtf(q[i] + a.eps);
+        }
+        launder();
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            const int64_t r = pair * R + i;
+            if (r >= a.rows) break;  // block-uniform
+#pragma unroll
+            for (int k = 0; k < NV; k++) {
+                float v[E], o[E];
+                RV::template unpack<DTI>(raw[i][k], v);
+                if (a.kind == SLHIP_NORM_LAYER) {
+#pragma unroll
+                    for (int e = 0; e < E; e++) o[e] = (v[e] - mean[i]) * scale[i];
+                } else {
+#pragma unroll
+                    for (int e = 0; e < E; e++) o[e] = v[e] * scale[i];
+                }
+                if (has_w) {
+#pragma unroll
+                    for (int e = 0; e < E; e++) o[e] *= w[k][e];
+                }
+                if (has_b) {
+#pragma unroll
+                    for (int e = 0; e < E; e++) o[e] += b[k][e];
+                }
+                char* yr = static_cast<char*>(a.y) + r * a.ys * Vec<DTO>::BYTES;
+                store_packed<DTO, E>(yr + static_cast<int64_t>(jv[k]) * E * Vec<DTO>::BYTES, o);
+            }
+        }
+    };
+    RV::T A[R][NV], C[R][NV];
+    int64_t pair = blockIdx.x;
+    load_pair(A, pair);
+    for (int64_t it = 0; it < per; it += 2) {  // two pairs per pass: the register sets alternate statically
+        if (it + 1 < per) load_pair(C, pair + B);
+        process(A, pair);
+        if (it + 1 >= per) break;
+        if (it + 2 < per) load_pair(A, pair + 2 * B);
+        process(C, pair + B);
+        pair += 2 * B;
+    }
+}
+
 // Scalar fallback: one 256-thread block per row, re-reading the row from global memory (cache-resident)
 // for each pass.
 template <int DTI, int DTO>
@@ -635,6 +799,33 @@ static int launch_rows(const RowNormArgs& a, int nv, int wpr, hipStream_t st)
     return check_launch("rownorm_rows");
 }
 
+template <int DTI, int DTO>
+static int launch_rows_p(const RowNormArgs& a, int64_t nvec, hipStream_t st)
+{
+    // the smallest row group whose lanes hold at most two vectors, then one block per group
+    int wpr = 1;
+    while (wpr < 16 && nvec > static_cast<int64_t>(2) * 64 * wpr) wpr *= 2;
+    const int nv = static_cast<int>((nvec + 64 * wpr - 1) / (64 * wpr));
+    const void* k = nv == 1 ? reinterpret_cast<const void*>(rownorm_rows_p<DTI, DTO, 1>)
+                            : reinterpret_cast<const void*>(rownorm_rows_p<DTI, DTO, 2>);
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, 64 * wpr, 0) != hipSuccess || per_cu < 1) per_cu = 1;
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            cus <= 0)
+            cus = 256;
+    }
+    const int64_t pairs = (a.rows + 1) / 2;
+    const int64_t resident = static_cast<int64_t>(cus) * per_cu;
+    const int64_t per = (pairs + resident - 1) / resident;
+    const dim3 grid(static_cast<unsigned>((pairs + per - 1) / per));
+    if (nv == 1) rownorm_rows_p<DTI, DTO, 1><<<grid, 64 * wpr, 0, st>>>(a, wpr, per);
+    else rownorm_rows_p<DTI, DTO, 2><<<grid, 64 * wpr, 0, st>>>(a, wpr, per);
+    return check_launch("rownorm_rows_p");
+}
+
 static bool aligned_to(const void* p, int n) { return reinterpret_cast<uintptr_t>(p) % n == 0; }
 
 // Whether the rows fit the vector kernel with VB-byte input vectors: D a multiple of the vector's values,
@@ -674,10 +865,15 @@ static int launch_fitting(const RowNormArgs& a, hipStream_t st)
     int64_t per = (nvec + 64 * wpr - 1) / (64 * wpr);
     int nv = per == 7 ? 8 : static_cast<int>(per);
     if constexpr (VB == 16 && Vec<DTI>::BYTES == 2) {
-        // two-byte rows without a residual or copies: R rows per row group (SLHIP_ROWNORM_ROWS, 1 or 2), up to
-        // 4 vectors per lane (beyond that two rows' registers spill at 1024-thread blocks)
-        const int r = env_int("SLHIP_ROWNORM_ROWS", 2);
-        if (!a.res && !a.yq && !a.y16 && a.y && r == 2 && nv <= 4) return launch_rows<DTI, DTO, 2>(a, nv, wpr, st);
+        // two-byte rows without a residual or copies (SLHIP_ROWNORM_ROWS): 3 (default), RMS and L2 rows up to
+        // 16384 values on persistent row groups holding their weight (bf16 [8192, 4096] RMSNorm 26.2 -> 25.5 us;
+        // LayerNorm measured slower so, 27.9 -> 29.5: two block barriers per row pair on 4-wave groups, and
+        // the bias's registers cost a wave per SIMD); 2 (and LayerNorm), two rows per row group up to 4 vectors
+        // per lane (beyond that two rows' registers spill at 1024-thread blocks); 1, rownorm_vec
+        const int r = env_int("SLHIP_ROWNORM_ROWS", 3);
+        if (!a.res && !a.yq && !a.y16 && a.y && r == 3 && a.kind != SLHIP_NORM_LAYER && nvec <= 2 * 64 * 16)
+            return launch_rows_p<DTI, DTO>(a, nvec, st);
+        if (!a.res && !a.yq && !a.y16 && a.y && r >= 2 && nv <= 4) return launch_rows<DTI, DTO, 2>(a, nv, wpr, st);
     }
     if constexpr (VB == 16) {
         if (a.yq)

@@ -224,3 +224,21 @@ def test_rownorm_forced_row_groups(device, monkeypatch):
         y, h = _run("rms", "bf16", "bf16", x, r, w, None, 1e-5, with_res=True, with_h=True)
         assert_bf16_close(y, yref, what=f"wpr={wpr}")
         assert_bf16_close(h, href, ulp=0, what=f"h wpr={wpr}")
+
+
+@pytest.mark.parametrize("kind,rows,D,with_w", [
+    ("rms", 1, 4096, True),        # one row pair, half empty
+    ("rms", 1001, 4096, True),     # many pairs per persistent group, an odd last row
+    ("rms", 3000, 64, True),       # one-wave groups, one vector per lane
+    ("rms", 37, 16384, True),      # 16-wave groups, two vectors per lane
+    ("rms", 9, 8200, False),       # 1025 vectors: the last lane of the group holds a second, partial vector set
+    ("l2", 515, 2048, False),
+])
+def test_rownorm_persistent_rows(device, kind, rows, D, with_w):
+    """bf16 RMS / L2 rows without a residual on the persistent row groups (weights held for the launch,
+    row pairs walked with the next pair in flight)."""
+    x, r, w, _ = _inputs(rows, D, "bf16", seed=rows * 7 + D, scale=2.0)
+    w = w if with_w else None
+    y, _ = _run(kind, "bf16", "bf16", x, r, w, None, 1e-6, with_res=False, with_h=False)
+    yref, _, _ = _reference(kind, "bf16", "bf16", x, r, w, None, 1e-6, False)
+    assert_bf16_close(y, yref, what=f"persistent {kind} [{rows},{D}] w={with_w}")
