@@ -523,7 +523,7 @@ WORKLOADS = {
     "dual_matvec_silu_q3_k_T16": lambda: DualMatvec(16, "q3_k"),
     **{f"dual_matvec_int8_silu_{f}_T{t}": (lambda f=f, t=t: DualMatvecQ8(t, f))
        for f, t in (("q4_k", 1), ("q6_k", 1), ("q4_0", 1), ("q8_0", 2), ("q5_k", 1), ("iq4_nl", 1), ("mxfp4", 1),
-                    ("q4_k", 4), ("q4_k", 8), ("q6_k", 8), ("q8_0", 16), ("q4_k", 16), ("q6_k", 16),
+                    ("q4_k", 4), ("q6_k", 4), ("iq4_xs", 1), ("q4_k", 8), ("q6_k", 8), ("q8_0", 16), ("q4_k", 16), ("q6_k", 16),
                     ("q4_0", 16))},
     "copy_256MiB": lambda: CopyRef(),
 }
