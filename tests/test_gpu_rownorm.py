@@ -242,3 +242,19 @@ def test_rownorm_persistent_rows(device, kind, rows, D, with_w):
     y, _ = _run(kind, "bf16", "bf16", x, r, w, None, 1e-6, with_res=False, with_h=False)
     yref, _, _ = _reference(kind, "bf16", "bf16", x, r, w, None, 1e-6, False)
     assert_bf16_close(y, yref, what=f"persistent {kind} [{rows},{D}] w={with_w}")
+
+
+@pytest.mark.parametrize("rows,D,offset", [
+    (33, 3000, 0.0),    # 375 vectors over two waves: lanes own 2 or 3 of them
+    (17, 520, 0.0),     # 65 vectors on one wave: lane 0 owns two, the rest one
+    (64, 4096, 300.0),  # rows whose mean (300) dwarfs their spread (~1): the variance must not cancel
+    (9, 4096, -2000.0),
+])
+def test_layernorm_rows_one_exchange(device, rows, D, offset):
+    """bf16 LayerNorm rows without a residual (two rows per row group, mean and variance combined across the
+    group's waves in one exchange), against the oracle's two-pass LayerNorm."""
+    x, r, w, b = _inputs(rows, D, "f32", seed=rows * 13 + D)
+    xb = oracle.to_bf16((x + np.float32(offset)).astype(np.float32))
+    y, _ = _run("layer", "bf16", "bf16", xb, r, w, b, 1e-5, with_res=False, with_h=False)
+    yref, _, _ = _reference("layer", "bf16", "bf16", xb, r, w, b, 1e-5, False)
+    assert_bf16_close(y, yref, what=f"layernorm rows [{rows},{D}] offset={offset}")
