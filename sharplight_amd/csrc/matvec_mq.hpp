@@ -96,17 +96,26 @@ constexpr int mq2_blocks()
     return XF32 && MqGeom<FMT>::SKB == 32 ? 16 : MqGeom<FMT>::SKB;
 }
 
-template <int FMT, bool DUAL, bool XF32>
-__global__ __launch_bounds__(64 * kMq2Waves) void matvec_mq2(MatvecArgs a)
+// 16-row tiles per block with f32 x: two for the 32-value block formats, so that each block splits x into
+// its three bf16 parts (and reads it) once for 32 rows -- [14336, 4096] pairs at 16 tokens, µs: Q4_0 51 -> 40,
+// Q8_0 56 -> 45, Q4_1 52 -> 37, Q5_0 59 -> 51, Q5_1 55 -> 46; one for the K-quants, whose extra decode state
+// then spills (Q4_K 52 -> 55, Q6_K 70 -> 102).
+template <int FMT>
+constexpr int kMq2Tiles = (FMT == SLHIP_FMT_Q8_0 || FMT == SLHIP_FMT_Q4_0 || FMT == SLHIP_FMT_Q4_1 || FMT == SLHIP_FMT_Q5_0 ||
+                           FMT == SLHIP_FMT_Q5_1) ? 2 : 1;
+
+template <int FMT, bool DUAL, bool XF32, int TN>
+__global__ __launch_bounds__(64 * kMq2Waves) __attribute__((amdgpu_waves_per_eu(TN == 2 ? 4 : 1))) void matvec_mq2(MatvecArgs a)
 {
     constexpr int NM = DUAL ? 2 : 1;
+    constexpr int G = NM * TN;  // row groups: 16 rows of one matrix; group q = tile (q / NM), matrix (q % NM)
     constexpr int SKB = mq2_blocks<FMT, XF32>();
     constexpr int RB = MqGeom<FMT>::RB * SKB / MqGeom<FMT>::SKB;
     constexpr int UB = RB % 16 == 0 ? 16 : 4;  // bytes per staging load (global_load_lds: 16 or 4)
     constexpr int PITCH = stage_pitch(RB, UB);
     constexpr int SPR = PITCH / UB;
     constexpr int MS = (16 * SPR + 63) / 64 * 64;  // slots per matrix: whole waves
-    constexpr int SLOTS = NM * MS;
+    constexpr int SLOTS = G * MS;
     constexpr int NT = 64 * kMq2Waves;
     constexpr int LPT = (SLOTS + NT - 1) / NT;
     constexpr int BPW = SKB / kMq2Waves;  // blocks per wave and stage
@@ -119,7 +128,7 @@ __global__ __launch_bounds__(64 * kMq2Waves) void matvec_mq2(MatvecArgs a)
     static_assert(RB % UB == 0 && SKB % kMq2Waves == 0, "stage shape");
     static_assert(!MIN || BPW <= 4, "the minimum terms take the wave's blocks as one 16 x 16 x 4 product");
     // per buffer: the stage, and at least half the cross-wave reduction's [wave][matrix][lane] sums
-    constexpr int RED_WORDS = kMq2Waves * NM * 64 * 4 / 2;
+    constexpr int RED_WORDS = kMq2Waves * G * 64 * 4 / 2;
     constexpr int STW = SLOTS * UB / 4 > RED_WORDS ? SLOTS * UB / 4 : RED_WORDS;
     __shared__ __align__(16) uint32_t stage[2][STW];
     auto rowp = [&](int b, int m, int rr) -> const uint8_t* {
@@ -128,7 +137,7 @@ __global__ __launch_bounds__(64 * kMq2Waves) void matvec_mq2(MatvecArgs a)
     const int lane = threadIdx.x & 63;
     const int wave = wave_id();
     const int r = lane & 15, g = lane >> 4;
-    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 16;
+    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 16 * TN;
     int64_t tok = a.t0 + r;
     tok = tok < a.T ? tok : a.T - 1;
     const int ns = static_cast<int>(a.K / (SKB * 32));
@@ -146,7 +155,7 @@ __global__ __launch_bounds__(64 * kMq2Waves) void matvec_mq2(MatvecArgs a)
             c = 0;
         }
         c = c < RB / UB ? c : RB / UB - 1;
-        int64_t row = n0 + rr;
+        int64_t row = n0 + 16 * (m / NM) + rr;
         row = row < a.N ? row : a.N - 1;
         src[i] = static_cast<uint32_t>(row * a.wrow + UB * c);
     }
@@ -156,7 +165,7 @@ __global__ __launch_bounds__(64 * kMq2Waves) void matvec_mq2(MatvecArgs a)
             if (NT * i + 64 * wave >= SLOTS) break;  // wave-uniform
             if (NT * (i + 1) > SLOTS && static_cast<int>(threadIdx.x) + NT * i >= SLOTS) continue;
             char* base = reinterpret_cast<char*>(&stage[b][0]) + UB * (NT * i + 64 * wave);
-            const char* mat = ((NT * i + 64 * wave) / MS ? a.wu : a.wg) + static_cast<int64_t>(s) * RB;
+            const char* mat = (((NT * i + 64 * wave) / MS) % NM ? a.wu : a.wg) + static_cast<int64_t>(s) * RB;
             load_to_lds<UB>(mat, src[i], base);
         }
     };
@@ -178,14 +187,14 @@ __global__ __launch_bounds__(64 * kMq2Waves) void matvec_mq2(MatvecArgs a)
             }
         }
     };
-    f32x4_t acc[NM];
+    f32x4_t acc[G];
 #pragma unroll
-    for (int m = 0; m < NM; m++) acc[m] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int m = 0; m < G; m++) acc[m] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
     auto compute = [&](int b, const Xs& x) {
         const int sbo = (KQ || K6) ? ((wave * BPW) >> 3) * SBB : 0;
         float xs0[BPW], xs1[BPW];  // the token's x sums of each block (Q2_K: of each half)
-        float mn0[NM][BPW], mn1[NM][BPW];  // the row's minimum coefficients of each block
+        float mn0[G][BPW], mn1[G][BPW];  // the row's minimum coefficients of each block
 #pragma unroll
         for (int j = 0; j < BPW; j++) {
             const int blk = wave * BPW + j;
@@ -221,7 +230,7 @@ __global__ __launch_bounds__(64 * kMq2Waves) void matvec_mq2(MatvecArgs a)
                 }
             }
 #pragma unroll
-            for (int m = 0; m < NM; m++) {
+            for (int m = 0; m < G; m++) {
                 const uint8_t* rw = rowp(b, m, r);
                 const uint4 C = mq2_codes<FMT>(rw, sbo, sj, off, g);
                 float a0, a1, m0, m1;
@@ -265,7 +274,7 @@ __global__ __launch_bounds__(64 * kMq2Waves) void matvec_mq2(MatvecArgs a)
             };
             const float xa = pick(xs0);
 #pragma unroll
-            for (int m = 0; m < NM; m++) {
+            for (int m = 0; m < G; m++) {
                 acc[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa, pick(mn0[m]), acc[m], 0, 0, 0);
                 if constexpr (Q2K) acc[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(pick(xs1), pick(mn1[m]), acc[m], 0, 0, 0);
             }
@@ -295,20 +304,22 @@ __global__ __launch_bounds__(64 * kMq2Waves) void matvec_mq2(MatvecArgs a)
         __builtin_amdgcn_s_waitcnt(kWaitLoads);
         __syncthreads();
     }
-    // the waves' partial sums meet in the (now idle) stage memory: [wave][matrix][lane]
+    // the waves' partial sums meet in the (now idle) stage memory: [wave][group][lane]
     f32x4_t* red = reinterpret_cast<f32x4_t*>(&stage[0][0]);
 #pragma unroll
-    for (int m = 0; m < NM; m++) red[(wave * NM + m) * 64 + lane] = acc[m];
+    for (int m = 0; m < G; m++) red[(wave * G + m) * 64 + lane] = acc[m];
     __syncthreads();
-    if (wave != 0) return;
-    f32x4_t sg = red[lane], su = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    if (DUAL) su = red[64 + lane];
+    if (wave >= TN) return;
+    // wave tl finishes tile tl: row n0 + 16 tl + r, tokens 4g + i
+    const int tl = wave;
+    f32x4_t sg = red[(tl * NM) * 64 + lane], su = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    if (DUAL) su = red[(tl * NM + 1) * 64 + lane];
 #pragma unroll
     for (int w = 1; w < kMq2Waves; w++) {
-        sg += red[(w * NM) * 64 + lane];
-        if (DUAL) su += red[(w * NM + 1) * 64 + lane];
+        sg += red[(w * G + tl * NM) * 64 + lane];
+        if (DUAL) su += red[(w * G + tl * NM + 1) * 64 + lane];
     }
-    const int64_t n = n0 + r;  // lane: row r, tokens 4g + i
+    const int64_t n = n0 + 16 * tl + r;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int64_t t = a.t0 + 4 * g + i;
@@ -347,15 +358,16 @@ inline bool mq2_fits(const MatvecArgs& a)
 template <int FMT>
 int run_mq2(MatvecArgs a, bool dual, hipStream_t st)
 {
-    const dim3 grid(static_cast<unsigned>((a.N + 15) / 16));
+    constexpr int TN = kMq2Tiles<FMT>;
+    const dim3 grid1(static_cast<unsigned>((a.N + 15) / 16)), gridx(static_cast<unsigned>((a.N + 16 * TN - 1) / (16 * TN)));
     for (int64_t t0 = 0; t0 < a.T; t0 += 16) {
         a.t0 = t0;
         if (a.xt == SLHIP_F32) {
-            if (dual) matvec_mq2<FMT, true, true><<<grid, 64 * kMq2Waves, 0, st>>>(a);
-            else matvec_mq2<FMT, false, true><<<grid, 64 * kMq2Waves, 0, st>>>(a);
+            if (dual) matvec_mq2<FMT, true, true, TN><<<gridx, 64 * kMq2Waves, 0, st>>>(a);
+            else matvec_mq2<FMT, false, true, TN><<<gridx, 64 * kMq2Waves, 0, st>>>(a);
         } else {
-            if (dual) matvec_mq2<FMT, true, false><<<grid, 64 * kMq2Waves, 0, st>>>(a);
-            else matvec_mq2<FMT, false, false><<<grid, 64 * kMq2Waves, 0, st>>>(a);
+            if (dual) matvec_mq2<FMT, true, false, 1><<<grid1, 64 * kMq2Waves, 0, st>>>(a);
+            else matvec_mq2<FMT, false, false, 1><<<grid1, 64 * kMq2Waves, 0, st>>>(a);
         }
         const int r = check_launch("matvec_mq2");
         if (r != SLHIP_OK) return r;
