@@ -904,8 +904,8 @@ static int launch_i8_reg(const I8Args& a, hipStream_t st)
     return check_launch("matvec_i8_reg");
 }
 
-// Whether the register-piece kernel takes T tokens: for its formats at one to four tokens with K a multiple of
-// 64 (SLHIP_MATVEC_I8_REG=0 turns it off).
+// Whether the register-piece kernel takes T tokens: for its formats at kRegPieceMinT to four tokens with K a
+// multiple of 64 (SLHIP_MATVEC_I8_REG=0 turns it off).
 template <int FMT>
 inline bool i8_reg_takes(const I8Args& a)
 {
@@ -914,7 +914,7 @@ inline bool i8_reg_takes(const I8Args& a)
         const char* e = getenv("SLHIP_MATVEC_I8_REG");
         v = e ? atoi(e) : 1;
     }
-    return v != 0 && kRegPieceKernel<FMT> && a.T <= 4 && a.K % 64 == 0 && 4 * (a.K + a.K / 2) <= static_cast<int64_t>(kI8MaxLds);
+    return v != 0 && kRegPieceKernel<FMT> && a.T >= kRegPieceMinT<FMT> && a.T <= 4 && a.K % 64 == 0 && 4 * (a.K + a.K / 2) <= static_cast<int64_t>(kI8MaxLds);
 }
 
 template <int FMT, bool DUAL>

@@ -4,9 +4,10 @@
 // A slice is two 32-value units of a row together with the bytes of their block or super-block scales;
 // RegPiece<FMT> decodes a slice from a few 16-byte words into two I8Units (codes, multipliers, offsets), so
 // that each lane decodes only its own scales, with word-wide arithmetic.
-//   * Q4_K / Q5_K: the LDS-staged kernel (matvec_i8) reads each lane's slice out of the row images as aligned
-//     16-byte words (lds_load).
-//   * Q6_K / IQ4_XS: the register-piece kernel below loads each lane's slice from HBM straight into
+//   * Q4_K / Q5_K (and Q6_K below three tokens, IQ4_XS in passes of more than four): the LDS-staged kernel
+//     (matvec_i8) reads each lane's slice out of the row images as words (lds_load): aligned 16- or 8-byte
+//     reads, or for Q6_K's 2-byte aligned super-blocks aligned words joined by funnel shifts.
+//   * Q6_K from three tokens and IQ4_XS: the register-piece kernel below loads each lane's slice from HBM straight into
 //     registers (unaligned loads: their blocks are only 2- or 8-byte aligned), with no row image in LDS, no
 //     LDS store and no per-chunk address arithmetic. A wave takes rows n, n + W, ... (W waves in the grid,
 //     sized so that each wave gets the same number of rows), one (row, group of 64 slices) item at a time:
@@ -95,6 +96,15 @@ template <> struct RegPiece<SLHIP_FMT_Q5_K> : RegPieceK45<SLHIP_FMT_Q5_K> {};
 
 template <> struct RegPiece<SLHIP_FMT_IQ4_XS> {  // {f16 d, u16 scales_h, u8 scales_l[4], u8 qs[128]}
     static constexpr int NW = 3;
+    // the same words from a row image in LDS (136-byte super-blocks: 8-byte aligned there)
+    static __device__ __forceinline__ void lds_load(uint4* w, const uint32_t* img, int s)
+    {
+        const uint2* b = reinterpret_cast<const uint2*>(img) + 17 * (s >> 2);
+        const uint2 h = b[0], q0 = b[1 + 4 * (s & 3)], q1 = b[2 + 4 * (s & 3)], q2 = b[3 + 4 * (s & 3)], q3 = b[4 + 4 * (s & 3)];
+        w[0] = make_uint4(h.x, h.y, 0u, 0u);
+        w[1] = make_uint4(q0.x, q0.y, q1.x, q1.y);
+        w[2] = make_uint4(q2.x, q2.y, q3.x, q3.y);
+    }
     static __device__ __forceinline__ void load(uint4* w, const char* row, int s)
     {
         const char* b = row + 136 * (s >> 2);
@@ -131,6 +141,34 @@ template <> struct RegPiece<SLHIP_FMT_Q6_K> {  // {ql[128], qh[64], i8 scales[16
     // slice quarter p: ql[32 p .. + 31] holds quarters qt = p & 1 (low nibbles) and qt + 2 (high nibbles) of
     // half n = p / 2, whose two high bits are in qh[32 n ..]: units 4 n + qt and 4 n + qt + 2 of the super-block
     static constexpr int NW = 5;
+    // the same words from a row image in LDS (210-byte super-blocks: 2-byte aligned there): each run of
+    // words as aligned reads joined by funnel shifts (the last super-block's scales read 2 bytes into the
+    // image's pad)
+    static __device__ __forceinline__ void lds_load(uint4* w, const uint32_t* img, int s)
+    {
+        const int p = s & 3, n = p >> 1;
+        const int o = 210 * (s >> 2);
+        auto run8 = [&](int off, uint4& a, uint4& b) {
+            const uint32_t* q = img + (off >> 2);
+            const uint32_t sh = static_cast<uint32_t>(off & 3) * 8;
+            uint32_t d[9];
+#pragma unroll
+            for (int k = 0; k < 9; k++) d[k] = q[k];
+            a = make_uint4(__builtin_amdgcn_alignbit(d[1], d[0], sh), __builtin_amdgcn_alignbit(d[2], d[1], sh),
+                           __builtin_amdgcn_alignbit(d[3], d[2], sh), __builtin_amdgcn_alignbit(d[4], d[3], sh));
+            b = make_uint4(__builtin_amdgcn_alignbit(d[5], d[4], sh), __builtin_amdgcn_alignbit(d[6], d[5], sh),
+                           __builtin_amdgcn_alignbit(d[7], d[6], sh), __builtin_amdgcn_alignbit(d[8], d[7], sh));
+        };
+        run8(o + 32 * p, w[0], w[1]);
+        run8(o + 128 + 32 * n, w[2], w[3]);
+        const int so = o + 192 + 8 * n;
+        const uint32_t* q = img + (so >> 2);
+        const uint32_t sh = static_cast<uint32_t>(so & 3) * 8;
+        const uint32_t e0 = q[0], e1 = q[1], e2 = q[2];
+        w[4].x = __builtin_amdgcn_alignbit(e1, e0, sh);
+        w[4].y = __builtin_amdgcn_alignbit(e2, e1, sh);
+        w[4].z = lds_u16(img, o + 208);
+    }
     static __device__ __forceinline__ void load(uint4* w, const char* row, int s)
     {
         const int p = s & 3, n = p >> 1;
@@ -168,13 +206,17 @@ template <> struct RegPiece<SLHIP_FMT_Q6_K> {  // {ql[128], qh[64], i8 scales[16
 };
 
 // Formats whose slices the LDS-staged kernel reads as aligned 16-byte words.
-template <int FMT> constexpr bool kLdsPiece = FMT == SLHIP_FMT_Q4_K || FMT == SLHIP_FMT_Q5_K;
+template <int FMT> constexpr bool kLdsPiece = FMT == SLHIP_FMT_Q4_K || FMT == SLHIP_FMT_Q5_K || FMT == SLHIP_FMT_Q6_K || FMT == SLHIP_FMT_IQ4_XS;
 
-// Formats the register-piece kernel takes (measured against the LDS-staged kernel on [14336, 4096] gate/up
-// pairs at one to four tokens: Q6_K 30.0 / 32.7 / 38.9 us against 30.3 / 35.7 / 49.6, IQ4_XS ~10% ahead; for
+// Formats the register-piece kernel takes (measured against the LDS-staged kernel with per-unit decode on
+// [14336, 4096] gate/up pairs at one to four tokens: Q6_K 30.0 / 32.7 / 38.9 us against 30.3 / 35.7 / 49.6,
+// IQ4_XS ~10% ahead, also against slices read from the row images; for
 // the 32-value block formats the scattered 16-byte pieces cost more L1 accesses than they save, and Q4_K /
 // Q5_K run faster as slices of the LDS row images).
 template <int FMT> constexpr bool kRegPieceKernel = FMT == SLHIP_FMT_Q6_K || FMT == SLHIP_FMT_IQ4_XS;
+// Q6_K below three tokens reads its slices from the LDS row images instead (T1 / T2 29.5 / 32.4 -> 23.4 /
+// 30.3 us; at four tokens the register kernel stays ahead, 38.4 against 39.6).
+template <int FMT> constexpr int kRegPieceMinT = FMT == SLHIP_FMT_Q6_K ? 3 : 1;
 
 constexpr int kI8RegThreads = 256;
 
