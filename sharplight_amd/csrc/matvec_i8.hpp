@@ -739,18 +739,14 @@ __global__ __launch_bounds__(kI8Threads) void matvec_i8(I8Args a)
                 }
             }
         };
-        if constexpr (kLdsPiece<FMT>) {
-            // a 64-value slice per lane, its bytes read from the row images as aligned 16-byte words
+        if (kSliceLds<FMT, TT> && K % 64 == 0) {  // wave-uniform; K-quants always, block formats with an even block count
+            // a 64-value slice per lane, its bytes read from the row images as words
             const int nsl = K / 64;
             auto slice = [&](int sl, bool own) {
-                using P = RegPiece<FMT>;
-                uint4 wg[P::NW], wu[P::NW];
-                P::lds_load(wg, rows, sl);
-                if constexpr (DUAL) P::lds_load(wu, rows + rbw, sl);
                 I8Unit g0, g1, u0, u1;
                 int j0, j1;
-                P::units(wg, sl, g0, g1, j0, j1);
-                if constexpr (DUAL) P::units(wu, sl, u0, u1, j0, j1);
+                slice_units<FMT>(rows, sl, g0, g1, j0, j1);
+                if constexpr (DUAL) slice_units<FMT>(rows + rbw, sl, u0, u1, j0, j1);
 #pragma unroll
                 for (int t = 0; t < TT; t++) {
                     const uint8_t* xt = xs + t * xrow;

@@ -7,8 +7,8 @@
 //   * Q4_K / Q5_K (and Q6_K below three tokens, IQ4_XS in passes of more than four): the LDS-staged kernel
 //     (matvec_i8) reads each lane's slice out of the row images as words (lds_load): aligned 16- or 8-byte
 //     reads, or for Q6_K's 2-byte aligned super-blocks aligned words joined by funnel shifts.
-//   * Q6_K from three tokens and IQ4_XS: the register-piece kernel below loads each lane's slice from HBM straight into
-//     registers (unaligned loads: their blocks are only 2- or 8-byte aligned), with no row image in LDS, no
+//   * Q6_K from three tokens and IQ4_XS: the register-piece kernel below loads each lane's slice from HBM
+//     straight into registers (unaligned loads: their blocks are only 2- or 8-byte aligned), with no row image in LDS, no
 //     LDS store and no per-chunk address arithmetic. A wave takes rows n, n + W, ... (W waves in the grid,
 //     sized so that each wave gets the same number of rows), one (row, group of 64 slices) item at a time:
 //     the next D - 1 items' loads are in flight while one is computed (D register sets in rotation). The
@@ -31,6 +31,100 @@ __device__ __forceinline__ uint32_t word_of(const uint4& v, int k) { return k ==
 // A lane's raw bytes for slice s of a row (NW 16-byte registers), and the two units they hold with the unit
 // index (32-value units from the row's start) of each; field layouts as in i8_unit.
 template <int FMT> struct RegPiece;
+
+// 32-value block formats: slice s is blocks 2 s and 2 s + 1, 2 BB bytes at byte 2 BB s of the row image (4-byte
+// aligned for every format but MXFP4), read as one run of words; the fields sit at fixed byte offsets in it.
+template <int BB>
+struct SliceWords {
+    static constexpr int N = (2 * BB + 3) / 4 + 1;  // words read (one spare for the funnel shifts)
+    uint32_t w[N];
+    // the run starting at byte off of the image (even): aligned reads joined by funnel shifts when off % 4 == 2
+    __device__ __forceinline__ void read(const uint32_t* img, int off)
+    {
+        const uint32_t* q = img + (off >> 2);
+        if (BB % 2 == 0) {  // 2 BB s is a multiple of 4
+#pragma unroll
+            for (int k = 0; k < N; k++) w[k] = q[k];
+        } else {
+            const uint32_t sh = static_cast<uint32_t>(off & 3) * 8;
+            uint32_t d[N + 1];
+#pragma unroll
+            for (int k = 0; k <= N; k++) d[k] = q[k];
+#pragma unroll
+            for (int k = 0; k < N; k++) w[k] = __builtin_amdgcn_alignbit(d[k + 1], d[k], sh);
+        }
+    }
+    // 4 bytes at byte b of the slice (b a compile-time constant)
+    __device__ __forceinline__ uint32_t at(int b) const
+    {
+        return (b & 3) ? __builtin_amdgcn_alignbit(w[(b >> 2) + 1], w[b >> 2], (b & 3) * 8) : w[b >> 2];
+    }
+};
+
+// the codes of one 32-value block from its 16 bytes of nibbles q (and, Q5_x, its 32 fifth bits qh), as i8_unit
+template <int FMT>
+__device__ __forceinline__ void nibble_codes(I8Unit& u, const uint32_t (&q)[4], uint32_t qh)
+{
+    using F = Fmt<FMT>;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        uint32_t lo = q[k] & 0x0F0F0F0Fu, hi = (q[k] >> 4) & 0x0F0F0F0Fu;
+        if constexpr (F::QH >= 0) {
+            lo |= ((((qh >> (4 * k)) & 0xFu) * 0x00204081u) & 0x01010101u) << 4;
+            hi |= ((((qh >> (16 + 4 * k)) & 0xFu) * 0x00204081u) & 0x01010101u) << 4;
+        }
+        if constexpr (FMT == SLHIP_FMT_IQ4_NL) {
+            lo = iq4_lookup4(lo);
+            hi = iq4_lookup4(hi);
+        } else if constexpr (FMT == SLHIP_FMT_MXFP4) {
+            lo = fp4_lookup4(lo);
+            hi = fp4_lookup4(hi);
+        }
+        u.c[k] = lo;
+        u.c[4 + k] = hi;
+    }
+}
+
+template <int FMT> struct SlicePiece32 {
+    static constexpr int BB = FMT == SLHIP_FMT_MXFP4 ? 17 : Fmt<FMT>::BB;
+    using W = SliceWords<BB>;
+    // block h (0, 1) of the slice into u
+    static __device__ __forceinline__ void block(const W& sw, int h, I8Unit& u)
+    {
+        const int o = h * BB;
+        if constexpr (FMT == SLHIP_FMT_Q8_0) {
+            u.a0 = u.a1 = f16_lo(sw.at(o));
+            u.b0 = u.b1 = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 8; k++) u.c[k] = sw.at(o + 2 + 4 * k);
+        } else if constexpr (FMT == SLHIP_FMT_MXFP4) {
+            u.a0 = u.a1 = e8m0_half(sw.at(o) & 0xFFu);
+            u.b0 = u.b1 = 0.0f;
+            const uint32_t q[4] = {sw.at(o + 1), sw.at(o + 5), sw.at(o + 9), sw.at(o + 13)};
+            nibble_codes<FMT>(u, q, 0);
+        } else {
+            using F = Fmt<FMT>;
+            const uint32_t h0 = sw.at(o);
+            const float d = f16_lo(h0);
+            u.a0 = u.a1 = d;
+            if constexpr (FMT == SLHIP_FMT_IQ4_NL) u.b0 = u.b1 = 0.0f;
+            else if constexpr (F::M) u.b0 = u.b1 = f16_hi(h0);
+            else u.b0 = u.b1 = static_cast<float>(F::OFF) * d;
+            const uint32_t qh = F::QH >= 0 ? sw.at(o + (F::QH >= 0 ? F::QH : 0)) : 0u;
+            const uint32_t q[4] = {sw.at(o + F::QS), sw.at(o + F::QS + 4), sw.at(o + F::QS + 8), sw.at(o + F::QS + 12)};
+            nibble_codes<FMT>(u, q, qh);
+        }
+    }
+    static __device__ __forceinline__ void lds_units(const uint32_t* img, int s, I8Unit& u0, I8Unit& u1, int& j0, int& j1)
+    {
+        W sw;
+        sw.read(img, 2 * BB * s);
+        block(sw, 0, u0);
+        block(sw, 1, u1);
+        j0 = 2 * s;
+        j1 = j0 + 1;
+    }
+};
 
 // Q4_K / Q5_K sub-blocks jj, jj + 1 (jj = 2 (p & 1), p = the slice's quarter of its super-block) of the 6-bit
 // scales and minimums from the header words (scales[0..3], [4..7], [8..11]): two bytes at a time.
@@ -207,6 +301,29 @@ template <> struct RegPiece<SLHIP_FMT_Q6_K> {  // {ql[128], qh[64], i8 scales[16
 
 // Formats whose slices the LDS-staged kernel reads as aligned 16-byte words.
 template <int FMT> constexpr bool kLdsPiece = FMT == SLHIP_FMT_Q4_K || FMT == SLHIP_FMT_Q5_K || FMT == SLHIP_FMT_Q6_K || FMT == SLHIP_FMT_IQ4_XS;
+// The 32-value block formats by slices in passes of TT tokens: where it measured ahead of the per-unit decode on
+// [14336, 4096] gate/up pairs (µs, slices against units: T1 Q4_0 16.5 / 17.8, Q8_0 25.5 / 29.2, Q5_0 19.1 /
+// 21.1, IQ4_NL 20.1 / 21.8, MXFP4 21.0 / 21.8; T4 Q8_0 39.2 / 44.8). Elsewhere the slices' registers (~140-160
+// against ~120) cost more than the reads they save (Q4_1, Q5_1 at one token; most formats at two or four).
+template <int FMT, int TT>
+constexpr bool kSlice32 = (TT == 1 && (FMT == SLHIP_FMT_Q8_0 || FMT == SLHIP_FMT_Q4_0 || FMT == SLHIP_FMT_Q5_0 ||
+                                       FMT == SLHIP_FMT_IQ4_NL || FMT == SLHIP_FMT_MXFP4)) ||
+                          (TT == 4 && FMT == SLHIP_FMT_Q8_0);
+// Formats whose LDS-staged decode goes by 64-value slices.
+template <int FMT, int TT> constexpr bool kSliceLds = kLdsPiece<FMT> || kSlice32<FMT, TT>;
+
+// A slice's two units from a row image in LDS.
+template <int FMT>
+__device__ __forceinline__ void slice_units(const uint32_t* img, int s, I8Unit& u0, I8Unit& u1, int& j0, int& j1)
+{
+    if constexpr (kLdsPiece<FMT>) {
+        uint4 w[RegPiece<FMT>::NW];
+        RegPiece<FMT>::lds_load(w, img, s);
+        RegPiece<FMT>::units(w, s, u0, u1, j0, j1);
+    } else {
+        SlicePiece32<FMT>::lds_units(img, s, u0, u1, j0, j1);
+    }
+}
 
 // Formats the register-piece kernel takes (measured against the LDS-staged kernel with per-unit decode on
 // [14336, 4096] gate/up pairs at one to four tokens: Q6_K 30.0 / 32.7 / 38.9 us against 30.3 / 35.7 / 49.6,
