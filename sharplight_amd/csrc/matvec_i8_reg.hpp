@@ -1,19 +1,21 @@
 #pragma once
 // The integer-dot matvec's 64-value slices (included by matvec_i8.hpp inside namespace slhip, after unit_dot).
 //
-// A slice is two 32-value units of a row together with the bytes of their block or super-block scales;
-// RegPiece<FMT> decodes a slice from a few 16-byte words into two I8Units (codes, multipliers, offsets), so
-// that each lane decodes only its own scales, with word-wide arithmetic.
-//   * Q4_K / Q5_K (and Q6_K below three tokens, IQ4_XS in passes of more than four): the LDS-staged kernel
-//     (matvec_i8) reads each lane's slice out of the row images as words (lds_load): aligned 16- or 8-byte
-//     reads, or for Q6_K's 2-byte aligned super-blocks aligned words joined by funnel shifts.
+// A slice is two 32-value units of a row together with the bytes of their block or super-block scales,
+// decoded from a few words into two I8Units (codes, multipliers, offsets) with word-wide arithmetic, so that
+// each lane decodes only its own scales.
+//   * The LDS-staged kernel (matvec_i8) reads each lane's slice out of the row images as words: Q4_K / Q5_K
+//     (RegPiece::lds_load: aligned 16-byte reads), Q6_K below three tokens (2-byte aligned super-blocks:
+//     aligned words joined by funnel shifts), IQ4_XS in passes of more than four tokens (8-byte reads), and the
+//     32-value block formats where that measured ahead (SlicePiece32: two blocks as one run of words).
 //   * Q6_K from three tokens and IQ4_XS: the register-piece kernel below loads each lane's slice from HBM
-//     straight into registers (unaligned loads: their blocks are only 2- or 8-byte aligned), with no row image in LDS, no
-//     LDS store and no per-chunk address arithmetic. A wave takes rows n, n + W, ... (W waves in the grid,
-//     sized so that each wave gets the same number of rows), one (row, group of 64 slices) item at a time:
-//     the next D - 1 items' loads are in flight while one is computed (D register sets in rotation). The
-//     block's quantized activation rows sit in LDS; a row's output is the wave sum of its lanes' unit terms
-//     (unit_dot, the same per-unit arithmetic as the LDS-staged kernel).
+//     straight into registers (unaligned loads: their blocks are only 2- or 8-byte aligned), with no row
+//     image in LDS, no LDS store and no per-chunk address arithmetic. A wave takes rows n, n + W, ... (W waves
+//     in the grid, sized so that each wave gets the same number of rows), one (row, group of 64 slices) item
+//     at a time: the next D - 1 items' loads are in flight while one is computed (D register sets in
+//     rotation). The block's quantized activation rows sit in LDS; a row's output is the wave sum of its
+//     lanes' unit terms (unit_dot, the same per-unit arithmetic as the LDS-staged kernel).
+// Reads of a row's last slice may run up to 12 bytes past it, into the image's 16-byte pad.
 
 typedef uint32_t u32x4_a2 __attribute__((ext_vector_type(4), aligned(2)));
 typedef uint32_t u32_a2 __attribute__((aligned(2)));
@@ -28,8 +30,8 @@ __device__ __forceinline__ uint32_t ldw2(const char* p) { return *reinterpret_ca
 
 __device__ __forceinline__ uint32_t word_of(const uint4& v, int k) { return k == 0 ? v.x : k == 1 ? v.y : k == 2 ? v.z : v.w; }
 
-// A lane's raw bytes for slice s of a row (NW 16-byte registers), and the two units they hold with the unit
-// index (32-value units from the row's start) of each; field layouts as in i8_unit.
+// A lane's raw bytes for slice s of a row (NW 16-byte registers) of the super-block formats, and the two units
+// they hold with the unit index (32-value units from the row's start) of each; field layouts as in i8_unit.
 template <int FMT> struct RegPiece;
 
 // 32-value block formats: slice s is blocks 2 s and 2 s + 1, 2 BB bytes at byte 2 BB s of the row image (4-byte
