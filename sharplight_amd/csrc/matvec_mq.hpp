@@ -122,6 +122,8 @@ __global__ __launch_bounds__(64 * kMq2Waves) __attribute__((amdgpu_waves_per_eu(
     constexpr bool KQ = FMT == SLHIP_FMT_Q4_K || FMT == SLHIP_FMT_Q5_K;
     constexpr bool K6 = FMT == SLHIP_FMT_Q6_K || FMT == SLHIP_FMT_Q2_K || FMT == SLHIP_FMT_Q3_K;  // 16-value groups
     constexpr bool Q2K = FMT == SLHIP_FMT_Q2_K;
+    // Q2_K / Q3_K: the 16-value groups' scales folded into the codes (one MFMA chain per block, not two)
+    constexpr bool FOLD = FMT == SLHIP_FMT_Q2_K || FMT == SLHIP_FMT_Q3_K;
     constexpr bool MIN = KQ || (Fmt<FMT>::M && !Fmt<FMT>::K) || Q2K;  // minimum terms
     constexpr int SBB = Fmt<FMT>::BB;
     constexpr int NP = XF32 ? 3 : 1;  // bf16 parts of x
@@ -232,6 +234,25 @@ __global__ __launch_bounds__(64 * kMq2Waves) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
             for (int m = 0; m < G; m++) {
                 const uint8_t* rw = rowp(b, m, r);
+                const f32x4_t z = {0.0f, 0.0f, 0.0f, 0.0f};
+                if constexpr (FOLD) {
+                    // Q2_K / Q3_K: the 16-value groups' scales folded into the codes, one chain per block
+                    float d;
+                    const uint4 C = q23k_codes_scaled<FMT == SLHIP_FMT_Q3_K>(rw, sbo, sj, g, d);
+                    if constexpr (MIN) {
+                        float a0, a1, m0, m1;
+                        mq2_scales<FMT>(rw, sbo, sj, off, a0, a1, m0, m1);
+                        mn0[m][j] = m0;
+                        mn1[m][j] = m1;
+                    }
+                    f32x4_t c = z;
+#pragma unroll
+                    for (int p = 0; p < NP; p++)
+                        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(P[p]), as_bf16x8(C), c, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) acc[m][i] = fmaf(d, c[i], acc[m][i]);
+                    continue;
+                }
                 const uint4 C = mq2_codes<FMT>(rw, sbo, sj, off, g);
                 float a0, a1, m0, m1;
                 mq2_scales<FMT>(rw, sbo, sj, off, a0, a1, m0, m1);
@@ -239,7 +260,6 @@ __global__ __launch_bounds__(64 * kMq2Waves) __attribute__((amdgpu_waves_per_eu(
                     mn0[m][j] = m0;
                     mn1[m][j] = m1;
                 }
-                const f32x4_t z = {0.0f, 0.0f, 0.0f, 0.0f};
                 if constexpr (K6) {
                     const uint32_t keep = g < 2 ? ~0u : 0u;
                     const uint4 C0 = make_uint4(C.x & keep, C.y & keep, C.z & keep, C.w & keep);

@@ -197,6 +197,49 @@ __device__ __forceinline__ uint4 q23k_codes(const uint8_t* row, int sbo, int u, 
     return make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]), pack_bf16x2(f[6], f[7]));
 }
 
+// The same eight Q2_K / Q3_K codes multiplied by the integer scale of their 16-value group (lane groups 0-1: the
+// block's first group, 2-3 its second), with the super-block's d: d * (code * scale) is the weight, and
+// code * scale is an exact bf16 integer (Q3_K |(q - 4) * (s - 32)| <= 128, Q2_K q * s <= 45), so that both
+// groups of a block take one MFMA chain (Quant.KQuants.cs:36-107: Q3_K scales are 6-bit fields, 4 low bits at
+// byte 96 + (i % 8), 2 high bits at byte 104 + i % 4, minus 32; Q2_K's are the low nibbles of bytes 0..15).
+template <bool Q3>
+__device__ __forceinline__ uint4 q23k_codes_scaled(const uint8_t* row, int sbo, int u, int g, float& d)
+{
+    auto u16 = [&](int o) { return static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(row + o)); };
+    float sc;
+    if constexpr (Q3) {
+        d = static_cast<float>(*reinterpret_cast<const _Float16*>(row + sbo + 108));
+        const int s0 = 2 * u, w = s0 >> 2, b0 = s0 & 3;
+        const uint32_t a = u16(sbo + 96 + 4 * (w & 1) + b0);
+        const uint32_t h = u16(sbo + 104 + b0);
+        const uint32_t lo = w < 2 ? (a & 0x0F0Fu) : ((a >> 4) & 0x0F0Fu);
+        const uint32_t s2 = lo | (((h >> (2 * w)) & 0x0303u) << 4);
+        sc = static_cast<float>(static_cast<int>(g < 2 ? (s2 & 0xFFu) : (s2 >> 8)) - 32);
+    } else {
+        d = static_cast<float>(*reinterpret_cast<const _Float16*>(row + sbo + 80));
+        const uint32_t v = u16(sbo + 2 * u);
+        sc = static_cast<float>(g < 2 ? (v & 0xFu) : ((v >> 8) & 0xFu));
+    }
+    const int n = u >> 2, j = u & 3;
+    const uint2 l = lds_bytes8(row, sbo + (Q3 ? 32 : 16) + 32 * n + 8 * g);
+    const uint32_t sh = 2 * static_cast<uint32_t>(j);
+    uint32_t q0 = (l.x >> sh) & 0x03030303u, q1 = (l.y >> sh) & 0x03030303u;
+    if constexpr (Q3) {
+        const uint2 hm = lds_bytes8(row, sbo + 8 * g);
+        const uint32_t hs = static_cast<uint32_t>(4 * n + j);
+        q0 |= ((hm.x >> hs) & 0x01010101u) << 2;
+        q1 |= ((hm.y >> hs) & 0x01010101u) << 2;
+    }
+    constexpr float OFF = Q3 ? -4.0f : 0.0f;
+    float f[8];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        f[e] = (static_cast<float>((q0 >> (8 * e)) & 0xFFu) + OFF) * sc;
+        f[4 + e] = (static_cast<float>((q1 >> (8 * e)) & 0xFFu) + OFF) * sc;
+    }
+    return make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]), pack_bf16x2(f[6], f[7]));
+}
+
 // Eight Q6_K codes q - 32 of lane group g: values l = 8g .. 8g + 7 of the 32-value block u = 4 hf + k of a
 // super-block {ql[128], qh[64], sc[16], f16 d}: q = (low (k < 2) or high nibble of ql[64 hf + 32 (k & 1) + l]) |
 // (bits 2k, 2k + 1 of qh[32 hf + l]) << 4 (ggml's Q6_K layout, Quant.KQuants.cs:36-107), as four bf16 pairs
