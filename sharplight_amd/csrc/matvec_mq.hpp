@@ -98,11 +98,12 @@ constexpr int mq2_blocks()
 
 // 16-row tiles per block with f32 x: two for the 32-value block formats, so that each block splits x into
 // its three bf16 parts (and reads it) once for 32 rows -- [14336, 4096] pairs at 16 tokens, µs: Q4_0 51 -> 40,
-// Q8_0 56 -> 45, Q4_1 52 -> 37, Q5_0 59 -> 51, Q5_1 55 -> 46; one for the K-quants, whose extra decode state
-// then spills (Q4_K 52 -> 55, Q6_K 70 -> 102).
+// Q8_0 56 -> 45, Q4_1 52 -> 37, Q5_0 59 -> 51, Q5_1 55 -> 46; and for Q2_K / Q3_K with their group scales
+// folded into the codes (Q2_K 52.7 -> 48.3, Q3_K 58.0 -> 56.7); one for Q4_K / Q5_K / Q6_K, whose extra
+// decode state then spills (Q4_K 52 -> 55, Q6_K 70 -> 102).
 template <int FMT>
 constexpr int kMq2Tiles = (FMT == SLHIP_FMT_Q8_0 || FMT == SLHIP_FMT_Q4_0 || FMT == SLHIP_FMT_Q4_1 || FMT == SLHIP_FMT_Q5_0 ||
-                           FMT == SLHIP_FMT_Q5_1) ? 2 : 1;
+                           FMT == SLHIP_FMT_Q5_1 || FMT == SLHIP_FMT_Q2_K || FMT == SLHIP_FMT_Q3_K) ? 2 : 1;
 
 template <int FMT, bool DUAL, bool XF32, int TN>
 __global__ __launch_bounds__(64 * kMq2Waves) __attribute__((amdgpu_waves_per_eu(TN == 2 ? 4 : 1))) void matvec_mq2(MatvecArgs a)
