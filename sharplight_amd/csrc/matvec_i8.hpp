@@ -916,12 +916,14 @@ inline bool i8_reg_takes(const I8Args& a)
 template <int FMT, bool DUAL>
 static int run_i8_reg(I8Args a, hipStream_t st)
 {
-    const int tt = a.T <= 1 ? 1 : a.T <= 2 ? 2 : 4;
+    const int tt = a.T <= 3 ? static_cast<int>(a.T) : 4;
     for (int64_t t0 = 0; t0 < a.T; t0 += tt) {
         a.t0 = t0;
         // two register sets (one item in flight while one is computed): three measured slower
-        const int r = tt == 1 ? launch_i8_reg<FMT, 1, DUAL, 2>(a, st) : tt == 2 ? launch_i8_reg<FMT, 2, DUAL, 2>(a, st)
-                                                                         : launch_i8_reg<FMT, 4, DUAL, 2>(a, st);
+        const int r = tt == 1   ? launch_i8_reg<FMT, 1, DUAL, 2>(a, st)
+                      : tt == 2 ? launch_i8_reg<FMT, 2, DUAL, 2>(a, st)
+                      : tt == 3 ? launch_i8_reg<FMT, 3, DUAL, 2>(a, st)
+                                : launch_i8_reg<FMT, 4, DUAL, 2>(a, st);
         if (r != SLHIP_OK) return r;
     }
     return SLHIP_OK;
@@ -933,6 +935,7 @@ static int i8_tt(const I8Args& a, int tt, hipStream_t st)
     switch (tt) {
     case 1: return i8_ch<FMT, 1, DUAL>(a, st);
     case 2: return i8_ch<FMT, 2, DUAL>(a, st);
+    case 3: return i8_ch<FMT, 3, DUAL>(a, st);
     case 4: return i8_ch<FMT, 4, DUAL>(a, st);
     default: return i8_ch<FMT, 8, DUAL>(a, st);
     }
@@ -978,6 +981,7 @@ int run_i8(I8Args a, bool dual, hipStream_t st)
         if (i8_reg_takes<FMT>(a)) return dual ? run_i8_reg<FMT, true>(a, st) : run_i8_reg<FMT, false>(a, st);
     int tt = 8;
     while (tt > 1 && (tt / 2 >= a.T || i8_lds(tt, a.K, a.wrow, dual) > kI8MaxLds)) tt /= 2;
+    if (a.T == 3 && tt == 4) tt = 3;  // three tokens: no idle fourth row in the pass
     if (i8_lds(tt, a.K, a.wrow, dual) > kI8MaxLds)
         return fail(SLHIP_ERR_UNSUPPORTED, "matvec_q8: K = %lld does not fit in LDS for this format", static_cast<long long>(a.K));
     for (int64_t t0 = 0; t0 < a.T; t0 += tt) {
