@@ -188,28 +188,32 @@ __device__ __forceinline__ float unit_dot(const I8Unit& u, const uint4& x0, cons
 // into exact int32 sums (lane l: tokens 4 (l / 16) + i, row l % 16, so each lane decodes its own row's
 // multiplier and offset once per unit), so each unit's sums for 16 rows x 16 tokens take one
 // instruction and the scaling a (d s) + b gs per output runs on the VALU. Q6_K's two 16-value scale groups take
-// two instructions, each with the other half's codes masked to zero. A block of 8 waves takes a tile (a gate/up
-// pair of tiles); stages of SU units (1024 values; 512 for Q8_0) of the 16 rows go through LDS, double-buffered:
-// the next stage's rows and q8 scales move from HBM straight into LDS (global_load_lds, no registers) while the
-// current one is computed; each wave takes SU / 8 units of a stage; the waves' partial sums meet in LDS at the
-// end.
+// two instructions, each with the other half's codes masked to zero. A block of 8 waves takes TN tiles (gate/up
+// pairs of tiles: TN = 1 or 2 by format); stages of SU units (512 or 1024 values) of the tiles' rows go through
+// LDS, double-buffered: the next stage's rows and q8 scales move from HBM straight into LDS (global_load_lds,
+// no registers) while the current one is computed; each wave takes SU / 8 units of a stage for every tile; the
+// waves' partial sums meet in LDS at the end.
 
-// Bytes of one row per 1024 values, the width of the staging loads, the 32-value units per stage (SU: Q8_0's
-// large rows take 512-value stages, which fit more blocks per CU -- [14336, 4096] pairs at 16 tokens 51.8 ->
-// 44 us; every other format measured slower so), and whether the multipliers go through a per-wave table
-// (below).
+// Bytes of one row per 1024 values, the width of the staging loads, the 32-value units per stage and 16-row
+// tiles per block (SU, TN), and whether the multipliers go through a per-wave table (below). Measured on
+// [14336, 4096] pairs at 16 tokens (µs): one tile of 1024-value stages is where the kernel started; Q8_0's large
+// rows take 512-value stages (51.8 -> 44); two tiles of 512-value stages per block (448 blocks: every tile in
+// one round of two blocks per CU, and each x load and q8 scale shared by two tiles) for Q4_0 / Q4_1 / Q5_0 /
+// Q5_1 / IQ4_NL / MXFP4 / Q4_K / IQ4_XS: 35.6 / 35.1 / 38.6 / 38.8 / 36.3 / 37.7 / 38.8 / 40.3 -> 29.4 / 28.2 /
+// 35.1 / 32.6 / 29.6 / 31.8 / 31.7 / 33.5. Q5_K and Q6_K measured level or slower with two (their decode
+// state: 135 registers), and two Q8_0 tiles would hold one block per CU.
 template <int FMT> struct I8Stage;
-template <> struct I8Stage<SLHIP_FMT_Q8_0> { static constexpr int RB = 32 * 34, UB = 16, SU = 16; static constexpr bool TABLE = false; };
-template <> struct I8Stage<SLHIP_FMT_Q4_0> { static constexpr int RB = 32 * 18, UB = 16, SU = 32; static constexpr bool TABLE = false; };
-template <> struct I8Stage<SLHIP_FMT_Q4_1> { static constexpr int RB = 32 * 20, UB = 16, SU = 32; static constexpr bool TABLE = false; };
-template <> struct I8Stage<SLHIP_FMT_Q5_0> { static constexpr int RB = 32 * 22, UB = 16, SU = 32; static constexpr bool TABLE = false; };
-template <> struct I8Stage<SLHIP_FMT_Q5_1> { static constexpr int RB = 32 * 24, UB = 16, SU = 32; static constexpr bool TABLE = false; };
-template <> struct I8Stage<SLHIP_FMT_IQ4_NL> { static constexpr int RB = 32 * 18, UB = 16, SU = 32; static constexpr bool TABLE = false; };
-template <> struct I8Stage<SLHIP_FMT_MXFP4> { static constexpr int RB = 32 * 17, UB = 16, SU = 32; static constexpr bool TABLE = false; };
-template <> struct I8Stage<SLHIP_FMT_Q4_K> { static constexpr int RB = 4 * 144, UB = 16, SU = 32; static constexpr bool TABLE = true; };
-template <> struct I8Stage<SLHIP_FMT_Q5_K> { static constexpr int RB = 4 * 176, UB = 16, SU = 32; static constexpr bool TABLE = true; };
-template <> struct I8Stage<SLHIP_FMT_Q6_K> { static constexpr int RB = 4 * 210, UB = 4, SU = 32; static constexpr bool TABLE = false; };
-template <> struct I8Stage<SLHIP_FMT_IQ4_XS> { static constexpr int RB = 4 * 136, UB = 16, SU = 32; static constexpr bool TABLE = true; };
+template <> struct I8Stage<SLHIP_FMT_Q8_0> { static constexpr int RB = 32 * 34, UB = 16, SU = 16, TN = 1; static constexpr bool TABLE = false; };
+template <> struct I8Stage<SLHIP_FMT_Q4_0> { static constexpr int RB = 32 * 18, UB = 16, SU = 16, TN = 2; static constexpr bool TABLE = false; };
+template <> struct I8Stage<SLHIP_FMT_Q4_1> { static constexpr int RB = 32 * 20, UB = 16, SU = 16, TN = 2; static constexpr bool TABLE = false; };
+template <> struct I8Stage<SLHIP_FMT_Q5_0> { static constexpr int RB = 32 * 22, UB = 16, SU = 16, TN = 2; static constexpr bool TABLE = false; };
+template <> struct I8Stage<SLHIP_FMT_Q5_1> { static constexpr int RB = 32 * 24, UB = 16, SU = 16, TN = 2; static constexpr bool TABLE = false; };
+template <> struct I8Stage<SLHIP_FMT_IQ4_NL> { static constexpr int RB = 32 * 18, UB = 16, SU = 16, TN = 2; static constexpr bool TABLE = false; };
+template <> struct I8Stage<SLHIP_FMT_MXFP4> { static constexpr int RB = 32 * 17, UB = 16, SU = 16, TN = 2; static constexpr bool TABLE = false; };
+template <> struct I8Stage<SLHIP_FMT_Q4_K> { static constexpr int RB = 4 * 144, UB = 16, SU = 16, TN = 2; static constexpr bool TABLE = true; };
+template <> struct I8Stage<SLHIP_FMT_Q5_K> { static constexpr int RB = 4 * 176, UB = 16, SU = 32, TN = 1; static constexpr bool TABLE = true; };
+template <> struct I8Stage<SLHIP_FMT_Q6_K> { static constexpr int RB = 4 * 210, UB = 4, SU = 32, TN = 1; static constexpr bool TABLE = false; };
+template <> struct I8Stage<SLHIP_FMT_IQ4_XS> { static constexpr int RB = 4 * 136, UB = 16, SU = 16, TN = 2; static constexpr bool TABLE = true; };
 
 constexpr int kI8MfWaves = 8;
 
@@ -353,22 +357,23 @@ typedef int i32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 
-template <int FMT, bool DUAL, int SU>
-__global__ __launch_bounds__(64 * kI8MfWaves) __attribute__((amdgpu_waves_per_eu(SU == 16 ? 6 : 1))) void matvec_i8_mfma(I8Args a)
+template <int FMT, bool DUAL, int SU, int TN>
+__global__ __launch_bounds__(64 * kI8MfWaves) __attribute__((amdgpu_waves_per_eu(SU == 16 && TN == 1 ? 6 : 1))) void matvec_i8_mfma(I8Args a)
 {
     constexpr int NM = DUAL ? 2 : 1;
+    constexpr int G = NM * TN;  // row groups of 16 rows: group q = tile q / NM of matrix q % NM
     constexpr int RB = I8Stage<FMT>::RB * SU / 32, UB = I8Stage<FMT>::UB;  // SU 32-value units per stage
     constexpr int PITCH = stage_pitch(RB, UB);
     constexpr int SPR = PITCH / UB;  // load slots per staged row; those past RB / UB are padding
     constexpr int MS = (16 * SPR + 63) / 64 * 64;  // slots per matrix: whole waves, so a wave's run is in one
-    constexpr int SLOTS = NM * MS;
+    constexpr int SLOTS = G * MS;
     constexpr int NT = 64 * kI8MfWaves;
     constexpr int LPT = (SLOTS + NT - 1) / NT;  // loads per thread and stage
     constexpr int BPW = SU / kI8MfWaves;  // units per wave and stage
     constexpr bool H16 = kUnitForm<FMT> == kScale16Off;
     static_assert(RB % UB == 0 && (UB == 16 || UB == 4), "stage shape");
     static_assert(NT >= 16 * SU && (SU == 16 || SU == 32), "one thread per token and unit of a stage stages the q8 scales");
-    static_assert(2 * SLOTS * UB >= static_cast<int>(sizeof(float)) * kI8MfWaves * NM * 4 * 64,
+    static_assert(2 * SLOTS * UB >= static_cast<int>(sizeof(float)) * kI8MfWaves * G * 4 * 64,
                   "the cross-wave reduction reuses the weight stage");
     __shared__ __align__(16) uint32_t stage[2][SLOTS * UB / 4];  // [matrix: 16 rows of PITCH bytes, padding]
     auto rowp = [&](int b, int m, int rr) -> const uint32_t* { return &stage[b][(m * MS * UB + rr * PITCH) / 4]; };
@@ -378,7 +383,7 @@ __global__ __launch_bounds__(64 * kI8MfWaves) __attribute__((amdgpu_waves_per_eu
     const int lane = threadIdx.x & 63;
     const int wave = wave_id();
     const int r = lane & 15, g = lane >> 4;
-    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 16;
+    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 16 * TN;
     const int K = static_cast<int>(a.K);
     const int ns = K / (32 * SU);
     const int64_t xstride = K + K / 2;
@@ -408,7 +413,7 @@ __global__ __launch_bounds__(64 * kI8MfWaves) __attribute__((amdgpu_waves_per_eu
             c = 0;
         }
         c = c < RB / UB ? c : RB / UB - 1;
-        int64_t row = n0 + rr;
+        int64_t row = n0 + 16 * (m / NM) + rr;
         row = row < a.N ? row : a.N - 1;
         src[i] = static_cast<uint32_t>(row * a.wrow + UB * c);
     }
@@ -418,7 +423,7 @@ __global__ __launch_bounds__(64 * kI8MfWaves) __attribute__((amdgpu_waves_per_eu
             if (NT * i + 64 * wave >= SLOTS) break;  // wave-uniform: the LDS run of a wave starts in the stage
             if (NT * (i + 1) > SLOTS && static_cast<int>(threadIdx.x) + NT * i >= SLOTS) continue;
             char* base = reinterpret_cast<char*>(&stage[b][0]) + UB * (NT * i + 64 * wave);
-            const char* mat = ((NT * i + 64 * wave) / MS ? a.wu : a.wg) + static_cast<int64_t>(s) * RB;
+            const char* mat = (((NT * i + 64 * wave) / MS) % NM ? a.wu : a.wg) + static_cast<int64_t>(s) * RB;
             load_to_lds<UB>(mat, src[i], base);
         }
         if (64 * wave < 16 * SU) {  // wave-uniform; the base made visibly uniform for the scalar operand
@@ -436,10 +441,10 @@ __global__ __launch_bounds__(64 * kI8MfWaves) __attribute__((amdgpu_waves_per_eu
     // loaded from HBM with the stage (the same lines the stage moves into LDS)
     const char* hdr_src = nullptr;
     if constexpr (TABLE) {
-        const int rr = lane % (NM * 16);
-        int64_t row = n0 + rr % 16;
+        const int rr = lane % (G * 16), grp = rr / 16;
+        int64_t row = n0 + 16 * (grp / NM) + rr % 16;
         row = row < a.N ? row : a.N - 1;
-        hdr_src = (rr >= 16 ? a.wu : a.wg) + row * a.wrow + (wave * BPW / 8) * SBB;
+        hdr_src = (grp % NM ? a.wu : a.wg) + row * a.wrow + (wave * BPW / 8) * SBB;
     }
     struct Xs {
         uint2 q[BPW];
@@ -452,30 +457,30 @@ __global__ __launch_bounds__(64 * kI8MfWaves) __attribute__((amdgpu_waves_per_eu
     };
     // acc[m][i]: weight row n0 + r of matrix m, token t0 + 4 g + i (the MFMA's A operand is the q8 tokens, B the
     // weight codes, so each lane decodes the multipliers of its own row once per unit)
-    float acc[NM][4];
+    float acc[G][4];
 #pragma unroll
-    for (int m = 0; m < NM; m++)
+    for (int m = 0; m < G; m++)
         for (int i = 0; i < 4; i++) acc[m][i] = 0.0f;
     constexpr bool OFF = kUnitForm<FMT> == kScale32Off;  // formats with one offset per unit
-    f32x4_t acc_off[NM];
+    f32x4_t acc_off[G];
 #pragma unroll
-    for (int m = 0; m < NM; m++) acc_off[m] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int m = 0; m < G; m++) acc_off[m] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
     // The K-quants' and IQ4_XS's multipliers and offsets (6-bit fields spread over the super-block header) for
     // the wave's units and the tile's rows are decoded once each, by the lane holding the row's header, into
     // the wave's own LDS table, and read there by the 4 lanes of a row; the other formats' (one f16 or e8m0
     // field) are read from the stage directly.
-    constexpr int NENT = NM * 16 * BPW;
+    constexpr int NENT = G * 16 * BPW;
     static_assert(8 % BPW == 0, "a wave's units lie in one super-block");
     __shared__ __align__(16) float2 wsc[TABLE ? kI8MfWaves : 1][TABLE ? NENT : 1];
     float2* my = wsc[TABLE ? wave : 0];
     auto compute = [&](int b, const Xs& x) {
         if constexpr (TABLE) {
             static_assert(!H16, "the table holds one multiplier and offset per unit");
-            if (lane < NM * 16) {
+            if (lane < G * 16) {
 #pragma unroll
                 for (int j = 0; j < BPW; j++) {
                     const int u8 = (wave * BPW + j) & 7;  // the unit's place in its super-block
-                    my[j * NM * 16 + lane] = hdr_scales<FMT>(x.hdr, u8 >> 2, u8 & 3);
+                    my[j * G * 16 + lane] = hdr_scales<FMT>(x.hdr, u8 >> 2, u8 & 3);
                 }
             }
             wave_lds_sync();
@@ -490,10 +495,10 @@ __global__ __launch_bounds__(64 * kI8MfWaves) __attribute__((amdgpu_waves_per_eu
             const float4 xo = xsc[b][wave * BPW + gu][r];
             const float xg = g < BPW ? xo.y + xo.z : 0.0f;
 #pragma unroll
-            for (int m = 0; m < NM; m++) {
+            for (int m = 0; m < G; m++) {
                 float4 so;
                 if constexpr (TABLE) {
-                    const float2 s2 = my[gu * NM * 16 + m * 16 + r];
+                    const float2 s2 = my[gu * G * 16 + m * 16 + r];
                     so = make_float4(s2.x, s2.x, s2.y, s2.y);
                 } else {
                     so = i8_scales<FMT>(rowp(b, m, r), wave * BPW + gu);
@@ -509,11 +514,11 @@ __global__ __launch_bounds__(64 * kI8MfWaves) __attribute__((amdgpu_waves_per_eu
 #pragma unroll
             for (int i = 0; i < 4; i++) d[i] = xsc[b][u][4 * g + i].x;
 #pragma unroll
-            for (int m = 0; m < NM; m++) {
+            for (int m = 0; m < G; m++) {
                 const uint2 c = i8_codes8<FMT>(rowp(b, m, r), u, g);
                 float4 sc;
                 if constexpr (TABLE) {
-                    sc.x = my[j * NM * 16 + m * 16 + r].x;
+                    sc.x = my[j * G * 16 + m * 16 + r].x;
                 } else {
                     sc = i8_scales<FMT>(rowp(b, m, r), u);
                 }
@@ -565,25 +570,26 @@ __global__ __launch_bounds__(64 * kI8MfWaves) __attribute__((amdgpu_waves_per_eu
     }
     if constexpr (OFF) {
 #pragma unroll
-        for (int m = 0; m < NM; m++)
+        for (int m = 0; m < G; m++)
             for (int i = 0; i < 4; i++) acc[m][i] += acc_off[m][i];
     }
     // every wave is past its last read of the stage (the loop ends on a barrier): reuse it for the reduction
-    float* red = reinterpret_cast<float*>(&stage[0][0]);  // [wave][m][i][lane]
+    float* red = reinterpret_cast<float*>(&stage[0][0]);  // [wave][group][i][lane]
 #pragma unroll
-    for (int m = 0; m < NM; m++)
-        for (int i = 0; i < 4; i++) red[((wave * NM + m) * 4 + i) * 64 + lane] = acc[m][i];
+    for (int m = 0; m < G; m++)
+        for (int i = 0; i < 4; i++) red[((wave * G + m) * 4 + i) * 64 + lane] = acc[m][i];
     __syncthreads();
-    if (wave == 0) {
+    if (wave < TN) {  // wave tl finishes tile tl
+        const int tl = wave;
         float v[NM][4];
 #pragma unroll
         for (int m = 0; m < NM; m++)
             for (int i = 0; i < 4; i++) {
                 float t = 0.0f;
-                for (int w = 0; w < kI8MfWaves; w++) t += red[((w * NM + m) * 4 + i) * 64 + lane];
+                for (int w = 0; w < kI8MfWaves; w++) t += red[((w * G + tl * NM + m) * 4 + i) * 64 + lane];
                 v[m][i] = t;
             }
-        const int64_t n = n0 + r;
+        const int64_t n = n0 + 16 * tl + r;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int64_t tt = a.t0 + 4 * g + i;
@@ -959,12 +965,12 @@ inline int i8_mfma_min_tokens()
 template <int FMT>
 int run_i8_mfma(I8Args a, bool dual, hipStream_t st)
 {
-    const dim3 grid(static_cast<unsigned>((a.N + 15) / 16));
-    constexpr int SU = I8Stage<FMT>::SU;
+    constexpr int SU = I8Stage<FMT>::SU, TN = I8Stage<FMT>::TN;
+    const dim3 gridt(static_cast<unsigned>((a.N + 16 * TN - 1) / (16 * TN)));
     for (int64_t t0 = 0; t0 < a.T; t0 += 16) {
         a.t0 = t0;
-        if (dual) matvec_i8_mfma<FMT, true, SU><<<grid, 64 * kI8MfWaves, 0, st>>>(a);
-        else matvec_i8_mfma<FMT, false, SU><<<grid, 64 * kI8MfWaves, 0, st>>>(a);
+        if (dual) matvec_i8_mfma<FMT, true, SU, TN><<<gridt, 64 * kI8MfWaves, 0, st>>>(a);
+        else matvec_i8_mfma<FMT, false, SU, TN><<<gridt, 64 * kI8MfWaves, 0, st>>>(a);
         const int r = check_launch("matvec_i8_mfma");
         if (r != SLHIP_OK) return r;
     }
