@@ -25,9 +25,11 @@ __device__ __forceinline__ void load_to_lds(const void* base, uint32_t off, void
 // Bytes per staged row of the matrix-core kernels (matvec_i8_mfma, matvec_mq2): at least 16 past the row (lds_u64 reads up to 12 bytes beyond
 // a piece), a whole number of staging loads, and 32 mod 64 bytes, so that the 16 rows a wave reads at once start
 // in 8 different 32-byte bank groups.
-constexpr int stage_pitch(int rb, int ub)
+// tight: no slack past the row (the caller's array then extends 16 bytes past its last row instead: the bytes
+// read past a piece are discarded, so reading the next row's are harmless).
+constexpr int stage_pitch(int rb, int ub, bool tight = false)
 {
-    int p = rb + 16;
+    int p = tight ? rb : rb + 16;
     while (p % ub != 0 || p % 64 != 32) p += 4;
     return p;
 }

@@ -190,8 +190,8 @@ __device__ __forceinline__ float unit_dot(const I8Unit& u, const uint4& x0, cons
 // instruction and the scaling a (d s) + b gs per output runs on the VALU. Q6_K's two 16-value scale groups take
 // two instructions, each with the other half's codes masked to zero. A block of 8 waves takes TN tiles (gate/up
 // pairs of tiles: TN = 1 or 2 by format); stages of SU units (512 or 1024 values) of the tiles' rows go through
-// LDS, double-buffered: the next stage's rows and q8 scales move from HBM straight into LDS (global_load_lds,
-// no registers) while the current one is computed; each wave takes SU / 8 units of a stage for every tile; the
+// LDS, double- or triple-buffered: the next stage's (or the next two stages') rows and q8 scales move from HBM
+// straight into LDS (global_load_lds, no registers) while the current one is computed; each wave takes SU / 8 units of a stage for every tile; the
 // waves' partial sums meet in LDS at the end.
 
 // Bytes of one row per 1024 values, the width of the staging loads, the 32-value units per stage and 16-row
@@ -201,19 +201,21 @@ __device__ __forceinline__ float unit_dot(const I8Unit& u, const uint4& x0, cons
 // one round of two blocks per CU, and each x load and q8 scale shared by two tiles) for Q4_0 / Q4_1 / Q5_0 /
 // Q5_1 / IQ4_NL / MXFP4 / Q4_K / IQ4_XS: 35.6 / 35.1 / 38.6 / 38.8 / 36.3 / 37.7 / 38.8 / 40.3 -> 29.4 / 28.2 /
 // 35.1 / 32.6 / 29.6 / 31.8 / 31.7 / 33.5. Q5_K and Q6_K measured level or slower with two (their decode
-// state: 135 registers), and two Q8_0 tiles would hold one block per CU.
+// state: 135 registers), and two Q8_0 tiles would hold one block per CU. NB: stage buffers; three (loads two
+// stages ahead) for Q8_0 only: 44.0 -> 39.9; the others measured level or slower with three (LDS then holds one
+// block per CU for Q4_1 / Q5_1 / Q5_K / Q6_K, and Q4_0 / Q4_K need more registers than two blocks leave).
 template <int FMT> struct I8Stage;
-template <> struct I8Stage<SLHIP_FMT_Q8_0> { static constexpr int RB = 32 * 34, UB = 16, SU = 16, TN = 1; static constexpr bool TABLE = false; };
-template <> struct I8Stage<SLHIP_FMT_Q4_0> { static constexpr int RB = 32 * 18, UB = 16, SU = 16, TN = 2; static constexpr bool TABLE = false; };
-template <> struct I8Stage<SLHIP_FMT_Q4_1> { static constexpr int RB = 32 * 20, UB = 16, SU = 16, TN = 2; static constexpr bool TABLE = false; };
-template <> struct I8Stage<SLHIP_FMT_Q5_0> { static constexpr int RB = 32 * 22, UB = 16, SU = 16, TN = 2; static constexpr bool TABLE = false; };
-template <> struct I8Stage<SLHIP_FMT_Q5_1> { static constexpr int RB = 32 * 24, UB = 16, SU = 16, TN = 2; static constexpr bool TABLE = false; };
-template <> struct I8Stage<SLHIP_FMT_IQ4_NL> { static constexpr int RB = 32 * 18, UB = 16, SU = 16, TN = 2; static constexpr bool TABLE = false; };
-template <> struct I8Stage<SLHIP_FMT_MXFP4> { static constexpr int RB = 32 * 17, UB = 16, SU = 16, TN = 2; static constexpr bool TABLE = false; };
-template <> struct I8Stage<SLHIP_FMT_Q4_K> { static constexpr int RB = 4 * 144, UB = 16, SU = 16, TN = 2; static constexpr bool TABLE = true; };
-template <> struct I8Stage<SLHIP_FMT_Q5_K> { static constexpr int RB = 4 * 176, UB = 16, SU = 32, TN = 1; static constexpr bool TABLE = true; };
-template <> struct I8Stage<SLHIP_FMT_Q6_K> { static constexpr int RB = 4 * 210, UB = 4, SU = 32, TN = 1; static constexpr bool TABLE = false; };
-template <> struct I8Stage<SLHIP_FMT_IQ4_XS> { static constexpr int RB = 4 * 136, UB = 16, SU = 16, TN = 2; static constexpr bool TABLE = true; };
+template <> struct I8Stage<SLHIP_FMT_Q8_0> { static constexpr int RB = 32 * 34, UB = 16, SU = 16, TN = 1, NB = 3; static constexpr bool TABLE = false; };
+template <> struct I8Stage<SLHIP_FMT_Q4_0> { static constexpr int RB = 32 * 18, UB = 16, SU = 16, TN = 2, NB = 2; static constexpr bool TABLE = false; };
+template <> struct I8Stage<SLHIP_FMT_Q4_1> { static constexpr int RB = 32 * 20, UB = 16, SU = 16, TN = 2, NB = 2; static constexpr bool TABLE = false; };
+template <> struct I8Stage<SLHIP_FMT_Q5_0> { static constexpr int RB = 32 * 22, UB = 16, SU = 16, TN = 2, NB = 2; static constexpr bool TABLE = false; };
+template <> struct I8Stage<SLHIP_FMT_Q5_1> { static constexpr int RB = 32 * 24, UB = 16, SU = 16, TN = 2, NB = 2; static constexpr bool TABLE = false; };
+template <> struct I8Stage<SLHIP_FMT_IQ4_NL> { static constexpr int RB = 32 * 18, UB = 16, SU = 16, TN = 2, NB = 2; static constexpr bool TABLE = false; };
+template <> struct I8Stage<SLHIP_FMT_MXFP4> { static constexpr int RB = 32 * 17, UB = 16, SU = 16, TN = 2, NB = 2; static constexpr bool TABLE = false; };
+template <> struct I8Stage<SLHIP_FMT_Q4_K> { static constexpr int RB = 4 * 144, UB = 16, SU = 16, TN = 2, NB = 2; static constexpr bool TABLE = true; };
+template <> struct I8Stage<SLHIP_FMT_Q5_K> { static constexpr int RB = 4 * 176, UB = 16, SU = 32, TN = 1, NB = 2; static constexpr bool TABLE = true; };
+template <> struct I8Stage<SLHIP_FMT_Q6_K> { static constexpr int RB = 4 * 210, UB = 4, SU = 32, TN = 1, NB = 2; static constexpr bool TABLE = false; };
+template <> struct I8Stage<SLHIP_FMT_IQ4_XS> { static constexpr int RB = 4 * 136, UB = 16, SU = 16, TN = 2, NB = 2; static constexpr bool TABLE = true; };
 
 constexpr int kI8MfWaves = 8;
 
@@ -357,29 +359,65 @@ typedef int i32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 
-template <int FMT, bool DUAL, int SU, int TN>
-__global__ __launch_bounds__(64 * kI8MfWaves) __attribute__((amdgpu_waves_per_eu(SU == 16 && TN == 1 ? 6 : 1))) void matvec_i8_mfma(I8Args a)
+// s_waitcnt vmcnt(n) (n < 16; expcnt and lgkmcnt left at their maxima); n from a wave-uniform value
+__device__ __forceinline__ void wait_vm_le(int n)
+{
+    switch (n < 15 ? n : 15) {
+#define SLHIP_VM_CASE(k) \
+    case k: __builtin_amdgcn_s_waitcnt(0x0F70 | k); break;
+        SLHIP_VM_CASE(0) SLHIP_VM_CASE(1) SLHIP_VM_CASE(2) SLHIP_VM_CASE(3) SLHIP_VM_CASE(4) SLHIP_VM_CASE(5)
+        SLHIP_VM_CASE(6) SLHIP_VM_CASE(7) SLHIP_VM_CASE(8) SLHIP_VM_CASE(9) SLHIP_VM_CASE(10) SLHIP_VM_CASE(11)
+        SLHIP_VM_CASE(12) SLHIP_VM_CASE(13) SLHIP_VM_CASE(14) SLHIP_VM_CASE(15)
+#undef SLHIP_VM_CASE
+    }
+}
+
+// Global loads into registers written as inline assembly: the compiler neither counts them nor waits for them,
+// so the caller's explicit vmcnt waits must cover every read of the result (the three-buffer pipeline below,
+// whose counted waits would otherwise be forced down to vmcnt(0) by the compiler's own wait for these).
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint2 ld_async_u2(const void* p)
+{
+    u32x2_t r;
+    asm volatile("global_load_dwordx2 %0, %1, off" : "=v"(r) : "v"(p) : "memory");
+    return make_uint2(r.x, r.y);
+}
+__device__ __forceinline__ uint4 ld_async_u4(const void* p)
+{
+    u32x4_t r;
+    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(r) : "v"(p) : "memory");
+    return make_uint4(r.x, r.y, r.z, r.w);
+}
+
+// NB stage buffers: 2 (the next stage loads while the current one is computed) or 3 (the stage after next
+// loads too: twice the bytes in flight per block, at 1.5x the LDS)
+template <int FMT, bool DUAL, int SU, int TN, int NB>
+__global__ __launch_bounds__(64 * kI8MfWaves) __attribute__((amdgpu_waves_per_eu(SU == 16 && TN == 1 ? 6 : NB == 3 || TN == 2 ? 4 : 1))) void matvec_i8_mfma(I8Args a)
 {
     constexpr int NM = DUAL ? 2 : 1;
     constexpr int G = NM * TN;  // row groups of 16 rows: group q = tile q / NM of matrix q % NM
     constexpr int RB = I8Stage<FMT>::RB * SU / 32, UB = I8Stage<FMT>::UB;  // SU 32-value units per stage
-    constexpr int PITCH = stage_pitch(RB, UB);
+    constexpr int PITCH = stage_pitch(RB, UB, NB == 3);
     constexpr int SPR = PITCH / UB;  // load slots per staged row; those past RB / UB are padding
     constexpr int MS = (16 * SPR + 63) / 64 * 64;  // slots per matrix: whole waves, so a wave's run is in one
     constexpr int SLOTS = G * MS;
+    constexpr int SW = SLOTS * UB / 4;  // words per stage buffer
     constexpr int NT = 64 * kI8MfWaves;
     constexpr int LPT = (SLOTS + NT - 1) / NT;  // loads per thread and stage
     constexpr int BPW = SU / kI8MfWaves;  // units per wave and stage
     constexpr bool H16 = kUnitForm<FMT> == kScale16Off;
     static_assert(RB % UB == 0 && (UB == 16 || UB == 4), "stage shape");
     static_assert(NT >= 16 * SU && (SU == 16 || SU == 32), "one thread per token and unit of a stage stages the q8 scales");
-    static_assert(2 * SLOTS * UB >= static_cast<int>(sizeof(float)) * kI8MfWaves * G * 4 * 64,
+    static_assert(NB * SLOTS * UB >= static_cast<int>(sizeof(float)) * kI8MfWaves * G * 4 * 64,
                   "the cross-wave reduction reuses the weight stage");
-    __shared__ __align__(16) uint32_t stage[2][SLOTS * UB / 4];  // [matrix: 16 rows of PITCH bytes, padding]
-    auto rowp = [&](int b, int m, int rr) -> const uint32_t* { return &stage[b][(m * MS * UB + rr * PITCH) / 4]; };
-    // the q8 scales {d, d s_lo, d s_hi, 0} of [unit][token] of a stage (the 4 tokens a lane group reads at
-    // once are 64 bytes apart: different banks)
-    __shared__ float4 xsc[2][SU][16];
+    static_assert(NB == 2 || NB == 3, "stage buffers");
+    // [buffer][matrix: 16 rows of PITCH bytes, padding], then the q8 scales {d, d s_lo, d s_hi, 0} of
+    // [buffer][unit][token] (the 4 tokens a lane group reads at once are 64 bytes apart: different banks; the
+    // reads past the last staged row land there)
+    __shared__ __align__(16) uint32_t stage_mem[NB * SW + NB * SU * 16 * 4];
+    float4* const xsc = reinterpret_cast<float4*>(&stage_mem[NB * SW]);
+    auto rowp = [&](int b, int m, int rr) -> const uint32_t* { return &stage_mem[b * SW + (m * MS * UB + rr * PITCH) / 4]; };
     const int lane = threadIdx.x & 63;
     const int wave = wave_id();
     const int r = lane & 15, g = lane >> 4;
@@ -422,7 +460,7 @@ __global__ __launch_bounds__(64 * kI8MfWaves) __attribute__((amdgpu_waves_per_eu
         for (int i = 0; i < LPT; i++) {
             if (NT * i + 64 * wave >= SLOTS) break;  // wave-uniform: the LDS run of a wave starts in the stage
             if (NT * (i + 1) > SLOTS && static_cast<int>(threadIdx.x) + NT * i >= SLOTS) continue;
-            char* base = reinterpret_cast<char*>(&stage[b][0]) + UB * (NT * i + 64 * wave);
+            char* base = reinterpret_cast<char*>(&stage_mem[b * SW]) + UB * (NT * i + 64 * wave);
             const char* mat = (((NT * i + 64 * wave) / MS) % NM ? a.wu : a.wg) + static_cast<int64_t>(s) * RB;
             load_to_lds<UB>(mat, src[i], base);
         }
@@ -432,7 +470,7 @@ __global__ __launch_bounds__(64 * kI8MfWaves) __attribute__((amdgpu_waves_per_eu
             const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(xb)));
             const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(xb >> 32)));
             const uint64_t xbu = (static_cast<uint64_t>(hi) << 32) | lo;
-            load_to_lds<16>(reinterpret_cast<const void*>(xbu), xs_off, &xsc[b][0][0] + 64 * wave);
+            load_to_lds<16>(reinterpret_cast<const void*>(xbu), xs_off, xsc + b * SU * 16 + 64 * wave);
         }
     };
     constexpr bool TABLE = I8Stage<FMT>::TABLE;
@@ -451,9 +489,22 @@ __global__ __launch_bounds__(64 * kI8MfWaves) __attribute__((amdgpu_waves_per_eu
         uint4 hdr;
     };
     auto fetch_x = [&](Xs& x, int s) {
+        if constexpr (NB == 3) {
 #pragma unroll
-        for (int j = 0; j < BPW; j++) x.q[j] = *reinterpret_cast<const uint2*>(xrow + (s * SU + wave * BPW + j) * 32 + 8 * g);
-        if constexpr (TABLE) x.hdr = *reinterpret_cast<const uint4*>(hdr_src + static_cast<int64_t>(s) * (SU / 8) * SBB);
+            for (int j = 0; j < BPW; j++) x.q[j] = ld_async_u2(xrow + (s * SU + wave * BPW + j) * 32 + 8 * g);
+            // (IQ4_XS: only the 8 header bytes it decodes; a register the load writes but the code never reads
+            // would be free for the compiler to reuse while the load is still in flight)
+            if constexpr (TABLE && FMT == SLHIP_FMT_IQ4_XS) {
+                const uint2 h = ld_async_u2(hdr_src + static_cast<int64_t>(s) * (SU / 8) * SBB);
+                x.hdr = make_uint4(h.x, h.y, 0u, 0u);
+            } else if constexpr (TABLE) {
+                x.hdr = ld_async_u4(hdr_src + static_cast<int64_t>(s) * (SU / 8) * SBB);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < BPW; j++) x.q[j] = *reinterpret_cast<const uint2*>(xrow + (s * SU + wave * BPW + j) * 32 + 8 * g);
+            if constexpr (TABLE) x.hdr = *reinterpret_cast<const uint4*>(hdr_src + static_cast<int64_t>(s) * (SU / 8) * SBB);
+        }
     };
     // acc[m][i]: weight row n0 + r of matrix m, token t0 + 4 g + i (the MFMA's A operand is the q8 tokens, B the
     // weight codes, so each lane decodes the multipliers of its own row once per unit)
@@ -492,7 +543,7 @@ __global__ __launch_bounds__(64 * kI8MfWaves) __attribute__((amdgpu_waves_per_eu
         if constexpr (OFF) {
             // (with two units per wave, lane groups 2 and 3 supply zeros for the instruction's other two)
             const int gu = g < BPW ? g : 0;
-            const float4 xo = xsc[b][wave * BPW + gu][r];
+            const float4 xo = xsc[(b * SU + wave * BPW + gu) * 16 + r];
             const float xg = g < BPW ? xo.y + xo.z : 0.0f;
 #pragma unroll
             for (int m = 0; m < G; m++) {
@@ -512,7 +563,7 @@ __global__ __launch_bounds__(64 * kI8MfWaves) __attribute__((amdgpu_waves_per_eu
             const long xb = static_cast<long>(__builtin_bit_cast(uint64_t, x.q[j]));
             float d[4];
 #pragma unroll
-            for (int i = 0; i < 4; i++) d[i] = xsc[b][u][4 * g + i].x;
+            for (int i = 0; i < 4; i++) d[i] = xsc[(b * SU + u) * 16 + 4 * g + i].x;
 #pragma unroll
             for (int m = 0; m < G; m++) {
                 const uint2 c = i8_codes8<FMT>(rowp(b, m, r), u, g);
@@ -531,7 +582,7 @@ __global__ __launch_bounds__(64 * kI8MfWaves) __attribute__((amdgpu_waves_per_eu
                     const i32x4_t S1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(xb, c1, z, 0, 0, 0);
 #pragma unroll
                     for (int i = 0; i < 4; i++) {
-                        const float4 xs = xsc[b][u][4 * g + i];
+                        const float4 xs = xsc[(b * SU + u) * 16 + 4 * g + i];
                         acc[m][i] += fmaf(sc.x, __fmul_rn(xs.x, static_cast<float>(S0[i])),
                                           fmaf(sc.y, __fmul_rn(xs.x, static_cast<float>(S1[i])),
                                                fmaf(sc.z, xs.y, __fmul_rn(sc.w, xs.z))));
@@ -546,27 +597,66 @@ __global__ __launch_bounds__(64 * kI8MfWaves) __attribute__((amdgpu_waves_per_eu
     };
     // vmcnt(0): the stage's LDS writes by global_load_lds (and the q8 codes in registers) have landed
     constexpr int kWaitLoads = 0x0F70;
-    Xs xa, xb2;
-    fetch(0, 0);
-    fetch_x(xa, 0);
-    __builtin_amdgcn_s_waitcnt(kWaitLoads);
-    __syncthreads();
-    for (int s = 0; s < ns; s += 2) {  // two stages per iteration: the code register sets alternate statically
-        if (s + 1 < ns) {
-            fetch(1, s + 1);
-            fetch_x(xb2, s + 1);
-        }
-        compute(0, xa);
+    if constexpr (NB == 2) {
+        Xs xa, xb2;
+        fetch(0, 0);
+        fetch_x(xa, 0);
         __builtin_amdgcn_s_waitcnt(kWaitLoads);
         __syncthreads();
-        if (s + 1 >= ns) break;
-        if (s + 2 < ns) {
-            fetch(0, s + 2);
-            fetch_x(xa, s + 2);
+        for (int s = 0; s < ns; s += 2) {  // two stages per iteration: the code register sets alternate statically
+            if (s + 1 < ns) {
+                fetch(1, s + 1);
+                fetch_x(xb2, s + 1);
+            }
+            compute(0, xa);
+            __builtin_amdgcn_s_waitcnt(kWaitLoads);
+            __syncthreads();
+            if (s + 1 >= ns) break;
+            if (s + 2 < ns) {
+                fetch(0, s + 2);
+                fetch_x(xa, s + 2);
+            }
+            compute(1, xb2);
+            __builtin_amdgcn_s_waitcnt(kWaitLoads);
+            __syncthreads();
         }
-        compute(1, xb2);
-        __builtin_amdgcn_s_waitcnt(kWaitLoads);
+    } else {
+        // The loads this wave issues per stage (every one a vector-memory instruction counted by vmcnt, and
+        // the only ones in the loop): waiting for vmcnt <= that number after issuing stage s + 2 leaves
+        // exactly stage s + 2 in flight, since loads complete in order.
+        int per_stage = BPW + (TABLE ? 1 : 0) + (64 * wave < 16 * SU ? 1 : 0);
+#pragma unroll
+        for (int i = 0; i < LPT; i++) per_stage += NT * i + 64 * wave < SLOTS ? 1 : 0;
+        per_stage = __builtin_amdgcn_readfirstlane(per_stage);
+        Xs x0, x1, x2;
+        // stage s in buffer and register set b = s % 3; its loads were issued two stages earlier
+        auto step = [&](int s, int b, const Xs& xc, Xs& xn) {
+            const bool more = s + 2 < ns;
+            if (more) {
+                fetch((b + 2) % 3, s + 2);
+                fetch_x(xn, s + 2);
+            }
+            // (the buffer index taken from s at run time, so that the compiler keeps one set of LDS addresses,
+            // not one per buffer)
+            compute(__builtin_amdgcn_readfirstlane(s - s / 3 * 3), xc);
+            wait_vm_le(more ? per_stage : 0);  // stage s + 1 has landed
+            __syncthreads();
+        };
+        fetch(0, 0);
+        fetch_x(x0, 0);
+        if (ns > 1) {
+            fetch(1, 1);
+            fetch_x(x1, 1);
+        }
+        wait_vm_le(ns > 1 ? per_stage : 0);
         __syncthreads();
+        for (int s = 0; s < ns; s += 3) {  // three stages per iteration: the register sets rotate statically
+            step(s, 0, x0, x2);
+            if (s + 1 >= ns) break;
+            step(s + 1, 1, x1, x0);
+            if (s + 2 >= ns) break;
+            step(s + 2, 2, x2, x1);
+        }
     }
     if constexpr (OFF) {
 #pragma unroll
@@ -574,7 +664,7 @@ __global__ __launch_bounds__(64 * kI8MfWaves) __attribute__((amdgpu_waves_per_eu
             for (int i = 0; i < 4; i++) acc[m][i] += acc_off[m][i];
     }
     // every wave is past its last read of the stage (the loop ends on a barrier): reuse it for the reduction
-    float* red = reinterpret_cast<float*>(&stage[0][0]);  // [wave][group][i][lane]
+    float* red = reinterpret_cast<float*>(&stage_mem[0]);  // [wave][group][i][lane]
 #pragma unroll
     for (int m = 0; m < G; m++)
         for (int i = 0; i < 4; i++) red[((wave * G + m) * 4 + i) * 64 + lane] = acc[m][i];
@@ -965,12 +1055,12 @@ inline int i8_mfma_min_tokens()
 template <int FMT>
 int run_i8_mfma(I8Args a, bool dual, hipStream_t st)
 {
-    constexpr int SU = I8Stage<FMT>::SU, TN = I8Stage<FMT>::TN;
+    constexpr int SU = I8Stage<FMT>::SU, TN = I8Stage<FMT>::TN, NB = I8Stage<FMT>::NB;
     const dim3 gridt(static_cast<unsigned>((a.N + 16 * TN - 1) / (16 * TN)));
     for (int64_t t0 = 0; t0 < a.T; t0 += 16) {
         a.t0 = t0;
-        if (dual) matvec_i8_mfma<FMT, true, SU, TN><<<gridt, 64 * kI8MfWaves, 0, st>>>(a);
-        else matvec_i8_mfma<FMT, false, SU, TN><<<gridt, 64 * kI8MfWaves, 0, st>>>(a);
+        if (dual) matvec_i8_mfma<FMT, true, SU, TN, NB><<<gridt, 64 * kI8MfWaves, 0, st>>>(a);
+        else matvec_i8_mfma<FMT, false, SU, TN, NB><<<gridt, 64 * kI8MfWaves, 0, st>>>(a);
         const int r = check_launch("matvec_i8_mfma");
         if (r != SLHIP_OK) return r;
     }
