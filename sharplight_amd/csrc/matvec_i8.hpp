@@ -1038,18 +1038,31 @@ static int i8_tt(const I8Args& a, int tt, hipStream_t st)
 }
 
 // Tokens from which the integer-dot matvec takes the matrix cores, when K is a multiple of the stage (whole
-// stages): 5 (measured on MI355X, [14336, 4096] gate/up pairs: at 4 tokens the VALU kernel's one 4-token pass
-// is level with the matrix cores or ahead for every format, from 5 it takes an 8-token pass and falls 1.6-1.9x
-// behind); SLHIP_MATVEC_I8_MFMA_MIN_T overrides it (0 disables).
+// stages), per format: measured on MI355X, [14336, 4096] gate/up pairs, µs at T = 2 / 3 / 4 (VALU kernel ->
+// matrix cores): Q8_0 29.3 / 36.9 / 39.6 -> 32.8 / 32.9 / 33.4; Q4_K 24.4 / 28.6 / 32.6 -> 25.0 / 26.2 / 26.9;
+// IQ4_NL 25.7 / 29.3 / 32.3 -> 27.1 / 28.4 / 28.0; Q5_K T4 37.4 -> 34.6; MXFP4 / Q4_0 / Q4_1 T4 32.1 / 28.7 /
+// 27.3 -> 31.0 / 28.1 / 26.4; Q5_0 / Q5_1 / IQ4_XS level or behind at T4 and Q6_K 37.4 -> 53.2, so those from
+// 5 (where the VALU kernel takes an 8-token pass and falls 1.6-1.9x behind). SLHIP_MATVEC_I8_MFMA_MIN_T
+// overrides it for every format (0 disables).
 template <int FMT>
 inline int i8_mfma_min_tokens()
 {
     static int v = -2;
     if (v == -2) {
         const char* e = getenv("SLHIP_MATVEC_I8_MFMA_MIN_T");
-        v = e ? atoi(e) : 5;
+        v = e ? atoi(e) : -1;
     }
-    return v;
+    if (v != -1) return v;
+    switch (FMT) {
+    case SLHIP_FMT_Q8_0:
+    case SLHIP_FMT_Q4_K:
+    case SLHIP_FMT_IQ4_NL: return 3;
+    case SLHIP_FMT_Q5_K:
+    case SLHIP_FMT_MXFP4:
+    case SLHIP_FMT_Q4_0:
+    case SLHIP_FMT_Q4_1: return 4;
+    default: return 5;
+    }
 }
 
 template <int FMT>

@@ -152,7 +152,7 @@ SINGLE_CASES = [  # (fmt, x dtype, y dtype, T, K, N)
     ("q8_0", "bf16", "f32", 1, 1056, 33),    # 1122 bytes
     ("q5_1", "f32", "bf16", 3, 2080, 24),    # 1560 bytes: 8-byte loads
     ("iq4_nl", "f32", "f32", 4, 96, 17),     # three blocks
-    # from five tokens with K a multiple of 1024: the integer matrix cores (16-row tiles, 1024-value stages)
+    # from 3-5 tokens (by format) with K whole stages: the integer matrix cores (16-row tiles, 512- or 1024-value stages)
     *[(f, "f32", "bf16", 9, 1024, 40) for f in FORMATS],      # one stage, a partial tile
     ("q4_k", "bf16", "f32", 16, 3072, 48),   # three stages (an odd count)
     ("q6_k", "f32", "f32", 20, 2048, 33),    # a full 16-token pass and a 4-token one
@@ -166,6 +166,14 @@ SINGLE_CASES = [  # (fmt, x dtype, y dtype, T, K, N)
     ("q5_k", "f32", "f32", 1, 14336, 19),
     ("q6_k", "f32", "bf16", 4, 256, 700),    # one slice group, many rows per wave
     ("q8_0", "f32", "f32", 6, 1536, 33),     # Q8_0's 512-value stages: three of them (K not a multiple of 1024)
+    # three and four tokens where the matrix cores take them from 3 or 4 tokens (Q8_0, Q4_K, IQ4_NL, Q5_K, ...)
+    # but K is not whole 512-value stages: the VALU kernel
+    ("q8_0", "f32", "f32", 3, 1056, 33),
+    ("iq4_nl", "bf16", "f32", 3, 1056, 21),
+    ("q4_k", "f32", "f32", 4, 1280, 21),
+    ("q5_k", "f32", "bf16", 4, 1280, 19),
+    ("mxfp4", "f32", "f32", 4, 768, 18),
+    ("q4_k", "f32", "bf16", 3, 14080, 21),   # 55 super-blocks: Q4_K's slices on the VALU kernel
 ]
 
 
@@ -183,7 +191,7 @@ def test_matvec_q8(device, fmt, dx, dy, T, K, N):
                                    ("q6_k", 16), ("mxfp4", 5)])
 def test_matvec_q8_bias_and_spread(device, fmt, T):
     """The bias epilogue (FoldMatMulBiases: y + b in f32 after the product) and x blocks spread over 2^-20..2^12,
-    on the VALU kernel (T <= 4) and the matrix cores."""
+    on the VALU kernel (Q4_0 and Q6_K at 3 tokens) and the matrix cores (the rest: Q4_K and IQ4_NL from 3)."""
     K, N = 2048, 50
     seed = _seed("bias", fmt, T)
     raw = synth.quant_table(fmt, N, K, seed=seed, tid=1)
