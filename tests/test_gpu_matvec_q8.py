@@ -255,7 +255,13 @@ def test_dual_matvec_q8(device, act, fmt, dx, dy, T, K, N):
     _compare(y, dy, ref, tol, f"dual_matvec_q8 {act} {fmt}")
 
 
-@pytest.mark.parametrize("fmt,dx,T,K,N", [("q4_k", "f32", 3, 4096, 200), ("q8_0", "bf16", 12, 2048, 64)])
+@pytest.mark.parametrize("fmt,dx,T,K,N", [
+    ("q4_k", "f32", 3, 4096, 200), ("q8_0", "bf16", 12, 2048, 64),
+    # few tokens on the VALU kernel
+    ("q4_k", "f32", 1, 4096, 300), ("q6_k", "bf16", 1, 4096, 130), ("q4_0", "bf16", 2, 2048, 70),
+    ("q5_1", "f32", 4, 1056, 33), ("q8_0", "f32", 2, 96, 17), ("mxfp4", "f32", 1, 768, 40),
+    # the register-piece kernel (IQ4_XS) and the matrix cores
+    ("iq4_xs", "f32", 1, 4096, 90), ("q5_k", "bf16", 4, 2048, 48)])
 def test_dual_matvec_int8_one_call(device, fmt, dx, T, K, N):
     """slhip_dual_matvec_int8 (quantize into the caller's workspace, then the dual matvec) equals the two calls
     bit for bit; a workspace below T q8 rows is refused."""
